@@ -1,0 +1,185 @@
+"""ctypes loader for the CPU oracle. TEST INFRASTRUCTURE ONLY.
+
+Two libraries share one Python interface:
+
+* ``liboracle_v{3,4}.so`` - this repository's C restatement of the reference's
+  CPU attention and RoPE (``oracle/smol_oracle.c``; each function there cites
+  the reference file:line it follows), symbol prefix ``orc_``.
+* ``_ref/libsmolref_v{3,4}.so`` - the reference's own
+  ``common/kernels/{attention,rope,vecops_*,threading}.c`` compiled from the
+  reference tree by ``oracle/Makefile``, symbol prefix ``smol_``. It exists
+  only where it was built; tests that need it skip otherwise.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the CPU-baseline leg of
+``bench.py`` import this module. Arrays are numpy, C-contiguous.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+_F = ctypes.POINTER(ctypes.c_float)
+_I = ctypes.POINTER(ctypes.c_int)
+_U16 = ctypes.POINTER(ctypes.c_uint16)
+
+
+def cpu_has_avx512():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    fl = line.split()
+                    return all(x in fl for x in ("avx512f", "avx512bw", "avx512vl", "avx512dq"))
+    except OSError:
+        pass
+    return False
+
+
+def simd_branch():
+    return "avx512" if cpu_has_avx512() else "avx2"
+
+
+def _fp(a):
+    return a.ctypes.data_as(_F)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class _Lib:
+    """Common wrapper; ``prefix`` is ``orc_`` (restatement) or ``smol_`` (reference)."""
+
+    def __init__(self, path, prefix):
+        self.path = path
+        self.prefix = prefix
+        self.lib = ctypes.CDLL(path)
+        self._bind()
+
+    def _fn(self, name, argtypes, restype=None):
+        f = getattr(self.lib, self.prefix + name)
+        f.argtypes = argtypes
+        f.restype = restype
+        return f
+
+    def _bind(self):
+        ci, cf = ctypes.c_int, ctypes.c_float
+        causal = [_F, _F, _F, _F, ci, ci, ci, ci, ci, cf, ci]
+        self._causal = self._fn("causal_attention", causal)
+        self._swa = self._fn("sliding_window_attention", causal + [ci])
+        self._softcap = self._fn("causal_attention_softcap", causal + [cf])
+        self._swa_softcap = self._fn("sliding_window_attention_softcap", causal + [ci, cf])
+        self._bidir = self._fn("bidirectional_attention", [_F, _F, _F, _F, ci, ci, ci, cf, _I, ci])
+        self._crope_neox = self._fn("compute_rope_neox", [_F, _F, _I, ci, ci, cf])
+        self._crope_inter = self._fn("compute_rope_interleaved", [_F, _F, _I, ci, ci, cf])
+        self._arope_neox = self._fn("apply_rope_neox", [_F, _F, _F, ci, ci, ci])
+        self._arope_inter = self._fn("apply_rope_interleaved", [_F, _F, _F, ci, ci, ci])
+        set_threads = "set_threads"
+        self._set_threads = self._fn(set_threads, [ci])
+
+    def set_threads(self, n):
+        self._set_threads(int(n))
+
+    # -- attention ---------------------------------------------------------
+    def causal_attention(self, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim,
+                         scale, q_offset, window=0, cap=0.0):
+        Q, K, V = _f32(Q), _f32(K), _f32(V)
+        assert Q.size >= seq_q * n_heads * head_dim
+        assert K.size >= seq_k * n_kv_heads * head_dim and V.size == K.size
+        out = np.zeros((seq_q, n_heads * head_dim), np.float32)
+        args = (_fp(out), _fp(Q), _fp(K), _fp(V), seq_q, seq_k, n_heads, n_kv_heads,
+                head_dim, ctypes.c_float(scale), q_offset)
+        if window > 0 and cap > 0:
+            self._swa_softcap(*args, window, ctypes.c_float(cap))
+        elif window > 0:
+            self._swa(*args, window)
+        elif cap > 0:
+            self._softcap(*args, ctypes.c_float(cap))
+        else:
+            self._causal(*args)
+        return out
+
+    def bidirectional_attention(self, Q, K, V, seq, n_heads, head_dim, scale, window_starts):
+        Q, K, V = _f32(Q), _f32(K), _f32(V)
+        ws = np.ascontiguousarray(window_starts, dtype=np.int32)
+        assert ws[-1] <= seq and Q.size >= seq * n_heads * head_dim
+        out = np.zeros((seq, n_heads * head_dim), np.float32)
+        self._bidir(_fp(out), _fp(Q), _fp(K), _fp(V), seq, n_heads, head_dim,
+                    ctypes.c_float(scale), ws.ctypes.data_as(_I), len(ws) - 1)
+        return out
+
+    # -- RoPE ----------------------------------------------------------------
+    def compute_rope(self, positions, head_dim, theta, interleaved=False):
+        pos = np.ascontiguousarray(positions, dtype=np.int32)
+        c = np.zeros((len(pos), head_dim), np.float32)
+        s = np.zeros_like(c)
+        f = self._crope_inter if interleaved else self._crope_neox
+        f(_fp(c), _fp(s), pos.ctypes.data_as(_I), len(pos), head_dim, ctypes.c_float(theta))
+        return c, s
+
+    def apply_rope(self, x, cos, sin, seq, n_heads, head_dim, interleaved=False):
+        y = np.array(x, dtype=np.float32, copy=True, order="C")
+        c, s = _f32(cos), _f32(sin)
+        assert c.size >= seq * head_dim
+        f = self._arope_inter if interleaved else self._arope_neox
+        f(_fp(y), _fp(c), _fp(s), seq, n_heads, head_dim)
+        return y
+
+
+class Oracle(_Lib):
+    """The C restatement (``orc_`` symbols) plus its extra entry points."""
+
+    def __init__(self, path=None):
+        if path is None:
+            path = os.path.join(HERE, "liboracle_v4.so" if cpu_has_avx512() else "liboracle_v3.so")
+        super().__init__(path, "orc_")
+        ci, cf = ctypes.c_int, ctypes.c_float
+        self._fill = self._fn("fill_rope_table", [_F, _F, ci, ci, ci, cf, ci])
+        self._inv = self._fn("rope_inv_freq", [_F, ci, cf])
+        self._generic = self._fn("set_vec_generic", [ci])
+        self._bf16_attn = self._fn("bf16_attention_softcap",
+                                   [_U16, _U16, _U16, _U16, ci, ci, ci, ci, ci, cf, ci, ci, cf])
+
+    def set_vec_generic(self, on):
+        self._generic(1 if on else 0)
+
+    def rope_inv_freq(self, head_dim, theta):
+        inv = np.zeros(head_dim // 2, np.float32)
+        self._inv(_fp(inv), head_dim, ctypes.c_float(theta))
+        return inv
+
+    def fill_rope_table(self, pos0, n_pos, head_dim, theta, interleaved=False):
+        c = np.zeros((n_pos, head_dim), np.float32)
+        s = np.zeros_like(c)
+        self._fill(_fp(c), _fp(s), pos0, n_pos, head_dim, ctypes.c_float(theta),
+                   1 if interleaved else 0)
+        return c, s
+
+    def bf16_attention(self, q, k, v, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale,
+                       q_offset, window=0, cap=0.0):
+        q = np.ascontiguousarray(q, np.uint16)
+        k = np.ascontiguousarray(k, np.uint16)
+        v = np.ascontiguousarray(v, np.uint16)
+        out = np.zeros((seq_q, n_heads * head_dim), np.uint16)
+        u = lambda a: a.ctypes.data_as(_U16)  # noqa: E731
+        self._bf16_attn(u(out), u(q), u(k), u(v), seq_q, seq_k, n_heads, n_kv_heads,
+                        head_dim, ctypes.c_float(scale), q_offset, window, ctypes.c_float(cap))
+        return out
+
+
+def ref_path():
+    """Path of the compiled reference library for this host, or None."""
+    p = os.path.join(HERE, "_ref", "libsmolref_v4.so" if cpu_has_avx512() else "libsmolref_v3.so")
+    return p if os.path.exists(p) else None
+
+
+class RefLib(_Lib):
+    """The reference's own sources, compiled by oracle/Makefile (``smol_`` symbols)."""
+
+    def __init__(self, path=None):
+        path = path or ref_path()
+        if path is None:
+            raise FileNotFoundError("oracle/_ref was not built")
+        super().__init__(path, "smol_")

@@ -1,0 +1,103 @@
+"""Writes the golden fixtures in this directory from the compiled reference.
+
+The reference's CPU attention and RoPE sources
+(common/kernels/{attention,rope,vecops_avx,vecops_generic,threading}.c) are
+compiled by ``oracle/Makefile`` into ``oracle/_ref/``; this script calls that
+library (single-threaded) on seeded inputs and stores the outputs. Inputs are
+not stored: they are regenerated from the recorded seeds with
+``smol-genius_amd/synth.py``, and a checksum of them is stored so a change in the
+generator is caught instead of silently comparing different data.
+
+Run from the repository root:  python tests/golden/gen_golden.py
+"""
+import json
+import os
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+sys.path.insert(0, os.path.join(ROOT, "smol-genius_amd"))
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+import synth  # noqa: E402
+from oracle import RefLib, simd_branch  # noqa: E402
+from gen_golden_inputs import bidir_inputs, causal_inputs, digest  # noqa: E402
+
+OUT = os.path.dirname(os.path.abspath(__file__))
+
+# (name, Hq, Hkv, hd, seq_q, seq_k, q_offset, window, cap)
+CAUSAL = [
+    ("c_16_8_128_q1_k300", 16, 8, 128, 1, 300, 299, 0, 0.0),
+    ("c_16_8_128_q7_k64_p0", 16, 8, 128, 7, 64, 0, 0, 0.0),
+    ("c_8_4_128_q26_k200", 8, 4, 128, 26, 200, 174, 0, 0.0),
+    ("c_4_2_128_q64_k64", 4, 2, 128, 64, 64, 0, 0, 0.0),
+    ("c_8_1_256_q1_k320", 8, 1, 256, 1, 320, 319, 0, 0.0),
+    ("c_8_1_256_q7_k96", 8, 1, 256, 7, 96, 89, 0, 0.0),
+    ("c_4_4_72_q26_k26", 4, 4, 72, 26, 26, 0, 0, 0.0),
+    ("c_4_4_72_q7_k150", 4, 4, 72, 7, 150, 143, 0, 0.0),
+    ("c_4_4_64_q64_k128", 4, 4, 64, 64, 128, 64, 0, 0.0),
+    ("c_4_4_64_q1_k1", 4, 4, 64, 1, 1, 0, 0, 0.0),
+    ("c_16_8_64_q7_k40_clip", 16, 8, 64, 7, 40, 36, 0, 0.0),
+    ("c_4_2_256_q26_k26_p0", 4, 2, 256, 26, 26, 0, 0, 0.0),
+    ("swa_8_4_128_q26_k200_w64", 8, 4, 128, 26, 200, 174, 64, 0.0),
+    ("swa_4_4_64_q64_k64_w16", 4, 4, 64, 64, 64, 0, 16, 0.0),
+    ("cap_8_4_128_q7_k100_c50", 8, 4, 128, 7, 100, 93, 0, 50.0),
+    ("cap_4_1_256_q26_k26_c30", 4, 1, 256, 26, 26, 0, 0, 30.0),
+    ("swacap_8_2_128_q26_k160_w32_c50", 8, 2, 128, 26, 160, 134, 32, 50.0),
+]
+
+# (name, H, hd, window_starts, std)
+BIDIR = [
+    ("b_4_72_w1x64", 4, 72, [0, 64], 0.5),
+    ("b_4_72_w4x32", 4, 72, [0, 32, 64, 96, 128], 0.5),
+    ("b_4_64_ragged", 4, 64, [0, 40, 80, 104], 1.0),
+    ("b_2_128_w3", 2, 128, [0, 7, 8, 50], 1.0),
+    ("b_2_256_w2", 2, 256, [0, 33, 66], 1.0),
+]
+
+ROPE_POS = [0, 1, 1023, 1024, 1535, 4095, 8191, 8281]
+ROPE = [(hd, theta) for hd in (64, 128, 256) for theta in (1e4, 1e6)]
+
+
+def main():
+    ref = RefLib()
+    ref.set_threads(1)
+    arrays, meta = {}, {"simd": simd_branch(), "ref": os.path.basename(ref.path),
+                        "causal": [], "bidir": [], "rope": []}
+    for i, (name, Hq, Hkv, hd, sq, sk, qo, win, cap) in enumerate(CAUSAL):
+        seed = 1000 + i
+        Q, K, V = causal_inputs(seed, Hq, Hkv, hd, sq, sk)
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+        out = ref.causal_attention(Q, K, V, sq, sk, Hq, Hkv, hd, scale, qo, window=win, cap=cap)
+        arrays[name] = out
+        meta["causal"].append(dict(name=name, seed=seed, Hq=Hq, Hkv=Hkv, hd=hd, seq_q=sq,
+                                   seq_k=sk, q_offset=qo, window=win, cap=cap, scale=scale,
+                                   digest=digest(Q, K, V)))
+    for i, (name, H, hd, ws, std) in enumerate(BIDIR):
+        seed = 2000 + i
+        seq = ws[-1]
+        Q, K, V = bidir_inputs(seed, H, hd, seq, std)
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+        arrays[name] = ref.bidirectional_attention(Q, K, V, seq, H, hd, scale, ws)
+        meta["bidir"].append(dict(name=name, seed=seed, H=H, hd=hd, window_starts=ws, std=std,
+                                  scale=scale, digest=digest(Q, K, V)))
+    pos = np.array(ROPE_POS, np.int32)
+    for hd, theta in ROPE:
+        for inter in (False, True):
+            tag = "rope_%s_%d_%g" % ("inter" if inter else "neox", hd, theta)
+            c, s = ref.compute_rope(pos, hd, theta, interleaved=inter)
+            seed = 3000 + hd + (1 if inter else 0) + (7 if theta > 1e5 else 0)
+            x = synth.normal(seed, (len(pos), 3 * hd))
+            y = ref.apply_rope(x, c, s, len(pos), 3, hd, interleaved=inter)
+            arrays[tag + "_cos"], arrays[tag + "_sin"], arrays[tag + "_applied"] = c, s, y
+            meta["rope"].append(dict(tag=tag, hd=hd, theta=theta, interleaved=inter,
+                                     positions=ROPE_POS, seed=seed, heads=3, digest=digest(x)))
+    np.savez_compressed(os.path.join(OUT, "ref_attention.npz"), **arrays)
+    with open(os.path.join(OUT, "ref_attention.json"), "w") as f:
+        json.dump(meta, f, indent=1)
+    print("wrote", len(arrays), "arrays; simd", meta["simd"])
+
+
+if __name__ == "__main__":
+    main()

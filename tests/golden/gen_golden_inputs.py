@@ -1,0 +1,28 @@
+"""Seeded inputs of the golden fixtures (shared by gen_golden.py and the tests)."""
+import hashlib
+import os
+import sys
+
+import numpy as np
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(
+    os.path.abspath(__file__)))), "smol-genius_amd"))
+import synth  # noqa: E402
+
+
+def digest(*arrays):
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()[:16]
+
+
+def causal_inputs(seed, Hq, Hkv, hd, seq_q, seq_k):
+    Q = synth.normal(seed * 3 + 0, (seq_q, Hq * hd))
+    K = synth.normal(seed * 3 + 1, (seq_k, Hkv * hd))
+    V = synth.normal(seed * 3 + 2, (seq_k, Hkv * hd))
+    return Q, K, V
+
+
+def bidir_inputs(seed, H, hd, seq, std):
+    return tuple(synth.normal(seed * 3 + i, (seq, H * hd), std) for i in range(3))

@@ -1,0 +1,250 @@
+"""Pins the CPU oracle with what the mathematics fixes, independent of the reference.
+
+* float64 brute force: softmax(scale * Q K^T + mask) V, with the causal,
+  sliding-window and softcap variants and GQA head mapping written out
+  independently of the oracle's online-softmax loop;
+* closed forms: one visible key, identical keys, scale 0, empty rows, clipping;
+* structural identities: decode == last row of prefill, chunked prefill ==
+  rows of the full prefill, GQA == MHA with repeated K/V heads, windowed
+  bidirectional == per-window calls;
+* RoPE: float64 tables, position 0 is the identity, pair norms are kept,
+  R(a) R(b) = R(a + b);
+* planted mistakes: mutated float64 restatements (off-by-one causal limit,
+  wrong RoPE sign, wrong GQA head map, transposed RoPE pairing) must fail the
+  same checks, so the checks can tell a right answer from a plausible wrong one.
+"""
+import numpy as np
+import pytest
+
+from conftest import synth
+
+
+def brute_causal(Q, K, V, seq_q, seq_k, Hq, Hkv, hd, scale, q_offset, window=0, cap=0.0,
+                 kv_head=None):
+    Q = Q.astype(np.float64).reshape(seq_q, Hq, hd)
+    K = K.astype(np.float64).reshape(seq_k, Hkv, hd)
+    V = V.astype(np.float64).reshape(seq_k, Hkv, hd)
+    out = np.zeros((seq_q, Hq, hd))
+    kv_head = kv_head or (lambda h: h // (Hq // Hkv))
+    for h in range(Hq):
+        g = kv_head(h)
+        s = Q[:, h, :] @ K[:, g, :].T * scale
+        if cap > 0:
+            s = cap * np.tanh(s / cap)
+        pos = q_offset + np.arange(seq_q)[:, None]
+        j = np.arange(seq_k)[None, :]
+        vis = j <= pos
+        if window > 0:
+            vis &= j > pos - window
+        s = np.where(vis, s, -np.inf)
+        for i in range(seq_q):
+            if not vis[i].any():
+                continue
+            p = np.exp(s[i] - s[i].max())
+            out[i, h] = (p @ V[:, g, :]) / p.sum()
+    return out.reshape(seq_q, Hq * hd)
+
+
+def rand(seed, shape, std=1.0):
+    return synth.normal(seed, shape, std)
+
+
+CASES = [  # Hq, Hkv, hd, seq_q, seq_k, q_offset
+    (4, 2, 64, 9, 9, 0), (8, 1, 128, 1, 77, 76), (2, 2, 72, 13, 40, 27),
+    (4, 4, 256, 5, 17, 12), (6, 3, 64, 8, 30, 25),
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_causal_brute_force(oracle, case):
+    Hq, Hkv, hd, sq, sk, qo = case
+    Q, K, V = rand(1, (sq, Hq * hd)), rand(2, (sk, Hkv * hd)), rand(3, (sk, Hkv * hd))
+    sc = 1.0 / np.sqrt(hd)
+    got = oracle.causal_attention(Q, K, V, sq, sk, Hq, Hkv, hd, sc, qo)
+    np.testing.assert_allclose(got, brute_causal(Q, K, V, sq, sk, Hq, Hkv, hd, sc, qo),
+                               rtol=2e-5, atol=2e-6)
+
+
+@pytest.mark.parametrize("window,cap", [(5, 0.0), (0, 20.0), (7, 5.0), (1, 0.0)])
+def test_window_softcap_brute_force(oracle, window, cap):
+    Hq, Hkv, hd, sq, sk, qo = 4, 2, 64, 12, 30, 18
+    Q, K, V = rand(4, (sq, Hq * hd), 2.0), rand(5, (sk, Hkv * hd), 2.0), rand(6, (sk, Hkv * hd))
+    sc = 1.0 / np.sqrt(hd)
+    got = oracle.causal_attention(Q, K, V, sq, sk, Hq, Hkv, hd, sc, qo, window=window, cap=cap)
+    want = brute_causal(Q, K, V, sq, sk, Hq, Hkv, hd, sc, qo, window=window, cap=cap)
+    np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-6)
+
+
+def test_bidirectional_brute_force_and_windows(oracle):
+    H, hd = 3, 72
+    ws = [0, 10, 11, 37]
+    seq = ws[-1]
+    Q, K, V = rand(7, (seq, H * hd)), rand(8, (seq, H * hd)), rand(9, (seq, H * hd))
+    sc = 1.0 / np.sqrt(hd)
+    got = oracle.bidirectional_attention(Q, K, V, seq, H, hd, sc, ws)
+    want = np.zeros_like(got)
+    for a, b in zip(ws[:-1], ws[1:]):
+        n = b - a
+        # a bidirectional window is causal attention of its last row over every row
+        blk = brute_causal(Q[a:b], K[a:b], V[a:b], n, n, H, H, hd, sc, n - 1)
+        want[a:b] = blk
+        # and the windowed call equals an independent call on that window
+        sub = oracle.bidirectional_attention(Q[a:b], K[a:b], V[a:b], n, H, hd, sc, [0, n])
+        np.testing.assert_array_equal(sub, got[a:b])
+    np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-6)
+
+
+def test_closed_forms(oracle):
+    Hq, Hkv, hd = 4, 2, 64
+    sk = 20
+    K, V = rand(10, (sk, Hkv * hd)), rand(11, (sk, Hkv * hd))
+    Q = rand(12, (sk, Hq * hd))
+    sc = 0.125
+    out = oracle.causal_attention(Q, K, V, sk, sk, Hq, Hkv, hd, sc, 0)
+    # row 0 sees one key: o = v_0 for every head of the group
+    for h in range(Hq):
+        g = h // 2
+        np.testing.assert_array_equal(out[0, h * hd:(h + 1) * hd], V[0, g * hd:(g + 1) * hd])
+    # scale 0: uniform weights, o_i = mean(v_0..v_i)
+    out0 = oracle.causal_attention(Q, K, V, sk, sk, Hq, Hkv, hd, 0.0, 0)
+    cm = np.cumsum(V.astype(np.float64), 0) / np.arange(1, sk + 1)[:, None]
+    for h in range(Hq):
+        g = h // 2
+        np.testing.assert_allclose(out0[:, h * hd:(h + 1) * hd], cm[:, g * hd:(g + 1) * hd],
+                                   rtol=1e-5, atol=1e-6)
+    # identical keys: o = mean of the visible values
+    Kc = np.tile(K[:1], (sk, 1))
+    outc = oracle.causal_attention(Q, Kc, V, sk, sk, Hq, Hkv, hd, sc, 0)
+    np.testing.assert_allclose(outc[:, :hd], cm[:, :hd], rtol=1e-5, atol=1e-6)
+    # empty rows (q_offset + i + 1 <= 0) are zero; seq_k = 0 gives zeros
+    outn = oracle.causal_attention(Q[:5], K, V, 5, sk, Hq, Hkv, hd, sc, -3)
+    assert not outn[:3].any() and outn[3:].any()
+    assert not oracle.causal_attention(Q[:2], K, V, 2, 0, Hq, Hkv, hd, sc, 0).any()
+    # q_offset + i >= seq_k clips to seq_k visible keys
+    a = oracle.causal_attention(Q[:1], K, V, 1, sk, Hq, Hkv, hd, sc, 500)
+    b = oracle.causal_attention(Q[:1], K, V, 1, sk, Hq, Hkv, hd, sc, sk - 1)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_structural_identities(oracle):
+    Hq, Hkv, hd, S = 8, 2, 128, 40
+    Q, K, V = rand(13, (S, Hq * hd)), rand(14, (S, Hkv * hd)), rand(15, (S, Hkv * hd))
+    sc = 1.0 / np.sqrt(hd)
+    full = oracle.causal_attention(Q, K, V, S, S, Hq, Hkv, hd, sc, 0)
+    # decode == last prefill row
+    dec = oracle.causal_attention(Q[-1:], K, V, 1, S, Hq, Hkv, hd, sc, S - 1)
+    np.testing.assert_array_equal(dec, full[-1:])
+    # chunked prefill == rows P..P+C-1 of the full prefill
+    P, C = 29, 11
+    ch = oracle.causal_attention(Q[P:P + C], K, V, C, S, Hq, Hkv, hd, sc, P)
+    np.testing.assert_array_equal(ch, full[P:P + C])
+    # GQA == MHA with K/V heads repeat-interleaved
+    rep = Hq // Hkv
+    Km = np.repeat(K.reshape(S, Hkv, hd), rep, axis=1).reshape(S, Hq * hd)
+    Vm = np.repeat(V.reshape(S, Hkv, hd), rep, axis=1).reshape(S, Hq * hd)
+    mha = oracle.causal_attention(Q, Km, Vm, S, S, Hq, Hq, hd, sc, 0)
+    np.testing.assert_array_equal(mha, full)
+
+
+def _rope64(x, pos, hd, theta, interleaved):
+    inv = 1.0 / np.power(np.float64(theta), np.arange(hd // 2) * 2.0 / hd)
+    a = np.asarray(pos, np.float64)[:, None] * inv[None, :]
+    c, s = np.cos(a), np.sin(a)
+    x = x.astype(np.float64).reshape(len(pos), -1, hd)
+    if interleaved:
+        x0, x1 = x[..., 0::2], x[..., 1::2]
+        y = np.empty_like(x)
+        y[..., 0::2] = x0 * c[:, None] - x1 * s[:, None]
+        y[..., 1::2] = x1 * c[:, None] + x0 * s[:, None]
+    else:
+        h = hd // 2
+        x1, x2 = x[..., :h], x[..., h:]
+        y = np.concatenate([x1 * c[:, None] - x2 * s[:, None], x2 * c[:, None] + x1 * s[:, None]], -1)
+    return y.reshape(len(pos), -1)
+
+
+@pytest.mark.parametrize("hd,theta,inter", [(128, 1e6, False), (256, 1e4, True), (64, 1e4, False),
+                                            (72, 1e4, False)])
+def test_rope_against_float64(oracle, hd, theta, inter):
+    pos = np.array([0, 1, 5, 100, 1023, 1024, 4095, 8281], np.int32)
+    c, s = oracle.fill_rope_table(0, 8282, hd, theta, inter)
+    c, s = c[pos], s[pos]
+    inv32 = oracle.rope_inv_freq(hd, theta)
+    ang = pos[:, None].astype(np.float32) * inv32[None, :]  # the float32 angle of the reference
+    k = np.arange(hd) // 2 if inter else np.arange(hd) % (hd // 2)
+    np.testing.assert_allclose(c, np.cos(ang.astype(np.float64))[:, k], atol=1e-6)
+    np.testing.assert_allclose(s, np.sin(ang.astype(np.float64))[:, k], atol=1e-6)
+    # the frequency itself is the float64 one to float32 rounding
+    np.testing.assert_allclose(inv32, 1.0 / np.power(theta, np.arange(hd // 2) * 2.0 / hd),
+                               rtol=3e-7)
+    x = rand(16, (len(pos), 2 * hd))
+    y = oracle.apply_rope(x, c, s, len(pos), 2, hd, interleaved=inter)
+    # position 0 is the identity
+    np.testing.assert_array_equal(y[0], x[0])
+    # each rotated pair keeps its norm
+    yy, xx = y.reshape(len(pos), 2, hd).astype(np.float64), x.reshape(len(pos), 2, hd).astype(np.float64)
+    if inter:
+        ny, nx = yy[..., 0::2] ** 2 + yy[..., 1::2] ** 2, xx[..., 0::2] ** 2 + xx[..., 1::2] ** 2
+    else:
+        h = hd // 2
+        ny, nx = yy[..., :h] ** 2 + yy[..., h:] ** 2, xx[..., :h] ** 2 + xx[..., h:] ** 2
+    np.testing.assert_allclose(ny, nx, rtol=2e-5, atol=1e-6)
+    # against a rotation by tables computed in float64 from the same float32 angle
+    a64 = ang.astype(np.float64)
+    cc, ss = np.cos(a64)[:, k], np.sin(a64)[:, k]
+    yr = oracle.apply_rope(x, cc.astype(np.float32), ss.astype(np.float32), len(pos), 2, hd, inter)
+    np.testing.assert_allclose(y, yr, atol=2e-5)
+
+
+def test_rope_composition(oracle):
+    hd, theta = 128, 1e6
+    a, b = 300, 211
+    c, s = oracle.fill_rope_table(0, a + b + 1, hd, theta, False)
+    x = rand(17, (1, 4 * hd))
+    ya = oracle.apply_rope(x, c[a:a + 1], s[a:a + 1], 1, 4, hd)
+    yab = oracle.apply_rope(ya, c[b:b + 1], s[b:b + 1], 1, 4, hd)
+    yd = oracle.apply_rope(x, c[a + b:a + b + 1], s[a + b:a + b + 1], 1, 4, hd)
+    np.testing.assert_allclose(yab, yd, atol=2e-4)  # float32 angles of 511 rad
+
+
+# ------------------------------------------------------------ planted mistakes
+
+def test_planted_mistakes_are_caught(oracle):
+    Hq, Hkv, hd, sq, sk, qo = 4, 2, 64, 9, 20, 11
+    Q, K, V = rand(18, (sq, Hq * hd)), rand(19, (sk, Hkv * hd)), rand(20, (sk, Hkv * hd))
+    sc = 1.0 / np.sqrt(hd)
+    got = oracle.causal_attention(Q, K, V, sq, sk, Hq, Hkv, hd, sc, qo)
+    ok = lambda w: np.allclose(got, w, rtol=2e-5, atol=2e-6)  # noqa: E731
+    assert ok(brute_causal(Q, K, V, sq, sk, Hq, Hkv, hd, sc, qo))
+    # causal limit off by one
+    assert not ok(brute_causal(Q, K, V, sq, sk, Hq, Hkv, hd, sc, qo + 1))
+    assert not ok(brute_causal(Q, K, V, sq, sk, Hq, Hkv, hd, sc, qo - 1))
+    # GQA head map h % Hkv instead of h // (Hq / Hkv)
+    assert not ok(brute_causal(Q, K, V, sq, sk, Hq, Hkv, hd, sc, qo, kv_head=lambda h: h % Hkv))
+    # dropped scale
+    assert not ok(brute_causal(Q, K, V, sq, sk, Hq, Hkv, hd, 1.0, qo))
+    # RoPE with the sign of the sine flipped, or pairs taken as interleaved
+    pos = np.array([3, 50], np.int32)
+    c, s = oracle.fill_rope_table(0, 51, hd, 1e4, False)
+    x = rand(21, (2, hd))
+    y = oracle.apply_rope(x, c[pos], s[pos], 2, 1, hd)
+    assert np.allclose(y, _rope64(x, pos, hd, 1e4, False), atol=1e-5)
+    assert not np.allclose(y, _rope64(x, -pos, hd, 1e4, False), atol=1e-5)
+    assert not np.allclose(y, _rope64(x, pos, hd, 1e4, True), atol=1e-5)
+
+
+def test_bf16_two_pass_attention(oracle):
+    """qkn_bf16_decoder.c two-pass attention: truncating bf16 output of the exact result."""
+    Hq, Hkv, hd, sq, sk, qo = 4, 1, 256, 6, 33, 27
+    q = synth.f32_to_bf16_bits(rand(22, (sq, Hq * hd)))
+    k = synth.f32_to_bf16_bits(rand(23, (sk, Hkv * hd)))
+    v = synth.f32_to_bf16_bits(rand(24, (sk, Hkv * hd)))
+    sc = 1.0 / np.sqrt(hd)
+    for win, cap in [(0, 0.0), (8, 0.0), (0, 50.0)]:
+        out = synth.bf16_bits_to_f32(oracle.bf16_attention(q, k, v, sq, sk, Hq, Hkv, hd, sc, qo,
+                                                           window=win, cap=cap))
+        want = brute_causal(synth.bf16_bits_to_f32(q), synth.bf16_bits_to_f32(k),
+                            synth.bf16_bits_to_f32(v), sq, sk, Hq, Hkv, hd, sc, qo,
+                            window=win, cap=cap)
+        # truncation toward zero: |out| <= |want| + tiny and within one bf16 ulp (2^-7 rel)
+        np.testing.assert_allclose(out, want, rtol=2 ** -7, atol=1e-6)
