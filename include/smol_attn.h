@@ -1,0 +1,177 @@
+/*
+ * smol_attn.h - C ABI of the MI355X (gfx950) attention path for smol-genius.
+ *
+ * Plain C types only (pointers, ints, floats); no HIP or torch types cross
+ * this boundary. Library: libsmol_attn.so (link with -lsmol_attn).
+ *
+ * Two layers:
+ *  1. Device-resident API (this section): a context (device + stream +
+ *     workspace), a RoPE table, a bf16 KV cache, and decode / prefill /
+ *     bidirectional attention on device pointers, enqueued on the context's
+ *     stream. Every call returns an int status (SMOL_ATTN_OK or a negative
+ *     code); smol_attn_last_error() describes the last failure of the calling
+ *     thread. These replace the attention block of the reference decoders:
+ *     RoPE on Q/K + cache append + attention
+ *     (common/decoder/qkn_decoder.c:493-528 in qkn_decoder_prefill and
+ *      :647-677 in qkn_decoder_forward).
+ *  2. Drop-ins with the reference's exact signatures on host fp32 arrays,
+ *     declared in smol_kernels_attn.h (common/kernels/smol_kernels.h:109-161).
+ *
+ * Tensor layouts are the reference's (common/kernels/attention.c:84-104):
+ *   Q, out      [tokens][n_heads * head_dim]        row-major
+ *   K, V (new)  [tokens][n_kv_heads * head_dim]     row-major
+ * head h uses KV head h / (n_heads / n_kv_heads). Outputs are fp32.
+ * Supported head_dim: 64, 72, 80, 96, 128, 256.
+ *
+ * Numerics: the softmax runs in fp32; the QK^T and PV products run on fp16
+ * MFMA operands (bf16 inputs convert exactly; |values| must stay below 65504).
+ * The KV cache stores post-RoPE K and V in bf16 (round to nearest even).
+ * Keys written by a call are used by that same call at fp16 precision.
+ *
+ * Threading: one context per host thread, as the reference's global thread
+ * pool is not re-entrant (common/kernels/threading.c:26-47). Calls on one
+ * context are ordered on its stream.
+ */
+#ifndef SMOL_ATTN_H
+#define SMOL_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SMOL_ATTN_API __attribute__((visibility("default")))
+
+/* status codes */
+#define SMOL_ATTN_OK 0
+#define SMOL_ATTN_ERR_ARG (-1)
+#define SMOL_ATTN_ERR_NOMEM (-2)
+#define SMOL_ATTN_ERR_DEVICE (-3)
+#define SMOL_ATTN_ERR_UNSUPPORTED (-4)
+#define SMOL_ATTN_ERR_NO_GPU (-5)
+
+/* element type of the Q / K / V inputs */
+#define SMOL_ATTN_F32 0
+#define SMOL_ATTN_BF16 1
+
+/* RoPE pairing; qkn_rope_type_t in common/decoder/qkn_decoder.h:33-36 */
+#define SMOL_ROPE_NONE (-1)
+#define SMOL_ROPE_NEOX 0        /* (x[d], x[half + d]): Qwen3 */
+#define SMOL_ROPE_INTERLEAVED 1 /* (x[2d], x[2d + 1]): Gemma / PaliGemma */
+
+typedef struct smol_attn_ctx smol_attn_ctx;
+typedef struct smol_rope_table smol_rope_table;
+typedef struct smol_kv_cache smol_kv_cache;
+
+/* ---- library / context -------------------------------------------------- */
+
+SMOL_ATTN_API const char *smol_attn_version(void);
+SMOL_ATTN_API const char *smol_attn_last_error(void);
+/* number of visible GPUs, or a negative status when the HIP runtime has none */
+SMOL_ATTN_API int smol_attn_device_count(void);
+
+/* stream: a hipStream_t passed as void*; NULL selects the device's null
+ * stream. The context never creates or destroys the stream. */
+SMOL_ATTN_API int smol_attn_ctx_create(int device, void *stream, smol_attn_ctx **out);
+SMOL_ATTN_API int smol_attn_ctx_destroy(smol_attn_ctx *ctx);
+SMOL_ATTN_API int smol_attn_ctx_synchronize(smol_attn_ctx *ctx);
+SMOL_ATTN_API void *smol_attn_ctx_stream(smol_attn_ctx *ctx);
+
+/* ---- RoPE table ----------------------------------------------------------
+ * Device fp32 cos/sin rows [capacity][head_dim], built on the host exactly as
+ * fill_rope_cache does (common/decoder/qkn_decoder.c:261-311):
+ * inv_freq[d] = 1 / powf(theta, 2d / head_dim), angle = (float)pos * inv_freq[d],
+ * duplicated to (d, half + d) or (2d, 2d + 1). Capacity starts at >= 1024 and
+ * doubles on demand, as there. */
+SMOL_ATTN_API int smol_rope_table_create(smol_attn_ctx *ctx, int head_dim, float theta,
+                                         int rope_type, int capacity, smol_rope_table **out);
+SMOL_ATTN_API int smol_rope_table_ensure(smol_rope_table *rt, int required_pos);
+SMOL_ATTN_API int smol_rope_table_capacity(const smol_rope_table *rt);
+SMOL_ATTN_API int smol_rope_table_destroy(smol_rope_table *rt);
+/* host rows [pos0, pos0 + n_pos) of a table, same formula (no device needed) */
+SMOL_ATTN_API void smol_rope_fill_host(float *cos_out, float *sin_out, int pos0, int n_pos,
+                                       int head_dim, float theta, int rope_type);
+
+/* ---- KV cache -------------------------------------------------------------
+ * Device bf16 cache for n_layers x n_slots sequences (a slot is one sequence,
+ * e.g. one of a batch of decode streams). The reference keeps one fp32 cache
+ * per decoder context (qkn_ctx_t.kv_cache_k/v, qkn_decoder.h:99-103;
+ * kv_cache_init/grow/k_at/v_at, qkn_decoder.c:172-220). As there, the valid
+ * length is the caller's: attention calls take explicit positions, so a
+ * rewind (qwen_asr.c:1609 assigns kv_cache_len) is just passing a smaller
+ * position next time. Capacity grows by doubling with contents kept.
+ * Memory is zero-filled at creation and growth. */
+SMOL_ATTN_API int smol_kv_cache_create(smol_attn_ctx *ctx, int n_layers, int n_slots,
+                                       int n_kv_heads, int head_dim, int max_seq,
+                                       smol_kv_cache **out);
+SMOL_ATTN_API int smol_kv_cache_destroy(smol_kv_cache *kv);
+SMOL_ATTN_API int smol_kv_cache_capacity(const smol_kv_cache *kv);
+/* grow (doubling) so that at least required_pos positions fit */
+SMOL_ATTN_API int smol_kv_cache_reserve(smol_kv_cache *kv, int required_pos);
+/* write already-rotated rows [pos0, pos0 + n) of one layer/slot from
+ * [n][n_kv_heads * head_dim] arrays (dtype SMOL_ATTN_F32 or _BF16; host
+ * pointers when on_device == 0, else device pointers) */
+SMOL_ATTN_API int smol_kv_cache_write(smol_kv_cache *kv, int layer, int slot, int pos0, int n,
+                                      const void *k, const void *v, int dtype, int on_device);
+/* read rows back as bf16 bits [n][n_kv_heads * head_dim] (host pointers) */
+SMOL_ATTN_API int smol_kv_cache_read(smol_kv_cache *kv, int layer, int slot, int pos0, int n,
+                                     uint16_t *k_out, uint16_t *v_out);
+
+/* ---- attention on device pointers -----------------------------------------
+ * window > 0: sliding window (keys with pos - window < key <= pos,
+ * attention.c:176-273); cap > 0: score = cap * tanh(score / cap)
+ * (attention.c:281-462). scale is the caller's (1/sqrtf(head_dim) in the
+ * reference decoders, qkn_decoder.c:430, 620).
+ */
+
+/* Prefill / chunked prefill of one sequence (replaces qkn_decoder.c:493-528):
+ * rotates Q [seq_q][n_heads*hd] and the new K [seq_q][n_kv*hd] at positions
+ * pos0..pos0+seq_q-1 with `rope` (NULL: no RoPE), appends K/V to the cache at
+ * (layer, slot), and writes out [seq_q][n_heads*hd] = causal attention of the
+ * new rows over cache positions [0, pos0 + seq_q). pos0 > 0 is chunked
+ * prefill on top of an existing prefix. */
+SMOL_ATTN_API int smol_attn_prefill(smol_attn_ctx *ctx, smol_kv_cache *kv, int layer, int slot,
+                                    const smol_rope_table *rope, int pos0, int seq_q,
+                                    const void *q, const void *k_new, const void *v_new,
+                                    int dtype, int n_heads, float scale, int window, float cap,
+                                    float *out);
+
+/* Batched single-token decode (replaces qkn_decoder.c:647-677): for each of
+ * n_seq sequences i, rotates q[i] and k_new[i] at position pos[i], appends
+ * K/V at (layer, slots[i], pos[i]) and writes out[i] = attention of q[i] over
+ * positions [0, pos[i]] of that slot. slots/pos are host arrays. q, out:
+ * [n_seq][n_heads*hd]; k_new, v_new: [n_seq][n_kv*hd]. */
+SMOL_ATTN_API int smol_attn_decode(smol_attn_ctx *ctx, smol_kv_cache *kv, int layer,
+                                   const smol_rope_table *rope, int n_seq, const int *slots,
+                                   const int *pos, const void *q, const void *k_new,
+                                   const void *v_new, int dtype, int n_heads, float scale,
+                                   int window, float cap, float *out);
+
+/* Causal attention on flat device arrays, no cache and no RoPE: the device
+ * form of smol_causal_attention (attention.c:153-170). K, V: [seq_k][n_kv*hd]. */
+SMOL_ATTN_API int smol_attn_causal(smol_attn_ctx *ctx, const void *q, const void *k,
+                                   const void *v, int dtype, int seq_q, int seq_k, int n_heads,
+                                   int n_kv_heads, int head_dim, float scale, int q_offset,
+                                   int window, float cap, float *out);
+
+/* Windowed bidirectional attention on device arrays: the device form of
+ * smol_bidirectional_attention (attention.c:32-77). Q, K, V, out:
+ * [seq][n_heads*hd]; window_starts: host array of n_windows + 1 offsets
+ * (a batch of independent sequences is one window each). */
+SMOL_ATTN_API int smol_attn_bidirectional(smol_attn_ctx *ctx, const void *q, const void *k,
+                                          const void *v, int dtype, int seq, int n_heads,
+                                          int head_dim, float scale, const int *window_starts,
+                                          int n_windows, float *out);
+
+/* In-place RoPE on a device fp32 array [seq][n_heads*hd] whose row s uses
+ * table position positions[s] (host array): the device form of
+ * smol_apply_rope_{neox,interleaved} (rope.c:68-164). */
+SMOL_ATTN_API int smol_attn_apply_rope(smol_attn_ctx *ctx, const smol_rope_table *rope, float *x,
+                                       const int *positions, int seq, int n_heads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SMOL_ATTN_H */

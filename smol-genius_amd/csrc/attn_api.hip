@@ -1,0 +1,946 @@
+/*
+ * attn_api.hip - host side of libsmol_attn.so: the C ABI of include/smol_attn.h
+ * and include/smol_kernels_attn.h.
+ *
+ * Each attention call builds small descriptor tables on the host (which rows
+ * and keys each kernel block covers), copies them to the device through a
+ * ring of pinned buffers, and enqueues two kernels on the context's stream:
+ * k_prep (RoPE + cache append + fp16 staging) and k_attn_sk (split-K flash
+ * attention with an in-kernel merge). Nothing here computes attention on the
+ * host; without a GPU every entry point fails with SMOL_ATTN_ERR_NO_GPU.
+ */
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "../../include/smol_attn.h"
+#include "../../include/smol_kernels_attn.h"
+#include "attn_internal.h"
+
+extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t st);
+extern "C" int smol_launch_sk(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st);
+extern "C" int smol_launch_rope_apply(float *x, const float *cos_t, const float *sin_t,
+                                      const int *pos, int seq, int n_heads, int hd, int kind,
+                                      hipStream_t st);
+
+#define LOG2E_D 1.4426950408889634
+
+/* ------------------------------------------------------------------ errors */
+
+static thread_local char g_err[512];
+
+static int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                    \
+    do {                                                                                 \
+        hipError_t e_ = (expr);                                                          \
+        if (e_ != hipSuccess)                                                            \
+            return fail(SMOL_ATTN_ERR_DEVICE, "%s: %s", #expr, hipGetErrorString(e_));   \
+    } while (0)
+
+extern "C" const char *smol_attn_version(void) { return "smol_attn 0.1 gfx950"; }
+extern "C" const char *smol_attn_last_error(void) { return g_err; }
+
+extern "C" int smol_attn_device_count(void) {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0)
+        return fail(SMOL_ATTN_ERR_NO_GPU, "no HIP device: %s", hipGetErrorString(e));
+    return n;
+}
+
+static bool hd_supported(int hd) {
+    return hd == 64 || hd == 72 || hd == 80 || hd == 96 || hd == 128 || hd == 256;
+}
+
+/* ---------------------------------------------------------------- buffers */
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+/* grow a device buffer; contents are not kept. The stream is drained first
+ * because earlier kernels may still read the old allocation. */
+static int dev_reserve(DevBuf &b, size_t bytes, hipStream_t st, bool zero = false) {
+    if (bytes <= b.cap) return 0;
+    size_t want = std::max(bytes, b.cap + b.cap / 2);
+    want = (want + 4095) & ~(size_t)4095;
+    if (b.p) {
+        HIP_TRY(hipStreamSynchronize(st));
+        HIP_TRY(hipFree(b.p));
+        b.p = nullptr;
+        b.cap = 0;
+    }
+    HIP_TRY(hipMalloc(&b.p, want));
+    if (zero) HIP_TRY(hipMemsetAsync(b.p, 0, want, st));
+    b.cap = want;
+    return 0;
+}
+
+/* Ring of pinned host staging buffers for the per-call descriptor tables.
+ * A slot is reused only after the copy that last read it has completed. */
+struct PinnedSlot {
+    void *h = nullptr;
+    size_t cap = 0;
+    hipEvent_t ev = nullptr;
+    bool pending = false;
+};
+
+#define SMOL_RING 16
+
+struct smol_attn_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool own_stream = false;
+    PinnedSlot ring[SMOL_RING];
+    int ring_next = 0;
+    DevBuf desc;   /* device copy of the descriptor tables */
+    DevBuf qs, kf, vtf, part_o, part_ml, counters;
+    int cu_count = 256;
+};
+
+struct smol_rope_table {
+    smol_attn_ctx *ctx;
+    int hd, type, cap;
+    float theta;
+    float *cos_d = nullptr, *sin_d = nullptr;
+};
+
+struct smol_kv_cache {
+    smol_attn_ctx *ctx;
+    int n_layers, n_slots, n_kv, hd, cap;
+    uint16_t *k = nullptr, *vt = nullptr;
+};
+
+static int set_device(smol_attn_ctx *ctx) {
+    HIP_TRY(hipSetDevice(ctx->device));
+    return 0;
+}
+
+/* copy `bytes` of descriptor data to ctx->desc via the pinned ring */
+static int upload_desc(smol_attn_ctx *ctx, const void *host, size_t bytes) {
+    int rc = dev_reserve(ctx->desc, bytes, ctx->stream);
+    if (rc) return rc;
+    PinnedSlot &s = ctx->ring[ctx->ring_next];
+    ctx->ring_next = (ctx->ring_next + 1) % SMOL_RING;
+    if (s.pending) {
+        HIP_TRY(hipEventSynchronize(s.ev));
+        s.pending = false;
+    }
+    if (bytes > s.cap) {
+        if (s.h) HIP_TRY(hipHostFree(s.h));
+        s.h = nullptr;
+        size_t want = std::max(bytes, (size_t)65536);
+        HIP_TRY(hipHostMalloc(&s.h, want, hipHostMallocDefault));
+        s.cap = want;
+    }
+    if (!s.ev) HIP_TRY(hipEventCreateWithFlags(&s.ev, hipEventDisableTiming));
+    memcpy(s.h, host, bytes);
+    HIP_TRY(hipMemcpyAsync(ctx->desc.p, s.h, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipEventRecord(s.ev, ctx->stream));
+    s.pending = true;
+    return 0;
+}
+
+/* ------------------------------------------------------------------ context */
+
+extern "C" int smol_attn_ctx_create(int device, void *stream, smol_attn_ctx **out) {
+    if (!out) return fail(SMOL_ATTN_ERR_ARG, "out is NULL");
+    *out = nullptr;
+    int n = smol_attn_device_count();
+    if (n < 0) return n;
+    if (device < 0 || device >= n) return fail(SMOL_ATTN_ERR_ARG, "device %d of %d", device, n);
+    smol_attn_ctx *c = new smol_attn_ctx();
+    c->device = device;
+    hipError_t e = hipSetDevice(device);
+    if (e == hipSuccess) {
+        /* NULL is the device's null stream, ordered with other work on it */
+        c->stream = (hipStream_t)stream;
+    }
+    int cus = 0;
+    if (e == hipSuccess && hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
+        c->cu_count = cus;
+    if (e != hipSuccess) {
+        delete c;
+        return fail(SMOL_ATTN_ERR_DEVICE, "context: %s", hipGetErrorString(e));
+    }
+    *out = c;
+    return SMOL_ATTN_OK;
+}
+
+extern "C" int smol_attn_ctx_destroy(smol_attn_ctx *ctx) {
+    if (!ctx) return SMOL_ATTN_OK;
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    DevBuf *bufs[] = {&ctx->desc, &ctx->qs, &ctx->kf, &ctx->vtf, &ctx->part_o, &ctx->part_ml, &ctx->counters};
+    for (DevBuf *b : bufs)
+        if (b->p) hipFree(b->p);
+    for (auto &s : ctx->ring) {
+        if (s.h) hipHostFree(s.h);
+        if (s.ev) hipEventDestroy(s.ev);
+    }
+    if (ctx->own_stream) hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return SMOL_ATTN_OK;
+}
+
+extern "C" int smol_attn_ctx_synchronize(smol_attn_ctx *ctx) {
+    if (!ctx) return fail(SMOL_ATTN_ERR_ARG, "ctx is NULL");
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return SMOL_ATTN_OK;
+}
+
+extern "C" void *smol_attn_ctx_stream(smol_attn_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+/* --------------------------------------------------------------- RoPE table */
+
+/* qkn_decoder.c:261-311: inv_freq[d] = 1/powf(theta, 2d/hd); angle = (float)pos * inv_freq[d] */
+extern "C" void smol_rope_fill_host(float *cos_out, float *sin_out, int pos0, int n_pos, int hd,
+                                    float theta, int rope_type) {
+    const int half = hd / 2;
+    std::vector<float> inv(half > 0 ? half : 1);
+    for (int d = 0; d < half; d++) {
+        volatile float e = (float)(2 * d) / (float)hd;
+        inv[d] = 1.0f / powf(theta, e);
+    }
+    for (int r = 0; r < n_pos; r++) {
+        const float p = (float)(pos0 + r);
+        float *cr = cos_out + (size_t)r * hd, *sr = sin_out + (size_t)r * hd;
+        for (int d = 0; d < half; d++) {
+            volatile float a = p * inv[d];
+            const float c = cosf(a), s = sinf(a);
+            if (rope_type == SMOL_ROPE_INTERLEAVED) {
+                cr[2 * d] = c; cr[2 * d + 1] = c; sr[2 * d] = s; sr[2 * d + 1] = s;
+            } else {
+                cr[d] = c; cr[half + d] = c; sr[d] = s; sr[half + d] = s;
+            }
+        }
+    }
+}
+
+static int rope_upload(smol_rope_table *rt, int new_cap) {
+    smol_attn_ctx *ctx = rt->ctx;
+    std::vector<float> c((size_t)new_cap * rt->hd), s((size_t)new_cap * rt->hd);
+    smol_rope_fill_host(c.data(), s.data(), 0, new_cap, rt->hd, rt->theta, rt->type);
+    float *cd = nullptr, *sd = nullptr;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    HIP_TRY(hipMalloc(&cd, c.size() * sizeof(float)));
+    HIP_TRY(hipMalloc(&sd, s.size() * sizeof(float)));
+    HIP_TRY(hipMemcpy(cd, c.data(), c.size() * sizeof(float), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(sd, s.data(), s.size() * sizeof(float), hipMemcpyHostToDevice));
+    if (rt->cos_d) hipFree(rt->cos_d);
+    if (rt->sin_d) hipFree(rt->sin_d);
+    rt->cos_d = cd;
+    rt->sin_d = sd;
+    rt->cap = new_cap;
+    return 0;
+}
+
+extern "C" int smol_rope_table_create(smol_attn_ctx *ctx, int hd, float theta, int type, int cap,
+                                      smol_rope_table **out) {
+    if (!ctx || !out) return fail(SMOL_ATTN_ERR_ARG, "NULL argument");
+    *out = nullptr;
+    if (hd <= 0 || (hd & 1) || hd > 512) return fail(SMOL_ATTN_ERR_ARG, "head_dim %d", hd);
+    if (type != SMOL_ROPE_NEOX && type != SMOL_ROPE_INTERLEAVED)
+        return fail(SMOL_ATTN_ERR_ARG, "rope_type %d", type);
+    if (!(theta > 0.0f)) return fail(SMOL_ATTN_ERR_ARG, "theta must be > 0");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    smol_rope_table *rt = new smol_rope_table();
+    rt->ctx = ctx;
+    rt->hd = hd;
+    rt->type = type;
+    rt->theta = theta;
+    rt->cap = 0;
+    int c = 1024;
+    while (c < cap) c *= 2;
+    rc = rope_upload(rt, c);
+    if (rc) { delete rt; return rc; }
+    *out = rt;
+    return SMOL_ATTN_OK;
+}
+
+extern "C" int smol_rope_table_ensure(smol_rope_table *rt, int required_pos) {
+    if (!rt) return fail(SMOL_ATTN_ERR_ARG, "NULL table");
+    if (required_pos <= rt->cap) return SMOL_ATTN_OK;
+    int c = rt->cap > 0 ? rt->cap : 1024;
+    while (c < required_pos) c *= 2;
+    int rc = set_device(rt->ctx);
+    return rc ? rc : rope_upload(rt, c);
+}
+
+extern "C" int smol_rope_table_capacity(const smol_rope_table *rt) { return rt ? rt->cap : 0; }
+
+extern "C" int smol_rope_table_destroy(smol_rope_table *rt) {
+    if (!rt) return SMOL_ATTN_OK;
+    hipSetDevice(rt->ctx->device);
+    hipStreamSynchronize(rt->ctx->stream);
+    if (rt->cos_d) hipFree(rt->cos_d);
+    if (rt->sin_d) hipFree(rt->sin_d);
+    delete rt;
+    return SMOL_ATTN_OK;
+}
+
+/* ----------------------------------------------------------------- KV cache */
+
+static size_t kv_slot_elems(const smol_kv_cache *kv) { return (size_t)kv->n_kv * kv->cap * kv->hd; }
+static size_t kv_layer_elems(const smol_kv_cache *kv) { return kv_slot_elems(kv) * kv->n_slots; }
+
+extern "C" int smol_kv_cache_create(smol_attn_ctx *ctx, int n_layers, int n_slots, int n_kv, int hd,
+                                    int max_seq, smol_kv_cache **out) {
+    if (!ctx || !out) return fail(SMOL_ATTN_ERR_ARG, "NULL argument");
+    *out = nullptr;
+    if (n_layers <= 0 || n_slots <= 0 || n_kv <= 0 || max_seq <= 0)
+        return fail(SMOL_ATTN_ERR_ARG, "cache shape %d/%d/%d/%d", n_layers, n_slots, n_kv, max_seq);
+    if (!hd_supported(hd)) return fail(SMOL_ATTN_ERR_UNSUPPORTED, "head_dim %d", hd);
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    smol_kv_cache *kv = new smol_kv_cache();
+    kv->ctx = ctx;
+    kv->n_layers = n_layers;
+    kv->n_slots = n_slots;
+    kv->n_kv = n_kv;
+    kv->hd = hd;
+    kv->cap = (max_seq + 63) & ~63;
+    size_t bytes = kv_layer_elems(kv) * n_layers * sizeof(uint16_t);
+    hipError_t e = hipMalloc(&kv->k, bytes);
+    if (e == hipSuccess) e = hipMalloc(&kv->vt, bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(kv->k, 0, bytes, ctx->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(kv->vt, 0, bytes, ctx->stream);
+    if (e != hipSuccess) {
+        if (kv->k) hipFree(kv->k);
+        if (kv->vt) hipFree(kv->vt);
+        delete kv;
+        return fail(e == hipErrorOutOfMemory ? SMOL_ATTN_ERR_NOMEM : SMOL_ATTN_ERR_DEVICE,
+                    "kv cache (%zu bytes): %s", bytes, hipGetErrorString(e));
+    }
+    *out = kv;
+    return SMOL_ATTN_OK;
+}
+
+extern "C" int smol_kv_cache_destroy(smol_kv_cache *kv) {
+    if (!kv) return SMOL_ATTN_OK;
+    hipSetDevice(kv->ctx->device);
+    hipStreamSynchronize(kv->ctx->stream);
+    hipFree(kv->k);
+    hipFree(kv->vt);
+    delete kv;
+    return SMOL_ATTN_OK;
+}
+
+extern "C" int smol_kv_cache_capacity(const smol_kv_cache *kv) { return kv ? kv->cap : 0; }
+
+/* kv_cache_grow (qkn_decoder.c:183-210): double until it fits, keep contents */
+extern "C" int smol_kv_cache_reserve(smol_kv_cache *kv, int required) {
+    if (!kv) return fail(SMOL_ATTN_ERR_ARG, "NULL cache");
+    if (required <= kv->cap) return SMOL_ATTN_OK;
+    smol_attn_ctx *ctx = kv->ctx;
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    int nc = kv->cap;
+    while (nc < required) nc *= 2;
+    smol_kv_cache nkv = *kv;
+    nkv.cap = nc;
+    size_t bytes = kv_layer_elems(&nkv) * kv->n_layers * sizeof(uint16_t);
+    uint16_t *nk = nullptr, *nvt = nullptr;
+    hipError_t e = hipMalloc(&nk, bytes);
+    if (e == hipSuccess) e = hipMalloc(&nvt, bytes);
+    if (e != hipSuccess) {
+        if (nk) hipFree(nk);
+        return fail(SMOL_ATTN_ERR_NOMEM, "kv cache grow to %d: %s", nc, hipGetErrorString(e));
+    }
+    HIP_TRY(hipMemsetAsync(nk, 0, bytes, ctx->stream));
+    HIP_TRY(hipMemsetAsync(nvt, 0, bytes, ctx->stream));
+    const int hd = kv->hd;
+    const size_t n_blocks = (size_t)kv->n_layers * kv->n_slots * kv->n_kv;
+    for (size_t blk = 0; blk < n_blocks; blk++) {
+        /* K: [cap][hd] contiguous per (layer, slot, head) */
+        HIP_TRY(hipMemcpyAsync(nk + blk * nc * hd, kv->k + blk * kv->cap * hd,
+                               (size_t)kv->cap * hd * sizeof(uint16_t), hipMemcpyDeviceToDevice, ctx->stream));
+        /* V^T: [hd][cap] rows of cap -> rows of nc */
+        HIP_TRY(hipMemcpy2DAsync(nvt + blk * nc * hd, (size_t)nc * sizeof(uint16_t),
+                                 kv->vt + blk * kv->cap * hd, (size_t)kv->cap * sizeof(uint16_t),
+                                 (size_t)kv->cap * sizeof(uint16_t), hd, hipMemcpyDeviceToDevice, ctx->stream));
+    }
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    hipFree(kv->k);
+    hipFree(kv->vt);
+    kv->k = nk;
+    kv->vt = nvt;
+    kv->cap = nc;
+    return SMOL_ATTN_OK;
+}
+
+/* ------------------------------------------------------------ the dispatcher */
+
+struct Plan {
+    std::vector<PrepBatch> pb;
+    std::vector<PrepBlock> pblk;
+    std::vector<SkBatch> sb;
+    std::vector<SkItem> items;
+    int n_groups = 0;
+    int q_rows = 0;      /* Q scratch rows per KV head */
+    int fresh_rows = 0;  /* fresh rows per KV head */
+};
+
+struct CallShape {
+    const void *q, *k, *v;
+    int dtype;
+    int Hq, Hkv, hd;
+    long long q_stride, kv_stride;
+    float scale, cap;
+    int window;
+    const smol_rope_table *rope;
+    int rope_q, rope_k;
+    smol_kv_cache *kv;
+    int layer;
+    float *out;
+};
+
+static int choose_nt(int hd, int max_rows) {
+    int nt = max_rows <= 16 ? 1 : (max_rows <= 32 ? 2 : 4);
+    if (hd > 128 && nt > 1) nt = 1;
+    if (hd > 64 && nt > 2) nt = 2;
+    return nt;
+}
+
+/* Row tiles x key splits for every batch. The split size is chosen so the
+ * whole call has a few waves per compute unit. */
+static void plan_items(Plan &pl, int Hkv, int G, int window, int nt, int cu_count) {
+    const int rows_per = 16 * nt;
+    struct Tile { int batch, row0, lo, hi; };
+    std::vector<Tile> tiles;
+    long long total_slabs = 0;
+    for (int bi = 0; bi < (int)pl.sb.size(); bi++) {
+        const SkBatch &b = pl.sb[bi];
+        for (int r0 = 0; r0 < b.n_rows; r0 += rows_per) {
+            const int r1 = std::min(r0 + rows_per, b.n_rows) - 1;
+            int lo = b.key_lo, hi = b.key_hi;
+            if (b.causal) {
+                hi = std::min(hi, b.q_pos0 + r1 / G + 1);
+                if (window > 0) lo = std::max(lo, b.q_pos0 + r0 / G - window + 1);
+            }
+            lo = std::max(lo, 0) & ~(SMOL_SLAB - 1);
+            if (hi < lo) hi = lo;
+            tiles.push_back({bi, r0, lo, hi});
+            total_slabs += (hi - lo + SMOL_SLAB - 1) / SMOL_SLAB;
+        }
+    }
+    const long long target_items = (long long)cu_count * 4;
+    long long per = (total_slabs * Hkv + target_items - 1) / std::max(1LL, target_items);
+    int slabs_per_item = (int)std::max(2LL, per);
+    int group = 0;
+    for (const Tile &t : tiles) {
+        const int n_slabs = (t.hi - t.lo + SMOL_SLAB - 1) / SMOL_SLAB;
+        const int n_split = std::max(1, (n_slabs + slabs_per_item - 1) / slabs_per_item);
+        const int per_split = (n_slabs + n_split - 1) / std::max(1, n_split);
+        int made = 0;
+        std::vector<SkItem> tmp;
+        for (int sp = 0; sp < n_split; sp++) {
+            int kb = t.lo + sp * per_split * SMOL_SLAB;
+            int ke = std::min(t.hi, kb + per_split * SMOL_SLAB);
+            if (sp > 0 && kb >= t.hi) break;
+            if (ke < kb) ke = kb;
+            tmp.push_back({t.batch, t.row0, kb, ke, group, 0, made++, 0});
+        }
+        for (SkItem &it : tmp) {
+            it.n_split = made;
+            pl.items.push_back(it);
+        }
+        group++;
+    }
+    pl.n_groups = group;
+}
+
+static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
+    const int hd = cs.hd, hdp = (hd + 31) & ~31;
+    const int G = cs.Hq / cs.Hkv;
+    int max_rows = 0;
+    for (auto &b : pl.sb) max_rows = std::max(max_rows, b.n_rows);
+    const int nt = choose_nt(hd, max_rows);
+    plan_items(pl, cs.Hkv, G, cs.window, nt, ctx->cu_count);
+    const int rows_per = 16 * nt;
+
+    /* workspace */
+    int rc;
+    const size_t fcap = (size_t)std::max(pl.fresh_rows, SMOL_SLAB);
+    if ((rc = dev_reserve(ctx->qs, (size_t)cs.Hkv * std::max(pl.q_rows, 1) * hdp * 2, ctx->stream))) return rc;
+    if ((rc = dev_reserve(ctx->kf, (size_t)cs.Hkv * fcap * hd * 2, ctx->stream))) return rc;
+    if ((rc = dev_reserve(ctx->vtf, (size_t)cs.Hkv * fcap * hd * 2, ctx->stream))) return rc;
+    const size_t n_items = pl.items.size();
+    if ((rc = dev_reserve(ctx->part_o, std::max<size_t>(1, n_items) * cs.Hkv * rows_per * hd * 4, ctx->stream))) return rc;
+    if ((rc = dev_reserve(ctx->part_ml, std::max<size_t>(1, n_items) * cs.Hkv * rows_per * 2 * 4, ctx->stream))) return rc;
+    if ((rc = dev_reserve(ctx->counters, (size_t)std::max(1, pl.n_groups) * cs.Hkv * 4, ctx->stream, true))) return rc;
+
+    /* descriptor tables in one upload */
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t o_pb = 0;
+    const size_t o_pblk = al(o_pb + pl.pb.size() * sizeof(PrepBatch));
+    const size_t o_sb = al(o_pblk + pl.pblk.size() * sizeof(PrepBlock));
+    const size_t o_it = al(o_sb + pl.sb.size() * sizeof(SkBatch));
+    const size_t total = al(o_it + pl.items.size() * sizeof(SkItem));
+    std::vector<unsigned char> host(total);
+    memcpy(host.data() + o_pb, pl.pb.data(), pl.pb.size() * sizeof(PrepBatch));
+    memcpy(host.data() + o_pblk, pl.pblk.data(), pl.pblk.size() * sizeof(PrepBlock));
+    memcpy(host.data() + o_sb, pl.sb.data(), pl.sb.size() * sizeof(SkBatch));
+    memcpy(host.data() + o_it, pl.items.data(), pl.items.size() * sizeof(SkItem));
+    if ((rc = upload_desc(ctx, host.data(), total))) return rc;
+    unsigned char *dd = (unsigned char *)ctx->desc.p;
+
+    const smol_kv_cache *kv = cs.kv;
+    uint16_t *kc = nullptr, *vtc = nullptr;
+    long long slot_stride = 0;
+    int cap = 0;
+    if (kv) {
+        kc = kv->k + (size_t)cs.layer * kv_layer_elems(kv);
+        vtc = kv->vt + (size_t)cs.layer * kv_layer_elems(kv);
+        slot_stride = (long long)kv_slot_elems(kv);
+        cap = kv->cap;
+    }
+
+    PrepParams pp;
+    memset(&pp, 0, sizeof(pp));
+    pp.q = cs.q; pp.q_dtype = cs.dtype; pp.q_stride = cs.q_stride;
+    pp.k = cs.k; pp.v = cs.v; pp.kv_dtype = cs.dtype; pp.kv_stride = cs.kv_stride;
+    if (cs.rope) {
+        pp.rope_cos = cs.rope->cos_d;
+        pp.rope_sin = cs.rope->sin_d;
+        pp.rope_kind = cs.rope->type == SMOL_ROPE_INTERLEAVED ? SMOL_ROPE_INTERLEAVED_K : SMOL_ROPE_NEOX_K;
+    } else {
+        pp.rope_kind = SMOL_ROPE_OFF;
+    }
+    pp.rope_q = cs.rope_q;
+    pp.rope_k = cs.rope_k;
+    pp.qscale = (float)(cs.scale * LOG2E_D);
+    pp.Hq = cs.Hq; pp.Hkv = cs.Hkv; pp.G = G; pp.hd = hd; pp.hdp = hdp;
+    pp.qs = (_Float16 *)ctx->qs.p;
+    pp.qs_head_stride = (long long)std::max(pl.q_rows, 1) * hdp;
+    pp.kc = kc; pp.vtc = vtc; pp.c_slot_stride = slot_stride; pp.cap = cap;
+    pp.kf = (_Float16 *)ctx->kf.p; pp.vtf = (_Float16 *)ctx->vtf.p; pp.fcap = (int)fcap;
+    pp.batches = (const PrepBatch *)(dd + o_pb);
+    pp.blocks = (const PrepBlock *)(dd + o_pblk);
+    if ((rc = smol_launch_prep(&pp, (int)pl.pblk.size(), ctx->stream)))
+        return fail(SMOL_ATTN_ERR_DEVICE, "k_prep launch: %s", hipGetErrorString(hipGetLastError()));
+
+    SkParams sp;
+    memset(&sp, 0, sizeof(sp));
+    sp.qs = (const _Float16 *)ctx->qs.p;
+    sp.qs_head_stride = pp.qs_head_stride;
+    sp.kc = kc; sp.vtc = vtc; sp.c_slot_stride = slot_stride; sp.cap = cap;
+    sp.kf = (const _Float16 *)ctx->kf.p; sp.vtf = (const _Float16 *)ctx->vtf.p; sp.fcap = (int)fcap;
+    sp.out = cs.out;
+    sp.Hq = cs.Hq; sp.Hkv = cs.Hkv; sp.G = G;
+    sp.window = cs.window;
+    sp.cap2 = cs.cap > 0.0f ? (float)(cs.cap * LOG2E_D) : 0.0f;
+    sp.batches = (const SkBatch *)(dd + o_sb);
+    sp.items = (const SkItem *)(dd + o_it);
+    sp.part_o = (float *)ctx->part_o.p;
+    sp.part_ml = (float *)ctx->part_ml.p;
+    sp.counters = (int *)ctx->counters.p;
+    if ((rc = smol_launch_sk(&sp, hd, (int)n_items, nt, ctx->stream)))
+        return fail(rc == -1 ? SMOL_ATTN_ERR_UNSUPPORTED : SMOL_ATTN_ERR_DEVICE,
+                    "k_attn_sk launch (hd %d): %s", hd, hipGetErrorString(hipGetLastError()));
+    return SMOL_ATTN_OK;
+}
+
+static void add_q_blocks(Plan &pl, int batch, int n_q) {
+    const int per = 8;
+    for (int t = 0; t < n_q; t += per) pl.pblk.push_back({batch, 1, t, std::min(per, n_q - t)});
+}
+
+static void add_fresh_blocks(Plan &pl, int batch, int n_fresh) {
+    for (int s = 0; s < n_fresh / SMOL_SLAB; s++) pl.pblk.push_back({batch, 0, s, 0});
+}
+
+static int check_common(smol_attn_ctx *ctx, int dtype, int Hq, int Hkv, int hd, const void *q,
+                        float *out) {
+    if (!ctx) return fail(SMOL_ATTN_ERR_ARG, "ctx is NULL");
+    if (dtype != SMOL_ATTN_F32 && dtype != SMOL_ATTN_BF16) return fail(SMOL_ATTN_ERR_ARG, "dtype %d", dtype);
+    if (Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0)
+        return fail(SMOL_ATTN_ERR_ARG, "n_heads %d not a multiple of n_kv_heads %d", Hq, Hkv);
+    if (!hd_supported(hd)) return fail(SMOL_ATTN_ERR_UNSUPPORTED, "head_dim %d", hd);
+    if (!q || !out) return fail(SMOL_ATTN_ERR_ARG, "NULL tensor");
+    return set_device(ctx);
+}
+
+static int check_rope(const smol_rope_table *rope, int hd, int need) {
+    if (!rope) return 0;
+    if (rope->hd != hd) return fail(SMOL_ATTN_ERR_ARG, "rope table head_dim %d != %d", rope->hd, hd);
+    return smol_rope_table_ensure(const_cast<smol_rope_table *>(rope), need);
+}
+
+extern "C" int smol_attn_prefill(smol_attn_ctx *ctx, smol_kv_cache *kv, int layer, int slot,
+                                 const smol_rope_table *rope, int pos0, int seq_q, const void *q,
+                                 const void *k_new, const void *v_new, int dtype, int n_heads,
+                                 float scale, int window, float cap, float *out) {
+    if (!kv) return fail(SMOL_ATTN_ERR_ARG, "cache is NULL");
+    int rc = check_common(ctx, dtype, n_heads, kv->n_kv, kv->hd, q, out);
+    if (rc) return rc;
+    if (kv->ctx != ctx) return fail(SMOL_ATTN_ERR_ARG, "cache belongs to another context");
+    if (layer < 0 || layer >= kv->n_layers || slot < 0 || slot >= kv->n_slots)
+        return fail(SMOL_ATTN_ERR_ARG, "layer %d / slot %d out of range", layer, slot);
+    if (pos0 < 0 || seq_q <= 0 || !k_new || !v_new) return fail(SMOL_ATTN_ERR_ARG, "pos0 %d seq_q %d", pos0, seq_q);
+    if ((rc = smol_kv_cache_reserve(kv, pos0 + seq_q))) return rc;
+    if ((rc = check_rope(rope, kv->hd, pos0 + seq_q))) return rc;
+    const int Hkv = kv->n_kv, G = n_heads / Hkv, hd = kv->hd;
+    Plan pl;
+    const int f0 = pos0 & ~(SMOL_SLAB - 1);
+    const int nf = ((pos0 + seq_q + SMOL_SLAB - 1) & ~(SMOL_SLAB - 1)) - f0;
+    pl.pb.push_back({0, seq_q, 0, pos0, 0, seq_q, pos0, f0, nf, 0, slot, 0});
+    add_fresh_blocks(pl, 0, nf);
+    add_q_blocks(pl, 0, seq_q);
+    pl.sb.push_back({seq_q * G, 0, 0, pos0, 0, pos0 + seq_q, 1, f0, 0, slot, 0, 0});
+    pl.q_rows = seq_q * G;
+    pl.fresh_rows = nf;
+    CallShape cs{q, k_new, v_new, dtype, n_heads, Hkv, hd, (long long)n_heads * hd,
+                 (long long)Hkv * hd, scale, cap, window, rope, 1, 1, kv, layer, out};
+    return run_plan(ctx, pl, cs);
+}
+
+extern "C" int smol_attn_decode(smol_attn_ctx *ctx, smol_kv_cache *kv, int layer,
+                                const smol_rope_table *rope, int n_seq, const int *slots,
+                                const int *pos, const void *q, const void *k_new, const void *v_new,
+                                int dtype, int n_heads, float scale, int window, float cap,
+                                float *out) {
+    if (!kv) return fail(SMOL_ATTN_ERR_ARG, "cache is NULL");
+    int rc = check_common(ctx, dtype, n_heads, kv->n_kv, kv->hd, q, out);
+    if (rc) return rc;
+    if (kv->ctx != ctx) return fail(SMOL_ATTN_ERR_ARG, "cache belongs to another context");
+    if (layer < 0 || layer >= kv->n_layers) return fail(SMOL_ATTN_ERR_ARG, "layer %d out of range", layer);
+    if (n_seq <= 0 || !slots || !pos || !k_new || !v_new) return fail(SMOL_ATTN_ERR_ARG, "bad decode batch");
+    int max_pos = 0;
+    std::vector<char> seen(kv->n_slots, 0);
+    for (int i = 0; i < n_seq; i++) {
+        if (slots[i] < 0 || slots[i] >= kv->n_slots) return fail(SMOL_ATTN_ERR_ARG, "slot %d out of range", slots[i]);
+        if (seen[slots[i]]) return fail(SMOL_ATTN_ERR_ARG, "slot %d appears twice", slots[i]);
+        seen[slots[i]] = 1;
+        if (pos[i] < 0) return fail(SMOL_ATTN_ERR_ARG, "pos %d", pos[i]);
+        max_pos = std::max(max_pos, pos[i]);
+    }
+    if ((rc = smol_kv_cache_reserve(kv, max_pos + 1))) return rc;
+    if ((rc = check_rope(rope, kv->hd, max_pos + 1))) return rc;
+    const int Hkv = kv->n_kv, G = n_heads / Hkv, hd = kv->hd;
+    Plan pl;
+    for (int i = 0; i < n_seq; i++) {
+        /* sequence i: Q token i at position pos[i], one fresh slab holding pos[i] */
+        const int f0 = pos[i] & ~(SMOL_SLAB - 1);
+        pl.pb.push_back({i, 1, i * G, pos[i], i, 1, pos[i], f0, SMOL_SLAB, i * SMOL_SLAB, slots[i], 0});
+        add_fresh_blocks(pl, i, SMOL_SLAB);
+        add_q_blocks(pl, i, 1);
+        pl.sb.push_back({G, i * G, i, pos[i], 0, pos[i] + 1, 1, f0, i * SMOL_SLAB, slots[i], 0, 0});
+    }
+    pl.q_rows = n_seq * G;
+    pl.fresh_rows = n_seq * SMOL_SLAB;
+    CallShape cs{q, k_new, v_new, dtype, n_heads, Hkv, hd, (long long)n_heads * hd,
+                 (long long)Hkv * hd, scale, cap, window, rope, 1, 1, kv, layer, out};
+    return run_plan(ctx, pl, cs);
+}
+
+extern "C" int smol_attn_causal(smol_attn_ctx *ctx, const void *q, const void *k, const void *v,
+                                int dtype, int seq_q, int seq_k, int n_heads, int n_kv_heads,
+                                int hd, float scale, int q_offset, int window, float cap, float *out) {
+    int rc = check_common(ctx, dtype, n_heads, n_kv_heads, hd, q, out);
+    if (rc) return rc;
+    if (seq_q <= 0 || seq_k < 0) return fail(SMOL_ATTN_ERR_ARG, "seq_q %d seq_k %d", seq_q, seq_k);
+    if (seq_k > 0 && (!k || !v)) return fail(SMOL_ATTN_ERR_ARG, "NULL K/V");
+    const int G = n_heads / n_kv_heads;
+    Plan pl;
+    const int nf = (seq_k + SMOL_SLAB - 1) & ~(SMOL_SLAB - 1);
+    pl.pb.push_back({0, seq_q, 0, 0, 0, seq_k, 0, 0, nf, 0, -1, 0});
+    add_fresh_blocks(pl, 0, nf);
+    add_q_blocks(pl, 0, seq_q);
+    pl.sb.push_back({seq_q * G, 0, 0, q_offset, 0, seq_k, 1, 0, 0, -1, 0, 0});
+    pl.q_rows = seq_q * G;
+    pl.fresh_rows = nf;
+    CallShape cs{q, k, v, dtype, n_heads, n_kv_heads, hd, (long long)n_heads * hd,
+                 (long long)n_kv_heads * hd, scale, cap, window, nullptr, 0, 0, nullptr, 0, out};
+    return run_plan(ctx, pl, cs);
+}
+
+extern "C" int smol_attn_bidirectional(smol_attn_ctx *ctx, const void *q, const void *k,
+                                       const void *v, int dtype, int seq, int n_heads, int hd,
+                                       float scale, const int *ws, int n_windows, float *out) {
+    int rc = check_common(ctx, dtype, n_heads, n_heads, hd, q, out);
+    if (rc) return rc;
+    if (!ws || n_windows <= 0 || !k || !v) return fail(SMOL_ATTN_ERR_ARG, "bad windows");
+    for (int w = 0; w < n_windows; w++)
+        if (ws[w] < 0 || ws[w + 1] < ws[w] || ws[w + 1] > seq)
+            return fail(SMOL_ATTN_ERR_ARG, "window %d = [%d, %d) outside [0, %d)", w, ws[w], ws[w + 1], seq);
+    Plan pl;
+    const int nf = (seq + SMOL_SLAB - 1) & ~(SMOL_SLAB - 1);
+    pl.pb.push_back({0, seq, 0, 0, 0, seq, 0, 0, nf, 0, -1, 0});
+    add_fresh_blocks(pl, 0, nf);
+    add_q_blocks(pl, 0, seq);
+    for (int w = 0; w < n_windows; w++) {
+        const int a = ws[w], b = ws[w + 1];
+        if (b <= a) continue;
+        pl.sb.push_back({b - a, a, a, 0, a, b, 0, 0, 0, -1, 0, 0});
+    }
+    pl.q_rows = seq;
+    pl.fresh_rows = nf;
+    CallShape cs{q, k, v, dtype, n_heads, n_heads, hd, (long long)n_heads * hd,
+                 (long long)n_heads * hd, scale, 0.0f, 0, nullptr, 0, 0, nullptr, 0, out};
+    return run_plan(ctx, pl, cs);
+}
+
+extern "C" int smol_kv_cache_write(smol_kv_cache *kv, int layer, int slot, int pos0, int n,
+                                   const void *k, const void *v, int dtype, int on_device) {
+    if (!kv || !k || !v) return fail(SMOL_ATTN_ERR_ARG, "NULL argument");
+    smol_attn_ctx *ctx = kv->ctx;
+    if (layer < 0 || layer >= kv->n_layers || slot < 0 || slot >= kv->n_slots || pos0 < 0 || n <= 0)
+        return fail(SMOL_ATTN_ERR_ARG, "layer %d slot %d pos0 %d n %d", layer, slot, pos0, n);
+    if (dtype != SMOL_ATTN_F32 && dtype != SMOL_ATTN_BF16) return fail(SMOL_ATTN_ERR_ARG, "dtype %d", dtype);
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    if ((rc = smol_kv_cache_reserve(kv, pos0 + n))) return rc;
+    const size_t row_bytes = (size_t)kv->n_kv * kv->hd * (dtype == SMOL_ATTN_BF16 ? 2 : 4);
+    void *kd = (void *)k, *vd = (void *)v;
+    if (!on_device) {
+        HIP_TRY(hipMalloc(&kd, row_bytes * n));
+        HIP_TRY(hipMalloc(&vd, row_bytes * n));
+        HIP_TRY(hipMemcpy(kd, k, row_bytes * n, hipMemcpyHostToDevice));
+        HIP_TRY(hipMemcpy(vd, v, row_bytes * n, hipMemcpyHostToDevice));
+    }
+    Plan pl;
+    const int f0 = pos0 & ~(SMOL_SLAB - 1);
+    const int nf = ((pos0 + n + SMOL_SLAB - 1) & ~(SMOL_SLAB - 1)) - f0;
+    pl.pb.push_back({0, 0, 0, 0, 0, n, pos0, f0, nf, 0, slot, 0});
+    add_fresh_blocks(pl, 0, nf);
+    pl.fresh_rows = nf;
+    const int hd = kv->hd;
+    const size_t fcap = (size_t)nf;
+    if ((rc = dev_reserve(ctx->kf, (size_t)kv->n_kv * fcap * hd * 2, ctx->stream))) return rc;
+    if ((rc = dev_reserve(ctx->vtf, (size_t)kv->n_kv * fcap * hd * 2, ctx->stream))) return rc;
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t o_blk = al(sizeof(PrepBatch));
+    std::vector<unsigned char> host(al(o_blk + pl.pblk.size() * sizeof(PrepBlock)));
+    memcpy(host.data(), pl.pb.data(), sizeof(PrepBatch));
+    memcpy(host.data() + o_blk, pl.pblk.data(), pl.pblk.size() * sizeof(PrepBlock));
+    if ((rc = upload_desc(ctx, host.data(), host.size()))) return rc;
+    PrepParams pp;
+    memset(&pp, 0, sizeof(pp));
+    pp.k = kd; pp.v = vd; pp.kv_dtype = dtype; pp.kv_stride = (long long)kv->n_kv * hd;
+    pp.rope_kind = SMOL_ROPE_OFF;
+    pp.Hq = kv->n_kv; pp.Hkv = kv->n_kv; pp.G = 1; pp.hd = hd; pp.hdp = (hd + 31) & ~31;
+    pp.kc = kv->k + (size_t)layer * kv_layer_elems(kv);
+    pp.vtc = kv->vt + (size_t)layer * kv_layer_elems(kv);
+    pp.c_slot_stride = (long long)kv_slot_elems(kv);
+    pp.cap = kv->cap;
+    pp.kf = (_Float16 *)ctx->kf.p; pp.vtf = (_Float16 *)ctx->vtf.p; pp.fcap = (int)fcap;
+    pp.batches = (const PrepBatch *)ctx->desc.p;
+    pp.blocks = (const PrepBlock *)((unsigned char *)ctx->desc.p + o_blk);
+    rc = smol_launch_prep(&pp, (int)pl.pblk.size(), ctx->stream);
+    if (!on_device) {
+        hipStreamSynchronize(ctx->stream);
+        hipFree(kd);
+        hipFree(vd);
+    }
+    if (rc) return fail(SMOL_ATTN_ERR_DEVICE, "cache write: %s", hipGetErrorString(hipGetLastError()));
+    return SMOL_ATTN_OK;
+}
+
+extern "C" int smol_kv_cache_read(smol_kv_cache *kv, int layer, int slot, int pos0, int n,
+                                  uint16_t *k_out, uint16_t *v_out) {
+    if (!kv || !k_out || !v_out) return fail(SMOL_ATTN_ERR_ARG, "NULL argument");
+    if (layer < 0 || layer >= kv->n_layers || slot < 0 || slot >= kv->n_slots || pos0 < 0 || n <= 0 ||
+        pos0 + n > kv->cap)
+        return fail(SMOL_ATTN_ERR_ARG, "layer %d slot %d rows [%d, %d) cap %d", layer, slot, pos0, pos0 + n, kv->cap);
+    int rc = set_device(kv->ctx);
+    if (rc) return rc;
+    HIP_TRY(hipStreamSynchronize(kv->ctx->stream));
+    const int hd = kv->hd, H = kv->n_kv;
+    std::vector<uint16_t> kt((size_t)n * hd), vt((size_t)hd * n);
+    for (int g = 0; g < H; g++) {
+        const size_t base = (size_t)layer * kv_layer_elems(kv) + (size_t)slot * kv_slot_elems(kv) + (size_t)g * kv->cap * hd;
+        HIP_TRY(hipMemcpy(kt.data(), kv->k + base + (size_t)pos0 * hd, kt.size() * 2, hipMemcpyDeviceToHost));
+        HIP_TRY(hipMemcpy2D(vt.data(), (size_t)n * 2, kv->vt + base + pos0, (size_t)kv->cap * 2, (size_t)n * 2, hd,
+                            hipMemcpyDeviceToHost));
+        for (int r = 0; r < n; r++)
+            for (int d = 0; d < hd; d++) {
+                k_out[((size_t)r * H + g) * hd + d] = kt[(size_t)r * hd + d];
+                v_out[((size_t)r * H + g) * hd + d] = vt[(size_t)d * n + r];
+            }
+    }
+    return SMOL_ATTN_OK;
+}
+
+extern "C" int smol_attn_apply_rope(smol_attn_ctx *ctx, const smol_rope_table *rope, float *x,
+                                    const int *positions, int seq, int n_heads) {
+    if (!ctx || !rope || !x || !positions || seq <= 0 || n_heads <= 0) return fail(SMOL_ATTN_ERR_ARG, "bad arguments");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    int mx = 0;
+    for (int s = 0; s < seq; s++) {
+        if (positions[s] < 0) return fail(SMOL_ATTN_ERR_ARG, "position %d", positions[s]);
+        mx = std::max(mx, positions[s]);
+    }
+    if ((rc = smol_rope_table_ensure(const_cast<smol_rope_table *>(rope), mx + 1))) return rc;
+    if ((rc = upload_desc(ctx, positions, (size_t)seq * sizeof(int)))) return rc;
+    if (smol_launch_rope_apply(x, rope->cos_d, rope->sin_d, (const int *)ctx->desc.p, seq, n_heads, rope->hd,
+                               rope->type == SMOL_ROPE_INTERLEAVED ? SMOL_ROPE_INTERLEAVED_K : SMOL_ROPE_NEOX_K,
+                               ctx->stream))
+        return fail(SMOL_ATTN_ERR_DEVICE, "rope launch: %s", hipGetErrorString(hipGetLastError()));
+    return SMOL_ATTN_OK;
+}
+
+/* ============================================ reference-signature drop-ins */
+
+namespace {
+
+struct Legacy {
+    smol_attn_ctx *ctx = nullptr;
+    DevBuf q, k, v, out, cs;
+    ~Legacy() {
+        if (!ctx) return;
+        DevBuf *bs[] = {&q, &k, &v, &out, &cs};
+        for (DevBuf *b : bs)
+            if (b->p) hipFree(b->p);
+        smol_attn_ctx_destroy(ctx);
+    }
+};
+
+thread_local Legacy g_legacy;
+
+[[noreturn]] void legacy_abort(const char *fn) {
+    fprintf(stderr, "smol_attn: %s failed on the GPU: %s\n", fn, smol_attn_last_error());
+    abort();
+}
+
+smol_attn_ctx *legacy_ctx(const char *fn) {
+    if (!g_legacy.ctx && smol_attn_ctx_create(0, nullptr, &g_legacy.ctx) != SMOL_ATTN_OK) legacy_abort(fn);
+    return g_legacy.ctx;
+}
+
+void legacy_upload(const char *fn, DevBuf &b, const void *h, size_t bytes) {
+    smol_attn_ctx *ctx = legacy_ctx(fn);
+    if (dev_reserve(b, std::max<size_t>(bytes, 4), ctx->stream)) legacy_abort(fn);
+    if (bytes && hipMemcpyAsync(b.p, h, bytes, hipMemcpyHostToDevice, ctx->stream) != hipSuccess) legacy_abort(fn);
+}
+
+void legacy_download(const char *fn, void *h, const DevBuf &b, size_t bytes) {
+    smol_attn_ctx *ctx = legacy_ctx(fn);
+    if (bytes && hipMemcpyAsync(h, b.p, bytes, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess) legacy_abort(fn);
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess) legacy_abort(fn);
+}
+
+void legacy_causal(const char *fn, float *out, const float *Q, const float *K, const float *V, int seq_q,
+                   int seq_k, int Hq, int Hkv, int hd, float scale, int q_offset, int window, float cap) {
+    if (seq_q <= 0) return;
+    smol_attn_ctx *ctx = legacy_ctx(fn);
+    const size_t qb = (size_t)seq_q * Hq * hd * 4, kb = (size_t)std::max(seq_k, 0) * Hkv * hd * 4;
+    legacy_upload(fn, g_legacy.q, Q, qb);
+    legacy_upload(fn, g_legacy.k, K, kb);
+    legacy_upload(fn, g_legacy.v, V, kb);
+    if (dev_reserve(g_legacy.out, qb, ctx->stream)) legacy_abort(fn);
+    if (smol_attn_causal(ctx, g_legacy.q.p, g_legacy.k.p, g_legacy.v.p, SMOL_ATTN_F32, seq_q, seq_k, Hq, Hkv, hd,
+                         scale, q_offset, window, cap, (float *)g_legacy.out.p) != SMOL_ATTN_OK)
+        legacy_abort(fn);
+    legacy_download(fn, out, g_legacy.out, qb);
+}
+
+}  // namespace
+
+extern "C" void smol_causal_attention(float *out, const float *Q, const float *K, const float *V, int seq_q,
+                                      int seq_k, int n_heads, int n_kv_heads, int head_dim, float scale,
+                                      int q_offset) {
+    legacy_causal(__func__, out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset, 0, 0.0f);
+}
+
+extern "C" void smol_sliding_window_attention(float *out, const float *Q, const float *K, const float *V,
+                                              int seq_q, int seq_k, int n_heads, int n_kv_heads, int head_dim,
+                                              float scale, int q_offset, int window_size) {
+    legacy_causal(__func__, out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset,
+                  window_size, 0.0f);
+}
+
+extern "C" void smol_causal_attention_softcap(float *out, const float *Q, const float *K, const float *V,
+                                              int seq_q, int seq_k, int n_heads, int n_kv_heads, int head_dim,
+                                              float scale, int q_offset, float cap) {
+    legacy_causal(__func__, out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset, 0, cap);
+}
+
+extern "C" void smol_sliding_window_attention_softcap(float *out, const float *Q, const float *K,
+                                                      const float *V, int seq_q, int seq_k, int n_heads,
+                                                      int n_kv_heads, int head_dim, float scale, int q_offset,
+                                                      int window_size, float cap) {
+    legacy_causal(__func__, out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset,
+                  window_size, cap);
+}
+
+extern "C" void smol_bidirectional_attention(float *out, const float *Q, const float *K, const float *V, int seq,
+                                             int n_heads, int head_dim, float scale, const int *window_starts,
+                                             int n_windows) {
+    (void)seq; /* unused by the reference too (attention.c:33); the windows define the rows */
+    if (n_windows <= 0) return;
+    const int rows = window_starts[n_windows];
+    if (rows <= 0) return;
+    smol_attn_ctx *ctx = legacy_ctx(__func__);
+    const size_t b = (size_t)rows * n_heads * head_dim * 4;
+    legacy_upload(__func__, g_legacy.q, Q, b);
+    legacy_upload(__func__, g_legacy.k, K, b);
+    legacy_upload(__func__, g_legacy.v, V, b);
+    if (dev_reserve(g_legacy.out, b, ctx->stream)) legacy_abort(__func__);
+    /* rows outside every window are left untouched by the reference; keep them */
+    if (hipMemcpyAsync(g_legacy.out.p, out, b, hipMemcpyHostToDevice, ctx->stream) != hipSuccess)
+        legacy_abort(__func__);
+    if (smol_attn_bidirectional(ctx, g_legacy.q.p, g_legacy.k.p, g_legacy.v.p, SMOL_ATTN_F32, rows, n_heads,
+                                head_dim, scale, window_starts, n_windows, (float *)g_legacy.out.p) != SMOL_ATTN_OK)
+        legacy_abort(__func__);
+    legacy_download(__func__, out, g_legacy.out, b);
+}
+
+/* rope.c:27-66: the table rows for explicit positions (host, as in the reference) */
+static void compute_rope_rows(float *c, float *s, const int *positions, int seq, int hd, float theta, int type) {
+    for (int i = 0; i < seq; i++)
+        smol_rope_fill_host(c + (size_t)i * hd, s + (size_t)i * hd, positions[i], 1, hd, theta, type);
+}
+
+extern "C" void smol_compute_rope_neox(float *cos_out, float *sin_out, const int *positions, int seq, int head_dim,
+                                       float theta) {
+    compute_rope_rows(cos_out, sin_out, positions, seq, head_dim, theta, SMOL_ROPE_NEOX);
+}
+
+extern "C" void smol_compute_rope_interleaved(float *cos_out, float *sin_out, const int *positions, int seq,
+                                              int head_dim, float theta) {
+    compute_rope_rows(cos_out, sin_out, positions, seq, head_dim, theta, SMOL_ROPE_INTERLEAVED);
+}
+
+static void legacy_rope(const char *fn, float *x, const float *c, const float *s, int seq, int H, int hd,
+                        int kind) {
+    if (seq <= 0 || H <= 0) return;
+    smol_attn_ctx *ctx = legacy_ctx(fn);
+    const size_t xb = (size_t)seq * H * hd * 4, tb = (size_t)seq * hd * 4;
+    legacy_upload(fn, g_legacy.q, x, xb);
+    if (dev_reserve(g_legacy.cs, 2 * tb, ctx->stream)) legacy_abort(fn);
+    if (hipMemcpyAsync(g_legacy.cs.p, c, tb, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+        hipMemcpyAsync((char *)g_legacy.cs.p + tb, s, tb, hipMemcpyHostToDevice, ctx->stream) != hipSuccess)
+        legacy_abort(fn);
+    if (smol_launch_rope_apply((float *)g_legacy.q.p, (const float *)g_legacy.cs.p,
+                               (const float *)((char *)g_legacy.cs.p + tb), nullptr, seq, H, hd, kind, ctx->stream))
+        legacy_abort(fn);
+    legacy_download(fn, x, g_legacy.q, xb);
+}
+
+extern "C" void smol_apply_rope_neox(float *x, const float *cos_vals, const float *sin_vals, int seq, int n_heads,
+                                     int head_dim) {
+    legacy_rope(__func__, x, cos_vals, sin_vals, seq, n_heads, head_dim, SMOL_ROPE_NEOX_K);
+}
+
+extern "C" void smol_apply_rope_interleaved(float *x, const float *cos_vals, const float *sin_vals, int seq,
+                                            int n_heads, int head_dim) {
+    legacy_rope(__func__, x, cos_vals, sin_vals, seq, n_heads, head_dim, SMOL_ROPE_INTERLEAVED_K);
+}

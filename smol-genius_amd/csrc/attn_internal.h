@@ -1,0 +1,115 @@
+/*
+ * attn_internal.h - descriptors shared by the host dispatcher (attn_api.hip)
+ * and the kernels (attn_kernels.hip). Not part of the public C ABI.
+ *
+ * Device data layout (one GPU):
+ *   KV cache   K  : bf16 [layer][slot][kv_head][cap][head_dim]   (post-RoPE)
+ *              V^T: bf16 [layer][slot][kv_head][head_dim][cap]   (transposed, so
+ *                   the P.V product reads 8 consecutive keys of one column)
+ *   fresh K/V  fp16 copies of the keys a call appends (and of the cache rows
+ *              that share their 32-key slab), same two layouts with `fcap`
+ *              rows; attention over a call's own keys uses these, so a key
+ *              rotated in fp32 is never read back through bf16 rounding.
+ *   Q scratch  fp16 [kv_head][row][hdp], row = q_index * G + head_in_group,
+ *              rotated and pre-multiplied by scale * log2(e); hdp = head_dim
+ *              rounded up to 32 and zero-filled.
+ */
+#ifndef SMOL_ATTN_INTERNAL_H
+#define SMOL_ATTN_INTERNAL_H
+
+#include <stdint.h>
+
+#define SMOL_SLAB 32          /* keys per inner step of the attention kernels */
+#define SMOL_ROWS_PER_TILE 16 /* query rows per MFMA tile (16x16x32 f16) */
+
+enum { SMOL_IN_F32 = 0, SMOL_IN_BF16 = 1 };
+enum { SMOL_ROPE_OFF = 0, SMOL_ROPE_NEOX_K = 1, SMOL_ROPE_INTERLEAVED_K = 2 };
+
+/* One attention "batch": a set of query rows sharing one key range and one
+ * K/V source (a sequence slot of the cache, or one bidirectional window). */
+typedef struct {
+    int n_rows;      /* query rows = n_q * G */
+    int q_row0;      /* first Q-scratch row of this batch */
+    int out_tok0;    /* first output token row */
+    int q_pos0;      /* causal position of query 0 (query i sits at q_pos0 + i) */
+    int key_lo;      /* visible keys are [key_lo, key_hi) (then causal / window) */
+    int key_hi;
+    int causal;      /* 1: key <= q_pos0 + i; 0: the whole [key_lo, key_hi) */
+    int fresh_pos0;  /* keys >= fresh_pos0 come from the fresh fp16 buffers */
+    int fresh_row0;  /* fresh row holding key fresh_pos0 */
+    int slot;        /* cache slot, or -1 when the batch has no cache */
+    int pad0, pad1;
+} SkBatch;
+
+/* One work item of the split-K kernel: a tile of rows of a batch against a
+ * contiguous key range. Items of one merge group are contiguous. */
+typedef struct {
+    int batch;
+    int row0;        /* first row (within the batch) of this item's row tiles */
+    int key_begin;   /* slab-aligned */
+    int key_end;
+    int group;       /* merge group id (one output row tile) */
+    int n_split;     /* items in the group */
+    int split;       /* index of this item in its group */
+    int pad;
+} SkItem;
+
+typedef struct {
+    const _Float16 *qs;        /* Q scratch */
+    long long qs_head_stride;  /* rows_total * hdp */
+    const uint16_t *kc;        /* cache K at (layer, slot 0), or null */
+    const uint16_t *vtc;       /* cache V^T at (layer, slot 0), or null */
+    long long c_slot_stride;   /* elements per slot (n_kv * cap * hd) */
+    int cap;                   /* cache rows per (slot, kv head) */
+    const _Float16 *kf;        /* fresh K [kv][fcap][hd] */
+    const _Float16 *vtf;       /* fresh V^T [kv][hd][fcap] */
+    int fcap;
+    float *out;                /* [token][Hq][hd] fp32 */
+    int Hq, Hkv, G;
+    int window;                /* > 0: sliding window (keys > pos - window) */
+    float cap2;                /* > 0: softcap in log2 units (cap * log2 e) */
+    const SkBatch *batches;
+    const SkItem *items;
+    float *part_o;             /* [item][kv][rows][hd] unnormalised partial outputs */
+    float *part_ml;            /* [item][kv][rows][2] (max, sum) */
+    int *counters;             /* [group][kv]; zero between calls */
+} SkParams;
+
+/* Pre-pass: rotates/scales Q into the Q scratch, appends rotated K and V to
+ * the bf16 cache and writes the fresh fp16 K/V slabs. */
+typedef struct {
+    int q_tok0, n_q;     /* Q input rows of this batch */
+    int q_row0;          /* Q-scratch row offset (already multiplied by G) */
+    int q_pos0;          /* RoPE table row of Q row 0 */
+    int kv_in0, n_kv;    /* new K/V input rows */
+    int kv_pos0;         /* position (cache row, RoPE row) of new K/V row 0 */
+    int fresh_pos0;      /* slab-aligned first position of the fresh window */
+    int n_fresh;         /* multiple of SMOL_SLAB */
+    int fresh_row0;      /* fresh row of fresh_pos0 */
+    int slot;            /* cache slot or -1 */
+    int pad;
+} PrepBatch;
+
+/* Block work of the pre-pass: a 32-position fresh slab of one batch, or a
+ * run of Q tokens of one batch. */
+typedef struct {
+    int batch;
+    int kind;            /* 0: fresh slab, 1: Q tokens */
+    int first;           /* slab index within the fresh window / first Q token */
+    int count;           /* Q tokens in this block */
+} PrepBlock;
+
+typedef struct {
+    const void *q; int q_dtype; long long q_stride;
+    const void *k; const void *v; int kv_dtype; long long kv_stride;
+    const float *rope_cos; const float *rope_sin; int rope_kind; int rope_q; int rope_k;
+    float qscale;
+    int Hq, Hkv, G, hd, hdp;
+    _Float16 *qs; long long qs_head_stride;
+    uint16_t *kc; uint16_t *vtc; long long c_slot_stride; int cap;
+    _Float16 *kf; _Float16 *vtf; int fcap;
+    const PrepBatch *batches;
+    const PrepBlock *blocks;
+} PrepParams;
+
+#endif

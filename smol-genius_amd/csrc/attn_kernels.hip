@@ -1,0 +1,481 @@
+/*
+ * attn_kernels.hip - gfx950 (CDNA4) kernels of the attention path.
+ *
+ *   k_prep      RoPE + cache append + fp16 staging, one pass over the new
+ *               rows: replaces smol_apply_rope_{neox,interleaved} on Q and K
+ *               and the K/V row memcpy into the cache
+ *               (common/decoder/qkn_decoder.c:493-503 and :647-652).
+ *   k_attn_sk   split-K flash attention on fp16 MFMA (v_mfma_f32_16x16x32_f16):
+ *               the causal / sliding-window / softcap / windowed-bidirectional
+ *               online softmax of common/kernels/attention.c:32-462, over the
+ *               bf16 KV cache plus the call's fresh fp16 keys, with a
+ *               last-arriving-wave log-sum-exp merge of the key splits.
+ *
+ * Numerics: softmax state in fp32 and in log2 units (Q is pre-multiplied by
+ * scale * log2 e, so exp(s - m) = exp2(s' - m')). MFMA operands are fp16:
+ * bf16 -> fp16 is exact for |x| < 65504, and fp16 keeps 3 more mantissa bits
+ * than bf16 for the rotated Q/K and the probabilities P, which is what keeps
+ * the result within 2e-3 + 1e-2 |ref| of the fp32 reference on early causal
+ * rows (bf16 operands do not).
+ */
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "attn_internal.h"
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+#define LOG2E_F 1.4426950408889634f
+
+/* ------------------------------------------------------------------ helpers */
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+    return __uint_as_float((uint32_t)b << 16);
+}
+
+/* float -> bf16 bits, round to nearest even (inputs are finite) */
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ h8 bf16x8_to_h8(uint4 w) {
+    h8 r;
+    const uint32_t a[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        r[2 * i] = (_Float16)__uint_as_float(a[i] << 16);
+        r[2 * i + 1] = (_Float16)__uint_as_float(a[i] & 0xFFFF0000u);
+    }
+    return r;
+}
+
+__device__ __forceinline__ h8 load_h8(const _Float16 *p) {
+    uint4 w = *reinterpret_cast<const uint4 *>(p);
+    return *reinterpret_cast<h8 *>(&w);
+}
+
+__device__ __forceinline__ h8 load_bf16x8(const uint16_t *p) {
+    return bf16x8_to_h8(*reinterpret_cast<const uint4 *>(p));
+}
+
+__device__ __forceinline__ h8 zero_h8() {
+    h8 z;
+#pragma unroll
+    for (int i = 0; i < 8; i++) z[i] = (_Float16)0.0f;
+    return z;
+}
+
+__device__ __forceinline__ float load_in(const void *base, int dtype, long long idx) {
+    return dtype == SMOL_IN_BF16 ? bf16_to_f32(((const uint16_t *)base)[idx])
+                                 : ((const float *)base)[idx];
+}
+
+/* Rotated value of element d of a head vector x (fp32), position row of the
+ * table. NeoX pairs (d, d + half); interleaved pairs (2i, 2i + 1). The
+ * arithmetic is rope.c:99-164 (fmsub / fmadd) and rope.c:68-93. */
+__device__ __forceinline__ float rope_elem(float xd, float xp, int d, int hd, int kind,
+                                           const float *c, const float *s) {
+    if (kind == SMOL_ROPE_NEOX_K) {
+        int half = hd >> 1;
+        if (d < half) return fmaf(xd, c[d], -(xp * s[d]));      /* x1 c - x2 s */
+        return fmaf(xd, c[d], xp * s[d]);                       /* x2 c + x1 s */
+    }
+    if (kind == SMOL_ROPE_INTERLEAVED_K) {
+        if ((d & 1) == 0) return xd * c[d] - xp * s[d];          /* x0 c - x1 s */
+        return xd * c[d] + xp * s[d];                            /* x1 c + x0 s */
+    }
+    return xd;
+}
+
+__device__ __forceinline__ int rope_partner(int d, int hd, int kind) {
+    if (kind == SMOL_ROPE_NEOX_K) { int half = hd >> 1; return d < half ? d + half : d - half; }
+    if (kind == SMOL_ROPE_INTERLEAVED_K) return d ^ 1;
+    return d;
+}
+
+/* ------------------------------------------------------------------ k_prep */
+
+/* grid (n_blocks, Hkv), 256 threads. A fresh-slab block covers 32 positions
+ * of one KV head: old cache rows are copied to the fresh buffers, new rows
+ * are rotated (K), appended to the bf16 cache and written to the fresh
+ * buffers, positions past the new rows are zero. V goes through LDS so the
+ * transposed stores are 32 consecutive positions of one column. */
+__global__ __launch_bounds__(256) void k_prep(PrepParams p) {
+    const PrepBlock blk = p.blocks[blockIdx.x];
+    const PrepBatch b = p.batches[blk.batch];
+    const int g = blockIdx.y;
+    const int hd = p.hd;
+    const int tid = threadIdx.x;
+    __shared__ float sv[SMOL_SLAB * 257];
+
+    if (blk.kind == 1) {
+        /* Q rows: token t, head g*G + hg -> scratch row q_row0 + t*G + hg */
+        const int G = p.G, hdp = p.hdp;
+        const int per_tok = G * hdp;
+        for (int e = tid; e < blk.count * per_tok; e += blockDim.x) {
+            int tl = e / per_tok, rem = e - tl * per_tok;
+            int hg = rem / hdp, d = rem - hg * hdp;
+            int t = blk.first + tl;
+            float val = 0.0f;
+            if (d < hd) {
+                long long base = (long long)(b.q_tok0 + t) * p.q_stride + (long long)(g * G + hg) * hd;
+                float xd = load_in(p.q, p.q_dtype, base + d);
+                if (p.rope_q && p.rope_kind != SMOL_ROPE_OFF) {
+                    int pd = rope_partner(d, hd, p.rope_kind);
+                    float xp = load_in(p.q, p.q_dtype, base + pd);
+                    long long row = (long long)(b.q_pos0 + t) * hd;
+                    xd = rope_elem(xd, xp, d, hd, p.rope_kind, p.rope_cos + row, p.rope_sin + row);
+                }
+                val = xd * p.qscale;
+            }
+            p.qs[(long long)g * p.qs_head_stride + (long long)(b.q_row0 + t * G + hg) * hdp + d] =
+                (_Float16)val;
+        }
+        return;
+    }
+
+    /* fresh slab */
+    const int pos_base = b.fresh_pos0 + blk.first * SMOL_SLAB;
+    const int frow_base = b.fresh_row0 + blk.first * SMOL_SLAB;
+    const bool has_cache = b.slot >= 0 && p.kc != nullptr;
+    const uint16_t *kc = has_cache ? p.kc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * hd : nullptr;
+    const uint16_t *vtc = has_cache ? p.vtc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * hd : nullptr;
+    uint16_t *kcw = has_cache ? p.kc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * hd : nullptr;
+    uint16_t *vtcw = has_cache ? p.vtc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * hd : nullptr;
+    _Float16 *kf = p.kf + (long long)g * p.fcap * hd;
+    _Float16 *vtf = p.vtf + (long long)g * p.fcap * hd;
+
+    /* K rows (row-major): element (r, d) */
+    for (int e = tid; e < SMOL_SLAB * hd; e += blockDim.x) {
+        int r = e / hd, d = e - r * hd;
+        int pos = pos_base + r;
+        float kv = 0.0f, vv = 0.0f;
+        if (pos < b.kv_pos0) {
+            if (has_cache) {
+                kv = bf16_to_f32(kc[(long long)pos * hd + d]);
+                vv = bf16_to_f32(vtc[(long long)d * p.cap + pos]);
+            }
+        } else if (pos < b.kv_pos0 + b.n_kv) {
+            int t = pos - b.kv_pos0;
+            long long base = (long long)(b.kv_in0 + t) * p.kv_stride + (long long)g * hd;
+            kv = load_in(p.k, p.kv_dtype, base + d);
+            if (p.rope_k && p.rope_kind != SMOL_ROPE_OFF) {
+                int pd = rope_partner(d, hd, p.rope_kind);
+                float xp = load_in(p.k, p.kv_dtype, base + pd);
+                long long row = (long long)pos * hd;
+                kv = rope_elem(kv, xp, d, hd, p.rope_kind, p.rope_cos + row, p.rope_sin + row);
+            }
+            vv = load_in(p.v, p.kv_dtype, base + d);
+            if (has_cache) kcw[(long long)pos * hd + d] = f32_to_bf16(kv);
+        }
+        kf[(long long)(frow_base + r) * hd + d] = (_Float16)kv;
+        sv[r * 257 + d] = vv;
+    }
+    __syncthreads();
+    /* V^T: element (d, r), r fastest */
+    for (int e = tid; e < SMOL_SLAB * hd; e += blockDim.x) {
+        int d = e / SMOL_SLAB, r = e - d * SMOL_SLAB;
+        int pos = pos_base + r;
+        float vv = sv[r * 257 + d];
+        vtf[(long long)d * p.fcap + frow_base + r] = (_Float16)vv;
+        if (has_cache && pos >= b.kv_pos0 && pos < b.kv_pos0 + b.n_kv)
+            vtcw[(long long)d * p.cap + pos] = f32_to_bf16(vv);
+    }
+}
+
+/* --------------------------------------------------------------- k_attn_sk */
+
+/*
+ * One wave (64 lanes) per item: NT tiles of 16 query rows of one KV head
+ * against the item's key range, in 32-key slabs.
+ *
+ * MFMA layouts (16x16x32 f16; lane l, c = l & 15, j = l >> 4):
+ *   S^T = K . Q^T : A = K rows, B = Q^T; D element i of lane l is
+ *                   S^T[key 4j+i (tile-local)][row c]
+ *   O^T = V^T . P^T: A = V^T (8 consecutive keys of column d), B = P^T.
+ * K rows are gathered in the order key(t, m) = 8 (m >> 2) + 4 t + (m & 3) so
+ * that the 8 probabilities a lane holds after the two S^T tiles are the 8
+ * consecutive keys 8j..8j+7 of the slab, i.e. exactly the B operand of the
+ * P.V step against a 16-byte load of V^T.
+ */
+template <int HD, int NT>
+__global__ __launch_bounds__(64) void k_attn_sk(SkParams p) {
+    constexpr int KS = (HD + 31) / 32;  /* 32-wide steps over head_dim for S */
+    constexpr int DT = (HD + 15) / 16;  /* 16-row tiles of head_dim for O */
+    constexpr int HDP = KS * 32;
+    constexpr int ROWS = NT * 16;
+    const int lane = threadIdx.x;
+    const int c = lane & 15, j = lane >> 4;
+    const int g = blockIdx.y;
+    const SkItem it = p.items[blockIdx.x];
+    const SkBatch b = p.batches[it.batch];
+    const int G = p.G;
+
+    /* per-lane row metadata and Q fragments */
+    h8 qf[NT][KS];
+    int lo[NT], hi[NT];
+    float m[NT], l[NT];
+    f4 o[NT][DT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int r = it.row0 + nt * 16 + c;
+        const bool valid = r < b.n_rows;
+        const int qi = r / G;
+        int rl = b.key_lo, rh = b.key_hi;
+        if (b.causal) {
+            rh = min(rh, b.q_pos0 + qi + 1);
+            if (p.window > 0) rl = max(rl, b.q_pos0 + qi - p.window + 1);
+        }
+        lo[nt] = valid ? rl : 0;
+        hi[nt] = valid ? rh : 0;
+        m[nt] = -INFINITY;
+        l[nt] = 0.0f;
+        const _Float16 *qrow = p.qs + (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid ? r : 0)) * HDP;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) qf[nt][ks] = valid ? load_h8(qrow + 32 * ks + 8 * j) : zero_h8();
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) o[nt][dt] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    const uint16_t *kc = nullptr, *vtc = nullptr;
+    if (b.slot >= 0 && p.kc != nullptr) {
+        kc = p.kc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * HD;
+        vtc = p.vtc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * HD;
+    }
+    const _Float16 *kf = p.kf + (long long)g * p.fcap * HD;
+    const _Float16 *vtf = p.vtf + (long long)g * p.fcap * HD;
+    const int kt_row = 8 * (c >> 2) + (c & 3); /* gathered key of A-operand row c, tile 0 */
+
+    for (int k0 = it.key_begin; k0 < it.key_end; k0 += SMOL_SLAB) {
+        const bool fresh = k0 >= b.fresh_pos0;
+        /* ---- S^T = K . Q^T for two 16-key tiles ---- */
+        h8 kfrag[2][KS];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int key = k0 + kt_row + 4 * t;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                const int d0 = 32 * ks + 8 * j;
+                if (HD % 32 != 0 && d0 >= HD) { kfrag[t][ks] = zero_h8(); continue; }
+                kfrag[t][ks] = fresh ? load_h8(kf + (long long)(b.fresh_row0 + key - b.fresh_pos0) * HD + d0)
+                                     : load_bf16x8(kc + (long long)key * HD + d0);
+            }
+        }
+        f4 s[NT][2];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kfrag[t][ks], qf[nt][ks], acc, 0, 0, 0);
+                s[nt][t] = acc;
+            }
+
+        /* ---- V^T fragments (shared by all row tiles) ---- */
+        h8 vfrag[DT];
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            const int d = 16 * dt + c;
+            if (HD % 16 != 0 && d >= HD) { vfrag[dt] = zero_h8(); continue; }
+            vfrag[dt] = fresh ? load_h8(vtf + (long long)d * p.fcap + b.fresh_row0 + (k0 - b.fresh_pos0) + 8 * j)
+                              : load_bf16x8(vtc + (long long)d * p.cap + k0 + 8 * j);
+        }
+
+        /* ---- online softmax per row (lane column), then O^T += V^T P^T ---- */
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            float sv[8];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int key = k0 + 8 * j + 4 * t + i;
+                    float x = s[nt][t][i];
+                    if (p.cap2 > 0.0f) x = p.cap2 * tanhf(x / p.cap2);
+                    x = (key >= lo[nt] && key < hi[nt]) ? x : -INFINITY;
+                    sv[4 * t + i] = x;
+                    mx = fmaxf(mx, x);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float m_new = fmaxf(m[nt], mx);
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            const float alpha = __builtin_amdgcn_exp2f(m[nt] - m_use);
+            m[nt] = m_new;
+            h8 pf;
+            float ps = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                float pe = __builtin_amdgcn_exp2f(sv[e] - m_use);
+                ps += pe;
+                pf[e] = (_Float16)pe;
+            }
+            l[nt] = l[nt] * alpha + ps;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                o[nt][dt] *= alpha;
+                o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vfrag[dt], pf, o[nt][dt], 0, 0, 0);
+            }
+        }
+    }
+
+    /* full row sums: lanes c, c+16, c+32, c+48 hold one row */
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        l[nt] += __shfl_xor(l[nt], 16);
+        l[nt] += __shfl_xor(l[nt], 32);
+    }
+
+    const int Hq = p.Hq;
+    if (it.n_split == 1) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int r = it.row0 + nt * 16 + c;
+            if (r >= b.n_rows) continue;
+            const int qi = r / G, hg = r - qi * G;
+            float *orow = p.out + ((long long)(b.out_tok0 + qi) * Hq + (g * G + hg)) * HD;
+            const float inv = l[nt] > 0.0f ? 1.0f / l[nt] : 0.0f;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                const int d = 16 * dt + 4 * j;
+                if (HD % 16 != 0 && d >= HD) continue;
+                *reinterpret_cast<f4 *>(orow + d) = o[nt][dt] * inv;
+            }
+        }
+        return;
+    }
+
+    /* ---- split-K: publish the partial, the last wave of the group merges ---- */
+    const long long pbase = ((long long)blockIdx.x * p.Hkv + g) * ROWS;
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int rr = nt * 16 + c;
+        float *po = p.part_o + (pbase + rr) * HD;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            const int d = 16 * dt + 4 * j;
+            if (HD % 16 != 0 && d >= HD) continue;
+            *reinterpret_cast<f4 *>(po + d) = o[nt][dt];
+        }
+        if (j == 0) {
+            p.part_ml[(pbase + rr) * 2 + 0] = m[nt];
+            p.part_ml[(pbase + rr) * 2 + 1] = l[nt];
+        }
+    }
+    int prev = 0;
+    if (lane == 0)
+        prev = __hip_atomic_fetch_add(p.counters + (long long)it.group * p.Hkv + g, 1,
+                                      __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __shfl(prev, 0);
+    if (prev != it.n_split - 1) return;
+    __atomic_thread_fence(__ATOMIC_ACQUIRE);
+
+    const int first = blockIdx.x - it.split;
+    for (int e = lane; e < ROWS * (HD / 4); e += 64) {
+        const int rr = e / (HD / 4), d = (e - rr * (HD / 4)) * 4;
+        const int r = it.row0 + rr;
+        if (r >= b.n_rows) continue;
+        float M = -INFINITY;
+        for (int sp = 0; sp < it.n_split; sp++)
+            M = fmaxf(M, p.part_ml[(((long long)(first + sp) * p.Hkv + g) * ROWS + rr) * 2]);
+        const float Mu = M == -INFINITY ? 0.0f : M;
+        float L = 0.0f;
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int sp = 0; sp < it.n_split; sp++) {
+            const long long pr = ((long long)(first + sp) * p.Hkv + g) * ROWS + rr;
+            const float w = __builtin_amdgcn_exp2f(p.part_ml[pr * 2] - Mu);
+            L += w * p.part_ml[pr * 2 + 1];
+            acc += w * *reinterpret_cast<const f4 *>(p.part_o + pr * HD + d);
+        }
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        const int qi = r / G, hg = r - qi * G;
+        *reinterpret_cast<f4 *>(p.out + ((long long)(b.out_tok0 + qi) * Hq + (g * G + hg)) * HD + d) = acc * inv;
+    }
+    if (lane == 0) p.counters[(long long)it.group * p.Hkv + g] = 0;
+}
+
+/* ------------------------------------------------------------ k_rope_apply */
+
+/* In-place RoPE on x [seq][H][hd] fp32, row s using table row pos[s] (or s
+ * when pos is null). One thread per rotated pair; the arithmetic is that of
+ * rope.c:99-164 (NeoX: fmsub / fmadd with the first-half table entries over
+ * the 16-wide vector body, the scalar tail with the second-half entries) and
+ * rope.c:68-93 (interleaved). */
+__global__ __launch_bounds__(256) void k_rope_apply(float *x, const float *cos_t, const float *sin_t,
+                                                    const int *pos, int seq, int H, int hd, int kind) {
+    const int half = hd >> 1;
+    const long long n = (long long)seq * H * half;
+    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < n;
+         e += (long long)gridDim.x * blockDim.x) {
+        const int i = (int)(e % half);
+        const long long sh = e / half;
+        const int s = (int)(sh / H);
+        const long long row = (long long)(pos ? pos[s] : s) * hd;
+        const float *c = cos_t + row, *sn = sin_t + row;
+        float *v = x + sh * hd;
+        if (kind == SMOL_ROPE_NEOX_K) {
+            const float x1 = v[i], x2 = v[half + i];
+            const int body = half - (half % 16);
+            if (i < body) {
+                v[i] = fmaf(x1, c[i], -(x2 * sn[i]));
+                v[half + i] = fmaf(x2, c[i], x1 * sn[i]);
+            } else {
+                v[i] = x1 * c[i] + (-x2) * sn[i];
+                v[half + i] = x2 * c[half + i] + x1 * sn[half + i];
+            }
+        } else {
+            const float x0 = v[2 * i], x1 = v[2 * i + 1];
+            v[2 * i] = x0 * c[2 * i] - x1 * sn[2 * i];
+            v[2 * i + 1] = x1 * c[2 * i + 1] + x0 * sn[2 * i + 1];
+        }
+    }
+}
+
+/* ------------------------------------------------------------ launchers */
+
+extern "C" int smol_launch_rope_apply(float *x, const float *cos_t, const float *sin_t, const int *pos,
+                                      int seq, int n_heads, int hd, int kind, hipStream_t st) {
+    const long long n = (long long)seq * n_heads * (hd / 2);
+    if (n <= 0) return 0;
+    const int blocks = (int)std::min<long long>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(k_rope_apply, dim3(blocks), dim3(256), 0, st, x, cos_t, sin_t, pos, seq, n_heads,
+                       hd, kind);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t st) {
+    if (n_blocks <= 0) return 0;
+    if (pp->hd > 256) return -1;
+    hipLaunchKernelGGL(k_prep, dim3(n_blocks, pp->Hkv), dim3(256), 0, st, *pp);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+template <int HD>
+static int launch_sk_hd(const SkParams *sp, int n_items, int nt, hipStream_t st) {
+    dim3 grid(n_items, sp->Hkv), block(64);
+    /* register budget: NT * HD <= 256 fits without spilling */
+    if (nt == 1) hipLaunchKernelGGL((k_attn_sk<HD, 1>), grid, block, 0, st, *sp);
+    else if (nt == 2 && HD <= 128) hipLaunchKernelGGL((k_attn_sk<HD, (HD <= 128 ? 2 : 1)>), grid, block, 0, st, *sp);
+    else if (nt == 4 && HD <= 64) hipLaunchKernelGGL((k_attn_sk<HD, (HD <= 64 ? 4 : 1)>), grid, block, 0, st, *sp);
+    else return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+extern "C" int smol_launch_sk(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st) {
+    if (n_items <= 0) return 0;
+    switch (hd) {
+    case 64: return launch_sk_hd<64>(sp, n_items, nt, st);
+    case 72: return launch_sk_hd<72>(sp, n_items, nt, st);
+    case 80: return launch_sk_hd<80>(sp, n_items, nt, st);
+    case 96: return launch_sk_hd<96>(sp, n_items, nt, st);
+    case 128: return launch_sk_hd<128>(sp, n_items, nt, st);
+    case 256: return launch_sk_hd<256>(sp, n_items, nt, st);
+    default: return -1;
+    }
+}

@@ -1,0 +1,359 @@
+"""Python mirror of the C ABI in include/smol_attn.h and include/smol_kernels_attn.h.
+
+The library is loaded from this directory (libsmol_attn.so, built by
+build.py); importing this module fails loudly when it is missing. Device
+tensors are torch tensors on a ROCm device: torch provides memory and the
+stream, the computation is the library's. Host arrays are numpy.
+
+The names mirror the reference's kernel API (common/kernels/smol_kernels.h):
+``smol_causal_attention``, ``smol_bidirectional_attention``,
+``smol_sliding_window_attention``, ``smol_causal_attention_softcap``,
+``smol_sliding_window_attention_softcap``, ``smol_compute_rope_neox`` ... with
+the same argument meaning (``out`` is overwritten in place).
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsmol_attn.so")
+
+F32, BF16 = 0, 1
+ROPE_NONE, ROPE_NEOX, ROPE_INTERLEAVED = -1, 0, 1
+
+_c_int, _c_float, _vp = ctypes.c_int, ctypes.c_float, ctypes.c_void_p
+_FP = ctypes.POINTER(ctypes.c_float)
+_IP = ctypes.POINTER(ctypes.c_int)
+_U16P = ctypes.POINTER(ctypes.c_uint16)
+
+# (name, argtypes, restype) of every exported entry point; the ABI test checks
+# this list against the header declarations and the library's symbol table.
+SIGNATURES = [
+    ("smol_attn_version", [], ctypes.c_char_p),
+    ("smol_attn_last_error", [], ctypes.c_char_p),
+    ("smol_attn_device_count", [], _c_int),
+    ("smol_attn_ctx_create", [_c_int, _vp, ctypes.POINTER(_vp)], _c_int),
+    ("smol_attn_ctx_destroy", [_vp], _c_int),
+    ("smol_attn_ctx_synchronize", [_vp], _c_int),
+    ("smol_attn_ctx_stream", [_vp], _vp),
+    ("smol_rope_table_create", [_vp, _c_int, _c_float, _c_int, _c_int, ctypes.POINTER(_vp)], _c_int),
+    ("smol_rope_table_ensure", [_vp, _c_int], _c_int),
+    ("smol_rope_table_capacity", [_vp], _c_int),
+    ("smol_rope_table_destroy", [_vp], _c_int),
+    ("smol_rope_fill_host", [_FP, _FP, _c_int, _c_int, _c_int, _c_float, _c_int], None),
+    ("smol_kv_cache_create", [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_vp)], _c_int),
+    ("smol_kv_cache_destroy", [_vp], _c_int),
+    ("smol_kv_cache_capacity", [_vp], _c_int),
+    ("smol_kv_cache_reserve", [_vp, _c_int], _c_int),
+    ("smol_kv_cache_write", [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _c_int], _c_int),
+    ("smol_kv_cache_read", [_vp, _c_int, _c_int, _c_int, _c_int, _U16P, _U16P], _c_int),
+    ("smol_attn_prefill", [_vp, _vp, _c_int, _c_int, _vp, _c_int, _c_int, _vp, _vp, _vp, _c_int,
+                           _c_int, _c_float, _c_int, _c_float, _vp], _c_int),
+    ("smol_attn_decode", [_vp, _vp, _c_int, _vp, _c_int, _IP, _IP, _vp, _vp, _vp, _c_int, _c_int,
+                          _c_float, _c_int, _c_float, _vp], _c_int),
+    ("smol_attn_causal", [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                          _c_float, _c_int, _c_int, _c_float, _vp], _c_int),
+    ("smol_attn_bidirectional", [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float, _IP,
+                                 _c_int, _vp], _c_int),
+    ("smol_attn_apply_rope", [_vp, _vp, _vp, _IP, _c_int, _c_int], _c_int),
+    # reference-signature drop-ins (host fp32 arrays)
+    ("smol_bidirectional_attention", [_FP, _FP, _FP, _FP, _c_int, _c_int, _c_int, _c_float, _IP, _c_int], None),
+    ("smol_causal_attention", [_FP, _FP, _FP, _FP, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int], None),
+    ("smol_sliding_window_attention", [_FP, _FP, _FP, _FP, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
+                                       _c_int, _c_int], None),
+    ("smol_causal_attention_softcap", [_FP, _FP, _FP, _FP, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
+                                       _c_int, _c_float], None),
+    ("smol_sliding_window_attention_softcap", [_FP, _FP, _FP, _FP, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                               _c_float, _c_int, _c_int, _c_float], None),
+    ("smol_compute_rope_neox", [_FP, _FP, _IP, _c_int, _c_int, _c_float], None),
+    ("smol_apply_rope_neox", [_FP, _FP, _FP, _c_int, _c_int, _c_int], None),
+    ("smol_compute_rope_interleaved", [_FP, _FP, _IP, _c_int, _c_int, _c_float], None),
+    ("smol_apply_rope_interleaved", [_FP, _FP, _FP, _c_int, _c_int, _c_int], None),
+]
+
+_lib = None
+
+
+class SmolAttnError(RuntimeError):
+    pass
+
+
+def load(path=LIB_PATH):
+    """The loaded library (ctypes.CDLL). Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise SmolAttnError("%s is missing: run `python smol-genius_amd/build.py` "
+                            "(the attention path has no CPU fallback)" % path)
+    lib = ctypes.CDLL(path)
+    for name, argtypes, restype in SIGNATURES:
+        f = getattr(lib, name)
+        f.argtypes = argtypes
+        f.restype = restype
+    _lib = lib
+    return lib
+
+
+def _check(rc, what):
+    if rc != 0:
+        raise SmolAttnError("%s failed (%d): %s" % (what, rc, load().smol_attn_last_error().decode()))
+
+
+def _dtype_code(t):
+    import torch
+    if t.dtype == torch.float32:
+        return F32
+    if t.dtype == torch.bfloat16:
+        return BF16
+    raise SmolAttnError("inputs must be float32 or bfloat16, got %s" % t.dtype)
+
+
+def _dev(t, what):
+    if not t.is_cuda or not t.is_contiguous():
+        raise SmolAttnError("%s must be a contiguous device tensor" % what)
+    return ctypes.c_void_p(t.data_ptr())
+
+
+class Context:
+    """Device + stream + workspace (smol_attn_ctx). Defaults to torch's current stream."""
+
+    def __init__(self, device=0, stream=None):
+        lib = load()
+        if stream is None:
+            import torch
+            stream = torch.cuda.current_stream(device).cuda_stream
+        self.h = ctypes.c_void_p()
+        _check(lib.smol_attn_ctx_create(device, ctypes.c_void_p(stream), ctypes.byref(self.h)),
+               "smol_attn_ctx_create")
+        self.device = device
+
+    def synchronize(self):
+        _check(load().smol_attn_ctx_synchronize(self.h), "synchronize")
+
+    def close(self):
+        if self.h:
+            load().smol_attn_ctx_destroy(self.h)
+            self.h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class RopeTable:
+    def __init__(self, ctx, head_dim, theta, rope_type=ROPE_NEOX, capacity=1024):
+        self.ctx = ctx
+        self.h = ctypes.c_void_p()
+        _check(load().smol_rope_table_create(ctx.h, head_dim, ctypes.c_float(theta), rope_type, capacity,
+                                             ctypes.byref(self.h)), "smol_rope_table_create")
+        self.head_dim, self.theta, self.rope_type = head_dim, theta, rope_type
+
+    @property
+    def capacity(self):
+        return load().smol_rope_table_capacity(self.h)
+
+    def ensure(self, required_pos):
+        _check(load().smol_rope_table_ensure(self.h, required_pos), "smol_rope_table_ensure")
+
+    def close(self):
+        if self.h:
+            load().smol_rope_table_destroy(self.h)
+            self.h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def rope_fill_host(pos0, n_pos, head_dim, theta, rope_type=ROPE_NEOX):
+    """Host rows [pos0, pos0 + n_pos) of the cos/sin table (qkn_decoder.c:261-311)."""
+    c = np.zeros((n_pos, head_dim), np.float32)
+    s = np.zeros_like(c)
+    load().smol_rope_fill_host(c.ctypes.data_as(_FP), s.ctypes.data_as(_FP), pos0, n_pos, head_dim,
+                               ctypes.c_float(theta), rope_type)
+    return c, s
+
+
+class KVCache:
+    """Device bf16 KV cache: layers x slots x kv_heads x capacity x head_dim."""
+
+    def __init__(self, ctx, n_layers, n_slots, n_kv_heads, head_dim, max_seq):
+        self.ctx = ctx
+        self.h = ctypes.c_void_p()
+        _check(load().smol_kv_cache_create(ctx.h, n_layers, n_slots, n_kv_heads, head_dim, max_seq,
+                                           ctypes.byref(self.h)), "smol_kv_cache_create")
+        self.n_layers, self.n_slots, self.n_kv_heads, self.head_dim = n_layers, n_slots, n_kv_heads, head_dim
+
+    @property
+    def capacity(self):
+        return load().smol_kv_cache_capacity(self.h)
+
+    def reserve(self, required_pos):
+        _check(load().smol_kv_cache_reserve(self.h, required_pos), "smol_kv_cache_reserve")
+
+    def write(self, layer, slot, pos0, k, v):
+        """Write already-rotated rows [pos0, pos0+n) from host numpy (f32 or bf16 bits as uint16) or device tensors."""
+        if isinstance(k, np.ndarray):
+            dt = BF16 if k.dtype == np.uint16 else F32
+            k = np.ascontiguousarray(k, np.uint16 if dt == BF16 else np.float32)
+            v = np.ascontiguousarray(v, k.dtype)
+            n = k.shape[0]
+            _check(load().smol_kv_cache_write(self.h, layer, slot, pos0, n, k.ctypes.data_as(_vp),
+                                              v.ctypes.data_as(_vp), dt, 0), "smol_kv_cache_write")
+        else:
+            n = k.shape[0]
+            _check(load().smol_kv_cache_write(self.h, layer, slot, pos0, n, _dev(k, "k"), _dev(v, "v"),
+                                              _dtype_code(k), 1), "smol_kv_cache_write")
+
+    def read(self, layer, slot, pos0, n):
+        """bf16 bits (uint16) [n][kv_heads*head_dim] of K and V."""
+        w = self.n_kv_heads * self.head_dim
+        k = np.zeros((n, w), np.uint16)
+        v = np.zeros((n, w), np.uint16)
+        _check(load().smol_kv_cache_read(self.h, layer, slot, pos0, n, k.ctypes.data_as(_U16P),
+                                         v.ctypes.data_as(_U16P)), "smol_kv_cache_read")
+        return k, v
+
+    def close(self):
+        if self.h:
+            load().smol_kv_cache_destroy(self.h)
+            self.h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _out_like(q_rows, n_heads, head_dim, device, out):
+    import torch
+    if out is None:
+        out = torch.empty((q_rows, n_heads * head_dim), dtype=torch.float32, device=device)
+    return out
+
+
+def prefill(ctx, kv, layer, slot, rope, pos0, q, k_new, v_new, n_heads, scale, window=0, cap=0.0, out=None):
+    """Chunked prefill of one sequence; see smol_attn_prefill."""
+    seq_q = q.shape[0]
+    out = _out_like(seq_q, n_heads, kv.head_dim, q.device, out)
+    _check(load().smol_attn_prefill(ctx.h, kv.h, layer, slot, rope.h if rope else None, pos0, seq_q,
+                                    _dev(q, "q"), _dev(k_new, "k"), _dev(v_new, "v"), _dtype_code(q),
+                                    n_heads, ctypes.c_float(scale), window, ctypes.c_float(cap),
+                                    _dev(out, "out")), "smol_attn_prefill")
+    return out
+
+
+def decode(ctx, kv, layer, rope, slots, pos, q, k_new, v_new, n_heads, scale, window=0, cap=0.0, out=None):
+    """Batched single-token decode; see smol_attn_decode."""
+    slots = np.ascontiguousarray(slots, np.int32)
+    pos = np.ascontiguousarray(pos, np.int32)
+    n = len(slots)
+    out = _out_like(n, n_heads, kv.head_dim, q.device, out)
+    _check(load().smol_attn_decode(ctx.h, kv.h, layer, rope.h if rope else None, n,
+                                   slots.ctypes.data_as(_IP), pos.ctypes.data_as(_IP), _dev(q, "q"),
+                                   _dev(k_new, "k"), _dev(v_new, "v"), _dtype_code(q), n_heads,
+                                   ctypes.c_float(scale), window, ctypes.c_float(cap), _dev(out, "out")),
+           "smol_attn_decode")
+    return out
+
+
+def causal(ctx, q, k, v, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset, window=0, cap=0.0,
+           out=None):
+    out = _out_like(seq_q, n_heads, head_dim, q.device, out)
+    _check(load().smol_attn_causal(ctx.h, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), _dtype_code(q), seq_q,
+                                   seq_k, n_heads, n_kv_heads, head_dim, ctypes.c_float(scale), q_offset,
+                                   window, ctypes.c_float(cap), _dev(out, "out")), "smol_attn_causal")
+    return out
+
+
+def bidirectional(ctx, q, k, v, seq, n_heads, head_dim, scale, window_starts, out=None):
+    ws = np.ascontiguousarray(window_starts, np.int32)
+    out = _out_like(seq, n_heads, head_dim, q.device, out)
+    _check(load().smol_attn_bidirectional(ctx.h, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), _dtype_code(q), seq,
+                                          n_heads, head_dim, ctypes.c_float(scale), ws.ctypes.data_as(_IP),
+                                          len(ws) - 1, _dev(out, "out")), "smol_attn_bidirectional")
+    return out
+
+
+def apply_rope(ctx, rope, x, positions, n_heads):
+    pos = np.ascontiguousarray(positions, np.int32)
+    _check(load().smol_attn_apply_rope(ctx.h, rope.h, _dev(x, "x"), pos.ctypes.data_as(_IP), len(pos), n_heads),
+           "smol_attn_apply_rope")
+    return x
+
+
+# ----------------------------------------------- reference-signature drop-ins
+
+def _f32(a):
+    a = np.ascontiguousarray(a, np.float32)
+    return a, a.ctypes.data_as(_FP)
+
+
+def smol_causal_attention(out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset):
+    assert out.dtype == np.float32 and out.flags.c_contiguous
+    Qa, q = _f32(Q); Ka, k = _f32(K); Va, v = _f32(V)
+    load().smol_causal_attention(out.ctypes.data_as(_FP), q, k, v, seq_q, seq_k, n_heads, n_kv_heads, head_dim,
+                                 ctypes.c_float(scale), q_offset)
+
+
+def smol_sliding_window_attention(out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset,
+                                  window_size):
+    assert out.dtype == np.float32 and out.flags.c_contiguous
+    Qa, q = _f32(Q); Ka, k = _f32(K); Va, v = _f32(V)
+    load().smol_sliding_window_attention(out.ctypes.data_as(_FP), q, k, v, seq_q, seq_k, n_heads, n_kv_heads,
+                                         head_dim, ctypes.c_float(scale), q_offset, window_size)
+
+
+def smol_causal_attention_softcap(out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset, cap):
+    assert out.dtype == np.float32 and out.flags.c_contiguous
+    Qa, q = _f32(Q); Ka, k = _f32(K); Va, v = _f32(V)
+    load().smol_causal_attention_softcap(out.ctypes.data_as(_FP), q, k, v, seq_q, seq_k, n_heads, n_kv_heads,
+                                         head_dim, ctypes.c_float(scale), q_offset, ctypes.c_float(cap))
+
+
+def smol_sliding_window_attention_softcap(out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale,
+                                          q_offset, window_size, cap):
+    assert out.dtype == np.float32 and out.flags.c_contiguous
+    Qa, q = _f32(Q); Ka, k = _f32(K); Va, v = _f32(V)
+    load().smol_sliding_window_attention_softcap(out.ctypes.data_as(_FP), q, k, v, seq_q, seq_k, n_heads,
+                                                 n_kv_heads, head_dim, ctypes.c_float(scale), q_offset,
+                                                 window_size, ctypes.c_float(cap))
+
+
+def smol_bidirectional_attention(out, Q, K, V, seq, n_heads, head_dim, scale, window_starts, n_windows):
+    assert out.dtype == np.float32 and out.flags.c_contiguous
+    Qa, q = _f32(Q); Ka, k = _f32(K); Va, v = _f32(V)
+    ws = np.ascontiguousarray(window_starts, np.int32)
+    load().smol_bidirectional_attention(out.ctypes.data_as(_FP), q, k, v, seq, n_heads, head_dim,
+                                        ctypes.c_float(scale), ws.ctypes.data_as(_IP), n_windows)
+
+
+def smol_compute_rope_neox(cos_out, sin_out, positions, seq, head_dim, theta):
+    pos = np.ascontiguousarray(positions, np.int32)
+    load().smol_compute_rope_neox(cos_out.ctypes.data_as(_FP), sin_out.ctypes.data_as(_FP),
+                                  pos.ctypes.data_as(_IP), seq, head_dim, ctypes.c_float(theta))
+
+
+def smol_compute_rope_interleaved(cos_out, sin_out, positions, seq, head_dim, theta):
+    pos = np.ascontiguousarray(positions, np.int32)
+    load().smol_compute_rope_interleaved(cos_out.ctypes.data_as(_FP), sin_out.ctypes.data_as(_FP),
+                                         pos.ctypes.data_as(_IP), seq, head_dim, ctypes.c_float(theta))
+
+
+def smol_apply_rope_neox(x, cos_vals, sin_vals, seq, n_heads, head_dim):
+    assert x.dtype == np.float32 and x.flags.c_contiguous
+    Ca, c = _f32(cos_vals); Sa, s = _f32(sin_vals)
+    load().smol_apply_rope_neox(x.ctypes.data_as(_FP), c, s, seq, n_heads, head_dim)
+
+
+def smol_apply_rope_interleaved(x, cos_vals, sin_vals, seq, n_heads, head_dim):
+    assert x.dtype == np.float32 and x.flags.c_contiguous
+    Ca, c = _f32(cos_vals); Sa, s = _f32(sin_vals)
+    load().smol_apply_rope_interleaved(x.ctypes.data_as(_FP), c, s, seq, n_heads, head_dim)

@@ -1,0 +1,207 @@
+"""The five attention workloads, as seeded synthetic inputs (numpy, host).
+
+Each workload is named by what it is; sizes follow the calls the reference's
+callers make (common/decoder/qkn_decoder.c:525-527 / :674-676,
+common/vision/siglip.c:126-128, exports/qwen_asr/qwen_asr.c:1595-1620):
+
+  qwen06b_decode      Qwen3-ASR-0.6B decoder, one decode step: Hq 16, Hkv 8,
+                      hd 128, 1024 cached keys + the new token at position
+                      1024 (seq_k 1025); NeoX RoPE theta 1e6.
+  qwen06b_prefill     Qwen3-ASR-0.6B causal prefill, 1536 tokens, Hq 16,
+                      Hkv 8, hd 128, bf16 Q/K/V, NeoX RoPE theta 1e6 over
+                      positions 0..1535.
+  siglip_bidir        SigLIP-so400m vision attention, 4 images x 256 patch
+                      tokens, 16 heads, hd 72, bf16 ~N(0, 0.5^2), one window per
+                      image, no RoPE, scale 1/sqrt(72).
+  gemma_mqa_decode    Gemma-2B-style MQA decode of 16 independent sequences:
+                      Hq 8, Hkv 1, hd 256, lengths L_i = 512 + (u64 % 3585),
+                      the new token at position L_i - 1; interleaved RoPE
+                      theta 1e4 (the Gemma / PaliGemma pairing).
+  qwen17b_stream      Qwen3-ASR-1.7B streaming: a 26-token chunk at positions
+                      8192..8217 on an 8192-token bf16 cache (chunked
+                      prefill), then 64 single-token decode steps.
+
+Cached rows are bf16 (round to nearest even) and are already rotated, as a
+decoder leaves them; the tokens a call appends are fp32 (projection outputs)
+unless the workload says bf16. The CPU oracle consumes the same bits widened
+to fp32.
+"""
+import numpy as np
+
+from . import synth
+
+ROPE_NEOX, ROPE_INTERLEAVED = 0, 1
+
+
+def scale_of(hd):
+    return float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+
+
+class Workload:
+    name = ""
+
+    def describe(self):
+        return {"workload": self.name}
+
+
+class Decode(Workload):
+    """Batched single-token decode: per sequence i, cache rows [0, pos_i) and one new token at pos_i."""
+
+    def __init__(self, name, Hq, Hkv, hd, lengths, theta, rope_type, seed, std=1.0):
+        self.name, self.Hq, self.Hkv, self.hd = name, Hq, Hkv, hd
+        self.lengths = [int(x) for x in lengths]  # seq_k of each sequence (new token included)
+        self.theta, self.rope_type, self.seed, self.std = theta, rope_type, seed, std
+        self.scale = scale_of(hd)
+
+    @property
+    def n_seq(self):
+        return len(self.lengths)
+
+    @property
+    def positions(self):
+        return np.array([L - 1 for L in self.lengths], np.int32)
+
+    def inputs(self):
+        """cache_k/cache_v: list of bf16 bit arrays [L_i - 1, Hkv*hd]; q [n, Hq*hd] f32; k/v new [n, Hkv*hd] f32."""
+        s = self.seed * 100
+        w = self.Hkv * self.hd
+        ck = [synth.f32_to_bf16_bits(synth.normal(s + 10 + 2 * i, (L - 1, w), self.std))
+              for i, L in enumerate(self.lengths)]
+        cv = [synth.f32_to_bf16_bits(synth.normal(s + 11 + 2 * i, (L - 1, w), self.std))
+              for i, L in enumerate(self.lengths)]
+        q = synth.normal(s + 1, (self.n_seq, self.Hq * self.hd), self.std)
+        k = synth.normal(s + 2, (self.n_seq, w), self.std)
+        v = synth.normal(s + 3, (self.n_seq, w), self.std)
+        return dict(cache_k=ck, cache_v=cv, q=q, k=k, v=v)
+
+    def kv_bytes(self):
+        return sum(self.lengths) * self.Hkv * self.hd * 2 * 2
+
+    def algorithmic_bytes(self):
+        """K+V bf16 of every visible key, Q and out fp32 (and the appended row)."""
+        return self.kv_bytes() + self.n_seq * self.Hq * self.hd * 4 * 2
+
+    def flops(self):
+        return sum(4 * self.hd * self.Hq * L for L in self.lengths)
+
+    def describe(self):
+        return {"workload": self.name, "n_seq": self.n_seq, "n_heads": self.Hq, "n_kv_heads": self.Hkv,
+                "head_dim": self.hd, "seq_k": self.lengths if self.n_seq <= 4 else
+                {"sum": int(sum(self.lengths)), "min": min(self.lengths), "max": max(self.lengths)},
+                "rope_theta": self.theta, "rope": "neox" if self.rope_type == ROPE_NEOX else "interleaved"}
+
+
+class Prefill(Workload):
+    """Causal (chunked) prefill of one sequence: cache rows [0, pos0) + seq_q new tokens."""
+
+    def __init__(self, name, Hq, Hkv, hd, pos0, seq_q, theta, seed, in_bf16=True, std=1.0):
+        self.name, self.Hq, self.Hkv, self.hd = name, Hq, Hkv, hd
+        self.pos0, self.seq_q, self.theta, self.seed = pos0, seq_q, theta, seed
+        self.in_bf16, self.std = in_bf16, std
+        self.rope_type = ROPE_NEOX
+        self.scale = scale_of(hd)
+
+    def inputs(self):
+        s = self.seed * 100
+        w = self.Hkv * self.hd
+        q = synth.normal(s + 1, (self.seq_q, self.Hq * self.hd), self.std)
+        k = synth.normal(s + 2, (self.seq_q, w), self.std)
+        v = synth.normal(s + 3, (self.seq_q, w), self.std)
+        if self.in_bf16:
+            q, k, v = (synth.f32_to_bf16_bits(x) for x in (q, k, v))
+        ck = synth.f32_to_bf16_bits(synth.normal(s + 4, (self.pos0, w), self.std))
+        cv = synth.f32_to_bf16_bits(synth.normal(s + 5, (self.pos0, w), self.std))
+        return dict(cache_k=ck, cache_v=cv, q=q, k=k, v=v)
+
+    def pairs(self):
+        """unmasked (query, key) pairs: sum over rows of pos0 + i + 1"""
+        return self.seq_q * self.pos0 + self.seq_q * (self.seq_q + 1) // 2
+
+    def flops(self):
+        return 4 * self.hd * self.Hq * self.pairs()
+
+    def algorithmic_bytes(self):
+        e = 2 if self.in_bf16 else 4
+        return (self.seq_q * (self.Hq + 2 * self.Hkv) * self.hd * e + self.pos0 * self.Hkv * self.hd * 4
+                + self.seq_q * self.Hq * self.hd * 4)
+
+    def describe(self):
+        return {"workload": self.name, "n_heads": self.Hq, "n_kv_heads": self.Hkv, "head_dim": self.hd,
+                "pos0": self.pos0, "seq_q": self.seq_q, "causal": True, "rope_theta": self.theta,
+                "inputs": "bf16" if self.in_bf16 else "f32"}
+
+
+class Bidir(Workload):
+    def __init__(self, name, H, hd, window_starts, seed, std=0.5):
+        self.name, self.H, self.hd = name, H, hd
+        self.window_starts = list(window_starts)
+        self.seq = window_starts[-1]
+        self.seed, self.std = seed, std
+        self.scale = scale_of(hd)
+
+    def inputs(self):
+        s = self.seed * 100
+        shp = (self.seq, self.H * self.hd)
+        return dict(q=synth.f32_to_bf16_bits(synth.normal(s + 1, shp, self.std)),
+                    k=synth.f32_to_bf16_bits(synth.normal(s + 2, shp, self.std)),
+                    v=synth.f32_to_bf16_bits(synth.normal(s + 3, shp, self.std)))
+
+    def flops(self):
+        ws = self.window_starts
+        return sum(4 * self.hd * self.H * (b - a) ** 2 for a, b in zip(ws[:-1], ws[1:]))
+
+    def algorithmic_bytes(self):
+        return self.seq * self.H * self.hd * (3 * 2 + 4)
+
+    def describe(self):
+        return {"workload": self.name, "n_heads": self.H, "head_dim": self.hd,
+                "windows": len(self.window_starts) - 1, "tokens": self.seq, "inputs": "bf16"}
+
+
+class Stream(Workload):
+    """Chunked prefill of `chunk` tokens on a `prefix`-token cache, then `steps` decode steps."""
+
+    def __init__(self, name, Hq, Hkv, hd, prefix, chunk, steps, theta, seed):
+        self.name, self.Hq, self.Hkv, self.hd = name, Hq, Hkv, hd
+        self.prefix, self.chunk, self.steps, self.theta, self.seed = prefix, chunk, steps, theta, seed
+        self.rope_type = ROPE_NEOX
+        self.scale = scale_of(hd)
+
+    def inputs(self):
+        s = self.seed * 100
+        w = self.Hkv * self.hd
+        return dict(cache_k=synth.f32_to_bf16_bits(synth.normal(s + 4, (self.prefix, w))),
+                    cache_v=synth.f32_to_bf16_bits(synth.normal(s + 5, (self.prefix, w))),
+                    q=synth.normal(s + 1, (self.chunk, self.Hq * self.hd)),
+                    k=synth.normal(s + 2, (self.chunk, w)),
+                    v=synth.normal(s + 3, (self.chunk, w)),
+                    dq=synth.normal(s + 6, (self.steps, self.Hq * self.hd)),
+                    dk=synth.normal(s + 7, (self.steps, w)),
+                    dv=synth.normal(s + 8, (self.steps, w)))
+
+    def chunk_flops(self):
+        return 4 * self.hd * self.Hq * sum(self.prefix + i + 1 for i in range(self.chunk))
+
+    def decode_bytes(self):
+        p = self.prefix + self.chunk
+        return sum((p + s + 1) * self.Hkv * self.hd * 4 for s in range(self.steps))
+
+    def describe(self):
+        return {"workload": self.name, "n_heads": self.Hq, "n_kv_heads": self.Hkv, "head_dim": self.hd,
+                "prefix": self.prefix, "chunk": self.chunk, "decode_steps": self.steps,
+                "rope_theta": self.theta}
+
+
+def gemma_lengths(seed=4, n=16, lo=512, hi=4096):
+    return [int(x) for x in synth.uniform_int(seed * 1000 + 7, n, lo, hi)]
+
+
+def all_workloads():
+    return {
+        "qwen06b_decode": Decode("qwen06b_decode", 16, 8, 128, [1025], 1e6, ROPE_NEOX, seed=1),
+        "qwen06b_prefill": Prefill("qwen06b_prefill", 16, 8, 128, 0, 1536, 1e6, seed=2),
+        "siglip_bidir": Bidir("siglip_bidir", 16, 72, [0, 256, 512, 768, 1024], seed=3),
+        "gemma_mqa_decode": Decode("gemma_mqa_decode", 8, 1, 256, gemma_lengths(), 1e4, ROPE_INTERLEAVED,
+                                   seed=4),
+        "qwen17b_stream": Stream("qwen17b_stream", 16, 8, 128, 8192, 26, 64, 1e6, seed=5),
+    }

@@ -1,0 +1,290 @@
+"""HIP path against the CPU oracle (and the compiled reference's golden vectors), on the GPU.
+
+Every case prints its name before it runs. The bar is |gpu - cpu| <= 2e-3 +
+1e-2 |cpu| for every element (conftest.ATOL / RTOL), on fp32 outputs.
+"""
+import numpy as np
+import pytest
+
+from conftest import assert_parity, pkg, synth  # noqa: F401
+from gen_golden_inputs import bidir_inputs, causal_inputs
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def sa():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from smol_genius_amd import smol_attn
+    smol_attn.load()
+    return smol_attn
+
+
+@pytest.fixture(scope="module")
+def ctx(sa):
+    c = sa.Context(0)
+    yield c
+    c.close()
+
+
+@pytest.fixture(scope="module")
+def wo():
+    import workload_oracle
+    return workload_oracle
+
+
+def dev(a, bf16=False):
+    if bf16:
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda().view(torch.bfloat16)
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+
+
+def widen(b):
+    return synth.bf16_bits_to_f32(b)
+
+
+# ------------------------------------------------------------- full workloads
+
+@pytest.mark.parametrize("name", ["qwen06b_decode", "qwen06b_prefill", "siglip_bidir", "gemma_mqa_decode",
+                                  "qwen17b_stream"])
+def test_workload_full_size(ctx, oracle, wo, name):
+    from smol_genius_amd import runner, workloads
+    print("case", name, flush=True)
+    wl = workloads.all_workloads()[name]
+    x = wl.inputs()
+    r = runner.prepare(ctx, wl, x)
+    r.step()
+    got = r.outputs()
+    want = wo.evaluate(oracle, wl, x)
+    if isinstance(want, tuple):
+        a = assert_parity(got[0], want[0], name + " chunk")
+        b = assert_parity(got[1], want[1], name + " decode")
+        print(name, "chunk", a, "decode", b)
+    else:
+        print(name, assert_parity(got, want, name))
+    # a second pass over the same inputs gives the same bits (appends are idempotent)
+    r.step()
+    again = r.outputs()
+    if isinstance(got, list):
+        for u, w in zip(got, again):
+            np.testing.assert_array_equal(u, w)
+    else:
+        np.testing.assert_array_equal(got, again)
+
+
+# ---------------------------------------------- reference golden vectors
+
+def test_golden_causal_through_reference_signature(sa, golden):
+    meta, data = golden
+    for c in meta["causal"]:
+        print("golden", c["name"], flush=True)
+        Q, K, V = causal_inputs(c["seed"], c["Hq"], c["Hkv"], c["hd"], c["seq_q"], c["seq_k"])
+        out = np.full((c["seq_q"], c["Hq"] * c["hd"]), np.nan, np.float32)
+        args = (out, Q, K, V, c["seq_q"], c["seq_k"], c["Hq"], c["Hkv"], c["hd"], c["scale"], c["q_offset"])
+        if c["window"] > 0 and c["cap"] > 0:
+            sa.smol_sliding_window_attention_softcap(*args, c["window"], c["cap"])
+        elif c["window"] > 0:
+            sa.smol_sliding_window_attention(*args, c["window"])
+        elif c["cap"] > 0:
+            sa.smol_causal_attention_softcap(*args, c["cap"])
+        else:
+            sa.smol_causal_attention(*args)
+        assert_parity(out, data[c["name"]], c["name"])
+
+
+def test_golden_bidirectional_through_reference_signature(sa, golden):
+    meta, data = golden
+    for b in meta["bidir"]:
+        print("golden", b["name"], flush=True)
+        ws = b["window_starts"]
+        seq = ws[-1]
+        Q, K, V = bidir_inputs(b["seed"], b["H"], b["hd"], seq, b["std"])
+        out = np.zeros((seq, b["H"] * b["hd"]), np.float32)
+        sa.smol_bidirectional_attention(out, Q, K, V, seq, b["H"], b["hd"], b["scale"], ws, len(ws) - 1)
+        assert_parity(out, data[b["name"]], b["name"])
+
+
+def test_golden_rope_through_reference_signature(sa, golden):
+    meta, data = golden
+    for r in meta["rope"]:
+        n = len(r["positions"])
+        pos = np.array(r["positions"], np.int32)
+        c = np.zeros((n, r["hd"]), np.float32)
+        s = np.zeros_like(c)
+        (sa.smol_compute_rope_interleaved if r["interleaved"] else sa.smol_compute_rope_neox)(
+            c, s, pos, n, r["hd"], r["theta"])
+        tol = 2e-7 * pos[:, None].astype(np.float64) + 2e-7
+        assert (np.abs(c - data[r["tag"] + "_cos"]) <= tol).all(), r["tag"]
+        x = synth.normal(r["seed"], (n, 3 * r["hd"]))
+        (sa.smol_apply_rope_interleaved if r["interleaved"] else sa.smol_apply_rope_neox)(
+            x, data[r["tag"] + "_cos"], data[r["tag"] + "_sin"], n, 3, r["hd"])
+        np.testing.assert_allclose(x, data[r["tag"] + "_applied"], rtol=1e-6, atol=1e-6)
+
+
+# ------------------------------------------------------------ shapes and edges
+
+CAUSAL_SHAPES = [  # Hq, Hkv, hd, seq_q, seq_k, q_offset, bf16
+    (4, 4, 64, 33, 33, 0, False), (8, 2, 72, 17, 50, 33, True), (6, 2, 80, 5, 70, 65, False),
+    (4, 1, 96, 40, 40, 0, True), (16, 8, 128, 1, 1, 0, False), (16, 8, 128, 70, 130, 60, True),
+    (8, 1, 256, 3, 200, 197, False), (2, 2, 256, 48, 48, 0, True), (32, 2, 128, 2, 90, 88, False),
+    (4, 2, 64, 9, 20, -3, False), (4, 2, 128, 6, 10, 30, False), (16, 16, 64, 100, 300, 200, True),
+]
+
+
+@pytest.mark.parametrize("shape", CAUSAL_SHAPES)
+def test_causal_shapes(ctx, sa, oracle, shape):
+    Hq, Hkv, hd, sq, sk, qo, bf = shape
+    print("causal", shape, flush=True)
+    Q = synth.normal(7, (sq, Hq * hd))
+    K = synth.normal(8, (sk, Hkv * hd))
+    V = synth.normal(9, (sk, Hkv * hd))
+    if bf:
+        Q, K, V = (synth.round_bf16(a) for a in (Q, K, V))
+    sc = 1.0 / np.sqrt(hd)
+    conv = (lambda a: dev(synth.f32_to_bf16_bits(a), True)) if bf else dev
+    out = sa.causal(ctx, conv(Q), conv(K), conv(V), sq, sk, Hq, Hkv, hd, sc, qo)
+    got = out.cpu().numpy()
+    want = oracle.causal_attention(Q, K, V, sq, sk, Hq, Hkv, hd, sc, qo)
+    assert_parity(got, want, str(shape))
+    if qo < 0:
+        assert not got[:-qo].any()
+
+
+@pytest.mark.parametrize("window,cap", [(16, 0.0), (0, 30.0), (40, 50.0), (1, 0.0)])
+def test_window_softcap(ctx, sa, oracle, window, cap):
+    Hq, Hkv, hd, sq, sk, qo = 8, 4, 128, 37, 150, 113
+    Q = synth.normal(17, (sq, Hq * hd), 2.0)
+    K = synth.normal(18, (sk, Hkv * hd), 2.0)
+    V = synth.normal(19, (sk, Hkv * hd))
+    sc = 1.0 / np.sqrt(hd)
+    got = sa.causal(ctx, dev(Q), dev(K), dev(V), sq, sk, Hq, Hkv, hd, sc, qo, window=window, cap=cap).cpu().numpy()
+    want = oracle.causal_attention(Q, K, V, sq, sk, Hq, Hkv, hd, sc, qo, window=window, cap=cap)
+    assert_parity(got, want, "window %d cap %g" % (window, cap))
+
+
+def test_bidirectional_ragged(ctx, sa, oracle):
+    for H, hd, ws in [(3, 72, [0, 1, 33, 34, 100, 257]), (2, 64, [5, 40, 41]), (4, 128, [0, 64, 128])]:
+        seq = ws[-1]
+        Q, K, V = (synth.round_bf16(synth.normal(30 + i, (seq, H * hd))) for i in range(3))
+        sc = 1.0 / np.sqrt(hd)
+        out = torch.zeros((seq, H * hd), dtype=torch.float32, device="cuda")
+        b = lambda a: dev(synth.f32_to_bf16_bits(a), True)  # noqa: E731
+        got = sa.bidirectional(ctx, b(Q), b(K), b(V), seq, H, hd, sc, ws, out=out).cpu().numpy()
+        want = oracle.bidirectional_attention(Q, K, V, seq, H, hd, sc, ws)
+        lo = ws[0]
+        assert_parity(got[lo:], want[lo:], "bidir %s" % ws)
+        assert not got[:lo].any()
+
+
+@pytest.mark.parametrize("P,S", [(0, 1), (0, 33), (5, 7), (31, 1), (32, 32), (40, 64), (63, 2), (100, 26)])
+@pytest.mark.parametrize("rope_type", [0, 1])
+def test_prefill_chunks(ctx, sa, oracle, wo, P, S, rope_type):
+    from smol_genius_amd.workloads import Prefill
+    print("prefill", P, S, rope_type, flush=True)
+    wl = Prefill("t", 8, 2, 128, P, S, 1e4 if rope_type else 1e6, seed=50 + P + S, in_bf16=(S % 2 == 0))
+    wl.rope_type = rope_type
+    x = wl.inputs()
+    kv = sa.KVCache(ctx, 1, 1, 2, 128, P + S)
+    if P:
+        kv.write(0, 0, 0, x["cache_k"], x["cache_v"])
+    rope = sa.RopeTable(ctx, 128, wl.theta, rope_type)
+    bf = wl.in_bf16
+    got = sa.prefill(ctx, kv, 0, 0, rope, P, dev(x["q"], bf), dev(x["k"], bf), dev(x["v"], bf), 8, wl.scale)
+    want = wo.prefill(oracle, wl, x)
+    assert_parity(got.cpu().numpy(), want, "prefill P=%d S=%d" % (P, S))
+    # the cache now holds the rotated new K (bf16, nearest even) and V
+    k_rows, v_rows = kv.read(0, 0, P, S)
+    pos = np.arange(P, P + S)
+    c, s = wo.rope_rows(oracle, pos, 128, wl.theta, rope_type == 1)
+    kn = oracle.apply_rope(wo._as_f32(x["k"]), c, s, S, 2, 128, rope_type == 1)
+    exact = (k_rows == synth.f32_to_bf16_bits(kn)).mean()
+    assert exact > 0.999, exact
+    np.testing.assert_array_equal(v_rows, synth.f32_to_bf16_bits(wo._as_f32(x["v"])))
+
+
+@pytest.mark.parametrize("positions", [[0], [1], [31], [32], [33], [64, 0, 95, 7], [1000, 31, 4095]])
+def test_decode_positions(ctx, sa, oracle, wo, positions):
+    from smol_genius_amd import runner
+    from smol_genius_amd.workloads import Decode
+    print("decode", positions, flush=True)
+    for hq, hkv, hd, rt in [(16, 8, 128, 0), (8, 1, 256, 1), (4, 4, 64, 0)]:
+        wl = Decode("t", hq, hkv, hd, [p + 1 for p in positions], 1e4, rt, seed=60 + len(positions))
+        x = wl.inputs()
+        r = runner.prepare(ctx, wl, x)
+        r.step()
+        assert_parity(r.outputs(), wo.decode(oracle, wl, x), "decode %s hd %d" % (positions, hd))
+
+
+def test_cache_roundtrip_growth_and_rewind(ctx, sa, oracle, wo):
+    from smol_genius_amd.workloads import Prefill
+    Hkv, hd = 2, 64
+    kv = sa.KVCache(ctx, 2, 2, Hkv, hd, 40)
+    assert kv.capacity == 64
+    k = synth.f32_to_bf16_bits(synth.normal(70, (50, Hkv * hd)))
+    v = synth.f32_to_bf16_bits(synth.normal(71, (50, Hkv * hd)))
+    kv.write(1, 1, 10, k, v)
+    rk, rv = kv.read(1, 1, 10, 50)
+    np.testing.assert_array_equal(rk, k)
+    np.testing.assert_array_equal(rv, v)
+    # f32 rows are stored rounded to nearest even
+    kf = synth.normal(72, (3, Hkv * hd))
+    kv.write(0, 0, 0, kf, kf)
+    np.testing.assert_array_equal(kv.read(0, 0, 0, 3)[0], synth.f32_to_bf16_bits(kf))
+    # growth (doubling) keeps every row of every layer and slot
+    kv.reserve(200)
+    assert kv.capacity == 256
+    rk, rv = kv.read(1, 1, 10, 50)
+    np.testing.assert_array_equal(rk, k)
+    np.testing.assert_array_equal(rv, v)
+    np.testing.assert_array_equal(kv.read(0, 0, 0, 3)[0], synth.f32_to_bf16_bits(kf))
+    # rewind: prefill 60 tokens, then re-prefill from position 20 with other tokens;
+    # the second call must see rows [0, 20) of the first and its own rows only.
+    rope = sa.RopeTable(ctx, hd, 1e6, 0)
+    a = Prefill("a", 4, 2, 64, 0, 60, 1e6, seed=73)
+    xa = a.inputs()
+    sa.prefill(ctx, kv, 0, 1, rope, 0, dev(xa["q"], True), dev(xa["k"], True), dev(xa["v"], True), 4, a.scale)
+    b = Prefill("b", 4, 2, 64, 20, 25, 1e6, seed=74)
+    xb = b.inputs()
+    ck, cv = kv.read(0, 1, 0, 20)
+    xb["cache_k"], xb["cache_v"] = ck, cv
+    got = sa.prefill(ctx, kv, 0, 1, rope, 20, dev(xb["q"], True), dev(xb["k"], True), dev(xb["v"], True), 4,
+                     b.scale)
+    assert_parity(got.cpu().numpy(), wo.prefill(oracle, b, xb), "rewind")
+
+
+def test_prefill_grows_cache_and_table(ctx, sa, oracle, wo):
+    from smol_genius_amd.workloads import Prefill
+    kv = sa.KVCache(ctx, 1, 1, 2, 128, 16)
+    rope = sa.RopeTable(ctx, 128, 1e6, 0, 16)
+    wl = Prefill("g", 4, 2, 128, 0, 1100, 1e6, seed=75)
+    x = wl.inputs()
+    got = sa.prefill(ctx, kv, 0, 0, rope, 0, dev(x["q"], True), dev(x["k"], True), dev(x["v"], True), 4, wl.scale)
+    assert kv.capacity >= 1100 and rope.capacity >= 1100
+    assert_parity(got.cpu().numpy(), wo.prefill(oracle, wl, x), "grow")
+
+
+def test_device_apply_rope(ctx, sa, oracle, wo):
+    for hd, rt in [(128, 0), (256, 1), (72, 0)]:
+        rope = sa.RopeTable(ctx, hd, 1e4, rt)
+        pos = np.array([0, 3, 1500, 77], np.int32)
+        x = synth.normal(80 + hd, (4, 3 * hd))
+        got = sa.apply_rope(ctx, rope, dev(x), pos, 3).cpu().numpy()
+        c, s = wo.rope_rows(oracle, pos, hd, 1e4, rt == 1)
+        np.testing.assert_allclose(got, oracle.apply_rope(x, c, s, 4, 3, hd, rt == 1), rtol=1e-6, atol=1e-6)
+
+
+def test_errors_are_reported(ctx, sa):
+    with pytest.raises(sa.SmolAttnError, match="head_dim"):
+        sa.KVCache(ctx, 1, 1, 2, 100, 16)
+    kv = sa.KVCache(ctx, 1, 2, 2, 64, 16)
+    q = torch.zeros((2, 4 * 64), device="cuda")
+    k = torch.zeros((2, 2 * 64), device="cuda")
+    with pytest.raises(sa.SmolAttnError, match="twice"):
+        sa.decode(ctx, kv, 0, None, [1, 1], [3, 4], q, k, k, 4, 0.125)
+    with pytest.raises(sa.SmolAttnError, match="multiple"):
+        sa.decode(ctx, kv, 0, None, [0], [3], q[:1], k[:1], k[:1], 3, 0.125)
+    with pytest.raises(sa.SmolAttnError, match="layer"):
+        sa.prefill(ctx, kv, 5, 0, None, 0, q, k, k, 4, 0.125)
