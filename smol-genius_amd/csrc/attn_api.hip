@@ -113,8 +113,12 @@ struct smol_attn_ctx {
     int cu_count = 256;
 };
 
+/* Tables and caches keep their own device and stream, so destroying them
+ * does not touch the context (which may already be gone). */
 struct smol_rope_table {
     smol_attn_ctx *ctx;
+    int device;
+    hipStream_t stream;
     int hd, type, cap;
     float theta;
     float *cos_d = nullptr, *sin_d = nullptr;
@@ -122,6 +126,8 @@ struct smol_rope_table {
 
 struct smol_kv_cache {
     smol_attn_ctx *ctx;
+    int device;
+    hipStream_t stream;
     int n_layers, n_slots, n_kv, hd, cap;
     uint16_t *k = nullptr, *vt = nullptr;
 };
@@ -262,6 +268,8 @@ extern "C" int smol_rope_table_create(smol_attn_ctx *ctx, int hd, float theta, i
     if (rc) return rc;
     smol_rope_table *rt = new smol_rope_table();
     rt->ctx = ctx;
+    rt->device = ctx->device;
+    rt->stream = ctx->stream;
     rt->hd = hd;
     rt->type = type;
     rt->theta = theta;
@@ -287,8 +295,8 @@ extern "C" int smol_rope_table_capacity(const smol_rope_table *rt) { return rt ?
 
 extern "C" int smol_rope_table_destroy(smol_rope_table *rt) {
     if (!rt) return SMOL_ATTN_OK;
-    hipSetDevice(rt->ctx->device);
-    hipStreamSynchronize(rt->ctx->stream);
+    hipSetDevice(rt->device);
+    hipStreamSynchronize(rt->stream);
     if (rt->cos_d) hipFree(rt->cos_d);
     if (rt->sin_d) hipFree(rt->sin_d);
     delete rt;
@@ -311,6 +319,8 @@ extern "C" int smol_kv_cache_create(smol_attn_ctx *ctx, int n_layers, int n_slot
     if (rc) return rc;
     smol_kv_cache *kv = new smol_kv_cache();
     kv->ctx = ctx;
+    kv->device = ctx->device;
+    kv->stream = ctx->stream;
     kv->n_layers = n_layers;
     kv->n_slots = n_slots;
     kv->n_kv = n_kv;
@@ -334,8 +344,8 @@ extern "C" int smol_kv_cache_create(smol_attn_ctx *ctx, int n_layers, int n_slot
 
 extern "C" int smol_kv_cache_destroy(smol_kv_cache *kv) {
     if (!kv) return SMOL_ATTN_OK;
-    hipSetDevice(kv->ctx->device);
-    hipStreamSynchronize(kv->ctx->stream);
+    hipSetDevice(kv->device);
+    hipStreamSynchronize(kv->stream);
     hipFree(kv->k);
     hipFree(kv->vt);
     delete kv;
@@ -801,16 +811,12 @@ extern "C" int smol_attn_apply_rope(smol_attn_ctx *ctx, const smol_rope_table *r
 
 namespace {
 
+/* Per-thread state of the drop-ins. It is never freed: releasing device
+ * memory from a thread-exit or static destructor can run after the HIP
+ * runtime has shut down; the process exit reclaims it. */
 struct Legacy {
     smol_attn_ctx *ctx = nullptr;
     DevBuf q, k, v, out, cs;
-    ~Legacy() {
-        if (!ctx) return;
-        DevBuf *bs[] = {&q, &k, &v, &out, &cs};
-        for (DevBuf *b : bs)
-            if (b->p) hipFree(b->p);
-        smol_attn_ctx_destroy(ctx);
-    }
 };
 
 thread_local Legacy g_legacy;

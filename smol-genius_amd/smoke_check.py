@@ -39,4 +39,6 @@ def run():
     r = runner.prepare(ctx, pre, x)
     r.step()
     _check("prefill", r.outputs(), wo.prefill(orc, pre, x))
+    r.kv.close()
+    r.rope.close()
     ctx.close()

@@ -11,8 +11,10 @@ The names mirror the reference's kernel API (common/kernels/smol_kernels.h):
 ``smol_sliding_window_attention_softcap``, ``smol_compute_rope_neox`` ... with
 the same argument meaning (``out`` is overwritten in place).
 """
+import atexit
 import ctypes
 import os
+import weakref
 
 import numpy as np
 
@@ -73,6 +75,18 @@ SIGNATURES = [
 ]
 
 _lib = None
+_live = weakref.WeakSet()  # open handles, closed at interpreter exit before the HIP runtime goes away
+
+
+@atexit.register
+def _close_all():
+    # caches and tables before contexts
+    objs = sorted(list(_live), key=lambda o: isinstance(o, Context))
+    for o in objs:
+        try:
+            o.close()
+        except Exception:
+            pass
 
 
 class SmolAttnError(RuntimeError):
@@ -128,6 +142,7 @@ class Context:
         _check(lib.smol_attn_ctx_create(device, ctypes.c_void_p(stream), ctypes.byref(self.h)),
                "smol_attn_ctx_create")
         self.device = device
+        _live.add(self)
 
     def synchronize(self):
         _check(load().smol_attn_ctx_synchronize(self.h), "synchronize")
@@ -151,6 +166,7 @@ class RopeTable:
         _check(load().smol_rope_table_create(ctx.h, head_dim, ctypes.c_float(theta), rope_type, capacity,
                                              ctypes.byref(self.h)), "smol_rope_table_create")
         self.head_dim, self.theta, self.rope_type = head_dim, theta, rope_type
+        _live.add(self)
 
     @property
     def capacity(self):
@@ -189,6 +205,7 @@ class KVCache:
         _check(load().smol_kv_cache_create(ctx.h, n_layers, n_slots, n_kv_heads, head_dim, max_seq,
                                            ctypes.byref(self.h)), "smol_kv_cache_create")
         self.n_layers, self.n_slots, self.n_kv_heads, self.head_dim = n_layers, n_slots, n_kv_heads, head_dim
+        _live.add(self)
 
     @property
     def capacity(self):

@@ -54,6 +54,7 @@ def parity_report(gpu, cpu):
 
 def assert_parity(gpu, cpu, what=""):
     r = parity_report(gpu, cpu)
+    print("parity %-40s max_abs %.3e ratio %.3f" % (what, r["max_abs"], r["ratio"]), flush=True)
     assert r["finite"], "%s: non-finite output" % what
     assert r["ratio"] <= 1.0, "%s: |gpu-cpu| exceeds %g + %g|cpu| (max_abs %.3e, ratio %.3f)" % (
         what, ATOL, RTOL, r["max_abs"], r["ratio"])

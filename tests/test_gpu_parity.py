@@ -153,11 +153,12 @@ def test_causal_shapes(ctx, sa, oracle, shape):
         assert not got[:-qo].any()
 
 
-@pytest.mark.parametrize("window,cap", [(16, 0.0), (0, 30.0), (40, 50.0), (1, 0.0)])
+@pytest.mark.parametrize("window,cap", [(16, 0.0), (0, 2.0), (40, 1.5), (1, 0.0), (7, 50.0)])
 def test_window_softcap(ctx, sa, oracle, window, cap):
+    # small caps so that tanh actually bends the N(0, 1) scores
     Hq, Hkv, hd, sq, sk, qo = 8, 4, 128, 37, 150, 113
-    Q = synth.normal(17, (sq, Hq * hd), 2.0)
-    K = synth.normal(18, (sk, Hkv * hd), 2.0)
+    Q = synth.normal(17, (sq, Hq * hd))
+    K = synth.normal(18, (sk, Hkv * hd))
     V = synth.normal(19, (sk, Hkv * hd))
     sc = 1.0 / np.sqrt(hd)
     got = sa.causal(ctx, dev(Q), dev(K), dev(V), sq, sk, Hq, Hkv, hd, sc, qo, window=window, cap=cap).cpu().numpy()
