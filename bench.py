@@ -1,0 +1,168 @@
+"""Benchmark of the MI355X attention path (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only NAME]
+
+Headline line: causal prefill of Qwen3-ASR-0.6B (1536 tokens, 16 Q heads,
+8 KV heads, head_dim 128, bf16 inputs, NeoX RoPE) in TFLOP/s of unmasked
+attention work, with every input resident in HBM when the timed region
+starts. A "step" is one smol_attn_prefill call (RoPE + cache append +
+attention). Steps rotate over `layers` distinct caches and input sets
+(>= 512 MB in total) so repeats stream HBM rather than the 256 MB
+last-level cache.
+
+The other workloads (decode, bidirectional, MQA decode, streaming chunk +
+decode) are measured the same way and reported under "detail".
+
+roofline: the attention kernel's own duration, from HIP events recorded
+around each launch on the context's stream during the timed steps;
+achieved = algorithmic flops (or bytes) per launch / mean kernel time.
+cpu_baseline: the reference's own CPU attention (oracle/_ref, compiled from
+the reference sources) on this host's cores, timed on the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_MFMA_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+MALL_BYTES = 256 << 20
+
+
+def layers_for(bytes_per_layer, lo=2, hi=64):
+    n = -(-2 * MALL_BYTES // max(1, bytes_per_layer))
+    return int(max(lo, min(hi, n)))
+
+
+def time_steps(ctx, run, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        run.step()
+    torch.cuda.synchronize()
+    ctx.timing_read()
+    ctx.set_timing(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        run.step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ctx.set_timing(False)
+    kt = ctx.timing_read()
+    return wall, kt
+
+
+def measure(ctx, wl, steps, warmup, runner, layers=None):
+    x = wl.inputs()
+    per_layer = getattr(wl, "algorithmic_bytes", lambda: 64 << 20)()
+    n_layers = layers or layers_for(per_layer)
+    run = runner.prepare(ctx, wl, x, layers=n_layers)
+    wall, kt = time_steps(ctx, run, steps, warmup)
+    return x, run, n_layers, wall, kt
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default=None, help="measure only this workload")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the attention would shard by KV "
+              "head with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import __graft_entry__
+    __graft_entry__.load_package()
+    from smol_genius_amd import runner, smol_attn as sa, workloads
+
+    sa.load()
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    ctx = sa.Context(0)
+    wls = workloads.all_workloads()
+    steps, warmup = args.steps, args.warmup
+
+    # ---------------- headline: causal prefill
+    main_wl = wls["qwen06b_prefill"]
+    detail = {}
+    if args.only in (None, main_wl.name):
+        x, run, n_layers, wall, kt = measure(ctx, main_wl, steps, warmup, runner)
+        flops = main_wl.flops()
+        ms_step = wall / steps * 1e3
+        attn_ms = kt["attn"][0] / max(1, kt["attn"][1])
+        prep_ms = kt["prep"][0] / max(1, kt["prep"][1])
+        value = flops / (wall / steps) / 1e12
+        achieved = flops / (attn_ms * 1e-3) / 1e12
+        head = {
+            "metric": "prefill attn TFLOP/s (causal, Qwen3-ASR-0.6B 1536 tokens)",
+            "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+            "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f16 MFMA operands, f32 softmax/accumulate (bf16 inputs and KV cache)",
+            "data": "synthetic (seeded N(0,1) bf16 Q/K/V)",
+            "config": dict(main_wl.describe(), layers_rotated=n_layers, parallelism="single GPU"),
+            "roofline": {"bound": "mfma", "kernel": "k_attn_sk", "achieved": round(achieved, 3),
+                         "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_TFLOPS, 5),
+                         "traffic": None, "kernel_ms": round(attn_ms, 5), "prep_kernel_ms": round(prep_ms, 5),
+                         "flops_per_launch": flops},
+        }
+    else:
+        head = None
+
+    # ---------------- the other workloads
+    for name in ["qwen06b_decode", "gemma_mqa_decode", "siglip_bidir", "qwen17b_stream"]:
+        if args.only not in (None, name):
+            continue
+        wl = wls[name]
+        if name == "qwen17b_stream":
+            x, run, n_layers, wall, kt = measure(ctx, wl, max(3, steps // 10), max(1, warmup // 5), runner,
+                                                 layers=8)
+            n = max(3, steps // 10)
+            attn_ms, attn_n = kt["attn"]
+            # per step: 1 chunk launch + `steps` decode launches of the attention kernel
+            detail[name] = {"config": wl.describe(), "ms_per_step": round(wall / n * 1e3, 4),
+                            "attn_kernel_ms_total_per_step": round(attn_ms / n, 4),
+                            "decode_GBps_path": round(wl.decode_bytes() / (wall / n) / 1e9, 1),
+                            "note": "wall time per step includes 65 launches and their host dispatch"}
+            continue
+        x, run, n_layers, wall, kt = measure(ctx, wl, steps, warmup, runner)
+        attn_ms = kt["attn"][0] / max(1, kt["attn"][1])
+        prep_ms = kt["prep"][0] / max(1, kt["prep"][1])
+        d = {"config": wl.describe(), "layers_rotated": n_layers, "ms_per_step": round(wall / steps * 1e3, 5),
+             "attn_kernel_ms": round(attn_ms, 5), "prep_kernel_ms": round(prep_ms, 5)}
+        if name == "siglip_bidir":
+            f = wl.flops()
+            d.update(tflops_kernel=round(f / (attn_ms * 1e-3) / 1e12, 3),
+                     mfma_frac=round(f / (attn_ms * 1e-3) / 1e12 / PEAK_MFMA_TFLOPS, 5),
+                     hbm_GBps_kernel=round(wl.algorithmic_bytes() / (attn_ms * 1e-3) / 1e9, 1))
+        else:
+            b = wl.algorithmic_bytes()
+            d.update(GBps_kernel=round(b / (attn_ms * 1e-3) / 1e9, 1),
+                     hbm_frac_kernel=round(b / (attn_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 5),
+                     GBps_path=round(b / ((attn_ms + prep_ms) * 1e-3) / 1e9, 1),
+                     bytes_per_launch=b)
+        detail[name] = d
+
+    # ---------------- CPU baseline (reference CPU attention on this host)
+    cpu = None
+    if not args.no_cpu and head is not None:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import cpu_baseline
+        cpu = cpu_baseline.prefill_sample(main_wl, main_wl.inputs())
+        head["cpu_baseline"] = cpu
+    if head is None:
+        head = {"metric": "detail only", "value": None}
+    head["detail"] = detail
+    print(json.dumps(head), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -78,6 +78,15 @@ SMOL_ATTN_API int smol_attn_ctx_destroy(smol_attn_ctx *ctx);
 SMOL_ATTN_API int smol_attn_ctx_synchronize(smol_attn_ctx *ctx);
 SMOL_ATTN_API void *smol_attn_ctx_stream(smol_attn_ctx *ctx);
 
+/* Kernel timing (no counterpart in the reference, which only has wall-clock
+ * perf fields, exports/qwen_asr/qwen_asr.h:147-152): when enabled, every
+ * kernel the context launches is bracketed by HIP events on its stream.
+ * timing_read synchronizes the stream and returns, per kind
+ * (0 = RoPE/cache pre-pass, 1 = attention, 2 = other), the summed kernel
+ * milliseconds ms[3] and launch counts count[3] since the last read. */
+SMOL_ATTN_API int smol_attn_ctx_set_timing(smol_attn_ctx *ctx, int enable);
+SMOL_ATTN_API int smol_attn_ctx_timing_read(smol_attn_ctx *ctx, double *ms, int *count);
+
 /* ---- RoPE table ----------------------------------------------------------
  * Device fp32 cos/sin rows [capacity][head_dim], built on the host exactly as
  * fill_rope_cache does (common/decoder/qkn_decoder.c:261-311):

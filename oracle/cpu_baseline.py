@@ -1,0 +1,104 @@
+"""Times the reference's CPU attention on a workload. TEST/BENCH INFRASTRUCTURE ONLY.
+
+Uses oracle/_ref (the reference's own attention.c / rope.c / vecops /
+threading.c, compiled by oracle/Makefile) when it exists, otherwise the C
+restatement (liboracle). The timed call sequence is the reference decoder's
+attention block for the workload: smol_apply_rope_* on Q and the new K
+(qkn_decoder.c:493-495 / :647-649), then smol_causal_attention or
+smol_bidirectional_attention (qkn_decoder.c:525-527 / :674-676,
+siglip.c:126-128). Threads: min(nproc, 16), as the reference's pool allows
+(threading.c:22).
+"""
+import os
+import time
+
+import numpy as np
+
+from oracle import Oracle, RefLib, ref_path, simd_branch
+
+
+def _widen(b):
+    return (np.ascontiguousarray(b, np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def _f32(a):
+    a = np.asarray(a)
+    return _widen(a) if a.dtype == np.uint16 else np.ascontiguousarray(a, np.float32)
+
+
+def _lib():
+    cores = min(os.cpu_count() or 1, 16)
+    if ref_path():
+        lib, kind = RefLib(), "reference"
+    else:
+        lib, kind = Oracle(), "port"
+    lib.set_threads(cores)
+    return lib, kind, cores
+
+
+def prefill_sample(wl, x, min_seconds=10.0, max_reps=50):
+    """Full causal prefill (RoPE on Q and K + attention) repeated for >= min_seconds."""
+    lib, kind, cores = _lib()
+    orc = Oracle()
+    P, S = wl.pos0, wl.seq_q
+    c, s = orc.fill_rope_table(0, P + S, wl.hd, wl.theta, wl.rope_type == 1)
+    c, s = c[P:], s[P:]
+    q0, k0, v = _f32(x["q"]), _f32(x["k"]), _f32(x["v"])
+    Kc = _widen(x["cache_k"]).reshape(P, -1)
+    Vc = _widen(x["cache_v"]).reshape(P, -1)
+    reps, t = 0, 0.0
+    while reps < 2 or (t < min_seconds and reps < max_reps):
+        t0 = time.perf_counter()
+        q = lib.apply_rope(q0, c, s, S, wl.Hq, wl.hd, wl.rope_type == 1)
+        kn = lib.apply_rope(k0, c, s, S, wl.Hkv, wl.hd, wl.rope_type == 1)
+        K = np.concatenate([Kc, kn], 0)
+        V = np.concatenate([Vc, v], 0)
+        lib.causal_attention(q, K, V, S, P + S, wl.Hq, wl.Hkv, wl.hd, wl.scale, P)
+        t += time.perf_counter() - t0
+        reps += 1
+    sec = t / reps
+    return {"value": round(wl.flops() / sec / 1e12, 6), "unit": "TFLOP/s", "cores": cores, "kind": kind,
+            "simd": simd_branch(), "ms_per_step": round(sec * 1e3, 3),
+            "sample": "%d full repetitions of the %s step (RoPE on Q and K + causal attention, %d x %d, "
+                      "%d heads)" % (reps, wl.name, S, P + S, wl.Hq)}
+
+
+def decode_sample(wl, x, min_seconds=3.0, max_reps=200):
+    """One decode step of every sequence (RoPE on q and k + attention over its cache)."""
+    lib, kind, cores = _lib()
+    orc = Oracle()
+    inter = wl.rope_type == 1
+    c, s = orc.fill_rope_table(0, max(wl.lengths), wl.hd, wl.theta, inter)
+    Ks = [np.concatenate([_widen(x["cache_k"][i]), np.zeros((1, wl.Hkv * wl.hd), np.float32)], 0)
+          for i in range(wl.n_seq)]
+    Vs = [np.concatenate([_widen(x["cache_v"][i]), x["v"][i:i + 1]], 0) for i in range(wl.n_seq)]
+    reps, t = 0, 0.0
+    while reps < 2 or (t < min_seconds and reps < max_reps):
+        t0 = time.perf_counter()
+        for i, L in enumerate(wl.lengths):
+            p = L - 1
+            q = lib.apply_rope(x["q"][i:i + 1], c[p:p + 1], s[p:p + 1], 1, wl.Hq, wl.hd, inter)
+            Ks[i][p] = lib.apply_rope(x["k"][i:i + 1], c[p:p + 1], s[p:p + 1], 1, wl.Hkv, wl.hd, inter)[0]
+            lib.causal_attention(q, Ks[i], Vs[i], 1, L, wl.Hq, wl.Hkv, wl.hd, wl.scale, p)
+        t += time.perf_counter() - t0
+        reps += 1
+    sec = t / reps
+    return {"value": round(wl.algorithmic_bytes() / sec / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind,
+            "ms_per_step": round(sec * 1e3, 3),
+            "sample": "%d repetitions of one decode step of %d sequences" % (reps, wl.n_seq)}
+
+
+def bidir_sample(wl, x, min_seconds=3.0, max_reps=50):
+    lib, kind, cores = _lib()
+    q, k, v = _widen(x["q"]), _widen(x["k"]), _widen(x["v"])
+    reps, t = 0, 0.0
+    while reps < 2 or (t < min_seconds and reps < max_reps):
+        t0 = time.perf_counter()
+        lib.bidirectional_attention(q, k, v, wl.seq, wl.H, wl.hd, wl.scale, wl.window_starts)
+        t += time.perf_counter() - t0
+        reps += 1
+    sec = t / reps
+    return {"value": round(wl.flops() / sec / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": kind,
+            "ms_per_step": round(sec * 1e3, 3),
+            "sample": "%d repetitions; smol_bidirectional_attention is single-threaded "
+                      "(attention.c:32-77)" % reps}

@@ -101,6 +101,7 @@ struct PinnedSlot {
 };
 
 #define SMOL_RING 16
+#define SMOL_TIMING_KINDS 3 /* 0: pre-pass, 1: attention, 2: other */
 
 struct smol_attn_ctx {
     int device = 0;
@@ -111,7 +112,39 @@ struct smol_attn_ctx {
     DevBuf desc;   /* device copy of the descriptor tables */
     DevBuf qs, kf, vtf, part_o, part_ml, counters;
     int cu_count = 256;
+    /* opt-in per-kernel timing: events bracketing each launch */
+    bool timing = false;
+    struct Mark { int kind; hipEvent_t a, b; };
+    std::vector<Mark> marks;
+    std::vector<hipEvent_t> event_pool;
+    double t_ms[SMOL_TIMING_KINDS] = {0, 0, 0};
+    int t_count[SMOL_TIMING_KINDS] = {0, 0, 0};
 };
+
+static hipEvent_t pool_event(smol_attn_ctx *ctx) {
+    if (!ctx->event_pool.empty()) {
+        hipEvent_t e = ctx->event_pool.back();
+        ctx->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+/* start / stop a timed launch of `kind` (no-ops unless timing is enabled) */
+static int timing_begin(smol_attn_ctx *ctx, int kind) {
+    if (!ctx->timing) return -1;
+    hipEvent_t a = pool_event(ctx), b = pool_event(ctx);
+    if (!a || !b) return -1;
+    hipEventRecord(a, ctx->stream);
+    ctx->marks.push_back({kind, a, b});
+    return (int)ctx->marks.size() - 1;
+}
+
+static void timing_end(smol_attn_ctx *ctx, int mark) {
+    if (mark >= 0) hipEventRecord(ctx->marks[mark].b, ctx->stream);
+}
 
 /* Tables and caches keep their own device and stream, so destroying them
  * does not touch the context (which may already be gone). */
@@ -199,6 +232,11 @@ extern "C" int smol_attn_ctx_destroy(smol_attn_ctx *ctx) {
         if (s.h) hipHostFree(s.h);
         if (s.ev) hipEventDestroy(s.ev);
     }
+    for (auto &m : ctx->marks) {
+        hipEventDestroy(m.a);
+        hipEventDestroy(m.b);
+    }
+    for (hipEvent_t e : ctx->event_pool) hipEventDestroy(e);
     if (ctx->own_stream) hipStreamDestroy(ctx->stream);
     delete ctx;
     return SMOL_ATTN_OK;
@@ -211,6 +249,33 @@ extern "C" int smol_attn_ctx_synchronize(smol_attn_ctx *ctx) {
 }
 
 extern "C" void *smol_attn_ctx_stream(smol_attn_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+extern "C" int smol_attn_ctx_set_timing(smol_attn_ctx *ctx, int enable) {
+    if (!ctx) return fail(SMOL_ATTN_ERR_ARG, "ctx is NULL");
+    ctx->timing = enable != 0;
+    return SMOL_ATTN_OK;
+}
+
+extern "C" int smol_attn_ctx_timing_read(smol_attn_ctx *ctx, double *ms, int *count) {
+    if (!ctx || !ms || !count) return fail(SMOL_ATTN_ERR_ARG, "NULL argument");
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    for (auto &m : ctx->marks) {
+        float t = 0.0f;
+        HIP_TRY(hipEventElapsedTime(&t, m.a, m.b));
+        ctx->t_ms[m.kind] += t;
+        ctx->t_count[m.kind] += 1;
+        ctx->event_pool.push_back(m.a);
+        ctx->event_pool.push_back(m.b);
+    }
+    ctx->marks.clear();
+    for (int k = 0; k < SMOL_TIMING_KINDS; k++) {
+        ms[k] = ctx->t_ms[k];
+        count[k] = ctx->t_count[k];
+        ctx->t_ms[k] = 0.0;
+        ctx->t_count[k] = 0;
+    }
+    return SMOL_ATTN_OK;
+}
 
 /* --------------------------------------------------------------- RoPE table */
 
@@ -543,8 +608,10 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     pp.kf = (_Float16 *)ctx->kf.p; pp.vtf = (_Float16 *)ctx->vtf.p; pp.fcap = (int)fcap;
     pp.batches = (const PrepBatch *)(dd + o_pb);
     pp.blocks = (const PrepBlock *)(dd + o_pblk);
-    if ((rc = smol_launch_prep(&pp, (int)pl.pblk.size(), ctx->stream)))
-        return fail(SMOL_ATTN_ERR_DEVICE, "k_prep launch: %s", hipGetErrorString(hipGetLastError()));
+    int mk = timing_begin(ctx, 0);
+    rc = smol_launch_prep(&pp, (int)pl.pblk.size(), ctx->stream);
+    timing_end(ctx, mk);
+    if (rc) return fail(SMOL_ATTN_ERR_DEVICE, "k_prep launch: %s", hipGetErrorString(hipGetLastError()));
 
     SkParams sp;
     memset(&sp, 0, sizeof(sp));
@@ -561,7 +628,10 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     sp.part_o = (float *)ctx->part_o.p;
     sp.part_ml = (float *)ctx->part_ml.p;
     sp.counters = (int *)ctx->counters.p;
-    if ((rc = smol_launch_sk(&sp, hd, (int)n_items, nt, ctx->stream)))
+    mk = timing_begin(ctx, 1);
+    rc = smol_launch_sk(&sp, hd, (int)n_items, nt, ctx->stream);
+    timing_end(ctx, mk);
+    if (rc)
         return fail(rc == -1 ? SMOL_ATTN_ERR_UNSUPPORTED : SMOL_ATTN_ERR_DEVICE,
                     "k_attn_sk launch (hd %d): %s", hd, hipGetErrorString(hipGetLastError()));
     return SMOL_ATTN_OK;

@@ -39,6 +39,8 @@ SIGNATURES = [
     ("smol_attn_ctx_destroy", [_vp], _c_int),
     ("smol_attn_ctx_synchronize", [_vp], _c_int),
     ("smol_attn_ctx_stream", [_vp], _vp),
+    ("smol_attn_ctx_set_timing", [_vp, _c_int], _c_int),
+    ("smol_attn_ctx_timing_read", [_vp, ctypes.POINTER(ctypes.c_double), _IP], _c_int),
     ("smol_rope_table_create", [_vp, _c_int, _c_float, _c_int, _c_int, ctypes.POINTER(_vp)], _c_int),
     ("smol_rope_table_ensure", [_vp, _c_int], _c_int),
     ("smol_rope_table_capacity", [_vp], _c_int),
@@ -146,6 +148,16 @@ class Context:
 
     def synchronize(self):
         _check(load().smol_attn_ctx_synchronize(self.h), "synchronize")
+
+    def set_timing(self, enable):
+        _check(load().smol_attn_ctx_set_timing(self.h, 1 if enable else 0), "set_timing")
+
+    def timing_read(self):
+        """{'prep': (ms, n), 'attn': (ms, n), 'other': (ms, n)} since the last read (synchronizes)."""
+        ms = (ctypes.c_double * 3)()
+        n = (ctypes.c_int * 3)()
+        _check(load().smol_attn_ctx_timing_read(self.h, ms, n), "timing_read")
+        return {"prep": (ms[0], n[0]), "attn": (ms[1], n[1]), "other": (ms[2], n[2])}
 
     def close(self):
         if self.h:
