@@ -73,8 +73,8 @@ def main():
     ap.add_argument("--only", default=None, help="measure only this workload")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the attention would shard by KV "
-              "head with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU only: this build has no multi-GPU path (the attention would shard "
+              "by KV head with no exchange inside attention). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
