@@ -44,8 +44,8 @@ def prefill_sample(wl, x, min_seconds=10.0, max_reps=50):
     c, s = orc.fill_rope_table(0, P + S, wl.hd, wl.theta, wl.rope_type == 1)
     c, s = c[P:], s[P:]
     q0, k0, v = _f32(x["q"]), _f32(x["k"]), _f32(x["v"])
-    Kc = _widen(x["cache_k"]).reshape(P, -1)
-    Vc = _widen(x["cache_v"]).reshape(P, -1)
+    Kc = _widen(x["cache_k"]).reshape(P, wl.Hkv * wl.hd)
+    Vc = _widen(x["cache_v"]).reshape(P, wl.Hkv * wl.hd)
     reps, t = 0, 0.0
     while reps < 2 or (t < min_seconds and reps < max_reps):
         t0 = time.perf_counter()
