@@ -13,6 +13,7 @@
 
 #include <math.h>
 #include <stdarg.h>
+#include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -654,7 +655,13 @@ static int check_common(smol_attn_ctx *ctx, int dtype, int Hq, int Hkv, int hd, 
         return fail(SMOL_ATTN_ERR_ARG, "n_heads %d not a multiple of n_kv_heads %d", Hq, Hkv);
     if (!hd_supported(hd)) return fail(SMOL_ATTN_ERR_UNSUPPORTED, "head_dim %d", hd);
     if (!q || !out) return fail(SMOL_ATTN_ERR_ARG, "NULL tensor");
+    if (((uintptr_t)q | (uintptr_t)out) & 15) return fail(SMOL_ATTN_ERR_ARG, "q/out must be 16-byte aligned");
     return set_device(ctx);
+}
+
+static int check_aligned(const void *a, const void *b) {
+    if (((uintptr_t)a | (uintptr_t)b) & 15) return fail(SMOL_ATTN_ERR_ARG, "k/v must be 16-byte aligned");
+    return 0;
 }
 
 static int check_rope(const smol_rope_table *rope, int hd, int need) {
@@ -674,6 +681,7 @@ extern "C" int smol_attn_prefill(smol_attn_ctx *ctx, smol_kv_cache *kv, int laye
     if (layer < 0 || layer >= kv->n_layers || slot < 0 || slot >= kv->n_slots)
         return fail(SMOL_ATTN_ERR_ARG, "layer %d / slot %d out of range", layer, slot);
     if (pos0 < 0 || seq_q <= 0 || !k_new || !v_new) return fail(SMOL_ATTN_ERR_ARG, "pos0 %d seq_q %d", pos0, seq_q);
+    if ((rc = check_aligned(k_new, v_new))) return rc;
     if ((rc = smol_kv_cache_reserve(kv, pos0 + seq_q))) return rc;
     if ((rc = check_rope(rope, kv->hd, pos0 + seq_q))) return rc;
     const int Hkv = kv->n_kv, G = n_heads / Hkv, hd = kv->hd;
@@ -702,6 +710,7 @@ extern "C" int smol_attn_decode(smol_attn_ctx *ctx, smol_kv_cache *kv, int layer
     if (kv->ctx != ctx) return fail(SMOL_ATTN_ERR_ARG, "cache belongs to another context");
     if (layer < 0 || layer >= kv->n_layers) return fail(SMOL_ATTN_ERR_ARG, "layer %d out of range", layer);
     if (n_seq <= 0 || !slots || !pos || !k_new || !v_new) return fail(SMOL_ATTN_ERR_ARG, "bad decode batch");
+    if ((rc = check_aligned(k_new, v_new))) return rc;
     int max_pos = 0;
     std::vector<char> seen(kv->n_slots, 0);
     for (int i = 0; i < n_seq; i++) {
@@ -737,6 +746,7 @@ extern "C" int smol_attn_causal(smol_attn_ctx *ctx, const void *q, const void *k
     if (rc) return rc;
     if (seq_q <= 0 || seq_k < 0) return fail(SMOL_ATTN_ERR_ARG, "seq_q %d seq_k %d", seq_q, seq_k);
     if (seq_k > 0 && (!k || !v)) return fail(SMOL_ATTN_ERR_ARG, "NULL K/V");
+    if ((rc = check_aligned(k, v))) return rc;
     const int G = n_heads / n_kv_heads;
     Plan pl;
     const int nf = (seq_k + SMOL_SLAB - 1) & ~(SMOL_SLAB - 1);
@@ -757,6 +767,7 @@ extern "C" int smol_attn_bidirectional(smol_attn_ctx *ctx, const void *q, const 
     int rc = check_common(ctx, dtype, n_heads, n_heads, hd, q, out);
     if (rc) return rc;
     if (!ws || n_windows <= 0 || !k || !v) return fail(SMOL_ATTN_ERR_ARG, "bad windows");
+    if ((rc = check_aligned(k, v))) return rc;
     for (int w = 0; w < n_windows; w++)
         if (ws[w] < 0 || ws[w + 1] < ws[w] || ws[w + 1] > seq)
             return fail(SMOL_ATTN_ERR_ARG, "window %d = [%d, %d) outside [0, %d)", w, ws[w], ws[w + 1], seq);

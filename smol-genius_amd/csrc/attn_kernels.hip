@@ -98,41 +98,115 @@ __device__ __forceinline__ int rope_partner(int d, int hd, int kind) {
 
 /* ------------------------------------------------------------------ k_prep */
 
+/* 8 consecutive input elements (fp32 or bf16) as fp32; idx is a multiple of 8 */
+__device__ __forceinline__ void load8(const void *base, int dtype, long long idx, float *v) {
+    if (dtype == SMOL_IN_BF16) {
+        const uint4 w = *reinterpret_cast<const uint4 *>((const uint16_t *)base + idx);
+        const uint32_t a[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            v[2 * i] = __uint_as_float(a[i] << 16);
+            v[2 * i + 1] = __uint_as_float(a[i] & 0xFFFF0000u);
+        }
+    } else {
+        const float4 x = *reinterpret_cast<const float4 *>((const float *)base + idx);
+        const float4 y = *reinterpret_cast<const float4 *>((const float *)base + idx + 4);
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+        v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+    }
+}
+
+__device__ __forceinline__ uint4 pack_bf16x8(const float *v) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) w[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__device__ __forceinline__ uint4 pack_h8(const float *v) {
+    h8 h;
+#pragma unroll
+    for (int i = 0; i < 8; i++) h[i] = (_Float16)v[i];
+    return *reinterpret_cast<uint4 *>(&h);
+}
+
+__device__ __forceinline__ void unpack_bf16x8(uint4 w, float *v) {
+    const uint32_t a[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[2 * i] = __uint_as_float(a[i] << 16);
+        v[2 * i + 1] = __uint_as_float(a[i] & 0xFFFF0000u);
+    }
+}
+
+/* Rotates the 8 elements [d0, d0+8) of a head vector whose row starts at
+ * `base + row` (fp32 or bf16 input), position `pos` of the table. */
+__device__ __forceinline__ void rope8(const void *base, int dtype, long long row, int d0, int hd, int kind,
+                                      const float *cos_t, const float *sin_t, long long pos, float *out) {
+    load8(base, dtype, row + d0, out);
+    if (kind == SMOL_ROPE_OFF) return;
+    const float *c = cos_t + pos * hd, *s = sin_t + pos * hd;
+    if (kind == SMOL_ROPE_INTERLEAVED_K) {
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            const float x0 = out[i], x1 = out[i + 1];
+            out[i] = x0 * c[d0 + i] - x1 * s[d0 + i];
+            out[i + 1] = x1 * c[d0 + i + 1] + x0 * s[d0 + i + 1];
+        }
+        return;
+    }
+    const int half = hd >> 1;
+    if ((half & 7) == 0) {
+        float pr[8];
+        const int pd0 = d0 < half ? d0 + half : d0 - half;
+        load8(base, dtype, row + pd0, pr);
+#pragma unroll
+        for (int i = 0; i < 8; i++) out[i] = rope_elem(out[i], pr[i], d0 + i, hd, kind, c, s);
+    } else {
+        /* half not a multiple of 8 (head_dim 72): partners element by element */
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int d = d0 + i;
+            const float xp = load_in(base, dtype, row + rope_partner(d, hd, kind));
+            out[i] = rope_elem(out[i], xp, d, hd, kind, c, s);
+        }
+    }
+}
+
 /* grid (n_blocks, Hkv), 256 threads. A fresh-slab block covers 32 positions
  * of one KV head: old cache rows are copied to the fresh buffers, new rows
  * are rotated (K), appended to the bf16 cache and written to the fresh
- * buffers, positions past the new rows are zero. V goes through LDS so the
- * transposed stores are 32 consecutive positions of one column. */
+ * buffers, positions past the new rows are zero. Work is done in chunks of
+ * 8 elements (16-byte stores); V goes through LDS so that the transposed
+ * stores are 8 consecutive positions of one column. */
 __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
     const PrepBlock blk = p.blocks[blockIdx.x];
     const PrepBatch b = p.batches[blk.batch];
     const int g = blockIdx.y;
     const int hd = p.hd;
     const int tid = threadIdx.x;
+    const int cpr = hd >> 3; /* 8-element chunks per head row */
     __shared__ float sv[SMOL_SLAB * 257];
 
     if (blk.kind == 1) {
         /* Q rows: token t, head g*G + hg -> scratch row q_row0 + t*G + hg */
         const int G = p.G, hdp = p.hdp;
-        const int per_tok = G * hdp;
+        const int cpp = hdp >> 3;
+        const int per_tok = G * cpp;
+        const int rk = (p.rope_q && p.rope_kind != SMOL_ROPE_OFF) ? p.rope_kind : SMOL_ROPE_OFF;
         for (int e = tid; e < blk.count * per_tok; e += blockDim.x) {
-            int tl = e / per_tok, rem = e - tl * per_tok;
-            int hg = rem / hdp, d = rem - hg * hdp;
-            int t = blk.first + tl;
-            float val = 0.0f;
-            if (d < hd) {
-                long long base = (long long)(b.q_tok0 + t) * p.q_stride + (long long)(g * G + hg) * hd;
-                float xd = load_in(p.q, p.q_dtype, base + d);
-                if (p.rope_q && p.rope_kind != SMOL_ROPE_OFF) {
-                    int pd = rope_partner(d, hd, p.rope_kind);
-                    float xp = load_in(p.q, p.q_dtype, base + pd);
-                    long long row = (long long)(b.q_pos0 + t) * hd;
-                    xd = rope_elem(xd, xp, d, hd, p.rope_kind, p.rope_cos + row, p.rope_sin + row);
-                }
-                val = xd * p.qscale;
+            const int tl = e / per_tok, rem = e - tl * per_tok;
+            const int hg = rem / cpp, d0 = (rem - hg * cpp) * 8;
+            const int t = blk.first + tl;
+            float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (d0 < hd) {
+                const long long row = (long long)(b.q_tok0 + t) * p.q_stride + (long long)(g * G + hg) * hd;
+                rope8(p.q, p.q_dtype, row, d0, hd, rk, p.rope_cos, p.rope_sin, b.q_pos0 + t, v);
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] *= p.qscale;
             }
-            p.qs[(long long)g * p.qs_head_stride + (long long)(b.q_row0 + t * G + hg) * hdp + d] =
-                (_Float16)val;
+            *reinterpret_cast<uint4 *>(p.qs + (long long)g * p.qs_head_stride +
+                                       (long long)(b.q_row0 + t * G + hg) * hdp + d0) = pack_h8(v);
         }
         return;
     }
@@ -141,48 +215,57 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
     const int pos_base = b.fresh_pos0 + blk.first * SMOL_SLAB;
     const int frow_base = b.fresh_row0 + blk.first * SMOL_SLAB;
     const bool has_cache = b.slot >= 0 && p.kc != nullptr;
-    const uint16_t *kc = has_cache ? p.kc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * hd : nullptr;
-    const uint16_t *vtc = has_cache ? p.vtc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * hd : nullptr;
-    uint16_t *kcw = has_cache ? p.kc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * hd : nullptr;
-    uint16_t *vtcw = has_cache ? p.vtc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * hd : nullptr;
+    const long long cbase = has_cache ? (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * hd : 0;
+    uint16_t *kc = has_cache ? p.kc + cbase : nullptr;
+    uint16_t *vtc = has_cache ? p.vtc + cbase : nullptr;
     _Float16 *kf = p.kf + (long long)g * p.fcap * hd;
     _Float16 *vtf = p.vtf + (long long)g * p.fcap * hd;
+    const int new_lo = b.kv_pos0, new_hi = b.kv_pos0 + b.n_kv;
+    const int rk = (p.rope_k && p.rope_kind != SMOL_ROPE_OFF) ? p.rope_kind : SMOL_ROPE_OFF;
 
-    /* K rows (row-major): element (r, d) */
-    for (int e = tid; e < SMOL_SLAB * hd; e += blockDim.x) {
-        int r = e / hd, d = e - r * hd;
-        int pos = pos_base + r;
-        float kv = 0.0f, vv = 0.0f;
-        if (pos < b.kv_pos0) {
-            if (has_cache) {
-                kv = bf16_to_f32(kc[(long long)pos * hd + d]);
-                vv = bf16_to_f32(vtc[(long long)d * p.cap + pos]);
-            }
-        } else if (pos < b.kv_pos0 + b.n_kv) {
-            int t = pos - b.kv_pos0;
-            long long base = (long long)(b.kv_in0 + t) * p.kv_stride + (long long)g * hd;
-            kv = load_in(p.k, p.kv_dtype, base + d);
-            if (p.rope_k && p.rope_kind != SMOL_ROPE_OFF) {
-                int pd = rope_partner(d, hd, p.rope_kind);
-                float xp = load_in(p.k, p.kv_dtype, base + pd);
-                long long row = (long long)pos * hd;
-                kv = rope_elem(kv, xp, d, hd, p.rope_kind, p.rope_cos + row, p.rope_sin + row);
-            }
-            vv = load_in(p.v, p.kv_dtype, base + d);
-            if (has_cache) kcw[(long long)pos * hd + d] = f32_to_bf16(kv);
+    /* K rows and the new V rows (into LDS), chunk (r, d0) */
+    for (int e = tid; e < SMOL_SLAB * cpr; e += blockDim.x) {
+        const int r = e / cpr, d0 = (e - r * cpr) * 8;
+        const int pos = pos_base + r;
+        float kv[8] = {0, 0, 0, 0, 0, 0, 0, 0}, vv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (pos < new_lo) {
+            if (has_cache) unpack_bf16x8(*reinterpret_cast<const uint4 *>(kc + (long long)pos * hd + d0), kv);
+        } else if (pos < new_hi) {
+            const long long row = (long long)(b.kv_in0 + pos - new_lo) * p.kv_stride + (long long)g * hd;
+            rope8(p.k, p.kv_dtype, row, d0, hd, rk, p.rope_cos, p.rope_sin, pos, kv);
+            load8(p.v, p.kv_dtype, row + d0, vv);
+            if (has_cache) *reinterpret_cast<uint4 *>(kc + (long long)pos * hd + d0) = pack_bf16x8(kv);
         }
-        kf[(long long)(frow_base + r) * hd + d] = (_Float16)kv;
-        sv[r * 257 + d] = vv;
+        *reinterpret_cast<uint4 *>(kf + (long long)(frow_base + r) * hd + d0) = pack_h8(kv);
+#pragma unroll
+        for (int i = 0; i < 8; i++) sv[r * 257 + d0 + i] = vv[i];
     }
     __syncthreads();
-    /* V^T: element (d, r), r fastest */
-    for (int e = tid; e < SMOL_SLAB * hd; e += blockDim.x) {
-        int d = e / SMOL_SLAB, r = e - d * SMOL_SLAB;
-        int pos = pos_base + r;
-        float vv = sv[r * 257 + d];
-        vtf[(long long)d * p.fcap + frow_base + r] = (_Float16)vv;
-        if (has_cache && pos >= b.kv_pos0 && pos < b.kv_pos0 + b.n_kv)
-            vtcw[(long long)d * p.cap + pos] = f32_to_bf16(vv);
+    /* V^T: chunk (d, 8 consecutive positions q0..q0+7) */
+    for (int e = tid; e < hd * (SMOL_SLAB / 8); e += blockDim.x) {
+        const int d = e / (SMOL_SLAB / 8), q0 = (e - d * (SMOL_SLAB / 8)) * 8;
+        const int pos = pos_base + q0;
+        float v[8];
+        if (pos + 8 <= new_lo) {
+            if (has_cache) unpack_bf16x8(*reinterpret_cast<const uint4 *>(vtc + (long long)d * p.cap + pos), v);
+            else { for (int i = 0; i < 8; i++) v[i] = 0.0f; }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int ps = pos + i;
+                v[i] = ps < new_lo ? (has_cache ? bf16_to_f32(vtc[(long long)d * p.cap + ps]) : 0.0f)
+                                   : sv[(q0 + i) * 257 + d];
+            }
+            if (has_cache) {
+                if (pos >= new_lo && pos + 8 <= new_hi) {
+                    *reinterpret_cast<uint4 *>(vtc + (long long)d * p.cap + pos) = pack_bf16x8(v);
+                } else {
+                    for (int i = 0; i < 8; i++)
+                        if (pos + i >= new_lo && pos + i < new_hi) vtc[(long long)d * p.cap + pos + i] = f32_to_bf16(v[i]);
+                }
+            }
+        }
+        *reinterpret_cast<uint4 *>(vtf + (long long)d * p.fcap + frow_base + q0) = pack_h8(v);
     }
 }
 
@@ -240,51 +323,79 @@ __global__ __launch_bounds__(64) void k_attn_sk(SkParams p) {
         for (int dt = 0; dt < DT; dt++) o[nt][dt] = f4{0.f, 0.f, 0.f, 0.f};
     }
 
+    /* K / V^T sources: cache rows (bf16) below fresh_pos0, the fresh fp16
+     * buffers from there on. Both are 2-byte elements with the same row
+     * layout, so a slab's loads differ only in base pointer and stride; the
+     * choice is uniform per slab and no load sits under a branch. */
     const uint16_t *kc = nullptr, *vtc = nullptr;
     if (b.slot >= 0 && p.kc != nullptr) {
         kc = p.kc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * HD;
         vtc = p.vtc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * HD;
     }
-    const _Float16 *kf = p.kf + (long long)g * p.fcap * HD;
-    const _Float16 *vtf = p.vtf + (long long)g * p.fcap * HD;
+    const uint16_t *kf = reinterpret_cast<const uint16_t *>(p.kf) + (long long)g * p.fcap * HD +
+                         (long long)(b.fresh_row0 - b.fresh_pos0) * HD;
+    const uint16_t *vtf = reinterpret_cast<const uint16_t *>(p.vtf) + (long long)g * p.fcap * HD +
+                          (b.fresh_row0 - b.fresh_pos0);
     const int kt_row = 8 * (c >> 2) + (c & 3); /* gathered key of A-operand row c, tile 0 */
 
-    for (int k0 = it.key_begin; k0 < it.key_end; k0 += SMOL_SLAB) {
-        const bool fresh = k0 >= b.fresh_pos0;
-        /* ---- S^T = K . Q^T for two 16-key tiles ---- */
-        h8 kfrag[2][KS];
+    uint4 kraw[2][KS], vraw[DT];
+    auto issue = [&](int k0) {
+        const bool fr = k0 >= b.fresh_pos0;
+        const uint16_t *kb = fr ? kf : kc;
+        const uint16_t *vb = fr ? vtf : vtc;
+        const long long vs = fr ? p.fcap : p.cap;
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-            const int key = k0 + kt_row + 4 * t;
+        for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
                 const int d0 = 32 * ks + 8 * j;
-                if (HD % 32 != 0 && d0 >= HD) { kfrag[t][ks] = zero_h8(); continue; }
-                kfrag[t][ks] = fresh ? load_h8(kf + (long long)(b.fresh_row0 + key - b.fresh_pos0) * HD + d0)
-                                     : load_bf16x8(kc + (long long)key * HD + d0);
+                if (HD % 32 != 0 && d0 >= HD) { kraw[t][ks] = make_uint4(0, 0, 0, 0); continue; }
+                kraw[t][ks] = *reinterpret_cast<const uint4 *>(kb + (long long)(k0 + kt_row + 4 * t) * HD + d0);
             }
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            const int d = 16 * dt + c;
+            if (HD % 16 != 0 && d >= HD) { vraw[dt] = make_uint4(0, 0, 0, 0); continue; }
+            vraw[dt] = *reinterpret_cast<const uint4 *>(vb + (long long)d * vs + k0 + 8 * j);
         }
+    };
+
+    if (it.key_begin < it.key_end) issue(it.key_begin);
+    for (int k0 = it.key_begin; k0 < it.key_end; k0 += SMOL_SLAB) {
+        const bool fresh = k0 >= b.fresh_pos0;
+        uint4 kcur[2][KS], vcur[DT];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) kcur[t][ks] = kraw[t][ks];
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) vcur[dt] = vraw[dt];
+        /* prefetch the next slab while this one is computed */
+        if (k0 + SMOL_SLAB < it.key_end) issue(k0 + SMOL_SLAB);
+
+        /* ---- S^T = K . Q^T for two 16-key tiles ---- */
         f4 s[NT][2];
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++)
+        for (int t = 0; t < 2; t++) {
+            h8 kfrag[KS];
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
+            for (int ks = 0; ks < KS; ks++)
+                kfrag[ks] = fresh ? *reinterpret_cast<h8 *>(&kcur[t][ks]) : bf16x8_to_h8(kcur[t][ks]);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
                 f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int ks = 0; ks < KS; ks++)
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kfrag[t][ks], qf[nt][ks], acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kfrag[ks], qf[nt][ks], acc, 0, 0, 0);
                 s[nt][t] = acc;
             }
+        }
 
         /* ---- V^T fragments (shared by all row tiles) ---- */
         h8 vfrag[DT];
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            const int d = 16 * dt + c;
-            if (HD % 16 != 0 && d >= HD) { vfrag[dt] = zero_h8(); continue; }
-            vfrag[dt] = fresh ? load_h8(vtf + (long long)d * p.fcap + b.fresh_row0 + (k0 - b.fresh_pos0) + 8 * j)
-                              : load_bf16x8(vtc + (long long)d * p.cap + k0 + 8 * j);
-        }
+        for (int dt = 0; dt < DT; dt++)
+            vfrag[dt] = fresh ? *reinterpret_cast<h8 *>(&vcur[dt]) : bf16x8_to_h8(vcur[dt]);
 
         /* ---- online softmax per row (lane column), then O^T += V^T P^T ---- */
 #pragma unroll
