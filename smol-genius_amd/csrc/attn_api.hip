@@ -516,9 +516,10 @@ static void plan_items(Plan &pl, int Hkv, int G, int window, int nt, int cu_coun
             total_slabs += (hi - lo + SMOL_SLAB - 1) / SMOL_SLAB;
         }
     }
-    const long long target_items = (long long)cu_count * 4;
+    /* one 4-wave workgroup per compute unit, each wave >= 2 slabs */
+    const long long target_items = (long long)cu_count;
     long long per = (total_slabs * Hkv + target_items - 1) / std::max(1LL, target_items);
-    int slabs_per_item = (int)std::max(2LL, per);
+    int slabs_per_item = (int)std::max(8LL, per);
     int group = 0;
     for (const Tile &t : tiles) {
         const int n_slabs = (t.hi - t.lo + SMOL_SLAB - 1) / SMOL_SLAB;

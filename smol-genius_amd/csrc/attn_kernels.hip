@@ -272,8 +272,10 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
 /* --------------------------------------------------------------- k_attn_sk */
 
 /*
- * One wave (64 lanes) per item: NT tiles of 16 query rows of one KV head
- * against the item's key range, in 32-key slabs.
+ * One workgroup of SK_WAVES waves per item: NT tiles of 16 query rows of one
+ * KV head against the item's key range, in 32-key slabs. Wave w takes slabs
+ * w, w + SK_WAVES, ... of the range (all waves stream at once); the waves'
+ * softmax states are combined through LDS, so an item produces one partial.
  *
  * MFMA layouts (16x16x32 f16; lane l, c = l & 15, j = l >> 4):
  *   S^T = K . Q^T : A = K rows, B = Q^T; D element i of lane l is
@@ -282,20 +284,28 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
  * K rows are gathered in the order key(t, m) = 8 (m >> 2) + 4 t + (m & 3) so
  * that the 8 probabilities a lane holds after the two S^T tiles are the 8
  * consecutive keys 8j..8j+7 of the slab, i.e. exactly the B operand of the
- * P.V step against a 16-byte load of V^T.
+ * P.V step against a 16-byte load of V^T. Every row lives in lanes c, c+16,
+ * c+32, c+48, so the softmax state of a row never leaves its lane column.
  */
+#define SK_WAVES 4
+
 template <int HD, int NT>
-__global__ __launch_bounds__(64) void k_attn_sk(SkParams p) {
+__global__ __launch_bounds__(64 * SK_WAVES) void k_attn_sk(SkParams p) {
     constexpr int KS = (HD + 31) / 32;  /* 32-wide steps over head_dim for S */
     constexpr int DT = (HD + 15) / 16;  /* 16-row tiles of head_dim for O */
     constexpr int HDP = KS * 32;
     constexpr int ROWS = NT * 16;
-    const int lane = threadIdx.x;
+    constexpr int OSTR = DT * 16 + 4;   /* LDS row stride (floats) of a combined state */
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
     const int c = lane & 15, j = lane >> 4;
     const int g = blockIdx.y;
     const SkItem it = p.items[blockIdx.x];
     const SkBatch b = p.batches[it.batch];
     const int G = p.G;
+    __shared__ float s_o[(SK_WAVES - 1) * ROWS * OSTR];
+    __shared__ float s_m[(SK_WAVES - 1) * ROWS], s_l[(SK_WAVES - 1) * ROWS];
+    __shared__ int s_last;
 
     /* per-lane row metadata and Q fragments */
     h8 qf[NT][KS];
@@ -360,8 +370,10 @@ __global__ __launch_bounds__(64) void k_attn_sk(SkParams p) {
         }
     };
 
-    if (it.key_begin < it.key_end) issue(it.key_begin);
-    for (int k0 = it.key_begin; k0 < it.key_end; k0 += SMOL_SLAB) {
+    const int step = SMOL_SLAB * SK_WAVES;
+    const int kb0 = it.key_begin + wave * SMOL_SLAB;
+    if (kb0 < it.key_end) issue(kb0);
+    for (int k0 = kb0; k0 < it.key_end; k0 += step) {
         const bool fresh = k0 >= b.fresh_pos0;
         uint4 kcur[2][KS], vcur[DT];
 #pragma unroll
@@ -370,8 +382,8 @@ __global__ __launch_bounds__(64) void k_attn_sk(SkParams p) {
             for (int ks = 0; ks < KS; ks++) kcur[t][ks] = kraw[t][ks];
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) vcur[dt] = vraw[dt];
-        /* prefetch the next slab while this one is computed */
-        if (k0 + SMOL_SLAB < it.key_end) issue(k0 + SMOL_SLAB);
+        /* prefetch this wave's next slab while this one is computed */
+        if (k0 + step < it.key_end) issue(k0 + step);
 
         /* ---- S^T = K . Q^T for two 16-key tiles ---- */
         f4 s[NT][2];
@@ -436,15 +448,54 @@ __global__ __launch_bounds__(64) void k_attn_sk(SkParams p) {
         }
     }
 
-    /* full row sums: lanes c, c+16, c+32, c+48 hold one row */
+    /* full row sums of this wave: lanes c, c+16, c+32, c+48 hold one row */
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         l[nt] += __shfl_xor(l[nt], 16);
         l[nt] += __shfl_xor(l[nt], 32);
     }
 
+    /* ---- combine the waves' states through LDS into wave 0 ---- */
+    if (wave > 0) {
+        const int sl = (wave - 1) * ROWS;
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int rr = nt * 16 + c;
+            float *so = s_o + (sl + rr) * OSTR;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) *reinterpret_cast<f4 *>(so + 16 * dt + 4 * j) = o[nt][dt];
+            if (j == 0) { s_m[sl + rr] = m[nt]; s_l[sl + rr] = l[nt]; }
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int rr = nt * 16 + c;
+            float M = m[nt];
+#pragma unroll
+            for (int w = 0; w < SK_WAVES - 1; w++) M = fmaxf(M, s_m[w * ROWS + rr]);
+            const float Mu = M == -INFINITY ? 0.0f : M;
+            const float a0 = __builtin_amdgcn_exp2f(m[nt] - Mu);
+            float L = l[nt] * a0;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) o[nt][dt] *= a0;
+#pragma unroll
+            for (int w = 0; w < SK_WAVES - 1; w++) {
+                const float aw = __builtin_amdgcn_exp2f(s_m[w * ROWS + rr] - Mu);
+                L += s_l[w * ROWS + rr] * aw;
+                const float *so = s_o + (w * ROWS + rr) * OSTR;
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) o[nt][dt] += aw * *reinterpret_cast<const f4 *>(so + 16 * dt + 4 * j);
+            }
+            m[nt] = M;
+            l[nt] = L;
+        }
+    }
+
     const int Hq = p.Hq;
     if (it.n_split == 1) {
+        if (wave != 0) return;
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             const int r = it.row0 + nt * 16 + c;
@@ -462,53 +513,84 @@ __global__ __launch_bounds__(64) void k_attn_sk(SkParams p) {
         return;
     }
 
-    /* ---- split-K: publish the partial, the last wave of the group merges ---- */
+    /* ---- split-K: publish the partial, the last workgroup of the group merges ---- */
     const long long pbase = ((long long)blockIdx.x * p.Hkv + g) * ROWS;
+    if (wave == 0) {
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++) {
-        const int rr = nt * 16 + c;
-        float *po = p.part_o + (pbase + rr) * HD;
+        for (int nt = 0; nt < NT; nt++) {
+            const int rr = nt * 16 + c;
+            float *po = p.part_o + (pbase + rr) * HD;
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            const int d = 16 * dt + 4 * j;
-            if (HD % 16 != 0 && d >= HD) continue;
-            *reinterpret_cast<f4 *>(po + d) = o[nt][dt];
+            for (int dt = 0; dt < DT; dt++) {
+                const int d = 16 * dt + 4 * j;
+                if (HD % 16 != 0 && d >= HD) continue;
+                *reinterpret_cast<f4 *>(po + d) = o[nt][dt];
+            }
+            if (j == 0) {
+                p.part_ml[(pbase + rr) * 2 + 0] = m[nt];
+                p.part_ml[(pbase + rr) * 2 + 1] = l[nt];
+            }
         }
-        if (j == 0) {
-            p.part_ml[(pbase + rr) * 2 + 0] = m[nt];
-            p.part_ml[(pbase + rr) * 2 + 1] = l[nt];
-        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        int prev = 0;
+        if (lane == 0)
+            prev = __hip_atomic_fetch_add(p.counters + (long long)it.group * p.Hkv + g, 1, __ATOMIC_ACQ_REL,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+        prev = __shfl(prev, 0);
+        if (lane == 0) s_last = prev == it.n_split - 1;
     }
-    int prev = 0;
-    if (lane == 0)
-        prev = __hip_atomic_fetch_add(p.counters + (long long)it.group * p.Hkv + g, 1,
-                                      __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    prev = __shfl(prev, 0);
-    if (prev != it.n_split - 1) return;
-    __atomic_thread_fence(__ATOMIC_ACQUIRE);
+    __syncthreads();
+    if (!s_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 
+    /* merge: per row the max and the rescaled sum over splits, then every
+     * (row, 4 columns) element as a weighted sum of the partials. The loads
+     * of one element's partials are independent, four in flight at a time. */
     const int first = blockIdx.x - it.split;
-    for (int e = lane; e < ROWS * (HD / 4); e += 64) {
-        const int rr = e / (HD / 4), d = (e - rr * (HD / 4)) * 4;
-        const int r = it.row0 + rr;
-        if (r >= b.n_rows) continue;
+    const int nsp = it.n_split;
+    float *s_w = s_o; /* reuse: per (row) max and 1/sum */
+    if (tid < ROWS) {
         float M = -INFINITY;
-        for (int sp = 0; sp < it.n_split; sp++)
-            M = fmaxf(M, p.part_ml[(((long long)(first + sp) * p.Hkv + g) * ROWS + rr) * 2]);
+        for (int sp = 0; sp < nsp; sp++)
+            M = fmaxf(M, p.part_ml[(((long long)(first + sp) * p.Hkv + g) * ROWS + tid) * 2]);
         const float Mu = M == -INFINITY ? 0.0f : M;
         float L = 0.0f;
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int sp = 0; sp < it.n_split; sp++) {
-            const long long pr = ((long long)(first + sp) * p.Hkv + g) * ROWS + rr;
-            const float w = __builtin_amdgcn_exp2f(p.part_ml[pr * 2] - Mu);
-            L += w * p.part_ml[pr * 2 + 1];
-            acc += w * *reinterpret_cast<const f4 *>(p.part_o + pr * HD + d);
+        for (int sp = 0; sp < nsp; sp++) {
+            const long long pr = ((long long)(first + sp) * p.Hkv + g) * ROWS + tid;
+            L += __builtin_amdgcn_exp2f(p.part_ml[pr * 2] - Mu) * p.part_ml[pr * 2 + 1];
         }
-        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        s_w[2 * tid] = Mu;
+        s_w[2 * tid + 1] = L > 0.0f ? 1.0f / L : 0.0f;
+    }
+    __syncthreads();
+    constexpr int C4 = HD / 4;
+    for (int e = tid; e < ROWS * C4; e += 64 * SK_WAVES) {
+        const int rr = e / C4, d = (e - rr * C4) * 4;
+        const int r = it.row0 + rr;
+        if (r >= b.n_rows) continue;
+        const float Mu = s_w[2 * rr], inv = s_w[2 * rr + 1];
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+        int sp = 0;
+        for (; sp + 4 <= nsp; sp += 4) {
+            f4 v[4];
+            float w[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const long long pr = ((long long)(first + sp + u) * p.Hkv + g) * ROWS + rr;
+                w[u] = p.part_ml[pr * 2];
+                v[u] = *reinterpret_cast<const f4 *>(p.part_o + pr * HD + d);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) acc += __builtin_amdgcn_exp2f(w[u] - Mu) * v[u];
+        }
+        for (; sp < nsp; sp++) {
+            const long long pr = ((long long)(first + sp) * p.Hkv + g) * ROWS + rr;
+            acc += __builtin_amdgcn_exp2f(p.part_ml[pr * 2] - Mu) * *reinterpret_cast<const f4 *>(p.part_o + pr * HD + d);
+        }
         const int qi = r / G, hg = r - qi * G;
         *reinterpret_cast<f4 *>(p.out + ((long long)(b.out_tok0 + qi) * Hq + (g * G + hg)) * HD + d) = acc * inv;
     }
-    if (lane == 0) p.counters[(long long)it.group * p.Hkv + g] = 0;
+    if (tid == 0) p.counters[(long long)it.group * p.Hkv + g] = 0;
 }
 
 /* ------------------------------------------------------------ k_rope_apply */
@@ -569,7 +651,7 @@ extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t 
 
 template <int HD>
 static int launch_sk_hd(const SkParams *sp, int n_items, int nt, hipStream_t st) {
-    dim3 grid(n_items, sp->Hkv), block(64);
+    dim3 grid(n_items, sp->Hkv), block(64 * SK_WAVES);
     /* register budget: NT * HD <= 256 fits without spilling */
     if (nt == 1) hipLaunchKernelGGL((k_attn_sk<HD, 1>), grid, block, 0, st, *sp);
     else if (nt == 2 && HD <= 128) hipLaunchKernelGGL((k_attn_sk<HD, (HD <= 128 ? 2 : 1)>), grid, block, 0, st, *sp);
