@@ -521,9 +521,10 @@ static void plan_items(Plan &pl, int Hkv, int G, int window, int nt, int cu_coun
     long long per = (total_slabs * Hkv + target_items - 1) / std::max(1LL, target_items);
     int slabs_per_item = (int)std::max(8LL, per);
     int group = 0;
+    const int max_split = 1024 / rows_per; /* the kernel's merge holds rows * n_split pairs in LDS */
     for (const Tile &t : tiles) {
         const int n_slabs = (t.hi - t.lo + SMOL_SLAB - 1) / SMOL_SLAB;
-        const int n_split = std::max(1, (n_slabs + slabs_per_item - 1) / slabs_per_item);
+        const int n_split = std::min(max_split, std::max(1, (n_slabs + slabs_per_item - 1) / slabs_per_item));
         const int per_split = (n_slabs + n_split - 1) / std::max(1, n_split);
         int made = 0;
         std::vector<SkItem> tmp;

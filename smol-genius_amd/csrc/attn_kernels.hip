@@ -288,6 +288,7 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
  * c+32, c+48, so the softmax state of a row never leaves its lane column.
  */
 #define SK_WAVES 4
+#define SK_MERGE_MAX 1024 /* max ROWS * n_split of one merge group (LDS) */
 
 template <int HD, int NT>
 __global__ __launch_bounds__(64 * SK_WAVES) void k_attn_sk(SkParams p) {
@@ -303,7 +304,9 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_attn_sk(SkParams p) {
     const SkItem it = p.items[blockIdx.x];
     const SkBatch b = p.batches[it.batch];
     const int G = p.G;
-    __shared__ float s_o[(SK_WAVES - 1) * ROWS * OSTR];
+    constexpr int SO = (SK_WAVES - 1) * ROWS * OSTR > 2 * SK_MERGE_MAX + 128 ? (SK_WAVES - 1) * ROWS * OSTR
+                                                                          : 2 * SK_MERGE_MAX + 128;
+    __shared__ float s_o[SO];
     __shared__ float s_m[(SK_WAVES - 1) * ROWS], s_l[(SK_WAVES - 1) * ROWS];
     __shared__ int s_last;
 
@@ -543,24 +546,39 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_attn_sk(SkParams p) {
     if (!s_last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 
-    /* merge: per row the max and the rescaled sum over splits, then every
-     * (row, 4 columns) element as a weighted sum of the partials. The loads
-     * of one element's partials are independent, four in flight at a time. */
+    /* merge: all (max, sum) pairs of the group are loaded in one parallel
+     * sweep into LDS, each row's max and 1/sum and every split's weight are
+     * formed there, then each (row, 4 columns) element sums the weighted
+     * partials with eight independent loads in flight. The host keeps
+     * ROWS * n_split within SK_MERGE_MAX. */
     const int first = blockIdx.x - it.split;
     const int nsp = it.n_split;
-    float *s_w = s_o; /* reuse: per (row) max and 1/sum */
+    float *s_ml = s_o;                       /* [nsp][ROWS][2], then weights [nsp][ROWS] */
+    float *s_row = s_o + 2 * SK_MERGE_MAX;   /* per row: max, 1/sum */
+    for (int e = tid; e < nsp * ROWS; e += 64 * SK_WAVES) {
+        const int sp = e / ROWS, rr = e - sp * ROWS;
+        const long long pr = ((long long)(first + sp) * p.Hkv + g) * ROWS + rr;
+        const float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + pr * 2);
+        s_ml[2 * e] = ml.x;
+        s_ml[2 * e + 1] = ml.y;
+    }
+    __syncthreads();
     if (tid < ROWS) {
         float M = -INFINITY;
-        for (int sp = 0; sp < nsp; sp++)
-            M = fmaxf(M, p.part_ml[(((long long)(first + sp) * p.Hkv + g) * ROWS + tid) * 2]);
+        for (int sp = 0; sp < nsp; sp++) M = fmaxf(M, s_ml[2 * (sp * ROWS + tid)]);
         const float Mu = M == -INFINITY ? 0.0f : M;
         float L = 0.0f;
         for (int sp = 0; sp < nsp; sp++) {
-            const long long pr = ((long long)(first + sp) * p.Hkv + g) * ROWS + tid;
-            L += __builtin_amdgcn_exp2f(p.part_ml[pr * 2] - Mu) * p.part_ml[pr * 2 + 1];
+            const int e = sp * ROWS + tid;
+            L += __builtin_amdgcn_exp2f(s_ml[2 * e] - Mu) * s_ml[2 * e + 1];
         }
-        s_w[2 * tid] = Mu;
-        s_w[2 * tid + 1] = L > 0.0f ? 1.0f / L : 0.0f;
+        s_row[2 * tid] = Mu;
+        s_row[2 * tid + 1] = L > 0.0f ? 1.0f / L : 0.0f;
+    }
+    __syncthreads();
+    for (int e = tid; e < nsp * ROWS; e += 64 * SK_WAVES) {
+        const int rr = e % ROWS;
+        s_ml[2 * e] = __builtin_amdgcn_exp2f(s_ml[2 * e] - s_row[2 * rr]); /* weight of (split, row) */
     }
     __syncthreads();
     constexpr int C4 = HD / 4;
@@ -568,27 +586,21 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_attn_sk(SkParams p) {
         const int rr = e / C4, d = (e - rr * C4) * 4;
         const int r = it.row0 + rr;
         if (r >= b.n_rows) continue;
-        const float Mu = s_w[2 * rr], inv = s_w[2 * rr + 1];
         f4 acc = {0.f, 0.f, 0.f, 0.f};
-        int sp = 0;
-        for (; sp + 4 <= nsp; sp += 4) {
-            f4 v[4];
-            float w[4];
+        for (int sp0 = 0; sp0 < nsp; sp0 += 8) {
+            f4 v[8];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const long long pr = ((long long)(first + sp + u) * p.Hkv + g) * ROWS + rr;
-                w[u] = p.part_ml[pr * 2];
-                v[u] = *reinterpret_cast<const f4 *>(p.part_o + pr * HD + d);
+            for (int u = 0; u < 8; u++) {
+                const int sp = min(sp0 + u, nsp - 1);
+                v[u] = *reinterpret_cast<const f4 *>(p.part_o + (((long long)(first + sp) * p.Hkv + g) * ROWS + rr) * HD + d);
             }
 #pragma unroll
-            for (int u = 0; u < 4; u++) acc += __builtin_amdgcn_exp2f(w[u] - Mu) * v[u];
-        }
-        for (; sp < nsp; sp++) {
-            const long long pr = ((long long)(first + sp) * p.Hkv + g) * ROWS + rr;
-            acc += __builtin_amdgcn_exp2f(p.part_ml[pr * 2] - Mu) * *reinterpret_cast<const f4 *>(p.part_o + pr * HD + d);
+            for (int u = 0; u < 8; u++)
+                if (sp0 + u < nsp) acc += s_ml[2 * ((sp0 + u) * ROWS + rr)] * v[u];
         }
         const int qi = r / G, hg = r - qi * G;
-        *reinterpret_cast<f4 *>(p.out + ((long long)(b.out_tok0 + qi) * Hq + (g * G + hg)) * HD + d) = acc * inv;
+        *reinterpret_cast<f4 *>(p.out + ((long long)(b.out_tok0 + qi) * Hq + (g * G + hg)) * HD + d) =
+            acc * s_row[2 * rr + 1];
     }
     if (tid == 0) p.counters[(long long)it.group * p.Hkv + g] = 0;
 }
