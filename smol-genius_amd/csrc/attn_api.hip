@@ -27,6 +27,7 @@
 
 extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t st);
 extern "C" int smol_launch_sk(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st);
+extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st);
 extern "C" int smol_launch_rope_apply(float *x, const float *cos_t, const float *sin_t,
                                       const int *pos, int seq, int n_heads, int hd, int kind,
                                       hipStream_t st);
@@ -112,6 +113,7 @@ struct smol_attn_ctx {
     int ring_next = 0;
     DevBuf desc;   /* device copy of the descriptor tables */
     DevBuf qs, kf, vtf, part_o, part_ml, counters;
+    DevBuf qs32; /* fp32 Q scratch of the decode kernel */
     int cu_count = 256;
     /* opt-in per-kernel timing: events bracketing each launch */
     bool timing = false;
@@ -226,7 +228,8 @@ extern "C" int smol_attn_ctx_destroy(smol_attn_ctx *ctx) {
     if (!ctx) return SMOL_ATTN_OK;
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
-    DevBuf *bufs[] = {&ctx->desc, &ctx->qs, &ctx->kf, &ctx->vtf, &ctx->part_o, &ctx->part_ml, &ctx->counters};
+    DevBuf *bufs[] = {&ctx->desc, &ctx->qs, &ctx->kf, &ctx->vtf, &ctx->part_o, &ctx->part_ml, &ctx->counters,
+                      &ctx->qs32};
     for (DevBuf *b : bufs)
         if (b->p) hipFree(b->p);
     for (auto &s : ctx->ring) {
@@ -474,6 +477,7 @@ struct Plan {
 };
 
 struct CallShape {
+    bool dec;             /* true: bf16 hi/lo staging + k_attn_dec; false: fp16 staging + k_attn_sk */
     const void *q, *k, *v;
     int dtype;
     int Hq, Hkv, hd;
@@ -520,6 +524,11 @@ static void plan_items(Plan &pl, int Hkv, int G, int window, int nt, int cu_coun
     const long long target_items = (long long)cu_count;
     long long per = (total_slabs * Hkv + target_items - 1) / std::max(1LL, target_items);
     int slabs_per_item = (int)std::max(8LL, per);
+    /* tuning override: SMOL_ATTN_SLABS_PER_ITEM=n fixes the key slabs per work item */
+    if (const char *ov = getenv("SMOL_ATTN_SLABS_PER_ITEM")) {
+        const int n = atoi(ov);
+        if (n > 0) slabs_per_item = n;
+    }
     int group = 0;
     const int max_split = 1024 / rows_per; /* the kernel's merge holds rows * n_split pairs in LDS */
     for (const Tile &t : tiles) {
@@ -549,14 +558,18 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     const int G = cs.Hq / cs.Hkv;
     int max_rows = 0;
     for (auto &b : pl.sb) max_rows = std::max(max_rows, b.n_rows);
-    const int nt = choose_nt(hd, max_rows);
+    const int nt = cs.dec ? (max_rows <= 16 || hd > 128 ? 1 : 2) : choose_nt(hd, max_rows);
     plan_items(pl, cs.Hkv, G, cs.window, nt, ctx->cu_count);
     const int rows_per = 16 * nt;
 
     /* workspace */
     int rc;
     const size_t fcap = (size_t)std::max(pl.fresh_rows, SMOL_SLAB);
-    if ((rc = dev_reserve(ctx->qs, (size_t)cs.Hkv * std::max(pl.q_rows, 1) * hdp * 2, ctx->stream))) return rc;
+    if (cs.dec) {
+        if ((rc = dev_reserve(ctx->qs32, (size_t)cs.Hkv * std::max(pl.q_rows, 1) * hdp * 4, ctx->stream))) return rc;
+    } else {
+        if ((rc = dev_reserve(ctx->qs, (size_t)cs.Hkv * std::max(pl.q_rows, 1) * hdp * 2, ctx->stream))) return rc;
+    }
     if ((rc = dev_reserve(ctx->kf, (size_t)cs.Hkv * fcap * hd * 2, ctx->stream))) return rc;
     if ((rc = dev_reserve(ctx->vtf, (size_t)cs.Hkv * fcap * hd * 2, ctx->stream))) return rc;
     const size_t n_items = pl.items.size();
@@ -609,6 +622,8 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     pp.qs_head_stride = (long long)std::max(pl.q_rows, 1) * hdp;
     pp.kc = kc; pp.vtc = vtc; pp.c_slot_stride = slot_stride; pp.cap = cap;
     pp.kf = (_Float16 *)ctx->kf.p; pp.vtf = (_Float16 *)ctx->vtf.p; pp.fcap = (int)fcap;
+    pp.stage = cs.dec ? SMOL_STAGE_QF32 : SMOL_STAGE_F16;
+    if (cs.dec) pp.qs32 = (float *)ctx->qs32.p;
     pp.batches = (const PrepBatch *)(dd + o_pb);
     pp.blocks = (const PrepBlock *)(dd + o_pblk);
     int mk = timing_begin(ctx, 0);
@@ -622,6 +637,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     sp.qs_head_stride = pp.qs_head_stride;
     sp.kc = kc; sp.vtc = vtc; sp.c_slot_stride = slot_stride; sp.cap = cap;
     sp.kf = (const _Float16 *)ctx->kf.p; sp.vtf = (const _Float16 *)ctx->vtf.p; sp.fcap = (int)fcap;
+    if (cs.dec) sp.qs32 = (const float *)ctx->qs32.p;
     sp.out = cs.out;
     sp.Hq = cs.Hq; sp.Hkv = cs.Hkv; sp.G = G;
     sp.window = cs.window;
@@ -632,7 +648,8 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     sp.part_ml = (float *)ctx->part_ml.p;
     sp.counters = (int *)ctx->counters.p;
     mk = timing_begin(ctx, 1);
-    rc = smol_launch_sk(&sp, hd, (int)n_items, nt, ctx->stream);
+    rc = cs.dec ? smol_launch_dec(&sp, hd, (int)n_items, nt, ctx->stream)
+                : smol_launch_sk(&sp, hd, (int)n_items, nt, ctx->stream);
     timing_end(ctx, mk);
     if (rc)
         return fail(rc == -1 ? SMOL_ATTN_ERR_UNSUPPORTED : SMOL_ATTN_ERR_DEVICE,
@@ -696,7 +713,9 @@ extern "C" int smol_attn_prefill(smol_attn_ctx *ctx, smol_kv_cache *kv, int laye
     pl.sb.push_back({seq_q * G, 0, 0, pos0, 0, pos0 + seq_q, 1, f0, 0, slot, 0, 0});
     pl.q_rows = seq_q * G;
     pl.fresh_rows = nf;
-    CallShape cs{q, k_new, v_new, dtype, n_heads, Hkv, hd, (long long)n_heads * hd,
+    /* short chunks stream the cache like a decode step; long ones are MFMA-bound */
+    const bool dec = seq_q * G <= 64;
+    CallShape cs{dec, q, k_new, v_new, dtype, n_heads, Hkv, hd, (long long)n_heads * hd,
                  (long long)Hkv * hd, scale, cap, window, rope, 1, 1, kv, layer, out};
     return run_plan(ctx, pl, cs);
 }
@@ -736,7 +755,7 @@ extern "C" int smol_attn_decode(smol_attn_ctx *ctx, smol_kv_cache *kv, int layer
     }
     pl.q_rows = n_seq * G;
     pl.fresh_rows = n_seq * SMOL_SLAB;
-    CallShape cs{q, k_new, v_new, dtype, n_heads, Hkv, hd, (long long)n_heads * hd,
+    CallShape cs{true, q, k_new, v_new, dtype, n_heads, Hkv, hd, (long long)n_heads * hd,
                  (long long)Hkv * hd, scale, cap, window, rope, 1, 1, kv, layer, out};
     return run_plan(ctx, pl, cs);
 }
@@ -758,7 +777,7 @@ extern "C" int smol_attn_causal(smol_attn_ctx *ctx, const void *q, const void *k
     pl.sb.push_back({seq_q * G, 0, 0, q_offset, 0, seq_k, 1, 0, 0, -1, 0, 0});
     pl.q_rows = seq_q * G;
     pl.fresh_rows = nf;
-    CallShape cs{q, k, v, dtype, n_heads, n_kv_heads, hd, (long long)n_heads * hd,
+    CallShape cs{false, q, k, v, dtype, n_heads, n_kv_heads, hd, (long long)n_heads * hd,
                  (long long)n_kv_heads * hd, scale, cap, window, nullptr, 0, 0, nullptr, 0, out};
     return run_plan(ctx, pl, cs);
 }
@@ -785,7 +804,7 @@ extern "C" int smol_attn_bidirectional(smol_attn_ctx *ctx, const void *q, const 
     }
     pl.q_rows = seq;
     pl.fresh_rows = nf;
-    CallShape cs{q, k, v, dtype, n_heads, n_heads, hd, (long long)n_heads * hd,
+    CallShape cs{false, q, k, v, dtype, n_heads, n_heads, hd, (long long)n_heads * hd,
                  (long long)n_heads * hd, scale, 0.0f, 0, nullptr, 0, 0, nullptr, 0, out};
     return run_plan(ctx, pl, cs);
 }

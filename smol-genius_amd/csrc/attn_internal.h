@@ -54,6 +54,12 @@ typedef struct {
     int pad;
 } SkItem;
 
+/* Q-scratch format written by k_prep (fresh K / V^T are fp16 in both):
+ *   SMOL_STAGE_F16    fp16 (the fp16-MFMA kernel k_attn_sk)
+ *   SMOL_STAGE_QF32   fp32 (k_attn_dec splits it into bf16 hi + lo for the
+ *                     bf16-MFMA cache slabs and rounds it to fp16 for the fresh slab) */
+enum { SMOL_STAGE_F16 = 0, SMOL_STAGE_QF32 = 1 };
+
 typedef struct {
     const _Float16 *qs;        /* Q scratch */
     long long qs_head_stride;  /* rows_total * hdp */
@@ -63,6 +69,7 @@ typedef struct {
     int cap;                   /* cache rows per (slot, kv head) */
     const _Float16 *kf;        /* fresh K [kv][fcap][hd] */
     const _Float16 *vtf;       /* fresh V^T [kv][hd][fcap] */
+    const float *qs32;         /* fp32 Q scratch (SMOL_STAGE_QF32) */
     int fcap;
     float *out;                /* [token][Hq][hd] fp32 */
     int Hq, Hkv, G;
@@ -108,6 +115,8 @@ typedef struct {
     _Float16 *qs; long long qs_head_stride;
     uint16_t *kc; uint16_t *vtc; long long c_slot_stride; int cap;
     _Float16 *kf; _Float16 *vtf; int fcap;
+    int stage;                 /* SMOL_STAGE_F16 or SMOL_STAGE_QF32 */
+    float *qs32;
     const PrepBatch *batches;
     const PrepBlock *blocks;
 } PrepParams;

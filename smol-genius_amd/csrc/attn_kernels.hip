@@ -21,6 +21,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "attn_internal.h"
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -205,8 +207,13 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
 #pragma unroll
                 for (int i = 0; i < 8; i++) v[i] *= p.qscale;
             }
-            *reinterpret_cast<uint4 *>(p.qs + (long long)g * p.qs_head_stride +
-                                       (long long)(b.q_row0 + t * G + hg) * hdp + d0) = pack_h8(v);
+            const long long qi = (long long)g * p.qs_head_stride + (long long)(b.q_row0 + t * G + hg) * hdp + d0;
+            if (p.stage == SMOL_STAGE_QF32) {
+                *reinterpret_cast<float4 *>(p.qs32 + qi) = make_float4(v[0], v[1], v[2], v[3]);
+                *reinterpret_cast<float4 *>(p.qs32 + qi + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            } else {
+                *reinterpret_cast<uint4 *>(p.qs + qi) = pack_h8(v);
+            }
         }
         return;
     }
@@ -289,6 +296,70 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
  */
 #define SK_WAVES 4
 #define SK_MERGE_MAX 1024 /* max ROWS * n_split of one merge group (LDS) */
+
+/* Merge of one split-K group by its last workgroup (all 64*SK_WAVES threads):
+ * all (max, sum) pairs of the group are loaded in one parallel sweep into
+ * LDS, each row's max and 1/sum and every split's weight are formed there,
+ * then each (row, 4 columns) element sums the weighted partials with eight
+ * independent loads in flight. The host keeps ROWS * n_split within
+ * SK_MERGE_MAX. Resets the group's counter for the next call. */
+template <int HD, int ROWS>
+__device__ __forceinline__ void merge_group(const SkParams &p, const SkItem &it, const SkBatch &b, int g, int tid,
+                                            float *s_o) {
+    const int G = p.G, Hq = p.Hq;
+    const int first = blockIdx.x - it.split;
+    const int nsp = it.n_split;
+    float *s_ml = s_o;                       /* [nsp][ROWS][2], then weights [nsp][ROWS] */
+    float *s_row = s_o + 2 * SK_MERGE_MAX;   /* per row: max, 1/sum */
+    for (int e = tid; e < nsp * ROWS; e += 64 * SK_WAVES) {
+        const int sp = e / ROWS, rr = e - sp * ROWS;
+        const long long pr = ((long long)(first + sp) * p.Hkv + g) * ROWS + rr;
+        const float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + pr * 2);
+        s_ml[2 * e] = ml.x;
+        s_ml[2 * e + 1] = ml.y;
+    }
+    __syncthreads();
+    if (tid < ROWS) {
+        float M = -INFINITY;
+        for (int sp = 0; sp < nsp; sp++) M = fmaxf(M, s_ml[2 * (sp * ROWS + tid)]);
+        const float Mu = M == -INFINITY ? 0.0f : M;
+        float L = 0.0f;
+        for (int sp = 0; sp < nsp; sp++) {
+            const int e = sp * ROWS + tid;
+            L += __builtin_amdgcn_exp2f(s_ml[2 * e] - Mu) * s_ml[2 * e + 1];
+        }
+        s_row[2 * tid] = Mu;
+        s_row[2 * tid + 1] = L > 0.0f ? 1.0f / L : 0.0f;
+    }
+    __syncthreads();
+    for (int e = tid; e < nsp * ROWS; e += 64 * SK_WAVES) {
+        const int rr = e % ROWS;
+        s_ml[2 * e] = __builtin_amdgcn_exp2f(s_ml[2 * e] - s_row[2 * rr]); /* weight of (split, row) */
+    }
+    __syncthreads();
+    constexpr int C4 = HD / 4;
+    for (int e = tid; e < ROWS * C4; e += 64 * SK_WAVES) {
+        const int rr = e / C4, d = (e - rr * C4) * 4;
+        const int r = it.row0 + rr;
+        if (r >= b.n_rows) continue;
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int sp0 = 0; sp0 < nsp; sp0 += 8) {
+            f4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int sp = min(sp0 + u, nsp - 1);
+                v[u] = *reinterpret_cast<const f4 *>(p.part_o + (((long long)(first + sp) * p.Hkv + g) * ROWS + rr) * HD + d);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (sp0 + u < nsp) acc += s_ml[2 * ((sp0 + u) * ROWS + rr)] * v[u];
+        }
+        const int qi = r / G, hg = r - qi * G;
+        *reinterpret_cast<f4 *>(p.out + ((long long)(b.out_tok0 + qi) * Hq + (g * G + hg)) * HD + d) =
+            acc * s_row[2 * rr + 1];
+    }
+    if (tid == 0) p.counters[(long long)it.group * p.Hkv + g] = 0;
+}
 
 template <int HD, int NT>
 __global__ __launch_bounds__(64 * SK_WAVES) void k_attn_sk(SkParams p) {
@@ -546,63 +617,299 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_attn_sk(SkParams p) {
     if (!s_last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 
-    /* merge: all (max, sum) pairs of the group are loaded in one parallel
-     * sweep into LDS, each row's max and 1/sum and every split's weight are
-     * formed there, then each (row, 4 columns) element sums the weighted
-     * partials with eight independent loads in flight. The host keeps
-     * ROWS * n_split within SK_MERGE_MAX. */
-    const int first = blockIdx.x - it.split;
-    const int nsp = it.n_split;
-    float *s_ml = s_o;                       /* [nsp][ROWS][2], then weights [nsp][ROWS] */
-    float *s_row = s_o + 2 * SK_MERGE_MAX;   /* per row: max, 1/sum */
-    for (int e = tid; e < nsp * ROWS; e += 64 * SK_WAVES) {
-        const int sp = e / ROWS, rr = e - sp * ROWS;
-        const long long pr = ((long long)(first + sp) * p.Hkv + g) * ROWS + rr;
-        const float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + pr * 2);
-        s_ml[2 * e] = ml.x;
-        s_ml[2 * e + 1] = ml.y;
-    }
-    __syncthreads();
-    if (tid < ROWS) {
-        float M = -INFINITY;
-        for (int sp = 0; sp < nsp; sp++) M = fmaxf(M, s_ml[2 * (sp * ROWS + tid)]);
-        const float Mu = M == -INFINITY ? 0.0f : M;
-        float L = 0.0f;
-        for (int sp = 0; sp < nsp; sp++) {
-            const int e = sp * ROWS + tid;
-            L += __builtin_amdgcn_exp2f(s_ml[2 * e] - Mu) * s_ml[2 * e + 1];
-        }
-        s_row[2 * tid] = Mu;
-        s_row[2 * tid + 1] = L > 0.0f ? 1.0f / L : 0.0f;
-    }
-    __syncthreads();
-    for (int e = tid; e < nsp * ROWS; e += 64 * SK_WAVES) {
-        const int rr = e % ROWS;
-        s_ml[2 * e] = __builtin_amdgcn_exp2f(s_ml[2 * e] - s_row[2 * rr]); /* weight of (split, row) */
-    }
-    __syncthreads();
-    constexpr int C4 = HD / 4;
-    for (int e = tid; e < ROWS * C4; e += 64 * SK_WAVES) {
-        const int rr = e / C4, d = (e - rr * C4) * 4;
-        const int r = it.row0 + rr;
-        if (r >= b.n_rows) continue;
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int sp0 = 0; sp0 < nsp; sp0 += 8) {
-            f4 v[8];
+    merge_group<HD, ROWS>(p, it, b, g, tid, s_o);
+}
+
+/* --------------------------------------------------------------- k_attn_dec */
+
+/*
+ * Key-parallel attention for decode and short chunks. Cache slabs run on
+ * bf16 MFMA (v_mfma_f32_16x16x32_bf16) with the cache's bf16 bits as the
+ * operands as loaded (no conversion); precision comes from splitting the
+ * other operand, Q = Qhi + Qlo and P = Phi + Plo (bf16 each, ~16
+ * significant bits together):  S = K.Qhi + K.Qlo,  O += V.Phi + V.Plo.
+ * The slab holding the keys this call appends runs on fp16 MFMA over the
+ * fp16 fresh staging (k_prep), with an fp16 copy of Q.
+ * Same lane layouts, wave split and merge as k_attn_sk. The running max is a
+ * lazy reference: the accumulator is rescaled only when some row's max grows
+ * by more than 2^LAZY_T (decided per wave by vote), so p <= 2^LAZY_T.
+ */
+typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+#define LAZY_T 8.0f
+
+__device__ __forceinline__ b8 as_b8(uint4 w) { return *reinterpret_cast<b8 *>(&w); }
+
+__device__ __forceinline__ void split8(const float *x, b8 &hi, b8 &lo) {
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int sp = min(sp0 + u, nsp - 1);
-                v[u] = *reinterpret_cast<const f4 *>(p.part_o + (((long long)(first + sp) * p.Hkv + g) * ROWS + rr) * HD + d);
+    for (int i = 0; i < 8; i++) {
+        const __bf16 h = (__bf16)x[i];
+        hi[i] = h;
+        lo[i] = (__bf16)(x[i] - (float)h);
+    }
+}
+
+template <int HD, int NT>
+__global__ __launch_bounds__(64 * SK_WAVES) void k_attn_dec(SkParams p) {
+    constexpr int KS = (HD + 31) / 32;
+    constexpr int DT = (HD + 15) / 16;
+    constexpr int HDP = KS * 32;
+    constexpr int ROWS = NT * 16;
+    constexpr int OSTR = DT * 16 + 4;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int c = lane & 15, j = lane >> 4;
+    const int g = blockIdx.y;
+    const SkItem it = p.items[blockIdx.x];
+    const SkBatch b = p.batches[it.batch];
+    const int G = p.G;
+    constexpr int SO = (SK_WAVES - 1) * ROWS * OSTR > 2 * SK_MERGE_MAX + 128 ? (SK_WAVES - 1) * ROWS * OSTR
+                                                                          : 2 * SK_MERGE_MAX + 128;
+    __shared__ float s_o[SO];
+    __shared__ float s_m[(SK_WAVES - 1) * ROWS], s_l[(SK_WAVES - 1) * ROWS];
+    __shared__ int s_last;
+
+    b8 qh[NT][KS], ql[NT][KS];
+    h8 qf[NT][KS];
+    int lo[NT], hi[NT];
+    float m[NT], l[NT];
+    f4 o[NT][DT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int r = it.row0 + nt * 16 + c;
+        const bool valid = r < b.n_rows;
+        const int qi = r / G;
+        int rl = b.key_lo, rh = b.key_hi;
+        if (b.causal) {
+            rh = min(rh, b.q_pos0 + qi + 1);
+            if (p.window > 0) rl = max(rl, b.q_pos0 + qi - p.window + 1);
+        }
+        lo[nt] = valid ? rl : 0;
+        hi[nt] = valid ? rh : 0;
+        m[nt] = -INFINITY;
+        l[nt] = 0.0f;
+        const float *qrow = p.qs32 + (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid ? r : 0)) * HDP;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (valid) {
+                const float4 a = *reinterpret_cast<const float4 *>(qrow + 32 * ks + 8 * j);
+                const float4 e = *reinterpret_cast<const float4 *>(qrow + 32 * ks + 8 * j + 4);
+                x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = e.x; x[5] = e.y; x[6] = e.z; x[7] = e.w;
+            }
+            split8(x, qh[nt][ks], ql[nt][ks]);
+#pragma unroll
+            for (int i = 0; i < 8; i++) qf[nt][ks][i] = (_Float16)x[i];
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) o[nt][dt] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    const uint16_t *kc = nullptr, *vtc = nullptr;
+    if (b.slot >= 0 && p.kc != nullptr) {
+        kc = p.kc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * HD;
+        vtc = p.vtc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * HD;
+    }
+    const uint16_t *kfh = reinterpret_cast<const uint16_t *>(p.kf) + (long long)g * p.fcap * HD +
+                          (long long)(b.fresh_row0 - b.fresh_pos0) * HD;
+    const uint16_t *vtfh = reinterpret_cast<const uint16_t *>(p.vtf) + (long long)g * p.fcap * HD +
+                           (b.fresh_row0 - b.fresh_pos0);
+    const int kt_row = 8 * (c >> 2) + (c & 3);
+
+    auto slab = [&](int k0, auto fresh_tag) {
+        constexpr bool FRESH = decltype(fresh_tag)::value;
+        const uint16_t *kb = FRESH ? kfh : kc;
+        const uint16_t *vb = FRESH ? vtfh : vtc;
+        const long long vs = FRESH ? p.fcap : p.cap;
+        uint4 kr[2][KS], vr[DT];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                const int d0 = 32 * ks + 8 * j;
+                const long long off = (long long)(k0 + kt_row + 4 * t) * HD + d0;
+                const bool ok = HD % 32 == 0 || d0 < HD;
+                kr[t][ks] = ok ? *reinterpret_cast<const uint4 *>(kb + off) : make_uint4(0, 0, 0, 0);
             }
 #pragma unroll
-            for (int u = 0; u < 8; u++)
-                if (sp0 + u < nsp) acc += s_ml[2 * ((sp0 + u) * ROWS + rr)] * v[u];
+        for (int dt = 0; dt < DT; dt++) {
+            const int d = 16 * dt + c;
+            const long long off = (long long)d * vs + k0 + 8 * j;
+            const bool ok = HD % 16 == 0 || d < HD;
+            vr[dt] = ok ? *reinterpret_cast<const uint4 *>(vb + off) : make_uint4(0, 0, 0, 0);
         }
-        const int qi = r / G, hg = r - qi * G;
-        *reinterpret_cast<f4 *>(p.out + ((long long)(b.out_tok0 + qi) * Hq + (g * G + hg)) * HD + d) =
-            acc * s_row[2 * rr + 1];
+        f4 sacc[NT][2];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) {
+                    if (FRESH) {
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<h8 *>(&kr[t][ks]), qf[nt][ks],
+                                                                     acc, 0, 0, 0);
+                    } else {
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(kr[t][ks]), qh[nt][ks], acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(kr[t][ks]), ql[nt][ks], acc, 0, 0, 0);
+                    }
+                }
+                sacc[nt][t] = acc;
+            }
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            float sv[8];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int key = k0 + 8 * j + 4 * t + i;
+                    float x = sacc[nt][t][i];
+                    if (p.cap2 > 0.0f) x = p.cap2 * tanhf(x / p.cap2);
+                    x = (key >= lo[nt] && key < hi[nt]) ? x : -INFINITY;
+                    sv[4 * t + i] = x;
+                    mx = fmaxf(mx, x);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const bool need = mx > m[nt] + LAZY_T;
+            if (__any(need)) {
+                const float m_new = need ? mx : m[nt];
+                const float alpha = need ? __builtin_amdgcn_exp2f(m[nt] - m_new) : 1.0f;
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) o[nt][dt] *= alpha;
+                l[nt] *= alpha;
+                m[nt] = m_new;
+            }
+            const float m_use = m[nt] == -INFINITY ? 0.0f : m[nt];
+            float pv[8];
+            float ps = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                pv[e] = __builtin_amdgcn_exp2f(sv[e] - m_use);
+                ps += pv[e];
+            }
+            l[nt] += ps;
+            if (FRESH) {
+                h8 pf;
+#pragma unroll
+                for (int e = 0; e < 8; e++) pf[e] = (_Float16)pv[e];
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++)
+                    o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<h8 *>(&vr[dt]), pf, o[nt][dt],
+                                                                       0, 0, 0);
+            } else {
+                b8 ph, pl;
+                split8(pv, ph, pl);
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) {
+                    o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(vr[dt]), ph, o[nt][dt], 0, 0, 0);
+                    o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(vr[dt]), pl, o[nt][dt], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    const int step = SMOL_SLAB * SK_WAVES;
+    for (int k0 = it.key_begin + wave * SMOL_SLAB; k0 < it.key_end; k0 += step) {
+        if (k0 >= b.fresh_pos0) slab(k0, std::true_type{});
+        else slab(k0, std::false_type{});
     }
-    if (tid == 0) p.counters[(long long)it.group * p.Hkv + g] = 0;
+
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        l[nt] += __shfl_xor(l[nt], 16);
+        l[nt] += __shfl_xor(l[nt], 32);
+    }
+
+    /* ---- combine the waves' states through LDS into wave 0 ---- */
+    if (wave > 0) {
+        const int sl = (wave - 1) * ROWS;
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int rr = nt * 16 + c;
+            float *so = s_o + (sl + rr) * OSTR;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) *reinterpret_cast<f4 *>(so + 16 * dt + 4 * j) = o[nt][dt];
+            if (j == 0) { s_m[sl + rr] = m[nt]; s_l[sl + rr] = l[nt]; }
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int rr = nt * 16 + c;
+            float M = m[nt];
+#pragma unroll
+            for (int w = 0; w < SK_WAVES - 1; w++) M = fmaxf(M, s_m[w * ROWS + rr]);
+            const float Mu = M == -INFINITY ? 0.0f : M;
+            const float a0 = __builtin_amdgcn_exp2f(m[nt] - Mu);
+            float L = l[nt] * a0;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) o[nt][dt] *= a0;
+#pragma unroll
+            for (int w = 0; w < SK_WAVES - 1; w++) {
+                const float aw = __builtin_amdgcn_exp2f(s_m[w * ROWS + rr] - Mu);
+                L += s_l[w * ROWS + rr] * aw;
+                const float *so = s_o + (w * ROWS + rr) * OSTR;
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) o[nt][dt] += aw * *reinterpret_cast<const f4 *>(so + 16 * dt + 4 * j);
+            }
+            m[nt] = M;
+            l[nt] = L;
+        }
+    }
+
+    const int Hq = p.Hq;
+    if (it.n_split == 1) {
+        if (wave != 0) return;
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int r = it.row0 + nt * 16 + c;
+            if (r >= b.n_rows) continue;
+            const int qi = r / G, hg = r - qi * G;
+            float *orow = p.out + ((long long)(b.out_tok0 + qi) * Hq + (g * G + hg)) * HD;
+            const float inv = l[nt] > 0.0f ? 1.0f / l[nt] : 0.0f;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                const int d = 16 * dt + 4 * j;
+                if (HD % 16 != 0 && d >= HD) continue;
+                *reinterpret_cast<f4 *>(orow + d) = o[nt][dt] * inv;
+            }
+        }
+        return;
+    }
+
+    const long long pbase = ((long long)blockIdx.x * p.Hkv + g) * ROWS;
+    if (wave == 0) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int rr = nt * 16 + c;
+            float *po = p.part_o + (pbase + rr) * HD;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                const int d = 16 * dt + 4 * j;
+                if (HD % 16 != 0 && d >= HD) continue;
+                *reinterpret_cast<f4 *>(po + d) = o[nt][dt];
+            }
+            if (j == 0) {
+                p.part_ml[(pbase + rr) * 2 + 0] = m[nt];
+                p.part_ml[(pbase + rr) * 2 + 1] = l[nt];
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        int prev = 0;
+        if (lane == 0)
+            prev = __hip_atomic_fetch_add(p.counters + (long long)it.group * p.Hkv + g, 1, __ATOMIC_ACQ_REL,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+        prev = __shfl(prev, 0);
+        if (lane == 0) s_last = prev == it.n_split - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    merge_group<HD, ROWS>(p, it, b, g, tid, s_o);
 }
 
 /* ------------------------------------------------------------ k_rope_apply */
@@ -670,6 +977,28 @@ static int launch_sk_hd(const SkParams *sp, int n_items, int nt, hipStream_t st)
     else if (nt == 4 && HD <= 64) hipLaunchKernelGGL((k_attn_sk<HD, (HD <= 64 ? 4 : 1)>), grid, block, 0, st, *sp);
     else return -1;
     return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+template <int HD>
+static int launch_dec_hd(const SkParams *sp, int n_items, int nt, hipStream_t st) {
+    dim3 grid(n_items, sp->Hkv), block(64 * SK_WAVES);
+    if (nt == 1) hipLaunchKernelGGL((k_attn_dec<HD, 1>), grid, block, 0, st, *sp);
+    else if (nt == 2 && HD <= 128) hipLaunchKernelGGL((k_attn_dec<HD, (HD <= 128 ? 2 : 1)>), grid, block, 0, st, *sp);
+    else return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st) {
+    if (n_items <= 0) return 0;
+    switch (hd) {
+    case 64: return launch_dec_hd<64>(sp, n_items, nt, st);
+    case 72: return launch_dec_hd<72>(sp, n_items, nt, st);
+    case 80: return launch_dec_hd<80>(sp, n_items, nt, st);
+    case 96: return launch_dec_hd<96>(sp, n_items, nt, st);
+    case 128: return launch_dec_hd<128>(sp, n_items, nt, st);
+    case 256: return launch_dec_hd<256>(sp, n_items, nt, st);
+    default: return -1;
+    }
 }
 
 extern "C" int smol_launch_sk(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st) {
