@@ -649,7 +649,7 @@ __device__ __forceinline__ void split8(const float *x, b8 &hi, b8 &lo) {
 }
 
 template <int HD, int NT>
-__global__ __launch_bounds__(64 * SK_WAVES) void k_attn_dec(SkParams p) {
+__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_attn_dec(SkParams p) {
     constexpr int KS = (HD + 31) / 32;
     constexpr int DT = (HD + 15) / 16;
     constexpr int HDP = KS * 32;
@@ -716,28 +716,35 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_attn_dec(SkParams p) {
                            (b.fresh_row0 - b.fresh_pos0);
     const int kt_row = 8 * (c >> 2) + (c & 3);
 
-    auto slab = [&](int k0, auto fresh_tag) {
-        constexpr bool FRESH = decltype(fresh_tag)::value;
-        const uint16_t *kb = FRESH ? kfh : kc;
-        const uint16_t *vb = FRESH ? vtfh : vtc;
-        const long long vs = FRESH ? p.fcap : p.cap;
-        uint4 kr[2][KS], vr[DT];
+    /* raw 16-byte words of one slab: K A-operands and V^T A-operands */
+    struct Raw {
+        uint4 k[2][KS];
+        uint4 v[DT];
+    };
+    auto issue = [&](int k0, Raw &r) {
+        const bool fr = k0 >= b.fresh_pos0;
+        const uint16_t *kb = fr ? kfh : kc;
+        const uint16_t *vb = fr ? vtfh : vtc;
+        const long long vs = fr ? p.fcap : p.cap;
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
                 const int d0 = 32 * ks + 8 * j;
-                const long long off = (long long)(k0 + kt_row + 4 * t) * HD + d0;
                 const bool ok = HD % 32 == 0 || d0 < HD;
-                kr[t][ks] = ok ? *reinterpret_cast<const uint4 *>(kb + off) : make_uint4(0, 0, 0, 0);
+                r.k[t][ks] = ok ? *reinterpret_cast<const uint4 *>(kb + (long long)(k0 + kt_row + 4 * t) * HD + d0)
+                                : make_uint4(0, 0, 0, 0);
             }
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) {
             const int d = 16 * dt + c;
-            const long long off = (long long)d * vs + k0 + 8 * j;
             const bool ok = HD % 16 == 0 || d < HD;
-            vr[dt] = ok ? *reinterpret_cast<const uint4 *>(vb + off) : make_uint4(0, 0, 0, 0);
+            r.v[dt] = ok ? *reinterpret_cast<const uint4 *>(vb + (long long)d * vs + k0 + 8 * j) : make_uint4(0, 0, 0, 0);
         }
+    };
+
+    auto compute = [&](int k0, const Raw &r, auto fresh_tag) {
+        constexpr bool FRESH = decltype(fresh_tag)::value;
         f4 sacc[NT][2];
 #pragma unroll
         for (int nt = 0; nt < NT; nt++)
@@ -747,11 +754,11 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_attn_dec(SkParams p) {
 #pragma unroll
                 for (int ks = 0; ks < KS; ks++) {
                     if (FRESH) {
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<h8 *>(&kr[t][ks]), qf[nt][ks],
-                                                                     acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const h8 *>(&r.k[t][ks]),
+                                                                     qf[nt][ks], acc, 0, 0, 0);
                     } else {
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(kr[t][ks]), qh[nt][ks], acc, 0, 0, 0);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(kr[t][ks]), ql[nt][ks], acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(r.k[t][ks]), qh[nt][ks], acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(r.k[t][ks]), ql[nt][ks], acc, 0, 0, 0);
                     }
                 }
                 sacc[nt][t] = acc;
@@ -797,24 +804,32 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_attn_dec(SkParams p) {
                 for (int e = 0; e < 8; e++) pf[e] = (_Float16)pv[e];
 #pragma unroll
                 for (int dt = 0; dt < DT; dt++)
-                    o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<h8 *>(&vr[dt]), pf, o[nt][dt],
-                                                                       0, 0, 0);
+                    o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const h8 *>(&r.v[dt]), pf,
+                                                                       o[nt][dt], 0, 0, 0);
             } else {
                 b8 ph, pl;
                 split8(pv, ph, pl);
 #pragma unroll
                 for (int dt = 0; dt < DT; dt++) {
-                    o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(vr[dt]), ph, o[nt][dt], 0, 0, 0);
-                    o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(vr[dt]), pl, o[nt][dt], 0, 0, 0);
+                    o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(r.v[dt]), ph, o[nt][dt], 0, 0, 0);
+                    o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(r.v[dt]), pl, o[nt][dt], 0, 0, 0);
                 }
             }
         }
     };
 
+    /* each wave streams slabs wave, wave + SK_WAVES, ... with the next slab's
+     * loads in flight while the current one is computed */
     const int step = SMOL_SLAB * SK_WAVES;
-    for (int k0 = it.key_begin + wave * SMOL_SLAB; k0 < it.key_end; k0 += step) {
-        if (k0 >= b.fresh_pos0) slab(k0, std::true_type{});
-        else slab(k0, std::false_type{});
+    int k0 = it.key_begin + wave * SMOL_SLAB;
+    Raw cur, nxt;
+    if (k0 < it.key_end) issue(k0, cur);
+    for (; k0 < it.key_end; k0 += step) {
+        const bool more = k0 + step < it.key_end;
+        if (more) issue(k0 + step, nxt);
+        if (k0 >= b.fresh_pos0) compute(k0, cur, std::true_type{});
+        else compute(k0, cur, std::false_type{});
+        cur = nxt;
     }
 
 #pragma unroll
