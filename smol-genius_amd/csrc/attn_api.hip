@@ -446,15 +446,13 @@ extern "C" int smol_kv_cache_reserve(smol_kv_cache *kv, int required) {
     HIP_TRY(hipMemsetAsync(nvt, 0, bytes, ctx->stream));
     const int hd = kv->hd;
     const size_t n_blocks = (size_t)kv->n_layers * kv->n_slots * kv->n_kv;
-    for (size_t blk = 0; blk < n_blocks; blk++) {
-        /* K: [cap][hd] contiguous per (layer, slot, head) */
-        HIP_TRY(hipMemcpyAsync(nk + blk * nc * hd, kv->k + blk * kv->cap * hd,
-                               (size_t)kv->cap * hd * sizeof(uint16_t), hipMemcpyDeviceToDevice, ctx->stream));
-        /* V^T: [hd][cap] rows of cap -> rows of nc */
-        HIP_TRY(hipMemcpy2DAsync(nvt + blk * nc * hd, (size_t)nc * sizeof(uint16_t),
-                                 kv->vt + blk * kv->cap * hd, (size_t)kv->cap * sizeof(uint16_t),
-                                 (size_t)kv->cap * sizeof(uint16_t), hd, hipMemcpyDeviceToDevice, ctx->stream));
-    }
+    /* per (layer, slot, head): K [cap][hd] and slab-blocked V^T [cap/32][hd][32]
+     * are both prefixes of the grown region */
+    const size_t old_bytes = (size_t)kv->cap * hd * sizeof(uint16_t);
+    HIP_TRY(hipMemcpy2DAsync(nk, (size_t)nc * hd * sizeof(uint16_t), kv->k, old_bytes, old_bytes, n_blocks,
+                             hipMemcpyDeviceToDevice, ctx->stream));
+    HIP_TRY(hipMemcpy2DAsync(nvt, (size_t)nc * hd * sizeof(uint16_t), kv->vt, old_bytes, old_bytes, n_blocks,
+                             hipMemcpyDeviceToDevice, ctx->stream));
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     hipFree(kv->k);
     hipFree(kv->vt);
@@ -875,17 +873,20 @@ extern "C" int smol_kv_cache_read(smol_kv_cache *kv, int layer, int slot, int po
     if (rc) return rc;
     HIP_TRY(hipStreamSynchronize(kv->ctx->stream));
     const int hd = kv->hd, H = kv->n_kv;
-    std::vector<uint16_t> kt((size_t)n * hd), vt((size_t)hd * n);
+    const int b0 = pos0 / SMOL_SLAB, b1 = (pos0 + n + SMOL_SLAB - 1) / SMOL_SLAB;
+    std::vector<uint16_t> kt((size_t)n * hd), vt((size_t)(b1 - b0) * SMOL_SLAB * hd);
     for (int g = 0; g < H; g++) {
         const size_t base = (size_t)layer * kv_layer_elems(kv) + (size_t)slot * kv_slot_elems(kv) + (size_t)g * kv->cap * hd;
         HIP_TRY(hipMemcpy(kt.data(), kv->k + base + (size_t)pos0 * hd, kt.size() * 2, hipMemcpyDeviceToHost));
-        HIP_TRY(hipMemcpy2D(vt.data(), (size_t)n * 2, kv->vt + base + pos0, (size_t)kv->cap * 2, (size_t)n * 2, hd,
-                            hipMemcpyDeviceToHost));
-        for (int r = 0; r < n; r++)
+        HIP_TRY(hipMemcpy(vt.data(), kv->vt + base + (size_t)b0 * SMOL_SLAB * hd, vt.size() * 2, hipMemcpyDeviceToHost));
+        for (int r = 0; r < n; r++) {
+            const int pos = pos0 + r;
+            const size_t vb = (size_t)(pos / SMOL_SLAB - b0) * SMOL_SLAB * hd + pos % SMOL_SLAB;
             for (int d = 0; d < hd; d++) {
                 k_out[((size_t)r * H + g) * hd + d] = kt[(size_t)r * hd + d];
-                v_out[((size_t)r * H + g) * hd + d] = vt[(size_t)d * n + r];
+                v_out[((size_t)r * H + g) * hd + d] = vt[vb + (size_t)d * SMOL_SLAB];
             }
+        }
     }
     return SMOL_ATTN_OK;
 }

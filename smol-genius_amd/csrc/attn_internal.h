@@ -4,15 +4,17 @@
  *
  * Device data layout (one GPU):
  *   KV cache   K  : bf16 [layer][slot][kv_head][cap][head_dim]   (post-RoPE)
- *              V^T: bf16 [layer][slot][kv_head][head_dim][cap]   (transposed, so
- *                   the P.V product reads 8 consecutive keys of one column)
+ *              V^T: bf16 [layer][slot][kv_head][cap/32][head_dim][32]
+ *                   (transposed within 32-key slabs: the P.V product reads 8
+ *                   consecutive keys of one column, and one slab of V is one
+ *                   contiguous block, as one slab of K is)
  *   fresh K/V  fp16 copies of the keys a call appends (and of the cache rows
  *              that share their 32-key slab), same two layouts with `fcap`
  *              rows; attention over a call's own keys uses these, so a key
  *              rotated in fp32 is never read back through bf16 rounding.
- *   Q scratch  fp16 [kv_head][row][hdp], row = q_index * G + head_in_group,
+ *   Q scratch  [kv_head][row][hdp], row = q_index * G + head_in_group,
  *              rotated and pre-multiplied by scale * log2(e); hdp = head_dim
- *              rounded up to 32 and zero-filled.
+ *              rounded up to 32 and zero-filled; fp16 or fp32 (see below).
  */
 #ifndef SMOL_ATTN_INTERNAL_H
 #define SMOL_ATTN_INTERNAL_H

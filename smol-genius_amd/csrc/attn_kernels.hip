@@ -248,31 +248,34 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
         for (int i = 0; i < 8; i++) sv[r * 257 + d0 + i] = vv[i];
     }
     __syncthreads();
-    /* V^T: chunk (d, 8 consecutive positions q0..q0+7) */
+    /* V^T (slab-blocked, the slab's 32 positions of column d are contiguous):
+     * chunk (d, 8 consecutive positions q0..q0+7) */
+    uint16_t *vtc_blk = has_cache ? vtc + (long long)(pos_base / SMOL_SLAB) * SMOL_SLAB * hd : nullptr;
+    _Float16 *vtf_blk = vtf + (long long)(frow_base / SMOL_SLAB) * SMOL_SLAB * hd;
     for (int e = tid; e < hd * (SMOL_SLAB / 8); e += blockDim.x) {
         const int d = e / (SMOL_SLAB / 8), q0 = (e - d * (SMOL_SLAB / 8)) * 8;
         const int pos = pos_base + q0;
+        const int ci = d * SMOL_SLAB + q0;
         float v[8];
         if (pos + 8 <= new_lo) {
-            if (has_cache) unpack_bf16x8(*reinterpret_cast<const uint4 *>(vtc + (long long)d * p.cap + pos), v);
+            if (has_cache) unpack_bf16x8(*reinterpret_cast<const uint4 *>(vtc_blk + ci), v);
             else { for (int i = 0; i < 8; i++) v[i] = 0.0f; }
         } else {
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const int ps = pos + i;
-                v[i] = ps < new_lo ? (has_cache ? bf16_to_f32(vtc[(long long)d * p.cap + ps]) : 0.0f)
-                                   : sv[(q0 + i) * 257 + d];
+                v[i] = ps < new_lo ? (has_cache ? bf16_to_f32(vtc_blk[ci + i]) : 0.0f) : sv[(q0 + i) * 257 + d];
             }
             if (has_cache) {
                 if (pos >= new_lo && pos + 8 <= new_hi) {
-                    *reinterpret_cast<uint4 *>(vtc + (long long)d * p.cap + pos) = pack_bf16x8(v);
+                    *reinterpret_cast<uint4 *>(vtc_blk + ci) = pack_bf16x8(v);
                 } else {
                     for (int i = 0; i < 8; i++)
-                        if (pos + i >= new_lo && pos + i < new_hi) vtc[(long long)d * p.cap + pos + i] = f32_to_bf16(v[i]);
+                        if (pos + i >= new_lo && pos + i < new_hi) vtc_blk[ci + i] = f32_to_bf16(v[i]);
                 }
             }
         }
-        *reinterpret_cast<uint4 *>(vtf + (long long)d * p.fcap + frow_base + q0) = pack_h8(v);
+        *reinterpret_cast<uint4 *>(vtf_blk + ci) = pack_h8(v);
     }
 }
 
@@ -418,16 +421,16 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_attn_sk(SkParams p) {
     }
     const uint16_t *kf = reinterpret_cast<const uint16_t *>(p.kf) + (long long)g * p.fcap * HD +
                          (long long)(b.fresh_row0 - b.fresh_pos0) * HD;
+    /* V^T is slab-blocked: key k, column d at (k / 32) * 32 HD + d * 32 + k % 32 */
     const uint16_t *vtf = reinterpret_cast<const uint16_t *>(p.vtf) + (long long)g * p.fcap * HD +
-                          (b.fresh_row0 - b.fresh_pos0);
+                          (long long)((b.fresh_row0 - b.fresh_pos0) / SMOL_SLAB) * SMOL_SLAB * HD;
     const int kt_row = 8 * (c >> 2) + (c & 3); /* gathered key of A-operand row c, tile 0 */
 
     uint4 kraw[2][KS], vraw[DT];
     auto issue = [&](int k0) {
         const bool fr = k0 >= b.fresh_pos0;
         const uint16_t *kb = fr ? kf : kc;
-        const uint16_t *vb = fr ? vtf : vtc;
-        const long long vs = fr ? p.fcap : p.cap;
+        const uint16_t *vb = (fr ? vtf : vtc) + (long long)(k0 / SMOL_SLAB) * SMOL_SLAB * HD;
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
@@ -440,7 +443,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_attn_sk(SkParams p) {
         for (int dt = 0; dt < DT; dt++) {
             const int d = 16 * dt + c;
             if (HD % 16 != 0 && d >= HD) { vraw[dt] = make_uint4(0, 0, 0, 0); continue; }
-            vraw[dt] = *reinterpret_cast<const uint4 *>(vb + (long long)d * vs + k0 + 8 * j);
+            vraw[dt] = *reinterpret_cast<const uint4 *>(vb + d * SMOL_SLAB + 8 * j);
         }
     };
 
@@ -713,7 +716,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
     const uint16_t *kfh = reinterpret_cast<const uint16_t *>(p.kf) + (long long)g * p.fcap * HD +
                           (long long)(b.fresh_row0 - b.fresh_pos0) * HD;
     const uint16_t *vtfh = reinterpret_cast<const uint16_t *>(p.vtf) + (long long)g * p.fcap * HD +
-                           (b.fresh_row0 - b.fresh_pos0);
+                           (long long)((b.fresh_row0 - b.fresh_pos0) / SMOL_SLAB) * SMOL_SLAB * HD;
     const int kt_row = 8 * (c >> 2) + (c & 3);
 
     /* raw 16-byte words of one slab: K A-operands and V^T A-operands */
@@ -724,8 +727,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
     auto issue = [&](int k0, Raw &r) {
         const bool fr = k0 >= b.fresh_pos0;
         const uint16_t *kb = fr ? kfh : kc;
-        const uint16_t *vb = fr ? vtfh : vtc;
-        const long long vs = fr ? p.fcap : p.cap;
+        const uint16_t *vb = (fr ? vtfh : vtc) + (long long)(k0 / SMOL_SLAB) * SMOL_SLAB * HD;
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
@@ -739,7 +741,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
         for (int dt = 0; dt < DT; dt++) {
             const int d = 16 * dt + c;
             const bool ok = HD % 16 == 0 || d < HD;
-            r.v[dt] = ok ? *reinterpret_cast<const uint4 *>(vb + (long long)d * vs + k0 + 8 * j) : make_uint4(0, 0, 0, 0);
+            r.v[dt] = ok ? *reinterpret_cast<const uint4 *>(vb + d * SMOL_SLAB + 8 * j) : make_uint4(0, 0, 0, 0);
         }
     };
 
