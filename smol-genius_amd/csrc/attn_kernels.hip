@@ -651,6 +651,24 @@ __device__ __forceinline__ void split8(const float *x, b8 &hi, b8 &lo) {
     }
 }
 
+/* Raw buffer resources: a base address plus a byte range; a load whose
+ * VGPR offset (+ immediate) is past the range returns zero, which is how the
+ * padded columns of head_dim 72 / 80 / 96 read as zeros. */
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef unsigned u4v __attribute__((ext_vector_type(4)));
+#define RSRC_WORD3 0x00020000
+#define OOB_OFF 0x7FFFFFF0u
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *ptr, long long bytes) {
+    const long long n = bytes < 0x7FFF0000LL ? bytes : 0x7FFF0000LL;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(ptr), (short)0, (int)n, RSRC_WORD3);
+}
+
+__device__ __forceinline__ uint4 bload(rsrc_t r, unsigned voff, unsigned soff) {
+    const u4v v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 template <int HD, int NT>
 __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_attn_dec(SkParams p) {
     constexpr int KS = (HD + 31) / 32;
@@ -658,6 +676,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
     constexpr int HDP = KS * 32;
     constexpr int ROWS = NT * 16;
     constexpr int OSTR = DT * 16 + 4;
+    constexpr unsigned SLAB_K_BYTES = SMOL_SLAB * HD * 2; /* one slab of K, and one slab-block of V^T */
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
@@ -677,6 +696,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
     int lo[NT], hi[NT];
     float m[NT], l[NT];
     f4 o[NT][DT];
+    int lo_max = -(1 << 30), hi_min = 1 << 30; /* over this lane's valid rows */
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         const int r = it.row0 + nt * 16 + c;
@@ -687,8 +707,11 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
             rh = min(rh, b.q_pos0 + qi + 1);
             if (p.window > 0) rl = max(rl, b.q_pos0 + qi - p.window + 1);
         }
-        lo[nt] = valid ? rl : 0;
-        hi[nt] = valid ? rh : 0;
+        /* rows past the batch are never stored: leave them unmasked */
+        lo[nt] = valid ? rl : -(1 << 30);
+        hi[nt] = valid ? rh : (1 << 30);
+        lo_max = max(lo_max, lo[nt]);
+        hi_min = min(hi_min, hi[nt]);
         m[nt] = -INFINITY;
         l[nt] = 0.0f;
         const float *qrow = p.qs32 + (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid ? r : 0)) * HDP;
@@ -707,42 +730,56 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) o[nt][dt] = f4{0.f, 0.f, 0.f, 0.f};
     }
-
-    const uint16_t *kc = nullptr, *vtc = nullptr;
-    if (b.slot >= 0 && p.kc != nullptr) {
-        kc = p.kc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * HD;
-        vtc = p.vtc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * HD;
+    /* the slab [k0, k0 + 32) needs no masking when it lies inside every row's range */
+#pragma unroll
+    for (int sh = 1; sh < 16; sh <<= 1) {
+        lo_max = max(lo_max, __shfl_xor(lo_max, sh));
+        hi_min = min(hi_min, __shfl_xor(hi_min, sh));
     }
-    const uint16_t *kfh = reinterpret_cast<const uint16_t *>(p.kf) + (long long)g * p.fcap * HD +
-                          (long long)(b.fresh_row0 - b.fresh_pos0) * HD;
-    const uint16_t *vtfh = reinterpret_cast<const uint16_t *>(p.vtf) + (long long)g * p.fcap * HD +
-                           (long long)((b.fresh_row0 - b.fresh_pos0) / SMOL_SLAB) * SMOL_SLAB * HD;
-    const int kt_row = 8 * (c >> 2) + (c & 3);
+    lo_max = __builtin_amdgcn_readfirstlane(lo_max);
+    hi_min = __builtin_amdgcn_readfirstlane(hi_min);
 
-    /* raw 16-byte words of one slab: K A-operands and V^T A-operands */
+    /* buffer resources: the cache region of (slot, head) and the fresh region of head */
+    rsrc_t rk_c = make_rsrc(nullptr, 0), rv_c = make_rsrc(nullptr, 0);
+    if (b.slot >= 0 && p.kc != nullptr) {
+        const long long cb = (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * HD;
+        rk_c = make_rsrc(p.kc + cb, (long long)p.cap * HD * 2);
+        rv_c = make_rsrc(p.vtc + cb, (long long)p.cap * HD * 2);
+    }
+    const rsrc_t rk_f = make_rsrc(p.kf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
+    const rsrc_t rv_f = make_rsrc(p.vtf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
+    /* lane-constant byte offsets within a slab */
+    const int kt_row = 8 * (c >> 2) + (c & 3);
+    unsigned vo_k[2][KS], vo_v[DT];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            const int d0 = 32 * ks + 8 * j;
+            vo_k[t][ks] = (HD % 32 == 0 || d0 < HD) ? (unsigned)(((kt_row + 4 * t) * HD + d0) * 2) : OOB_OFF;
+        }
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) {
+        const int d = 16 * dt + c;
+        vo_v[dt] = (HD % 16 == 0 || d < HD) ? (unsigned)((d * SMOL_SLAB + 8 * j) * 2) : OOB_OFF;
+    }
+
     struct Raw {
         uint4 k[2][KS];
         uint4 v[DT];
     };
+    /* a slab's loads: uniform choice of resource and slab offset (SGPRs) */
     auto issue = [&](int k0, Raw &r) {
         const bool fr = k0 >= b.fresh_pos0;
-        const uint16_t *kb = fr ? kfh : kc;
-        const uint16_t *vb = (fr ? vtfh : vtc) + (long long)(k0 / SMOL_SLAB) * SMOL_SLAB * HD;
+        const int kr = fr ? b.fresh_row0 + (k0 - b.fresh_pos0) : k0;
+        const unsigned so = (unsigned)(kr / SMOL_SLAB) * SLAB_K_BYTES;
+        const rsrc_t rk = fr ? rk_f : rk_c, rv = fr ? rv_f : rv_c;
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) {
-                const int d0 = 32 * ks + 8 * j;
-                const bool ok = HD % 32 == 0 || d0 < HD;
-                r.k[t][ks] = ok ? *reinterpret_cast<const uint4 *>(kb + (long long)(k0 + kt_row + 4 * t) * HD + d0)
-                                : make_uint4(0, 0, 0, 0);
-            }
+            for (int ks = 0; ks < KS; ks++) r.k[t][ks] = bload(rk, vo_k[t][ks], so);
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            const int d = 16 * dt + c;
-            const bool ok = HD % 16 == 0 || d < HD;
-            r.v[dt] = ok ? *reinterpret_cast<const uint4 *>(vb + d * SMOL_SLAB + 8 * j) : make_uint4(0, 0, 0, 0);
-        }
+        for (int dt = 0; dt < DT; dt++) r.v[dt] = bload(rv, vo_v[dt], so);
     };
 
     auto compute = [&](int k0, const Raw &r, auto fresh_tag) {
@@ -765,21 +802,28 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
                 }
                 sacc[nt][t] = acc;
             }
+        const bool full = k0 >= lo_max && k0 + SMOL_SLAB <= hi_min;
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             float sv[8];
-            float mx = -INFINITY;
 #pragma unroll
             for (int t = 0; t < 2; t++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int key = k0 + 8 * j + 4 * t + i;
-                    float x = sacc[nt][t][i];
-                    if (p.cap2 > 0.0f) x = p.cap2 * tanhf(x / p.cap2);
-                    x = (key >= lo[nt] && key < hi[nt]) ? x : -INFINITY;
-                    sv[4 * t + i] = x;
-                    mx = fmaxf(mx, x);
+                for (int i = 0; i < 4; i++) sv[4 * t + i] = sacc[nt][t][i];
+            if (p.cap2 > 0.0f) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) sv[e] = p.cap2 * tanhf(sv[e] / p.cap2);
+            }
+            if (!full) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int key = k0 + 8 * j + e;
+                    sv[e] = (key >= lo[nt] && key < hi[nt]) ? sv[e] : -INFINITY;
                 }
+            }
+            float mx = sv[0];
+#pragma unroll
+            for (int e = 1; e < 8; e++) mx = fmaxf(mx, sv[e]);
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
             const bool need = mx > m[nt] + LAZY_T;
@@ -819,19 +863,37 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
             }
         }
     };
+    auto process = [&](int k0, const Raw &r) {
+        if (k0 >= b.fresh_pos0) compute(k0, r, std::true_type{});
+        else compute(k0, r, std::false_type{});
+    };
 
-    /* each wave streams slabs wave, wave + SK_WAVES, ... with the next slab's
-     * loads in flight while the current one is computed */
+    /* each wave streams slabs wave, wave + SK_WAVES, ...; two register
+     * buffers alternate so the next slab's loads are in flight while the
+     * current one is computed */
     const int step = SMOL_SLAB * SK_WAVES;
+    const int end = it.key_end;
     int k0 = it.key_begin + wave * SMOL_SLAB;
-    Raw cur, nxt;
-    if (k0 < it.key_end) issue(k0, cur);
-    for (; k0 < it.key_end; k0 += step) {
-        const bool more = k0 + step < it.key_end;
-        if (more) issue(k0 + step, nxt);
-        if (k0 >= b.fresh_pos0) compute(k0, cur, std::true_type{});
-        else compute(k0, cur, std::false_type{});
-        cur = nxt;
+    if constexpr (HD <= 128) {
+        Raw ra, rb;
+        if (k0 < end) issue(k0, ra);
+        while (k0 < end) {
+            const int k1 = k0 + step;
+            if (k1 < end) issue(k1, rb);
+            process(k0, ra);
+            if (k1 >= end) break;
+            const int k2 = k1 + step;
+            if (k2 < end) issue(k2, ra);
+            process(k1, rb);
+            k0 = k2;
+        }
+    } else {
+        /* head_dim 256: one slab of K and V is 128 registers; no second buffer */
+        for (; k0 < end; k0 += step) {
+            Raw ra;
+            issue(k0, ra);
+            process(k0, ra);
+        }
     }
 
 #pragma unroll
