@@ -5,8 +5,8 @@
  * Each attention call builds small descriptor tables on the host (which rows
  * and keys each kernel block covers), copies them to the device through a
  * ring of pinned buffers, and enqueues two kernels on the context's stream:
- * k_prep (RoPE + cache append + fp16 staging) and k_attn_sk (split-K flash
- * attention with an in-kernel merge). Nothing here computes attention on the
+ * k_prep (RoPE + cache append + staging) and k_attn_pf or k_attn_dec (flash
+ * attention, long key ranges split across workgroups and merged in-kernel). Nothing here computes attention on the
  * host; without a GPU every entry point fails with SMOL_ATTN_ERR_NO_GPU.
  */
 #include <hip/hip_runtime.h>
@@ -26,7 +26,7 @@
 #include "attn_internal.h"
 
 extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t st);
-extern "C" int smol_launch_sk(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st);
+extern "C" int smol_launch_pf(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st);
 extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st);
 extern "C" int smol_launch_rope_apply(float *x, const float *cos_t, const float *sin_t,
                                       const int *pos, int seq, int n_heads, int hd, int kind,
@@ -475,7 +475,7 @@ struct Plan {
 };
 
 struct CallShape {
-    bool dec;             /* true: bf16 hi/lo staging + k_attn_dec; false: fp16 staging + k_attn_sk */
+    bool dec;             /* true: fp32 Q staging + k_attn_dec; false: fp16 Q staging + k_attn_pf */
     const void *q, *k, *v;
     int dtype;
     int Hq, Hkv, hd;
@@ -489,10 +489,12 @@ struct CallShape {
     float *out;
 };
 
+/* row tiles (16 rows each) per workgroup of k_attn_pf, within the register
+ * file without spilling: 4 up to head_dim 96, 2 at 128, 1 at 256 */
 static int choose_nt(int hd, int max_rows) {
     int nt = max_rows <= 16 ? 1 : (max_rows <= 32 ? 2 : 4);
-    if (hd > 128 && nt > 1) nt = 1;
-    if (hd > 64 && nt > 2) nt = 2;
+    if (hd > 96 && nt > 2) nt = 2;
+    if (hd > 128) nt = 1;
     return nt;
 }
 
@@ -647,11 +649,11 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     sp.counters = (int *)ctx->counters.p;
     mk = timing_begin(ctx, 1);
     rc = cs.dec ? smol_launch_dec(&sp, hd, (int)n_items, nt, ctx->stream)
-                : smol_launch_sk(&sp, hd, (int)n_items, nt, ctx->stream);
+                : smol_launch_pf(&sp, hd, (int)n_items, nt, ctx->stream);
     timing_end(ctx, mk);
     if (rc)
         return fail(rc == -1 ? SMOL_ATTN_ERR_UNSUPPORTED : SMOL_ATTN_ERR_DEVICE,
-                    "k_attn_sk launch (hd %d): %s", hd, hipGetErrorString(hipGetLastError()));
+                    "attention launch (hd %d): %s", hd, hipGetErrorString(hipGetLastError()));
     return SMOL_ATTN_OK;
 }
 

@@ -5,11 +5,16 @@
  *               rows: replaces smol_apply_rope_{neox,interleaved} on Q and K
  *               and the K/V row memcpy into the cache
  *               (common/decoder/qkn_decoder.c:493-503 and :647-652).
- *   k_attn_sk   split-K flash attention on fp16 MFMA (v_mfma_f32_16x16x32_f16):
- *               the causal / sliding-window / softcap / windowed-bidirectional
- *               online softmax of common/kernels/attention.c:32-462, over the
- *               bf16 KV cache plus the call's fresh fp16 keys, with a
- *               last-arriving-wave log-sum-exp merge of the key splits.
+ *   k_attn_pf   prefill / chunked prefill / bidirectional flash attention on
+ *               fp16 MFMA (v_mfma_f32_16x16x32_f16), 64 query rows per
+ *               workgroup;
+ *   k_attn_dec  decode and short chunks: bf16 MFMA straight on the bf16 cache
+ *               with hi/lo-split Q and P;
+ *               both compute the causal / sliding-window / softcap /
+ *               windowed-bidirectional online softmax of
+ *               common/kernels/attention.c:32-462 over the bf16 KV cache plus
+ *               the call's fresh fp16 keys, splitting long key ranges across
+ *               workgroups with a log-sum-exp merge by the last one.
  *
  * Numerics: softmax state in fp32 and in log2 units (Q is pre-multiplied by
  * scale * log2 e, so exp(s - m) = exp2(s' - m')). MFMA operands are fp16:
@@ -279,24 +284,8 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
     }
 }
 
-/* --------------------------------------------------------------- k_attn_sk */
+/* --------------------------------------------------------- shared by kernels */
 
-/*
- * One workgroup of SK_WAVES waves per item: NT tiles of 16 query rows of one
- * KV head against the item's key range, in 32-key slabs. Wave w takes slabs
- * w, w + SK_WAVES, ... of the range (all waves stream at once); the waves'
- * softmax states are combined through LDS, so an item produces one partial.
- *
- * MFMA layouts (16x16x32 f16; lane l, c = l & 15, j = l >> 4):
- *   S^T = K . Q^T : A = K rows, B = Q^T; D element i of lane l is
- *                   S^T[key 4j+i (tile-local)][row c]
- *   O^T = V^T . P^T: A = V^T (8 consecutive keys of column d), B = P^T.
- * K rows are gathered in the order key(t, m) = 8 (m >> 2) + 4 t + (m & 3) so
- * that the 8 probabilities a lane holds after the two S^T tiles are the 8
- * consecutive keys 8j..8j+7 of the slab, i.e. exactly the B operand of the
- * P.V step against a 16-byte load of V^T. Every row lives in lanes c, c+16,
- * c+32, c+48, so the softmax state of a row never leaves its lane column.
- */
 #define SK_WAVES 4
 #define SK_MERGE_MAX 1024 /* max ROWS * n_split of one merge group (LDS) */
 
@@ -364,175 +353,25 @@ __device__ __forceinline__ void merge_group(const SkParams &p, const SkItem &it,
     if (tid == 0) p.counters[(long long)it.group * p.Hkv + g] = 0;
 }
 
+/* Epilogue shared by the attention kernels: combines the SK_WAVES waves'
+ * (max, sum, O) through LDS into wave 0, then either writes the normalised
+ * rows (single split) or publishes the partial and lets the group's last
+ * workgroup merge. Every row's state lives in lanes c, c+16, c+32, c+48. */
 template <int HD, int NT>
-__global__ __launch_bounds__(64 * SK_WAVES) void k_attn_sk(SkParams p) {
-    constexpr int KS = (HD + 31) / 32;  /* 32-wide steps over head_dim for S */
-    constexpr int DT = (HD + 15) / 16;  /* 16-row tiles of head_dim for O */
-    constexpr int HDP = KS * 32;
+__device__ __forceinline__ void finish_item(const SkParams &p, const SkItem &it, const SkBatch &b, int g, int tid,
+                                            float (&m)[NT], float (&l)[NT], f4 (&o)[NT][(HD + 15) / 16], float *s_o,
+                                            float *s_m, float *s_l, int *s_last) {
+    constexpr int DT = (HD + 15) / 16;
     constexpr int ROWS = NT * 16;
-    constexpr int OSTR = DT * 16 + 4;   /* LDS row stride (floats) of a combined state */
-    const int tid = threadIdx.x;
+    constexpr int OSTR = DT * 16 + 4;
     const int wave = tid >> 6, lane = tid & 63;
     const int c = lane & 15, j = lane >> 4;
-    const int g = blockIdx.y;
-    const SkItem it = p.items[blockIdx.x];
-    const SkBatch b = p.batches[it.batch];
-    const int G = p.G;
-    constexpr int SO = (SK_WAVES - 1) * ROWS * OSTR > 2 * SK_MERGE_MAX + 128 ? (SK_WAVES - 1) * ROWS * OSTR
-                                                                          : 2 * SK_MERGE_MAX + 128;
-    __shared__ float s_o[SO];
-    __shared__ float s_m[(SK_WAVES - 1) * ROWS], s_l[(SK_WAVES - 1) * ROWS];
-    __shared__ int s_last;
-
-    /* per-lane row metadata and Q fragments */
-    h8 qf[NT][KS];
-    int lo[NT], hi[NT];
-    float m[NT], l[NT];
-    f4 o[NT][DT];
-#pragma unroll
-    for (int nt = 0; nt < NT; nt++) {
-        const int r = it.row0 + nt * 16 + c;
-        const bool valid = r < b.n_rows;
-        const int qi = r / G;
-        int rl = b.key_lo, rh = b.key_hi;
-        if (b.causal) {
-            rh = min(rh, b.q_pos0 + qi + 1);
-            if (p.window > 0) rl = max(rl, b.q_pos0 + qi - p.window + 1);
-        }
-        lo[nt] = valid ? rl : 0;
-        hi[nt] = valid ? rh : 0;
-        m[nt] = -INFINITY;
-        l[nt] = 0.0f;
-        const _Float16 *qrow = p.qs + (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid ? r : 0)) * HDP;
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) qf[nt][ks] = valid ? load_h8(qrow + 32 * ks + 8 * j) : zero_h8();
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++) o[nt][dt] = f4{0.f, 0.f, 0.f, 0.f};
-    }
-
-    /* K / V^T sources: cache rows (bf16) below fresh_pos0, the fresh fp16
-     * buffers from there on. Both are 2-byte elements with the same row
-     * layout, so a slab's loads differ only in base pointer and stride; the
-     * choice is uniform per slab and no load sits under a branch. */
-    const uint16_t *kc = nullptr, *vtc = nullptr;
-    if (b.slot >= 0 && p.kc != nullptr) {
-        kc = p.kc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * HD;
-        vtc = p.vtc + (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * HD;
-    }
-    const uint16_t *kf = reinterpret_cast<const uint16_t *>(p.kf) + (long long)g * p.fcap * HD +
-                         (long long)(b.fresh_row0 - b.fresh_pos0) * HD;
-    /* V^T is slab-blocked: key k, column d at (k / 32) * 32 HD + d * 32 + k % 32 */
-    const uint16_t *vtf = reinterpret_cast<const uint16_t *>(p.vtf) + (long long)g * p.fcap * HD +
-                          (long long)((b.fresh_row0 - b.fresh_pos0) / SMOL_SLAB) * SMOL_SLAB * HD;
-    const int kt_row = 8 * (c >> 2) + (c & 3); /* gathered key of A-operand row c, tile 0 */
-
-    uint4 kraw[2][KS], vraw[DT];
-    auto issue = [&](int k0) {
-        const bool fr = k0 >= b.fresh_pos0;
-        const uint16_t *kb = fr ? kf : kc;
-        const uint16_t *vb = (fr ? vtf : vtc) + (long long)(k0 / SMOL_SLAB) * SMOL_SLAB * HD;
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++) {
-                const int d0 = 32 * ks + 8 * j;
-                if (HD % 32 != 0 && d0 >= HD) { kraw[t][ks] = make_uint4(0, 0, 0, 0); continue; }
-                kraw[t][ks] = *reinterpret_cast<const uint4 *>(kb + (long long)(k0 + kt_row + 4 * t) * HD + d0);
-            }
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            const int d = 16 * dt + c;
-            if (HD % 16 != 0 && d >= HD) { vraw[dt] = make_uint4(0, 0, 0, 0); continue; }
-            vraw[dt] = *reinterpret_cast<const uint4 *>(vb + d * SMOL_SLAB + 8 * j);
-        }
-    };
-
-    const int step = SMOL_SLAB * SK_WAVES;
-    const int kb0 = it.key_begin + wave * SMOL_SLAB;
-    if (kb0 < it.key_end) issue(kb0);
-    for (int k0 = kb0; k0 < it.key_end; k0 += step) {
-        const bool fresh = k0 >= b.fresh_pos0;
-        uint4 kcur[2][KS], vcur[DT];
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++) kcur[t][ks] = kraw[t][ks];
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++) vcur[dt] = vraw[dt];
-        /* prefetch this wave's next slab while this one is computed */
-        if (k0 + step < it.key_end) issue(k0 + step);
-
-        /* ---- S^T = K . Q^T for two 16-key tiles ---- */
-        f4 s[NT][2];
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
-            h8 kfrag[KS];
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-                kfrag[ks] = fresh ? *reinterpret_cast<h8 *>(&kcur[t][ks]) : bf16x8_to_h8(kcur[t][ks]);
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ks = 0; ks < KS; ks++)
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kfrag[ks], qf[nt][ks], acc, 0, 0, 0);
-                s[nt][t] = acc;
-            }
-        }
-
-        /* ---- V^T fragments (shared by all row tiles) ---- */
-        h8 vfrag[DT];
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++)
-            vfrag[dt] = fresh ? *reinterpret_cast<h8 *>(&vcur[dt]) : bf16x8_to_h8(vcur[dt]);
-
-        /* ---- online softmax per row (lane column), then O^T += V^T P^T ---- */
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            float sv[8];
-            float mx = -INFINITY;
-#pragma unroll
-            for (int t = 0; t < 2; t++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int key = k0 + 8 * j + 4 * t + i;
-                    float x = s[nt][t][i];
-                    if (p.cap2 > 0.0f) x = p.cap2 * tanhf(x / p.cap2);
-                    x = (key >= lo[nt] && key < hi[nt]) ? x : -INFINITY;
-                    sv[4 * t + i] = x;
-                    mx = fmaxf(mx, x);
-                }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float m_new = fmaxf(m[nt], mx);
-            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            const float alpha = __builtin_amdgcn_exp2f(m[nt] - m_use);
-            m[nt] = m_new;
-            h8 pf;
-            float ps = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                float pe = __builtin_amdgcn_exp2f(sv[e] - m_use);
-                ps += pe;
-                pf[e] = (_Float16)pe;
-            }
-            l[nt] = l[nt] * alpha + ps;
-#pragma unroll
-            for (int dt = 0; dt < DT; dt++) {
-                o[nt][dt] *= alpha;
-                o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vfrag[dt], pf, o[nt][dt], 0, 0, 0);
-            }
-        }
-    }
-
-    /* full row sums of this wave: lanes c, c+16, c+32, c+48 hold one row */
+    const int G = p.G, Hq = p.Hq;
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         l[nt] += __shfl_xor(l[nt], 16);
         l[nt] += __shfl_xor(l[nt], 32);
     }
-
-    /* ---- combine the waves' states through LDS into wave 0 ---- */
     if (wave > 0) {
         const int sl = (wave - 1) * ROWS;
 #pragma unroll
@@ -569,8 +408,6 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_attn_sk(SkParams p) {
             l[nt] = L;
         }
     }
-
-    const int Hq = p.Hq;
     if (it.n_split == 1) {
         if (wave != 0) return;
 #pragma unroll
@@ -589,8 +426,6 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_attn_sk(SkParams p) {
         }
         return;
     }
-
-    /* ---- split-K: publish the partial, the last workgroup of the group merges ---- */
     const long long pbase = ((long long)blockIdx.x * p.Hkv + g) * ROWS;
     if (wave == 0) {
 #pragma unroll
@@ -614,12 +449,11 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_attn_sk(SkParams p) {
             prev = __hip_atomic_fetch_add(p.counters + (long long)it.group * p.Hkv + g, 1, __ATOMIC_ACQ_REL,
                                           __HIP_MEMORY_SCOPE_AGENT);
         prev = __shfl(prev, 0);
-        if (lane == 0) s_last = prev == it.n_split - 1;
+        if (lane == 0) *s_last = prev == it.n_split - 1;
     }
     __syncthreads();
-    if (!s_last) return;
+    if (!*s_last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-
     merge_group<HD, ROWS>(p, it, b, g, tid, s_o);
 }
 
@@ -633,7 +467,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_attn_sk(SkParams p) {
  * significant bits together):  S = K.Qhi + K.Qlo,  O += V.Phi + V.Plo.
  * The slab holding the keys this call appends runs on fp16 MFMA over the
  * fp16 fresh staging (k_prep), with an fp16 copy of Q.
- * Same lane layouts, wave split and merge as k_attn_sk. The running max is a
+ * Lane layouts, wave split and merge as k_attn_pf. The running max is a
  * lazy reference: the accumulator is rescaled only when some row's max grows
  * by more than 2^LAZY_T (decided per wave by vote), so p <= 2^LAZY_T.
  */
@@ -896,99 +730,218 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
         }
     }
 
+    finish_item<HD, NT>(p, it, b, g, tid, m, l, o, s_o, s_m, s_l, &s_last);
+}
+
+/* ---------------------------------------------------------------- k_attn_pf */
+
+/*
+ * Attention for prefill, chunked prefill and windowed bidirectional calls:
+ * fp16 MFMA (v_mfma_f32_16x16x32_f16) over the fresh fp16 staging; slabs of
+ * an existing bf16 cache prefix are widened to fp16 in registers (exact).
+ * A workgroup is SK_WAVES waves on the same NT*16 query rows, each wave
+ * streaming every SK_WAVES-th 32-key slab of the item's range from L2 with
+ * buffer loads (slab offset in an SGPR, the next slab in flight while the
+ * current one is computed); the waves are combined by finish_item. Each K/V
+ * element a wave loads is used by NT*16 rows. Lazy rescale and unmasked
+ * interior slabs as in k_attn_dec.
+ */
+template <int HD, int NT>
+__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_attn_pf(SkParams p) {
+    constexpr int KS = (HD + 31) / 32;
+    constexpr int DT = (HD + 15) / 16;
+    constexpr int HDP = KS * 32;
+    constexpr int ROWS = NT * 16;
+    constexpr int OSTR = DT * 16 + 4;
+    constexpr unsigned SLAB_BYTES = SMOL_SLAB * HD * 2;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int c = lane & 15, j = lane >> 4;
+    const int g = blockIdx.y;
+    const SkItem it = p.items[blockIdx.x];
+    const SkBatch b = p.batches[it.batch];
+    const int G = p.G;
+    constexpr int SO = (SK_WAVES - 1) * ROWS * OSTR > 2 * SK_MERGE_MAX + 128 ? (SK_WAVES - 1) * ROWS * OSTR
+                                                                          : 2 * SK_MERGE_MAX + 128;
+    __shared__ float s_o[SO];
+    __shared__ float s_m[(SK_WAVES - 1) * ROWS], s_l[(SK_WAVES - 1) * ROWS];
+    __shared__ int s_last;
+
+    h8 qf[NT][KS];
+    int lo[NT], hi[NT];
+    float m[NT], l[NT];
+    f4 o[NT][DT];
+    int lo_max = -(1 << 30), hi_min = 1 << 30;
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
-        l[nt] += __shfl_xor(l[nt], 16);
-        l[nt] += __shfl_xor(l[nt], 32);
+        const int r = it.row0 + nt * 16 + c;
+        const bool valid = r < b.n_rows;
+        const int qi = r / G;
+        int rl = b.key_lo, rh = b.key_hi;
+        if (b.causal) {
+            rh = min(rh, b.q_pos0 + qi + 1);
+            if (p.window > 0) rl = max(rl, b.q_pos0 + qi - p.window + 1);
+        }
+        lo[nt] = valid ? rl : -(1 << 30);
+        hi[nt] = valid ? rh : (1 << 30);
+        lo_max = max(lo_max, lo[nt]);
+        hi_min = min(hi_min, hi[nt]);
+        m[nt] = -INFINITY;
+        l[nt] = 0.0f;
+        const _Float16 *qrow = p.qs + (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid ? r : 0)) * HDP;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) qf[nt][ks] = valid ? load_h8(qrow + 32 * ks + 8 * j) : zero_h8();
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) o[nt][dt] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int sh = 1; sh < 16; sh <<= 1) {
+        lo_max = max(lo_max, __shfl_xor(lo_max, sh));
+        hi_min = min(hi_min, __shfl_xor(hi_min, sh));
+    }
+    lo_max = __builtin_amdgcn_readfirstlane(lo_max);
+    hi_min = __builtin_amdgcn_readfirstlane(hi_min);
+
+    rsrc_t rk_c = make_rsrc(nullptr, 0), rv_c = make_rsrc(nullptr, 0);
+    if (b.slot >= 0 && p.kc != nullptr) {
+        const long long cb = (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * HD;
+        rk_c = make_rsrc(p.kc + cb, (long long)p.cap * HD * 2);
+        rv_c = make_rsrc(p.vtc + cb, (long long)p.cap * HD * 2);
+    }
+    const rsrc_t rk_f = make_rsrc(p.kf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
+    const rsrc_t rv_f = make_rsrc(p.vtf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
+    const int kt_row = 8 * (c >> 2) + (c & 3);
+    unsigned vo_k[2][KS], vo_v[DT];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            const int d0 = 32 * ks + 8 * j;
+            vo_k[t][ks] = (HD % 32 == 0 || d0 < HD) ? (unsigned)(((kt_row + 4 * t) * HD + d0) * 2) : OOB_OFF;
+        }
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) {
+        const int d = 16 * dt + c;
+        vo_v[dt] = (HD % 16 == 0 || d < HD) ? (unsigned)((d * SMOL_SLAB + 8 * j) * 2) : OOB_OFF;
     }
 
-    /* ---- combine the waves' states through LDS into wave 0 ---- */
-    if (wave > 0) {
-        const int sl = (wave - 1) * ROWS;
+    struct Raw {
+        uint4 k[2][KS];
+        uint4 v[DT];
+    };
+    auto issue = [&](int k0, Raw &r) {
+        const bool fr = k0 >= b.fresh_pos0;
+        const int kr = fr ? b.fresh_row0 + (k0 - b.fresh_pos0) : k0;
+        const unsigned so = (unsigned)(kr / SMOL_SLAB) * SLAB_BYTES;
+        const rsrc_t rk = fr ? rk_f : rk_c, rv = fr ? rv_f : rv_c;
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            const int rr = nt * 16 + c;
-            float *so = s_o + (sl + rr) * OSTR;
+        for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++) *reinterpret_cast<f4 *>(so + 16 * dt + 4 * j) = o[nt][dt];
-            if (j == 0) { s_m[sl + rr] = m[nt]; s_l[sl + rr] = l[nt]; }
-        }
-    }
-    __syncthreads();
-    if (wave == 0) {
+            for (int ks = 0; ks < KS; ks++) r.k[t][ks] = bload(rk, vo_k[t][ks], so);
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            const int rr = nt * 16 + c;
-            float M = m[nt];
-#pragma unroll
-            for (int w = 0; w < SK_WAVES - 1; w++) M = fmaxf(M, s_m[w * ROWS + rr]);
-            const float Mu = M == -INFINITY ? 0.0f : M;
-            const float a0 = __builtin_amdgcn_exp2f(m[nt] - Mu);
-            float L = l[nt] * a0;
-#pragma unroll
-            for (int dt = 0; dt < DT; dt++) o[nt][dt] *= a0;
-#pragma unroll
-            for (int w = 0; w < SK_WAVES - 1; w++) {
-                const float aw = __builtin_amdgcn_exp2f(s_m[w * ROWS + rr] - Mu);
-                L += s_l[w * ROWS + rr] * aw;
-                const float *so = s_o + (w * ROWS + rr) * OSTR;
-#pragma unroll
-                for (int dt = 0; dt < DT; dt++) o[nt][dt] += aw * *reinterpret_cast<const f4 *>(so + 16 * dt + 4 * j);
-            }
-            m[nt] = M;
-            l[nt] = L;
-        }
-    }
+        for (int dt = 0; dt < DT; dt++) r.v[dt] = bload(rv, vo_v[dt], so);
+    };
 
-    const int Hq = p.Hq;
-    if (it.n_split == 1) {
-        if (wave != 0) return;
+    auto compute = [&](int k0, const Raw &r, auto fresh_tag) {
+        constexpr bool FRESH = decltype(fresh_tag)::value;
+        f4 sacc[NT][2];
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            const int r = it.row0 + nt * 16 + c;
-            if (r >= b.n_rows) continue;
-            const int qi = r / G, hg = r - qi * G;
-            float *orow = p.out + ((long long)(b.out_tok0 + qi) * Hq + (g * G + hg)) * HD;
-            const float inv = l[nt] > 0.0f ? 1.0f / l[nt] : 0.0f;
+        for (int t = 0; t < 2; t++) {
+            h8 kfrag[KS];
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++) {
-                const int d = 16 * dt + 4 * j;
-                if (HD % 16 != 0 && d >= HD) continue;
-                *reinterpret_cast<f4 *>(orow + d) = o[nt][dt] * inv;
+            for (int ks = 0; ks < KS; ks++)
+                kfrag[ks] = FRESH ? *reinterpret_cast<const h8 *>(&r.k[t][ks]) : bf16x8_to_h8(r.k[t][ks]);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kfrag[ks], qf[nt][ks], acc, 0, 0, 0);
+                sacc[nt][t] = acc;
             }
         }
-        return;
-    }
+        h8 vfrag[DT];
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+            vfrag[dt] = FRESH ? *reinterpret_cast<const h8 *>(&r.v[dt]) : bf16x8_to_h8(r.v[dt]);
+        const bool full = k0 >= lo_max && k0 + SMOL_SLAB <= hi_min;
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            float sv[8];
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) sv[4 * t + i] = sacc[nt][t][i];
+            if (p.cap2 > 0.0f) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) sv[e] = p.cap2 * tanhf(sv[e] / p.cap2);
+            }
+            if (!full) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int key = k0 + 8 * j + e;
+                    sv[e] = (key >= lo[nt] && key < hi[nt]) ? sv[e] : -INFINITY;
+                }
+            }
+            float mx = sv[0];
+#pragma unroll
+            for (int e = 1; e < 8; e++) mx = fmaxf(mx, sv[e]);
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const bool need = mx > m[nt] + LAZY_T;
+            if (__any(need)) {
+                const float m_new = need ? mx : m[nt];
+                const float alpha = need ? __builtin_amdgcn_exp2f(m[nt] - m_new) : 1.0f;
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) o[nt][dt] *= alpha;
+                l[nt] *= alpha;
+                m[nt] = m_new;
+            }
+            const float m_use = m[nt] == -INFINITY ? 0.0f : m[nt];
+            h8 pf;
+            float ps = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float pe = __builtin_amdgcn_exp2f(sv[e] - m_use);
+                ps += pe;
+                pf[e] = (_Float16)pe;
+            }
+            l[nt] += ps;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+                o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vfrag[dt], pf, o[nt][dt], 0, 0, 0);
+        }
+    };
+    auto process = [&](int k0, const Raw &r) {
+        if (k0 >= b.fresh_pos0) compute(k0, r, std::true_type{});
+        else compute(k0, r, std::false_type{});
+    };
 
-    const long long pbase = ((long long)blockIdx.x * p.Hkv + g) * ROWS;
-    if (wave == 0) {
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            const int rr = nt * 16 + c;
-            float *po = p.part_o + (pbase + rr) * HD;
-#pragma unroll
-            for (int dt = 0; dt < DT; dt++) {
-                const int d = 16 * dt + 4 * j;
-                if (HD % 16 != 0 && d >= HD) continue;
-                *reinterpret_cast<f4 *>(po + d) = o[nt][dt];
-            }
-            if (j == 0) {
-                p.part_ml[(pbase + rr) * 2 + 0] = m[nt];
-                p.part_ml[(pbase + rr) * 2 + 1] = l[nt];
-            }
+    const int step = SMOL_SLAB * SK_WAVES;
+    const int end = it.key_end;
+    int k0 = it.key_begin + wave * SMOL_SLAB;
+    if constexpr (NT * HD <= 256) {
+        Raw ra, rb;
+        if (k0 < end) issue(k0, ra);
+        while (k0 < end) {
+            const int k1 = k0 + step;
+            if (k1 < end) issue(k1, rb);
+            process(k0, ra);
+            if (k1 >= end) break;
+            const int k2 = k1 + step;
+            if (k2 < end) issue(k2, ra);
+            process(k1, rb);
+            k0 = k2;
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        int prev = 0;
-        if (lane == 0)
-            prev = __hip_atomic_fetch_add(p.counters + (long long)it.group * p.Hkv + g, 1, __ATOMIC_ACQ_REL,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-        prev = __shfl(prev, 0);
-        if (lane == 0) s_last = prev == it.n_split - 1;
+    } else {
+        for (; k0 < end; k0 += step) {
+            Raw ra;
+            issue(k0, ra);
+            process(k0, ra);
+        }
     }
-    __syncthreads();
-    if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    merge_group<HD, ROWS>(p, it, b, g, tid, s_o);
+    finish_item<HD, NT>(p, it, b, g, tid, m, l, o, s_o, s_m, s_l, &s_last);
 }
 
 /* ------------------------------------------------------------ k_rope_apply */
@@ -1048,17 +1001,6 @@ extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t 
 }
 
 template <int HD>
-static int launch_sk_hd(const SkParams *sp, int n_items, int nt, hipStream_t st) {
-    dim3 grid(n_items, sp->Hkv), block(64 * SK_WAVES);
-    /* register budget: NT * HD <= 256 fits without spilling */
-    if (nt == 1) hipLaunchKernelGGL((k_attn_sk<HD, 1>), grid, block, 0, st, *sp);
-    else if (nt == 2 && HD <= 128) hipLaunchKernelGGL((k_attn_sk<HD, (HD <= 128 ? 2 : 1)>), grid, block, 0, st, *sp);
-    else if (nt == 4 && HD <= 64) hipLaunchKernelGGL((k_attn_sk<HD, (HD <= 64 ? 4 : 1)>), grid, block, 0, st, *sp);
-    else return -1;
-    return hipGetLastError() == hipSuccess ? 0 : -3;
-}
-
-template <int HD>
 static int launch_dec_hd(const SkParams *sp, int n_items, int nt, hipStream_t st) {
     dim3 grid(n_items, sp->Hkv), block(64 * SK_WAVES);
     if (nt == 1) hipLaunchKernelGGL((k_attn_dec<HD, 1>), grid, block, 0, st, *sp);
@@ -1080,15 +1022,25 @@ extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, 
     }
 }
 
-extern "C" int smol_launch_sk(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st) {
+template <int HD>
+static int launch_pf_hd(const SkParams *sp, int n_items, int nt, hipStream_t st) {
+    dim3 grid(n_items, sp->Hkv), block(64 * SK_WAVES);
+    if (nt == 1) hipLaunchKernelGGL((k_attn_pf<HD, 1>), grid, block, 0, st, *sp);
+    else if (nt == 2 && HD <= 128) hipLaunchKernelGGL((k_attn_pf<HD, (HD <= 128 ? 2 : 1)>), grid, block, 0, st, *sp);
+    else if (nt == 4 && HD <= 96) hipLaunchKernelGGL((k_attn_pf<HD, (HD <= 96 ? 4 : 1)>), grid, block, 0, st, *sp);
+    else return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+extern "C" int smol_launch_pf(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st) {
     if (n_items <= 0) return 0;
     switch (hd) {
-    case 64: return launch_sk_hd<64>(sp, n_items, nt, st);
-    case 72: return launch_sk_hd<72>(sp, n_items, nt, st);
-    case 80: return launch_sk_hd<80>(sp, n_items, nt, st);
-    case 96: return launch_sk_hd<96>(sp, n_items, nt, st);
-    case 128: return launch_sk_hd<128>(sp, n_items, nt, st);
-    case 256: return launch_sk_hd<256>(sp, n_items, nt, st);
+    case 64: return launch_pf_hd<64>(sp, n_items, nt, st);
+    case 72: return launch_pf_hd<72>(sp, n_items, nt, st);
+    case 80: return launch_pf_hd<80>(sp, n_items, nt, st);
+    case 96: return launch_pf_hd<96>(sp, n_items, nt, st);
+    case 128: return launch_pf_hd<128>(sp, n_items, nt, st);
+    case 256: return launch_pf_hd<256>(sp, n_items, nt, st);
     default: return -1;
     }
 }
