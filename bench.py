@@ -71,6 +71,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None, help="measure only this workload")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="first run 5 plain device copies of MIB MiB (a known-size reference for "
+                         "the HBM byte counters of a profiler run)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the attention would shard "
@@ -86,6 +89,16 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
+    if args.copy_calibration:
+        n = args.copy_calibration << 18
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print("copy calibration: 5 copies of %d MiB (%d bytes read + %d written per copy)"
+              % (args.copy_calibration, 4 * n, 4 * n), flush=True)
+        del src, dst
     ctx = sa.Context(0)
     wls = workloads.all_workloads()
     steps, warmup = args.steps, args.warmup
@@ -108,7 +121,7 @@ def main():
             "dtype": "f16 MFMA operands, f32 softmax/accumulate (bf16 inputs and KV cache)",
             "data": "synthetic (seeded N(0,1) bf16 Q/K/V)",
             "config": dict(main_wl.describe(), layers_rotated=n_layers, parallelism="single GPU"),
-            "roofline": {"bound": "mfma", "kernel": "k_attn_sk", "achieved": round(achieved, 3),
+            "roofline": {"bound": "mfma", "kernel": "k_attn_pf", "achieved": round(achieved, 3),
                          "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_TFLOPS, 5),
                          "traffic": None, "kernel_ms": round(attn_ms, 5), "prep_kernel_ms": round(prep_ms, 5),
                          "flops_per_launch": flops},

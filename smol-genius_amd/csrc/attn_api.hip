@@ -26,8 +26,8 @@
 #include "attn_internal.h"
 
 extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t st);
-extern "C" int smol_launch_pf(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st);
-extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st);
+extern "C" int smol_launch_pf(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
+extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
 extern "C" int smol_launch_rope_apply(float *x, const float *cos_t, const float *sin_t,
                                       const int *pos, int seq, int n_heads, int hd, int kind,
                                       hipStream_t st);
@@ -500,6 +500,22 @@ static int choose_nt(int hd, int max_rows) {
 
 /* Row tiles x key splits for every batch. The split size is chosen so the
  * whole call has a few waves per compute unit. */
+/* tuning overrides read from the environment (0 when unset) */
+static int env_int(const char *name) {
+    const char *v = getenv(name);
+    return v ? atoi(v) : 0;
+}
+
+/* waves per SIMD the attention kernel is compiled for: 2 where a wave's
+ * registers fit in half the file (latency hidden by the other wave), else 1 */
+static int choose_waves(bool dec, int hd, int nt) {
+    const int ov = env_int("SMOL_ATTN_WAVES");
+    if (ov == 1 || ov == 2) return ov;
+    if (hd > 128) return 1;
+    if (dec) return nt == 1 ? 2 : 1;
+    return (nt == 4 || (nt == 2 && hd > 96)) ? 1 : 2;
+}
+
 static void plan_items(Plan &pl, int Hkv, int G, int window, int nt, int cu_count) {
     const int rows_per = 16 * nt;
     struct Tile { int batch, row0, lo, hi; };
@@ -520,13 +536,12 @@ static void plan_items(Plan &pl, int Hkv, int G, int window, int nt, int cu_coun
             total_slabs += (hi - lo + SMOL_SLAB - 1) / SMOL_SLAB;
         }
     }
-    /* one 4-wave workgroup per compute unit, each wave >= 2 slabs */
+    /* a workgroup per compute unit and wave slot, each wave >= 2 slabs */
     const long long target_items = (long long)cu_count;
     long long per = (total_slabs * Hkv + target_items - 1) / std::max(1LL, target_items);
     int slabs_per_item = (int)std::max(8LL, per);
     /* tuning override: SMOL_ATTN_SLABS_PER_ITEM=n fixes the key slabs per work item */
-    if (const char *ov = getenv("SMOL_ATTN_SLABS_PER_ITEM")) {
-        const int n = atoi(ov);
+    if (const int n = env_int("SMOL_ATTN_SLABS_PER_ITEM")) {
         if (n > 0) slabs_per_item = n;
     }
     int group = 0;
@@ -558,8 +573,13 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     const int G = cs.Hq / cs.Hkv;
     int max_rows = 0;
     for (auto &b : pl.sb) max_rows = std::max(max_rows, b.n_rows);
-    const int nt = cs.dec ? (max_rows <= 16 || hd > 128 ? 1 : 2) : choose_nt(hd, max_rows);
-    plan_items(pl, cs.Hkv, G, cs.window, nt, ctx->cu_count);
+    int nt = cs.dec ? (max_rows <= 16 || hd > 128 ? 1 : 2) : choose_nt(hd, max_rows);
+    if (const int ov = env_int("SMOL_ATTN_NT")) {
+        if ((ov == 1 || ov == 2 || ov == 4) && (ov <= 2 || hd <= 96) && (ov == 1 || hd <= 128) && !(cs.dec && ov == 4))
+            nt = ov;
+    }
+    const int w = choose_waves(cs.dec, hd, nt);
+    plan_items(pl, cs.Hkv, G, cs.window, nt, ctx->cu_count * w);
     const int rows_per = 16 * nt;
 
     /* workspace */
@@ -648,8 +668,8 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     sp.part_ml = (float *)ctx->part_ml.p;
     sp.counters = (int *)ctx->counters.p;
     mk = timing_begin(ctx, 1);
-    rc = cs.dec ? smol_launch_dec(&sp, hd, (int)n_items, nt, ctx->stream)
-                : smol_launch_pf(&sp, hd, (int)n_items, nt, ctx->stream);
+    rc = cs.dec ? smol_launch_dec(&sp, hd, (int)n_items, nt, w, ctx->stream)
+                : smol_launch_pf(&sp, hd, (int)n_items, nt, w, ctx->stream);
     timing_end(ctx, mk);
     if (rc)
         return fail(rc == -1 ? SMOL_ATTN_ERR_UNSUPPORTED : SMOL_ATTN_ERR_DEVICE,

@@ -187,9 +187,9 @@ __device__ __forceinline__ void rope8(const void *base, int dtype, long long row
  * 8 elements (16-byte stores); V goes through LDS so that the transposed
  * stores are 8 consecutive positions of one column. */
 __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
-    const PrepBlock blk = p.blocks[blockIdx.x];
+    const PrepBlock blk = p.blocks[blockIdx.x / (unsigned)p.Hkv];
     const PrepBatch b = p.batches[blk.batch];
-    const int g = blockIdx.y;
+    const int g = (int)(blockIdx.x % (unsigned)p.Hkv); /* kv head fastest: XCD-local, as the attention kernels */
     const int hd = p.hd;
     const int tid = threadIdx.x;
     const int cpr = hd >> 3; /* 8-element chunks per head row */
@@ -289,6 +289,24 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
 #define SK_WAVES 4
 #define SK_MERGE_MAX 1024 /* max ROWS * n_split of one merge group (LDS) */
 
+/* Reductions over the four lanes c, c+16, c+32, c+48 that hold one softmax
+ * row, with the gfx950 cross-row swaps (VALU, no LDS round trip). Each swap
+ * hands every lane the pair {x[l], x[l ^ 32]} (resp. l ^ 16), so all four
+ * lanes end with the same value. */
+__device__ __forceinline__ float row_max4(float v) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float row_sum4(float v) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 /* Merge of one split-K group by its last workgroup (all 64*SK_WAVES threads):
  * all (max, sum) pairs of the group are loaded in one parallel sweep into
  * LDS, each row's max and 1/sum and every split's weight are formed there,
@@ -296,10 +314,10 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
  * independent loads in flight. The host keeps ROWS * n_split within
  * SK_MERGE_MAX. Resets the group's counter for the next call. */
 template <int HD, int ROWS>
-__device__ __forceinline__ void merge_group(const SkParams &p, const SkItem &it, const SkBatch &b, int g, int tid,
-                                            float *s_o) {
+__device__ __forceinline__ void merge_group(const SkParams &p, const SkItem &it, const SkBatch &b, int item, int g,
+                                            int tid, float *s_o) {
     const int G = p.G, Hq = p.Hq;
-    const int first = blockIdx.x - it.split;
+    const int first = item - it.split;
     const int nsp = it.n_split;
     float *s_ml = s_o;                       /* [nsp][ROWS][2], then weights [nsp][ROWS] */
     float *s_row = s_o + 2 * SK_MERGE_MAX;   /* per row: max, 1/sum */
@@ -358,7 +376,8 @@ __device__ __forceinline__ void merge_group(const SkParams &p, const SkItem &it,
  * rows (single split) or publishes the partial and lets the group's last
  * workgroup merge. Every row's state lives in lanes c, c+16, c+32, c+48. */
 template <int HD, int NT>
-__device__ __forceinline__ void finish_item(const SkParams &p, const SkItem &it, const SkBatch &b, int g, int tid,
+__device__ __forceinline__ void finish_item(const SkParams &p, const SkItem &it, const SkBatch &b, int item, int g,
+                                            int tid,
                                             float (&m)[NT], float (&l)[NT], f4 (&o)[NT][(HD + 15) / 16], float *s_o,
                                             float *s_m, float *s_l, int *s_last) {
     constexpr int DT = (HD + 15) / 16;
@@ -369,8 +388,7 @@ __device__ __forceinline__ void finish_item(const SkParams &p, const SkItem &it,
     const int G = p.G, Hq = p.Hq;
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
-        l[nt] += __shfl_xor(l[nt], 16);
-        l[nt] += __shfl_xor(l[nt], 32);
+        l[nt] = row_sum4(l[nt]);
     }
     if (wave > 0) {
         const int sl = (wave - 1) * ROWS;
@@ -426,7 +444,7 @@ __device__ __forceinline__ void finish_item(const SkParams &p, const SkItem &it,
         }
         return;
     }
-    const long long pbase = ((long long)blockIdx.x * p.Hkv + g) * ROWS;
+    const long long pbase = ((long long)item * p.Hkv + g) * ROWS;
     if (wave == 0) {
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
@@ -454,7 +472,7 @@ __device__ __forceinline__ void finish_item(const SkParams &p, const SkItem &it,
     __syncthreads();
     if (!*s_last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    merge_group<HD, ROWS>(p, it, b, g, tid, s_o);
+    merge_group<HD, ROWS>(p, it, b, item, g, tid, s_o);
 }
 
 /* --------------------------------------------------------------- k_attn_dec */
@@ -503,8 +521,8 @@ __device__ __forceinline__ uint4 bload(rsrc_t r, unsigned voff, unsigned soff) {
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-template <int HD, int NT>
-__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_attn_dec(SkParams p) {
+template <int HD, int NT, int W>
+__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W, W))) void k_attn_dec(SkParams p) {
     constexpr int KS = (HD + 31) / 32;
     constexpr int DT = (HD + 15) / 16;
     constexpr int HDP = KS * 32;
@@ -515,8 +533,11 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
     const int c = lane & 15, j = lane >> 4;
-    const int g = blockIdx.y;
-    const SkItem it = p.items[blockIdx.x];
+    /* kv head fastest in the block index: consecutive workgroups go to
+     * consecutive XCDs, so each XCD's L2 holds the K/V of its own heads */
+    const int g = (int)(blockIdx.x % (unsigned)p.Hkv);
+    const int item = (int)(blockIdx.x / (unsigned)p.Hkv);
+    const SkItem it = p.items[item];
     const SkBatch b = p.batches[it.batch];
     const int G = p.G;
     constexpr int SO = (SK_WAVES - 1) * ROWS * OSTR > 2 * SK_MERGE_MAX + 128 ? (SK_WAVES - 1) * ROWS * OSTR
@@ -526,7 +547,6 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
     __shared__ int s_last;
 
     b8 qh[NT][KS], ql[NT][KS];
-    h8 qf[NT][KS];
     int lo[NT], hi[NT];
     float m[NT], l[NT];
     f4 o[NT][DT];
@@ -558,8 +578,6 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
                 x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = e.x; x[5] = e.y; x[6] = e.z; x[7] = e.w;
             }
             split8(x, qh[nt][ks], ql[nt][ks]);
-#pragma unroll
-            for (int i = 0; i < 8; i++) qf[nt][ks][i] = (_Float16)x[i];
         }
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) o[nt][dt] = f4{0.f, 0.f, 0.f, 0.f};
@@ -598,27 +616,38 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
         vo_v[dt] = (HD % 16 == 0 || d < HD) ? (unsigned)((d * SMOL_SLAB + 8 * j) * 2) : OOB_OFF;
     }
 
-    struct Raw {
+    struct KRaw {
         uint4 k[2][KS];
+    };
+    struct VRaw {
         uint4 v[DT];
     };
-    /* a slab's loads: uniform choice of resource and slab offset (SGPRs) */
-    auto issue = [&](int k0, Raw &r) {
+    /* slab k0's resource and slab offset: a uniform choice (SGPRs) */
+    auto slab_src = [&](int k0, bool value, rsrc_t &r, unsigned &so) {
         const bool fr = k0 >= b.fresh_pos0;
         const int kr = fr ? b.fresh_row0 + (k0 - b.fresh_pos0) : k0;
-        const unsigned so = (unsigned)(kr / SMOL_SLAB) * SLAB_K_BYTES;
-        const rsrc_t rk = fr ? rk_f : rk_c, rv = fr ? rv_f : rv_c;
+        so = (unsigned)(kr / SMOL_SLAB) * SLAB_K_BYTES;
+        r = value ? (fr ? rv_f : rv_c) : (fr ? rk_f : rk_c);
+    };
+    auto issue_k = [&](int k0, KRaw &r) {
+        rsrc_t rs;
+        unsigned so;
+        slab_src(k0, false, rs, so);
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) r.k[t][ks] = bload(rk, vo_k[t][ks], so);
+            for (int ks = 0; ks < KS; ks++) r.k[t][ks] = bload(rs, vo_k[t][ks], so);
+    };
+    auto issue_v = [&](int k0, VRaw &r) {
+        rsrc_t rs;
+        unsigned so;
+        slab_src(k0, true, rs, so);
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) r.v[dt] = bload(rv, vo_v[dt], so);
+        for (int dt = 0; dt < DT; dt++) r.v[dt] = bload(rs, vo_v[dt], so);
     };
 
-    auto compute = [&](int k0, const Raw &r, auto fresh_tag) {
+    auto qk = [&](const KRaw &r, f4 (&sacc)[NT][2], auto fresh_tag) {
         constexpr bool FRESH = decltype(fresh_tag)::value;
-        f4 sacc[NT][2];
 #pragma unroll
         for (int nt = 0; nt < NT; nt++)
 #pragma unroll
@@ -627,8 +656,12 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
 #pragma unroll
                 for (int ks = 0; ks < KS; ks++) {
                     if (FRESH) {
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const h8 *>(&r.k[t][ks]),
-                                                                     qf[nt][ks], acc, 0, 0, 0);
+                        /* fp16 Q for the fp16 fresh slab, re-formed from its two bf16 parts */
+                        h8 qf;
+#pragma unroll
+                        for (int i = 0; i < 8; i++) qf[i] = (_Float16)((float)qh[nt][ks][i] + (float)ql[nt][ks][i]);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const h8 *>(&r.k[t][ks]), qf,
+                                                                     acc, 0, 0, 0);
                     } else {
                         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(r.k[t][ks]), qh[nt][ks], acc, 0, 0, 0);
                         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(r.k[t][ks]), ql[nt][ks], acc, 0, 0, 0);
@@ -636,6 +669,10 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
                 }
                 sacc[nt][t] = acc;
             }
+    };
+
+    auto smpv = [&](int k0, const f4 (&sacc)[NT][2], const VRaw &r, auto fresh_tag) {
+        constexpr bool FRESH = decltype(fresh_tag)::value;
         const bool full = k0 >= lo_max && k0 + SMOL_SLAB <= hi_min;
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
@@ -658,8 +695,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
             float mx = sv[0];
 #pragma unroll
             for (int e = 1; e < 8; e++) mx = fmaxf(mx, sv[e]);
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            mx = row_max4(mx);
             const bool need = mx > m[nt] + LAZY_T;
             if (__any(need)) {
                 const float m_new = need ? mx : m[nt];
@@ -697,40 +733,37 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
             }
         }
     };
-    auto process = [&](int k0, const Raw &r) {
-        if (k0 >= b.fresh_pos0) compute(k0, r, std::true_type{});
-        else compute(k0, r, std::false_type{});
-    };
 
-    /* each wave streams slabs wave, wave + SK_WAVES, ...; two register
-     * buffers alternate so the next slab's loads are in flight while the
-     * current one is computed */
+    /* Each wave streams slabs wave, wave + SK_WAVES, ... with one K and one V
+     * register buffer: the next slab's K is requested as soon as the current
+     * S is formed and its V as soon as the current P.V is issued. The request
+     * is made on every path (past the end it re-reads the current slab), so
+     * every wait sees the same number of loads in flight. */
     const int step = SMOL_SLAB * SK_WAVES;
     const int end = it.key_end;
     int k0 = it.key_begin + wave * SMOL_SLAB;
-    if constexpr (HD <= 128) {
-        Raw ra, rb;
-        if (k0 < end) issue(k0, ra);
-        while (k0 < end) {
+    if (k0 < end) {
+        KRaw kr;
+        VRaw vr;
+        issue_k(k0, kr);
+        issue_v(k0, vr);
+        while (true) {
             const int k1 = k0 + step;
-            if (k1 < end) issue(k1, rb);
-            process(k0, ra);
+            const int kn = k1 < end ? k1 : k0;
+            f4 sacc[NT][2];
+            const bool fr = k0 >= b.fresh_pos0;
+            if (fr) qk(kr, sacc, std::true_type{});
+            else qk(kr, sacc, std::false_type{});
+            issue_k(kn, kr);
+            if (fr) smpv(k0, sacc, vr, std::true_type{});
+            else smpv(k0, sacc, vr, std::false_type{});
+            issue_v(kn, vr);
             if (k1 >= end) break;
-            const int k2 = k1 + step;
-            if (k2 < end) issue(k2, ra);
-            process(k1, rb);
-            k0 = k2;
-        }
-    } else {
-        /* head_dim 256: one slab of K and V is 128 registers; no second buffer */
-        for (; k0 < end; k0 += step) {
-            Raw ra;
-            issue(k0, ra);
-            process(k0, ra);
+            k0 = k1;
         }
     }
 
-    finish_item<HD, NT>(p, it, b, g, tid, m, l, o, s_o, s_m, s_l, &s_last);
+    finish_item<HD, NT>(p, it, b, item, g, tid, m, l, o, s_o, s_m, s_l, &s_last);
 }
 
 /* ---------------------------------------------------------------- k_attn_pf */
@@ -746,8 +779,8 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
  * element a wave loads is used by NT*16 rows. Lazy rescale and unmasked
  * interior slabs as in k_attn_dec.
  */
-template <int HD, int NT>
-__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_attn_pf(SkParams p) {
+template <int HD, int NT, int W>
+__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W, W))) void k_attn_pf(SkParams p) {
     constexpr int KS = (HD + 31) / 32;
     constexpr int DT = (HD + 15) / 16;
     constexpr int HDP = KS * 32;
@@ -758,8 +791,11 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
     const int c = lane & 15, j = lane >> 4;
-    const int g = blockIdx.y;
-    const SkItem it = p.items[blockIdx.x];
+    /* kv head fastest in the block index: consecutive workgroups go to
+     * consecutive XCDs, so each XCD's L2 holds the K/V of its own heads */
+    const int g = (int)(blockIdx.x % (unsigned)p.Hkv);
+    const int item = (int)(blockIdx.x / (unsigned)p.Hkv);
+    const SkItem it = p.items[item];
     const SkBatch b = p.batches[it.batch];
     const int G = p.G;
     constexpr int SO = (SK_WAVES - 1) * ROWS * OSTR > 2 * SK_MERGE_MAX + 128 ? (SK_WAVES - 1) * ROWS * OSTR
@@ -826,26 +862,39 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
         vo_v[dt] = (HD % 16 == 0 || d < HD) ? (unsigned)((d * SMOL_SLAB + 8 * j) * 2) : OOB_OFF;
     }
 
-    struct Raw {
+    struct KRaw {
         uint4 k[2][KS];
+    };
+    struct VRaw {
         uint4 v[DT];
     };
-    auto issue = [&](int k0, Raw &r) {
+    /* slab k0's resource and slab offset (uniform: SGPRs) */
+    auto slab_src = [&](int k0, bool value, rsrc_t &r, unsigned &so) {
         const bool fr = k0 >= b.fresh_pos0;
         const int kr = fr ? b.fresh_row0 + (k0 - b.fresh_pos0) : k0;
-        const unsigned so = (unsigned)(kr / SMOL_SLAB) * SLAB_BYTES;
-        const rsrc_t rk = fr ? rk_f : rk_c, rv = fr ? rv_f : rv_c;
+        so = (unsigned)(kr / SMOL_SLAB) * SLAB_BYTES;
+        r = value ? (fr ? rv_f : rv_c) : (fr ? rk_f : rk_c);
+    };
+    auto issue_k = [&](int k0, KRaw &r) {
+        rsrc_t rs;
+        unsigned so;
+        slab_src(k0, false, rs, so);
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) r.k[t][ks] = bload(rk, vo_k[t][ks], so);
+            for (int ks = 0; ks < KS; ks++) r.k[t][ks] = bload(rs, vo_k[t][ks], so);
+    };
+    auto issue_v = [&](int k0, VRaw &r) {
+        rsrc_t rs;
+        unsigned so;
+        slab_src(k0, true, rs, so);
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) r.v[dt] = bload(rv, vo_v[dt], so);
+        for (int dt = 0; dt < DT; dt++) r.v[dt] = bload(rs, vo_v[dt], so);
     };
 
-    auto compute = [&](int k0, const Raw &r, auto fresh_tag) {
+    /* S^T = K . Q^T for the slab */
+    auto qk = [&](const KRaw &r, f4 (&sacc)[NT][2], auto fresh_tag) {
         constexpr bool FRESH = decltype(fresh_tag)::value;
-        f4 sacc[NT][2];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             h8 kfrag[KS];
@@ -861,6 +910,10 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
                 sacc[nt][t] = acc;
             }
         }
+    };
+    /* mask / softcap, online softmax, O^T += V^T . P^T */
+    auto smpv = [&](int k0, const f4 (&sacc)[NT][2], const VRaw &r, auto fresh_tag) {
+        constexpr bool FRESH = decltype(fresh_tag)::value;
         h8 vfrag[DT];
 #pragma unroll
         for (int dt = 0; dt < DT; dt++)
@@ -887,8 +940,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
             float mx = sv[0];
 #pragma unroll
             for (int e = 1; e < 8; e++) mx = fmaxf(mx, sv[e]);
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            mx = row_max4(mx);
             const bool need = mx > m[nt] + LAZY_T;
             if (__any(need)) {
                 const float m_new = need ? mx : m[nt];
@@ -913,35 +965,37 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(1
                 o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vfrag[dt], pf, o[nt][dt], 0, 0, 0);
         }
     };
-    auto process = [&](int k0, const Raw &r) {
-        if (k0 >= b.fresh_pos0) compute(k0, r, std::true_type{});
-        else compute(k0, r, std::false_type{});
-    };
 
+    /* Each wave streams slabs wave, wave + SK_WAVES, ... with one K and one V
+     * register buffer: the next slab's K is requested as soon as the current
+     * S is formed and its V as soon as the current P.V is issued, so each
+     * load has about half a slab of work to arrive. The request is made on
+     * every path (past the end it re-reads the current slab), so every wait
+     * sees the same number of loads in flight. */
     const int step = SMOL_SLAB * SK_WAVES;
     const int end = it.key_end;
     int k0 = it.key_begin + wave * SMOL_SLAB;
-    if constexpr (NT * HD <= 256) {
-        Raw ra, rb;
-        if (k0 < end) issue(k0, ra);
-        while (k0 < end) {
+    if (k0 < end) {
+        KRaw kr;
+        VRaw vr;
+        issue_k(k0, kr);
+        issue_v(k0, vr);
+        while (true) {
             const int k1 = k0 + step;
-            if (k1 < end) issue(k1, rb);
-            process(k0, ra);
+            const int kn = k1 < end ? k1 : k0;
+            f4 sacc[NT][2];
+            const bool fr = k0 >= b.fresh_pos0;
+            if (fr) qk(kr, sacc, std::true_type{});
+            else qk(kr, sacc, std::false_type{});
+            issue_k(kn, kr);
+            if (fr) smpv(k0, sacc, vr, std::true_type{});
+            else smpv(k0, sacc, vr, std::false_type{});
+            issue_v(kn, vr);
             if (k1 >= end) break;
-            const int k2 = k1 + step;
-            if (k2 < end) issue(k2, ra);
-            process(k1, rb);
-            k0 = k2;
-        }
-    } else {
-        for (; k0 < end; k0 += step) {
-            Raw ra;
-            issue(k0, ra);
-            process(k0, ra);
+            k0 = k1;
         }
     }
-    finish_item<HD, NT>(p, it, b, g, tid, m, l, o, s_o, s_m, s_l, &s_last);
+    finish_item<HD, NT>(p, it, b, item, g, tid, m, l, o, s_o, s_m, s_l, &s_last);
 }
 
 /* ------------------------------------------------------------ k_rope_apply */
@@ -996,51 +1050,66 @@ extern "C" int smol_launch_rope_apply(float *x, const float *cos_t, const float 
 extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t st) {
     if (n_blocks <= 0) return 0;
     if (pp->hd > 256) return -1;
-    hipLaunchKernelGGL(k_prep, dim3(n_blocks, pp->Hkv), dim3(256), 0, st, *pp);
+    hipLaunchKernelGGL(k_prep, dim3(n_blocks * pp->Hkv), dim3(256), 0, st, *pp);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
+template <int HD, int NT, int W>
+static void launch_dec_v(const SkParams *sp, dim3 grid, hipStream_t st) {
+    hipLaunchKernelGGL((k_attn_dec<HD, NT, W>), grid, dim3(64 * SK_WAVES), 0, st, *sp);
+}
+
 template <int HD>
-static int launch_dec_hd(const SkParams *sp, int n_items, int nt, hipStream_t st) {
-    dim3 grid(n_items, sp->Hkv), block(64 * SK_WAVES);
-    if (nt == 1) hipLaunchKernelGGL((k_attn_dec<HD, 1>), grid, block, 0, st, *sp);
-    else if (nt == 2 && HD <= 128) hipLaunchKernelGGL((k_attn_dec<HD, (HD <= 128 ? 2 : 1)>), grid, block, 0, st, *sp);
+static int launch_dec_hd(const SkParams *sp, int n_items, int nt, int w, hipStream_t st) {
+    const dim3 grid(n_items * sp->Hkv);
+    if (nt == 1 && w == 1) launch_dec_v<HD, 1, 1>(sp, grid, st);
+    else if (nt == 1 && w == 2) launch_dec_v<HD, 1, 2>(sp, grid, st);
+    else if (nt == 2 && w == 1 && HD <= 128) launch_dec_v<HD, (HD <= 128 ? 2 : 1), 1>(sp, grid, st);
+    else if (nt == 2 && w == 2 && HD <= 128) launch_dec_v<HD, (HD <= 128 ? 2 : 1), 2>(sp, grid, st);
     else return -1;
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st) {
+extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st) {
     if (n_items <= 0) return 0;
     switch (hd) {
-    case 64: return launch_dec_hd<64>(sp, n_items, nt, st);
-    case 72: return launch_dec_hd<72>(sp, n_items, nt, st);
-    case 80: return launch_dec_hd<80>(sp, n_items, nt, st);
-    case 96: return launch_dec_hd<96>(sp, n_items, nt, st);
-    case 128: return launch_dec_hd<128>(sp, n_items, nt, st);
-    case 256: return launch_dec_hd<256>(sp, n_items, nt, st);
+    case 64: return launch_dec_hd<64>(sp, n_items, nt, w, st);
+    case 72: return launch_dec_hd<72>(sp, n_items, nt, w, st);
+    case 80: return launch_dec_hd<80>(sp, n_items, nt, w, st);
+    case 96: return launch_dec_hd<96>(sp, n_items, nt, w, st);
+    case 128: return launch_dec_hd<128>(sp, n_items, nt, w, st);
+    case 256: return launch_dec_hd<256>(sp, n_items, nt, w, st);
     default: return -1;
     }
 }
 
+template <int HD, int NT, int W>
+static void launch_pf_v(const SkParams *sp, dim3 grid, hipStream_t st) {
+    hipLaunchKernelGGL((k_attn_pf<HD, NT, W>), grid, dim3(64 * SK_WAVES), 0, st, *sp);
+}
+
 template <int HD>
-static int launch_pf_hd(const SkParams *sp, int n_items, int nt, hipStream_t st) {
-    dim3 grid(n_items, sp->Hkv), block(64 * SK_WAVES);
-    if (nt == 1) hipLaunchKernelGGL((k_attn_pf<HD, 1>), grid, block, 0, st, *sp);
-    else if (nt == 2 && HD <= 128) hipLaunchKernelGGL((k_attn_pf<HD, (HD <= 128 ? 2 : 1)>), grid, block, 0, st, *sp);
-    else if (nt == 4 && HD <= 96) hipLaunchKernelGGL((k_attn_pf<HD, (HD <= 96 ? 4 : 1)>), grid, block, 0, st, *sp);
+static int launch_pf_hd(const SkParams *sp, int n_items, int nt, int w, hipStream_t st) {
+    const dim3 grid(n_items * sp->Hkv);
+    if (nt == 1 && w == 1) launch_pf_v<HD, 1, 1>(sp, grid, st);
+    else if (nt == 1 && w == 2) launch_pf_v<HD, 1, 2>(sp, grid, st);
+    else if (nt == 2 && w == 1 && HD <= 128) launch_pf_v<HD, (HD <= 128 ? 2 : 1), 1>(sp, grid, st);
+    else if (nt == 2 && w == 2 && HD <= 128) launch_pf_v<HD, (HD <= 128 ? 2 : 1), 2>(sp, grid, st);
+    else if (nt == 4 && w == 1 && HD <= 96) launch_pf_v<HD, (HD <= 96 ? 4 : 1), 1>(sp, grid, st);
+    else if (nt == 4 && w == 2 && HD <= 96) launch_pf_v<HD, (HD <= 96 ? 4 : 1), 2>(sp, grid, st);
     else return -1;
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-extern "C" int smol_launch_pf(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st) {
+extern "C" int smol_launch_pf(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st) {
     if (n_items <= 0) return 0;
     switch (hd) {
-    case 64: return launch_pf_hd<64>(sp, n_items, nt, st);
-    case 72: return launch_pf_hd<72>(sp, n_items, nt, st);
-    case 80: return launch_pf_hd<80>(sp, n_items, nt, st);
-    case 96: return launch_pf_hd<96>(sp, n_items, nt, st);
-    case 128: return launch_pf_hd<128>(sp, n_items, nt, st);
-    case 256: return launch_pf_hd<256>(sp, n_items, nt, st);
+    case 64: return launch_pf_hd<64>(sp, n_items, nt, w, st);
+    case 72: return launch_pf_hd<72>(sp, n_items, nt, w, st);
+    case 80: return launch_pf_hd<80>(sp, n_items, nt, w, st);
+    case 96: return launch_pf_hd<96>(sp, n_items, nt, w, st);
+    case 128: return launch_pf_hd<128>(sp, n_items, nt, w, st);
+    case 256: return launch_pf_hd<256>(sp, n_items, nt, w, st);
     default: return -1;
     }
 }
