@@ -286,6 +286,49 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
 
 /* --------------------------------------------------------- shared by kernels */
 
+/* Raw buffer resources: a base address plus a byte range; a load whose
+ * VGPR offset (+ immediate) is past the range returns zero, which is how the
+ * padded columns of head_dim 72 / 80 / 96 read as zeros. */
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef unsigned u4v __attribute__((ext_vector_type(4)));
+#define RSRC_WORD3 0x00020000
+#define OOB_OFF 0x7FFFFFF0u
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *ptr, long long bytes) {
+    const long long n = bytes < 0x7FFF0000LL ? bytes : 0x7FFF0000LL;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(ptr), (short)0, (int)n, RSRC_WORD3);
+}
+
+__device__ __forceinline__ uint4 bload(rsrc_t r, unsigned voff, unsigned soff) {
+    const u4v v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+/* Device-coherent (SC1) buffer accesses for the split-K partials. The L2s
+ * of the XCDs are not coherent with each other; SC1 stores write through to
+ * the device coherence point and SC1 loads read from it, so partials pass
+ * between workgroups on different XCDs without an L2 write-back or
+ * invalidate (what an agent-scope release / acquire fence would cost). */
+#define CPOL_SC1 16
+__device__ __forceinline__ void store_f4_sc1(rsrc_t r, unsigned voff, f4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(u4v{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                               __float_as_uint(v[3])},
+                                           r, voff, 0, CPOL_SC1);
+}
+__device__ __forceinline__ f4 load_f4_sc1(rsrc_t r, unsigned voff) {
+    const u4v v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, CPOL_SC1);
+    return f4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
+}
+__device__ __forceinline__ void store_f2_sc1(rsrc_t r, unsigned voff, float a, float b) {
+    typedef unsigned u2v __attribute__((ext_vector_type(2)));
+    __builtin_amdgcn_raw_buffer_store_b64(u2v{__float_as_uint(a), __float_as_uint(b)}, r, voff, 0, CPOL_SC1);
+}
+__device__ __forceinline__ float2 load_f2_sc1(rsrc_t r, unsigned voff) {
+    typedef unsigned u2v __attribute__((ext_vector_type(2)));
+    const u2v v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, CPOL_SC1);
+    return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+}
+
 #define SK_WAVES 4
 #define SK_MERGE_MAX 1024 /* max ROWS * n_split of one merge group (LDS) */
 
@@ -321,10 +364,13 @@ __device__ __forceinline__ void merge_group(const SkParams &p, const SkItem &it,
     const int nsp = it.n_split;
     float *s_ml = s_o;                       /* [nsp][ROWS][2], then weights [nsp][ROWS] */
     float *s_row = s_o + 2 * SK_MERGE_MAX;   /* per row: max, 1/sum */
+    /* the group's items are contiguous: item `first + sp` holds split sp */
+    const rsrc_t rml = make_rsrc(p.part_ml, (long long)(first + nsp) * p.Hkv * ROWS * 2 * 4);
+    const rsrc_t ro = make_rsrc(p.part_o, (long long)(first + nsp) * p.Hkv * ROWS * HD * 4);
     for (int e = tid; e < nsp * ROWS; e += 64 * SK_WAVES) {
         const int sp = e / ROWS, rr = e - sp * ROWS;
         const long long pr = ((long long)(first + sp) * p.Hkv + g) * ROWS + rr;
-        const float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + pr * 2);
+        const float2 ml = load_f2_sc1(rml, (unsigned)(pr * 8));
         s_ml[2 * e] = ml.x;
         s_ml[2 * e + 1] = ml.y;
     }
@@ -358,7 +404,7 @@ __device__ __forceinline__ void merge_group(const SkParams &p, const SkItem &it,
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 const int sp = min(sp0 + u, nsp - 1);
-                v[u] = *reinterpret_cast<const f4 *>(p.part_o + (((long long)(first + sp) * p.Hkv + g) * ROWS + rr) * HD + d);
+                v[u] = load_f4_sc1(ro, (unsigned)(((((long long)(first + sp) * p.Hkv + g) * ROWS + rr) * HD + d) * 4));
             }
 #pragma unroll
             for (int u = 0; u < 8; u++)
@@ -368,7 +414,8 @@ __device__ __forceinline__ void merge_group(const SkParams &p, const SkItem &it,
         *reinterpret_cast<f4 *>(p.out + ((long long)(b.out_tok0 + qi) * Hq + (g * G + hg)) * HD + d) =
             acc * s_row[2 * rr + 1];
     }
-    if (tid == 0) p.counters[(long long)it.group * p.Hkv + g] = 0;
+    if (tid == 0)
+        __hip_atomic_store(p.counters + (long long)it.group * p.Hkv + g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* Epilogue shared by the attention kernels: combines the SK_WAVES waves'
@@ -444,34 +491,36 @@ __device__ __forceinline__ void finish_item(const SkParams &p, const SkItem &it,
         }
         return;
     }
+    /* Publish the partial with device-coherent stores, wait until they are
+     * complete, then count in; the group's last workgroup merges (reading
+     * with device-coherent loads). */
     const long long pbase = ((long long)item * p.Hkv + g) * ROWS;
     if (wave == 0) {
+        const rsrc_t ro = make_rsrc(p.part_o + pbase * HD, (long long)ROWS * HD * 4);
+        const rsrc_t rml = make_rsrc(p.part_ml + pbase * 2, (long long)ROWS * 2 * 4);
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             const int rr = nt * 16 + c;
-            float *po = p.part_o + (pbase + rr) * HD;
 #pragma unroll
             for (int dt = 0; dt < DT; dt++) {
                 const int d = 16 * dt + 4 * j;
                 if (HD % 16 != 0 && d >= HD) continue;
-                *reinterpret_cast<f4 *>(po + d) = o[nt][dt];
+                store_f4_sc1(ro, (unsigned)((rr * HD + d) * 4), o[nt][dt]);
             }
-            if (j == 0) {
-                p.part_ml[(pbase + rr) * 2 + 0] = m[nt];
-                p.part_ml[(pbase + rr) * 2 + 1] = l[nt];
-            }
+            if (j == 0) store_f2_sc1(rml, (unsigned)(rr * 8), m[nt], l[nt]);
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0); /* every store above acknowledged */
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
         int prev = 0;
         if (lane == 0)
-            prev = __hip_atomic_fetch_add(p.counters + (long long)it.group * p.Hkv + g, 1, __ATOMIC_ACQ_REL,
+            prev = __hip_atomic_fetch_add(p.counters + (long long)it.group * p.Hkv + g, 1, __ATOMIC_RELAXED,
                                           __HIP_MEMORY_SCOPE_AGENT);
         prev = __shfl(prev, 0);
         if (lane == 0) *s_last = prev == it.n_split - 1;
     }
     __syncthreads();
     if (!*s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     merge_group<HD, ROWS>(p, it, b, item, g, tid, s_o);
 }
 
@@ -501,24 +550,6 @@ __device__ __forceinline__ void split8(const float *x, b8 &hi, b8 &lo) {
         hi[i] = h;
         lo[i] = (__bf16)(x[i] - (float)h);
     }
-}
-
-/* Raw buffer resources: a base address plus a byte range; a load whose
- * VGPR offset (+ immediate) is past the range returns zero, which is how the
- * padded columns of head_dim 72 / 80 / 96 read as zeros. */
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-typedef unsigned u4v __attribute__((ext_vector_type(4)));
-#define RSRC_WORD3 0x00020000
-#define OOB_OFF 0x7FFFFFF0u
-
-__device__ __forceinline__ rsrc_t make_rsrc(const void *ptr, long long bytes) {
-    const long long n = bytes < 0x7FFF0000LL ? bytes : 0x7FFF0000LL;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(ptr), (short)0, (int)n, RSRC_WORD3);
-}
-
-__device__ __forceinline__ uint4 bload(rsrc_t r, unsigned voff, unsigned soff) {
-    const u4v v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-    return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
 template <int HD, int NT, int W>
