@@ -33,6 +33,19 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 MALL_BYTES = 256 << 20
 
 
+def profiled_traffic(name):
+    """HBM bytes per launch of a kernel, as measured by the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+    summarised in profiles/<name>.md (None when there is no such summary)."""
+    path = os.path.join(ROOT, "profiles", name + ".md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def layers_for(bytes_per_layer, lo=2, hi=64):
     n = -(-2 * MALL_BYTES // max(1, bytes_per_layer))
     return int(max(lo, min(hi, n)))
@@ -123,7 +136,10 @@ def main():
             "config": dict(main_wl.describe(), layers_rotated=n_layers, parallelism="single GPU"),
             "roofline": {"bound": "mfma", "kernel": "k_attn_pf", "achieved": round(achieved, 3),
                          "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_TFLOPS, 5),
-                         "traffic": None, "kernel_ms": round(attn_ms, 5), "prep_kernel_ms": round(prep_ms, 5),
+                         "traffic": profiled_traffic("k_attn_pf_qwen06b_prefill"),
+                         "traffic_source": "profiles/k_attn_pf_qwen06b_prefill.md (rocprofv3 FETCH_SIZE x2.0 + "
+                                           "WRITE_SIZE x1.0, copy-calibrated)",
+                         "kernel_ms": round(attn_ms, 5), "prep_kernel_ms": round(prep_ms, 5),
                          "flops_per_launch": flops},
         }
     else:
