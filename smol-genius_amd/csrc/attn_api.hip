@@ -28,6 +28,7 @@
 extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t st);
 extern "C" int smol_launch_pf(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
 extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
+extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, int kg, hipStream_t st);
 extern "C" int smol_launch_rope_apply(float *x, const float *cos_t, const float *sin_t,
                                       const int *pos, int seq, int n_heads, int hd, int kind,
                                       hipStream_t st);
@@ -516,8 +517,10 @@ static int choose_waves(bool dec, int hd, int nt) {
     return (nt == 4 || (nt == 2 && hd > 96)) ? 1 : 2;
 }
 
-static void plan_items(Plan &pl, int Hkv, int G, int window, int nt, int cu_count) {
-    const int rows_per = 16 * nt;
+/* rows_per: query rows of one work item; longest_first: order the merge
+ * groups by descending key count, so the last workgroups dispatched are the
+ * short ones */
+static void plan_items(Plan &pl, int Hkv, int G, int window, int rows_per, int cu_count, bool longest_first) {
     struct Tile { int batch, row0, lo, hi; };
     std::vector<Tile> tiles;
     long long total_slabs = 0;
@@ -536,10 +539,14 @@ static void plan_items(Plan &pl, int Hkv, int G, int window, int nt, int cu_coun
             total_slabs += (hi - lo + SMOL_SLAB - 1) / SMOL_SLAB;
         }
     }
+    if (longest_first)
+        std::stable_sort(tiles.begin(), tiles.end(),
+                         [](const Tile &a, const Tile &b) { return a.hi - a.lo > b.hi - b.lo; });
     /* a workgroup per compute unit and wave slot, each wave >= 2 slabs */
     const long long target_items = (long long)cu_count;
     long long per = (total_slabs * Hkv + target_items - 1) / std::max(1LL, target_items);
-    int slabs_per_item = (int)std::max(8LL, per);
+    /* k_attn_pf splits an item's slabs over its 4 waves, k_attn_fa gives each slab to all of them */
+    int slabs_per_item = (int)std::max(longest_first ? 4LL : 8LL, per);
     /* tuning override: SMOL_ATTN_SLABS_PER_ITEM=n fixes the key slabs per work item */
     if (const int n = env_int("SMOL_ATTN_SLABS_PER_ITEM")) {
         if (n > 0) slabs_per_item = n;
@@ -573,14 +580,31 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     const int G = cs.Hq / cs.Hkv;
     int max_rows = 0;
     for (auto &b : pl.sb) max_rows = std::max(max_rows, b.n_rows);
-    int nt = cs.dec ? (max_rows <= 16 || hd > 128 ? 1 : 2) : choose_nt(hd, max_rows);
-    if (const int ov = env_int("SMOL_ATTN_NT")) {
-        if ((ov == 1 || ov == 2 || ov == 4) && (ov <= 2 || hd <= 96) && (ov == 1 || hd <= 128) && !(cs.dec && ov == 4))
-            nt = ov;
+    /* prefill kernel: k_attn_fa (waves split the rows, K/V shared through
+     * LDS) unless SMOL_ATTN_PREFILL_KERNEL=pf selects k_attn_pf */
+    const char *pk = getenv("SMOL_ATTN_PREFILL_KERNEL");
+    const bool fa = !cs.dec && !(pk && strcmp(pk, "pf") == 0);
+    int nt, w, rows_per, kg = 1;
+    if (fa) {
+        nt = (hd <= 128 && max_rows > 64) ? 2 : 1;
+        if (const int ov = env_int("SMOL_ATTN_NT"))
+            if (ov == 1 || (ov == 2 && hd <= 128)) nt = ov;
+        /* SMOL_ATTN_FA_KG=2: two key groups (8 waves, two per SIMD in one
+         * workgroup), up to head_dim 128 */
+        kg = (hd <= 128 && env_int("SMOL_ATTN_FA_KG") == 2) ? 2 : 1;
+        w = kg == 2 ? 2 : (hd > 128 || env_int("SMOL_ATTN_FA_WAVES") == 1 ? 1 : 2);
+        rows_per = 64 * nt;
+    } else {
+        nt = cs.dec ? (max_rows <= 16 || hd > 128 ? 1 : 2) : choose_nt(hd, max_rows);
+        if (const int ov = env_int("SMOL_ATTN_NT")) {
+            if ((ov == 1 || ov == 2 || ov == 4) && (ov <= 2 || hd <= 96) && (ov == 1 || hd <= 128) &&
+                !(cs.dec && ov == 4))
+                nt = ov;
+        }
+        w = choose_waves(cs.dec, hd, nt);
+        rows_per = 16 * nt;
     }
-    const int w = choose_waves(cs.dec, hd, nt);
-    plan_items(pl, cs.Hkv, G, cs.window, nt, ctx->cu_count * w);
-    const int rows_per = 16 * nt;
+    plan_items(pl, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * (kg == 2 ? 1 : w), fa);
 
     /* workspace */
     int rc;
@@ -669,6 +693,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     sp.counters = (int *)ctx->counters.p;
     mk = timing_begin(ctx, 1);
     rc = cs.dec ? smol_launch_dec(&sp, hd, (int)n_items, nt, w, ctx->stream)
+         : fa   ? smol_launch_fa(&sp, hd, (int)n_items, nt, w, kg, ctx->stream)
                 : smol_launch_pf(&sp, hd, (int)n_items, nt, w, ctx->stream);
     timing_end(ctx, mk);
     if (rc)

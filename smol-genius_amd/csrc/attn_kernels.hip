@@ -356,7 +356,7 @@ __device__ __forceinline__ float row_sum4(float v) {
  * then each (row, 4 columns) element sums the weighted partials with eight
  * independent loads in flight. The host keeps ROWS * n_split within
  * SK_MERGE_MAX. Resets the group's counter for the next call. */
-template <int HD, int ROWS>
+template <int HD, int ROWS, int TPB = 64 * SK_WAVES>
 __device__ __forceinline__ void merge_group(const SkParams &p, const SkItem &it, const SkBatch &b, int item, int g,
                                             int tid, float *s_o) {
     const int G = p.G, Hq = p.Hq;
@@ -365,11 +365,11 @@ __device__ __forceinline__ void merge_group(const SkParams &p, const SkItem &it,
     float *s_ml = s_o;                       /* [nsp][ROWS][2], then weights [nsp][ROWS] */
     float *s_row = s_o + 2 * SK_MERGE_MAX;   /* per row: max, 1/sum */
     /* the group's items are contiguous: item `first + sp` holds split sp */
-    const rsrc_t rml = make_rsrc(p.part_ml, (long long)(first + nsp) * p.Hkv * ROWS * 2 * 4);
-    const rsrc_t ro = make_rsrc(p.part_o, (long long)(first + nsp) * p.Hkv * ROWS * HD * 4);
-    for (int e = tid; e < nsp * ROWS; e += 64 * SK_WAVES) {
+    const rsrc_t rml = make_rsrc(p.part_ml + (long long)first * p.Hkv * ROWS * 2, (long long)nsp * p.Hkv * ROWS * 2 * 4);
+    const rsrc_t ro = make_rsrc(p.part_o + (long long)first * p.Hkv * ROWS * HD, (long long)nsp * p.Hkv * ROWS * HD * 4);
+    for (int e = tid; e < nsp * ROWS; e += TPB) {
         const int sp = e / ROWS, rr = e - sp * ROWS;
-        const long long pr = ((long long)(first + sp) * p.Hkv + g) * ROWS + rr;
+        const long long pr = ((long long)sp * p.Hkv + g) * ROWS + rr;
         const float2 ml = load_f2_sc1(rml, (unsigned)(pr * 8));
         s_ml[2 * e] = ml.x;
         s_ml[2 * e + 1] = ml.y;
@@ -388,31 +388,59 @@ __device__ __forceinline__ void merge_group(const SkParams &p, const SkItem &it,
         s_row[2 * tid + 1] = L > 0.0f ? 1.0f / L : 0.0f;
     }
     __syncthreads();
-    for (int e = tid; e < nsp * ROWS; e += 64 * SK_WAVES) {
+    for (int e = tid; e < nsp * ROWS; e += TPB) {
         const int rr = e % ROWS;
         s_ml[2 * e] = __builtin_amdgcn_exp2f(s_ml[2 * e] - s_row[2 * rr]); /* weight of (split, row) */
     }
     __syncthreads();
+    /* every thread owns E (row, 4-column) elements, taken EB at a time; the
+     * splits are walked U at a time with all EB * U (about 16) loads in
+     * flight, so the merge costs about (E / EB) * n_split / U memory round
+     * trips */
     constexpr int C4 = HD / 4;
-    for (int e = tid; e < ROWS * C4; e += 64 * SK_WAVES) {
-        const int rr = e / C4, d = (e - rr * C4) * 4;
-        const int r = it.row0 + rr;
-        if (r >= b.n_rows) continue;
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int sp0 = 0; sp0 < nsp; sp0 += 8) {
-            f4 v[8];
+    constexpr int E = (ROWS * C4 + TPB - 1) / (TPB);
+    constexpr int EB = E < 8 ? E : 8;
+    constexpr int U = 16 / EB > 8 ? 8 : 16 / EB;
+    const unsigned sp_stride = (unsigned)((long long)p.Hkv * ROWS * HD * 4);
+    for (int e0 = 0; e0 < E; e0 += EB) {
+        f4 acc[EB];
+        int prow[EB], pcol[EB];
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int sp = min(sp0 + u, nsp - 1);
-                v[u] = load_f4_sc1(ro, (unsigned)(((((long long)(first + sp) * p.Hkv + g) * ROWS + rr) * HD + d) * 4));
+        for (int e = 0; e < EB; e++) {
+            acc[e] = f4{0.f, 0.f, 0.f, 0.f};
+            const int idx = tid + TPB * (e0 + e);
+            const int rr = idx / C4;
+            const bool ok = e0 + e < E && idx < ROWS * C4 && it.row0 + rr < b.n_rows;
+            prow[e] = ok ? rr : -1;
+            pcol[e] = (idx - rr * C4) * 4;
+        }
+        for (int sp0 = 0; sp0 < nsp; sp0 += U) {
+            f4 v[U][EB];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const unsigned so = (unsigned)min(sp0 + u, nsp - 1) * sp_stride;
+#pragma unroll
+                for (int e = 0; e < EB; e++) {
+                    const int rr = prow[e] < 0 ? 0 : prow[e];
+                    v[u][e] = load_f4_sc1(ro, (unsigned)(((g * ROWS + rr) * HD + pcol[e]) * 4) + so);
+                }
             }
 #pragma unroll
-            for (int u = 0; u < 8; u++)
-                if (sp0 + u < nsp) acc += s_ml[2 * ((sp0 + u) * ROWS + rr)] * v[u];
+            for (int u = 0; u < U; u++) {
+                if (sp0 + u >= nsp) break;
+#pragma unroll
+                for (int e = 0; e < EB; e++)
+                    if (prow[e] >= 0) acc[e] += s_ml[2 * ((sp0 + u) * ROWS + prow[e])] * v[u][e];
+            }
         }
-        const int qi = r / G, hg = r - qi * G;
-        *reinterpret_cast<f4 *>(p.out + ((long long)(b.out_tok0 + qi) * Hq + (g * G + hg)) * HD + d) =
-            acc * s_row[2 * rr + 1];
+#pragma unroll
+        for (int e = 0; e < EB; e++) {
+            if (prow[e] < 0) continue;
+            const int r = it.row0 + prow[e];
+            const int qi = r / G, hg = r - qi * G;
+            *reinterpret_cast<f4 *>(p.out + ((long long)(b.out_tok0 + qi) * Hq + (g * G + hg)) * HD + pcol[e]) =
+                acc[e] * s_row[2 * prow[e] + 1];
+        }
     }
     if (tid == 0)
         __hip_atomic_store(p.counters + (long long)it.group * p.Hkv + g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1029,6 +1057,418 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
     finish_item<HD, NT>(p, it, b, item, g, tid, m, l, o, s_o, s_m, s_l, &s_last);
 }
 
+/* ---------------------------------------------------------------- k_attn_fa */
+
+/*
+ * Prefill, chunked prefill and windowed bidirectional attention with the
+ * four waves of a workgroup on different query rows and the K/V slabs shared
+ * through LDS. Wave w owns row tiles w*NT .. w*NT+NT-1 of the item's 64*NT
+ * rows; all four walk the item's 32-key slabs together.
+ *
+ * Staging: every thread loads its 1/256 share of a slab (16-byte chunks) into
+ * registers two slabs ahead, and stores one slab per step into one of two
+ * LDS stages (bf16 cache slabs are widened to fp16 on the way, once per
+ * workgroup rather than once per wave). One barrier per slab both publishes
+ * the next stage and frees the previous one.
+ *
+ * LDS image, XOR-swizzled so that each ds_read_b128 of an MFMA fragment and
+ * each staging store touches every bank group once:
+ *   K   : 32 key rows of KROW bytes; 16-byte chunk cb of key row r sits in
+ *         slot cb ^ f(r), f(r) = (r & 3) | ((r >> 3) & 3) << 2. The A-operand
+ *         rows of lane c are r = 8(c>>2) + (c&3) + 4t, for which f(r) = c.
+ *   V^T : 16*DT rows of 64 bytes (32 keys); chunk j of row d sits in slot
+ *         j ^ ((d >> 2) & 3).
+ * Chunks of a K row past head_dim are zero (the stages are cleared once and
+ * those slots are never stored), so padded head dims contribute 0 * 0. V^T
+ * rows past head_dim only feed output rows that are never written.
+ *
+ * Softmax, lazy rescale and MFMA layouts as in k_attn_pf; no cross-wave
+ * combine is needed since each wave holds whole rows.
+ */
+template <int HD>
+struct FaGeom {
+    static constexpr int KS = (HD + 31) / 32;
+    static constexpr int DT = (HD + 15) / 16;
+    static constexpr int HDP = KS * 32;
+    static constexpr int KROW = HD <= 128 ? 256 : 512;
+    static constexpr int K_BYTES = SMOL_SLAB * KROW;
+    static constexpr int V_BYTES = 16 * DT * 64;
+    static constexpr int STAGE = K_BYTES + V_BYTES;
+    static constexpr int CK = SMOL_SLAB * HD / 8; /* 16-byte chunks in a K (or V^T) slab */
+    static constexpr int PER = (CK + 255) / 256;  /* K (and V) chunks per thread */
+};
+
+template <int HD, int NT, int W, int KG>
+__global__ __launch_bounds__(256 * KG) __attribute__((amdgpu_waves_per_eu(W, W))) void k_attn_fa(SkParams p) {
+    using Gm = FaGeom<HD>;
+    constexpr int KS = Gm::KS, DT = Gm::DT, HDP = Gm::HDP, KROW = Gm::KROW;
+    constexpr int STAGE = Gm::STAGE, K_BYTES = Gm::K_BYTES, CK = Gm::CK, PER = Gm::PER;
+    constexpr int ROWS = 4 * 16 * NT;
+    constexpr unsigned SLAB_BYTES = SMOL_SLAB * HD * 2;
+    constexpr int MERGE_BYTES = (2 * SK_MERGE_MAX + 128) * 4;
+    constexpr int OSTR = DT * 16 + 4;                      /* row stride of the key-group combine (floats) */
+    constexpr int COMB_BYTES = KG > 1 ? ROWS * OSTR * 4 : 0;
+    /* LDS stages: two for group 0 (and for KG = 1), four for group 1, which
+     * still reads step s-1's slab while step s+1's is stored */
+    constexpr int NSTAGES = KG > 1 ? 6 : 2;
+    constexpr int SMEM0 = NSTAGES * STAGE > MERGE_BYTES ? NSTAGES * STAGE : MERGE_BYTES;
+    constexpr int SMEM = SMEM0 > COMB_BYTES ? SMEM0 : COMB_BYTES;
+    constexpr int TPB = 256 * KG;
+    const int tid = threadIdx.x;
+    const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave_id >> 2;    /* key group: takes slabs grp, grp + KG, ... */
+    const int wave = wave_id & 3;    /* row wave within the group */
+    const int tg = tid & 255;        /* thread within the key group */
+    const int lane = tid & 63;
+    const int c = lane & 15, j = lane >> 4;
+    const int g = (int)(blockIdx.x % (unsigned)p.Hkv);
+    const int item = (int)(blockIdx.x / (unsigned)p.Hkv);
+    const SkItem it = p.items[item];
+    const SkBatch b = p.batches[it.batch];
+    const int G = p.G;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
+    __shared__ int s_last;
+    __shared__ float s_cm[KG > 1 ? ROWS : 1], s_cl[KG > 1 ? ROWS : 1];
+    unsigned char *gsm = smem + grp * 2 * STAGE; /* this key group's stages */
+
+    for (int e = tid; e < NSTAGES * STAGE / 16; e += TPB) reinterpret_cast<uint4 *>(smem)[e] = make_uint4(0, 0, 0, 0);
+
+    /* this wave's rows: Q fragments, visible key ranges */
+    h8 qf[NT][KS];
+    int lo[NT], hi[NT];
+    float m[NT], l[NT];
+    f4 o[NT][DT];
+    int lo_max = -(1 << 30), hi_min = 1 << 30, lo_min = 1 << 30, hi_max = -(1 << 30);
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int r = it.row0 + (wave * NT + nt) * 16 + c;
+        const bool valid = r < b.n_rows;
+        const int qi = r / G;
+        int rl = b.key_lo, rh = b.key_hi;
+        if (b.causal) {
+            rh = min(rh, b.q_pos0 + qi + 1);
+            if (p.window > 0) rl = max(rl, b.q_pos0 + qi - p.window + 1);
+        }
+        lo[nt] = valid ? rl : -(1 << 30);
+        hi[nt] = valid ? rh : (1 << 30);
+        lo_max = max(lo_max, lo[nt]);
+        hi_min = min(hi_min, hi[nt]);
+        if (valid) {
+            lo_min = min(lo_min, rl);
+            hi_max = max(hi_max, rh);
+        }
+        m[nt] = -INFINITY;
+        l[nt] = 0.0f;
+        const _Float16 *qrow = p.qs + (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid ? r : 0)) * HDP;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) qf[nt][ks] = valid ? load_h8(qrow + 32 * ks + 8 * j) : zero_h8();
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) o[nt][dt] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int sh = 1; sh < 64; sh <<= 1) {
+        lo_max = max(lo_max, __shfl_xor(lo_max, sh));
+        hi_min = min(hi_min, __shfl_xor(hi_min, sh));
+        lo_min = min(lo_min, __shfl_xor(lo_min, sh));
+        hi_max = max(hi_max, __shfl_xor(hi_max, sh));
+    }
+    lo_max = __builtin_amdgcn_readfirstlane(lo_max);
+    hi_min = __builtin_amdgcn_readfirstlane(hi_min);
+    lo_min = __builtin_amdgcn_readfirstlane(lo_min);
+    hi_max = __builtin_amdgcn_readfirstlane(hi_max);
+
+    /* sources: cache region of (slot, head) and fresh region of head */
+    rsrc_t rk_c = make_rsrc(nullptr, 0), rv_c = make_rsrc(nullptr, 0);
+    if (b.slot >= 0 && p.kc != nullptr) {
+        const long long cb = (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * HD;
+        rk_c = make_rsrc(p.kc + cb, (long long)p.cap * HD * 2);
+        rv_c = make_rsrc(p.vtc + cb, (long long)p.cap * HD * 2);
+    }
+    const rsrc_t rk_f = make_rsrc(p.kf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
+    const rsrc_t rv_f = make_rsrc(p.vtf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
+
+    /* this thread's staging chunks: global byte offset within the slab and LDS slot */
+    unsigned g_off[PER], lk_off[PER], lv_off[PER];
+    bool c_ok[PER];
+#pragma unroll
+    for (int e = 0; e < PER; e++) {
+        const int q = tg + 256 * e;
+        c_ok[e] = (CK % 256 == 0) || q < CK;
+        const int kr = q / (HD / 8), cb = q - kr * (HD / 8);
+        const int f = (kr & 3) | (((kr >> 3) & 3) << 2);
+        lk_off[e] = (unsigned)(kr * KROW + 16 * (cb ^ f));
+        const int d = q >> 2, jj = q & 3;
+        lv_off[e] = (unsigned)(K_BYTES + d * 64 + 16 * (jj ^ ((d >> 2) & 3)));
+        g_off[e] = c_ok[e] ? (unsigned)(q * 16) : OOB_OFF;
+    }
+    /* this lane's fragment addresses within a stage */
+    const int kt_row = 8 * (c >> 2) + (c & 3);
+    unsigned kfo[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) kfo[ks] = (unsigned)(kt_row * KROW + 16 * ((4 * ks + j) ^ c));
+    const unsigned vfo = (unsigned)(K_BYTES + c * 64 + 16 * (j ^ (c >> 2)));
+
+    struct Stg {
+        uint4 k[PER], v[PER];
+        bool bf; /* bf16 cache slab (widen to fp16 when storing) */
+    };
+    auto issue = [&](int k0, Stg &s) __attribute__((always_inline)) {
+        const bool fr = k0 >= b.fresh_pos0;
+        const int kr = fr ? b.fresh_row0 + (k0 - b.fresh_pos0) : k0;
+        const unsigned so = (unsigned)(kr / SMOL_SLAB) * SLAB_BYTES;
+        const rsrc_t rk = fr ? rk_f : rk_c, rv = fr ? rv_f : rv_c;
+#pragma unroll
+        for (int e = 0; e < PER; e++) s.k[e] = bload(rk, g_off[e], so);
+#pragma unroll
+        for (int e = 0; e < PER; e++) s.v[e] = bload(rv, g_off[e], so);
+        s.bf = !fr;
+    };
+    auto store = [&](const Stg &s, int stage) __attribute__((always_inline)) {
+        unsigned char *base = gsm + stage * STAGE;
+#pragma unroll
+        for (int e = 0; e < PER; e++) {
+            if (!c_ok[e]) continue;
+            uint4 kw = s.k[e], vw = s.v[e];
+            if (s.bf) {
+                const h8 kh = bf16x8_to_h8(kw), vh = bf16x8_to_h8(vw);
+                kw = *reinterpret_cast<const uint4 *>(&kh);
+                vw = *reinterpret_cast<const uint4 *>(&vh);
+            }
+            *reinterpret_cast<uint4 *>(base + lk_off[e]) = kw;
+            *reinterpret_cast<uint4 *>(base + lv_off[e]) = vw;
+        }
+    };
+    auto lds_h8 = [&](int stage, unsigned off) __attribute__((always_inline)) -> h8 {
+        const uint4 w = *reinterpret_cast<const uint4 *>(gsm + stage * STAGE + off);
+        return *reinterpret_cast<const h8 *>(&w);
+    };
+
+    /* A slab is two phases: qk forms S^T = K.Q^T; smpv masks / caps it, runs
+     * the online softmax (lazy rescale) and adds V^T.P^T into O^T. */
+    auto seen = [&](int k0) __attribute__((always_inline)) { return k0 < hi_max && k0 + SMOL_SLAB > lo_min; }; /* some row of the wave sees the slab */
+    auto qk = [&](int k0, int stage, f4 (&sacc)[NT][2]) __attribute__((always_inline)) {
+        if (!seen(k0)) return;
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            h8 kfr[KS];
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) kfr[ks] = lds_h8(stage, kfo[ks] + t * 4 * KROW);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kfr[ks], qf[nt][ks], acc, 0, 0, 0);
+                sacc[nt][t] = acc;
+            }
+        }
+    };
+    auto smpv = [&](int k0, int stage, const f4 (&sacc)[NT][2]) __attribute__((always_inline)) {
+        if (!seen(k0)) return;
+        const bool full = k0 >= lo_max && k0 + SMOL_SLAB <= hi_min;
+        h8 pf[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            float sv[8];
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) sv[4 * t + i] = sacc[nt][t][i];
+            if (p.cap2 > 0.0f) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) sv[e] = p.cap2 * tanhf(sv[e] / p.cap2);
+            }
+            if (!full) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int key = k0 + 8 * j + e;
+                    sv[e] = (key >= lo[nt] && key < hi[nt]) ? sv[e] : -INFINITY;
+                }
+            }
+            float mx = sv[0];
+#pragma unroll
+            for (int e = 1; e < 8; e++) mx = fmaxf(mx, sv[e]);
+            mx = row_max4(mx);
+            const bool need = mx > m[nt] + LAZY_T;
+            if (__any(need)) {
+                const float m_new = need ? mx : m[nt];
+                const float alpha = need ? __builtin_amdgcn_exp2f(m[nt] - m_new) : 1.0f;
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) o[nt][dt] *= alpha;
+                l[nt] *= alpha;
+                m[nt] = m_new;
+            }
+            const float m_use = m[nt] == -INFINITY ? 0.0f : m[nt];
+            float ps = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float pe = __builtin_amdgcn_exp2f(sv[e] - m_use);
+                ps += pe;
+                pf[nt][e] = (_Float16)pe;
+            }
+            l[nt] += ps;
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            const h8 vfr = lds_h8(stage, vfo + dt * 1024);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+                o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vfr, pf[nt], o[nt][dt], 0, 0, 0);
+        }
+    };
+
+    /* The item's n slabs are walked in a rotated order (slab index
+     * (i + rot) mod n; the softmax does not depend on the order), so the
+     * workgroups of one head, which start together, read different slabs.
+     * Key group grp takes indices grp, grp + KG, ... : its step s covers index
+     * KG*s + grp. Stage s % 2 (group 0) or s % 4 (group 1) holds step s's
+     * slab; SETS register sets hold steps s+1 .. s+SETS in flight (the set of
+     * step s+1 is stored to its stage during step s and refilled with step
+     * s+1+SETS). Every load and
+     * store is issued unconditionally (clamped to the last slab), so the
+     * waits are the same on every path; one barrier per step serves both
+     * groups.
+     * Group 1 runs half a slab behind group 0: in step s it finishes slab
+     * s-1 (softmax, P.V) and then forms S for slab s, while group 0 does
+     * slab s whole. The two waves sharing a SIMD are then in different
+     * phases (one on MFMA, the other on VALU) instead of in lockstep. */
+    const int kb = it.key_begin, ke = it.key_end;
+    __syncthreads(); /* stages cleared */
+    if (ke > kb) {
+        const int n = (ke - kb + SMOL_SLAB - 1) / SMOL_SLAB;
+        const int ns = (n + KG - 1) / KG;
+        const int rot = (int)(((unsigned)item * 7u + (unsigned)g * 3u) % (unsigned)n);
+        auto slab_k = [&](int s) __attribute__((always_inline)) {
+            const int idx = KG * s + grp;
+            int r = (idx < n ? idx : n - 1) + rot;
+            r = r >= n ? r - n : r;
+            return kb + SMOL_SLAB * r;
+        };
+        auto valid = [&](int s) __attribute__((always_inline)) { return s >= 0 && KG * s + grp < n; };
+        /* register sets of staged slabs in flight: four with one wave per
+         * SIMD, two with two (the other wave hides the latency) */
+        constexpr int SETS = KG > 1 ? 2 : 4;
+        Stg st[SETS];
+        f4 sacc[NT][2];
+#pragma unroll
+        for (int q = 0; q < SETS; q++) issue(slab_k(q), st[q]);
+        store(st[0], 0);
+        issue(slab_k(SETS), st[0]);
+        __syncthreads();
+        /* u = i % 4 (compile-time in each unrolled step) */
+        auto step = [&](int i, auto u_tag) __attribute__((always_inline)) {
+            constexpr int u = decltype(u_tag)::value;
+            Stg &nxt = st[(u + 1) % SETS];
+            if (KG == 1 || grp == 0) {
+                if (valid(i)) {
+                    qk(slab_k(i), u & 1, sacc);
+                    smpv(slab_k(i), u & 1, sacc);
+                }
+                store(nxt, (u + 1) & 1);
+            } else {
+                if (valid(i - 1)) smpv(slab_k(i - 1), (u + 3) & 3, sacc);
+                if (valid(i)) qk(slab_k(i), u, sacc);
+                store(nxt, (u + 1) & 3);
+            }
+            issue(slab_k(i + 1 + SETS), nxt);
+            __syncthreads();
+            return i + 1 >= ns;
+        };
+        int i = 0;
+        for (;; i += 4) {
+            if (step(i, std::integral_constant<int, 0>{})) break;
+            if (step(i + 1, std::integral_constant<int, 1>{})) { i += 1; break; }
+            if (step(i + 2, std::integral_constant<int, 2>{})) { i += 2; break; }
+            if (step(i + 3, std::integral_constant<int, 3>{})) { i += 3; break; }
+        }
+        if (KG > 1 && grp == 1 && valid(i)) smpv(slab_k(i), i & 3, sacc);
+        if (KG > 1) __syncthreads(); /* the combine below reuses the stages */
+    }
+
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) l[nt] = row_sum4(l[nt]);
+    if constexpr (KG > 1) {
+        /* key group 1 hands (m, l, O) of its rows to group 0 through LDS (the
+         * stages are free after the barrier that closed the loop) */
+        float *cb = reinterpret_cast<float *>(smem);
+        if (grp == 1) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const int rr = (wave * NT + nt) * 16 + c;
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) *reinterpret_cast<f4 *>(cb + rr * OSTR + 16 * dt + 4 * j) = o[nt][dt];
+                if (j == 0) { s_cm[rr] = m[nt]; s_cl[rr] = l[nt]; }
+            }
+        }
+        __syncthreads();
+        if (grp == 0) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const int rr = (wave * NT + nt) * 16 + c;
+                const float m1 = s_cm[rr], l1 = s_cl[rr];
+                const float M = fmaxf(m[nt], m1);
+                const float Mu = M == -INFINITY ? 0.0f : M;
+                const float a0 = __builtin_amdgcn_exp2f(m[nt] - Mu), a1 = __builtin_amdgcn_exp2f(m1 - Mu);
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++)
+                    o[nt][dt] = o[nt][dt] * a0 + a1 * *reinterpret_cast<const f4 *>(cb + rr * OSTR + 16 * dt + 4 * j);
+                l[nt] = l[nt] * a0 + l1 * a1;
+                m[nt] = M;
+            }
+        }
+    }
+
+    /* epilogue: group 0's rows are complete over the item's keys */
+    if (it.n_split == 1) {
+        if (grp != 0) return;
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int r = it.row0 + (wave * NT + nt) * 16 + c;
+            if (r >= b.n_rows) continue;
+            const int qi = r / G, hg = r - qi * G;
+            float *orow = p.out + ((long long)(b.out_tok0 + qi) * p.Hq + (g * G + hg)) * HD;
+            const float inv = l[nt] > 0.0f ? 1.0f / l[nt] : 0.0f;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                const int d = 16 * dt + 4 * j;
+                if (HD % 16 != 0 && d >= HD) continue;
+                *reinterpret_cast<f4 *>(orow + d) = o[nt][dt] * inv;
+            }
+        }
+        return;
+    }
+    /* split item: publish this wave's rows with device-coherent stores, then
+     * the workgroup counts in once; the group's last workgroup merges */
+    const long long pbase = ((long long)item * p.Hkv + g) * ROWS;
+    if (grp == 0) {
+        const rsrc_t ro = make_rsrc(p.part_o + pbase * HD, (long long)ROWS * HD * 4);
+        const rsrc_t rml = make_rsrc(p.part_ml + pbase * 2, (long long)ROWS * 2 * 4);
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int rr = (wave * NT + nt) * 16 + c;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                const int d = 16 * dt + 4 * j;
+                if (HD % 16 != 0 && d >= HD) continue;
+                store_f4_sc1(ro, (unsigned)((rr * HD + d) * 4), o[nt][dt]);
+            }
+            if (j == 0) store_f2_sc1(rml, (unsigned)(rr * 8), m[nt], l[nt]);
+        }
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads(); /* every wave's stores are acknowledged */
+    if (tid == 0) {
+        const int prev = __hip_atomic_fetch_add(p.counters + (long long)it.group * p.Hkv + g, 1, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == it.n_split - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    merge_group<HD, ROWS, TPB>(p, it, b, item, g, tid, reinterpret_cast<float *>(smem));
+}
+
 /* ------------------------------------------------------------ k_rope_apply */
 
 /* In-place RoPE on x [seq][H][hd] fp32, row s using table row pos[s] (or s
@@ -1141,6 +1581,45 @@ extern "C" int smol_launch_pf(const SkParams *sp, int hd, int n_items, int nt, i
     case 96: return launch_pf_hd<96>(sp, n_items, nt, w, st);
     case 128: return launch_pf_hd<128>(sp, n_items, nt, w, st);
     case 256: return launch_pf_hd<256>(sp, n_items, nt, w, st);
+    default: return -1;
+    }
+}
+
+template <int HD, int NT, int W, int KG>
+static void launch_fa_v(const SkParams *sp, dim3 grid, hipStream_t st) {
+    hipLaunchKernelGGL((k_attn_fa<HD, NT, W, KG>), grid, dim3(256 * KG), 0, st, *sp);
+}
+
+/* w: waves per SIMD the kernel is built for; kg: key groups (kg = 2 is two
+ * four-wave groups on alternate slabs, i.e. two waves per SIMD in one
+ * workgroup) */
+template <int HD>
+static int launch_fa_hd(const SkParams *sp, int n_items, int nt, int w, int kg, hipStream_t st) {
+    constexpr int NT2 = HD <= 128 ? 2 : 1;
+    const dim3 grid(n_items * sp->Hkv);
+    constexpr int KG2 = HD <= 128 ? 2 : 1;
+    if (kg == 2) {
+        if (HD > 128) return -1;
+        if (nt == 1) launch_fa_v<HD, 1, 2, KG2>(sp, grid, st);
+        else if (nt == 2) launch_fa_v<HD, NT2, 2, KG2>(sp, grid, st);
+        else return -1;
+    } else if (nt == 1 && w == 1) launch_fa_v<HD, 1, 1, 1>(sp, grid, st);
+    else if (nt == 1 && w == 2) launch_fa_v<HD, 1, 2, 1>(sp, grid, st);
+    else if (nt == 2 && w == 1 && HD <= 128) launch_fa_v<HD, NT2, 1, 1>(sp, grid, st);
+    else if (nt == 2 && w == 2 && HD <= 128) launch_fa_v<HD, NT2, 2, 1>(sp, grid, st);
+    else return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, int kg, hipStream_t st) {
+    if (n_items <= 0) return 0;
+    switch (hd) {
+    case 64: return launch_fa_hd<64>(sp, n_items, nt, w, kg, st);
+    case 72: return launch_fa_hd<72>(sp, n_items, nt, w, kg, st);
+    case 80: return launch_fa_hd<80>(sp, n_items, nt, w, kg, st);
+    case 96: return launch_fa_hd<96>(sp, n_items, nt, w, kg, st);
+    case 128: return launch_fa_hd<128>(sp, n_items, nt, w, kg, st);
+    case 256: return launch_fa_hd<256>(sp, n_items, nt, w, kg, st);
     default: return -1;
     }
 }

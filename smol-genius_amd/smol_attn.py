@@ -19,7 +19,8 @@ import weakref
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libsmol_attn.so")
+# SMOL_ATTN_LIB selects another build of the library (same C ABI)
+LIB_PATH = os.environ.get("SMOL_ATTN_LIB") or os.path.join(HERE, "libsmol_attn.so")
 
 F32, BF16 = 0, 1
 ROPE_NONE, ROPE_NEOX, ROPE_INTERLEAVED = -1, 0, 1
