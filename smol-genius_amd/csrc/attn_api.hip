@@ -28,7 +28,7 @@
 extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t st);
 extern "C" int smol_launch_pf(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
 extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
-extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, int kg, hipStream_t st);
+extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
 extern "C" int smol_launch_rope_apply(float *x, const float *cos_t, const float *sin_t,
                                       const int *pos, int seq, int n_heads, int hd, int kind,
                                       hipStream_t st);
@@ -113,6 +113,7 @@ struct smol_attn_ctx {
     PinnedSlot ring[SMOL_RING];
     int ring_next = 0;
     DevBuf desc;   /* device copy of the descriptor tables */
+    std::vector<unsigned char> desc_last; /* host bytes of the last upload to `desc` */
     DevBuf qs, kf, vtf, part_o, part_ml, counters;
     DevBuf qs32; /* fp32 Q scratch of the decode kernel */
     int cu_count = 256;
@@ -175,7 +176,12 @@ static int set_device(smol_attn_ctx *ctx) {
 }
 
 /* copy `bytes` of descriptor data to ctx->desc via the pinned ring */
+/* Copies the descriptor tables to the device, unless the device buffer already
+ * holds exactly these bytes (a decoder calls with the same shapes layer after
+ * layer; stream order keeps the buffer valid for every later kernel). */
 static int upload_desc(smol_attn_ctx *ctx, const void *host, size_t bytes) {
+    if (ctx->desc.p && bytes == ctx->desc_last.size() && memcmp(ctx->desc_last.data(), host, bytes) == 0) return 0;
+    ctx->desc_last.clear();
     int rc = dev_reserve(ctx->desc, bytes, ctx->stream);
     if (rc) return rc;
     PinnedSlot &s = ctx->ring[ctx->ring_next];
@@ -196,6 +202,7 @@ static int upload_desc(smol_attn_ctx *ctx, const void *host, size_t bytes) {
     HIP_TRY(hipMemcpyAsync(ctx->desc.p, s.h, bytes, hipMemcpyHostToDevice, ctx->stream));
     HIP_TRY(hipEventRecord(s.ev, ctx->stream));
     s.pending = true;
+    ctx->desc_last.assign((const unsigned char *)host, (const unsigned char *)host + bytes);
     return 0;
 }
 
@@ -584,15 +591,12 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
      * LDS) unless SMOL_ATTN_PREFILL_KERNEL=pf selects k_attn_pf */
     const char *pk = getenv("SMOL_ATTN_PREFILL_KERNEL");
     const bool fa = !cs.dec && !(pk && strcmp(pk, "pf") == 0);
-    int nt, w, rows_per, kg = 1;
+    int nt, w, rows_per;
     if (fa) {
         nt = (hd <= 128 && max_rows > 64) ? 2 : 1;
         if (const int ov = env_int("SMOL_ATTN_NT"))
             if (ov == 1 || (ov == 2 && hd <= 128)) nt = ov;
-        /* SMOL_ATTN_FA_KG=2: two key groups (8 waves, two per SIMD in one
-         * workgroup), up to head_dim 128 */
-        kg = (hd <= 128 && env_int("SMOL_ATTN_FA_KG") == 2) ? 2 : 1;
-        w = kg == 2 ? 2 : (hd > 128 || env_int("SMOL_ATTN_FA_WAVES") == 1 ? 1 : 2);
+        w = (hd > 128 || env_int("SMOL_ATTN_FA_WAVES") == 1) ? 1 : 2;
         rows_per = 64 * nt;
     } else {
         nt = cs.dec ? (max_rows <= 16 || hd > 128 ? 1 : 2) : choose_nt(hd, max_rows);
@@ -604,14 +608,20 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
         w = choose_waves(cs.dec, hd, nt);
         rows_per = 16 * nt;
     }
-    plan_items(pl, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * (kg == 2 ? 1 : w), fa);
+    plan_items(pl, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, fa);
+    /* SMOL_ATTN_FA_QDIRECT=1: k_attn_fa rotates and scales Q as it loads it
+     * and the pre-pass only handles the new K/V */
+    const bool q_direct = fa && env_int("SMOL_ATTN_FA_QDIRECT") == 1;
+    if (q_direct)
+        pl.pblk.erase(std::remove_if(pl.pblk.begin(), pl.pblk.end(), [](const PrepBlock &k) { return k.kind == 1; }),
+                      pl.pblk.end());
 
     /* workspace */
     int rc;
     const size_t fcap = (size_t)std::max(pl.fresh_rows, SMOL_SLAB);
     if (cs.dec) {
         if ((rc = dev_reserve(ctx->qs32, (size_t)cs.Hkv * std::max(pl.q_rows, 1) * hdp * 4, ctx->stream))) return rc;
-    } else {
+    } else if (!q_direct) {
         if ((rc = dev_reserve(ctx->qs, (size_t)cs.Hkv * std::max(pl.q_rows, 1) * hdp * 2, ctx->stream))) return rc;
     }
     if ((rc = dev_reserve(ctx->kf, (size_t)cs.Hkv * fcap * hd * 2, ctx->stream))) return rc;
@@ -691,9 +701,16 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     sp.part_o = (float *)ctx->part_o.p;
     sp.part_ml = (float *)ctx->part_ml.p;
     sp.counters = (int *)ctx->counters.p;
+    if (q_direct) {
+        sp.q_direct = 1;
+        sp.q_in = cs.q; sp.q_dtype = cs.dtype; sp.q_stride = cs.q_stride;
+        sp.rope_cos = pp.rope_cos; sp.rope_sin = pp.rope_sin;
+        sp.rope_q_kind = cs.rope_q ? pp.rope_kind : SMOL_ROPE_OFF;
+        sp.qscale = pp.qscale;
+    }
     mk = timing_begin(ctx, 1);
     rc = cs.dec ? smol_launch_dec(&sp, hd, (int)n_items, nt, w, ctx->stream)
-         : fa   ? smol_launch_fa(&sp, hd, (int)n_items, nt, w, kg, ctx->stream)
+         : fa   ? smol_launch_fa(&sp, hd, (int)n_items, nt, w, ctx->stream)
                 : smol_launch_pf(&sp, hd, (int)n_items, nt, w, ctx->stream);
     timing_end(ctx, mk);
     if (rc)
@@ -703,7 +720,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
 }
 
 static void add_q_blocks(Plan &pl, int batch, int n_q) {
-    const int per = 8;
+    const int per = 32; /* tokens per pre-pass block */
     for (int t = 0; t < n_q; t += per) pl.pblk.push_back({batch, 1, t, std::min(per, n_q - t)});
 }
 

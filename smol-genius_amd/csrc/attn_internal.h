@@ -82,6 +82,12 @@ typedef struct {
     float *part_o;             /* [item][kv][rows][hd] unnormalised partial outputs */
     float *part_ml;            /* [item][kv][rows][2] (max, sum) */
     int *counters;             /* [group][kv]; zero between calls */
+    /* k_attn_fa reads Q itself (q_direct = 1): input row out_tok0 + i of a
+     * batch, rotated at table row q_pos0 + i and scaled by qscale */
+    int q_direct;
+    const void *q_in; int q_dtype; long long q_stride;
+    const float *rope_cos; const float *rope_sin; int rope_q_kind;
+    float qscale;
 } SkParams;
 
 /* Pre-pass: rotates/scales Q into the Q scratch, appends rotated K and V to

@@ -80,23 +80,6 @@ __device__ __forceinline__ float load_in(const void *base, int dtype, long long 
                                  : ((const float *)base)[idx];
 }
 
-/* Rotated value of element d of a head vector x (fp32), position row of the
- * table. NeoX pairs (d, d + half); interleaved pairs (2i, 2i + 1). The
- * arithmetic is rope.c:99-164 (fmsub / fmadd) and rope.c:68-93. */
-__device__ __forceinline__ float rope_elem(float xd, float xp, int d, int hd, int kind,
-                                           const float *c, const float *s) {
-    if (kind == SMOL_ROPE_NEOX_K) {
-        int half = hd >> 1;
-        if (d < half) return fmaf(xd, c[d], -(xp * s[d]));      /* x1 c - x2 s */
-        return fmaf(xd, c[d], xp * s[d]);                       /* x2 c + x1 s */
-    }
-    if (kind == SMOL_ROPE_INTERLEAVED_K) {
-        if ((d & 1) == 0) return xd * c[d] - xp * s[d];          /* x0 c - x1 s */
-        return xd * c[d] + xp * s[d];                            /* x1 c + x0 s */
-    }
-    return xd;
-}
-
 __device__ __forceinline__ int rope_partner(int d, int hd, int kind) {
     if (kind == SMOL_ROPE_NEOX_K) { int half = hd >> 1; return d < half ? d + half : d - half; }
     if (kind == SMOL_ROPE_INTERLEAVED_K) return d ^ 1;
@@ -146,6 +129,12 @@ __device__ __forceinline__ void unpack_bf16x8(uint4 w, float *v) {
     }
 }
 
+/* 8 consecutive fp32 table entries (16-byte aligned: d0 % 8 == 0) */
+__device__ __forceinline__ void tab8(const float *t, float *v) {
+    const float4 a = *reinterpret_cast<const float4 *>(t), b = *reinterpret_cast<const float4 *>(t + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
 /* Rotates the 8 elements [d0, d0+8) of a head vector whose row starts at
  * `base + row` (fp32 or bf16 input), position `pos` of the table. */
 __device__ __forceinline__ void rope8(const void *base, int dtype, long long row, int d0, int hd, int kind,
@@ -153,31 +142,32 @@ __device__ __forceinline__ void rope8(const void *base, int dtype, long long row
     load8(base, dtype, row + d0, out);
     if (kind == SMOL_ROPE_OFF) return;
     const float *c = cos_t + pos * hd, *s = sin_t + pos * hd;
+    float cv[8], sv[8];
+    tab8(c + d0, cv);
+    tab8(s + d0, sv);
     if (kind == SMOL_ROPE_INTERLEAVED_K) {
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
             const float x0 = out[i], x1 = out[i + 1];
-            out[i] = x0 * c[d0 + i] - x1 * s[d0 + i];
-            out[i + 1] = x1 * c[d0 + i + 1] + x0 * s[d0 + i + 1];
+            out[i] = x0 * cv[i] - x1 * sv[i];
+            out[i + 1] = x1 * cv[i + 1] + x0 * sv[i + 1];
         }
         return;
     }
     const int half = hd >> 1;
+    float pr[8];
     if ((half & 7) == 0) {
-        float pr[8];
-        const int pd0 = d0 < half ? d0 + half : d0 - half;
-        load8(base, dtype, row + pd0, pr);
-#pragma unroll
-        for (int i = 0; i < 8; i++) out[i] = rope_elem(out[i], pr[i], d0 + i, hd, kind, c, s);
+        load8(base, dtype, row + (d0 < half ? d0 + half : d0 - half), pr);
     } else {
         /* half not a multiple of 8 (head_dim 72): partners element by element */
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int d = d0 + i;
-            const float xp = load_in(base, dtype, row + rope_partner(d, hd, kind));
-            out[i] = rope_elem(out[i], xp, d, hd, kind, c, s);
-        }
+        for (int i = 0; i < 8; i++) pr[i] = load_in(base, dtype, row + rope_partner(d0 + i, hd, kind));
     }
+    /* NeoX: x1 c - x2 s for the first half, x2 c + x1 s for the second
+     * (rope.c:99-164, fmsub / fmadd) */
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        out[i] = d0 + i < half ? fmaf(out[i], cv[i], -(pr[i] * sv[i])) : fmaf(out[i], cv[i], pr[i] * sv[i]);
 }
 
 /* grid (n_blocks, Hkv), 256 threads. A fresh-slab block covers 32 positions
@@ -201,23 +191,38 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
         const int cpp = hdp >> 3;
         const int per_tok = G * cpp;
         const int rk = (p.rope_q && p.rope_kind != SMOL_ROPE_OFF) ? p.rope_kind : SMOL_ROPE_OFF;
-        for (int e = tid; e < blk.count * per_tok; e += blockDim.x) {
-            const int tl = e / per_tok, rem = e - tl * per_tok;
-            const int hg = rem / cpp, d0 = (rem - hg * cpp) * 8;
-            const int t = blk.first + tl;
-            float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (d0 < hd) {
-                const long long row = (long long)(b.q_tok0 + t) * p.q_stride + (long long)(g * G + hg) * hd;
-                rope8(p.q, p.q_dtype, row, d0, hd, rk, p.rope_cos, p.rope_sin, b.q_pos0 + t, v);
+        /* four 8-element chunks per thread per pass, all loads issued before
+         * any store */
+        const int total = blk.count * per_tok;
+        for (int e0 = tid; e0 < total; e0 += 4 * 256) {
+            float v[4][8];
+            long long qi[4];
 #pragma unroll
-                for (int i = 0; i < 8; i++) v[i] *= p.qscale;
+            for (int u = 0; u < 4; u++) {
+                const int e = e0 + 256 * u;
+                const int ee = e < total ? e : total - 1;
+                const int tl = ee / per_tok, rem = ee - tl * per_tok;
+                const int hg = rem / cpp, d0 = (rem - hg * cpp) * 8;
+                const int t = blk.first + tl;
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[u][i] = 0.0f;
+                if (d0 < hd) {
+                    const long long row = (long long)(b.q_tok0 + t) * p.q_stride + (long long)(g * G + hg) * hd;
+                    rope8(p.q, p.q_dtype, row, d0, hd, rk, p.rope_cos, p.rope_sin, b.q_pos0 + t, v[u]);
+                }
+                qi[u] = e < total ? (long long)g * p.qs_head_stride + (long long)(b.q_row0 + t * G + hg) * hdp + d0 : -1;
             }
-            const long long qi = (long long)g * p.qs_head_stride + (long long)(b.q_row0 + t * G + hg) * hdp + d0;
-            if (p.stage == SMOL_STAGE_QF32) {
-                *reinterpret_cast<float4 *>(p.qs32 + qi) = make_float4(v[0], v[1], v[2], v[3]);
-                *reinterpret_cast<float4 *>(p.qs32 + qi + 4) = make_float4(v[4], v[5], v[6], v[7]);
-            } else {
-                *reinterpret_cast<uint4 *>(p.qs + qi) = pack_h8(v);
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (qi[u] < 0) continue;
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[u][i] *= p.qscale;
+                if (p.stage == SMOL_STAGE_QF32) {
+                    *reinterpret_cast<float4 *>(p.qs32 + qi[u]) = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
+                    *reinterpret_cast<float4 *>(p.qs32 + qi[u] + 4) = make_float4(v[u][4], v[u][5], v[u][6], v[u][7]);
+                } else {
+                    *reinterpret_cast<uint4 *>(p.qs + qi[u]) = pack_h8(v[u]);
+                }
             }
         }
         return;
@@ -1065,11 +1070,15 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
  * through LDS. Wave w owns row tiles w*NT .. w*NT+NT-1 of the item's 64*NT
  * rows; all four walk the item's 32-key slabs together.
  *
- * Staging: every thread loads its 1/256 share of a slab (16-byte chunks) into
- * registers two slabs ahead, and stores one slab per step into one of two
- * LDS stages (bf16 cache slabs are widened to fp16 on the way, once per
- * workgroup rather than once per wave). One barrier per slab both publishes
- * the next stage and frees the previous one.
+ * Staging: every thread loads its 1/256 share of a slab (16-byte chunks)
+ * into registers a few slabs ahead and stores one slab per step into a ring
+ * of four LDS stages (bf16 cache slabs are widened to fp16 on the way, once
+ * per workgroup rather than once per wave). One barrier per slab both
+ * publishes the next stage and frees the oldest.
+ *
+ * Per wave the slabs are software-pipelined: S^T = K.Q^T of slab i+1 is
+ * formed on the matrix cores while the vector ALU computes the
+ * exponentials of slab i.
  *
  * LDS image, XOR-swizzled so that each ds_read_b128 of an MFMA fragment and
  * each staging store touches every bank group once:
@@ -1082,8 +1091,8 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
  * those slots are never stored), so padded head dims contribute 0 * 0. V^T
  * rows past head_dim only feed output rows that are never written.
  *
- * Softmax, lazy rescale and MFMA layouts as in k_attn_pf; no cross-wave
- * combine is needed since each wave holds whole rows.
+ * Softmax, lazy rescale and MFMA layouts as in k_attn_pf; each wave holds
+ * whole rows, so no cross-wave combine is needed.
  */
 template <int HD>
 struct FaGeom {
@@ -1098,27 +1107,19 @@ struct FaGeom {
     static constexpr int PER = (CK + 255) / 256;  /* K (and V) chunks per thread */
 };
 
-template <int HD, int NT, int W, int KG>
-__global__ __launch_bounds__(256 * KG) __attribute__((amdgpu_waves_per_eu(W, W))) void k_attn_fa(SkParams p) {
+template <int HD, int NT, int W>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) void k_attn_fa(SkParams p) {
     using Gm = FaGeom<HD>;
     constexpr int KS = Gm::KS, DT = Gm::DT, HDP = Gm::HDP, KROW = Gm::KROW;
     constexpr int STAGE = Gm::STAGE, K_BYTES = Gm::K_BYTES, CK = Gm::CK, PER = Gm::PER;
     constexpr int ROWS = 4 * 16 * NT;
     constexpr unsigned SLAB_BYTES = SMOL_SLAB * HD * 2;
+    constexpr int NSTG = 4;                /* LDS stages: slabs i, i+1 read while i+2 is stored */
+    constexpr int SETS = W == 1 ? 4 : 2;   /* register sets of staged slabs in flight */
     constexpr int MERGE_BYTES = (2 * SK_MERGE_MAX + 128) * 4;
-    constexpr int OSTR = DT * 16 + 4;                      /* row stride of the key-group combine (floats) */
-    constexpr int COMB_BYTES = KG > 1 ? ROWS * OSTR * 4 : 0;
-    /* LDS stages: two for group 0 (and for KG = 1), four for group 1, which
-     * still reads step s-1's slab while step s+1's is stored */
-    constexpr int NSTAGES = KG > 1 ? 6 : 2;
-    constexpr int SMEM0 = NSTAGES * STAGE > MERGE_BYTES ? NSTAGES * STAGE : MERGE_BYTES;
-    constexpr int SMEM = SMEM0 > COMB_BYTES ? SMEM0 : COMB_BYTES;
-    constexpr int TPB = 256 * KG;
+    constexpr int SMEM = NSTG * STAGE > MERGE_BYTES ? NSTG * STAGE : MERGE_BYTES;
     const int tid = threadIdx.x;
-    const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int grp = wave_id >> 2;    /* key group: takes slabs grp, grp + KG, ... */
-    const int wave = wave_id & 3;    /* row wave within the group */
-    const int tg = tid & 255;        /* thread within the key group */
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
     const int c = lane & 15, j = lane >> 4;
     const int g = (int)(blockIdx.x % (unsigned)p.Hkv);
@@ -1128,17 +1129,15 @@ __global__ __launch_bounds__(256 * KG) __attribute__((amdgpu_waves_per_eu(W, W))
     const int G = p.G;
     __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
     __shared__ int s_last;
-    __shared__ float s_cm[KG > 1 ? ROWS : 1], s_cl[KG > 1 ? ROWS : 1];
-    unsigned char *gsm = smem + grp * 2 * STAGE; /* this key group's stages */
 
-    for (int e = tid; e < NSTAGES * STAGE / 16; e += TPB) reinterpret_cast<uint4 *>(smem)[e] = make_uint4(0, 0, 0, 0);
+    for (int e = tid; e < NSTG * STAGE / 16; e += 256) reinterpret_cast<uint4 *>(smem)[e] = make_uint4(0, 0, 0, 0);
 
     /* this wave's rows: Q fragments, visible key ranges */
     h8 qf[NT][KS];
     int lo[NT], hi[NT];
     float m[NT], l[NT];
     f4 o[NT][DT];
-    int lo_max = -(1 << 30), hi_min = 1 << 30, lo_min = 1 << 30, hi_max = -(1 << 30);
+    int lo_max = -(1 << 30), hi_min = 1 << 30;
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         const int r = it.row0 + (wave * NT + nt) * 16 + c;
@@ -1153,15 +1152,30 @@ __global__ __launch_bounds__(256 * KG) __attribute__((amdgpu_waves_per_eu(W, W))
         hi[nt] = valid ? rh : (1 << 30);
         lo_max = max(lo_max, lo[nt]);
         hi_min = min(hi_min, hi[nt]);
-        if (valid) {
-            lo_min = min(lo_min, rl);
-            hi_max = max(hi_max, rh);
-        }
         m[nt] = -INFINITY;
         l[nt] = 0.0f;
-        const _Float16 *qrow = p.qs + (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid ? r : 0)) * HDP;
+        if (p.q_direct) {
+            /* rotate and scale Q here: row r is query qi of head g*G + hg */
+            const int hg = r - qi * G;
+            const long long row = (long long)(b.out_tok0 + (valid ? qi : 0)) * p.q_stride + (long long)(g * G + hg) * HD;
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) qf[nt][ks] = valid ? load_h8(qrow + 32 * ks + 8 * j) : zero_h8();
+            for (int ks = 0; ks < KS; ks++) {
+                const int d0 = 32 * ks + 8 * j;
+                float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                if (valid && (HD % 32 == 0 || d0 < HD)) {
+                    rope8(p.q_in, p.q_dtype, row, d0, HD, p.rope_q_kind, p.rope_cos, p.rope_sin, b.q_pos0 + qi, v);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) v[i] *= p.qscale;
+                }
+#pragma unroll
+                for (int i = 0; i < 8; i++) qf[nt][ks][i] = (_Float16)v[i];
+            }
+        } else {
+            const _Float16 *qrow =
+                p.qs + (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid ? r : 0)) * HDP;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) qf[nt][ks] = valid ? load_h8(qrow + 32 * ks + 8 * j) : zero_h8();
+        }
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) o[nt][dt] = f4{0.f, 0.f, 0.f, 0.f};
     }
@@ -1169,13 +1183,9 @@ __global__ __launch_bounds__(256 * KG) __attribute__((amdgpu_waves_per_eu(W, W))
     for (int sh = 1; sh < 64; sh <<= 1) {
         lo_max = max(lo_max, __shfl_xor(lo_max, sh));
         hi_min = min(hi_min, __shfl_xor(hi_min, sh));
-        lo_min = min(lo_min, __shfl_xor(lo_min, sh));
-        hi_max = max(hi_max, __shfl_xor(hi_max, sh));
     }
     lo_max = __builtin_amdgcn_readfirstlane(lo_max);
     hi_min = __builtin_amdgcn_readfirstlane(hi_min);
-    lo_min = __builtin_amdgcn_readfirstlane(lo_min);
-    hi_max = __builtin_amdgcn_readfirstlane(hi_max);
 
     /* sources: cache region of (slot, head) and fresh region of head */
     rsrc_t rk_c = make_rsrc(nullptr, 0), rv_c = make_rsrc(nullptr, 0);
@@ -1192,7 +1202,7 @@ __global__ __launch_bounds__(256 * KG) __attribute__((amdgpu_waves_per_eu(W, W))
     bool c_ok[PER];
 #pragma unroll
     for (int e = 0; e < PER; e++) {
-        const int q = tg + 256 * e;
+        const int q = tid + 256 * e;
         c_ok[e] = (CK % 256 == 0) || q < CK;
         const int kr = q / (HD / 8), cb = q - kr * (HD / 8);
         const int f = (kr & 3) | (((kr >> 3) & 3) << 2);
@@ -1224,7 +1234,7 @@ __global__ __launch_bounds__(256 * KG) __attribute__((amdgpu_waves_per_eu(W, W))
         s.bf = !fr;
     };
     auto store = [&](const Stg &s, int stage) __attribute__((always_inline)) {
-        unsigned char *base = gsm + stage * STAGE;
+        unsigned char *base = smem + stage * STAGE;
 #pragma unroll
         for (int e = 0; e < PER; e++) {
             if (!c_ok[e]) continue;
@@ -1239,15 +1249,11 @@ __global__ __launch_bounds__(256 * KG) __attribute__((amdgpu_waves_per_eu(W, W))
         }
     };
     auto lds_h8 = [&](int stage, unsigned off) __attribute__((always_inline)) -> h8 {
-        const uint4 w = *reinterpret_cast<const uint4 *>(gsm + stage * STAGE + off);
+        const uint4 w = *reinterpret_cast<const uint4 *>(smem + stage * STAGE + off);
         return *reinterpret_cast<const h8 *>(&w);
     };
-
-    /* A slab is two phases: qk forms S^T = K.Q^T; smpv masks / caps it, runs
-     * the online softmax (lazy rescale) and adds V^T.P^T into O^T. */
-    auto seen = [&](int k0) __attribute__((always_inline)) { return k0 < hi_max && k0 + SMOL_SLAB > lo_min; }; /* some row of the wave sees the slab */
-    auto qk = [&](int k0, int stage, f4 (&sacc)[NT][2]) __attribute__((always_inline)) {
-        if (!seen(k0)) return;
+    /* S^T = K.Q^T of the slab in `stage` */
+    auto qk = [&](int stage, f4 (&sacc)[NT][2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             h8 kfr[KS];
@@ -1263,32 +1269,30 @@ __global__ __launch_bounds__(256 * KG) __attribute__((amdgpu_waves_per_eu(W, W))
             }
         }
     };
-    auto smpv = [&](int k0, int stage, const f4 (&sacc)[NT][2]) __attribute__((always_inline)) {
-        if (!seen(k0)) return;
+    /* softmax front: scores of slab k0 with softcap / mask applied, rows'
+     * running max (lazy rescale of O and l), returned relative to the row
+     * reference */
+    auto front = [&](int k0, const f4 (&sacc)[NT][2], float (&sv)[NT][8]) __attribute__((always_inline)) {
         const bool full = k0 >= lo_max && k0 + SMOL_SLAB <= hi_min;
-        h8 pf[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
-            float sv[8];
 #pragma unroll
             for (int t = 0; t < 2; t++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) sv[4 * t + i] = sacc[nt][t][i];
+                for (int i = 0; i < 4; i++) sv[nt][4 * t + i] = sacc[nt][t][i];
             if (p.cap2 > 0.0f) {
 #pragma unroll
-                for (int e = 0; e < 8; e++) sv[e] = p.cap2 * tanhf(sv[e] / p.cap2);
+                for (int e = 0; e < 8; e++) sv[nt][e] = p.cap2 * tanhf(sv[nt][e] / p.cap2);
             }
             if (!full) {
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
                     const int key = k0 + 8 * j + e;
-                    sv[e] = (key >= lo[nt] && key < hi[nt]) ? sv[e] : -INFINITY;
+                    sv[nt][e] = (key >= lo[nt] && key < hi[nt]) ? sv[nt][e] : -INFINITY;
                 }
             }
-            float mx = sv[0];
-#pragma unroll
-            for (int e = 1; e < 8; e++) mx = fmaxf(mx, sv[e]);
-            mx = row_max4(mx);
+            const float mx = row_max4(fmaxf(fmaxf(fmaxf(sv[nt][0], sv[nt][1]), fmaxf(sv[nt][2], sv[nt][3])),
+                                            fmaxf(fmaxf(sv[nt][4], sv[nt][5]), fmaxf(sv[nt][6], sv[nt][7]))));
             const bool need = mx > m[nt] + LAZY_T;
             if (__any(need)) {
                 const float m_new = need ? mx : m[nt];
@@ -1299,15 +1303,24 @@ __global__ __launch_bounds__(256 * KG) __attribute__((amdgpu_waves_per_eu(W, W))
                 m[nt] = m_new;
             }
             const float m_use = m[nt] == -INFINITY ? 0.0f : m[nt];
-            float ps = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) sv[nt][e] -= m_use;
+        }
+    };
+    /* P = exp2(S - m) as fp16, row sums */
+    auto expo = [&](const float (&sv)[NT][8], h8 (&pf)[NT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            float pe[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                const float pe = __builtin_amdgcn_exp2f(sv[e] - m_use);
-                ps += pe;
-                pf[nt][e] = (_Float16)pe;
+                pe[e] = __builtin_amdgcn_exp2f(sv[nt][e]);
+                pf[nt][e] = (_Float16)pe[e];
             }
-            l[nt] += ps;
+            l[nt] += ((pe[0] + pe[1]) + (pe[2] + pe[3])) + ((pe[4] + pe[5]) + (pe[6] + pe[7]));
         }
+    };
+    auto pv = [&](int stage, const h8 (&pf)[NT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) {
             const h8 vfr = lds_h8(stage, vfo + dt * 1024);
@@ -1317,110 +1330,63 @@ __global__ __launch_bounds__(256 * KG) __attribute__((amdgpu_waves_per_eu(W, W))
         }
     };
 
-    /* The item's n slabs are walked in a rotated order (slab index
-     * (i + rot) mod n; the softmax does not depend on the order), so the
+    /* The item's n slabs are walked in a rotated order (slab (i + rot) mod n
+     * at step i; the softmax does not depend on the order), so the
      * workgroups of one head, which start together, read different slabs.
-     * Key group grp takes indices grp, grp + KG, ... : its step s covers index
-     * KG*s + grp. Stage s % 2 (group 0) or s % 4 (group 1) holds step s's
-     * slab; SETS register sets hold steps s+1 .. s+SETS in flight (the set of
-     * step s+1 is stored to its stage during step s and refilled with step
-     * s+1+SETS). Every load and
-     * store is issued unconditionally (clamped to the last slab), so the
-     * waits are the same on every path; one barrier per step serves both
-     * groups.
-     * Group 1 runs half a slab behind group 0: in step s it finishes slab
-     * s-1 (softmax, P.V) and then forms S for slab s, while group 0 does
-     * slab s whole. The two waves sharing a SIMD are then in different
-     * phases (one on MFMA, the other on VALU) instead of in lockstep. */
+     * Slab i sits in LDS stage i % 4 from the barrier that ends step i-2 to
+     * the one that ends step i. Step i: softmax front of slab i; then its
+     * exponentials alongside S of slab i+1 (MFMA and VALU work of the same
+     * wave with no dependence between them); then P.V of slab i; then slab
+     * i+2 is stored from its register set, which is refilled with slab
+     * i+2+SETS. Loads and stores are issued unconditionally (clamped to the
+     * last slab), so the waits are the same on every path. */
     const int kb = it.key_begin, ke = it.key_end;
     __syncthreads(); /* stages cleared */
     if (ke > kb) {
         const int n = (ke - kb + SMOL_SLAB - 1) / SMOL_SLAB;
-        const int ns = (n + KG - 1) / KG;
         const int rot = (int)(((unsigned)item * 7u + (unsigned)g * 3u) % (unsigned)n);
-        auto slab_k = [&](int s) __attribute__((always_inline)) {
-            const int idx = KG * s + grp;
-            int r = (idx < n ? idx : n - 1) + rot;
+        auto slab_k = [&](int i) __attribute__((always_inline)) {
+            int r = (i < n ? i : n - 1) + rot;
             r = r >= n ? r - n : r;
             return kb + SMOL_SLAB * r;
         };
-        auto valid = [&](int s) __attribute__((always_inline)) { return s >= 0 && KG * s + grp < n; };
-        /* register sets of staged slabs in flight: four with one wave per
-         * SIMD, two with two (the other wave hides the latency) */
-        constexpr int SETS = KG > 1 ? 2 : 4;
         Stg st[SETS];
-        f4 sacc[NT][2];
 #pragma unroll
         for (int q = 0; q < SETS; q++) issue(slab_k(q), st[q]);
         store(st[0], 0);
         issue(slab_k(SETS), st[0]);
+        store(st[1], 1);
+        issue(slab_k(SETS + 1), st[1]);
         __syncthreads();
-        /* u = i % 4 (compile-time in each unrolled step) */
-        auto step = [&](int i, auto u_tag) __attribute__((always_inline)) {
+        f4 sa[NT][2], sb[NT][2];
+        qk(0, sa);
+        /* u = i % 4, compile-time in each unrolled step */
+        auto step = [&](int i, auto u_tag, f4 (&scur)[NT][2], f4 (&snext)[NT][2]) __attribute__((always_inline)) {
             constexpr int u = decltype(u_tag)::value;
-            Stg &nxt = st[(u + 1) % SETS];
-            if (KG == 1 || grp == 0) {
-                if (valid(i)) {
-                    qk(slab_k(i), u & 1, sacc);
-                    smpv(slab_k(i), u & 1, sacc);
-                }
-                store(nxt, (u + 1) & 1);
-            } else {
-                if (valid(i - 1)) smpv(slab_k(i - 1), (u + 3) & 3, sacc);
-                if (valid(i)) qk(slab_k(i), u, sacc);
-                store(nxt, (u + 1) & 3);
-            }
-            issue(slab_k(i + 1 + SETS), nxt);
+            float sv[NT][8];
+            h8 pf[NT];
+            front(slab_k(i), scur, sv);
+            qk((u + 1) & 3, snext);
+            expo(sv, pf);
+            pv(u, pf);
+            Stg &s2 = st[(u + 2) % SETS];
+            store(s2, (u + 2) & 3);
+            issue(slab_k(i + 2 + SETS), s2);
             __syncthreads();
-            return i + 1 >= ns;
+            return i + 1 >= n;
         };
-        int i = 0;
-        for (;; i += 4) {
-            if (step(i, std::integral_constant<int, 0>{})) break;
-            if (step(i + 1, std::integral_constant<int, 1>{})) { i += 1; break; }
-            if (step(i + 2, std::integral_constant<int, 2>{})) { i += 2; break; }
-            if (step(i + 3, std::integral_constant<int, 3>{})) { i += 3; break; }
+        for (int i = 0;; i += 4) {
+            if (step(i, std::integral_constant<int, 0>{}, sa, sb)) break;
+            if (step(i + 1, std::integral_constant<int, 1>{}, sb, sa)) break;
+            if (step(i + 2, std::integral_constant<int, 2>{}, sa, sb)) break;
+            if (step(i + 3, std::integral_constant<int, 3>{}, sb, sa)) break;
         }
-        if (KG > 1 && grp == 1 && valid(i)) smpv(slab_k(i), i & 3, sacc);
-        if (KG > 1) __syncthreads(); /* the combine below reuses the stages */
     }
 
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) l[nt] = row_sum4(l[nt]);
-    if constexpr (KG > 1) {
-        /* key group 1 hands (m, l, O) of its rows to group 0 through LDS (the
-         * stages are free after the barrier that closed the loop) */
-        float *cb = reinterpret_cast<float *>(smem);
-        if (grp == 1) {
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                const int rr = (wave * NT + nt) * 16 + c;
-#pragma unroll
-                for (int dt = 0; dt < DT; dt++) *reinterpret_cast<f4 *>(cb + rr * OSTR + 16 * dt + 4 * j) = o[nt][dt];
-                if (j == 0) { s_cm[rr] = m[nt]; s_cl[rr] = l[nt]; }
-            }
-        }
-        __syncthreads();
-        if (grp == 0) {
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                const int rr = (wave * NT + nt) * 16 + c;
-                const float m1 = s_cm[rr], l1 = s_cl[rr];
-                const float M = fmaxf(m[nt], m1);
-                const float Mu = M == -INFINITY ? 0.0f : M;
-                const float a0 = __builtin_amdgcn_exp2f(m[nt] - Mu), a1 = __builtin_amdgcn_exp2f(m1 - Mu);
-#pragma unroll
-                for (int dt = 0; dt < DT; dt++)
-                    o[nt][dt] = o[nt][dt] * a0 + a1 * *reinterpret_cast<const f4 *>(cb + rr * OSTR + 16 * dt + 4 * j);
-                l[nt] = l[nt] * a0 + l1 * a1;
-                m[nt] = M;
-            }
-        }
-    }
-
-    /* epilogue: group 0's rows are complete over the item's keys */
+    /* epilogue: each wave's rows are complete over the item's keys */
     if (it.n_split == 1) {
-        if (grp != 0) return;
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             const int r = it.row0 + (wave * NT + nt) * 16 + c;
@@ -1440,7 +1406,7 @@ __global__ __launch_bounds__(256 * KG) __attribute__((amdgpu_waves_per_eu(W, W))
     /* split item: publish this wave's rows with device-coherent stores, then
      * the workgroup counts in once; the group's last workgroup merges */
     const long long pbase = ((long long)item * p.Hkv + g) * ROWS;
-    if (grp == 0) {
+    {
         const rsrc_t ro = make_rsrc(p.part_o + pbase * HD, (long long)ROWS * HD * 4);
         const rsrc_t rml = make_rsrc(p.part_ml + pbase * 2, (long long)ROWS * 2 * 4);
 #pragma unroll
@@ -1466,7 +1432,7 @@ __global__ __launch_bounds__(256 * KG) __attribute__((amdgpu_waves_per_eu(W, W))
     }
     __syncthreads();
     if (!s_last) return;
-    merge_group<HD, ROWS, TPB>(p, it, b, item, g, tid, reinterpret_cast<float *>(smem));
+    merge_group<HD, ROWS>(p, it, b, item, g, tid, reinterpret_cast<float *>(smem));
 }
 
 /* ------------------------------------------------------------ k_rope_apply */
@@ -1585,41 +1551,33 @@ extern "C" int smol_launch_pf(const SkParams *sp, int hd, int n_items, int nt, i
     }
 }
 
-template <int HD, int NT, int W, int KG>
+template <int HD, int NT, int W>
 static void launch_fa_v(const SkParams *sp, dim3 grid, hipStream_t st) {
-    hipLaunchKernelGGL((k_attn_fa<HD, NT, W, KG>), grid, dim3(256 * KG), 0, st, *sp);
+    hipLaunchKernelGGL((k_attn_fa<HD, NT, W>), grid, dim3(256), 0, st, *sp);
 }
 
-/* w: waves per SIMD the kernel is built for; kg: key groups (kg = 2 is two
- * four-wave groups on alternate slabs, i.e. two waves per SIMD in one
- * workgroup) */
+/* w: waves per SIMD the kernel is built for (2 with fewer staged slabs) */
 template <int HD>
-static int launch_fa_hd(const SkParams *sp, int n_items, int nt, int w, int kg, hipStream_t st) {
+static int launch_fa_hd(const SkParams *sp, int n_items, int nt, int w, hipStream_t st) {
     constexpr int NT2 = HD <= 128 ? 2 : 1;
     const dim3 grid(n_items * sp->Hkv);
-    constexpr int KG2 = HD <= 128 ? 2 : 1;
-    if (kg == 2) {
-        if (HD > 128) return -1;
-        if (nt == 1) launch_fa_v<HD, 1, 2, KG2>(sp, grid, st);
-        else if (nt == 2) launch_fa_v<HD, NT2, 2, KG2>(sp, grid, st);
-        else return -1;
-    } else if (nt == 1 && w == 1) launch_fa_v<HD, 1, 1, 1>(sp, grid, st);
-    else if (nt == 1 && w == 2) launch_fa_v<HD, 1, 2, 1>(sp, grid, st);
-    else if (nt == 2 && w == 1 && HD <= 128) launch_fa_v<HD, NT2, 1, 1>(sp, grid, st);
-    else if (nt == 2 && w == 2 && HD <= 128) launch_fa_v<HD, NT2, 2, 1>(sp, grid, st);
+    if (nt == 1 && w == 1) launch_fa_v<HD, 1, 1>(sp, grid, st);
+    else if (nt == 1 && w == 2) launch_fa_v<HD, 1, 2>(sp, grid, st);
+    else if (nt == 2 && w == 1 && HD <= 128) launch_fa_v<HD, NT2, 1>(sp, grid, st);
+    else if (nt == 2 && w == 2 && HD <= 128) launch_fa_v<HD, NT2, 2>(sp, grid, st);
     else return -1;
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, int kg, hipStream_t st) {
+extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st) {
     if (n_items <= 0) return 0;
     switch (hd) {
-    case 64: return launch_fa_hd<64>(sp, n_items, nt, w, kg, st);
-    case 72: return launch_fa_hd<72>(sp, n_items, nt, w, kg, st);
-    case 80: return launch_fa_hd<80>(sp, n_items, nt, w, kg, st);
-    case 96: return launch_fa_hd<96>(sp, n_items, nt, w, kg, st);
-    case 128: return launch_fa_hd<128>(sp, n_items, nt, w, kg, st);
-    case 256: return launch_fa_hd<256>(sp, n_items, nt, w, kg, st);
+    case 64: return launch_fa_hd<64>(sp, n_items, nt, w, st);
+    case 72: return launch_fa_hd<72>(sp, n_items, nt, w, st);
+    case 80: return launch_fa_hd<80>(sp, n_items, nt, w, st);
+    case 96: return launch_fa_hd<96>(sp, n_items, nt, w, st);
+    case 128: return launch_fa_hd<128>(sp, n_items, nt, w, st);
+    case 256: return launch_fa_hd<256>(sp, n_items, nt, w, st);
     default: return -1;
     }
 }
