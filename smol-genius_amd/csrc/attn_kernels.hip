@@ -1136,6 +1136,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
     h8 qf[NT][KS];
     int lo[NT], hi[NT];
     float m[NT], l[NT];
+    f4 negm[NT];   /* -m (0 while m = -inf): the accumulator input of S = K.Q^T - m */
+    float thr[NT]; /* a score above thr (relative to m) calls for a rescale */
     f4 o[NT][DT];
     int lo_max = -(1 << 30), hi_min = 1 << 30;
 #pragma unroll
@@ -1154,6 +1156,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
         hi_min = min(hi_min, hi[nt]);
         m[nt] = -INFINITY;
         l[nt] = 0.0f;
+        negm[nt] = f4{0.f, 0.f, 0.f, 0.f};
+        thr[nt] = -INFINITY;
         if (p.q_direct) {
             /* rotate and scale Q here: row r is query qi of head g*G + hg */
             const int hg = r - qi * G;
@@ -1252,7 +1256,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
         const uint4 w = *reinterpret_cast<const uint4 *>(smem + stage * STAGE + off);
         return *reinterpret_cast<const h8 *>(&w);
     };
-    /* S^T = K.Q^T of the slab in `stage` */
+    /* S^T - m = K.Q^T - m of the slab in `stage` (raw S with a softcap) */
+    const bool capped = p.cap2 > 0.0f;
     auto qk = [&](int stage, f4 (&sacc)[NT][2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < 2; t++) {
@@ -1261,7 +1266,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
             for (int ks = 0; ks < KS; ks++) kfr[ks] = lds_h8(stage, kfo[ks] + t * 4 * KROW);
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
-                f4 acc = {0.f, 0.f, 0.f, 0.f};
+                f4 acc = capped ? f4{0.f, 0.f, 0.f, 0.f} : negm[nt];
 #pragma unroll
                 for (int ks = 0; ks < KS; ks++)
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kfr[ks], qf[nt][ks], acc, 0, 0, 0);
@@ -1269,9 +1274,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
             }
         }
     };
-    /* softmax front: scores of slab k0 with softcap / mask applied, rows'
-     * running max (lazy rescale of O and l), returned relative to the row
-     * reference */
+    /* softmax front: scores relative to the row reference m, softcap and
+     * mask applied. m is lazy: while no score exceeds thr (2^8 above m) the
+     * common path is one compare per score; otherwise the row max is formed
+     * and O, l and m are rescaled */
     auto front = [&](int k0, const f4 (&sacc)[NT][2], float (&sv)[NT][8]) __attribute__((always_inline)) {
         const bool full = k0 >= lo_max && k0 + SMOL_SLAB <= hi_min;
 #pragma unroll
@@ -1280,9 +1286,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
             for (int t = 0; t < 2; t++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) sv[nt][4 * t + i] = sacc[nt][t][i];
-            if (p.cap2 > 0.0f) {
+            if (capped) {
 #pragma unroll
-                for (int e = 0; e < 8; e++) sv[nt][e] = p.cap2 * tanhf(sv[nt][e] / p.cap2);
+                for (int e = 0; e < 8; e++) sv[nt][e] = p.cap2 * tanhf(sv[nt][e] / p.cap2) + negm[nt][0];
             }
             if (!full) {
 #pragma unroll
@@ -1291,20 +1297,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
                     sv[nt][e] = (key >= lo[nt] && key < hi[nt]) ? sv[nt][e] : -INFINITY;
                 }
             }
-            const float mx = row_max4(fmaxf(fmaxf(fmaxf(sv[nt][0], sv[nt][1]), fmaxf(sv[nt][2], sv[nt][3])),
-                                            fmaxf(fmaxf(sv[nt][4], sv[nt][5]), fmaxf(sv[nt][6], sv[nt][7]))));
-            const bool need = mx > m[nt] + LAZY_T;
-            if (__any(need)) {
-                const float m_new = need ? mx : m[nt];
+            bool hit = sv[nt][0] > thr[nt];
+#pragma unroll
+            for (int e = 1; e < 8; e++) hit |= sv[nt][e] > thr[nt];
+            if (__any(hit)) {
+                const float mx = row_max4(fmaxf(fmaxf(fmaxf(sv[nt][0], sv[nt][1]), fmaxf(sv[nt][2], sv[nt][3])),
+                                                fmaxf(fmaxf(sv[nt][4], sv[nt][5]), fmaxf(sv[nt][6], sv[nt][7]))));
+                const bool need = mx > thr[nt];
+                const float sh = need ? mx : 0.0f;
+                const float m_new = need ? -negm[nt][0] + mx : m[nt];
                 const float alpha = need ? __builtin_amdgcn_exp2f(m[nt] - m_new) : 1.0f;
 #pragma unroll
                 for (int dt = 0; dt < DT; dt++) o[nt][dt] *= alpha;
                 l[nt] *= alpha;
                 m[nt] = m_new;
-            }
-            const float m_use = m[nt] == -INFINITY ? 0.0f : m[nt];
+                const float mu = m_new == -INFINITY ? 0.0f : m_new;
+                negm[nt] = f4{-mu, -mu, -mu, -mu};
+                thr[nt] = m_new == -INFINITY ? -INFINITY : LAZY_T;
 #pragma unroll
-            for (int e = 0; e < 8; e++) sv[nt][e] -= m_use;
+                for (int e = 0; e < 8; e++) sv[nt][e] -= sh;
+            }
         }
     };
     /* P = exp2(S - m) as fp16, row sums */
@@ -1373,13 +1385,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
             store(s2, (u + 2) & 3);
             issue(slab_k(i + 2 + SETS), s2);
             __syncthreads();
-            return i + 1 >= n;
         };
-        for (int i = 0;; i += 4) {
-            if (step(i, std::integral_constant<int, 0>{}, sa, sb)) break;
-            if (step(i + 1, std::integral_constant<int, 1>{}, sb, sa)) break;
-            if (step(i + 2, std::integral_constant<int, 2>{}, sa, sb)) break;
-            if (step(i + 3, std::integral_constant<int, 3>{}, sb, sa)) break;
+        /* whole groups of four steps in a loop with one exit, then the last
+         * one to four steps: a loop left from the middle of its body would
+         * merge that exit's outstanding loads into the loop head, and the
+         * head would wait for them on every pass */
+        using P0 = std::integral_constant<int, 0>;
+        using P1 = std::integral_constant<int, 1>;
+        using P2 = std::integral_constant<int, 2>;
+        using P3 = std::integral_constant<int, 3>;
+        int i = 0;
+        for (; i + 4 < n; i += 4) {
+            step(i, P0{}, sa, sb);
+            step(i + 1, P1{}, sb, sa);
+            step(i + 2, P2{}, sa, sb);
+            step(i + 3, P3{}, sb, sa);
+        }
+        step(i, P0{}, sa, sb);
+        if (i + 1 < n) {
+            step(i + 1, P1{}, sb, sa);
+            if (i + 2 < n) {
+                step(i + 2, P2{}, sa, sb);
+                if (i + 3 < n) step(i + 3, P3{}, sb, sa);
+            }
         }
     }
 
