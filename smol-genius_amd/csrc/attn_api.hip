@@ -29,6 +29,7 @@ extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t 
 extern "C" int smol_launch_pf(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
 extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
 extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
+extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st);
 extern "C" int smol_launch_rope_apply(float *x, const float *cos_t, const float *sin_t,
                                       const int *pos, int seq, int n_heads, int hd, int kind,
                                       hipStream_t st);
@@ -527,7 +528,8 @@ static int choose_waves(bool dec, int hd, int nt) {
 /* rows_per: query rows of one work item; longest_first: order the merge
  * groups by descending key count, so the last workgroups dispatched are the
  * short ones */
-static void plan_items(Plan &pl, int Hkv, int G, int window, int rows_per, int cu_count, bool longest_first) {
+static void plan_items(Plan &pl, int Hkv, int G, int window, int rows_per, int cu_count, bool longest_first,
+                       bool no_split = false) {
     struct Tile { int batch, row0, lo, hi; };
     std::vector<Tile> tiles;
     long long total_slabs = 0;
@@ -558,6 +560,7 @@ static void plan_items(Plan &pl, int Hkv, int G, int window, int rows_per, int c
     if (const int n = env_int("SMOL_ATTN_SLABS_PER_ITEM")) {
         if (n > 0) slabs_per_item = n;
     }
+    if (no_split) slabs_per_item = 1 << 28;
     int group = 0;
     const int max_split = 1024 / rows_per; /* the kernel's merge holds rows * n_split pairs in LDS */
     for (const Tile &t : tiles) {
@@ -591,8 +594,28 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
      * LDS) unless SMOL_ATTN_PREFILL_KERNEL=pf selects k_attn_pf */
     const char *pk = getenv("SMOL_ATTN_PREFILL_KERNEL");
     const bool fa = !cs.dec && !(pk && strcmp(pk, "pf") == 0);
+    /* k_attn_fb (one workgroup per 64-row tile, no merges between
+     * workgroups) when every key is in the fresh buffers and the call has
+     * enough tiles to occupy the device; SMOL_ATTN_PREFILL_KERNEL=fa keeps
+     * k_attn_fa */
+    bool fb = fa && hd <= 128 && !(pk && strcmp(pk, "fa") == 0);
+    if (fb) {
+        long long tiles = 0;
+        for (auto &b : pl.sb) {
+            if (b.key_lo < b.fresh_pos0) fb = false;
+            tiles += (b.n_rows + 63) / 64;
+        }
+        /* SMOL_ATTN_PREFILL_KERNEL=fb takes it whenever the keys allow */
+        const bool forced = pk && strcmp(pk, "fb") == 0;
+        if (!forced && tiles * cs.Hkv < ctx->cu_count / 4) fb = false;
+    }
     int nt, w, rows_per;
-    if (fa) {
+    if (fb) {
+        /* SMOL_ATTN_FB_NT=2: two row tiles per wave (128-row tiles) */
+        nt = env_int("SMOL_ATTN_FB_NT") == 2 ? 2 : 1;
+        w = 2;
+        rows_per = 64 * nt;
+    } else if (fa) {
         nt = (hd <= 128 && max_rows > 64) ? 2 : 1;
         if (const int ov = env_int("SMOL_ATTN_NT"))
             if (ov == 1 || (ov == 2 && hd <= 128)) nt = ov;
@@ -608,10 +631,10 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
         w = choose_waves(cs.dec, hd, nt);
         rows_per = 16 * nt;
     }
-    plan_items(pl, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, fa);
+    plan_items(pl, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, fa, fb);
     /* SMOL_ATTN_FA_QDIRECT=1: k_attn_fa rotates and scales Q as it loads it
      * and the pre-pass only handles the new K/V */
-    const bool q_direct = fa && env_int("SMOL_ATTN_FA_QDIRECT") == 1;
+    const bool q_direct = fa && !fb && env_int("SMOL_ATTN_FA_QDIRECT") == 1;
     if (q_direct)
         pl.pblk.erase(std::remove_if(pl.pblk.begin(), pl.pblk.end(), [](const PrepBlock &k) { return k.kind == 1; }),
                       pl.pblk.end());
@@ -710,6 +733,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     }
     mk = timing_begin(ctx, 1);
     rc = cs.dec ? smol_launch_dec(&sp, hd, (int)n_items, nt, w, ctx->stream)
+         : fb   ? smol_launch_fb(&sp, hd, (int)n_items, nt, ctx->stream)
          : fa   ? smol_launch_fa(&sp, hd, (int)n_items, nt, w, ctx->stream)
                 : smol_launch_pf(&sp, hd, (int)n_items, nt, w, ctx->stream);
     timing_end(ctx, mk);

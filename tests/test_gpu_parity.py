@@ -153,6 +153,25 @@ def test_causal_shapes(ctx, sa, oracle, shape):
         assert not got[:-qo].any()
 
 
+@pytest.mark.parametrize("shape", [s for s in CAUSAL_SHAPES if s[2] <= 128 and s[5] >= 0])
+def test_causal_shapes_fb(ctx, sa, oracle, shape, monkeypatch):
+    """The same cases through k_attn_fb (one workgroup per 64-row tile, taken
+    here whatever the call's size)."""
+    monkeypatch.setenv("SMOL_ATTN_PREFILL_KERNEL", "fb")
+    test_causal_shapes(ctx, sa, oracle, shape)
+
+
+@pytest.mark.parametrize("window,cap", [(16, 0.0), (0, 2.0), (40, 1.5), (1, 0.0), (7, 50.0)])
+def test_window_softcap_fb(ctx, sa, oracle, window, cap, monkeypatch):
+    monkeypatch.setenv("SMOL_ATTN_PREFILL_KERNEL", "fb")
+    test_window_softcap(ctx, sa, oracle, window, cap)
+
+
+def test_bidirectional_ragged_fb(ctx, sa, oracle, monkeypatch):
+    monkeypatch.setenv("SMOL_ATTN_PREFILL_KERNEL", "fb")
+    test_bidirectional_ragged(ctx, sa, oracle)
+
+
 @pytest.mark.parametrize("window,cap", [(16, 0.0), (0, 2.0), (40, 1.5), (1, 0.0), (7, 50.0)])
 def test_window_softcap(ctx, sa, oracle, window, cap):
     # small caps so that tanh actually bends the N(0, 1) scores
