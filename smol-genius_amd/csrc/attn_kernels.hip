@@ -1664,8 +1664,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     };
     /* softmax front, in place on the scores: softcap, mask, lazy rescale as
      * in k_attn_fa (lane (c, j) holds keys 8j + 4t + i of row c in s[t][i]) */
-    auto front = [&](int k0, f4 (&s)[NT][2]) __attribute__((always_inline)) {
-        const bool full = k0 >= lo_max && k0 + SMOL_SLAB <= hi_min;
+    auto front = [&](int k0, bool act, f4 (&s)[NT][2]) __attribute__((always_inline)) {
+        /* a step past the group's own slabs masks every key, so its
+         * arithmetic adds nothing and needs no branch of its own */
+        const bool full = act && k0 >= lo_max && k0 + SMOL_SLAB <= hi_min;
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             if (capped) {
@@ -1680,7 +1682,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
                         const int key = k0 + 8 * j + 4 * t + i;
-                        s[nt][t][i] = (key >= lo[nt] && key < hi[nt]) ? s[nt][t][i] : -INFINITY;
+                        s[nt][t][i] = (act && key >= lo[nt] && key < hi[nt]) ? s[nt][t][i] : -INFINITY;
                     }
             }
             bool hit = false;
@@ -1756,28 +1758,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const bool act = i < n_own;
         h8 pf[NT];
         if constexpr (DB) {
-            if (act) {
-                front(slab_k(i), scur);
-                qk(kcur, snext);
-            }
-            __builtin_amdgcn_sched_barrier(0);
+            /* the next step's LDS reads and the transfer of slab i+NSTG go
+             * out first and proceed during this step's arithmetic, which
+             * works from registers filled before the last barrier */
             read_k(st_k, knext);
             read_v(st_v, vnext);
-            if (act) {
-                expo(scur, pf);
-                pv(vcur, pf);
-            }
+            dma(slab_k(i + NSTG), st_d);
+            __builtin_amdgcn_sched_barrier(0);
+            front(slab_k(i), act, scur);
+            qk(kcur, snext);
+            expo(scur, pf);
+            pv(vcur, pf);
         } else {
             read_k(st_k, kcur);
             read_v(st_v, vcur);
-            if (act) {
-                front(slab_k(i), scur);
-                expo(scur, pf);
-                qk(kcur, snext);
-                pv(vcur, pf);
-            }
+            front(slab_k(i), act, scur);
+            expo(scur, pf);
+            qk(kcur, snext);
+            pv(vcur, pf);
+            dma(slab_k(i + NSTG), st_d);
         }
-        dma(slab_k(i + NSTG), st_d);
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
         __syncthreads();
         st_k = st_k + 1 == NSTG ? 0 : st_k + 1;
