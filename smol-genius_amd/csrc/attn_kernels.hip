@@ -355,32 +355,70 @@ __device__ __forceinline__ float row_sum4(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-/* Merge of one split-K group by its last workgroup (all 64*SK_WAVES threads):
- * all (max, sum) pairs of the group are loaded in one parallel sweep into
- * LDS, each row's max and 1/sum and every split's weight are formed there,
- * then each (row, 4 columns) element sums the weighted partials with eight
- * independent loads in flight. The host keeps ROWS * n_split within
- * SK_MERGE_MAX. Resets the group's counter for the next call. */
-template <int HD, int ROWS, int TPB = 64 * SK_WAVES>
+/* Merge of one split-K group by its last workgroup (all 64*SK_WAVES threads).
+ * Only the batch's real rows are read and written. Every thread owns E
+ * (row, 4-column) elements, taken EB at a time, and walks the splits U at a
+ * time with all EB * U loads in flight (MAXL at most), so the merge costs
+ * about (E / EB) * n_split / U memory round trips; when one round covers
+ * everything (decode), those loads are issued before the group's (max, sum)
+ * pairs are even read, and the two sweeps share one round trip. Each row's
+ * max and 1/sum and every split's weight are formed in LDS. The host keeps
+ * ROWS * n_split within SK_MERGE_MAX. Resets the group's counter for the
+ * next call. */
+template <int HD, int ROWS, int MAXL = 16, int TPB = 64 * SK_WAVES>
 __device__ __forceinline__ void merge_group(const SkParams &p, const SkItem &it, const SkBatch &b, int item, int g,
                                             int tid, float *s_o) {
     const int G = p.G, Hq = p.Hq;
     const int first = item - it.split;
     const int nsp = it.n_split;
+    const int n_valid = min(ROWS, b.n_rows - it.row0);
     float *s_ml = s_o;                       /* [nsp][ROWS][2], then weights [nsp][ROWS] */
     float *s_row = s_o + 2 * SK_MERGE_MAX;   /* per row: max, 1/sum */
     /* the group's items are contiguous: item `first + sp` holds split sp */
     const rsrc_t rml = make_rsrc(p.part_ml + (long long)first * p.Hkv * ROWS * 2, (long long)nsp * p.Hkv * ROWS * 2 * 4);
     const rsrc_t ro = make_rsrc(p.part_o + (long long)first * p.Hkv * ROWS * HD, (long long)nsp * p.Hkv * ROWS * HD * 4);
+    constexpr int C4 = HD / 4;
+    constexpr int E = (ROWS * C4 + TPB - 1) / (TPB);
+    constexpr int EB = E < 8 ? E : 8;
+    constexpr int U = MAXL / EB > 16 ? 16 : (MAXL / EB < 1 ? 1 : MAXL / EB);
+    const int nel = n_valid * C4;
+    const unsigned sp_stride = (unsigned)((long long)p.Hkv * ROWS * HD * 4);
+    auto setup = [&](int e0, int (&prow)[EB], int (&pcol)[EB]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int e = 0; e < EB; e++) {
+            const int idx = tid + TPB * (e0 + e);
+            const int rr = idx / C4;
+            prow[e] = (e0 + e < E && idx < nel) ? rr : -1;
+            pcol[e] = (idx - rr * C4) * 4;
+        }
+    };
+    auto issue = [&](int sp0, const int (&prow)[EB], const int (&pcol)[EB], f4 (&v)[U][EB]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const unsigned so = (unsigned)min(sp0 + u, nsp - 1) * sp_stride;
+#pragma unroll
+            for (int e = 0; e < EB; e++) {
+                v[u][e] = f4{0.f, 0.f, 0.f, 0.f};
+                if (prow[e] >= 0 && sp0 + u < nsp)
+                    v[u][e] = load_f4_sc1(ro, (unsigned)(((g * ROWS + prow[e]) * HD + pcol[e]) * 4) + so);
+            }
+        }
+    };
+    const bool one_round = E <= EB && nsp <= U;
+    int prow[EB], pcol[EB];
+    f4 v[U][EB];
+    setup(0, prow, pcol);
+    if (one_round) issue(0, prow, pcol, v);
     for (int e = tid; e < nsp * ROWS; e += TPB) {
         const int sp = e / ROWS, rr = e - sp * ROWS;
+        if (rr >= n_valid) continue;
         const long long pr = ((long long)sp * p.Hkv + g) * ROWS + rr;
         const float2 ml = load_f2_sc1(rml, (unsigned)(pr * 8));
         s_ml[2 * e] = ml.x;
         s_ml[2 * e + 1] = ml.y;
     }
     __syncthreads();
-    if (tid < ROWS) {
+    if (tid < n_valid) {
         float M = -INFINITY;
         for (int sp = 0; sp < nsp; sp++) M = fmaxf(M, s_ml[2 * (sp * ROWS + tid)]);
         const float Mu = M == -INFINITY ? 0.0f : M;
@@ -395,41 +433,18 @@ __device__ __forceinline__ void merge_group(const SkParams &p, const SkItem &it,
     __syncthreads();
     for (int e = tid; e < nsp * ROWS; e += TPB) {
         const int rr = e % ROWS;
+        if (rr >= n_valid) continue;
         s_ml[2 * e] = __builtin_amdgcn_exp2f(s_ml[2 * e] - s_row[2 * rr]); /* weight of (split, row) */
     }
     __syncthreads();
-    /* every thread owns E (row, 4-column) elements, taken EB at a time; the
-     * splits are walked U at a time with all EB * U (about 16) loads in
-     * flight, so the merge costs about (E / EB) * n_split / U memory round
-     * trips */
-    constexpr int C4 = HD / 4;
-    constexpr int E = (ROWS * C4 + TPB - 1) / (TPB);
-    constexpr int EB = E < 8 ? E : 8;
-    constexpr int U = 16 / EB > 8 ? 8 : 16 / EB;
-    const unsigned sp_stride = (unsigned)((long long)p.Hkv * ROWS * HD * 4);
     for (int e0 = 0; e0 < E; e0 += EB) {
+        if (TPB * e0 >= nel) break;
+        if (e0 > 0) setup(e0, prow, pcol);
         f4 acc[EB];
-        int prow[EB], pcol[EB];
 #pragma unroll
-        for (int e = 0; e < EB; e++) {
-            acc[e] = f4{0.f, 0.f, 0.f, 0.f};
-            const int idx = tid + TPB * (e0 + e);
-            const int rr = idx / C4;
-            const bool ok = e0 + e < E && idx < ROWS * C4 && it.row0 + rr < b.n_rows;
-            prow[e] = ok ? rr : -1;
-            pcol[e] = (idx - rr * C4) * 4;
-        }
+        for (int e = 0; e < EB; e++) acc[e] = f4{0.f, 0.f, 0.f, 0.f};
         for (int sp0 = 0; sp0 < nsp; sp0 += U) {
-            f4 v[U][EB];
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const unsigned so = (unsigned)min(sp0 + u, nsp - 1) * sp_stride;
-#pragma unroll
-                for (int e = 0; e < EB; e++) {
-                    const int rr = prow[e] < 0 ? 0 : prow[e];
-                    v[u][e] = load_f4_sc1(ro, (unsigned)(((g * ROWS + rr) * HD + pcol[e]) * 4) + so);
-                }
-            }
+            if (!one_round) issue(sp0, prow, pcol, v);
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 if (sp0 + u >= nsp) break;
@@ -455,7 +470,7 @@ __device__ __forceinline__ void merge_group(const SkParams &p, const SkItem &it,
  * (max, sum, O) through LDS into wave 0, then either writes the normalised
  * rows (single split) or publishes the partial and lets the group's last
  * workgroup merge. Every row's state lives in lanes c, c+16, c+32, c+48. */
-template <int HD, int NT>
+template <int HD, int NT, int MAXL = 16>
 __device__ __forceinline__ void finish_item(const SkParams &p, const SkItem &it, const SkBatch &b, int item, int g,
                                             int tid,
                                             float (&m)[NT], float (&l)[NT], f4 (&o)[NT][(HD + 15) / 16], float *s_o,
@@ -534,6 +549,7 @@ __device__ __forceinline__ void finish_item(const SkParams &p, const SkItem &it,
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             const int rr = nt * 16 + c;
+            if (it.row0 + rr >= b.n_rows) continue;
 #pragma unroll
             for (int dt = 0; dt < DT; dt++) {
                 const int d = 16 * dt + 4 * j;
@@ -554,7 +570,7 @@ __device__ __forceinline__ void finish_item(const SkParams &p, const SkItem &it,
     }
     __syncthreads();
     if (!*s_last) return;
-    merge_group<HD, ROWS>(p, it, b, item, g, tid, s_o);
+    merge_group<HD, ROWS, MAXL>(p, it, b, item, g, tid, s_o);
 }
 
 /* --------------------------------------------------------------- k_attn_dec */
@@ -565,8 +581,9 @@ __device__ __forceinline__ void finish_item(const SkParams &p, const SkItem &it,
  * operands as loaded (no conversion); precision comes from splitting the
  * other operand, Q = Qhi + Qlo and P = Phi + Plo (bf16 each, ~16
  * significant bits together):  S = K.Qhi + K.Qlo,  O += V.Phi + V.Plo.
- * The slab holding the keys this call appends runs on fp16 MFMA over the
- * fp16 fresh staging (k_prep), with an fp16 copy of Q.
+ * The slab holding the keys this call appends comes from the fp16 fresh
+ * staging (k_prep): each fp16 fragment is split into bf16 hi + lo (exact) in
+ * registers and the product takes three bf16 MFMAs (hi.hi, hi.lo, lo.hi).
  * Lane layouts, wave split and merge as k_attn_pf. The running max is a
  * lazy reference: the accumulator is rescaled only when some row's max grows
  * by more than 2^LAZY_T (decided per wave by vote), so p <= 2^LAZY_T.
@@ -593,6 +610,8 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
     constexpr int ROWS = NT * 16;
     constexpr int OSTR = DT * 16 + 4;
     constexpr unsigned SLAB_K_BYTES = SMOL_SLAB * HD * 2; /* one slab of K, and one slab-block of V^T */
+    /* two slabs in flight per wave where the registers allow */
+    constexpr bool DBUF = W == 1 && HD <= 128;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
@@ -632,20 +651,29 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
         hi_min = min(hi_min, hi[nt]);
         m[nt] = -INFINITY;
         l[nt] = 0.0f;
-        const float *qrow = p.qs32 + (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid ? r : 0)) * HDP;
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-            float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (valid) {
-                const float4 a = *reinterpret_cast<const float4 *>(qrow + 32 * ks + 8 * j);
-                const float4 e = *reinterpret_cast<const float4 *>(qrow + 32 * ks + 8 * j + 4);
-                x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = e.x; x[5] = e.y; x[6] = e.z; x[7] = e.w;
-            }
-            split8(x, qh[nt][ks], ql[nt][ks]);
-        }
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) o[nt][dt] = f4{0.f, 0.f, 0.f, 0.f};
     }
+    /* Q fragments (after the first slabs' loads are in flight) */
+    auto load_q = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int r = it.row0 + nt * 16 + c;
+            const bool valid = r < b.n_rows;
+            const float *qrow =
+                p.qs32 + (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid ? r : 0)) * HDP;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                if (valid) {
+                    const float4 a = *reinterpret_cast<const float4 *>(qrow + 32 * ks + 8 * j);
+                    const float4 e = *reinterpret_cast<const float4 *>(qrow + 32 * ks + 8 * j + 4);
+                    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = e.x; x[5] = e.y; x[6] = e.z; x[7] = e.w;
+                }
+                split8(x, qh[nt][ks], ql[nt][ks]);
+            }
+        }
+    };
     /* the slab [k0, k0 + 32) needs no masking when it lies inside every row's range */
 #pragma unroll
     for (int sh = 1; sh < 16; sh <<= 1) {
@@ -693,21 +721,29 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
         so = (unsigned)(kr / SMOL_SLAB) * SLAB_K_BYTES;
         r = value ? (fr ? rv_f : rv_c) : (fr ? rk_f : rk_c);
     };
-    auto issue_k = [&](int k0, KRaw &r) {
+    /* with head_dim a multiple of 32 (resp. 16) every lane's fragment
+     * offsets are one lane base plus constants, which ride in the scalar
+     * offset instead of occupying a register each */
+    const unsigned kbase = (unsigned)((kt_row * HD + 8 * j) * 2);
+    const unsigned vbase = (unsigned)((c * SMOL_SLAB + 8 * j) * 2);
+    auto issue_k = [&](int k0, KRaw &r) __attribute__((always_inline)) {
         rsrc_t rs;
         unsigned so;
         slab_src(k0, false, rs, so);
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) r.k[t][ks] = bload(rs, vo_k[t][ks], so);
+            for (int ks = 0; ks < KS; ks++)
+                r.k[t][ks] = HD % 32 == 0 ? bload(rs, kbase, so + (unsigned)((4 * t * HD + 32 * ks) * 2))
+                                          : bload(rs, vo_k[t][ks], so);
     };
-    auto issue_v = [&](int k0, VRaw &r) {
+    auto issue_v = [&](int k0, VRaw &r) __attribute__((always_inline)) {
         rsrc_t rs;
         unsigned so;
         slab_src(k0, true, rs, so);
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) r.v[dt] = bload(rs, vo_v[dt], so);
+        for (int dt = 0; dt < DT; dt++)
+            r.v[dt] = HD % 16 == 0 ? bload(rs, vbase, so + (unsigned)(16 * dt * SMOL_SLAB * 2)) : bload(rs, vo_v[dt], so);
     };
 
     auto qk = [&](const KRaw &r, f4 (&sacc)[NT][2], auto fresh_tag) {
@@ -720,12 +756,17 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
 #pragma unroll
                 for (int ks = 0; ks < KS; ks++) {
                     if (FRESH) {
-                        /* fp16 Q for the fp16 fresh slab, re-formed from its two bf16 parts */
-                        h8 qf;
+                        /* the fresh slab's fp16 K as bf16 hi + lo (exact: 11 significant
+                         * bits), K.Q = Khi.Qhi + Khi.Qlo + Klo.Qhi */
+                        b8 kh, kl;
+                        float kx[8];
+                        const h8 k16 = *reinterpret_cast<const h8 *>(&r.k[t][ks]);
 #pragma unroll
-                        for (int i = 0; i < 8; i++) qf[i] = (_Float16)((float)qh[nt][ks][i] + (float)ql[nt][ks][i]);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const h8 *>(&r.k[t][ks]), qf,
-                                                                     acc, 0, 0, 0);
+                        for (int i = 0; i < 8; i++) kx[i] = (float)k16[i];
+                        split8(kx, kh, kl);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[nt][ks], acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[nt][ks], acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[nt][ks], acc, 0, 0, 0);
                     } else {
                         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(r.k[t][ks]), qh[nt][ks], acc, 0, 0, 0);
                         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(r.k[t][ks]), ql[nt][ks], acc, 0, 0, 0);
@@ -778,17 +819,23 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
                 ps += pv[e];
             }
             l[nt] += ps;
+            b8 ph, pl;
+            split8(pv, ph, pl);
             if (FRESH) {
-                h8 pf;
+                /* fp16 V^T as bf16 hi + lo: O += Vhi.Phi + Vhi.Plo + Vlo.Phi */
 #pragma unroll
-                for (int e = 0; e < 8; e++) pf[e] = (_Float16)pv[e];
+                for (int dt = 0; dt < DT; dt++) {
+                    b8 vh, vl;
+                    float vx[8];
+                    const h8 v16 = *reinterpret_cast<const h8 *>(&r.v[dt]);
 #pragma unroll
-                for (int dt = 0; dt < DT; dt++)
-                    o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const h8 *>(&r.v[dt]), pf,
-                                                                       o[nt][dt], 0, 0, 0);
+                    for (int i = 0; i < 8; i++) vx[i] = (float)v16[i];
+                    split8(vx, vh, vl);
+                    o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph, o[nt][dt], 0, 0, 0);
+                    o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl, o[nt][dt], 0, 0, 0);
+                    o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph, o[nt][dt], 0, 0, 0);
+                }
             } else {
-                b8 ph, pl;
-                split8(pv, ph, pl);
 #pragma unroll
                 for (int dt = 0; dt < DT; dt++) {
                     o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(r.v[dt]), ph, o[nt][dt], 0, 0, 0);
@@ -798,36 +845,59 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
         }
     };
 
-    /* Each wave streams slabs wave, wave + SK_WAVES, ... with one K and one V
-     * register buffer: the next slab's K is requested as soon as the current
-     * S is formed and its V as soon as the current P.V is issued. The request
-     * is made on every path (past the end it re-reads the current slab), so
-     * every wait sees the same number of loads in flight. */
+    /* Each wave streams slabs wave, wave + SK_WAVES, ... with two K/V
+     * register buffers: slabs i and i+1 are in flight while slab i is
+     * computed, and the first two are requested before Q is loaded. A
+     * request past the wave's last slab re-reads that slab, so every wait
+     * sees the same number of loads in flight. */
     const int step = SMOL_SLAB * SK_WAVES;
     const int end = it.key_end;
     int k0 = it.key_begin + wave * SMOL_SLAB;
     if (k0 < end) {
-        KRaw kr;
-        VRaw vr;
-        issue_k(k0, kr);
-        issue_v(k0, vr);
-        while (true) {
-            const int k1 = k0 + step;
-            const int kn = k1 < end ? k1 : k0;
+        int last = k0 + ((end - 1 - k0) / step) * step; /* this wave's last slab */
+        auto clampk = [&](int k) __attribute__((always_inline)) { return k < last ? k : last; };
+        auto slab = [&](int kk, KRaw &kr, VRaw &vr, int ahead) __attribute__((always_inline)) {
             f4 sacc[NT][2];
-            const bool fr = k0 >= b.fresh_pos0;
+            const bool fr = kk >= b.fresh_pos0;
             if (fr) qk(kr, sacc, std::true_type{});
             else qk(kr, sacc, std::false_type{});
-            issue_k(kn, kr);
-            if (fr) smpv(k0, sacc, vr, std::true_type{});
-            else smpv(k0, sacc, vr, std::false_type{});
-            issue_v(kn, vr);
-            if (k1 >= end) break;
-            k0 = k1;
+            issue_k(clampk(kk + ahead), kr);
+            if (fr) smpv(kk, sacc, vr, std::true_type{});
+            else smpv(kk, sacc, vr, std::false_type{});
+            issue_v(clampk(kk + ahead), vr);
+        };
+        if constexpr (DBUF) {
+            KRaw ka, kb;
+            VRaw va, vb;
+            issue_k(k0, ka);
+            issue_v(k0, va);
+            issue_k(clampk(k0 + step), kb);
+            issue_v(clampk(k0 + step), vb);
+            load_q();
+            while (true) {
+                slab(k0, ka, va, 2 * step);
+                if (k0 + step >= end) break;
+                slab(k0 + step, kb, vb, 2 * step);
+                k0 += 2 * step;
+                if (k0 >= end) break;
+            }
+        } else {
+            KRaw kr;
+            VRaw vr;
+            issue_k(k0, kr);
+            issue_v(k0, vr);
+            load_q();
+            while (true) {
+                slab(k0, kr, vr, step);
+                k0 += step;
+                if (k0 >= end) break;
+            }
         }
+    } else {
+        load_q();
     }
 
-    finish_item<HD, NT>(p, it, b, item, g, tid, m, l, o, s_o, s_m, s_l, &s_last);
+    finish_item<HD, NT, W == 1 ? 64 : 32>(p, it, b, item, g, tid, m, l, o, s_o, s_m, s_l, &s_last);
 }
 
 /* ---------------------------------------------------------------- k_attn_pf */
