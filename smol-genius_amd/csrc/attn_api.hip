@@ -5,9 +5,10 @@
  * Each attention call builds small descriptor tables on the host (which rows
  * and keys each kernel block covers), copies them to the device through a
  * ring of pinned buffers, and enqueues two kernels on the context's stream:
- * k_prep (RoPE + cache append + staging) and k_attn_pf or k_attn_dec (flash
- * attention, long key ranges split across workgroups and merged in-kernel). Nothing here computes attention on the
- * host; without a GPU every entry point fails with SMOL_ATTN_ERR_NO_GPU.
+ * k_prep (RoPE + cache append + staging) and one attention kernel:
+ * k_attn_fb (prefill over new keys), k_attn_fa (prefill over a cache prefix)
+ * or k_attn_dec (decode and short chunks). Nothing here computes attention on
+ * the host; without a GPU every entry point fails with SMOL_ATTN_ERR_NO_GPU.
  */
 #include <hip/hip_runtime.h>
 
@@ -26,7 +27,6 @@
 #include "attn_internal.h"
 
 extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t st);
-extern "C" int smol_launch_pf(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
 extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
 extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
 extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st);
@@ -484,7 +484,7 @@ struct Plan {
 };
 
 struct CallShape {
-    bool dec;             /* true: fp32 Q staging + k_attn_dec; false: fp16 Q staging + k_attn_pf */
+    bool dec;             /* true: fp32 Q staging + k_attn_dec; false: fp16 Q staging + k_attn_fb / k_attn_fa */
     const void *q, *k, *v;
     int dtype;
     int Hq, Hkv, hd;
@@ -498,14 +498,6 @@ struct CallShape {
     float *out;
 };
 
-/* row tiles (16 rows each) per workgroup of k_attn_pf, within the register
- * file without spilling: 4 up to head_dim 96, 2 at 128, 1 at 256 */
-static int choose_nt(int hd, int max_rows) {
-    int nt = max_rows <= 16 ? 1 : (max_rows <= 32 ? 2 : 4);
-    if (hd > 96 && nt > 2) nt = 2;
-    if (hd > 128) nt = 1;
-    return nt;
-}
 
 /* Row tiles x key splits for every batch. The split size is chosen so the
  * whole call has a few waves per compute unit. */
@@ -517,12 +509,13 @@ static int env_int(const char *name) {
 
 /* waves per SIMD the attention kernel is compiled for: 2 where a wave's
  * registers fit in half the file (latency hidden by the other wave), else 1 */
-static int choose_waves(bool dec, int hd, int nt) {
+/* waves per SIMD k_attn_dec is built for: two when one row tile leaves the
+ * registers for it */
+static int choose_waves_dec(int hd, int nt) {
     const int ov = env_int("SMOL_ATTN_WAVES");
     if (ov == 1 || ov == 2) return ov;
     if (hd > 128) return 1;
-    if (dec) return nt == 1 ? 2 : 1;
-    return (nt == 4 || (nt == 2 && hd > 96)) ? 1 : 2;
+    return nt == 1 ? 2 : 1;
 }
 
 /* rows_per: query rows of one work item; longest_first: order the merge
@@ -554,7 +547,7 @@ static void plan_items(Plan &pl, int Hkv, int G, int window, int rows_per, int c
     /* a workgroup per compute unit and wave slot, each wave >= 2 slabs */
     const long long target_items = (long long)cu_count;
     long long per = (total_slabs * Hkv + target_items - 1) / std::max(1LL, target_items);
-    /* k_attn_pf splits an item's slabs over its 4 waves, k_attn_fa gives each slab to all of them */
+    /* k_attn_dec splits an item's slabs over its 4 waves, k_attn_fa gives each slab to all of them */
     int slabs_per_item = (int)std::max(longest_first ? 4LL : 8LL, per);
     /* tuning override: SMOL_ATTN_SLABS_PER_ITEM=n fixes the key slabs per work item */
     if (const int n = env_int("SMOL_ATTN_SLABS_PER_ITEM")) {
@@ -590,10 +583,10 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     const int G = cs.Hq / cs.Hkv;
     int max_rows = 0;
     for (auto &b : pl.sb) max_rows = std::max(max_rows, b.n_rows);
-    /* prefill kernel: k_attn_fa (waves split the rows, K/V shared through
-     * LDS) unless SMOL_ATTN_PREFILL_KERNEL=pf selects k_attn_pf */
+    /* prefill kernel: k_attn_fb where it applies, else k_attn_fa (waves
+     * split the rows, K/V shared through LDS, split-K across workgroups) */
     const char *pk = getenv("SMOL_ATTN_PREFILL_KERNEL");
-    const bool fa = !cs.dec && !(pk && strcmp(pk, "pf") == 0);
+    const bool fa = !cs.dec;
     /* k_attn_fb (one workgroup per 64-row tile, no merges between
      * workgroups) when every key is in the fresh buffers and the call has
      * enough tiles to occupy the device; SMOL_ATTN_PREFILL_KERNEL=fa keeps
@@ -622,13 +615,10 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
         w = (hd > 128 || env_int("SMOL_ATTN_FA_WAVES") == 1) ? 1 : 2;
         rows_per = 64 * nt;
     } else {
-        nt = cs.dec ? (max_rows <= 16 || hd > 128 ? 1 : 2) : choose_nt(hd, max_rows);
-        if (const int ov = env_int("SMOL_ATTN_NT")) {
-            if ((ov == 1 || ov == 2 || ov == 4) && (ov <= 2 || hd <= 96) && (ov == 1 || hd <= 128) &&
-                !(cs.dec && ov == 4))
-                nt = ov;
-        }
-        w = choose_waves(cs.dec, hd, nt);
+        nt = max_rows <= 16 || hd > 128 ? 1 : 2;
+        if (const int ov = env_int("SMOL_ATTN_NT"))
+            if (ov == 1 || (ov == 2 && hd <= 128)) nt = ov;
+        w = choose_waves_dec(hd, nt);
         rows_per = 16 * nt;
     }
     plan_items(pl, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, fa, fb);
@@ -734,8 +724,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     mk = timing_begin(ctx, 1);
     rc = cs.dec ? smol_launch_dec(&sp, hd, (int)n_items, nt, w, ctx->stream)
          : fb   ? smol_launch_fb(&sp, hd, (int)n_items, nt, ctx->stream)
-         : fa   ? smol_launch_fa(&sp, hd, (int)n_items, nt, w, ctx->stream)
-                : smol_launch_pf(&sp, hd, (int)n_items, nt, w, ctx->stream);
+                : smol_launch_fa(&sp, hd, (int)n_items, nt, w, ctx->stream);
     timing_end(ctx, mk);
     if (rc)
         return fail(rc == -1 ? SMOL_ATTN_ERR_UNSUPPORTED : SMOL_ATTN_ERR_DEVICE,

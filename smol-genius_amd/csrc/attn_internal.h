@@ -57,7 +57,7 @@ typedef struct {
 } SkItem;
 
 /* Q-scratch format written by k_prep (fresh K / V^T are fp16 in both):
- *   SMOL_STAGE_F16    fp16 (the fp16-MFMA kernel k_attn_pf)
+ *   SMOL_STAGE_F16    fp16 (the fp16-MFMA kernels k_attn_fb and k_attn_fa)
  *   SMOL_STAGE_QF32   fp32 (k_attn_dec splits it into bf16 hi + lo for the
  *                     bf16-MFMA cache slabs and rounds it to fp16 for the fresh slab) */
 enum { SMOL_STAGE_F16 = 0, SMOL_STAGE_QF32 = 1 };

@@ -5,16 +5,18 @@
  *               rows: replaces smol_apply_rope_{neox,interleaved} on Q and K
  *               and the K/V row memcpy into the cache
  *               (common/decoder/qkn_decoder.c:493-503 and :647-652).
- *   k_attn_pf   prefill / chunked prefill / bidirectional flash attention on
- *               fp16 MFMA (v_mfma_f32_16x16x32_f16), 64 query rows per
- *               workgroup;
+ *   k_attn_fb   prefill / bidirectional attention whose keys are all new:
+ *               fp16 MFMA (v_mfma_f32_16x16x32_f16), one workgroup per
+ *               64-row tile, K/V staged into LDS by direct transfers;
+ *   k_attn_fa   prefill over an existing cache prefix (and head_dim 256):
+ *               the same LDS image, key ranges split across workgroups;
  *   k_attn_dec  decode and short chunks: bf16 MFMA straight on the bf16 cache
  *               with hi/lo-split Q and P;
- *               both compute the causal / sliding-window / softcap /
+ *               all compute the causal / sliding-window / softcap /
  *               windowed-bidirectional online softmax of
  *               common/kernels/attention.c:32-462 over the bf16 KV cache plus
- *               the call's fresh fp16 keys, splitting long key ranges across
- *               workgroups with a log-sum-exp merge by the last one.
+ *               the call's fresh fp16 keys; split key ranges end in a
+ *               log-sum-exp merge by the group's last workgroup.
  *
  * Numerics: softmax state in fp32 and in log2 units (Q is pre-multiplied by
  * scale * log2 e, so exp(s - m) = exp2(s' - m')). MFMA operands are fp16:
@@ -584,9 +586,14 @@ __device__ __forceinline__ void finish_item(const SkParams &p, const SkItem &it,
  * The slab holding the keys this call appends comes from the fp16 fresh
  * staging (k_prep): each fp16 fragment is split into bf16 hi + lo (exact) in
  * registers and the product takes three bf16 MFMAs (hi.hi, hi.lo, lo.hi).
- * Lane layouts, wave split and merge as k_attn_pf. The running max is a
- * lazy reference: the accumulator is rescaled only when some row's max grows
- * by more than 2^LAZY_T (decided per wave by vote), so p <= 2^LAZY_T.
+ * The four waves of a workgroup stream every fourth 32-key slab of the item
+ * with buffer loads into registers (slab offset in an SGPR) and are combined
+ * by finish_item. S^T = K.Q^T takes K as the A operand with rows gathered as
+ * key(t, m) = 8(m >> 2) + 4t + (m & 3), so a lane's 8 probabilities are 8
+ * consecutive keys and O^T += V^T.P^T reads V^T with one 16-byte load per
+ * lane; a softmax row lives in lanes c, c+16, c+32, c+48. The running max is
+ * a lazy reference: the accumulator is rescaled only when some row's max
+ * grows by more than 2^LAZY_T (decided per wave by vote), so p <= 2^LAZY_T.
  */
 typedef __bf16 b8 __attribute__((ext_vector_type(8)));
 #define LAZY_T 8.0f
@@ -900,238 +907,6 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
     finish_item<HD, NT, W == 1 ? 64 : 32>(p, it, b, item, g, tid, m, l, o, s_o, s_m, s_l, &s_last);
 }
 
-/* ---------------------------------------------------------------- k_attn_pf */
-
-/*
- * Attention for prefill, chunked prefill and windowed bidirectional calls:
- * fp16 MFMA (v_mfma_f32_16x16x32_f16) over the fresh fp16 staging; slabs of
- * an existing bf16 cache prefix are widened to fp16 in registers (exact).
- * A workgroup is SK_WAVES waves on the same NT*16 query rows, each wave
- * streaming every SK_WAVES-th 32-key slab of the item's range from L2 with
- * buffer loads (slab offset in an SGPR, the next slab in flight while the
- * current one is computed); the waves are combined by finish_item. Each K/V
- * element a wave loads is used by NT*16 rows. Lazy rescale and unmasked
- * interior slabs as in k_attn_dec.
- */
-template <int HD, int NT, int W>
-__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W, W))) void k_attn_pf(SkParams p) {
-    constexpr int KS = (HD + 31) / 32;
-    constexpr int DT = (HD + 15) / 16;
-    constexpr int HDP = KS * 32;
-    constexpr int ROWS = NT * 16;
-    constexpr int OSTR = DT * 16 + 4;
-    constexpr unsigned SLAB_BYTES = SMOL_SLAB * HD * 2;
-    const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lane = tid & 63;
-    const int c = lane & 15, j = lane >> 4;
-    /* kv head fastest in the block index: consecutive workgroups go to
-     * consecutive XCDs, so each XCD's L2 holds the K/V of its own heads */
-    const int g = (int)(blockIdx.x % (unsigned)p.Hkv);
-    const int item = (int)(blockIdx.x / (unsigned)p.Hkv);
-    const SkItem it = p.items[item];
-    const SkBatch b = p.batches[it.batch];
-    const int G = p.G;
-    constexpr int SO = (SK_WAVES - 1) * ROWS * OSTR > 2 * SK_MERGE_MAX + 128 ? (SK_WAVES - 1) * ROWS * OSTR
-                                                                          : 2 * SK_MERGE_MAX + 128;
-    __shared__ float s_o[SO];
-    __shared__ float s_m[(SK_WAVES - 1) * ROWS], s_l[(SK_WAVES - 1) * ROWS];
-    __shared__ int s_last;
-
-    h8 qf[NT][KS];
-    int lo[NT], hi[NT];
-    float m[NT], l[NT];
-    f4 o[NT][DT];
-    int lo_max = -(1 << 30), hi_min = 1 << 30;
-#pragma unroll
-    for (int nt = 0; nt < NT; nt++) {
-        const int r = it.row0 + nt * 16 + c;
-        const bool valid = r < b.n_rows;
-        const int qi = r / G;
-        int rl = b.key_lo, rh = b.key_hi;
-        if (b.causal) {
-            rh = min(rh, b.q_pos0 + qi + 1);
-            if (p.window > 0) rl = max(rl, b.q_pos0 + qi - p.window + 1);
-        }
-        lo[nt] = valid ? rl : -(1 << 30);
-        hi[nt] = valid ? rh : (1 << 30);
-        lo_max = max(lo_max, lo[nt]);
-        hi_min = min(hi_min, hi[nt]);
-        m[nt] = -INFINITY;
-        l[nt] = 0.0f;
-        const _Float16 *qrow = p.qs + (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid ? r : 0)) * HDP;
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) qf[nt][ks] = valid ? load_h8(qrow + 32 * ks + 8 * j) : zero_h8();
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++) o[nt][dt] = f4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int sh = 1; sh < 16; sh <<= 1) {
-        lo_max = max(lo_max, __shfl_xor(lo_max, sh));
-        hi_min = min(hi_min, __shfl_xor(hi_min, sh));
-    }
-    lo_max = __builtin_amdgcn_readfirstlane(lo_max);
-    hi_min = __builtin_amdgcn_readfirstlane(hi_min);
-
-    rsrc_t rk_c = make_rsrc(nullptr, 0), rv_c = make_rsrc(nullptr, 0);
-    if (b.slot >= 0 && p.kc != nullptr) {
-        const long long cb = (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * HD;
-        rk_c = make_rsrc(p.kc + cb, (long long)p.cap * HD * 2);
-        rv_c = make_rsrc(p.vtc + cb, (long long)p.cap * HD * 2);
-    }
-    const rsrc_t rk_f = make_rsrc(p.kf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
-    const rsrc_t rv_f = make_rsrc(p.vtf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
-    const int kt_row = 8 * (c >> 2) + (c & 3);
-    unsigned vo_k[2][KS], vo_v[DT];
-#pragma unroll
-    for (int t = 0; t < 2; t++)
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-            const int d0 = 32 * ks + 8 * j;
-            vo_k[t][ks] = (HD % 32 == 0 || d0 < HD) ? (unsigned)(((kt_row + 4 * t) * HD + d0) * 2) : OOB_OFF;
-        }
-#pragma unroll
-    for (int dt = 0; dt < DT; dt++) {
-        const int d = 16 * dt + c;
-        vo_v[dt] = (HD % 16 == 0 || d < HD) ? (unsigned)((d * SMOL_SLAB + 8 * j) * 2) : OOB_OFF;
-    }
-
-    struct KRaw {
-        uint4 k[2][KS];
-    };
-    struct VRaw {
-        uint4 v[DT];
-    };
-    /* slab k0's resource and slab offset (uniform: SGPRs) */
-    auto slab_src = [&](int k0, bool value, rsrc_t &r, unsigned &so) {
-        const bool fr = k0 >= b.fresh_pos0;
-        const int kr = fr ? b.fresh_row0 + (k0 - b.fresh_pos0) : k0;
-        so = (unsigned)(kr / SMOL_SLAB) * SLAB_BYTES;
-        r = value ? (fr ? rv_f : rv_c) : (fr ? rk_f : rk_c);
-    };
-    auto issue_k = [&](int k0, KRaw &r) {
-        rsrc_t rs;
-        unsigned so;
-        slab_src(k0, false, rs, so);
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++) r.k[t][ks] = bload(rs, vo_k[t][ks], so);
-    };
-    auto issue_v = [&](int k0, VRaw &r) {
-        rsrc_t rs;
-        unsigned so;
-        slab_src(k0, true, rs, so);
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++) r.v[dt] = bload(rs, vo_v[dt], so);
-    };
-
-    /* S^T = K . Q^T for the slab */
-    auto qk = [&](const KRaw &r, f4 (&sacc)[NT][2], auto fresh_tag) {
-        constexpr bool FRESH = decltype(fresh_tag)::value;
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
-            h8 kfrag[KS];
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-                kfrag[ks] = FRESH ? *reinterpret_cast<const h8 *>(&r.k[t][ks]) : bf16x8_to_h8(r.k[t][ks]);
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ks = 0; ks < KS; ks++)
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kfrag[ks], qf[nt][ks], acc, 0, 0, 0);
-                sacc[nt][t] = acc;
-            }
-        }
-    };
-    /* mask / softcap, online softmax, O^T += V^T . P^T */
-    auto smpv = [&](int k0, const f4 (&sacc)[NT][2], const VRaw &r, auto fresh_tag) {
-        constexpr bool FRESH = decltype(fresh_tag)::value;
-        h8 vfrag[DT];
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++)
-            vfrag[dt] = FRESH ? *reinterpret_cast<const h8 *>(&r.v[dt]) : bf16x8_to_h8(r.v[dt]);
-        const bool full = k0 >= lo_max && k0 + SMOL_SLAB <= hi_min;
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            float sv[8];
-#pragma unroll
-            for (int t = 0; t < 2; t++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) sv[4 * t + i] = sacc[nt][t][i];
-            if (p.cap2 > 0.0f) {
-#pragma unroll
-                for (int e = 0; e < 8; e++) sv[e] = p.cap2 * tanhf(sv[e] / p.cap2);
-            }
-            if (!full) {
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const int key = k0 + 8 * j + e;
-                    sv[e] = (key >= lo[nt] && key < hi[nt]) ? sv[e] : -INFINITY;
-                }
-            }
-            float mx = sv[0];
-#pragma unroll
-            for (int e = 1; e < 8; e++) mx = fmaxf(mx, sv[e]);
-            mx = row_max4(mx);
-            const bool need = mx > m[nt] + LAZY_T;
-            if (__any(need)) {
-                const float m_new = need ? mx : m[nt];
-                const float alpha = need ? __builtin_amdgcn_exp2f(m[nt] - m_new) : 1.0f;
-#pragma unroll
-                for (int dt = 0; dt < DT; dt++) o[nt][dt] *= alpha;
-                l[nt] *= alpha;
-                m[nt] = m_new;
-            }
-            const float m_use = m[nt] == -INFINITY ? 0.0f : m[nt];
-            h8 pf;
-            float ps = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float pe = __builtin_amdgcn_exp2f(sv[e] - m_use);
-                ps += pe;
-                pf[e] = (_Float16)pe;
-            }
-            l[nt] += ps;
-#pragma unroll
-            for (int dt = 0; dt < DT; dt++)
-                o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vfrag[dt], pf, o[nt][dt], 0, 0, 0);
-        }
-    };
-
-    /* Each wave streams slabs wave, wave + SK_WAVES, ... with one K and one V
-     * register buffer: the next slab's K is requested as soon as the current
-     * S is formed and its V as soon as the current P.V is issued, so each
-     * load has about half a slab of work to arrive. The request is made on
-     * every path (past the end it re-reads the current slab), so every wait
-     * sees the same number of loads in flight. */
-    const int step = SMOL_SLAB * SK_WAVES;
-    const int end = it.key_end;
-    int k0 = it.key_begin + wave * SMOL_SLAB;
-    if (k0 < end) {
-        KRaw kr;
-        VRaw vr;
-        issue_k(k0, kr);
-        issue_v(k0, vr);
-        while (true) {
-            const int k1 = k0 + step;
-            const int kn = k1 < end ? k1 : k0;
-            f4 sacc[NT][2];
-            const bool fr = k0 >= b.fresh_pos0;
-            if (fr) qk(kr, sacc, std::true_type{});
-            else qk(kr, sacc, std::false_type{});
-            issue_k(kn, kr);
-            if (fr) smpv(k0, sacc, vr, std::true_type{});
-            else smpv(k0, sacc, vr, std::false_type{});
-            issue_v(kn, vr);
-            if (k1 >= end) break;
-            k0 = k1;
-        }
-    }
-    finish_item<HD, NT>(p, it, b, item, g, tid, m, l, o, s_o, s_m, s_l, &s_last);
-}
-
 /* ---------------------------------------------------------------- k_attn_fa */
 
 /*
@@ -1164,7 +939,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
  * those slots are never stored), so padded head dims contribute 0 * 0. V^T
  * rows past head_dim only feed output rows that are never written.
  *
- * Softmax, lazy rescale and MFMA layouts as in k_attn_pf; each wave holds
+ * Softmax, lazy rescale and MFMA layouts as in k_attn_dec; each wave holds
  * whole rows, so no cross-wave combine is needed.
  */
 template <int HD>
@@ -1971,11 +1746,12 @@ static void launch_dec_v(const SkParams *sp, dim3 grid, hipStream_t st) {
 
 template <int HD>
 static int launch_dec_hd(const SkParams *sp, int n_items, int nt, int w, hipStream_t st) {
+    /* two waves per SIMD only where the registers allow it (one row tile,
+     * head_dim <= 128); other requests run at one */
     const dim3 grid(n_items * sp->Hkv);
-    if (nt == 1 && w == 1) launch_dec_v<HD, 1, 1>(sp, grid, st);
-    else if (nt == 1 && w == 2) launch_dec_v<HD, 1, 2>(sp, grid, st);
-    else if (nt == 2 && w == 1 && HD <= 128) launch_dec_v<HD, (HD <= 128 ? 2 : 1), 1>(sp, grid, st);
-    else if (nt == 2 && w == 2 && HD <= 128) launch_dec_v<HD, (HD <= 128 ? 2 : 1), 2>(sp, grid, st);
+    if (nt == 1 && w == 2 && HD <= 128) launch_dec_v<HD, 1, (HD <= 128 ? 2 : 1)>(sp, grid, st);
+    else if (nt == 1) launch_dec_v<HD, 1, 1>(sp, grid, st);
+    else if (nt == 2 && HD <= 128) launch_dec_v<HD, (HD <= 128 ? 2 : 1), 1>(sp, grid, st);
     else return -1;
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
@@ -1989,37 +1765,6 @@ extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, 
     case 96: return launch_dec_hd<96>(sp, n_items, nt, w, st);
     case 128: return launch_dec_hd<128>(sp, n_items, nt, w, st);
     case 256: return launch_dec_hd<256>(sp, n_items, nt, w, st);
-    default: return -1;
-    }
-}
-
-template <int HD, int NT, int W>
-static void launch_pf_v(const SkParams *sp, dim3 grid, hipStream_t st) {
-    hipLaunchKernelGGL((k_attn_pf<HD, NT, W>), grid, dim3(64 * SK_WAVES), 0, st, *sp);
-}
-
-template <int HD>
-static int launch_pf_hd(const SkParams *sp, int n_items, int nt, int w, hipStream_t st) {
-    const dim3 grid(n_items * sp->Hkv);
-    if (nt == 1 && w == 1) launch_pf_v<HD, 1, 1>(sp, grid, st);
-    else if (nt == 1 && w == 2) launch_pf_v<HD, 1, 2>(sp, grid, st);
-    else if (nt == 2 && w == 1 && HD <= 128) launch_pf_v<HD, (HD <= 128 ? 2 : 1), 1>(sp, grid, st);
-    else if (nt == 2 && w == 2 && HD <= 128) launch_pf_v<HD, (HD <= 128 ? 2 : 1), 2>(sp, grid, st);
-    else if (nt == 4 && w == 1 && HD <= 96) launch_pf_v<HD, (HD <= 96 ? 4 : 1), 1>(sp, grid, st);
-    else if (nt == 4 && w == 2 && HD <= 96) launch_pf_v<HD, (HD <= 96 ? 4 : 1), 2>(sp, grid, st);
-    else return -1;
-    return hipGetLastError() == hipSuccess ? 0 : -3;
-}
-
-extern "C" int smol_launch_pf(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st) {
-    if (n_items <= 0) return 0;
-    switch (hd) {
-    case 64: return launch_pf_hd<64>(sp, n_items, nt, w, st);
-    case 72: return launch_pf_hd<72>(sp, n_items, nt, w, st);
-    case 80: return launch_pf_hd<80>(sp, n_items, nt, w, st);
-    case 96: return launch_pf_hd<96>(sp, n_items, nt, w, st);
-    case 128: return launch_pf_hd<128>(sp, n_items, nt, w, st);
-    case 256: return launch_pf_hd<256>(sp, n_items, nt, w, st);
     default: return -1;
     }
 }

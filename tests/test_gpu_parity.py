@@ -131,6 +131,7 @@ CAUSAL_SHAPES = [  # Hq, Hkv, hd, seq_q, seq_k, q_offset, bf16
     (4, 1, 96, 40, 40, 0, True), (16, 8, 128, 1, 1, 0, False), (16, 8, 128, 70, 130, 60, True),
     (8, 1, 256, 3, 200, 197, False), (2, 2, 256, 48, 48, 0, True), (32, 2, 128, 2, 90, 88, False),
     (4, 2, 64, 9, 20, -3, False), (4, 2, 128, 6, 10, 30, False), (16, 16, 64, 100, 300, 200, True),
+    (4, 2, 256, 70, 70, 0, True), (8, 4, 128, 40, 200, 160, False), (6, 3, 96, 130, 130, 0, True),
 ]
 
 
@@ -199,7 +200,8 @@ def test_bidirectional_ragged(ctx, sa, oracle):
         assert not got[:lo].any()
 
 
-@pytest.mark.parametrize("P,S", [(0, 1), (0, 33), (5, 7), (31, 1), (32, 32), (40, 64), (63, 2), (100, 26)])
+@pytest.mark.parametrize("P,S", [(0, 1), (0, 33), (5, 7), (31, 1), (32, 32), (40, 64), (63, 2), (100, 26),
+                                 (64, 100), (250, 130)])
 @pytest.mark.parametrize("rope_type", [0, 1])
 def test_prefill_chunks(ctx, sa, oracle, wo, P, S, rope_type):
     from smol_genius_amd.workloads import Prefill
