@@ -27,7 +27,7 @@
 #include "attn_internal.h"
 
 extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t st);
-extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
+extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, int w, int staged, hipStream_t st);
 extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
 extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st);
 extern "C" int smol_launch_rope_apply(float *x, const float *cos_t, const float *sin_t,
@@ -481,6 +481,7 @@ struct Plan {
     int n_groups = 0;
     int q_rows = 0;      /* Q scratch rows per KV head */
     int fresh_rows = 0;  /* fresh rows per KV head */
+    bool staged_ok = true; /* every item fits the staged decode kernel's LDS */
 };
 
 struct CallShape {
@@ -522,7 +523,7 @@ static int choose_waves_dec(int hd, int nt) {
  * groups by descending key count, so the last workgroups dispatched are the
  * short ones */
 static void plan_items(Plan &pl, int Hkv, int G, int window, int rows_per, int cu_count, bool longest_first,
-                       bool no_split = false) {
+                       bool no_split = false, int max_slabs = 0) {
     struct Tile { int batch, row0, lo, hi; };
     std::vector<Tile> tiles;
     long long total_slabs = 0;
@@ -548,17 +549,21 @@ static void plan_items(Plan &pl, int Hkv, int G, int window, int rows_per, int c
     const long long target_items = (long long)cu_count;
     long long per = (total_slabs * Hkv + target_items - 1) / std::max(1LL, target_items);
     /* k_attn_dec splits an item's slabs over its 4 waves, k_attn_fa gives each slab to all of them */
-    int slabs_per_item = (int)std::max(longest_first ? 4LL : 8LL, per);
+    int slabs_per_item = (int)std::max(max_slabs ? 2LL : (longest_first ? 4LL : 8LL), per);
+    if (max_slabs) slabs_per_item = std::min(slabs_per_item, max_slabs);
     /* tuning override: SMOL_ATTN_SLABS_PER_ITEM=n fixes the key slabs per work item */
     if (const int n = env_int("SMOL_ATTN_SLABS_PER_ITEM")) {
         if (n > 0) slabs_per_item = n;
     }
+    if (max_slabs) slabs_per_item = std::min(slabs_per_item, max_slabs); /* the staged kernel's LDS holds no more */
     if (no_split) slabs_per_item = 1 << 28;
     int group = 0;
-    const int max_split = 1024 / rows_per; /* the kernel's merge holds rows * n_split pairs in LDS */
+    const int max_split = SK_MERGE_MAX / rows_per; /* the kernel's merge holds rows * n_split pairs in LDS */
     for (const Tile &t : tiles) {
         const int n_slabs = (t.hi - t.lo + SMOL_SLAB - 1) / SMOL_SLAB;
-        const int n_split = std::min(max_split, std::max(1, (n_slabs + slabs_per_item - 1) / slabs_per_item));
+        const int want = std::max(1, (n_slabs + slabs_per_item - 1) / slabs_per_item);
+        if (max_slabs && want > max_split) pl.staged_ok = false; /* items would outgrow the staged LDS */
+        const int n_split = std::min(max_split, want);
         const int per_split = (n_slabs + n_split - 1) / std::max(1, n_split);
         int made = 0;
         std::vector<SkItem> tmp;
@@ -621,7 +626,20 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
         w = choose_waves_dec(hd, nt);
         rows_per = 16 * nt;
     }
-    plan_items(pl, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, fa, fb);
+    /* decode streams slabs through registers; SMOL_ATTN_DEC_STAGED=1 selects
+     * k_attn_dec's staged build (every slab of an item DMA'd into LDS at once),
+     * which measured no faster on the decode workloads */
+    bool staged = cs.dec && env_int("SMOL_ATTN_DEC_STAGED") == 1;
+    {
+        Plan trial = pl;
+        plan_items(trial, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, fa, fb, staged ? (hd > 128 ? 5 : 4) : 0);
+        if (!trial.staged_ok) {
+            staged = false;
+            plan_items(pl, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, fa, fb, 0);
+        } else {
+            pl = std::move(trial);
+        }
+    }
     /* SMOL_ATTN_FA_QDIRECT=1: k_attn_fa rotates and scales Q as it loads it
      * and the pre-pass only handles the new K/V */
     const bool q_direct = fa && !fb && env_int("SMOL_ATTN_FA_QDIRECT") == 1;
@@ -722,7 +740,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
         sp.qscale = pp.qscale;
     }
     mk = timing_begin(ctx, 1);
-    rc = cs.dec ? smol_launch_dec(&sp, hd, (int)n_items, nt, w, ctx->stream)
+    rc = cs.dec ? smol_launch_dec(&sp, hd, (int)n_items, nt, w, staged ? 1 : 0, ctx->stream)
          : fb   ? smol_launch_fb(&sp, hd, (int)n_items, nt, ctx->stream)
                 : smol_launch_fa(&sp, hd, (int)n_items, nt, w, ctx->stream);
     timing_end(ctx, mk);

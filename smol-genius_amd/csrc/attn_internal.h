@@ -22,6 +22,7 @@
 #include <stdint.h>
 
 #define SMOL_SLAB 32          /* keys per inner step of the attention kernels */
+#define SK_MERGE_MAX 4096     /* max rows * n_split of one split-K merge group (the merge's LDS) */
 #define SMOL_ROWS_PER_TILE 16 /* query rows per MFMA tile (16x16x32 f16) */
 
 enum { SMOL_IN_F32 = 0, SMOL_IN_BF16 = 1 };

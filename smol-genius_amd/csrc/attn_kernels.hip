@@ -336,8 +336,13 @@ __device__ __forceinline__ float2 load_f2_sc1(rsrc_t r, unsigned voff) {
     return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
 }
 
+/* one 1 KB direct-to-LDS transfer: lane l's 16 bytes land at lds + 16 l */
+__device__ __forceinline__ void dma_1k(rsrc_t r, unsigned voff, unsigned soff, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
+                 : "memory");
+}
+
 #define SK_WAVES 4
-#define SK_MERGE_MAX 1024 /* max ROWS * n_split of one merge group (LDS) */
 
 /* Reductions over the four lanes c, c+16, c+32, c+48 that hold one softmax
  * row, with the gfx950 cross-row swaps (VALU, no LDS round trip). Each swap
@@ -609,7 +614,7 @@ __device__ __forceinline__ void split8(const float *x, b8 &hi, b8 &lo) {
     }
 }
 
-template <int HD, int NT, int W>
+template <int HD, int NT, int W, bool ST>
 __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W, W))) void k_attn_dec(SkParams p) {
     constexpr int KS = (HD + 31) / 32;
     constexpr int DT = (HD + 15) / 16;
@@ -617,8 +622,15 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
     constexpr int ROWS = NT * 16;
     constexpr int OSTR = DT * 16 + 4;
     constexpr unsigned SLAB_K_BYTES = SMOL_SLAB * HD * 2; /* one slab of K, and one slab-block of V^T */
-    /* two slabs in flight per wave where the registers allow */
-    constexpr bool DBUF = W == 1 && HD <= 128;
+    /* ST: every slab of the item (at most SMAX) is requested at once into
+     * LDS by direct transfers, before Q is read; the waves then take their
+     * slabs' fragments from LDS. Otherwise each wave loads its slabs'
+     * fragments into registers, one slab ahead. */
+    constexpr int KROW = HD <= 128 ? 256 : 512; /* LDS bytes per key row */
+    constexpr int K_LDS = SMOL_SLAB * KROW, V_LDS = 16 * DT * 64;
+    constexpr int SLAB_LDS = (K_LDS + V_LDS + 4095) / 4096 * 4096;
+    constexpr int NDMA = SLAB_LDS / 4096; /* transfers per wave per slab */
+    constexpr int SMAX = ST ? (HD > 128 ? 5 : 4) : 0;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
@@ -632,9 +644,15 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
     const int G = p.G;
     constexpr int SO = (SK_WAVES - 1) * ROWS * OSTR > 2 * SK_MERGE_MAX + 128 ? (SK_WAVES - 1) * ROWS * OSTR
                                                                           : 2 * SK_MERGE_MAX + 128;
-    __shared__ float s_o[SO];
-    __shared__ float s_m[(SK_WAVES - 1) * ROWS], s_l[(SK_WAVES - 1) * ROWS];
-    __shared__ int s_last;
+    /* the epilogue's arrays; with ST they reuse the slab area once every
+     * wave is done with it */
+    constexpr int FIN_BYTES = (SO + 2 * (SK_WAVES - 1) * ROWS + 1) * 4;
+    constexpr int SMEM = SMAX * SLAB_LDS > FIN_BYTES ? SMAX * SLAB_LDS : FIN_BYTES;
+    static_assert(SMEM <= 160 * 1024, "LDS");
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[SMEM];
+    float *s_o = reinterpret_cast<float *>(smem);
+    float *s_m = s_o + SO, *s_l = s_m + (SK_WAVES - 1) * ROWS;
+    int *s_last = reinterpret_cast<int *>(s_l + (SK_WAVES - 1) * ROWS);
 
     b8 qh[NT][KS], ql[NT][KS];
     int lo[NT], hi[NT];
@@ -852,59 +870,102 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
         }
     };
 
-    /* Each wave streams slabs wave, wave + SK_WAVES, ... with two K/V
-     * register buffers: slabs i and i+1 are in flight while slab i is
-     * computed, and the first two are requested before Q is loaded. A
-     * request past the wave's last slab re-reads that slab, so every wait
-     * sees the same number of loads in flight. */
     const int step = SMOL_SLAB * SK_WAVES;
     const int end = it.key_end;
-    int k0 = it.key_begin + wave * SMOL_SLAB;
-    if (k0 < end) {
-        int last = k0 + ((end - 1 - k0) / step) * step; /* this wave's last slab */
-        auto clampk = [&](int k) __attribute__((always_inline)) { return k < last ? k : last; };
-        auto slab = [&](int kk, KRaw &kr, VRaw &vr, int ahead) __attribute__((always_inline)) {
+    if constexpr (ST) {
+        /* all n <= SMAX slabs of the item into LDS (slab s at s * SLAB_LDS,
+         * the image of k_attn_fb: K rows XOR-swizzled, V^T rows of 64 bytes) */
+        const int n = min(SMAX, (end - it.key_begin + SMOL_SLAB - 1) / SMOL_SLAB); /* the host plans n <= SMAX */
+        unsigned d_off[NDMA];
+        bool d_isk[NDMA];
+#pragma unroll
+        for (int e = 0; e < NDMA; e++) {
+            const int q = wave + 4 * e;
+            d_isk[e] = q * 1024 < K_LDS;
+            if (d_isk[e]) {
+                constexpr int RPR = 1024 / KROW, SPR = KROW / 16; /* rows per region, slots per row */
+                const int kr = q * RPR + lane / SPR, slot = lane % SPR;
+                const int cb = slot ^ ((kr & 3) | (((kr >> 3) & 3) << 2));
+                d_off[e] = cb < HD / 8 ? (unsigned)((kr * HD + cb * 8) * 2) : OOB_OFF;
+            } else {
+                const int d = (q * 1024 - K_LDS) / 64 + (lane >> 2), slot = lane & 3;
+                const int jj = slot ^ ((d >> 1) & 3);
+                d_off[e] = (d < HD && q * 1024 < K_LDS + V_LDS) ? (unsigned)((d * SMOL_SLAB + jj * 8) * 2) : OOB_OFF;
+            }
+        }
+        const unsigned lds0 = (unsigned)(size_t)smem;
+#pragma unroll
+        for (int sl = 0; sl < SMAX; sl++) {
+            if (sl >= n) break;
+            rsrc_t rk, rv;
+            unsigned so;
+            slab_src(it.key_begin + SMOL_SLAB * sl, false, rk, so);
+            slab_src(it.key_begin + SMOL_SLAB * sl, true, rv, so);
+#pragma unroll
+            for (int e = 0; e < NDMA; e++)
+                dma_1k(d_isk[e] ? rk : rv, d_off[e], so,
+                       __builtin_amdgcn_readfirstlane(lds0 + sl * SLAB_LDS + (wave + 4 * e) * 1024));
+        }
+        load_q();
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const int kt_row = 8 * (c >> 2) + (c & 3);
+        unsigned kfo[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) kfo[ks] = (unsigned)(kt_row * KROW + 16 * ((4 * ks + j) ^ c));
+        const unsigned vfo = (unsigned)(K_LDS + c * 64 + 16 * (j ^ ((c >> 1) & 3)));
+        for (int sl = wave; sl < n; sl += SK_WAVES) {
+            const unsigned char *base = smem + sl * SLAB_LDS;
+            const int kk = it.key_begin + SMOL_SLAB * sl;
+            KRaw kr;
+            VRaw vr;
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) kr.k[t][ks] = *reinterpret_cast<const uint4 *>(base + kfo[ks] + t * 4 * KROW);
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) vr.v[dt] = *reinterpret_cast<const uint4 *>(base + vfo + dt * 1024);
             f4 sacc[NT][2];
             const bool fr = kk >= b.fresh_pos0;
             if (fr) qk(kr, sacc, std::true_type{});
             else qk(kr, sacc, std::false_type{});
-            issue_k(clampk(kk + ahead), kr);
             if (fr) smpv(kk, sacc, vr, std::true_type{});
             else smpv(kk, sacc, vr, std::false_type{});
-            issue_v(clampk(kk + ahead), vr);
-        };
-        if constexpr (DBUF) {
-            KRaw ka, kb;
-            VRaw va, vb;
-            issue_k(k0, ka);
-            issue_v(k0, va);
-            issue_k(clampk(k0 + step), kb);
-            issue_v(clampk(k0 + step), vb);
-            load_q();
-            while (true) {
-                slab(k0, ka, va, 2 * step);
-                if (k0 + step >= end) break;
-                slab(k0 + step, kb, vb, 2 * step);
-                k0 += 2 * step;
-                if (k0 >= end) break;
-            }
-        } else {
+        }
+        __syncthreads(); /* the slab area becomes the epilogue's */
+    } else {
+        /* Each wave streams slabs wave, wave + SK_WAVES, ... with one K/V
+         * register buffer, the next slab requested while the current one is
+         * computed and the first one before Q is loaded. A request past the
+         * wave's last slab re-reads that slab, so every wait sees the same
+         * number of loads in flight. */
+        int k0 = it.key_begin + wave * SMOL_SLAB;
+        if (k0 < end) {
+            const int last = k0 + ((end - 1 - k0) / step) * step; /* this wave's last slab */
             KRaw kr;
             VRaw vr;
             issue_k(k0, kr);
             issue_v(k0, vr);
             load_q();
             while (true) {
-                slab(k0, kr, vr, step);
+                const int kn = k0 + step < last ? k0 + step : last;
+                f4 sacc[NT][2];
+                const bool fr = k0 >= b.fresh_pos0;
+                if (fr) qk(kr, sacc, std::true_type{});
+                else qk(kr, sacc, std::false_type{});
+                issue_k(kn, kr);
+                if (fr) smpv(k0, sacc, vr, std::true_type{});
+                else smpv(k0, sacc, vr, std::false_type{});
+                issue_v(kn, vr);
                 k0 += step;
                 if (k0 >= end) break;
             }
+        } else {
+            load_q();
         }
-    } else {
-        load_q();
     }
 
-    finish_item<HD, NT, W == 1 ? 64 : 32>(p, it, b, item, g, tid, m, l, o, s_o, s_m, s_l, &s_last);
+    finish_item<HD, NT, W == 1 ? 64 : 32>(p, it, b, item, g, tid, m, l, o, s_o, s_m, s_l, s_last);
 }
 
 /* ---------------------------------------------------------------- k_attn_fa */
@@ -1354,12 +1415,6 @@ struct FbGeom {
     static constexpr int GROUP_BYTES = NSTG * STAGE;
 };
 
-/* one 1 KB direct-to-LDS transfer: lane l's 16 bytes land at lds + 16 l */
-__device__ __forceinline__ void dma_1k(rsrc_t r, unsigned voff, unsigned soff, unsigned lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
-                 : "memory");
-}
-
 template <int HD, int NT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attn_fb(SkParams p) {
     using Gm = FbGeom<HD>;
@@ -1740,31 +1795,34 @@ extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t 
 }
 
 template <int HD, int NT, int W>
-static void launch_dec_v(const SkParams *sp, dim3 grid, hipStream_t st) {
-    hipLaunchKernelGGL((k_attn_dec<HD, NT, W>), grid, dim3(64 * SK_WAVES), 0, st, *sp);
+static void launch_dec_v(const SkParams *sp, dim3 grid, bool staged, hipStream_t st) {
+    if (staged) hipLaunchKernelGGL((k_attn_dec<HD, NT, W, true>), grid, dim3(64 * SK_WAVES), 0, st, *sp);
+    else hipLaunchKernelGGL((k_attn_dec<HD, NT, W, false>), grid, dim3(64 * SK_WAVES), 0, st, *sp);
 }
 
 template <int HD>
-static int launch_dec_hd(const SkParams *sp, int n_items, int nt, int w, hipStream_t st) {
+static int launch_dec_hd(const SkParams *sp, int n_items, int nt, int w, bool staged, hipStream_t st) {
     /* two waves per SIMD only where the registers allow it (one row tile,
      * head_dim <= 128); other requests run at one */
     const dim3 grid(n_items * sp->Hkv);
-    if (nt == 1 && w == 2 && HD <= 128) launch_dec_v<HD, 1, (HD <= 128 ? 2 : 1)>(sp, grid, st);
-    else if (nt == 1) launch_dec_v<HD, 1, 1>(sp, grid, st);
-    else if (nt == 2 && HD <= 128) launch_dec_v<HD, (HD <= 128 ? 2 : 1), 1>(sp, grid, st);
+    if (nt == 1 && w == 2 && HD <= 128) launch_dec_v<HD, 1, (HD <= 128 ? 2 : 1)>(sp, grid, staged, st);
+    else if (nt == 1) launch_dec_v<HD, 1, 1>(sp, grid, staged, st);
+    else if (nt == 2 && HD <= 128) launch_dec_v<HD, (HD <= 128 ? 2 : 1), 1>(sp, grid, staged, st);
     else return -1;
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st) {
+/* staged: every slab of an item goes to LDS in one round of direct
+ * transfers (items of at most smol_dec_staged_slabs(hd) slabs) */
+extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, int w, int staged, hipStream_t st) {
     if (n_items <= 0) return 0;
     switch (hd) {
-    case 64: return launch_dec_hd<64>(sp, n_items, nt, w, st);
-    case 72: return launch_dec_hd<72>(sp, n_items, nt, w, st);
-    case 80: return launch_dec_hd<80>(sp, n_items, nt, w, st);
-    case 96: return launch_dec_hd<96>(sp, n_items, nt, w, st);
-    case 128: return launch_dec_hd<128>(sp, n_items, nt, w, st);
-    case 256: return launch_dec_hd<256>(sp, n_items, nt, w, st);
+    case 64: return launch_dec_hd<64>(sp, n_items, nt, w, staged != 0, st);
+    case 72: return launch_dec_hd<72>(sp, n_items, nt, w, staged != 0, st);
+    case 80: return launch_dec_hd<80>(sp, n_items, nt, w, staged != 0, st);
+    case 96: return launch_dec_hd<96>(sp, n_items, nt, w, staged != 0, st);
+    case 128: return launch_dec_hd<128>(sp, n_items, nt, w, staged != 0, st);
+    case 256: return launch_dec_hd<256>(sp, n_items, nt, w, staged != 0, st);
     default: return -1;
     }
 }
@@ -1777,13 +1835,14 @@ static void launch_fa_v(const SkParams *sp, dim3 grid, hipStream_t st) {
 /* w: waves per SIMD the kernel is built for (2 with fewer staged slabs) */
 template <int HD>
 static int launch_fa_hd(const SkParams *sp, int n_items, int nt, int w, hipStream_t st) {
-    constexpr int NT2 = HD <= 128 ? 2 : 1;
     const dim3 grid(n_items * sp->Hkv);
     if (nt == 1 && w == 1) launch_fa_v<HD, 1, 1>(sp, grid, st);
-    else if (nt == 1 && w == 2) launch_fa_v<HD, 1, 2>(sp, grid, st);
-    else if (nt == 2 && w == 1 && HD <= 128) launch_fa_v<HD, NT2, 1>(sp, grid, st);
-    else if (nt == 2 && w == 2 && HD <= 128) launch_fa_v<HD, NT2, 2>(sp, grid, st);
-    else return -1;
+    else if constexpr (HD <= 128) { /* two tiles or two waves per SIMD fit the registers */
+        if (nt == 1 && w == 2) launch_fa_v<HD, 1, 2>(sp, grid, st);
+        else if (nt == 2 && w == 1) launch_fa_v<HD, 2, 1>(sp, grid, st);
+        else if (nt == 2 && w == 2) launch_fa_v<HD, 2, 2>(sp, grid, st);
+        else return -1;
+    } else return -1;
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 

@@ -240,6 +240,20 @@ def test_decode_positions(ctx, sa, oracle, wo, positions):
         assert_parity(r.outputs(), wo.decode(oracle, wl, x), "decode %s hd %d" % (positions, hd))
 
 
+@pytest.mark.parametrize("positions", [[0], [33], [64, 0, 95, 7], [1000, 31, 4095]])
+def test_decode_positions_staged(ctx, sa, oracle, wo, positions, monkeypatch):
+    """The same cases through k_attn_dec's staged build (all slabs of an item
+    in LDS at once)."""
+    monkeypatch.setenv("SMOL_ATTN_DEC_STAGED", "1")
+    test_decode_positions(ctx, sa, oracle, wo, positions)
+
+
+@pytest.mark.parametrize("name", ["qwen06b_decode", "gemma_mqa_decode", "qwen17b_stream"])
+def test_workload_full_size_staged_decode(ctx, oracle, wo, name, monkeypatch):
+    monkeypatch.setenv("SMOL_ATTN_DEC_STAGED", "1")
+    test_workload_full_size(ctx, oracle, wo, name)
+
+
 def test_cache_roundtrip_growth_and_rewind(ctx, sa, oracle, wo):
     from smol_genius_amd.workloads import Prefill
     Hkv, hd = 2, 64
