@@ -11,7 +11,8 @@ attention). Steps rotate over `layers` distinct caches and input sets
 last-level cache.
 
 The other workloads (decode, bidirectional, MQA decode, streaming chunk +
-decode) are measured the same way and reported under "detail".
+decode, and the decode step and prefill with the per-head Q/K RMSNorm fused
+into the pre-pass) are measured the same way and reported under "detail".
 
 value / ms_per_step: wall clock over the timed steps with nothing but the
 library's own launches in the stream.
@@ -155,7 +156,8 @@ def main():
         head = None
 
     # ---------------- the other workloads
-    for name in ["qwen06b_decode", "gemma_mqa_decode", "siglip_bidir", "qwen17b_stream"]:
+    for name in ["qwen06b_decode", "gemma_mqa_decode", "siglip_bidir", "qwen17b_stream", "qwen06b_decode_qknorm",
+                 "qwen06b_prefill_qknorm"]:
         if args.only not in (None, name):
             continue
         wl = wls[name]
@@ -175,7 +177,11 @@ def main():
         prep_ms = kt["prep"][0] / max(1, kt["prep"][1])
         d = {"config": wl.describe(), "layers_rotated": n_layers, "ms_per_step": round(wall / steps * 1e3, 5),
              "attn_kernel_ms": round(attn_ms, 5), "prep_kernel_ms": round(prep_ms, 5)}
-        if name == "siglip_bidir":
+        if name == "qwen06b_prefill_qknorm":
+            f = wl.flops()
+            d.update(tflops_kernel=round(f / (attn_ms * 1e-3) / 1e12, 3),
+                     tflops_step=round(f / (wall / steps) / 1e12, 3))
+        elif name == "siglip_bidir":
             f = wl.flops()
             d.update(tflops_kernel=round(f / (attn_ms * 1e-3) / 1e12, 3),
                      mfma_frac=round(f / (attn_ms * 1e-3) / 1e12 / PEAK_MFMA_TFLOPS, 5),

@@ -157,6 +157,26 @@ SMOL_ATTN_API int smol_attn_decode(smol_attn_ctx *ctx, smol_kv_cache *kv, int la
                                    const void *v_new, int dtype, int n_heads, float scale,
                                    int window, float cap, float *out);
 
+/* The two calls above with the per-head Q/K RMSNorm of the reference
+ * decoders fused in front of RoPE (qkn_decoder.c:487-491 and :640-644,
+ * rmsnorm.c:78-140): each head_dim segment of q and of k_new becomes
+ * x * w[d] / sqrt(mean(x^2) + eps) before it is rotated. q_norm / k_norm are
+ * device fp32 [head_dim] weights (NULL skips that norm, as a NULL
+ * q_norm_weight / k_norm_weight does in the reference); loaders that fold
+ * Gemma's 1 + w into the weight (gemma.c:166-169) pass the folded weight. */
+SMOL_ATTN_API int smol_attn_prefill_qknorm(smol_attn_ctx *ctx, smol_kv_cache *kv, int layer, int slot,
+                                           const smol_rope_table *rope, int pos0, int seq_q,
+                                           const void *q, const void *k_new, const void *v_new,
+                                           int dtype, int n_heads, float scale, int window, float cap,
+                                           const float *q_norm, const float *k_norm, float eps,
+                                           float *out);
+SMOL_ATTN_API int smol_attn_decode_qknorm(smol_attn_ctx *ctx, smol_kv_cache *kv, int layer,
+                                          const smol_rope_table *rope, int n_seq, const int *slots,
+                                          const int *pos, const void *q, const void *k_new,
+                                          const void *v_new, int dtype, int n_heads, float scale,
+                                          int window, float cap, const float *q_norm,
+                                          const float *k_norm, float eps, float *out);
+
 /* Causal attention on flat device arrays, no cache and no RoPE: the device
  * form of smol_causal_attention (attention.c:153-170). K, V: [seq_k][n_kv*hd]. */
 SMOL_ATTN_API int smol_attn_causal(smol_attn_ctx *ctx, const void *q, const void *k,
@@ -178,6 +198,15 @@ SMOL_ATTN_API int smol_attn_bidirectional(smol_attn_ctx *ctx, const void *q, con
  * smol_apply_rope_{neox,interleaved} (rope.c:68-164). */
 SMOL_ATTN_API int smol_attn_apply_rope(smol_attn_ctx *ctx, const smol_rope_table *rope, float *x,
                                        const int *positions, int seq, int n_heads);
+
+/* In place on a device fp32 array x [seq][n_heads*head_dim]: per-head
+ * RMSNorm with the device weight [head_dim] (skipped when weight is NULL;
+ * the device form of smol_rms_norm_per_head, rmsnorm.c:78-140), then RoPE
+ * with row s at table position positions[s] (skipped when rope is NULL;
+ * positions is then unused). */
+SMOL_ATTN_API int smol_attn_norm_rope(smol_attn_ctx *ctx, const smol_rope_table *rope, float *x,
+                                      const float *weight, float eps, const int *positions, int seq,
+                                      int n_heads, int head_dim);
 
 #ifdef __cplusplus
 }

@@ -4,7 +4,8 @@
  *
  * Each prototype below is the one in the reference's
  * common/kernels/smol_kernels.h (line numbers given); linking libsmol_attn.so
- * in place of common/kernels/{attention,rope}.c makes the existing callers
+ * in place of common/kernels/{attention,rope}.c (and rmsnorm.c's per-head
+ * norm) makes the existing callers
  * (qkn_decoder.c:425-528 / :615-677, siglip.c:126, encoder.c:463, nomic.c:180,
  * smolvlm/decoder.c:340, :454) run on the GPU unchanged.
  *
@@ -77,6 +78,12 @@ SMOL_KERNELS_API void smol_compute_rope_interleaved(float *cos_out, float *sin_o
 SMOL_KERNELS_API void smol_apply_rope_interleaved(float *x, const float *cos_vals,
                                                   const float *sin_vals, int seq, int n_heads,
                                                   int head_dim);
+
+/* smol_kernels.h:86-88, rmsnorm.c:78-140: each head_dim segment of x
+ * [seq_len][n_heads*head_dim] becomes x * weight / sqrt(mean(x^2) + eps), in
+ * place (the per-head Q/K norm of qkn_decoder.c:487-491) */
+SMOL_KERNELS_API void smol_rms_norm_per_head(float *x, const float *weight, int seq_len,
+                                             int n_heads, int head_dim, float eps);
 
 #ifdef __cplusplus
 }

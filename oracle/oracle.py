@@ -78,6 +78,10 @@ class _Lib:
         self._arope_inter = self._fn("apply_rope_interleaved", [_F, _F, _F, ci, ci, ci])
         set_threads = "set_threads"
         self._set_threads = self._fn(set_threads, [ci])
+        # rmsnorm.c is part of the reference build since per-head RMSNorm joined
+        # the path; an older _ref build lacks it
+        self._rms_ph = (self._fn("rms_norm_per_head", [_F, _F, ci, ci, ci, cf])
+                        if hasattr(self.lib, self.prefix + "rms_norm_per_head") else None)
 
     def set_threads(self, n):
         self._set_threads(int(n))
@@ -109,6 +113,17 @@ class _Lib:
         self._bidir(_fp(out), _fp(Q), _fp(K), _fp(V), seq, n_heads, head_dim,
                     ctypes.c_float(scale), ws.ctypes.data_as(_I), len(ws) - 1)
         return out
+
+    # -- per-head RMSNorm ----------------------------------------------------
+    def rms_norm_per_head(self, x, weight, seq, n_heads, head_dim, eps):
+        """x [seq, n_heads*head_dim] normalised per head_dim segment (a copy)."""
+        if self._rms_ph is None:
+            raise NotImplementedError("%s has no rms_norm_per_head" % self.path)
+        y = np.array(x, dtype=np.float32, copy=True, order="C")
+        w = _f32(weight)
+        assert y.size >= seq * n_heads * head_dim and w.size >= head_dim
+        self._rms_ph(_fp(y), _fp(w), seq, n_heads, head_dim, ctypes.c_float(eps))
+        return y
 
     # -- RoPE ----------------------------------------------------------------
     def compute_rope(self, positions, head_dim, theta, interleaved=False):

@@ -24,6 +24,9 @@
  *   orc_apply_rope_interleaved      rope.c:68-93
  *   orc_bf16_attention_softcap      common/decoder/qkn_bf16_decoder.c:120-229
  *       (two-pass softmax, truncating bf16 output, optional window/softcap)
+ *   orc_rms_norm_per_head           common/kernels/rmsnorm.c:78-140
+ *       (AVX-512 order: 16-lane fused multiply-add accumulators over the
+ *       16-wide blocks, a halving tree, then a scalar tail)
  *
  * Parity pins (see tests/test_oracle_*.py): golden vectors written by the
  * compiled reference (oracle/_ref), closed forms (one visible key, identical
@@ -351,6 +354,38 @@ void orc_apply_rope_interleaved(float *x, const float *cos_vals, const float *si
                 v[2 * d] = x0 * c[2 * d] - x1 * sn[2 * d];
                 v[2 * d + 1] = x1 * c[2 * d + 1] + x0 * sn[2 * d + 1];
             }
+        }
+    }
+}
+
+/* ------------------------------------------------------- per-head RMSNorm */
+
+/* rmsnorm.c:78-140: each head_dim segment of x [seq][n_heads * hd] becomes
+ * x * w / sqrt(mean(x^2) + eps), in place. The sum of squares follows the
+ * AVX-512 body (86-94): 16 lane accumulators updated by fused multiply-adds
+ * over the 16-wide blocks, the halving-tree reduction, then the tail added
+ * element by element; the 16-wide blocks scale as (x * w) * r (119-121), the
+ * tail as x * r * w (123). ORC_VEC_GENERIC follows the scalar branch
+ * (107-112, 134-136): a sequential sum and x * r * w throughout. */
+void orc_rms_norm_per_head(float *x, const float *w, int seq, int n_heads, int hd, float eps) {
+    int hidden = n_heads * hd;
+    for (int s = 0; s < seq; s++) {
+        for (int h = 0; h < n_heads; h++) {
+            float *v = x + (size_t)s * hidden + (size_t)h * hd;
+            int body = orc_vec_generic ? 0 : hd - (hd % ORC_LANES);
+            float ss;
+            if (body > 0) {
+                float acc[ORC_LANES] = {0};
+                for (int d = 0; d < body; d += ORC_LANES)
+                    for (int i = 0; i < ORC_LANES; i++) acc[i] = fmaf(v[d + i], v[d + i], acc[i]);
+                ss = lane_tree_sum(acc);
+            } else {
+                ss = 0.0f;
+            }
+            for (int d = body; d < hd; d++) ss += v[d] * v[d];
+            float r = 1.0f / sqrtf(ss / hd + eps);
+            for (int d = 0; d < body; d++) v[d] = (v[d] * w[d]) * r;
+            for (int d = body; d < hd; d++) v[d] = v[d] * r * w[d];
         }
     }
 }

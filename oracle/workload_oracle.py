@@ -3,7 +3,8 @@ TEST INFRASTRUCTURE ONLY (tests, smoke check, CPU-baseline leg of the bench).
 
 Each function follows the reference decoder's order of operations on the
 same input bits: widen bf16 to fp32, build the RoPE table as fill_rope_cache
-does (qkn_decoder.c:276-311), rotate Q and the new K in fp32
+does (qkn_decoder.c:276-311), optionally apply the per-head RMSNorm
+(qkn_decoder.c:487-491), rotate Q and the new K in fp32
 (smol_apply_rope_*, qkn_decoder.c:493-495 / :647-649), keep an fp32 cache
 (qkn_decoder.c:498-503 / :651-652), then smol_causal_attention or
 smol_bidirectional_attention (attention.c:32-170).
@@ -35,28 +36,36 @@ def rope_rows(orc, positions, hd, theta, interleaved, cache={}):
     return c[0][positions], c[1][positions]
 
 
-def decode(orc: Oracle, wl, x):
-    """out [n_seq, Hq*hd]: per sequence, attention of the rotated new query over
-    its widened cache plus the rotated new key."""
+def _norm(orc, a, w, rows, heads, hd, eps):
+    """per-head RMSNorm before RoPE (qkn_decoder.c:487-491); w None: none"""
+    a = _as_f32(a)
+    return a if w is None else orc.rms_norm_per_head(a, w, rows, heads, hd, eps)
+
+
+def decode(orc: Oracle, wl, x, q_norm=None, k_norm=None, eps=1e-6):
+    """out [n_seq, Hq*hd]: per sequence, attention of the (normalised and)
+    rotated new query over its widened cache plus the rotated new key."""
     inter = wl.rope_type == 1
     outs = []
     for i, L in enumerate(wl.lengths):
         p = L - 1
         c, s = rope_rows(orc, np.array([p]), wl.hd, wl.theta, inter)
-        q = orc.apply_rope(x["q"][i:i + 1], c, s, 1, wl.Hq, wl.hd, inter)
-        kn = orc.apply_rope(x["k"][i:i + 1], c, s, 1, wl.Hkv, wl.hd, inter)
+        q = orc.apply_rope(_norm(orc, x["q"][i:i + 1], q_norm, 1, wl.Hq, wl.hd, eps), c, s, 1, wl.Hq, wl.hd, inter)
+        kn = orc.apply_rope(_norm(orc, x["k"][i:i + 1], k_norm, 1, wl.Hkv, wl.hd, eps), c, s, 1, wl.Hkv, wl.hd,
+                            inter)
         K = np.concatenate([_widen(x["cache_k"][i]), kn], 0)
         V = np.concatenate([_widen(x["cache_v"][i]), x["v"][i:i + 1]], 0)
         outs.append(orc.causal_attention(q, K, V, 1, L, wl.Hq, wl.Hkv, wl.hd, wl.scale, p))
     return np.concatenate(outs, 0)
 
 
-def prefill(orc: Oracle, wl, x, window=0, cap=0.0):
+def prefill(orc: Oracle, wl, x, window=0, cap=0.0, q_norm=None, k_norm=None, eps=1e-6):
     P, S = wl.pos0, wl.seq_q
     pos = np.arange(P, P + S)
     c, s = rope_rows(orc, pos, wl.hd, wl.theta, wl.rope_type == 1)
-    q = orc.apply_rope(_as_f32(x["q"]), c, s, S, wl.Hq, wl.hd, wl.rope_type == 1)
-    kn = orc.apply_rope(_as_f32(x["k"]), c, s, S, wl.Hkv, wl.hd, wl.rope_type == 1)
+    q = orc.apply_rope(_norm(orc, x["q"], q_norm, S, wl.Hq, wl.hd, eps), c, s, S, wl.Hq, wl.hd, wl.rope_type == 1)
+    kn = orc.apply_rope(_norm(orc, x["k"], k_norm, S, wl.Hkv, wl.hd, eps), c, s, S, wl.Hkv, wl.hd,
+                        wl.rope_type == 1)
     K = np.concatenate([_widen(x["cache_k"]).reshape(P, wl.Hkv * wl.hd), kn], 0)
     V = np.concatenate([_widen(x["cache_v"]).reshape(P, wl.Hkv * wl.hd), _as_f32(x["v"])], 0)
     return orc.causal_attention(q, K, V, S, P + S, wl.Hq, wl.Hkv, wl.hd, wl.scale, P, window=window, cap=cap)
@@ -92,4 +101,7 @@ def stream(orc: Oracle, wl, x):
 
 def evaluate(orc, wl, x):
     kind = type(wl).__name__
+    if getattr(wl, "qk_norm", False):
+        qw, kw = wl.norm_weights()
+        return {"Decode": decode, "Prefill": prefill}[kind](orc, wl, x, q_norm=qw, k_norm=kw, eps=wl.norm_eps)
     return {"Decode": decode, "Prefill": prefill, "Bidir": bidir, "Stream": stream}[kind](orc, wl, x)

@@ -30,9 +30,8 @@ extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t 
 extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, int w, int staged, hipStream_t st);
 extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
 extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st);
-extern "C" int smol_launch_rope_apply(float *x, const float *cos_t, const float *sin_t,
-                                      const int *pos, int seq, int n_heads, int hd, int kind,
-                                      hipStream_t st);
+extern "C" int smol_launch_norm_rope(float *x, const float *w, float eps, const float *cos_t, const float *sin_t,
+                                     const int *pos, int seq, int n_heads, int hd, int kind, hipStream_t st);
 
 #define LOG2E_D 1.4426950408889634
 
@@ -497,6 +496,8 @@ struct CallShape {
     smol_kv_cache *kv;
     int layer;
     float *out;
+    const float *q_norm = nullptr, *k_norm = nullptr; /* per-head RMSNorm weights [hd] or null */
+    float norm_eps = 0.0f;
 };
 
 
@@ -642,7 +643,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     }
     /* SMOL_ATTN_FA_QDIRECT=1: k_attn_fa rotates and scales Q as it loads it
      * and the pre-pass only handles the new K/V */
-    const bool q_direct = fa && !fb && env_int("SMOL_ATTN_FA_QDIRECT") == 1;
+    const bool q_direct = fa && !fb && !cs.q_norm && env_int("SMOL_ATTN_FA_QDIRECT") == 1;
     if (q_direct)
         pl.pblk.erase(std::remove_if(pl.pblk.begin(), pl.pblk.end(), [](const PrepBlock &k) { return k.kind == 1; }),
                       pl.pblk.end());
@@ -711,6 +712,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     if (cs.dec) pp.qs32 = (float *)ctx->qs32.p;
     pp.batches = (const PrepBatch *)(dd + o_pb);
     pp.blocks = (const PrepBlock *)(dd + o_pblk);
+    pp.q_norm = cs.q_norm; pp.k_norm = cs.k_norm; pp.norm_eps = cs.norm_eps;
     int mk = timing_begin(ctx, 0);
     rc = smol_launch_prep(&pp, (int)pl.pblk.size(), ctx->stream);
     timing_end(ctx, mk);
@@ -782,13 +784,32 @@ static int check_rope(const smol_rope_table *rope, int hd, int need) {
     return smol_rope_table_ensure(const_cast<smol_rope_table *>(rope), need);
 }
 
+/* per-head RMSNorm weights: device fp32 [hd], 4-byte aligned; a Q block of
+ * the pre-pass keeps 1/rms of its 32 tokens x G heads in LDS */
+static int check_norm(const float *q_norm, const float *k_norm, float eps, int G) {
+    if (((uintptr_t)q_norm | (uintptr_t)k_norm) & 3) return fail(SMOL_ATTN_ERR_ARG, "norm weights must be 4-byte aligned");
+    if ((q_norm || k_norm) && !(eps >= 0.0f)) return fail(SMOL_ATTN_ERR_ARG, "norm eps %g", (double)eps);
+    if (q_norm && G > 256) return fail(SMOL_ATTN_ERR_UNSUPPORTED, "q norm with %d query heads per KV head", G);
+    return 0;
+}
+
 extern "C" int smol_attn_prefill(smol_attn_ctx *ctx, smol_kv_cache *kv, int layer, int slot,
                                  const smol_rope_table *rope, int pos0, int seq_q, const void *q,
                                  const void *k_new, const void *v_new, int dtype, int n_heads,
                                  float scale, int window, float cap, float *out) {
+    return smol_attn_prefill_qknorm(ctx, kv, layer, slot, rope, pos0, seq_q, q, k_new, v_new, dtype, n_heads, scale,
+                                    window, cap, nullptr, nullptr, 0.0f, out);
+}
+
+extern "C" int smol_attn_prefill_qknorm(smol_attn_ctx *ctx, smol_kv_cache *kv, int layer, int slot,
+                                        const smol_rope_table *rope, int pos0, int seq_q, const void *q,
+                                        const void *k_new, const void *v_new, int dtype, int n_heads,
+                                        float scale, int window, float cap, const float *q_norm,
+                                        const float *k_norm, float eps, float *out) {
     if (!kv) return fail(SMOL_ATTN_ERR_ARG, "cache is NULL");
     int rc = check_common(ctx, dtype, n_heads, kv->n_kv, kv->hd, q, out);
     if (rc) return rc;
+    if ((rc = check_norm(q_norm, k_norm, eps, n_heads / kv->n_kv))) return rc;
     if (kv->ctx != ctx) return fail(SMOL_ATTN_ERR_ARG, "cache belongs to another context");
     if (layer < 0 || layer >= kv->n_layers || slot < 0 || slot >= kv->n_slots)
         return fail(SMOL_ATTN_ERR_ARG, "layer %d / slot %d out of range", layer, slot);
@@ -809,7 +830,7 @@ extern "C" int smol_attn_prefill(smol_attn_ctx *ctx, smol_kv_cache *kv, int laye
     /* short chunks stream the cache like a decode step; long ones are MFMA-bound */
     const bool dec = seq_q * G <= 64;
     CallShape cs{dec, q, k_new, v_new, dtype, n_heads, Hkv, hd, (long long)n_heads * hd,
-                 (long long)Hkv * hd, scale, cap, window, rope, 1, 1, kv, layer, out};
+                 (long long)Hkv * hd, scale, cap, window, rope, 1, 1, kv, layer, out, q_norm, k_norm, eps};
     return run_plan(ctx, pl, cs);
 }
 
@@ -818,9 +839,20 @@ extern "C" int smol_attn_decode(smol_attn_ctx *ctx, smol_kv_cache *kv, int layer
                                 const int *pos, const void *q, const void *k_new, const void *v_new,
                                 int dtype, int n_heads, float scale, int window, float cap,
                                 float *out) {
+    return smol_attn_decode_qknorm(ctx, kv, layer, rope, n_seq, slots, pos, q, k_new, v_new, dtype, n_heads, scale,
+                                   window, cap, nullptr, nullptr, 0.0f, out);
+}
+
+extern "C" int smol_attn_decode_qknorm(smol_attn_ctx *ctx, smol_kv_cache *kv, int layer,
+                                       const smol_rope_table *rope, int n_seq, const int *slots,
+                                       const int *pos, const void *q, const void *k_new,
+                                       const void *v_new, int dtype, int n_heads, float scale,
+                                       int window, float cap, const float *q_norm,
+                                       const float *k_norm, float eps, float *out) {
     if (!kv) return fail(SMOL_ATTN_ERR_ARG, "cache is NULL");
     int rc = check_common(ctx, dtype, n_heads, kv->n_kv, kv->hd, q, out);
     if (rc) return rc;
+    if ((rc = check_norm(q_norm, k_norm, eps, n_heads / kv->n_kv))) return rc;
     if (kv->ctx != ctx) return fail(SMOL_ATTN_ERR_ARG, "cache belongs to another context");
     if (layer < 0 || layer >= kv->n_layers) return fail(SMOL_ATTN_ERR_ARG, "layer %d out of range", layer);
     if (n_seq <= 0 || !slots || !pos || !k_new || !v_new) return fail(SMOL_ATTN_ERR_ARG, "bad decode batch");
@@ -849,7 +881,7 @@ extern "C" int smol_attn_decode(smol_attn_ctx *ctx, smol_kv_cache *kv, int layer
     pl.q_rows = n_seq * G;
     pl.fresh_rows = n_seq * SMOL_SLAB;
     CallShape cs{true, q, k_new, v_new, dtype, n_heads, Hkv, hd, (long long)n_heads * hd,
-                 (long long)Hkv * hd, scale, cap, window, rope, 1, 1, kv, layer, out};
+                 (long long)Hkv * hd, scale, cap, window, rope, 1, 1, kv, layer, out, q_norm, k_norm, eps};
     return run_plan(ctx, pl, cs);
 }
 
@@ -988,20 +1020,37 @@ extern "C" int smol_kv_cache_read(smol_kv_cache *kv, int layer, int slot, int po
 
 extern "C" int smol_attn_apply_rope(smol_attn_ctx *ctx, const smol_rope_table *rope, float *x,
                                     const int *positions, int seq, int n_heads) {
-    if (!ctx || !rope || !x || !positions || seq <= 0 || n_heads <= 0) return fail(SMOL_ATTN_ERR_ARG, "bad arguments");
+    if (!rope) return fail(SMOL_ATTN_ERR_ARG, "rope table is NULL");
+    return smol_attn_norm_rope(ctx, rope, x, nullptr, 0.0f, positions, seq, n_heads, rope->hd);
+}
+
+extern "C" int smol_attn_norm_rope(smol_attn_ctx *ctx, const smol_rope_table *rope, float *x, const float *weight,
+                                   float eps, const int *positions, int seq, int n_heads, int head_dim) {
+    if (!ctx || !x || seq <= 0 || n_heads <= 0 || head_dim <= 0 || (head_dim & 1))
+        return fail(SMOL_ATTN_ERR_ARG, "bad arguments");
+    if (rope && (!positions || rope->hd != head_dim))
+        return fail(SMOL_ATTN_ERR_ARG, "rope needs positions and head_dim %d", rope ? rope->hd : 0);
+    if (weight && !(eps >= 0.0f)) return fail(SMOL_ATTN_ERR_ARG, "norm eps %g", (double)eps);
+    if (((uintptr_t)x | (uintptr_t)weight) & 3) return fail(SMOL_ATTN_ERR_ARG, "x / weight must be 4-byte aligned");
     int rc = set_device(ctx);
     if (rc) return rc;
-    int mx = 0;
-    for (int s = 0; s < seq; s++) {
-        if (positions[s] < 0) return fail(SMOL_ATTN_ERR_ARG, "position %d", positions[s]);
-        mx = std::max(mx, positions[s]);
+    if (!rope && !weight) return SMOL_ATTN_OK;
+    const int *pos_d = nullptr;
+    if (rope) {
+        int mx = 0;
+        for (int s = 0; s < seq; s++) {
+            if (positions[s] < 0) return fail(SMOL_ATTN_ERR_ARG, "position %d", positions[s]);
+            mx = std::max(mx, positions[s]);
+        }
+        if ((rc = smol_rope_table_ensure(const_cast<smol_rope_table *>(rope), mx + 1))) return rc;
+        if ((rc = upload_desc(ctx, positions, (size_t)seq * sizeof(int)))) return rc;
+        pos_d = (const int *)ctx->desc.p;
     }
-    if ((rc = smol_rope_table_ensure(const_cast<smol_rope_table *>(rope), mx + 1))) return rc;
-    if ((rc = upload_desc(ctx, positions, (size_t)seq * sizeof(int)))) return rc;
-    if (smol_launch_rope_apply(x, rope->cos_d, rope->sin_d, (const int *)ctx->desc.p, seq, n_heads, rope->hd,
-                               rope->type == SMOL_ROPE_INTERLEAVED ? SMOL_ROPE_INTERLEAVED_K : SMOL_ROPE_NEOX_K,
-                               ctx->stream))
-        return fail(SMOL_ATTN_ERR_DEVICE, "rope launch: %s", hipGetErrorString(hipGetLastError()));
+    const int kind = !rope ? SMOL_ROPE_OFF
+                     : rope->type == SMOL_ROPE_INTERLEAVED ? SMOL_ROPE_INTERLEAVED_K : SMOL_ROPE_NEOX_K;
+    if (smol_launch_norm_rope(x, weight, eps, rope ? rope->cos_d : nullptr, rope ? rope->sin_d : nullptr, pos_d, seq,
+                              n_heads, head_dim, kind, ctx->stream))
+        return fail(SMOL_ATTN_ERR_DEVICE, "norm/rope launch: %s", hipGetErrorString(hipGetLastError()));
     return SMOL_ATTN_OK;
 }
 
@@ -1133,8 +1182,8 @@ static void legacy_rope(const char *fn, float *x, const float *c, const float *s
     if (hipMemcpyAsync(g_legacy.cs.p, c, tb, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
         hipMemcpyAsync((char *)g_legacy.cs.p + tb, s, tb, hipMemcpyHostToDevice, ctx->stream) != hipSuccess)
         legacy_abort(fn);
-    if (smol_launch_rope_apply((float *)g_legacy.q.p, (const float *)g_legacy.cs.p,
-                               (const float *)((char *)g_legacy.cs.p + tb), nullptr, seq, H, hd, kind, ctx->stream))
+    if (smol_launch_norm_rope((float *)g_legacy.q.p, nullptr, 0.0f, (const float *)g_legacy.cs.p,
+                              (const float *)((char *)g_legacy.cs.p + tb), nullptr, seq, H, hd, kind, ctx->stream))
         legacy_abort(fn);
     legacy_download(fn, x, g_legacy.q, xb);
 }
@@ -1147,4 +1196,18 @@ extern "C" void smol_apply_rope_neox(float *x, const float *cos_vals, const floa
 extern "C" void smol_apply_rope_interleaved(float *x, const float *cos_vals, const float *sin_vals, int seq,
                                             int n_heads, int head_dim) {
     legacy_rope(__func__, x, cos_vals, sin_vals, seq, n_heads, head_dim, SMOL_ROPE_INTERLEAVED_K);
+}
+
+extern "C" void smol_rms_norm_per_head(float *x, const float *weight, int seq_len, int n_heads, int head_dim,
+                                       float eps) {
+    const char *fn = __func__;
+    if (seq_len <= 0 || n_heads <= 0 || head_dim <= 0) return;
+    smol_attn_ctx *ctx = legacy_ctx(fn);
+    const size_t xb = (size_t)seq_len * n_heads * head_dim * 4, wb = (size_t)head_dim * 4;
+    legacy_upload(fn, g_legacy.q, x, xb);
+    legacy_upload(fn, g_legacy.cs, weight, wb);
+    if (smol_launch_norm_rope((float *)g_legacy.q.p, (const float *)g_legacy.cs.p, eps, nullptr, nullptr, nullptr,
+                              seq_len, n_heads, head_dim, SMOL_ROPE_OFF, ctx->stream))
+        legacy_abort(fn);
+    legacy_download(fn, x, g_legacy.q, xb);
 }

@@ -91,8 +91,9 @@ typedef struct {
     float qscale;
 } SkParams;
 
-/* Pre-pass: rotates/scales Q into the Q scratch, appends rotated K and V to
- * the bf16 cache and writes the fresh fp16 K/V slabs. */
+/* Pre-pass: normalises (optional per-head RMSNorm), rotates and scales Q into
+ * the Q scratch, appends the normalised and rotated K and V to the bf16 cache
+ * and writes the fresh fp16 K/V slabs. */
 typedef struct {
     int q_tok0, n_q;     /* Q input rows of this batch */
     int q_row0;          /* Q-scratch row offset (already multiplied by G) */
@@ -128,6 +129,8 @@ typedef struct {
     float *qs32;
     const PrepBatch *batches;
     const PrepBlock *blocks;
+    /* per-head RMSNorm before RoPE (null: none): weights [hd] fp32 */
+    const float *q_norm; const float *k_norm; float norm_eps;
 } PrepParams;
 
 #endif

@@ -1,10 +1,12 @@
 /*
  * attn_kernels.hip - gfx950 (CDNA4) kernels of the attention path.
  *
- *   k_prep      RoPE + cache append + fp16 staging, one pass over the new
- *               rows: replaces smol_apply_rope_{neox,interleaved} on Q and K
- *               and the K/V row memcpy into the cache
- *               (common/decoder/qkn_decoder.c:493-503 and :647-652).
+ *   k_prep      per-head RMSNorm + RoPE + cache append + fp16 staging, one
+ *               pass over the new rows: replaces smol_rms_norm_per_head and
+ *               smol_apply_rope_{neox,interleaved} on Q and K and the K/V row
+ *               memcpy into the cache (common/decoder/qkn_decoder.c:487-503
+ *               and :640-652).
+ *   k_norm_rope per-head RMSNorm and / or RoPE in place on an fp32 array.
  *   k_attn_fb   prefill / bidirectional attention whose keys are all new:
  *               fp16 MFMA (v_mfma_f32_16x16x32_f16), one workgroup per
  *               64-row tile, K/V staged into LDS by direct transfers;
@@ -137,11 +139,37 @@ __device__ __forceinline__ void tab8(const float *t, float *v) {
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
+/* 1 / sqrt(mean(x^2) + eps) of the head row at `base + row` (hd elements,
+ * fp32 or bf16), computed by the 8 lanes of an aligned lane group (j = lane
+ * & 7): lane j sums the squares of chunks j, j + 8, ... in order, then a
+ * butterfly over the 8 lanes, so every lane returns the same value. This is
+ * rmsnorm.c:78-113 with another summation order. All 8 lanes must call it. */
+__device__ __forceinline__ float head_rinv8(const void *base, int dtype, long long row, int hd, float eps, int j) {
+    float ss = 0.0f;
+    for (int d0 = j * 8; d0 < hd; d0 += 64) {
+        float v[8];
+        load8(base, dtype, row + d0, v);
+#pragma unroll
+        for (int i = 0; i < 8; i++) ss = fmaf(v[i], v[i], ss);
+    }
+    ss += __shfl_xor(ss, 1, 8);
+    ss += __shfl_xor(ss, 2, 8);
+    ss += __shfl_xor(ss, 4, 8);
+    return 1.0f / sqrtf(ss / (float)hd + eps);
+}
+
 /* Rotates the 8 elements [d0, d0+8) of a head vector whose row starts at
- * `base + row` (fp32 or bf16 input), position `pos` of the table. */
+ * `base + row` (fp32 or bf16 input), position `pos` of the table. With a
+ * norm weight `nw`, each element (and each rotation partner) is first
+ * normalised as (x * nw[d]) * rinv, the order of rmsnorm.c:119-121. */
 __device__ __forceinline__ void rope8(const void *base, int dtype, long long row, int d0, int hd, int kind,
-                                      const float *cos_t, const float *sin_t, long long pos, float *out) {
+                                      const float *cos_t, const float *sin_t, long long pos, float *out,
+                                      const float *nw = nullptr, float rinv = 1.0f) {
     load8(base, dtype, row + d0, out);
+    if (nw) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) out[i] = (out[i] * nw[d0 + i]) * rinv;
+    }
     if (kind == SMOL_ROPE_OFF) return;
     const float *c = cos_t + pos * hd, *s = sin_t + pos * hd;
     float cv[8], sv[8];
@@ -159,11 +187,20 @@ __device__ __forceinline__ void rope8(const void *base, int dtype, long long row
     const int half = hd >> 1;
     float pr[8];
     if ((half & 7) == 0) {
-        load8(base, dtype, row + (d0 < half ? d0 + half : d0 - half), pr);
+        const int p0 = d0 < half ? d0 + half : d0 - half;
+        load8(base, dtype, row + p0, pr);
+        if (nw) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) pr[i] = (pr[i] * nw[p0 + i]) * rinv;
+        }
     } else {
         /* half not a multiple of 8 (head_dim 72): partners element by element */
 #pragma unroll
-        for (int i = 0; i < 8; i++) pr[i] = load_in(base, dtype, row + rope_partner(d0 + i, hd, kind));
+        for (int i = 0; i < 8; i++) {
+            const int pd = rope_partner(d0 + i, hd, kind);
+            pr[i] = load_in(base, dtype, row + pd);
+            if (nw) pr[i] = (pr[i] * nw[pd]) * rinv;
+        }
     }
     /* NeoX: x1 c - x2 s for the first half, x2 c + x1 s for the second
      * (rope.c:99-164, fmsub / fmadd) */
@@ -172,10 +209,12 @@ __device__ __forceinline__ void rope8(const void *base, int dtype, long long row
         out[i] = d0 + i < half ? fmaf(out[i], cv[i], -(pr[i] * sv[i])) : fmaf(out[i], cv[i], pr[i] * sv[i]);
 }
 
-/* grid (n_blocks, Hkv), 256 threads. A fresh-slab block covers 32 positions
- * of one KV head: old cache rows are copied to the fresh buffers, new rows
- * are rotated (K), appended to the bf16 cache and written to the fresh
- * buffers, positions past the new rows are zero. Work is done in chunks of
+/* grid (n_blocks, Hkv), 256 threads. A Q block normalises (when a q_norm
+ * weight is given), rotates and scales the G heads of its tokens into the Q
+ * scratch. A fresh-slab block covers 32 positions of one KV head: old cache
+ * rows are copied to the fresh buffers, new rows are normalised and rotated
+ * (K), appended to the bf16 cache and written to the fresh buffers,
+ * positions past the new rows are zero. Work is done in chunks of
  * 8 elements (16-byte stores); V goes through LDS so that the transposed
  * stores are 8 consecutive positions of one column. */
 __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
@@ -193,6 +232,19 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
         const int cpp = hdp >> 3;
         const int per_tok = G * cpp;
         const int rk = (p.rope_q && p.rope_kind != SMOL_ROPE_OFF) ? p.rope_kind : SMOL_ROPE_OFF;
+        /* per-head RMSNorm: 1/rms of each of the block's count * G head rows
+         * (the host keeps that within the LDS array) */
+        float *s_qr = sv;
+        if (p.q_norm) {
+            for (int r = tid >> 3; r < blk.count * G; r += 32) {
+                const int tl = r / G, hg = r - tl * G;
+                const long long row =
+                    (long long)(b.q_tok0 + blk.first + tl) * p.q_stride + (long long)(g * G + hg) * hd;
+                const float ri = head_rinv8(p.q, p.q_dtype, row, hd, p.norm_eps, tid & 7);
+                if ((tid & 7) == 0) s_qr[r] = ri;
+            }
+            __syncthreads();
+        }
         /* four 8-element chunks per thread per pass, all loads issued before
          * any store */
         const int total = blk.count * per_tok;
@@ -210,7 +262,8 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
                 for (int i = 0; i < 8; i++) v[u][i] = 0.0f;
                 if (d0 < hd) {
                     const long long row = (long long)(b.q_tok0 + t) * p.q_stride + (long long)(g * G + hg) * hd;
-                    rope8(p.q, p.q_dtype, row, d0, hd, rk, p.rope_cos, p.rope_sin, b.q_pos0 + t, v[u]);
+                    rope8(p.q, p.q_dtype, row, d0, hd, rk, p.rope_cos, p.rope_sin, b.q_pos0 + t, v[u], p.q_norm,
+                          p.q_norm ? s_qr[tl * G + hg] : 1.0f);
                 }
                 qi[u] = e < total ? (long long)g * p.qs_head_stride + (long long)(b.q_row0 + t * G + hg) * hdp + d0 : -1;
             }
@@ -242,6 +295,18 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
     const int new_lo = b.kv_pos0, new_hi = b.kv_pos0 + b.n_kv;
     const int rk = (p.rope_k && p.rope_kind != SMOL_ROPE_OFF) ? p.rope_kind : SMOL_ROPE_OFF;
 
+    /* per-head RMSNorm of the new K rows: row r by lanes 8r .. 8r+7 */
+    __shared__ float s_kr[SMOL_SLAB];
+    if (p.k_norm) {
+        const int r = tid >> 3, pos = pos_base + r;
+        if (pos >= new_lo && pos < new_hi) {
+            const long long row = (long long)(b.kv_in0 + pos - new_lo) * p.kv_stride + (long long)g * hd;
+            const float ri = head_rinv8(p.k, p.kv_dtype, row, hd, p.norm_eps, tid & 7);
+            if ((tid & 7) == 0) s_kr[r] = ri;
+        }
+        __syncthreads();
+    }
+
     /* K rows and the new V rows (into LDS), chunk (r, d0) */
     for (int e = tid; e < SMOL_SLAB * cpr; e += blockDim.x) {
         const int r = e / cpr, d0 = (e - r * cpr) * 8;
@@ -251,7 +316,8 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
             if (has_cache) unpack_bf16x8(*reinterpret_cast<const uint4 *>(kc + (long long)pos * hd + d0), kv);
         } else if (pos < new_hi) {
             const long long row = (long long)(b.kv_in0 + pos - new_lo) * p.kv_stride + (long long)g * hd;
-            rope8(p.k, p.kv_dtype, row, d0, hd, rk, p.rope_cos, p.rope_sin, pos, kv);
+            rope8(p.k, p.kv_dtype, row, d0, hd, rk, p.rope_cos, p.rope_sin, pos, kv, p.k_norm,
+                  p.k_norm ? s_kr[r] : 1.0f);
             load8(p.v, p.kv_dtype, row + d0, vv);
             if (has_cache) *reinterpret_cast<uint4 *>(kc + (long long)pos * hd + d0) = pack_bf16x8(kv);
         }
@@ -1738,52 +1804,72 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
-/* ------------------------------------------------------------ k_rope_apply */
+/* ------------------------------------------------------------- k_norm_rope */
 
-/* In-place RoPE on x [seq][H][hd] fp32, row s using table row pos[s] (or s
- * when pos is null). One thread per rotated pair; the arithmetic is that of
- * rope.c:99-164 (NeoX: fmsub / fmadd with the first-half table entries over
- * the 16-wide vector body, the scalar tail with the second-half entries) and
- * rope.c:68-93 (interleaved). */
-__global__ __launch_bounds__(256) void k_rope_apply(float *x, const float *cos_t, const float *sin_t,
-                                                    const int *pos, int seq, int H, int hd, int kind) {
+/* In place on x [seq][H][hd] fp32: per-head RMSNorm with weight w [hd]
+ * (skipped when w is null; rmsnorm.c:78-140), then RoPE (kind != OFF), row s
+ * rotated at table row pos[s] (or s when pos is null). Eight lanes per head
+ * row: the sum of squares reads the whole row before any lane writes (the
+ * butterfly consumes every load), then lane j handles pairs j, j + 8, ... The rotation
+ * is that of rope.c:99-164 (NeoX: fmsub / fmadd with the first-half table
+ * entries over the 16-wide vector body, the scalar tail with the second-half
+ * entries) and rope.c:68-93 (interleaved). */
+__global__ __launch_bounds__(256) void k_norm_rope(float *x, const float *w, float eps, const float *cos_t,
+                                                   const float *sin_t, const int *pos, int seq, int H, int hd,
+                                                   int kind) {
+    const int j = threadIdx.x & 7;
     const int half = hd >> 1;
-    const long long n = (long long)seq * H * half;
-    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < n;
-         e += (long long)gridDim.x * blockDim.x) {
-        const int i = (int)(e % half);
-        const long long sh = e / half;
-        const int s = (int)(sh / H);
-        const long long row = (long long)(pos ? pos[s] : s) * hd;
-        const float *c = cos_t + row, *sn = sin_t + row;
-        float *v = x + sh * hd;
+    const long long rows = (long long)seq * H;
+    const long long step = ((long long)gridDim.x * blockDim.x) >> 3;
+    for (long long r = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 3; r < rows; r += step) {
+        float *v = x + r * hd;
+        float ri = 1.0f;
+        if (w) { /* any head_dim and alignment: element-strided sum of squares */
+            float ss = 0.0f;
+            for (int d = j; d < hd; d += 8) ss = fmaf(v[d], v[d], ss);
+            ss += __shfl_xor(ss, 1, 8);
+            ss += __shfl_xor(ss, 2, 8);
+            ss += __shfl_xor(ss, 4, 8);
+            ri = 1.0f / sqrtf(ss / (float)hd + eps);
+        }
+        auto nrm = [&](int d) { return w ? (v[d] * w[d]) * ri : v[d]; };
+        if (kind == SMOL_ROPE_OFF) {
+            for (int d = j; d < hd; d += 8) v[d] = nrm(d);
+            continue;
+        }
+        const long long trow = (long long)(pos ? pos[r / H] : r / H) * hd;
+        const float *c = cos_t + trow, *sn = sin_t + trow;
         if (kind == SMOL_ROPE_NEOX_K) {
-            const float x1 = v[i], x2 = v[half + i];
             const int body = half - (half % 16);
-            if (i < body) {
-                v[i] = fmaf(x1, c[i], -(x2 * sn[i]));
-                v[half + i] = fmaf(x2, c[i], x1 * sn[i]);
-            } else {
-                v[i] = x1 * c[i] + (-x2) * sn[i];
-                v[half + i] = x2 * c[half + i] + x1 * sn[half + i];
+            for (int i = j; i < half; i += 8) {
+                const float x1 = nrm(i), x2 = nrm(half + i);
+                if (i < body) {
+                    v[i] = fmaf(x1, c[i], -(x2 * sn[i]));
+                    v[half + i] = fmaf(x2, c[i], x1 * sn[i]);
+                } else {
+                    v[i] = x1 * c[i] + (-x2) * sn[i];
+                    v[half + i] = x2 * c[half + i] + x1 * sn[half + i];
+                }
             }
         } else {
-            const float x0 = v[2 * i], x1 = v[2 * i + 1];
-            v[2 * i] = x0 * c[2 * i] - x1 * sn[2 * i];
-            v[2 * i + 1] = x1 * c[2 * i + 1] + x0 * sn[2 * i + 1];
+            for (int i = j; i < half; i += 8) {
+                const float x0 = nrm(2 * i), x1 = nrm(2 * i + 1);
+                v[2 * i] = x0 * c[2 * i] - x1 * sn[2 * i];
+                v[2 * i + 1] = x1 * c[2 * i + 1] + x0 * sn[2 * i + 1];
+            }
         }
     }
 }
 
 /* ------------------------------------------------------------ launchers */
 
-extern "C" int smol_launch_rope_apply(float *x, const float *cos_t, const float *sin_t, const int *pos,
-                                      int seq, int n_heads, int hd, int kind, hipStream_t st) {
-    const long long n = (long long)seq * n_heads * (hd / 2);
-    if (n <= 0) return 0;
-    const int blocks = (int)std::min<long long>((n + 255) / 256, 4096);
-    hipLaunchKernelGGL(k_rope_apply, dim3(blocks), dim3(256), 0, st, x, cos_t, sin_t, pos, seq, n_heads,
-                       hd, kind);
+extern "C" int smol_launch_norm_rope(float *x, const float *w, float eps, const float *cos_t, const float *sin_t,
+                                     const int *pos, int seq, int n_heads, int hd, int kind, hipStream_t st) {
+    const long long rows = (long long)seq * n_heads;
+    if (rows <= 0) return 0;
+    const int blocks = (int)std::min<long long>((rows + 31) / 32, 4096);
+    hipLaunchKernelGGL(k_norm_rope, dim3(blocks), dim3(256), 0, st, x, w, eps, cos_t, sin_t, pos, seq, n_heads, hd,
+                       kind);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 

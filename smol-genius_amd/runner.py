@@ -41,6 +41,11 @@ class Run:
         return o.cpu().numpy()
 
 
+def _norm_tensors(wl, device):
+    qw, kw = wl.norm_weights()
+    return tuple(None if w is None else _t(w, device) for w in (qw, kw))
+
+
 def _fill_cache(kv, layer, slot, ck, cv):
     if len(ck):
         kv.write(layer, slot, 0, ck, cv)
@@ -74,9 +79,11 @@ def _prep_decode(ctx, wl, x, layers, device):
     r.outs = [torch.empty((wl.n_seq, wl.Hq * wl.hd), dtype=torch.float32, device=device) for _ in range(layers)]
     slots = np.arange(wl.n_seq, dtype=np.int32)
     pos = wl.positions
+    qn, kn = _norm_tensors(wl, device)
 
     def _step(l):
-        return sa.decode(ctx, r.kv, l, r.rope, slots, pos, r.q[l], r.k[l], r.v[l], wl.Hq, wl.scale, out=r.outs[l])
+        return sa.decode(ctx, r.kv, l, r.rope, slots, pos, r.q[l], r.k[l], r.v[l], wl.Hq, wl.scale, out=r.outs[l],
+                         q_norm=qn, k_norm=kn, eps=wl.norm_eps)
     r._step = _step
     return r
 
@@ -95,10 +102,11 @@ def _prep_prefill(ctx, wl, x, layers, device):
     r.k = [_t(x["k"], device, bf) for _ in range(layers)]
     r.v = [_t(x["v"], device, bf) for _ in range(layers)]
     r.outs = [torch.empty((wl.seq_q, wl.Hq * wl.hd), dtype=torch.float32, device=device) for _ in range(layers)]
+    qn, kn = _norm_tensors(wl, device)
 
     def _step(l):
         return sa.prefill(ctx, r.kv, l, 0, r.rope, wl.pos0, r.q[l], r.k[l], r.v[l], wl.Hq, wl.scale,
-                          out=r.outs[l])
+                          out=r.outs[l], q_norm=qn, k_norm=kn, eps=wl.norm_eps)
     r._step = _step
     return r
 

@@ -61,7 +61,12 @@ SIGNATURES = [
                           _c_float, _c_int, _c_int, _c_float, _vp], _c_int),
     ("smol_attn_bidirectional", [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float, _IP,
                                  _c_int, _vp], _c_int),
+    ("smol_attn_prefill_qknorm", [_vp, _vp, _c_int, _c_int, _vp, _c_int, _c_int, _vp, _vp, _vp, _c_int,
+                                  _c_int, _c_float, _c_int, _c_float, _vp, _vp, _c_float, _vp], _c_int),
+    ("smol_attn_decode_qknorm", [_vp, _vp, _c_int, _vp, _c_int, _IP, _IP, _vp, _vp, _vp, _c_int, _c_int,
+                                 _c_float, _c_int, _c_float, _vp, _vp, _c_float, _vp], _c_int),
     ("smol_attn_apply_rope", [_vp, _vp, _vp, _IP, _c_int, _c_int], _c_int),
+    ("smol_attn_norm_rope", [_vp, _vp, _vp, _vp, _c_float, _IP, _c_int, _c_int, _c_int], _c_int),
     # reference-signature drop-ins (host fp32 arrays)
     ("smol_bidirectional_attention", [_FP, _FP, _FP, _FP, _c_int, _c_int, _c_int, _c_float, _IP, _c_int], None),
     ("smol_causal_attention", [_FP, _FP, _FP, _FP, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int], None),
@@ -75,6 +80,7 @@ SIGNATURES = [
     ("smol_apply_rope_neox", [_FP, _FP, _FP, _c_int, _c_int, _c_int], None),
     ("smol_compute_rope_interleaved", [_FP, _FP, _IP, _c_int, _c_int, _c_float], None),
     ("smol_apply_rope_interleaved", [_FP, _FP, _FP, _c_int, _c_int, _c_int], None),
+    ("smol_rms_norm_per_head", [_FP, _FP, _c_int, _c_int, _c_int, _c_float], None),
 ]
 
 _lib = None
@@ -269,28 +275,47 @@ def _out_like(q_rows, n_heads, head_dim, device, out):
     return out
 
 
-def prefill(ctx, kv, layer, slot, rope, pos0, q, k_new, v_new, n_heads, scale, window=0, cap=0.0, out=None):
-    """Chunked prefill of one sequence; see smol_attn_prefill."""
+def _norm_w(w, what):
+    if w is None:
+        return None
+    import torch
+    if w.dtype != torch.float32:
+        raise SmolAttnError("%s must be float32" % what)
+    return _dev(w, what)
+
+
+def prefill(ctx, kv, layer, slot, rope, pos0, q, k_new, v_new, n_heads, scale, window=0, cap=0.0, out=None,
+            q_norm=None, k_norm=None, eps=1e-6):
+    """Chunked prefill of one sequence; see smol_attn_prefill. q_norm / k_norm
+    (device float32 [head_dim]) select smol_attn_prefill_qknorm."""
     seq_q = q.shape[0]
     out = _out_like(seq_q, n_heads, kv.head_dim, q.device, out)
-    _check(load().smol_attn_prefill(ctx.h, kv.h, layer, slot, rope.h if rope else None, pos0, seq_q,
-                                    _dev(q, "q"), _dev(k_new, "k"), _dev(v_new, "v"), _dtype_code(q),
-                                    n_heads, ctypes.c_float(scale), window, ctypes.c_float(cap),
-                                    _dev(out, "out")), "smol_attn_prefill")
+    args = (ctx.h, kv.h, layer, slot, rope.h if rope else None, pos0, seq_q, _dev(q, "q"), _dev(k_new, "k"),
+            _dev(v_new, "v"), _dtype_code(q), n_heads, ctypes.c_float(scale), window, ctypes.c_float(cap))
+    if q_norm is None and k_norm is None:
+        _check(load().smol_attn_prefill(*args, _dev(out, "out")), "smol_attn_prefill")
+    else:
+        _check(load().smol_attn_prefill_qknorm(*args, _norm_w(q_norm, "q_norm"), _norm_w(k_norm, "k_norm"),
+                                               ctypes.c_float(eps), _dev(out, "out")), "smol_attn_prefill_qknorm")
     return out
 
 
-def decode(ctx, kv, layer, rope, slots, pos, q, k_new, v_new, n_heads, scale, window=0, cap=0.0, out=None):
-    """Batched single-token decode; see smol_attn_decode."""
+def decode(ctx, kv, layer, rope, slots, pos, q, k_new, v_new, n_heads, scale, window=0, cap=0.0, out=None,
+           q_norm=None, k_norm=None, eps=1e-6):
+    """Batched single-token decode; see smol_attn_decode. q_norm / k_norm
+    (device float32 [head_dim]) select smol_attn_decode_qknorm."""
     slots = np.ascontiguousarray(slots, np.int32)
     pos = np.ascontiguousarray(pos, np.int32)
     n = len(slots)
     out = _out_like(n, n_heads, kv.head_dim, q.device, out)
-    _check(load().smol_attn_decode(ctx.h, kv.h, layer, rope.h if rope else None, n,
-                                   slots.ctypes.data_as(_IP), pos.ctypes.data_as(_IP), _dev(q, "q"),
-                                   _dev(k_new, "k"), _dev(v_new, "v"), _dtype_code(q), n_heads,
-                                   ctypes.c_float(scale), window, ctypes.c_float(cap), _dev(out, "out")),
-           "smol_attn_decode")
+    args = (ctx.h, kv.h, layer, rope.h if rope else None, n, slots.ctypes.data_as(_IP), pos.ctypes.data_as(_IP),
+            _dev(q, "q"), _dev(k_new, "k"), _dev(v_new, "v"), _dtype_code(q), n_heads, ctypes.c_float(scale),
+            window, ctypes.c_float(cap))
+    if q_norm is None and k_norm is None:
+        _check(load().smol_attn_decode(*args, _dev(out, "out")), "smol_attn_decode")
+    else:
+        _check(load().smol_attn_decode_qknorm(*args, _norm_w(q_norm, "q_norm"), _norm_w(k_norm, "k_norm"),
+                                              ctypes.c_float(eps), _dev(out, "out")), "smol_attn_decode_qknorm")
     return out
 
 
@@ -316,6 +341,19 @@ def apply_rope(ctx, rope, x, positions, n_heads):
     pos = np.ascontiguousarray(positions, np.int32)
     _check(load().smol_attn_apply_rope(ctx.h, rope.h, _dev(x, "x"), pos.ctypes.data_as(_IP), len(pos), n_heads),
            "smol_attn_apply_rope")
+    return x
+
+
+def norm_rope(ctx, rope, x, weight, eps, positions, n_heads, head_dim):
+    """In place: per-head RMSNorm (weight None: skipped) then RoPE (rope None:
+    skipped); see smol_attn_norm_rope."""
+    seq = x.shape[0]
+    pos = None if positions is None else np.ascontiguousarray(positions, np.int32)
+    if pos is not None and len(pos) != seq:
+        raise SmolAttnError("%d positions for %d rows" % (len(pos), seq))
+    _check(load().smol_attn_norm_rope(ctx.h, rope.h if rope else None, _dev(x, "x"), _norm_w(weight, "weight"),
+                                      ctypes.c_float(eps), None if pos is None else pos.ctypes.data_as(_IP), seq,
+                                      n_heads, head_dim), "smol_attn_norm_rope")
     return x
 
 
@@ -387,3 +425,9 @@ def smol_apply_rope_interleaved(x, cos_vals, sin_vals, seq, n_heads, head_dim):
     assert x.dtype == np.float32 and x.flags.c_contiguous
     Ca, c = _f32(cos_vals); Sa, s = _f32(sin_vals)
     load().smol_apply_rope_interleaved(x.ctypes.data_as(_FP), c, s, seq, n_heads, head_dim)
+
+
+def smol_rms_norm_per_head(x, weight, seq_len, n_heads, head_dim, eps):
+    assert x.dtype == np.float32 and x.flags.c_contiguous
+    Wa, w = _f32(weight)
+    load().smol_rms_norm_per_head(x.ctypes.data_as(_FP), w, seq_len, n_heads, head_dim, ctypes.c_float(eps))

@@ -1,4 +1,4 @@
-"""The five attention workloads, as seeded synthetic inputs (numpy, host).
+"""The attention workloads, as seeded synthetic inputs (numpy, host).
 
 Each workload is named by what it is; sizes follow the calls the reference's
 callers make (common/decoder/qkn_decoder.c:525-527 / :674-676,
@@ -20,6 +20,9 @@ common/vision/siglip.c:126-128, exports/qwen_asr/qwen_asr.c:1595-1620):
   qwen17b_stream      Qwen3-ASR-1.7B streaming: a 26-token chunk at positions
                       8192..8217 on an 8192-token bf16 cache (chunked
                       prefill), then 64 single-token decode steps.
+  *_qknorm            qwen06b_decode / qwen06b_prefill with the decoder's
+                      per-head Q/K RMSNorm (weights near 1, eps 1e-6) in
+                      front of RoPE (qkn_decoder.c:487-491).
 
 Cached rows are bf16 (round to nearest even) and are already rotated, as a
 decoder leaves them; the tokens a call appends are fp32 (projection outputs)
@@ -39,9 +42,23 @@ def scale_of(hd):
 
 class Workload:
     name = ""
+    qk_norm = False   # per-head Q/K RMSNorm in front of RoPE (the Qwen3 decoders' q_norm / k_norm)
+    norm_eps = 1e-6
 
     def describe(self):
         return {"workload": self.name}
+
+    def norm_weights(self):
+        """(q_norm, k_norm) weights [hd] fp32 near 1, seeded, when qk_norm is set."""
+        if not self.qk_norm:
+            return None, None
+        s = self.seed * 100
+        return tuple((1.0 + 0.1 * synth.normal(s + 20 + i, (self.hd,))).astype(np.float32) for i in range(2))
+
+
+def with_qk_norm(wl, name):
+    wl.name, wl.qk_norm = name, True
+    return wl
 
 
 class Decode(Workload):
@@ -85,10 +102,13 @@ class Decode(Workload):
         return sum(4 * self.hd * self.Hq * L for L in self.lengths)
 
     def describe(self):
-        return {"workload": self.name, "n_seq": self.n_seq, "n_heads": self.Hq, "n_kv_heads": self.Hkv,
-                "head_dim": self.hd, "seq_k": self.lengths if self.n_seq <= 4 else
-                {"sum": int(sum(self.lengths)), "min": min(self.lengths), "max": max(self.lengths)},
-                "rope_theta": self.theta, "rope": "neox" if self.rope_type == ROPE_NEOX else "interleaved"}
+        d = {"workload": self.name, "n_seq": self.n_seq, "n_heads": self.Hq, "n_kv_heads": self.Hkv,
+             "head_dim": self.hd, "seq_k": self.lengths if self.n_seq <= 4 else
+             {"sum": int(sum(self.lengths)), "min": min(self.lengths), "max": max(self.lengths)},
+             "rope_theta": self.theta, "rope": "neox" if self.rope_type == ROPE_NEOX else "interleaved"}
+        if self.qk_norm:
+            d["qk_norm_eps"] = self.norm_eps
+        return d
 
 
 class Prefill(Workload):
@@ -126,9 +146,12 @@ class Prefill(Workload):
                 + self.seq_q * self.Hq * self.hd * 4)
 
     def describe(self):
-        return {"workload": self.name, "n_heads": self.Hq, "n_kv_heads": self.Hkv, "head_dim": self.hd,
-                "pos0": self.pos0, "seq_q": self.seq_q, "causal": True, "rope_theta": self.theta,
-                "inputs": "bf16" if self.in_bf16 else "f32"}
+        d = {"workload": self.name, "n_heads": self.Hq, "n_kv_heads": self.Hkv, "head_dim": self.hd,
+             "pos0": self.pos0, "seq_q": self.seq_q, "causal": True, "rope_theta": self.theta,
+             "inputs": "bf16" if self.in_bf16 else "f32"}
+        if self.qk_norm:
+            d["qk_norm_eps"] = self.norm_eps
+        return d
 
 
 class Bidir(Workload):
@@ -204,4 +227,9 @@ def all_workloads():
         "gemma_mqa_decode": Decode("gemma_mqa_decode", 8, 1, 256, gemma_lengths(), 1e4, ROPE_INTERLEAVED,
                                    seed=4),
         "qwen17b_stream": Stream("qwen17b_stream", 16, 8, 128, 8192, 26, 64, 1e6, seed=5),
+        # the same decode step and prefill with the per-head Q/K RMSNorm fused in front of RoPE
+        "qwen06b_decode_qknorm": with_qk_norm(Decode("", 16, 8, 128, [1025], 1e6, ROPE_NEOX, seed=1),
+                                              "qwen06b_decode_qknorm"),
+        "qwen06b_prefill_qknorm": with_qk_norm(Prefill("", 16, 8, 128, 0, 1536, 1e6, seed=2),
+                                               "qwen06b_prefill_qknorm"),
     }

@@ -1,7 +1,7 @@
 """Writes the golden fixtures in this directory from the compiled reference.
 
 The reference's CPU attention and RoPE sources
-(common/kernels/{attention,rope,vecops_avx,vecops_generic,threading}.c) are
+(common/kernels/{attention,rope,rmsnorm,vecops_avx,vecops_generic,threading}.c) are
 compiled by ``oracle/Makefile`` into ``oracle/_ref/``; this script calls that
 library (single-threaded) on seeded inputs and stores the outputs. Inputs are
 not stored: they are regenerated from the recorded seeds with
@@ -22,7 +22,7 @@ sys.path.insert(0, os.path.join(ROOT, "smol-genius_amd"))
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 import synth  # noqa: E402
 from oracle import RefLib, simd_branch  # noqa: E402
-from gen_golden_inputs import bidir_inputs, causal_inputs, digest  # noqa: E402
+from gen_golden_inputs import bidir_inputs, causal_inputs, digest, norm_inputs  # noqa: E402
 
 OUT = os.path.dirname(os.path.abspath(__file__))
 
@@ -56,6 +56,19 @@ BIDIR = [
     ("b_2_256_w2", 2, 256, [0, 33, 66], 1.0),
 ]
 
+# (name, seq, H, hd, eps, std): hd 72 and 80 have a scalar tail after the
+# 16-wide blocks; std 1e-3 makes eps matter, std 30 checks the large end
+NORM = [
+    ("n_3_4_64", 3, 4, 64, 1e-6, 1.0),
+    ("n_2_4_72", 2, 4, 72, 1e-6, 1.0),
+    ("n_2_3_80", 2, 3, 80, 1e-5, 1.0),
+    ("n_2_2_96", 2, 2, 96, 1e-6, 1.0),
+    ("n_3_8_128", 3, 8, 128, 1e-6, 1.0),
+    ("n_2_2_256", 2, 2, 256, 1e-6, 1.0),
+    ("n_2_2_128_small", 2, 2, 128, 1e-5, 1e-3),
+    ("n_2_2_72_large", 2, 2, 72, 1e-6, 30.0),
+]
+
 ROPE_POS = [0, 1, 1023, 1024, 1535, 4095, 8191, 8281]
 ROPE = [(hd, theta) for hd in (64, 128, 256) for theta in (1e4, 1e6)]
 
@@ -64,7 +77,7 @@ def main():
     ref = RefLib()
     ref.set_threads(1)
     arrays, meta = {}, {"simd": simd_branch(), "ref": os.path.basename(ref.path),
-                        "causal": [], "bidir": [], "rope": []}
+                        "causal": [], "bidir": [], "rope": [], "norm": []}
     for i, (name, Hq, Hkv, hd, sq, sk, qo, win, cap) in enumerate(CAUSAL):
         seed = 1000 + i
         Q, K, V = causal_inputs(seed, Hq, Hkv, hd, sq, sk)
@@ -93,6 +106,12 @@ def main():
             arrays[tag + "_cos"], arrays[tag + "_sin"], arrays[tag + "_applied"] = c, s, y
             meta["rope"].append(dict(tag=tag, hd=hd, theta=theta, interleaved=inter,
                                      positions=ROPE_POS, seed=seed, heads=3, digest=digest(x)))
+    for i, (name, seq, H, hd, eps, std) in enumerate(NORM):
+        seed = 4000 + i
+        x, w = norm_inputs(seed, seq, H, hd, std)
+        arrays[name] = ref.rms_norm_per_head(x, w, seq, H, hd, eps)
+        meta["norm"].append(dict(name=name, seed=seed, seq=seq, H=H, hd=hd, eps=eps, std=std,
+                                 digest=digest(x, w)))
     np.savez_compressed(os.path.join(OUT, "ref_attention.npz"), **arrays)
     with open(os.path.join(OUT, "ref_attention.json"), "w") as f:
         json.dump(meta, f, indent=1)

@@ -26,3 +26,11 @@ def causal_inputs(seed, Hq, Hkv, hd, seq_q, seq_k):
 
 def bidir_inputs(seed, H, hd, seq, std):
     return tuple(synth.normal(seed * 3 + i, (seq, H * hd), std) for i in range(3))
+
+
+def norm_inputs(seed, seq, H, hd, std):
+    """x [seq, H*hd] and a per-head weight [hd] near 1 (loaders fold Gemma's
+    1 + w into the stored weight, gemma.c:166-169)."""
+    x = synth.normal(seed * 3 + 0, (seq, H * hd), std)
+    w = (1.0 + 0.1 * synth.normal(seed * 3 + 1, (hd,))).astype(np.float32)
+    return x, w

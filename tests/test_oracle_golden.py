@@ -74,3 +74,16 @@ def test_rope_apply_matches_reference(golden, oracle):
         y = oracle.apply_rope(x, data[r["tag"] + "_cos"], data[r["tag"] + "_sin"], n, 3, r["hd"],
                               interleaved=r["interleaved"])
         np.testing.assert_allclose(y, data[r["tag"] + "_applied"], rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("idx", range(8))
+def test_rms_norm_per_head_matches_reference(golden, oracle, idx):
+    from gen_golden_inputs import norm_inputs
+    meta, data = golden
+    n = meta["norm"][idx]
+    x, w = norm_inputs(n["seed"], n["seq"], n["H"], n["hd"], n["std"])
+    assert digest(x, w) == n["digest"]
+    y = oracle.rms_norm_per_head(x, w, n["seq"], n["H"], n["hd"], n["eps"])
+    # the reference is built with -ffast-math (1/sqrtf may become an estimate
+    # refined by one Newton step); the restatement computes it exactly
+    np.testing.assert_allclose(y, data[n["name"]], rtol=2e-6, atol=1e-7 * n["std"])

@@ -248,3 +248,61 @@ def test_bf16_two_pass_attention(oracle):
                             window=win, cap=cap)
         # truncation toward zero: |out| <= |want| + tiny and within one bf16 ulp (2^-7 rel)
         np.testing.assert_allclose(out, want, rtol=2 ** -7, atol=1e-6)
+
+
+# ------------------------------------------------------- per-head RMSNorm
+
+def _norm64(x, w, seq, H, hd, eps):
+    v = np.asarray(x, np.float64).reshape(seq, H, hd)
+    r = 1.0 / np.sqrt((v * v).mean(-1, keepdims=True) + eps)
+    return (v * r * np.asarray(w, np.float64)).reshape(seq, H * hd)
+
+
+@pytest.mark.parametrize("hd", [64, 72, 80, 96, 128, 256])
+def test_rms_norm_per_head_against_float64(oracle, hd):
+    seq, H, eps = 3, 5, 1e-6
+    x = rand(40 + hd, (seq, H * hd))
+    w = 1.0 + 0.1 * rand(41 + hd, (hd,))
+    for generic in (False, True):
+        oracle.set_vec_generic(generic)
+        try:
+            y = oracle.rms_norm_per_head(x, w, seq, H, hd, eps)
+        finally:
+            oracle.set_vec_generic(False)
+        np.testing.assert_allclose(y, _norm64(x, w, seq, H, hd, eps), rtol=2e-6, atol=1e-7)
+
+
+def test_rms_norm_per_head_identities(oracle):
+    seq, H, hd = 2, 3, 128
+    x = rand(50, (seq, H * hd))
+    one = np.ones(hd, np.float32)
+    # unit weight: every head row has mean square ms / (ms + eps)
+    for eps in (1e-6, 0.5):
+        y = oracle.rms_norm_per_head(x, one, seq, H, hd, eps).reshape(seq, H, hd).astype(np.float64)
+        ms = (x.reshape(seq, H, hd).astype(np.float64) ** 2).mean(-1)
+        np.testing.assert_allclose((y ** 2).mean(-1), ms / (ms + eps), rtol=1e-5)
+    # scale invariance (eps negligible) and linearity in the weight
+    y1 = oracle.rms_norm_per_head(x, one, seq, H, hd, 1e-12)
+    np.testing.assert_allclose(oracle.rms_norm_per_head(64.0 * x, one, seq, H, hd, 1e-12), y1, rtol=1e-6, atol=1e-7)
+    w = 1.0 + 0.1 * rand(51, (hd,))
+    np.testing.assert_allclose(oracle.rms_norm_per_head(x, 3.0 * w, seq, H, hd, 1e-6),
+                               3.0 * oracle.rms_norm_per_head(x, w, seq, H, hd, 1e-6), rtol=1e-6, atol=1e-7)
+    # a zero row stays zero; each head is normalised on its own
+    z = x.copy()
+    z[0, :hd] = 0.0
+    yz = oracle.rms_norm_per_head(z, w, seq, H, hd, 1e-6)
+    assert not yz[0, :hd].any()
+    np.testing.assert_array_equal(yz[0, hd:], oracle.rms_norm_per_head(x, w, seq, H, hd, 1e-6)[0, hd:])
+
+
+def test_rms_norm_planted_mistakes_are_caught(oracle):
+    seq, H, hd, eps = 2, 4, 72, 1e-5
+    x = 1e-3 * rand(52, (seq, H * hd))  # small values: eps is a visible part of the mean square
+    w = 1.0 + 0.1 * rand(53, (hd,))
+    y = oracle.rms_norm_per_head(x, w, seq, H, hd, eps)
+    ok = lambda r: np.allclose(y, r, rtol=1e-5, atol=1e-7)  # noqa: E731
+    assert ok(_norm64(x, w, seq, H, hd, eps))
+    assert not ok(_norm64(x, w, seq, H, hd, 0.0))            # eps dropped
+    assert not ok(_norm64(x, np.tile(w, H), seq, 1, H * hd, eps))  # one norm over all heads of a row
+    assert not ok(_norm64(x, w[::-1].copy(), seq, H, hd, eps))  # weight reversed
+    assert not ok(_norm64(x, np.ones(hd), seq, H, hd, eps))     # weight ignored
