@@ -79,11 +79,23 @@ def time_steps(ctx, run, steps, warmup):
 
 
 def measure(ctx, wl, steps, warmup, runner, layers=None):
+    """Runs of earlier workloads hold device caches whose release (hipFree)
+    synchronises the device; they are collected here, before the timing, and
+    the collector stays off while the steps are timed."""
+    import gc
+    import torch
+    gc.collect()
+    torch.cuda.synchronize()
     x = wl.inputs()
     per_layer = getattr(wl, "algorithmic_bytes", lambda: 64 << 20)()
     n_layers = layers or layers_for(per_layer)
     run = runner.prepare(ctx, wl, x, layers=n_layers)
-    wall, kt = time_steps(ctx, run, steps, warmup)
+    gc.collect()
+    gc.disable()
+    try:
+        wall, kt = time_steps(ctx, run, steps, warmup)
+    finally:
+        gc.enable()
     return x, run, n_layers, wall, kt
 
 
@@ -131,6 +143,7 @@ def main():
     detail = {}
     if args.only in (None, main_wl.name):
         x, run, n_layers, wall, kt = measure(ctx, main_wl, steps, warmup, runner)
+        del x, run
         flops = main_wl.flops()
         ms_step = wall / steps * 1e3
         attn_ms = kt["attn"][0] / max(1, kt["attn"][1])
@@ -164,6 +177,7 @@ def main():
         if name == "qwen17b_stream":
             x, run, n_layers, wall, kt = measure(ctx, wl, max(3, steps // 10), max(1, warmup // 5), runner,
                                                  layers=8)
+            del x, run
             n = max(3, steps // 10)
             attn_ms, attn_n = kt["attn"]
             # per step: 1 chunk launch + `steps` decode launches of the attention kernel
@@ -173,6 +187,7 @@ def main():
                             "note": "wall time per step includes 65 launches and their host dispatch"}
             continue
         x, run, n_layers, wall, kt = measure(ctx, wl, steps, warmup, runner)
+        del x, run
         attn_ms = kt["attn"][0] / max(1, kt["attn"][1])
         prep_ms = kt["prep"][0] / max(1, kt["prep"][1])
         d = {"config": wl.describe(), "layers_rotated": n_layers, "ms_per_step": round(wall / steps * 1e3, 5),

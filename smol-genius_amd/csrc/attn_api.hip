@@ -716,7 +716,9 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     int mk = timing_begin(ctx, 0);
     rc = smol_launch_prep(&pp, (int)pl.pblk.size(), ctx->stream);
     timing_end(ctx, mk);
-    if (rc) return fail(SMOL_ATTN_ERR_DEVICE, "k_prep launch: %s", hipGetErrorString(hipGetLastError()));
+    if (rc)
+        return fail(rc == -1 ? SMOL_ATTN_ERR_UNSUPPORTED : SMOL_ATTN_ERR_DEVICE, "k_prep launch (hd %d): %s", hd,
+                    rc == -1 ? "unsupported configuration" : hipGetErrorString(hipGetLastError()));
 
     SkParams sp;
     memset(&sp, 0, sizeof(sp));
@@ -971,6 +973,7 @@ extern "C" int smol_kv_cache_write(smol_kv_cache *kv, int layer, int slot, int p
     PrepParams pp;
     memset(&pp, 0, sizeof(pp));
     pp.k = kd; pp.v = vd; pp.kv_dtype = dtype; pp.kv_stride = (long long)kv->n_kv * hd;
+    pp.q_dtype = dtype; /* no Q blocks; the pre-pass is built per input type */
     pp.rope_kind = SMOL_ROPE_OFF;
     pp.Hq = kv->n_kv; pp.Hkv = kv->n_kv; pp.G = 1; pp.hd = hd; pp.hdp = (hd + 31) & ~31;
     pp.kc = kv->k + (size_t)layer * kv_layer_elems(kv);

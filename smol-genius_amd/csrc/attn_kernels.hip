@@ -209,141 +209,318 @@ __device__ __forceinline__ void rope8(const void *base, int dtype, long long row
         out[i] = d0 + i < half ? fmaf(out[i], cv[i], -(pr[i] * sv[i])) : fmaf(out[i], cv[i], pr[i] * sv[i]);
 }
 
+/* Raw bits of 8 consecutive input elements (bf16: one 16-byte load, fp32:
+ * two), held without use so that a thread's loads can all be in flight. */
+template <bool BF> struct Raw8 { uint4 a[BF ? 1 : 2]; };
+
+template <bool BF>
+__device__ __forceinline__ void raw_load(Raw8<BF> &r, const void *base, long long idx) {
+    if constexpr (BF) {
+        r.a[0] = *reinterpret_cast<const uint4 *>((const uint16_t *)base + idx);
+    } else {
+        r.a[0] = *reinterpret_cast<const uint4 *>((const float *)base + idx);
+        r.a[1] = *reinterpret_cast<const uint4 *>((const float *)base + idx + 4);
+    }
+}
+
+template <bool BF>
+__device__ __forceinline__ void raw_unpack(const Raw8<BF> &r, float *v) {
+    if constexpr (BF) {
+        unpack_bf16x8(r.a[0], v);
+    } else {
+        v[0] = __uint_as_float(r.a[0].x); v[1] = __uint_as_float(r.a[0].y);
+        v[2] = __uint_as_float(r.a[0].z); v[3] = __uint_as_float(r.a[0].w);
+        v[4] = __uint_as_float(r.a[1].x); v[5] = __uint_as_float(r.a[1].y);
+        v[6] = __uint_as_float(r.a[1].z); v[7] = __uint_as_float(r.a[1].w);
+    }
+}
+
+/* Operands of the normalised rotation of one 8-element chunk [d0, d0+8) of
+ * a head row: load() only issues loads, finish() turns them into the
+ * rotated values. NeoX partners (d0 +- hd/2) come from another lane by
+ * __shfl_xor when head_dim is 64, 128 or 256 (a row's chunks are then an
+ * aligned power-of-two group of consecutive lanes), otherwise from memory
+ * (whole chunks when hd/2 is a multiple of 8, element by element for hd 72).
+ * With a norm weight each element becomes (x * w[d]) * rinv
+ * (rmsnorm.c:119-121), then the rotation of rope.c:99-164 (NeoX) or
+ * rope.c:68-93 (interleaved) is applied. */
+template <int HD, bool BF, int RK, bool NORM>
+struct RopeChunk {
+    static constexpr int HALF = HD / 2;
+    static constexpr bool NEOX = RK == SMOL_ROPE_NEOX_K;
+    static constexpr bool SHFL = NEOX && (HD == 64 || HD == 128 || HD == 256);
+    static constexpr bool PCHUNK = NEOX && !SHFL && HALF % 8 == 0;
+    static constexpr bool PELEM = NEOX && !SHFL && HALF % 8 != 0;
+    Raw8<BF> x, p;
+    uint32_t pe[8];
+    float4 c0, c1, s0, s1, w0, w1, wp0, wp1;
+    float wpe[8];
+
+    __device__ __forceinline__ void load(const void *base, long long row, int d0, const float *cos_t,
+                                         const float *sin_t, long long pos, const float *nw) {
+        raw_load<BF>(x, base, row + d0);
+        const int p0 = d0 < HALF ? d0 + HALF : d0 - HALF;
+        if constexpr (PCHUNK) raw_load<BF>(p, base, row + p0);
+        if constexpr (PELEM) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int pd = rope_partner(d0 + i, HD, RK);
+                pe[i] = BF ? (uint32_t)((const uint16_t *)base)[row + pd] << 16
+                           : __float_as_uint(((const float *)base)[row + pd]);
+                if constexpr (NORM) wpe[i] = nw[pd];
+            }
+        }
+        if constexpr (RK != SMOL_ROPE_OFF) {
+            const float *c = cos_t + pos * HD + d0, *s = sin_t + pos * HD + d0;
+            c0 = *reinterpret_cast<const float4 *>(c); c1 = *reinterpret_cast<const float4 *>(c + 4);
+            s0 = *reinterpret_cast<const float4 *>(s); s1 = *reinterpret_cast<const float4 *>(s + 4);
+        }
+        if constexpr (NORM) {
+            w0 = make_float4(nw[d0], nw[d0 + 1], nw[d0 + 2], nw[d0 + 3]);
+            w1 = make_float4(nw[d0 + 4], nw[d0 + 5], nw[d0 + 6], nw[d0 + 7]);
+            if constexpr (PCHUNK) {
+                wp0 = make_float4(nw[p0], nw[p0 + 1], nw[p0 + 2], nw[p0 + 3]);
+                wp1 = make_float4(nw[p0 + 4], nw[p0 + 5], nw[p0 + 6], nw[p0 + 7]);
+            }
+        }
+    }
+
+    /* out = the normalised, rotated chunk; every lane of the wave must call
+     * this together when SHFL (the partner exchange is a lane shuffle) */
+    __device__ __forceinline__ void finish(float *out, int d0, float rinv) const {
+        raw_unpack<BF>(x, out);
+        if constexpr (NORM) {
+            const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) out[i] = (out[i] * w[i]) * rinv;
+        }
+        if constexpr (RK == SMOL_ROPE_OFF) return;
+        const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        if constexpr (RK == SMOL_ROPE_INTERLEAVED_K) {
+#pragma unroll
+            for (int i = 0; i < 8; i += 2) {
+                const float x0 = out[i], x1 = out[i + 1];
+                out[i] = x0 * cv[i] - x1 * sv[i];
+                out[i + 1] = x1 * cv[i + 1] + x0 * sv[i + 1];
+            }
+            return;
+        } else {
+            float pr[8];
+            if constexpr (SHFL) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) pr[i] = __shfl_xor(out[i], HALF / 8);
+            } else if constexpr (PCHUNK) {
+                raw_unpack<BF>(p, pr);
+                if constexpr (NORM) {
+                    const float w[8] = {wp0.x, wp0.y, wp0.z, wp0.w, wp1.x, wp1.y, wp1.z, wp1.w};
+#pragma unroll
+                    for (int i = 0; i < 8; i++) pr[i] = (pr[i] * w[i]) * rinv;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    pr[i] = __uint_as_float(pe[i]);
+                    if constexpr (NORM) pr[i] = (pr[i] * wpe[i]) * rinv;
+                }
+            }
+            /* NeoX: x1 c - x2 s for the first half, x2 c + x1 s for the
+             * second (rope.c:99-164, fmsub / fmadd) */
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                out[i] = d0 + i < HALF ? fmaf(out[i], cv[i], -(pr[i] * sv[i])) : fmaf(out[i], cv[i], pr[i] * sv[i]);
+        }
+    }
+};
+
 /* grid (n_blocks, Hkv), 256 threads. A Q block normalises (when a q_norm
  * weight is given), rotates and scales the G heads of its tokens into the Q
  * scratch. A fresh-slab block covers 32 positions of one KV head: old cache
  * rows are copied to the fresh buffers, new rows are normalised and rotated
  * (K), appended to the bf16 cache and written to the fresh buffers,
- * positions past the new rows are zero. Work is done in chunks of
- * 8 elements (16-byte stores); V goes through LDS so that the transposed
- * stores are 8 consecutive positions of one column. */
-__global__ __launch_bounds__(256) void k_prep(PrepParams p) {
-    const PrepBlock blk = p.blocks[blockIdx.x / (unsigned)p.Hkv];
-    const PrepBatch b = p.batches[blk.batch];
-    const int g = (int)(blockIdx.x % (unsigned)p.Hkv); /* kv head fastest: XCD-local, as the attention kernels */
-    const int hd = p.hd;
-    const int tid = threadIdx.x;
-    const int cpr = hd >> 3; /* 8-element chunks per head row */
-    __shared__ float sv[SMOL_SLAB * 257];
-
-    if (blk.kind == 1) {
-        /* Q rows: token t, head g*G + hg -> scratch row q_row0 + t*G + hg */
-        const int G = p.G, hdp = p.hdp;
-        const int cpp = hdp >> 3;
-        const int per_tok = G * cpp;
-        const int rk = (p.rope_q && p.rope_kind != SMOL_ROPE_OFF) ? p.rope_kind : SMOL_ROPE_OFF;
+ * positions past the new rows are zero. Work is done in chunks of 8 elements
+ * (16-byte stores); V goes through LDS so that the transposed stores are 8
+ * consecutive positions of one column.
+ *
+ * Built per (head_dim, input type, RoPE pairing, norm) so that a thread's
+ * chunks are a fixed, unrolled count whose loads are all issued before any
+ * of them is used: one memory round trip per pass instead of one per chunk. */
+/* Q rows of one block: token t, head g*G + hg -> scratch row q_row0 + t*G + hg */
+template <int HD, bool BF, int RK, bool NORM>
+__device__ __forceinline__ void prep_q(const PrepParams &p, const PrepBlock &blk, const PrepBatch &b, int g, int tid,
+                                       float *sv) {
+    constexpr int DT = BF ? SMOL_IN_BF16 : SMOL_IN_F32;
+    constexpr int HDP = (HD + 31) & ~31;     /* Q-scratch row, zero-padded */
+    constexpr int CPP = HDP / 8;
+    using RC = RopeChunk<HD, BF, RK, NORM>;
+    {
+        const int G = p.G;
+        const int per_tok = G * CPP;
         /* per-head RMSNorm: 1/rms of each of the block's count * G head rows
          * (the host keeps that within the LDS array) */
         float *s_qr = sv;
-        if (p.q_norm) {
+        if constexpr (NORM) {
             for (int r = tid >> 3; r < blk.count * G; r += 32) {
                 const int tl = r / G, hg = r - tl * G;
                 const long long row =
-                    (long long)(b.q_tok0 + blk.first + tl) * p.q_stride + (long long)(g * G + hg) * hd;
-                const float ri = head_rinv8(p.q, p.q_dtype, row, hd, p.norm_eps, tid & 7);
+                    (long long)(b.q_tok0 + blk.first + tl) * p.q_stride + (long long)(g * G + hg) * HD;
+                const float ri = head_rinv8(p.q, DT, row, HD, p.norm_eps, tid & 7);
                 if ((tid & 7) == 0) s_qr[r] = ri;
             }
             __syncthreads();
         }
-        /* four 8-element chunks per thread per pass, all loads issued before
-         * any store */
+        /* passes of four 8-element chunks per thread (the loop bound is
+         * block-uniform: every lane takes part in the partner shuffles) */
         const int total = blk.count * per_tok;
-        for (int e0 = tid; e0 < total; e0 += 4 * 256) {
-            float v[4][8];
+        for (int base = 0; base < total; base += 4 * 256) {
+            RC in[4];
+            float rinv[4];
             long long qi[4];
+            int dd[4];
 #pragma unroll
             for (int u = 0; u < 4; u++) {
-                const int e = e0 + 256 * u;
+                const int e = base + tid + 256 * u;
                 const int ee = e < total ? e : total - 1;
                 const int tl = ee / per_tok, rem = ee - tl * per_tok;
-                const int hg = rem / cpp, d0 = (rem - hg * cpp) * 8;
+                const int hg = rem / CPP, d0 = (rem - hg * CPP) * 8;
                 const int t = blk.first + tl;
-#pragma unroll
-                for (int i = 0; i < 8; i++) v[u][i] = 0.0f;
-                if (d0 < hd) {
-                    const long long row = (long long)(b.q_tok0 + t) * p.q_stride + (long long)(g * G + hg) * hd;
-                    rope8(p.q, p.q_dtype, row, d0, hd, rk, p.rope_cos, p.rope_sin, b.q_pos0 + t, v[u], p.q_norm,
-                          p.q_norm ? s_qr[tl * G + hg] : 1.0f);
+                dd[u] = d0;
+                rinv[u] = NORM ? s_qr[tl * G + hg] : 1.0f;
+                if (HDP == HD || d0 < HD) {
+                    const long long row = (long long)(b.q_tok0 + t) * p.q_stride + (long long)(g * G + hg) * HD;
+                    in[u].load(p.q, row, d0, p.rope_cos, p.rope_sin, b.q_pos0 + t, p.q_norm);
                 }
-                qi[u] = e < total ? (long long)g * p.qs_head_stride + (long long)(b.q_row0 + t * G + hg) * hdp + d0 : -1;
+                qi[u] = e < total ? (long long)g * p.qs_head_stride + (long long)(b.q_row0 + t * G + hg) * HDP + d0 : -1;
             }
 #pragma unroll
             for (int u = 0; u < 4; u++) {
+                float v[8];
+                in[u].finish(v, dd[u], rinv[u]);
+                if (HDP != HD && dd[u] >= HD) {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) v[i] = 0.0f;
+                }
                 if (qi[u] < 0) continue;
 #pragma unroll
-                for (int i = 0; i < 8; i++) v[u][i] *= p.qscale;
+                for (int i = 0; i < 8; i++) v[i] *= p.qscale;
                 if (p.stage == SMOL_STAGE_QF32) {
-                    *reinterpret_cast<float4 *>(p.qs32 + qi[u]) = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
-                    *reinterpret_cast<float4 *>(p.qs32 + qi[u] + 4) = make_float4(v[u][4], v[u][5], v[u][6], v[u][7]);
+                    *reinterpret_cast<float4 *>(p.qs32 + qi[u]) = make_float4(v[0], v[1], v[2], v[3]);
+                    *reinterpret_cast<float4 *>(p.qs32 + qi[u] + 4) = make_float4(v[4], v[5], v[6], v[7]);
                 } else {
-                    *reinterpret_cast<uint4 *>(p.qs + qi[u]) = pack_h8(v[u]);
+                    *reinterpret_cast<uint4 *>(p.qs + qi[u]) = pack_h8(v);
                 }
             }
         }
-        return;
     }
+}
 
-    /* fresh slab */
+/* One 32-position fresh slab of one KV head */
+template <int HD, bool BF, int RK, bool NORM>
+__device__ __forceinline__ void prep_fresh(const PrepParams &p, const PrepBlock &blk, const PrepBatch &b, int g,
+                                           int tid, float *sv, float *s_kr) {
+    constexpr int DT = BF ? SMOL_IN_BF16 : SMOL_IN_F32;
+    constexpr int CPR = HD / 8;              /* 8-element chunks per head row */
+    using RC = RopeChunk<HD, BF, RK, NORM>;
     const int pos_base = b.fresh_pos0 + blk.first * SMOL_SLAB;
     const int frow_base = b.fresh_row0 + blk.first * SMOL_SLAB;
     const bool has_cache = b.slot >= 0 && p.kc != nullptr;
-    const long long cbase = has_cache ? (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * hd : 0;
+    const long long cbase = has_cache ? (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * HD : 0;
     uint16_t *kc = has_cache ? p.kc + cbase : nullptr;
     uint16_t *vtc = has_cache ? p.vtc + cbase : nullptr;
-    _Float16 *kf = p.kf + (long long)g * p.fcap * hd;
-    _Float16 *vtf = p.vtf + (long long)g * p.fcap * hd;
+    _Float16 *kf = p.kf + (long long)g * p.fcap * HD;
+    _Float16 *vtf = p.vtf + (long long)g * p.fcap * HD;
     const int new_lo = b.kv_pos0, new_hi = b.kv_pos0 + b.n_kv;
-    const int rk = (p.rope_k && p.rope_kind != SMOL_ROPE_OFF) ? p.rope_kind : SMOL_ROPE_OFF;
 
     /* per-head RMSNorm of the new K rows: row r by lanes 8r .. 8r+7 */
-    __shared__ float s_kr[SMOL_SLAB];
-    if (p.k_norm) {
+    if constexpr (NORM) {
         const int r = tid >> 3, pos = pos_base + r;
         if (pos >= new_lo && pos < new_hi) {
-            const long long row = (long long)(b.kv_in0 + pos - new_lo) * p.kv_stride + (long long)g * hd;
-            const float ri = head_rinv8(p.k, p.kv_dtype, row, hd, p.norm_eps, tid & 7);
+            const long long row = (long long)(b.kv_in0 + pos - new_lo) * p.kv_stride + (long long)g * HD;
+            const float ri = head_rinv8(p.k, DT, row, HD, p.norm_eps, tid & 7);
             if ((tid & 7) == 0) s_kr[r] = ri;
         }
         __syncthreads();
     }
 
-    /* K rows and the new V rows (into LDS), chunk (r, d0) */
-    for (int e = tid; e < SMOL_SLAB * cpr; e += blockDim.x) {
-        const int r = e / cpr, d0 = (e - r * cpr) * 8;
+    /* K rows and the new V rows (into LDS): chunk e = (r, d0), NK per
+     * thread. Loads only sit inside the row-kind branches; the values are
+     * used after all of them are issued. */
+    constexpr int NKC = SMOL_SLAB * CPR;
+    constexpr int NK = (NKC + 255) / 256;
+    RC kin[NK];
+    Raw8<BF> vin[NK];
+    uint4 kold[NK];
+#pragma unroll
+    for (int u = 0; u < NK; u++) {
+        const int e = tid + 256 * u;
+        const int r = e / CPR, d0 = (e - r * CPR) * 8;
         const int pos = pos_base + r;
-        float kv[8] = {0, 0, 0, 0, 0, 0, 0, 0}, vv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (NKC % 256 != 0 && e >= NKC) continue;
         if (pos < new_lo) {
-            if (has_cache) unpack_bf16x8(*reinterpret_cast<const uint4 *>(kc + (long long)pos * hd + d0), kv);
+            if (has_cache) kold[u] = *reinterpret_cast<const uint4 *>(kc + (long long)pos * HD + d0);
         } else if (pos < new_hi) {
-            const long long row = (long long)(b.kv_in0 + pos - new_lo) * p.kv_stride + (long long)g * hd;
-            rope8(p.k, p.kv_dtype, row, d0, hd, rk, p.rope_cos, p.rope_sin, pos, kv, p.k_norm,
-                  p.k_norm ? s_kr[r] : 1.0f);
-            load8(p.v, p.kv_dtype, row + d0, vv);
-            if (has_cache) *reinterpret_cast<uint4 *>(kc + (long long)pos * hd + d0) = pack_bf16x8(kv);
+            const long long row = (long long)(b.kv_in0 + pos - new_lo) * p.kv_stride + (long long)g * HD;
+            kin[u].load(p.k, row, d0, p.rope_cos, p.rope_sin, pos, p.k_norm);
+            raw_load<BF>(vin[u], p.v, row + d0);
         }
-        *reinterpret_cast<uint4 *>(kf + (long long)(frow_base + r) * hd + d0) = pack_h8(kv);
+    }
+#pragma unroll
+    for (int u = 0; u < NK; u++) {
+        const int e = tid + 256 * u;
+        const int r = e / CPR, d0 = (e - r * CPR) * 8;
+        const int pos = pos_base + r;
+        const bool valid = NKC % 256 == 0 || e < NKC;
+        const bool is_new = valid && pos >= new_lo && pos < new_hi;
+        float kv[8], vv[8];
+        /* every lane computes the new-row values (the NeoX partner shuffle
+         * needs all lanes); rows that are not new discard them */
+        kin[u].finish(kv, d0, NORM && is_new ? s_kr[r] : 1.0f);
+        raw_unpack<BF>(vin[u], vv);
+        if (!valid) continue;
+        if (!is_new) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) vv[i] = 0.0f;
+            if (pos < new_lo && has_cache) unpack_bf16x8(kold[u], kv);
+            else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) kv[i] = 0.0f;
+            }
+        }
+        if (has_cache && is_new) *reinterpret_cast<uint4 *>(kc + (long long)pos * HD + d0) = pack_bf16x8(kv);
+        *reinterpret_cast<uint4 *>(kf + (long long)(frow_base + r) * HD + d0) = pack_h8(kv);
 #pragma unroll
         for (int i = 0; i < 8; i++) sv[r * 257 + d0 + i] = vv[i];
     }
     __syncthreads();
     /* V^T (slab-blocked, the slab's 32 positions of column d are contiguous):
      * chunk (d, 8 consecutive positions q0..q0+7) */
-    uint16_t *vtc_blk = has_cache ? vtc + (long long)(pos_base / SMOL_SLAB) * SMOL_SLAB * hd : nullptr;
-    _Float16 *vtf_blk = vtf + (long long)(frow_base / SMOL_SLAB) * SMOL_SLAB * hd;
-    for (int e = tid; e < hd * (SMOL_SLAB / 8); e += blockDim.x) {
+    uint16_t *vtc_blk = has_cache ? vtc + (long long)(pos_base / SMOL_SLAB) * SMOL_SLAB * HD : nullptr;
+    _Float16 *vtf_blk = vtf + (long long)(frow_base / SMOL_SLAB) * SMOL_SLAB * HD;
+    constexpr int NVC = HD * (SMOL_SLAB / 8);
+    constexpr int NV = (NVC + 255) / 256;
+    /* older cache rows of the slab: whole 16-byte chunks, all loads first */
+    uint4 vold[NV];
+#pragma unroll
+    for (int u = 0; u < NV; u++) {
+        const int e = tid + 256 * u;
+        const int d = e / (SMOL_SLAB / 8), q0 = (e - d * (SMOL_SLAB / 8)) * 8;
+        vold[u] = make_uint4(0, 0, 0, 0);
+        if ((NVC % 256 == 0 || e < NVC) && has_cache && pos_base + q0 < new_lo)
+            vold[u] = *reinterpret_cast<const uint4 *>(vtc_blk + d * SMOL_SLAB + q0);
+    }
+#pragma unroll
+    for (int u = 0; u < NV; u++) {
+        const int e = tid + 256 * u;
+        if (NVC % 256 != 0 && e >= NVC) continue;
         const int d = e / (SMOL_SLAB / 8), q0 = (e - d * (SMOL_SLAB / 8)) * 8;
         const int pos = pos_base + q0;
         const int ci = d * SMOL_SLAB + q0;
         float v[8];
-        if (pos + 8 <= new_lo) {
-            if (has_cache) unpack_bf16x8(*reinterpret_cast<const uint4 *>(vtc_blk + ci), v);
-            else { for (int i = 0; i < 8; i++) v[i] = 0.0f; }
-        } else {
+        unpack_bf16x8(vold[u], v);
+        if (pos + 8 > new_lo) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int ps = pos + i;
-                v[i] = ps < new_lo ? (has_cache ? bf16_to_f32(vtc_blk[ci + i]) : 0.0f) : sv[(q0 + i) * 257 + d];
-            }
+            for (int i = 0; i < 8; i++)
+                if (pos + i >= new_lo) v[i] = sv[(q0 + i) * 257 + d];
             if (has_cache) {
                 if (pos >= new_lo && pos + 8 <= new_hi) {
                     *reinterpret_cast<uint4 *>(vtc_blk + ci) = pack_bf16x8(v);
@@ -354,6 +531,26 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
             }
         }
         *reinterpret_cast<uint4 *>(vtf_blk + ci) = pack_h8(v);
+    }
+}
+
+/* NORM builds normalise Q when q_norm is given and K when k_norm is given */
+template <int HD, bool BF, int RK, bool NORM>
+__global__ __launch_bounds__(256) void k_prep(PrepParams p) {
+    /* block-uniform indices in scalar registers: the descriptors come through
+     * scalar loads */
+    const int bi = __builtin_amdgcn_readfirstlane((int)(blockIdx.x / (unsigned)p.Hkv));
+    const int g = __builtin_amdgcn_readfirstlane((int)(blockIdx.x % (unsigned)p.Hkv)); /* kv head fastest: XCD-local */
+    const PrepBlock blk = p.blocks[bi];
+    const PrepBatch b = p.batches[__builtin_amdgcn_readfirstlane(blk.batch)];
+    __shared__ float sv[SMOL_SLAB * 257];
+    __shared__ float s_kr[SMOL_SLAB];
+    if (blk.kind == 1) {
+        if (NORM && p.q_norm) prep_q<HD, BF, RK, NORM>(p, blk, b, g, threadIdx.x, sv);
+        else prep_q<HD, BF, RK, false>(p, blk, b, g, threadIdx.x, sv);
+    } else {
+        if (NORM && p.k_norm) prep_fresh<HD, BF, RK, NORM>(p, blk, b, g, threadIdx.x, sv, s_kr);
+        else prep_fresh<HD, BF, RK, false>(p, blk, b, g, threadIdx.x, sv, s_kr);
     }
 }
 
@@ -1873,11 +2070,39 @@ extern "C" int smol_launch_norm_rope(float *x, const float *w, float eps, const 
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
+template <int HD>
+static int launch_prep_hd(const PrepParams *pp, dim3 grid, hipStream_t st) {
+    /* Q and the new K are rotated together or not at all (the host sets both flags from one table) */
+    const int rk = (pp->rope_q && pp->rope_k) ? pp->rope_kind : SMOL_ROPE_OFF;
+    /* one input type for Q and the new K/V (the host passes one dtype per call) */
+    const bool bf = pp->kv_dtype == SMOL_IN_BF16;
+    if (pp->kv_dtype != pp->q_dtype || pp->rope_q != pp->rope_k) return -1;
+#define SMOL_PREP(BF, RK)                                                                        \
+    do {                                                                                         \
+        if (pp->q_norm || pp->k_norm) hipLaunchKernelGGL((k_prep<HD, BF, RK, true>), grid, dim3(256), 0, st, *pp); \
+        else hipLaunchKernelGGL((k_prep<HD, BF, RK, false>), grid, dim3(256), 0, st, *pp);      \
+    } while (0)
+    if (rk == SMOL_ROPE_OFF) { if (bf) SMOL_PREP(true, SMOL_ROPE_OFF); else SMOL_PREP(false, SMOL_ROPE_OFF); }
+    else if (rk == SMOL_ROPE_NEOX_K) { if (bf) SMOL_PREP(true, SMOL_ROPE_NEOX_K); else SMOL_PREP(false, SMOL_ROPE_NEOX_K); }
+    else if (rk == SMOL_ROPE_INTERLEAVED_K) {
+        if (bf) SMOL_PREP(true, SMOL_ROPE_INTERLEAVED_K); else SMOL_PREP(false, SMOL_ROPE_INTERLEAVED_K);
+    } else return -1;
+#undef SMOL_PREP
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
 extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t st) {
     if (n_blocks <= 0) return 0;
-    if (pp->hd > 256) return -1;
-    hipLaunchKernelGGL(k_prep, dim3(n_blocks * pp->Hkv), dim3(256), 0, st, *pp);
-    return hipGetLastError() == hipSuccess ? 0 : -3;
+    const dim3 grid(n_blocks * pp->Hkv);
+    switch (pp->hd) {
+    case 64: return launch_prep_hd<64>(pp, grid, st);
+    case 72: return launch_prep_hd<72>(pp, grid, st);
+    case 80: return launch_prep_hd<80>(pp, grid, st);
+    case 96: return launch_prep_hd<96>(pp, grid, st);
+    case 128: return launch_prep_hd<128>(pp, grid, st);
+    case 256: return launch_prep_hd<256>(pp, grid, st);
+    default: return -1;
+    }
 }
 
 template <int HD, int NT, int W>

@@ -227,6 +227,30 @@ def test_prefill_chunks(ctx, sa, oracle, wo, P, S, rope_type):
     np.testing.assert_array_equal(v_rows, synth.f32_to_bf16_bits(wo._as_f32(x["v"])))
 
 
+@pytest.mark.parametrize("hd", [64, 72, 80, 96, 128, 256])
+@pytest.mark.parametrize("rope_type", [0, 1])
+@pytest.mark.parametrize("bf", [False, True])
+def test_prefill_rope_every_head_dim(ctx, sa, oracle, wo, hd, rope_type, bf):
+    """The pre-pass's three NeoX partner paths (lane shuffle at hd 64/128/256,
+    partner chunks at 80/96, partner elements at 72) and the interleaved
+    pairing, through a chunk on a prefix (fa) and a decode step (dec)."""
+    from smol_genius_amd.workloads import Prefill
+    for P, S in [(37, 45), (40, 1)]:
+        print("prefill rope", hd, rope_type, bf, P, S, flush=True)
+        wl = Prefill("t", 4, 2, hd, P, S, 1e4, seed=90 + hd + P, in_bf16=bf)
+        wl.rope_type = rope_type
+        x = wl.inputs()
+        kv = sa.KVCache(ctx, 1, 1, 2, hd, P + S)
+        kv.write(0, 0, 0, x["cache_k"], x["cache_v"])
+        rope = sa.RopeTable(ctx, hd, wl.theta, rope_type)
+        got = sa.prefill(ctx, kv, 0, 0, rope, P, dev(x["q"], bf), dev(x["k"], bf), dev(x["v"], bf), 4, wl.scale)
+        assert_parity(got.cpu().numpy(), wo.prefill(oracle, wl, x), "hd %d rope %d P=%d S=%d" % (hd, rope_type, P, S))
+        k_rows, _ = kv.read(0, 0, P, S)
+        c, s = wo.rope_rows(oracle, np.arange(P, P + S), hd, wl.theta, rope_type == 1)
+        kn = oracle.apply_rope(wo._as_f32(x["k"]), c, s, S, 2, hd, rope_type == 1)
+        assert (k_rows == synth.f32_to_bf16_bits(kn)).mean() > 0.999
+
+
 @pytest.mark.parametrize("positions", [[0], [1], [31], [32], [33], [64, 0, 95, 7], [1000, 31, 4095]])
 def test_decode_positions(ctx, sa, oracle, wo, positions):
     from smol_genius_amd import runner
