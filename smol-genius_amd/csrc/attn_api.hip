@@ -610,10 +610,11 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     }
     int nt, w, rows_per;
     if (fb) {
-        /* SMOL_ATTN_FB_NT=2: two row tiles per wave (128-row tiles) */
+        /* 64-row tiles; SMOL_ATTN_FB_NT=2: two row tiles per wave (four
+         * waves per workgroup instead of eight) */
         nt = env_int("SMOL_ATTN_FB_NT") == 2 ? 2 : 1;
         w = 2;
-        rows_per = 64 * nt;
+        rows_per = 64;
     } else if (fa) {
         nt = (hd <= 128 && max_rows > 64) ? 2 : 1;
         if (const int ov = env_int("SMOL_ATTN_NT"))

@@ -1640,10 +1640,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
 /*
  * Prefill and windowed bidirectional attention over keys that all sit in the
  * fresh fp16 buffers (no cache slabs), for head_dim <= 128. One workgroup
- * owns one 64-row tile and needs no other workgroup: its eight waves form two
- * groups of four, the groups take the first and second half of the tile's
- * key slabs, and the two partial softmax states are merged through LDS at
- * the end. Within a group, wave w holds rows 16w .. 16w+15 of the tile.
+ * owns one 64-row tile and needs no other workgroup: its waves form two
+ * groups, the groups take the first and second half of the tile's key slabs,
+ * and the two partial softmax states are merged through LDS at the end.
+ * Within a group, wave w holds the NT row tiles 16 (w NT + t) .. +15 of the
+ * 64-row tile (four waves of one tile, or two waves of two).
  *
  * Staging is direct-to-LDS: each wave issues buffer_load_dwordx4 ... lds for
  * its share of a slab (one 1 KB LDS region per instruction, 16 bytes per
@@ -1664,7 +1665,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
  * P.V of slab i, while K of slab i+2 and V^T of slab i+1 are read from LDS;
  * then the transfer of slab i+3 is waited for and one barrier publishes it.
  */
-template <int HD>
+/* WPG waves per key group, each holding NT 16-row tiles of the 64-row item */
+template <int HD, int WPG>
 struct FbGeom {
     static constexpr int KS = (HD + 31) / 32;
     static constexpr int DT = (HD + 15) / 16;
@@ -1672,28 +1674,33 @@ struct FbGeom {
     static constexpr int KROW = 256;
     static constexpr int K_BYTES = SMOL_SLAB * KROW;
     static constexpr int V_BYTES = 16 * DT * 64;
-    static constexpr int STAGE = (K_BYTES + V_BYTES + 4095) / 4096 * 4096;
-    static constexpr int NDMA = STAGE / 4096;   /* DMA instructions per wave per slab */
+    static constexpr int STAGE = (K_BYTES + V_BYTES + 1024 * WPG - 1) / (1024 * WPG) * (1024 * WPG);
+    static constexpr int NDMA = STAGE / (1024 * WPG); /* DMA instructions per wave per slab */
     static constexpr int NSTG = 2 * 5 * STAGE <= 160 * 1024 ? 5 : 4;
     static constexpr int GROUP_BYTES = NSTG * STAGE;
 };
 
+/* NT = 1: four waves per key group (two per SIMD, 512 threads); NT = 2: two
+ * waves per key group, each holding two row tiles (one wave per SIMD, 256
+ * threads): every K / V^T fragment read from LDS then feeds two MFMAs, which
+ * halves the LDS reads per flop. One MFMA pipe per SIMD is kept busy by a
+ * single wave (measured: 16x16x32 f16 MFMAs with independent accumulators
+ * issue at the same rate from one wave per SIMD as from two). */
 template <int HD, int NT>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attn_fb(SkParams p) {
-    using Gm = FbGeom<HD>;
+__global__ __launch_bounds__(NT == 1 ? 512 : 256)
+__attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_attn_fb(SkParams p) {
+    constexpr int WPG = 4 / NT;
+    using Gm = FbGeom<HD, WPG>;
     constexpr int KS = Gm::KS, DT = Gm::DT, HDP = Gm::HDP, KROW = Gm::KROW;
     constexpr int K_BYTES = Gm::K_BYTES, STAGE = Gm::STAGE, NDMA = Gm::NDMA, NSTG = Gm::NSTG;
     constexpr int WAITN = (NSTG - 3) * NDMA; /* transfers that may stay outstanding at a step's end */
     constexpr unsigned SLAB_BYTES = SMOL_SLAB * HD * 2;
-    /* one row tile per wave: the fragments of step i+1 are read during step
-     * i into a second register set; two row tiles: one set, read at the top
-     * of the step (the registers go to the second tile's state) */
-    constexpr bool DB = NT == 1;
     static_assert(HD <= 128, "k_attn_fb covers head_dim <= 128");
     static_assert(2 * Gm::GROUP_BYTES <= 160 * 1024, "LDS");
+    static_assert(NSTG >= 3, "the step pipeline keeps three slabs resident");
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int grp = wave >> 2, wg = wave & 3;
+    const int grp = wave / WPG, wg = wave % WPG;
     const int lane = tid & 63;
     const int c = lane & 15, j = lane >> 4;
     const int g = (int)(blockIdx.x % (unsigned)p.Hkv);
@@ -1715,15 +1722,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         return it.key_begin + SMOL_SLAB * q;
     };
 
-    /* DMA geometry: region q = wg + 4e of a stage; lane offsets within the
-     * slab. The first transfers go out before anything else is set up. */
+    /* DMA geometry: region q = wg + WPG e of a stage; lane offsets within
+     * the slab. The first transfers go out before anything else is set up. */
     const rsrc_t rk = make_rsrc(p.kf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
     const rsrc_t rv = make_rsrc(p.vtf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
     unsigned d_off[NDMA];
     bool d_isk[NDMA];
 #pragma unroll
     for (int e = 0; e < NDMA; e++) {
-        const int q = wg + 4 * e;
+        const int q = wg + WPG * e;
         d_isk[e] = q * 1024 < K_BYTES;
         if (d_isk[e]) {
             const int kr = q * 4 + (lane >> 4), slot = lane & 15;
@@ -1741,7 +1748,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int e = 0; e < NDMA; e++)
             dma_1k(d_isk[e] ? rk : rv, d_off[e], so,
-                   __builtin_amdgcn_readfirstlane(lds_group + stage * STAGE + (wg + 4 * e) * 1024));
+                   __builtin_amdgcn_readfirstlane(lds_group + stage * STAGE + (wg + WPG * e) * 1024));
     };
 #pragma unroll
     for (int q = 0; q < NSTG; q++) dma(slab_k(q), q);
@@ -1896,51 +1903,38 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     /* Slab j of this group sits in stage j % NSTG. Its transfer is issued in
      * step j-NSTG (the prologue for j < NSTG) and waited for at the end of
      * step j-3. Step i computes the softmax of slab i, S of slab i+1 and P.V
-     * of slab i. With one row tile per wave, the K fragments of slab i+2 and
-     * the V^T fragments of slab i+1 are read during step i, after its QK
-     * MFMAs, so step i+1 starts from registers; with two, K of slab i+1 and
-     * V^T of slab i are read at the top of step i and arrive during its
-     * softmax. Every wave issues NDMA transfers per step: waiting until at
-     * most (NSTG-3)*NDMA are outstanding completes slab i+3. Steps past the
-     * group's own slab count (the second group may have one fewer, or none)
-     * keep the reads, transfers and barriers and skip the arithmetic. */
+     * of slab i. The K fragments of slab i+2 and the V^T fragments of slab
+     * i+1 are read at the top of step i into the second register set, so
+     * step i+1 starts from registers. Every wave issues NDMA transfers per
+     * step: waiting until at most (NSTG-3)*NDMA are outstanding completes
+     * slab i+3. Steps past the group's own slab count (the second group may
+     * have one fewer, or none) keep the reads, transfers and barriers and
+     * skip the arithmetic. */
     const int steps = n0;
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
     __syncthreads();
     f4 sa[NT][2], sb[NT][2];
-    h8 kfa[2][KS], kfb[DB ? 2 : 1][DB ? KS : 1], vfa[DT], vfb[DB ? DT : 1];
+    h8 kfa[2][KS], kfb[2][KS], vfa[DT], vfb[DT];
     read_k(0, kfa);
     qk(kfa, sa);
-    if constexpr (DB) {
-        read_k(1, kfa);
-        read_v(0, vfa);
-    }
-    int st_k = DB ? 2 % NSTG : 1, st_v = DB ? 1 : 0, st_d = 0; /* stages read in a step, stage refilled */
+    read_k(1, kfa);
+    read_v(0, vfa);
+    int st_k = 2 % NSTG, st_v = 1, st_d = 0; /* stages read in a step, stage refilled */
     auto step = [&](int i, f4 (&scur)[NT][2], f4 (&snext)[NT][2], auto &kcur, auto &knext, auto &vcur, auto &vnext)
         __attribute__((always_inline)) {
         const bool act = i < n_own;
         h8 pf[NT];
-        if constexpr (DB) {
-            /* the next step's LDS reads and the transfer of slab i+NSTG go
-             * out first and proceed during this step's arithmetic, which
-             * works from registers filled before the last barrier */
-            read_k(st_k, knext);
-            read_v(st_v, vnext);
-            dma(slab_k(i + NSTG), st_d);
-            __builtin_amdgcn_sched_barrier(0);
-            front(slab_k(i), act, scur);
-            qk(kcur, snext);
-            expo(scur, pf);
-            pv(vcur, pf);
-        } else {
-            read_k(st_k, kcur);
-            read_v(st_v, vcur);
-            front(slab_k(i), act, scur);
-            expo(scur, pf);
-            qk(kcur, snext);
-            pv(vcur, pf);
-            dma(slab_k(i + NSTG), st_d);
-        }
+        /* the next step's LDS reads and the transfer of slab i+NSTG go out
+         * first and proceed during this step's arithmetic, which works from
+         * registers filled before the last barrier */
+        read_k(st_k, knext);
+        read_v(st_v, vnext);
+        dma(slab_k(i + NSTG), st_d);
+        __builtin_amdgcn_sched_barrier(0);
+        front(slab_k(i), act, scur);
+        qk(kcur, snext);
+        expo(scur, pf);
+        pv(vcur, pf);
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
         __syncthreads();
         st_k = st_k + 1 == NSTG ? 0 : st_k + 1;
@@ -1948,19 +1942,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         st_d = st_d + 1 == NSTG ? 0 : st_d + 1;
     };
     int i = 0;
-    if constexpr (DB) {
-        for (; i + 2 <= steps; i += 2) {
-            step(i, sa, sb, kfa, kfb, vfa, vfb);
-            step(i + 1, sb, sa, kfb, kfa, vfb, vfa);
-        }
-        if (i < steps) step(i, sa, sb, kfa, kfb, vfa, vfb);
-    } else {
-        for (; i + 2 <= steps; i += 2) {
-            step(i, sa, sb, kfa, kfa, vfa, vfa);
-            step(i + 1, sb, sa, kfa, kfa, vfa, vfa);
-        }
-        if (i < steps) step(i, sa, sb, kfa, kfa, vfa, vfa);
+    for (; i + 2 <= steps; i += 2) {
+        step(i, sa, sb, kfa, kfb, vfa, vfb);
+        step(i + 1, sb, sa, kfb, kfa, vfb, vfa);
     }
+    if (i < steps) step(i, sa, sb, kfa, kfb, vfa, vfb);
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) l[nt] = row_sum4(l[nt]);
 
@@ -2173,12 +2159,13 @@ extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, i
 template <int HD>
 static int launch_fb_hd(const SkParams *sp, int n_items, int nt, hipStream_t st) {
     if (nt == 1) hipLaunchKernelGGL((k_attn_fb<HD, 1>), dim3(n_items * sp->Hkv), dim3(512), 0, st, *sp);
-    else if (nt == 2) hipLaunchKernelGGL((k_attn_fb<HD, 2>), dim3(n_items * sp->Hkv), dim3(512), 0, st, *sp);
+    else if (nt == 2) hipLaunchKernelGGL((k_attn_fb<HD, 2>), dim3(n_items * sp->Hkv), dim3(256), 0, st, *sp);
     else return -1;
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-/* k_attn_fb: one (64 nt)-row tile per item, every key in the fresh buffers */
+/* k_attn_fb: one 64-row tile per item, every key in the fresh buffers; nt
+ * row tiles per wave (512 threads for nt 1, 256 for nt 2) */
 extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st) {
     if (n_items <= 0) return 0;
     switch (hd) {
