@@ -170,7 +170,7 @@ def main():
 
     # ---------------- the other workloads
     for name in ["qwen06b_decode", "gemma_mqa_decode", "siglip_bidir", "qwen17b_stream", "qwen06b_decode_qknorm",
-                 "qwen06b_prefill_qknorm"]:
+                 "qwen06b_prefill_qknorm", "asr_encoder_bidir"]:
         if args.only not in (None, name):
             continue
         wl = wls[name]
@@ -196,7 +196,7 @@ def main():
             f = wl.flops()
             d.update(tflops_kernel=round(f / (attn_ms * 1e-3) / 1e12, 3),
                      tflops_step=round(f / (wall / steps) / 1e12, 3))
-        elif name == "siglip_bidir":
+        elif name in ("siglip_bidir", "asr_encoder_bidir"):
             f = wl.flops()
             d.update(tflops_kernel=round(f / (attn_ms * 1e-3) / 1e12, 3),
                      mfma_frac=round(f / (attn_ms * 1e-3) / 1e12 / PEAK_MFMA_TFLOPS, 5),

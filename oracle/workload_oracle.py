@@ -72,7 +72,7 @@ def prefill(orc: Oracle, wl, x, window=0, cap=0.0, q_norm=None, k_norm=None, eps
 
 
 def bidir(orc: Oracle, wl, x):
-    return orc.bidirectional_attention(_widen(x["q"]), _widen(x["k"]), _widen(x["v"]), wl.seq, wl.H, wl.hd,
+    return orc.bidirectional_attention(_as_f32(x["q"]), _as_f32(x["k"]), _as_f32(x["v"]), wl.seq, wl.H, wl.hd,
                                        wl.scale, wl.window_starts)
 
 

@@ -115,9 +115,9 @@ def _prep_bidir(ctx, wl, x, layers, device):
     import torch
     r = Run()
     r.n_layers = layers
-    r.q = [_t(x["q"], device, True) for _ in range(layers)]
-    r.k = [_t(x["k"], device, True) for _ in range(layers)]
-    r.v = [_t(x["v"], device, True) for _ in range(layers)]
+    r.q = [_t(x["q"], device, wl.in_bf16) for _ in range(layers)]
+    r.k = [_t(x["k"], device, wl.in_bf16) for _ in range(layers)]
+    r.v = [_t(x["v"], device, wl.in_bf16) for _ in range(layers)]
     r.outs = [torch.empty((wl.seq, wl.H * wl.hd), dtype=torch.float32, device=device) for _ in range(layers)]
 
     def _step(l):

@@ -20,6 +20,9 @@ common/vision/siglip.c:126-128, exports/qwen_asr/qwen_asr.c:1595-1620):
   qwen17b_stream      Qwen3-ASR-1.7B streaming: a 26-token chunk at positions
                       8192..8217 on an 8192-token bf16 cache (chunked
                       prefill), then 64 single-token decode steps.
+  asr_encoder_bidir   Qwen3-ASR-0.6B audio encoder self-attention: 14 heads of
+                      64, fp32 Q/K/V, 104-token windows over 900 tokens (the
+                      last one 68 tokens), no RoPE, scale 1/8.
   *_qknorm            qwen06b_decode / qwen06b_prefill with the decoder's
                       per-head Q/K RMSNorm (weights near 1, eps 1e-6) in
                       front of RoPE (qkn_decoder.c:487-491).
@@ -155,30 +158,32 @@ class Prefill(Workload):
 
 
 class Bidir(Workload):
-    def __init__(self, name, H, hd, window_starts, seed, std=0.5):
+    def __init__(self, name, H, hd, window_starts, seed, std=0.5, in_bf16=True):
         self.name, self.H, self.hd = name, H, hd
         self.window_starts = list(window_starts)
         self.seq = window_starts[-1]
-        self.seed, self.std = seed, std
+        self.seed, self.std, self.in_bf16 = seed, std, in_bf16
         self.scale = scale_of(hd)
 
     def inputs(self):
         s = self.seed * 100
         shp = (self.seq, self.H * self.hd)
-        return dict(q=synth.f32_to_bf16_bits(synth.normal(s + 1, shp, self.std)),
-                    k=synth.f32_to_bf16_bits(synth.normal(s + 2, shp, self.std)),
-                    v=synth.f32_to_bf16_bits(synth.normal(s + 3, shp, self.std)))
+        cvt = synth.f32_to_bf16_bits if self.in_bf16 else (lambda a: a)
+        return dict(q=cvt(synth.normal(s + 1, shp, self.std)),
+                    k=cvt(synth.normal(s + 2, shp, self.std)),
+                    v=cvt(synth.normal(s + 3, shp, self.std)))
 
     def flops(self):
         ws = self.window_starts
         return sum(4 * self.hd * self.H * (b - a) ** 2 for a, b in zip(ws[:-1], ws[1:]))
 
     def algorithmic_bytes(self):
-        return self.seq * self.H * self.hd * (3 * 2 + 4)
+        return self.seq * self.H * self.hd * (3 * (2 if self.in_bf16 else 4) + 4)
 
     def describe(self):
         return {"workload": self.name, "n_heads": self.H, "head_dim": self.hd,
-                "windows": len(self.window_starts) - 1, "tokens": self.seq, "inputs": "bf16"}
+                "windows": len(self.window_starts) - 1, "tokens": self.seq,
+                "inputs": "bf16" if self.in_bf16 else "f32"}
 
 
 class Stream(Workload):
@@ -227,6 +232,10 @@ def all_workloads():
         "gemma_mqa_decode": Decode("gemma_mqa_decode", 8, 1, 256, gemma_lengths(), 1e4, ROPE_INTERLEAVED,
                                    seed=4),
         "qwen17b_stream": Stream("qwen17b_stream", 16, 8, 128, 8192, 26, 64, 1e6, seed=5),
+        # Qwen3-ASR-0.6B audio encoder self-attention: 14 heads of 64, fp32 projections, 104-token
+        # windows (encoder.c:426-434) over 900 tokens, the last window ragged
+        "asr_encoder_bidir": Bidir("asr_encoder_bidir", 14, 64, list(range(0, 900, 104)) + [900], seed=6, std=1.0,
+                                   in_bf16=False),
         # the same decode step and prefill with the per-head Q/K RMSNorm fused in front of RoPE
         "qwen06b_decode_qknorm": with_qk_norm(Decode("", 16, 8, 128, [1025], 1e6, ROPE_NEOX, seed=1),
                                               "qwen06b_decode_qknorm"),

@@ -49,7 +49,8 @@ def widen(b):
 # ------------------------------------------------------------- full workloads
 
 @pytest.mark.parametrize("name", ["qwen06b_decode", "qwen06b_prefill", "siglip_bidir", "gemma_mqa_decode",
-                                  "qwen17b_stream", "qwen06b_decode_qknorm", "qwen06b_prefill_qknorm"])
+                                  "qwen17b_stream", "qwen06b_decode_qknorm", "qwen06b_prefill_qknorm",
+                                  "asr_encoder_bidir"])
 def test_workload_full_size(ctx, oracle, wo, name):
     from smol_genius_amd import runner, workloads
     print("case", name, flush=True)
