@@ -170,7 +170,7 @@ def main():
 
     # ---------------- the other workloads
     for name in ["qwen06b_decode", "gemma_mqa_decode", "siglip_bidir", "qwen17b_stream", "qwen06b_decode_qknorm",
-                 "qwen06b_prefill_qknorm", "asr_encoder_bidir"]:
+                 "qwen06b_prefill_qknorm", "asr_encoder_bidir", "qwen06b_decode_x28"]:
         if args.only not in (None, name):
             continue
         wl = wls[name]

@@ -184,6 +184,16 @@ SMOL_ATTN_API int smol_attn_causal(smol_attn_ctx *ctx, const void *q, const void
                                    int n_kv_heads, int head_dim, float scale, int q_offset,
                                    int window, float cap, float *out);
 
+/* The attention of the bf16 decoder (common/decoder/qkn_bf16_decoder.c:
+ * 120-229, bf16_causal_attention_softcap / bf16_swa_attention_softcap): bf16
+ * Q/K/V in, bf16 out rounded by truncation (f32_to_bf16, :30-35); window
+ * and cap as in smol_attn_causal. The result is computed in fp32 first
+ * (a workspace of seq_q * n_heads * head_dim floats in the context). */
+SMOL_ATTN_API int smol_attn_causal_bf16(smol_attn_ctx *ctx, const uint16_t *q, const uint16_t *k,
+                                        const uint16_t *v, int seq_q, int seq_k, int n_heads,
+                                        int n_kv_heads, int head_dim, float scale, int q_offset,
+                                        int window, float cap, uint16_t *out);
+
 /* Windowed bidirectional attention on device arrays: the device form of
  * smol_bidirectional_attention (attention.c:32-77). Q, K, V, out:
  * [seq][n_heads*hd]; window_starts: host array of n_windows + 1 offsets

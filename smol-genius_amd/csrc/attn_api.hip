@@ -30,6 +30,7 @@ extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t 
 extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, int w, int staged, hipStream_t st);
 extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
 extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st);
+extern "C" int smol_launch_to_bf16_trunc(const float *x, uint16_t *y, long long n, hipStream_t st);
 extern "C" int smol_launch_norm_rope(float *x, const float *w, float eps, const float *cos_t, const float *sin_t,
                                      const int *pos, int seq, int n_heads, int hd, int kind, hipStream_t st);
 
@@ -116,6 +117,7 @@ struct smol_attn_ctx {
     std::vector<unsigned char> desc_last; /* host bytes of the last upload to `desc` */
     DevBuf qs, kf, vtf, part_o, part_ml, counters;
     DevBuf qs32; /* fp32 Q scratch of the decode kernel */
+    DevBuf out32; /* fp32 result of a call whose output is bf16 */
     int cu_count = 256;
     /* opt-in per-kernel timing: events bracketing each launch */
     bool timing = false;
@@ -237,7 +239,7 @@ extern "C" int smol_attn_ctx_destroy(smol_attn_ctx *ctx) {
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
     DevBuf *bufs[] = {&ctx->desc, &ctx->qs, &ctx->kf, &ctx->vtf, &ctx->part_o, &ctx->part_ml, &ctx->counters,
-                      &ctx->qs32};
+                      &ctx->qs32, &ctx->out32};
     for (DevBuf *b : bufs)
         if (b->p) hipFree(b->p);
     for (auto &s : ctx->ring) {
@@ -908,6 +910,24 @@ extern "C" int smol_attn_causal(smol_attn_ctx *ctx, const void *q, const void *k
     CallShape cs{false, q, k, v, dtype, n_heads, n_kv_heads, hd, (long long)n_heads * hd,
                  (long long)n_kv_heads * hd, scale, cap, window, nullptr, 0, 0, nullptr, 0, out};
     return run_plan(ctx, pl, cs);
+}
+
+extern "C" int smol_attn_causal_bf16(smol_attn_ctx *ctx, const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                     int seq_q, int seq_k, int n_heads, int n_kv_heads, int hd, float scale,
+                                     int q_offset, int window, float cap, uint16_t *out) {
+    if (!ctx) return fail(SMOL_ATTN_ERR_ARG, "ctx is NULL");
+    if (!out || ((uintptr_t)out & 15)) return fail(SMOL_ATTN_ERR_ARG, "out must be a 16-byte aligned array");
+    if (seq_q <= 0 || n_heads <= 0 || hd <= 0) return fail(SMOL_ATTN_ERR_ARG, "seq_q %d", seq_q);
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    const long long n = (long long)seq_q * n_heads * hd;
+    if ((rc = dev_reserve(ctx->out32, (size_t)n * 4, ctx->stream))) return rc;
+    if ((rc = smol_attn_causal(ctx, q, k, v, SMOL_ATTN_BF16, seq_q, seq_k, n_heads, n_kv_heads, hd, scale, q_offset,
+                               window, cap, (float *)ctx->out32.p)))
+        return rc;
+    if (smol_launch_to_bf16_trunc((const float *)ctx->out32.p, out, n, ctx->stream))
+        return fail(SMOL_ATTN_ERR_DEVICE, "bf16 output: %s", hipGetErrorString(hipGetLastError()));
+    return SMOL_ATTN_OK;
 }
 
 extern "C" int smol_attn_bidirectional(smol_attn_ctx *ctx, const void *q, const void *k,

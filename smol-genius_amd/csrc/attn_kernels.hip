@@ -2044,7 +2044,32 @@ __global__ __launch_bounds__(256) void k_norm_rope(float *x, const float *w, flo
     }
 }
 
+/* ------------------------------------------------------------ k_to_bf16 */
+
+/* y = the upper 16 bits of x (bf16 by truncation, the f32_to_bf16 of
+ * common/decoder/qkn_bf16_decoder.c:30-35), 8 elements per thread */
+__global__ __launch_bounds__(256) void k_to_bf16_trunc(const float *x, uint16_t *y, long long n) {
+    const long long i0 = ((long long)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (i0 + 8 <= n) {
+        const float4 a = *reinterpret_cast<const float4 *>(x + i0), b = *reinterpret_cast<const float4 *>(x + i0 + 4);
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) w[k] = (__float_as_uint(v[2 * k]) >> 16) | (__float_as_uint(v[2 * k + 1]) & 0xFFFF0000u);
+        *reinterpret_cast<uint4 *>(y + i0) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+        for (long long i = i0; i < n; i++) y[i] = (uint16_t)(__float_as_uint(x[i]) >> 16);
+    }
+}
+
 /* ------------------------------------------------------------ launchers */
+
+extern "C" int smol_launch_to_bf16_trunc(const float *x, uint16_t *y, long long n, hipStream_t st) {
+    if (n <= 0) return 0;
+    const long long threads = (n + 7) / 8;
+    hipLaunchKernelGGL(k_to_bf16_trunc, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, x, y, n);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
 
 extern "C" int smol_launch_norm_rope(float *x, const float *w, float eps, const float *cos_t, const float *sin_t,
                                      const int *pos, int seq, int n_heads, int hd, int kind, hipStream_t st) {

@@ -59,6 +59,8 @@ SIGNATURES = [
                           _c_float, _c_int, _c_float, _vp], _c_int),
     ("smol_attn_causal", [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                           _c_float, _c_int, _c_int, _c_float, _vp], _c_int),
+    ("smol_attn_causal_bf16", [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int,
+                               _c_float, _vp], _c_int),
     ("smol_attn_bidirectional", [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float, _IP,
                                  _c_int, _vp], _c_int),
     ("smol_attn_prefill_qknorm", [_vp, _vp, _c_int, _c_int, _vp, _c_int, _c_int, _vp, _vp, _vp, _c_int,
@@ -325,6 +327,22 @@ def causal(ctx, q, k, v, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_o
     _check(load().smol_attn_causal(ctx.h, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), _dtype_code(q), seq_q,
                                    seq_k, n_heads, n_kv_heads, head_dim, ctypes.c_float(scale), q_offset,
                                    window, ctypes.c_float(cap), _dev(out, "out")), "smol_attn_causal")
+    return out
+
+
+def causal_bf16(ctx, q, k, v, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset, window=0, cap=0.0,
+                out=None):
+    """bf16 in, bf16 out (truncated); see smol_attn_causal_bf16. Returns a
+    torch int16 tensor holding the bf16 bits."""
+    import torch
+    for t, nm in ((q, "q"), (k, "k"), (v, "v")):
+        if t.dtype != torch.bfloat16:
+            raise SmolAttnError("%s must be bfloat16" % nm)
+    if out is None:
+        out = torch.empty((seq_q, n_heads * head_dim), dtype=torch.int16, device=q.device)
+    _check(load().smol_attn_causal_bf16(ctx.h, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), seq_q, seq_k, n_heads,
+                                        n_kv_heads, head_dim, ctypes.c_float(scale), q_offset, window,
+                                        ctypes.c_float(cap), _dev(out, "out")), "smol_attn_causal_bf16")
     return out
 
 

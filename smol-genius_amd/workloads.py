@@ -20,6 +20,7 @@ common/vision/siglip.c:126-128, exports/qwen_asr/qwen_asr.c:1595-1620):
   qwen17b_stream      Qwen3-ASR-1.7B streaming: a 26-token chunk at positions
                       8192..8217 on an 8192-token bf16 cache (chunked
                       prefill), then 64 single-token decode steps.
+  qwen06b_decode_x28  qwen06b_decode's step for 28 sequences in one call.
   asr_encoder_bidir   Qwen3-ASR-0.6B audio encoder self-attention: 14 heads of
                       64, fp32 Q/K/V, 104-token windows over 900 tokens (the
                       last one 68 tokens), no RoPE, scale 1/8.
@@ -232,6 +233,9 @@ def all_workloads():
         "gemma_mqa_decode": Decode("gemma_mqa_decode", 8, 1, 256, gemma_lengths(), 1e4, ROPE_INTERLEAVED,
                                    seed=4),
         "qwen17b_stream": Stream("qwen17b_stream", 16, 8, 128, 8192, 26, 64, 1e6, seed=5),
+        # C1's decode step for 28 sequences in one call (28 x 4.2 MB): the same kernel when the launch
+        # and the memory latency are spread over enough bytes
+        "qwen06b_decode_x28": Decode("qwen06b_decode_x28", 16, 8, 128, [1025] * 28, 1e6, ROPE_NEOX, seed=7),
         # Qwen3-ASR-0.6B audio encoder self-attention: 14 heads of 64, fp32 projections, 104-token
         # windows (encoder.c:426-434) over 900 tokens, the last window ragged
         "asr_encoder_bidir": Bidir("asr_encoder_bidir", 14, 64, list(range(0, 900, 104)) + [900], seed=6, std=1.0,

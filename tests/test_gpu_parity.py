@@ -349,3 +349,22 @@ def test_errors_are_reported(ctx, sa):
         sa.decode(ctx, kv, 0, None, [0], [3], q[:1], k[:1], k[:1], 3, 0.125)
     with pytest.raises(sa.SmolAttnError, match="layer"):
         sa.prefill(ctx, kv, 5, 0, None, 0, q, k, k, 4, 0.125)
+
+
+@pytest.mark.parametrize("Hq,Hkv,hd,sq,sk,qo,window,cap", [
+    (8, 1, 256, 6, 33, 27, 0, 0.0), (8, 1, 256, 1, 300, 299, 0, 50.0), (4, 2, 128, 26, 200, 174, 64, 30.0),
+    (8, 4, 64, 40, 40, 0, 16, 0.0), (4, 4, 72, 9, 9, 0, 0, 0.0)])
+def test_causal_bf16_out(ctx, sa, oracle, Hq, Hkv, hd, sq, sk, qo, window, cap):
+    """bf16 in / bf16 out (truncated) against the restated two-pass attention of
+    the bf16 decoder (qkn_bf16_decoder.c:120-229); both sides truncate an fp32
+    result, so they differ by at most one bf16 step where the fp32 results
+    straddle one."""
+    print("causal_bf16", Hq, Hkv, hd, sq, sk, qo, window, cap, flush=True)
+    q = synth.f32_to_bf16_bits(synth.normal(110 + hd, (sq, Hq * hd)))
+    k = synth.f32_to_bf16_bits(synth.normal(111 + hd, (sk, Hkv * hd)))
+    v = synth.f32_to_bf16_bits(synth.normal(112 + hd, (sk, Hkv * hd)))
+    sc = 1.0 / np.sqrt(hd)
+    got = sa.causal_bf16(ctx, dev(q, True), dev(k, True), dev(v, True), sq, sk, Hq, Hkv, hd, sc, qo, window=window,
+                         cap=cap).cpu().numpy().view(np.uint16)
+    want = oracle.bf16_attention(q, k, v, sq, sk, Hq, Hkv, hd, sc, qo, window=window, cap=cap)
+    assert_parity(widen(got), widen(want), "causal_bf16 hd %d" % hd)
