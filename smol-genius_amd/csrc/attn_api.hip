@@ -575,7 +575,8 @@ static void plan_items(Plan &pl, int Hkv, int G, int window, int rows_per, int c
             int ke = std::min(t.hi, kb + per_split * SMOL_SLAB);
             if (sp > 0 && kb >= t.hi) break;
             if (ke < kb) ke = kb;
-            tmp.push_back({t.batch, t.row0, kb, ke, group, 0, made++, 0});
+            const SkBatch &sb = pl.sb[t.batch];
+            tmp.push_back({t.batch, t.row0, kb, ke, group, 0, made++, sb.fresh_row0 - sb.fresh_pos0});
         }
         for (SkItem &it : tmp) {
             it.n_split = made;

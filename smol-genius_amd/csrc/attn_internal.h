@@ -54,7 +54,7 @@ typedef struct {
     int group;       /* merge group id (one output row tile) */
     int n_split;     /* items in the group */
     int split;       /* index of this item in its group */
-    int pad;
+    int fresh_off;   /* the batch's fresh_row0 - fresh_pos0: fresh row of key k is k + fresh_off */
 } SkItem;
 
 /* Q-scratch format written by k_prep (fresh K / V^T are fp16 in both):

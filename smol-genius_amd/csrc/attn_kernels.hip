@@ -1005,7 +1005,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
     /* slab k0's resource and slab offset: a uniform choice (SGPRs) */
     auto slab_src = [&](int k0, bool value, rsrc_t &r, unsigned &so) {
         const bool fr = k0 >= b.fresh_pos0;
-        const int kr = fr ? b.fresh_row0 + (k0 - b.fresh_pos0) : k0;
+        const int kr = fr ? k0 + it.fresh_off : k0;
         so = (unsigned)(kr / SMOL_SLAB) * SLAB_K_BYTES;
         r = value ? (fr ? rv_f : rv_c) : (fr ? rk_f : rk_c);
     };
@@ -1400,7 +1400,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
     };
     auto issue = [&](int k0, Stg &s) __attribute__((always_inline)) {
         const bool fr = k0 >= b.fresh_pos0;
-        const int kr = fr ? b.fresh_row0 + (k0 - b.fresh_pos0) : k0;
+        const int kr = fr ? k0 + it.fresh_off : k0;
         const unsigned so = (unsigned)(kr / SMOL_SLAB) * SLAB_BYTES;
         const rsrc_t rk = fr ? rk_f : rk_c, rv = fr ? rv_f : rv_c;
 #pragma unroll
@@ -1743,7 +1743,7 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
         }
     }
     auto dma = [&](int k0, int stage) __attribute__((always_inline)) {
-        const int kr = b.fresh_row0 + (k0 - b.fresh_pos0);
+        const int kr = k0 + it.fresh_off; /* from the item: the transfers need no batch load */
         const unsigned so = (unsigned)(kr / SMOL_SLAB) * SLAB_BYTES;
 #pragma unroll
         for (int e = 0; e < NDMA; e++)
