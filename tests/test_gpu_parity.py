@@ -368,3 +368,85 @@ def test_causal_bf16_out(ctx, sa, oracle, Hq, Hkv, hd, sq, sk, qo, window, cap):
                          cap=cap).cpu().numpy().view(np.uint16)
     want = oracle.bf16_attention(q, k, v, sq, sk, Hq, Hkv, hd, sc, qo, window=window, cap=cap)
     assert_parity(widen(got), widen(want), "causal_bf16 hd %d" % hd)
+
+
+# ------------------------------------------------------------- large sizes
+
+def test_long_causal_prefill(ctx, sa, oracle, wo):
+    """4096-token causal prefill from position 0 (k_attn_fb, 64 slabs per row tile at the end)."""
+    from smol_genius_amd.workloads import Prefill
+    print("long prefill 4096", flush=True)
+    wl = Prefill("t", 8, 2, 128, 0, 4096, 1e6, seed=120)
+    x = wl.inputs()
+    kv = sa.KVCache(ctx, 1, 1, 2, 128, 4096)
+    rope = sa.RopeTable(ctx, 128, wl.theta, 0)
+    got = sa.prefill(ctx, kv, 0, 0, rope, 0, dev(x["q"], True), dev(x["k"], True), dev(x["v"], True), 8, wl.scale)
+    assert_parity(got.cpu().numpy(), wo.prefill(oracle, wl, x), "prefill 4096")
+
+
+def test_long_prefix_chunk(ctx, sa, oracle, wo):
+    """A 64-token chunk on a 16384-token cache (k_attn_fa, key ranges split across workgroups)."""
+    from smol_genius_amd.workloads import Prefill
+    print("chunk 64 on 16384", flush=True)
+    wl = Prefill("t", 8, 2, 128, 16384, 64, 1e6, seed=121)
+    x = wl.inputs()
+    kv = sa.KVCache(ctx, 1, 1, 2, 128, 16384 + 64)
+    kv.write(0, 0, 0, x["cache_k"], x["cache_v"])
+    rope = sa.RopeTable(ctx, 128, wl.theta, 0)
+    got = sa.prefill(ctx, kv, 0, 0, rope, 16384, dev(x["q"], True), dev(x["k"], True), dev(x["v"], True), 8,
+                     wl.scale)
+    assert_parity(got.cpu().numpy(), wo.prefill(oracle, wl, x), "chunk 64 on 16384")
+
+
+@pytest.mark.parametrize("hq,hkv,hd", [(16, 8, 128), (8, 1, 256)])
+def test_long_decode(ctx, sa, oracle, wo, hq, hkv, hd):
+    """Decode at position 65535 and, in the same call, at 70 (one long and one short split group)."""
+    from smol_genius_amd import runner
+    from smol_genius_amd.workloads import Decode
+    print("decode 65536 hd", hd, flush=True)
+    wl = Decode("t", hq, hkv, hd, [65536, 71], 1e6, 0, seed=122 + hd)
+    x = wl.inputs()
+    r = runner.prepare(ctx, wl, x)
+    r.step()
+    assert_parity(r.outputs(), wo.decode(oracle, wl, x), "decode 65536 hd %d" % hd)
+
+
+def test_contexts_on_two_threads(sa, oracle):
+    """One context per host thread (the reference's pool is not re-entrant,
+    threading.c:26-47): two threads, each with its own context and its own
+    stream, run causal calls concurrently; every result matches the oracle."""
+    import threading
+    print("two threads", flush=True)
+    cases = [(8, 2, 128, 40, 300, 260, 1), (4, 4, 64, 64, 64, 0, 2)]
+    inputs = []
+    for Hq, Hkv, hd, sq, sk, qo, seed in cases:
+        Q = synth.normal(130 + seed, (sq, Hq * hd))
+        K = synth.normal(131 + seed, (sk, Hkv * hd))
+        V = synth.normal(132 + seed, (sk, Hkv * hd))
+        inputs.append((Q, K, V, oracle.causal_attention(Q, K, V, sq, sk, Hq, Hkv, hd, 1.0 / np.sqrt(hd), qo)))
+    results, errors = {}, []
+
+    def worker(idx):
+        try:
+            Hq, Hkv, hd, sq, sk, qo, _ = cases[idx]
+            Q, K, V, _ = inputs[idx]
+            stream = torch.cuda.Stream()
+            with torch.cuda.stream(stream):
+                c = sa.Context(0, stream=stream.cuda_stream)
+                q, k, v = dev(Q), dev(K), dev(V)
+                outs = [sa.causal(c, q, k, v, sq, sk, Hq, Hkv, hd, 1.0 / np.sqrt(hd), qo) for _ in range(20)]
+                c.synchronize()
+                results[idx] = [o.cpu().numpy() for o in outs]
+                c.close()
+        except Exception as e:  # reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(cases))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for idx, (_, _, _, want) in enumerate(inputs):
+        for got in results[idx]:
+            assert_parity(got, want, "thread %d" % idx)
