@@ -665,7 +665,11 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     const size_t n_items = pl.items.size();
     if ((rc = dev_reserve(ctx->part_o, std::max<size_t>(1, n_items) * cs.Hkv * rows_per * hd * 4, ctx->stream))) return rc;
     if ((rc = dev_reserve(ctx->part_ml, std::max<size_t>(1, n_items) * cs.Hkv * rows_per * 2 * 4, ctx->stream))) return rc;
-    if ((rc = dev_reserve(ctx->counters, (size_t)std::max(1, pl.n_groups) * cs.Hkv * 4, ctx->stream, true))) return rc;
+    /* one counter per 256-byte line: the workgroups of different groups count in
+     * at about the same time, and atomics on one line are serialised */
+    if ((rc = dev_reserve(ctx->counters, (size_t)std::max(1, pl.n_groups) * cs.Hkv * 4 * SK_COUNTER_STRIDE, ctx->stream,
+                          true)))
+        return rc;
 
     /* descriptor tables in one upload */
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };

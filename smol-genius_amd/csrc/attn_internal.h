@@ -23,6 +23,7 @@
 
 #define SMOL_SLAB 32          /* keys per inner step of the attention kernels */
 #define SK_MERGE_MAX 4096     /* max rows * n_split of one split-K merge group (the merge's LDS) */
+#define SK_COUNTER_STRIDE 64  /* ints between two merge groups' counters: one 256-byte line each */
 #define SMOL_ROWS_PER_TILE 16 /* query rows per MFMA tile (16x16x32 f16) */
 
 enum { SMOL_IN_F32 = 0, SMOL_IN_BF16 = 1 };
@@ -82,7 +83,7 @@ typedef struct {
     const SkItem *items;
     float *part_o;             /* [item][kv][rows][hd] unnormalised partial outputs */
     float *part_ml;            /* [item][kv][rows][2] (max, sum) */
-    int *counters;             /* [group][kv]; zero between calls */
+    int *counters;             /* [group][kv] at a stride of SK_COUNTER_STRIDE; zero between calls */
     /* k_attn_fa reads Q itself (q_direct = 1): input row out_tok0 + i of a
      * batch, rotated at table row q_pos0 + i and scaled by qscale */
     int q_direct;

@@ -733,7 +733,7 @@ __device__ __forceinline__ void merge_group(const SkParams &p, const SkItem &it,
         }
     }
     if (tid == 0)
-        __hip_atomic_store(p.counters + (long long)it.group * p.Hkv + g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.counters + ((long long)it.group * p.Hkv + g) * SK_COUNTER_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* Epilogue shared by the attention kernels: combines the SK_WAVES waves'
@@ -833,7 +833,7 @@ __device__ __forceinline__ void finish_item(const SkParams &p, const SkItem &it,
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         int prev = 0;
         if (lane == 0)
-            prev = __hip_atomic_fetch_add(p.counters + (long long)it.group * p.Hkv + g, 1, __ATOMIC_RELAXED,
+            prev = __hip_atomic_fetch_add(p.counters + ((long long)it.group * p.Hkv + g) * SK_COUNTER_STRIDE, 1, __ATOMIC_RELAXED,
                                           __HIP_MEMORY_SCOPE_AGENT);
         prev = __shfl(prev, 0);
         if (lane == 0) *s_last = prev == it.n_split - 1;
@@ -1626,7 +1626,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __syncthreads(); /* every wave's stores are acknowledged */
     if (tid == 0) {
-        const int prev = __hip_atomic_fetch_add(p.counters + (long long)it.group * p.Hkv + g, 1, __ATOMIC_RELAXED,
+        const int prev = __hip_atomic_fetch_add(p.counters + ((long long)it.group * p.Hkv + g) * SK_COUNTER_STRIDE, 1, __ATOMIC_RELAXED,
                                                 __HIP_MEMORY_SCOPE_AGENT);
         s_last = prev == it.n_split - 1;
     }
