@@ -1199,30 +1199,30 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
     } else {
         /* Each wave streams slabs wave, wave + SK_WAVES, ... with one K/V
          * register buffer, the next slab requested while the current one is
-         * computed and the first one before Q is loaded. A request past the
-         * wave's last slab re-reads that slab, so every wait sees the same
+         * computed and the first one before Q is loaded. The last slab is
+         * peeled off the loop, so no load is left in flight for the
+         * epilogue's wait, and every wait inside the loop sees the same
          * number of loads in flight. */
         int k0 = it.key_begin + wave * SMOL_SLAB;
         if (k0 < end) {
-            const int last = k0 + ((end - 1 - k0) / step) * step; /* this wave's last slab */
             KRaw kr;
             VRaw vr;
             issue_k(k0, kr);
             issue_v(k0, vr);
             load_q();
-            while (true) {
-                const int kn = k0 + step < last ? k0 + step : last;
+            auto slab = [&](auto issue_tag) __attribute__((always_inline)) {
+                constexpr bool ISSUE = decltype(issue_tag)::value;
                 f4 sacc[NT][2];
                 const bool fr = k0 >= b.fresh_pos0;
                 if (fr) qk(kr, sacc, std::true_type{});
                 else qk(kr, sacc, std::false_type{});
-                issue_k(kn, kr);
+                if constexpr (ISSUE) issue_k(k0 + step, kr);
                 if (fr) smpv(k0, sacc, vr, std::true_type{});
                 else smpv(k0, sacc, vr, std::false_type{});
-                issue_v(kn, vr);
-                k0 += step;
-                if (k0 >= end) break;
-            }
+                if constexpr (ISSUE) issue_v(k0 + step, vr);
+            };
+            for (; k0 + step < end; k0 += step) slab(std::true_type{});
+            slab(std::false_type{});
         } else {
             load_q();
         }
