@@ -20,6 +20,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <queue>
 #include <vector>
 
 #include "../../include/smol_attn.h"
@@ -587,6 +588,49 @@ static void plan_items(Plan &pl, int Hkv, int G, int window, int rows_per, int c
     pl.n_groups = group;
 }
 
+/* k_attn_fb item lists for n_wg workgroups (per kv head): each item, longest
+ * first, goes to the list with the least work so far. An item costs its
+ * steps (two slabs each, one per key group) plus about six steps of start-up
+ * and epilogue. The items are reordered so that item w heads list w; the
+ * result holds each item's successor in its list, -1 at the end. */
+static std::vector<int> fb_schedule(Plan &pl, int n_wg) {
+    const int n = (int)pl.items.size();
+    std::vector<int> order(n);
+    for (int i = 0; i < n; i++) order[i] = i;
+    auto cost = [&](int i) {
+        const SkItem &it = pl.items[i];
+        const int slabs = (it.key_end - it.key_begin + SMOL_SLAB - 1) / SMOL_SLAB;
+        return (slabs + 1) / 2 + 6;
+    };
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return cost(a) > cost(b); });
+    using Load = std::pair<long long, int>; /* (work, list) */
+    std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+    for (int w = 0; w < n_wg; w++) heap.push({0, w});
+    std::vector<std::vector<int>> lists(n_wg);
+    for (int i : order) {
+        Load l = heap.top();
+        heap.pop();
+        lists[l.second].push_back(i);
+        heap.push({l.first + cost(i), l.second});
+    }
+    /* new index of every item: the heads first, then the rest list by list */
+    std::vector<int> at(n, -1);
+    int k = n_wg;
+    for (int w = 0; w < n_wg; w++)
+        for (size_t e = 0; e < lists[w].size(); e++) at[lists[w][e]] = e == 0 ? w : k++;
+    std::vector<SkItem> items(n);
+    std::vector<int> next(n, -1);
+    for (int w = 0; w < n_wg; w++)
+        for (size_t e = 0; e < lists[w].size(); e++) {
+            SkItem it = pl.items[lists[w][e]];
+            it.group = at[lists[w][e]]; /* one item per merge group */
+            items[at[lists[w][e]]] = it;
+            if (e + 1 < lists[w].size()) next[at[lists[w][e]]] = at[lists[w][e + 1]];
+        }
+    pl.items.swap(items);
+    return next;
+}
+
 static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     const int hd = cs.hd, hdp = (hd + 31) & ~31;
     const int G = cs.Hq / cs.Hkv;
@@ -671,18 +715,28 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
                           true)))
         return rc;
 
+    /* k_attn_fb with more tiles than compute units: one workgroup per unit
+     * and kv head runs a list of tiles, assigned longest first to the least
+     * loaded list, instead of a second wave of workgroups that would each
+     * start up again behind the first */
+    std::vector<int> sched;
+    const int fb_wg = std::max(1, ctx->cu_count / cs.Hkv);
+    if (fb && (int)n_items > fb_wg && env_int("SMOL_ATTN_FB_SCHED") != -1) sched = fb_schedule(pl, fb_wg);
+
     /* descriptor tables in one upload */
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     const size_t o_pb = 0;
     const size_t o_pblk = al(o_pb + pl.pb.size() * sizeof(PrepBatch));
     const size_t o_sb = al(o_pblk + pl.pblk.size() * sizeof(PrepBlock));
     const size_t o_it = al(o_sb + pl.sb.size() * sizeof(SkBatch));
-    const size_t total = al(o_it + pl.items.size() * sizeof(SkItem));
+    const size_t o_sc = al(o_it + pl.items.size() * sizeof(SkItem));
+    const size_t total = al(o_sc + sched.size() * sizeof(int));
     std::vector<unsigned char> host(total);
     memcpy(host.data() + o_pb, pl.pb.data(), pl.pb.size() * sizeof(PrepBatch));
     memcpy(host.data() + o_pblk, pl.pblk.data(), pl.pblk.size() * sizeof(PrepBlock));
     memcpy(host.data() + o_sb, pl.sb.data(), pl.sb.size() * sizeof(SkBatch));
     memcpy(host.data() + o_it, pl.items.data(), pl.items.size() * sizeof(SkItem));
+    if (!sched.empty()) memcpy(host.data() + o_sc, sched.data(), sched.size() * sizeof(int));
     if ((rc = upload_desc(ctx, host.data(), total))) return rc;
     unsigned char *dd = (unsigned char *)ctx->desc.p;
 
@@ -744,6 +798,10 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     sp.part_o = (float *)ctx->part_o.p;
     sp.part_ml = (float *)ctx->part_ml.p;
     sp.counters = (int *)ctx->counters.p;
+    if (!sched.empty()) {
+        sp.sched = (const int *)(dd + o_sc);
+        sp.n_wg = fb_wg;
+    }
     if (q_direct) {
         sp.q_direct = 1;
         sp.q_in = cs.q; sp.q_dtype = cs.dtype; sp.q_stride = cs.q_stride;

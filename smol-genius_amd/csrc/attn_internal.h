@@ -84,6 +84,11 @@ typedef struct {
     float *part_o;             /* [item][kv][rows][hd] unnormalised partial outputs */
     float *part_ml;            /* [item][kv][rows][2] (max, sum) */
     int *counters;             /* [group][kv] at a stride of SK_COUNTER_STRIDE; zero between calls */
+    /* k_attn_fb: null (one item per workgroup), or [item] the next item of
+     * the same workgroup's list, -1 at its end; workgroup w starts at item w
+     * (w < n_wg, per kv head) */
+    const int *sched;
+    int n_wg;
     /* k_attn_fa reads Q itself (q_direct = 1): input row out_tok0 + i of a
      * batch, rotated at table row q_pos0 + i and scaled by qscale */
     int q_direct;

@@ -174,6 +174,51 @@ def test_bidirectional_ragged_fb(ctx, sa, oracle, monkeypatch):
     test_bidirectional_ragged(ctx, sa, oracle)
 
 
+@pytest.mark.parametrize("case", [  # Hq, Hkv, hd, seq, window, bf16 / bidirectional window starts
+    (16, 8, 128, 1536, 0, True), (32, 4, 96, 700, 0, False), (16, 4, 64, 1100, 300, False),
+    (16, 16, 64, [0, 100, 700, 750, 1600, 1601, 2000]), (12, 12, 72, [3, 500, 1025, 1090, 1700, 1800]),
+])
+def test_fb_tile_lists(ctx, sa, oracle, case, monkeypatch):
+    """More 64-row tiles than compute units: each k_attn_fb workgroup runs a
+    list of tiles (longest first to the least loaded list). Every tile is
+    computed as it is with one workgroup per tile, so the two launches agree
+    bit for bit, and both meet the oracle."""
+    print("fb lists", case, flush=True)
+    monkeypatch.setenv("SMOL_ATTN_PREFILL_KERNEL", "fb")
+    bidir = isinstance(case[3], list)
+    if bidir:
+        H, _, hd, ws = case
+        seq, Hq, Hkv = ws[-1], H, H
+        Q, K, V = (synth.round_bf16(synth.normal(60 + i, (seq, H * hd))) for i in range(3))
+        bf = True
+    else:
+        Hq, Hkv, hd, seq, window, bf = case
+        Q = synth.normal(63, (seq, Hq * hd))
+        K = synth.normal(64, (seq, Hkv * hd))
+        V = synth.normal(65, (seq, Hkv * hd))
+        if bf:
+            Q, K, V = (synth.round_bf16(a) for a in (Q, K, V))
+    sc = 1.0 / np.sqrt(hd)
+    conv = (lambda a: dev(synth.f32_to_bf16_bits(a), True)) if bf else dev
+
+    def run():
+        if bidir:
+            out = torch.zeros((seq, Hq * hd), dtype=torch.float32, device="cuda")
+            return sa.bidirectional(ctx, conv(Q), conv(K), conv(V), seq, Hq, hd, sc, ws, out=out).cpu().numpy()
+        return sa.causal(ctx, conv(Q), conv(K), conv(V), seq, seq, Hq, Hkv, hd, sc, 0, window=window).cpu().numpy()
+
+    lists = run()
+    monkeypatch.setenv("SMOL_ATTN_FB_SCHED", "-1")
+    per_tile = run()
+    assert np.array_equal(lists, per_tile)
+    if bidir:
+        want = oracle.bidirectional_attention(Q, K, V, seq, Hq, hd, sc, ws)
+        assert_parity(lists[ws[0]:], want[ws[0]:], "fb lists %s" % (case,))
+    else:
+        want = oracle.causal_attention(Q, K, V, seq, seq, Hq, Hkv, hd, sc, 0, window=window)
+        assert_parity(lists, want, "fb lists %s" % (case,))
+
+
 @pytest.mark.parametrize("window,cap", [(16, 0.0), (0, 2.0), (40, 1.5), (1, 0.0), (7, 50.0)])
 def test_window_softcap(ctx, sa, oracle, window, cap):
     # small caps so that tanh actually bends the N(0, 1) scores
