@@ -271,7 +271,11 @@ struct RopeChunk {
             }
         }
         if constexpr (RK != SMOL_ROPE_OFF) {
-            const float *c = cos_t + pos * HD + d0, *s = sin_t + pos * HD + d0;
+            /* the tables repeat the first half of a NeoX row in the second:
+             * chunks of the second half read the first, so only half of each
+             * row's cache lines are fetched */
+            const int dc = (SHFL || PCHUNK) && d0 >= HALF ? d0 - HALF : d0;
+            const float *c = cos_t + pos * HD + dc, *s = sin_t + pos * HD + dc;
             c0 = *reinterpret_cast<const float4 *>(c); c1 = *reinterpret_cast<const float4 *>(c + 4);
             s0 = *reinterpret_cast<const float4 *>(s); s1 = *reinterpret_cast<const float4 *>(s + 4);
         }
@@ -1917,7 +1921,7 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
      * step: waiting until at most (NSTG-3)*NDMA are outstanding completes
      * slab i+3. Steps past the group's own slab count (the second group may
      * have one fewer, or none) keep the reads, transfers and barriers and
-     * skip the arithmetic. */
+     * mask every key. */
     const int steps = n0;
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
     __syncthreads();
