@@ -588,13 +588,28 @@ static void plan_items(Plan &pl, int Hkv, int G, int window, int rows_per, int c
     pl.n_groups = group;
 }
 
-/* k_attn_fb item lists for n_wg workgroups (per kv head): each item, longest
- * first, goes to the list with the least work so far. An item costs its
- * steps (two slabs each, one per key group) plus about six steps of start-up
- * and epilogue. The items are reordered so that item w heads list w; the
- * result holds each item's successor in its list, -1 at the end. */
-static std::vector<int> fb_schedule(Plan &pl, int n_wg) {
+/* k_attn_fb items with their batches' fields. With n_wg > 0 (fewer
+ * workgroups per kv head than items) each item, longest first, goes to the
+ * list with the least work so far: an item costs its steps (two slabs each,
+ * one per key group) plus about six steps of start-up and epilogue. Item w
+ * heads list w; `next` links the rest. */
+static std::vector<FbItem> fb_items(const Plan &pl, int n_wg) {
     const int n = (int)pl.items.size();
+    auto record = [&](int i) {
+        const SkItem &it = pl.items[i];
+        const SkBatch &b = pl.sb[it.batch];
+        FbItem f;
+        memset(&f, 0, sizeof(f));
+        f.key_begin = it.key_begin; f.key_end = it.key_end; f.fresh_off = it.fresh_off; f.row0 = it.row0;
+        f.n_rows = b.n_rows; f.q_row0 = b.q_row0; f.out_tok0 = b.out_tok0; f.q_pos0 = b.q_pos0;
+        f.key_lo = b.key_lo; f.key_hi = b.key_hi; f.causal = b.causal; f.next = -1;
+        return f;
+    };
+    std::vector<FbItem> out(n);
+    if (n_wg <= 0) {
+        for (int i = 0; i < n; i++) out[i] = record(i);
+        return out;
+    }
     std::vector<int> order(n);
     for (int i = 0; i < n; i++) order[i] = i;
     auto cost = [&](int i) {
@@ -618,17 +633,13 @@ static std::vector<int> fb_schedule(Plan &pl, int n_wg) {
     int k = n_wg;
     for (int w = 0; w < n_wg; w++)
         for (size_t e = 0; e < lists[w].size(); e++) at[lists[w][e]] = e == 0 ? w : k++;
-    std::vector<SkItem> items(n);
-    std::vector<int> next(n, -1);
     for (int w = 0; w < n_wg; w++)
         for (size_t e = 0; e < lists[w].size(); e++) {
-            SkItem it = pl.items[lists[w][e]];
-            it.group = at[lists[w][e]]; /* one item per merge group */
-            items[at[lists[w][e]]] = it;
-            if (e + 1 < lists[w].size()) next[at[lists[w][e]]] = at[lists[w][e + 1]];
+            FbItem f = record(lists[w][e]);
+            if (e + 1 < lists[w].size()) f.next = at[lists[w][e + 1]];
+            out[at[lists[w][e]]] = f;
         }
-    pl.items.swap(items);
-    return next;
+    return out;
 }
 
 static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
@@ -719,9 +730,10 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
      * and kv head runs a list of tiles, assigned longest first to the least
      * loaded list, instead of a second wave of workgroups that would each
      * start up again behind the first */
-    std::vector<int> sched;
-    const int fb_wg = std::max(1, ctx->cu_count / cs.Hkv);
-    if (fb && (int)n_items > fb_wg && env_int("SMOL_ATTN_FB_SCHED") != -1) sched = fb_schedule(pl, fb_wg);
+    std::vector<FbItem> fbi;
+    int fb_wg = std::max(1, ctx->cu_count / cs.Hkv);
+    if (!((int)n_items > fb_wg && env_int("SMOL_ATTN_FB_SCHED") != -1)) fb_wg = 0;
+    if (fb) fbi = fb_items(pl, fb_wg);
 
     /* descriptor tables in one upload */
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
@@ -730,13 +742,13 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     const size_t o_sb = al(o_pblk + pl.pblk.size() * sizeof(PrepBlock));
     const size_t o_it = al(o_sb + pl.sb.size() * sizeof(SkBatch));
     const size_t o_sc = al(o_it + pl.items.size() * sizeof(SkItem));
-    const size_t total = al(o_sc + sched.size() * sizeof(int));
+    const size_t total = al(o_sc + fbi.size() * sizeof(FbItem));
     std::vector<unsigned char> host(total);
     memcpy(host.data() + o_pb, pl.pb.data(), pl.pb.size() * sizeof(PrepBatch));
     memcpy(host.data() + o_pblk, pl.pblk.data(), pl.pblk.size() * sizeof(PrepBlock));
     memcpy(host.data() + o_sb, pl.sb.data(), pl.sb.size() * sizeof(SkBatch));
     memcpy(host.data() + o_it, pl.items.data(), pl.items.size() * sizeof(SkItem));
-    if (!sched.empty()) memcpy(host.data() + o_sc, sched.data(), sched.size() * sizeof(int));
+    if (!fbi.empty()) memcpy(host.data() + o_sc, fbi.data(), fbi.size() * sizeof(FbItem));
     if ((rc = upload_desc(ctx, host.data(), total))) return rc;
     unsigned char *dd = (unsigned char *)ctx->desc.p;
 
@@ -798,8 +810,8 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     sp.part_o = (float *)ctx->part_o.p;
     sp.part_ml = (float *)ctx->part_ml.p;
     sp.counters = (int *)ctx->counters.p;
-    if (!sched.empty()) {
-        sp.sched = (const int *)(dd + o_sc);
+    if (fb) {
+        sp.fb_items = (const FbItem *)(dd + o_sc);
         sp.n_wg = fb_wg;
     }
     if (q_direct) {

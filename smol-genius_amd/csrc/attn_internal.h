@@ -58,6 +58,16 @@ typedef struct {
     int fresh_off;   /* the batch's fresh_row0 - fresh_pos0: fresh row of key k is k + fresh_off */
 } SkItem;
 
+/* A work item of k_attn_fb with its batch's fields (one scalar load): a
+ * 64-row tile of a batch against the keys [key_begin, key_end), all in the
+ * fresh buffers. next: the next item of the same workgroup, or -1. */
+typedef struct {
+    int key_begin, key_end, fresh_off, row0;
+    int n_rows, q_row0, out_tok0, q_pos0;
+    int key_lo, key_hi, causal, next;
+    int pad[4];
+} FbItem;
+
 /* Q-scratch format written by k_prep (fresh K / V^T are fp16 in both):
  *   SMOL_STAGE_F16    fp16 (the fp16-MFMA kernels k_attn_fb and k_attn_fa)
  *   SMOL_STAGE_QF32   fp32 (k_attn_dec splits it into bf16 hi + lo for the
@@ -84,10 +94,9 @@ typedef struct {
     float *part_o;             /* [item][kv][rows][hd] unnormalised partial outputs */
     float *part_ml;            /* [item][kv][rows][2] (max, sum) */
     int *counters;             /* [group][kv] at a stride of SK_COUNTER_STRIDE; zero between calls */
-    /* k_attn_fb: null (one item per workgroup), or [item] the next item of
-     * the same workgroup's list, -1 at its end; workgroup w starts at item w
-     * (w < n_wg, per kv head) */
-    const int *sched;
+    /* k_attn_fb: its items; workgroup w (per kv head) starts at item w and
+     * follows the items' next links */
+    const FbItem *fb_items;
     int n_wg;
     /* k_attn_fa reads Q itself (q_direct = 1): input row out_tok0 + i of a
      * batch, rotated at table row q_pos0 + i and scaled by qscale */

@@ -1708,18 +1708,18 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     const int g = (int)(blockIdx.x % (unsigned)p.Hkv);
     const int w = (int)(blockIdx.x / (unsigned)p.Hkv);
     __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * Gm::GROUP_BYTES];
-    /* item w, then (p.sched) the rest of this workgroup's list: the host's
+    /* item w, then the rest of this workgroup's list (the host's
      * longest-first assignment when the items outnumber the compute units,
-     * where a second wave of workgroups would pay its start-up again */
+     * where a second wave of workgroups would pay its start-up again) */
     int item = w;
     for (;;) {
-    const int next = p.sched ? __builtin_amdgcn_readfirstlane(p.sched[item]) : -1;
     /* lane terms are remade per item rather than held in registers across it */
     int lane = tid & 63;
     asm volatile("" : "+v"(lane));
     const int c = lane & 15, j = lane >> 4;
-    const SkItem it = p.items[item];
-    const SkBatch b = p.batches[it.batch];
+    const FbItem it = p.fb_items[item]; /* the batch's fields included: one round trip */
+    const FbItem &b = it;
+    const int next = it.next;
     const int G = p.G;
     unsigned char *gbase = smem + grp * Gm::GROUP_BYTES;
     const unsigned lds_group = (unsigned)(size_t)gbase;
@@ -2199,7 +2199,7 @@ extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, i
 
 template <int HD>
 static int launch_fb_hd(const SkParams *sp, int n_items, int nt, hipStream_t st) {
-    const int n_wg = sp->sched ? sp->n_wg : n_items; /* workgroups per kv head: the heads of the lists */
+    const int n_wg = sp->n_wg > 0 ? sp->n_wg : n_items; /* workgroups per kv head: the heads of the lists */
     if (nt == 1) hipLaunchKernelGGL((k_attn_fb<HD, 1>), dim3(n_wg * sp->Hkv), dim3(512), 0, st, *sp);
     else if (nt == 2) hipLaunchKernelGGL((k_attn_fb<HD, 2>), dim3(n_wg * sp->Hkv), dim3(256), 0, st, *sp);
     else return -1;
@@ -2207,8 +2207,8 @@ static int launch_fb_hd(const SkParams *sp, int n_items, int nt, hipStream_t st)
 }
 
 /* k_attn_fb: one 64-row tile per item, every key in the fresh buffers; nt
- * row tiles per wave (512 threads for nt 1, 256 for nt 2); with sp->sched,
- * sp->n_wg workgroups per kv head each run their list of items */
+ * row tiles per wave (512 threads for nt 1, 256 for nt 2); sp->n_wg
+ * workgroups per kv head (0: one per item) each run their list of items */
 extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st) {
     if (n_items <= 0) return 0;
     switch (hd) {
