@@ -588,6 +588,13 @@ static void plan_items(Plan &pl, int Hkv, int G, int window, int rows_per, int c
     pl.n_groups = group;
 }
 
+/* the pre-pass blocks with their batches */
+static std::vector<PrepBlockB> prep_records(const Plan &pl) {
+    std::vector<PrepBlockB> r(pl.pblk.size());
+    for (size_t i = 0; i < pl.pblk.size(); i++) r[i] = {pl.pblk[i], pl.pb[pl.pblk[i].batch]};
+    return r;
+}
+
 /* k_attn_fb items with their batches' fields. With n_wg > 0 (fewer
  * workgroups per kv head than items) each item, longest first, goes to the
  * list with the least work so far: an item costs its steps (two slabs each,
@@ -735,19 +742,22 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     if (!((int)n_items > fb_wg && env_int("SMOL_ATTN_FB_SCHED") != -1)) fb_wg = 0;
     if (fb) fbi = fb_items(pl, fb_wg);
 
-    /* descriptor tables in one upload */
+    /* descriptor tables in one upload: pre-pass blocks and items, each with
+     * its batch */
+    const std::vector<PrepBlockB> pbr = prep_records(pl);
+    std::vector<SkItemB> itr;
+    if (!fb) {
+        itr.resize(pl.items.size());
+        for (size_t i = 0; i < pl.items.size(); i++) itr[i] = {pl.items[i], pl.sb[pl.items[i].batch]};
+    }
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-    const size_t o_pb = 0;
-    const size_t o_pblk = al(o_pb + pl.pb.size() * sizeof(PrepBatch));
-    const size_t o_sb = al(o_pblk + pl.pblk.size() * sizeof(PrepBlock));
-    const size_t o_it = al(o_sb + pl.sb.size() * sizeof(SkBatch));
-    const size_t o_sc = al(o_it + pl.items.size() * sizeof(SkItem));
+    const size_t o_pblk = 0;
+    const size_t o_it = al(o_pblk + pbr.size() * sizeof(PrepBlockB));
+    const size_t o_sc = al(o_it + itr.size() * sizeof(SkItemB));
     const size_t total = al(o_sc + fbi.size() * sizeof(FbItem));
     std::vector<unsigned char> host(total);
-    memcpy(host.data() + o_pb, pl.pb.data(), pl.pb.size() * sizeof(PrepBatch));
-    memcpy(host.data() + o_pblk, pl.pblk.data(), pl.pblk.size() * sizeof(PrepBlock));
-    memcpy(host.data() + o_sb, pl.sb.data(), pl.sb.size() * sizeof(SkBatch));
-    memcpy(host.data() + o_it, pl.items.data(), pl.items.size() * sizeof(SkItem));
+    memcpy(host.data() + o_pblk, pbr.data(), pbr.size() * sizeof(PrepBlockB));
+    if (!itr.empty()) memcpy(host.data() + o_it, itr.data(), itr.size() * sizeof(SkItemB));
     if (!fbi.empty()) memcpy(host.data() + o_sc, fbi.data(), fbi.size() * sizeof(FbItem));
     if ((rc = upload_desc(ctx, host.data(), total))) return rc;
     unsigned char *dd = (unsigned char *)ctx->desc.p;
@@ -784,8 +794,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     pp.kf = (_Float16 *)ctx->kf.p; pp.vtf = (_Float16 *)ctx->vtf.p; pp.fcap = (int)fcap;
     pp.stage = cs.dec ? SMOL_STAGE_QF32 : SMOL_STAGE_F16;
     if (cs.dec) pp.qs32 = (float *)ctx->qs32.p;
-    pp.batches = (const PrepBatch *)(dd + o_pb);
-    pp.blocks = (const PrepBlock *)(dd + o_pblk);
+    pp.blocks = (const PrepBlockB *)(dd + o_pblk);
     pp.q_norm = cs.q_norm; pp.k_norm = cs.k_norm; pp.norm_eps = cs.norm_eps;
     int mk = timing_begin(ctx, 0);
     rc = smol_launch_prep(&pp, (int)pl.pblk.size(), ctx->stream);
@@ -805,8 +814,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     sp.Hq = cs.Hq; sp.Hkv = cs.Hkv; sp.G = G;
     sp.window = cs.window;
     sp.cap2 = cs.cap > 0.0f ? (float)(cs.cap * LOG2E_D) : 0.0f;
-    sp.batches = (const SkBatch *)(dd + o_sb);
-    sp.items = (const SkItem *)(dd + o_it);
+    sp.items = (const SkItemB *)(dd + o_it);
     sp.part_o = (float *)ctx->part_o.p;
     sp.part_ml = (float *)ctx->part_ml.p;
     sp.counters = (int *)ctx->counters.p;
@@ -1060,12 +1068,8 @@ extern "C" int smol_kv_cache_write(smol_kv_cache *kv, int layer, int slot, int p
     const size_t fcap = (size_t)nf;
     if ((rc = dev_reserve(ctx->kf, (size_t)kv->n_kv * fcap * hd * 2, ctx->stream))) return rc;
     if ((rc = dev_reserve(ctx->vtf, (size_t)kv->n_kv * fcap * hd * 2, ctx->stream))) return rc;
-    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-    const size_t o_blk = al(sizeof(PrepBatch));
-    std::vector<unsigned char> host(al(o_blk + pl.pblk.size() * sizeof(PrepBlock)));
-    memcpy(host.data(), pl.pb.data(), sizeof(PrepBatch));
-    memcpy(host.data() + o_blk, pl.pblk.data(), pl.pblk.size() * sizeof(PrepBlock));
-    if ((rc = upload_desc(ctx, host.data(), host.size()))) return rc;
+    const std::vector<PrepBlockB> pbr = prep_records(pl);
+    if ((rc = upload_desc(ctx, pbr.data(), pbr.size() * sizeof(PrepBlockB)))) return rc;
     PrepParams pp;
     memset(&pp, 0, sizeof(pp));
     pp.k = kd; pp.v = vd; pp.kv_dtype = dtype; pp.kv_stride = (long long)kv->n_kv * hd;
@@ -1077,8 +1081,7 @@ extern "C" int smol_kv_cache_write(smol_kv_cache *kv, int layer, int slot, int p
     pp.c_slot_stride = (long long)kv_slot_elems(kv);
     pp.cap = kv->cap;
     pp.kf = (_Float16 *)ctx->kf.p; pp.vtf = (_Float16 *)ctx->vtf.p; pp.fcap = (int)fcap;
-    pp.batches = (const PrepBatch *)ctx->desc.p;
-    pp.blocks = (const PrepBlock *)((unsigned char *)ctx->desc.p + o_blk);
+    pp.blocks = (const PrepBlockB *)ctx->desc.p;
     rc = smol_launch_prep(&pp, (int)pl.pblk.size(), ctx->stream);
     if (!on_device) {
         hipStreamSynchronize(ctx->stream);

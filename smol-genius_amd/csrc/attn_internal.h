@@ -58,6 +58,13 @@ typedef struct {
     int fresh_off;   /* the batch's fresh_row0 - fresh_pos0: fresh row of key k is k + fresh_off */
 } SkItem;
 
+/* An item with its batch, loaded together (the kernels issue one round of
+ * scalar loads for both instead of two dependent rounds) */
+typedef struct {
+    SkItem it;
+    SkBatch b;
+} SkItemB;
+
 /* A work item of k_attn_fb with its batch's fields (one scalar load): a
  * 64-row tile of a batch against the keys [key_begin, key_end), all in the
  * fresh buffers. next: the next item of the same workgroup, or -1. */
@@ -89,8 +96,7 @@ typedef struct {
     int Hq, Hkv, G;
     int window;                /* > 0: sliding window (keys > pos - window) */
     float cap2;                /* > 0: softcap in log2 units (cap * log2 e) */
-    const SkBatch *batches;
-    const SkItem *items;
+    const SkItemB *items;      /* k_attn_dec / k_attn_fa items with their batches */
     float *part_o;             /* [item][kv][rows][hd] unnormalised partial outputs */
     float *part_ml;            /* [item][kv][rows][2] (max, sum) */
     int *counters;             /* [group][kv] at a stride of SK_COUNTER_STRIDE; zero between calls */
@@ -131,6 +137,12 @@ typedef struct {
     int count;           /* Q tokens in this block */
 } PrepBlock;
 
+/* A pre-pass block with its batch (one round of scalar loads) */
+typedef struct {
+    PrepBlock blk;
+    PrepBatch b;
+} PrepBlockB;
+
 typedef struct {
     const void *q; int q_dtype; long long q_stride;
     const void *k; const void *v; int kv_dtype; long long kv_stride;
@@ -142,8 +154,7 @@ typedef struct {
     _Float16 *kf; _Float16 *vtf; int fcap;
     int stage;                 /* SMOL_STAGE_F16 or SMOL_STAGE_QF32 */
     float *qs32;
-    const PrepBatch *batches;
-    const PrepBlock *blocks;
+    const PrepBlockB *blocks;
     /* per-head RMSNorm before RoPE (null: none): weights [hd] fp32 */
     const float *q_norm; const float *k_norm; float norm_eps;
 } PrepParams;

@@ -545,8 +545,9 @@ __global__ __launch_bounds__(256) void k_prep(PrepParams p) {
      * scalar loads */
     const int bi = __builtin_amdgcn_readfirstlane((int)(blockIdx.x / (unsigned)p.Hkv));
     const int g = __builtin_amdgcn_readfirstlane((int)(blockIdx.x % (unsigned)p.Hkv)); /* kv head fastest: XCD-local */
-    const PrepBlock blk = p.blocks[bi];
-    const PrepBatch b = p.batches[__builtin_amdgcn_readfirstlane(blk.batch)];
+    const PrepBlockB rec = p.blocks[bi];
+    const PrepBlock &blk = rec.blk;
+    const PrepBatch &b = rec.b;
     __shared__ float sv[SMOL_SLAB * 257];
     __shared__ float s_kr[SMOL_SLAB];
     if (blk.kind == 1) {
@@ -906,8 +907,9 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
      * consecutive XCDs, so each XCD's L2 holds the K/V of its own heads */
     const int g = (int)(blockIdx.x % (unsigned)p.Hkv);
     const int item = (int)(blockIdx.x / (unsigned)p.Hkv);
-    const SkItem it = p.items[item];
-    const SkBatch b = p.batches[it.batch];
+    const SkItemB rec = p.items[item];
+    const SkItem &it = rec.it;
+    const SkBatch &b = rec.b;
     const int G = p.G;
     constexpr int SO = (SK_WAVES - 1) * ROWS * OSTR > 2 * SK_MERGE_MAX + 128 ? (SK_WAVES - 1) * ROWS * OSTR
                                                                           : 2 * SK_MERGE_MAX + 128;
@@ -1300,8 +1302,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
     const int c = lane & 15, j = lane >> 4;
     const int g = (int)(blockIdx.x % (unsigned)p.Hkv);
     const int item = (int)(blockIdx.x / (unsigned)p.Hkv);
-    const SkItem it = p.items[item];
-    const SkBatch b = p.batches[it.batch];
+    const SkItemB rec = p.items[item];
+    const SkItem &it = rec.it;
+    const SkBatch &b = rec.b;
     const int G = p.G;
     __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
     __shared__ int s_last;
