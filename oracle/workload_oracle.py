@@ -42,9 +42,11 @@ def _norm(orc, a, w, rows, heads, hd, eps):
     return a if w is None else orc.rms_norm_per_head(a, w, rows, heads, hd, eps)
 
 
-def decode(orc: Oracle, wl, x, q_norm=None, k_norm=None, eps=1e-6):
+def decode(orc: Oracle, wl, x, q_norm=None, k_norm=None, eps=1e-6, window=0, cap=0.0):
     """out [n_seq, Hq*hd]: per sequence, attention of the (normalised and)
-    rotated new query over its widened cache plus the rotated new key."""
+    rotated new query over its widened cache plus the rotated new key
+    (optionally a sliding window and a softcap, attention.c:153-170 and its
+    variants)."""
     inter = wl.rope_type == 1
     outs = []
     for i, L in enumerate(wl.lengths):
@@ -55,7 +57,7 @@ def decode(orc: Oracle, wl, x, q_norm=None, k_norm=None, eps=1e-6):
                             inter)
         K = np.concatenate([_widen(x["cache_k"][i]), kn], 0)
         V = np.concatenate([_widen(x["cache_v"][i]), x["v"][i:i + 1]], 0)
-        outs.append(orc.causal_attention(q, K, V, 1, L, wl.Hq, wl.Hkv, wl.hd, wl.scale, p))
+        outs.append(orc.causal_attention(q, K, V, 1, L, wl.Hq, wl.Hkv, wl.hd, wl.scale, p, window=window, cap=cap))
     return np.concatenate(outs, 0)
 
 

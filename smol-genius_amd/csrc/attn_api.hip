@@ -501,6 +501,7 @@ struct CallShape {
     float *out;
     const float *q_norm = nullptr, *k_norm = nullptr; /* per-head RMSNorm weights [hd] or null */
     float norm_eps = 0.0f;
+    bool direct = false;  /* k_attn_dec without the pre-pass (one query token and one new key per batch) */
 };
 
 
@@ -696,7 +697,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     /* decode streams slabs through registers; SMOL_ATTN_DEC_STAGED=1 selects
      * k_attn_dec's staged build (every slab of an item DMA'd into LDS at once),
      * which measured no faster on the decode workloads */
-    bool staged = cs.dec && env_int("SMOL_ATTN_DEC_STAGED") == 1;
+    bool staged = cs.dec && !cs.direct && env_int("SMOL_ATTN_DEC_STAGED") == 1;
     {
         Plan trial = pl;
         plan_items(trial, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, fa, fb, staged ? (hd > 128 ? 5 : 4) : 0);
@@ -821,6 +822,15 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     if (fb) {
         sp.fb_items = (const FbItem *)(dd + o_sc);
         sp.n_wg = fb_wg;
+    }
+    if (cs.direct) {
+        sp.dec_direct = 1;
+        sp.q_in = cs.q; sp.q_dtype = cs.dtype; sp.q_stride = cs.q_stride;
+        sp.k_in = cs.k; sp.v_in = cs.v; sp.kv_stride = cs.kv_stride;
+        sp.rope_cos = pp.rope_cos; sp.rope_sin = pp.rope_sin;
+        sp.rope_q_kind = cs.rope_q ? pp.rope_kind : SMOL_ROPE_OFF;
+        sp.qscale = pp.qscale;
+        sp.q_norm = cs.q_norm; sp.k_norm = cs.k_norm; sp.norm_eps = cs.norm_eps;
     }
     if (q_direct) {
         sp.q_direct = 1;
@@ -958,6 +968,17 @@ extern "C" int smol_attn_decode_qknorm(smol_attn_ctx *ctx, smol_kv_cache *kv, in
     if ((rc = check_rope(rope, kv->hd, max_pos + 1))) return rc;
     const int Hkv = kv->n_kv, G = n_heads / Hkv, hd = kv->hd;
     Plan pl;
+    /* k_attn_dec reads Q and the new K/V itself (no pre-pass launch):
+     * SMOL_ATTN_DEC_DIRECT=-1 keeps the pre-pass and the fresh slab */
+    const bool direct = env_int("SMOL_ATTN_DEC_DIRECT") != -1 && env_int("SMOL_ATTN_DEC_STAGED") != 1;
+    if (direct) {
+        for (int i = 0; i < n_seq; i++) /* sequence i: the cache's keys [0, pos[i]) in slabs, the new key apart */
+            pl.sb.push_back({G, i * G, i, pos[i], 0, pos[i], 1, 1 << 30, 0, slots[i], 0, 0});
+        pl.q_rows = n_seq * G;
+        CallShape cs{true, q, k_new, v_new, dtype, n_heads, Hkv, hd, (long long)n_heads * hd,
+                     (long long)Hkv * hd, scale, cap, window, rope, 1, 1, kv, layer, out, q_norm, k_norm, eps, true};
+        return run_plan(ctx, pl, cs);
+    }
     for (int i = 0; i < n_seq; i++) {
         /* sequence i: Q token i at position pos[i], one fresh slab holding pos[i] */
         const int f0 = pos[i] & ~(SMOL_SLAB - 1);

@@ -911,8 +911,11 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
     const SkItem &it = rec.it;
     const SkBatch &b = rec.b;
     const int G = p.G;
-    constexpr int SO = (SK_WAVES - 1) * ROWS * OSTR > 2 * SK_MERGE_MAX + 128 ? (SK_WAVES - 1) * ROWS * OSTR
-                                                                          : 2 * SK_MERGE_MAX + 128;
+    /* s_o: the other waves' (o) rows in the combine, the merge's arrays, and
+     * (direct decode) the staged Q rows; past the combine's rows, the new
+     * value, which wave 0 reads while the other waves fill theirs */
+    constexpr int SVN = (SK_WAVES - 1) * ROWS * OSTR;
+    constexpr int SO = SVN + HD > 2 * SK_MERGE_MAX + 128 ? SVN + HD : 2 * SK_MERGE_MAX + 128;
     /* the epilogue's arrays; with ST they reuse the slab area once every
      * wave is done with it */
     constexpr int FIN_BYTES = (SO + 2 * (SK_WAVES - 1) * ROWS + 1) * 4;
@@ -966,6 +969,226 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
                 }
                 split8(x, qh[nt][ks], ql[nt][ks]);
             }
+        }
+    };
+    /* p.dec_direct: the WG stages its Q rows, the table row of the position
+     * and the norm weights (and, for the batch's last split, the new key and
+     * value) through LDS as fp32 with one round of loads issued before the
+     * first slab's; every lane then normalises, rotates (the pre-pass's
+     * formulas) and scales its Q fragments from LDS. The last split's wave 0
+     * scores the new key against every row (s_new) and appends its bf16 K
+     * row to the cache; the value joins that wave's softmax state after the
+     * slabs (add_new_key). */
+    constexpr int QSTR = HD + 4; /* padded LDS row of a staged Q row */
+    const bool last_split = it.split == it.n_split - 1;
+    const bool owner = p.dec_direct && wave == 0 && last_split;
+    const long long cbase = (long long)b.slot * p.c_slot_stride + (long long)g * p.cap * HD;
+    float *s_vnew = s_o + SVN;             /* the new value [HD], read after the slabs */
+    float *s_q = s_o;                      /* [ROWS][QSTR] */
+    float *s_k = s_q + ROWS * QSTR;        /* new key [HD] */
+    float *s_cos = s_k + HD, *s_sin = s_cos + HD, *s_wq = s_sin + HD, *s_wk = s_wq + HD;
+    static_assert(ROWS * QSTR + 5 * HD <= SVN, "direct decode staging");
+    constexpr int C4Q = HD / 4;            /* 4-element chunks per row */
+    constexpr int NSTAGE = (ROWS * C4Q + 6 * C4Q + 64 * SK_WAVES - 1) / (64 * SK_WAVES);
+    const int n_qrows = min(ROWS, b.n_rows - it.row0);
+    const bool bf_in = p.q_dtype == SMOL_IN_BF16;
+    /* chunk e of the staged list: Q rows, cos, sin, q weights, then (last
+     * split) k, v, k weights; its global source and LDS destination */
+    auto stage_src = [&](int e, const void *&src, long long &idx, bool &f32, float *&dst) -> bool {
+        const int nq = n_qrows * C4Q;
+        if (e < nq) {
+            const int r = e / C4Q, c0 = (e - r * C4Q) * 4;
+            const int rr = it.row0 + r, qi = rr / G, hg = rr - qi * G;
+            src = p.q_in; f32 = !bf_in; dst = s_q + r * QSTR + c0;
+            idx = (long long)(b.out_tok0 + qi) * p.q_stride + (long long)(g * G + hg) * HD + c0;
+            return true;
+        }
+        e -= nq;
+        const int seg = e / C4Q, c0 = (e - seg * C4Q) * 4;
+        const long long kvrow = (long long)b.out_tok0 * p.kv_stride + (long long)g * HD;
+        switch (seg) {
+        case 0: if (p.rope_q_kind == SMOL_ROPE_OFF) return false;
+                src = p.rope_cos; f32 = true; idx = (long long)b.q_pos0 * HD + c0; dst = s_cos + c0; return true;
+        case 1: if (p.rope_q_kind == SMOL_ROPE_OFF) return false;
+                src = p.rope_sin; f32 = true; idx = (long long)b.q_pos0 * HD + c0; dst = s_sin + c0; return true;
+        case 2: if (!p.q_norm) return false;
+                src = p.q_norm; f32 = true; idx = c0; dst = s_wq + c0; return true;
+        case 3: if (!last_split) return false;
+                src = p.k_in; f32 = !bf_in; idx = kvrow + c0; dst = s_k + c0; return true;
+        case 4: if (!last_split) return false;
+                src = p.v_in; f32 = !bf_in; idx = kvrow + c0; dst = s_vnew + c0; return true;
+        case 5: if (!last_split || !p.k_norm) return false;
+                src = p.k_norm; f32 = true; idx = c0; dst = s_wk + c0; return true;
+        default: return false;
+        }
+    };
+    uint4 st_raw[NSTAGE];
+    auto stage_issue = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < NSTAGE; u++) {
+            const void *src; long long idx; bool f32; float *dst;
+            st_raw[u] = make_uint4(0, 0, 0, 0);
+            if (stage_src(tid + 64 * SK_WAVES * u, src, idx, f32, dst)) {
+                if (f32) st_raw[u] = *reinterpret_cast<const uint4 *>((const float *)src + idx);
+                else {
+                    const uint2 h = *reinterpret_cast<const uint2 *>((const uint16_t *)src + idx);
+                    st_raw[u] = make_uint4(h.x, h.y, 0, 0);
+                }
+            }
+        }
+    };
+    auto stage_store = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < NSTAGE; u++) {
+            const void *src; long long idx; bool f32; float *dst;
+            if (stage_src(tid + 64 * SK_WAVES * u, src, idx, f32, dst)) {
+                float4 v;
+                if (f32) v = make_float4(__uint_as_float(st_raw[u].x), __uint_as_float(st_raw[u].y),
+                                         __uint_as_float(st_raw[u].z), __uint_as_float(st_raw[u].w));
+                else v = make_float4(__uint_as_float(st_raw[u].x << 16), __uint_as_float(st_raw[u].x & 0xFFFF0000u),
+                                     __uint_as_float(st_raw[u].y << 16), __uint_as_float(st_raw[u].y & 0xFFFF0000u));
+                *reinterpret_cast<float4 *>(dst) = v;
+            }
+        }
+    };
+    float s_new[NT];
+    /* 8 consecutive fp32 values of LDS (16-byte aligned) */
+    auto ld8 = [&](const float *a, float *v) __attribute__((always_inline)) {
+        const float4 x = *reinterpret_cast<const float4 *>(a), y = *reinterpret_cast<const float4 *>(a + 4);
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w; v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+    };
+    /* x[i] of the staged row `row`, normalised with weights w (null: none)
+     * and rotated at element d0 + i, as rope8 does */
+    auto rot8 = [&](const float *row, int d0, const float *w, float rinv, float *x) __attribute__((always_inline)) {
+        constexpr int HALF = HD / 2;
+        float v[8];
+        ld8(row + d0, v);
+        if (w) {
+            float wv[8];
+            ld8(w + d0, wv);
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = (v[i] * wv[i]) * rinv;
+        }
+        const int kind = p.rope_q_kind;
+        if (kind == SMOL_ROPE_OFF) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) x[i] = v[i];
+            return;
+        }
+        float cv[8], sv[8];
+        ld8(s_cos + d0, cv);
+        ld8(s_sin + d0, sv);
+        if (kind == SMOL_ROPE_INTERLEAVED_K) {
+#pragma unroll
+            for (int i = 0; i < 8; i += 2) {
+                const float x0 = v[i], x1 = v[i + 1];
+                x[i] = x0 * cv[i] - x1 * sv[i];
+                x[i + 1] = x1 * cv[i + 1] + x0 * sv[i + 1];
+            }
+            return;
+        }
+        float pr[8];
+        if constexpr (HALF % 8 == 0) {
+            const int p0 = d0 < HALF ? d0 + HALF : d0 - HALF;
+            ld8(row + p0, pr);
+            if (w) {
+                float wp[8];
+                ld8(w + p0, wp);
+#pragma unroll
+                for (int i = 0; i < 8; i++) pr[i] = (pr[i] * wp[i]) * rinv;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int d = d0 + i, pd = d < HALF ? d + HALF : d - HALF;
+                pr[i] = w ? (row[pd] * w[pd]) * rinv : row[pd];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            x[i] = d0 + i < HALF ? fmaf(v[i], cv[i], -(pr[i] * sv[i])) : fmaf(v[i], cv[i], pr[i] * sv[i]);
+    };
+    auto rinv_of = [&](const float *row) __attribute__((always_inline)) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            const int d0 = 32 * ks + 8 * j;
+            if (HD % 32 == 0 || d0 < HD) {
+                float v[8];
+                ld8(row + d0, v);
+#pragma unroll
+                for (int i = 0; i < 8; i++) ss = fmaf(v[i], v[i], ss);
+            }
+        }
+        ss = row_sum4(ss);
+        return 1.0f / sqrtf(ss / (float)HD + p.norm_eps);
+    };
+    auto load_q_direct = [&]() __attribute__((always_inline)) {
+        const float krinv = owner && p.k_norm ? rinv_of(s_k) : 1.0f;
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int r = nt * 16 + c;
+            const bool valid = it.row0 + r < b.n_rows;
+            const float *qrow = s_q + (valid ? r : 0) * QSTR;
+            const float qrinv = p.q_norm ? rinv_of(qrow) : 1.0f;
+            float sd = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                const int d0 = 32 * ks + 8 * j;
+                float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                if (HD % 32 == 0 || d0 < HD) {
+                    rot8(qrow, d0, p.q_norm ? s_wq : nullptr, qrinv, x);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) x[i] = valid ? x[i] * p.qscale : 0.0f;
+                    if (owner) {
+                        float kx[8];
+                        rot8(s_k, d0, p.k_norm ? s_wk : nullptr, krinv, kx);
+#pragma unroll
+                        for (int i = 0; i < 8; i++) sd = fmaf(x[i], kx[i], sd);
+                        if (nt == 0 && c == 0)
+                            *reinterpret_cast<uint4 *>(const_cast<uint16_t *>(p.kc) + cbase + (long long)b.q_pos0 * HD + d0) =
+                                pack_bf16x8(kx); /* the cache itself: writable */
+                    }
+                }
+                split8(x, qh[nt][ks], ql[nt][ks]);
+            }
+            s_new[nt] = owner ? row_sum4(sd) : 0.0f;
+        }
+    };
+    /* the new key's term in the last split's state (exact max, no laziness),
+     * and its bf16 V^T entries in the cache */
+    auto add_new_key = [&]() __attribute__((always_inline)) {
+        float vv[DT][4];
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            const int d = 16 * dt + 4 * j;
+#pragma unroll
+            for (int i = 0; i < 4; i++) vv[dt][i] = (HD % 16 == 0 || d + i < HD) ? s_vnew[d + i] : 0.0f;
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            float sc = s_new[nt];
+            if (p.cap2 > 0.0f) sc = p.cap2 * tanhf(sc / p.cap2);
+            const float m_new = fmaxf(m[nt], sc);
+            const float alpha = __builtin_amdgcn_exp2f(m[nt] - m_new);
+            const float pn = __builtin_amdgcn_exp2f(sc - m_new);
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) o[nt][dt][i] = fmaf(pn, vv[dt][i], o[nt][dt][i] * alpha);
+            l[nt] = l[nt] * alpha + (j == 0 ? pn : 0.0f); /* l is summed over the row's four lanes later */
+            m[nt] = m_new;
+        }
+        if (c == 0) {
+            uint16_t *vt = const_cast<uint16_t *>(p.vtc) + cbase + (long long)(b.q_pos0 / SMOL_SLAB) * SMOL_SLAB * HD +
+                           b.q_pos0 % SMOL_SLAB;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int d = 16 * dt + 4 * j + i;
+                    if (HD % 16 == 0 || d < HD) vt[(long long)d * SMOL_SLAB] = f32_to_bf16(vv[dt][i]);
+                }
         }
     };
     /* the slab [k0, k0 + 32) needs no masking when it lies inside every row's range */
@@ -1210,12 +1433,28 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
          * epilogue's wait, and every wait inside the loop sees the same
          * number of loads in flight. */
         int k0 = it.key_begin + wave * SMOL_SLAB;
+        KRaw kr;
+        VRaw vr;
+        if (p.dec_direct) {
+            /* staging loads, the first slab's loads, then the staged values
+             * into LDS (waiting for the staging loads only), Q from LDS, and
+             * a barrier before the epilogue may reuse the area */
+            stage_issue();
+            if (k0 < end) {
+                issue_k(k0, kr);
+                issue_v(k0, vr);
+            }
+            stage_store();
+            __syncthreads();
+            load_q_direct();
+            __syncthreads();
+        }
         if (k0 < end) {
-            KRaw kr;
-            VRaw vr;
-            issue_k(k0, kr);
-            issue_v(k0, vr);
-            load_q();
+            if (!p.dec_direct) {
+                issue_k(k0, kr);
+                issue_v(k0, vr);
+                load_q();
+            }
             auto slab = [&](auto issue_tag) __attribute__((always_inline)) {
                 constexpr bool ISSUE = decltype(issue_tag)::value;
                 f4 sacc[NT][2];
@@ -1229,10 +1468,11 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
             };
             for (; k0 + step < end; k0 += step) slab(std::true_type{});
             slab(std::false_type{});
-        } else {
+        } else if (!p.dec_direct) {
             load_q();
         }
     }
+    if (owner) add_new_key();
 
     finish_item<HD, NT, W == 1 ? 64 : 32>(p, it, b, item, g, tid, m, l, o, s_o, s_m, s_l, s_last);
 }

@@ -318,6 +318,61 @@ def test_decode_positions_staged(ctx, sa, oracle, wo, positions, monkeypatch):
     test_decode_positions(ctx, sa, oracle, wo, positions)
 
 
+@pytest.mark.parametrize("positions", [[0], [33], [64, 0, 95, 7], [1000, 31, 4095]])
+def test_decode_positions_prepass(ctx, sa, oracle, wo, positions, monkeypatch):
+    """The same cases with the pre-pass and the fresh fp16 slab (the kernel
+    otherwise reads Q and the new key itself)."""
+    monkeypatch.setenv("SMOL_ATTN_DEC_DIRECT", "-1")
+    test_decode_positions(ctx, sa, oracle, wo, positions)
+
+
+@pytest.mark.parametrize("hq,hkv,hd,rt,bf", [(16, 8, 128, 0, False), (8, 1, 256, 1, False), (6, 2, 72, 0, True),
+                                             (4, 4, 80, 1, False), (8, 2, 96, 0, True), (4, 4, 64, 0, True),
+                                             (32, 2, 128, 0, False)])
+def test_decode_direct_cache_rows(ctx, sa, oracle, wo, hq, hkv, hd, rt, bf, monkeypatch):
+    """Decode without the pre-pass appends the same bf16 cache rows as the
+    pre-pass (the rotation formulas are the same) and both outputs meet the
+    oracle; G = 16 puts two row tiles in a work item."""
+    from smol_genius_amd import runner
+    from smol_genius_amd.workloads import Decode
+    positions = [0, 40, 200, 31]
+    print("decode direct rows", hq, hkv, hd, rt, bf, flush=True)
+    wl = Decode("t", hq, hkv, hd, [p + 1 for p in positions], 1e4, rt, seed=140 + hd)
+    x = wl.inputs()
+    if bf:
+        for k in ("q", "k", "v"):
+            x[k] = synth.f32_to_bf16_bits(x[k])
+    want = wo.decode(oracle, wl, {k: (widen(a) if bf and k in ("q", "k", "v") else a) for k, a in x.items()})
+    got, rows = [], []
+    for mode in ("0", "-1"):
+        monkeypatch.setenv("SMOL_ATTN_DEC_DIRECT", mode)
+        r = runner.prepare(ctx, wl, x)
+        out = sa.decode(ctx, r.kv, 0, r.rope, np.arange(wl.n_seq), wl.positions, dev(x["q"], bf), dev(x["k"], bf),
+                        dev(x["v"], bf), wl.Hq, wl.scale).cpu().numpy()
+        assert_parity(out, want, "decode direct=%s hd %d" % (mode, hd))
+        got.append(out)
+        rows.append([r.kv.read(0, i, p, 1) for i, p in enumerate(positions)])
+    for a, b in zip(rows[0], rows[1]):
+        np.testing.assert_array_equal(a[0], b[0])
+        np.testing.assert_array_equal(a[1], b[1])
+
+
+@pytest.mark.parametrize("window,cap", [(16, 0.0), (0, 2.0), (1, 0.0), (40, 1.5), (1, 3.0)])
+def test_decode_window_softcap(ctx, sa, oracle, wo, window, cap):
+    """Sliding window and softcap on decode (the new key is scored apart
+    from the cache slabs; window 1 leaves it alone)."""
+    from smol_genius_amd import runner
+    from smol_genius_amd.workloads import Decode
+    positions = [0, 40, 200, 1000]
+    print("decode window", window, "cap", cap, flush=True)
+    wl = Decode("t", 16, 8, 128, [p + 1 for p in positions], 1e6, 0, seed=150 + window)
+    x = wl.inputs()
+    r = runner.prepare(ctx, wl, x)
+    got = sa.decode(ctx, r.kv, 0, r.rope, np.arange(wl.n_seq), wl.positions, r.q[0], r.k[0], r.v[0], wl.Hq,
+                    wl.scale, window=window, cap=cap).cpu().numpy()
+    assert_parity(got, wo.decode(oracle, wl, x, window=window, cap=cap), "decode window %d cap %g" % (window, cap))
+
+
 @pytest.mark.parametrize("name", ["qwen06b_decode", "gemma_mqa_decode", "qwen17b_stream"])
 def test_workload_full_size_staged_decode(ctx, oracle, wo, name, monkeypatch):
     monkeypatch.setenv("SMOL_ATTN_DEC_STAGED", "1")
