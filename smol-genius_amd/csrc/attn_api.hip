@@ -28,7 +28,8 @@
 #include "attn_internal.h"
 
 extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t st);
-extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, int w, int staged, hipStream_t st);
+extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, int w, int nw, int staged,
+                               hipStream_t st);
 extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
 extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st);
 extern "C" int smol_launch_to_bf16_trunc(const float *x, uint16_t *y, long long n, hipStream_t st);
@@ -698,7 +699,30 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
      * k_attn_dec's staged build (every slab of an item DMA'd into LDS at once),
      * which measured no faster on the decode workloads */
     bool staged = cs.dec && !cs.direct && env_int("SMOL_ATTN_DEC_STAGED") == 1;
-    {
+    /* k_attn_dec with eight waves and one item per (row tile, kv head) when
+     * no sequence has more than SMOL_ATTN_DEC_WHOLE slabs (default 48, six
+     * per wave) and the items cover at least half the compute units: no
+     * split-K merge, whose chain of device-coherent round trips costs more
+     * than the longer slab loop. With fewer items a compute unit's own load
+     * rate would bound each whole sequence (a C1-sized step: 15.2 against
+     * 20.2 µs), so those keep the split. */
+    int nw = 4;
+    if (cs.dec && !staged && nt == 1 && w == 2 && hd <= 128) {
+        const int whole = env_int("SMOL_ATTN_DEC_WHOLE") ? env_int("SMOL_ATTN_DEC_WHOLE") : 48;
+        int most = 0;
+        long long tiles = 0;
+        for (auto &b : pl.sb) {
+            most = std::max(most, (b.key_hi - std::max(b.key_lo, 0) + SMOL_SLAB - 1) / SMOL_SLAB + 1);
+            tiles += (b.n_rows + rows_per - 1) / rows_per;
+        }
+        if (most <= whole && tiles * cs.Hkv * 2 >= ctx->cu_count) nw = 8;
+        /* SMOL_ATTN_DEC_NW=8 / 4 overrides the item count rule */
+        const int ov = env_int("SMOL_ATTN_DEC_NW");
+        if (ov == 4 || (ov == 8 && most <= whole)) nw = ov;
+    }
+    if (nw == 8) {
+        plan_items(pl, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, false, true, 0);
+    } else {
         Plan trial = pl;
         plan_items(trial, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, fa, fb, staged ? (hd > 128 ? 5 : 4) : 0);
         if (!trial.staged_ok) {
@@ -840,7 +864,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
         sp.qscale = pp.qscale;
     }
     mk = timing_begin(ctx, 1);
-    rc = cs.dec ? smol_launch_dec(&sp, hd, (int)n_items, nt, w, staged ? 1 : 0, ctx->stream)
+    rc = cs.dec ? smol_launch_dec(&sp, hd, (int)n_items, nt, w, nw, staged ? 1 : 0, ctx->stream)
          : fb   ? smol_launch_fb(&sp, hd, (int)n_items, nt, ctx->stream)
                 : smol_launch_fa(&sp, hd, (int)n_items, nt, w, ctx->stream);
     timing_end(ctx, mk);

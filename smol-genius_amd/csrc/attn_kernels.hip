@@ -741,11 +741,11 @@ __device__ __forceinline__ void merge_group(const SkParams &p, const SkItem &it,
         __hip_atomic_store(p.counters + ((long long)it.group * p.Hkv + g) * SK_COUNTER_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-/* Epilogue shared by the attention kernels: combines the SK_WAVES waves'
- * (max, sum, O) through LDS into wave 0, then either writes the normalised
- * rows (single split) or publishes the partial and lets the group's last
- * workgroup merge. Every row's state lives in lanes c, c+16, c+32, c+48. */
-template <int HD, int NT, int MAXL = 16>
+/* Epilogue of k_attn_dec: combines the NW waves' (max, sum, O) through LDS
+ * into wave 0, then either writes the normalised rows (single split) or
+ * publishes the partial and lets the group's last workgroup merge. Every
+ * row's state lives in lanes c, c+16, c+32, c+48. */
+template <int HD, int NT, int MAXL = 16, int NW = SK_WAVES>
 __device__ __forceinline__ void finish_item(const SkParams &p, const SkItem &it, const SkBatch &b, int item, int g,
                                             int tid,
                                             float (&m)[NT], float (&l)[NT], f4 (&o)[NT][(HD + 15) / 16], float *s_o,
@@ -778,14 +778,14 @@ __device__ __forceinline__ void finish_item(const SkParams &p, const SkItem &it,
             const int rr = nt * 16 + c;
             float M = m[nt];
 #pragma unroll
-            for (int w = 0; w < SK_WAVES - 1; w++) M = fmaxf(M, s_m[w * ROWS + rr]);
+            for (int w = 0; w < NW - 1; w++) M = fmaxf(M, s_m[w * ROWS + rr]);
             const float Mu = M == -INFINITY ? 0.0f : M;
             const float a0 = __builtin_amdgcn_exp2f(m[nt] - Mu);
             float L = l[nt] * a0;
 #pragma unroll
             for (int dt = 0; dt < DT; dt++) o[nt][dt] *= a0;
 #pragma unroll
-            for (int w = 0; w < SK_WAVES - 1; w++) {
+            for (int w = 0; w < NW - 1; w++) {
                 const float aw = __builtin_amdgcn_exp2f(s_m[w * ROWS + rr] - Mu);
                 L += s_l[w * ROWS + rr] * aw;
                 const float *so = s_o + (w * ROWS + rr) * OSTR;
@@ -845,7 +845,7 @@ __device__ __forceinline__ void finish_item(const SkParams &p, const SkItem &it,
     }
     __syncthreads();
     if (!*s_last) return;
-    merge_group<HD, ROWS, MAXL>(p, it, b, item, g, tid, s_o);
+    merge_group<HD, ROWS, MAXL, 64 * NW>(p, it, b, item, g, tid, s_o);
 }
 
 /* --------------------------------------------------------------- k_attn_dec */
@@ -882,8 +882,9 @@ __device__ __forceinline__ void split8(const float *x, b8 &hi, b8 &lo) {
     }
 }
 
-template <int HD, int NT, int W, bool ST>
-__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W, W))) void k_attn_dec(SkParams p) {
+template <int HD, int NT, int W, bool ST, int NW = SK_WAVES>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W, W))) void k_attn_dec(SkParams p) {
+    static_assert(!ST || NW == 4, "the staged build's transfers are laid out for four waves");
     constexpr int KS = (HD + 31) / 32;
     constexpr int DT = (HD + 15) / 16;
     constexpr int HDP = KS * 32;
@@ -914,17 +915,17 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
     /* s_o: the other waves' (o) rows in the combine, the merge's arrays, and
      * (direct decode) the staged Q rows; past the combine's rows, the new
      * value, which wave 0 reads while the other waves fill theirs */
-    constexpr int SVN = (SK_WAVES - 1) * ROWS * OSTR;
+    constexpr int SVN = (NW - 1) * ROWS * OSTR;
     constexpr int SO = SVN + HD > 2 * SK_MERGE_MAX + 128 ? SVN + HD : 2 * SK_MERGE_MAX + 128;
     /* the epilogue's arrays; with ST they reuse the slab area once every
      * wave is done with it */
-    constexpr int FIN_BYTES = (SO + 2 * (SK_WAVES - 1) * ROWS + 1) * 4;
+    constexpr int FIN_BYTES = (SO + 2 * (NW - 1) * ROWS + 1) * 4;
     constexpr int SMEM = SMAX * SLAB_LDS > FIN_BYTES ? SMAX * SLAB_LDS : FIN_BYTES;
     static_assert(SMEM <= 160 * 1024, "LDS");
     __shared__ __attribute__((aligned(1024))) unsigned char smem[SMEM];
     float *s_o = reinterpret_cast<float *>(smem);
-    float *s_m = s_o + SO, *s_l = s_m + (SK_WAVES - 1) * ROWS;
-    int *s_last = reinterpret_cast<int *>(s_l + (SK_WAVES - 1) * ROWS);
+    float *s_m = s_o + SO, *s_l = s_m + (NW - 1) * ROWS;
+    int *s_last = reinterpret_cast<int *>(s_l + (NW - 1) * ROWS);
 
     b8 qh[NT][KS], ql[NT][KS];
     int lo[NT], hi[NT];
@@ -989,7 +990,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
     float *s_cos = s_k + HD, *s_sin = s_cos + HD, *s_wq = s_sin + HD, *s_wk = s_wq + HD;
     static_assert(ROWS * QSTR + 5 * HD <= SVN, "direct decode staging");
     constexpr int C4Q = HD / 4;            /* 4-element chunks per row */
-    constexpr int NSTAGE = (ROWS * C4Q + 6 * C4Q + 64 * SK_WAVES - 1) / (64 * SK_WAVES);
+    constexpr int NSTAGE = (ROWS * C4Q + 6 * C4Q + 64 * NW - 1) / (64 * NW);
     const int n_qrows = min(ROWS, b.n_rows - it.row0);
     const bool bf_in = p.q_dtype == SMOL_IN_BF16;
     /* chunk e of the staged list: Q rows, cos, sin, q weights, then (last
@@ -1028,7 +1029,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
         for (int u = 0; u < NSTAGE; u++) {
             const void *src; long long idx; bool f32; float *dst;
             st_raw[u] = make_uint4(0, 0, 0, 0);
-            if (stage_src(tid + 64 * SK_WAVES * u, src, idx, f32, dst)) {
+            if (stage_src(tid + 64 * NW * u, src, idx, f32, dst)) {
                 if (f32) st_raw[u] = *reinterpret_cast<const uint4 *>((const float *)src + idx);
                 else {
                     const uint2 h = *reinterpret_cast<const uint2 *>((const uint16_t *)src + idx);
@@ -1041,7 +1042,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
 #pragma unroll
         for (int u = 0; u < NSTAGE; u++) {
             const void *src; long long idx; bool f32; float *dst;
-            if (stage_src(tid + 64 * SK_WAVES * u, src, idx, f32, dst)) {
+            if (stage_src(tid + 64 * NW * u, src, idx, f32, dst)) {
                 float4 v;
                 if (f32) v = make_float4(__uint_as_float(st_raw[u].x), __uint_as_float(st_raw[u].y),
                                          __uint_as_float(st_raw[u].z), __uint_as_float(st_raw[u].w));
@@ -1362,7 +1363,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
         }
     };
 
-    const int step = SMOL_SLAB * SK_WAVES;
+    const int step = SMOL_SLAB * NW;
     const int end = it.key_end;
     if constexpr (ST) {
         /* all n <= SMAX slabs of the item into LDS (slab s at s * SLAB_LDS,
@@ -1406,7 +1407,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) kfo[ks] = (unsigned)(kt_row * KROW + 16 * ((4 * ks + j) ^ c));
         const unsigned vfo = (unsigned)(K_LDS + c * 64 + 16 * (j ^ ((c >> 1) & 3)));
-        for (int sl = wave; sl < n; sl += SK_WAVES) {
+        for (int sl = wave; sl < n; sl += NW) {
             const unsigned char *base = smem + sl * SLAB_LDS;
             const int kk = it.key_begin + SMOL_SLAB * sl;
             KRaw kr;
@@ -1426,7 +1427,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
         }
         __syncthreads(); /* the slab area becomes the epilogue's */
     } else {
-        /* Each wave streams slabs wave, wave + SK_WAVES, ... with one K/V
+        /* Each wave streams slabs wave, wave + NW, ... with one K/V
          * register buffer, the next slab requested while the current one is
          * computed and the first one before Q is loaded. The last slab is
          * peeled off the loop, so no load is left in flight for the
@@ -1474,7 +1475,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(W
     }
     if (owner) add_new_key();
 
-    finish_item<HD, NT, W == 1 ? 64 : 32>(p, it, b, item, g, tid, m, l, o, s_o, s_m, s_l, s_last);
+    finish_item<HD, NT, W == 1 ? 64 : 32, NW>(p, it, b, item, g, tid, m, l, o, s_o, s_m, s_l, s_last);
 }
 
 /* ---------------------------------------------------------------- k_attn_fa */
@@ -2174,6 +2175,10 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     qk(kfa, sa);
     read_k(1, kfa);
     read_v(0, vfa);
+    /* step 0 refills stage 0 with no barrier in between: V^T of slab 0 must
+     * be in registers first. A transfer of a slab already in L2 can land
+     * before LDS reads queued behind the other waves' reads are served. */
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     int st_k = 2 % NSTG, st_v = 1, st_d = 0; /* stages read in a step, stage refilled */
     auto step = [&](int i, f4 (&scur)[NT][2], f4 (&snext)[NT][2], auto &kcur, auto &knext, auto &vcur, auto &vnext)
         __attribute__((always_inline)) {
@@ -2382,10 +2387,19 @@ static void launch_dec_v(const SkParams *sp, dim3 grid, bool staged, hipStream_t
 }
 
 template <int HD>
-static int launch_dec_hd(const SkParams *sp, int n_items, int nt, int w, bool staged, hipStream_t st) {
+static int launch_dec_hd(const SkParams *sp, int n_items, int nt, int w, int nw, bool staged, hipStream_t st) {
     /* two waves per SIMD only where the registers allow it (one row tile,
-     * head_dim <= 128); other requests run at one */
+     * head_dim <= 128); other requests run at one. nw = 8: eight waves per
+     * workgroup (two per SIMD), for items that hold a whole sequence */
     const dim3 grid(n_items * sp->Hkv);
+    if (nw == 8) {
+        if constexpr (HD <= 128) {
+            if (nt != 1 || w != 2 || staged) return -1;
+            hipLaunchKernelGGL((k_attn_dec<HD, 1, 2, false, 8>), grid, dim3(64 * 8), 0, st, *sp);
+            return hipGetLastError() == hipSuccess ? 0 : -3;
+        }
+        return -1;
+    }
     if (nt == 1 && w == 2 && HD <= 128) launch_dec_v<HD, 1, (HD <= 128 ? 2 : 1)>(sp, grid, staged, st);
     else if (nt == 1) launch_dec_v<HD, 1, 1>(sp, grid, staged, st);
     else if (nt == 2 && HD <= 128) launch_dec_v<HD, (HD <= 128 ? 2 : 1), 1>(sp, grid, staged, st);
@@ -2395,15 +2409,16 @@ static int launch_dec_hd(const SkParams *sp, int n_items, int nt, int w, bool st
 
 /* staged: every slab of an item goes to LDS in one round of direct
  * transfers (items of at most smol_dec_staged_slabs(hd) slabs) */
-extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, int w, int staged, hipStream_t st) {
+extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, int w, int nw, int staged,
+                               hipStream_t st) {
     if (n_items <= 0) return 0;
     switch (hd) {
-    case 64: return launch_dec_hd<64>(sp, n_items, nt, w, staged != 0, st);
-    case 72: return launch_dec_hd<72>(sp, n_items, nt, w, staged != 0, st);
-    case 80: return launch_dec_hd<80>(sp, n_items, nt, w, staged != 0, st);
-    case 96: return launch_dec_hd<96>(sp, n_items, nt, w, staged != 0, st);
-    case 128: return launch_dec_hd<128>(sp, n_items, nt, w, staged != 0, st);
-    case 256: return launch_dec_hd<256>(sp, n_items, nt, w, staged != 0, st);
+    case 64: return launch_dec_hd<64>(sp, n_items, nt, w, nw, staged != 0, st);
+    case 72: return launch_dec_hd<72>(sp, n_items, nt, w, nw, staged != 0, st);
+    case 80: return launch_dec_hd<80>(sp, n_items, nt, w, nw, staged != 0, st);
+    case 96: return launch_dec_hd<96>(sp, n_items, nt, w, nw, staged != 0, st);
+    case 128: return launch_dec_hd<128>(sp, n_items, nt, w, nw, staged != 0, st);
+    case 256: return launch_dec_hd<256>(sp, n_items, nt, w, nw, staged != 0, st);
     default: return -1;
     }
 }

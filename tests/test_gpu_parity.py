@@ -50,7 +50,7 @@ def widen(b):
 
 @pytest.mark.parametrize("name", ["qwen06b_decode", "qwen06b_prefill", "siglip_bidir", "gemma_mqa_decode",
                                   "qwen17b_stream", "qwen06b_decode_qknorm", "qwen06b_prefill_qknorm",
-                                  "asr_encoder_bidir"])
+                                  "asr_encoder_bidir", "qwen06b_decode_x28"])
 def test_workload_full_size(ctx, oracle, wo, name):
     from smol_genius_amd import runner, workloads
     print("case", name, flush=True)
@@ -324,6 +324,37 @@ def test_decode_positions_prepass(ctx, sa, oracle, wo, positions, monkeypatch):
     otherwise reads Q and the new key itself)."""
     monkeypatch.setenv("SMOL_ATTN_DEC_DIRECT", "-1")
     test_decode_positions(ctx, sa, oracle, wo, positions)
+
+
+@pytest.mark.parametrize("positions", [[0], [33], [64, 0, 95, 7], [1000, 31, 1400]])
+def test_decode_positions_whole(ctx, sa, oracle, wo, positions, monkeypatch):
+    """The same cases with eight waves per workgroup and one item per
+    sequence and kv head (no split-K merge), forced whatever the item count
+    (head_dim 256 keeps four waves)."""
+    monkeypatch.setenv("SMOL_ATTN_DEC_NW", "8")
+    test_decode_positions(ctx, sa, oracle, wo, positions)
+
+
+@pytest.mark.parametrize("window,cap,qk", [(0, 0.0, False), (16, 2.0, False), (0, 0.0, True)])
+def test_decode_whole_window_norm(ctx, sa, oracle, wo, window, cap, qk, monkeypatch):
+    """Eight-wave whole-sequence decode with a window and softcap, and with
+    per-head Q/K norms (72-wide heads: a row tile's chunks past head_dim)."""
+    from smol_genius_amd import runner
+    from smol_genius_amd.workloads import Decode
+    monkeypatch.setenv("SMOL_ATTN_DEC_NW", "8")
+    for hq, hkv, hd in [(16, 8, 128), (6, 2, 72)]:
+        positions = [0, 40, 200, 1000]
+        print("decode whole", hd, window, cap, qk, flush=True)
+        wl = Decode("t", hq, hkv, hd, [p + 1 for p in positions], 1e4, 0, seed=160 + hd)
+        x = wl.inputs()
+        qw = (1.0 + 0.1 * synth.normal(161, (hd,))).astype(np.float32) if qk else None
+        kw = (1.0 + 0.1 * synth.normal(162, (hd,))).astype(np.float32) if qk else None
+        r = runner.prepare(ctx, wl, x)
+        got = sa.decode(ctx, r.kv, 0, r.rope, np.arange(wl.n_seq), wl.positions, r.q[0], r.k[0], r.v[0], wl.Hq,
+                        wl.scale, window=window, cap=cap, q_norm=None if qw is None else dev(qw),
+                        k_norm=None if kw is None else dev(kw), eps=1e-6).cpu().numpy()
+        want = wo.decode(oracle, wl, x, q_norm=qw, k_norm=kw, eps=1e-6, window=window, cap=cap)
+        assert_parity(got, want, "decode whole hd %d window %d cap %g qk %s" % (hd, window, cap, qk))
 
 
 @pytest.mark.parametrize("hq,hkv,hd,rt,bf", [(16, 8, 128, 0, False), (8, 1, 256, 1, False), (6, 2, 72, 0, True),
