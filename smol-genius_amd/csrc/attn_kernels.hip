@@ -2167,7 +2167,10 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
      * have one fewer, or none) keep the reads, transfers and barriers and
      * mask every key. */
     const int steps = n0;
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
+    /* every prologue transfer (and Q) has landed: the first touch of an
+     * item's pages can return its transfers out of order, so the count
+     * alone does not show which slabs are in */
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     f4 sa[NT][2], sb[NT][2];
     h8 kfa[2][KS], kfb[2][KS], vfa[DT], vfb[DT];
