@@ -359,11 +359,11 @@ def test_decode_whole_window_norm(ctx, sa, oracle, wo, window, cap, qk, monkeypa
 
 @pytest.mark.parametrize("hq,hkv,hd,rt,bf", [(16, 8, 128, 0, False), (8, 1, 256, 1, False), (6, 2, 72, 0, True),
                                              (4, 4, 80, 1, False), (8, 2, 96, 0, True), (4, 4, 64, 0, True),
-                                             (32, 2, 128, 0, False)])
+                                             (32, 2, 128, 0, False), (64, 2, 64, 0, False)])
 def test_decode_direct_cache_rows(ctx, sa, oracle, wo, hq, hkv, hd, rt, bf, monkeypatch):
     """Decode without the pre-pass appends the same bf16 cache rows as the
     pre-pass (the rotation formulas are the same) and both outputs meet the
-    oracle; G = 16 puts two row tiles in a work item."""
+    oracle; G = 32 puts two row tiles in a work item."""
     from smol_genius_amd import runner
     from smol_genius_amd.workloads import Decode
     positions = [0, 40, 200, 31]
@@ -513,6 +513,28 @@ def test_long_causal_prefill(ctx, sa, oracle, wo):
     rope = sa.RopeTable(ctx, 128, wl.theta, 0)
     got = sa.prefill(ctx, kv, 0, 0, rope, 0, dev(x["q"], True), dev(x["k"], True), dev(x["v"], True), 8, wl.scale)
     assert_parity(got.cpu().numpy(), wo.prefill(oracle, wl, x), "prefill 4096")
+
+
+def test_fresh_context_long_prefill(sa, oracle, wo):
+    """The first call on a new context (staging buffers never touched before)
+    with 8192 keys per kv head, so a tile's key slabs span more than the
+    first transfers touch; LDS left by earlier kernels would show as wrong
+    rows if a transfer were read before it landed."""
+    from smol_genius_amd.workloads import Prefill
+    print("fresh context prefill 8192", flush=True)
+    c = sa.Context(0)
+    try:
+        wl = Prefill("t", 4, 2, 128, 0, 8192, 1e6, seed=125, in_bf16=True)
+        x = wl.inputs()
+        kv = sa.KVCache(c, 1, 1, 2, 128, 8192)
+        rope = sa.RopeTable(c, 128, wl.theta, 0, 8192)
+        got = sa.prefill(c, kv, 0, 0, rope, 0, dev(x["q"], True), dev(x["k"], True), dev(x["v"], True), 4,
+                         wl.scale)
+        assert_parity(got.cpu().numpy(), wo.prefill(oracle, wl, x), "fresh context prefill 8192")
+        kv.close()
+        rope.close()
+    finally:
+        c.close()
 
 
 def test_long_prefix_chunk(ctx, sa, oracle, wo):
