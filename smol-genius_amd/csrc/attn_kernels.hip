@@ -2045,10 +2045,20 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     float m[NT], l[NT], thr[NT];
     f4 negm[NT];
     f4 o[NT][DT];
+    /* head_dim <= 96 leaves registers for the row sums on the matrix cores:
+     * one more MFMA per step against a fragment of ones (every element of
+     * lsum is the row's sum of its fp16 probabilities, the same weights the
+     * P.V product uses) instead of seven vector adds */
+    constexpr bool MSUM = HD <= 96 && NT == 1;
+    f4 lsum[NT];
+    h8 ones;
+#pragma unroll
+    for (int i = 0; i < 8; i++) ones[i] = (_Float16)1.0f;
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         m[nt] = -INFINITY;
         l[nt] = 0.0f;
+        lsum[nt] = f4{0.f, 0.f, 0.f, 0.f};
         thr[nt] = -INFINITY;
         negm[nt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -2125,7 +2135,8 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
                 const float alpha = need ? __builtin_amdgcn_exp2f(m[nt] - m_new) : 1.0f;
 #pragma unroll
                 for (int dt = 0; dt < DT; dt++) o[nt][dt] *= alpha;
-                l[nt] *= alpha;
+                if constexpr (MSUM) lsum[nt] *= alpha;
+                else l[nt] *= alpha;
                 m[nt] = m_new;
                 const float mu = m_new == -INFINITY ? 0.0f : m_new;
                 negm[nt] = f4{-mu, -mu, -mu, -mu};
@@ -2145,7 +2156,7 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
                 pe[e] = __builtin_amdgcn_exp2f(s[nt][e >> 2][e & 3]);
                 pf[nt][e] = (_Float16)pe[e];
             }
-            l[nt] += ((pe[0] + pe[1]) + (pe[2] + pe[3])) + ((pe[4] + pe[5]) + (pe[6] + pe[7]));
+            if constexpr (!MSUM) l[nt] += ((pe[0] + pe[1]) + (pe[2] + pe[3])) + ((pe[4] + pe[5]) + (pe[6] + pe[7]));
         }
     };
     auto pv = [&](const h8 (&vf)[DT], const h8 (&pf)[NT]) __attribute__((always_inline)) {
@@ -2154,6 +2165,10 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
 #pragma unroll
             for (int nt = 0; nt < NT; nt++)
                 o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pf[nt], o[nt][dt], 0, 0, 0);
+        if constexpr (MSUM) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) lsum[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[nt], lsum[nt], 0, 0, 0);
+        }
     };
 
     /* Slab j of this group sits in stage j % NSTG. Its transfer is issued in
@@ -2211,7 +2226,7 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     }
     if (i < steps) step(i, sa, sb, kfa, kfb, vfa, vfb);
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++) l[nt] = row_sum4(l[nt]);
+    for (int nt = 0; nt < NT; nt++) l[nt] = MSUM ? lsum[nt][0] : row_sum4(l[nt]);
 
     /* merge: group 1 hands its state to group 0 through LDS (lane-wise: the
      * two waves wg of the groups hold the same rows in the same lanes), one
