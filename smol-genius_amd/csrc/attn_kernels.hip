@@ -2045,11 +2045,11 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     float m[NT], l[NT], thr[NT];
     f4 negm[NT];
     f4 o[NT][DT];
-    /* head_dim <= 96 leaves registers for the row sums on the matrix cores:
-     * one more MFMA per step against a fragment of ones (every element of
-     * lsum is the row's sum of its fp16 probabilities, the same weights the
-     * P.V product uses) instead of seven vector adds */
-    constexpr bool MSUM = HD <= 96 && NT == 1;
+    /* the row sums on the matrix cores (one row tile per wave): one more
+     * MFMA per step against a fragment of ones (every element of lsum is the
+     * row's sum of its fp16 probabilities, the same weights the P.V product
+     * uses) instead of seven vector adds */
+    constexpr bool MSUM = HD <= 128 && NT == 1;
     f4 lsum[NT];
     h8 ones;
 #pragma unroll
