@@ -554,8 +554,12 @@ static void plan_items(Plan &pl, int Hkv, int G, int window, int rows_per, int c
     /* a workgroup per compute unit and wave slot, each wave >= 2 slabs */
     const long long target_items = (long long)cu_count;
     long long per = (total_slabs * Hkv + target_items - 1) / std::max(1LL, target_items);
-    /* k_attn_dec splits an item's slabs over its 4 waves, k_attn_fa gives each slab to all of them */
-    int slabs_per_item = (int)std::max(max_slabs ? 2LL : (longest_first ? 4LL : 8LL), per);
+    /* k_attn_dec splits an item's slabs over its 4 waves (at least 8 per item, or 4 when the whole
+     * call has fewer than two slabs per planned workgroup: a 1025-key decode step measured 14.2
+     * against 14.7 µs, while 4 on a call with more work lengthened it), k_attn_fa gives each slab
+     * to all of them */
+    const long long dec_min = total_slabs * Hkv < 2 * target_items ? 4 : 8;
+    int slabs_per_item = (int)std::max(max_slabs ? 2LL : (longest_first ? 4LL : dec_min), per);
     if (max_slabs) slabs_per_item = std::min(slabs_per_item, max_slabs);
     /* tuning override: SMOL_ATTN_SLABS_PER_ITEM=n fixes the key slabs per work item */
     if (const int n = env_int("SMOL_ATTN_SLABS_PER_ITEM")) {
