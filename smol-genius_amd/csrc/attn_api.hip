@@ -571,7 +571,10 @@ static void plan_items(Plan &pl, int Hkv, int G, int window, int rows_per, int c
     const int max_split = SK_MERGE_MAX / rows_per; /* the kernel's merge holds rows * n_split pairs in LDS */
     for (const Tile &t : tiles) {
         const int n_slabs = (t.hi - t.lo + SMOL_SLAB - 1) / SMOL_SLAB;
-        const int want = std::max(1, (n_slabs + slabs_per_item - 1) / slabs_per_item);
+        int want = std::max(1, (n_slabs + slabs_per_item - 1) / slabs_per_item);
+        /* k_attn_dec: at most 24 splits per group, whose merge reads every split's partial (a decode
+         * step over 8218 keys and 8 kv heads: 64 steps in 1.64 ms with 33 splits, 1.50 ms with 22) */
+        if (!longest_first && !max_slabs) want = std::min(want, 24);
         if (max_slabs && want > max_split) pl.staged_ok = false; /* items would outgrow the staged LDS */
         const int n_split = std::min(max_split, want);
         const int per_split = (n_slabs + n_split - 1) / std::max(1, n_split);
