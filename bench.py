@@ -168,6 +168,13 @@ def main():
     else:
         head = None
 
+    # CPU baselines: the reference's own CPU attention (oracle/_ref) on this host, after each
+    # workload's GPU timing, on a bounded sample of the same inputs
+    cpu_mod = None
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import cpu_baseline as cpu_mod
+
     # ---------------- the other workloads
     for name in ["qwen06b_decode", "gemma_mqa_decode", "siglip_bidir", "qwen17b_stream", "qwen06b_decode_qknorm",
                  "qwen06b_prefill_qknorm", "asr_encoder_bidir", "qwen06b_decode_x28"]:
@@ -185,6 +192,8 @@ def main():
                             "attn_kernel_ms_total_per_step": round(attn_ms / n, 4),
                             "decode_GBps_path": round(wl.decode_bytes() / (wall / n) / 1e9, 1),
                             "note": "wall time per step includes 65 launches and their host dispatch"}
+            if cpu_mod:
+                detail[name]["cpu_baseline"] = cpu_mod.stream_sample(wl, wl.inputs())
             continue
         x, run, n_layers, wall, kt = measure(ctx, wl, steps, warmup, runner)
         del x, run
@@ -207,15 +216,18 @@ def main():
                      hbm_frac_kernel=round(b / (attn_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 5),
                      GBps_path=round(b / ((attn_ms + prep_ms) * 1e-3) / 1e9, 1),
                      bytes_per_launch=b)
+        if cpu_mod:
+            if isinstance(wl, workloads.Decode):
+                d["cpu_baseline"] = cpu_mod.decode_sample(wl, wl.inputs())
+            elif isinstance(wl, workloads.Bidir):
+                d["cpu_baseline"] = cpu_mod.bidir_sample(wl, wl.inputs())
+            elif isinstance(wl, workloads.Prefill):
+                d["cpu_baseline"] = cpu_mod.prefill_sample(wl, wl.inputs(), min_seconds=3.0)
         detail[name] = d
 
-    # ---------------- CPU baseline (reference CPU attention on this host)
-    cpu = None
-    if not args.no_cpu and head is not None:
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        import cpu_baseline
-        cpu = cpu_baseline.prefill_sample(main_wl, main_wl.inputs())
-        head["cpu_baseline"] = cpu
+    # ---------------- CPU baseline of the headline (reference CPU attention on this host)
+    if cpu_mod and head is not None:
+        head["cpu_baseline"] = cpu_mod.prefill_sample(main_wl, main_wl.inputs())
     if head is None:
         head = {"metric": "detail only", "value": None}
     head["detail"] = detail

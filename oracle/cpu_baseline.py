@@ -26,6 +26,21 @@ def _f32(a):
     return _widen(a) if a.dtype == np.uint16 else np.ascontiguousarray(a, np.float32)
 
 
+def host_facts():
+    """nproc, the CPU model and the SIMD branch the reference's vector code takes here
+    (vecops_avx.c:14: AVX-512 when the compiler targets it, else AVX2)."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu_model": model, "simd": simd_branch()}
+
+
 def _lib():
     cores = min(os.cpu_count() or 1, 16)
     if ref_path():
@@ -58,7 +73,7 @@ def prefill_sample(wl, x, min_seconds=10.0, max_reps=50):
         reps += 1
     sec = t / reps
     return {"value": round(wl.flops() / sec / 1e12, 6), "unit": "TFLOP/s", "cores": cores, "kind": kind,
-            "simd": simd_branch(), "ms_per_step": round(sec * 1e3, 3),
+            "ms_per_step": round(sec * 1e3, 3), **host_facts(),
             "sample": "%d full repetitions of the %s step (RoPE on Q and K + causal attention, %d x %d, "
                       "%d heads)" % (reps, wl.name, S, P + S, wl.Hq)}
 
@@ -84,7 +99,7 @@ def decode_sample(wl, x, min_seconds=3.0, max_reps=200):
         reps += 1
     sec = t / reps
     return {"value": round(wl.algorithmic_bytes() / sec / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind,
-            "ms_per_step": round(sec * 1e3, 3),
+            "ms_per_step": round(sec * 1e3, 3), **host_facts(),
             "sample": "%d repetitions of one decode step of %d sequences" % (reps, wl.n_seq)}
 
 
@@ -99,6 +114,41 @@ def bidir_sample(wl, x, min_seconds=3.0, max_reps=50):
         reps += 1
     sec = t / reps
     return {"value": round(wl.flops() / sec / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": kind,
-            "ms_per_step": round(sec * 1e3, 3),
+            "ms_per_step": round(sec * 1e3, 3), **host_facts(),
             "sample": "%d repetitions; smol_bidirectional_attention is single-threaded "
                       "(attention.c:32-77)" % reps}
+
+
+def stream_sample(wl, x, min_seconds=5.0, max_reps=20):
+    """The streaming step: RoPE + the chunk's causal attention over the cache, then
+    `steps` single-token decode calls against the growing cache (qkn_decoder.c:493-528,
+    :647-677)."""
+    lib, kind, cores = _lib()
+    orc = Oracle()
+    P, C, n = wl.prefix, wl.chunk, wl.steps
+    total = P + C + n
+    c, s = orc.fill_rope_table(0, total, wl.hd, wl.theta, False)
+    w = wl.Hkv * wl.hd
+    K = np.zeros((total, w), np.float32)
+    V = np.zeros((total, w), np.float32)
+    K[:P] = _widen(x["cache_k"]).reshape(P, w)
+    V[:P] = _widen(x["cache_v"]).reshape(P, w)
+    reps, t = 0, 0.0
+    while reps < 1 or (t < min_seconds and reps < max_reps):
+        t0 = time.perf_counter()
+        q = lib.apply_rope(x["q"], c[P:P + C], s[P:P + C], C, wl.Hq, wl.hd, False)
+        K[P:P + C] = lib.apply_rope(x["k"], c[P:P + C], s[P:P + C], C, wl.Hkv, wl.hd, False)
+        V[P:P + C] = x["v"]
+        lib.causal_attention(q, K, V, C, P + C, wl.Hq, wl.Hkv, wl.hd, wl.scale, P)
+        for st in range(n):
+            p = P + C + st
+            q = lib.apply_rope(x["dq"][st:st + 1], c[p:p + 1], s[p:p + 1], 1, wl.Hq, wl.hd, False)
+            K[p] = lib.apply_rope(x["dk"][st:st + 1], c[p:p + 1], s[p:p + 1], 1, wl.Hkv, wl.hd, False)[0]
+            V[p] = x["dv"][st]
+            lib.causal_attention(q, K, V, 1, p + 1, wl.Hq, wl.Hkv, wl.hd, wl.scale, p)
+        t += time.perf_counter() - t0
+        reps += 1
+    sec = t / reps
+    return {"value": round(wl.decode_bytes() / sec / 1e9, 3), "unit": "GB/s (decode bytes over the whole step)",
+            "cores": cores, "kind": kind, "ms_per_step": round(sec * 1e3, 3), **host_facts(),
+            "sample": "%d repetitions of the chunk call + %d decode calls" % (reps, n)}

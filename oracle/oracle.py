@@ -41,6 +41,16 @@ def simd_branch():
     return "avx512" if cpu_has_avx512() else "avx2"
 
 
+def causal_kind(window, cap):
+    """The entry point the reference decoders call for (window, cap)
+    (qkn_decoder.c:505-528: a sliding window when > 0, a softcap when > 0)."""
+    if window > 0 and cap > 0:
+        return "swa_softcap"
+    if window > 0:
+        return "swa"
+    return "softcap" if cap > 0 else "causal"
+
+
 def _fp(a):
     return a.ctypes.data_as(_F)
 
@@ -88,21 +98,28 @@ class _Lib:
 
     # -- attention ---------------------------------------------------------
     def causal_attention(self, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim,
-                         scale, q_offset, window=0, cap=0.0):
+                         scale, q_offset, window=0, cap=0.0, kind=None):
+        """kind picks the entry point: "causal", "swa" (window), "softcap" (cap) or
+        "swa_softcap"; None picks it from the values (window > 0, cap > 0), the
+        dispatch of the reference decoders (qkn_decoder.c:505-528)."""
         Q, K, V = _f32(Q), _f32(K), _f32(V)
         assert Q.size >= seq_q * n_heads * head_dim
         assert K.size >= seq_k * n_kv_heads * head_dim and V.size == K.size
         out = np.zeros((seq_q, n_heads * head_dim), np.float32)
         args = (_fp(out), _fp(Q), _fp(K), _fp(V), seq_q, seq_k, n_heads, n_kv_heads,
                 head_dim, ctypes.c_float(scale), q_offset)
-        if window > 0 and cap > 0:
-            self._swa_softcap(*args, window, ctypes.c_float(cap))
-        elif window > 0:
-            self._swa(*args, window)
-        elif cap > 0:
+        if kind is None:
+            kind = causal_kind(window, cap)
+        if kind == "swa_softcap":
+            self._swa_softcap(*args, int(window), ctypes.c_float(cap))
+        elif kind == "swa":
+            self._swa(*args, int(window))
+        elif kind == "softcap":
             self._softcap(*args, ctypes.c_float(cap))
-        else:
+        elif kind == "causal":
             self._causal(*args)
+        else:
+            raise ValueError(kind)
         return out
 
     def bidirectional_attention(self, Q, K, V, seq, n_heads, head_dim, scale, window_starts):

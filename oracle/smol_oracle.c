@@ -141,18 +141,22 @@ static void orc_parallel_for(orc_fn fn, void *arg) {
 /* ------------------------------------------------------------- attention */
 
 /* One row of online softmax over keys [k_begin, k_end), as in
- * attention.c:98-123. K/V rows are kv_stride floats apart. */
+ * attention.c:98-123. K/V rows are kv_stride floats apart. With use_cap the
+ * score becomes cap * tanhf(score * (1 / cap)) for any cap, as in
+ * attention.c:284-308 (a negative cap is the same as |cap|); cap == 0 is
+ * restated as a zero score, which is what the reference computes for every
+ * nonzero score (0 * tanhf(+-inf)). */
 static void orc_row(float *o, const float *q, const float *K, const float *V,
                     int k_begin, int k_end, int kv_stride, int hd, float scale,
-                    float cap) {
+                    int use_cap, float cap) {
     float m = -1e30f, l = 0.0f;
     for (int d = 0; d < hd; d++) o[d] = 0.0f;
-    float inv_cap = cap > 0.0f ? 1.0f / cap : 0.0f;
+    float inv_cap = cap != 0.0f ? 1.0f / cap : 0.0f;
     for (int j = k_begin; j < k_end; j++) {
         const float *k = K + (size_t)j * kv_stride;
         const float *v = V + (size_t)j * kv_stride;
         float s = orc_dot(q, k, hd) * scale;
-        if (cap > 0.0f) s = cap * tanhf(s * inv_cap);
+        if (use_cap) s = cap != 0.0f ? cap * tanhf(s * inv_cap) : 0.0f;
         if (s > m) {
             float c = expf(m - s);
             l = l * c + 1.0f;
@@ -171,7 +175,8 @@ typedef struct {
     float *out; const float *Q, *K, *V;
     int seq_q, seq_k, n_heads, n_kv_heads, hd;
     float scale, cap;
-    int q_offset, window; /* window <= 0: no sliding window */
+    int q_offset, window;
+    int use_window, use_cap; /* the sliding-window / softcap variants */
 } orc_causal_task;
 
 static void orc_causal_worker(int tid, int nt, void *arg) {
@@ -187,21 +192,24 @@ static void orc_causal_worker(int tid, int nt, void *arg) {
             int gp = t->q_offset + i;
             int k_end = gp + 1;
             if (k_end > t->seq_k) k_end = t->seq_k;
+            /* attention.c:190-192: the window starts at gp - window + 1 once
+             * gp >= window, for any window_size (<= 0 leaves no key) */
             int k_begin = 0;
-            if (t->window > 0 && gp >= t->window) k_begin = gp - t->window + 1;
+            if (t->use_window && gp >= t->window) k_begin = gp - t->window + 1;
             orc_row(t->out + (size_t)i * qh + (size_t)h * t->hd,
                     t->Q + (size_t)i * qh + (size_t)h * t->hd,
                     t->K + (size_t)g * t->hd, t->V + (size_t)g * t->hd,
-                    k_begin, k_end, kvh, t->hd, t->scale, t->cap);
+                    k_begin, k_end, kvh, t->hd, t->scale, t->use_cap, t->cap);
         }
     }
 }
 
 static void orc_causal_common(float *out, const float *Q, const float *K, const float *V,
                               int seq_q, int seq_k, int n_heads, int n_kv_heads, int hd,
-                              float scale, int q_offset, int window, float cap) {
+                              float scale, int q_offset, int use_window, int window,
+                              int use_cap, float cap) {
     orc_causal_task t = {out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, hd,
-                         scale, cap, q_offset, window};
+                         scale, cap, q_offset, window, use_window, use_cap};
     /* attention.c:156 threads only when n_heads >= 2 and the call is not tiny */
     if (orc_threads > 1 && n_heads >= 2 && (seq_q >= 2 || seq_k >= 128))
         orc_parallel_for(orc_causal_worker, &t);
@@ -213,7 +221,7 @@ void orc_causal_attention(float *out, const float *Q, const float *K, const floa
                           int seq_q, int seq_k, int n_heads, int n_kv_heads, int hd,
                           float scale, int q_offset) {
     orc_causal_common(out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, hd, scale,
-                      q_offset, 0, 0.0f);
+                      q_offset, 0, 0, 0, 0.0f);
 }
 
 void orc_sliding_window_attention(float *out, const float *Q, const float *K,
@@ -221,7 +229,7 @@ void orc_sliding_window_attention(float *out, const float *Q, const float *K,
                                   int n_kv_heads, int hd, float scale, int q_offset,
                                   int window) {
     orc_causal_common(out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, hd, scale,
-                      q_offset, window, 0.0f);
+                      q_offset, 1, window, 0, 0.0f);
 }
 
 void orc_causal_attention_softcap(float *out, const float *Q, const float *K,
@@ -229,7 +237,7 @@ void orc_causal_attention_softcap(float *out, const float *Q, const float *K,
                                   int n_kv_heads, int hd, float scale, int q_offset,
                                   float cap) {
     orc_causal_common(out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, hd, scale,
-                      q_offset, 0, cap);
+                      q_offset, 0, 0, 1, cap);
 }
 
 void orc_sliding_window_attention_softcap(float *out, const float *Q, const float *K,
@@ -238,7 +246,7 @@ void orc_sliding_window_attention_softcap(float *out, const float *Q, const floa
                                           float scale, int q_offset, int window,
                                           float cap) {
     orc_causal_common(out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, hd, scale,
-                      q_offset, window, cap);
+                      q_offset, 1, window, 1, cap);
 }
 
 /* attention.c:32-77: heads x windows x rows, single-threaded in the reference;
@@ -255,7 +263,7 @@ void orc_bidirectional_attention(float *out, const float *Q, const float *K,
                 orc_row(out + (size_t)i * hidden + (size_t)h * hd,
                         Q + (size_t)i * hidden + (size_t)h * hd,
                         K + (size_t)h * hd, V + (size_t)h * hd, ws, we, hidden, hd,
-                        scale, 0.0f);
+                        scale, 0, 0.0f);
         }
 }
 

@@ -828,7 +828,9 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     if (cs.dec) pp.qs32 = (float *)ctx->qs32.p;
     pp.blocks = (const PrepBlockB *)(dd + o_pblk);
     pp.q_norm = cs.q_norm; pp.k_norm = cs.k_norm; pp.norm_eps = cs.norm_eps;
-    int mk = timing_begin(ctx, 0);
+    /* a call with no pre-pass blocks (decode without the pre-pass) launches
+     * nothing here and records no timing mark */
+    int mk = pl.pblk.empty() ? -1 : timing_begin(ctx, 0);
     rc = smol_launch_prep(&pp, (int)pl.pblk.size(), ctx->stream);
     timing_end(ctx, mk);
     if (rc)
@@ -907,8 +909,11 @@ static int check_aligned(const void *a, const void *b) {
     return 0;
 }
 
-static int check_rope(const smol_rope_table *rope, int hd, int need) {
+static int check_rope(smol_attn_ctx *ctx, const smol_rope_table *rope, int hd, int need) {
     if (!rope) return 0;
+    /* a table grows on its own context's stream and frees the old arrays once
+     * that stream is idle: kernels of another context could still read them */
+    if (rope->ctx != ctx) return fail(SMOL_ATTN_ERR_ARG, "rope table belongs to another context");
     if (rope->hd != hd) return fail(SMOL_ATTN_ERR_ARG, "rope table head_dim %d != %d", rope->hd, hd);
     return smol_rope_table_ensure(const_cast<smol_rope_table *>(rope), need);
 }
@@ -945,7 +950,7 @@ extern "C" int smol_attn_prefill_qknorm(smol_attn_ctx *ctx, smol_kv_cache *kv, i
     if (pos0 < 0 || seq_q <= 0 || !k_new || !v_new) return fail(SMOL_ATTN_ERR_ARG, "pos0 %d seq_q %d", pos0, seq_q);
     if ((rc = check_aligned(k_new, v_new))) return rc;
     if ((rc = smol_kv_cache_reserve(kv, pos0 + seq_q))) return rc;
-    if ((rc = check_rope(rope, kv->hd, pos0 + seq_q))) return rc;
+    if ((rc = check_rope(ctx, rope, kv->hd, pos0 + seq_q))) return rc;
     const int Hkv = kv->n_kv, G = n_heads / Hkv, hd = kv->hd;
     Plan pl;
     const int f0 = pos0 & ~(SMOL_SLAB - 1);
@@ -996,7 +1001,7 @@ extern "C" int smol_attn_decode_qknorm(smol_attn_ctx *ctx, smol_kv_cache *kv, in
         max_pos = std::max(max_pos, pos[i]);
     }
     if ((rc = smol_kv_cache_reserve(kv, max_pos + 1))) return rc;
-    if ((rc = check_rope(rope, kv->hd, max_pos + 1))) return rc;
+    if ((rc = check_rope(ctx, rope, kv->hd, max_pos + 1))) return rc;
     const int Hkv = kv->n_kv, G = n_heads / Hkv, hd = kv->hd;
     Plan pl;
     /* k_attn_dec reads Q and the new K/V itself (no pre-pass launch):
@@ -1184,6 +1189,7 @@ extern "C" int smol_attn_norm_rope(smol_attn_ctx *ctx, const smol_rope_table *ro
         return fail(SMOL_ATTN_ERR_ARG, "bad arguments");
     if (rope && (!positions || rope->hd != head_dim))
         return fail(SMOL_ATTN_ERR_ARG, "rope needs positions and head_dim %d", rope ? rope->hd : 0);
+    if (rope && rope->ctx != ctx) return fail(SMOL_ATTN_ERR_ARG, "rope table belongs to another context");
     if (weight && !(eps >= 0.0f)) return fail(SMOL_ATTN_ERR_ARG, "norm eps %g", (double)eps);
     if (((uintptr_t)x | (uintptr_t)weight) & 3) return fail(SMOL_ATTN_ERR_ARG, "x / weight must be 4-byte aligned");
     int rc = set_device(ctx);
@@ -1244,11 +1250,30 @@ void legacy_download(const char *fn, void *h, const DevBuf &b, size_t bytes) {
     if (hipStreamSynchronize(ctx->stream) != hipSuccess) legacy_abort(fn);
 }
 
+/* The four causal variants of attention.c. use_window / use_cap say which
+ * entry point was called; the reference's rules for their values are applied
+ * here (attention.c:190-192, 284-308): a window_size <= 0 leaves every row
+ * without keys, so the output is zero; cap * tanhf(s / cap) is the same for
+ * cap and -cap; cap == 0 turns every score into 0 (0 * tanhf(+-inf)), which
+ * is plain attention with scale 0. The device entry points take window > 0
+ * and cap > 0 as "on". */
 void legacy_causal(const char *fn, float *out, const float *Q, const float *K, const float *V, int seq_q,
-                   int seq_k, int Hq, int Hkv, int hd, float scale, int q_offset, int window, float cap) {
+                   int seq_k, int Hq, int Hkv, int hd, float scale, int q_offset, bool use_window, int window,
+                   bool use_cap, float cap) {
     if (seq_q <= 0) return;
-    smol_attn_ctx *ctx = legacy_ctx(fn);
     const size_t qb = (size_t)seq_q * Hq * hd * 4, kb = (size_t)std::max(seq_k, 0) * Hkv * hd * 4;
+    if (use_window && window <= 0) {
+        memset(out, 0, qb);
+        return;
+    }
+    if (!use_window) window = 0;
+    if (use_cap) {
+        if (cap == 0.0f) scale = 0.0f;
+        cap = fabsf(cap);
+    } else {
+        cap = 0.0f;
+    }
+    smol_attn_ctx *ctx = legacy_ctx(fn);
     legacy_upload(fn, g_legacy.q, Q, qb);
     legacy_upload(fn, g_legacy.k, K, kb);
     legacy_upload(fn, g_legacy.v, V, kb);
@@ -1264,28 +1289,30 @@ void legacy_causal(const char *fn, float *out, const float *Q, const float *K, c
 extern "C" void smol_causal_attention(float *out, const float *Q, const float *K, const float *V, int seq_q,
                                       int seq_k, int n_heads, int n_kv_heads, int head_dim, float scale,
                                       int q_offset) {
-    legacy_causal(__func__, out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset, 0, 0.0f);
+    legacy_causal(__func__, out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset, false, 0,
+                  false, 0.0f);
 }
 
 extern "C" void smol_sliding_window_attention(float *out, const float *Q, const float *K, const float *V,
                                               int seq_q, int seq_k, int n_heads, int n_kv_heads, int head_dim,
                                               float scale, int q_offset, int window_size) {
-    legacy_causal(__func__, out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset,
-                  window_size, 0.0f);
+    legacy_causal(__func__, out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset, true,
+                  window_size, false, 0.0f);
 }
 
 extern "C" void smol_causal_attention_softcap(float *out, const float *Q, const float *K, const float *V,
                                               int seq_q, int seq_k, int n_heads, int n_kv_heads, int head_dim,
                                               float scale, int q_offset, float cap) {
-    legacy_causal(__func__, out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset, 0, cap);
+    legacy_causal(__func__, out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset, false, 0,
+                  true, cap);
 }
 
 extern "C" void smol_sliding_window_attention_softcap(float *out, const float *Q, const float *K,
                                                       const float *V, int seq_q, int seq_k, int n_heads,
                                                       int n_kv_heads, int head_dim, float scale, int q_offset,
                                                       int window_size, float cap) {
-    legacy_causal(__func__, out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset,
-                  window_size, cap);
+    legacy_causal(__func__, out, Q, K, V, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset, true,
+                  window_size, true, cap);
 }
 
 extern "C" void smol_bidirectional_attention(float *out, const float *Q, const float *K, const float *V, int seq,

@@ -604,11 +604,26 @@ __device__ __forceinline__ float2 load_f2_sc1(rsrc_t r, unsigned voff) {
     return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
 }
 
-/* one 1 KB direct-to-LDS transfer: lane l's 16 bytes land at lds + 16 l */
+/* One 1 KB direct-to-LDS transfer: lane l's 16 bytes land at lds + 16 l.
+ * The LDS address travels in M0. GFX9-family parts (gfx950 included) need
+ * one wait state between an SALU write of M0 and an LDS-DMA load that reads
+ * it; without the s_nop the load can take the previous transfer's M0 and
+ * land in the previous 1 KB region, leaving its own region stale. The
+ * compiler inserts that nop for LDS-DMA it emits itself but cannot see into
+ * inline asm. M0 is a reserved register to the compiler, so listing it below
+ * only documents the write: the kernels of this file contain no other M0
+ * writer or reader (tests/test_abi.py disassembles the built code object and
+ * checks that every M0 write is this sequence). The compiler's own LDS-DMA
+ * builtin is not used because its wait insertion drains every transfer
+ * (vmcnt(0)) before any LDS read, which would serialise the staging ring. */
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma_1k(rsrc_t r, unsigned voff, unsigned soff, unsigned lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
-                 : "memory");
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff),
+                 "s"(r), "s"(soff)
+                 : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 #define SK_WAVES 4
 
@@ -2182,10 +2197,14 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
      * have one fewer, or none) keep the reads, transfers and barriers and
      * mask every key. */
     const int steps = n0;
-    /* every prologue transfer (and Q) has landed: the first touch of an
-     * item's pages can return its transfers out of order, so the count
-     * alone does not show which slabs are in */
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    /* Slabs 0..NSTG-1 were requested (NDMA transfers each), then the Q
+     * loads (NT * KS). Vector-memory loads, LDS transfers included, count
+     * down vmcnt in the order they were issued, so waiting until WAITN
+     * remain completes every transfer but the last WAITN issued: slabs
+     * 0..NSTG-3 are in LDS (step 0 reads slabs 0, 1 and 2), and the barrier
+     * extends that to every wave's transfers. (A stale 1 KB region on a
+     * process's first call was the M0 hazard of dma_1k, fixed there.) */
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
     __syncthreads();
     f4 sa[NT][2], sb[NT][2];
     h8 kfa[2][KS], kfb[2][KS], vfa[DT], vfb[DT];

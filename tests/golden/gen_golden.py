@@ -21,7 +21,7 @@ sys.path.insert(0, os.path.join(ROOT, "oracle"))
 sys.path.insert(0, os.path.join(ROOT, "smol-genius_amd"))
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 import synth  # noqa: E402
-from oracle import RefLib, simd_branch  # noqa: E402
+from oracle import RefLib, causal_kind, simd_branch  # noqa: E402
 from gen_golden_inputs import bidir_inputs, causal_inputs, digest, norm_inputs  # noqa: E402
 
 OUT = os.path.dirname(os.path.abspath(__file__))
@@ -45,6 +45,19 @@ CAUSAL = [
     ("cap_8_4_128_q7_k100_c50", 8, 4, 128, 7, 100, 93, 0, 50.0),
     ("cap_4_1_256_q26_k26_c30", 4, 1, 256, 26, 26, 0, 0, 30.0),
     ("swacap_8_2_128_q26_k160_w32_c50", 8, 2, 128, 26, 160, 134, 32, 50.0),
+]
+
+# Edge values of the reference-signature variants (attention.c:190-192, 284-308):
+# (name, kind, Hq, Hkv, hd, seq_q, seq_k, q_offset, window, cap). A window_size <= 0
+# leaves every row without keys (zeros); a negative cap acts as |cap|; cap 0 makes
+# every score 0 (the mean of the visible values).
+EDGE = [
+    ("swa0_8_4_128_q7_k64", "swa", 8, 4, 128, 7, 64, 57, 0, 0.0),
+    ("swaneg_4_2_64_q5_k40", "swa", 4, 2, 64, 5, 40, 35, -3, 0.0),
+    ("swacap0_8_2_128_q26_k160", "swa_softcap", 8, 2, 128, 26, 160, 134, 0, 50.0),
+    ("capneg_8_4_128_q7_k100", "softcap", 8, 4, 128, 7, 100, 93, 0, -30.0),
+    ("cap0_4_2_64_q5_k40", "softcap", 4, 2, 64, 5, 40, 35, 0, 0.0),
+    ("swacapneg_8_2_128_q26_k160", "swa_softcap", 8, 2, 128, 26, 160, 134, 32, -50.0),
 ]
 
 # (name, H, hd, window_starts, std)
@@ -78,13 +91,15 @@ def main():
     ref.set_threads(1)
     arrays, meta = {}, {"simd": simd_branch(), "ref": os.path.basename(ref.path),
                         "causal": [], "bidir": [], "rope": [], "norm": []}
-    for i, (name, Hq, Hkv, hd, sq, sk, qo, win, cap) in enumerate(CAUSAL):
+    cases = [(name, causal_kind(win, cap), Hq, Hkv, hd, sq, sk, qo, win, cap)
+             for (name, Hq, Hkv, hd, sq, sk, qo, win, cap) in CAUSAL] + EDGE
+    for i, (name, kind, Hq, Hkv, hd, sq, sk, qo, win, cap) in enumerate(cases):
         seed = 1000 + i
         Q, K, V = causal_inputs(seed, Hq, Hkv, hd, sq, sk)
         scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
-        out = ref.causal_attention(Q, K, V, sq, sk, Hq, Hkv, hd, scale, qo, window=win, cap=cap)
+        out = ref.causal_attention(Q, K, V, sq, sk, Hq, Hkv, hd, scale, qo, window=win, cap=cap, kind=kind)
         arrays[name] = out
-        meta["causal"].append(dict(name=name, seed=seed, Hq=Hq, Hkv=Hkv, hd=hd, seq_q=sq,
+        meta["causal"].append(dict(name=name, kind=kind, seed=seed, Hq=Hq, Hkv=Hkv, hd=hd, seq_q=sq,
                                    seq_k=sk, q_offset=qo, window=win, cap=cap, scale=scale,
                                    digest=digest(Q, K, V)))
     for i, (name, H, hd, ws, std) in enumerate(BIDIR):

@@ -74,3 +74,41 @@ def test_no_gpu_means_no_compute():
     assert b"no HIP device" in lib.smol_attn_last_error()
     with pytest.raises(sa.SmolAttnError):
         sa.Context(0, stream=0)
+
+
+LLVM_BIN = "/opt/rocm/llvm/bin"
+
+
+def _gfx950_disassembly(tmp_path):
+    """Disassembly of the gfx950 code object embedded in the built library."""
+    from smol_genius_amd import smol_attn as sa
+    tools = [os.path.join(LLVM_BIN, t) for t in ("llvm-objcopy", "clang-offload-bundler", "llvm-objdump")]
+    if not all(os.path.exists(t) for t in tools):
+        pytest.skip("ROCm LLVM tools not present")
+    objcopy, bundler, objdump = tools
+    fb, co = str(tmp_path / "fatbin.bin"), str(tmp_path / "gfx950.co")
+    subprocess.run([objcopy, "--dump-section", ".hip_fatbin=" + fb, sa.LIB_PATH, str(tmp_path / "x.so")],
+                   check=True, capture_output=True)
+    subprocess.run([bundler, "--type=o", "--unbundle", "--input=" + fb, "--output=" + co,
+                    "--targets=hipv4-amdgcn-amd-amdhsa--gfx950"], check=True, capture_output=True)
+    out = subprocess.run([objdump, "-d", "--mcpu=gfx950", co], check=True, capture_output=True, text=True).stdout
+    return [l.split("//")[0].strip() for l in out.splitlines() if l.startswith("\t") or l.startswith(" ")]
+
+
+def test_m0_only_written_for_lds_transfers(tmp_path):
+    """Every instruction of the library's gfx950 code that names M0 is the LDS-DMA sequence
+    s_mov_b32 m0, sN / s_nop 0 / buffer_load_dwordx4 ... lds (one wait state between the M0
+    write and the transfer that reads it), and every LDS transfer is preceded by it. The
+    kernels' transfers are inline asm, invisible to the compiler's hazard recognizer, so this
+    checks the built code rather than the source."""
+    ins = [l for l in _gfx950_disassembly(tmp_path) if l]
+    n_dma = 0
+    for i, l in enumerate(ins):
+        if re.search(r"\bm0\b", l):
+            assert re.fullmatch(r"s_mov_b32 m0, s\d+", l), l
+            assert ins[i + 1] == "s_nop 0", (l, ins[i + 1])
+            assert ins[i + 2].startswith("buffer_load_dwordx4") and ins[i + 2].endswith(" lds"), ins[i + 2]
+        if l.startswith("buffer_load") and l.endswith(" lds"):
+            n_dma += 1
+            assert ins[i - 1] == "s_nop 0" and ins[i - 2].startswith("s_mov_b32 m0,"), (ins[i - 2], ins[i - 1], l)
+    assert n_dma > 0

@@ -85,11 +85,12 @@ def test_golden_causal_through_reference_signature(sa, golden):
         Q, K, V = causal_inputs(c["seed"], c["Hq"], c["Hkv"], c["hd"], c["seq_q"], c["seq_k"])
         out = np.full((c["seq_q"], c["Hq"] * c["hd"]), np.nan, np.float32)
         args = (out, Q, K, V, c["seq_q"], c["seq_k"], c["Hq"], c["Hkv"], c["hd"], c["scale"], c["q_offset"])
-        if c["window"] > 0 and c["cap"] > 0:
+        kind = c["kind"]
+        if kind == "swa_softcap":
             sa.smol_sliding_window_attention_softcap(*args, c["window"], c["cap"])
-        elif c["window"] > 0:
+        elif kind == "swa":
             sa.smol_sliding_window_attention(*args, c["window"])
-        elif c["cap"] > 0:
+        elif kind == "softcap":
             sa.smol_causal_attention_softcap(*args, c["cap"])
         else:
             sa.smol_causal_attention(*args)

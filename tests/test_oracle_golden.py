@@ -23,15 +23,20 @@ def test_fixture_generator_unchanged(golden):
         assert digest(Q, K, V) == c["digest"]
 
 
-@pytest.mark.parametrize("idx", range(17))
+@pytest.mark.parametrize("idx", range(23))
 def test_causal_matches_reference(golden, oracle, idx):
     meta, data = golden
     c = meta["causal"][idx]
     Q, K, V = causal_inputs(c["seed"], c["Hq"], c["Hkv"], c["hd"], c["seq_q"], c["seq_k"])
     assert digest(Q, K, V) == c["digest"]
     out = oracle.causal_attention(Q, K, V, c["seq_q"], c["seq_k"], c["Hq"], c["Hkv"], c["hd"],
-                                  c["scale"], c["q_offset"], window=c["window"], cap=c["cap"])
+                                  c["scale"], c["q_offset"], window=c["window"], cap=c["cap"],
+                                  kind=c["kind"])
     np.testing.assert_allclose(out, data[c["name"]], rtol=1e-5, atol=1e-5)
+
+
+def test_golden_case_count(golden):
+    assert len(golden[0]["causal"]) == 23
 
 
 @pytest.mark.parametrize("idx", range(5))
