@@ -87,6 +87,23 @@ SMOL_ATTN_API void *smol_attn_ctx_stream(smol_attn_ctx *ctx);
 SMOL_ATTN_API int smol_attn_ctx_set_timing(smol_attn_ctx *ctx, int enable);
 SMOL_ATTN_API int smol_attn_ctx_timing_read(smol_attn_ctx *ctx, double *ms, int *count);
 
+/* Options of a context (no counterpart in the reference): switches that pick
+ * between equivalent kernels or work splits, for tests and tuning. All are 0
+ * by default, which selects by call shape. Results stay within the path's
+ * tolerance whatever they are set to. */
+#define SMOL_OPT_PREFILL_KERNEL 0 /* 1: k_attn_fb wherever its keys allow, 2: k_attn_fa */
+#define SMOL_OPT_FB_LISTS 1       /* -1: one k_attn_fb workgroup per tile (no tile lists) */
+#define SMOL_OPT_FB_NT 2          /* 2: two row tiles per k_attn_fb wave */
+#define SMOL_OPT_DEC_SLABS 3      /* k_dec: 32-key slabs per workgroup (0: by call size) */
+#define SMOL_OPT_DEC_WAVES 4      /* k_dec: 4 or 8 waves per workgroup (0: by shape) */
+#define SMOL_OPT_DEC_SPLIT 5      /* k_dec: -1 keeps every (sequence, kv head) in one workgroup */
+#define SMOL_OPT_XCD_CHECK 6      /* read only: 1 when workgroup b was seen on XCD b % n_xcc at
+                                   * creation (k_dec's split merge needs it), 0 when not (then
+                                   * k_dec does not split) */
+#define SMOL_OPT_COUNT 7
+SMOL_ATTN_API int smol_attn_ctx_set_option(smol_attn_ctx *ctx, int option, int value);
+SMOL_ATTN_API int smol_attn_ctx_get_option(smol_attn_ctx *ctx, int option, int *value);
+
 /* ---- RoPE table ----------------------------------------------------------
  * Device fp32 cos/sin rows [capacity][head_dim], built on the host exactly as
  * fill_rope_cache does (common/decoder/qkn_decoder.c:261-311):

@@ -20,6 +20,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <numeric>
 #include <queue>
 #include <vector>
 
@@ -28,8 +29,10 @@
 #include "attn_internal.h"
 
 extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t st);
-extern "C" int smol_launch_dec(const SkParams *sp, int hd, int n_items, int nt, int w, int nw, int staged,
-                               hipStream_t st);
+extern "C" int smol_launch_decode(const DecParams *dp, int hd, int rows, int nw, hipStream_t st, hipEvent_t ev0,
+                                  hipEvent_t ev1);
+extern "C" int smol_launch_xcc_probe(unsigned *out, int n, hipStream_t st);
+extern "C" int smol_decode_occupancy(int hd, int rows, int nw);
 extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
 extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st);
 extern "C" int smol_launch_to_bf16_trunc(const float *x, uint16_t *y, long long n, hipStream_t st);
@@ -120,10 +123,15 @@ struct smol_attn_ctx {
     DevBuf qs, kf, vtf, part_o, part_ml, counters;
     DevBuf qs32; /* fp32 Q scratch of the decode kernel */
     DevBuf out32; /* fp32 result of a call whose output is bf16 */
+    DevBuf dec_part; /* k_dec partial slots and flags */
     int cu_count = 256;
+    int n_xcc = 1;       /* XCDs of the device */
+    bool xcd_ok = true;  /* workgroup b runs on XCD b % n_xcc (checked at creation) */
+    unsigned epoch = 0;  /* k_dec launches so far: each one's flags carry its own value */
+    int opt[SMOL_OPT_COUNT] = {};
     /* opt-in per-kernel timing: events bracketing each launch */
     bool timing = false;
-    struct Mark { int kind; hipEvent_t a, b; };
+    struct Mark { int kind; hipEvent_t a, b; bool recorded; };
     std::vector<Mark> marks;
     std::vector<hipEvent_t> event_pool;
     double t_ms[SMOL_TIMING_KINDS] = {0, 0, 0};
@@ -141,18 +149,21 @@ static hipEvent_t pool_event(smol_attn_ctx *ctx) {
     return e;
 }
 
-/* start / stop a timed launch of `kind` (no-ops unless timing is enabled) */
-static int timing_begin(smol_attn_ctx *ctx, int kind) {
+/* start / stop a timed launch of `kind` (no-ops unless timing is enabled).
+ * by_launch: the launch records the pair itself (hipExtLaunchKernelGGL with
+ * start and stop events, which time the kernel's own execution), so nothing
+ * is recorded here */
+static int timing_begin(smol_attn_ctx *ctx, int kind, bool by_launch = false) {
     if (!ctx->timing) return -1;
     hipEvent_t a = pool_event(ctx), b = pool_event(ctx);
     if (!a || !b) return -1;
-    hipEventRecord(a, ctx->stream);
-    ctx->marks.push_back({kind, a, b});
+    if (!by_launch) hipEventRecord(a, ctx->stream);
+    ctx->marks.push_back({kind, a, b, by_launch});
     return (int)ctx->marks.size() - 1;
 }
 
 static void timing_end(smol_attn_ctx *ctx, int mark) {
-    if (mark >= 0) hipEventRecord(ctx->marks[mark].b, ctx->stream);
+    if (mark >= 0 && !ctx->marks[mark].recorded) hipEventRecord(ctx->marks[mark].b, ctx->stream);
 }
 
 /* Tables and caches keep their own device and stream, so destroying them
@@ -212,6 +223,30 @@ static int upload_desc(smol_attn_ctx *ctx, const void *host, size_t bytes) {
 
 /* ------------------------------------------------------------------ context */
 
+/* k_dec merges the splits of a group through one XCD's L2, which needs
+ * workgroup b of a launch to run on XCD b % n_xcc (the round-robin dispatch
+ * of a device in one partition). A probe grid records each workgroup's XCC
+ * id; when any differs, k_dec keeps every group in one workgroup. */
+static int check_xcd_dispatch(smol_attn_ctx *c) {
+    int nx = 0;
+    if (hipDeviceGetAttribute(&nx, hipDeviceAttributeNumberOfXccs, c->device) != hipSuccess || nx <= 0) nx = 1;
+    c->n_xcc = nx;
+    c->xcd_ok = true;
+    if (nx == 1) return 0;
+    const int n = 64 * nx;
+    unsigned *d = nullptr;
+    HIP_TRY(hipMalloc(&d, n * sizeof(unsigned)));
+    std::vector<unsigned> h(n, 0xFFFFFFFFu);
+    int rc = smol_launch_xcc_probe(d, n, c->stream);
+    hipError_t e = rc ? hipErrorLaunchFailure : hipMemcpyAsync(h.data(), d, n * sizeof(unsigned), hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    hipFree(d);
+    if (e != hipSuccess) return fail(SMOL_ATTN_ERR_DEVICE, "XCD probe: %s", hipGetErrorString(e));
+    for (int b = 0; b < n; b++)
+        if (h[b] != (unsigned)(b % nx)) c->xcd_ok = false;
+    return 0;
+}
+
 extern "C" int smol_attn_ctx_create(int device, void *stream, smol_attn_ctx **out) {
     if (!out) return fail(SMOL_ATTN_ERR_ARG, "out is NULL");
     *out = nullptr;
@@ -232,6 +267,11 @@ extern "C" int smol_attn_ctx_create(int device, void *stream, smol_attn_ctx **ou
         delete c;
         return fail(SMOL_ATTN_ERR_DEVICE, "context: %s", hipGetErrorString(e));
     }
+    int rc = check_xcd_dispatch(c);
+    if (rc) {
+        delete c;
+        return rc;
+    }
     *out = c;
     return SMOL_ATTN_OK;
 }
@@ -241,7 +281,7 @@ extern "C" int smol_attn_ctx_destroy(smol_attn_ctx *ctx) {
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
     DevBuf *bufs[] = {&ctx->desc, &ctx->qs, &ctx->kf, &ctx->vtf, &ctx->part_o, &ctx->part_ml, &ctx->counters,
-                      &ctx->qs32, &ctx->out32};
+                      &ctx->qs32, &ctx->out32, &ctx->dec_part};
     for (DevBuf *b : bufs)
         if (b->p) hipFree(b->p);
     for (auto &s : ctx->ring) {
@@ -265,6 +305,21 @@ extern "C" int smol_attn_ctx_synchronize(smol_attn_ctx *ctx) {
 }
 
 extern "C" void *smol_attn_ctx_stream(smol_attn_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+extern "C" int smol_attn_ctx_set_option(smol_attn_ctx *ctx, int option, int value) {
+    if (!ctx) return fail(SMOL_ATTN_ERR_ARG, "ctx is NULL");
+    if (option < 0 || option >= SMOL_OPT_COUNT || option == SMOL_OPT_XCD_CHECK)
+        return fail(SMOL_ATTN_ERR_ARG, "option %d cannot be set", option);
+    ctx->opt[option] = value;
+    return SMOL_ATTN_OK;
+}
+
+extern "C" int smol_attn_ctx_get_option(smol_attn_ctx *ctx, int option, int *value) {
+    if (!ctx || !value) return fail(SMOL_ATTN_ERR_ARG, "NULL argument");
+    if (option < 0 || option >= SMOL_OPT_COUNT) return fail(SMOL_ATTN_ERR_ARG, "option %d", option);
+    *value = option == SMOL_OPT_XCD_CHECK ? (ctx->xcd_ok ? 1 : 0) : ctx->opt[option];
+    return SMOL_ATTN_OK;
+}
 
 extern "C" int smol_attn_ctx_set_timing(smol_attn_ctx *ctx, int enable) {
     if (!ctx) return fail(SMOL_ATTN_ERR_ARG, "ctx is NULL");
@@ -484,7 +539,6 @@ struct Plan {
     int n_groups = 0;
     int q_rows = 0;      /* Q scratch rows per KV head */
     int fresh_rows = 0;  /* fresh rows per KV head */
-    bool staged_ok = true; /* every item fits the staged decode kernel's LDS */
 };
 
 struct CallShape {
@@ -506,30 +560,11 @@ struct CallShape {
 };
 
 
-/* Row tiles x key splits for every batch. The split size is chosen so the
- * whole call has a few waves per compute unit. */
-/* tuning overrides read from the environment (0 when unset) */
-static int env_int(const char *name) {
-    const char *v = getenv(name);
-    return v ? atoi(v) : 0;
-}
-
-/* waves per SIMD the attention kernel is compiled for: 2 where a wave's
- * registers fit in half the file (latency hidden by the other wave), else 1 */
-/* waves per SIMD k_attn_dec is built for: two when one row tile leaves the
- * registers for it */
-static int choose_waves_dec(int hd, int nt) {
-    const int ov = env_int("SMOL_ATTN_WAVES");
-    if (ov == 1 || ov == 2) return ov;
-    if (hd > 128) return 1;
-    return nt == 1 ? 2 : 1;
-}
-
 /* rows_per: query rows of one work item; longest_first: order the merge
  * groups by descending key count, so the last workgroups dispatched are the
  * short ones */
 static void plan_items(Plan &pl, int Hkv, int G, int window, int rows_per, int cu_count, bool longest_first,
-                       bool no_split = false, int max_slabs = 0) {
+                       bool no_split = false) {
     struct Tile { int batch, row0, lo, hi; };
     std::vector<Tile> tiles;
     long long total_slabs = 0;
@@ -554,28 +589,14 @@ static void plan_items(Plan &pl, int Hkv, int G, int window, int rows_per, int c
     /* a workgroup per compute unit and wave slot, each wave >= 2 slabs */
     const long long target_items = (long long)cu_count;
     long long per = (total_slabs * Hkv + target_items - 1) / std::max(1LL, target_items);
-    /* k_attn_dec splits an item's slabs over its 4 waves (at least 8 per item, or 4 when the whole
-     * call has fewer than two slabs per planned workgroup: a 1025-key decode step measured 14.2
-     * against 14.7 µs, while 4 on a call with more work lengthened it), k_attn_fa gives each slab
-     * to all of them */
-    const long long dec_min = total_slabs * Hkv < 2 * target_items ? 4 : 8;
-    int slabs_per_item = (int)std::max(max_slabs ? 2LL : (longest_first ? 4LL : dec_min), per);
-    if (max_slabs) slabs_per_item = std::min(slabs_per_item, max_slabs);
-    /* tuning override: SMOL_ATTN_SLABS_PER_ITEM=n fixes the key slabs per work item */
-    if (const int n = env_int("SMOL_ATTN_SLABS_PER_ITEM")) {
-        if (n > 0) slabs_per_item = n;
-    }
-    if (max_slabs) slabs_per_item = std::min(slabs_per_item, max_slabs); /* the staged kernel's LDS holds no more */
+    /* k_attn_fa gives each slab to all four waves: at least four slabs per item */
+    int slabs_per_item = (int)std::max(4LL, per);
     if (no_split) slabs_per_item = 1 << 28;
     int group = 0;
     const int max_split = SK_MERGE_MAX / rows_per; /* the kernel's merge holds rows * n_split pairs in LDS */
     for (const Tile &t : tiles) {
         const int n_slabs = (t.hi - t.lo + SMOL_SLAB - 1) / SMOL_SLAB;
         int want = std::max(1, (n_slabs + slabs_per_item - 1) / slabs_per_item);
-        /* k_attn_dec: at most 24 splits per group, whose merge reads every split's partial (a decode
-         * step over 8218 keys and 8 kv heads: 64 steps in 1.64 ms with 33 splits, 1.50 ms with 22) */
-        if (!longest_first && !max_slabs) want = std::min(want, 24);
-        if (max_slabs && want > max_split) pl.staged_ok = false; /* items would outgrow the staged LDS */
         const int n_split = std::min(max_split, want);
         const int per_split = (n_slabs + n_split - 1) / std::max(1, n_split);
         int made = 0;
@@ -658,112 +679,228 @@ static std::vector<FbItem> fb_items(const Plan &pl, int n_wg) {
     return out;
 }
 
+/* ---------------------------------------------------------------- k_dec plan */
+
+/* query rows one k_dec workgroup holds: 8 (hi/lo packed in the MFMA columns),
+ * 16, or a row block of DEC_RB(hd) */
+static int dec_tile_rows(int hd, int rows) { return rows <= 8 ? 8 : rows <= 16 ? 16 : DEC_RB(hd); }
+
+struct DecCall {
+    bool direct;                  /* single-token decode, no pre-pass */
+    std::vector<DecSeq> seqs;
+    /* chunk mode: the pre-pass's fresh window and Q scratch */
+    int fresh_pos0 = 0, fresh_row0 = 0, fcap = 0;
+    long long qs_head_stride = 0;
+};
+
+/* Splits every (sequence, kv head, row block) into workgroups of about
+ * `per_wg` slabs (the call's slabs over the compute units, or the option),
+ * assigns the (sequence, kv head) units to XCDs longest first, and orders
+ * each XCD's workgroups with every group's last split after all of its
+ * other splits: the last split merges, and the workgroups an XCD dispatches
+ * before it include every split it waits for. Workgroup b is slot b / n_xcc
+ * of XCD b % n_xcc; slots past an XCD's list are idle. per_wg doubles until
+ * no XCD has more workgroups than it holds at once (`fit`), so none waits
+ * for another to finish before it starts. */
+static void plan_decode(smol_attn_ctx *ctx, const DecCall &dc, int Hkv, int window, int n_rb, int fit,
+                        std::vector<DecItem> &items) {
+    const int nx = ctx->n_xcc;
+    const int n_seq = (int)dc.seqs.size();
+    auto slabs_of = [&](const DecSeq &q) {
+        const int kend = dc.direct ? q.pos : q.pos + q.n_q;
+        const int klo = (window > 0 ? std::max(0, q.pos - window + 1) : 0) & ~(SMOL_SLAB - 1);
+        return kend > klo ? (kend - klo + SMOL_SLAB - 1) / SMOL_SLAB : 0;
+    };
+    long long total = 0;
+    for (const DecSeq &q : dc.seqs) total += (long long)slabs_of(q) * Hkv * n_rb;
+    const bool forced = ctx->opt[SMOL_OPT_DEC_SLABS] > 0;
+    int per_wg = forced ? ctx->opt[SMOL_OPT_DEC_SLABS] : (int)std::max(1LL, (total + ctx->cu_count - 1) / ctx->cu_count);
+    const bool no_split = !ctx->xcd_ok || ctx->opt[SMOL_OPT_DEC_SPLIT] == -1;
+    struct Unit { int seq, kvh, n_split, xcd; long long cost; };
+    std::vector<Unit> units;
+    for (;;) {
+        units.clear();
+        for (int i = 0; i < n_seq; i++) {
+            const int ns = slabs_of(dc.seqs[i]);
+            int sp = no_split ? 1 : std::max(1, std::min(DEC_MAX_SPLIT, (ns + per_wg - 1) / per_wg));
+            for (int g = 0; g < Hkv; g++) units.push_back({i, g, sp, 0, (long long)sp * n_rb});
+        }
+        /* longest first onto the XCD with the fewest workgroups so far */
+        std::vector<int> order(units.size());
+        std::iota(order.begin(), order.end(), 0);
+        std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return units[a].cost > units[b].cost; });
+        std::vector<long long> load(nx, 0);
+        for (int u : order) {
+            const int x = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+            units[u].xcd = x;
+            load[x] += units[u].cost;
+        }
+        const long long most = *std::max_element(load.begin(), load.end());
+        bool all_one = true;
+        for (const Unit &u : units) all_one = all_one && u.n_split == 1;
+        if (forced || no_split || most <= fit || all_one) break;
+        per_wg *= 2;
+    }
+    std::vector<std::vector<DecItem>> lists(nx), lasts(nx);
+    for (const Unit &u : units)
+        for (int rb = 0; rb < n_rb; rb++)
+            for (int sp = 0; sp < u.n_split; sp++) {
+                DecItem it;
+                it.seq = (short)u.seq;
+                it.kvh = (unsigned char)u.kvh;
+                it.rb = (unsigned char)rb;
+                it.split = (unsigned char)sp;
+                it.n_split = (unsigned char)u.n_split;
+                it.pad = 0;
+                (sp == u.n_split - 1 ? lasts : lists)[u.xcd].push_back(it);
+            }
+    size_t slots = 0;
+    for (int x = 0; x < nx; x++) {
+        lists[x].insert(lists[x].end(), lasts[x].begin(), lasts[x].end());
+        slots = std::max(slots, lists[x].size());
+    }
+    DecItem idle;
+    memset(&idle, 0, sizeof(idle));
+    idle.seq = -1;
+    items.assign(slots * nx, idle);
+    for (int x = 0; x < nx; x++)
+        for (size_t k = 0; k < lists[x].size(); k++) items[k * nx + x] = lists[x][k];
+}
+
+/* Plans and launches k_dec for the sequences of `dc` */
+static int run_decode(smol_attn_ctx *ctx, const CallShape &cs, const DecCall &dc) {
+    const int hd = cs.hd, G = cs.Hq / cs.Hkv;
+    int max_q = 0;
+    for (const DecSeq &q : dc.seqs) max_q = std::max(max_q, q.n_q);
+    const int rows = max_q * G;
+    const int TR = dec_tile_rows(hd, rows);
+    const int n_rb = (rows + TR - 1) / TR;
+    if (n_rb > 255 || (int)dc.seqs.size() > 32767 || cs.Hkv > 255)
+        return fail(SMOL_ATTN_ERR_UNSUPPORTED, "decode call too large (%d rows, %d sequences)", rows, (int)dc.seqs.size());
+    const int nw = rows <= 8 && hd <= 128 ? (ctx->opt[SMOL_OPT_DEC_WAVES] == 8 ? 8 : 4) : 4;
+    /* workgroups an XCD holds at once */
+    const int fit = std::max(1, ctx->cu_count / ctx->n_xcc) * smol_decode_occupancy(hd, rows, nw);
+    std::vector<DecItem> items;
+    plan_decode(ctx, dc, cs.Hkv, cs.window, n_rb, fit, items);
+
+    static DecParams dp; /* large (kernel arguments of about 3.6 KB): built in place, one thread per context */
+    static_assert(sizeof(DecParams) <= 4096, "kernel arguments");
+    memset(&dp, 0, sizeof(dp));
+    const smol_kv_cache *kv = cs.kv;
+    dp.kc = kv->k + (size_t)cs.layer * kv_layer_elems(kv);
+    dp.vtc = kv->vt + (size_t)cs.layer * kv_layer_elems(kv);
+    dp.c_slot_stride = (long long)kv_slot_elems(kv);
+    dp.cap = kv->cap;
+    dp.direct = dc.direct ? 1 : 0;
+    if (dc.direct) {
+        dp.q_in = cs.q; dp.k_in = cs.k; dp.v_in = cs.v; dp.in_dtype = cs.dtype;
+        dp.q_stride = cs.q_stride; dp.kv_stride = cs.kv_stride;
+        if (cs.rope) {
+            dp.rope_cos = cs.rope->cos_d;
+            dp.rope_sin = cs.rope->sin_d;
+            dp.rope_kind = cs.rope->type == SMOL_ROPE_INTERLEAVED ? SMOL_ROPE_INTERLEAVED_K : SMOL_ROPE_NEOX_K;
+        } else {
+            dp.rope_kind = SMOL_ROPE_OFF;
+        }
+        dp.q_norm = cs.q_norm; dp.k_norm = cs.k_norm; dp.norm_eps = cs.norm_eps;
+    } else {
+        dp.kf = (const _Float16 *)ctx->kf.p; dp.vtf = (const _Float16 *)ctx->vtf.p; dp.fcap = dc.fcap;
+        dp.fresh_pos0 = dc.fresh_pos0; dp.fresh_row0 = dc.fresh_row0;
+        dp.qs32 = (const float *)ctx->qs32.p; dp.qs_head_stride = dc.qs_head_stride;
+    }
+    dp.qscale = (float)(cs.scale * LOG2E_D);
+    dp.out = cs.out; dp.Hq = cs.Hq; dp.Hkv = cs.Hkv; dp.G = G;
+    dp.window = cs.window;
+    dp.cap2 = cs.cap > 0.0f ? (float)(cs.cap * LOG2E_D) : 0.0f;
+    /* partial slots: O [TR][hd], (m, l) [TR][2], the flag; 256-byte aligned */
+    dp.slot_floats = (TR * (hd + 2) + 1 + 63) & ~63;
+    const size_t n_groups = dc.seqs.size() * cs.Hkv * n_rb;
+    int rc;
+    if ((rc = dev_reserve(ctx->dec_part, n_groups * DEC_MAX_SPLIT * dp.slot_floats * 4, ctx->stream, true))) return rc;
+    dp.part = (float *)ctx->dec_part.p;
+    if (++ctx->epoch == 0) ctx->epoch = 1;
+    dp.epoch = ctx->epoch;
+    dp.n_rb = n_rb;
+    dp.n_items = (int)items.size();
+    dp.n_seq = (int)dc.seqs.size();
+    /* the items and sequences ride in the kernel arguments when they fit;
+     * otherwise one upload of both */
+    const bool items_arg = items.size() <= DEC_ARG_ITEMS, seqs_arg = dc.seqs.size() <= DEC_ARG_SEQS;
+    if (items_arg) memcpy(dp.items, items.data(), items.size() * sizeof(DecItem));
+    if (seqs_arg) memcpy(dp.seqs, dc.seqs.data(), dc.seqs.size() * sizeof(DecSeq));
+    if (!items_arg || !seqs_arg) {
+        const size_t o_seq = ((items_arg ? 0 : items.size() * sizeof(DecItem)) + 255) & ~(size_t)255;
+        std::vector<unsigned char> host(o_seq + (seqs_arg ? 0 : dc.seqs.size() * sizeof(DecSeq)));
+        if (!items_arg) memcpy(host.data(), items.data(), items.size() * sizeof(DecItem));
+        if (!seqs_arg) memcpy(host.data() + o_seq, dc.seqs.data(), dc.seqs.size() * sizeof(DecSeq));
+        if ((rc = upload_desc(ctx, host.data(), host.size()))) return rc;
+        if (!items_arg) dp.items_dev = (const DecItem *)ctx->desc.p;
+        if (!seqs_arg) dp.seqs_dev = (const DecSeq *)((unsigned char *)ctx->desc.p + o_seq);
+    }
+    const int mk = timing_begin(ctx, 1, true);
+    hipEvent_t e0 = mk >= 0 ? ctx->marks[mk].a : nullptr, e1 = mk >= 0 ? ctx->marks[mk].b : nullptr;
+    rc = smol_launch_decode(&dp, hd, rows, nw, ctx->stream, e0, e1);
+    if (rc)
+        return fail(rc == -1 ? SMOL_ATTN_ERR_UNSUPPORTED : SMOL_ATTN_ERR_DEVICE, "k_dec launch (hd %d, %d rows): %s", hd,
+                    rows, rc == -1 ? "unsupported configuration" : hipGetErrorString(hipGetLastError()));
+    return SMOL_ATTN_OK;
+}
+
 static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     const int hd = cs.hd, hdp = (hd + 31) & ~31;
     const int G = cs.Hq / cs.Hkv;
     int max_rows = 0;
     for (auto &b : pl.sb) max_rows = std::max(max_rows, b.n_rows);
-    /* prefill kernel: k_attn_fb where it applies, else k_attn_fa (waves
-     * split the rows, K/V shared through LDS, split-K across workgroups) */
-    const char *pk = getenv("SMOL_ATTN_PREFILL_KERNEL");
+    /* prefill kernel: k_attn_fb (one workgroup per 64-row tile, no merges
+     * between workgroups) when every key is in the fresh buffers and the
+     * call has enough tiles to occupy the device, else k_attn_fa (waves
+     * split the rows, K/V shared through LDS, split-K across workgroups);
+     * SMOL_OPT_PREFILL_KERNEL forces one where the keys allow it */
+    const int pk = ctx->opt[SMOL_OPT_PREFILL_KERNEL];
     const bool fa = !cs.dec;
-    /* k_attn_fb (one workgroup per 64-row tile, no merges between
-     * workgroups) when every key is in the fresh buffers and the call has
-     * enough tiles to occupy the device; SMOL_ATTN_PREFILL_KERNEL=fa keeps
-     * k_attn_fa */
-    bool fb = fa && hd <= 128 && !(pk && strcmp(pk, "fa") == 0);
+    bool fb = fa && hd <= 128 && pk != 2;
     if (fb) {
         long long tiles = 0;
         for (auto &b : pl.sb) {
             if (b.key_lo < b.fresh_pos0) fb = false;
             tiles += (b.n_rows + 63) / 64;
         }
-        /* SMOL_ATTN_PREFILL_KERNEL=fb takes it whenever the keys allow */
-        const bool forced = pk && strcmp(pk, "fb") == 0;
-        if (!forced && tiles * cs.Hkv < ctx->cu_count / 4) fb = false;
+        if (pk != 1 && tiles * cs.Hkv < ctx->cu_count / 4) fb = false;
     }
-    int nt, w, rows_per;
+    int nt = 1, w = 2, rows_per = 64;
     if (fb) {
-        /* 64-row tiles; SMOL_ATTN_FB_NT=2: two row tiles per wave (four
-         * waves per workgroup instead of eight) */
-        nt = env_int("SMOL_ATTN_FB_NT") == 2 ? 2 : 1;
+        /* 64-row tiles; SMOL_OPT_FB_NT 2: two row tiles per wave (four waves
+         * per workgroup instead of eight) */
+        nt = ctx->opt[SMOL_OPT_FB_NT] == 2 ? 2 : 1;
         w = 2;
         rows_per = 64;
     } else if (fa) {
         nt = (hd <= 128 && max_rows > 64) ? 2 : 1;
-        if (const int ov = env_int("SMOL_ATTN_NT"))
-            if (ov == 1 || (ov == 2 && hd <= 128)) nt = ov;
-        w = (hd > 128 || env_int("SMOL_ATTN_FA_WAVES") == 1) ? 1 : 2;
+        w = hd > 128 ? 1 : 2;
         rows_per = 64 * nt;
-    } else {
-        nt = max_rows <= 16 || hd > 128 ? 1 : 2;
-        if (const int ov = env_int("SMOL_ATTN_NT"))
-            if (ov == 1 || (ov == 2 && hd <= 128)) nt = ov;
-        w = choose_waves_dec(hd, nt);
-        rows_per = 16 * nt;
     }
-    /* decode streams slabs through registers; SMOL_ATTN_DEC_STAGED=1 selects
-     * k_attn_dec's staged build (every slab of an item DMA'd into LDS at once),
-     * which measured no faster on the decode workloads */
-    bool staged = cs.dec && !cs.direct && env_int("SMOL_ATTN_DEC_STAGED") == 1;
-    /* k_attn_dec with eight waves and one item per (row tile, kv head) when
-     * no sequence has more than SMOL_ATTN_DEC_WHOLE slabs (default 48, six
-     * per wave) and the items cover at least half the compute units: no
-     * split-K merge, whose chain of device-coherent round trips costs more
-     * than the longer slab loop. With fewer items a compute unit's own load
-     * rate would bound each whole sequence (a C1-sized step: 15.2 against
-     * 20.2 µs), so those keep the split. */
-    int nw = 4;
-    if (cs.dec && !staged && nt == 1 && w == 2 && hd <= 128) {
-        const int whole = env_int("SMOL_ATTN_DEC_WHOLE") ? env_int("SMOL_ATTN_DEC_WHOLE") : 48;
-        int most = 0;
-        long long tiles = 0;
-        for (auto &b : pl.sb) {
-            most = std::max(most, (b.key_hi - std::max(b.key_lo, 0) + SMOL_SLAB - 1) / SMOL_SLAB + 1);
-            tiles += (b.n_rows + rows_per - 1) / rows_per;
-        }
-        if (most <= whole && tiles * cs.Hkv * 2 >= ctx->cu_count) nw = 8;
-        /* SMOL_ATTN_DEC_NW=8 / 4 overrides the item count rule */
-        const int ov = env_int("SMOL_ATTN_DEC_NW");
-        if (ov == 4 || (ov == 8 && most <= whole)) nw = ov;
-    }
-    if (nw == 8) {
-        plan_items(pl, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, false, true, 0);
-    } else {
-        Plan trial = pl;
-        plan_items(trial, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, fa, fb, staged ? (hd > 128 ? 5 : 4) : 0);
-        if (!trial.staged_ok) {
-            staged = false;
-            plan_items(pl, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, fa, fb, 0);
-        } else {
-            pl = std::move(trial);
-        }
-    }
-    /* SMOL_ATTN_FA_QDIRECT=1: k_attn_fa rotates and scales Q as it loads it
-     * and the pre-pass only handles the new K/V */
-    const bool q_direct = fa && !fb && !cs.q_norm && env_int("SMOL_ATTN_FA_QDIRECT") == 1;
-    if (q_direct)
-        pl.pblk.erase(std::remove_if(pl.pblk.begin(), pl.pblk.end(), [](const PrepBlock &k) { return k.kind == 1; }),
-                      pl.pblk.end());
+    if (fa) plan_items(pl, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, true, fb);
 
     /* workspace */
     int rc;
     const size_t fcap = (size_t)std::max(pl.fresh_rows, SMOL_SLAB);
     if (cs.dec) {
         if ((rc = dev_reserve(ctx->qs32, (size_t)cs.Hkv * std::max(pl.q_rows, 1) * hdp * 4, ctx->stream))) return rc;
-    } else if (!q_direct) {
+    } else {
         if ((rc = dev_reserve(ctx->qs, (size_t)cs.Hkv * std::max(pl.q_rows, 1) * hdp * 2, ctx->stream))) return rc;
     }
     if ((rc = dev_reserve(ctx->kf, (size_t)cs.Hkv * fcap * hd * 2, ctx->stream))) return rc;
     if ((rc = dev_reserve(ctx->vtf, (size_t)cs.Hkv * fcap * hd * 2, ctx->stream))) return rc;
     const size_t n_items = pl.items.size();
-    if ((rc = dev_reserve(ctx->part_o, std::max<size_t>(1, n_items) * cs.Hkv * rows_per * hd * 4, ctx->stream))) return rc;
-    if ((rc = dev_reserve(ctx->part_ml, std::max<size_t>(1, n_items) * cs.Hkv * rows_per * 2 * 4, ctx->stream))) return rc;
-    /* one counter per 256-byte line: the workgroups of different groups count in
-     * at about the same time, and atomics on one line are serialised */
-    if ((rc = dev_reserve(ctx->counters, (size_t)std::max(1, pl.n_groups) * cs.Hkv * 4 * SK_COUNTER_STRIDE, ctx->stream,
-                          true)))
-        return rc;
+    if (fa) {
+        if ((rc = dev_reserve(ctx->part_o, std::max<size_t>(1, n_items) * cs.Hkv * rows_per * hd * 4, ctx->stream))) return rc;
+        if ((rc = dev_reserve(ctx->part_ml, std::max<size_t>(1, n_items) * cs.Hkv * rows_per * 2 * 4, ctx->stream))) return rc;
+        /* one counter per 256-byte line: the workgroups of different groups count in
+         * at about the same time, and atomics on one line are serialised */
+        if ((rc = dev_reserve(ctx->counters, (size_t)std::max(1, pl.n_groups) * cs.Hkv * 4 * SK_COUNTER_STRIDE,
+                              ctx->stream, true)))
+            return rc;
+    }
 
     /* k_attn_fb with more tiles than compute units: one workgroup per unit
      * and kv head runs a list of tiles, assigned longest first to the least
@@ -771,14 +908,14 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
      * start up again behind the first */
     std::vector<FbItem> fbi;
     int fb_wg = std::max(1, ctx->cu_count / cs.Hkv);
-    if (!((int)n_items > fb_wg && env_int("SMOL_ATTN_FB_SCHED") != -1)) fb_wg = 0;
+    if (!((int)n_items > fb_wg && ctx->opt[SMOL_OPT_FB_LISTS] != -1)) fb_wg = 0;
     if (fb) fbi = fb_items(pl, fb_wg);
 
     /* descriptor tables in one upload: pre-pass blocks and items, each with
      * its batch */
     const std::vector<PrepBlockB> pbr = prep_records(pl);
     std::vector<SkItemB> itr;
-    if (!fb) {
+    if (fa && !fb) {
         itr.resize(pl.items.size());
         for (size_t i = 0; i < pl.items.size(); i++) itr[i] = {pl.items[i], pl.sb[pl.items[i].batch]};
     }
@@ -828,8 +965,8 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     if (cs.dec) pp.qs32 = (float *)ctx->qs32.p;
     pp.blocks = (const PrepBlockB *)(dd + o_pblk);
     pp.q_norm = cs.q_norm; pp.k_norm = cs.k_norm; pp.norm_eps = cs.norm_eps;
-    /* a call with no pre-pass blocks (decode without the pre-pass) launches
-     * nothing here and records no timing mark */
+    /* a call with no pre-pass blocks launches nothing here and records no
+     * timing mark */
     int mk = pl.pblk.empty() ? -1 : timing_begin(ctx, 0);
     rc = smol_launch_prep(&pp, (int)pl.pblk.size(), ctx->stream);
     timing_end(ctx, mk);
@@ -837,13 +974,25 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
         return fail(rc == -1 ? SMOL_ATTN_ERR_UNSUPPORTED : SMOL_ATTN_ERR_DEVICE, "k_prep launch (hd %d): %s", hd,
                     rc == -1 ? "unsupported configuration" : hipGetErrorString(hipGetLastError()));
 
+    if (cs.dec) {
+        /* a short chunk: k_dec over the cache and the fresh staging, Q from the fp32 scratch */
+        const SkBatch &b = pl.sb[0];
+        DecCall dc;
+        dc.direct = false;
+        dc.seqs.push_back({b.q_pos0, b.slot, 0, b.n_rows / G});
+        dc.fresh_pos0 = b.fresh_pos0;
+        dc.fresh_row0 = b.fresh_row0;
+        dc.fcap = (int)fcap;
+        dc.qs_head_stride = pp.qs_head_stride;
+        return run_decode(ctx, cs, dc);
+    }
+
     SkParams sp;
     memset(&sp, 0, sizeof(sp));
     sp.qs = (const _Float16 *)ctx->qs.p;
     sp.qs_head_stride = pp.qs_head_stride;
     sp.kc = kc; sp.vtc = vtc; sp.c_slot_stride = slot_stride; sp.cap = cap;
     sp.kf = (const _Float16 *)ctx->kf.p; sp.vtf = (const _Float16 *)ctx->vtf.p; sp.fcap = (int)fcap;
-    if (cs.dec) sp.qs32 = (const float *)ctx->qs32.p;
     sp.out = cs.out;
     sp.Hq = cs.Hq; sp.Hkv = cs.Hkv; sp.G = G;
     sp.window = cs.window;
@@ -856,26 +1005,8 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
         sp.fb_items = (const FbItem *)(dd + o_sc);
         sp.n_wg = fb_wg;
     }
-    if (cs.direct) {
-        sp.dec_direct = 1;
-        sp.q_in = cs.q; sp.q_dtype = cs.dtype; sp.q_stride = cs.q_stride;
-        sp.k_in = cs.k; sp.v_in = cs.v; sp.kv_stride = cs.kv_stride;
-        sp.rope_cos = pp.rope_cos; sp.rope_sin = pp.rope_sin;
-        sp.rope_q_kind = cs.rope_q ? pp.rope_kind : SMOL_ROPE_OFF;
-        sp.qscale = pp.qscale;
-        sp.q_norm = cs.q_norm; sp.k_norm = cs.k_norm; sp.norm_eps = cs.norm_eps;
-    }
-    if (q_direct) {
-        sp.q_direct = 1;
-        sp.q_in = cs.q; sp.q_dtype = cs.dtype; sp.q_stride = cs.q_stride;
-        sp.rope_cos = pp.rope_cos; sp.rope_sin = pp.rope_sin;
-        sp.rope_q_kind = cs.rope_q ? pp.rope_kind : SMOL_ROPE_OFF;
-        sp.qscale = pp.qscale;
-    }
     mk = timing_begin(ctx, 1);
-    rc = cs.dec ? smol_launch_dec(&sp, hd, (int)n_items, nt, w, nw, staged ? 1 : 0, ctx->stream)
-         : fb   ? smol_launch_fb(&sp, hd, (int)n_items, nt, ctx->stream)
-                : smol_launch_fa(&sp, hd, (int)n_items, nt, w, ctx->stream);
+    rc = fb ? smol_launch_fb(&sp, hd, (int)n_items, nt, ctx->stream) : smol_launch_fa(&sp, hd, (int)n_items, nt, w, ctx->stream);
     timing_end(ctx, mk);
     if (rc)
         return fail(rc == -1 ? SMOL_ATTN_ERR_UNSUPPORTED : SMOL_ATTN_ERR_DEVICE,
@@ -1002,32 +1133,15 @@ extern "C" int smol_attn_decode_qknorm(smol_attn_ctx *ctx, smol_kv_cache *kv, in
     }
     if ((rc = smol_kv_cache_reserve(kv, max_pos + 1))) return rc;
     if ((rc = check_rope(ctx, rope, kv->hd, max_pos + 1))) return rc;
-    const int Hkv = kv->n_kv, G = n_heads / Hkv, hd = kv->hd;
-    Plan pl;
-    /* k_attn_dec reads Q and the new K/V itself (no pre-pass launch):
-     * SMOL_ATTN_DEC_DIRECT=-1 keeps the pre-pass and the fresh slab */
-    const bool direct = env_int("SMOL_ATTN_DEC_DIRECT") != -1 && env_int("SMOL_ATTN_DEC_STAGED") != 1;
-    if (direct) {
-        for (int i = 0; i < n_seq; i++) /* sequence i: the cache's keys [0, pos[i]) in slabs, the new key apart */
-            pl.sb.push_back({G, i * G, i, pos[i], 0, pos[i], 1, 1 << 30, 0, slots[i], 0, 0});
-        pl.q_rows = n_seq * G;
-        CallShape cs{true, q, k_new, v_new, dtype, n_heads, Hkv, hd, (long long)n_heads * hd,
-                     (long long)Hkv * hd, scale, cap, window, rope, 1, 1, kv, layer, out, q_norm, k_norm, eps, true};
-        return run_plan(ctx, pl, cs);
-    }
-    for (int i = 0; i < n_seq; i++) {
-        /* sequence i: Q token i at position pos[i], one fresh slab holding pos[i] */
-        const int f0 = pos[i] & ~(SMOL_SLAB - 1);
-        pl.pb.push_back({i, 1, i * G, pos[i], i, 1, pos[i], f0, SMOL_SLAB, i * SMOL_SLAB, slots[i], 0});
-        add_fresh_blocks(pl, i, SMOL_SLAB);
-        add_q_blocks(pl, i, 1);
-        pl.sb.push_back({G, i * G, i, pos[i], 0, pos[i] + 1, 1, f0, i * SMOL_SLAB, slots[i], 0, 0});
-    }
-    pl.q_rows = n_seq * G;
-    pl.fresh_rows = n_seq * SMOL_SLAB;
+    const int Hkv = kv->n_kv, hd = kv->hd;
+    /* one launch: k_dec normalises and rotates Q and the new key itself,
+     * scores the new key in fp32 and appends it to the cache */
+    DecCall dc;
+    dc.direct = true;
+    for (int i = 0; i < n_seq; i++) dc.seqs.push_back({pos[i], slots[i], i, 1});
     CallShape cs{true, q, k_new, v_new, dtype, n_heads, Hkv, hd, (long long)n_heads * hd,
-                 (long long)Hkv * hd, scale, cap, window, rope, 1, 1, kv, layer, out, q_norm, k_norm, eps};
-    return run_plan(ctx, pl, cs);
+                 (long long)Hkv * hd, scale, cap, window, rope, 1, 1, kv, layer, out, q_norm, k_norm, eps, true};
+    return run_decode(ctx, cs, dc);
 }
 
 extern "C" int smol_attn_causal(smol_attn_ctx *ctx, const void *q, const void *k, const void *v,

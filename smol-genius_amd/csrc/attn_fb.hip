@@ -1,0 +1,420 @@
+/*
+ * attn_fb.hip - k_attn_fb: prefill and windowed bidirectional attention over
+ * keys that all sit in the fresh fp16 staging.
+ */
+#include "attn_device.h"
+
+/* ---------------------------------------------------------------- k_attn_fb */
+
+/*
+ * Prefill and windowed bidirectional attention over keys that all sit in the
+ * fresh fp16 buffers (no cache slabs), for head_dim <= 128. One workgroup
+ * owns one 64-row tile and needs no other workgroup: its waves form two
+ * groups, the groups take the first and second half of the tile's key slabs,
+ * and the two partial softmax states are merged through LDS at the end.
+ * Within a group, wave w holds the NT row tiles 16 (w NT + t) .. +15 of the
+ * 64-row tile (four waves of one tile, or two waves of two).
+ *
+ * Staging is direct-to-LDS: each wave issues buffer_load_dwordx4 ... lds for
+ * its share of a slab (one 1 KB LDS region per instruction, 16 bytes per
+ * lane, the lane's global chunk chosen so the region receives the swizzled
+ * image below) into a ring of NSTG stages per group. No registers hold
+ * staged data, which leaves room to double-buffer the MFMA fragments: the
+ * fragments a step uses were read from LDS during the step before. Offsets
+ * past the slab (padding of K rows and V^T rows past head_dim) are out of
+ * range of the buffer and arrive as zeros.
+ *
+ * LDS image of a slab (as in k_attn_fa):
+ *   K   : 32 key rows of KROW bytes; 16-byte chunk cb of key row r sits in
+ *         slot cb ^ f(r), f(r) = (r & 3) | ((r >> 3) & 3) << 2.
+ *   V^T : 16*DT rows of 64 bytes; chunk j of row d sits in slot
+ *         j ^ ((d >> 1) & 3).
+ * Step i of a group: the softmax front and exponentials of slab i run on
+ * the vector ALU next to S = K.Q^T of slab i+1 on the matrix cores, then
+ * P.V of slab i, while K of slab i+2 and V^T of slab i+1 are read from LDS;
+ * then the transfer the step issued is waited for and one barrier publishes
+ * it.
+ */
+/* WPG waves per key group, each holding NT 16-row tiles of the 64-row item */
+template <int HD, int WPG>
+struct FbGeom {
+    static constexpr int KS = (HD + 31) / 32;
+    static constexpr int DT = (HD + 15) / 16;
+    static constexpr int HDP = KS * 32;
+    static constexpr int KROW = 256;
+    static constexpr int K_BYTES = SMOL_SLAB * KROW;
+    static constexpr int V_BYTES = 16 * DT * 64;
+    static constexpr int STAGE = (K_BYTES + V_BYTES + 1024 * WPG - 1) / (1024 * WPG) * (1024 * WPG);
+    static constexpr int NDMA = STAGE / (1024 * WPG); /* DMA instructions per wave per slab */
+    static constexpr int NSTG = 2 * 5 * STAGE <= 160 * 1024 ? 5 : 4;
+    static constexpr int GROUP_BYTES = NSTG * STAGE;
+};
+
+/* NT = 1: four waves per key group (two per SIMD, 512 threads); NT = 2: two
+ * waves per key group, each holding two row tiles (one wave per SIMD, 256
+ * threads): every K / V^T fragment read from LDS then feeds two MFMAs, which
+ * halves the LDS reads per flop. One MFMA pipe per SIMD is kept busy by a
+ * single wave (measured: 16x16x32 f16 MFMAs with independent accumulators
+ * issue at the same rate from one wave per SIMD as from two). */
+template <int HD, int NT>
+__global__ __launch_bounds__(NT == 1 ? 512 : 256)
+__attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_attn_fb(SkParams p) {
+    constexpr int WPG = 4 / NT;
+    using Gm = FbGeom<HD, WPG>;
+    constexpr int KS = Gm::KS, DT = Gm::DT, HDP = Gm::HDP, KROW = Gm::KROW;
+    constexpr int K_BYTES = Gm::K_BYTES, STAGE = Gm::STAGE, NDMA = Gm::NDMA, NSTG = Gm::NSTG;
+    constexpr unsigned SLAB_BYTES = SMOL_SLAB * HD * 2;
+    static_assert(HD <= 128, "k_attn_fb covers head_dim <= 128");
+    static_assert(2 * Gm::GROUP_BYTES <= 160 * 1024, "LDS");
+    static_assert(NSTG >= 3, "the step pipeline keeps three slabs resident");
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave / WPG, wg = wave % WPG;
+    const int g = (int)(blockIdx.x % (unsigned)p.Hkv);
+    const int w = (int)(blockIdx.x / (unsigned)p.Hkv);
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * Gm::GROUP_BYTES];
+    /* item w, then the rest of this workgroup's list (the host's
+     * longest-first assignment when the items outnumber the compute units,
+     * where a second wave of workgroups would pay its start-up again) */
+    int item = w;
+    for (;;) {
+    /* lane terms are remade per item rather than held in registers across it */
+    int lane = tid & 63;
+    asm volatile("" : "+v"(lane));
+    const int c = lane & 15, j = lane >> 4;
+    const FbItem it = p.fb_items[item]; /* the batch's fields included: one round trip */
+    const FbItem &b = it;
+    const int next = it.next;
+    const int G = p.G;
+    unsigned char *gbase = smem + grp * Gm::GROUP_BYTES;
+    const unsigned lds_group = (unsigned)(size_t)gbase;
+
+    /* this group's slabs: the first or second half of the item's */
+    const int n_all = (it.key_end - it.key_begin + SMOL_SLAB - 1) / SMOL_SLAB;
+    const int n0 = (n_all + 1) >> 1;
+    const int s_first = grp == 0 ? 0 : n0;
+    const int n_own = grp == 0 ? n0 : n_all - n0;
+    auto slab_k = [&](int i) __attribute__((always_inline)) {
+        const int q = n_own > 0 ? s_first + (i < n_own ? i : n_own - 1) : 0;
+        return it.key_begin + SMOL_SLAB * q;
+    };
+
+    /* DMA geometry: region q = wg + WPG e of a stage; lane offsets within
+     * the slab. The first transfers go out before anything else is set up. */
+    const rsrc_t rk = make_rsrc(p.kf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
+    const rsrc_t rv = make_rsrc(p.vtf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
+    unsigned d_off[NDMA];
+    bool d_isk[NDMA];
+#pragma unroll
+    for (int e = 0; e < NDMA; e++) {
+        const int q = wg + WPG * e;
+        d_isk[e] = q * 1024 < K_BYTES;
+        if (d_isk[e]) {
+            const int kr = q * 4 + (lane >> 4), slot = lane & 15;
+            const int cb = slot ^ ((kr & 3) | (((kr >> 3) & 3) << 2));
+            d_off[e] = cb < HD / 8 ? (unsigned)((kr * HD + cb * 8) * 2) : OOB_OFF;
+        } else {
+            const int d = (q * 1024 - K_BYTES) / 64 + (lane >> 2), slot = lane & 3;
+            const int jj = slot ^ ((d >> 1) & 3);
+            d_off[e] = d < HD ? (unsigned)((d * SMOL_SLAB + jj * 8) * 2) : OOB_OFF;
+        }
+    }
+    auto dma = [&](int k0, int stage) __attribute__((always_inline)) {
+        const int kr = k0 + it.fresh_off; /* from the item: the transfers need no batch load */
+        const unsigned so = (unsigned)(kr / SMOL_SLAB) * SLAB_BYTES;
+#pragma unroll
+        for (int e = 0; e < NDMA; e++)
+            dma_1k(d_isk[e] ? rk : rv, d_off[e], so,
+                   __builtin_amdgcn_readfirstlane(lds_group + stage * STAGE + (wg + WPG * e) * 1024));
+    };
+#pragma unroll
+    for (int q = 0; q < NSTG; q++) dma(slab_k(q), q);
+
+    /* rows of this wave (the same in both groups): tile nt holds rows
+     * 16 (wg NT + nt) + c of the item */
+    int lo[NT], hi[NT];
+    bool valid[NT];
+    h8 qf[NT][KS];
+    int lo_max = -(1 << 30), hi_min = 1 << 30;
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int r = it.row0 + (wg * NT + nt) * 16 + c;
+        valid[nt] = r < b.n_rows;
+        const int qi = r / G;
+        int rl = b.key_lo, rh = b.key_hi;
+        if (b.causal) {
+            rh = min(rh, b.q_pos0 + qi + 1);
+            if (p.window > 0) rl = max(rl, b.q_pos0 + qi - p.window + 1);
+        }
+        lo[nt] = valid[nt] ? rl : -(1 << 30);
+        hi[nt] = valid[nt] ? rh : (1 << 30);
+        lo_max = max(lo_max, lo[nt]);
+        hi_min = min(hi_min, hi[nt]);
+        const _Float16 *qrow =
+            p.qs + (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid[nt] ? r : 0)) * HDP;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) qf[nt][ks] = valid[nt] ? load_h8(qrow + 32 * ks + 8 * j) : zero_h8();
+    }
+#pragma unroll
+    for (int sh = 1; sh < 64; sh <<= 1) {
+        lo_max = max(lo_max, __shfl_xor(lo_max, sh));
+        hi_min = min(hi_min, __shfl_xor(hi_min, sh));
+    }
+    lo_max = __builtin_amdgcn_readfirstlane(lo_max);
+    hi_min = __builtin_amdgcn_readfirstlane(hi_min);
+
+    float m[NT], l[NT], thr[NT];
+    f4 negm[NT];
+    f4 o[NT][DT];
+    /* the row sums on the matrix cores (one row tile per wave): one more
+     * MFMA per step against a fragment of ones (every element of lsum is the
+     * row's sum of its fp16 probabilities, the same weights the P.V product
+     * uses) instead of seven vector adds */
+    constexpr bool MSUM = HD <= 128 && NT == 1;
+    f4 lsum[NT];
+    h8 ones;
+#pragma unroll
+    for (int i = 0; i < 8; i++) ones[i] = (_Float16)1.0f;
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        m[nt] = -INFINITY;
+        l[nt] = 0.0f;
+        lsum[nt] = f4{0.f, 0.f, 0.f, 0.f};
+        thr[nt] = -INFINITY;
+        negm[nt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) o[nt][dt] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    const int kt_row = 8 * (c >> 2) + (c & 3);
+    unsigned kfo[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) kfo[ks] = (unsigned)(kt_row * KROW + 16 * ((4 * ks + j) ^ c));
+    const unsigned vfo = (unsigned)(K_BYTES + c * 64 + 16 * (j ^ ((c >> 1) & 3)));
+    auto lds_h8 = [&](int stage, unsigned off) __attribute__((always_inline)) -> h8 {
+        const uint4 w = *reinterpret_cast<const uint4 *>(gbase + stage * STAGE + off);
+        return *reinterpret_cast<const h8 *>(&w);
+    };
+    const bool capped = p.cap2 > 0.0f;
+    auto read_k = [&](int stage, h8 (&kf)[2][KS]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) kf[t][ks] = lds_h8(stage, kfo[ks] + t * 4 * KROW);
+    };
+    auto read_v = [&](int stage, h8 (&vf)[DT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) vf[dt] = lds_h8(stage, vfo + dt * 1024);
+    };
+    /* S^T - m = K.Q^T - m (raw S with a softcap) */
+    auto qk = [&](const h8 (&kf)[2][KS], f4 (&sacc)[NT][2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                f4 acc = capped ? f4{0.f, 0.f, 0.f, 0.f} : negm[nt];
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t][ks], qf[nt][ks], acc, 0, 0, 0);
+                sacc[nt][t] = acc;
+            }
+    };
+    /* softmax front, in place on the scores: softcap, mask, lazy rescale as
+     * in k_attn_fa (lane (c, j) holds keys 8j + 4t + i of row c in s[t][i]) */
+    auto front = [&](int k0, bool act, f4 (&s)[NT][2]) __attribute__((always_inline)) {
+        /* a step past the group's own slabs masks every key, so its
+         * arithmetic adds nothing and needs no branch of its own */
+        const bool full = act && k0 >= lo_max && k0 + SMOL_SLAB <= hi_min;
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            if (capped) {
+#pragma unroll
+                for (int t = 0; t < 2; t++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) s[nt][t][i] = p.cap2 * tanhf(s[nt][t][i] / p.cap2) + negm[nt][0];
+            }
+            if (!full) {
+#pragma unroll
+                for (int t = 0; t < 2; t++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int key = k0 + 8 * j + 4 * t + i;
+                        s[nt][t][i] = (act && key >= lo[nt] && key < hi[nt]) ? s[nt][t][i] : -INFINITY;
+                    }
+            }
+            bool hit = false;
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) hit |= s[nt][t][i] > thr[nt];
+            if (__any(hit)) {
+                const float mx = row_max4(fmaxf(fmaxf(fmaxf(s[nt][0][0], s[nt][0][1]), fmaxf(s[nt][0][2], s[nt][0][3])),
+                                                fmaxf(fmaxf(s[nt][1][0], s[nt][1][1]), fmaxf(s[nt][1][2], s[nt][1][3]))));
+                const bool need = mx > thr[nt];
+                const float sh = need ? mx : 0.0f;
+                const float m_new = need ? -negm[nt][0] + mx : m[nt];
+                const float alpha = need ? __builtin_amdgcn_exp2f(m[nt] - m_new) : 1.0f;
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) o[nt][dt] *= alpha;
+                if constexpr (MSUM) lsum[nt] *= alpha;
+                else l[nt] *= alpha;
+                m[nt] = m_new;
+                const float mu = m_new == -INFINITY ? 0.0f : m_new;
+                negm[nt] = f4{-mu, -mu, -mu, -mu};
+                thr[nt] = m_new == -INFINITY ? -INFINITY : LAZY_T;
+#pragma unroll
+                for (int t = 0; t < 2; t++) s[nt][t] -= sh;
+            }
+        }
+    };
+    /* P = exp2(S - m) as fp16, row sums */
+    auto expo = [&](const f4 (&s)[NT][2], h8 (&pf)[NT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            float pe[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                pe[e] = __builtin_amdgcn_exp2f(s[nt][e >> 2][e & 3]);
+                pf[nt][e] = (_Float16)pe[e];
+            }
+            if constexpr (!MSUM) l[nt] += ((pe[0] + pe[1]) + (pe[2] + pe[3])) + ((pe[4] + pe[5]) + (pe[6] + pe[7]));
+        }
+    };
+    auto pv = [&](const h8 (&vf)[DT], const h8 (&pf)[NT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+                o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pf[nt], o[nt][dt], 0, 0, 0);
+        if constexpr (MSUM) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) lsum[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[nt], lsum[nt], 0, 0, 0);
+        }
+    };
+
+    /* Slab j of this group sits in stage j % NSTG. Its transfer is issued at
+     * the top of step j-NSTG (the prologue for j < NSTG) and waited for at the
+     * end of that same step (vmcnt(0)), so it has that step's arithmetic to
+     * land. Step i computes the softmax of slab i, S of slab i+1 and P.V of
+     * slab i. The K fragments of slab i+2 and the V^T fragments of slab i+1
+     * are read at the top of step i into the second register set, so step
+     * i+1 starts from registers. Steps past the group's own slab count (the
+     * second group may have one fewer, or none) keep the reads, transfers and
+     * barriers and mask every key. */
+    const int steps = n0;
+    /* Every transfer of the prologue (and Q) has landed before the first
+     * barrier. Counted waits (all but the last slabs' transfers) are not used
+     * for LDS transfers: on pages touched for the first time they let a
+     * barrier pass with earlier transfers' bytes not yet in LDS, so the
+     * transfers do not complete in issue order there. */
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    f4 sa[NT][2], sb[NT][2];
+    h8 kfa[2][KS], kfb[2][KS], vfa[DT], vfb[DT];
+    read_k(0, kfa);
+    qk(kfa, sa);
+    read_k(1, kfa);
+    read_v(0, vfa);
+    /* step 0 refills stage 0 with no barrier in between: V^T of slab 0 must
+     * be in registers first. A transfer of a slab already in L2 can land
+     * before LDS reads queued behind the other waves' reads are served. */
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    int st_k = 2 % NSTG, st_v = 1, st_d = 0; /* stages read in a step, stage refilled */
+    auto step = [&](int i, f4 (&scur)[NT][2], f4 (&snext)[NT][2], auto &kcur, auto &knext, auto &vcur, auto &vnext)
+        __attribute__((always_inline)) {
+        const bool act = i < n_own;
+        h8 pf[NT];
+        /* the next step's LDS reads and the transfer of slab i+NSTG go out
+         * first and proceed during this step's arithmetic, which works from
+         * registers filled before the last barrier */
+        read_k(st_k, knext);
+        read_v(st_v, vnext);
+        dma(slab_k(i + NSTG), st_d);
+        __builtin_amdgcn_sched_barrier(0);
+        front(slab_k(i), act, scur);
+        qk(kcur, snext);
+        expo(scur, pf);
+        pv(vcur, pf);
+        /* the only transfers in flight are the ones this step issued at its
+         * top (slab i+NSTG); the step's arithmetic has covered most of their
+         * latency */
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        st_k = st_k + 1 == NSTG ? 0 : st_k + 1;
+        st_v = st_v + 1 == NSTG ? 0 : st_v + 1;
+        st_d = st_d + 1 == NSTG ? 0 : st_d + 1;
+    };
+    int i = 0;
+    for (; i + 2 <= steps; i += 2) {
+        step(i, sa, sb, kfa, kfb, vfa, vfb);
+        step(i + 1, sb, sa, kfb, kfa, vfb, vfa);
+    }
+    if (i < steps) step(i, sa, sb, kfa, kfb, vfa, vfb);
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) l[nt] = MSUM ? lsum[nt][0] : row_sum4(l[nt]);
+
+    /* merge: group 1 hands its state to group 0 through LDS (lane-wise: the
+     * two waves wg of the groups hold the same rows in the same lanes), one
+     * row tile at a time */
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads(); /* every transfer has landed and every stage read is done */
+    float *xo = reinterpret_cast<float *>(smem) + (wg * 64 + lane) * (4 * DT + 4);
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        if (nt > 0) __syncthreads();
+        if (grp == 1) {
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) *reinterpret_cast<f4 *>(xo + 4 * dt) = o[nt][dt];
+            xo[4 * DT] = m[nt];
+            xo[4 * DT + 1] = l[nt];
+        }
+        __syncthreads();
+        if (grp == 1 || !valid[nt]) continue;
+        const int r = it.row0 + (wg * NT + nt) * 16 + c;
+        const int qi = r / G, hg = r - qi * G;
+        const float m1 = xo[4 * DT], l1 = xo[4 * DT + 1];
+        const float M = fmaxf(m[nt], m1);
+        const float Mu = M == -INFINITY ? 0.0f : M;
+        const float w0 = __builtin_amdgcn_exp2f(m[nt] - Mu), w1 = __builtin_amdgcn_exp2f(m1 - Mu);
+        const float L = l[nt] * w0 + l1 * w1;
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        const float a0 = w0 * inv, a1 = w1 * inv;
+        float *orow = p.out + ((long long)(b.out_tok0 + qi) * p.Hq + (g * G + hg)) * HD;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            const int d = 16 * dt + 4 * j;
+            if (HD % 16 != 0 && d >= HD) continue;
+            const f4 o1 = *reinterpret_cast<const f4 *>(xo + 4 * dt);
+            *reinterpret_cast<f4 *>(orow + d) = o[nt][dt] * a0 + o1 * a1;
+        }
+    }
+    if (next < 0) break;
+    item = next;
+    __syncthreads(); /* the epilogue is done with LDS */
+    } /* items */
+}
+
+template <int HD>
+static int launch_fb_hd(const SkParams *sp, int n_items, int nt, hipStream_t st) {
+    const int n_wg = sp->n_wg > 0 ? sp->n_wg : n_items; /* workgroups per kv head: the heads of the lists */
+    if (nt == 1) hipLaunchKernelGGL((k_attn_fb<HD, 1>), dim3(n_wg * sp->Hkv), dim3(512), 0, st, *sp);
+    else if (nt == 2) hipLaunchKernelGGL((k_attn_fb<HD, 2>), dim3(n_wg * sp->Hkv), dim3(256), 0, st, *sp);
+    else return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+/* k_attn_fb: one 64-row tile per item, every key in the fresh buffers; nt
+ * row tiles per wave (512 threads for nt 1, 256 for nt 2); sp->n_wg
+ * workgroups per kv head (0: one per item) each run their list of items */
+extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st) {
+    if (n_items <= 0) return 0;
+    switch (hd) {
+    case 64: return launch_fb_hd<64>(sp, n_items, nt, st);
+    case 72: return launch_fb_hd<72>(sp, n_items, nt, st);
+    case 80: return launch_fb_hd<80>(sp, n_items, nt, st);
+    case 96: return launch_fb_hd<96>(sp, n_items, nt, st);
+    case 128: return launch_fb_hd<128>(sp, n_items, nt, st);
+    default: return -1;
+    }
+}
+

@@ -167,4 +167,68 @@ typedef struct {
     const float *q_norm; const float *k_norm; float norm_eps;
 } PrepParams;
 
+/* ---- k_dec: decode and short chunks, split over the workgroups of one XCD ----
+ *
+ * A group is one (sequence, kv head): its R = n_q * G query rows (R <= 64)
+ * against the sequence's keys, split into n_split contiguous slab ranges,
+ * one workgroup each. Every workgroup of a group runs on the same XCD
+ * (workgroup b runs on XCD b % n_xcc, checked when a context is created), so
+ * the partials and flags of a group meet in that XCD's L2. There is no
+ * atomic: each split publishes its partial, waits for the stores, then
+ * writes the call's epoch into its flag; the group's last split, placed
+ * after every other split of its XCD in dispatch order (so each split it
+ * waits for has been dispatched before it), polls the flags and merges. */
+#define DEC_MAX_SPLIT 32      /* splits per group (the merge's LDS and the partial slots) */
+#define DEC_ARG_SEQS 32       /* sequences passed in the kernel arguments */
+#define DEC_ARG_ITEMS 320     /* workgroup items passed in the kernel arguments */
+#define DEC_SPIN_LIMIT (1 << 22) /* flag polls before a merger gives up (writes NaN) */
+
+/* one workgroup of the grid (index = blockIdx.x); seq < 0: nothing to do.
+ * A group's rows are cut into row blocks of at most DEC_RB(hd) rows; each
+ * (sequence, kv head, row block) is merged on its own. */
+typedef struct {
+    short seq;
+    unsigned char kvh, rb, split, n_split;
+    short pad;
+} DecItem;
+
+#define DEC_RB(hd) ((hd) <= 128 ? 32 : 16) /* rows of a row block (registers of one wave) */
+
+typedef struct {
+    int pos;       /* decode: position of the new token (cache keys [0, pos) + the new key);
+                      chunk: position of query 0 (keys [0, pos + n_q)) */
+    int slot;      /* cache slot */
+    int tok0;      /* input / output token row of query 0 (decode: the new K/V row too) */
+    int n_q;       /* query tokens (1 for decode) */
+} DecSeq;
+
+typedef struct {
+    /* bf16 cache of the layer: K [slot][kv][cap][hd], V^T [slot][kv][cap/32][hd][32] */
+    const uint16_t *kc; const uint16_t *vtc; long long c_slot_stride; int cap;
+    /* chunk mode: the call's new keys (and the older rows of their first
+     * slab) in the fp16 staging; key k >= fresh_pos0 is fresh row fresh_row0 + k - fresh_pos0 */
+    const _Float16 *kf; const _Float16 *vtf; int fcap; int fresh_pos0; int fresh_row0;
+    /* chunk mode: fp32 Q scratch [kv][rows][hdp], rotated and scaled; row q * G + h */
+    const float *qs32; long long qs_head_stride;
+    /* decode mode (direct = 1): Q, the new K and V rows of the inputs, rotated here */
+    int direct;
+    const void *q_in; const void *k_in; const void *v_in; int in_dtype; long long q_stride; long long kv_stride;
+    const float *rope_cos; const float *rope_sin; int rope_kind;
+    const float *q_norm; const float *k_norm; float norm_eps;
+    float qscale;              /* scale * log2 e */
+    float *out; int Hq, Hkv, G;
+    int window; float cap2;    /* window > 0: sliding window; cap2 > 0: softcap in log2 units */
+    /* split-K: partial slot (merge group * DEC_MAX_SPLIT + split), merge group
+     * (seq * Hkv + kvh) * n_rb + rb, of slot_floats floats:
+     * O [R][hd], (m, l) [R][2], then the flag (an int) at slot_floats - 1 */
+    float *part; int slot_floats; unsigned epoch;
+    int n_rb;                  /* row blocks per (sequence, kv head) */
+    int n_items;               /* grid size */
+    const DecItem *items_dev;  /* the items when n_items > DEC_ARG_ITEMS */
+    int n_seq;
+    const DecSeq *seqs_dev;    /* the sequences when n_seq > DEC_ARG_SEQS */
+    DecSeq seqs[DEC_ARG_SEQS];
+    DecItem items[DEC_ARG_ITEMS];
+} DecParams;
+
 #endif

@@ -41,6 +41,8 @@ SIGNATURES = [
     ("smol_attn_ctx_synchronize", [_vp], _c_int),
     ("smol_attn_ctx_stream", [_vp], _vp),
     ("smol_attn_ctx_set_timing", [_vp, _c_int], _c_int),
+    ("smol_attn_ctx_set_option", [_vp, _c_int, _c_int], _c_int),
+    ("smol_attn_ctx_get_option", [_vp, _c_int, _IP], _c_int),
     ("smol_attn_ctx_timing_read", [_vp, ctypes.POINTER(ctypes.c_double), _IP], _c_int),
     ("smol_rope_table_create", [_vp, _c_int, _c_float, _c_int, _c_int, ctypes.POINTER(_vp)], _c_int),
     ("smol_rope_table_ensure", [_vp, _c_int], _c_int),
@@ -141,6 +143,10 @@ def _dev(t, what):
     return ctypes.c_void_p(t.data_ptr())
 
 
+# context options (include/smol_attn.h SMOL_OPT_*)
+OPT_PREFILL_KERNEL, OPT_FB_LISTS, OPT_FB_NT, OPT_DEC_SLABS, OPT_DEC_WAVES, OPT_DEC_SPLIT, OPT_XCD_CHECK = range(7)
+
+
 class Context:
     """Device + stream + workspace (smol_attn_ctx). Defaults to torch's current stream."""
 
@@ -160,6 +166,15 @@ class Context:
 
     def set_timing(self, enable):
         _check(load().smol_attn_ctx_set_timing(self.h, 1 if enable else 0), "set_timing")
+
+    def set_option(self, option, value):
+        """Context switch SMOL_OPT_* (OPT_* here); 0 is the default choice by call shape."""
+        _check(load().smol_attn_ctx_set_option(self.h, int(option), int(value)), "set_option")
+
+    def get_option(self, option):
+        v = ctypes.c_int()
+        _check(load().smol_attn_ctx_get_option(self.h, int(option), ctypes.byref(v)), "get_option")
+        return v.value
 
     def timing_read(self):
         """{'prep': (ms, n), 'attn': (ms, n), 'other': (ms, n)} since the last read (synchronizes)."""

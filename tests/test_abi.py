@@ -80,19 +80,31 @@ LLVM_BIN = "/opt/rocm/llvm/bin"
 
 
 def _gfx950_disassembly(tmp_path):
-    """Disassembly of the gfx950 code object embedded in the built library."""
+    """Disassembly of the gfx950 code objects embedded in the built library (the
+    .hip_fatbin section holds one offload bundle per translation unit)."""
     from smol_genius_amd import smol_attn as sa
     tools = [os.path.join(LLVM_BIN, t) for t in ("llvm-objcopy", "clang-offload-bundler", "llvm-objdump")]
     if not all(os.path.exists(t) for t in tools):
         pytest.skip("ROCm LLVM tools not present")
     objcopy, bundler, objdump = tools
-    fb, co = str(tmp_path / "fatbin.bin"), str(tmp_path / "gfx950.co")
+    fb = str(tmp_path / "fatbin.bin")
     subprocess.run([objcopy, "--dump-section", ".hip_fatbin=" + fb, sa.LIB_PATH, str(tmp_path / "x.so")],
                    check=True, capture_output=True)
-    subprocess.run([bundler, "--type=o", "--unbundle", "--input=" + fb, "--output=" + co,
-                    "--targets=hipv4-amdgcn-amd-amdhsa--gfx950"], check=True, capture_output=True)
-    out = subprocess.run([objdump, "-d", "--mcpu=gfx950", co], check=True, capture_output=True, text=True).stdout
-    return [l.split("//")[0].strip() for l in out.splitlines() if l.startswith("\t") or l.startswith(" ")]
+    data = open(fb, "rb").read()
+    magic = b"__CLANG_OFFLOAD_BUNDLE__"
+    starts = [i for i in range(len(data)) if data.startswith(magic, i)] if magic in data else []
+    assert starts, "no offload bundle in the library"
+    lines = []
+    for n, a in enumerate(starts):
+        b = starts[n + 1] if n + 1 < len(starts) else len(data)
+        part, co = str(tmp_path / ("b%d.bin" % n)), str(tmp_path / ("b%d.co" % n))
+        open(part, "wb").write(data[a:b])
+        subprocess.run([bundler, "--type=o", "--unbundle", "--input=" + part, "--output=" + co,
+                        "--targets=hipv4-amdgcn-amd-amdhsa--gfx950"], check=True, capture_output=True)
+        out = subprocess.run([objdump, "-d", "--mcpu=gfx950", co], check=True, capture_output=True,
+                             text=True).stdout
+        lines += [l.split("//")[0].strip() for l in out.splitlines() if l.startswith("\t") or l.startswith(" ")]
+    return lines
 
 
 def test_m0_only_written_for_lds_transfers(tmp_path):

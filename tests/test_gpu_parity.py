@@ -30,6 +30,20 @@ def ctx(sa):
     c.close()
 
 
+@pytest.fixture
+def opts(ctx):
+    """Sets context options (SMOL_OPT_*) for one test and restores the defaults after it."""
+    touched = []
+
+    def set_option(option, value):
+        ctx.set_option(option, value)
+        touched.append(option)
+
+    yield set_option
+    for o in touched:
+        ctx.set_option(o, 0)
+
+
 @pytest.fixture(scope="module")
 def wo():
     import workload_oracle
@@ -157,21 +171,21 @@ def test_causal_shapes(ctx, sa, oracle, shape):
 
 
 @pytest.mark.parametrize("shape", [s for s in CAUSAL_SHAPES if s[2] <= 128 and s[5] >= 0])
-def test_causal_shapes_fb(ctx, sa, oracle, shape, monkeypatch):
+def test_causal_shapes_fb(ctx, sa, oracle, shape, opts):
     """The same cases through k_attn_fb (one workgroup per 64-row tile, taken
     here whatever the call's size)."""
-    monkeypatch.setenv("SMOL_ATTN_PREFILL_KERNEL", "fb")
+    opts(sa.OPT_PREFILL_KERNEL, 1)
     test_causal_shapes(ctx, sa, oracle, shape)
 
 
 @pytest.mark.parametrize("window,cap", [(16, 0.0), (0, 2.0), (40, 1.5), (1, 0.0), (7, 50.0)])
-def test_window_softcap_fb(ctx, sa, oracle, window, cap, monkeypatch):
-    monkeypatch.setenv("SMOL_ATTN_PREFILL_KERNEL", "fb")
+def test_window_softcap_fb(ctx, sa, oracle, window, cap, opts):
+    opts(sa.OPT_PREFILL_KERNEL, 1)
     test_window_softcap(ctx, sa, oracle, window, cap)
 
 
-def test_bidirectional_ragged_fb(ctx, sa, oracle, monkeypatch):
-    monkeypatch.setenv("SMOL_ATTN_PREFILL_KERNEL", "fb")
+def test_bidirectional_ragged_fb(ctx, sa, oracle, opts):
+    opts(sa.OPT_PREFILL_KERNEL, 1)
     test_bidirectional_ragged(ctx, sa, oracle)
 
 
@@ -179,13 +193,13 @@ def test_bidirectional_ragged_fb(ctx, sa, oracle, monkeypatch):
     (16, 8, 128, 1536, 0, True), (32, 4, 96, 700, 0, False), (16, 4, 64, 1100, 300, False),
     (16, 16, 64, [0, 100, 700, 750, 1600, 1601, 2000]), (12, 12, 72, [3, 500, 1025, 1090, 1700, 1800]),
 ])
-def test_fb_tile_lists(ctx, sa, oracle, case, monkeypatch):
+def test_fb_tile_lists(ctx, sa, oracle, case, opts):
     """More 64-row tiles than compute units: each k_attn_fb workgroup runs a
     list of tiles (longest first to the least loaded list). Every tile is
     computed as it is with one workgroup per tile, so the two launches agree
     bit for bit, and both meet the oracle."""
     print("fb lists", case, flush=True)
-    monkeypatch.setenv("SMOL_ATTN_PREFILL_KERNEL", "fb")
+    opts(sa.OPT_PREFILL_KERNEL, 1)
     bidir = isinstance(case[3], list)
     if bidir:
         H, _, hd, ws = case
@@ -209,7 +223,7 @@ def test_fb_tile_lists(ctx, sa, oracle, case, monkeypatch):
         return sa.causal(ctx, conv(Q), conv(K), conv(V), seq, seq, Hq, Hkv, hd, sc, 0, window=window).cpu().numpy()
 
     lists = run()
-    monkeypatch.setenv("SMOL_ATTN_FB_SCHED", "-1")
+    opts(sa.OPT_FB_LISTS, -1)
     per_tile = run()
     assert np.array_equal(lists, per_tile)
     if bidir:
@@ -312,37 +326,32 @@ def test_decode_positions(ctx, sa, oracle, wo, positions):
 
 
 @pytest.mark.parametrize("positions", [[0], [33], [64, 0, 95, 7], [1000, 31, 4095]])
-def test_decode_positions_staged(ctx, sa, oracle, wo, positions, monkeypatch):
-    """The same cases through k_attn_dec's staged build (all slabs of an item
-    in LDS at once)."""
-    monkeypatch.setenv("SMOL_ATTN_DEC_STAGED", "1")
-    test_decode_positions(ctx, sa, oracle, wo, positions)
-
-
-@pytest.mark.parametrize("positions", [[0], [33], [64, 0, 95, 7], [1000, 31, 4095]])
-def test_decode_positions_prepass(ctx, sa, oracle, wo, positions, monkeypatch):
-    """The same cases with the pre-pass and the fresh fp16 slab (the kernel
-    otherwise reads Q and the new key itself)."""
-    monkeypatch.setenv("SMOL_ATTN_DEC_DIRECT", "-1")
+@pytest.mark.parametrize("slabs", [1, 3])
+def test_decode_positions_split(ctx, sa, oracle, wo, positions, slabs, opts):
+    """The same cases with every k_dec workgroup holding 1 or 3 key slabs, so
+    the long sequences split into up to 32 workgroups merged through the
+    flags (1000 keys in 1-slab splits: the 32-split cap)."""
+    opts(sa.OPT_DEC_SLABS, slabs)
     test_decode_positions(ctx, sa, oracle, wo, positions)
 
 
 @pytest.mark.parametrize("positions", [[0], [33], [64, 0, 95, 7], [1000, 31, 1400]])
-def test_decode_positions_whole(ctx, sa, oracle, wo, positions, monkeypatch):
-    """The same cases with eight waves per workgroup and one item per
-    sequence and kv head (no split-K merge), forced whatever the item count
-    (head_dim 256 keeps four waves)."""
-    monkeypatch.setenv("SMOL_ATTN_DEC_NW", "8")
+def test_decode_positions_whole(ctx, sa, oracle, wo, positions, opts):
+    """The same cases with one k_dec workgroup per (sequence, kv head) (no
+    merge), with eight waves where the shape allows them."""
+    opts(sa.OPT_DEC_SPLIT, -1)
+    opts(sa.OPT_DEC_WAVES, 8)
     test_decode_positions(ctx, sa, oracle, wo, positions)
 
 
 @pytest.mark.parametrize("window,cap,qk", [(0, 0.0, False), (16, 2.0, False), (0, 0.0, True)])
-def test_decode_whole_window_norm(ctx, sa, oracle, wo, window, cap, qk, monkeypatch):
+def test_decode_whole_window_norm(ctx, sa, oracle, wo, window, cap, qk, opts):
     """Eight-wave whole-sequence decode with a window and softcap, and with
     per-head Q/K norms (72-wide heads: a row tile's chunks past head_dim)."""
     from smol_genius_amd import runner
     from smol_genius_amd.workloads import Decode
-    monkeypatch.setenv("SMOL_ATTN_DEC_NW", "8")
+    opts(sa.OPT_DEC_SPLIT, -1)
+    opts(sa.OPT_DEC_WAVES, 8)
     for hq, hkv, hd in [(16, 8, 128), (6, 2, 72)]:
         positions = [0, 40, 200, 1000]
         print("decode whole", hd, window, cap, qk, flush=True)
@@ -360,11 +369,13 @@ def test_decode_whole_window_norm(ctx, sa, oracle, wo, window, cap, qk, monkeypa
 
 @pytest.mark.parametrize("hq,hkv,hd,rt,bf", [(16, 8, 128, 0, False), (8, 1, 256, 1, False), (6, 2, 72, 0, True),
                                              (4, 4, 80, 1, False), (8, 2, 96, 0, True), (4, 4, 64, 0, True),
-                                             (32, 2, 128, 0, False), (64, 2, 64, 0, False)])
-def test_decode_direct_cache_rows(ctx, sa, oracle, wo, hq, hkv, hd, rt, bf, monkeypatch):
-    """Decode without the pre-pass appends the same bf16 cache rows as the
-    pre-pass (the rotation formulas are the same) and both outputs meet the
-    oracle; G = 32 puts two row tiles in a work item."""
+                                             (32, 2, 128, 0, False), (64, 2, 64, 0, False), (24, 1, 256, 0, True)])
+def test_decode_direct_cache_rows(ctx, sa, oracle, wo, hq, hkv, hd, rt, bf):
+    """k_dec normalises, rotates and appends the new key itself; a one-token
+    prefill at the same position goes through the pre-pass (k_prep) and
+    k_dec's chunk mode. Both append the same bf16 cache rows (the rotation
+    formulas are the same) and both outputs meet the oracle. G = 32 and 64
+    cut the rows into row blocks; 24 heads at hd 256, into blocks of 16."""
     from smol_genius_amd import runner
     from smol_genius_amd.workloads import Decode
     positions = [0, 40, 200, 31]
@@ -375,18 +386,19 @@ def test_decode_direct_cache_rows(ctx, sa, oracle, wo, hq, hkv, hd, rt, bf, monk
         for k in ("q", "k", "v"):
             x[k] = synth.f32_to_bf16_bits(x[k])
     want = wo.decode(oracle, wl, {k: (widen(a) if bf and k in ("q", "k", "v") else a) for k, a in x.items()})
-    got, rows = [], []
-    for mode in ("0", "-1"):
-        monkeypatch.setenv("SMOL_ATTN_DEC_DIRECT", mode)
-        r = runner.prepare(ctx, wl, x)
-        out = sa.decode(ctx, r.kv, 0, r.rope, np.arange(wl.n_seq), wl.positions, dev(x["q"], bf), dev(x["k"], bf),
-                        dev(x["v"], bf), wl.Hq, wl.scale).cpu().numpy()
-        assert_parity(out, want, "decode direct=%s hd %d" % (mode, hd))
-        got.append(out)
-        rows.append([r.kv.read(0, i, p, 1) for i, p in enumerate(positions)])
-    for a, b in zip(rows[0], rows[1]):
-        np.testing.assert_array_equal(a[0], b[0])
-        np.testing.assert_array_equal(a[1], b[1])
+    r = runner.prepare(ctx, wl, x)
+    out = sa.decode(ctx, r.kv, 0, r.rope, np.arange(wl.n_seq), wl.positions, dev(x["q"], bf), dev(x["k"], bf),
+                    dev(x["v"], bf), wl.Hq, wl.scale).cpu().numpy()
+    assert_parity(out, want, "decode direct hd %d" % hd)
+    direct_rows = [r.kv.read(0, i, p, 1) for i, p in enumerate(positions)]
+    r2 = runner.prepare(ctx, wl, x)
+    for i, p in enumerate(positions):
+        q1, k1, v1 = (dev(x[k][i:i + 1], bf) for k in ("q", "k", "v"))
+        o1 = sa.prefill(ctx, r2.kv, 0, i, r2.rope, p, q1, k1, v1, wl.Hq, wl.scale).cpu().numpy()
+        assert_parity(o1, want[i:i + 1], "one-token prefill hd %d pos %d" % (hd, p))
+        k_row, v_row = r2.kv.read(0, i, p, 1)
+        np.testing.assert_array_equal(k_row, direct_rows[i][0])
+        np.testing.assert_array_equal(v_row, direct_rows[i][1])
 
 
 @pytest.mark.parametrize("window,cap", [(16, 0.0), (0, 2.0), (1, 0.0), (40, 1.5), (1, 3.0)])
@@ -406,8 +418,14 @@ def test_decode_window_softcap(ctx, sa, oracle, wo, window, cap):
 
 
 @pytest.mark.parametrize("name", ["qwen06b_decode", "gemma_mqa_decode", "qwen17b_stream"])
-def test_workload_full_size_staged_decode(ctx, oracle, wo, name, monkeypatch):
-    monkeypatch.setenv("SMOL_ATTN_DEC_STAGED", "1")
+@pytest.mark.parametrize("split", [-1, 1])
+def test_workload_full_size_dec_splits(ctx, sa, oracle, wo, name, split, opts):
+    """The decode workloads with no split (one workgroup per sequence and kv
+    head) and with the most splits (one slab per workgroup, capped at 32)."""
+    if split == -1:
+        opts(sa.OPT_DEC_SPLIT, -1)
+    else:
+        opts(sa.OPT_DEC_SLABS, 1)
     test_workload_full_size(ctx, oracle, wo, name)
 
 
