@@ -235,6 +235,21 @@ SMOL_ATTN_API int smol_attn_norm_rope(smol_attn_ctx *ctx, const smol_rope_table 
                                       const float *weight, float eps, const int *positions, int seq,
                                       int n_heads, int head_dim);
 
+/* The bf16 decoder's rounding of Q and the new K rows, in place on a device
+ * bf16 array x [seq][n_heads*head_dim] (16-byte aligned, head_dim a multiple
+ * of 8): per-head RMSNorm with the device fp32 weight (skipped when NULL),
+ * then the interleaved rotation of row s at table position pos0 + s (skipped
+ * when rope is NULL; the table must be SMOL_ROPE_INTERLEAVED), each result
+ * rounded to bf16 by truncation (bf16_rms_norm_per_head and
+ * bf16_apply_rope_interleaved, common/decoder/qkn_bf16_decoder.c:73-91 and
+ * :264-283). The order of operations is fixed, so the bits do not depend on
+ * the launch: the sum of squares is one fused multiply-add per element in
+ * element order, 1/sqrt(ss/head_dim + eps) is correctly rounded, the norm
+ * is (x*r)*w, and a pair rotates as fma(x0,c,-(x1*s)), fma(x1,c,x0*s). */
+SMOL_ATTN_API int smol_attn_norm_rope_bf16(smol_attn_ctx *ctx, const smol_rope_table *rope, uint16_t *x,
+                                           const float *weight, float eps, int pos0, int seq,
+                                           int n_heads, int head_dim);
+
 #ifdef __cplusplus
 }
 #endif

@@ -173,6 +173,8 @@ class Oracle(_Lib):
         self._generic = self._fn("set_vec_generic", [ci])
         self._bf16_attn = self._fn("bf16_attention_softcap",
                                    [_U16, _U16, _U16, _U16, ci, ci, ci, ci, ci, cf, ci, ci, cf])
+        self._bf16_norm = self._fn("bf16_rms_norm_per_head", [_U16, _F, ci, ci, ci, cf])
+        self._bf16_rope = self._fn("bf16_apply_rope_interleaved", [_U16, _F, _F, ci, ci, ci])
 
     def set_vec_generic(self, on):
         self._generic(1 if on else 0)
@@ -199,6 +201,22 @@ class Oracle(_Lib):
         self._bf16_attn(u(out), u(q), u(k), u(v), seq_q, seq_k, n_heads, n_kv_heads,
                         head_dim, ctypes.c_float(scale), q_offset, window, ctypes.c_float(cap))
         return out
+
+
+    def bf16_rms_norm_per_head(self, x, w, seq, n_heads, head_dim, eps):
+        """bf16 bits [seq, n_heads*head_dim] -> normalised bf16 bits (truncating)"""
+        y = np.array(x, np.uint16, copy=True, order="C")
+        w = np.ascontiguousarray(w, np.float32)
+        self._bf16_norm(y.ctypes.data_as(_U16), _fp(w), seq, n_heads, head_dim, ctypes.c_float(eps))
+        return y
+
+    def bf16_apply_rope_interleaved(self, x, cos, sin, seq, n_heads, head_dim):
+        """bf16 bits [seq, n_heads*head_dim] rotated with table rows cos/sin [seq, head_dim] (truncating)"""
+        y = np.array(x, np.uint16, copy=True, order="C")
+        c = np.ascontiguousarray(cos, np.float32)
+        s = np.ascontiguousarray(sin, np.float32)
+        self._bf16_rope(y.ctypes.data_as(_U16), _fp(c), _fp(s), seq, n_heads, head_dim)
+        return y
 
 
 def ref_path():

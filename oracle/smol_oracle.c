@@ -24,6 +24,9 @@
  *   orc_apply_rope_interleaved      rope.c:68-93
  *   orc_bf16_attention_softcap      common/decoder/qkn_bf16_decoder.c:120-229
  *       (two-pass softmax, truncating bf16 output, optional window/softcap)
+ *   orc_bf16_rms_norm_per_head      common/decoder/qkn_bf16_decoder.c:73-91
+ *   orc_bf16_apply_rope_interleaved common/decoder/qkn_bf16_decoder.c:264-283
+ *       (truncating bf16 after each step, with a stated operation order)
  *   orc_rms_norm_per_head           common/kernels/rmsnorm.c:78-140
  *       (AVX-512 order: 16-lane fused multiply-add accumulators over the
  *       16-wide blocks, a halving tree, then a scalar tail)
@@ -415,6 +418,53 @@ static inline uint16_t orc_f32_to_bf16_trunc(float f) {
 
 void orc_bf16_widen(float *dst, const uint16_t *src, size_t n) {
     for (size_t i = 0; i < n; i++) dst[i] = orc_bf16_to_f32(src[i]);
+}
+
+/* qkn_bf16_decoder.c:73-91 (bf16_rms_norm_per_head), in place on bf16 rows
+ * x [seq][n_heads * hd], with the operation order that the GPU path fixes:
+ * ss = fmaf(v, v, ss) element by element from 0, r = 1 / sqrtf(ss / hd +
+ * eps) (each step correctly rounded), v' = trunc((v * r) * w[d]).
+ * (The reference's clang -O3 -ffast-math build may reassociate the sum and
+ * use a reciprocal square root estimate, so its own bits depend on the build;
+ * this is the order written in its source with the multiply-add fused.) */
+void orc_bf16_rms_norm_per_head(uint16_t *x, const float *w, int seq, int n_heads, int hd, float eps) {
+    for (size_t r = 0; r < (size_t)seq * n_heads; r++) {
+        uint16_t *v = x + r * hd;
+        float ss = 0.0f;
+        for (int d = 0; d < hd; d++) {
+            float a = orc_bf16_to_f32(v[d]);
+            ss = fmaf(a, a, ss);
+        }
+        float ri = 1.0f / sqrtf(ss / (float)hd + eps);
+        for (int d = 0; d < hd; d++) {
+            float a = orc_bf16_to_f32(v[d]) * ri;
+            v[d] = orc_f32_to_bf16_trunc(a * w[d]);
+        }
+    }
+}
+
+/* qkn_bf16_decoder.c:264-283 (bf16_apply_rope_interleaved), in place on
+ * bf16 rows x [seq][n_heads * hd]; row s uses cos_t / sin_t row s. Pair
+ * (2i, 2i + 1) with c = cos[2i], s = sin[2i]:
+ *   x0' = trunc(fmaf(x0, c, -(x1 * s))), x1' = trunc(fmaf(x1, c, x0 * s))
+ * (the source's x0*c - x1*s and x1*c + x0*s with the first product fused,
+ * as a contracting compiler emits them). */
+void orc_bf16_apply_rope_interleaved(uint16_t *x, const float *cos_t, const float *sin_t, int seq,
+                                     int n_heads, int hd) {
+    int half = hd / 2;
+    for (int s = 0; s < seq; s++) {
+        const float *cr = cos_t + (size_t)s * hd, *sr = sin_t + (size_t)s * hd;
+        for (int h = 0; h < n_heads; h++) {
+            uint16_t *v = x + ((size_t)s * n_heads + h) * hd;
+            for (int i = 0; i < half; i++) {
+                float x0 = orc_bf16_to_f32(v[2 * i]), x1 = orc_bf16_to_f32(v[2 * i + 1]);
+                float c = cr[2 * i], sn = sr[2 * i];
+                float p1 = x1 * sn, p0 = x0 * sn;
+                v[2 * i] = orc_f32_to_bf16_trunc(fmaf(x0, c, -p1));
+                v[2 * i + 1] = orc_f32_to_bf16_trunc(fmaf(x1, c, p0));
+            }
+        }
+    }
 }
 
 /* qkn_bf16_decoder.c:120-229: scores into a buffer, max, expf, sum, weighted

@@ -36,6 +36,8 @@ extern "C" int smol_decode_occupancy(int hd, int rows, int nw);
 extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
 extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st);
 extern "C" int smol_launch_to_bf16_trunc(const float *x, uint16_t *y, long long n, hipStream_t st);
+extern "C" int smol_launch_bf16_norm_rope(uint16_t *x, const float *w, float eps, const float *cos_t,
+                                          const float *sin_t, int pos0, int seq, int H, int hd, hipStream_t st);
 extern "C" int smol_launch_norm_rope(float *x, const float *w, float eps, const float *cos_t, const float *sin_t,
                                      const int *pos, int seq, int n_heads, int hd, int kind, hipStream_t st);
 
@@ -52,6 +54,9 @@ static int fail(int code, const char *fmt, ...) {
     va_end(ap);
     return code;
 }
+
+/* the same error channel for the library's other translation units */
+extern "C" int smol_internal_fail(int code, const char *msg) { return fail(code, "%s", msg); }
 
 #define HIP_TRY(expr)                                                                    \
     do {                                                                                 \
@@ -1325,6 +1330,27 @@ extern "C" int smol_attn_norm_rope(smol_attn_ctx *ctx, const smol_rope_table *ro
     if (smol_launch_norm_rope(x, weight, eps, rope ? rope->cos_d : nullptr, rope ? rope->sin_d : nullptr, pos_d, seq,
                               n_heads, head_dim, kind, ctx->stream))
         return fail(SMOL_ATTN_ERR_DEVICE, "norm/rope launch: %s", hipGetErrorString(hipGetLastError()));
+    return SMOL_ATTN_OK;
+}
+
+extern "C" int smol_attn_norm_rope_bf16(smol_attn_ctx *ctx, const smol_rope_table *rope, uint16_t *x,
+                                        const float *weight, float eps, int pos0, int seq, int n_heads,
+                                        int head_dim) {
+    if (!ctx || !x || seq <= 0 || n_heads <= 0 || head_dim <= 0 || (head_dim & 7) || pos0 < 0)
+        return fail(SMOL_ATTN_ERR_ARG, "bad arguments (head_dim must be a multiple of 8)");
+    if (rope && (rope->hd != head_dim || rope->type != SMOL_ROPE_INTERLEAVED))
+        return fail(SMOL_ATTN_ERR_ARG, "the bf16 rotation needs an interleaved table of head_dim %d", head_dim);
+    if (rope && rope->ctx != ctx) return fail(SMOL_ATTN_ERR_ARG, "rope table belongs to another context");
+    if (weight && !(eps >= 0.0f)) return fail(SMOL_ATTN_ERR_ARG, "norm eps %g", (double)eps);
+    if (((uintptr_t)x & 15) || ((uintptr_t)weight & 3))
+        return fail(SMOL_ATTN_ERR_ARG, "x must be 16-byte and weight 4-byte aligned");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    if (!rope && !weight) return SMOL_ATTN_OK;
+    if (rope && (rc = smol_rope_table_ensure(const_cast<smol_rope_table *>(rope), pos0 + seq))) return rc;
+    if (smol_launch_bf16_norm_rope(x, weight, eps, rope ? rope->cos_d : nullptr, rope ? rope->sin_d : nullptr, pos0,
+                                   seq, n_heads, head_dim, ctx->stream))
+        return fail(SMOL_ATTN_ERR_DEVICE, "bf16 norm/rope launch: %s", hipGetErrorString(hipGetLastError()));
     return SMOL_ATTN_OK;
 }
 

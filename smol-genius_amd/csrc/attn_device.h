@@ -66,10 +66,6 @@ __device__ __forceinline__ h8 zero_h8() {
     return z;
 }
 
-__device__ __forceinline__ float load_in(const void *base, int dtype, long long idx) {
-    return dtype == SMOL_IN_BF16 ? bf16_to_f32(((const uint16_t *)base)[idx])
-                                 : ((const float *)base)[idx];
-}
 
 __device__ __forceinline__ int rope_partner(int d, int hd, int kind) {
     if (kind == SMOL_ROPE_NEOX_K) { int half = hd >> 1; return d < half ? d + half : d - half; }
@@ -119,11 +115,6 @@ __device__ __forceinline__ void unpack_bf16x8(uint4 w, float *v) {
     }
 }
 
-/* 8 consecutive fp32 table entries (16-byte aligned: d0 % 8 == 0) */
-__device__ __forceinline__ void tab8(const float *t, float *v) {
-    const float4 a = *reinterpret_cast<const float4 *>(t), b = *reinterpret_cast<const float4 *>(t + 4);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-}
 
 /* 1 / sqrt(mean(x^2) + eps) of the head row at `base + row` (hd elements,
  * fp32 or bf16), computed by the 8 lanes of an aligned lane group (j = lane
@@ -142,57 +133,6 @@ __device__ __forceinline__ float head_rinv8(const void *base, int dtype, long lo
     ss += __shfl_xor(ss, 2, 8);
     ss += __shfl_xor(ss, 4, 8);
     return 1.0f / sqrtf(ss / (float)hd + eps);
-}
-
-/* Rotates the 8 elements [d0, d0+8) of a head vector whose row starts at
- * `base + row` (fp32 or bf16 input), position `pos` of the table. With a
- * norm weight `nw`, each element (and each rotation partner) is first
- * normalised as (x * nw[d]) * rinv, the order of rmsnorm.c:119-121. */
-__device__ __forceinline__ void rope8(const void *base, int dtype, long long row, int d0, int hd, int kind,
-                                      const float *cos_t, const float *sin_t, long long pos, float *out,
-                                      const float *nw = nullptr, float rinv = 1.0f) {
-    load8(base, dtype, row + d0, out);
-    if (nw) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) out[i] = (out[i] * nw[d0 + i]) * rinv;
-    }
-    if (kind == SMOL_ROPE_OFF) return;
-    const float *c = cos_t + pos * hd, *s = sin_t + pos * hd;
-    float cv[8], sv[8];
-    tab8(c + d0, cv);
-    tab8(s + d0, sv);
-    if (kind == SMOL_ROPE_INTERLEAVED_K) {
-#pragma unroll
-        for (int i = 0; i < 8; i += 2) {
-            const float x0 = out[i], x1 = out[i + 1];
-            out[i] = x0 * cv[i] - x1 * sv[i];
-            out[i + 1] = x1 * cv[i + 1] + x0 * sv[i + 1];
-        }
-        return;
-    }
-    const int half = hd >> 1;
-    float pr[8];
-    if ((half & 7) == 0) {
-        const int p0 = d0 < half ? d0 + half : d0 - half;
-        load8(base, dtype, row + p0, pr);
-        if (nw) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) pr[i] = (pr[i] * nw[p0 + i]) * rinv;
-        }
-    } else {
-        /* half not a multiple of 8 (head_dim 72): partners element by element */
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int pd = rope_partner(d0 + i, hd, kind);
-            pr[i] = load_in(base, dtype, row + pd);
-            if (nw) pr[i] = (pr[i] * nw[pd]) * rinv;
-        }
-    }
-    /* NeoX: x1 c - x2 s for the first half, x2 c + x1 s for the second
-     * (rope.c:99-164, fmsub / fmadd) */
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-        out[i] = d0 + i < half ? fmaf(out[i], cv[i], -(pr[i] * sv[i])) : fmaf(out[i], cv[i], pr[i] * sv[i]);
 }
 
 /* Raw bits of 8 consecutive input elements (bf16: one 16-byte load, fp32:

@@ -103,23 +103,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
         l[nt] = 0.0f;
         negm[nt] = f4{0.f, 0.f, 0.f, 0.f};
         thr[nt] = -INFINITY;
-        if (p.q_direct) {
-            /* rotate and scale Q here: row r is query qi of head g*G + hg */
-            const int hg = r - qi * G;
-            const long long row = (long long)(b.out_tok0 + (valid ? qi : 0)) * p.q_stride + (long long)(g * G + hg) * HD;
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++) {
-                const int d0 = 32 * ks + 8 * j;
-                float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-                if (valid && (HD % 32 == 0 || d0 < HD)) {
-                    rope8(p.q_in, p.q_dtype, row, d0, HD, p.rope_q_kind, p.rope_cos, p.rope_sin, b.q_pos0 + qi, v);
-#pragma unroll
-                    for (int i = 0; i < 8; i++) v[i] *= p.qscale;
-                }
-#pragma unroll
-                for (int i = 0; i < 8; i++) qf[nt][ks][i] = (_Float16)v[i];
-            }
-        } else {
+        {
             const _Float16 *qrow =
                 p.qs + (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid ? r : 0)) * HDP;
 #pragma unroll

@@ -104,20 +104,6 @@ typedef struct {
      * follows the items' next links */
     const FbItem *fb_items;
     int n_wg;
-    /* k_attn_fa reads Q itself (q_direct = 1): input row out_tok0 + i of a
-     * batch, rotated at table row q_pos0 + i and scaled by qscale */
-    int q_direct;
-    const void *q_in; int q_dtype; long long q_stride;
-    const float *rope_cos; const float *rope_sin; int rope_q_kind;
-    float qscale;
-    /* k_attn_dec without a pre-pass (dec_direct = 1, one query token per
-     * batch): Q as above (normalised by q_norm first when given); the batch's
-     * new key and value are input row out_tok0 of k_in / v_in (kv_stride
-     * elements per row), at position q_pos0, and the slabs cover the keys
-     * before it; the batch's last split appends the new row to the cache */
-    int dec_direct;
-    const void *k_in; const void *v_in; long long kv_stride;
-    const float *q_norm; const float *k_norm; float norm_eps;
 } SkParams;
 
 /* Pre-pass: normalises (optional per-head RMSNorm), rotates and scales Q into

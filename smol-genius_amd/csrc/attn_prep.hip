@@ -285,6 +285,90 @@ __global__ __launch_bounds__(256) void k_norm_rope(float *x, const float *w, flo
     }
 }
 
+/* ------------------------------------------------------- k_bf16_norm_rope */
+
+/* Correctly rounded square root of a finite x >= 0: the hardware square
+ * root is within one ulp, and the neighbour whose square brackets x is
+ * chosen by the sign of the fused residuals x - s'*s (no float lies
+ * between the residual threshold and the true midpoint, so the choice is
+ * exact). Inputs below 2^-96 are scaled by 2^32 first, out of the range
+ * where the hardware flushes. */
+__device__ __forceinline__ float sqrt_rn(float x) {
+    const bool tiny = x < 0x1.0p-96f;
+    const float xs = tiny ? x * 0x1.0p+32f : x;
+    float s = __builtin_amdgcn_sqrtf(xs);
+    const float dn = __int_as_float(__float_as_int(s) - 1), up = __int_as_float(__float_as_int(s) + 1);
+    const float vp = __fmaf_rn(-dn, s, xs), vs = __fmaf_rn(-up, s, xs);
+    if (vp <= 0.0f) s = dn;
+    if (vs > 0.0f) s = up;
+    return tiny ? s * 0x1.0p-16f : s;
+}
+
+/* In place on x [seq][H][hd] bf16 (the bf16 decoder's Q or new K rows):
+ * per-head RMSNorm with weight w (skipped when w is null), then the
+ * interleaved rotation at table row pos0 + s (skipped when cos_t is null),
+ * each result rounded to bf16 by truncation: bf16_rms_norm_per_head and
+ * bf16_apply_rope_interleaved, common/decoder/qkn_bf16_decoder.c:73-91 and
+ * :264-283. The operation order is fixed so that the bits are reproducible:
+ *   ss = fma(v[d], v[d], ss) for d = 0, 1, ... (one thread per head row)
+ *   r  = 1 / sqrt(ss / hd + eps), every step correctly rounded
+ *   v' = trunc((v * r) * w[d])
+ *   x0' = trunc(fma(x0, c, -(x1 * s))), x1' = trunc(fma(x1, c, x0 * s))
+ * with c, s the table entries of column 2i. hd is a multiple of 8. */
+__global__ __launch_bounds__(256) void k_bf16_norm_rope(uint16_t *x, const float *w, float eps, const float *cos_t,
+                                                        const float *sin_t, int pos0, int seq, int H, int hd) {
+    const long long rows = (long long)seq * H;
+    const long long step = (long long)gridDim.x * blockDim.x;
+    for (long long r = (long long)blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += step) {
+        uint4 *row = reinterpret_cast<uint4 *>(x + r * hd);
+        const int n8 = hd >> 3;
+        float ri = 1.0f;
+        if (w) {
+            float ss = 0.0f;
+            for (int c8 = 0; c8 < n8; c8++) {
+                float v[8];
+                unpack_bf16x8(row[c8], v);
+#pragma unroll
+                for (int i = 0; i < 8; i++) ss = __fmaf_rn(v[i], v[i], ss);
+            }
+            ri = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)hd), eps)));
+        }
+        const float *ct = cos_t ? cos_t + (long long)(pos0 + r / H) * hd : nullptr;
+        const float *st = cos_t ? sin_t + (long long)(pos0 + r / H) * hd : nullptr;
+        for (int c8 = 0; c8 < n8; c8++) {
+            float v[8];
+            unpack_bf16x8(row[c8], v);
+            if (w) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] = __uint_as_float(__float_as_uint(__fmul_rn(__fmul_rn(v[i], ri), w[c8 * 8 + i])) & 0xFFFF0000u);
+            }
+            if (ct) {
+#pragma unroll
+                for (int i = 0; i < 8; i += 2) {
+                    const float c = ct[c8 * 8 + i], s = st[c8 * 8 + i];
+                    const float x0 = v[i], x1 = v[i + 1];
+                    v[i] = __fmaf_rn(x0, c, -__fmul_rn(x1, s));
+                    v[i + 1] = __fmaf_rn(x1, c, __fmul_rn(x0, s));
+                }
+            }
+            uint32_t o[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                o[k] = (__float_as_uint(v[2 * k]) >> 16) | (__float_as_uint(v[2 * k + 1]) & 0xFFFF0000u);
+            row[c8] = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+    }
+}
+
+extern "C" int smol_launch_bf16_norm_rope(uint16_t *x, const float *w, float eps, const float *cos_t,
+                                          const float *sin_t, int pos0, int seq, int H, int hd, hipStream_t st) {
+    const long long rows = (long long)seq * H;
+    if (rows <= 0) return 0;
+    const int blocks = (int)std::min<long long>((rows + 255) / 256, 4096);
+    hipLaunchKernelGGL(k_bf16_norm_rope, dim3(blocks), dim3(256), 0, st, x, w, eps, cos_t, sin_t, pos0, seq, H, hd);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
 /* ------------------------------------------------------------ k_to_bf16 */
 
 /* y = the upper 16 bits of x (bf16 by truncation, the f32_to_bf16 of

@@ -1,0 +1,288 @@
+/*
+ * qkn_attn.hip - the reference decoders' attention block on the GPU, keyed by
+ * the decoder context's address (include/smol_qkn_attn.h). Host code only:
+ * it composes the device API of attn_api.hip.
+ *
+ * Per call it does what common/decoder/qkn_decoder.c:460-528 (prefill) and
+ * :625-677 (one decode step) do between the projections and o_proj, and what
+ * common/decoder/qkn_bf16_decoder.c:486-546 / :638-674 do in bf16:
+ *   table  = local-theta table if the layer is sliding and a local table
+ *            exists (:460-468), else the global one
+ *   window = sliding_window if (is_sliding && sliding_window > 0), else none
+ *   cap    = attn_logit_softcap if > 0, else none          (:505-528)
+ * and the four attention entry points become one device call with those
+ * two arguments.
+ */
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include <math.h>
+#include <string.h>
+
+#include "smol_qkn_attn.h"
+
+extern "C" int smol_internal_fail(int code, const char *msg);
+extern "C" int smol_launch_to_bf16_trunc(const float *x, uint16_t *y, long long n, hipStream_t st);
+
+namespace {
+
+int qfail(int code, const char *msg) { return smol_internal_fail(code, msg); }
+
+#define QHIP(expr)                                                                          \
+    do {                                                                                    \
+        hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess) return qfail(SMOL_ATTN_ERR_DEVICE, hipGetErrorString(e_));    \
+    } while (0)
+
+struct Buf {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+struct Binding {
+    smol_qkn_attn_config cfg{};
+    hipStream_t stream = nullptr;
+    smol_attn_ctx *ctx = nullptr;
+    smol_kv_cache *kv = nullptr;
+    smol_rope_table *rope_global = nullptr, *rope_local = nullptr;
+    std::vector<int> sliding;
+    std::vector<float *> q_norm, k_norm; /* device [head_dim] or null */
+    Buf q, k, v, out32, out16;           /* staging */
+};
+
+std::mutex g_mu;
+std::unordered_map<const void *, Binding *> g_bind;
+
+Binding *find(const void *owner) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_bind.find(owner);
+    return it == g_bind.end() ? nullptr : it->second;
+}
+
+/* grows a staging buffer; the binding's stream is drained first, since
+ * earlier work on it may still read the old allocation */
+int reserve(Binding *b, Buf &buf, size_t bytes) {
+    if (bytes <= buf.cap) return 0;
+    size_t want = std::max(bytes, buf.cap * 2);
+    want = (want + 255) & ~(size_t)255;
+    if (buf.p) {
+        QHIP(hipStreamSynchronize(b->stream));
+        QHIP(hipFree(buf.p));
+        buf.p = nullptr;
+        buf.cap = 0;
+    }
+    QHIP(hipMalloc(&buf.p, want));
+    buf.cap = want;
+    return 0;
+}
+
+void release(Binding *b) {
+    if (!b) return;
+    hipSetDevice(b->cfg.device);
+    if (b->stream) hipStreamSynchronize(b->stream);
+    for (float *p : b->q_norm)
+        if (p) hipFree(p);
+    for (float *p : b->k_norm)
+        if (p) hipFree(p);
+    for (Buf *x : {&b->q, &b->k, &b->v, &b->out32, &b->out16})
+        if (x->p) hipFree(x->p);
+    if (b->kv) smol_kv_cache_destroy(b->kv);
+    if (b->rope_global) smol_rope_table_destroy(b->rope_global);
+    if (b->rope_local) smol_rope_table_destroy(b->rope_local);
+    if (b->ctx) smol_attn_ctx_destroy(b->ctx);
+    if (b->stream) hipStreamDestroy(b->stream);
+    delete b;
+}
+
+bool hd_ok(int hd) { return hd == 64 || hd == 72 || hd == 80 || hd == 96 || hd == 128 || hd == 256; }
+
+/* The whole block for seq_len rows at start_pos (decode: one launch of the
+ * direct decode kernel when seq_len == 1 and `decode` is set). */
+int run_block(Binding *b, int layer, int start_pos, int seq_len, const void *q, const void *k, const void *v,
+              void *attn_out, bool decode) {
+    const smol_qkn_attn_config &c = b->cfg;
+    if (layer < 0 || layer >= c.n_layers) return qfail(SMOL_ATTN_ERR_ARG, "layer out of range");
+    if (start_pos < 0 || seq_len <= 0) return qfail(SMOL_ATTN_ERR_ARG, "bad start_pos / seq_len");
+    if (!q || !k || !v || !attn_out) return qfail(SMOL_ATTN_ERR_ARG, "NULL q / k / v / attn_out");
+    QHIP(hipSetDevice(c.device));
+    const int hd = c.head_dim;
+    const size_t es = c.bf16 ? 2 : 4;
+    const size_t q_elems = (size_t)seq_len * c.n_heads * hd, kv_elems = (size_t)seq_len * c.n_kv_heads * hd;
+    const bool sliding = b->sliding[layer] != 0;
+    const smol_rope_table *rope = sliding && b->rope_local ? b->rope_local : b->rope_global;
+    const int window = sliding && c.sliding_window > 0 ? c.sliding_window : 0;
+    const float cap = c.attn_logit_softcap > 0.0f ? c.attn_logit_softcap : 0.0f;
+    const float scale = 1.0f / sqrtf((float)hd);
+    int rc;
+
+    /* device inputs: the caller's arrays when they are on the device and are
+     * only read; staged copies otherwise (the bf16 contract rounds Q and K in
+     * place, and the caller's inputs stay unmodified) */
+    const void *dq = q, *dk = k, *dv = v;
+    const bool copy_qk = !c.on_device || c.bf16;
+    const hipMemcpyKind kind = c.on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+    if (copy_qk) {
+        if ((rc = reserve(b, b->q, q_elems * es)) || (rc = reserve(b, b->k, kv_elems * es))) return rc;
+        QHIP(hipMemcpyAsync(b->q.p, q, q_elems * es, kind, b->stream));
+        QHIP(hipMemcpyAsync(b->k.p, k, kv_elems * es, kind, b->stream));
+        dq = b->q.p;
+        dk = b->k.p;
+    }
+    if (!c.on_device) {
+        if ((rc = reserve(b, b->v, kv_elems * es))) return rc;
+        QHIP(hipMemcpyAsync(b->v.p, v, kv_elems * es, kind, b->stream));
+        dv = b->v.p;
+    }
+    /* the fp32 result: the caller's array when it is a device fp32 array */
+    float *out = nullptr;
+    if (c.bf16 || !c.on_device) {
+        if ((rc = reserve(b, b->out32, q_elems * 4))) return rc;
+        out = (float *)b->out32.p;
+    } else {
+        out = (float *)attn_out;
+    }
+    const float *qn = b->q_norm[layer], *kn = b->k_norm[layer];
+    if (c.bf16) {
+        /* per-head norm + rotation rounded by truncation, then the rows go
+         * into the cache as their bits (no further rounding: bf16 in) */
+        if ((rc = smol_attn_norm_rope_bf16(b->ctx, rope, (uint16_t *)dq, qn, c.eps, start_pos, seq_len, c.n_heads, hd)))
+            return rc;
+        if ((rc = smol_attn_norm_rope_bf16(b->ctx, rope, (uint16_t *)dk, kn, c.eps, start_pos, seq_len, c.n_kv_heads,
+                                           hd)))
+            return rc;
+        if (decode) {
+            const int slot = 0;
+            rc = smol_attn_decode(b->ctx, b->kv, layer, nullptr, 1, &slot, &start_pos, dq, dk, dv, SMOL_ATTN_BF16,
+                                  c.n_heads, scale, window, cap, out);
+        } else {
+            rc = smol_attn_prefill(b->ctx, b->kv, layer, 0, nullptr, start_pos, seq_len, dq, dk, dv, SMOL_ATTN_BF16,
+                                   c.n_heads, scale, window, cap, out);
+        }
+        if (rc) return rc;
+        uint16_t *o16 = (uint16_t *)attn_out;
+        if (!c.on_device) {
+            if ((rc = reserve(b, b->out16, q_elems * 2))) return rc;
+            o16 = (uint16_t *)b->out16.p;
+        }
+        if (smol_launch_to_bf16_trunc(out, o16, (long long)q_elems, b->stream))
+            return qfail(SMOL_ATTN_ERR_DEVICE, "bf16 output conversion failed");
+        if (!c.on_device) QHIP(hipMemcpyAsync(attn_out, o16, q_elems * 2, hipMemcpyDeviceToHost, b->stream));
+    } else {
+        if (decode) {
+            const int slot = 0;
+            rc = smol_attn_decode_qknorm(b->ctx, b->kv, layer, rope, 1, &slot, &start_pos, dq, dk, dv, SMOL_ATTN_F32,
+                                         c.n_heads, scale, window, cap, qn, kn, c.eps, out);
+        } else {
+            rc = smol_attn_prefill_qknorm(b->ctx, b->kv, layer, 0, rope, start_pos, seq_len, dq, dk, dv, SMOL_ATTN_F32,
+                                          c.n_heads, scale, window, cap, qn, kn, c.eps, out);
+        }
+        if (rc) return rc;
+        if (!c.on_device) QHIP(hipMemcpyAsync(attn_out, out, q_elems * 4, hipMemcpyDeviceToHost, b->stream));
+    }
+    QHIP(hipStreamSynchronize(b->stream));
+    return SMOL_ATTN_OK;
+}
+
+}  // namespace
+
+extern "C" int smol_qkn_attn_bind(const void *owner, const smol_qkn_attn_config *cfg) {
+    if (!owner || !cfg) return qfail(SMOL_ATTN_ERR_ARG, "NULL owner / config");
+    const smol_qkn_attn_config &c = *cfg;
+    if (c.n_layers <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads || !hd_ok(c.head_dim) ||
+        c.max_seq <= 0 || !(c.rope_theta > 0.0f) || !(c.eps >= 0.0f))
+        return qfail(SMOL_ATTN_ERR_ARG, "bad decoder config");
+    if (!c.bf16 && c.rope_type != SMOL_ROPE_NEOX && c.rope_type != SMOL_ROPE_INTERLEAVED)
+        return qfail(SMOL_ATTN_ERR_ARG, "rope_type must be SMOL_ROPE_NEOX or SMOL_ROPE_INTERLEAVED");
+    const int n_dev = smol_attn_device_count();
+    if (n_dev < 0) return n_dev;
+    if (c.device < 0 || c.device >= n_dev) return qfail(SMOL_ATTN_ERR_ARG, "device ordinal out of range");
+    smol_qkn_attn_unbind(owner);
+    Binding *b = new Binding();
+    b->cfg = c;
+    b->sliding.assign(c.n_layers, 0);
+    b->q_norm.assign(c.n_layers, nullptr);
+    b->k_norm.assign(c.n_layers, nullptr);
+    int rc = SMOL_ATTN_OK;
+    hipError_t e = hipSetDevice(c.device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) rc = qfail(SMOL_ATTN_ERR_DEVICE, hipGetErrorString(e));
+    if (!rc) rc = smol_attn_ctx_create(c.device, b->stream, &b->ctx);
+    if (!rc) rc = smol_kv_cache_create(b->ctx, c.n_layers, 1, c.n_kv_heads, c.head_dim, c.max_seq, &b->kv);
+    /* the bf16 decoder rotates interleaved pairs whatever rope_type says
+     * (bf16_apply_rope_interleaved, qkn_bf16_decoder.c:522-523) */
+    const int rt = c.bf16 ? SMOL_ROPE_INTERLEAVED : c.rope_type;
+    const int rcap = std::max(1024, c.max_seq);
+    if (!rc) rc = smol_rope_table_create(b->ctx, c.head_dim, c.rope_theta, rt, rcap, &b->rope_global);
+    /* a local table only when its theta differs (qkn_decoder.c:326-337);
+     * the bf16 decoder builds one for any local theta > 0 (:368-370), whose
+     * rows equal the global ones when the thetas are equal */
+    if (!rc && c.rope_local_theta > 0.0f && c.rope_local_theta != c.rope_theta)
+        rc = smol_rope_table_create(b->ctx, c.head_dim, c.rope_local_theta, rt, rcap, &b->rope_local);
+    if (rc) {
+        release(b);
+        return rc;
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_bind[owner] = b;
+    return SMOL_ATTN_OK;
+}
+
+extern "C" int smol_qkn_attn_set_layer(const void *owner, int layer, int is_sliding, const float *q_norm_weight,
+                                       const float *k_norm_weight) {
+    Binding *b = find(owner);
+    if (!b) return qfail(SMOL_ATTN_ERR_ARG, "owner is not bound");
+    if (layer < 0 || layer >= b->cfg.n_layers) return qfail(SMOL_ATTN_ERR_ARG, "layer out of range");
+    QHIP(hipSetDevice(b->cfg.device));
+    QHIP(hipStreamSynchronize(b->stream));
+    b->sliding[layer] = is_sliding ? 1 : 0;
+    const size_t bytes = (size_t)b->cfg.head_dim * sizeof(float);
+    const float *src[2] = {q_norm_weight, k_norm_weight};
+    float **dst[2] = {&b->q_norm[layer], &b->k_norm[layer]};
+    for (int i = 0; i < 2; i++) {
+        if (!src[i]) {
+            if (*dst[i]) QHIP(hipFree(*dst[i]));
+            *dst[i] = nullptr;
+            continue;
+        }
+        if (!*dst[i]) QHIP(hipMalloc((void **)dst[i], bytes));
+        QHIP(hipMemcpy(*dst[i], src[i], bytes, hipMemcpyHostToDevice));
+    }
+    return SMOL_ATTN_OK;
+}
+
+extern "C" int smol_qkn_attn_prefill(const void *owner, int layer, int start_pos, int seq_len, const void *q,
+                                     const void *k, const void *v, void *attn_out) {
+    Binding *b = find(owner);
+    if (!b) return qfail(SMOL_ATTN_ERR_ARG, "owner is not bound");
+    return run_block(b, layer, start_pos, seq_len, q, k, v, attn_out, false);
+}
+
+extern "C" int smol_qkn_attn_forward(const void *owner, int layer, int pos, const void *q, const void *k,
+                                     const void *v, void *attn_out) {
+    Binding *b = find(owner);
+    if (!b) return qfail(SMOL_ATTN_ERR_ARG, "owner is not bound");
+    return run_block(b, layer, pos, 1, q, k, v, attn_out, true);
+}
+
+extern "C" int smol_qkn_attn_read_cache(const void *owner, int layer, int pos0, int n, uint16_t *k_out,
+                                        uint16_t *v_out) {
+    Binding *b = find(owner);
+    if (!b) return qfail(SMOL_ATTN_ERR_ARG, "owner is not bound");
+    return smol_kv_cache_read(b->kv, layer, 0, pos0, n, k_out, v_out);
+}
+
+extern "C" int smol_qkn_attn_unbind(const void *owner) {
+    Binding *b = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_bind.find(owner);
+        if (it == g_bind.end()) return SMOL_ATTN_OK;
+        b = it->second;
+        g_bind.erase(it);
+    }
+    release(b);
+    return SMOL_ATTN_OK;
+}

@@ -71,6 +71,14 @@ SIGNATURES = [
                                  _c_float, _c_int, _c_float, _vp, _vp, _c_float, _vp], _c_int),
     ("smol_attn_apply_rope", [_vp, _vp, _vp, _IP, _c_int, _c_int], _c_int),
     ("smol_attn_norm_rope", [_vp, _vp, _vp, _vp, _c_float, _IP, _c_int, _c_int, _c_int], _c_int),
+    ("smol_attn_norm_rope_bf16", [_vp, _vp, _vp, _vp, _c_float, _c_int, _c_int, _c_int, _c_int], _c_int),
+    # decoder attention block keyed by the decoder context (include/smol_qkn_attn.h)
+    ("smol_qkn_attn_bind", [_vp, _vp], _c_int),
+    ("smol_qkn_attn_set_layer", [_vp, _c_int, _c_int, _FP, _FP], _c_int),
+    ("smol_qkn_attn_prefill", [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp], _c_int),
+    ("smol_qkn_attn_forward", [_vp, _c_int, _c_int, _vp, _vp, _vp, _vp], _c_int),
+    ("smol_qkn_attn_read_cache", [_vp, _c_int, _c_int, _c_int, _U16P, _U16P], _c_int),
+    ("smol_qkn_attn_unbind", [_vp], _c_int),
     # reference-signature drop-ins (host fp32 arrays)
     ("smol_bidirectional_attention", [_FP, _FP, _FP, _FP, _c_int, _c_int, _c_int, _c_float, _IP, _c_int], None),
     ("smol_causal_attention", [_FP, _FP, _FP, _FP, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int], None),
@@ -388,6 +396,93 @@ def norm_rope(ctx, rope, x, weight, eps, positions, n_heads, head_dim):
                                       ctypes.c_float(eps), None if pos is None else pos.ctypes.data_as(_IP), seq,
                                       n_heads, head_dim), "smol_attn_norm_rope")
     return x
+
+
+def norm_rope_bf16(ctx, rope, x, weight, eps, pos0, n_heads, head_dim):
+    """In place on a device bf16 tensor [seq, n_heads*head_dim]: the bf16
+    decoder's truncating per-head norm (weight None: skipped) and interleaved
+    rotation at rows pos0.. (rope None: skipped); see smol_attn_norm_rope_bf16."""
+    _check(load().smol_attn_norm_rope_bf16(ctx.h, rope.h if rope else None, _dev(x, "x"), _norm_w(weight, "weight"),
+                                           ctypes.c_float(eps), pos0, x.shape[0], n_heads, head_dim),
+           "smol_attn_norm_rope_bf16")
+    return x
+
+
+class QknConfig(ctypes.Structure):
+    """smol_qkn_attn_config (include/smol_qkn_attn.h): the qkn_config_t fields of the attention block."""
+    _fields_ = [("n_layers", _c_int), ("n_heads", _c_int), ("n_kv_heads", _c_int), ("head_dim", _c_int),
+                ("eps", _c_float), ("rope_theta", _c_float), ("rope_local_theta", _c_float),
+                ("rope_type", _c_int), ("sliding_window", _c_int), ("attn_logit_softcap", _c_float),
+                ("bf16", _c_int), ("on_device", _c_int), ("device", _c_int), ("max_seq", _c_int)]
+
+
+class QknAttn:
+    """The decoder attention block bound to a decoder context (`owner`, any
+    object whose address keys the registry; a ctypes buffer stands for the
+    qkn_ctx_t). Host numpy arrays in and out when on_device is 0 (fp32, or
+    bf16 bits as uint16 with bf16=1); device tensors when on_device is 1."""
+
+    def __init__(self, owner, **cfg):
+        self.owner = owner
+        self.cfg = QknConfig(**cfg)
+        self.addr = ctypes.c_void_p(ctypes.addressof(owner))
+        _check(load().smol_qkn_attn_bind(self.addr, ctypes.byref(self.cfg)), "smol_qkn_attn_bind")
+        _live.add(self)
+
+    def set_layer(self, layer, is_sliding=0, q_norm=None, k_norm=None):
+        def w(a):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a, np.float32)
+            self._keep = getattr(self, "_keep", []) + [a]
+            return a.ctypes.data_as(_FP)
+        _check(load().smol_qkn_attn_set_layer(self.addr, layer, 1 if is_sliding else 0, w(q_norm), w(k_norm)),
+               "smol_qkn_attn_set_layer")
+
+    def _io(self, q, k, v, rows):
+        c = self.cfg
+        qd, kvd = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
+        if c.on_device:
+            import torch
+            out = torch.empty((rows, qd), dtype=torch.bfloat16 if c.bf16 else torch.float32, device=q.device)
+            return (_dev(q, "q"), _dev(k, "k"), _dev(v, "v"), _dev(out, "attn_out")), out
+        dt = np.uint16 if c.bf16 else np.float32
+        q = np.ascontiguousarray(q, dt).reshape(rows, qd)
+        k = np.ascontiguousarray(k, dt).reshape(rows, kvd)
+        v = np.ascontiguousarray(v, dt).reshape(rows, kvd)
+        out = np.zeros((rows, qd), dt)
+        self._hold = (q, k, v)
+        return tuple(ctypes.c_void_p(a.ctypes.data) for a in (q, k, v, out)), out
+
+    def prefill(self, layer, start_pos, q, k, v):
+        rows = q.shape[0]
+        ptrs, out = self._io(q, k, v, rows)
+        _check(load().smol_qkn_attn_prefill(self.addr, layer, start_pos, rows, *ptrs), "smol_qkn_attn_prefill")
+        return out
+
+    def forward(self, layer, pos, q, k, v):
+        ptrs, out = self._io(q, k, v, 1)
+        _check(load().smol_qkn_attn_forward(self.addr, layer, pos, *ptrs), "smol_qkn_attn_forward")
+        return out
+
+    def read_cache(self, layer, pos0, n):
+        kvd = self.cfg.n_kv_heads * self.cfg.head_dim
+        k = np.zeros((n, kvd), np.uint16)
+        v = np.zeros_like(k)
+        _check(load().smol_qkn_attn_read_cache(self.addr, layer, pos0, n, k.ctypes.data_as(_U16P),
+                                               v.ctypes.data_as(_U16P)), "smol_qkn_attn_read_cache")
+        return k, v
+
+    def close(self):
+        if self.addr:
+            load().smol_qkn_attn_unbind(self.addr)
+            self.addr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 # ----------------------------------------------- reference-signature drop-ins

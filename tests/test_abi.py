@@ -124,3 +124,62 @@ def test_m0_only_written_for_lds_transfers(tmp_path):
             n_dma += 1
             assert ins[i - 1] == "s_nop 0" and ins[i - 2].startswith("s_mov_b32 m0,"), (ins[i - 2], ins[i - 1], l)
     assert n_dma > 0
+
+
+def test_decoder_block_argument_errors_without_device_work():
+    """The decoder-level block rejects an unbound owner and a bad config
+    before any device call; unbinding an unknown owner is not an error."""
+    from smol_genius_amd import smol_attn as sa
+    lib = sa.load()
+    owner = ctypes.create_string_buffer(64)
+    addr = ctypes.c_void_p(ctypes.addressof(owner))
+    assert lib.smol_qkn_attn_prefill(addr, 0, 0, 1, None, None, None, None) == -1
+    assert b"not bound" in lib.smol_attn_last_error()
+    assert lib.smol_qkn_attn_forward(addr, 0, 0, None, None, None, None) == -1
+    assert lib.smol_qkn_attn_set_layer(addr, 0, 0, None, None) == -1
+    assert lib.smol_qkn_attn_unbind(addr) == 0
+    bad = sa.QknConfig(n_layers=2, n_heads=6, n_kv_heads=4, head_dim=128, eps=1e-6, rope_theta=1e6,
+                       rope_type=0, max_seq=64)   # 6 heads over 4 KV heads
+    assert lib.smol_qkn_attn_bind(addr, ctypes.byref(bad)) == -1
+    bad.n_kv_heads, bad.head_dim = 2, 100     # unsupported head_dim
+    assert lib.smol_qkn_attn_bind(addr, ctypes.byref(bad)) == -1
+    bad.head_dim = 128
+    rc = lib.smol_qkn_attn_bind(addr, ctypes.byref(bad))
+    if rc == 0:   # a GPU is present
+        assert lib.smol_qkn_attn_unbind(addr) == 0
+    else:
+        assert rc == -5   # SMOL_ATTN_ERR_NO_GPU
+
+
+REF_KERNELS_H = "/root/reference/common/kernels/smol_kernels.h"
+
+
+@pytest.mark.skipif(not os.path.exists(REF_KERNELS_H), reason="reference tree not present")
+def test_drop_in_header_agrees_with_reference_header(tmp_path):
+    """include/smol_kernels_attn.h and the reference's smol_kernels.h in one
+    C translation unit (the reference header is C only: it has no extern "C"
+    block): a prototype that differs in any parameter or return type is a
+    conflicting redeclaration, which the compiler rejects."""
+    cc, std = "gcc", "-std=c11"
+    src = tmp_path / "tu.c"
+    src.write_text('#include "%s"\n#include "smol_kernels_attn.h"\n#include "smol_qkn_attn.h"\n'
+                   'int main(void) { return 0; }\n' % REF_KERNELS_H)
+    r = subprocess.run([cc, std, "-Wall", "-Werror", "-fsyntax-only", "-I" + INCLUDE, str(src)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    # the check bites: a drifted prototype is rejected
+    bad = tmp_path / "bad.c"
+    bad.write_text('#include "%s"\nvoid smol_causal_attention(float *out, const float *Q, const float *K, '
+                   'const float *V, int seq_q, int seq_k, int n_heads, int n_kv_heads, int head_dim, '
+                   'double scale, int q_offset);\n' % REF_KERNELS_H)
+    r = subprocess.run([cc, std, "-fsyntax-only", str(bad)], capture_output=True, text=True)
+    assert r.returncode != 0
+
+
+@pytest.mark.parametrize("hdr", ["smol_attn.h", "smol_kernels_attn.h", "smol_qkn_attn.h"])
+def test_public_headers_compile_alone_as_c(tmp_path, hdr):
+    src = tmp_path / "one.c"
+    src.write_text('#include "%s"\n' % hdr)
+    r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Wextra", "-Werror", "-pedantic", "-fsyntax-only",
+                        "-I" + INCLUDE, str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr

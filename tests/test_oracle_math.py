@@ -306,3 +306,142 @@ def test_rms_norm_planted_mistakes_are_caught(oracle):
     assert not ok(_norm64(x, np.tile(w, H), seq, 1, H * hd, eps))  # one norm over all heads of a row
     assert not ok(_norm64(x, w[::-1].copy(), seq, H, hd, eps))  # weight reversed
     assert not ok(_norm64(x, np.ones(hd), seq, H, hd, eps))     # weight ignored
+
+
+# ---- the bf16 decoder's truncating norm and rotation (qkn_bf16_decoder.c:73-91, :264-283)
+#
+# Brute force in exact rational arithmetic: every operation of the stated
+# order is computed exactly and rounded once to float32 (round to nearest
+# even), then truncated to bf16, independently of the C restatement.
+
+from fractions import Fraction  # noqa: E402
+import math  # noqa: E402
+
+
+def _f32_round(q):
+    """The float32 nearest to the rational q (ties to even), as a Fraction."""
+    q = Fraction(q)
+    if q == 0:
+        return Fraction(0)
+    sign = -1 if q < 0 else 1
+    a = abs(q)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    e = max(e, -126)
+    scaled = a / Fraction(2) ** (e - 23)
+    m = scaled.numerator // scaled.denominator
+    rem = scaled - m
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and m % 2 == 1):
+        m += 1
+    return sign * Fraction(m) * Fraction(2) ** (e - 23)
+
+
+def _f32_sqrt(x):
+    """Correctly rounded float32 square root of a float32 x >= 0."""
+    r = Fraction(float(np.float32(math.sqrt(float(x)))))
+    best = None
+    for cand in (r, *(Fraction(float(np.nextafter(np.float32(r), np.float32(d)))) for d in (0, np.inf))):
+        err = abs(cand * cand - x)
+        if best is None or err < best[0]:
+            best = (err, cand)
+    return best[1]
+
+
+def _bits(q):
+    return int(np.float32(float(q)).view(np.uint32))
+
+
+def _trunc16(q):
+    return _bits(q) >> 16
+
+
+def _widen16(b):
+    return Fraction(float(np.uint32(int(b) << 16).view(np.float32)))
+
+
+def _bf16_norm_exact(x, w, seq, H, hd, eps):
+    y = np.array(x, np.uint16, copy=True).reshape(seq * H, hd)
+    e = Fraction(float(np.float32(eps)))
+    for r in range(seq * H):
+        v = [_widen16(b) for b in y[r]]
+        ss = Fraction(0)
+        for a in v:
+            ss = _f32_round(a * a + ss)
+        ri = _f32_round(1 / _f32_sqrt(_f32_round(_f32_round(ss / hd) + e)))
+        y[r] = [_trunc16(_f32_round(_f32_round(a * ri) * Fraction(float(w[d])))) for d, a in enumerate(v)]
+    return y.reshape(seq, H * hd)
+
+
+def _bf16_rope_exact(x, c, s, seq, H, hd):
+    y = np.array(x, np.uint16, copy=True).reshape(seq, H, hd)
+    for t in range(seq):
+        for h in range(H):
+            for i in range(hd // 2):
+                x0, x1 = _widen16(y[t, h, 2 * i]), _widen16(y[t, h, 2 * i + 1])
+                cc, sn = Fraction(float(c[t, 2 * i])), Fraction(float(s[t, 2 * i]))
+                p1, p0 = _f32_round(x1 * sn), _f32_round(x0 * sn)
+                y[t, h, 2 * i] = _trunc16(_f32_round(x0 * cc - p1))
+                y[t, h, 2 * i + 1] = _trunc16(_f32_round(x1 * cc + p0))
+    return y.reshape(seq, H * hd)
+
+
+def _bf16_inputs(seed, shape):
+    """bf16 bits over several binades (exponents 2^-6 .. 2^5), both signs"""
+    r = np.random.default_rng(seed)
+    v = r.standard_normal(shape) * np.exp2(r.integers(-6, 6, shape))
+    return synth.f32_to_bf16_bits(v.astype(np.float32))
+
+
+@pytest.mark.parametrize("hd,eps", [(8, 1e-6), (16, 1e-5), (8, 0.25)])
+def test_bf16_norm_brute_force(oracle, hd, eps):
+    seq, H = 3, 2
+    x = _bf16_inputs(70 + hd, (seq, H * hd))
+    w = (1.0 + 0.25 * np.random.default_rng(71).standard_normal(hd)).astype(np.float32)
+    got = oracle.bf16_rms_norm_per_head(x, w, seq, H, hd, eps)
+    np.testing.assert_array_equal(got, _bf16_norm_exact(x, w, seq, H, hd, eps))
+
+
+@pytest.mark.parametrize("hd,theta", [(8, 1e4), (16, 1e6)])
+def test_bf16_rope_brute_force(oracle, hd, theta):
+    seq, H = 4, 3
+    x = _bf16_inputs(80 + hd, (seq, H * hd))
+    c, s = oracle.fill_rope_table(0, 4096, hd, theta, True)
+    pos = np.array([0, 1, 1000, 4095])
+    got = oracle.bf16_apply_rope_interleaved(x, c[pos], s[pos], seq, H, hd)
+    np.testing.assert_array_equal(got, _bf16_rope_exact(x, c[pos], s[pos], seq, H, hd))
+    # position 0 is the identity (cos 1, sin 0): the bits come back unchanged
+    np.testing.assert_array_equal(got[0], x[0])
+
+
+def test_bf16_norm_rope_planted_mistakes_are_caught(oracle):
+    """Rounding to nearest instead of truncating, rotating with the partner
+    swapped and the NeoX pairing all change bits that the restatement keeps.
+    (Fusing or not fusing the first product moves a result by at most one
+    float32 ulp, which survives the truncation to bf16 only rarely: the
+    brute-force tests above pin that choice on their inputs.)"""
+    seq, H, hd = 4, 4, 16
+    x = _bf16_inputs(90, (seq, H * hd))
+    w = np.ones(hd, np.float32)
+    ref = oracle.bf16_rms_norm_per_head(x, w, seq, H, hd, 1e-6)
+    xf = synth.bf16_bits_to_f32(x).reshape(seq * H, hd).astype(np.float64)
+    r = 1.0 / np.sqrt((xf ** 2).mean(-1, keepdims=True) + 1e-6)
+    rne = synth.f32_to_bf16_bits((xf * r).astype(np.float32)).reshape(seq, H * hd)
+    trunc = ((xf * r).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16).reshape(seq, H * hd)
+    assert (rne != ref).any()                                    # rounding to nearest
+    assert np.abs(trunc.astype(np.int32) - ref.astype(np.int32)).max() <= 1   # float64 norm: within one step
+    c, s = oracle.fill_rope_table(0, 2048, hd, 1e4, True)
+    pos = np.array([3, 100, 1500, 2047])
+    rot = oracle.bf16_apply_rope_interleaved(x, c[pos], s[pos], seq, H, hd).reshape(seq, H, hd // 2, 2)
+    xv = synth.bf16_bits_to_f32(x).reshape(seq, H, hd // 2, 2).astype(np.float64)
+    cc, ss = c[pos][:, None, 0::2], s[pos][:, None, 0::2]
+    x0, x1 = xv[..., 0], xv[..., 1]
+    tr = lambda a: (a.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)  # noqa: E731
+    good = np.stack([x0 * cc - x1 * ss, x1 * cc + x0 * ss], -1)
+    assert np.abs(tr(good).astype(np.int32) - rot.astype(np.int32)).max() <= 1
+    assert (synth.f32_to_bf16_bits(good.astype(np.float32)) != rot).any()          # rounding to nearest
+    assert (tr(np.stack([x1 * cc - x0 * ss, x0 * cc + x1 * ss], -1)) != rot).any()  # partner swapped
+    xn = synth.bf16_bits_to_f32(x).reshape(seq, H, 2, hd // 2).astype(np.float64)   # NeoX halves
+    cn, sn = c[pos][:, None, :hd // 2], s[pos][:, None, :hd // 2]
+    neox = np.stack([xn[:, :, 0] * cn - xn[:, :, 1] * sn, xn[:, :, 1] * cn + xn[:, :, 0] * sn], 2)
+    assert (tr(neox).reshape(seq, H, hd // 2, 2) != rot).any()
