@@ -194,6 +194,29 @@ SMOL_ATTN_API int smol_attn_decode_qknorm(smol_attn_ctx *ctx, smol_kv_cache *kv,
                                           int window, float cap, const float *q_norm,
                                           const float *k_norm, float eps, float *out);
 
+/* smol_attn_decode_qknorm for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. Nothing is allocated: the
+ * decode kernel's split partials and flags live in a fixed per-GPU scratch
+ * array of SMOL_ATTN_NOALLOC_SCRATCH_BYTES (held by each GPU the library
+ * runs on until the process ends), the work list rides in the kernel
+ * arguments, the cache and RoPE table do not grow, and kernel timing is not
+ * recorded. Limits (SMOL_ATTN_ERR_UNSUPPORTED / _ARG otherwise): n_seq <= 32;
+ * every pos[i] below the cache's capacity and the table's (reserve / ensure
+ * them beforehand with smol_kv_cache_reserve / smol_rope_table_ensure); a
+ * call whose split partials would not fit the scratch runs unsplit, one
+ * workgroup per (sequence, KV head). All calls on one GPU share its scratch:
+ * calls that overlap in time on one GPU (other streams, other contexts,
+ * other threads) race and must be serialised by the caller. Results equal
+ * smol_attn_decode_qknorm's whenever both split the same way. */
+#define SMOL_ATTN_NOALLOC_SCRATCH_BYTES (16u << 20)
+SMOL_ATTN_API int smol_attn_decode_noalloc(smol_attn_ctx *ctx, smol_kv_cache *kv, int layer,
+                                           const smol_rope_table *rope, int n_seq, const int *slots,
+                                           const int *pos, const void *q, const void *k_new,
+                                           const void *v_new, int dtype, int n_heads, float scale,
+                                           int window, float cap, const float *q_norm,
+                                           const float *k_norm, float eps, float *out);
+
 /* Causal attention on flat device arrays, no cache and no RoPE: the device
  * form of smol_causal_attention (attention.c:153-170). K, V: [seq_k][n_kv*hd]. */
 SMOL_ATTN_API int smol_attn_causal(smol_attn_ctx *ctx, const void *q, const void *k,

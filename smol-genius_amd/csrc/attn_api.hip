@@ -20,6 +20,8 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 #include <numeric>
 #include <queue>
 #include <vector>
@@ -102,6 +104,38 @@ static int dev_reserve(DevBuf &b, size_t bytes, hipStream_t st, bool zero = fals
     HIP_TRY(hipMalloc(&b.p, want));
     if (zero) HIP_TRY(hipMemsetAsync(b.p, 0, want, st));
     b.cap = want;
+    return 0;
+}
+
+/* ------------------------------------------------ no-alloc decode scratch */
+
+/* k_dec's partial slots and flags for smol_attn_decode_noalloc: one copy of
+ * this array per GPU, reserved when the code object loads on that GPU and
+ * held until the process ends. On the host the name only stands for the
+ * symbol and is never used as an address: each device's address comes from
+ * hipGetSymbolAddress, called with that device current, and is kept in
+ * g_scratch. */
+static __device__ __align__(256) float scratch[SMOL_ATTN_NOALLOC_SCRATCH_BYTES / 4];
+
+#define SMOL_MAX_DEVICES 64
+struct ScratchDev {
+    void *ptr = nullptr;               /* this device's copy of `scratch` */
+    std::atomic<unsigned> epoch{0};    /* last epoch handed to a no-alloc call */
+};
+static ScratchDev g_scratch[SMOL_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+/* once per device, with that device current (context creation) */
+static int scratch_setup(int device) {
+    if (device < 0 || device >= SMOL_MAX_DEVICES)
+        return fail(SMOL_ATTN_ERR_UNSUPPORTED, "device ordinal %d (at most %d devices)", device, SMOL_MAX_DEVICES);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch[device].ptr) return 0;
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+        return fail(SMOL_ATTN_ERR_DEVICE, "decode scratch on device %d: %s", device, hipGetErrorString(e));
+    g_scratch[device].ptr = ptr;
     return 0;
 }
 
@@ -272,7 +306,8 @@ extern "C" int smol_attn_ctx_create(int device, void *stream, smol_attn_ctx **ou
         delete c;
         return fail(SMOL_ATTN_ERR_DEVICE, "context: %s", hipGetErrorString(e));
     }
-    int rc = check_xcd_dispatch(c);
+    int rc = scratch_setup(device);
+    if (!rc) rc = check_xcd_dispatch(c);
     if (rc) {
         delete c;
         return rc;
@@ -692,6 +727,8 @@ static int dec_tile_rows(int hd, int rows) { return rows <= 8 ? 8 : rows <= 16 ?
 
 struct DecCall {
     bool direct;                  /* single-token decode, no pre-pass */
+    bool noalloc = false;         /* partials in the per-device scratch; nothing allocated */
+    bool whole = false;           /* one workgroup per (sequence, kv head, row block) */
     std::vector<DecSeq> seqs;
     /* chunk mode: the pre-pass's fresh window and Q scratch */
     int fresh_pos0 = 0, fresh_row0 = 0, fcap = 0;
@@ -720,7 +757,7 @@ static void plan_decode(smol_attn_ctx *ctx, const DecCall &dc, int Hkv, int wind
     for (const DecSeq &q : dc.seqs) total += (long long)slabs_of(q) * Hkv * n_rb;
     const bool forced = ctx->opt[SMOL_OPT_DEC_SLABS] > 0;
     int per_wg = forced ? ctx->opt[SMOL_OPT_DEC_SLABS] : (int)std::max(1LL, (total + ctx->cu_count - 1) / ctx->cu_count);
-    const bool no_split = !ctx->xcd_ok || ctx->opt[SMOL_OPT_DEC_SPLIT] == -1;
+    const bool no_split = !ctx->xcd_ok || ctx->opt[SMOL_OPT_DEC_SPLIT] == -1 || dc.whole;
     struct Unit { int seq, kvh, n_split, xcd; long long cost; };
     std::vector<Unit> units;
     for (;;) {
@@ -785,8 +822,30 @@ static int run_decode(smol_attn_ctx *ctx, const CallShape &cs, const DecCall &dc
     const int nw = rows <= 8 && hd <= 128 ? (ctx->opt[SMOL_OPT_DEC_WAVES] == 8 ? 8 : 4) : 4;
     /* workgroups an XCD holds at once */
     const int fit = std::max(1, ctx->cu_count / ctx->n_xcc) * smol_decode_occupancy(hd, rows, nw);
+    /* partial slots: O [TR][hd], (m, l) [TR][2], the flag; 256-byte aligned */
+    const int slot_floats = (TR * (hd + 2) + 1 + 63) & ~63;
+    const size_t n_groups = dc.seqs.size() * cs.Hkv * n_rb;
+    const size_t part_bytes = n_groups * DEC_MAX_SPLIT * slot_floats * 4;
+    DecCall whole_dc;
+    const DecCall *pdc = &dc;
+    if (dc.noalloc && part_bytes > SMOL_ATTN_NOALLOC_SCRATCH_BYTES) {
+        /* the scratch cannot hold every group's split slots: no splits */
+        whole_dc = dc;
+        whole_dc.whole = true;
+        pdc = &whole_dc;
+    }
     std::vector<DecItem> items;
-    plan_decode(ctx, dc, cs.Hkv, cs.window, n_rb, fit, items);
+    plan_decode(ctx, *pdc, cs.Hkv, cs.window, n_rb, fit, items);
+    if (dc.noalloc && items.size() > DEC_ARG_ITEMS && !pdc->whole) {
+        whole_dc = dc;
+        whole_dc.whole = true;
+        pdc = &whole_dc;
+        plan_decode(ctx, *pdc, cs.Hkv, cs.window, n_rb, fit, items);
+    }
+    if (dc.noalloc && (items.size() > DEC_ARG_ITEMS || dc.seqs.size() > DEC_ARG_SEQS))
+        return fail(SMOL_ATTN_ERR_UNSUPPORTED, "%d sequences / %d workgroups exceed what the no-alloc decode passes "
+                    "in its kernel arguments (%d / %d)", (int)dc.seqs.size(), (int)items.size(), DEC_ARG_SEQS,
+                    DEC_ARG_ITEMS);
 
     static DecParams dp; /* large (kernel arguments of about 3.6 KB): built in place, one thread per context */
     static_assert(sizeof(DecParams) <= 4096, "kernel arguments");
@@ -817,14 +876,23 @@ static int run_decode(smol_attn_ctx *ctx, const CallShape &cs, const DecCall &dc
     dp.out = cs.out; dp.Hq = cs.Hq; dp.Hkv = cs.Hkv; dp.G = G;
     dp.window = cs.window;
     dp.cap2 = cs.cap > 0.0f ? (float)(cs.cap * LOG2E_D) : 0.0f;
-    /* partial slots: O [TR][hd], (m, l) [TR][2], the flag; 256-byte aligned */
-    dp.slot_floats = (TR * (hd + 2) + 1 + 63) & ~63;
-    const size_t n_groups = dc.seqs.size() * cs.Hkv * n_rb;
+    dp.slot_floats = slot_floats;
     int rc;
-    if ((rc = dev_reserve(ctx->dec_part, n_groups * DEC_MAX_SPLIT * dp.slot_floats * 4, ctx->stream, true))) return rc;
-    dp.part = (float *)ctx->dec_part.p;
-    if (++ctx->epoch == 0) ctx->epoch = 1;
-    dp.epoch = ctx->epoch;
+    if (dc.noalloc) {
+        /* the per-device scratch: its flags hold earlier calls' epochs (or
+         * zero), never this call's, which comes from the device's counter */
+        ScratchDev &sd = g_scratch[ctx->device];
+        if (!sd.ptr) return fail(SMOL_ATTN_ERR_DEVICE, "no decode scratch on device %d", ctx->device);
+        dp.part = (float *)sd.ptr;
+        unsigned e = sd.epoch.fetch_add(1) + 1;
+        if (e == 0) e = sd.epoch.fetch_add(1) + 1;
+        dp.epoch = e;
+    } else {
+        if ((rc = dev_reserve(ctx->dec_part, part_bytes, ctx->stream, true))) return rc;
+        dp.part = (float *)ctx->dec_part.p;
+        if (++ctx->epoch == 0) ctx->epoch = 1;
+        dp.epoch = ctx->epoch;
+    }
     dp.n_rb = n_rb;
     dp.n_items = (int)items.size();
     dp.n_seq = (int)dc.seqs.size();
@@ -842,7 +910,7 @@ static int run_decode(smol_attn_ctx *ctx, const CallShape &cs, const DecCall &dc
         if (!items_arg) dp.items_dev = (const DecItem *)ctx->desc.p;
         if (!seqs_arg) dp.seqs_dev = (const DecSeq *)((unsigned char *)ctx->desc.p + o_seq);
     }
-    const int mk = timing_begin(ctx, 1, true);
+    const int mk = dc.noalloc ? -1 : timing_begin(ctx, 1, true);
     hipEvent_t e0 = mk >= 0 ? ctx->marks[mk].a : nullptr, e1 = mk >= 0 ? ctx->marks[mk].b : nullptr;
     rc = smol_launch_decode(&dp, hd, rows, nw, ctx->stream, e0, e1);
     if (rc)
@@ -1144,6 +1212,46 @@ extern "C" int smol_attn_decode_qknorm(smol_attn_ctx *ctx, smol_kv_cache *kv, in
     DecCall dc;
     dc.direct = true;
     for (int i = 0; i < n_seq; i++) dc.seqs.push_back({pos[i], slots[i], i, 1});
+    CallShape cs{true, q, k_new, v_new, dtype, n_heads, Hkv, hd, (long long)n_heads * hd,
+                 (long long)Hkv * hd, scale, cap, window, rope, 1, 1, kv, layer, out, q_norm, k_norm, eps, true};
+    return run_decode(ctx, cs, dc);
+}
+
+extern "C" int smol_attn_decode_noalloc(smol_attn_ctx *ctx, smol_kv_cache *kv, int layer,
+                                        const smol_rope_table *rope, int n_seq, const int *slots,
+                                        const int *pos, const void *q, const void *k_new,
+                                        const void *v_new, int dtype, int n_heads, float scale,
+                                        int window, float cap, const float *q_norm,
+                                        const float *k_norm, float eps, float *out) {
+    if (!kv) return fail(SMOL_ATTN_ERR_ARG, "cache is NULL");
+    int rc = check_common(ctx, dtype, n_heads, kv->n_kv, kv->hd, q, out);
+    if (rc) return rc;
+    if ((rc = check_norm(q_norm, k_norm, eps, n_heads / kv->n_kv))) return rc;
+    if (kv->ctx != ctx) return fail(SMOL_ATTN_ERR_ARG, "cache belongs to another context");
+    if (layer < 0 || layer >= kv->n_layers) return fail(SMOL_ATTN_ERR_ARG, "layer %d out of range", layer);
+    if (n_seq <= 0 || !slots || !pos || !k_new || !v_new) return fail(SMOL_ATTN_ERR_ARG, "bad decode batch");
+    if (n_seq > DEC_ARG_SEQS)
+        return fail(SMOL_ATTN_ERR_UNSUPPORTED, "%d sequences: the no-alloc decode takes at most %d", n_seq,
+                    DEC_ARG_SEQS);
+    if ((rc = check_aligned(k_new, v_new))) return rc;
+    if (rope && rope->ctx != ctx) return fail(SMOL_ATTN_ERR_ARG, "rope table belongs to another context");
+    if (rope && rope->hd != kv->hd) return fail(SMOL_ATTN_ERR_ARG, "rope table head_dim %d != %d", rope->hd, kv->hd);
+    DecCall dc;
+    dc.direct = true;
+    dc.noalloc = true;
+    for (int i = 0; i < n_seq; i++) {
+        if (slots[i] < 0 || slots[i] >= kv->n_slots) return fail(SMOL_ATTN_ERR_ARG, "slot %d out of range", slots[i]);
+        for (int j = 0; j < i; j++)
+            if (slots[j] == slots[i]) return fail(SMOL_ATTN_ERR_ARG, "slot %d appears twice", slots[i]);
+        /* no growth here: the cache and the table must already hold the position */
+        if (pos[i] < 0 || pos[i] >= kv->cap)
+            return fail(SMOL_ATTN_ERR_ARG, "pos %d outside the cache's %d rows (reserve them first)", pos[i], kv->cap);
+        if (rope && pos[i] >= rope->cap)
+            return fail(SMOL_ATTN_ERR_ARG, "pos %d outside the rope table's %d rows (ensure them first)", pos[i],
+                        rope->cap);
+        dc.seqs.push_back({pos[i], slots[i], i, 1});
+    }
+    const int Hkv = kv->n_kv, hd = kv->hd;
     CallShape cs{true, q, k_new, v_new, dtype, n_heads, Hkv, hd, (long long)n_heads * hd,
                  (long long)Hkv * hd, scale, cap, window, rope, 1, 1, kv, layer, out, q_norm, k_norm, eps, true};
     return run_decode(ctx, cs, dc);

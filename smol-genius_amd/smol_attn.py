@@ -69,6 +69,8 @@ SIGNATURES = [
                                   _c_int, _c_float, _c_int, _c_float, _vp, _vp, _c_float, _vp], _c_int),
     ("smol_attn_decode_qknorm", [_vp, _vp, _c_int, _vp, _c_int, _IP, _IP, _vp, _vp, _vp, _c_int, _c_int,
                                  _c_float, _c_int, _c_float, _vp, _vp, _c_float, _vp], _c_int),
+    ("smol_attn_decode_noalloc", [_vp, _vp, _c_int, _vp, _c_int, _IP, _IP, _vp, _vp, _vp, _c_int, _c_int,
+                                  _c_float, _c_int, _c_float, _vp, _vp, _c_float, _vp], _c_int),
     ("smol_attn_apply_rope", [_vp, _vp, _vp, _IP, _c_int, _c_int], _c_int),
     ("smol_attn_norm_rope", [_vp, _vp, _vp, _vp, _c_float, _IP, _c_int, _c_int, _c_int], _c_int),
     ("smol_attn_norm_rope_bf16", [_vp, _vp, _vp, _vp, _c_float, _c_int, _c_int, _c_int, _c_int], _c_int),
