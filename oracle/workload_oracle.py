@@ -5,9 +5,11 @@ Each function follows the reference decoder's order of operations on the
 same input bits: widen bf16 to fp32, build the RoPE table as fill_rope_cache
 does (qkn_decoder.c:276-311), optionally apply the per-head RMSNorm
 (qkn_decoder.c:487-491), rotate Q and the new K in fp32
-(smol_apply_rope_*, qkn_decoder.c:493-495 / :647-649), keep an fp32 cache
+(smol_apply_rope_*, qkn_decoder.c:493-495 / :647-649), append to the cache
 (qkn_decoder.c:498-503 / :651-652), then smol_causal_attention or
-smol_bidirectional_attention (attention.c:32-170).
+smol_bidirectional_attention (attention.c:32-170). The cache is the
+workloads' bf16 cache: a call attends to its own new rows at fp32 and to
+rows written before it as bf16.
 """
 import numpy as np
 
@@ -78,9 +80,17 @@ def bidir(orc: Oracle, wl, x):
                                        wl.scale, wl.window_starts)
 
 
+def _bf16_round(a):
+    """a rounded to bf16 (nearest even) and widened back: what a bf16 cache returns"""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    return _widen(((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16))
+
+
 def stream(orc: Oracle, wl, x):
-    """(chunk_out [chunk, Hq*hd], decode_out [steps, Hq*hd]) with an fp32 cache that
-    grows by the rotated chunk rows and then one rotated row per decode step."""
+    """(chunk_out [chunk, Hq*hd], decode_out [steps, Hq*hd]). The cache is the
+    workload's bf16 cache: each call uses its own new rows at fp32 (as the
+    reference decoder does, qkn_decoder.c:498-528) and the rows appended by
+    earlier calls as stored, rounded to bf16 (nearest even)."""
     P, C = wl.prefix, wl.chunk
     pos = np.arange(P, P + C)
     c, s = rope_rows(orc, pos, wl.hd, wl.theta, False)
@@ -95,6 +105,12 @@ def stream(orc: Oracle, wl, x):
         c, s = rope_rows(orc, np.array([p]), wl.hd, wl.theta, False)
         qd = orc.apply_rope(x["dq"][st:st + 1], c, s, 1, wl.Hq, wl.hd)
         kd = orc.apply_rope(x["dk"][st:st + 1], c, s, 1, wl.Hkv, wl.hd)
+        if st == 0:  # the chunk's rows come back from the bf16 cache
+            K = np.concatenate([K[:P], _bf16_round(K[P:])], 0)
+            V = np.concatenate([V[:P], _bf16_round(V[P:])], 0)
+        else:        # so does the previous step's row
+            K[-1] = _bf16_round(K[-1])
+            V[-1] = _bf16_round(V[-1])
         K = np.concatenate([K, kd], 0)
         V = np.concatenate([V, x["dv"][st:st + 1]], 0)
         dec.append(orc.causal_attention(qd, K, V, 1, p + 1, wl.Hq, wl.Hkv, wl.hd, wl.scale, p))

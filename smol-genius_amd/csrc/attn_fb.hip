@@ -292,10 +292,10 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
         }
     };
 
-    /* Slab j of this group sits in stage j % NSTG. Its transfer is issued at
-     * the top of step j-NSTG (the prologue for j < NSTG) and waited for at the
-     * end of that same step (vmcnt(0)), so it has that step's arithmetic to
-     * land. Step i computes the softmax of slab i, S of slab i+1 and P.V of
+    /* Slab j of this group sits in stage j % NSTG. Its transfer is issued in
+     * the prologue (j < NSTG) or at the top of a step at least two steps
+     * before the step that first reads it, and every transfer is waited for
+     * with vmcnt(0) before a barrier that precedes that read. Step i computes the softmax of slab i, S of slab i+1 and P.V of
      * slab i. The K fragments of slab i+2 and the V^T fragments of slab i+1
      * are read at the top of step i into the second register set, so step
      * i+1 starts from registers. Steps past the group's own slab count (the
@@ -319,26 +319,36 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
      * be in registers first. A transfer of a slab already in L2 can land
      * before LDS reads queued behind the other waves' reads are served. */
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    int st_k = 2 % NSTG, st_v = 1, st_d = 0; /* stages read in a step, stage refilled */
-    auto step = [&](int i, f4 (&scur)[NT][2], f4 (&snext)[NT][2], auto &kcur, auto &knext, auto &vcur, auto &vnext)
-        __attribute__((always_inline)) {
+    int st_k = 2 % NSTG, st_v = 1, st_d = 0; /* stages read in a step, stage of slab i */
+    /* With five stages the transfers go out in pairs: odd step i refills the
+     * stages of slabs i-1 and i (both fully read by then) with slabs
+     * i-1+NSTG and i+NSTG, and the even step after it waits for them
+     * (vmcnt(0)) before its closing barrier. The first of the two is read at
+     * the top of step i+2, after that barrier, so each pair has two steps of
+     * arithmetic to land. With fewer stages every step refills the stage of
+     * its own slab and waits at its end. */
+    constexpr bool PAIRS = NSTG >= 5;
+    auto step = [&](int i, bool odd, f4 (&scur)[NT][2], f4 (&snext)[NT][2], auto &kcur, auto &knext, auto &vcur,
+                    auto &vnext) __attribute__((always_inline)) {
         const bool act = i < n_own;
         h8 pf[NT];
-        /* the next step's LDS reads and the transfer of slab i+NSTG go out
-         * first and proceed during this step's arithmetic, which works from
-         * registers filled before the last barrier */
+        /* the next step's LDS reads and this step's transfers go out first
+         * and proceed during its arithmetic, which works from registers
+         * filled before the last barrier */
         read_k(st_k, knext);
         read_v(st_v, vnext);
-        dma(slab_k(i + NSTG), st_d);
+        if (!PAIRS) {
+            dma(slab_k(i + NSTG), st_d);
+        } else if (odd) {
+            dma(slab_k(i - 1 + NSTG), st_d == 0 ? NSTG - 1 : st_d - 1);
+            dma(slab_k(i + NSTG), st_d);
+        }
         __builtin_amdgcn_sched_barrier(0);
         front(slab_k(i), act, scur);
         qk(kcur, snext);
         expo(scur, pf);
         pv(vcur, pf);
-        /* the only transfers in flight are the ones this step issued at its
-         * top (slab i+NSTG); the step's arithmetic has covered most of their
-         * latency */
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (!PAIRS || !odd) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         st_k = st_k + 1 == NSTG ? 0 : st_k + 1;
         st_v = st_v + 1 == NSTG ? 0 : st_v + 1;
@@ -346,10 +356,10 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     };
     int i = 0;
     for (; i + 2 <= steps; i += 2) {
-        step(i, sa, sb, kfa, kfb, vfa, vfb);
-        step(i + 1, sb, sa, kfb, kfa, vfb, vfa);
+        step(i, false, sa, sb, kfa, kfb, vfa, vfb);
+        step(i + 1, true, sb, sa, kfb, kfa, vfb, vfa);
     }
-    if (i < steps) step(i, sa, sb, kfa, kfb, vfa, vfb);
+    if (i < steps) step(i, false, sa, sb, kfa, kfb, vfa, vfb);
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) l[nt] = MSUM ? lsum[nt][0] : row_sum4(l[nt]);
 

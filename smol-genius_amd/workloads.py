@@ -190,23 +190,24 @@ class Bidir(Workload):
 class Stream(Workload):
     """Chunked prefill of `chunk` tokens on a `prefix`-token cache, then `steps` decode steps."""
 
-    def __init__(self, name, Hq, Hkv, hd, prefix, chunk, steps, theta, seed):
+    def __init__(self, name, Hq, Hkv, hd, prefix, chunk, steps, theta, seed, std=1.0):
         self.name, self.Hq, self.Hkv, self.hd = name, Hq, Hkv, hd
         self.prefix, self.chunk, self.steps, self.theta, self.seed = prefix, chunk, steps, theta, seed
         self.rope_type = ROPE_NEOX
         self.scale = scale_of(hd)
+        self.std = std
 
     def inputs(self):
-        s = self.seed * 100
+        s, sd = self.seed * 100, self.std
         w = self.Hkv * self.hd
-        return dict(cache_k=synth.f32_to_bf16_bits(synth.normal(s + 4, (self.prefix, w))),
-                    cache_v=synth.f32_to_bf16_bits(synth.normal(s + 5, (self.prefix, w))),
-                    q=synth.normal(s + 1, (self.chunk, self.Hq * self.hd)),
-                    k=synth.normal(s + 2, (self.chunk, w)),
-                    v=synth.normal(s + 3, (self.chunk, w)),
-                    dq=synth.normal(s + 6, (self.steps, self.Hq * self.hd)),
-                    dk=synth.normal(s + 7, (self.steps, w)),
-                    dv=synth.normal(s + 8, (self.steps, w)))
+        return dict(cache_k=synth.f32_to_bf16_bits(synth.normal(s + 4, (self.prefix, w), sd)),
+                    cache_v=synth.f32_to_bf16_bits(synth.normal(s + 5, (self.prefix, w), sd)),
+                    q=synth.normal(s + 1, (self.chunk, self.Hq * self.hd), sd),
+                    k=synth.normal(s + 2, (self.chunk, w), sd),
+                    v=synth.normal(s + 3, (self.chunk, w), sd),
+                    dq=synth.normal(s + 6, (self.steps, self.Hq * self.hd), sd),
+                    dk=synth.normal(s + 7, (self.steps, w), sd),
+                    dv=synth.normal(s + 8, (self.steps, w), sd))
 
     def chunk_flops(self):
         return 4 * self.hd * self.Hq * sum(self.prefix + i + 1 for i in range(self.chunk))
