@@ -16,9 +16,12 @@ into the pre-pass) are measured the same way and reported under "detail".
 
 value / ms_per_step: wall clock over the timed steps with nothing but the
 library's own launches in the stream.
-roofline: the attention kernel's own duration, from HIP events recorded
-around each launch on the context's stream in a second pass over the same
-steps; achieved = algorithmic flops (or bytes) per launch / mean kernel time.
+roofline: the attention kernel's own duration, from the HIP events its
+launch records around it (hipExtLaunchKernelGGL) on the context's stream, in
+a second pass over the same steps; achieved = algorithmic flops (or bytes)
+per launch / mean kernel time. profile_kernel_ms / profile_frac repeat the
+figure from the rocprofv3 kernel trace summarised in profiles/, and traffic
+is that summary's HBM bytes per launch.
 cpu_baseline: the reference's own CPU attention (oracle/_ref, compiled from
 the reference sources) on this host's cores, timed on the same workload.
 """
@@ -36,17 +39,27 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 MALL_BYTES = 256 << 20
 
 
-def profiled_traffic(name):
-    """HBM bytes per launch of a kernel, as measured by the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
-    summarised in profiles/<name>.md (None when there is no such summary)."""
-    path = os.path.join(ROOT, "profiles", name + ".md")
+# the kernel each workload's roofline is quoted for (its profiles/<kernel>_<workload>.md summary)
+DOMINANT = {"qwen06b_prefill": "k_attn_fb", "qwen06b_prefill_qknorm": "k_attn_fb", "siglip_bidir": "k_attn_fb",
+            "asr_encoder_bidir": "k_attn_fb", "qwen06b_decode": "k_dec", "qwen06b_decode_qknorm": "k_dec",
+            "gemma_mqa_decode": "k_dec", "qwen06b_decode_x28": "k_dec", "qwen17b_stream": "k_dec"}
+
+
+def profiled(workload):
+    """(kernel mean ns, HBM bytes per launch) of the workload's dominant kernel as measured by
+    rocprofv3 (kernel trace; FETCH_SIZE / WRITE_SIZE passes) and summarised in
+    profiles/<kernel>_<workload>.md; None for what the summary lacks."""
+    path = os.path.join(ROOT, "profiles", "%s_%s.md" % (DOMINANT.get(workload, "k_attn_fb"), workload))
+    ns = traffic = None
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_launch:"):
-                return int(line.split(":")[1])
+                traffic = int(line.split(":")[1])
+            elif line.startswith("kernel_avg_ns:"):
+                ns = float(line.split(":")[1])
     except OSError:
         pass
-    return None
+    return ns, traffic
 
 
 def layers_for(bytes_per_layer, lo=2, hi=64):
@@ -150,6 +163,7 @@ def main():
         prep_ms = kt["prep"][0] / max(1, kt["prep"][1])
         value = flops / (wall / steps) / 1e12
         achieved = flops / (attn_ms * 1e-3) / 1e12
+        prof_ns, traffic = profiled(main_wl.name)
         head = {
             "metric": "prefill attn TFLOP/s (causal, Qwen3-ASR-0.6B 1536 tokens)",
             "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
@@ -159,12 +173,17 @@ def main():
             "config": dict(main_wl.describe(), layers_rotated=n_layers, parallelism="single GPU"),
             "roofline": {"bound": "mfma", "kernel": "k_attn_fb", "achieved": round(achieved, 3),
                          "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_TFLOPS, 5),
-                         "traffic": profiled_traffic("k_attn_fb_qwen06b_prefill"),
-                         "traffic_source": "profiles/k_attn_fb_qwen06b_prefill.md (rocprofv3 FETCH_SIZE x2.0 + "
-                                           "WRITE_SIZE x1.0, copy-calibrated)",
+                         "traffic": traffic,
+                         "traffic_source": "profiles/k_attn_fb_qwen06b_prefill.md (rocprofv3 FETCH_SIZE and "
+                                           "WRITE_SIZE, copy-calibrated)",
                          "kernel_ms": round(attn_ms, 5), "prep_kernel_ms": round(prep_ms, 5),
+                         "kernel_ms_source": "HIP events recorded by the kernel's own launch, live in this run",
                          "flops_per_launch": flops},
         }
+        if prof_ns:
+            pa = flops / (prof_ns * 1e-9) / 1e12
+            head["roofline"].update(profile_kernel_ms=round(prof_ns * 1e-6, 5), profile_achieved=round(pa, 3),
+                                    profile_frac=round(pa / PEAK_MFMA_TFLOPS, 5))
     else:
         head = None
 
@@ -216,6 +235,10 @@ def main():
                      hbm_frac_kernel=round(b / (attn_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 5),
                      GBps_path=round(b / ((attn_ms + prep_ms) * 1e-3) / 1e9, 1),
                      bytes_per_launch=b)
+        pns, ptraffic = profiled(name)
+        if pns:
+            d["profile_kernel_ms"] = round(pns * 1e-6, 5)
+            d["profile_traffic_bytes"] = ptraffic
         if cpu_mod:
             if isinstance(wl, workloads.Decode):
                 d["cpu_baseline"] = cpu_mod.decode_sample(wl, wl.inputs())

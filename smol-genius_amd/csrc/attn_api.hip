@@ -30,13 +30,15 @@
 #include "../../include/smol_kernels_attn.h"
 #include "attn_internal.h"
 
-extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t st);
+extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1);
 extern "C" int smol_launch_decode(const DecParams *dp, int hd, int rows, int nw, hipStream_t st, hipEvent_t ev0,
                                   hipEvent_t ev1);
 extern "C" int smol_launch_xcc_probe(unsigned *out, int n, hipStream_t st);
 extern "C" int smol_decode_occupancy(int hd, int rows, int nw);
-extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st);
-extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st);
+extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st, hipEvent_t ev0,
+                              hipEvent_t ev1);
+extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st, hipEvent_t ev0,
+                              hipEvent_t ev1);
 extern "C" int smol_launch_to_bf16_trunc(const float *x, uint16_t *y, long long n, hipStream_t st);
 extern "C" int smol_launch_bf16_norm_rope(uint16_t *x, const float *w, float eps, const float *cos_t,
                                           const float *sin_t, int pos0, int seq, int H, int hd, hipStream_t st);
@@ -170,7 +172,7 @@ struct smol_attn_ctx {
     int opt[SMOL_OPT_COUNT] = {};
     /* opt-in per-kernel timing: events bracketing each launch */
     bool timing = false;
-    struct Mark { int kind; hipEvent_t a, b; bool recorded; };
+    struct Mark { int kind; hipEvent_t a, b; };
     std::vector<Mark> marks;
     std::vector<hipEvent_t> event_pool;
     double t_ms[SMOL_TIMING_KINDS] = {0, 0, 0};
@@ -188,22 +190,19 @@ static hipEvent_t pool_event(smol_attn_ctx *ctx) {
     return e;
 }
 
-/* start / stop a timed launch of `kind` (no-ops unless timing is enabled).
- * by_launch: the launch records the pair itself (hipExtLaunchKernelGGL with
- * start and stop events, which time the kernel's own execution), so nothing
- * is recorded here */
-static int timing_begin(smol_attn_ctx *ctx, int kind, bool by_launch = false) {
+/* A timed launch of `kind` (-1 unless timing is enabled): the launch itself
+ * records the pair (hipExtLaunchKernelGGL with start and stop events), so the
+ * events bracket the kernel's own execution and nothing else in the stream. */
+static int timing_begin(smol_attn_ctx *ctx, int kind) {
     if (!ctx->timing) return -1;
     hipEvent_t a = pool_event(ctx), b = pool_event(ctx);
     if (!a || !b) return -1;
-    if (!by_launch) hipEventRecord(a, ctx->stream);
-    ctx->marks.push_back({kind, a, b, by_launch});
+    ctx->marks.push_back({kind, a, b});
     return (int)ctx->marks.size() - 1;
 }
 
-static void timing_end(smol_attn_ctx *ctx, int mark) {
-    if (mark >= 0 && !ctx->marks[mark].recorded) hipEventRecord(ctx->marks[mark].b, ctx->stream);
-}
+static hipEvent_t mark_a(smol_attn_ctx *ctx, int mark) { return mark >= 0 ? ctx->marks[mark].a : nullptr; }
+static hipEvent_t mark_b(smol_attn_ctx *ctx, int mark) { return mark >= 0 ? ctx->marks[mark].b : nullptr; }
 
 /* Tables and caches keep their own device and stream, so destroying them
  * does not touch the context (which may already be gone). */
@@ -910,7 +909,7 @@ static int run_decode(smol_attn_ctx *ctx, const CallShape &cs, const DecCall &dc
         if (!items_arg) dp.items_dev = (const DecItem *)ctx->desc.p;
         if (!seqs_arg) dp.seqs_dev = (const DecSeq *)((unsigned char *)ctx->desc.p + o_seq);
     }
-    const int mk = dc.noalloc ? -1 : timing_begin(ctx, 1, true);
+    const int mk = dc.noalloc ? -1 : timing_begin(ctx, 1);
     hipEvent_t e0 = mk >= 0 ? ctx->marks[mk].a : nullptr, e1 = mk >= 0 ? ctx->marks[mk].b : nullptr;
     rc = smol_launch_decode(&dp, hd, rows, nw, ctx->stream, e0, e1);
     if (rc)
@@ -1041,8 +1040,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     /* a call with no pre-pass blocks launches nothing here and records no
      * timing mark */
     int mk = pl.pblk.empty() ? -1 : timing_begin(ctx, 0);
-    rc = smol_launch_prep(&pp, (int)pl.pblk.size(), ctx->stream);
-    timing_end(ctx, mk);
+    rc = smol_launch_prep(&pp, (int)pl.pblk.size(), ctx->stream, mark_a(ctx, mk), mark_b(ctx, mk));
     if (rc)
         return fail(rc == -1 ? SMOL_ATTN_ERR_UNSUPPORTED : SMOL_ATTN_ERR_DEVICE, "k_prep launch (hd %d): %s", hd,
                     rc == -1 ? "unsupported configuration" : hipGetErrorString(hipGetLastError()));
@@ -1079,8 +1077,8 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
         sp.n_wg = fb_wg;
     }
     mk = timing_begin(ctx, 1);
-    rc = fb ? smol_launch_fb(&sp, hd, (int)n_items, nt, ctx->stream) : smol_launch_fa(&sp, hd, (int)n_items, nt, w, ctx->stream);
-    timing_end(ctx, mk);
+    rc = fb ? smol_launch_fb(&sp, hd, (int)n_items, nt, ctx->stream, mark_a(ctx, mk), mark_b(ctx, mk))
+            : smol_launch_fa(&sp, hd, (int)n_items, nt, w, ctx->stream, mark_a(ctx, mk), mark_b(ctx, mk));
     if (rc)
         return fail(rc == -1 ? SMOL_ATTN_ERR_UNSUPPORTED : SMOL_ATTN_ERR_DEVICE,
                     "attention launch (hd %d): %s", hd, hipGetErrorString(hipGetLastError()));
@@ -1366,7 +1364,7 @@ extern "C" int smol_kv_cache_write(smol_kv_cache *kv, int layer, int slot, int p
     pp.cap = kv->cap;
     pp.kf = (_Float16 *)ctx->kf.p; pp.vtf = (_Float16 *)ctx->vtf.p; pp.fcap = (int)fcap;
     pp.blocks = (const PrepBlockB *)ctx->desc.p;
-    rc = smol_launch_prep(&pp, (int)pl.pblk.size(), ctx->stream);
+    rc = smol_launch_prep(&pp, (int)pl.pblk.size(), ctx->stream, nullptr, nullptr);
     if (!on_device) {
         hipStreamSynchronize(ctx->stream);
         hipFree(kd);

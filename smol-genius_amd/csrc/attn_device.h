@@ -14,6 +14,7 @@
 #ifndef SMOL_ATTN_DEVICE_H
 #define SMOL_ATTN_DEVICE_H
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 

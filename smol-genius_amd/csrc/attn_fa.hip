@@ -392,34 +392,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
     merge_group<HD, ROWS>(p, it, b, item, g, tid, reinterpret_cast<float *>(smem));
 }
 
+/* ev0 / ev1 (may be null): events recorded around the kernel alone */
 template <int HD, int NT, int W>
-static void launch_fa_v(const SkParams *sp, dim3 grid, hipStream_t st) {
-    hipLaunchKernelGGL((k_attn_fa<HD, NT, W>), grid, dim3(256), 0, st, *sp);
+static void launch_fa_v(const SkParams *sp, dim3 grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    hipExtLaunchKernelGGL((k_attn_fa<HD, NT, W>), grid, dim3(256), 0, st, ev0, ev1, 0, *sp);
 }
 
 /* w: waves per SIMD the kernel is built for (2 with fewer staged slabs) */
 template <int HD>
-static int launch_fa_hd(const SkParams *sp, int n_items, int nt, int w, hipStream_t st) {
+static int launch_fa_hd(const SkParams *sp, int n_items, int nt, int w, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     const dim3 grid(n_items * sp->Hkv);
-    if (nt == 1 && w == 1) launch_fa_v<HD, 1, 1>(sp, grid, st);
+    if (nt == 1 && w == 1) launch_fa_v<HD, 1, 1>(sp, grid, st, e0, e1);
     else if constexpr (HD <= 128) { /* two tiles or two waves per SIMD fit the registers */
-        if (nt == 1 && w == 2) launch_fa_v<HD, 1, 2>(sp, grid, st);
-        else if (nt == 2 && w == 1) launch_fa_v<HD, 2, 1>(sp, grid, st);
-        else if (nt == 2 && w == 2) launch_fa_v<HD, 2, 2>(sp, grid, st);
+        if (nt == 1 && w == 2) launch_fa_v<HD, 1, 2>(sp, grid, st, e0, e1);
+        else if (nt == 2 && w == 1) launch_fa_v<HD, 2, 1>(sp, grid, st, e0, e1);
+        else if (nt == 2 && w == 2) launch_fa_v<HD, 2, 2>(sp, grid, st, e0, e1);
         else return -1;
     } else return -1;
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st) {
+extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st, hipEvent_t e0,
+                              hipEvent_t e1) {
     if (n_items <= 0) return 0;
     switch (hd) {
-    case 64: return launch_fa_hd<64>(sp, n_items, nt, w, st);
-    case 72: return launch_fa_hd<72>(sp, n_items, nt, w, st);
-    case 80: return launch_fa_hd<80>(sp, n_items, nt, w, st);
-    case 96: return launch_fa_hd<96>(sp, n_items, nt, w, st);
-    case 128: return launch_fa_hd<128>(sp, n_items, nt, w, st);
-    case 256: return launch_fa_hd<256>(sp, n_items, nt, w, st);
+    case 64: return launch_fa_hd<64>(sp, n_items, nt, w, st, e0, e1);
+    case 72: return launch_fa_hd<72>(sp, n_items, nt, w, st, e0, e1);
+    case 80: return launch_fa_hd<80>(sp, n_items, nt, w, st, e0, e1);
+    case 96: return launch_fa_hd<96>(sp, n_items, nt, w, st, e0, e1);
+    case 128: return launch_fa_hd<128>(sp, n_items, nt, w, st, e0, e1);
+    case 256: return launch_fa_hd<256>(sp, n_items, nt, w, st, e0, e1);
     default: return -1;
     }
 }

@@ -405,25 +405,27 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
 }
 
 template <int HD>
-static int launch_fb_hd(const SkParams *sp, int n_items, int nt, hipStream_t st) {
+static int launch_fb_hd(const SkParams *sp, int n_items, int nt, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     const int n_wg = sp->n_wg > 0 ? sp->n_wg : n_items; /* workgroups per kv head: the heads of the lists */
-    if (nt == 1) hipLaunchKernelGGL((k_attn_fb<HD, 1>), dim3(n_wg * sp->Hkv), dim3(512), 0, st, *sp);
-    else if (nt == 2) hipLaunchKernelGGL((k_attn_fb<HD, 2>), dim3(n_wg * sp->Hkv), dim3(256), 0, st, *sp);
+    if (nt == 1) hipExtLaunchKernelGGL((k_attn_fb<HD, 1>), dim3(n_wg * sp->Hkv), dim3(512), 0, st, e0, e1, 0, *sp);
+    else if (nt == 2) hipExtLaunchKernelGGL((k_attn_fb<HD, 2>), dim3(n_wg * sp->Hkv), dim3(256), 0, st, e0, e1, 0, *sp);
     else return -1;
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 /* k_attn_fb: one 64-row tile per item, every key in the fresh buffers; nt
  * row tiles per wave (512 threads for nt 1, 256 for nt 2); sp->n_wg
- * workgroups per kv head (0: one per item) each run their list of items */
-extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st) {
+ * workgroups per kv head (0: one per item) each run their list of items;
+ * e0 / e1 (may be null): events recorded around the kernel alone */
+extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st, hipEvent_t e0,
+                              hipEvent_t e1) {
     if (n_items <= 0) return 0;
     switch (hd) {
-    case 64: return launch_fb_hd<64>(sp, n_items, nt, st);
-    case 72: return launch_fb_hd<72>(sp, n_items, nt, st);
-    case 80: return launch_fb_hd<80>(sp, n_items, nt, st);
-    case 96: return launch_fb_hd<96>(sp, n_items, nt, st);
-    case 128: return launch_fb_hd<128>(sp, n_items, nt, st);
+    case 64: return launch_fb_hd<64>(sp, n_items, nt, st, e0, e1);
+    case 72: return launch_fb_hd<72>(sp, n_items, nt, st, e0, e1);
+    case 80: return launch_fb_hd<80>(sp, n_items, nt, st, e0, e1);
+    case 96: return launch_fb_hd<96>(sp, n_items, nt, st, e0, e1);
+    case 128: return launch_fb_hd<128>(sp, n_items, nt, st, e0, e1);
     default: return -1;
     }
 }

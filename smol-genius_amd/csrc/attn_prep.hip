@@ -407,7 +407,7 @@ extern "C" int smol_launch_norm_rope(float *x, const float *w, float eps, const 
 }
 
 template <int HD>
-static int launch_prep_hd(const PrepParams *pp, dim3 grid, hipStream_t st) {
+static int launch_prep_hd(const PrepParams *pp, dim3 grid, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     /* Q and the new K are rotated together or not at all (the host sets both flags from one table) */
     const int rk = (pp->rope_q && pp->rope_k) ? pp->rope_kind : SMOL_ROPE_OFF;
     /* one input type for Q and the new K/V (the host passes one dtype per call) */
@@ -415,8 +415,9 @@ static int launch_prep_hd(const PrepParams *pp, dim3 grid, hipStream_t st) {
     if (pp->kv_dtype != pp->q_dtype || pp->rope_q != pp->rope_k) return -1;
 #define SMOL_PREP(BF, RK)                                                                        \
     do {                                                                                         \
-        if (pp->q_norm || pp->k_norm) hipLaunchKernelGGL((k_prep<HD, BF, RK, true>), grid, dim3(256), 0, st, *pp); \
-        else hipLaunchKernelGGL((k_prep<HD, BF, RK, false>), grid, dim3(256), 0, st, *pp);      \
+        if (pp->q_norm || pp->k_norm)                                                            \
+            hipExtLaunchKernelGGL((k_prep<HD, BF, RK, true>), grid, dim3(256), 0, st, e0, e1, 0, *pp); \
+        else hipExtLaunchKernelGGL((k_prep<HD, BF, RK, false>), grid, dim3(256), 0, st, e0, e1, 0, *pp); \
     } while (0)
     if (rk == SMOL_ROPE_OFF) { if (bf) SMOL_PREP(true, SMOL_ROPE_OFF); else SMOL_PREP(false, SMOL_ROPE_OFF); }
     else if (rk == SMOL_ROPE_NEOX_K) { if (bf) SMOL_PREP(true, SMOL_ROPE_NEOX_K); else SMOL_PREP(false, SMOL_ROPE_NEOX_K); }
@@ -427,16 +428,17 @@ static int launch_prep_hd(const PrepParams *pp, dim3 grid, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t st) {
+/* e0 / e1 (may be null): events recorded around the kernel alone */
+extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     if (n_blocks <= 0) return 0;
     const dim3 grid(n_blocks * pp->Hkv);
     switch (pp->hd) {
-    case 64: return launch_prep_hd<64>(pp, grid, st);
-    case 72: return launch_prep_hd<72>(pp, grid, st);
-    case 80: return launch_prep_hd<80>(pp, grid, st);
-    case 96: return launch_prep_hd<96>(pp, grid, st);
-    case 128: return launch_prep_hd<128>(pp, grid, st);
-    case 256: return launch_prep_hd<256>(pp, grid, st);
+    case 64: return launch_prep_hd<64>(pp, grid, st, e0, e1);
+    case 72: return launch_prep_hd<72>(pp, grid, st, e0, e1);
+    case 80: return launch_prep_hd<80>(pp, grid, st, e0, e1);
+    case 96: return launch_prep_hd<96>(pp, grid, st, e0, e1);
+    case 128: return launch_prep_hd<128>(pp, grid, st, e0, e1);
+    case 256: return launch_prep_hd<256>(pp, grid, st, e0, e1);
     default: return -1;
     }
 }
