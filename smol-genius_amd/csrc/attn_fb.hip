@@ -29,11 +29,13 @@
  *         slot cb ^ f(r), f(r) = (r & 3) | ((r >> 3) & 3) << 2.
  *   V^T : 16*DT rows of 64 bytes; chunk j of row d sits in slot
  *         j ^ ((d >> 1) & 3).
- * Step i of a group: the softmax front and exponentials of slab i run on
- * the vector ALU next to S = K.Q^T of slab i+1 on the matrix cores, then
- * P.V of slab i, while K of slab i+2 and V^T of slab i+1 are read from LDS;
- * then the transfer the step issued is waited for and one barrier publishes
- * it.
+ * Step i of a group: the softmax of slab i runs on the vector ALU next to
+ * P.V of slab i-1 and S = K.Q^T of slab i+1 on the matrix cores (neither
+ * depends on the softmax, so the two units work at once), while K of slab
+ * i+1 and V^T of slab i are read from LDS; a row whose maximum passes its
+ * threshold takes a rare path at the end of the step; then the transfers
+ * are waited for where the schedule needs them and one barrier publishes
+ * them.
  */
 /* WPG waves per key group, each holding NT 16-row tiles of the 64-row item */
 template <int HD, int WPG>
@@ -56,7 +58,7 @@ struct FbGeom {
  * halves the LDS reads per flop. One MFMA pipe per SIMD is kept busy by a
  * single wave (measured: 16x16x32 f16 MFMAs with independent accumulators
  * issue at the same rate from one wave per SIMD as from two). */
-template <int HD, int NT>
+template <int HD, int NT, bool CAP>
 __global__ __launch_bounds__(NT == 1 ? 512 : 256)
 __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_attn_fb(SkParams p) {
     constexpr int WPG = 4 / NT;
@@ -70,6 +72,7 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = wave / WPG, wg = wave % WPG;
+    const float icap2 = CAP ? 1.0f / p.cap2 : 0.0f;
     const int g = (int)(blockIdx.x % (unsigned)p.Hkv);
     const int w = (int)(blockIdx.x / (unsigned)p.Hkv);
     __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * Gm::GROUP_BYTES];
@@ -166,11 +169,9 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     float m[NT], l[NT], thr[NT];
     f4 negm[NT];
     f4 o[NT][DT];
-    /* the row sums on the matrix cores (one row tile per wave): one more
-     * MFMA per step against a fragment of ones (every element of lsum is the
-     * row's sum of its fp16 probabilities, the same weights the P.V product
-     * uses) instead of seven vector adds */
-    constexpr bool MSUM = HD <= 128 && NT == 1;
+    /* the row sums on the matrix cores: one more MFMA per step against a
+     * fragment of ones (every element of lsum is the row's sum of its fp16
+     * probabilities, the same weights the P.V product uses) */
     f4 lsum[NT];
     h8 ones;
 #pragma unroll
@@ -178,7 +179,6 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         m[nt] = -INFINITY;
-        l[nt] = 0.0f;
         lsum[nt] = f4{0.f, 0.f, 0.f, 0.f};
         thr[nt] = -INFINITY;
         negm[nt] = f4{0.f, 0.f, 0.f, 0.f};
@@ -195,7 +195,6 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
         const uint4 w = *reinterpret_cast<const uint4 *>(gbase + stage * STAGE + off);
         return *reinterpret_cast<const h8 *>(&w);
     };
-    const bool capped = p.cap2 > 0.0f;
     auto read_k = [&](int stage, h8 (&kf)[2][KS]) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < 2; t++)
@@ -206,79 +205,18 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) vf[dt] = lds_h8(stage, vfo + dt * 1024);
     };
-    /* S^T - m = K.Q^T - m (raw S with a softcap) */
+    /* S^T = K.Q^T, less the running max m (raw S with a softcap) */
     auto qk = [&](const h8 (&kf)[2][KS], f4 (&sacc)[NT][2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
-                f4 acc = capped ? f4{0.f, 0.f, 0.f, 0.f} : negm[nt];
+                f4 acc = CAP ? f4{0.f, 0.f, 0.f, 0.f} : negm[nt];
 #pragma unroll
                 for (int ks = 0; ks < KS; ks++)
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t][ks], qf[nt][ks], acc, 0, 0, 0);
                 sacc[nt][t] = acc;
             }
-    };
-    /* softmax front, in place on the scores: softcap, mask, lazy rescale as
-     * in k_attn_fa (lane (c, j) holds keys 8j + 4t + i of row c in s[t][i]) */
-    auto front = [&](int k0, bool act, f4 (&s)[NT][2]) __attribute__((always_inline)) {
-        /* a step past the group's own slabs masks every key, so its
-         * arithmetic adds nothing and needs no branch of its own */
-        const bool full = act && k0 >= lo_max && k0 + SMOL_SLAB <= hi_min;
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            if (capped) {
-#pragma unroll
-                for (int t = 0; t < 2; t++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) s[nt][t][i] = p.cap2 * tanhf(s[nt][t][i] / p.cap2) + negm[nt][0];
-            }
-            if (!full) {
-#pragma unroll
-                for (int t = 0; t < 2; t++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int key = k0 + 8 * j + 4 * t + i;
-                        s[nt][t][i] = (act && key >= lo[nt] && key < hi[nt]) ? s[nt][t][i] : -INFINITY;
-                    }
-            }
-            bool hit = false;
-#pragma unroll
-            for (int t = 0; t < 2; t++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) hit |= s[nt][t][i] > thr[nt];
-            if (__any(hit)) {
-                const float mx = row_max4(fmaxf(fmaxf(fmaxf(s[nt][0][0], s[nt][0][1]), fmaxf(s[nt][0][2], s[nt][0][3])),
-                                                fmaxf(fmaxf(s[nt][1][0], s[nt][1][1]), fmaxf(s[nt][1][2], s[nt][1][3]))));
-                const bool need = mx > thr[nt];
-                const float sh = need ? mx : 0.0f;
-                const float m_new = need ? -negm[nt][0] + mx : m[nt];
-                const float alpha = need ? __builtin_amdgcn_exp2f(m[nt] - m_new) : 1.0f;
-#pragma unroll
-                for (int dt = 0; dt < DT; dt++) o[nt][dt] *= alpha;
-                if constexpr (MSUM) lsum[nt] *= alpha;
-                else l[nt] *= alpha;
-                m[nt] = m_new;
-                const float mu = m_new == -INFINITY ? 0.0f : m_new;
-                negm[nt] = f4{-mu, -mu, -mu, -mu};
-                thr[nt] = m_new == -INFINITY ? -INFINITY : LAZY_T;
-#pragma unroll
-                for (int t = 0; t < 2; t++) s[nt][t] -= sh;
-            }
-        }
-    };
-    /* P = exp2(S - m) as fp16, row sums */
-    auto expo = [&](const f4 (&s)[NT][2], h8 (&pf)[NT]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            float pe[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                pe[e] = __builtin_amdgcn_exp2f(s[nt][e >> 2][e & 3]);
-                pf[nt][e] = (_Float16)pe[e];
-            }
-            if constexpr (!MSUM) l[nt] += ((pe[0] + pe[1]) + (pe[2] + pe[3])) + ((pe[4] + pe[5]) + (pe[6] + pe[7]));
-        }
     };
     auto pv = [&](const h8 (&vf)[DT], const h8 (&pf)[NT]) __attribute__((always_inline)) {
 #pragma unroll
@@ -286,21 +224,97 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
 #pragma unroll
             for (int nt = 0; nt < NT; nt++)
                 o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pf[nt], o[nt][dt], 0, 0, 0);
-        if constexpr (MSUM) {
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++) lsum[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[nt], lsum[nt], 0, 0, 0);
+        for (int nt = 0; nt < NT; nt++) lsum[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[nt], lsum[nt], 0, 0, 0);
+    };
+    /* softcap (raw S -> capped S - m), then the mask of a step that is not
+     * wholly inside every row's key range: lane (c, j) holds keys
+     * 8j + 4t + i of row c in s[t][i] */
+    auto prep_s = [&](int k0, bool act, bool masked, f4 (&s)[NT][2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            if constexpr (CAP) {
+#pragma unroll
+                for (int t = 0; t < 2; t++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) s[nt][t][i] = p.cap2 * tanhf(s[nt][t][i] * icap2) + negm[nt][0];
+            }
+            if (masked) {
+                /* lo <= key < hi as one unsigned compare; a step past the
+                 * group's slabs has an empty range */
+                const unsigned span = act ? (unsigned)hi[nt] - (unsigned)lo[nt] : 0u;
+                const unsigned rel0 = (unsigned)(k0 + 8 * j) - (unsigned)lo[nt];
+#pragma unroll
+                for (int t = 0; t < 2; t++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        s[nt][t][i] = rel0 + (unsigned)(4 * t + i) < span ? s[nt][t][i] : -INFINITY;
+            }
+        }
+    };
+    /* P = exp2(S - m) as fp16, assuming no row's max passes its threshold;
+     * returns whether one does (then the rare path below redoes it) */
+    auto expo = [&](const f4 (&s)[NT][2], h8 (&pf)[NT]) __attribute__((always_inline)) -> bool {
+        bool hit = false;
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                hit |= s[nt][e >> 2][e & 3] > thr[nt];
+                pf[nt][e] = (_Float16)__builtin_amdgcn_exp2f(s[nt][e >> 2][e & 3]);
+            }
+        /* the probabilities are computed here, next to this step's MFMAs,
+         * and not sunk into the branch after it (the rare path redoes them) */
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) asm volatile("" : "+v"(pf[nt]));
+        return __any(hit);
+    };
+    /* Rare path (a row's max passed its threshold): move m to the row max,
+     * redo P, and rescale what was accumulated against the old m: O and the
+     * row sums (after the P.V of the previous slab, issued earlier in the
+     * step) and S of the next slab (computed against the old m). */
+    auto rescale = [&](f4 (&s)[NT][2], h8 (&pf)[NT], f4 (&snext)[NT][2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const float mx = row_max4(fmaxf(fmaxf(fmaxf(s[nt][0][0], s[nt][0][1]), fmaxf(s[nt][0][2], s[nt][0][3])),
+                                            fmaxf(fmaxf(s[nt][1][0], s[nt][1][1]), fmaxf(s[nt][1][2], s[nt][1][3]))));
+            const bool need = mx > thr[nt];
+            const float sh = need ? mx : 0.0f;
+            const float m_new = need ? -negm[nt][0] + mx : m[nt];
+            const float alpha = need ? __builtin_amdgcn_exp2f(m[nt] - m_new) : 1.0f;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) o[nt][dt] *= alpha;
+            lsum[nt] *= alpha;
+            m[nt] = m_new;
+            const float mu = m_new == -INFINITY ? 0.0f : m_new;
+            negm[nt] = f4{-mu, -mu, -mu, -mu};
+            thr[nt] = m_new == -INFINITY ? -INFINITY : LAZY_T;
+#pragma unroll
+            for (int e = 0; e < 8; e++) pf[nt][e] = (_Float16)__builtin_amdgcn_exp2f(s[nt][e >> 2][e & 3] - sh);
+            if constexpr (!CAP) {
+#pragma unroll
+                for (int t = 0; t < 2; t++) snext[nt][t] -= sh;
+            }
         }
     };
 
-    /* Slab j of this group sits in stage j % NSTG. Its transfer is issued in
-     * the prologue (j < NSTG) or at the top of a step at least two steps
-     * before the step that first reads it, and every transfer is waited for
-     * with vmcnt(0) before a barrier that precedes that read. Step i computes the softmax of slab i, S of slab i+1 and P.V of
-     * slab i. The K fragments of slab i+2 and the V^T fragments of slab i+1
-     * are read at the top of step i into the second register set, so step
-     * i+1 starts from registers. Steps past the group's own slab count (the
-     * second group may have one fewer, or none) keep the reads, transfers and
-     * barriers and mask every key. */
+    /* Slab j of this group sits in stage j % NSTG. Step i reads the K
+     * fragments of slab i+1 and the V^T fragments of slab i, and computes
+     * P.V of slab i-1 and S of slab i+1 on the matrix cores next to the
+     * softmax of slab i on the vector ALU: the MFMAs of a step depend on
+     * nothing the step computes, so one wave keeps both units busy. The
+     * stage of slab j is read for the last time in step j. Odd step s
+     * refills the stages of slabs s-2 and s-1 with slabs s+3 and s+4
+     * (step 1: only slab 5, into the stage of slab 0), and the even step
+     * after it waits for them (vmcnt(0)) before its closing barrier; slab
+     * s+3 is first read at the top of step s+2. Every transfer is waited
+     * for with vmcnt(0) before a barrier that precedes the first read of its
+     * stage, and every read of a stage precedes a barrier that precedes its
+     * refill; odd steps need no barrier of their own, so the waves of a
+     * workgroup drift apart by up to a step. Steps past the group's own slab count (the second group may
+     * have one fewer, or none) keep the reads, transfers and barriers and
+     * mask every key. */
+    static_assert(NSTG == 5, "the transfer schedule is built for five stages");
     const int steps = n0;
     /* Every transfer of the prologue (and Q) has landed before the first
      * barrier. Counted waits (all but the last slabs' transfers) are not used
@@ -310,58 +324,53 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     f4 sa[NT][2], sb[NT][2];
-    h8 kfa[2][KS], kfb[2][KS], vfa[DT], vfb[DT];
-    read_k(0, kfa);
-    qk(kfa, sa);
-    read_k(1, kfa);
-    read_v(0, vfa);
-    /* step 0 refills stage 0 with no barrier in between: V^T of slab 0 must
-     * be in registers first. A transfer of a slab already in L2 can land
-     * before LDS reads queued behind the other waves' reads are served. */
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    int st_k = 2 % NSTG, st_v = 1, st_d = 0; /* stages read in a step, stage of slab i */
-    /* With five stages the transfers go out in pairs: odd step i refills the
-     * stages of slabs i-1 and i (both fully read by then) with slabs
-     * i-1+NSTG and i+NSTG, and the even step after it waits for them
-     * (vmcnt(0)) before its closing barrier. The first of the two is read at
-     * the top of step i+2, after that barrier, so each pair has two steps of
-     * arithmetic to land. With fewer stages every step refills the stage of
-     * its own slab and waits at its end. */
-    constexpr bool PAIRS = NSTG >= 5;
-    auto step = [&](int i, bool odd, f4 (&scur)[NT][2], f4 (&snext)[NT][2], auto &kcur, auto &knext, auto &vcur,
-                    auto &vnext) __attribute__((always_inline)) {
+    h8 kf[2][KS], vfa[DT], vfb[DT], pfa[NT], pfb[NT];
+    read_k(0, kf);
+    qk(kf, sa);
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) vfa[dt] = zero_h8();
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) pfa[nt] = zero_h8();
+    int st_k = 1, st_v = 0; /* stages of slabs i+1 and i */
+    auto step = [&](int i, bool odd, f4 (&scur)[NT][2], f4 (&snext)[NT][2], auto &vprev, auto &vnow, auto &pprev,
+                    auto &pnow) __attribute__((always_inline)) {
+        const int k0 = slab_k(i);
         const bool act = i < n_own;
-        h8 pf[NT];
-        /* the next step's LDS reads and this step's transfers go out first
-         * and proceed during its arithmetic, which works from registers
-         * filled before the last barrier */
-        read_k(st_k, knext);
-        read_v(st_v, vnext);
-        if (!PAIRS) {
-            dma(slab_k(i + NSTG), st_d);
-        } else if (odd) {
-            dma(slab_k(i - 1 + NSTG), st_d == 0 ? NSTG - 1 : st_d - 1);
-            dma(slab_k(i + NSTG), st_d);
+        const bool full = act && k0 >= lo_max && k0 + SMOL_SLAB <= hi_min;
+        read_k(st_k, kf);
+        read_v(st_v, vnow);
+        if (odd) {
+            if (i + 3 >= NSTG) dma(slab_k(i + 3), (i + 3) % NSTG);
+            dma(slab_k(i + 4), (i + 4) % NSTG);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        front(slab_k(i), act, scur);
-        qk(kcur, snext);
-        expo(scur, pf);
-        pv(vcur, pf);
-        if (!PAIRS || !odd) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+        prep_s(k0, act, !full, scur);
+        pv(vprev, pprev);
+        const bool hit = expo(scur, pnow);
+        qk(kf, snext);
+        if (hit) rescale(scur, pnow, snext);
+        /* only even steps end in a barrier: the odd step after it overwrites
+         * the stages of slabs i-1 and i, whose last reads (steps i-1 and i)
+         * it orders, and the pair's bytes are published by the next one */
+        if (!odd) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+        }
         st_k = st_k + 1 == NSTG ? 0 : st_k + 1;
         st_v = st_v + 1 == NSTG ? 0 : st_v + 1;
-        st_d = st_d + 1 == NSTG ? 0 : st_d + 1;
     };
     int i = 0;
     for (; i + 2 <= steps; i += 2) {
-        step(i, false, sa, sb, kfa, kfb, vfa, vfb);
-        step(i + 1, true, sb, sa, kfb, kfa, vfb, vfa);
+        step(i, false, sa, sb, vfa, vfb, pfa, pfb);
+        step(i + 1, true, sb, sa, vfb, vfa, pfb, pfa);
     }
-    if (i < steps) step(i, false, sa, sb, kfa, kfb, vfa, vfb);
+    if (i < steps) {
+        step(i, false, sa, sb, vfa, vfb, pfa, pfb);
+        pv(vfb, pfb);
+    } else {
+        pv(vfa, pfa);
+    }
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++) l[nt] = MSUM ? lsum[nt][0] : row_sum4(l[nt]);
+    for (int nt = 0; nt < NT; nt++) l[nt] = lsum[nt][0];
 
     /* merge: group 1 hands its state to group 0 through LDS (lane-wise: the
      * two waves wg of the groups hold the same rows in the same lanes), one
@@ -407,9 +416,15 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
 template <int HD>
 static int launch_fb_hd(const SkParams *sp, int n_items, int nt, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     const int n_wg = sp->n_wg > 0 ? sp->n_wg : n_items; /* workgroups per kv head: the heads of the lists */
-    if (nt == 1) hipExtLaunchKernelGGL((k_attn_fb<HD, 1>), dim3(n_wg * sp->Hkv), dim3(512), 0, st, e0, e1, 0, *sp);
-    else if (nt == 2) hipExtLaunchKernelGGL((k_attn_fb<HD, 2>), dim3(n_wg * sp->Hkv), dim3(256), 0, st, e0, e1, 0, *sp);
-    else return -1;
+    const dim3 grid(n_wg * sp->Hkv);
+    const bool cap = sp->cap2 > 0.0f;
+    if (nt == 1) {
+        if (cap) hipExtLaunchKernelGGL((k_attn_fb<HD, 1, true>), grid, dim3(512), 0, st, e0, e1, 0, *sp);
+        else hipExtLaunchKernelGGL((k_attn_fb<HD, 1, false>), grid, dim3(512), 0, st, e0, e1, 0, *sp);
+    } else if (nt == 2) {
+        if (cap) hipExtLaunchKernelGGL((k_attn_fb<HD, 2, true>), grid, dim3(256), 0, st, e0, e1, 0, *sp);
+        else hipExtLaunchKernelGGL((k_attn_fb<HD, 2, false>), grid, dim3(256), 0, st, e0, e1, 0, *sp);
+    } else return -1;
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
