@@ -130,8 +130,9 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
             dma_1k(d_isk[e] ? rk : rv, d_off[e], so,
                    __builtin_amdgcn_readfirstlane(lds_group + stage * STAGE + (wg + WPG * e) * 1024));
     };
+    /* the prologue stages three slabs; the steps bring the rest in pairs */
 #pragma unroll
-    for (int q = 0; q < NSTG; q++) dma(slab_k(q), q);
+    for (int q = 0; q < 3; q++) dma(slab_k(q), q);
 
     /* rows of this wave (the same in both groups): tile nt holds rows
      * 16 (wg NT + nt) + c of the item */
@@ -303,15 +304,15 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
      * P.V of slab i-1 and S of slab i+1 on the matrix cores next to the
      * softmax of slab i on the vector ALU: the MFMAs of a step depend on
      * nothing the step computes, so one wave keeps both units busy. The
-     * stage of slab j is read for the last time in step j. Odd step s
-     * refills the stages of slabs s-2 and s-1 with slabs s+3 and s+4
-     * (step 1: only slab 5, into the stage of slab 0), and the even step
-     * after it waits for them (vmcnt(0)) before its closing barrier; slab
-     * s+3 is first read at the top of step s+2. Every transfer is waited
-     * for with vmcnt(0) before a barrier that precedes the first read of its
-     * stage, and every read of a stage precedes a barrier that precedes its
-     * refill; odd steps need no barrier of their own, so the waves of a
-     * workgroup drift apart by up to a step. Steps past the group's own slab count (the second group may
+     * prologue stages slabs 0..2. Even step s brings slabs s+3 and s+4 into
+     * the stages of slabs s-2 and s-1 (step 0: the two unused stages), whose
+     * last reads were in steps s-2 and s-1; the odd step after it waits for
+     * them (vmcnt(0)) and ends in a barrier, and slab s+3 is first read at
+     * the top of step s+2. Every transfer is waited for with vmcnt(0) before
+     * a barrier that precedes the first read of its stage, and every read of
+     * a stage precedes a barrier that precedes its refill; even steps need
+     * no barrier of their own, so the waves of a workgroup drift apart by up
+     * to a step. Steps past the group's own slab count (the second group may
      * have one fewer, or none) keep the reads, transfers and barriers and
      * mask every key. */
     static_assert(NSTG == 5, "the transfer schedule is built for five stages");
@@ -339,8 +340,8 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
         const bool full = act && k0 >= lo_max && k0 + SMOL_SLAB <= hi_min;
         read_k(st_k, kf);
         read_v(st_v, vnow);
-        if (odd) {
-            if (i + 3 >= NSTG) dma(slab_k(i + 3), (i + 3) % NSTG);
+        if (!odd) {
+            dma(slab_k(i + 3), (i + 3) % NSTG);
             dma(slab_k(i + 4), (i + 4) % NSTG);
         }
         prep_s(k0, act, !full, scur);
@@ -348,10 +349,10 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
         const bool hit = expo(scur, pnow);
         qk(kf, snext);
         if (hit) rescale(scur, pnow, snext);
-        /* only even steps end in a barrier: the odd step after it overwrites
-         * the stages of slabs i-1 and i, whose last reads (steps i-1 and i)
-         * it orders, and the pair's bytes are published by the next one */
-        if (!odd) {
+        /* only odd steps end in a barrier: it publishes the pair issued by
+         * the step before, and the even step after it refills the stages of
+         * slabs i-1 and i, whose last reads (steps i-1 and i) it orders */
+        if (odd) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
         }
