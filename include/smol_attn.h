@@ -24,7 +24,14 @@
  * Supported head_dim: 64, 72, 80, 96, 128, 256.
  *
  * Numerics: the softmax runs in fp32; the QK^T and PV products run on fp16
- * MFMA operands (bf16 inputs convert exactly; |values| must stay below 65504).
+ * MFMA operands (bf16 inputs convert exactly). Prefill and bidirectional
+ * calls stage Q (times scale * log2 e), K and V as fp16: a staged value that
+ * is not finite or whose magnitude reaches 65520 raises the context's range
+ * flag, and the next smol_attn_ctx_synchronize returns SMOL_ATTN_ERR_RANGE
+ * (the affected outputs are not valid). Single-token decode has no such
+ * limit (its cache operands are bf16, Q is split into bf16 hi + lo, and the
+ * new key is scored in fp32). The reference-signature drop-ins rescale their
+ * inputs by powers of two and repeat the call when the flag is raised.
  * The KV cache stores post-RoPE K and V in bf16 (round to nearest even).
  * Keys written by a call are used by that same call at fp16 precision.
  *
@@ -50,6 +57,7 @@ extern "C" {
 #define SMOL_ATTN_ERR_DEVICE (-3)
 #define SMOL_ATTN_ERR_UNSUPPORTED (-4)
 #define SMOL_ATTN_ERR_NO_GPU (-5)
+#define SMOL_ATTN_ERR_RANGE (-6) /* a value left the fp16 staging's range (see Numerics) */
 
 /* element type of the Q / K / V inputs */
 #define SMOL_ATTN_F32 0
@@ -75,6 +83,8 @@ SMOL_ATTN_API int smol_attn_device_count(void);
  * stream. The context never creates or destroys the stream. */
 SMOL_ATTN_API int smol_attn_ctx_create(int device, void *stream, smol_attn_ctx **out);
 SMOL_ATTN_API int smol_attn_ctx_destroy(smol_attn_ctx *ctx);
+/* waits for the context's stream; returns SMOL_ATTN_ERR_RANGE (and clears
+ * the flag) when a call since the last synchronize raised the range flag */
 SMOL_ATTN_API int smol_attn_ctx_synchronize(smol_attn_ctx *ctx);
 SMOL_ATTN_API void *smol_attn_ctx_stream(smol_attn_ctx *ctx);
 

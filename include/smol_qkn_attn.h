@@ -40,7 +40,11 @@
  * Errors: every function returns SMOL_ATTN_OK or a negative SMOL_ATTN_ERR_*
  * code and leaves a message in smol_attn_last_error(); the decoders map a
  * failure to their existing silent return (qkn_decoder.c:383-389) or
- * sentinel token (:605-611; 1 in qkn_bf16_decoder.c:626-629).
+ * sentinel token (:605-611; 1 in qkn_bf16_decoder.c:626-629). A prefill
+ * whose fp16 staging overflowed (a normed, rotated Q or K value times the
+ * softmax scale, or a V value, at or beyond 65520 in magnitude) returns
+ * SMOL_ATTN_ERR_RANGE; its attn_out is not valid, and the rows it appended
+ * to the cache are.
  *
  * Threading: one binding is used by one thread at a time (the decoders'
  * contexts are single-threaded); the registry itself is thread-safe.

@@ -12,6 +12,8 @@
  */
 #include <hip/hip_runtime.h>
 
+#include <float.h>
+#include <limits.h>
 #include <math.h>
 #include <stdarg.h>
 #include <stdint.h>
@@ -165,6 +167,7 @@ struct smol_attn_ctx {
     DevBuf qs32; /* fp32 Q scratch of the decode kernel */
     DevBuf out32; /* fp32 result of a call whose output is bf16 */
     DevBuf dec_part; /* k_dec partial slots and flags */
+    int *range_flag = nullptr; /* device int, set by kernels when fp16 staging overflows */
     int cu_count = 256;
     int n_xcc = 1;       /* XCDs of the device */
     bool xcd_ok = true;  /* workgroup b runs on XCD b % n_xcc (checked at creation) */
@@ -307,7 +310,13 @@ extern "C" int smol_attn_ctx_create(int device, void *stream, smol_attn_ctx **ou
     }
     int rc = scratch_setup(device);
     if (!rc) rc = check_xcd_dispatch(c);
+    if (!rc) {
+        if (hipMalloc((void **)&c->range_flag, 256) != hipSuccess ||
+            hipMemset(c->range_flag, 0, 256) != hipSuccess)
+            rc = fail(SMOL_ATTN_ERR_NOMEM, "range flag: %s", hipGetErrorString(hipGetLastError()));
+    }
     if (rc) {
+        if (c->range_flag) hipFree(c->range_flag);
         delete c;
         return rc;
     }
@@ -323,6 +332,7 @@ extern "C" int smol_attn_ctx_destroy(smol_attn_ctx *ctx) {
                       &ctx->qs32, &ctx->out32, &ctx->dec_part};
     for (DevBuf *b : bufs)
         if (b->p) hipFree(b->p);
+    if (ctx->range_flag) hipFree(ctx->range_flag);
     for (auto &s : ctx->ring) {
         if (s.h) hipHostFree(s.h);
         if (s.ev) hipEventDestroy(s.ev);
@@ -339,7 +349,16 @@ extern "C" int smol_attn_ctx_destroy(smol_attn_ctx *ctx) {
 
 extern "C" int smol_attn_ctx_synchronize(smol_attn_ctx *ctx) {
     if (!ctx) return fail(SMOL_ATTN_ERR_ARG, "ctx is NULL");
+    HIP_TRY(hipSetDevice(ctx->device));
     HIP_TRY(hipStreamSynchronize(ctx->stream));
+    int flag = 0;
+    HIP_TRY(hipMemcpy(&flag, ctx->range_flag, sizeof(int), hipMemcpyDeviceToHost));
+    if (flag) {
+        const int zero = 0;
+        HIP_TRY(hipMemcpy(ctx->range_flag, &zero, sizeof(int), hipMemcpyHostToDevice));
+        return fail(SMOL_ATTN_ERR_RANGE, "a staged Q, K or V value was not finite or reached 65520 in magnitude "
+                    "(fp16 staging of the prefill and bidirectional kernels)");
+    }
     return SMOL_ATTN_OK;
 }
 
@@ -1037,6 +1056,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     if (cs.dec) pp.qs32 = (float *)ctx->qs32.p;
     pp.blocks = (const PrepBlockB *)(dd + o_pblk);
     pp.q_norm = cs.q_norm; pp.k_norm = cs.k_norm; pp.norm_eps = cs.norm_eps;
+    pp.range_flag = ctx->range_flag;
     /* a call with no pre-pass blocks launches nothing here and records no
      * timing mark */
     int mk = pl.pblk.empty() ? -1 : timing_begin(ctx, 0);
@@ -1068,6 +1088,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     sp.Hq = cs.Hq; sp.Hkv = cs.Hkv; sp.G = G;
     sp.window = cs.window;
     sp.cap2 = cs.cap > 0.0f ? (float)(cs.cap * LOG2E_D) : 0.0f;
+    sp.range_flag = ctx->range_flag;
     sp.items = (const SkItemB *)(dd + o_it);
     sp.part_o = (float *)ctx->part_o.p;
     sp.part_ml = (float *)ctx->part_ml.p;
@@ -1490,10 +1511,69 @@ void legacy_upload(const char *fn, DevBuf &b, const void *h, size_t bytes) {
     if (bytes && hipMemcpyAsync(b.p, h, bytes, hipMemcpyHostToDevice, ctx->stream) != hipSuccess) legacy_abort(fn);
 }
 
-void legacy_download(const char *fn, void *h, const DevBuf &b, size_t bytes) {
+/* copies the result back and waits; returns SMOL_ATTN_OK or
+ * SMOL_ATTN_ERR_RANGE (any other failure aborts) */
+int legacy_download(const char *fn, void *h, const DevBuf &b, size_t bytes) {
     smol_attn_ctx *ctx = legacy_ctx(fn);
     if (bytes && hipMemcpyAsync(h, b.p, bytes, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess) legacy_abort(fn);
-    if (hipStreamSynchronize(ctx->stream) != hipSuccess) legacy_abort(fn);
+    const int rc = smol_attn_ctx_synchronize(ctx);
+    if (rc != SMOL_ATTN_OK && rc != SMOL_ATTN_ERR_RANGE) legacy_abort(fn);
+    return rc;
+}
+
+/* largest |x|; *finite is cleared when a value is NaN or infinite */
+float host_absmax(const float *x, size_t n, bool *finite) {
+    float m = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        const float a = fabsf(x[i]);
+        if (!(a <= FLT_MAX)) *finite = false;
+        else if (a > m) m = a;
+    }
+    return m;
+}
+
+/* smallest e with x < 2^e (x > 0) */
+int pow2_above(float x) {
+    int e;
+    frexpf(x, &e);
+    return e;
+}
+
+/* The drop-ins' answer to a range error of the fp16 staging. The prefill
+ * kernels stage Q * scale * log2 e, K and V as fp16; the same result comes
+ * from Q 2^-a, K 2^a (Q K^T unchanged) and V 2^-b with the output times
+ * 2^b, exactly while the scaled values stay clear of fp16's subnormal and
+ * overflow ranges. This picks a to balance the largest staged |Q| and |K|
+ * (both then below 2^15) and b to bring the largest |V| below 2^15.
+ * Returns 0 with (a, b) set; 1 when an input is not finite (the output
+ * stands as computed: non-finite inputs give non-finite scores in the
+ * reference too); -1 when no such a exists
+ * (max|Q| * scale * log2 e * max|K| >= 2^30). */
+int legacy_range_fix(const float *Q, size_t nq, const float *K, const float *V, size_t nk, float qmul, int *a,
+                     int *b) {
+    bool finite = true;
+    const float mq = host_absmax(Q, nq, &finite) * qmul, mk = host_absmax(K, nk, &finite);
+    const float mv = host_absmax(V, nk, &finite);
+    if (!finite || !(mq <= FLT_MAX)) return 1;
+    const int eq = mq > 0.0f ? pow2_above(mq) : 0, ek = mk > 0.0f ? pow2_above(mk) : 0;
+    const int lo = mq > 0.0f ? eq - 15 : INT_MIN / 2, hi = mk > 0.0f ? 15 - ek : INT_MAX / 2;
+    if (lo > hi) return -1;
+    const int x = (mq > 0.0f && mk > 0.0f) ? (eq - ek) / 2 : 0;
+    *a = std::min(std::max(x, lo), hi);
+    *b = mv > 0.0f ? std::max(0, pow2_above(mv) - 15) : 0;
+    return 0;
+}
+
+std::vector<float> scaled_copy(const float *x, size_t n, int e) {
+    std::vector<float> y(x, x + n);
+    if (e)
+        for (float &v : y) v = ldexpf(v, e);
+    return y;
+}
+
+void scale_out(float *out, size_t n, int e) {
+    if (e)
+        for (size_t i = 0; i < n; i++) out[i] = ldexpf(out[i], e);
 }
 
 /* The four causal variants of attention.c. use_window / use_cap say which
@@ -1520,14 +1600,25 @@ void legacy_causal(const char *fn, float *out, const float *Q, const float *K, c
         cap = 0.0f;
     }
     smol_attn_ctx *ctx = legacy_ctx(fn);
-    legacy_upload(fn, g_legacy.q, Q, qb);
-    legacy_upload(fn, g_legacy.k, K, kb);
-    legacy_upload(fn, g_legacy.v, V, kb);
-    if (dev_reserve(g_legacy.out, qb, ctx->stream)) legacy_abort(fn);
-    if (smol_attn_causal(ctx, g_legacy.q.p, g_legacy.k.p, g_legacy.v.p, SMOL_ATTN_F32, seq_q, seq_k, Hq, Hkv, hd,
-                         scale, q_offset, window, cap, (float *)g_legacy.out.p) != SMOL_ATTN_OK)
-        legacy_abort(fn);
-    legacy_download(fn, out, g_legacy.out, qb);
+    auto run = [&](const float *q, const float *k, const float *v) {
+        legacy_upload(fn, g_legacy.q, q, qb);
+        legacy_upload(fn, g_legacy.k, k, kb);
+        legacy_upload(fn, g_legacy.v, v, kb);
+        if (dev_reserve(g_legacy.out, qb, ctx->stream)) legacy_abort(fn);
+        if (smol_attn_causal(ctx, g_legacy.q.p, g_legacy.k.p, g_legacy.v.p, SMOL_ATTN_F32, seq_q, seq_k, Hq, Hkv, hd,
+                             scale, q_offset, window, cap, (float *)g_legacy.out.p) != SMOL_ATTN_OK)
+            legacy_abort(fn);
+        return legacy_download(fn, out, g_legacy.out, qb);
+    };
+    if (run(Q, K, V) == SMOL_ATTN_OK) return;
+    const size_t nq = qb / 4, nk = kb / 4;
+    int a = 0, b = 0;
+    const int fix = legacy_range_fix(Q, nq, K, V, nk, fabsf(scale) * (float)LOG2E_D, &a, &b);
+    if (fix > 0) return;
+    if (fix < 0) legacy_abort(fn);
+    const std::vector<float> q2 = scaled_copy(Q, nq, -a), k2 = scaled_copy(K, nk, a), v2 = scaled_copy(V, nk, -b);
+    if (run(q2.data(), k2.data(), v2.data()) != SMOL_ATTN_OK) legacy_abort(fn);
+    scale_out(out, nq, b);
 }
 
 }  // namespace
@@ -1568,19 +1659,35 @@ extern "C" void smol_bidirectional_attention(float *out, const float *Q, const f
     if (n_windows <= 0) return;
     const int rows = window_starts[n_windows];
     if (rows <= 0) return;
-    smol_attn_ctx *ctx = legacy_ctx(__func__);
-    const size_t b = (size_t)rows * n_heads * head_dim * 4;
-    legacy_upload(__func__, g_legacy.q, Q, b);
-    legacy_upload(__func__, g_legacy.k, K, b);
-    legacy_upload(__func__, g_legacy.v, V, b);
-    if (dev_reserve(g_legacy.out, b, ctx->stream)) legacy_abort(__func__);
-    /* rows outside every window are left untouched by the reference; keep them */
-    if (hipMemcpyAsync(g_legacy.out.p, out, b, hipMemcpyHostToDevice, ctx->stream) != hipSuccess)
-        legacy_abort(__func__);
-    if (smol_attn_bidirectional(ctx, g_legacy.q.p, g_legacy.k.p, g_legacy.v.p, SMOL_ATTN_F32, rows, n_heads,
-                                head_dim, scale, window_starts, n_windows, (float *)g_legacy.out.p) != SMOL_ATTN_OK)
-        legacy_abort(__func__);
-    legacy_download(__func__, out, g_legacy.out, b);
+    const char *fn = __func__;
+    smol_attn_ctx *ctx = legacy_ctx(fn);
+    const size_t bytes = (size_t)rows * n_heads * head_dim * 4, n = bytes / 4;
+    /* rows outside every window are left untouched by the reference; keep
+     * them (a copy, since a repeated call must start from the same rows) */
+    const std::vector<float> keep(out, out + n);
+    auto run = [&](const float *q, const float *k, const float *v) {
+        legacy_upload(fn, g_legacy.q, q, bytes);
+        legacy_upload(fn, g_legacy.k, k, bytes);
+        legacy_upload(fn, g_legacy.v, v, bytes);
+        legacy_upload(fn, g_legacy.out, keep.data(), bytes);
+        if (smol_attn_bidirectional(ctx, g_legacy.q.p, g_legacy.k.p, g_legacy.v.p, SMOL_ATTN_F32, rows, n_heads,
+                                    head_dim, scale, window_starts, n_windows, (float *)g_legacy.out.p) != SMOL_ATTN_OK)
+            legacy_abort(fn);
+        return legacy_download(fn, out, g_legacy.out, bytes);
+    };
+    if (run(Q, K, V) == SMOL_ATTN_OK) return;
+    int a = 0, b = 0;
+    const int fix = legacy_range_fix(Q, n, K, V, n, fabsf(scale) * (float)LOG2E_D, &a, &b);
+    if (fix > 0) return;
+    if (fix < 0) legacy_abort(fn);
+    const std::vector<float> q2 = scaled_copy(Q, n, -a), k2 = scaled_copy(K, n, a), v2 = scaled_copy(V, n, -b);
+    if (run(q2.data(), k2.data(), v2.data()) != SMOL_ATTN_OK) legacy_abort(fn);
+    /* only the windows' rows were computed with V 2^-b */
+    const size_t row = (size_t)n_heads * head_dim;
+    for (int w = 0; w < n_windows; w++) {
+        const int r0 = std::max(window_starts[w], 0), r1 = std::min(window_starts[w + 1], rows);
+        if (r1 > r0) scale_out(out + (size_t)r0 * row, (size_t)(r1 - r0) * row, b);
+    }
 }
 
 /* rope.c:27-66: the table rows for explicit positions (host, as in the reference) */

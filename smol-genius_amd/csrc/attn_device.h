@@ -100,6 +100,27 @@ __device__ __forceinline__ uint4 pack_bf16x8(const float *v) {
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+/* The fp16 staging's range: a value that is not finite, or whose magnitude
+ * reaches 65520 (which rounds to inf in fp16), raises the context's range
+ * flag (read by smol_attn_ctx_synchronize). One plain store by every lane
+ * that finds one. */
+__device__ __forceinline__ void note_h_range(int *flag, const float *v) {
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 8; i++) bad |= !(fabsf(v[i]) < 65520.0f);
+    if (bad && flag) *flag = 1;
+}
+
+/* the same test on 8 bf16 values as loaded: |x| >= 65536 (the next bf16
+ * above 65280) or not finite */
+__device__ __forceinline__ bool bf16x8_out_of_h_range(uint4 w) {
+    const uint32_t a[4] = {w.x, w.y, w.z, w.w};
+    bool bad = false;
+#pragma unroll
+    for (int k = 0; k < 4; k++) bad |= (a[k] & 0x7FFFu) >= 0x4780u || ((a[k] >> 16) & 0x7FFFu) >= 0x4780u;
+    return bad;
+}
+
 __device__ __forceinline__ uint4 pack_h8(const float *v) {
     h8 h;
 #pragma unroll

@@ -173,6 +173,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
             if (!c_ok[e]) continue;
             uint4 kw = s.k[e], vw = s.v[e];
             if (s.bf) {
+                if (bf16x8_out_of_h_range(kw) || bf16x8_out_of_h_range(vw)) {
+                    if (p.range_flag) *p.range_flag = 1;
+                }
                 const h8 kh = bf16x8_to_h8(kw), vh = bf16x8_to_h8(vw);
                 kw = *reinterpret_cast<const uint4 *>(&kh);
                 vw = *reinterpret_cast<const uint4 *>(&vh);

@@ -104,6 +104,7 @@ typedef struct {
      * follows the items' next links */
     const FbItem *fb_items;
     int n_wg;
+    int *range_flag;           /* k_attn_fa: set to 1 when a cache value widened to fp16 overflows */
 } SkParams;
 
 /* Pre-pass: normalises (optional per-head RMSNorm), rotates and scales Q into
@@ -151,6 +152,7 @@ typedef struct {
     const PrepBlockB *blocks;
     /* per-head RMSNorm before RoPE (null: none): weights [hd] fp32 */
     const float *q_norm; const float *k_norm; float norm_eps;
+    int *range_flag;           /* set to 1 when a value written to fp16 would overflow */
 } PrepParams;
 
 /* ---- k_dec: decode and short chunks, split over the workgroups of one XCD ----

@@ -80,6 +80,7 @@ __device__ __forceinline__ void prep_q(const PrepParams &p, const PrepBlock &blk
                     *reinterpret_cast<float4 *>(p.qs32 + qi[u]) = make_float4(v[0], v[1], v[2], v[3]);
                     *reinterpret_cast<float4 *>(p.qs32 + qi[u] + 4) = make_float4(v[4], v[5], v[6], v[7]);
                 } else {
+                    note_h_range(p.range_flag, v);
                     *reinterpret_cast<uint4 *>(p.qs + qi[u]) = pack_h8(v);
                 }
             }
@@ -160,6 +161,7 @@ __device__ __forceinline__ void prep_fresh(const PrepParams &p, const PrepBlock 
             }
         }
         if (has_cache && is_new) *reinterpret_cast<uint4 *>(kc + (long long)pos * HD + d0) = pack_bf16x8(kv);
+        note_h_range(p.range_flag, kv);
         *reinterpret_cast<uint4 *>(kf + (long long)(frow_base + r) * HD + d0) = pack_h8(kv);
 #pragma unroll
         for (int i = 0; i < 8; i++) sv[r * 257 + d0 + i] = vv[i];
@@ -203,6 +205,7 @@ __device__ __forceinline__ void prep_fresh(const PrepParams &p, const PrepBlock 
                 }
             }
         }
+        note_h_range(p.range_flag, v);
         *reinterpret_cast<uint4 *>(vtf_blk + ci) = pack_h8(v);
     }
 }

@@ -182,8 +182,8 @@ int run_block(Binding *b, int layer, int start_pos, int seq_len, const void *q, 
         if (rc) return rc;
         if (!c.on_device) QHIP(hipMemcpyAsync(attn_out, out, q_elems * 4, hipMemcpyDeviceToHost, b->stream));
     }
-    QHIP(hipStreamSynchronize(b->stream));
-    return SMOL_ATTN_OK;
+    /* waits; SMOL_ATTN_ERR_RANGE when the prefill's fp16 staging overflowed */
+    return smol_attn_ctx_synchronize(b->ctx);
 }
 
 }  // namespace

@@ -116,6 +116,14 @@ class SmolAttnError(RuntimeError):
     pass
 
 
+class SmolAttnRangeError(SmolAttnError):
+    """SMOL_ATTN_ERR_RANGE: a prefill or bidirectional call's fp16 staging
+    overflowed since the last synchronize; those calls' outputs are not valid."""
+
+
+ERR_RANGE = -6  # SMOL_ATTN_ERR_RANGE
+
+
 def load(path=LIB_PATH):
     """The loaded library (ctypes.CDLL). Raises if it has not been built."""
     global _lib
@@ -135,7 +143,8 @@ def load(path=LIB_PATH):
 
 def _check(rc, what):
     if rc != 0:
-        raise SmolAttnError("%s failed (%d): %s" % (what, rc, load().smol_attn_last_error().decode()))
+        cls = SmolAttnRangeError if rc == ERR_RANGE else SmolAttnError
+        raise cls("%s failed (%d): %s" % (what, rc, load().smol_attn_last_error().decode()))
 
 
 def _dtype_code(t):

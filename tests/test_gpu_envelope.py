@@ -131,3 +131,119 @@ def test_stream_envelope(sa, ctx, oracle, wo, sigma):
     want = wo.stream(oracle, wl, x)
     assert_parity(got[0], want[0], "stream chunk s%g" % sigma)
     assert_parity(got[1], want[1], "stream decode s%g" % sigma)
+
+
+# Powers of two that move the inputs out of fp16's range while leaving the
+# attention unchanged in exact arithmetic: Q 2^EQ with K 2^-EQ gives the same
+# logits, V 2^EV gives the output times 2^EV. Every comparison divides the
+# output by 2^EV (exact) and applies the bar of unit-scale data.
+EQ, EV = 20, 17
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+
+
+def test_fp16_range_guard(sa, ctx, oracle):
+    """Device entry points: a staged value beyond fp16 raises the context's
+    range flag, synchronize reports it once, and the next call is clean."""
+    Hq, Hkv, hd, sq = 8, 2, 128, 200
+    Q, K, V = synth.normal(41, (sq, Hq * hd)), synth.normal(42, (sq, Hkv * hd)), synth.normal(43, (sq, Hkv * hd))
+    sc = 1.0 / np.sqrt(hd)
+    want = oracle.causal_attention(Q, K, V, sq, sq, Hq, Hkv, hd, sc, 0)
+    ctx.synchronize()
+    for kernel in (1, 2):
+        ctx.set_option(sa.OPT_PREFILL_KERNEL, kernel)
+        try:
+            for what, q, k, v in (("q", Q * 2.0 ** EQ, K * 2.0 ** -EQ, V), ("v", Q, K, V * 2.0 ** EV),
+                                  ("k", Q * 2.0 ** -EQ, K * 2.0 ** EQ, V)):
+                print("range guard causal kernel", kernel, what, flush=True)
+                sa.causal(ctx, _dev(q), _dev(k), _dev(v), sq, sq, Hq, Hkv, hd, sc, 0)
+                with pytest.raises(sa.SmolAttnRangeError):
+                    ctx.synchronize()
+                ctx.synchronize()
+            got = sa.causal(ctx, _dev(Q), _dev(K), _dev(V), sq, sq, Hq, Hkv, hd, sc, 0).cpu().numpy()
+            ctx.synchronize()
+            assert_parity(got, want, "after the range error, kernel %d" % kernel)
+        finally:
+            ctx.set_option(sa.OPT_PREFILL_KERNEL, 0)
+
+    print("range guard bidirectional", flush=True)
+    H, seq = 4, 160
+    Qb, Kb, Vb = (synth.normal(44 + i, (seq, H * hd)) for i in range(3))
+    sa.bidirectional(ctx, _dev(Qb), _dev(Kb), _dev(Vb * 2.0 ** EV), seq, H, hd, sc, [0, 64, 160])
+    with pytest.raises(sa.SmolAttnRangeError):
+        ctx.synchronize()
+
+    # a cached prefix widened from bf16 to fp16 inside k_attn_fa
+    print("range guard cached prefix", flush=True)
+    pre, n = 300, 200
+    kv = sa.KVCache(ctx, 1, 1, Hkv, hd, pre + n)
+    try:
+        Kc, Vc = synth.normal(47, (pre, Hkv * hd)), synth.normal(48, (pre, Hkv * hd))
+        Kc[7, 5] = 2.0 ** EV
+        kv.write(0, 0, 0, Kc, Vc)
+        sa.prefill(ctx, kv, 0, 0, None, pre, _dev(Q), _dev(K), _dev(V), Hq, sc)
+        with pytest.raises(sa.SmolAttnRangeError):
+            ctx.synchronize()
+    finally:
+        kv.close()
+    ctx.synchronize()
+
+
+def test_fp16_range_reference_signatures(sa, oracle):
+    """The reference-signature drop-ins rescale by powers of two and repeat
+    the call: their results for out-of-range inputs equal those of the
+    unit-scale inputs."""
+    Hq, Hkv, hd, sq, sk = 8, 2, 128, 120, 260
+    Q, K, V = synth.normal(51, (sq, Hq * hd)), synth.normal(52, (sk, Hkv * hd)), synth.normal(53, (sk, Hkv * hd))
+    sc = 1.0 / np.sqrt(hd)
+    for eq in (EQ, -EQ):
+        for ev in (0, EV):
+            print("range drop-in causal", eq, ev, flush=True)
+            out = np.full((sq, Hq * hd), np.nan, np.float32)
+            sa.smol_causal_attention(out, Q * 2.0 ** eq, K * 2.0 ** -eq, V * 2.0 ** ev, sq, sk, Hq, Hkv, hd, sc,
+                                     sk - sq)
+            want = oracle.causal_attention(Q, K, V, sq, sk, Hq, Hkv, hd, sc, sk - sq)
+            assert_parity(out / 2.0 ** ev, want, "causal drop-in q2^%d v2^%d" % (eq, ev))
+    print("range drop-in softcap window", flush=True)
+    out = np.full((sq, Hq * hd), np.nan, np.float32)
+    sa.smol_sliding_window_attention_softcap(out, Q * 2.0 ** EQ, K * 2.0 ** -EQ, V * 2.0 ** EV, sq, sk, Hq, Hkv, hd,
+                                             sc, sk - sq, 96, 30.0)
+    want = oracle.causal_attention(Q, K, V, sq, sk, Hq, Hkv, hd, sc, sk - sq, window=96, cap=30.0)
+    assert_parity(out / 2.0 ** EV, want, "softcap window drop-in")
+
+    print("range drop-in bidirectional", flush=True)
+    H, seq = 4, 160
+    ws = [30, 100, 160]
+    Qb, Kb, Vb = (synth.normal(54 + i, (seq, H * hd)) for i in range(3))
+    init = synth.normal(57, (seq, H * hd)).astype(np.float32)
+    out = init.copy()
+    sa.smol_bidirectional_attention(out, Qb * 2.0 ** EQ, Kb * 2.0 ** -EQ, Vb * 2.0 ** EV, seq, H, hd, sc, ws, 2)
+    want = oracle.bidirectional_attention(Qb, Kb, Vb, seq, H, hd, sc, ws)
+    np.testing.assert_array_equal(out[:30], init[:30])
+    assert_parity(out[30:] / 2.0 ** EV, want[30:], "bidirectional drop-in")
+
+
+def test_decode_full_range(sa, ctx, oracle, wo):
+    """Single-token decode stages nothing in fp16: the scaled inputs raise no
+    range error and give the unit-scale result times 2^EV."""
+    from smol_genius_amd.workloads import Decode
+    wl = Decode("range", 16, 8, 128, [1025, 300], 1e6, 0, seed=35)
+    x = wl.inputs()
+    want = wo.decode(oracle, wl, x)
+    s = dict(q=2.0 ** EQ, k=2.0 ** -EQ, cache_k=2.0 ** -EQ, v=2.0 ** EV, cache_v=2.0 ** EV)
+    kv = sa.KVCache(ctx, 1, wl.n_seq, wl.Hkv, wl.hd, max(wl.lengths))
+    rope = sa.RopeTable(ctx, wl.hd, wl.theta, wl.rope_type, max(wl.lengths))
+    try:
+        for i in range(wl.n_seq):
+            kv.write(0, i, 0, synth.bf16_bits_to_f32(x["cache_k"][i]) * s["cache_k"],
+                     synth.bf16_bits_to_f32(x["cache_v"][i]) * s["cache_v"])
+        out = sa.decode(ctx, kv, 0, rope, np.arange(wl.n_seq), wl.positions, _dev(x["q"] * s["q"]),
+                        _dev(x["k"] * s["k"]), _dev(x["v"] * s["v"]), wl.Hq, wl.scale)
+        got = out.cpu().numpy()
+        ctx.synchronize()
+    finally:
+        kv.close()
+        rope.close()
+    assert_parity(got / 2.0 ** EV, want, "decode q2^%d v2^%d" % (EQ, EV))
