@@ -15,7 +15,11 @@
  * arrays through device memory; the device-resident API in smol_attn.h avoids
  * the copies. The reference returns void and has no error channel: on a
  * device error these functions print the error to stderr and abort(), rather
- * than return unwritten output.
+ * than return unwritten output. The attention functions take any head_dim
+ * up to 256 (the kernels' sizes 64, 72, 80, 96, 128, 256 run directly; the
+ * others run zero-padded to the next of them) and abort above 256. Inputs
+ * beyond the kernels' fp16 staging range are rescaled by powers of two and
+ * the call repeated (smol_attn.h, Numerics).
  */
 #ifndef SMOL_KERNELS_ATTN_H
 #define SMOL_KERNELS_ATTN_H

@@ -1521,6 +1521,39 @@ int legacy_download(const char *fn, void *h, const DevBuf &b, size_t bytes) {
     return rc;
 }
 
+/* The attention kernels take head_dim 64, 72, 80, 96, 128 and 256; the
+ * reference takes any (attention.c:79-126). A drop-in call with another
+ * head_dim up to 256 runs at the next supported one with every head row
+ * zero-padded: the zero columns add nothing to Q K^T (the caller's scale is
+ * passed as given) and the output's padded columns are dropped. */
+int padded_hd(int hd) {
+    for (int h : {64, 72, 80, 96, 128, 256})
+        if (hd <= h) return h;
+    return 0;
+}
+
+/* rows of hd floats into device rows of hdp floats (the padding zeroed) */
+void legacy_upload_rows(const char *fn, DevBuf &b, const float *h, size_t rows, int hd, int hdp) {
+    if (hd == hdp) return legacy_upload(fn, b, h, rows * hd * 4);
+    smol_attn_ctx *ctx = legacy_ctx(fn);
+    const size_t bytes = rows * hdp * 4;
+    if (dev_reserve(b, std::max<size_t>(bytes, 4), ctx->stream)) legacy_abort(fn);
+    if (!rows) return;
+    if (hipMemsetAsync(b.p, 0, bytes, ctx->stream) != hipSuccess ||
+        hipMemcpy2DAsync(b.p, (size_t)hdp * 4, h, (size_t)hd * 4, (size_t)hd * 4, rows, hipMemcpyHostToDevice,
+                         ctx->stream) != hipSuccess)
+        legacy_abort(fn);
+}
+
+int legacy_download_rows(const char *fn, float *h, const DevBuf &b, size_t rows, int hd, int hdp) {
+    if (hd == hdp) return legacy_download(fn, h, b, rows * hd * 4);
+    smol_attn_ctx *ctx = legacy_ctx(fn);
+    if (rows && hipMemcpy2DAsync(h, (size_t)hd * 4, b.p, (size_t)hdp * 4, (size_t)hd * 4, rows,
+                                 hipMemcpyDeviceToHost, ctx->stream) != hipSuccess)
+        legacy_abort(fn);
+    return legacy_download(fn, nullptr, b, 0);
+}
+
 /* largest |x|; *finite is cleared when a value is NaN or infinite */
 float host_absmax(const float *x, size_t n, bool *finite) {
     float m = 0.0f;
@@ -1586,7 +1619,7 @@ void scale_out(float *out, size_t n, int e) {
 void legacy_causal(const char *fn, float *out, const float *Q, const float *K, const float *V, int seq_q,
                    int seq_k, int Hq, int Hkv, int hd, float scale, int q_offset, bool use_window, int window,
                    bool use_cap, float cap) {
-    if (seq_q <= 0) return;
+    if (seq_q <= 0 || Hq <= 0 || hd <= 0) return; /* no output elements */
     const size_t qb = (size_t)seq_q * Hq * hd * 4, kb = (size_t)std::max(seq_k, 0) * Hkv * hd * 4;
     if (use_window && window <= 0) {
         memset(out, 0, qb);
@@ -1600,15 +1633,21 @@ void legacy_causal(const char *fn, float *out, const float *Q, const float *K, c
         cap = 0.0f;
     }
     smol_attn_ctx *ctx = legacy_ctx(fn);
+    const int hdp = padded_hd(hd);
+    if (!hdp) {
+        fail(SMOL_ATTN_ERR_UNSUPPORTED, "head_dim %d (at most 256)", hd);
+        legacy_abort(fn);
+    }
+    const size_t q_rows = (size_t)seq_q * Hq, k_rows = (size_t)std::max(seq_k, 0) * Hkv;
     auto run = [&](const float *q, const float *k, const float *v) {
-        legacy_upload(fn, g_legacy.q, q, qb);
-        legacy_upload(fn, g_legacy.k, k, kb);
-        legacy_upload(fn, g_legacy.v, v, kb);
-        if (dev_reserve(g_legacy.out, qb, ctx->stream)) legacy_abort(fn);
-        if (smol_attn_causal(ctx, g_legacy.q.p, g_legacy.k.p, g_legacy.v.p, SMOL_ATTN_F32, seq_q, seq_k, Hq, Hkv, hd,
-                             scale, q_offset, window, cap, (float *)g_legacy.out.p) != SMOL_ATTN_OK)
+        legacy_upload_rows(fn, g_legacy.q, q, q_rows, hd, hdp);
+        legacy_upload_rows(fn, g_legacy.k, k, k_rows, hd, hdp);
+        legacy_upload_rows(fn, g_legacy.v, v, k_rows, hd, hdp);
+        if (dev_reserve(g_legacy.out, q_rows * hdp * 4, ctx->stream)) legacy_abort(fn);
+        if (smol_attn_causal(ctx, g_legacy.q.p, g_legacy.k.p, g_legacy.v.p, SMOL_ATTN_F32, seq_q, seq_k, Hq, Hkv,
+                             hdp, scale, q_offset, window, cap, (float *)g_legacy.out.p) != SMOL_ATTN_OK)
             legacy_abort(fn);
-        return legacy_download(fn, out, g_legacy.out, qb);
+        return legacy_download_rows(fn, out, g_legacy.out, q_rows, hd, hdp);
     };
     if (run(Q, K, V) == SMOL_ATTN_OK) return;
     const size_t nq = qb / 4, nk = kb / 4;
@@ -1656,24 +1695,29 @@ extern "C" void smol_bidirectional_attention(float *out, const float *Q, const f
                                              int n_heads, int head_dim, float scale, const int *window_starts,
                                              int n_windows) {
     (void)seq; /* unused by the reference too (attention.c:33); the windows define the rows */
-    if (n_windows <= 0) return;
+    if (n_windows <= 0 || n_heads <= 0 || head_dim <= 0) return;
     const int rows = window_starts[n_windows];
     if (rows <= 0) return;
     const char *fn = __func__;
     smol_attn_ctx *ctx = legacy_ctx(fn);
-    const size_t bytes = (size_t)rows * n_heads * head_dim * 4, n = bytes / 4;
+    const int hdp = padded_hd(head_dim);
+    if (!hdp) {
+        fail(SMOL_ATTN_ERR_UNSUPPORTED, "head_dim %d (at most 256)", head_dim);
+        legacy_abort(fn);
+    }
+    const size_t hrows = (size_t)rows * n_heads, n = hrows * head_dim;
     /* rows outside every window are left untouched by the reference; keep
      * them (a copy, since a repeated call must start from the same rows) */
     const std::vector<float> keep(out, out + n);
     auto run = [&](const float *q, const float *k, const float *v) {
-        legacy_upload(fn, g_legacy.q, q, bytes);
-        legacy_upload(fn, g_legacy.k, k, bytes);
-        legacy_upload(fn, g_legacy.v, v, bytes);
-        legacy_upload(fn, g_legacy.out, keep.data(), bytes);
-        if (smol_attn_bidirectional(ctx, g_legacy.q.p, g_legacy.k.p, g_legacy.v.p, SMOL_ATTN_F32, rows, n_heads,
-                                    head_dim, scale, window_starts, n_windows, (float *)g_legacy.out.p) != SMOL_ATTN_OK)
+        legacy_upload_rows(fn, g_legacy.q, q, hrows, head_dim, hdp);
+        legacy_upload_rows(fn, g_legacy.k, k, hrows, head_dim, hdp);
+        legacy_upload_rows(fn, g_legacy.v, v, hrows, head_dim, hdp);
+        legacy_upload_rows(fn, g_legacy.out, keep.data(), hrows, head_dim, hdp);
+        if (smol_attn_bidirectional(ctx, g_legacy.q.p, g_legacy.k.p, g_legacy.v.p, SMOL_ATTN_F32, rows, n_heads, hdp,
+                                    scale, window_starts, n_windows, (float *)g_legacy.out.p) != SMOL_ATTN_OK)
             legacy_abort(fn);
-        return legacy_download(fn, out, g_legacy.out, bytes);
+        return legacy_download_rows(fn, out, g_legacy.out, hrows, head_dim, hdp);
     };
     if (run(Q, K, V) == SMOL_ATTN_OK) return;
     int a = 0, b = 0;

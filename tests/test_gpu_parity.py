@@ -140,6 +140,28 @@ def test_golden_rope_through_reference_signature(sa, golden):
         np.testing.assert_allclose(x, data[r["tag"] + "_applied"], rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize("hd", [1, 16, 32, 65, 100, 112, 200, 255])
+def test_reference_signatures_any_head_dim(sa, oracle, hd):
+    """The drop-ins take any head_dim up to 256 (zero-padded to a kernel
+    size); the bidirectional call keeps the rows before its first window."""
+    print("any head_dim", hd, flush=True)
+    Hq, Hkv, sq, sk = 4, 2, 37, 90
+    Q, K, V = synth.normal(61, (sq, Hq * hd)), synth.normal(62, (sk, Hkv * hd)), synth.normal(63, (sk, Hkv * hd))
+    sc = 1.0 / np.sqrt(hd)
+    out = np.full((sq, Hq * hd), np.nan, np.float32)
+    sa.smol_sliding_window_attention_softcap(out, Q, K, V, sq, sk, Hq, Hkv, hd, sc, sk - sq, 40, 20.0)
+    assert_parity(out, oracle.causal_attention(Q, K, V, sq, sk, Hq, Hkv, hd, sc, sk - sq, window=40, cap=20.0),
+                  "causal hd %d" % hd)
+    ws = [5, 40, 41, 90]
+    out = synth.normal(64, (sk, Hkv * hd)).astype(np.float32)
+    init = out.copy()
+    V2 = synth.normal(65, (sk, Hkv * hd))
+    sa.smol_bidirectional_attention(out, K, V, V2, sk, Hkv, hd, sc, ws, 3)
+    want = oracle.bidirectional_attention(K, V, V2, sk, Hkv, hd, sc, ws)
+    np.testing.assert_array_equal(out[:5], init[:5])
+    assert_parity(out[5:], want[5:], "bidirectional hd %d" % hd)
+
+
 # ------------------------------------------------------------ shapes and edges
 
 CAUSAL_SHAPES = [  # Hq, Hkv, hd, seq_q, seq_k, q_offset, bf16
