@@ -36,7 +36,7 @@ extern "C" int smol_launch_prep(const PrepParams *pp, int n_blocks, hipStream_t 
 extern "C" int smol_launch_decode(const DecParams *dp, int hd, int rows, int nw, hipStream_t st, hipEvent_t ev0,
                                   hipEvent_t ev1);
 extern "C" int smol_launch_xcc_probe(unsigned *out, int n, hipStream_t st);
-extern "C" int smol_decode_occupancy(int hd, int rows, int nw);
+extern "C" int smol_decode_occupancy(int hd, int rows, int nw, int direct);
 extern "C" int smol_launch_fa(const SkParams *sp, int hd, int n_items, int nt, int w, hipStream_t st, hipEvent_t ev0,
                               hipEvent_t ev1);
 extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st, hipEvent_t ev0,
@@ -753,16 +753,19 @@ struct DecCall {
     long long qs_head_stride = 0;
 };
 
-/* Splits every (sequence, kv head, row block) into workgroups of about
- * `per_wg` slabs (the call's slabs over the compute units, or the option),
- * assigns the (sequence, kv head) units to XCDs longest first, and orders
- * each XCD's workgroups with every group's last split after all of its
- * other splits: the last split merges, and the workgroups an XCD dispatches
- * before it include every split it waits for. Workgroup b is slot b / n_xcc
- * of XCD b % n_xcc; slots past an XCD's list are idle. per_wg doubles until
- * no XCD has more workgroups than it holds at once (`fit`), so none waits
- * for another to finish before it starts. */
-static void plan_decode(smol_attn_ctx *ctx, const DecCall &dc, int Hkv, int window, int n_rb, int fit,
+/* Places the (sequence, kv head) units on XCDs, longest first onto the XCD
+ * with the least work so far, then splits each unit's slab range so that
+ * every XCD's units fill the workgroups it holds at once (`fit`): a unit
+ * gets a share of the XCD's slots in proportion to its slabs, at least
+ * `min_per` slabs per workgroup (one per wave) and at most DEC_MAX_SPLIT
+ * splits. Then each XCD's workgroups are ordered with every group's last
+ * split after all of its other splits: the last split merges, and the
+ * workgroups an XCD dispatches before it include every split it waits for.
+ * Since no XCD gets more workgroups than it holds at once, none waits for
+ * another to finish before it starts. Workgroup b is slot b / n_xcc of XCD
+ * b % n_xcc; slots past an XCD's list are idle. SMOL_OPT_DEC_SLABS > 0
+ * instead cuts every unit into workgroups of that many slabs. */
+static void plan_decode(smol_attn_ctx *ctx, const DecCall &dc, int Hkv, int window, int n_rb, int fit, int min_per,
                         std::vector<DecItem> &items) {
     const int nx = ctx->n_xcc;
     const int n_seq = (int)dc.seqs.size();
@@ -771,35 +774,54 @@ static void plan_decode(smol_attn_ctx *ctx, const DecCall &dc, int Hkv, int wind
         const int klo = (window > 0 ? std::max(0, q.pos - window + 1) : 0) & ~(SMOL_SLAB - 1);
         return kend > klo ? (kend - klo + SMOL_SLAB - 1) / SMOL_SLAB : 0;
     };
-    long long total = 0;
-    for (const DecSeq &q : dc.seqs) total += (long long)slabs_of(q) * Hkv * n_rb;
-    const bool forced = ctx->opt[SMOL_OPT_DEC_SLABS] > 0;
-    int per_wg = forced ? ctx->opt[SMOL_OPT_DEC_SLABS] : (int)std::max(1LL, (total + ctx->cu_count - 1) / ctx->cu_count);
+    const int forced = ctx->opt[SMOL_OPT_DEC_SLABS];
     const bool no_split = !ctx->xcd_ok || ctx->opt[SMOL_OPT_DEC_SPLIT] == -1 || dc.whole;
-    struct Unit { int seq, kvh, n_split, xcd; long long cost; };
+    struct Unit { int seq, kvh, ns, n_split, xcd; };
     std::vector<Unit> units;
-    for (;;) {
-        units.clear();
-        for (int i = 0; i < n_seq; i++) {
-            const int ns = slabs_of(dc.seqs[i]);
-            int sp = no_split ? 1 : std::max(1, std::min(DEC_MAX_SPLIT, (ns + per_wg - 1) / per_wg));
-            for (int g = 0; g < Hkv; g++) units.push_back({i, g, sp, 0, (long long)sp * n_rb});
+    for (int i = 0; i < n_seq; i++) {
+        const int ns = slabs_of(dc.seqs[i]);
+        for (int g = 0; g < Hkv; g++) units.push_back({i, g, ns, 1, 0});
+    }
+    std::vector<int> order(units.size());
+    std::iota(order.begin(), order.end(), 0);
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return units[a].ns > units[b].ns; });
+    std::vector<long long> load(nx, 0);
+    for (int u : order) {
+        const int x = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+        units[u].xcd = x;
+        load[x] += std::max(units[u].ns, 1);
+    }
+    if (!no_split && forced > 0) {
+        for (Unit &u : units) u.n_split = std::max(1, std::min(DEC_MAX_SPLIT, (u.ns + forced - 1) / forced));
+    } else if (!no_split) {
+        for (int x = 0; x < nx; x++) {
+            std::vector<Unit *> mine;
+            long long groups = 0, work = 0;
+            for (Unit &u : units)
+                if (u.xcd == x) {
+                    mine.push_back(&u);
+                    groups += n_rb;
+                    work += u.ns;
+                }
+            if (mine.empty() || groups >= fit) continue; /* every slot taken without splits */
+            const double per = std::max<double>(min_per, (double)work * n_rb / fit);
+            long long used = 0;
+            for (Unit *u : mine) {
+                const int cap = std::min(DEC_MAX_SPLIT, std::max(1, u->ns));
+                u->n_split = std::max(1, std::min(cap, (int)std::lround(u->ns / per)));
+                used += (long long)u->n_split * n_rb;
+            }
+            /* over the slots by rounding: take splits from the units whose
+             * splits are shortest */
+            while (used > fit) {
+                Unit *v = nullptr;
+                for (Unit *u : mine)
+                    if (u->n_split > 1 && (!v || (double)u->ns / u->n_split < (double)v->ns / v->n_split)) v = u;
+                if (!v) break;
+                v->n_split--;
+                used -= n_rb;
+            }
         }
-        /* longest first onto the XCD with the fewest workgroups so far */
-        std::vector<int> order(units.size());
-        std::iota(order.begin(), order.end(), 0);
-        std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return units[a].cost > units[b].cost; });
-        std::vector<long long> load(nx, 0);
-        for (int u : order) {
-            const int x = (int)(std::min_element(load.begin(), load.end()) - load.begin());
-            units[u].xcd = x;
-            load[x] += units[u].cost;
-        }
-        const long long most = *std::max_element(load.begin(), load.end());
-        bool all_one = true;
-        for (const Unit &u : units) all_one = all_one && u.n_split == 1;
-        if (forced || no_split || most <= fit || all_one) break;
-        per_wg *= 2;
     }
     std::vector<std::vector<DecItem>> lists(nx), lasts(nx);
     for (const Unit &u : units)
@@ -839,9 +861,11 @@ static int run_decode(smol_attn_ctx *ctx, const CallShape &cs, const DecCall &dc
         return fail(SMOL_ATTN_ERR_UNSUPPORTED, "decode call too large (%d rows, %d sequences)", rows, (int)dc.seqs.size());
     const int nw = rows <= 8 && hd <= 128 ? (ctx->opt[SMOL_OPT_DEC_WAVES] == 8 ? 8 : 4) : 4;
     /* workgroups an XCD holds at once */
-    const int fit = std::max(1, ctx->cu_count / ctx->n_xcc) * smol_decode_occupancy(hd, rows, nw);
-    /* partial slots: O [TR][hd], (m, l) [TR][2], the flag; 256-byte aligned */
-    const int slot_floats = (TR * (hd + 2) + 1 + 63) & ~63;
+    const int fit = std::max(1, ctx->cu_count / ctx->n_xcc) * smol_decode_occupancy(hd, rows, nw, dc.direct ? 1 : 0);
+    /* partial slots: O [TR][hd], (m, l) [TR][2], then the flag alone in the
+     * slot's last 128-byte line (the merger polls that line device-coherently
+     * and reads the others through L2); 256-byte aligned */
+    const int slot_floats = ((((TR * (hd + 2) + 31) & ~31) + 32) + 63) & ~63;
     const size_t n_groups = dc.seqs.size() * cs.Hkv * n_rb;
     const size_t part_bytes = n_groups * DEC_MAX_SPLIT * slot_floats * 4;
     DecCall whole_dc;
@@ -853,12 +877,12 @@ static int run_decode(smol_attn_ctx *ctx, const CallShape &cs, const DecCall &dc
         pdc = &whole_dc;
     }
     std::vector<DecItem> items;
-    plan_decode(ctx, *pdc, cs.Hkv, cs.window, n_rb, fit, items);
+    plan_decode(ctx, *pdc, cs.Hkv, cs.window, n_rb, fit, nw, items);
     if (dc.noalloc && items.size() > DEC_ARG_ITEMS && !pdc->whole) {
         whole_dc = dc;
         whole_dc.whole = true;
         pdc = &whole_dc;
-        plan_decode(ctx, *pdc, cs.Hkv, cs.window, n_rb, fit, items);
+        plan_decode(ctx, *pdc, cs.Hkv, cs.window, n_rb, fit, nw, items);
     }
     if (dc.noalloc && (items.size() > DEC_ARG_ITEMS || dc.seqs.size() > DEC_ARG_SEQS))
         return fail(SMOL_ATTN_ERR_UNSUPPORTED, "%d sequences / %d workgroups exceed what the no-alloc decode passes "

@@ -60,7 +60,31 @@ __device__ __forceinline__ float ror8(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
 }
 
-__device__ __forceinline__ void store_f4_dc(rsrc_t r, unsigned voff, f4 v) { store_f4_sc1(r, voff, v); }
+/* The split partials stay in the XCD's L2: every split of a group runs on
+ * one XCD, whose L2 is the point of coherence for its compute units (their
+ * L1s write through). Plain stores, acknowledged by L2 before the flag is
+ * stored, and plain loads after the flag has been seen (the reading compute
+ * unit has not touched those lines in this kernel, and its L1 starts the
+ * kernel invalidated). The flag itself travels device-coherently (SC1 store,
+ * agent-scope poll). */
+__device__ __forceinline__ void store_f4_l2(rsrc_t r, unsigned voff, f4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(u4v{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                               __float_as_uint(v[3])},
+                                           r, voff, 0, 0);
+}
+__device__ __forceinline__ void store_f2_l2(rsrc_t r, unsigned voff, float a, float b) {
+    typedef unsigned u2v __attribute__((ext_vector_type(2)));
+    __builtin_amdgcn_raw_buffer_store_b64(u2v{__float_as_uint(a), __float_as_uint(b)}, r, voff, 0, 0);
+}
+__device__ __forceinline__ f4 load_f4_l2(rsrc_t r, unsigned voff) {
+    const u4v v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
+    return f4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
+}
+__device__ __forceinline__ float2 load_f2_l2(rsrc_t r, unsigned voff) {
+    typedef unsigned u2v __attribute__((ext_vector_type(2)));
+    const u2v v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 0);
+    return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+}
 
 /* a flag read for polling: an atomic load is issued on every call */
 __device__ __forceinline__ unsigned poll_u32(const unsigned *f) {
@@ -77,7 +101,7 @@ struct DecGeom {
 
 } // namespace
 
-template <int HD, int NT, bool PACK, int NW>
+template <int HD, int NT, bool PACK, int NW, bool DIRECT>
 __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
     using Gm = DecGeom<HD>;
     constexpr int KS = Gm::KS, DT = Gm::DT, HDP = Gm::HDP;
@@ -92,20 +116,38 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
     const int lane = tid & 63, c = lane & 15, j = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int bid = blockIdx.x;
-    DecItem it0 = p.n_items <= DEC_ARG_ITEMS ? p.items[bid] : p.items_dev[bid];
-    /* the item and its sequence are wave-uniform: keep them in scalar registers */
-    const int seq = __builtin_amdgcn_readfirstlane((int)it0.seq);
+    /* The item and, in the same round of loads, sequence `lane` in every
+     * lane (the item names one of them; its fields are then read from that
+     * lane), so the sequence costs no second memory round trip. A sequence
+     * index past 63 is loaded after the item. */
+    static_assert(sizeof(DecItem) == 8 && sizeof(DecSeq) == 16, "item / sequence records");
+    const DecSeq *seqs = p.n_seq <= DEC_ARG_SEQS ? p.seqs : p.seqs_dev;
+    const uint2 iw = reinterpret_cast<const uint2 *>(p.n_items <= DEC_ARG_ITEMS ? p.items : p.items_dev)[bid];
+    const int4 sl = reinterpret_cast<const int4 *>(seqs)[min(lane, max(p.n_seq - 1, 0))];
+    /* both loads are in flight before either is used (the compiler would
+     * otherwise issue the second after the test of the first) */
+    asm volatile("" ::"v"(iw.x), "v"(iw.y), "v"(sl.x), "v"(sl.y), "v"(sl.z), "v"(sl.w));
+    /* the item and its sequence are wave-uniform: keep them in scalar
+     * registers (DecItem: seq 16 bits, kvh, rb, split, n_split 8 bits) */
+    const int seq = (int)(short)(__builtin_amdgcn_readfirstlane((int)iw.x) & 0xFFFF);
     if (seq < 0) return;
-    const int g = __builtin_amdgcn_readfirstlane((int)it0.kvh);
-    const int rb = __builtin_amdgcn_readfirstlane((int)it0.rb);
-    const int split = __builtin_amdgcn_readfirstlane((int)it0.split);
-    const int n_split = __builtin_amdgcn_readfirstlane((int)it0.n_split);
-    DecSeq sq0 = p.n_seq <= DEC_ARG_SEQS ? p.seqs[seq] : p.seqs_dev[seq];
+    const int g = (__builtin_amdgcn_readfirstlane((int)iw.x) >> 16) & 0xFF;
+    const int rb = (int)((unsigned)__builtin_amdgcn_readfirstlane((int)iw.x) >> 24);
+    const int split = __builtin_amdgcn_readfirstlane((int)iw.y) & 0xFF;
+    const int n_split = (__builtin_amdgcn_readfirstlane((int)iw.y) >> 8) & 0xFF;
     DecSeq sq;
-    sq.pos = __builtin_amdgcn_readfirstlane(sq0.pos);
-    sq.slot = __builtin_amdgcn_readfirstlane(sq0.slot);
-    sq.tok0 = __builtin_amdgcn_readfirstlane(sq0.tok0);
-    sq.n_q = __builtin_amdgcn_readfirstlane(sq0.n_q);
+    if (seq < 64) {
+        sq.pos = __builtin_amdgcn_readlane(sl.x, seq);
+        sq.slot = __builtin_amdgcn_readlane(sl.y, seq);
+        sq.tok0 = __builtin_amdgcn_readlane(sl.z, seq);
+        sq.n_q = __builtin_amdgcn_readlane(sl.w, seq);
+    } else {
+        const DecSeq sq0 = seqs[seq];
+        sq.pos = __builtin_amdgcn_readfirstlane(sq0.pos);
+        sq.slot = __builtin_amdgcn_readfirstlane(sq0.slot);
+        sq.tok0 = __builtin_amdgcn_readfirstlane(sq0.tok0);
+        sq.n_q = __builtin_amdgcn_readfirstlane(sq0.n_q);
+    }
     const int G = p.G;
     const int r_base = rb * TR;                   /* first row of this row block */
     const int R = min(TR, sq.n_q * G - r_base);   /* its real rows */
@@ -113,7 +155,7 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
 
     /* the group's slab keys: decode [lo, pos) plus the new key apart; chunk
      * [lo, pos + n_q); lo: the lowest row's window start, slab-aligned */
-    const int kend = p.direct ? sq.pos : sq.pos + sq.n_q;
+    const int kend = DIRECT ? sq.pos : sq.pos + sq.n_q;
     const int klo = (p.window > 0 ? max(0, sq.pos - p.window + 1) : 0) & ~(SMOL_SLAB - 1);
     const int n_slabs = kend > klo ? (kend - klo + SMOL_SLAB - 1) / SMOL_SLAB : 0;
     const int per = (n_slabs + n_split - 1) / n_split;
@@ -122,14 +164,12 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
 
     /* sources: the (slot, head) region of the cache, the head's fresh region */
     const long long cbase = (long long)sq.slot * p.c_slot_stride + (long long)g * p.cap * HD;
-    const rsrc_t rk_c = make_rsrc(p.kc + cbase, (long long)p.cap * HD * 2);
-    const rsrc_t rv_c = make_rsrc(p.vtc + cbase, (long long)p.cap * HD * 2);
-    rsrc_t rk_f = make_rsrc(nullptr, 0), rv_f = make_rsrc(nullptr, 0);
-    const int fresh_pos0 = p.direct ? (1 << 30) : p.fresh_pos0;
-    if (!p.direct) {
-        rk_f = make_rsrc(p.kf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
-        rv_f = make_rsrc(p.vtf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
-    }
+    const uint16_t *kc_base = p.kc + cbase, *vc_base = p.vtc + cbase;
+    const long long c_bytes = (long long)p.cap * HD * 2;
+    const int fresh_pos0 = DIRECT ? (1 << 30) : p.fresh_pos0;
+    const _Float16 *kf_base = DIRECT ? nullptr : p.kf + (long long)g * p.fcap * HD;
+    const _Float16 *vf_base = DIRECT ? nullptr : p.vtf + (long long)g * p.fcap * HD;
+    const long long f_bytes = DIRECT ? 0 : (long long)p.fcap * HD * 2;
     const int kt_row = 8 * (c >> 2) + (c & 3);
     const unsigned kbase = HD % 32 == 0 ? (unsigned)((kt_row * HD + 8 * j) * 2) : 0u;
     const unsigned vbase = HD % 16 == 0 ? (unsigned)((c * SMOL_SLAB + 8 * j) * 2) : 0u;
@@ -148,11 +188,19 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
     }
     struct KRaw { uint4 k[2][KS]; };
     struct VRaw { uint4 v[DT]; };
+    /* The resource of the slab at key k0: the cache or the fresh staging; a
+     * slab at or past ke (a request made ahead of need that turns out to be
+     * past the wave's range) gets an empty range, so its loads return zeros
+     * without touching memory. Requests are then unconditional, and the
+     * compiler's wait counts are the same on every path. */
     auto slab_src = [&](int k0, bool value, rsrc_t &r, unsigned &so) __attribute__((always_inline)) {
-        const bool fr = k0 >= fresh_pos0;
+        const bool live = k0 < ke;
+        const bool fr = !DIRECT && k0 >= fresh_pos0;
         const int kr = fr ? k0 - fresh_pos0 + p.fresh_row0 : k0;
-        so = (unsigned)(kr / SMOL_SLAB) * SLAB_BYTES;
-        r = value ? (fr ? rv_f : rv_c) : (fr ? rk_f : rk_c);
+        so = live ? (unsigned)(kr / SMOL_SLAB) * SLAB_BYTES : 0u;
+        const void *base = value ? (fr ? (const void *)vf_base : (const void *)vc_base)
+                                 : (fr ? (const void *)kf_base : (const void *)kc_base);
+        r = make_rsrc(base, live ? (fr ? f_bytes : c_bytes) : 0);
     };
     auto issue_k = [&](int k0, KRaw &r) __attribute__((always_inline)) {
         rsrc_t rs;
@@ -201,73 +249,85 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
     int k0 = kb + wave * SMOL_SLAB;
     KRaw kr;
     VRaw vr;
-    if (p.direct) {
+    if constexpr (DIRECT) {
         const bool bf_in = p.in_dtype == SMOL_IN_BF16;
         const bool rope = p.rope_kind != SMOL_ROPE_OFF;
         const int n_rows = R + (last_split ? 1 : 0); /* row R: the new key */
-        /* 1. Every staging load of the workgroup goes out in one round
-         * (4 elements per thread and chunk), then this wave's first slab; the
-         * staged values reach LDS as soon as they return (their loads are
-         * older than the slab's, and loads return in order). */
-        constexpr int C4 = HD / 4;
-        constexpr int NST = ((TR + 1) * C4 + 5 * C4 + TPB - 1) / TPB;
-        auto stage_src = [&](int e, const void *&src, long long &idx, bool &f32, float *&dst) __attribute__((always_inline)) -> bool {
-            if (e < n_rows * C4) {
-                const int r = e / C4, c0 = (e - r * C4) * 4;
-                src = r < R ? p.q_in : p.k_in;
-                f32 = !bf_in;
-                dst = s_raw + r * QSTR + c0;
-                if (r < R) {
-                    const int qi = (r_base + r) / G, hg = (r_base + r) - qi * G;
-                    idx = (long long)(sq.tok0 + qi) * p.q_stride + (long long)(g * G + hg) * HD + c0;
-                } else {
-                    idx = (long long)sq.tok0 * p.kv_stride + (long long)g * HD + c0;
-                }
-                return true;
-            }
-            const int e2 = e - n_rows * C4, seg = e2 / C4, c0 = (e2 - seg * C4) * 4;
-            f32 = true;
-            switch (seg) {
-            case 0: if (!rope) return false; src = p.rope_cos; idx = (long long)sq.pos * HD + c0; dst = s_cos + c0; return true;
-            case 1: if (!rope) return false; src = p.rope_sin; idx = (long long)sq.pos * HD + c0; dst = s_sin + c0; return true;
-            case 2: if (!p.q_norm) return false; src = p.q_norm; idx = c0; dst = s_wq + c0; return true;
-            case 3: if (!p.k_norm || !last_split) return false; src = p.k_norm; idx = c0; dst = s_wk + c0; return true;
-            case 4:
-                if (!last_split) return false;
-                src = p.v_in; f32 = !bf_in; dst = s_vnew + c0;
-                idx = (long long)sq.tok0 * p.kv_stride + (long long)g * HD + c0;
-                return true;
-            default: return false;
+        /* 1. Every staging load of the workgroup goes out in one round, then
+         * this wave's first slab; the staged values reach LDS as soon as they
+         * return (their loads are older than the slab's, and loads return in
+         * order). The loads are unconditional: a lane with nothing to fetch
+         * reads a valid dummy address and discards it, so no branch splits
+         * the round (the compiler would wait for each load in turn). Chunks
+         * of 8 elements: one 16-byte load of bf16, two of fp32. */
+        constexpr int CH8 = HD / 8;
+        constexpr int NQC = (TR * CH8 + TPB - 1) / TPB; /* Q-row chunks per thread */
+        static_assert(6 * CH8 <= TPB, "one chunk of the single-row sources per thread");
+        const char *dummy = reinterpret_cast<const char *>(p.q_in);
+        const unsigned esz = bf_in ? 2u : 4u;
+        uint4 qa[NQC], qb[NQC];
+#pragma unroll
+        for (int u = 0; u < NQC; u++) {
+            const int e = tid + TPB * u, r = e / CH8, d0 = (e - r * CH8) * 8;
+            const bool ok = r < R;
+            const int qi = (r_base + r) / G, hg = (r_base + r) - qi * G;
+            const long long idx = (long long)(sq.tok0 + qi) * p.q_stride + (long long)(g * G + hg) * HD + d0;
+            const char *a = ok ? reinterpret_cast<const char *>(p.q_in) + idx * esz : dummy;
+            qa[u] = *reinterpret_cast<const uint4 *>(a);
+            qb[u] = *reinterpret_cast<const uint4 *>(ok && !bf_in ? a + 16 : dummy);
+        }
+        /* the single-row sources, thread t: source t / CH8, chunk t % CH8:
+         * 0 new K, 1 new V (last split), 2 cos, 3 sin (RoPE), 4 q_norm,
+         * 5 k_norm (last split) */
+        const int sseg = tid / CH8, sd0 = (tid - sseg * CH8) * 8;
+        const long long kv_idx = (long long)sq.tok0 * p.kv_stride + (long long)g * HD + sd0;
+        const bool s_in = sseg <= 1; /* an input row (bf16 or fp32), else an fp32 table row */
+        const void *sbase = sseg == 0 ? p.k_in : sseg == 1 ? p.v_in : sseg == 2 ? (const void *)p.rope_cos
+                          : sseg == 3 ? (const void *)p.rope_sin : sseg == 4 ? (const void *)p.q_norm
+                                                                             : (const void *)p.k_norm;
+        const long long sidx = s_in ? kv_idx : (sseg <= 3 ? (long long)sq.pos * HD + sd0 : (long long)sd0);
+        const bool s_ok = sseg <= 1 ? last_split : sseg <= 3 ? rope : sseg == 4 ? p.q_norm != nullptr
+                        : sseg == 5 ? (p.k_norm != nullptr && last_split) : false;
+        const bool s_f32 = !s_in || !bf_in;
+        const char *sa = s_ok ? reinterpret_cast<const char *>(sbase) + sidx * (s_f32 ? 4 : 2) : dummy;
+        const uint4 sa0 = *reinterpret_cast<const uint4 *>(sa);
+        const uint4 sa1 = *reinterpret_cast<const uint4 *>(s_ok && s_f32 ? sa + 16 : dummy);
+        /* Every wave's staging loads are queued before any wave's slab loads
+         * (a compute unit returns its waves' data in request order, so a
+         * slab requested first would delay the other waves' staging by its
+         * whole transfer). The barrier orders only the requests: nothing
+         * here waits for their data. */
+        __builtin_amdgcn_s_barrier();
+        issue_k(k0, kr);
+        issue_v(k0, vr);
+        auto unpack8 = [&](uint4 a, uint4 b, bool f32, float *v) __attribute__((always_inline)) {
+            if (f32) {
+                v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z);
+                v[3] = __uint_as_float(a.w); v[4] = __uint_as_float(b.x); v[5] = __uint_as_float(b.y);
+                v[6] = __uint_as_float(b.z); v[7] = __uint_as_float(b.w);
+            } else {
+                unpack_bf16x8(a, v);
             }
         };
-        uint4 st_raw[NST];
+        auto st8 = [&](float *dst, const float *v) __attribute__((always_inline)) {
+            *reinterpret_cast<float4 *>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+            *reinterpret_cast<float4 *>(dst + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        };
 #pragma unroll
-        for (int u = 0; u < NST; u++) {
-            const void *src; long long idx; bool f32; float *dst;
-            st_raw[u] = make_uint4(0, 0, 0, 0);
-            if (stage_src(tid + TPB * u, src, idx, f32, dst)) {
-                if (f32) st_raw[u] = *reinterpret_cast<const uint4 *>((const float *)src + idx);
-                else {
-                    const uint2 h = *reinterpret_cast<const uint2 *>((const uint16_t *)src + idx);
-                    st_raw[u] = make_uint4(h.x, h.y, 0, 0);
-                }
+        for (int u = 0; u < NQC; u++) {
+            const int e = tid + TPB * u, r = e / CH8, d0 = (e - r * CH8) * 8;
+            if (r < R) {
+                float v[8];
+                unpack8(qa[u], qb[u], !bf_in, v);
+                st8(s_raw + r * QSTR + d0, v);
             }
         }
-        if (k0 < ke) {
-            issue_k(k0, kr);
-            issue_v(k0, vr);
-        }
-#pragma unroll
-        for (int u = 0; u < NST; u++) {
-            const void *src; long long idx; bool f32; float *dst;
-            if (stage_src(tid + TPB * u, src, idx, f32, dst)) {
-                float4 v;
-                if (f32) v = make_float4(__uint_as_float(st_raw[u].x), __uint_as_float(st_raw[u].y),
-                                         __uint_as_float(st_raw[u].z), __uint_as_float(st_raw[u].w));
-                else v = make_float4(__uint_as_float(st_raw[u].x << 16), __uint_as_float(st_raw[u].x & 0xFFFF0000u),
-                                     __uint_as_float(st_raw[u].y << 16), __uint_as_float(st_raw[u].y & 0xFFFF0000u));
-                *reinterpret_cast<float4 *>(dst) = v;
-            }
+        if (s_ok) {
+            float v[8];
+            unpack8(sa0, sa1, s_f32, v);
+            float *dst = sseg == 0 ? s_raw + R * QSTR : sseg == 1 ? s_vnew : sseg == 2 ? s_cos
+                       : sseg == 3 ? s_sin : sseg == 4 ? s_wq : s_wk;
+            st8(dst + sd0, v);
         }
         __syncthreads();
         /* 2. 1 / rms of each row: eight lanes per row, lane j summing the
@@ -276,7 +336,13 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
         constexpr int CH = HD / 8; /* 8-element chunks of a row */
         auto row_dot8 = [&](const float *a, const float *b, int jj) __attribute__((always_inline)) {
             float sd = 0.0f;
-            for (int ch = jj; ch < CH; ch += 8) {
+            /* loops of this staging phase have compile-time trip counts and
+             * unroll: a loop here would make the compiler wait for every
+             * outstanding load (the first slab's too) before entering it */
+#pragma unroll
+            for (int ci = 0; ci < (CH + 7) / 8; ci++) {
+                const int ch = jj + 8 * ci;
+                if (ch >= CH) break;
                 float x[8], y[8];
                 ld8(a + 8 * ch, x);
                 ld8(b + 8 * ch, y);
@@ -289,7 +355,10 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
             return sd;
         };
         if (nq || nk) {
-            for (int r0 = 0; r0 < n_rows; r0 += TPB / 8) {
+#pragma unroll
+            for (int ri = 0; ri < (TR + 1 + TPB / 8 - 1) / (TPB / 8); ri++) {
+                const int r0 = ri * (TPB / 8);
+                if (r0 >= n_rows) break;
                 const int r = min(r0 + (tid >> 3), n_rows - 1);
                 const float ss = row_dot8(s_raw + r * QSTR, s_raw + r * QSTR, tid & 7);
                 if (r0 + (tid >> 3) < n_rows && (tid & 7) == 0) s_rinv[r] = 1.0f / sqrtf(ss / (float)HD + p.norm_eps);
@@ -300,7 +369,10 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
          * the new key's bf16 row and its value's V^T column go to the cache
          * (one row block writes them) */
         constexpr int CHP = HDP / 8;
-        for (int e = tid; e < n_rows * CHP; e += TPB) {
+#pragma unroll
+        for (int ei = 0; ei < ((TR + 1) * CHP + TPB - 1) / TPB; ei++) {
+            const int e = tid + ei * TPB;
+            if (e >= n_rows * CHP) break;
             const int r = e / CHP, d0 = (e - r * CHP) * 8;
             const bool is_k = r >= R;
             float y[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -355,16 +427,12 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
                             y[i] = d0 + i < HALF ? fmaf(x[i], cv[i], -(pr[i] * sv[i])) : fmaf(x[i], cv[i], pr[i] * sv[i]);
                     }
                 }
-                if (is_k) {
-                    if (rb == 0) {
-                        uint16_t *kc = const_cast<uint16_t *>(p.kc) + cbase;
-                        uint16_t *vt = const_cast<uint16_t *>(p.vtc) + cbase +
-                                       (long long)(sq.pos / SMOL_SLAB) * SMOL_SLAB * HD + sq.pos % SMOL_SLAB;
-                        *reinterpret_cast<uint4 *>(kc + (long long)sq.pos * HD + d0) = pack_bf16x8(y);
-#pragma unroll
-                        for (int i = 0; i < 8; i++) vt[(long long)(d0 + i) * SMOL_SLAB] = f32_to_bf16(s_vnew[d0 + i]);
-                    }
-                } else {
+                /* the new key's row stays in s_rot (row R): it joins the
+                 * cache after the slab loop (this call reads keys [klo, pos)
+                 * from the cache and the new one from LDS; a store here
+                 * would sit among the slab loads and blur the compiler's
+                 * count of them) */
+                if (!is_k) {
 #pragma unroll
                     for (int i = 0; i < 8; i++) y[i] *= p.qscale;
                 }
@@ -375,7 +443,10 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
         __syncthreads();
         /* 4. the new key's fp32 score against every row (last split) */
         if (last_split) {
-            for (int r0 = 0; r0 < R; r0 += TPB / 8) {
+#pragma unroll
+            for (int ri = 0; ri < (TR + TPB / 8 - 1) / (TPB / 8); ri++) {
+                const int r0 = ri * (TPB / 8);
+                if (r0 >= R) break;
                 const int r = min(r0 + (tid >> 3), R - 1);
                 const float sd = row_dot8(s_rot + r * QSTR, s_rot + R * QSTR, tid & 7);
                 if (r0 + (tid >> 3) < R && (tid & 7) == 0) s_snew[r] = sd;
@@ -407,39 +478,43 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
         __syncthreads(); /* s_snew complete */
         if (last_split && PACK) s_new = (c & 7) < R ? s_snew[c & 7] : 0.0f;
     } else {
-        if (k0 < ke) {
-            issue_k(k0, kr);
-            issue_v(k0, vr);
-        }
-        /* chunk mode: Q rows from the fp32 scratch (k_prep rotated and scaled them) */
+        /* chunk mode: Q rows from the fp32 scratch (k_prep rotated and
+         * scaled them). All Q loads, then the first slab's, go out before
+         * any is used, unconditionally (a lane past the real rows reads row
+         * 0 and drops it), so the loop starts with only the slab loads
+         * outstanding and the Q latency overlaps the slab's. */
         const float *qbase = p.qs32 + (long long)g * p.qs_head_stride;
         auto qrow = [&](int r) { return qbase + (long long)(sq.tok0 * G + r_base + r) * HDP; };
-        if constexpr (PACK) {
-            const int r = c & 7;
+        constexpr int QT = PACK ? 1 : NT;
+        float4 qa[QT][KS], qb[QT][KS];
+#pragma unroll
+        for (int nt = 0; nt < QT; nt++) {
+            const int r = PACK ? (c & 7) : nt * 16 + c;
+            const float *row = qrow(r < R ? r : 0);
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
-                b8 hi, lo;
-                float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-                if (r < R) {
-                    const float4 a = *reinterpret_cast<const float4 *>(qrow(r) + 32 * ks + 8 * j);
-                    const float4 e = *reinterpret_cast<const float4 *>(qrow(r) + 32 * ks + 8 * j + 4);
-                    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = e.x; v[5] = e.y; v[6] = e.z; v[7] = e.w;
-                }
-                split8(v, hi, lo);
-                qf[ks] = c < 8 ? hi : lo;
+                qa[nt][ks] = *reinterpret_cast<const float4 *>(row + 32 * ks + 8 * j);
+                qb[nt][ks] = *reinterpret_cast<const float4 *>(row + 32 * ks + 8 * j + 4);
             }
-        } else {
+        }
+        issue_k(k0, kr);
+        issue_v(k0, vr);
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                const int r = nt * 16 + c;
+        for (int nt = 0; nt < QT; nt++) {
+            const int r = PACK ? (c & 7) : nt * 16 + c;
 #pragma unroll
-                for (int ks = 0; ks < KS; ks++) {
-                    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-                    if (r < R) {
-                        const float4 a = *reinterpret_cast<const float4 *>(qrow(r) + 32 * ks + 8 * j);
-                        const float4 e = *reinterpret_cast<const float4 *>(qrow(r) + 32 * ks + 8 * j + 4);
-                        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = e.x; v[5] = e.y; v[6] = e.z; v[7] = e.w;
-                    }
+            for (int ks = 0; ks < KS; ks++) {
+                const float4 a = qa[nt][ks], e = qb[nt][ks];
+                float v[8] = {a.x, a.y, a.z, a.w, e.x, e.y, e.z, e.w};
+                if (r >= R) {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) v[i] = 0.0f;
+                }
+                if constexpr (PACK) {
+                    b8 hi, lo;
+                    split8(v, hi, lo);
+                    qf[ks] = c < 8 ? hi : lo;
+                } else {
                     split8(v, qh[nt][ks], ql[nt][ks]);
                 }
             }
@@ -458,7 +533,7 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
         const bool valid = r < R;
         const int qi = (r_base + r) / G;
         int rl = 0, rh = kend;
-        if (!p.direct) rh = min(rh, sq.pos + qi + 1);
+        if (!DIRECT) rh = min(rh, sq.pos + qi + 1);
         if (p.window > 0) rl = max(0, sq.pos + qi - p.window + 1);
         lo[nt] = valid ? rl : -(1 << 30);
         hi[nt] = valid ? rh : (1 << 30);
@@ -609,28 +684,58 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
         }
     };
 
-    /* ---- the wave's slabs: the next one's K is requested once the current
-     * one's K fragments are consumed, its V once the current V is; the last
-     * slab is peeled so no load is left in flight after the loop ---- */
+    /* ---- the wave's slabs: slab i's K fragments are replaced by the
+     * request of slab i + DEPTH once they are consumed, its V fragments once
+     * they are. Requests past the wave's range are empty, so every path
+     * issues the same loads and the loop needs no peeled last slab. DEPTH 2
+     * (two register sets, alternating) measured slower than 1: the
+     * compiler's wait counts at the loop head cover the second set too. ---- */
     const int step = SMOL_SLAB * NW;
-    if (k0 < ke) {
-        auto slab = [&](auto issue_tag) __attribute__((always_inline)) {
-            constexpr bool ISSUE = decltype(issue_tag)::value;
-            f4 sacc[NR][2];
-            const bool fr = k0 >= fresh_pos0;
-            if (fr) qk(kr, sacc, std::true_type{});
-            else qk(kr, sacc, std::false_type{});
-            if constexpr (ISSUE) issue_k(k0 + step, kr);
-            if (fr) smpv(k0, sacc, vr, std::true_type{});
-            else smpv(k0, sacc, vr, std::false_type{});
-            if constexpr (ISSUE) issue_v(k0 + step, vr);
-        };
-        for (; k0 + step < ke; k0 += step) slab(std::true_type{});
-        slab(std::false_type{});
+    constexpr int DEPTH = 1;
+    auto slab = [&](KRaw &kx, VRaw &vx) __attribute__((always_inline)) {
+        f4 sacc[NR][2];
+        const bool fr = !DIRECT && k0 >= fresh_pos0;
+        if (fr) qk(kx, sacc, std::true_type{});
+        else qk(kx, sacc, std::false_type{});
+        issue_k(k0 + DEPTH * step, kx);
+        if (fr) smpv(k0, sacc, vx, std::true_type{});
+        else smpv(k0, sacc, vx, std::false_type{});
+        issue_v(k0 + DEPTH * step, vx);
+        k0 += step;
+    };
+    if constexpr (DEPTH == 2) {
+        KRaw kr2;
+        VRaw vr2;
+        issue_k(k0 + step, kr2);
+        issue_v(k0 + step, vr2);
+        while (k0 < ke) {
+            slab(kr, vr);
+            if (k0 >= ke) break;
+            slab(kr2, vr2);
+        }
+    } else {
+        while (k0 < ke) slab(kr, vr);
+    }
+
+    /* ---- decode: the new key's bf16 K row and V^T column join the cache
+     * (row block 0 of the last split; the rows are still in LDS) ---- */
+    if constexpr (DIRECT) {
+        if (last_split && rb == 0) {
+            for (int d0 = tid * 8; d0 < HD; d0 += TPB * 8) {
+                float y[8];
+                ld8(s_rot + R * QSTR + d0, y);
+                uint16_t *kc = const_cast<uint16_t *>(p.kc) + cbase;
+                uint16_t *vt = const_cast<uint16_t *>(p.vtc) + cbase +
+                               (long long)(sq.pos / SMOL_SLAB) * SMOL_SLAB * HD + sq.pos % SMOL_SLAB;
+                *reinterpret_cast<uint4 *>(kc + (long long)sq.pos * HD + d0) = pack_bf16x8(y);
+#pragma unroll
+                for (int i = 0; i < 8; i++) vt[(long long)(d0 + i) * SMOL_SLAB] = f32_to_bf16(s_vnew[d0 + i]);
+            }
+        }
     }
 
     /* ---- decode, last split, wave 0: the new key joins with an exact max ---- */
-    if (p.direct && last_split && wave == 0) {
+    if (DIRECT && last_split && wave == 0) {
 #pragma unroll
         for (int nt = 0; nt < NR; nt++) {
             const int r = PACK ? (c & 7) : nt * 16 + c;
@@ -743,9 +848,9 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
                 for (int dt = 0; dt < DT; dt++) {
                     const int d = 16 * dt + 4 * j;
                     if (HD % 16 != 0 && d >= HD) continue;
-                    store_f4_dc(rpart, my + (unsigned)((r * HD + d) * 4), o[nt][dt]);
+                    store_f4_l2(rpart, my + (unsigned)((r * HD + d) * 4), o[nt][dt]);
                 }
-                if (j == 0) store_f2_sc1(rpart, my + ML_OFF + (unsigned)(r * 8), m[nt], l[nt]);
+                if (j == 0) store_f2_l2(rpart, my + ML_OFF + (unsigned)(r * 8), m[nt], l[nt]);
             }
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __builtin_amdgcn_s_waitcnt(0); /* every store above acknowledged */
@@ -772,6 +877,48 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
         }
     }
     ok = __syncthreads_and(ok);
+    /* Every load of the merge goes out in one round before anything waits
+     * on it: the others' (m, l), then their O partials (which do not depend
+     * on the weights). Element e (a row's 4 columns) gets tpe threads,
+     * thread k of them holding splits k, k + tpe, ...; with more elements
+     * than threads a thread takes elements eo, eo + TPB, ... (NBM at most).
+     * UM splits per element a round; more splits take further rounds. Each
+     * load is unconditional (an out-of-range offset reads zeros). */
+    constexpr int C4 = HD / 4;
+    constexpr int NBM = (TR * C4 + TPB - 1) / TPB;
+    constexpr int UM = (NW > 4 ? 16 : 32) / NBM; /* loads in flight: the registers of one or two waves a SIMD */
+    constexpr int NML = (DEC_MAX_SPLIT * TR + TPB - 1) / TPB;
+    const int E = R * C4;
+    const int tpe = max(1, min(TPB / E, nsp - 1));
+    const int per_batch = TPB / tpe;             /* elements per batch */
+    const int n_batch = (E + per_batch - 1) / per_batch;
+    const int k = tid / per_batch, eo = tid - k * per_batch;
+    const int n_u = (nsp - 1 + tpe - 1) / tpe;   /* splits of one element per thread */
+    float2 mlv[NML];
+#pragma unroll
+    for (int i = 0; i < NML; i++) {
+        const int e = tid + TPB * i, sp = e / R, r = e - sp * R;
+        mlv[i] = load_f2_l2(rpart, e < (nsp - 1) * R ? (unsigned)sp * SLOTB + ML_OFF + (unsigned)(r * 8) : OOB_OFF);
+    }
+    auto o_off = [&](int bb, int u) -> unsigned {
+        const int e = bb * per_batch + eo, sp = k + tpe * u;
+        if (k >= tpe || e >= E || u >= n_u || sp >= nsp - 1) return OOB_OFF;
+        const int r = e / C4, d = (e - r * C4) * 4;
+        return (unsigned)sp * SLOTB + (unsigned)((r * HD + d) * 4);
+    };
+    f4 v[NBM][UM];
+    /* only the round's real splits are requested (n_u is uniform: the
+     * branches are scalar); an out-of-range request still costs the address
+     * unit its lanes */
+    auto load_round = [&](int u0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int uu = 0; uu < UM; uu++) {
+            if (u0 + uu >= n_u) break;
+#pragma unroll
+            for (int bb = 0; bb < NBM; bb++) v[bb][uu] = load_f4_l2(rpart, o_off(bb, u0 + uu));
+        }
+    };
+    load_round(0);
     /* this split's own state goes into LDS next to the others' */
     if (wave == 0) {
 #pragma unroll
@@ -781,11 +928,13 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
             if (j == 0) { s_ml[2 * ((nsp - 1) * TR + r)] = m[nt]; s_ml[2 * ((nsp - 1) * TR + r) + 1] = l[nt]; }
         }
     }
-    for (int e = tid; e < (nsp - 1) * R; e += TPB) {
-        const int sp = e / R, r = e - sp * R;
-        const float2 ml = load_f2_sc1(rpart, (unsigned)sp * SLOTB + ML_OFF + (unsigned)(r * 8));
-        s_ml[2 * (sp * TR + r)] = ml.x;
-        s_ml[2 * (sp * TR + r) + 1] = ml.y;
+#pragma unroll
+    for (int i = 0; i < NML; i++) {
+        const int e = tid + TPB * i, sp = e / R, r = e - sp * R;
+        if (e < (nsp - 1) * R) {
+            s_ml[2 * (sp * TR + r)] = mlv[i].x;
+            s_ml[2 * (sp * TR + r) + 1] = mlv[i].y;
+        }
     }
     __syncthreads();
     if (tid < R) {
@@ -800,7 +949,6 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
         }
         s_row[tid] = L > 0.0f ? 1.0f / L : 0.0f;
     }
-    __syncthreads();
     /* O of every row: this split's own part from wave 0's registers (through
      * LDS), the others' from their slots */
     float *s_own = smem + 3 * DEC_MAX_SPLIT * TR + TR; /* [TR][OSTR] */
@@ -814,37 +962,36 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
         }
     }
     __syncthreads();
-    /* every other split's O in one round of loads: element e (a row's 4
-     * columns) gets tpe threads, thread k of them summing splits k, k + tpe,
-     * ... in order; the tpe partial sums and this split's own part are added
-     * in a fixed order, so the result does not depend on timing */
-    constexpr int C4 = HD / 4;
-    const int E = R * C4;
-    const int tpe = max(1, min(TPB / E, nsp - 1));
-    const int per_batch = TPB / tpe;             /* elements per batch */
+    /* each thread's splits in increasing order, then the tpe partial sums
+     * and this split's own part in a fixed order: the result does not
+     * depend on timing */
+    f4 acc[NBM];
+#pragma unroll
+    for (int bb = 0; bb < NBM; bb++) acc[bb] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int u0 = 0; u0 < n_u; u0 += UM) {
+        if (u0 > 0) load_round(u0);
+#pragma unroll
+        for (int bb = 0; bb < NBM; bb++) {
+            const int e = bb * per_batch + eo, r = e / C4;
+#pragma unroll
+            for (int uu = 0; uu < UM; uu++) {
+                if (u0 + uu >= n_u) break;
+                const int sp = k + tpe * (u0 + uu);
+                if (k < tpe && e < E && sp < nsp - 1) acc[bb] += s_w[sp * TR + r] * v[bb][uu];
+            }
+        }
+    }
     f4 *s_part = reinterpret_cast<f4 *>(s_own + TR * OSTR); /* [tpe][per_batch] */
-    for (int e0 = 0; e0 < E; e0 += per_batch) {
-        const int k = tid / per_batch, e = e0 + (tid - k * per_batch);
-        const bool act = k < tpe && e < E;
-        const int r = act ? e / C4 : 0, d = act ? (e - r * C4) * 4 : 0;
-        f4 v[DEC_MAX_SPLIT];
 #pragma unroll
-        for (int u = 0; u < DEC_MAX_SPLIT; u++) {
-            const int sp = k + tpe * u;
-            v[u] = (act && sp < nsp - 1) ? load_f4_sc1(rpart, (unsigned)sp * SLOTB + (unsigned)((r * HD + d) * 4))
-                                         : f4{0.f, 0.f, 0.f, 0.f};
-        }
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int u = 0; u < DEC_MAX_SPLIT; u++) {
-            const int sp = k + tpe * u;
-            if (act && sp < nsp - 1) acc += s_w[sp * TR + r] * v[u];
-        }
-        if (k < tpe) s_part[k * per_batch + (tid - k * per_batch)] = acc;
+    for (int bb = 0; bb < NBM; bb++) {
+        if (bb >= n_batch) break;
+        const int e = bb * per_batch + eo;
+        if (k < tpe) s_part[k * per_batch + eo] = acc[bb];
         __syncthreads();
         if (k == 0 && e < E) {
+            const int r = e / C4, d = (e - r * C4) * 4;
             f4 res = s_w[(nsp - 1) * TR + r] * *reinterpret_cast<const f4 *>(s_own + r * OSTR + d);
-            for (int kk = 0; kk < tpe; kk++) res += s_part[kk * per_batch + tid];
+            for (int kk = 0; kk < tpe; kk++) res += s_part[kk * per_batch + eo];
             res *= s_row[r];
             if (!ok) res = f4{NAN, NAN, NAN, NAN};
             *reinterpret_cast<f4 *>(out_row(r) + d) = res;
@@ -855,46 +1002,55 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
 
 /* ------------------------------------------------------------------ launcher */
 
+template <int HD, int NT, bool PACK, int NW, bool DIRECT>
+static int launch_dec_d(const DecParams *dp, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    if (ev0)
+        hipExtLaunchKernelGGL((k_dec<HD, NT, PACK, NW, DIRECT>), dim3(dp->n_items), dim3(64 * NW), 0, st, ev0, ev1, 0, *dp);
+    else
+        hipLaunchKernelGGL((k_dec<HD, NT, PACK, NW, DIRECT>), dim3(dp->n_items), dim3(64 * NW), 0, st, *dp);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
 template <int HD, int NT, bool PACK, int NW>
 static int launch_dec_v(const DecParams *dp, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
-    if (ev0)
-        hipExtLaunchKernelGGL((k_dec<HD, NT, PACK, NW>), dim3(dp->n_items), dim3(64 * NW), 0, st, ev0, ev1, 0, *dp);
-    else
-        hipLaunchKernelGGL((k_dec<HD, NT, PACK, NW>), dim3(dp->n_items), dim3(64 * NW), 0, st, *dp);
-    return hipGetLastError() == hipSuccess ? 0 : -3;
+    return dp->direct ? launch_dec_d<HD, NT, PACK, NW, true>(dp, st, ev0, ev1)
+                      : launch_dec_d<HD, NT, PACK, NW, false>(dp, st, ev0, ev1);
 }
 
 /* workgroups of one k_dec build that fit on a compute unit at once */
 template <int HD, int NT, bool PACK, int NW>
-static int occ_v() {
+static int occ_v(bool direct) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(&k_dec<HD, NT, PACK, NW>), 64 * NW,
+    const void *f = direct ? reinterpret_cast<const void *>(&k_dec<HD, NT, PACK, NW, true>)
+                           : reinterpret_cast<const void *>(&k_dec<HD, NT, PACK, NW, false>);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, 64 * NW,
                                                      0) != hipSuccess)
         return 1;
     return n > 0 ? n : 1;
 }
 
 template <int HD>
-static int occ_hd(int rows, int nw) {
+static int occ_hd(int rows, int nw, bool d) {
     if (rows <= 8) {
         if constexpr (HD <= 128) {
-            if (nw == 8) return occ_v<HD, 1, true, 8>();
+            if (nw == 8) return occ_v<HD, 1, true, 8>(d);
         }
-        return occ_v<HD, 1, true, 4>();
+        return occ_v<HD, 1, true, 4>(d);
     }
-    if (rows <= 16 || HD > 128) return occ_v<HD, 1, false, 4>();
-    if constexpr (HD <= 128) return occ_v<HD, 2, false, 4>();
+    if (rows <= 16 || HD > 128) return occ_v<HD, 1, false, 4>(d);
+    if constexpr (HD <= 128) return occ_v<HD, 2, false, 4>(d);
     return 1;
 }
 
-extern "C" int smol_decode_occupancy(int hd, int rows, int nw) {
+extern "C" int smol_decode_occupancy(int hd, int rows, int nw, int direct) {
+    const bool d = direct != 0;
     switch (hd) {
-    case 64: return occ_hd<64>(rows, nw);
-    case 72: return occ_hd<72>(rows, nw);
-    case 80: return occ_hd<80>(rows, nw);
-    case 96: return occ_hd<96>(rows, nw);
-    case 128: return occ_hd<128>(rows, nw);
-    case 256: return occ_hd<256>(rows, nw);
+    case 64: return occ_hd<64>(rows, nw, d);
+    case 72: return occ_hd<72>(rows, nw, d);
+    case 80: return occ_hd<80>(rows, nw, d);
+    case 96: return occ_hd<96>(rows, nw, d);
+    case 128: return occ_hd<128>(rows, nw, d);
+    case 256: return occ_hd<256>(rows, nw, d);
     default: return 1;
     }
 }

@@ -208,7 +208,8 @@ typedef struct {
     int window; float cap2;    /* window > 0: sliding window; cap2 > 0: softcap in log2 units */
     /* split-K: partial slot (merge group * DEC_MAX_SPLIT + split), merge group
      * (seq * Hkv + kvh) * n_rb + rb, of slot_floats floats:
-     * O [R][hd], (m, l) [R][2], then the flag (an int) at slot_floats - 1 */
+     * O [R][hd], (m, l) [R][2], then the flag (an int) at slot_floats - 1,
+     * alone in the slot's last 128 bytes */
     float *part; int slot_floats; unsigned epoch;
     int n_rb;                  /* row blocks per (sequence, kv head) */
     int n_items;               /* grid size */
