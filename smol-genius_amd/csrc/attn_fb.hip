@@ -344,8 +344,14 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
             dma(slab_k(i + 3), (i + 3) % NSTG);
             dma(slab_k(i + 4), (i + 4) % NSTG);
         }
-        prep_s(k0, act, !full, scur);
+        /* the LDS reads and transfers go out first, then P.V of the
+         * previous slab (its fragments are in registers) covers the reads'
+         * latency; the compiler would otherwise start the S MFMAs, which
+         * wait for this step's K fragments (measured 4% on the C2 shape) */
+        __builtin_amdgcn_sched_barrier(0);
         pv(vprev, pprev);
+        __builtin_amdgcn_sched_barrier(0);
+        prep_s(k0, act, !full, scur);
         const bool hit = expo(scur, pnow);
         qk(kf, snext);
         if (hit) rescale(scur, pnow, snext);

@@ -155,6 +155,23 @@ typedef struct {
     int *range_flag;           /* set to 1 when a value written to fp16 would overflow */
 } PrepParams;
 
+/* ---- k_attn_win: bidirectional windows resident in LDS ----
+ * One workgroup per 128-row tile of a (window, head); the window's K and V
+ * are read from the inputs (fp32 or bf16), converted to fp16 and written
+ * to LDS once; no pre-pass. */
+#define WIN_ARG_WINDOWS 255   /* windows passed in the kernel arguments */
+#define WIN_TPB 512           /* threads of a k_attn_win workgroup: 8 waves, two per SIMD */
+#define WIN_ROWS 128          /* rows of its tile: 16 per wave */
+typedef struct {
+    const void *q; const void *k; const void *v; int in_dtype;
+    long long row_stride;      /* elements between consecutive tokens (n_heads * hd) */
+    float *out; float qscale; int H; int n_windows;
+    int tpu;                   /* 64-row tiles of the longest window */
+    int n_xcc;                 /* XCDs: workgroup b runs on XCD b % n_xcc */
+    int *range_flag;           /* set to 1 when a value written as fp16 would overflow */
+    int ws[WIN_ARG_WINDOWS + 1];
+} WinParams;
+
 /* ---- k_dec: decode and short chunks, split over the workgroups of one XCD ----
  *
  * A group is one (sequence, kv head): its R = n_q * G query rows (R <= 64)

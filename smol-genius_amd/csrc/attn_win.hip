@@ -1,0 +1,382 @@
+/*
+ * attn_win.hip - k_attn_win: windowed bidirectional attention with each
+ * window's keys resident in LDS (common/kernels/attention.c:32-77, the
+ * vision encoders' and the audio encoder's windows).
+ *
+ * A workgroup owns one 128-row tile of one (window, head): its eight waves
+ * read the window's K and V rows straight from the inputs (fp32 or bf16),
+ * convert them to fp16 (bf16 exactly, fp32 rounded to nearest even, as the
+ * pre-pass of the other kernels does) and write them once into an LDS image
+ * of the whole window; Q is read into registers the same way, times
+ * scale * log2 e. After one barrier every wave runs through the window's
+ * 32-key slabs with no further synchronisation: S = K.Q^T and O += V^T.P^T
+ * on v_mfma_f32_16x16x32_f16, the softmax in fp32 with an exact running
+ * maximum per slab. No pre-pass and no staging buffer in HBM: the inputs
+ * are read once per row tile (a 104-token audio window is one tile; the
+ * tiles of a window share its K and V in one XCD's L2).
+ *
+ * LDS image of slab s (the layout k_attn_fb reads, conflict-free):
+ *   K   : 32 key rows of 256 bytes; 16-byte chunk cb of key row r sits in
+ *         slot cb ^ f(r), f(r) = (r & 3) | ((r >> 3) & 3) << 2.
+ *   V^T : 16*DT rows of 64 bytes (32 keys); chunk jc (keys 8jc..8jc+7) of
+ *         row d sits in slot jc ^ ((d >> 1) & 3).
+ * Columns past head_dim and keys past the window are zeros.
+ */
+#include "attn_device.h"
+
+namespace {
+
+template <int HD>
+struct WinGeom {
+    static constexpr int KS = (HD + 31) / 32;  /* 32-wide d chunks of a K fragment */
+    static constexpr int DT = (HD + 15) / 16;  /* 16-wide d tiles of the output */
+    static constexpr int HDP = KS * 32;
+    static constexpr int KROW = 256;
+    static constexpr int K_BYTES = SMOL_SLAB * KROW;
+    static constexpr int V_BYTES = 16 * DT * 64;
+    static constexpr int SLABB = K_BYTES + V_BYTES;
+    static constexpr int NS_MAX = (160 * 1024) / SLABB; /* slabs the LDS holds */
+};
+
+/* 8 elements of an input row as fp32 (bf16 widened exactly) */
+template <bool BF>
+struct Raw8In {
+    uint4 a, b;
+    __device__ __forceinline__ void load(const void *base, long long idx) {
+        if constexpr (BF) {
+            a = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(base) + idx);
+        } else {
+            const float *f = reinterpret_cast<const float *>(base) + idx;
+            a = *reinterpret_cast<const uint4 *>(f);
+            b = *reinterpret_cast<const uint4 *>(f + 4);
+        }
+    }
+    __device__ __forceinline__ void unpack(float *v) const {
+        if constexpr (BF) {
+            unpack_bf16x8(a, v);
+        } else {
+            v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z);
+            v[3] = __uint_as_float(a.w); v[4] = __uint_as_float(b.x); v[5] = __uint_as_float(b.y);
+            v[6] = __uint_as_float(b.z); v[7] = __uint_as_float(b.w);
+        }
+    }
+};
+
+} // namespace
+
+template <int HD, bool BF, int NS>
+__global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
+    using Gm = WinGeom<HD>;
+    constexpr int KS = Gm::KS, DT = Gm::DT, HDP = Gm::HDP, KROW = Gm::KROW;
+    constexpr int K_BYTES = Gm::K_BYTES, SLABB = Gm::SLABB;
+    static_assert(HD % 8 == 0 && HD <= 128, "head_dim");
+    static_assert(NS * SLABB <= 160 * 1024, "LDS");
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * SLABB];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, c = lane & 15, j = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    /* Unit u = (window u / H, head u % H) has up to tpu tiles of WIN_ROWS. The
+     * units go round-robin over the XCDs and a unit's tiles to one XCD
+     * (workgroup b runs on XCD b % n_xcc), so the window's K and V come
+     * from memory into one L2 and its tiles share them there. */
+    const int b = blockIdx.x, nx = p.n_xcc;
+    const int x = b % nx, slot = b / nx;
+    const int u = (slot / p.tpu) * nx + x, tile = slot % p.tpu;
+    if (u >= p.n_windows * p.H) return;
+    const int w = u / p.H, h = u - w * p.H;
+    const int w0 = p.ws[w], len = p.ws[w + 1] - w0;
+    const int row0 = tile * WIN_ROWS;
+    if (row0 >= len) return;
+    const int nslab = (len + SMOL_SLAB - 1) / SMOL_SLAB; /* <= NS (the host's choice of build) */
+    const long long hoff = (long long)h * HD;
+
+    /* ---- Q fragments of this wave's 16 rows: row rq, dims 32 ks + 8 j ---- */
+    const int rq = row0 + 16 * wave + c;
+    const bool q_ok = rq < len;
+    Raw8In<BF> qin[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+        const int d0 = 32 * ks + 8 * j;
+        const bool ok = q_ok && (HDP == HD || d0 < HD);
+        /* rows and columns past the window read the window's first row */
+        qin[ks].load(p.q, (long long)(w0 + (ok ? rq : 0)) * p.row_stride + hoff + (ok ? d0 : 0));
+    }
+
+    /* ---- the window's K and V into LDS ----
+     * K: LDS chunk e (key e / 16, slot e % 16 of its 256-byte row) receives
+     * the key's 8 dims cb = slot ^ f(key % 32): a wave writes 1 KB of
+     * consecutive LDS, and the 16 lanes of a key read its row. Slots past
+     * HDP are never read and are skipped.
+     * V^T: unit (slab, row pair d, d + 1, slot jc) gathers dims d, d + 1 of
+     * the 8 keys that slot holds (one 4- or 8-byte load per key) and writes
+     * the two rows' 16-byte chunks.
+     * All loads of a part are issued before any is used; out-of-range
+     * lanes read the window's first row and write zeros. */
+    constexpr int CK = HDP / 8;
+    const int nkey = nslab * SMOL_SLAB;
+    constexpr int NKT = NS * SMOL_SLAB * 16 / WIN_TPB;              /* K chunks per thread (the build's capacity) */
+    constexpr int RK = (BF ? 16 : 8) < NKT ? (BF ? 16 : 8) : NKT;  /* K chunks a round */
+    constexpr int NVT = (NS * 8 * DT * 4 + WIN_TPB - 1) / WIN_TPB; /* V^T units per thread */
+    constexpr int RV = (BF ? 5 : 3) < NVT ? (BF ? 5 : 3) : NVT;    /* V^T units a round */
+    typedef typename std::conditional<BF, uint32_t, uint2>::type V2;
+    auto k_chunk = [&](int e, int &key, int &slot, int &rr, int &cb) __attribute__((always_inline)) {
+        key = e >> 4; slot = e & 15; rr = key & 31;
+        cb = slot ^ ((rr & 3) | (((rr >> 3) & 3) << 2));
+    };
+    auto k_issue = [&](int r0, Raw8In<BF> (&in)[RK]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < RK; u++) {
+            int key, slot, rr, cb;
+            k_chunk(tid + WIN_TPB * (r0 + u), key, slot, rr, cb);
+            const bool ok = r0 + u < NKT && key < len && cb * 8 < HD;
+            in[u].load(p.k, (long long)(w0 + (ok ? key : 0)) * p.row_stride + hoff + (ok ? cb * 8 : 0));
+        }
+    };
+    auto k_store = [&](int r0, const Raw8In<BF> (&in)[RK]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < RK; u++) {
+            int key, slot, rr, cb;
+            k_chunk(tid + WIN_TPB * (r0 + u), key, slot, rr, cb);
+            if (r0 + u >= NKT || key >= nkey || cb >= CK) continue;
+            float v[8];
+            in[u].unpack(v);
+            if (key >= len || cb * 8 >= HD) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] = 0.0f;
+            }
+            note_h_range(p.range_flag, v);
+            *reinterpret_cast<uint4 *>(smem + (key >> 5) * SLABB + rr * KROW + 16 * slot) = pack_h8(v);
+        }
+    };
+    auto v_unit = [&](int e, int &sl, int &d, int &jc, int &kb) __attribute__((always_inline)) {
+        sl = e / (32 * DT);
+        const int rem = e - sl * (32 * DT);
+        d = 2 * (rem >> 2); jc = rem & 3;
+        kb = sl * SMOL_SLAB + 8 * (jc ^ ((d >> 1) & 3));
+    };
+    auto v_issue = [&](int r0, V2 (&in)[RV][8]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < RV; u++) {
+            int sl, d, jc, kb;
+            v_unit(tid + WIN_TPB * (r0 + u), sl, d, jc, kb);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const bool ok = r0 + u < NVT && sl < nslab && kb + i < len && d < HD;
+                const long long idx = (long long)(w0 + (ok ? kb + i : 0)) * p.row_stride + hoff + (ok ? d : 0);
+                if constexpr (BF) in[u][i] = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.v) + idx);
+                else in[u][i] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const float *>(p.v) + idx);
+            }
+        }
+    };
+    auto v_store = [&](int r0, const V2 (&in)[RV][8]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < RV; u++) {
+            int sl, d, jc, kb;
+            v_unit(tid + WIN_TPB * (r0 + u), sl, d, jc, kb);
+            if (r0 + u >= NVT || sl >= nslab) continue;
+            float v0[8], v1[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const bool ok = kb + i < len && d < HD;
+                float a, b2;
+                if constexpr (BF) {
+                    a = __uint_as_float(in[u][i] << 16);
+                    b2 = __uint_as_float(in[u][i] & 0xFFFF0000u);
+                } else {
+                    a = __uint_as_float(in[u][i].x);
+                    b2 = __uint_as_float(in[u][i].y);
+                }
+                v0[i] = ok ? a : 0.0f;
+                v1[i] = ok ? b2 : 0.0f;
+            }
+            note_h_range(p.range_flag, v0);
+            note_h_range(p.range_flag, v1);
+            unsigned char *row = smem + sl * SLABB + K_BYTES + d * 64 + 16 * jc;
+            *reinterpret_cast<uint4 *>(row) = pack_h8(v0);
+            *reinterpret_cast<uint4 *>(row + 64) = pack_h8(v1);
+        }
+    };
+    {
+        /* the first rounds of K and V go out together */
+        Raw8In<BF> kin[RK];
+        V2 vin[RV][8];
+        k_issue(0, kin);
+        v_issue(0, vin);
+        k_store(0, kin);
+        v_store(0, vin);
+#pragma unroll
+        for (int r0 = RK; r0 < NKT; r0 += RK) {
+            k_issue(r0, kin);
+            k_store(r0, kin);
+        }
+#pragma unroll
+        for (int r0 = RV; r0 < NVT; r0 += RV) {
+            v_issue(r0, vin);
+            v_store(r0, vin);
+        }
+    }
+    h8 qf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+        float v[8];
+        qin[ks].unpack(v);
+        const bool ok = q_ok && (HDP == HD || 32 * ks + 8 * j < HD);
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = ok ? v[i] * p.qscale : 0.0f;
+        note_h_range(p.range_flag, v);
+        const uint4 hw = pack_h8(v);
+        qf[ks] = *reinterpret_cast<const h8 *>(&hw);
+    }
+    __syncthreads();
+
+    /* ---- the slabs: S^T = K.Q^T (lane (c, j) holds keys 8 j + 4 t + i of
+     * row c in s[t][i]), exact running max, P in fp16, O^T += V^T.P^T and
+     * the row sums against a fragment of ones ---- */
+    const int kt_row = 8 * (c >> 2) + (c & 3);
+    unsigned kfo[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) kfo[ks] = (unsigned)(kt_row * KROW + 16 * ((4 * ks + j) ^ c));
+    const unsigned vfo = (unsigned)(K_BYTES + c * 64 + 16 * (j ^ ((c >> 1) & 3)));
+    auto lds_h8 = [&](int s, unsigned off) __attribute__((always_inline)) -> h8 {
+        const uint4 x = *reinterpret_cast<const uint4 *>(smem + s * SLABB + off);
+        return *reinterpret_cast<const h8 *>(&x);
+    };
+    h8 ones;
+#pragma unroll
+    for (int i = 0; i < 8; i++) ones[i] = (_Float16)1.0f;
+    f4 o[DT], lsum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) o[dt] = f4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY;
+    /* S of slab s + 1 is formed before the softmax of slab s: the matrix
+     * cores work on it while the vector ALU does the softmax */
+    auto read_k = [&](int s, h8 (&kf)[2][KS]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) kf[tt][ks] = lds_h8(s, kfo[ks] + tt * 4 * KROW);
+    };
+    auto qk = [&](const h8 (&kf)[2][KS], f4 (&sc)[2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+            f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[tt][ks], qf[ks], acc, 0, 0, 0);
+            sc[tt] = acc;
+        }
+    };
+    h8 kf[2][KS];
+    f4 scur[2], snext[2];
+    read_k(0, kf);
+    qk(kf, scur);
+    for (int s = 0; s < nslab; s++) {
+        h8 vf[DT];
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) vf[dt] = lds_h8(s, vfo + dt * 1024);
+        const bool more = s + 1 < nslab;
+        if (more) {
+            read_k(s + 1, kf);
+            qk(kf, snext);
+        }
+        float sv[8];
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) sv[4 * tt + i] = scur[tt][i];
+        if (s * SMOL_SLAB + SMOL_SLAB > len) {
+            /* the last slab: keys past the window */
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                if (s * SMOL_SLAB + 8 * j + e >= len) sv[e] = -INFINITY;
+        }
+        float mx = sv[0];
+#pragma unroll
+        for (int e = 1; e < 8; e++) mx = fmaxf(mx, sv[e]);
+        mx = row_max4(mx);
+        const float m_new = fmaxf(m, mx); /* finite: every slab holds a key of the window */
+        const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+        m = m_new;
+        h8 pf;
+#pragma unroll
+        for (int e = 0; e < 8; e++) pf[e] = (_Float16)__builtin_amdgcn_exp2f(sv[e] - m_new);
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pf, o[dt] * alpha, 0, 0, 0);
+        lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, lsum * alpha, 0, 0, 0);
+        if (more) {
+            scur[0] = snext[0];
+            scur[1] = snext[1];
+        }
+    }
+
+    /* ---- out rows of the window (rows past it are not written) ---- */
+    if (!q_ok) return;
+    const float inv = lsum[0] > 0.0f ? 1.0f / lsum[0] : 0.0f;
+    float *orow = p.out + (long long)(w0 + rq) * p.row_stride + hoff;
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) {
+        const int d = 16 * dt + 4 * j;
+        if (HD % 16 != 0 && d >= HD) continue;
+        *reinterpret_cast<f4 *>(orow + d) = o[dt] * inv;
+    }
+}
+
+namespace {
+
+template <int HD, bool BF, int NS>
+int launch_win_v(const WinParams *wp, int n_tiles, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+    (void)n_tiles;
+    const long long units = (long long)wp->n_windows * wp->H;
+    const dim3 grid((unsigned)((units + wp->n_xcc - 1) / wp->n_xcc * wp->n_xcc * wp->tpu));
+    if (e0)
+        hipExtLaunchKernelGGL((k_attn_win<HD, BF, NS>), grid, dim3(WIN_TPB), 0, st, e0, e1, 0, *wp);
+    else
+        hipLaunchKernelGGL((k_attn_win<HD, BF, NS>), grid, dim3(WIN_TPB), 0, st, *wp);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+/* builds by window capacity: 4 or 8 slabs (the short windows of the audio
+ * and vision encoders), or as many as the LDS holds */
+template <int HD, bool BF>
+int launch_win_bf(const WinParams *wp, int n_tiles, int max_len, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+    const int ns = (max_len + SMOL_SLAB - 1) / SMOL_SLAB;
+    if (ns <= 4) return launch_win_v<HD, BF, 4>(wp, n_tiles, st, e0, e1);
+    if (ns <= 8) return launch_win_v<HD, BF, 8>(wp, n_tiles, st, e0, e1);
+    if (ns <= WinGeom<HD>::NS_MAX) return launch_win_v<HD, BF, WinGeom<HD>::NS_MAX>(wp, n_tiles, st, e0, e1);
+    return -1;
+}
+
+template <int HD>
+int launch_win_hd(const WinParams *wp, int n_tiles, int max_len, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+    return wp->in_dtype == SMOL_IN_BF16 ? launch_win_bf<HD, true>(wp, n_tiles, max_len, st, e0, e1)
+                                        : launch_win_bf<HD, false>(wp, n_tiles, max_len, st, e0, e1);
+}
+
+} // namespace
+
+/* The longest window k_attn_win holds at head_dim hd (0: not supported) */
+extern "C" int smol_win_max_keys(int hd) {
+    switch (hd) {
+    case 64: return WinGeom<64>::NS_MAX * SMOL_SLAB;
+    case 72: return WinGeom<72>::NS_MAX * SMOL_SLAB;
+    case 80: return WinGeom<80>::NS_MAX * SMOL_SLAB;
+    case 96: return WinGeom<96>::NS_MAX * SMOL_SLAB;
+    case 128: return WinGeom<128>::NS_MAX * SMOL_SLAB;
+    default: return 0;
+    }
+}
+
+/* n_tiles: 64-row tiles over all windows; max_len: the longest window;
+ * e0 / e1 (may be null): events recorded around the kernel alone */
+extern "C" int smol_launch_win(const WinParams *wp, int hd, int n_tiles, int max_len, hipStream_t st, hipEvent_t e0,
+                               hipEvent_t e1) {
+    if (n_tiles <= 0) return 0;
+    switch (hd) {
+    case 64: return launch_win_hd<64>(wp, n_tiles, max_len, st, e0, e1);
+    case 72: return launch_win_hd<72>(wp, n_tiles, max_len, st, e0, e1);
+    case 80: return launch_win_hd<80>(wp, n_tiles, max_len, st, e0, e1);
+    case 96: return launch_win_hd<96>(wp, n_tiles, max_len, st, e0, e1);
+    case 128: return launch_win_hd<128>(wp, n_tiles, max_len, st, e0, e1);
+    default: return -1;
+    }
+}

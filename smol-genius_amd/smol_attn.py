@@ -163,7 +163,8 @@ def _dev(t, what):
 
 
 # context options (include/smol_attn.h SMOL_OPT_*)
-OPT_PREFILL_KERNEL, OPT_FB_LISTS, OPT_FB_NT, OPT_DEC_SLABS, OPT_DEC_WAVES, OPT_DEC_SPLIT, OPT_XCD_CHECK = range(7)
+(OPT_PREFILL_KERNEL, OPT_FB_LISTS, OPT_FB_NT, OPT_DEC_SLABS, OPT_DEC_WAVES, OPT_DEC_SPLIT, OPT_XCD_CHECK,
+ OPT_BIDIR_WIN) = range(8)
 
 
 class Context:

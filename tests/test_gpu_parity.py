@@ -206,9 +206,44 @@ def test_window_softcap_fb(ctx, sa, oracle, window, cap, opts):
     test_window_softcap(ctx, sa, oracle, window, cap)
 
 
-def test_bidirectional_ragged_fb(ctx, sa, oracle, opts):
-    opts(sa.OPT_PREFILL_KERNEL, 1)
+@pytest.mark.parametrize("kernel", [1, 2], ids=["fb", "fa"])
+def test_bidirectional_ragged_staged(ctx, sa, oracle, opts, kernel):
+    """The pre-pass + k_attn_fb / k_attn_fa path of bidirectional calls."""
+    opts(sa.OPT_BIDIR_WIN, -1)
+    opts(sa.OPT_PREFILL_KERNEL, kernel)
     test_bidirectional_ragged(ctx, sa, oracle)
+
+
+@pytest.mark.parametrize("hd", [64, 72, 80, 96, 128])
+@pytest.mark.parametrize("bf", [False, True], ids=["f32", "bf16"])
+def test_window_kernel(ctx, sa, oracle, opts, hd, bf):
+    """k_attn_win: windows resident in LDS, read from fp32 or bf16 inputs;
+    ragged windows (1, 31, 33 keys ...), a window at the LDS limit of the
+    head_dim, and the same call through the staged path for comparison. A
+    window past the limit takes the staged path by itself."""
+    # the LDS holds 160 KB of 32-key slabs: K 32 x 256 B, V^T 16 ceil(hd / 16) x 64 B
+    lim = (160 * 1024 // (8192 + 16 * ((hd + 15) // 16) * 64)) * 32
+    assert lim >= 256
+    H = 3
+    for ws in ([0, 1, 32, 65, 130, 200], [7, 7 + lim], [0, lim + 1, lim + 40]):
+        print("window kernel", hd, bf, ws, flush=True)
+        seq = ws[-1]
+        Q, K, V = (synth.normal(70 + i, (seq, H * hd)) for i in range(3))
+        if bf:
+            Q, K, V = (synth.round_bf16(a) for a in (Q, K, V))
+        conv = (lambda a: dev(synth.f32_to_bf16_bits(a), True)) if bf else dev
+        sc = 1.0 / np.sqrt(hd)
+        want = oracle.bidirectional_attention(Q, K, V, seq, H, hd, sc, ws)
+        res = []
+        for w in (1, -1):
+            opts(sa.OPT_BIDIR_WIN, w)
+            init = synth.normal(79, (seq, H * hd)).astype(np.float32)
+            out = dev(init)
+            got = sa.bidirectional(ctx, conv(Q), conv(K), conv(V), seq, H, hd, sc, ws, out=out).cpu().numpy()
+            np.testing.assert_array_equal(got[:ws[0]], init[:ws[0]])
+            assert_parity(got[ws[0]:], want[ws[0]:], "win %d hd %d %s" % (w, hd, ws))
+            res.append(got)
+        opts(sa.OPT_BIDIR_WIN, 0)
 
 
 @pytest.mark.parametrize("case", [  # Hq, Hkv, hd, seq, window, bf16 / bidirectional window starts
@@ -222,6 +257,7 @@ def test_fb_tile_lists(ctx, sa, oracle, case, opts):
     bit for bit, and both meet the oracle."""
     print("fb lists", case, flush=True)
     opts(sa.OPT_PREFILL_KERNEL, 1)
+    opts(sa.OPT_BIDIR_WIN, -1)
     bidir = isinstance(case[3], list)
     if bidir:
         H, _, hd, ws = case
