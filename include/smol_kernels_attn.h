@@ -28,7 +28,9 @@
 extern "C" {
 #endif
 
+#ifndef SMOL_KERNELS_API
 #define SMOL_KERNELS_API __attribute__((visibility("default")))
+#endif
 
 /* smol_kernels.h:109-113, attention.c:32-77 */
 SMOL_KERNELS_API void smol_bidirectional_attention(float *out, const float *Q, const float *K,

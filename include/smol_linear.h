@@ -1,0 +1,62 @@
+/*
+ * smol_linear.h - the decoders' bf16-weight projections on the GPU
+ * (device-resident API; the reference-signature drop-ins are declared in
+ * smol_kernels_linear.h). Library: libsmol_attn.so.
+ *
+ * One call computes, for s < seq and o < out_dim,
+ *     y[s][o] = sum_i x[s][i] * W[o][i]  (+ bias[o])
+ * which is smol_linear_bf16 / smol_linear_nobias_bf16
+ * (common/kernels/matmul.c:336-358) when x and y are fp32, and the bf16
+ * decoder's bf16_linear_nobias (common/decoder/qkn_bf16_decoder.c:99-117)
+ * when x and y are bf16: fp32 sums, the result rounded to bf16 by
+ * truncation.
+ *
+ * Layouts (all row-major, rows contiguous, device pointers of the context's
+ * device): x [seq][in_dim] (fp32 or bf16), W [out_dim][in_dim] bf16,
+ * bias [out_dim] fp32 or NULL, y [seq][out_dim] (fp32 or bf16). y must not
+ * overlap x or W. Work is enqueued on the context's stream.
+ *
+ * Numerics: every product and sum is fp32 arithmetic on the exact bf16
+ * weights. For seq <= SMOL_LINEAR_GEMV_MAX_SEQ a GEMV kernel reads fp32 x
+ * as it is. Longer inputs run on bf16 MFMA (hipBLASLt): an fp32 x is split
+ * into x_hi = bf16(x) and x_lo = bf16(x - x_hi), and y = W x_hi + W x_lo
+ * with fp32 accumulation, which carries x to about 2^-17 relative. A bf16 x
+ * is used as it is.
+ *
+ * Errors: SMOL_ATTN_OK or a negative SMOL_ATTN_ERR_* status, with the
+ * message in smol_attn_last_error().
+ */
+#ifndef SMOL_LINEAR_H
+#define SMOL_LINEAR_H
+
+#include "smol_attn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* inputs of at most this many rows run on the GEMV kernel */
+#define SMOL_LINEAR_GEMV_MAX_SEQ 4
+
+/* y = x W^T (+ bias). x_dtype, y_dtype: SMOL_ATTN_F32 or SMOL_ATTN_BF16
+ * (a bf16 y is truncated from the fp32 sum). Replaces
+ * smol_linear_bf16 / smol_linear_nobias_bf16 (common/kernels/matmul.c:336-358)
+ * and bf16_linear_nobias (common/decoder/qkn_bf16_decoder.c:99-117). */
+SMOL_ATTN_API int smol_linear_dev(smol_attn_ctx *ctx, void *y, int y_dtype, const void *x, int x_dtype,
+                                  const uint16_t *w, const float *bias, int seq, int in_dim, int out_dim);
+
+/* The three projections of one decoder layer from one input:
+ * q = x Wq^T [seq][q_dim], k = x Wk^T and v = x Wv^T [seq][kv_dim], without
+ * bias. For seq <= SMOL_LINEAR_GEMV_MAX_SEQ the three run as one launch.
+ * Replaces smol_linear_nobias_bf16_qkv (common/kernels/matmul.c:308-334)
+ * and the three separate projections of qkn_decoder.c:474-476 and
+ * qkn_bf16_decoder.c:498-500 / :647-649. */
+SMOL_ATTN_API int smol_linear_qkv_dev(smol_attn_ctx *ctx, void *q, void *k, void *v, int y_dtype, const void *x,
+                                      int x_dtype, const uint16_t *wq, const uint16_t *wk, const uint16_t *wv,
+                                      int seq, int in_dim, int q_dim, int kv_dim);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -175,6 +175,28 @@ class Oracle(_Lib):
                                    [_U16, _U16, _U16, _U16, ci, ci, ci, ci, ci, cf, ci, ci, cf])
         self._bf16_norm = self._fn("bf16_rms_norm_per_head", [_U16, _F, ci, ci, ci, cf])
         self._bf16_rope = self._fn("bf16_apply_rope_interleaved", [_U16, _F, _F, ci, ci, ci])
+        self._linear = self._fn("linear_bf16", [_F, _F, _U16, _F, ci, ci, ci])
+        self._bf16_linear = self._fn("bf16_linear_nobias", [_U16, _U16, _U16, ci, ci, ci])
+
+    def linear_bf16(self, x, w_bits, bias=None):
+        """y [seq, out] = x [seq, in] W^T (+ bias), W given as bf16 bits [out, in]"""
+        x = _f32(x)
+        w = np.ascontiguousarray(w_bits, np.uint16)
+        seq, n_in = x.shape
+        n_out = w.shape[0]
+        y = np.zeros((seq, n_out), np.float32)
+        b = _f32(bias) if bias is not None else None
+        self._linear(_fp(y), _fp(x), w.ctypes.data_as(_U16), _fp(b) if b is not None else None, seq, n_in, n_out)
+        return y
+
+    def bf16_linear_nobias(self, x_bits, w_bits):
+        """bf16 bits y [seq, out] = trunc(x W^T), x [seq, in] and W [out, in] bf16 bits"""
+        x = np.ascontiguousarray(x_bits, np.uint16)
+        w = np.ascontiguousarray(w_bits, np.uint16)
+        y = np.zeros((x.shape[0], w.shape[0]), np.uint16)
+        u = lambda a: a.ctypes.data_as(_U16)  # noqa: E731
+        self._bf16_linear(u(y), u(x), u(w), x.shape[0], x.shape[1], w.shape[0])
+        return y
 
     def set_vec_generic(self, on):
         self._generic(1 if on else 0)
@@ -233,3 +255,41 @@ class RefLib(_Lib):
         if path is None:
             raise FileNotFoundError("oracle/_ref was not built")
         super().__init__(path, "smol_")
+        ci = ctypes.c_int
+        self._lin = self._fn("linear_bf16", [_F, _F, _U16, _F, ci, ci, ci])
+        self._lin_nb = self._fn("linear_nobias_bf16", [_F, _F, _U16, ci, ci, ci])
+        self._lin_qkv = self._fn("linear_nobias_bf16_qkv", [_F, _F, _F, _F, _U16, _U16, _U16, ci, ci, ci])
+        self._mm_t = self._fn("matmul_t_bf16", [_F, _F, _U16, ci, ci, ci])
+
+    def linear_bf16(self, x, w_bits, bias=None):
+        """smol_linear_bf16 / smol_linear_nobias_bf16 (matmul.c:336-358)"""
+        x = _f32(x)
+        w = np.ascontiguousarray(w_bits, np.uint16)
+        seq, n_in = x.shape
+        y = np.zeros((seq, w.shape[0]), np.float32)
+        if bias is None:
+            self._lin_nb(_fp(y), _fp(x), w.ctypes.data_as(_U16), seq, n_in, w.shape[0])
+        else:
+            b = _f32(bias)
+            self._lin(_fp(y), _fp(x), w.ctypes.data_as(_U16), _fp(b), seq, n_in, w.shape[0])
+        return y
+
+    def linear_qkv(self, x, wq, wk, wv):
+        """smol_linear_nobias_bf16_qkv (matmul.c:308-334): one token"""
+        x = _f32(x).reshape(-1)
+        ws = [np.ascontiguousarray(w, np.uint16) for w in (wq, wk, wv)]
+        q = np.zeros(ws[0].shape[0], np.float32)
+        k = np.zeros(ws[1].shape[0], np.float32)
+        v = np.zeros(ws[2].shape[0], np.float32)
+        u = lambda a: a.ctypes.data_as(_U16)  # noqa: E731
+        self._lin_qkv(_fp(q), _fp(k), _fp(v), _fp(x), u(ws[0]), u(ws[1]), u(ws[2]), x.shape[0], q.shape[0],
+                      k.shape[0])
+        return q, k, v
+
+    def matmul_t_bf16(self, a, b_bits):
+        """smol_matmul_t_bf16 (matmul.c:419-429): C [M, N] = A [M, K] B^T"""
+        a = _f32(a)
+        b = np.ascontiguousarray(b_bits, np.uint16)
+        c = np.zeros((a.shape[0], b.shape[0]), np.float32)
+        self._mm_t(_fp(c), _fp(a), b.ctypes.data_as(_U16), a.shape[0], a.shape[1], b.shape[0])
+        return c

@@ -1,5 +1,6 @@
 /*
- * smol_oracle.c - CPU oracle for the attention path. TEST INFRASTRUCTURE ONLY.
+ * smol_oracle.c - CPU oracle for the attention path and the decoders' bf16
+ * projections. TEST INFRASTRUCTURE ONLY.
  *
  * This file restates, in plain C, the reference's CPU attention, RoPE and
  * RoPE-table arithmetic so that the HIP path can be checked against it on the
@@ -30,6 +31,11 @@
  *   orc_rms_norm_per_head           common/kernels/rmsnorm.c:78-140
  *       (AVX-512 order: 16-lane fused multiply-add accumulators over the
  *       16-wide blocks, a halving tree, then a scalar tail)
+ *   orc_linear_bf16                 common/kernels/matmul.c:70-97 (smol_linear's
+ *       loops) on the exactly widened bf16 weights (matmul.c:101-106, 196-205),
+ *       as smol_linear_bf16 / smol_linear_nobias_bf16 / smol_matmul_t_bf16 run
+ *       them for seq_len > 1 (matmul.c:336-358, 419-429)
+ *   orc_bf16_linear_nobias          common/decoder/qkn_bf16_decoder.c:99-117
  *
  * Parity pins (see tests/test_oracle_*.py): golden vectors written by the
  * compiled reference (oracle/_ref), closed forms (one visible key, identical
@@ -510,4 +516,40 @@ void orc_bf16_attention_softcap(uint16_t *out, const uint16_t *q, const uint16_t
         }
     }
     free(scores);
+}
+
+/* ---------------------------------------------------------------- linear */
+
+/* matmul.c:70-97 (smol_linear without BLAS) with W widened from bf16 bits:
+ * y[s][o] = b[o] (or 0), then + x[s][i] * W[o][i] for i ascending, every
+ * product and sum rounded to fp32 (this file is built without contraction).
+ * The reference's seq_len == 1 path (bf16_matvec_fused, matmul.c:210-247)
+ * adds the same products in its SIMD order; threads there split output rows,
+ * which does not change any row's arithmetic. */
+void orc_linear_bf16(float *y, const float *x, const uint16_t *W, const float *b, int seq, int in, int out) {
+    for (int s = 0; s < seq; s++) {
+        const float *xr = x + (size_t)s * in;
+        float *yr = y + (size_t)s * out;
+        for (int o = 0; o < out; o++) {
+            const uint16_t *wr = W + (size_t)o * in;
+            float sum = b ? b[o] : 0.0f;
+            for (int i = 0; i < in; i++) sum += xr[i] * orc_bf16_to_f32(wr[i]);
+            yr[o] = sum;
+        }
+    }
+}
+
+/* qkn_bf16_decoder.c:99-117 (bf16_linear_nobias): bf16 x and W widened,
+ * sum from 0 over i ascending in fp32, the result truncated to bf16 */
+void orc_bf16_linear_nobias(uint16_t *y, const uint16_t *x, const uint16_t *W, int seq, int in, int out) {
+    for (int s = 0; s < seq; s++) {
+        const uint16_t *xr = x + (size_t)s * in;
+        uint16_t *yr = y + (size_t)s * out;
+        for (int o = 0; o < out; o++) {
+            const uint16_t *wr = W + (size_t)o * in;
+            float sum = 0.0f;
+            for (int i = 0; i < in; i++) sum += orc_bf16_to_f32(xr[i]) * orc_bf16_to_f32(wr[i]);
+            yr[o] = orc_f32_to_bf16_trunc(sum);
+        }
+    }
 }

@@ -183,7 +183,18 @@ struct smol_attn_ctx {
     std::vector<hipEvent_t> event_pool;
     double t_ms[SMOL_TIMING_KINDS] = {0, 0, 0};
     int t_count[SMOL_TIMING_KINDS] = {0, 0, 0};
+    /* state of the projection GEMMs (linear.hip), released with the context */
+    void *lin = nullptr;
+    void (*lin_free)(void *) = nullptr;
 };
+
+/* for linear.hip: the context's device, the slot of its GEMM state and that
+ * state's destructor (called by smol_attn_ctx_destroy) */
+extern "C" int smol_internal_ctx_device(smol_attn_ctx *ctx) { return ctx->device; }
+extern "C" void **smol_internal_ctx_lin(smol_attn_ctx *ctx, void (***freer)(void *)) {
+    *freer = &ctx->lin_free;
+    return &ctx->lin;
+}
 
 static hipEvent_t pool_event(smol_attn_ctx *ctx) {
     if (!ctx->event_pool.empty()) {
@@ -209,6 +220,14 @@ static int timing_begin(smol_attn_ctx *ctx, int kind) {
 
 static hipEvent_t mark_a(smol_attn_ctx *ctx, int mark) { return mark >= 0 ? ctx->marks[mark].a : nullptr; }
 static hipEvent_t mark_b(smol_attn_ctx *ctx, int mark) { return mark >= 0 ? ctx->marks[mark].b : nullptr; }
+
+/* for linear.hip: the pair of events that brackets one timed launch of the
+ * given kind (both null when timing is off) */
+extern "C" void smol_internal_timing_events(smol_attn_ctx *ctx, int kind, hipEvent_t *a, hipEvent_t *b) {
+    const int mk = timing_begin(ctx, kind);
+    *a = mark_a(ctx, mk);
+    *b = mark_b(ctx, mk);
+}
 
 /* Tables and caches keep their own device and stream, so destroying them
  * does not touch the context (which may already be gone). */
@@ -345,6 +364,7 @@ extern "C" int smol_attn_ctx_destroy(smol_attn_ctx *ctx) {
         hipEventDestroy(m.b);
     }
     for (hipEvent_t e : ctx->event_pool) hipEventDestroy(e);
+    if (ctx->lin && ctx->lin_free) ctx->lin_free(ctx->lin);
     if (ctx->own_stream) hipStreamDestroy(ctx->stream);
     delete ctx;
     return SMOL_ATTN_OK;
@@ -1568,6 +1588,14 @@ smol_attn_ctx *legacy_ctx(const char *fn) {
     if (!g_legacy.ctx && smol_attn_ctx_create(0, nullptr, &g_legacy.ctx) != SMOL_ATTN_OK) legacy_abort(fn);
     return g_legacy.ctx;
 }
+
+} // namespace
+
+/* for linear.hip's drop-ins: the calling thread's context of the
+ * reference-signature entry points (created on first use, device 0) */
+extern "C" smol_attn_ctx *smol_internal_legacy_ctx(const char *fn) { return legacy_ctx(fn); }
+
+namespace {
 
 void legacy_upload(const char *fn, DevBuf &b, const void *h, size_t bytes) {
     smol_attn_ctx *ctx = legacy_ctx(fn);

@@ -1,0 +1,771 @@
+/*
+ * linear.hip - the decoders' bf16-weight projections on gfx950
+ * (include/smol_linear.h, include/smol_kernels_linear.h).
+ *
+ *   y[s][o] = sum_i x[s][i] W[o][i] (+ b[o])
+ *     common/kernels/matmul.c:70-97   smol_linear (the loops the seq > 1 path runs)
+ *     common/kernels/matmul.c:210-247 bf16_matvec_fused / _threaded (seq == 1)
+ *     common/kernels/matmul.c:250-334 the fused Q/K/V matvec
+ *     common/decoder/qkn_bf16_decoder.c:99-117 bf16_linear_nobias (bf16 in, truncated bf16 out)
+ *
+ * Two device paths:
+ *   k_gemv   seq <= SMOL_LINEAR_GEMV_MAX_SEQ (decode). HBM-bound: every
+ *            weight byte is read once. A workgroup owns GEMV_R consecutive
+ *            output rows (of the joint row space of up to three weight
+ *            segments, so Q/K/V is one launch) and `kp` waves that split
+ *            in_dim; lane l of wave w reads the 16-byte chunks
+ *            w*64 + l + j*64*kp of each of its rows, and the x chunk it
+ *            multiplies them with (x stays L1/L2 resident). Every load of a
+ *            step is issued before the first FMA. Sums: per-lane fp32, then
+ *            a wave all-reduce (cross-row swaps + DPP row rotations), then
+ *            the kp waves' totals in a fixed order through LDS.
+ *   GEMM     longer inputs: hipBLASLt bf16 x bf16 -> fp32 on MFMA. An fp32
+ *            x is first split by k_split_hilo into x_hi = bf16_rne(x) and
+ *            x_lo = bf16_rne(x - x_hi), and y = W x_hi + W x_lo (second
+ *            product accumulates with beta = 1): x is carried to ~2^-17
+ *            relative, the weights are exact. A bias is written into y
+ *            first (k_bias_rows) and the first product adds to it.
+ *            hipBLASLt is column-major: y^T (out x seq, ld out) =
+ *            op(A) B with A = W as an (in x out, ld in) matrix and op = T,
+ *            B = x as (in x seq, ld in).
+ */
+#include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
+
+#include <limits.h>
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <unordered_map>
+#include <vector>
+
+#include "attn_device.h"
+#include "smol_kernels_linear.h"
+#include "smol_linear.h"
+
+extern "C" int smol_internal_fail(int code, const char *msg);
+extern "C" int smol_internal_ctx_device(smol_attn_ctx *ctx);
+extern "C" void **smol_internal_ctx_lin(smol_attn_ctx *ctx, void (***freer)(void *));
+extern "C" void smol_internal_timing_events(smol_attn_ctx *ctx, int kind, hipEvent_t *a, hipEvent_t *b);
+extern "C" smol_attn_ctx *smol_internal_legacy_ctx(const char *fn);
+extern "C" int smol_launch_to_bf16_trunc(const float *x, uint16_t *y, long long n, hipStream_t st);
+
+#define GEMV_R 4      /* output rows per workgroup */
+#define GEMV_U 2      /* chunks of 8 elements per lane per step */
+#define GEMV_MAX_KP 8 /* waves per workgroup along in_dim */
+#define GEMV_SEGS 3
+#define LIN_TIMING_KIND 2 /* the context's "other" timing kind */
+
+struct GemvSeg {
+    const uint16_t *w;  /* [out][in] bf16 */
+    const float *bias;  /* [out] or null */
+    void *y;            /* [seq][out] */
+    int out;
+    int row0;           /* first row of this segment in the joint row space (INT_MAX: unused) */
+};
+
+struct GemvParams {
+    const void *x; /* [seq][in] */
+    int in;
+    int rows;      /* rows of all segments */
+    int kp;        /* waves per workgroup */
+    GemvSeg seg[GEMV_SEGS];
+};
+
+/* ---------------------------------------------------------------- kernels */
+
+/* sum over the 64 lanes, the total in every lane */
+__device__ __forceinline__ float wave_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+    /* DPP row_ror:8, 4, 2, 1 (rotations within each row of 16 lanes) */
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x122, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xF, 0xF, false));
+    return v;
+}
+
+/* segment of joint row `row` (uniform when row is) */
+__device__ __forceinline__ int seg_of(const GemvParams &p, int row) {
+    return (row >= p.seg[1].row0) + (row >= p.seg[2].row0);
+}
+
+/* VEC: in % 8 == 0 and 16-byte aligned x / W (every chunk one 16-byte
+ * load); otherwise elementwise loads. Loads past a row or past x read
+ * zero (buffer range checks), so no branch guards them. */
+template <int SEQ, bool XBF, bool YBF, bool VEC>
+__global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
+    __shared__ float red[GEMV_MAX_KP][GEMV_R * SEQ];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kp = p.kp;
+    const int in = p.in;
+    const int row_base = blockIdx.x * GEMV_R;
+
+    rsrc_t wr[GEMV_R];
+#pragma unroll
+    for (int r = 0; r < GEMV_R; r++) {
+        const int row = row_base + r;
+        const int sg = seg_of(p, row);
+        const uint16_t *w = sg == 0 ? p.seg[0].w : sg == 1 ? p.seg[1].w : p.seg[2].w;
+        const int r0 = sg == 0 ? p.seg[0].row0 : sg == 1 ? p.seg[1].row0 : p.seg[2].row0;
+        const bool live = row < p.rows;
+        wr[r] = make_rsrc(live ? w + (long long)(row - r0) * in : p.seg[0].w, live ? (long long)in * 2 : 0);
+    }
+    const rsrc_t xr = make_rsrc(p.x, (long long)SEQ * in * (XBF ? 2 : 4));
+
+    float acc[GEMV_R][SEQ];
+#pragma unroll
+    for (int r = 0; r < GEMV_R; r++)
+#pragma unroll
+        for (int s = 0; s < SEQ; s++) acc[r][s] = 0.0f;
+
+    const int C = (in + 7) >> 3; /* chunks per row */
+    const int stride = 64 * kp;
+    for (int c0 = wave * 64; c0 < C; c0 += stride * GEMV_U) {
+        float wf[GEMV_U][GEMV_R][8];
+        float xf[GEMV_U][SEQ][8];
+        if constexpr (VEC) {
+            uint4 wv[GEMV_U][GEMV_R];
+            uint4 xv[GEMV_U][SEQ][XBF ? 1 : 2];
+#pragma unroll
+            for (int u = 0; u < GEMV_U; u++) {
+                const int c = c0 + lane + u * stride;
+                const bool ok = c < C;
+#pragma unroll
+                for (int r = 0; r < GEMV_R; r++) wv[u][r] = bload(wr[r], ok ? (unsigned)c * 16u : OOB_OFF, 0);
+#pragma unroll
+                for (int s = 0; s < SEQ; s++) {
+                    if constexpr (XBF) {
+                        xv[u][s][0] = bload(xr, ok ? (unsigned)(s * in + c * 8) * 2u : OOB_OFF, 0);
+                    } else {
+                        const unsigned o = (unsigned)(s * in + c * 8) * 4u;
+                        xv[u][s][0] = bload(xr, ok ? o : OOB_OFF, 0);
+                        xv[u][s][1] = bload(xr, ok ? o + 16u : OOB_OFF, 0);
+                    }
+                }
+            }
+            /* keeps every load of the step ahead of the first use: the
+             * scheduler would otherwise sink loads below waits to save
+             * registers, turning one memory round trip into several */
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < GEMV_U; u++) {
+#pragma unroll
+                for (int r = 0; r < GEMV_R; r++) unpack_bf16x8(wv[u][r], wf[u][r]);
+#pragma unroll
+                for (int s = 0; s < SEQ; s++) {
+                    if constexpr (XBF) {
+                        unpack_bf16x8(xv[u][s][0], xf[u][s]);
+                    } else {
+                        const uint4 a = xv[u][s][0], b = xv[u][s][1];
+                        const uint32_t t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                        for (int e = 0; e < 8; e++) xf[u][s][e] = __uint_as_float(t[e]);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < GEMV_U; u++) {
+                const int c = c0 + lane + u * stride;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int i = c * 8 + e;
+                    const bool ok = c < C && i < in;
+#pragma unroll
+                    for (int r = 0; r < GEMV_R; r++) {
+                        const unsigned short h = __builtin_amdgcn_raw_buffer_load_b16(
+                            wr[r], ok ? (unsigned)i * 2u : OOB_OFF, 0, 0);
+                        wf[u][r][e] = __uint_as_float((uint32_t)h << 16);
+                    }
+#pragma unroll
+                    for (int s = 0; s < SEQ; s++) {
+                        if constexpr (XBF) {
+                            const unsigned short h = __builtin_amdgcn_raw_buffer_load_b16(
+                                xr, ok ? (unsigned)(s * in + i) * 2u : OOB_OFF, 0, 0);
+                            xf[u][s][e] = __uint_as_float((uint32_t)h << 16);
+                        } else {
+                            xf[u][s][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                                xr, ok ? (unsigned)(s * in + i) * 4u : OOB_OFF, 0, 0));
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < GEMV_U; u++)
+#pragma unroll
+            for (int r = 0; r < GEMV_R; r++)
+#pragma unroll
+                for (int s = 0; s < SEQ; s++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[r][s] = fmaf(wf[u][r][e], xf[u][s][e], acc[r][s]);
+    }
+
+    /* lane i = s * GEMV_R + r ends with the total of (row r, input s) */
+    float mine = 0.0f;
+#pragma unroll
+    for (int r = 0; r < GEMV_R; r++)
+#pragma unroll
+        for (int s = 0; s < SEQ; s++) {
+            const float t = wave_sum(acc[r][s]);
+            if (lane == s * GEMV_R + r) mine = t;
+        }
+    if (kp > 1) {
+        if (lane < GEMV_R * SEQ) red[wave][lane] = mine;
+        __syncthreads();
+        if (wave != 0) return;
+        if (lane < GEMV_R * SEQ) {
+            mine = 0.0f;
+            for (int w = 0; w < kp; w++) mine += red[w][lane];
+        }
+    }
+    if (lane < GEMV_R * SEQ) {
+        const int r = lane % GEMV_R, s = lane / GEMV_R;
+        const int row = row_base + r;
+        if (row < p.rows) {
+            /* selects, not p.seg[sg]: a lane-dependent index into the kernel
+             * arguments would be lowered through scratch memory */
+            const int sg = seg_of(p, row);
+            const int r0 = sg == 0 ? p.seg[0].row0 : sg == 1 ? p.seg[1].row0 : p.seg[2].row0;
+            const int out = sg == 0 ? p.seg[0].out : sg == 1 ? p.seg[1].out : p.seg[2].out;
+            const float *bias = sg == 0 ? p.seg[0].bias : sg == 1 ? p.seg[1].bias : p.seg[2].bias;
+            void *y = sg == 0 ? p.seg[0].y : sg == 1 ? p.seg[1].y : p.seg[2].y;
+            const int o = row - r0;
+            const float v = mine + (bias ? bias[o] : 0.0f);
+            if constexpr (YBF)
+                static_cast<uint16_t *>(y)[(long long)s * out + o] = (uint16_t)(__float_as_uint(v) >> 16);
+            else
+                static_cast<float *>(y)[(long long)s * out + o] = v;
+        }
+    }
+}
+
+/* x fp32 -> x_hi = bf16_rne(x), x_lo = bf16_rne(x - x_hi); 8 elements per
+ * thread. A finite x whose rounding overflows keeps the truncated hi; a
+ * non-finite x goes to hi with lo = 0, so it reaches y as it would in fp32. */
+__device__ __forceinline__ void split1(float x, uint16_t &h, uint16_t &l) {
+    const bool fin = fabsf(x) <= 3.402823466e38f;
+    uint16_t hb = f32_to_bf16(x);
+    if (fin && !(fabsf(__uint_as_float((uint32_t)hb << 16)) <= 3.402823466e38f))
+        hb = (uint16_t)(__float_as_uint(x) >> 16);
+    h = hb;
+    l = fin ? f32_to_bf16(x - __uint_as_float((uint32_t)hb << 16)) : (uint16_t)0;
+}
+
+__global__ __launch_bounds__(256) void k_split_hilo(const float *x, uint16_t *hi, uint16_t *lo, long long n,
+                                                    bool vec) {
+    const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+    const long long i0 = t * 8;
+    if (i0 >= n) return;
+    if (vec && i0 + 8 <= n) {
+        const float4 a = *reinterpret_cast<const float4 *>(x + i0);
+        const float4 b = *reinterpret_cast<const float4 *>(x + i0 + 4);
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        uint16_t h[8], l[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) split1(v[e], h[e], l[e]);
+        uint4 H, L;
+        H.x = h[0] | ((uint32_t)h[1] << 16); H.y = h[2] | ((uint32_t)h[3] << 16);
+        H.z = h[4] | ((uint32_t)h[5] << 16); H.w = h[6] | ((uint32_t)h[7] << 16);
+        L.x = l[0] | ((uint32_t)l[1] << 16); L.y = l[2] | ((uint32_t)l[3] << 16);
+        L.z = l[4] | ((uint32_t)l[5] << 16); L.w = l[6] | ((uint32_t)l[7] << 16);
+        *reinterpret_cast<uint4 *>(hi + i0) = H;
+        *reinterpret_cast<uint4 *>(lo + i0) = L;
+    } else {
+        for (long long i = i0; i < n; i++) split1(x[i], hi[i], lo[i]);
+    }
+}
+
+/* y[s][o] = b[o] (or 0) */
+__global__ __launch_bounds__(256) void k_bias_rows(float *y, const float *b, int seq, int out) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long long)seq * out) return;
+    y[i] = b ? b[i % out] : 0.0f;
+}
+
+/* ------------------------------------------------------------------ host */
+
+namespace {
+
+int lfail(int code, const char *msg) { return smol_internal_fail(code, msg); }
+
+#define LHIP(expr)                                                                          \
+    do {                                                                                    \
+        hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess) return lfail(SMOL_ATTN_ERR_DEVICE, hipGetErrorString(e_));    \
+    } while (0)
+
+#define LBLAS(expr)                                                                         \
+    do {                                                                                    \
+        hipblasStatus_t s_ = (expr);                                                        \
+        if (s_ != HIPBLAS_STATUS_SUCCESS) {                                                 \
+            char m_[160];                                                                   \
+            snprintf(m_, sizeof m_, "hipBLASLt: %s failed (status %d)", #expr, (int)s_);    \
+            return lfail(SMOL_ATTN_ERR_DEVICE, m_);                                         \
+        }                                                                                   \
+    } while (0)
+
+struct Buf {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+/* grows a device buffer (contents not kept); the stream is drained first */
+int reserve(Buf &b, size_t bytes, hipStream_t st) {
+    if (bytes <= b.cap) return 0;
+    size_t want = std::max(bytes, b.cap + b.cap / 2);
+    want = (want + 4095) & ~(size_t)4095;
+    if (b.p) {
+        LHIP(hipStreamSynchronize(st));
+        LHIP(hipFree(b.p));
+        b.p = nullptr;
+        b.cap = 0;
+    }
+    LHIP(hipMalloc(&b.p, want));
+    b.cap = want;
+    return 0;
+}
+
+/* one GEMM shape: y^T (out x seq) = W (in x out)^T x (in x seq) */
+struct Plan {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+    size_t ws = 0;
+};
+
+#define LIN_WS_BYTES ((size_t)64 << 20)
+
+struct LinState {
+    int device = 0;
+    hipblasLtHandle_t h = nullptr;
+    void *ws = nullptr;
+    Buf xs;  /* x_hi then x_lo, bf16 */
+    Buf y32; /* fp32 result of a bf16-output GEMM */
+    std::map<std::tuple<int, int, int>, Plan> plans;
+};
+
+void lin_free(void *p) {
+    LinState *L = static_cast<LinState *>(p);
+    hipSetDevice(L->device);
+    for (auto &kv : L->plans) {
+        Plan &pl = kv.second;
+        if (pl.a) hipblasLtMatrixLayoutDestroy(pl.a);
+        if (pl.b) hipblasLtMatrixLayoutDestroy(pl.b);
+        if (pl.c) hipblasLtMatrixLayoutDestroy(pl.c);
+        if (pl.desc) hipblasLtMatmulDescDestroy(pl.desc);
+    }
+    if (L->h) hipblasLtDestroy(L->h);
+    if (L->ws) hipFree(L->ws);
+    if (L->xs.p) hipFree(L->xs.p);
+    if (L->y32.p) hipFree(L->y32.p);
+    delete L;
+}
+
+/* the context's GEMM state, created on first use */
+int lin_state(smol_attn_ctx *ctx, LinState **out) {
+    void (**freer)(void *) = nullptr;
+    void **slot = smol_internal_ctx_lin(ctx, &freer);
+    if (!*slot) {
+        LinState *L = new LinState();
+        L->device = smol_internal_ctx_device(ctx);
+        if (hipblasLtCreate(&L->h) != HIPBLAS_STATUS_SUCCESS) {
+            delete L;
+            return lfail(SMOL_ATTN_ERR_DEVICE, "hipBLASLt: hipblasLtCreate failed");
+        }
+        if (hipMalloc(&L->ws, LIN_WS_BYTES) != hipSuccess) {
+            hipblasLtDestroy(L->h);
+            delete L;
+            return lfail(SMOL_ATTN_ERR_NOMEM, "linear: workspace allocation failed");
+        }
+        *slot = L;
+        *freer = lin_free;
+    }
+    *out = static_cast<LinState *>(*slot);
+    return 0;
+}
+
+int get_plan(LinState *L, int seq, int in, int out, Plan **res) {
+    const auto key = std::make_tuple(seq, in, out);
+    auto it = L->plans.find(key);
+    if (it != L->plans.end()) {
+        *res = &it->second;
+        return 0;
+    }
+    Plan pl;
+    auto drop = [&]() {
+        if (pl.a) hipblasLtMatrixLayoutDestroy(pl.a);
+        if (pl.b) hipblasLtMatrixLayoutDestroy(pl.b);
+        if (pl.c) hipblasLtMatrixLayoutDestroy(pl.c);
+        if (pl.desc) hipblasLtMatmulDescDestroy(pl.desc);
+    };
+    hipblasLtMatmulPreference_t pref = nullptr;
+    hipblasLtMatmulHeuristicResult_t heur[1];
+    int n_found = 0;
+    const hipblasOperation_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N;
+    const uint64_t ws = LIN_WS_BYTES;
+    hipblasStatus_t st = hipblasLtMatmulDescCreate(&pl.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
+    if (st == HIPBLAS_STATUS_SUCCESS)
+        st = hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof opT);
+    if (st == HIPBLAS_STATUS_SUCCESS)
+        st = hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof opN);
+    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&pl.a, HIP_R_16BF, in, out, in);
+    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&pl.b, HIP_R_16BF, in, seq, in);
+    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&pl.c, HIP_R_32F, out, seq, out);
+    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatmulPreferenceCreate(&pref);
+    if (st == HIPBLAS_STATUS_SUCCESS)
+        st = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof ws);
+    if (st == HIPBLAS_STATUS_SUCCESS)
+        st = hipblasLtMatmulAlgoGetHeuristic(L->h, pl.desc, pl.a, pl.b, pl.c, pl.c, pref, 1, heur, &n_found);
+    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+    if (st == HIPBLAS_STATUS_NOT_SUPPORTED || (st == HIPBLAS_STATUS_SUCCESS && n_found < 1)) {
+        drop();
+        return 1; /* no algorithm for this shape */
+    }
+    if (st != HIPBLAS_STATUS_SUCCESS) {
+        drop();
+        char m[160];
+        snprintf(m, sizeof m, "hipBLASLt: GEMM set-up failed for seq %d, in %d, out %d (status %d)", seq, in, out,
+                 (int)st);
+        return lfail(SMOL_ATTN_ERR_DEVICE, m);
+    }
+    pl.algo = heur[0].algo;
+    pl.ws = heur[0].workspaceSize;
+    auto ins = L->plans.emplace(key, pl);
+    *res = &ins.first->second;
+    return 0;
+}
+
+int gemm(LinState *L, hipStream_t st, float *y, const uint16_t *w, const uint16_t *xb, int seq, int in, int out,
+         float beta) {
+    Plan *pl = nullptr;
+    if (int rc = get_plan(L, seq, in, out, &pl)) return rc < 0 ? rc : lfail(SMOL_ATTN_ERR_UNSUPPORTED, "no GEMM");
+    const float alpha = 1.0f;
+    LBLAS(hipblasLtMatmul(L->h, pl->desc, &alpha, w, pl->a, xb, pl->b, &beta, y, pl->c, y, pl->c, &pl->algo, L->ws,
+                          pl->ws, st));
+    return 0;
+}
+
+int launch_bias(float *y, const float *b, int seq, int out, hipStream_t st) {
+    const long long n = (long long)seq * out;
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(k_bias_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y, b, seq, out);
+    LHIP(hipGetLastError());
+    return 0;
+}
+
+template <int SEQ, bool XBF, bool YBF>
+int launch_gemv_v(const GemvParams &p, bool vec, hipStream_t st) {
+    const dim3 grid((unsigned)((p.rows + GEMV_R - 1) / GEMV_R)), block(64 * p.kp);
+    if (vec)
+        hipLaunchKernelGGL((k_gemv<SEQ, XBF, YBF, true>), grid, block, 0, st, p);
+    else
+        hipLaunchKernelGGL((k_gemv<SEQ, XBF, YBF, false>), grid, block, 0, st, p);
+    LHIP(hipGetLastError());
+    return 0;
+}
+
+template <int SEQ>
+int launch_gemv_s(const GemvParams &p, bool xbf, bool ybf, bool vec, hipStream_t st) {
+    if (xbf) return ybf ? launch_gemv_v<SEQ, true, true>(p, vec, st) : launch_gemv_v<SEQ, true, false>(p, vec, st);
+    return ybf ? launch_gemv_v<SEQ, false, true>(p, vec, st) : launch_gemv_v<SEQ, false, false>(p, vec, st);
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+/* one GEMV launch over n_seg weight segments */
+int run_gemv(smol_attn_ctx *ctx, hipStream_t st, const void *x, bool xbf, bool ybf, int seq, int in, int n_seg,
+             const GemvSeg *segs) {
+    GemvParams p{};
+    p.x = x;
+    p.in = in;
+    int rows = 0;
+    bool vec = (in % 8) == 0 && aligned16(x);
+    for (int i = 0; i < GEMV_SEGS; i++) {
+        if (i < n_seg) {
+            p.seg[i] = segs[i];
+            p.seg[i].row0 = rows;
+            rows += segs[i].out;
+            vec = vec && aligned16(segs[i].w);
+        } else {
+            p.seg[i] = GemvSeg{segs[0].w, nullptr, nullptr, 0, INT_MAX};
+        }
+    }
+    p.rows = rows;
+    const int chunks = (in + 7) / 8;
+    p.kp = std::max(1, std::min(GEMV_MAX_KP, (chunks + 64 * GEMV_U - 1) / (64 * GEMV_U)));
+    if (rows <= 0) return 0;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    smol_internal_timing_events(ctx, LIN_TIMING_KIND, &e0, &e1);
+    if (e0) LHIP(hipEventRecord(e0, st));
+    int rc;
+    switch (seq) {
+    case 1: rc = launch_gemv_s<1>(p, xbf, ybf, vec, st); break;
+    case 2: rc = launch_gemv_s<2>(p, xbf, ybf, vec, st); break;
+    case 3: rc = launch_gemv_s<3>(p, xbf, ybf, vec, st); break;
+    default: rc = launch_gemv_s<4>(p, xbf, ybf, vec, st); break;
+    }
+    if (rc) return rc;
+    if (e1) LHIP(hipEventRecord(e1, st));
+    return 0;
+}
+
+/* y = x W^T (+ bias) as GEMV launches over blocks of up to
+ * SMOL_LINEAR_GEMV_MAX_SEQ rows (in_dim 0, and shapes hipBLASLt has no
+ * kernel for) */
+int run_gemv_rows(smol_attn_ctx *ctx, hipStream_t st, void *y, bool ybf, const void *x, bool xbf,
+                  const uint16_t *w, const float *bias, int seq, int in, int out) {
+    const size_t xe = xbf ? 2 : 4, ye = ybf ? 2 : 4;
+    for (int s0 = 0; s0 < seq; s0 += SMOL_LINEAR_GEMV_MAX_SEQ) {
+        const int n = std::min(SMOL_LINEAR_GEMV_MAX_SEQ, seq - s0);
+        const GemvSeg sg{w, bias, static_cast<char *>(y) + (size_t)s0 * out * ye, out, 0};
+        const void *xs = x ? static_cast<const char *>(x) + (size_t)s0 * in * xe : nullptr;
+        if (int rc = run_gemv(ctx, st, xs, xbf, ybf, n, in, 1, &sg)) return rc;
+    }
+    return 0;
+}
+
+/* the GEMM path for one weight: y (fp32 or bf16) = x W^T (+ bias) */
+int run_gemm(smol_attn_ctx *ctx, LinState *L, hipStream_t st, void *y, bool ybf, const void *x, bool xbf,
+             const uint16_t *w, const float *bias, int seq, int in, int out) {
+    {
+        Plan *pl = nullptr;
+        const int rc = get_plan(L, seq, in, out, &pl);
+        if (rc < 0) return rc;
+        if (rc > 0) return run_gemv_rows(ctx, st, y, ybf, x, xbf, w, bias, seq, in, out);
+    }
+    const size_t ny = (size_t)seq * out;
+    float *y32 = static_cast<float *>(y);
+    if (ybf) {
+        if (int rc = reserve(L->y32, ny * 4, st)) return rc;
+        y32 = static_cast<float *>(L->y32.p);
+    }
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    smol_internal_timing_events(ctx, LIN_TIMING_KIND, &e0, &e1);
+    if (e0) LHIP(hipEventRecord(e0, st));
+    const uint16_t *xh = static_cast<const uint16_t *>(x), *xl = nullptr;
+    if (!xbf) {
+        const long long n = (long long)seq * in;
+        const long long lo_off = (n + 127) & ~127LL; /* x_lo starts 256-byte aligned */
+        if (int rc = reserve(L->xs, (size_t)(lo_off + n) * 2, st)) return rc;
+        uint16_t *h = static_cast<uint16_t *>(L->xs.p);
+        uint16_t *l = h + lo_off;
+        const long long threads = (n + 7) / 8;
+        hipLaunchKernelGGL(k_split_hilo, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                           static_cast<const float *>(x), h, l, n, aligned16(x));
+        LHIP(hipGetLastError());
+        xh = h;
+        xl = l;
+    }
+    if (bias)
+        if (int rc = launch_bias(y32, bias, seq, out, st)) return rc;
+    if (int rc = gemm(L, st, y32, w, xh, seq, in, out, bias ? 1.0f : 0.0f)) return rc;
+    if (xl)
+        if (int rc = gemm(L, st, y32, w, xl, seq, in, out, 1.0f)) return rc;
+    if (e1) LHIP(hipEventRecord(e1, st));
+    if (ybf && smol_launch_to_bf16_trunc(y32, static_cast<uint16_t *>(y), (long long)ny, st))
+        return lfail(SMOL_ATTN_ERR_DEVICE, "linear: truncation launch failed");
+    return 0;
+}
+
+int check_dtype(int t) { return t == SMOL_ATTN_F32 || t == SMOL_ATTN_BF16; }
+
+}  // namespace
+
+extern "C" int smol_linear_dev(smol_attn_ctx *ctx, void *y, int y_dtype, const void *x, int x_dtype,
+                               const uint16_t *w, const float *bias, int seq, int in_dim, int out_dim) {
+    if (!ctx) return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_dev: null context");
+    if (!check_dtype(x_dtype) || !check_dtype(y_dtype)) return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_dev: dtype");
+    if (seq < 0 || in_dim < 0 || out_dim < 0) return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_dev: negative size");
+    if (seq == 0 || out_dim == 0) return SMOL_ATTN_OK;
+    if (!y || (in_dim > 0 && (!x || !w))) return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_dev: null pointer");
+    if ((long long)seq * in_dim > INT_MAX / 4 || (long long)seq * out_dim > INT_MAX / 4 ||
+        (long long)out_dim * in_dim > (1LL << 40))
+        return lfail(SMOL_ATTN_ERR_UNSUPPORTED, "smol_linear_dev: sizes beyond the supported range");
+    LHIP(hipSetDevice(smol_internal_ctx_device(ctx)));
+    hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
+    const bool xbf = x_dtype == SMOL_ATTN_BF16, ybf = y_dtype == SMOL_ATTN_BF16;
+    if (seq <= SMOL_LINEAR_GEMV_MAX_SEQ || in_dim == 0)
+        return run_gemv_rows(ctx, st, y, ybf, x, xbf, w, bias, seq, in_dim, out_dim);
+    LinState *L = nullptr;
+    if (int rc = lin_state(ctx, &L)) return rc;
+    return run_gemm(ctx, L, st, y, ybf, x, xbf, w, bias, seq, in_dim, out_dim);
+}
+
+extern "C" int smol_linear_qkv_dev(smol_attn_ctx *ctx, void *q, void *k, void *v, int y_dtype, const void *x,
+                                   int x_dtype, const uint16_t *wq, const uint16_t *wk, const uint16_t *wv, int seq,
+                                   int in_dim, int q_dim, int kv_dim) {
+    if (!ctx) return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_qkv_dev: null context");
+    if (!check_dtype(x_dtype) || !check_dtype(y_dtype)) return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_qkv_dev: dtype");
+    if (seq < 0 || in_dim < 0 || q_dim < 0 || kv_dim < 0)
+        return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_qkv_dev: negative size");
+    if (seq > SMOL_LINEAR_GEMV_MAX_SEQ || in_dim == 0) {
+        if (int rc = smol_linear_dev(ctx, q, y_dtype, x, x_dtype, wq, nullptr, seq, in_dim, q_dim)) return rc;
+        if (int rc = smol_linear_dev(ctx, k, y_dtype, x, x_dtype, wk, nullptr, seq, in_dim, kv_dim)) return rc;
+        return smol_linear_dev(ctx, v, y_dtype, x, x_dtype, wv, nullptr, seq, in_dim, kv_dim);
+    }
+    if (seq == 0 || (q_dim == 0 && kv_dim == 0)) return SMOL_ATTN_OK;
+    if (!x || (q_dim && (!q || !wq)) || (kv_dim && (!k || !v || !wk || !wv)))
+        return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_qkv_dev: null pointer");
+    if ((long long)seq * in_dim > INT_MAX / 4 || (long long)q_dim + 2LL * kv_dim > INT_MAX / 4)
+        return lfail(SMOL_ATTN_ERR_UNSUPPORTED, "smol_linear_qkv_dev: sizes beyond the supported range");
+    LHIP(hipSetDevice(smol_internal_ctx_device(ctx)));
+    hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
+    GemvSeg segs[GEMV_SEGS];
+    int n = 0;
+    if (q_dim) segs[n++] = GemvSeg{wq, nullptr, q, q_dim, 0};
+    if (kv_dim) {
+        segs[n++] = GemvSeg{wk, nullptr, k, kv_dim, 0};
+        segs[n++] = GemvSeg{wv, nullptr, v, kv_dim, 0};
+    }
+    return run_gemv(ctx, st, x, x_dtype == SMOL_ATTN_BF16, y_dtype == SMOL_ATTN_BF16, seq, in_dim, n, segs);
+}
+
+/* ------------------------------------------------- reference-signature drop-ins */
+
+namespace {
+
+[[noreturn]] void dropin_abort(const char *fn) {
+    fprintf(stderr, "smol_attn: %s failed on the GPU: %s\n", fn, smol_attn_last_error());
+    abort();
+}
+
+/* device copies of weights kept by (host pointer, elements) when
+ * SMOL_BF16_CACHE_MB is set (common/kernels/matmul.c:136-189) */
+struct WeightCache {
+    bool init = false;
+    size_t limit = 0, used = 0;
+    std::map<std::pair<const void *, size_t>, void *> map;
+};
+
+struct DropIn {
+    Buf x, w[3], b, y[3];
+    WeightCache cache;
+};
+
+thread_local DropIn g_drop;
+
+void upload(const char *fn, smol_attn_ctx *ctx, Buf &b, const void *h, size_t bytes) {
+    hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
+    if (reserve(b, std::max<size_t>(bytes, 16), st)) dropin_abort(fn);
+    if (bytes && hipMemcpyAsync(b.p, h, bytes, hipMemcpyHostToDevice, st) != hipSuccess) dropin_abort(fn);
+}
+
+/* device weight for a host weight array */
+const uint16_t *weight(const char *fn, smol_attn_ctx *ctx, int slot, const uint16_t *h, size_t n) {
+    WeightCache &c = g_drop.cache;
+    if (!c.init) {
+        c.init = true;
+        const char *env = getenv("SMOL_BF16_CACHE_MB");
+        if (env && env[0]) {
+            char *end = nullptr;
+            const unsigned long long mb = strtoull(env, &end, 10);
+            if (end != env) c.limit = (size_t)mb << 20;
+        }
+    }
+    const auto key = std::make_pair((const void *)h, n);
+    auto it = c.map.find(key);
+    if (it != c.map.end()) return static_cast<const uint16_t *>(it->second);
+    const size_t bytes = n * 2;
+    hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
+    if (c.limit && bytes <= c.limit && c.used + bytes <= c.limit) {
+        void *d = nullptr;
+        if (hipMalloc(&d, std::max<size_t>(bytes, 16)) == hipSuccess) {
+            if (bytes && hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, st) != hipSuccess) dropin_abort(fn);
+            c.map.emplace(key, d);
+            c.used += bytes;
+            return static_cast<const uint16_t *>(d);
+        }
+    }
+    upload(fn, ctx, g_drop.w[slot], h, bytes);
+    return static_cast<const uint16_t *>(g_drop.w[slot].p);
+}
+
+void download(const char *fn, smol_attn_ctx *ctx, void *h, const Buf &b, size_t bytes) {
+    hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
+    if (bytes && hipMemcpyAsync(h, b.p, bytes, hipMemcpyDeviceToHost, st) != hipSuccess) dropin_abort(fn);
+}
+
+void finish(const char *fn, smol_attn_ctx *ctx) {
+    if (smol_attn_ctx_synchronize(ctx) != SMOL_ATTN_OK) dropin_abort(fn);
+}
+
+void linear_dropin(const char *fn, float *y, const float *x, const uint16_t *W, const float *b, int seq, int in,
+                   int out) {
+    if (seq <= 0 || out <= 0) return;
+    smol_attn_ctx *ctx = smol_internal_legacy_ctx(fn);
+    if (in < 0) in = 0;
+    const size_t nx = (size_t)seq * in, ny = (size_t)seq * out;
+    hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
+    if (hipSetDevice(smol_internal_ctx_device(ctx)) != hipSuccess) dropin_abort(fn);
+    upload(fn, ctx, g_drop.x, x, nx * 4);
+    const uint16_t *wd = in ? weight(fn, ctx, 0, W, (size_t)out * in) : nullptr;
+    const float *bd = nullptr;
+    if (b) {
+        upload(fn, ctx, g_drop.b, b, (size_t)out * 4);
+        bd = static_cast<const float *>(g_drop.b.p);
+    }
+    if (reserve(g_drop.y[0], ny * 4, st)) dropin_abort(fn);
+    if (smol_linear_dev(ctx, g_drop.y[0].p, SMOL_ATTN_F32, g_drop.x.p, SMOL_ATTN_F32, wd, bd, seq, in, out))
+        dropin_abort(fn);
+    download(fn, ctx, y, g_drop.y[0], ny * 4);
+    finish(fn, ctx);
+}
+
+}  // namespace
+
+extern "C" void smol_linear_bf16(float *y, const float *x, const uint16_t *W_bf16, const float *b, int seq_len,
+                                 int in_dim, int out_dim) {
+    linear_dropin("smol_linear_bf16", y, x, W_bf16, b, seq_len, in_dim, out_dim);
+}
+
+extern "C" void smol_linear_nobias_bf16(float *y, const float *x, const uint16_t *W_bf16, int seq_len, int in_dim,
+                                        int out_dim) {
+    linear_dropin("smol_linear_nobias_bf16", y, x, W_bf16, nullptr, seq_len, in_dim, out_dim);
+}
+
+extern "C" void smol_matmul_t_bf16(float *C, const float *A, const uint16_t *B_bf16, int M, int K, int N) {
+    linear_dropin("smol_matmul_t_bf16", C, A, B_bf16, nullptr, M, K, N);
+}
+
+extern "C" void smol_linear_nobias_bf16_qkv(float *q, float *k, float *v, const float *x, const uint16_t *Wq_bf16,
+                                            const uint16_t *Wk_bf16, const uint16_t *Wv_bf16, int in_dim, int q_dim,
+                                            int kv_dim) {
+    const char *fn = "smol_linear_nobias_bf16_qkv";
+    if (q_dim < 0) q_dim = 0;
+    if (kv_dim < 0) kv_dim = 0;
+    if (q_dim == 0 && kv_dim == 0) return;
+    smol_attn_ctx *ctx = smol_internal_legacy_ctx(fn);
+    if (in_dim < 0) in_dim = 0;
+    hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
+    if (hipSetDevice(smol_internal_ctx_device(ctx)) != hipSuccess) dropin_abort(fn);
+    upload(fn, ctx, g_drop.x, x, (size_t)in_dim * 4);
+    const uint16_t *wq = nullptr, *wk = nullptr, *wv = nullptr;
+    if (in_dim) {
+        if (q_dim) wq = weight(fn, ctx, 0, Wq_bf16, (size_t)q_dim * in_dim);
+        if (kv_dim) {
+            wk = weight(fn, ctx, 1, Wk_bf16, (size_t)kv_dim * in_dim);
+            wv = weight(fn, ctx, 2, Wv_bf16, (size_t)kv_dim * in_dim);
+        }
+    }
+    const int dims[3] = {q_dim, kv_dim, kv_dim};
+    for (int i = 0; i < 3; i++)
+        if (reserve(g_drop.y[i], (size_t)std::max(dims[i], 4) * 4, st)) dropin_abort(fn);
+    if (smol_linear_qkv_dev(ctx, g_drop.y[0].p, g_drop.y[1].p, g_drop.y[2].p, SMOL_ATTN_F32, g_drop.x.p,
+                            SMOL_ATTN_F32, wq, wk, wv, 1, in_dim, q_dim, kv_dim))
+        dropin_abort(fn);
+    download(fn, ctx, q, g_drop.y[0], (size_t)q_dim * 4);
+    download(fn, ctx, k, g_drop.y[1], (size_t)kv_dim * 4);
+    download(fn, ctx, v, g_drop.y[2], (size_t)kv_dim * 4);
+    finish(fn, ctx);
+}

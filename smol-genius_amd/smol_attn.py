@@ -81,7 +81,15 @@ SIGNATURES = [
     ("smol_qkn_attn_forward", [_vp, _c_int, _c_int, _vp, _vp, _vp, _vp], _c_int),
     ("smol_qkn_attn_read_cache", [_vp, _c_int, _c_int, _c_int, _U16P, _U16P], _c_int),
     ("smol_qkn_attn_unbind", [_vp], _c_int),
+    # bf16-weight projections on device pointers (include/smol_linear.h)
+    ("smol_linear_dev", [_vp, _vp, _c_int, _vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int], _c_int),
+    ("smol_linear_qkv_dev", [_vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _vp, _vp, _vp, _c_int, _c_int, _c_int,
+                             _c_int], _c_int),
     # reference-signature drop-ins (host fp32 arrays)
+    ("smol_linear_bf16", [_FP, _FP, _U16P, _FP, _c_int, _c_int, _c_int], None),
+    ("smol_linear_nobias_bf16", [_FP, _FP, _U16P, _c_int, _c_int, _c_int], None),
+    ("smol_linear_nobias_bf16_qkv", [_FP, _FP, _FP, _FP, _U16P, _U16P, _U16P, _c_int, _c_int, _c_int], None),
+    ("smol_matmul_t_bf16", [_FP, _FP, _U16P, _c_int, _c_int, _c_int], None),
     ("smol_bidirectional_attention", [_FP, _FP, _FP, _FP, _c_int, _c_int, _c_int, _c_float, _IP, _c_int], None),
     ("smol_causal_attention", [_FP, _FP, _FP, _FP, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int], None),
     ("smol_sliding_window_attention", [_FP, _FP, _FP, _FP, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
@@ -571,3 +579,81 @@ def smol_rms_norm_per_head(x, weight, seq_len, n_heads, head_dim, eps):
     assert x.dtype == np.float32 and x.flags.c_contiguous
     Wa, w = _f32(weight)
     load().smol_rms_norm_per_head(x.ctypes.data_as(_FP), w, seq_len, n_heads, head_dim, ctypes.c_float(eps))
+
+
+# ------------------------------------------------ bf16-weight projections
+
+GEMV_MAX_SEQ = 4  # SMOL_LINEAR_GEMV_MAX_SEQ
+
+
+def _wbits(w, what):
+    """a device weight as bf16 bits: a bfloat16 tensor, or int16 / uint16 bits"""
+    import torch
+    if w.dtype not in (torch.bfloat16, torch.int16, torch.uint16):
+        raise SmolAttnError("%s must be bfloat16 (or its bits as int16)" % what)
+    return _dev(w, what)
+
+
+def linear(ctx, x, w, bias=None, out=None, out_bf16=False):
+    """y = x W^T (+ bias) on the device (smol_linear_dev). x [seq, in] float32 or
+    bfloat16; w [out, in] bf16; bias [out] float32 or None. Returns y
+    [seq, out], float32, or the truncated bf16 bits as int16 when out_bf16."""
+    import torch
+    seq, in_dim = x.shape
+    out_dim = w.shape[0]
+    if w.shape[1] != in_dim:
+        raise SmolAttnError("w must be [out, in]")
+    if out is None:
+        out = torch.empty((seq, out_dim), dtype=torch.int16 if out_bf16 else torch.float32, device=x.device)
+    b = _dev(bias, "bias") if bias is not None else None
+    _check(load().smol_linear_dev(ctx.h, _dev(out, "out"), BF16 if out_bf16 else F32, _dev(x, "x"),
+                                  _dtype_code(x), _wbits(w, "w"), b, seq, in_dim, out_dim), "smol_linear_dev")
+    return out
+
+
+def linear_qkv(ctx, x, wq, wk, wv, out_bf16=False):
+    """q, k, v = x Wq^T, x Wk^T, x Wv^T (smol_linear_qkv_dev)"""
+    import torch
+    seq, in_dim = x.shape
+    q_dim, kv_dim = wq.shape[0], wk.shape[0]
+    dt = torch.int16 if out_bf16 else torch.float32
+    q = torch.empty((seq, q_dim), dtype=dt, device=x.device)
+    k = torch.empty((seq, kv_dim), dtype=dt, device=x.device)
+    v = torch.empty((seq, kv_dim), dtype=dt, device=x.device)
+    _check(load().smol_linear_qkv_dev(ctx.h, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), BF16 if out_bf16 else F32,
+                                      _dev(x, "x"), _dtype_code(x), _wbits(wq, "wq"), _wbits(wk, "wk"),
+                                      _wbits(wv, "wv"), seq, in_dim, q_dim, kv_dim), "smol_linear_qkv_dev")
+    return q, k, v
+
+
+def _u16(a):
+    a = np.ascontiguousarray(a, np.uint16)
+    return a, a.ctypes.data_as(_U16P)
+
+
+def smol_linear_bf16(y, x, W_bf16, b, seq_len, in_dim, out_dim):
+    assert y.dtype == np.float32 and y.flags.c_contiguous
+    Xa, xp = _f32(x); Wa, wp = _u16(W_bf16)
+    Ba, bp = _f32(b) if b is not None else (None, None)
+    load().smol_linear_bf16(y.ctypes.data_as(_FP), xp, wp, bp, seq_len, in_dim, out_dim)
+
+
+def smol_linear_nobias_bf16(y, x, W_bf16, seq_len, in_dim, out_dim):
+    assert y.dtype == np.float32 and y.flags.c_contiguous
+    Xa, xp = _f32(x); Wa, wp = _u16(W_bf16)
+    load().smol_linear_nobias_bf16(y.ctypes.data_as(_FP), xp, wp, seq_len, in_dim, out_dim)
+
+
+def smol_linear_nobias_bf16_qkv(q, k, v, x, Wq_bf16, Wk_bf16, Wv_bf16, in_dim, q_dim, kv_dim):
+    for a in (q, k, v):
+        assert a.dtype == np.float32 and a.flags.c_contiguous
+    Xa, xp = _f32(x)
+    Qa, wq = _u16(Wq_bf16); Ka, wk = _u16(Wk_bf16); Va, wv = _u16(Wv_bf16)
+    load().smol_linear_nobias_bf16_qkv(q.ctypes.data_as(_FP), k.ctypes.data_as(_FP), v.ctypes.data_as(_FP), xp,
+                                       wq, wk, wv, in_dim, q_dim, kv_dim)
+
+
+def smol_matmul_t_bf16(C, A, B_bf16, M, K, N):
+    assert C.dtype == np.float32 and C.flags.c_contiguous
+    Aa, ap = _f32(A); Ba, bp = _u16(B_bf16)
+    load().smol_matmul_t_bf16(C.ctypes.data_as(_FP), ap, bp, M, K, N)

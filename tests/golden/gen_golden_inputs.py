@@ -34,3 +34,13 @@ def norm_inputs(seed, seq, H, hd, std):
     x = synth.normal(seed * 3 + 0, (seq, H * hd), std)
     w = (1.0 + 0.1 * synth.normal(seed * 3 + 1, (hd,))).astype(np.float32)
     return x, w
+
+
+def linear_inputs(seed, seq, n_in, n_out, bias):
+    """x [seq, n_in] ~N(0, 1) fp32, W [n_out, n_in] as bf16 bits of
+    N(0, 1/n_in) samples (the scale of a trained projection), and a bias
+    [n_out] ~N(0, 0.1) or None."""
+    x = synth.normal(seed * 3 + 0, (seq, n_in))
+    w = synth.f32_to_bf16_bits(synth.normal(seed * 3 + 1, (n_out, n_in), 1.0 / np.sqrt(max(n_in, 1))))
+    b = synth.normal(seed * 3 + 2, (n_out,), 0.1) if bias else None
+    return x, w, b

@@ -162,8 +162,9 @@ def test_drop_in_header_agrees_with_reference_header(tmp_path):
     conflicting redeclaration, which the compiler rejects."""
     cc, std = "gcc", "-std=c11"
     src = tmp_path / "tu.c"
-    src.write_text('#include "%s"\n#include "smol_kernels_attn.h"\n#include "smol_qkn_attn.h"\n'
-                   'int main(void) { return 0; }\n' % REF_KERNELS_H)
+    src.write_text('#include "%s"\n#include "smol_kernels_attn.h"\n#include "smol_kernels_linear.h"\n'
+                   '#include "smol_qkn_attn.h"\n#include "smol_linear.h"\nint main(void) { return 0; }\n'
+                   % REF_KERNELS_H)
     r = subprocess.run([cc, std, "-Wall", "-Werror", "-fsyntax-only", "-I" + INCLUDE, str(src)],
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
@@ -176,7 +177,8 @@ def test_drop_in_header_agrees_with_reference_header(tmp_path):
     assert r.returncode != 0
 
 
-@pytest.mark.parametrize("hdr", ["smol_attn.h", "smol_kernels_attn.h", "smol_qkn_attn.h"])
+@pytest.mark.parametrize("hdr", ["smol_attn.h", "smol_kernels_attn.h", "smol_qkn_attn.h", "smol_linear.h",
+                                 "smol_kernels_linear.h"])
 def test_public_headers_compile_alone_as_c(tmp_path, hdr):
     src = tmp_path / "one.c"
     src.write_text('#include "%s"\n' % hdr)

@@ -1,0 +1,269 @@
+"""The bf16-weight projections on the GPU against the CPU oracle.
+
+Every case prints its name before it runs. Two bars on fp32 outputs:
+  * the path's bar, |gpu - cpu| <= 2e-3 + 1e-2 |cpu| (conftest.ATOL / RTOL);
+  * the arithmetic's own bound: both sides are fp32 sums of the same exact
+    products (the GEMM path carries x as bf16 hi + lo, 2^-17 relative), so
+    |gpu - cpu| <= (2 n 2^-24 + 2^-16) sum_i |x_i w_i| + |b| 2^-23.
+bf16 outputs (truncated) match bit for bit when every partial sum is exact
+(integer-valued inputs) and within one bf16 step otherwise.
+"""
+import os
+import threading
+
+import numpy as np
+import pytest
+
+from conftest import assert_parity, pkg, synth  # noqa: F401
+from gen_golden_inputs import linear_inputs
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def sa():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from smol_genius_amd import smol_attn
+    smol_attn.load()
+    return smol_attn
+
+
+@pytest.fixture(scope="module")
+def ctx(sa):
+    c = sa.Context(0)
+    yield c
+    c.close()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def dev_bits(bits):
+    return torch.from_numpy(np.ascontiguousarray(bits, np.uint16).view(np.int16)).cuda()
+
+
+def w32(bits):
+    return synth.bf16_bits_to_f32(bits).astype(np.float64)
+
+
+def bound(x, w_bits, b=None):
+    a = np.abs(np.asarray(x, np.float64)) @ np.abs(w32(w_bits)).T
+    n = w_bits.shape[1]
+    t = a * (2 * (n + 1) * 2.0 ** -24 + 2.0 ** -16)
+    if b is not None:
+        t = t + np.abs(np.asarray(b, np.float64)) * 2.0 ** -22
+    return t + 1e-30
+
+
+def check(y, ref, x, w_bits, b, what):
+    y = np.asarray(y, np.float64)
+    assert_parity(y, ref, what)
+    err = np.abs(y - np.asarray(ref, np.float64))
+    lim = bound(x, w_bits, b)
+    assert (err <= lim).all(), "%s: error %.3e above the fp32 bound (ratio %.2f)" % (
+        what, err.max(), (err / lim).max())
+
+
+GEMV_CASES = [
+    # seq, in, out, bias
+    (1, 1024, 4096, False),   # Q+K+V rows of Qwen3-0.6B, one wave per workgroup
+    (1, 2048, 1024, False),   # o_proj: two waves split in_dim
+    (1, 3072, 1024, True),    # down projection: three waves
+    (1, 1024, 6144, False),   # gate_up
+    (2, 1003, 33, True),      # in % 8 != 0: element loads
+    (3, 72, 40, True),
+    (4, 16384, 64, False),    # eight waves, two steps each
+    (4, 7, 5, True),
+    (1, 1, 3, True),
+    (2, 24000, 9, False),     # eight waves, three steps, out not a multiple of 4
+]
+
+
+@pytest.mark.parametrize("case", GEMV_CASES, ids=lambda c: "s%d_in%d_out%d%s" % (c[0], c[1], c[2], "_b" * c[3]))
+def test_gemv(ctx, sa, oracle, case):
+    seq, n_in, n_out, has_b = case
+    print("gemv", case, flush=True)
+    x, w, b = linear_inputs(6000 + n_in + n_out, seq, n_in, n_out, has_b)
+    y = sa.linear(ctx, dev(x), dev_bits(w), dev(b) if has_b else None)
+    ctx.synchronize()
+    check(y.cpu().numpy(), oracle.linear_bf16(x, w, b), x, w, b, "gemv %s" % (case,))
+
+
+def test_gemv_bf16_io(ctx, sa, oracle):
+    """bf16 x, truncated bf16 y (the bf16 decoder's contract)"""
+    rng = np.random.default_rng(11)
+    for seq, n_in, n_out in [(1, 1024, 256), (3, 96, 7), (4, 1003, 13)]:
+        print("gemv bf16", seq, n_in, n_out, flush=True)
+        xi = rng.integers(-16, 17, (seq, n_in)).astype(np.float32)
+        wi = rng.integers(-16, 17, (n_out, n_in)).astype(np.float32)
+        xb, wb = synth.f32_to_bf16_bits(xi), synth.f32_to_bf16_bits(wi)
+        y = sa.linear(ctx, dev_bits(xb).view(torch.bfloat16), dev_bits(wb), out_bf16=True)
+        ctx.synchronize()
+        got = y.cpu().numpy().view(np.uint16)
+        np.testing.assert_array_equal(got, oracle.bf16_linear_nobias(xb, wb))
+        # random values: within one bf16 step of the oracle's truncated sum
+        xb = synth.f32_to_bf16_bits(synth.normal(12 + seq, (seq, n_in)))
+        wb = synth.f32_to_bf16_bits(synth.normal(13 + seq, (n_out, n_in), 1.0 / np.sqrt(n_in)))
+        y = sa.linear(ctx, dev_bits(xb).view(torch.bfloat16), dev_bits(wb), out_bf16=True)
+        ctx.synchronize()
+        g = synth.bf16_bits_to_f32(y.cpu().numpy().view(np.uint16)).astype(np.float64)
+        r = synth.bf16_bits_to_f32(oracle.bf16_linear_nobias(xb, wb)).astype(np.float64)
+        assert (np.abs(g - r) <= np.abs(r) * 2.0 ** -7 + 1e-6).all()
+        # fp32 x with a truncated bf16 y
+        x = synth.normal(14 + seq, (seq, n_in))
+        y = sa.linear(ctx, dev(x), dev_bits(wb), out_bf16=True)
+        ctx.synchronize()
+        g = synth.bf16_bits_to_f32(y.cpu().numpy().view(np.uint16)).astype(np.float64)
+        r = oracle.linear_bf16(x, wb).astype(np.float64)
+        assert (np.abs(g - r) <= np.abs(r) * 2.0 ** -7 + bound(x, wb)).all()
+
+
+@pytest.mark.parametrize("shape", [(1, 1024, 2048, 1024), (3, 72, 40, 12), (1, 1003, 5, 0), (2, 64, 0, 8),
+                                   (1, 2048, 2048, 1024), (26, 1024, 2048, 1024)])
+def test_qkv(ctx, sa, oracle, shape):
+    seq, n_in, q_dim, kv_dim = shape
+    print("qkv", shape, flush=True)
+    x, wq, _ = linear_inputs(7000 + n_in, seq, n_in, q_dim, False)
+    _, wk, _ = linear_inputs(7100 + n_in, seq, n_in, kv_dim, False)
+    _, wv, _ = linear_inputs(7200 + n_in, seq, n_in, kv_dim, False)
+    q, k, v = sa.linear_qkv(ctx, dev(x), dev_bits(wq), dev_bits(wk), dev_bits(wv))
+    ctx.synchronize()
+    for got, w, nm in ((q, wq, "q"), (k, wk, "k"), (v, wv, "v")):
+        if w.shape[0]:
+            check(got.cpu().numpy(), oracle.linear_bf16(x, w), x, w, None, "qkv %s %s" % (shape, nm))
+
+
+GEMM_CASES = [
+    # seq, in, out, bias, x bf16, y bf16
+    (5, 1024, 4096, False, False, False),
+    (26, 2048, 1024, False, False, False),
+    (40, 512, 96, True, False, False),
+    (7, 1003, 37, True, False, False),      # ld not a multiple of 8
+    (64, 3072, 1024, False, False, False),
+    (40, 512, 96, False, True, True),
+    (33, 256, 80, True, False, True),
+]
+
+
+@pytest.mark.parametrize("case", GEMM_CASES, ids=lambda c: "s%d_in%d_out%d%s%s%s" % (
+    c[0], c[1], c[2], "_b" * c[3], "_xbf" * c[4], "_ybf" * c[5]))
+def test_gemm(ctx, sa, oracle, case):
+    seq, n_in, n_out, has_b, xbf, ybf = case
+    print("gemm", case, flush=True)
+    x, w, b = linear_inputs(8000 + n_in + n_out, seq, n_in, n_out, has_b)
+    if xbf:
+        xbits = synth.f32_to_bf16_bits(x)
+        x = synth.bf16_bits_to_f32(xbits)
+        xd = dev_bits(xbits).view(torch.bfloat16)
+    else:
+        xd = dev(x)
+    y = sa.linear(ctx, xd, dev_bits(w), dev(b) if has_b else None, out_bf16=ybf)
+    ctx.synchronize()
+    ref = oracle.linear_bf16(x, w, b)
+    if ybf:
+        g = synth.bf16_bits_to_f32(y.cpu().numpy().view(np.uint16)).astype(np.float64)
+        assert (np.abs(g - ref) <= np.abs(ref) * 2.0 ** -7 + bound(x, w, b)).all()
+    else:
+        check(y.cpu().numpy(), ref, x, w, b, "gemm %s" % (case,))
+
+
+def test_gemm_full_prefill_shapes(ctx, sa, oracle):
+    """Qwen3-0.6B projections of a 1536-token prefill: sampled rows against the
+    oracle, every row against a float64 product on the device."""
+    seq = 1536
+    for n_in, n_out in [(1024, 4096), (2048, 1024), (1024, 6144), (3072, 1024)]:
+        print("gemm prefill", seq, n_in, n_out, flush=True)
+        x, w, _ = linear_inputs(9000 + n_out, seq, n_in, n_out, False)
+        xd, wd = dev(x), dev_bits(w)
+        y = sa.linear(ctx, xd, wd)
+        ctx.synchronize()
+        yh = y.cpu().numpy()
+        rows = np.array([0, 1, 2, 511, 777, 1024, 1535])
+        check(yh[rows], oracle.linear_bf16(x[rows], w), x[rows], w, None, "prefill %d->%d rows" % (n_in, n_out))
+        w64 = wd.view(torch.bfloat16).to(torch.float64)
+        ref = (xd.to(torch.float64) @ w64.T).cpu().numpy()
+        check(yh, ref, x, w, None, "prefill %d->%d all" % (n_in, n_out))
+
+
+def test_gemm_carries_the_low_part(ctx, sa):
+    """x = 1 + 3 * 2^-10 is not a bf16 value (x_hi = 1, x_lo = 3 * 2^-10):
+    with W = 1, every output is exactly n * x; without the low part it would be n."""
+    for seq in (1, 8, 100):
+        n = 1024
+        x = np.full((seq, n), 1.0 + 3 * 2.0 ** -10, np.float32)
+        w = synth.f32_to_bf16_bits(np.ones((16, n), np.float32))
+        y = sa.linear(ctx, dev(x), dev_bits(w))
+        ctx.synchronize()
+        np.testing.assert_array_equal(y.cpu().numpy(), np.full((seq, 16), 1027.0, np.float32))
+
+
+def test_empty_and_bias_only(ctx, sa):
+    b = synth.normal(3, (9,))
+    for seq in (2, 9):
+        y = sa.linear(ctx, torch.zeros((seq, 0), device="cuda"), torch.zeros((9, 0), dtype=torch.int16,
+                                                                               device="cuda"), dev(b))
+        ctx.synchronize()
+        np.testing.assert_array_equal(y.cpu().numpy(), np.broadcast_to(b, (seq, 9)))
+    y = sa.linear(ctx, torch.zeros((0, 16), device="cuda"), torch.zeros((9, 16), dtype=torch.int16, device="cuda"))
+    assert y.shape == (0, 9)
+
+
+def test_golden_through_reference_signatures(sa):
+    import json
+    from conftest import GOLDEN
+    with open(os.path.join(GOLDEN, "ref_linear.json")) as f:
+        meta = json.load(f)
+    data = np.load(os.path.join(GOLDEN, "ref_linear.npz"))
+    for c in meta["cases"]:
+        print("golden", c["name"], flush=True)
+        n_in, n_out, seq = c["in_dim"], c["out_dim"], c["seq"]
+        if c["kind"] == "qkv":
+            x, wq, _ = linear_inputs(c["seed"], 1, n_in, n_out, False)
+            _, wk, _ = linear_inputs(c["seed"] + 100, 1, n_in, n_out // 2, False)
+            _, wv, _ = linear_inputs(c["seed"] + 200, 1, n_in, n_out // 2, False)
+            q = np.zeros(n_out, np.float32)
+            k = np.zeros(n_out // 2, np.float32)
+            v = np.zeros(n_out // 2, np.float32)
+            sa.smol_linear_nobias_bf16_qkv(q, k, v, x, wq, wk, wv, n_in, n_out, n_out // 2)
+            for got, w, tag in ((q, wq, "_q"), (k, wk, "_k"), (v, wv, "_v")):
+                check(got[None], data[c["name"] + tag][None], x, w, None, c["name"] + tag)
+            continue
+        x, w, b = linear_inputs(c["seed"], seq, n_in, n_out, c["bias"])
+        y = np.zeros((seq, n_out), np.float32)
+        if c["kind"] == "matmul_t":
+            sa.smol_matmul_t_bf16(y, x, w, seq, n_in, n_out)
+        elif b is None:
+            sa.smol_linear_nobias_bf16(y, x, w, seq, n_in, n_out)
+        else:
+            sa.smol_linear_bf16(y, x, w, b, seq, n_in, n_out)
+        check(y, data[c["name"]], x, w, b, c["name"])
+
+
+def test_dropin_weight_cache(sa, oracle):
+    """SMOL_BF16_CACHE_MB keeps device copies of weights by host pointer (a
+    fresh thread reads the variable, as each thread has its own drop-in state)."""
+    x, w1, _ = linear_inputs(31, 1, 256, 64, False)
+    _, w2, _ = linear_inputs(32, 1, 256, 64, False)
+    res = {}
+
+    def body():
+        os.environ["SMOL_BF16_CACHE_MB"] = "64"
+        try:
+            for i, w in enumerate((w1, w2, w1, w2)):
+                y = np.zeros((1, 64), np.float32)
+                sa.smol_linear_nobias_bf16(y, x, w, 1, 256, 64)
+                res[i] = y
+        finally:
+            del os.environ["SMOL_BF16_CACHE_MB"]
+
+    t = threading.Thread(target=body)
+    t.start()
+    t.join()
+    for i, w in enumerate((w1, w2, w1, w2)):
+        check(res[i], oracle.linear_bf16(x, w), x, w, None, "cached weight %d" % i)
+    np.testing.assert_array_equal(res[0], res[2])
+    np.testing.assert_array_equal(res[1], res[3])
