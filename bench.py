@@ -12,7 +12,9 @@ last-level cache.
 
 The other workloads (decode, bidirectional, MQA decode, streaming chunk +
 decode, and the decode step and prefill with the per-head Q/K RMSNorm fused
-into the pre-pass) are measured the same way and reported under "detail".
+into the pre-pass) are measured the same way and reported under "detail",
+as are the bf16-weight projections of one decoder layer (decode GEMV and
+prefill GEMM, rotating over 28 layers of weights).
 
 value / ms_per_step: wall clock over the timed steps with nothing but the
 library's own launches in the stream.
@@ -110,6 +112,90 @@ def measure(ctx, wl, steps, warmup, runner, layers=None):
     finally:
         gc.enable()
     return x, run, n_layers, wall, kt
+
+
+def measure_projections(ctx, sa, wl, steps, warmup):
+    """One decoder layer's four projections per step (smol_linear_qkv_dev for Q/K/V,
+    smol_linear_dev for o_proj, gate_up and down), rotating over wl.layers layers of
+    distinct device weights (random bf16, generated on the device: values do not
+    change the work). Wall clock per layer, then each kind's own launches timed by
+    the HIP events the library records around them."""
+    import gc
+    import ctypes
+    import torch
+    lib = sa.load()
+    gc.collect()
+    torch.cuda.synchronize()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(wl.seed)
+    W = [{k: [(torch.randn((o, n_in), generator=g, device="cuda") * n_in ** -0.5).to(torch.bfloat16)
+              for o in outs] for k, (n_in, outs) in wl.kinds.items()} for _ in range(wl.layers)]
+    X = {k: torch.randn((wl.seq, n_in), generator=g, device="cuda") for k, (n_in, _) in wl.kinds.items()}
+    Y = {k: [torch.empty((wl.seq, o), device="cuda") for o in outs] for k, (_, outs) in wl.kinds.items()}
+    vp = ctypes.c_void_p
+    calls = {}
+    for k, (n_in, outs) in wl.kinds.items():
+        x, ys = vp(X[k].data_ptr()), [vp(y.data_ptr()) for y in Y[k]]
+        if k == "qkv":
+            calls[k] = [(lib.smol_linear_qkv_dev, (ctx.h, ys[0], ys[1], ys[2], 0, x, 0,
+                                                   vp(W[l][k][0].data_ptr()), vp(W[l][k][1].data_ptr()),
+                                                   vp(W[l][k][2].data_ptr()), wl.seq, n_in, outs[0], outs[1]))
+                        for l in range(wl.layers)]
+        else:
+            calls[k] = [(lib.smol_linear_dev, (ctx.h, ys[0], 0, x, 0, vp(W[l][k][0].data_ptr()), None, wl.seq,
+                                               n_in, outs[0])) for l in range(wl.layers)]
+
+    def layer(l):
+        for k in wl.kinds:
+            f, a = calls[k][l]
+            if f(*a):
+                raise RuntimeError(lib.smol_attn_last_error().decode())
+
+    gc.disable()
+    try:
+        for i in range(warmup):
+            layer(i % wl.layers)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            layer(i % wl.layers)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        per = {}
+        ctx.timing_read()
+        for k in wl.kinds:
+            ctx.set_timing(True)
+            for i in range(steps):
+                f, a = calls[k][i % wl.layers]
+                f(*a)
+            torch.cuda.synchronize()
+            ctx.set_timing(False)
+            ms, cnt = ctx.timing_read()["other"]
+            per[k] = ms / max(1, cnt)
+    finally:
+        gc.enable()
+    d = {"config": wl.describe(), "ms_per_step": round(wall / steps * 1e3, 5),
+         "step": "one layer: 4 projection calls"}
+    tot_ms = sum(per.values())
+    for k, ms in per.items():
+        e = {"kernel_ms": round(ms, 5), "bytes_per_launch": wl.algorithmic_bytes(k)}
+        if wl.seq <= 4:
+            gbs = wl.algorithmic_bytes(k) / (ms * 1e-3) / 1e9
+            e.update(GBps_kernel=round(gbs, 1), hbm_frac=round(gbs / PEAK_HBM_GBS, 4))
+        else:
+            tf = wl.flops(k) / (ms * 1e-3) / 1e12
+            # an fp32 input runs as two bf16 products (x_hi, x_lo)
+            e.update(tflops=round(tf, 2), mfma_frac_executed=round(2 * tf / PEAK_MFMA_TFLOPS, 4))
+        d[k] = e
+    if wl.seq <= 4:
+        gbs = wl.algorithmic_bytes() / (tot_ms * 1e-3) / 1e9
+        d.update(GBps_layer_kernels=round(gbs, 1), hbm_frac_layer=round(gbs / PEAK_HBM_GBS, 4),
+                 GBps_layer_wall=round(wl.algorithmic_bytes() / (wall / steps) / 1e9, 1))
+    else:
+        tf = wl.flops() / (tot_ms * 1e-3) / 1e12
+        d.update(tflops_layer_kernels=round(tf, 2), tflops_layer_wall=round(wl.flops() / (wall / steps) / 1e12, 2))
+    del W, X, Y, calls
+    return d
 
 
 def main():
@@ -246,6 +332,17 @@ def main():
                 d["cpu_baseline"] = cpu_mod.bidir_sample(wl, wl.inputs())
             elif isinstance(wl, workloads.Prefill):
                 d["cpu_baseline"] = cpu_mod.prefill_sample(wl, wl.inputs(), min_seconds=3.0)
+        detail[name] = d
+
+    # ---------------- the decoder layer's bf16-weight projections (decode GEMV, prefill GEMM)
+    for name in ["qwen06b_proj_decode", "qwen06b_proj_prefill"]:
+        if args.only not in (None, name):
+            continue
+        wl = wls[name]
+        n = steps if wl.seq == 1 else max(5, steps // 5)
+        d = measure_projections(ctx, sa, wl, n, max(2, warmup // 2))
+        if cpu_mod:
+            d["cpu_baseline"] = cpu_mod.projections_sample(wl, wl.inputs())
         detail[name] = d
 
     # ---------------- CPU baseline of the headline (reference CPU attention on this host)

@@ -55,6 +55,51 @@ SMOL_ATTN_API int smol_linear_qkv_dev(smol_attn_ctx *ctx, void *q, void *k, void
                                       int x_dtype, const uint16_t *wq, const uint16_t *wk, const uint16_t *wv,
                                       int seq, int in_dim, int q_dim, int kv_dim);
 
+/* ---- a decoder layer's operations around its projections ----------------
+ *
+ * The decoders wrap their projections in an RMSNorm of the input, a gated
+ * activation of the gate/up product and a residual add
+ * (common/decoder/qkn_decoder.c:633-705 for one token, :470-560 for a
+ * prefill). smol_linear_ops_dev runs them with the projection; for
+ * seq <= SMOL_LINEAR_GEMV_MAX_SEQ all of them happen inside the one GEMV
+ * launch (the input row's sum of squares is accumulated by the waves that
+ * read it, the activation and the add are applied as each output is
+ * written), so a Qwen3 decoder layer's MLP is two launches. */
+#define SMOL_LINEAR_ACT_NONE 0
+#define SMOL_LINEAR_ACT_SWIGLU 1 /* silu(g) * u = g / (1 + expf(-g)) * u (activation.c:55-88) */
+#define SMOL_LINEAR_ACT_GEGLU 2  /* gelu_tanh(g) * u (activation.c:104-125) */
+
+typedef struct {
+    /* non-NULL: x is first RMS-normalised with this weight [in_dim]:
+     * x'[s][i] = x[s][i] * w[i] / sqrt(mean_i x[s][i]^2 + norm_eps)
+     * (smol_rms_norm, common/kernels/rmsnorm.c:17-75) */
+    const float *norm_weight;
+    float norm_eps;
+    /* SMOL_LINEAR_ACT_*: the weight's rows are (gate, up) pairs, row 2j the
+     * gate and row 2j + 1 the up projection of unit j (the decoders' fused
+     * gate_up weight, qkn_decoder.c:139-152); y [seq][out_dim / 2] gets
+     * act(gate) * up (smol_swiglu_multiply / smol_geglu_multiply) */
+    int act;
+    /* non-NULL: added to the result, y = residual + ...; may equal y (the
+     * decoders' smol_add_inplace of the sublayer output into the residual
+     * stream, qkn_decoder.c:684-704) */
+    const float *residual;
+} smol_linear_ops;
+
+/* y = residual + act(norm(x) W^T + bias) with the parts ops selects; ops may
+ * be NULL (then this is smol_linear_dev on fp32). x, y, residual fp32
+ * [seq][...] on the device; y must not overlap x; in_dim > 0. */
+SMOL_ATTN_API int smol_linear_ops_dev(smol_attn_ctx *ctx, float *y, const float *x, const uint16_t *w,
+                                      const float *bias, int seq, int in_dim, int out_dim,
+                                      const smol_linear_ops *ops);
+
+/* out[s][i] = (x[s][i] * weight[i]) * (1 / sqrtf(sum_i x[s][i]^2 / dim + eps));
+ * smol_rms_norm (common/kernels/rmsnorm.c:17-75): the decoders' final norm
+ * and the Gemma 3 post-sublayer norms (qkn_decoder.c:682-686, 701-702).
+ * out may equal x. */
+SMOL_ATTN_API int smol_rms_norm_dev(smol_attn_ctx *ctx, float *out, const float *x, const float *weight, int seq,
+                                    int dim, float eps);
+
 #ifdef __cplusplus
 }
 #endif

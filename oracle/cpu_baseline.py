@@ -152,3 +152,38 @@ def stream_sample(wl, x, min_seconds=5.0, max_reps=20):
     return {"value": round(wl.decode_bytes() / sec / 1e9, 3), "unit": "GB/s (decode bytes over the whole step)",
             "cores": cores, "kind": kind, "ms_per_step": round(sec * 1e3, 3), **host_facts(),
             "sample": "%d repetitions of the chunk call + %d decode calls" % (reps, n)}
+
+
+def projections_sample(wl, x, min_seconds=3.0, max_reps=100, max_rows=64):
+    """One layer's projections as the reference decoder calls them: for one token
+    smol_linear_nobias_bf16_qkv + smol_linear_nobias_bf16 x 3 (qkn_decoder.c:635, 679,
+    693, 699: threaded bf16 matvecs); for a prefill smol_linear_nobias_bf16 per weight
+    (qkn_decoder.c:474-476, 531, 546, 552: a bf16 -> fp32 weight copy and single-threaded
+    loops, matmul.c:336-346), on at most `max_rows` rows of the input (the work per row
+    is the same for every row)."""
+    lib, kind, cores = _lib()
+    rows = min(wl.seq, max_rows)
+    ws = {k: wl.layer_weights(0, k) for k in wl.kinds}
+    xs = {k: np.ascontiguousarray(x["x"][k][:rows]) for k in wl.kinds}
+    reps, t = 0, 0.0
+    while reps < 2 or (t < min_seconds and reps < max_reps):
+        t0 = time.perf_counter()
+        for k in wl.kinds:
+            if k == "qkv" and rows == 1 and hasattr(lib, "linear_qkv"):
+                lib.linear_qkv(xs[k], *ws[k])
+            else:
+                for w in ws[k]:
+                    lib.linear_bf16(xs[k], w)
+        t += time.perf_counter() - t0
+        reps += 1
+    sec = t / reps * (wl.seq / rows)
+    if wl.seq == 1:
+        val, unit = round(wl.algorithmic_bytes() / sec / 1e9, 3), "GB/s"
+        threads = cores
+    else:
+        val, unit = round(wl.flops() / sec / 1e12, 6), "TFLOP/s"
+        threads = 1  # smol_linear's loops are not threaded (matmul.c:70-97)
+    return {"value": val, "unit": unit, "cores": threads, "kind": kind, "ms_per_step": round(sec * 1e3, 3),
+            **host_facts(),
+            "sample": "%d repetitions of one layer's projections on %d of %d rows%s" % (
+                reps, rows, wl.seq, "" if rows == wl.seq else ", scaled to all rows")}

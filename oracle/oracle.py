@@ -176,7 +176,24 @@ class Oracle(_Lib):
         self._bf16_norm = self._fn("bf16_rms_norm_per_head", [_U16, _F, ci, ci, ci, cf])
         self._bf16_rope = self._fn("bf16_apply_rope_interleaved", [_U16, _F, _F, ci, ci, ci])
         self._linear = self._fn("linear_bf16", [_F, _F, _U16, _F, ci, ci, ci])
+        self._rms = self._fn("rms_norm", [_F, _F, _F, ci, ci, cf])
+        self._swiglu = self._fn("swiglu", [_F, _F, ci, ci])
+        self._geglu = self._fn("geglu", [_F, _F, ci, ci])
         self._bf16_linear = self._fn("bf16_linear_nobias", [_U16, _U16, _U16, ci, ci, ci])
+
+    def rms_norm(self, x, w, eps):
+        """smol_rms_norm (rmsnorm.c:17-75) of rows x [seq, dim]"""
+        x = _f32(x)
+        y = np.zeros_like(x)
+        self._rms(_fp(y), _fp(x), _fp(_f32(w)), x.shape[0], x.shape[1], ctypes.c_float(eps))
+        return y
+
+    def glu(self, gu, act):
+        """act 1: SwiGLU, 2: GeGLU of interleaved (gate, up) rows gu [seq, 2 * inter]"""
+        gu = _f32(gu)
+        y = np.zeros((gu.shape[0], gu.shape[1] // 2), np.float32)
+        (self._swiglu if act == 1 else self._geglu)(_fp(y), _fp(gu), gu.shape[0], gu.shape[1] // 2)
+        return y
 
     def linear_bf16(self, x, w_bits, bias=None):
         """y [seq, out] = x [seq, in] W^T (+ bias), W given as bf16 bits [out, in]"""
@@ -260,6 +277,10 @@ class RefLib(_Lib):
         self._lin_nb = self._fn("linear_nobias_bf16", [_F, _F, _U16, ci, ci, ci])
         self._lin_qkv = self._fn("linear_nobias_bf16_qkv", [_F, _F, _F, _F, _U16, _U16, _U16, ci, ci, ci])
         self._mm_t = self._fn("matmul_t_bf16", [_F, _F, _U16, ci, ci, ci])
+        cf = ctypes.c_float
+        self._rms_ref = self._fn("rms_norm", [_F, _F, _F, ci, ci, cf])
+        self._swiglu_ref = self._fn("swiglu_multiply", [_F, _F, ci, ci])
+        self._geglu_ref = self._fn("geglu_multiply", [_F, _F, ci, ci])
 
     def linear_bf16(self, x, w_bits, bias=None):
         """smol_linear_bf16 / smol_linear_nobias_bf16 (matmul.c:336-358)"""
@@ -293,3 +314,15 @@ class RefLib(_Lib):
         c = np.zeros((a.shape[0], b.shape[0]), np.float32)
         self._mm_t(_fp(c), _fp(a), b.ctypes.data_as(_U16), a.shape[0], a.shape[1], b.shape[0])
         return c
+
+    def rms_norm(self, x, w, eps):
+        x = _f32(x)
+        y = np.zeros_like(x)
+        self._rms_ref(_fp(y), _fp(x), _fp(_f32(w)), x.shape[0], x.shape[1], ctypes.c_float(eps))
+        return y
+
+    def glu(self, gu, act):
+        gu = _f32(gu)
+        y = np.zeros((gu.shape[0], gu.shape[1] // 2), np.float32)
+        (self._swiglu_ref if act == 1 else self._geglu_ref)(_fp(y), _fp(gu), gu.shape[0], gu.shape[1] // 2)
+        return y

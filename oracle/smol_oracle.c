@@ -36,6 +36,9 @@
  *       as smol_linear_bf16 / smol_linear_nobias_bf16 / smol_matmul_t_bf16 run
  *       them for seq_len > 1 (matmul.c:336-358, 419-429)
  *   orc_bf16_linear_nobias          common/decoder/qkn_bf16_decoder.c:99-117
+ *   orc_rms_norm                    common/kernels/rmsnorm.c:17-75 (the AVX-512 order
+ *       of orc_rms_norm_per_head with the whole row as one head)
+ *   orc_swiglu / orc_geglu          common/kernels/activation.c:55-88, 104-125
  *
  * Parity pins (see tests/test_oracle_*.py): golden vectors written by the
  * compiled reference (oracle/_ref), closed forms (one visible key, identical
@@ -552,4 +555,36 @@ void orc_bf16_linear_nobias(uint16_t *y, const uint16_t *x, const uint16_t *W, i
             yr[o] = orc_f32_to_bf16_trunc(sum);
         }
     }
+}
+
+/* rmsnorm.c:17-75: the same arithmetic as rmsnorm.c:78-140 per head, over
+ * the whole row (16-lane fused multiply-add accumulators, a halving tree, a
+ * scalar tail; (x * w) * r on the 16-wide body, x * r * w on the tail) */
+void orc_rms_norm(float *out, const float *x, const float *w, int seq, int dim, float eps) {
+    if (out != x) memcpy(out, x, (size_t)seq * dim * sizeof(float));
+    orc_rms_norm_per_head(out, w, seq, 1, dim, eps);
+}
+
+/* activation.c:55-88 (SwiGLU) and :104-125 (GeGLU, tanh form) on interleaved
+ * (gate, up) pairs: out[s][j] = act(gu[s][2j]) * gu[s][2j + 1] */
+void orc_swiglu(float *out, const float *gu, int seq, int inter) {
+    for (int s = 0; s < seq; s++)
+        for (int j = 0; j < inter; j++) {
+            float g = gu[(size_t)s * 2 * inter + 2 * j];
+            float u = gu[(size_t)s * 2 * inter + 2 * j + 1];
+            g = g / (1.0f + expf(-g));
+            out[(size_t)s * inter + j] = g * u;
+        }
+}
+
+void orc_geglu(float *out, const float *gu, int seq, int inter) {
+    for (int s = 0; s < seq; s++)
+        for (int j = 0; j < inter; j++) {
+            float g = gu[(size_t)s * 2 * inter + 2 * j];
+            float u = gu[(size_t)s * 2 * inter + 2 * j + 1];
+            float x3 = g * g * g;
+            float inner = 0.7978845608028654f * (g + 0.044715f * x3);
+            g = 0.5f * g * (1.0f + tanhf(inner));
+            out[(size_t)s * inter + j] = g * u;
+        }
 }

@@ -10,10 +10,11 @@
  *
  * Two device paths:
  *   k_gemv   seq <= SMOL_LINEAR_GEMV_MAX_SEQ (decode). HBM-bound: every
- *            weight byte is read once. A workgroup owns GEMV_R consecutive
+ *            weight byte is read once. A row group is GEMV_R consecutive
  *            output rows (of the joint row space of up to three weight
  *            segments, so Q/K/V is one launch) and `kp` waves that split
- *            in_dim; lane l of wave w reads the 16-byte chunks
+ *            in_dim; a workgroup packs `groups` row groups (up to
+ *            GEMV_WG_WAVES waves). Lane l of wave w (of kp) reads the 16-byte chunks
  *            w*64 + l + j*64*kp of each of its rows, and the x chunk it
  *            multiplies them with (x stays L1/L2 resident). Every load of a
  *            step is issued before the first FMA. Sums: per-lane fp32, then
@@ -55,26 +56,40 @@ extern "C" void smol_internal_timing_events(smol_attn_ctx *ctx, int kind, hipEve
 extern "C" smol_attn_ctx *smol_internal_legacy_ctx(const char *fn);
 extern "C" int smol_launch_to_bf16_trunc(const float *x, uint16_t *y, long long n, hipStream_t st);
 
-#define GEMV_R 4      /* output rows per workgroup */
+#define GEMV_R 4      /* output rows per row group (one wave, or kp waves) */
 #define GEMV_U 2      /* chunks of 8 elements per lane per step */
-#define GEMV_MAX_KP 8 /* waves per workgroup along in_dim */
+#define GEMV_MAX_KP 8 /* waves per row group along in_dim */
+#ifndef GEMV_WG_WAVES
+#define GEMV_WG_WAVES 4 /* target waves per workgroup: row groups are packed up to it */
+#endif
 #define GEMV_SEGS 3
 #define LIN_TIMING_KIND 2 /* the context's "other" timing kind */
 
+/* one weight of a GEMV launch (host side) */
 struct GemvSeg {
     const uint16_t *w;  /* [out][in] bf16 */
     const float *bias;  /* [out] or null */
     void *y;            /* [seq][out] */
     int out;
-    int row0;           /* first row of this segment in the joint row space (INT_MAX: unused) */
 };
 
+/* the fields the loads depend on first, the epilogue's after them */
 struct GemvParams {
-    const void *x; /* [seq][in] */
+    const uint16_t *w[GEMV_SEGS];
+    const void *x;           /* [seq][in] */
+    int row0[GEMV_SEGS];     /* first row of each segment in the joint row space (INT_MAX: unused) */
     int in;
-    int rows;      /* rows of all segments */
-    int kp;        /* waves per workgroup */
-    GemvSeg seg[GEMV_SEGS];
+    int rows;                /* rows of all segments */
+    int kp;                  /* waves per row group (split in_dim) */
+    int groups;              /* row groups per workgroup (kp * groups <= GEMV_MAX_KP) */
+    const float *bias[GEMV_SEGS];
+    void *y[GEMV_SEGS];
+    int out[GEMV_SEGS];
+    /* fused operations (fp32 x and y, one segment) */
+    const float *norm_w; /* [in] or null: each x row is RMS-normalised with this weight first */
+    float eps;
+    int act;             /* SMOL_LINEAR_ACT_*: rows (2j, 2j + 1) are (gate, up), y[s][j] = act(gate) up */
+    const float *res;    /* [seq][y columns] or null: added to the result (may equal y) */
 };
 
 /* ---------------------------------------------------------------- kernels */
@@ -95,32 +110,41 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 /* segment of joint row `row` (uniform when row is) */
 __device__ __forceinline__ int seg_of(const GemvParams &p, int row) {
-    return (row >= p.seg[1].row0) + (row >= p.seg[2].row0);
+    return (row >= p.row0[1]) + (row >= p.row0[2]);
 }
 
 /* VEC: in % 8 == 0 and 16-byte aligned x / W (every chunk one 16-byte
  * load); otherwise elementwise loads. Loads past a row or past x read
  * zero (buffer range checks), so no branch guards them. */
-template <int SEQ, bool XBF, bool YBF, bool VEC>
+template <int SEQ, bool XBF, bool YBF, bool VEC, bool FUSE>
 __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
     __shared__ float red[GEMV_MAX_KP][GEMV_R * SEQ];
+    __shared__ float red_ss[GEMV_MAX_KP][GEMV_R * SEQ];
+    const GemvParams &h = p;
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int kp = p.kp;
-    const int in = p.in;
-    const int row_base = blockIdx.x * GEMV_R;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kp = h.kp;
+    const int wave = wid % kp;  /* position along in_dim */
+    const int in = h.in;
+    const int row_base = (blockIdx.x * h.groups + wid / kp) * GEMV_R;
 
     rsrc_t wr[GEMV_R];
 #pragma unroll
     for (int r = 0; r < GEMV_R; r++) {
         const int row = row_base + r;
-        const int sg = seg_of(p, row);
-        const uint16_t *w = sg == 0 ? p.seg[0].w : sg == 1 ? p.seg[1].w : p.seg[2].w;
-        const int r0 = sg == 0 ? p.seg[0].row0 : sg == 1 ? p.seg[1].row0 : p.seg[2].row0;
-        const bool live = row < p.rows;
-        wr[r] = make_rsrc(live ? w + (long long)(row - r0) * in : p.seg[0].w, live ? (long long)in * 2 : 0);
+        const int sg = (row >= h.row0[1]) + (row >= h.row0[2]);
+        const uint16_t *w = sg == 0 ? h.w[0] : sg == 1 ? h.w[1] : h.w[2];
+        const int r0 = sg == 0 ? h.row0[0] : sg == 1 ? h.row0[1] : h.row0[2];
+        const bool live = row < h.rows;
+        wr[r] = make_rsrc(live ? w + (long long)(row - r0) * in : h.w[0], live ? (long long)in * 2 : 0);
     }
-    const rsrc_t xr = make_rsrc(p.x, (long long)SEQ * in * (XBF ? 2 : 4));
+    const rsrc_t xr = make_rsrc(h.x, (long long)SEQ * in * (XBF ? 2 : 4));
+    /* the norm weight (reads zero when there is none, then unused) */
+    const bool norm = FUSE && p.norm_w;
+    const rsrc_t gr = make_rsrc(norm ? (const void *)p.norm_w : (const void *)h.w[0], norm ? (long long)in * 4 : 0);
+    float ssq[SEQ];
+#pragma unroll
+    for (int s = 0; s < SEQ; s++) ssq[s] = 0.0f;
 
     float acc[GEMV_R][SEQ];
 #pragma unroll
@@ -133,13 +157,19 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
     for (int c0 = wave * 64; c0 < C; c0 += stride * GEMV_U) {
         float wf[GEMV_U][GEMV_R][8];
         float xf[GEMV_U][SEQ][8];
+        float gf[GEMV_U][8];
         if constexpr (VEC) {
             uint4 wv[GEMV_U][GEMV_R];
             uint4 xv[GEMV_U][SEQ][XBF ? 1 : 2];
+            uint4 gv[GEMV_U][2];
 #pragma unroll
             for (int u = 0; u < GEMV_U; u++) {
                 const int c = c0 + lane + u * stride;
                 const bool ok = c < C;
+                if constexpr (FUSE) {
+                    gv[u][0] = bload(gr, ok ? (unsigned)c * 32u : OOB_OFF, 0);
+                    gv[u][1] = bload(gr, ok ? (unsigned)c * 32u + 16u : OOB_OFF, 0);
+                }
 #pragma unroll
                 for (int r = 0; r < GEMV_R; r++) wv[u][r] = bload(wr[r], ok ? (unsigned)c * 16u : OOB_OFF, 0);
 #pragma unroll
@@ -159,6 +189,12 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int u = 0; u < GEMV_U; u++) {
+                if constexpr (FUSE) {
+                    const uint32_t t[8] = {gv[u][0].x, gv[u][0].y, gv[u][0].z, gv[u][0].w,
+                                           gv[u][1].x, gv[u][1].y, gv[u][1].z, gv[u][1].w};
+#pragma unroll
+                    for (int e = 0; e < 8; e++) gf[u][e] = __uint_as_float(t[e]);
+                }
 #pragma unroll
                 for (int r = 0; r < GEMV_R; r++) unpack_bf16x8(wv[u][r], wf[u][r]);
 #pragma unroll
@@ -181,6 +217,9 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
                 for (int e = 0; e < 8; e++) {
                     const int i = c * 8 + e;
                     const bool ok = c < C && i < in;
+                    if constexpr (FUSE)
+                        gf[u][e] = __uint_as_float(
+                            __builtin_amdgcn_raw_buffer_load_b32(gr, ok ? (unsigned)i * 4u : OOB_OFF, 0, 0));
 #pragma unroll
                     for (int r = 0; r < GEMV_R; r++) {
                         const unsigned short h = __builtin_amdgcn_raw_buffer_load_b16(
@@ -201,6 +240,18 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
                 }
             }
         }
+        if constexpr (FUSE) {
+            /* sum of squares of the raw x, then x * g (rmsnorm.c:17-75 scales after the product) */
+#pragma unroll
+            for (int u = 0; u < GEMV_U; u++)
+#pragma unroll
+                for (int s = 0; s < SEQ; s++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        ssq[s] = fmaf(xf[u][s][e], xf[u][s][e], ssq[s]);
+                        xf[u][s][e] = norm ? xf[u][s][e] * gf[u][e] : xf[u][s][e];
+                    }
+        }
 #pragma unroll
         for (int u = 0; u < GEMV_U; u++)
 #pragma unroll
@@ -212,7 +263,7 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
     }
 
     /* lane i = s * GEMV_R + r ends with the total of (row r, input s) */
-    float mine = 0.0f;
+    float mine = 0.0f, myss = 0.0f;
 #pragma unroll
     for (int r = 0; r < GEMV_R; r++)
 #pragma unroll
@@ -220,26 +271,72 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
             const float t = wave_sum(acc[r][s]);
             if (lane == s * GEMV_R + r) mine = t;
         }
+    if constexpr (FUSE) {
+        if (norm) {
+#pragma unroll
+            for (int s = 0; s < SEQ; s++) {
+                const float t = wave_sum(ssq[s]);
+                if (lane / GEMV_R == s) myss = t;
+            }
+        }
+    }
     if (kp > 1) {
-        if (lane < GEMV_R * SEQ) red[wave][lane] = mine;
+        if (lane < GEMV_R * SEQ) {
+            red[wid][lane] = mine;
+            if constexpr (FUSE) red_ss[wid][lane] = myss;
+        }
         __syncthreads();
         if (wave != 0) return;
         if (lane < GEMV_R * SEQ) {
             mine = 0.0f;
-            for (int w = 0; w < kp; w++) mine += red[w][lane];
+            myss = 0.0f;
+            for (int w = 0; w < kp; w++) {
+                mine += red[wid + w][lane];
+                if constexpr (FUSE) myss += red_ss[wid + w][lane];
+            }
         }
+    }
+    if constexpr (FUSE) {
+        /* one segment: rows are segment 0's */
+        const int r = lane % GEMV_R, s = lane / GEMV_R;
+        const int o = row_base + r;
+        float v = mine;
+        if (norm) v *= 1.0f / sqrtf(myss / (float)in + p.eps);
+        if (lane < GEMV_R * SEQ && o < p.rows && p.bias[0]) v += p.bias[0][o];
+        const int out = p.out[0];
+        if (p.act) {
+            /* lane i holds row r; the up row of gate row r (even) is in lane i + 1 */
+            const float up = __shfl_down(v, 1);
+            float g = v;
+            if (p.act == SMOL_LINEAR_ACT_SWIGLU) {
+                g = g / (1.0f + expf(-g));
+            } else {
+                const float x3 = g * g * g;
+                const float inner = 0.7978845608028654f * (g + 0.044715f * x3);
+                g = 0.5f * g * (1.0f + tanhf(inner));
+            }
+            if (lane < GEMV_R * SEQ && (r & 1) == 0 && o + 1 < p.rows) {
+                const long long j = (long long)s * (out >> 1) + (o >> 1);
+                const float val = g * up;
+                static_cast<float *>(p.y[0])[j] = p.res ? p.res[j] + val : val;
+            }
+        } else if (lane < GEMV_R * SEQ && o < p.rows) {
+            const long long j = (long long)s * out + o;
+            static_cast<float *>(p.y[0])[j] = p.res ? p.res[j] + v : v;
+        }
+        return;
     }
     if (lane < GEMV_R * SEQ) {
         const int r = lane % GEMV_R, s = lane / GEMV_R;
         const int row = row_base + r;
         if (row < p.rows) {
-            /* selects, not p.seg[sg]: a lane-dependent index into the kernel
+            /* selects, not p.y[sg]: a lane-dependent index into the kernel
              * arguments would be lowered through scratch memory */
             const int sg = seg_of(p, row);
-            const int r0 = sg == 0 ? p.seg[0].row0 : sg == 1 ? p.seg[1].row0 : p.seg[2].row0;
-            const int out = sg == 0 ? p.seg[0].out : sg == 1 ? p.seg[1].out : p.seg[2].out;
-            const float *bias = sg == 0 ? p.seg[0].bias : sg == 1 ? p.seg[1].bias : p.seg[2].bias;
-            void *y = sg == 0 ? p.seg[0].y : sg == 1 ? p.seg[1].y : p.seg[2].y;
+            const int r0 = sg == 0 ? p.row0[0] : sg == 1 ? p.row0[1] : p.row0[2];
+            const int out = sg == 0 ? p.out[0] : sg == 1 ? p.out[1] : p.out[2];
+            const float *bias = sg == 0 ? p.bias[0] : sg == 1 ? p.bias[1] : p.bias[2];
+            void *y = sg == 0 ? p.y[0] : sg == 1 ? p.y[1] : p.y[2];
             const int o = row - r0;
             const float v = mine + (bias ? bias[o] : 0.0f);
             if constexpr (YBF)
@@ -286,11 +383,52 @@ __global__ __launch_bounds__(256) void k_split_hilo(const float *x, uint16_t *hi
     }
 }
 
-/* y[s][o] = b[o] (or 0) */
-__global__ __launch_bounds__(256) void k_bias_rows(float *y, const float *b, int seq, int out) {
+/* y[s][o] = b[o] (or 0); add: y[s][o] += b[o] */
+__global__ __launch_bounds__(256) void k_bias_rows(float *y, const float *b, int seq, int out, bool add) {
     const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
     if (i >= (long long)seq * out) return;
-    y[i] = b ? b[i % out] : 0.0f;
+    const float v = b ? b[i % out] : 0.0f;
+    y[i] = add ? y[i] + v : v;
+}
+
+/* out[s][i] = (x[s][i] * w[i]) * r_s, r_s = 1 / sqrtf(sum_i x[s][i]^2 / dim + eps)
+ * (rmsnorm.c:17-75); one workgroup per row, the sum in a fixed order
+ * (per-thread strided partials, then a tree in LDS) */
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(float *out, const float *x, const float *w, int dim,
+                                                      float eps) {
+    __shared__ float part[256];
+    const float *xr = x + (long long)blockIdx.x * dim;
+    float *orow = out + (long long)blockIdx.x * dim;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < dim; i += 256) ss = fmaf(xr[i], xr[i], ss);
+    part[threadIdx.x] = ss;
+    __syncthreads();
+    for (int h = 128; h > 0; h >>= 1) {
+        if ((int)threadIdx.x < h) part[threadIdx.x] += part[threadIdx.x + h];
+        __syncthreads();
+    }
+    const float rinv = 1.0f / sqrtf(part[0] / (float)dim + eps);
+    for (int i = threadIdx.x; i < dim; i += 256) orow[i] = (xr[i] * w[i]) * rinv;
+}
+
+/* y[s][j] = act(t[s][2j]) * t[s][2j + 1] (+ res[s][j]); activation.c:55-88
+ * (SiLU) and :104-125 (GELU, tanh form) */
+__global__ __launch_bounds__(256) void k_act_rows(float *y, const float *t, const float *res, int seq, int half,
+                                                  int act) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long long)seq * half) return;
+    const long long s = i / half, j = i % half;
+    float g = t[s * 2 * half + 2 * j];
+    const float u = t[s * 2 * half + 2 * j + 1];
+    if (act == SMOL_LINEAR_ACT_SWIGLU) {
+        g = g / (1.0f + expf(-g));
+    } else {
+        const float x3 = g * g * g;
+        const float inner = 0.7978845608028654f * (g + 0.044715f * x3);
+        g = 0.5f * g * (1.0f + tanhf(inner));
+    }
+    const float v = g * u;
+    y[i] = res ? res[i] + v : v;
 }
 
 /* ------------------------------------------------------------------ host */
@@ -352,6 +490,8 @@ struct LinState {
     void *ws = nullptr;
     Buf xs;  /* x_hi then x_lo, bf16 */
     Buf y32; /* fp32 result of a bf16-output GEMM */
+    Buf xn;  /* normalised input of a fused-norm GEMM */
+    Buf t;   /* pre-activation product of a fused-activation GEMM */
     std::map<std::tuple<int, int, int>, Plan> plans;
 };
 
@@ -369,6 +509,8 @@ void lin_free(void *p) {
     if (L->ws) hipFree(L->ws);
     if (L->xs.p) hipFree(L->xs.p);
     if (L->y32.p) hipFree(L->y32.p);
+    if (L->xn.p) hipFree(L->xn.p);
+    if (L->t.p) hipFree(L->t.p);
     delete L;
 }
 
@@ -456,64 +598,100 @@ int gemm(LinState *L, hipStream_t st, float *y, const uint16_t *w, const uint16_
     return 0;
 }
 
-int launch_bias(float *y, const float *b, int seq, int out, hipStream_t st) {
+int launch_bias(float *y, const float *b, int seq, int out, hipStream_t st, bool add = false) {
     const long long n = (long long)seq * out;
     if (n <= 0) return 0;
-    hipLaunchKernelGGL(k_bias_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y, b, seq, out);
+    hipLaunchKernelGGL(k_bias_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y, b, seq, out, add);
     LHIP(hipGetLastError());
     return 0;
 }
 
-template <int SEQ, bool XBF, bool YBF>
+int launch_rmsnorm(float *out, const float *x, const float *w, int seq, int dim, float eps, hipStream_t st) {
+    if (seq <= 0 || dim <= 0) return 0;
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3((unsigned)seq), dim3(256), 0, st, out, x, w, dim, eps);
+    LHIP(hipGetLastError());
+    return 0;
+}
+
+/* the operations fused into a GEMV launch (fp32 x and y, one weight) */
+struct GemvFuse {
+    const float *norm_w;
+    float eps;
+    int act;
+    const float *res;
+};
+
+template <int SEQ, bool XBF, bool YBF, bool FUSE>
 int launch_gemv_v(const GemvParams &p, bool vec, hipStream_t st) {
-    const dim3 grid((unsigned)((p.rows + GEMV_R - 1) / GEMV_R)), block(64 * p.kp);
+    const int row_groups = (p.rows + GEMV_R - 1) / GEMV_R;
+    const dim3 grid((unsigned)((row_groups + p.groups - 1) / p.groups)), block(64 * p.kp * p.groups);
     if (vec)
-        hipLaunchKernelGGL((k_gemv<SEQ, XBF, YBF, true>), grid, block, 0, st, p);
+        hipLaunchKernelGGL((k_gemv<SEQ, XBF, YBF, true, FUSE>), grid, block, 0, st, p);
     else
-        hipLaunchKernelGGL((k_gemv<SEQ, XBF, YBF, false>), grid, block, 0, st, p);
+        hipLaunchKernelGGL((k_gemv<SEQ, XBF, YBF, false, FUSE>), grid, block, 0, st, p);
     LHIP(hipGetLastError());
     return 0;
 }
 
 template <int SEQ>
-int launch_gemv_s(const GemvParams &p, bool xbf, bool ybf, bool vec, hipStream_t st) {
-    if (xbf) return ybf ? launch_gemv_v<SEQ, true, true>(p, vec, st) : launch_gemv_v<SEQ, true, false>(p, vec, st);
-    return ybf ? launch_gemv_v<SEQ, false, true>(p, vec, st) : launch_gemv_v<SEQ, false, false>(p, vec, st);
+int launch_gemv_s(const GemvParams &p, bool xbf, bool ybf, bool vec, bool fuse, hipStream_t st) {
+    if (fuse) return launch_gemv_v<SEQ, false, false, true>(p, vec, st);
+    if (xbf)
+        return ybf ? launch_gemv_v<SEQ, true, true, false>(p, vec, st)
+                   : launch_gemv_v<SEQ, true, false, false>(p, vec, st);
+    return ybf ? launch_gemv_v<SEQ, false, true, false>(p, vec, st)
+               : launch_gemv_v<SEQ, false, false, false>(p, vec, st);
 }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
-/* one GEMV launch over n_seg weight segments */
+/* one GEMV launch over n_seg weight segments (f: fused operations, one
+ * segment, fp32 x and y) */
 int run_gemv(smol_attn_ctx *ctx, hipStream_t st, const void *x, bool xbf, bool ybf, int seq, int in, int n_seg,
-             const GemvSeg *segs) {
+             const GemvSeg *segs, const GemvFuse *f = nullptr) {
     GemvParams p{};
     p.x = x;
     p.in = in;
+    if (f) {
+        p.norm_w = f->norm_w;
+        p.eps = f->eps;
+        p.act = f->act;
+        p.res = f->res;
+    }
     int rows = 0;
-    bool vec = (in % 8) == 0 && aligned16(x);
+    bool vec = (in % 8) == 0 && aligned16(x) && aligned16(p.norm_w);
     for (int i = 0; i < GEMV_SEGS; i++) {
         if (i < n_seg) {
-            p.seg[i] = segs[i];
-            p.seg[i].row0 = rows;
+            p.w[i] = segs[i].w;
+            p.bias[i] = segs[i].bias;
+            p.y[i] = segs[i].y;
+            p.out[i] = segs[i].out;
+            p.row0[i] = rows;
             rows += segs[i].out;
             vec = vec && aligned16(segs[i].w);
         } else {
-            p.seg[i] = GemvSeg{segs[0].w, nullptr, nullptr, 0, INT_MAX};
+            p.w[i] = segs[0].w;
+            p.bias[i] = nullptr;
+            p.y[i] = nullptr;
+            p.out[i] = 0;
+            p.row0[i] = INT_MAX;
         }
     }
     p.rows = rows;
     const int chunks = (in + 7) / 8;
     p.kp = std::max(1, std::min(GEMV_MAX_KP, (chunks + 64 * GEMV_U - 1) / (64 * GEMV_U)));
+    p.groups = std::max(1, std::min(GEMV_WG_WAVES / p.kp, (rows + GEMV_R - 1) / GEMV_R));
     if (rows <= 0) return 0;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     smol_internal_timing_events(ctx, LIN_TIMING_KIND, &e0, &e1);
     if (e0) LHIP(hipEventRecord(e0, st));
     int rc;
+    const bool fuse = f != nullptr;
     switch (seq) {
-    case 1: rc = launch_gemv_s<1>(p, xbf, ybf, vec, st); break;
-    case 2: rc = launch_gemv_s<2>(p, xbf, ybf, vec, st); break;
-    case 3: rc = launch_gemv_s<3>(p, xbf, ybf, vec, st); break;
-    default: rc = launch_gemv_s<4>(p, xbf, ybf, vec, st); break;
+    case 1: rc = launch_gemv_s<1>(p, xbf, ybf, vec, fuse, st); break;
+    case 2: rc = launch_gemv_s<2>(p, xbf, ybf, vec, fuse, st); break;
+    case 3: rc = launch_gemv_s<3>(p, xbf, ybf, vec, fuse, st); break;
+    default: rc = launch_gemv_s<4>(p, xbf, ybf, vec, fuse, st); break;
     }
     if (rc) return rc;
     if (e1) LHIP(hipEventRecord(e1, st));
@@ -524,35 +702,33 @@ int run_gemv(smol_attn_ctx *ctx, hipStream_t st, const void *x, bool xbf, bool y
  * SMOL_LINEAR_GEMV_MAX_SEQ rows (in_dim 0, and shapes hipBLASLt has no
  * kernel for) */
 int run_gemv_rows(smol_attn_ctx *ctx, hipStream_t st, void *y, bool ybf, const void *x, bool xbf,
-                  const uint16_t *w, const float *bias, int seq, int in, int out) {
+                  const uint16_t *w, const float *bias, int seq, int in, int out, const GemvFuse *f = nullptr) {
     const size_t xe = xbf ? 2 : 4, ye = ybf ? 2 : 4;
+    const int ycols = f && f->act ? out / 2 : out;
     for (int s0 = 0; s0 < seq; s0 += SMOL_LINEAR_GEMV_MAX_SEQ) {
         const int n = std::min(SMOL_LINEAR_GEMV_MAX_SEQ, seq - s0);
-        const GemvSeg sg{w, bias, static_cast<char *>(y) + (size_t)s0 * out * ye, out, 0};
+        const GemvSeg sg{w, bias, static_cast<char *>(y) + (size_t)s0 * ycols * ye, out};
         const void *xs = x ? static_cast<const char *>(x) + (size_t)s0 * in * xe : nullptr;
-        if (int rc = run_gemv(ctx, st, xs, xbf, ybf, n, in, 1, &sg)) return rc;
+        GemvFuse fb;
+        if (f) {
+            fb = *f;
+            if (fb.res) fb.res += (size_t)s0 * ycols;
+        }
+        if (int rc = run_gemv(ctx, st, xs, xbf, ybf, n, in, 1, &sg, f ? &fb : nullptr)) return rc;
     }
     return 0;
 }
 
-/* the GEMM path for one weight: y (fp32 or bf16) = x W^T (+ bias) */
-int run_gemm(smol_attn_ctx *ctx, LinState *L, hipStream_t st, void *y, bool ybf, const void *x, bool xbf,
-             const uint16_t *w, const float *bias, int seq, int in, int out) {
-    {
-        Plan *pl = nullptr;
-        const int rc = get_plan(L, seq, in, out, &pl);
-        if (rc < 0) return rc;
-        if (rc > 0) return run_gemv_rows(ctx, st, y, ybf, x, xbf, w, bias, seq, in, out);
-    }
-    const size_t ny = (size_t)seq * out;
-    float *y32 = static_cast<float *>(y);
-    if (ybf) {
-        if (int rc = reserve(L->y32, ny * 4, st)) return rc;
-        y32 = static_cast<float *>(L->y32.p);
-    }
-    hipEvent_t e0 = nullptr, e1 = nullptr;
-    smol_internal_timing_events(ctx, LIN_TIMING_KIND, &e0, &e1);
-    if (e0) LHIP(hipEventRecord(e0, st));
+/* 1: hipBLASLt has a kernel for the shape, 0: it has none, < 0: error */
+int gemm_available(LinState *L, int seq, int in, int out) {
+    Plan *pl = nullptr;
+    const int rc = get_plan(L, seq, in, out, &pl);
+    return rc < 0 ? rc : rc == 0;
+}
+
+/* y32 (+)= x W^T on MFMA (acc: y32 already holds the start value) */
+int gemm_core(LinState *L, hipStream_t st, float *y32, const void *x, bool xbf, const uint16_t *w, int seq,
+              int in, int out, bool acc) {
     const uint16_t *xh = static_cast<const uint16_t *>(x), *xl = nullptr;
     if (!xbf) {
         const long long n = (long long)seq * in;
@@ -567,11 +743,65 @@ int run_gemm(smol_attn_ctx *ctx, LinState *L, hipStream_t st, void *y, bool ybf,
         xh = h;
         xl = l;
     }
-    if (bias)
-        if (int rc = launch_bias(y32, bias, seq, out, st)) return rc;
-    if (int rc = gemm(L, st, y32, w, xh, seq, in, out, bias ? 1.0f : 0.0f)) return rc;
+    if (int rc = gemm(L, st, y32, w, xh, seq, in, out, acc ? 1.0f : 0.0f)) return rc;
     if (xl)
         if (int rc = gemm(L, st, y32, w, xl, seq, in, out, 1.0f)) return rc;
+    return 0;
+}
+
+/* the GEMM path with the fused operations run as their own kernels:
+ * norm -> L->xn, product (+ bias) -> y or L->t, activation (+ residual) -> y */
+int run_gemm_ops(smol_attn_ctx *ctx, LinState *L, hipStream_t st, float *y, const float *x, const uint16_t *w,
+                 const float *bias, int seq, int in, int out, const GemvFuse &f) {
+    if (int ok = gemm_available(L, seq, in, out); ok <= 0)
+        return ok < 0 ? ok : run_gemv_rows(ctx, st, y, false, x, false, w, bias, seq, in, out, &f);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    smol_internal_timing_events(ctx, LIN_TIMING_KIND, &e0, &e1);
+    if (e0) LHIP(hipEventRecord(e0, st));
+    const float *xin = x;
+    if (f.norm_w) {
+        if (int rc = reserve(L->xn, (size_t)seq * in * 4, st)) return rc;
+        if (int rc = launch_rmsnorm(static_cast<float *>(L->xn.p), x, f.norm_w, seq, in, f.eps, st)) return rc;
+        xin = static_cast<const float *>(L->xn.p);
+    }
+    if (f.act) {
+        if (int rc = reserve(L->t, (size_t)seq * out * 4, st)) return rc;
+        float *t = static_cast<float *>(L->t.p);
+        if (bias)
+            if (int rc = launch_bias(t, bias, seq, out, st)) return rc;
+        if (int rc = gemm_core(L, st, t, xin, false, w, seq, in, out, bias != nullptr)) return rc;
+        const long long n = (long long)seq * (out / 2);
+        hipLaunchKernelGGL(k_act_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y, t, f.res, seq,
+                           out / 2, f.act);
+        LHIP(hipGetLastError());
+    } else {
+        if (f.res && f.res != y)
+            LHIP(hipMemcpyAsync(y, f.res, (size_t)seq * out * 4, hipMemcpyDeviceToDevice, st));
+        if (bias)
+            if (int rc = launch_bias(y, bias, seq, out, st, f.res != nullptr)) return rc;
+        if (int rc = gemm_core(L, st, y, xin, false, w, seq, in, out, f.res || bias)) return rc;
+    }
+    if (e1) LHIP(hipEventRecord(e1, st));
+    return 0;
+}
+
+/* the GEMM path for one weight: y (fp32 or bf16) = x W^T (+ bias) */
+int run_gemm(smol_attn_ctx *ctx, LinState *L, hipStream_t st, void *y, bool ybf, const void *x, bool xbf,
+             const uint16_t *w, const float *bias, int seq, int in, int out) {
+    if (int ok = gemm_available(L, seq, in, out); ok <= 0)
+        return ok < 0 ? ok : run_gemv_rows(ctx, st, y, ybf, x, xbf, w, bias, seq, in, out);
+    const size_t ny = (size_t)seq * out;
+    float *y32 = static_cast<float *>(y);
+    if (ybf) {
+        if (int rc = reserve(L->y32, ny * 4, st)) return rc;
+        y32 = static_cast<float *>(L->y32.p);
+    }
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    smol_internal_timing_events(ctx, LIN_TIMING_KIND, &e0, &e1);
+    if (e0) LHIP(hipEventRecord(e0, st));
+    if (bias)
+        if (int rc = launch_bias(y32, bias, seq, out, st)) return rc;
+    if (int rc = gemm_core(L, st, y32, x, xbf, w, seq, in, out, bias != nullptr)) return rc;
     if (e1) LHIP(hipEventRecord(e1, st));
     if (ybf && smol_launch_to_bf16_trunc(y32, static_cast<uint16_t *>(y), (long long)ny, st))
         return lfail(SMOL_ATTN_ERR_DEVICE, "linear: truncation launch failed");
@@ -623,12 +853,57 @@ extern "C" int smol_linear_qkv_dev(smol_attn_ctx *ctx, void *q, void *k, void *v
     hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
     GemvSeg segs[GEMV_SEGS];
     int n = 0;
-    if (q_dim) segs[n++] = GemvSeg{wq, nullptr, q, q_dim, 0};
+    if (q_dim) segs[n++] = GemvSeg{wq, nullptr, q, q_dim};
     if (kv_dim) {
-        segs[n++] = GemvSeg{wk, nullptr, k, kv_dim, 0};
-        segs[n++] = GemvSeg{wv, nullptr, v, kv_dim, 0};
+        segs[n++] = GemvSeg{wk, nullptr, k, kv_dim};
+        segs[n++] = GemvSeg{wv, nullptr, v, kv_dim};
     }
     return run_gemv(ctx, st, x, x_dtype == SMOL_ATTN_BF16, y_dtype == SMOL_ATTN_BF16, seq, in_dim, n, segs);
+}
+
+extern "C" int smol_linear_ops_dev(smol_attn_ctx *ctx, float *y, const float *x, const uint16_t *w,
+                                   const float *bias, int seq, int in_dim, int out_dim, const smol_linear_ops *ops) {
+    if (!ctx) return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_ops_dev: null context");
+    const smol_linear_ops none{};
+    if (!ops) ops = &none;
+    if (seq < 0 || in_dim <= 0 || out_dim < 0) return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_ops_dev: sizes");
+    if (ops->act != SMOL_LINEAR_ACT_NONE && ops->act != SMOL_LINEAR_ACT_SWIGLU && ops->act != SMOL_LINEAR_ACT_GEGLU)
+        return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_ops_dev: act");
+    if (ops->act && (out_dim & 1)) return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_ops_dev: act needs an even out_dim");
+    if (seq == 0 || out_dim == 0) return SMOL_ATTN_OK;
+    if (!y || !x || !w) return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_ops_dev: null pointer");
+    if (x == y || (ops->residual && ops->residual != y &&
+                   !((const char *)ops->residual + (size_t)seq * (ops->act ? out_dim / 2 : out_dim) * 4 <=
+                         (const char *)y ||
+                     (const char *)y + (size_t)seq * (ops->act ? out_dim / 2 : out_dim) * 4 <=
+                         (const char *)ops->residual)))
+        return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_ops_dev: y overlaps x, or partly overlaps the residual");
+    if ((long long)seq * in_dim > INT_MAX / 4 || (long long)seq * out_dim > INT_MAX / 4 ||
+        (long long)out_dim * in_dim > (1LL << 40))
+        return lfail(SMOL_ATTN_ERR_UNSUPPORTED, "smol_linear_ops_dev: sizes beyond the supported range");
+    LHIP(hipSetDevice(smol_internal_ctx_device(ctx)));
+    hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
+    const GemvFuse f{ops->norm_weight, ops->norm_eps, ops->act, ops->residual};
+    if (seq <= SMOL_LINEAR_GEMV_MAX_SEQ) return run_gemv_rows(ctx, st, y, false, x, false, w, bias, seq, in_dim, out_dim, &f);
+    LinState *L = nullptr;
+    if (int rc = lin_state(ctx, &L)) return rc;
+    return run_gemm_ops(ctx, L, st, y, x, w, bias, seq, in_dim, out_dim, f);
+}
+
+extern "C" int smol_rms_norm_dev(smol_attn_ctx *ctx, float *out, const float *x, const float *weight, int seq,
+                                 int dim, float eps) {
+    if (!ctx) return lfail(SMOL_ATTN_ERR_ARG, "smol_rms_norm_dev: null context");
+    if (seq < 0 || dim < 0) return lfail(SMOL_ATTN_ERR_ARG, "smol_rms_norm_dev: negative size");
+    if (seq == 0 || dim == 0) return SMOL_ATTN_OK;
+    if (!out || !x || !weight) return lfail(SMOL_ATTN_ERR_ARG, "smol_rms_norm_dev: null pointer");
+    LHIP(hipSetDevice(smol_internal_ctx_device(ctx)));
+    hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    smol_internal_timing_events(ctx, LIN_TIMING_KIND, &e0, &e1);
+    if (e0) LHIP(hipEventRecord(e0, st));
+    if (int rc = launch_rmsnorm(out, x, weight, seq, dim, eps, st)) return rc;
+    if (e1) LHIP(hipEventRecord(e1, st));
+    return 0;
 }
 
 /* ------------------------------------------------- reference-signature drop-ins */

@@ -85,6 +85,8 @@ SIGNATURES = [
     ("smol_linear_dev", [_vp, _vp, _c_int, _vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int], _c_int),
     ("smol_linear_qkv_dev", [_vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _vp, _vp, _vp, _c_int, _c_int, _c_int,
                              _c_int], _c_int),
+    ("smol_linear_ops_dev", [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp], _c_int),
+    ("smol_rms_norm_dev", [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_float], _c_int),
     # reference-signature drop-ins (host fp32 arrays)
     ("smol_linear_bf16", [_FP, _FP, _U16P, _FP, _c_int, _c_int, _c_int], None),
     ("smol_linear_nobias_bf16", [_FP, _FP, _U16P, _c_int, _c_int, _c_int], None),
@@ -624,6 +626,40 @@ def linear_qkv(ctx, x, wq, wk, wv, out_bf16=False):
                                       _dev(x, "x"), _dtype_code(x), _wbits(wq, "wq"), _wbits(wk, "wk"),
                                       _wbits(wv, "wv"), seq, in_dim, q_dim, kv_dim), "smol_linear_qkv_dev")
     return q, k, v
+
+
+ACT_NONE, ACT_SWIGLU, ACT_GEGLU = 0, 1, 2
+
+
+class _LinearOps(ctypes.Structure):
+    _fields_ = [("norm_weight", _vp), ("norm_eps", _c_float), ("act", _c_int), ("residual", _vp)]
+
+
+def linear_ops(ctx, x, w, bias=None, norm_weight=None, eps=1e-6, act=ACT_NONE, residual=None, out=None):
+    """y = residual + act(rmsnorm(x) W^T + bias) on the device (smol_linear_ops_dev); fp32 x [seq, in],
+    bf16 w [out, in]; y [seq, out] (or [seq, out / 2] with an activation). `out` may be `residual`."""
+    import torch
+    seq, in_dim = x.shape
+    out_dim = w.shape[0]
+    if out is None:
+        out = torch.empty((seq, out_dim // 2 if act else out_dim), dtype=torch.float32, device=x.device)
+    ops = _LinearOps(_dev(norm_weight, "norm_weight") if norm_weight is not None else None, eps, act,
+                     _dev(residual, "residual") if residual is not None else None)
+    _check(load().smol_linear_ops_dev(ctx.h, _dev(out, "out"), _dev(x, "x"), _wbits(w, "w"),
+                                      _dev(bias, "bias") if bias is not None else None, seq, in_dim, out_dim,
+                                      ctypes.byref(ops)), "smol_linear_ops_dev")
+    return out
+
+
+def rms_norm(ctx, x, weight, eps, out=None):
+    """smol_rms_norm_dev: fp32 rows [seq, dim]"""
+    import torch
+    seq, dim = x.shape
+    if out is None:
+        out = torch.empty_like(x)
+    _check(load().smol_rms_norm_dev(ctx.h, _dev(out, "out"), _dev(x, "x"), _dev(weight, "weight"), seq, dim,
+                                    ctypes.c_float(eps)), "smol_rms_norm_dev")
+    return out
 
 
 def _u16(a):

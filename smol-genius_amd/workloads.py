@@ -27,6 +27,14 @@ common/vision/siglip.c:126-128, exports/qwen_asr/qwen_asr.c:1595-1620):
   *_qknorm            qwen06b_decode / qwen06b_prefill with the decoder's
                       per-head Q/K RMSNorm (weights near 1, eps 1e-6) in
                       front of RoPE (qkn_decoder.c:487-491).
+  qwen06b_proj_decode / qwen06b_proj_prefill
+                      the bf16-weight projections of one Qwen3-ASR-0.6B
+                      decoder layer (hidden 1024, Q 16 x 128, K/V 8 x 128,
+                      intermediate 3072): fused Q/K/V 1024 -> 2048 + 1024 +
+                      1024, o_proj 2048 -> 1024, gate_up 1024 -> 6144, down
+                      3072 -> 1024 (qkn_decoder.c:474-476, 531, 546, 552 and
+                      :635, 679, 693, 699), for 1 token and for 1536 tokens;
+                      28 layers of distinct weights.
 
 Cached rows are bf16 (round to nearest even) and are already rotated, as a
 decoder leaves them; the tokens a call appends are fp32 (projection outputs)
@@ -222,6 +230,52 @@ class Stream(Workload):
                 "rope_theta": self.theta}
 
 
+class Projections(Workload):
+    """The four bf16-weight projections of one decoder layer on `seq` fp32 rows.
+    kinds: name -> (in_dim, [out_dim of each weight]); "qkv" has three weights."""
+
+    def __init__(self, name, seq, hidden, q_dim, kv_dim, inter, layers, seed):
+        self.name, self.seq, self.layers, self.seed = name, seq, layers, seed
+        self.kinds = {"qkv": (hidden, [q_dim, kv_dim, kv_dim]), "o_proj": (q_dim, [hidden]),
+                      "gate_up": (hidden, [2 * inter]), "down": (inter, [hidden])}
+
+    def weight_bytes(self, kind):
+        n_in, outs = self.kinds[kind]
+        return 2 * n_in * sum(outs)
+
+    def algorithmic_bytes(self, kind=None):
+        """weights (bf16) + x (fp32) + y (fp32) of one launch (or one layer)"""
+        kinds = [kind] if kind else list(self.kinds)
+        b = 0
+        for k in kinds:
+            n_in, outs = self.kinds[k]
+            b += self.weight_bytes(k) + 4 * self.seq * (n_in + sum(outs))
+        return b
+
+    def flops(self, kind=None):
+        kinds = [kind] if kind else list(self.kinds)
+        return sum(2 * self.seq * self.kinds[k][0] * sum(self.kinds[k][1]) for k in kinds)
+
+    def inputs(self):
+        """x [seq, in] fp32 per kind, and bf16 weight bits per (layer, kind) as a list per kind"""
+        x = {k: synth.normal(self.seed * 10 + i, (self.seq, n_in)) for i, (k, (n_in, _)) in
+             enumerate(self.kinds.items())}
+        return {"x": x}
+
+    def layer_weights(self, layer, kind):
+        """bf16 bits of the weights of one kind in one layer (seeded; for the CPU side)"""
+        n_in, outs = self.kinds[kind]
+        ki = list(self.kinds).index(kind)
+        return [synth.f32_to_bf16_bits(synth.normal(self.seed * 1000 + layer * 16 + ki * 4 + j, (o, n_in),
+                                                    1.0 / np.sqrt(n_in)))
+                for j, o in enumerate(outs)]
+
+    def describe(self):
+        return {"workload": self.name, "tokens": self.seq, "layers_rotated": self.layers,
+                "projections": {k: {"in": v[0], "out": v[1]} for k, v in self.kinds.items()},
+                "weights": "bf16 [out][in], N(0, 1/in)", "x": "fp32 N(0,1)"}
+
+
 def gemma_lengths(seed=4, n=16, lo=512, hi=4096):
     return [int(x) for x in synth.uniform_int(seed * 1000 + 7, n, lo, hi)]
 
@@ -246,4 +300,6 @@ def all_workloads():
                                               "qwen06b_decode_qknorm"),
         "qwen06b_prefill_qknorm": with_qk_norm(Prefill("", 16, 8, 128, 0, 1536, 1e6, seed=2),
                                                "qwen06b_prefill_qknorm"),
+        "qwen06b_proj_decode": Projections("qwen06b_proj_decode", 1, 1024, 2048, 1024, 3072, 28, seed=8),
+        "qwen06b_proj_prefill": Projections("qwen06b_proj_prefill", 1536, 1024, 2048, 1024, 3072, 28, seed=9),
     }

@@ -44,3 +44,15 @@ def linear_inputs(seed, seq, n_in, n_out, bias):
     w = synth.f32_to_bf16_bits(synth.normal(seed * 3 + 1, (n_out, n_in), 1.0 / np.sqrt(max(n_in, 1))))
     b = synth.normal(seed * 3 + 2, (n_out,), 0.1) if bias else None
     return x, w, b
+
+
+def norm_row_inputs(seed, seq, dim):
+    """x [seq, dim] ~N(0, 1) and a weight [dim] near 1"""
+    x = synth.normal(seed * 3 + 0, (seq, dim))
+    w = (1.0 + 0.1 * synth.normal(seed * 3 + 1, (dim,))).astype(np.float32)
+    return x, w
+
+
+def glu_inputs(seed, seq, inter):
+    """interleaved (gate, up) rows [seq, 2 * inter] ~N(0, 2^2)"""
+    return synth.normal(seed * 3, (seq, 2 * inter), 2.0)

@@ -1,10 +1,11 @@
 """Writes the projection fixtures (ref_linear.json / ref_linear.npz) from the
 compiled reference.
 
-The reference's common/kernels/matmul.c, bf16_matvec_{avx,generic}.c and
-threading.c are compiled by ``oracle/Makefile`` into ``oracle/_ref/``; this
+The reference's common/kernels/matmul.c, bf16_matvec_{avx,generic}.c,
+rmsnorm.c, activation.c and threading.c are compiled by ``oracle/Makefile`` into ``oracle/_ref/``; this
 script calls smol_linear_bf16, smol_linear_nobias_bf16,
-smol_linear_nobias_bf16_qkv and smol_matmul_t_bf16 there (one thread) on
+smol_linear_nobias_bf16_qkv, smol_matmul_t_bf16, smol_rms_norm,
+smol_swiglu_multiply and smol_geglu_multiply there (one thread) on
 seeded inputs and stores the outputs. Inputs are regenerated from the seeds by
 ``linear_inputs``; their checksum is stored with the outputs.
 
@@ -20,7 +21,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 from oracle import RefLib, simd_branch  # noqa: E402
-from gen_golden_inputs import digest, linear_inputs  # noqa: E402
+from gen_golden_inputs import digest, glu_inputs, linear_inputs, norm_row_inputs  # noqa: E402
 
 OUT = os.path.dirname(os.path.abspath(__file__))
 
@@ -42,6 +43,12 @@ CASES = [
     ("mmt_4_256_130", "matmul_t", 4, 256, 130, False),
     ("mmt_1_128_64", "matmul_t", 1, 128, 64, False),
 ]
+
+
+# (seq, dim) of the full-row RMSNorm cases; 72 and 7 have a scalar tail
+NORM_ROWS = [(1, 1024), (3, 2048), (2, 72), (2, 7)]
+# (seq, intermediate, act): 1 SwiGLU, 2 GeGLU
+GLU = [(1, 3072, 1), (4, 100, 1), (1, 3072, 2), (3, 17, 2)]
 
 
 def main():
@@ -66,6 +73,20 @@ def main():
             dg = digest(x, w) if b is None else digest(x, w, b)
         meta["cases"].append(dict(name=name, kind=kind, seed=seed, seq=seq, in_dim=n_in, out_dim=n_out,
                                   bias=has_b, digest=dg))
+    # smol_rms_norm (rmsnorm.c:17-75) and the gated activations (activation.c:55-125)
+    meta["norm"], meta["glu"] = [], []
+    for i, (seq, dim) in enumerate(NORM_ROWS):
+        seed = 5500 + i
+        x, w = norm_row_inputs(seed, seq, dim)
+        name = "rms_%d_%d" % (seq, dim)
+        arrays[name] = ref.rms_norm(x, w, 1e-6)
+        meta["norm"].append(dict(name=name, seed=seed, seq=seq, dim=dim, eps=1e-6, digest=digest(x, w)))
+    for i, (seq, inter, act) in enumerate(GLU):
+        seed = 5600 + i
+        gu = glu_inputs(seed, seq, inter)
+        name = "%s_%d_%d" % ("swiglu" if act == 1 else "geglu", seq, inter)
+        arrays[name] = ref.glu(gu, act)
+        meta["glu"].append(dict(name=name, seed=seed, seq=seq, inter=inter, act=act, digest=digest(gu)))
     np.savez_compressed(os.path.join(OUT, "ref_linear.npz"), **arrays)
     with open(os.path.join(OUT, "ref_linear.json"), "w") as f:
         json.dump(meta, f, indent=1)

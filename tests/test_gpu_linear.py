@@ -267,3 +267,66 @@ def test_dropin_weight_cache(sa, oracle):
         check(res[i], oracle.linear_bf16(x, w), x, w, None, "cached weight %d" % i)
     np.testing.assert_array_equal(res[0], res[2])
     np.testing.assert_array_equal(res[1], res[3])
+
+
+# ------------------------------------------- the decoder layer's fused operations
+
+OPS_CASES = [
+    # seq, in, out, norm, act, residual ("y": in place, "sep": separate), bias
+    (1, 1024, 6144, True, 1, None, False),    # post-attention norm + gate_up + SwiGLU
+    (1, 2048, 1024, False, 0, "y", False),    # o_proj + residual add in place
+    (1, 3072, 1024, False, 0, "y", False),    # down + residual add (three waves)
+    (1, 1024, 4096, True, 0, None, False),    # input norm + projection
+    (2, 512, 96, True, 2, "sep", True),       # GeGLU with bias and a separate residual
+    (3, 1003, 40, True, 1, "y", True),        # element loads
+    (4, 3072, 64, True, 0, "sep", False),
+    (26, 1024, 6144, True, 1, None, False),   # the same operations on the GEMM path
+    (26, 2048, 1024, False, 0, "y", False),
+    (64, 512, 96, True, 2, "sep", True),
+    (40, 1003, 40, True, 1, "y", True),
+    (300, 3072, 1024, False, 0, "sep", True),
+]
+
+
+@pytest.mark.parametrize("case", OPS_CASES, ids=lambda c: "s%d_in%d_out%d_n%d_a%d_%s%s" % (
+    c[0], c[1], c[2], c[3], c[4], c[5] or "nores", "_b" * c[6]))
+def test_linear_ops(ctx, sa, oracle, case):
+    seq, n_in, n_out, norm, act, res, has_b = case
+    print("ops", case, flush=True)
+    x, w, b = linear_inputs(9500 + n_in + n_out, seq, n_in, n_out, has_b)
+    g = (1.0 + 0.1 * synth.normal(9600 + n_in, (n_in,))).astype(np.float32) if norm else None
+    cols = n_out // 2 if act else n_out
+    r = synth.normal(9700 + n_out, (seq, cols)) if res else None
+    # oracle composition: rms_norm -> linear (+ bias) -> activation -> + residual
+    xn = oracle.rms_norm(x, g, 1e-6) if norm else x
+    t = oracle.linear_bf16(xn, w, b)
+    ref = oracle.glu(t, act) if act else t
+    if res:
+        ref = (r.astype(np.float64) + ref).astype(np.float32)
+    rd = dev(r) if res else None
+    out = rd if res == "y" else None
+    y = sa.linear_ops(ctx, dev(x), dev_bits(w), dev(b) if has_b else None, norm_weight=dev(g) if norm else None,
+                      eps=1e-6, act=act, residual=rd, out=out)
+    ctx.synchronize()
+    got = y.cpu().numpy()
+    assert got.shape == (seq, cols)
+    assert_parity(got, ref, "ops %s" % (case,))
+    if not act:
+        # without an activation the fp32 bound of the product applies (plus the norm's rounding)
+        lim = bound(xn, w, b) + 4 * 2.0 ** -24 * (np.abs(t) + (np.abs(r) if res else 0))
+        assert (np.abs(got.astype(np.float64) - ref) <= lim).all()
+
+
+def test_rms_norm_dev(ctx, sa, oracle):
+    for seq, dim in [(1, 1024), (5, 72), (2, 7), (3, 3072), (1536, 1024)]:
+        print("rms_norm", seq, dim, flush=True)
+        x = synth.normal(77 + dim, (seq, dim), 3.0)
+        w = (1.0 + 0.1 * synth.normal(78 + dim, (dim,))).astype(np.float32)
+        ref = oracle.rms_norm(x, w, 1e-6)
+        xd = dev(x)
+        y = sa.rms_norm(ctx, xd, dev(w), 1e-6)
+        ctx.synchronize()
+        np.testing.assert_allclose(y.cpu().numpy(), ref, rtol=2e-6, atol=1e-6)
+        sa.rms_norm(ctx, xd, dev(w), 1e-6, out=xd)   # in place
+        ctx.synchronize()
+        np.testing.assert_allclose(xd.cpu().numpy(), ref, rtol=2e-6, atol=1e-6)

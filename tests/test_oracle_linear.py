@@ -158,3 +158,62 @@ def test_planted_mistakes_are_caught(golden_linear, oracle):
     ws = synth.f32_to_bf16_bits(np.array([[256.0, 2.0, 1.0]], np.float32))
     rne = synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(np.array([259.0], np.float32)))[0]
     assert rne == 260.0 and synth.bf16_bits_to_f32(oracle.bf16_linear_nobias(xs, ws))[0, 0] != rne
+
+
+# ------------------------------------------------- RMSNorm and the gated activations
+
+def test_rms_norm_matches_reference(golden_linear, oracle):
+    from gen_golden_inputs import norm_row_inputs
+    meta, data = golden_linear
+    assert len(meta["norm"]) == 4
+    for c in meta["norm"]:
+        x, w = norm_row_inputs(c["seed"], c["seq"], c["dim"])
+        assert digest(x, w) == c["digest"]
+        y = oracle.rms_norm(x, w, c["eps"])
+        np.testing.assert_allclose(y, data[c["name"]], rtol=4e-6, atol=1e-7)
+
+
+def test_rms_norm_closed_forms(oracle):
+    # a constant row normalises to the weight times the sign; float64 brute force elsewhere
+    w = (1.0 + 0.1 * synth.normal(41, (96,))).astype(np.float32)
+    x = np.full((2, 96), 3.0, np.float32)
+    x[1] *= -1
+    y = oracle.rms_norm(x, w, 0.0)
+    np.testing.assert_allclose(y[0], w, rtol=2e-7)
+    np.testing.assert_allclose(y[1], -w, rtol=2e-7)
+    x = synth.normal(42, (3, 200), 5.0)
+    w2 = (1.0 + 0.1 * synth.normal(43, (200,))).astype(np.float32)
+    r = 1.0 / np.sqrt((x.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-5)
+    np.testing.assert_allclose(oracle.rms_norm(x, w2, 1e-5), x * w2 * r, rtol=2e-6)
+    # eps matters for a tiny row
+    t = np.full((1, 16), 1e-4, np.float32)
+    np.testing.assert_allclose(oracle.rms_norm(t, np.ones(16, np.float32), 1e-6)[0],
+                               1e-4 / np.sqrt(1e-8 + 1e-6), rtol=1e-5)
+
+
+def test_glu_matches_reference(golden_linear, oracle):
+    from gen_golden_inputs import glu_inputs
+    meta, data = golden_linear
+    assert len(meta["glu"]) == 4
+    for c in meta["glu"]:
+        gu = glu_inputs(c["seed"], c["seq"], c["inter"])
+        assert digest(gu) == c["digest"]
+        np.testing.assert_allclose(oracle.glu(gu, c["act"]), data[c["name"]], rtol=5e-5, atol=1e-6)
+
+
+def test_glu_closed_forms_and_float64(oracle):
+    gu = np.array([[0.0, 5.0, 30.0, 2.0, -30.0, 2.0, 1.0, 1.0]], np.float32)
+    s = oracle.glu(gu, 1)[0]
+    assert s[0] == 0.0 and abs(s[1] - 60.0) < 1e-4 and abs(s[2]) < 1e-10
+    g = oracle.glu(gu, 2)[0]
+    assert g[0] == 0.0 and abs(g[1] - 60.0) < 1e-4 and abs(g[2]) < 1e-10
+    x = synth.normal(44, (3, 2 * 64), 2.0).astype(np.float64)
+    gate, up = x[:, 0::2], x[:, 1::2]
+    silu = gate / (1 + np.exp(-gate)) * up
+    gelu = 0.5 * gate * (1 + np.tanh(np.sqrt(2 / np.pi) * (gate + 0.044715 * gate ** 3))) * up
+    np.testing.assert_allclose(oracle.glu(x, 1), silu, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(oracle.glu(x, 2), gelu, rtol=1e-5, atol=1e-6)
+    # planted: gate and up swapped, or the pairs read as halves, are caught
+    assert not np.allclose(up / (1 + np.exp(-up)) * gate, oracle.glu(x, 1), rtol=1e-3)
+    halves = x[:, :64] / (1 + np.exp(-x[:, :64])) * x[:, 64:]
+    assert not np.allclose(halves, oracle.glu(x, 1), rtol=1e-3)
