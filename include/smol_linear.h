@@ -93,12 +93,21 @@ SMOL_ATTN_API int smol_linear_ops_dev(smol_attn_ctx *ctx, float *y, const float 
                                       const float *bias, int seq, int in_dim, int out_dim,
                                       const smol_linear_ops *ops);
 
-/* out[s][i] = (x[s][i] * weight[i]) * (1 / sqrtf(sum_i x[s][i]^2 / dim + eps));
- * smol_rms_norm (common/kernels/rmsnorm.c:17-75): the decoders' final norm
- * and the Gemma 3 post-sublayer norms (qkn_decoder.c:682-686, 701-702).
- * out may equal x. */
-SMOL_ATTN_API int smol_rms_norm_dev(smol_attn_ctx *ctx, float *out, const float *x, const float *weight, int seq,
-                                    int dim, float eps);
+/* The Q/K/V projections of smol_linear_qkv_dev (fp32) behind the layer's
+ * input RMSNorm (norm_weight [in_dim], or NULL for none): one launch for
+ * seq <= SMOL_LINEAR_GEMV_MAX_SEQ (qkn_decoder.c:634-639). */
+SMOL_ATTN_API int smol_linear_qkv_norm_dev(smol_attn_ctx *ctx, float *q, float *k, float *v, const float *x,
+                                           const uint16_t *wq, const uint16_t *wk, const uint16_t *wv, int seq,
+                                           int in_dim, int q_dim, int kv_dim, const float *norm_weight,
+                                           float norm_eps);
+
+/* out[s][i] = residual[s][i] + (x[s][i] * weight[i]) * (1 / sqrtf(sum_i x[s][i]^2 / dim + eps)),
+ * without the residual term when residual is NULL; smol_rms_norm
+ * (common/kernels/rmsnorm.c:17-75), plus the smol_add_inplace that follows
+ * it in the Gemma 3 post-sublayer norms (qkn_decoder.c:682-686, 701-704).
+ * out may equal x or residual. */
+SMOL_ATTN_API int smol_rms_norm_dev(smol_attn_ctx *ctx, float *out, const float *x, const float *weight,
+                                    const float *residual, int seq, int dim, float eps);
 
 #ifdef __cplusplus
 }

@@ -113,6 +113,51 @@ SMOL_ATTN_API int smol_qkn_attn_read_cache(const void *owner, int layer, int pos
  * context). Unbinding an unknown owner is not an error. */
 SMOL_ATTN_API int smol_qkn_attn_unbind(const void *owner);
 
+/* ---- the whole decoder layer on the device ------------------------------
+ *
+ * With the projections on the GPU (smol_linear.h), a binding with
+ * on_device = 1 and bf16 = 0 runs a complete layer of qkn_decoder_forward
+ * (common/decoder/qkn_decoder.c:633-705) or of qkn_decoder_prefill
+ * (:470-560) per call, the residual stream x staying in device memory:
+ *
+ *   q, k, v  = rmsnorm(x, input_norm) (Wq, Wk, Wv)^T
+ *   attn     = the attention block above (per-head norm, RoPE, cache, attention)
+ *   Qwen3   (pre_ffn_norm NULL): x += attn Wo^T; h = rmsnorm(x, post_attn_norm)
+ *   Gemma 3 (pre_ffn_norm set):  x += rmsnorm(attn Wo^T, post_attn_norm);
+ *                                h = rmsnorm(x, pre_ffn_norm)
+ *   g        = act(h Wgu^T)     rows of gate_up are (gate j, up j) pairs
+ *   x       += g Wd^T, or rmsnorm(g Wd^T, post_ffn_norm) when that is set
+ *
+ * For one token that is five launches (the norms, the activation and the
+ * residual adds are fused into the projections). All pointers are device
+ * pointers on the binding's device; the weights are the decoder's own
+ * tensors (bf16 [out][in] row-major, fp32 norm weights) copied to the device
+ * once by the caller. Calls are enqueued on the binding's stream
+ * (smol_qkn_attn_stream) and return without waiting, except the prefill,
+ * which waits for its attention block (SMOL_ATTN_ERR_RANGE check).
+ * smol_qkn_layer_synchronize waits for the stream. */
+typedef struct {
+    const float *input_norm;     /* [dim] */
+    const uint16_t *wq;          /* [n_heads * head_dim][dim] */
+    const uint16_t *wk, *wv;     /* [n_kv_heads * head_dim][dim] */
+    const uint16_t *wo;          /* [dim][n_heads * head_dim] */
+    const float *post_attn_norm; /* [dim] */
+    const float *pre_ffn_norm;   /* [dim] or NULL (Gemma 3 post-sublayer norms when set) */
+    const float *post_ffn_norm;  /* [dim] or NULL */
+    const uint16_t *gate_up;     /* [2 * intermediate][dim] */
+    const uint16_t *down;        /* [dim][intermediate] */
+} smol_qkn_layer_weights;
+
+/* act: SMOL_LINEAR_ACT_SWIGLU or SMOL_LINEAR_ACT_GEGLU (qkn_decoder.c:548-551).
+ * x [1][dim] at position pos (forward) or [seq_len][dim] from start_pos (prefill). */
+SMOL_ATTN_API int smol_qkn_layer_forward(const void *owner, int layer, int pos, float *x,
+                                         const smol_qkn_layer_weights *w, int dim, int intermediate, int act);
+SMOL_ATTN_API int smol_qkn_layer_prefill(const void *owner, int layer, int start_pos, int seq_len, float *x,
+                                         const smol_qkn_layer_weights *w, int dim, int intermediate, int act);
+SMOL_ATTN_API int smol_qkn_layer_synchronize(const void *owner);
+/* the binding's stream (a hipStream_t), for ordering the caller's own work */
+SMOL_ATTN_API void *smol_qkn_attn_stream(const void *owner);
+
 #ifdef __cplusplus
 }
 #endif

@@ -103,3 +103,44 @@ class Bf16Block(_Block):
         self.cv[layer, start:start + S] = np.asarray(v, np.uint16)
         return o.bf16_attention(qb, self.ck[layer, :start + S], self.cv[layer, :start + S], S, start + S, H, Hkv,
                                 hd, self.scale, start, window=window, cap=cap)
+
+
+class Fp32Layer:
+    """A whole fp32 decoder layer around Fp32Block: qkn_decoder.c:633-705 (one
+    token) / :470-560 (prefill), with the restated smol_rms_norm, the bf16
+    projections (orc_linear_bf16), SwiGLU / GeGLU and the residual adds:
+
+      xn = rms_norm(x, input_norm); q, k, v = xn Wq^T, xn Wk^T, xn Wv^T
+      a  = block(q, k, v); p = a Wo^T
+      Qwen3:   x = x + p;             h = rms_norm(x, post_attn_norm)
+      Gemma 3: x = x + rms_norm(p, post_attn_norm); h = rms_norm(x, pre_ffn_norm)
+      f = act(h Wgu^T) Wd^T; x = x + f (or x + rms_norm(f, post_ffn_norm))
+
+    `weights[layer]` holds numpy arrays under the smol_qkn_layer_weights
+    names (bf16 bits for the projections)."""
+
+    def __init__(self, orc, block, weights, act):
+        self.orc, self.block, self.w, self.act = orc, block, weights, act
+        self.gain = 1.0  # of the last step: max(1, 1 / rms of the rows post_attn_norm rescales)
+
+    def step(self, layer, start, x):
+        o, w, eps = self.orc, self.w[layer], self.block.eps
+        x = np.asarray(x, np.float32)
+        xn = o.rms_norm(x, w["input_norm"], eps)
+        q, k, v = o.linear_bf16(xn, w["wq"]), o.linear_bf16(xn, w["wk"]), o.linear_bf16(xn, w["wv"])
+        a = self.block.block(layer, start, q, k, v)
+        p = o.linear_bf16(a, w["wo"])
+        self.gain = 1.0
+        if w.get("pre_ffn_norm") is not None:
+            # the norm rescales the attention sublayer's output (and its error) by 1 / rms(p)
+            rms = np.sqrt((p.astype(np.float64) ** 2).mean(1) + eps)
+            self.gain = float(max(1.0, (1.0 / rms).max()))
+            x = x + o.rms_norm(p, w["post_attn_norm"], eps)
+            h = o.rms_norm(x, w["pre_ffn_norm"], eps)
+        else:
+            x = x + p
+            h = o.rms_norm(x, w["post_attn_norm"], eps)
+        f = o.linear_bf16(o.glu(o.linear_bf16(h, w["gate_up"]), self.act), w["down"])
+        if w.get("post_ffn_norm") is not None:
+            f = o.rms_norm(f, w["post_ffn_norm"], eps)
+        return (x + f).astype(np.float32)

@@ -297,15 +297,22 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
         }
     }
     if constexpr (FUSE) {
-        /* one segment: rows are segment 0's */
         const int r = lane % GEMV_R, s = lane / GEMV_R;
         const int o = row_base + r;
+        const bool live = lane < GEMV_R * SEQ && o < p.rows;
+        /* selects, not p.y[sg]: a lane-dependent index into the kernel
+         * arguments would be lowered through scratch memory */
+        const int sg = seg_of(p, o);
+        const int r0 = sg == 0 ? p.row0[0] : sg == 1 ? p.row0[1] : p.row0[2];
+        const int so = sg == 0 ? p.out[0] : sg == 1 ? p.out[1] : p.out[2];
+        const float *bias = sg == 0 ? p.bias[0] : sg == 1 ? p.bias[1] : p.bias[2];
+        float *y = static_cast<float *>(sg == 0 ? p.y[0] : sg == 1 ? p.y[1] : p.y[2]);
         float v = mine;
         if (norm) v *= 1.0f / sqrtf(myss / (float)in + p.eps);
-        if (lane < GEMV_R * SEQ && o < p.rows && p.bias[0]) v += p.bias[0][o];
-        const int out = p.out[0];
+        if (live && bias) v += bias[o - r0];
         if (p.act) {
-            /* lane i holds row r; the up row of gate row r (even) is in lane i + 1 */
+            /* one segment. Lane i holds row r; the up row of gate row r (even)
+             * is in lane i + 1 */
             const float up = __shfl_down(v, 1);
             float g = v;
             if (p.act == SMOL_LINEAR_ACT_SWIGLU) {
@@ -315,14 +322,15 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
                 const float inner = 0.7978845608028654f * (g + 0.044715f * x3);
                 g = 0.5f * g * (1.0f + tanhf(inner));
             }
-            if (lane < GEMV_R * SEQ && (r & 1) == 0 && o + 1 < p.rows) {
-                const long long j = (long long)s * (out >> 1) + (o >> 1);
+            if (live && (r & 1) == 0) {
+                const long long j = (long long)s * (so >> 1) + (o >> 1);
                 const float val = g * up;
-                static_cast<float *>(p.y[0])[j] = p.res ? p.res[j] + val : val;
+                y[j] = p.res ? p.res[j] + val : val;
             }
-        } else if (lane < GEMV_R * SEQ && o < p.rows) {
-            const long long j = (long long)s * out + o;
-            static_cast<float *>(p.y[0])[j] = p.res ? p.res[j] + v : v;
+        } else if (live) {
+            /* the residual belongs to segment 0 */
+            const long long j = (long long)s * so + (o - r0);
+            y[j] = (sg == 0 && p.res) ? p.res[j] + v : v;
         }
         return;
     }
@@ -394,8 +402,8 @@ __global__ __launch_bounds__(256) void k_bias_rows(float *y, const float *b, int
 /* out[s][i] = (x[s][i] * w[i]) * r_s, r_s = 1 / sqrtf(sum_i x[s][i]^2 / dim + eps)
  * (rmsnorm.c:17-75); one workgroup per row, the sum in a fixed order
  * (per-thread strided partials, then a tree in LDS) */
-__global__ __launch_bounds__(256) void k_rmsnorm_rows(float *out, const float *x, const float *w, int dim,
-                                                      float eps) {
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(float *out, const float *x, const float *w,
+                                                      const float *res, int dim, float eps) {
     __shared__ float part[256];
     const float *xr = x + (long long)blockIdx.x * dim;
     float *orow = out + (long long)blockIdx.x * dim;
@@ -408,7 +416,11 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(float *out, const float *x
         __syncthreads();
     }
     const float rinv = 1.0f / sqrtf(part[0] / (float)dim + eps);
-    for (int i = threadIdx.x; i < dim; i += 256) orow[i] = (xr[i] * w[i]) * rinv;
+    const float *rr = res ? res + (long long)blockIdx.x * dim : nullptr;
+    for (int i = threadIdx.x; i < dim; i += 256) {
+        const float v = (xr[i] * w[i]) * rinv;
+        orow[i] = rr ? rr[i] + v : v;
+    }
 }
 
 /* y[s][j] = act(t[s][2j]) * t[s][2j + 1] (+ res[s][j]); activation.c:55-88
@@ -606,9 +618,10 @@ int launch_bias(float *y, const float *b, int seq, int out, hipStream_t st, bool
     return 0;
 }
 
-int launch_rmsnorm(float *out, const float *x, const float *w, int seq, int dim, float eps, hipStream_t st) {
+int launch_rmsnorm(float *out, const float *x, const float *w, int seq, int dim, float eps, hipStream_t st,
+                   const float *res = nullptr) {
     if (seq <= 0 || dim <= 0) return 0;
-    hipLaunchKernelGGL(k_rmsnorm_rows, dim3((unsigned)seq), dim3(256), 0, st, out, x, w, dim, eps);
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3((unsigned)seq), dim3(256), 0, st, out, x, w, res, dim, eps);
     LHIP(hipGetLastError());
     return 0;
 }
@@ -890,8 +903,49 @@ extern "C" int smol_linear_ops_dev(smol_attn_ctx *ctx, float *y, const float *x,
     return run_gemm_ops(ctx, L, st, y, x, w, bias, seq, in_dim, out_dim, f);
 }
 
-extern "C" int smol_rms_norm_dev(smol_attn_ctx *ctx, float *out, const float *x, const float *weight, int seq,
-                                 int dim, float eps) {
+extern "C" int smol_linear_qkv_norm_dev(smol_attn_ctx *ctx, float *q, float *k, float *v, const float *x,
+                                        const uint16_t *wq, const uint16_t *wk, const uint16_t *wv, int seq,
+                                        int in_dim, int q_dim, int kv_dim, const float *norm_weight,
+                                        float norm_eps) {
+    if (!norm_weight)
+        return smol_linear_qkv_dev(ctx, q, k, v, SMOL_ATTN_F32, x, SMOL_ATTN_F32, wq, wk, wv, seq, in_dim, q_dim,
+                                   kv_dim);
+    if (!ctx) return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_qkv_norm_dev: null context");
+    if (seq < 0 || in_dim <= 0 || q_dim < 0 || kv_dim < 0)
+        return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_qkv_norm_dev: sizes");
+    if (seq == 0 || (q_dim == 0 && kv_dim == 0)) return SMOL_ATTN_OK;
+    if (!x || (q_dim && (!q || !wq)) || (kv_dim && (!k || !v || !wk || !wv)))
+        return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_qkv_norm_dev: null pointer");
+    if ((long long)seq * in_dim > INT_MAX / 4 || (long long)seq * (q_dim + 2LL * kv_dim) > INT_MAX / 4)
+        return lfail(SMOL_ATTN_ERR_UNSUPPORTED, "smol_linear_qkv_norm_dev: sizes beyond the supported range");
+    LHIP(hipSetDevice(smol_internal_ctx_device(ctx)));
+    hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
+    if (seq > SMOL_LINEAR_GEMV_MAX_SEQ) {
+        /* the GEMM path: normalise once, then the three products */
+        LinState *L = nullptr;
+        if (int rc = lin_state(ctx, &L)) return rc;
+        if (int rc = reserve(L->xn, (size_t)seq * in_dim * 4, st)) return rc;
+        float *xn = static_cast<float *>(L->xn.p);
+        if (int rc = launch_rmsnorm(xn, x, norm_weight, seq, in_dim, norm_eps, st)) return rc;
+        /* xn is the state's own buffer: the products below must not reuse it */
+        const float *w_in = xn;
+        if (int rc = run_gemm(ctx, L, st, q, false, w_in, false, wq, nullptr, seq, in_dim, q_dim)) return rc;
+        if (int rc = run_gemm(ctx, L, st, k, false, w_in, false, wk, nullptr, seq, in_dim, kv_dim)) return rc;
+        return run_gemm(ctx, L, st, v, false, w_in, false, wv, nullptr, seq, in_dim, kv_dim);
+    }
+    GemvSeg segs[GEMV_SEGS];
+    int n = 0;
+    if (q_dim) segs[n++] = GemvSeg{wq, nullptr, q, q_dim};
+    if (kv_dim) {
+        segs[n++] = GemvSeg{wk, nullptr, k, kv_dim};
+        segs[n++] = GemvSeg{wv, nullptr, v, kv_dim};
+    }
+    const GemvFuse f{norm_weight, norm_eps, SMOL_LINEAR_ACT_NONE, nullptr};
+    return run_gemv(ctx, st, x, false, false, seq, in_dim, n, segs, &f);
+}
+
+extern "C" int smol_rms_norm_dev(smol_attn_ctx *ctx, float *out, const float *x, const float *weight,
+                                 const float *residual, int seq, int dim, float eps) {
     if (!ctx) return lfail(SMOL_ATTN_ERR_ARG, "smol_rms_norm_dev: null context");
     if (seq < 0 || dim < 0) return lfail(SMOL_ATTN_ERR_ARG, "smol_rms_norm_dev: negative size");
     if (seq == 0 || dim == 0) return SMOL_ATTN_OK;
@@ -901,7 +955,7 @@ extern "C" int smol_rms_norm_dev(smol_attn_ctx *ctx, float *out, const float *x,
     hipEvent_t e0 = nullptr, e1 = nullptr;
     smol_internal_timing_events(ctx, LIN_TIMING_KIND, &e0, &e1);
     if (e0) LHIP(hipEventRecord(e0, st));
-    if (int rc = launch_rmsnorm(out, x, weight, seq, dim, eps, st)) return rc;
+    if (int rc = launch_rmsnorm(out, x, weight, seq, dim, eps, st, residual)) return rc;
     if (e1) LHIP(hipEventRecord(e1, st));
     return 0;
 }

@@ -22,6 +22,7 @@
 #include <math.h>
 #include <string.h>
 
+#include "smol_linear.h"
 #include "smol_qkn_attn.h"
 
 extern "C" int smol_internal_fail(int code, const char *msg);
@@ -51,6 +52,7 @@ struct Binding {
     std::vector<int> sliding;
     std::vector<float *> q_norm, k_norm; /* device [head_dim] or null */
     Buf q, k, v, out32, out16;           /* staging */
+    Buf lq, lk, lv, la, lp, lg;          /* a whole layer's activations (smol_qkn_layer_*) */
 };
 
 std::mutex g_mu;
@@ -87,7 +89,7 @@ void release(Binding *b) {
         if (p) hipFree(p);
     for (float *p : b->k_norm)
         if (p) hipFree(p);
-    for (Buf *x : {&b->q, &b->k, &b->v, &b->out32, &b->out16})
+    for (Buf *x : {&b->q, &b->k, &b->v, &b->out32, &b->out16, &b->lq, &b->lk, &b->lv, &b->la, &b->lp, &b->lg})
         if (x->p) hipFree(x->p);
     if (b->kv) smol_kv_cache_destroy(b->kv);
     if (b->rope_global) smol_rope_table_destroy(b->rope_global);
@@ -102,7 +104,7 @@ bool hd_ok(int hd) { return hd == 64 || hd == 72 || hd == 80 || hd == 96 || hd =
 /* The whole block for seq_len rows at start_pos (decode: one launch of the
  * direct decode kernel when seq_len == 1 and `decode` is set). */
 int run_block(Binding *b, int layer, int start_pos, int seq_len, const void *q, const void *k, const void *v,
-              void *attn_out, bool decode) {
+              void *attn_out, bool decode, bool sync = true) {
     const smol_qkn_attn_config &c = b->cfg;
     if (layer < 0 || layer >= c.n_layers) return qfail(SMOL_ATTN_ERR_ARG, "layer out of range");
     if (start_pos < 0 || seq_len <= 0) return qfail(SMOL_ATTN_ERR_ARG, "bad start_pos / seq_len");
@@ -183,10 +185,93 @@ int run_block(Binding *b, int layer, int start_pos, int seq_len, const void *q, 
         if (!c.on_device) QHIP(hipMemcpyAsync(attn_out, out, q_elems * 4, hipMemcpyDeviceToHost, b->stream));
     }
     /* waits; SMOL_ATTN_ERR_RANGE when the prefill's fp16 staging overflowed */
-    return smol_attn_ctx_synchronize(b->ctx);
+    return sync ? smol_attn_ctx_synchronize(b->ctx) : SMOL_ATTN_OK;
+}
+
+/* One decoder layer on the device (qkn_decoder.c:633-705 for one token,
+ * :470-560 for a prefill), x [n][dim] the residual stream, updated in place:
+ *   q, k, v = (rmsnorm(x, input_norm)) Wq/Wk/Wv^T          one launch (n <= 4)
+ *   attention block of the binding                           run_block
+ *   Qwen3:   x += attn Wo^T;  g = act(rmsnorm(x, post_attn_norm) Wgu^T)
+ *   Gemma 3: x += rmsnorm(attn Wo^T, post_attn_norm);
+ *            g = act(rmsnorm(x, pre_ffn_norm) Wgu^T)
+ *   x += g Wd^T, or x += rmsnorm(g Wd^T, post_ffn_norm) when that norm exists
+ * Nothing waits for the device except the prefill's attention block (its
+ * range check). */
+int run_layer(Binding *b, int layer, int pos, int n, float *x, const smol_qkn_layer_weights *w, int dim, int inter,
+              int act, bool decode) {
+    const smol_qkn_attn_config &c = b->cfg;
+    if (!c.on_device || c.bf16)
+        return qfail(SMOL_ATTN_ERR_ARG, "the device layer step needs a binding with on_device = 1 and bf16 = 0");
+    if (layer < 0 || layer >= c.n_layers) return qfail(SMOL_ATTN_ERR_ARG, "layer out of range");
+    if (!x || !w || dim <= 0 || inter <= 0 || n <= 0 || pos < 0) return qfail(SMOL_ATTN_ERR_ARG, "bad layer arguments");
+    if (act != SMOL_LINEAR_ACT_SWIGLU && act != SMOL_LINEAR_ACT_GEGLU)
+        return qfail(SMOL_ATTN_ERR_ARG, "act must be SMOL_LINEAR_ACT_SWIGLU or SMOL_LINEAR_ACT_GEGLU");
+    if (!w->input_norm || !w->wq || !w->wk || !w->wv || !w->wo || !w->post_attn_norm || !w->gate_up || !w->down)
+        return qfail(SMOL_ATTN_ERR_ARG, "a required layer weight is NULL");
+    QHIP(hipSetDevice(c.device));
+    const int q_dim = c.n_heads * c.head_dim, kv_dim = c.n_kv_heads * c.head_dim;
+    int rc;
+    if ((rc = reserve(b, b->lq, (size_t)n * q_dim * 4)) || (rc = reserve(b, b->lk, (size_t)n * kv_dim * 4)) ||
+        (rc = reserve(b, b->lv, (size_t)n * kv_dim * 4)) || (rc = reserve(b, b->la, (size_t)n * q_dim * 4)) ||
+        (rc = reserve(b, b->lp, (size_t)n * dim * 4)) || (rc = reserve(b, b->lg, (size_t)n * inter * 4)))
+        return rc;
+    float *q = (float *)b->lq.p, *k = (float *)b->lk.p, *v = (float *)b->lv.p;
+    float *attn = (float *)b->la.p, *p = (float *)b->lp.p, *g = (float *)b->lg.p;
+    smol_attn_ctx *ctx = b->ctx;
+    if ((rc = smol_linear_qkv_norm_dev(ctx, q, k, v, x, w->wq, w->wk, w->wv, n, dim, q_dim, kv_dim, w->input_norm,
+                                       c.eps)))
+        return rc;
+    if ((rc = run_block(b, layer, pos, n, q, k, v, attn, decode, !decode))) return rc;
+    smol_linear_ops ops{};
+    if (w->pre_ffn_norm) {
+        if ((rc = smol_linear_ops_dev(ctx, p, attn, w->wo, nullptr, n, q_dim, dim, nullptr))) return rc;
+        if ((rc = smol_rms_norm_dev(ctx, x, p, w->post_attn_norm, x, n, dim, c.eps))) return rc;
+        ops.norm_weight = w->pre_ffn_norm;
+    } else {
+        ops.residual = x;
+        if ((rc = smol_linear_ops_dev(ctx, x, attn, w->wo, nullptr, n, q_dim, dim, &ops))) return rc;
+        ops.residual = nullptr;
+        ops.norm_weight = w->post_attn_norm;
+    }
+    ops.norm_eps = c.eps;
+    ops.act = act;
+    if ((rc = smol_linear_ops_dev(ctx, g, x, w->gate_up, nullptr, n, dim, 2 * inter, &ops))) return rc;
+    if (w->post_ffn_norm) {
+        if ((rc = smol_linear_ops_dev(ctx, p, g, w->down, nullptr, n, inter, dim, nullptr))) return rc;
+        return smol_rms_norm_dev(ctx, x, p, w->post_ffn_norm, x, n, dim, c.eps);
+    }
+    smol_linear_ops res{};
+    res.residual = x;
+    return smol_linear_ops_dev(ctx, x, g, w->down, nullptr, n, inter, dim, &res);
 }
 
 }  // namespace
+
+extern "C" int smol_qkn_layer_forward(const void *owner, int layer, int pos, float *x,
+                                      const smol_qkn_layer_weights *w, int dim, int intermediate, int act) {
+    Binding *b = find(owner);
+    if (!b) return qfail(SMOL_ATTN_ERR_ARG, "owner is not bound");
+    return run_layer(b, layer, pos, 1, x, w, dim, intermediate, act, true);
+}
+
+extern "C" int smol_qkn_layer_prefill(const void *owner, int layer, int start_pos, int seq_len, float *x,
+                                      const smol_qkn_layer_weights *w, int dim, int intermediate, int act) {
+    Binding *b = find(owner);
+    if (!b) return qfail(SMOL_ATTN_ERR_ARG, "owner is not bound");
+    return run_layer(b, layer, start_pos, seq_len, x, w, dim, intermediate, act, false);
+}
+
+extern "C" int smol_qkn_layer_synchronize(const void *owner) {
+    Binding *b = find(owner);
+    if (!b) return qfail(SMOL_ATTN_ERR_ARG, "owner is not bound");
+    return smol_attn_ctx_synchronize(b->ctx);
+}
+
+extern "C" void *smol_qkn_attn_stream(const void *owner) {
+    Binding *b = find(owner);
+    return b ? (void *)b->stream : nullptr;
+}
 
 extern "C" int smol_qkn_attn_bind(const void *owner, const smol_qkn_attn_config *cfg) {
     if (!owner || !cfg) return qfail(SMOL_ATTN_ERR_ARG, "NULL owner / config");

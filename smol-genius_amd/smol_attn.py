@@ -81,12 +81,18 @@ SIGNATURES = [
     ("smol_qkn_attn_forward", [_vp, _c_int, _c_int, _vp, _vp, _vp, _vp], _c_int),
     ("smol_qkn_attn_read_cache", [_vp, _c_int, _c_int, _c_int, _U16P, _U16P], _c_int),
     ("smol_qkn_attn_unbind", [_vp], _c_int),
+    ("smol_qkn_layer_forward", [_vp, _c_int, _c_int, _vp, _vp, _c_int, _c_int, _c_int], _c_int),
+    ("smol_qkn_layer_prefill", [_vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _c_int, _c_int], _c_int),
+    ("smol_qkn_layer_synchronize", [_vp], _c_int),
+    ("smol_qkn_attn_stream", [_vp], _vp),
     # bf16-weight projections on device pointers (include/smol_linear.h)
     ("smol_linear_dev", [_vp, _vp, _c_int, _vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int], _c_int),
     ("smol_linear_qkv_dev", [_vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _vp, _vp, _vp, _c_int, _c_int, _c_int,
                              _c_int], _c_int),
     ("smol_linear_ops_dev", [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp], _c_int),
-    ("smol_rms_norm_dev", [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_float], _c_int),
+    ("smol_rms_norm_dev", [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_float], _c_int),
+    ("smol_linear_qkv_norm_dev", [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp,
+                                  _c_float], _c_int),
     # reference-signature drop-ins (host fp32 arrays)
     ("smol_linear_bf16", [_FP, _FP, _U16P, _FP, _c_int, _c_int, _c_int], None),
     ("smol_linear_nobias_bf16", [_FP, _FP, _U16P, _c_int, _c_int, _c_int], None),
@@ -438,6 +444,21 @@ class QknConfig(ctypes.Structure):
                 ("bf16", _c_int), ("on_device", _c_int), ("device", _c_int), ("max_seq", _c_int)]
 
 
+class _LayerWeights(ctypes.Structure):
+    _fields_ = [(n, _vp) for n in ("input_norm", "wq", "wk", "wv", "wo", "post_attn_norm", "pre_ffn_norm",
+                                   "post_ffn_norm", "gate_up", "down")]
+
+
+class QknLayerWeights:
+    """smol_qkn_layer_weights from device tensors (fp32 norms, bf16 / int16-bit weights);
+    the tensors are kept alive with the struct."""
+
+    def __init__(self, **t):
+        self.t = t
+        self.s = _LayerWeights(**{k: (ctypes.c_void_p(v.data_ptr()) if v is not None else None)
+                                  for k, v in t.items()})
+
+
 class QknAttn:
     """The decoder attention block bound to a decoder context (`owner`, any
     object whose address keys the registry; a ctypes buffer stands for the
@@ -486,6 +507,21 @@ class QknAttn:
         ptrs, out = self._io(q, k, v, 1)
         _check(load().smol_qkn_attn_forward(self.addr, layer, pos, *ptrs), "smol_qkn_attn_forward")
         return out
+
+    def layer_forward(self, layer, pos, x, weights, dim, inter, act=1):
+        """smol_qkn_layer_forward: x [1, dim] device fp32, updated in place;
+        weights a QknLayerWeights of device tensors"""
+        _check(load().smol_qkn_layer_forward(self.addr, layer, pos, _dev(x, "x"), ctypes.byref(weights.s), dim,
+                                             inter, act), "smol_qkn_layer_forward")
+        return x
+
+    def layer_prefill(self, layer, start_pos, x, weights, dim, inter, act=1):
+        _check(load().smol_qkn_layer_prefill(self.addr, layer, start_pos, x.shape[0], _dev(x, "x"),
+                                             ctypes.byref(weights.s), dim, inter, act), "smol_qkn_layer_prefill")
+        return x
+
+    def synchronize(self):
+        _check(load().smol_qkn_layer_synchronize(self.addr), "smol_qkn_layer_synchronize")
 
     def read_cache(self, layer, pos0, n):
         kvd = self.cfg.n_kv_heads * self.cfg.head_dim
@@ -651,15 +687,32 @@ def linear_ops(ctx, x, w, bias=None, norm_weight=None, eps=1e-6, act=ACT_NONE, r
     return out
 
 
-def rms_norm(ctx, x, weight, eps, out=None):
-    """smol_rms_norm_dev: fp32 rows [seq, dim]"""
+def rms_norm(ctx, x, weight, eps, out=None, residual=None):
+    """smol_rms_norm_dev: fp32 rows [seq, dim] (+ residual)"""
     import torch
     seq, dim = x.shape
     if out is None:
         out = torch.empty_like(x)
-    _check(load().smol_rms_norm_dev(ctx.h, _dev(out, "out"), _dev(x, "x"), _dev(weight, "weight"), seq, dim,
+    _check(load().smol_rms_norm_dev(ctx.h, _dev(out, "out"), _dev(x, "x"), _dev(weight, "weight"),
+                                    _dev(residual, "residual") if residual is not None else None, seq, dim,
                                     ctypes.c_float(eps)), "smol_rms_norm_dev")
     return out
+
+
+def linear_qkv_norm(ctx, x, wq, wk, wv, norm_weight, eps):
+    """smol_linear_qkv_norm_dev: q, k, v of rmsnorm(x) (fp32)"""
+    import torch
+    seq, in_dim = x.shape
+    q_dim, kv_dim = wq.shape[0], wk.shape[0]
+    q = torch.empty((seq, q_dim), dtype=torch.float32, device=x.device)
+    k = torch.empty((seq, kv_dim), dtype=torch.float32, device=x.device)
+    v = torch.empty((seq, kv_dim), dtype=torch.float32, device=x.device)
+    _check(load().smol_linear_qkv_norm_dev(ctx.h, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), _dev(x, "x"),
+                                           _wbits(wq, "wq"), _wbits(wk, "wk"), _wbits(wv, "wv"), seq, in_dim,
+                                           q_dim, kv_dim,
+                                           _dev(norm_weight, "norm") if norm_weight is not None else None,
+                                           ctypes.c_float(eps)), "smol_linear_qkv_norm_dev")
+    return q, k, v
 
 
 def _u16(a):

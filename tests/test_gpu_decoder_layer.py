@@ -1,0 +1,116 @@
+"""Whole decoder layers on the GPU (smol_qkn_layer_prefill / _forward), the
+residual stream in device memory, against the CPU oracle's layer model
+(oracle/decoder_oracle.py Fp32Layer: restated RMSNorm, bf16 projections,
+attention block, SwiGLU / GeGLU, residual adds).
+
+Each case runs every layer over a prefill at position 0, then decode steps,
+then a rewind and a chunk, comparing the residual stream after every layer
+call with the path's bar |gpu - cpu| <= 2e-3 G + 1e-2 |cpu|. G is 1 for
+Qwen3-style layers. A Gemma 3 layer RMS-normalises the attention sublayer's
+output p before adding it, which multiplies the attention kernels' error
+(within their own bar, on fp16 operands) by 1 / rms(p); there G is the sum,
+over the layers run so far in the call, of max(1, 1 / rms(p)) as the oracle
+measures it.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import synth  # noqa: F401
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def sa():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from smol_genius_amd import smol_attn
+    smol_attn.load()
+    return smol_attn
+
+
+@pytest.fixture(scope="module")
+def dorc():
+    import decoder_oracle
+    return decoder_oracle
+
+
+def _norm_w(seed, n):
+    return (1.0 + 0.1 * synth.normal(seed, (n,))).astype(np.float32)
+
+
+def _proj(seed, n_out, n_in):
+    return synth.f32_to_bf16_bits(synth.normal(seed, (n_out, n_in), 1.0 / np.sqrt(n_in)))
+
+
+# (name, attention config, dim, intermediate, act, gemma3 norms, sliding layers)
+CONFIGS = [
+    ("qwen3_small", dict(n_layers=2, n_heads=8, n_kv_heads=4, head_dim=64, eps=1e-6, rope_theta=1e6,
+                         rope_local_theta=0.0, rope_type=0, sliding_window=0, attn_logit_softcap=0.0),
+     256, 384, 1, False, [0, 0]),
+    ("gemma3_small", dict(n_layers=2, n_heads=4, n_kv_heads=2, head_dim=128, eps=1e-6, rope_theta=1e6,
+                          rope_local_theta=1e4, rope_type=1, sliding_window=16, attn_logit_softcap=0.0),
+     320, 640, 2, True, [1, 0]),
+    ("qwen3_0.6b_layer", dict(n_layers=1, n_heads=16, n_kv_heads=8, head_dim=128, eps=1e-6, rope_theta=1e6,
+                              rope_local_theta=0.0, rope_type=0, sliding_window=0, attn_logit_softcap=0.0),
+     1024, 3072, 1, False, [0]),
+]
+
+# (kind, start, rows): prefill 40 at 0; 3 decode steps; rewind to 30 and a 12-row chunk; 2 decode steps
+SEQUENCE = [("prefill", 0, 40), ("forward", 40, 1), ("forward", 41, 1), ("forward", 42, 1),
+            ("prefill", 30, 12), ("forward", 42, 1), ("forward", 43, 1)]
+
+
+@pytest.mark.parametrize("name,cfg,dim,inter,act,gemma,sliding", CONFIGS, ids=[c[0] for c in CONFIGS])
+def test_layer_sequence(sa, oracle, dorc, name, cfg, dim, inter, act, gemma, sliding):
+    H, Hkv, hd, L = cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["n_layers"]
+    owner = ctypes.create_string_buffer(256)
+    blk = sa.QknAttn(owner, **cfg, bf16=0, on_device=1, device=0, max_seq=64)
+    model_blk = dorc.Fp32Block(oracle, **cfg)
+    weights, dweights = [], []
+    for li in range(L):
+        s = 100 * (li + 1)
+        w = dict(input_norm=_norm_w(s, dim), wq=_proj(s + 1, H * hd, dim), wk=_proj(s + 2, Hkv * hd, dim),
+                 wv=_proj(s + 3, Hkv * hd, dim), wo=_proj(s + 4, dim, H * hd), post_attn_norm=_norm_w(s + 5, dim),
+                 pre_ffn_norm=_norm_w(s + 6, dim) if gemma else None,
+                 post_ffn_norm=_norm_w(s + 7, dim) if gemma else None,
+                 gate_up=_proj(s + 8, 2 * inter, dim), down=_proj(s + 9, dim, inter))
+        qn, kn = _norm_w(s + 10, hd), _norm_w(s + 11, hd)
+        blk.set_layer(li, sliding[li], qn, kn)
+        model_blk.set_layer(li, sliding[li], qn, kn)
+        weights.append(w)
+
+        def d(a):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a)
+            return torch.from_numpy(a.view(np.int16) if a.dtype == np.uint16 else a).cuda()
+        dweights.append(sa.QknLayerWeights(**{k: d(v) for k, v in w.items()}))
+    model = dorc.Fp32Layer(oracle, model_blk, weights, act)
+    try:
+        for step, (kind, start, rows) in enumerate(SEQUENCE):
+            x = synth.normal(7000 + step, (rows, dim))
+            xd = torch.from_numpy(x).cuda()
+            xm = x
+            G = 0.0
+            for li in range(L):
+                print("layer %s %s start %d rows %d layer %d" % (name, kind, start, rows, li), flush=True)
+                if kind == "prefill":
+                    blk.layer_prefill(li, start, xd, dweights[li], dim, inter, act)
+                else:
+                    blk.layer_forward(li, start, xd, dweights[li], dim, inter, act)
+                blk.synchronize()
+                xm = model.step(li, start, xm)
+                G += model.gain
+                got = xd.cpu().numpy()
+                d = np.abs(got.astype(np.float64) - xm)
+                ratio = float((d / (2e-3 * G + 1e-2 * np.abs(xm))).max())
+                print("parity layer %s %s@%d L%d max_abs %.3e G %.2f ratio %.3f" % (
+                    name, kind, start, li, d.max(), G, ratio), flush=True)
+                assert np.isfinite(got).all() and ratio <= 1.0
+    finally:
+        blk.close()
