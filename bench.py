@@ -33,6 +33,8 @@ import os
 import sys
 import time
 
+import numpy as np
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
@@ -44,7 +46,8 @@ MALL_BYTES = 256 << 20
 # the kernel each workload's roofline is quoted for (its profiles/<kernel>_<workload>.md summary)
 DOMINANT = {"qwen06b_prefill": "k_attn_fb", "qwen06b_prefill_qknorm": "k_attn_fb", "siglip_bidir": "k_attn_fb",
             "asr_encoder_bidir": "k_attn_win", "qwen06b_decode": "k_dec", "qwen06b_decode_qknorm": "k_dec",
-            "gemma_mqa_decode": "k_dec", "qwen06b_decode_x28": "k_dec", "qwen17b_stream": "k_dec"}
+            "gemma_mqa_decode": "k_dec", "qwen06b_decode_x28": "k_dec", "qwen17b_stream": "k_dec",
+            "qwen06b_proj_decode": "k_gemv", "qwen06b_proj_prefill": "Cijk_"}
 
 
 def profiled(workload):
@@ -198,6 +201,99 @@ def measure_projections(ctx, sa, wl, steps, warmup):
     return d
 
 
+def measure_decoder(ctx, sa, steps, warmup, prefix=1024, n_layers=28, dim=1024, inter=3072):
+    """Whole Qwen3-ASR-0.6B decoder layers on the device (smol_qkn_layer_*): the
+    28 layers' caches filled by a `prefix`-token prefill, then single-token
+    steps through all 28 layers (5 launches per layer). Random bf16 weights
+    generated on the device (values do not change the work). Returns per-token
+    and per-prefill-token figures."""
+    import ctypes
+    import gc
+    import torch
+    gc.collect()
+    torch.cuda.synchronize()
+    H, Hkv, hd = 16, 8, 128
+    owner = ctypes.create_string_buffer(256)
+    blk = sa.QknAttn(owner, n_layers=n_layers, n_heads=H, n_kv_heads=Hkv, head_dim=hd, eps=1e-6, rope_theta=1e6,
+                     rope_local_theta=0.0, rope_type=0, sliding_window=0, attn_logit_softcap=0.0, bf16=0,
+                     on_device=1, device=0, max_seq=prefix + steps + warmup + 8)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+
+    def proj(o, i):
+        return (torch.randn((o, i), generator=g, device="cuda") * i ** -0.5).to(torch.bfloat16)
+
+    def nw(n):
+        return 1.0 + 0.1 * torch.randn((n,), generator=g, device="cuda")
+
+    W = []
+    for li in range(n_layers):
+        blk.set_layer(li, 0, (1.0 + 0.1 * np.random.default_rng(li).standard_normal(hd)).astype(np.float32),
+                      (1.0 + 0.1 * np.random.default_rng(100 + li).standard_normal(hd)).astype(np.float32))
+        W.append(sa.QknLayerWeights(input_norm=nw(dim), wq=proj(H * hd, dim), wk=proj(Hkv * hd, dim),
+                                    wv=proj(Hkv * hd, dim), wo=proj(dim, H * hd), post_attn_norm=nw(dim),
+                                    pre_ffn_norm=None, post_ffn_norm=None, gate_up=proj(2 * inter, dim),
+                                    down=proj(dim, inter)))
+    lib = sa.load()
+    addr = blk.addr
+    x = torch.randn((prefix, dim), generator=g, device="cuda")
+    x0 = x.clone()
+    prefill_s = []
+    for rep in range(3):  # the first pass pays one-time set-up (GEMM heuristics, buffers); a rewind to 0 repeats it
+        x.copy_(x0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for li in range(n_layers):
+            if lib.smol_qkn_layer_prefill(addr, li, 0, prefix, ctypes.c_void_p(x.data_ptr()),
+                                          ctypes.byref(W[li].s), dim, inter, 1):
+                raise RuntimeError(lib.smol_attn_last_error().decode())
+        blk.synchronize()
+        prefill_s.append(time.perf_counter() - t0)
+    prefill_cold = prefill_s[0]
+    prefill_s = min(prefill_s[1:])
+    xt = torch.randn((1, dim), generator=g, device="cuda")
+    xp = ctypes.c_void_p(xt.data_ptr())
+
+    def token(pos):
+        for li in range(n_layers):
+            if lib.smol_qkn_layer_forward(addr, li, pos, xp, ctypes.byref(W[li].s), dim, inter, 1):
+                raise RuntimeError(lib.smol_attn_last_error().decode())
+
+    pos = prefix
+    gc.disable()
+    try:
+        for _ in range(warmup):
+            token(pos)
+            pos += 1
+        blk.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            token(pos)
+            pos += 1
+        blk.synchronize()
+        wall = time.perf_counter() - t0
+    finally:
+        gc.enable()
+    wbytes = n_layers * 2 * dim * (H * hd + 2 * Hkv * hd + H * hd + 3 * inter)
+    kv_bytes = n_layers * 2 * Hkv * hd * 2 * (prefix + warmup + steps / 2)
+    ms_tok = wall / steps * 1e3
+    d = {"config": {"workload": "qwen06b_decoder_step", "layers": n_layers, "hidden": dim, "heads": [H, Hkv, hd],
+                    "intermediate": inter, "cached_tokens": prefix, "weights": "random bf16 on the device"},
+         "ms_per_token": round(ms_tok, 4), "tokens_per_s": round(1e3 / ms_tok, 1),
+         "launches_per_token": 5 * n_layers,
+         "hbm_GBps_per_token": round((wbytes + kv_bytes) / (wall / steps) / 1e9, 1),
+         "bytes_per_token": int(wbytes + kv_bytes),
+         "prefill_tokens_per_s": round(prefix / prefill_s, 1),
+         "prefill_ms_%d_tokens" % prefix: round(prefill_s * 1e3, 3),
+         "prefill_ms_first_call": round(prefill_cold * 1e3, 3),
+         "note": "decode: 28 layers per token, norms/activation/residuals fused into the projections, "
+                 "one host wait per timed run; prefill: 28 smol_qkn_layer_prefill calls, each waiting for its "
+                 "attention block"}
+    blk.close()
+    del W, x, xt
+    return d
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -344,6 +440,13 @@ def main():
         if cpu_mod:
             d["cpu_baseline"] = cpu_mod.projections_sample(wl, wl.inputs())
         detail[name] = d
+
+    # ---------------- whole decoder layers on the device (28-layer token step)
+    if args.only in (None, "qwen06b_decoder_step"):
+        d = measure_decoder(ctx, sa, max(10, steps // 5), max(2, warmup // 2))
+        if cpu_mod:
+            d["cpu_baseline"] = cpu_mod.decoder_step_sample()
+        detail["qwen06b_decoder_step"] = d
 
     # ---------------- CPU baseline of the headline (reference CPU attention on this host)
     if cpu_mod and head is not None:

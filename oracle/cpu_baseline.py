@@ -187,3 +187,63 @@ def projections_sample(wl, x, min_seconds=3.0, max_reps=100, max_rows=64):
             **host_facts(),
             "sample": "%d repetitions of one layer's projections on %d of %d rows%s" % (
                 reps, rows, wl.seq, "" if rows == wl.seq else ", scaled to all rows")}
+
+
+def decoder_step_sample(n_layers=28, dim=1024, inter=3072, H=16, Hkv=8, hd=128, prefix=1024, sample_layers=2,
+                        min_seconds=3.0, max_reps=50):
+    """One token through Qwen3-0.6B decoder layers as qkn_decoder_forward runs them
+    (qkn_decoder.c:633-705): smol_rms_norm, smol_linear_nobias_bf16_qkv, per-head
+    RMSNorm, NeoX RoPE, smol_causal_attention over a `prefix`-row cache,
+    smol_linear_nobias_bf16 (o_proj), the residual add, smol_rms_norm,
+    smol_linear_nobias_bf16 (gate_up), smol_swiglu_multiply,
+    smol_linear_nobias_bf16 (down), the residual add. Timed on `sample_layers`
+    layers and scaled to n_layers (every layer does the same work)."""
+    lib, kind, cores = _lib()
+    orc = Oracle()
+    rng = np.random.default_rng(5)
+
+    def bits(o, i):
+        w = (rng.standard_normal((o, i)) / np.sqrt(i)).astype(np.float32)
+        return (w.view(np.uint32) >> 16).astype(np.uint16)
+
+    layers = []
+    for _ in range(sample_layers):
+        layers.append(dict(
+            inorm=(1 + 0.1 * rng.standard_normal(dim)).astype(np.float32),
+            pnorm=(1 + 0.1 * rng.standard_normal(dim)).astype(np.float32),
+            qn=(1 + 0.1 * rng.standard_normal(hd)).astype(np.float32),
+            kn=(1 + 0.1 * rng.standard_normal(hd)).astype(np.float32),
+            wq=bits(H * hd, dim), wk=bits(Hkv * hd, dim), wv=bits(Hkv * hd, dim), wo=bits(dim, H * hd),
+            gu=bits(2 * inter, dim), down=bits(dim, inter),
+            K=rng.standard_normal((prefix + 1, Hkv * hd)).astype(np.float32),
+            V=rng.standard_normal((prefix + 1, Hkv * hd)).astype(np.float32)))
+    c, s = orc.fill_rope_table(0, prefix + 1, hd, 1e6, False)
+    c, s = c[prefix:prefix + 1], s[prefix:prefix + 1]
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    x0 = rng.standard_normal((1, dim)).astype(np.float32)
+    reps, t = 0, 0.0
+    while reps < 2 or (t < min_seconds and reps < max_reps):
+        x = x0.copy()
+        t0 = time.perf_counter()
+        for L in layers:
+            xn = lib.rms_norm(x, L["inorm"], 1e-6)
+            if hasattr(lib, "linear_qkv"):
+                q, k, v = lib.linear_qkv(xn, L["wq"], L["wk"], L["wv"])
+            else:
+                q, k, v = (lib.linear_bf16(xn, L[n])[0] for n in ("wq", "wk", "wv"))
+            q = lib.rms_norm_per_head(q[None], L["qn"], 1, H, hd, 1e-6)
+            k = lib.rms_norm_per_head(k[None], L["kn"], 1, Hkv, hd, 1e-6)
+            q = lib.apply_rope(q, c, s, 1, H, hd, False)
+            L["K"][prefix] = lib.apply_rope(k, c, s, 1, Hkv, hd, False)[0]
+            L["V"][prefix] = v
+            a = lib.causal_attention(q, L["K"], L["V"], 1, prefix + 1, H, Hkv, hd, scale, prefix)
+            x = x + lib.linear_bf16(a, L["wo"])
+            h = lib.rms_norm(x, L["pnorm"], 1e-6)
+            x = x + lib.linear_bf16(lib.glu(lib.linear_bf16(h, L["gu"]), 1), L["down"])
+        t += time.perf_counter() - t0
+        reps += 1
+    sec = t / reps * n_layers / sample_layers
+    return {"value": round(1.0 / sec, 2), "unit": "tokens/s", "cores": cores, "kind": kind,
+            "ms_per_token": round(sec * 1e3, 3), **host_facts(),
+            "sample": "%d repetitions of one token through %d layers (%d cached tokens), scaled to %d layers" % (
+                reps, sample_layers, prefix, n_layers)}
