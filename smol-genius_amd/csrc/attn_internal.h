@@ -159,7 +159,9 @@ typedef struct {
  * One workgroup per 128-row tile of a (window, head); the window's K and V
  * are read from the inputs (fp32 or bf16), converted to fp16 and written
  * to LDS once; no pre-pass. */
+#ifndef WIN_ARG_WINDOWS
 #define WIN_ARG_WINDOWS 255   /* windows passed in the kernel arguments */
+#endif
 #define WIN_TPB 512           /* threads of a k_attn_win workgroup: 8 waves, two per SIMD */
 #define WIN_ROWS 128          /* rows of its tile: 16 per wave */
 typedef struct {

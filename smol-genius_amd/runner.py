@@ -2,6 +2,9 @@
 
 ``prepare(ctx, wl, inputs, layers=1)`` uploads the inputs, fills the device KV
 cache(s) and returns a ``Run`` whose ``step()`` enqueues one pass of the path
+(calls whose arguments were converted once, so the host issues a step in a few
+microseconds and short kernels run back to back instead of each waking an idle
+GPU)
 (on the context's stream) and whose ``outputs()`` returns the fp32 results
 as numpy. ``layers > 1`` gives every layer its own cache region and inputs,
 so repeated steps stream distinct HBM buffers instead of re-reading data
@@ -81,10 +84,9 @@ def _prep_decode(ctx, wl, x, layers, device):
     pos = wl.positions
     qn, kn = _norm_tensors(wl, device)
 
-    def _step(l):
-        return sa.decode(ctx, r.kv, l, r.rope, slots, pos, r.q[l], r.k[l], r.v[l], wl.Hq, wl.scale, out=r.outs[l],
-                         q_norm=qn, k_norm=kn, eps=wl.norm_eps)
-    r._step = _step
+    calls = [sa.decode_call(ctx, r.kv, l, r.rope, slots, pos, r.q[l], r.k[l], r.v[l], wl.Hq, wl.scale,
+                            out=r.outs[l], q_norm=qn, k_norm=kn, eps=wl.norm_eps) for l in range(layers)]
+    r._step = lambda l: calls[l]()
     return r
 
 
@@ -104,10 +106,9 @@ def _prep_prefill(ctx, wl, x, layers, device):
     r.outs = [torch.empty((wl.seq_q, wl.Hq * wl.hd), dtype=torch.float32, device=device) for _ in range(layers)]
     qn, kn = _norm_tensors(wl, device)
 
-    def _step(l):
-        return sa.prefill(ctx, r.kv, l, 0, r.rope, wl.pos0, r.q[l], r.k[l], r.v[l], wl.Hq, wl.scale,
-                          out=r.outs[l], q_norm=qn, k_norm=kn, eps=wl.norm_eps)
-    r._step = _step
+    calls = [sa.prefill_call(ctx, r.kv, l, 0, r.rope, wl.pos0, r.q[l], r.k[l], r.v[l], wl.Hq, wl.scale,
+                             out=r.outs[l], q_norm=qn, k_norm=kn, eps=wl.norm_eps) for l in range(layers)]
+    r._step = lambda l: calls[l]()
     return r
 
 
@@ -120,10 +121,9 @@ def _prep_bidir(ctx, wl, x, layers, device):
     r.v = [_t(x["v"], device, wl.in_bf16) for _ in range(layers)]
     r.outs = [torch.empty((wl.seq, wl.H * wl.hd), dtype=torch.float32, device=device) for _ in range(layers)]
 
-    def _step(l):
-        return sa.bidirectional(ctx, r.q[l], r.k[l], r.v[l], wl.seq, wl.H, wl.hd, wl.scale, wl.window_starts,
-                                out=r.outs[l])
-    r._step = _step
+    calls = [sa.bidirectional_call(ctx, r.q[l], r.k[l], r.v[l], wl.seq, wl.H, wl.hd, wl.scale, wl.window_starts,
+                                   out=r.outs[l]) for l in range(layers)]
+    r._step = lambda l: calls[l]()
     return r
 
 
@@ -146,14 +146,19 @@ def _prep_stream(ctx, wl, x, layers, device):
     r.outs = [[torch.empty((wl.chunk, wl.Hq * wl.hd), dtype=torch.float32, device=device),
                torch.empty((wl.steps, wl.Hq * wl.hd), dtype=torch.float32, device=device)] for _ in range(layers)]
     slot0 = np.zeros(1, np.int32)
-
-    def _step(l):
+    calls = []
+    for l in range(layers):
         oc, od = r.outs[l]
-        sa.prefill(ctx, r.kv, l, 0, r.rope, wl.prefix, r.q[l], r.k[l], r.v[l], wl.Hq, wl.scale, out=oc)
+        cl = [sa.prefill_call(ctx, r.kv, l, 0, r.rope, wl.prefix, r.q[l], r.k[l], r.v[l], wl.Hq, wl.scale, out=oc)]
         for s in range(wl.steps):
             p = np.array([wl.prefix + wl.chunk + s], np.int32)
-            sa.decode(ctx, r.kv, l, r.rope, slot0, p, r.dq[l][s:s + 1], r.dk[l][s:s + 1], r.dv[l][s:s + 1],
-                      wl.Hq, wl.scale, out=od[s:s + 1])
+            cl.append(sa.decode_call(ctx, r.kv, l, r.rope, slot0, p, r.dq[l][s:s + 1], r.dk[l][s:s + 1],
+                                     r.dv[l][s:s + 1], wl.Hq, wl.scale, out=od[s:s + 1]))
+        calls.append(cl)
+
+    def _step(l):
+        for c in calls[l]:
+            c()
         return r.outs[l]
     r._step = _step
     return r

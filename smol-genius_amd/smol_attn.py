@@ -337,26 +337,46 @@ def _norm_w(w, what):
     return _dev(w, what)
 
 
-def prefill(ctx, kv, layer, slot, rope, pos0, q, k_new, v_new, n_heads, scale, window=0, cap=0.0, out=None,
-            q_norm=None, k_norm=None, eps=1e-6):
-    """Chunked prefill of one sequence; see smol_attn_prefill. q_norm / k_norm
-    (device float32 [head_dim]) select smol_attn_prefill_qknorm."""
+class Prepared:
+    """One C call with its arguments converted once, for loops that repeat it
+    (the bench): calling it runs the call and raises on a failure status.
+    `out` is the output tensor the call writes."""
+
+    def __init__(self, fn, args, name, out, keep=()):
+        self.fn, self.args, self.name, self.out, self.keep = fn, args, name, out, keep
+
+    def __call__(self):
+        rc = self.fn(*self.args)
+        if rc:
+            _check(rc, self.name)
+        return self.out
+
+
+def prefill_call(ctx, kv, layer, slot, rope, pos0, q, k_new, v_new, n_heads, scale, window=0, cap=0.0, out=None,
+                 q_norm=None, k_norm=None, eps=1e-6):
+    """smol_attn_prefill(_qknorm) as a Prepared call"""
     seq_q = q.shape[0]
     out = _out_like(seq_q, n_heads, kv.head_dim, q.device, out)
     args = (ctx.h, kv.h, layer, slot, rope.h if rope else None, pos0, seq_q, _dev(q, "q"), _dev(k_new, "k"),
             _dev(v_new, "v"), _dtype_code(q), n_heads, ctypes.c_float(scale), window, ctypes.c_float(cap))
     if q_norm is None and k_norm is None:
-        _check(load().smol_attn_prefill(*args, _dev(out, "out")), "smol_attn_prefill")
-    else:
-        _check(load().smol_attn_prefill_qknorm(*args, _norm_w(q_norm, "q_norm"), _norm_w(k_norm, "k_norm"),
-                                               ctypes.c_float(eps), _dev(out, "out")), "smol_attn_prefill_qknorm")
-    return out
+        return Prepared(load().smol_attn_prefill, args + (_dev(out, "out"),), "smol_attn_prefill", out)
+    return Prepared(load().smol_attn_prefill_qknorm,
+                    args + (_norm_w(q_norm, "q_norm"), _norm_w(k_norm, "k_norm"), ctypes.c_float(eps),
+                            _dev(out, "out")), "smol_attn_prefill_qknorm", out)
 
 
-def decode(ctx, kv, layer, rope, slots, pos, q, k_new, v_new, n_heads, scale, window=0, cap=0.0, out=None,
-           q_norm=None, k_norm=None, eps=1e-6):
-    """Batched single-token decode; see smol_attn_decode. q_norm / k_norm
-    (device float32 [head_dim]) select smol_attn_decode_qknorm."""
+def prefill(ctx, kv, layer, slot, rope, pos0, q, k_new, v_new, n_heads, scale, window=0, cap=0.0, out=None,
+            q_norm=None, k_norm=None, eps=1e-6):
+    """Chunked prefill of one sequence; see smol_attn_prefill. q_norm / k_norm
+    (device float32 [head_dim]) select smol_attn_prefill_qknorm."""
+    return prefill_call(ctx, kv, layer, slot, rope, pos0, q, k_new, v_new, n_heads, scale, window, cap, out,
+                        q_norm, k_norm, eps)()
+
+
+def decode_call(ctx, kv, layer, rope, slots, pos, q, k_new, v_new, n_heads, scale, window=0, cap=0.0, out=None,
+                q_norm=None, k_norm=None, eps=1e-6):
+    """smol_attn_decode(_qknorm) as a Prepared call"""
     slots = np.ascontiguousarray(slots, np.int32)
     pos = np.ascontiguousarray(pos, np.int32)
     n = len(slots)
@@ -365,11 +385,18 @@ def decode(ctx, kv, layer, rope, slots, pos, q, k_new, v_new, n_heads, scale, wi
             _dev(q, "q"), _dev(k_new, "k"), _dev(v_new, "v"), _dtype_code(q), n_heads, ctypes.c_float(scale),
             window, ctypes.c_float(cap))
     if q_norm is None and k_norm is None:
-        _check(load().smol_attn_decode(*args, _dev(out, "out")), "smol_attn_decode")
-    else:
-        _check(load().smol_attn_decode_qknorm(*args, _norm_w(q_norm, "q_norm"), _norm_w(k_norm, "k_norm"),
-                                              ctypes.c_float(eps), _dev(out, "out")), "smol_attn_decode_qknorm")
-    return out
+        return Prepared(load().smol_attn_decode, args + (_dev(out, "out"),), "smol_attn_decode", out, (slots, pos))
+    return Prepared(load().smol_attn_decode_qknorm,
+                    args + (_norm_w(q_norm, "q_norm"), _norm_w(k_norm, "k_norm"), ctypes.c_float(eps),
+                            _dev(out, "out")), "smol_attn_decode_qknorm", out, (slots, pos))
+
+
+def decode(ctx, kv, layer, rope, slots, pos, q, k_new, v_new, n_heads, scale, window=0, cap=0.0, out=None,
+           q_norm=None, k_norm=None, eps=1e-6):
+    """Batched single-token decode; see smol_attn_decode. q_norm / k_norm
+    (device float32 [head_dim]) select smol_attn_decode_qknorm."""
+    return decode_call(ctx, kv, layer, rope, slots, pos, q, k_new, v_new, n_heads, scale, window, cap, out,
+                       q_norm, k_norm, eps)()
 
 
 def causal(ctx, q, k, v, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset, window=0, cap=0.0,
@@ -397,13 +424,17 @@ def causal_bf16(ctx, q, k, v, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale
     return out
 
 
-def bidirectional(ctx, q, k, v, seq, n_heads, head_dim, scale, window_starts, out=None):
+def bidirectional_call(ctx, q, k, v, seq, n_heads, head_dim, scale, window_starts, out=None):
+    """smol_attn_bidirectional as a Prepared call"""
     ws = np.ascontiguousarray(window_starts, np.int32)
     out = _out_like(seq, n_heads, head_dim, q.device, out)
-    _check(load().smol_attn_bidirectional(ctx.h, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), _dtype_code(q), seq,
-                                          n_heads, head_dim, ctypes.c_float(scale), ws.ctypes.data_as(_IP),
-                                          len(ws) - 1, _dev(out, "out")), "smol_attn_bidirectional")
-    return out
+    args = (ctx.h, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), _dtype_code(q), seq, n_heads, head_dim,
+            ctypes.c_float(scale), ws.ctypes.data_as(_IP), len(ws) - 1, _dev(out, "out"))
+    return Prepared(load().smol_attn_bidirectional, args, "smol_attn_bidirectional", out, (ws,))
+
+
+def bidirectional(ctx, q, k, v, seq, n_heads, head_dim, scale, window_starts, out=None):
+    return bidirectional_call(ctx, q, k, v, seq, n_heads, head_dim, scale, window_starts, out)()
 
 
 def apply_rope(ctx, rope, x, positions, n_heads):
