@@ -340,9 +340,9 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
         const bool full = act && k0 >= lo_max && k0 + SMOL_SLAB <= hi_min;
         read_k(st_k, kf);
         read_v(st_v, vnow);
-        if (!odd) {
-            dma(slab_k(i + 3), (i + 3) % NSTG);
-            dma(slab_k(i + 4), (i + 4) % NSTG);
+        if (!odd) { /* slab 'steps' (K read in the last step, its S unused) and later ones are not staged */
+            if (i + 3 < steps) dma(slab_k(i + 3), (i + 3) % NSTG);
+            if (i + 4 < steps) dma(slab_k(i + 4), (i + 4) % NSTG);
         }
         /* the LDS reads and transfers go out first, then P.V of the
          * previous slab (its fragments are in registers) covers the reads'
