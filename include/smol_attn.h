@@ -110,11 +110,13 @@ SMOL_ATTN_API int smol_attn_ctx_timing_read(smol_attn_ctx *ctx, double *ms, int 
 #define SMOL_OPT_XCD_CHECK 6      /* read only: 1 when workgroup b was seen on XCD b % n_xcc at
                                    * creation (k_dec's split merge needs it), 0 when not (then
                                    * k_dec does not split) */
-#define SMOL_OPT_BIDIR_WIN 7      /* bidirectional windows: 0 k_attn_win (LDS-resident, reads the
-                                   * inputs directly) for windows of at most 128 keys, else the
-                                   * pre-pass and k_attn_fb / k_attn_fa; 1: k_attn_win whenever the
-                                   * windows fit in LDS; -1: never */
-#define SMOL_OPT_COUNT 8
+#define SMOL_OPT_BIDIR_WIN 7      /* bidirectional windows: 0 (or 1) k_attn_win (LDS-resident,
+                                   * reads the inputs directly) whenever the windows fit in LDS,
+                                   * else the pre-pass and k_attn_fb / k_attn_fa; -1: never */
+#define SMOL_OPT_WIN_KSPLIT 8     /* k_attn_win: 1: 128-row tiles over every key; 2: 64-row tiles,
+                                   * two key groups (0: 2 when 128-row tiles would leave compute
+                                   * units idle) */
+#define SMOL_OPT_COUNT 9
 SMOL_ATTN_API int smol_attn_ctx_set_option(smol_attn_ctx *ctx, int option, int value);
 SMOL_ATTN_API int smol_attn_ctx_get_option(smol_attn_ctx *ctx, int option, int *value);
 

@@ -1374,10 +1374,10 @@ extern "C" int smol_attn_bidirectional(smol_attn_ctx *ctx, const void *q, const 
         if (ws[w] < 0 || ws[w + 1] < ws[w] || ws[w + 1] > seq)
             return fail(SMOL_ATTN_ERR_ARG, "window %d = [%d, %d) outside [0, %d)", w, ws[w], ws[w + 1], seq);
     /* k_attn_win reads the inputs directly (no pre-pass, no staging in
-     * HBM); each 128-row tile stages its whole window, which pays for short
-     * windows (audio encoder, 104 keys: 9.5 us against 14 us for the
-     * pre-pass and k_attn_fb) and not for long ones (SigLIP, 256 keys: about
-     * even), so by default it takes windows of at most 128 keys */
+     * HBM, one launch); each tile stages its whole window, and it still
+     * beats the pre-pass and k_attn_fb wherever the window fits in LDS
+     * (audio encoder, 104 keys: 9.2 us against 14 us; SigLIP, 256 keys:
+     * 14.3 us against 15.7 us per call) */
     {
         int max_len = 0;
         long long n_tiles = 0;
@@ -1387,7 +1387,7 @@ extern "C" int smol_attn_bidirectional(smol_attn_ctx *ctx, const void *q, const 
         }
         const int wmax = smol_win_max_keys(hd);
         const int opt = ctx->opt[SMOL_OPT_BIDIR_WIN];
-        if (opt >= 0 && wmax > 0 && max_len <= (opt == 1 ? wmax : std::min(wmax, 128)) && n_windows <= WIN_ARG_WINDOWS &&
+        if (opt >= 0 && wmax > 0 && max_len <= wmax && n_windows <= WIN_ARG_WINDOWS &&
             (long long)n_windows * n_heads * ((max_len + 63) / 64) + 8LL * ((max_len + 63) / 64) <= 0x7FFFFFFF) {
             if ((rc = set_device(ctx))) return rc;
             if (n_tiles == 0) return SMOL_ATTN_OK;
@@ -1400,7 +1400,14 @@ extern "C" int smol_attn_bidirectional(smol_attn_ctx *ctx, const void *q, const 
             wp.qscale = (float)(scale * LOG2E_D);
             wp.H = n_heads;
             wp.n_windows = n_windows;
-            wp.tpu = (max_len + WIN_ROWS - 1) / WIN_ROWS;
+            /* 128-row tiles, or 64-row tiles over two key groups when the
+             * 128-row tiles would leave compute units idle */
+            const long long units = (long long)n_windows * n_heads;
+            const int ko = ctx->opt[SMOL_OPT_WIN_KSPLIT];
+            wp.ksplit = ko == 1 || ko == 2 ? ko
+                        : max_len > SMOL_SLAB && units * ((max_len + WIN_ROWS - 1) / WIN_ROWS) < ctx->cu_count ? 2 : 1;
+            const int rows = WIN_ROWS / wp.ksplit;
+            wp.tpu = (max_len + rows - 1) / rows;
             wp.n_xcc = std::max(1, ctx->n_xcc);
             wp.range_flag = ctx->range_flag;
             memcpy(wp.ws, ws, (size_t)(n_windows + 1) * sizeof(int));

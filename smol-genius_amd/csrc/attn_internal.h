@@ -163,12 +163,14 @@ typedef struct {
 #define WIN_ARG_WINDOWS 255   /* windows passed in the kernel arguments */
 #endif
 #define WIN_TPB 512           /* threads of a k_attn_win workgroup: 8 waves, two per SIMD */
-#define WIN_ROWS 128          /* rows of its tile: 16 per wave */
+#define WIN_ROWS 128          /* rows of its tile (ksplit 1; 64 for ksplit 2): 16 per wave */
 typedef struct {
     const void *q; const void *k; const void *v; int in_dtype;
     long long row_stride;      /* elements between consecutive tokens (n_heads * hd) */
     float *out; float qscale; int H; int n_windows;
-    int tpu;                   /* 64-row tiles of the longest window */
+    int tpu;                   /* tiles of the longest window */
+    int ksplit;                /* 1: a workgroup's 8 waves hold 128 rows over every key; 2: two groups of
+                                  4 waves hold 64 rows, each over half the window's slabs, merged in LDS */
     int n_xcc;                 /* XCDs: workgroup b runs on XCD b % n_xcc */
     int *range_flag;           /* set to 1 when a value written as fp16 would overflow */
     int ws[WIN_ARG_WINDOWS + 1];

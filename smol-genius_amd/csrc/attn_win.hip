@@ -3,8 +3,11 @@
  * window's keys resident in LDS (common/kernels/attention.c:32-77, the
  * vision encoders' and the audio encoder's windows).
  *
- * A workgroup owns one 128-row tile of one (window, head): its eight waves
- * read the window's K and V rows straight from the inputs (fp32 or bf16),
+ * A workgroup owns one 128-row tile of one (window, head) (or, when the
+ * windows are too few to fill the GPU that way, a 64-row tile whose two
+ * groups of four waves take the first and second half of the window's
+ * slabs and merge their softmax states through LDS at the end): its eight
+ * waves read the window's K and V rows straight from the inputs (fp32 or bf16),
  * convert them to fp16 (bf16 exactly, fp32 rounded to nearest even, as the
  * pre-pass of the other kernels does) and write them once into an LDS image
  * of the whole window; Q is read into registers the same way, times
@@ -86,13 +89,18 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
     if (u >= p.n_windows * p.H) return;
     const int w = u / p.H, h = u - w * p.H;
     const int w0 = p.ws[w], len = p.ws[w + 1] - w0;
-    const int row0 = tile * WIN_ROWS;
+    const int split = p.ksplit == 2;
+    const int row0 = tile * (WIN_ROWS >> split);
     if (row0 >= len) return;
     const int nslab = (len + SMOL_SLAB - 1) / SMOL_SLAB; /* <= NS (the host's choice of build) */
     const long long hoff = (long long)h * HD;
+    /* the wave's rows and its group's slabs [s_lo, s_hi) */
+    const int grp = split ? wave >> 2 : 0, wr = split ? wave & 3 : wave;
+    const int s_half = (nslab + 1) >> 1;
+    const int s_lo = grp == 0 ? 0 : s_half, s_hi = split && grp == 0 ? s_half : nslab;
 
     /* ---- Q fragments of this wave's 16 rows: row rq, dims 32 ks + 8 j ---- */
-    const int rq = row0 + 16 * wave + c;
+    const int rq = row0 + 16 * wr + c;
     const bool q_ok = rq < len;
     Raw8In<BF> qin[KS];
 #pragma unroll
@@ -108,18 +116,15 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
      * the key's 8 dims cb = slot ^ f(key % 32): a wave writes 1 KB of
      * consecutive LDS, and the 16 lanes of a key read its row. Slots past
      * HDP are never read and are skipped.
-     * V^T: unit (slab, row pair d, d + 1, slot jc) gathers dims d, d + 1 of
-     * the 8 keys that slot holds (one 4- or 8-byte load per key) and writes
-     * the two rows' 16-byte chunks.
+     * V^T: 8 x 8 blocks, below.
      * All loads of a part are issued before any is used; out-of-range
      * lanes read the window's first row and write zeros. */
     constexpr int CK = HDP / 8;
     const int nkey = nslab * SMOL_SLAB;
     constexpr int NKT = NS * SMOL_SLAB * 16 / WIN_TPB;              /* K chunks per thread (the build's capacity) */
     constexpr int RK = (BF ? 16 : 8) < NKT ? (BF ? 16 : 8) : NKT;  /* K chunks a round */
-    constexpr int NVT = (NS * 8 * DT * 4 + WIN_TPB - 1) / WIN_TPB; /* V^T units per thread */
-    constexpr int RV = (BF ? 5 : 3) < NVT ? (BF ? 5 : 3) : NVT;    /* V^T units a round */
-    typedef typename std::conditional<BF, uint32_t, uint2>::type V2;
+    constexpr int NDB = 2 * DT;                                     /* 8-row blocks of a V^T image */
+    constexpr int NVB = (NS * 4 * NDB + WIN_TPB - 1) / WIN_TPB;     /* 8 x 8 V blocks per thread */
     auto k_chunk = [&](int e, int &key, int &slot, int &rr, int &cb) __attribute__((always_inline)) {
         key = e >> 4; slot = e & 15; rr = key & 31;
         cb = slot ^ ((rr & 3) | (((rr >> 3) & 3) << 2));
@@ -149,58 +154,54 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
             *reinterpret_cast<uint4 *>(smem + (key >> 5) * SLABB + rr * KROW + 16 * slot) = pack_h8(v);
         }
     };
-    auto v_unit = [&](int e, int &sl, int &d, int &jc, int &kb) __attribute__((always_inline)) {
-        sl = e / (32 * DT);
-        const int rem = e - sl * (32 * DT);
-        d = 2 * (rem >> 2); jc = rem & 3;
-        kb = sl * SMOL_SLAB + 8 * (jc ^ ((d >> 1) & 3));
-    };
-    auto v_issue = [&](int r0, V2 (&in)[RV][8]) __attribute__((always_inline)) {
+    /* V^T: block e (keys 8 kb .. 8 kb + 7, dims 8 db .. 8 db + 7; consecutive
+     * lanes take consecutive dim blocks of a key row, so a load instruction
+     * reads whole row segments) is eight 16-byte row loads, transposed in
+     * registers into eight 16-byte chunks of V^T rows */
+    const int nvb = nslab * 4 * NDB;
+    auto v_issue = [&](int u, Raw8In<BF> (&in)[8]) __attribute__((always_inline)) {
+        const int e = tid + WIN_TPB * u, db = e % NDB, kb = e / NDB;
 #pragma unroll
-        for (int u = 0; u < RV; u++) {
-            int sl, d, jc, kb;
-            v_unit(tid + WIN_TPB * (r0 + u), sl, d, jc, kb);
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const bool ok = r0 + u < NVT && sl < nslab && kb + i < len && d < HD;
-                const long long idx = (long long)(w0 + (ok ? kb + i : 0)) * p.row_stride + hoff + (ok ? d : 0);
-                if constexpr (BF) in[u][i] = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.v) + idx);
-                else in[u][i] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const float *>(p.v) + idx);
-            }
+        for (int i = 0; i < 8; i++) {
+            const bool ok = e < nvb && 8 * kb + i < len && 8 * db < HD;
+            in[i].load(p.v, (long long)(w0 + (ok ? 8 * kb + i : 0)) * p.row_stride + hoff + (ok ? 8 * db : 0));
         }
     };
-    auto v_store = [&](int r0, const V2 (&in)[RV][8]) __attribute__((always_inline)) {
+    auto v_store = [&](int u, const Raw8In<BF> (&in)[8]) __attribute__((always_inline)) {
+        const int e = tid + WIN_TPB * u, db = e % NDB, kb = e / NDB;
+        if (e >= nvb) return;
+        uint4 r[8]; /* fp16 rows: r[i] holds dims 8 db .. 8 db + 7 of key 8 kb + i */
 #pragma unroll
-        for (int u = 0; u < RV; u++) {
-            int sl, d, jc, kb;
-            v_unit(tid + WIN_TPB * (r0 + u), sl, d, jc, kb);
-            if (r0 + u >= NVT || sl >= nslab) continue;
-            float v0[8], v1[8];
+        for (int i = 0; i < 8; i++) {
+            float v[8];
+            in[i].unpack(v);
+            if (!(8 * kb + i < len && 8 * db < HD)) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const bool ok = kb + i < len && d < HD;
-                float a, b2;
-                if constexpr (BF) {
-                    a = __uint_as_float(in[u][i] << 16);
-                    b2 = __uint_as_float(in[u][i] & 0xFFFF0000u);
-                } else {
-                    a = __uint_as_float(in[u][i].x);
-                    b2 = __uint_as_float(in[u][i].y);
-                }
-                v0[i] = ok ? a : 0.0f;
-                v1[i] = ok ? b2 : 0.0f;
+                for (int t = 0; t < 8; t++) v[t] = 0.0f;
             }
-            note_h_range(p.range_flag, v0);
-            note_h_range(p.range_flag, v1);
-            unsigned char *row = smem + sl * SLABB + K_BYTES + d * 64 + 16 * jc;
-            *reinterpret_cast<uint4 *>(row) = pack_h8(v0);
-            *reinterpret_cast<uint4 *>(row + 64) = pack_h8(v1);
+            note_h_range(p.range_flag, v);
+            r[i] = pack_h8(v);
+        }
+        const int sl = kb >> 2, jc = kb & 3;
+        unsigned char *vbase = smem + sl * SLABB + K_BYTES;
+#pragma unroll
+        for (int dd = 0; dd < 8; dd++) {
+            /* column dd: key pairs (2m, 2m + 1) of dim 8 db + dd */
+            uint32_t c4[4];
+#pragma unroll
+            for (int mm = 0; mm < 4; mm++) {
+                const uint32_t x = reinterpret_cast<const uint32_t *>(&r[2 * mm])[dd >> 1];
+                const uint32_t y = reinterpret_cast<const uint32_t *>(&r[2 * mm + 1])[dd >> 1];
+                c4[mm] = (dd & 1) ? (x >> 16) | (y & 0xFFFF0000u) : (x & 0xFFFFu) | (y << 16);
+            }
+            const int d = 8 * db + dd;
+            *reinterpret_cast<uint4 *>(vbase + d * 64 + 16 * (jc ^ ((d >> 1) & 3))) = make_uint4(c4[0], c4[1], c4[2], c4[3]);
         }
     };
     {
         /* the first rounds of K and V go out together */
         Raw8In<BF> kin[RK];
-        V2 vin[RV][8];
+        Raw8In<BF> vin[8];
         k_issue(0, kin);
         v_issue(0, vin);
         k_store(0, kin);
@@ -211,9 +212,9 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
             k_store(r0, kin);
         }
 #pragma unroll
-        for (int r0 = RV; r0 < NVT; r0 += RV) {
-            v_issue(r0, vin);
-            v_store(r0, vin);
+        for (int u = 1; u < NVB; u++) {
+            v_issue(u, vin);
+            v_store(u, vin);
         }
     }
     h8 qf[KS];
@@ -268,13 +269,15 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
     };
     h8 kf[2][KS];
     f4 scur[2], snext[2];
-    read_k(0, kf);
-    qk(kf, scur);
-    for (int s = 0; s < nslab; s++) {
+    if (s_lo < s_hi) {
+        read_k(s_lo, kf);
+        qk(kf, scur);
+    }
+    for (int s = s_lo; s < s_hi; s++) {
         h8 vf[DT];
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) vf[dt] = lds_h8(s, vfo + dt * 1024);
-        const bool more = s + 1 < nslab;
+        const bool more = s + 1 < s_hi;
         if (more) {
             read_k(s + 1, kf);
             qk(kf, snext);
@@ -295,6 +298,7 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
         for (int e = 1; e < 8; e++) mx = fmaxf(mx, sv[e]);
         mx = row_max4(mx);
         const float m_new = fmaxf(m, mx); /* finite: every slab holds a key of the window */
+        /* (a group without slabs keeps m = -inf, lsum = 0, o = 0) */
         const float alpha = __builtin_amdgcn_exp2f(m - m_new);
         m = m_new;
         h8 pf;
@@ -309,9 +313,33 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
         }
     }
 
+    /* ---- two groups: group 1 hands (O, m, l) to group 0 through LDS, lane
+     * by lane (wave wr of either group holds the same rows in the same
+     * lanes) ---- */
+    float l = lsum[0];
+    if (split) {
+        float *xo = reinterpret_cast<float *>(smem) + (wr * 64 + lane) * (4 * DT + 4);
+        static_assert(4 * 64 * (4 * DT + 4) * 4 <= NS * SLABB, "merge scratch");
+        __syncthreads(); /* every slab read is done */
+        if (grp == 1) {
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) *reinterpret_cast<f4 *>(xo + 4 * dt) = o[dt];
+            xo[4 * DT] = m;
+            xo[4 * DT + 1] = l;
+        }
+        __syncthreads();
+        if (grp == 1) return;
+        const float m1 = xo[4 * DT], l1 = xo[4 * DT + 1];
+        const float M = fmaxf(m, m1); /* finite: group 0 has a slab with a key of the window */
+        const float w0 = __builtin_amdgcn_exp2f(m - M), w1 = __builtin_amdgcn_exp2f(m1 - M);
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) o[dt] = o[dt] * w0 + *reinterpret_cast<const f4 *>(xo + 4 * dt) * w1;
+        l = l * w0 + l1 * w1;
+    }
+
     /* ---- out rows of the window (rows past it are not written) ---- */
     if (!q_ok) return;
-    const float inv = lsum[0] > 0.0f ? 1.0f / lsum[0] : 0.0f;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     float *orow = p.out + (long long)(w0 + rq) * p.row_stride + hoff;
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) {

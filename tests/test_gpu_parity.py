@@ -219,8 +219,10 @@ def test_bidirectional_ragged_staged(ctx, sa, oracle, opts, kernel):
 def test_window_kernel(ctx, sa, oracle, opts, hd, bf):
     """k_attn_win: windows resident in LDS, read from fp32 or bf16 inputs;
     ragged windows (1, 31, 33 keys ...), a window at the LDS limit of the
-    head_dim, and the same call through the staged path for comparison. A
-    window past the limit takes the staged path by itself."""
+    head_dim, with 128-row tiles over every key and with 64-row tiles over
+    two key groups (a 1-key window leaves the second group without slabs),
+    and the same call through the staged path for comparison. A window past
+    the limit takes the staged path by itself."""
     # the LDS holds 160 KB of 32-key slabs: K 32 x 256 B, V^T 16 ceil(hd / 16) x 64 B
     lim = (160 * 1024 // (8192 + 16 * ((hd + 15) // 16) * 64)) * 32
     assert lim >= 256
@@ -235,15 +237,17 @@ def test_window_kernel(ctx, sa, oracle, opts, hd, bf):
         sc = 1.0 / np.sqrt(hd)
         want = oracle.bidirectional_attention(Q, K, V, seq, H, hd, sc, ws)
         res = []
-        for w in (1, -1):
+        for w, ks in ((1, 1), (1, 2), (-1, 0)):
             opts(sa.OPT_BIDIR_WIN, w)
+            opts(sa.OPT_WIN_KSPLIT, ks)
             init = synth.normal(79, (seq, H * hd)).astype(np.float32)
             out = dev(init)
             got = sa.bidirectional(ctx, conv(Q), conv(K), conv(V), seq, H, hd, sc, ws, out=out).cpu().numpy()
             np.testing.assert_array_equal(got[:ws[0]], init[:ws[0]])
-            assert_parity(got[ws[0]:], want[ws[0]:], "win %d hd %d %s" % (w, hd, ws))
+            assert_parity(got[ws[0]:], want[ws[0]:], "win %d ksplit %d hd %d %s" % (w, ks, hd, ws))
             res.append(got)
         opts(sa.OPT_BIDIR_WIN, 0)
+        opts(sa.OPT_WIN_KSPLIT, 0)
 
 
 @pytest.mark.parametrize("case", [  # Hq, Hkv, hd, seq, window, bf16 / bidirectional window starts
