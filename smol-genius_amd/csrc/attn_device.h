@@ -24,6 +24,16 @@
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef unsigned u4v __attribute__((ext_vector_type(4)));
+
+/* Streaming 16-byte stores for outputs no later work of the same kernel
+ * reads (staging, cache rows, attention outputs): non-temporal, so they
+ * drain to memory as they are written instead of collecting in L2 for the
+ * end-of-kernel write-back. */
+__device__ __forceinline__ void st_stream(void *p, uint4 v) {
+    __builtin_nontemporal_store(u4v{v.x, v.y, v.z, v.w}, reinterpret_cast<u4v *>(p));
+}
+__device__ __forceinline__ void st_stream(float *p, f4 v) { __builtin_nontemporal_store(v, reinterpret_cast<f4 *>(p)); }
 
 #define LOG2E_F 1.4426950408889634f
 

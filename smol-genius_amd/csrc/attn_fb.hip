@@ -411,7 +411,7 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
             const int d = 16 * dt + 4 * j;
             if (HD % 16 != 0 && d >= HD) continue;
             const f4 o1 = *reinterpret_cast<const f4 *>(xo + 4 * dt);
-            *reinterpret_cast<f4 *>(orow + d) = o[nt][dt] * a0 + o1 * a1;
+            st_stream(orow + d, o[nt][dt] * a0 + o1 * a1);
         }
     }
     if (next < 0) break;
