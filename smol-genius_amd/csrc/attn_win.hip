@@ -345,7 +345,7 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
     for (int dt = 0; dt < DT; dt++) {
         const int d = 16 * dt + 4 * j;
         if (HD % 16 != 0 && d >= HD) continue;
-        st_stream(orow + d, o[dt] * inv);
+        *reinterpret_cast<f4 *>(orow + d) = o[dt] * inv;
     }
 }
 
