@@ -899,13 +899,17 @@ static int run_decode(smol_attn_ctx *ctx, const CallShape &cs, const DecCall &dc
         whole_dc.whole = true;
         pdc = &whole_dc;
     }
+    /* at least one slab per wave of a split, two at head_dim 256: the merger
+     * reads every split's rows x head_dim partial, and at head_dim 256 fewer,
+     * longer splits win (C4: 23.4 -> 21.5 us) */
+    const int min_per = hd > 128 ? 2 * nw : nw;
     std::vector<DecItem> items;
-    plan_decode(ctx, *pdc, cs.Hkv, cs.window, n_rb, fit, nw, items);
+    plan_decode(ctx, *pdc, cs.Hkv, cs.window, n_rb, fit, min_per, items);
     if (dc.noalloc && items.size() > DEC_ARG_ITEMS && !pdc->whole) {
         whole_dc = dc;
         whole_dc.whole = true;
         pdc = &whole_dc;
-        plan_decode(ctx, *pdc, cs.Hkv, cs.window, n_rb, fit, nw, items);
+        plan_decode(ctx, *pdc, cs.Hkv, cs.window, n_rb, fit, min_per, items);
     }
     if (dc.noalloc && (items.size() > DEC_ARG_ITEMS || dc.seqs.size() > DEC_ARG_SEQS))
         return fail(SMOL_ATTN_ERR_UNSUPPORTED, "%d sequences / %d workgroups exceed what the no-alloc decode passes "
