@@ -81,7 +81,7 @@ __device__ __forceinline__ void prep_q(const PrepParams &p, const PrepBlock &blk
                     *reinterpret_cast<float4 *>(p.qs32 + qi[u] + 4) = make_float4(v[4], v[5], v[6], v[7]);
                 } else {
                     note_h_range(p.range_flag, v);
-                    st_stream(p.qs + qi[u], pack_h8(v));
+                    *reinterpret_cast<uint4 *>(p.qs + qi[u]) = pack_h8(v);
                 }
             }
         }
@@ -160,9 +160,9 @@ __device__ __forceinline__ void prep_fresh(const PrepParams &p, const PrepBlock 
                 for (int i = 0; i < 8; i++) kv[i] = 0.0f;
             }
         }
-        if (has_cache && is_new) st_stream(kc + (long long)pos * HD + d0, pack_bf16x8(kv));
+        if (has_cache && is_new) *reinterpret_cast<uint4 *>(kc + (long long)pos * HD + d0) = pack_bf16x8(kv);
         note_h_range(p.range_flag, kv);
-        st_stream(kf + (long long)(frow_base + r) * HD + d0, pack_h8(kv));
+        *reinterpret_cast<uint4 *>(kf + (long long)(frow_base + r) * HD + d0) = pack_h8(kv);
 #pragma unroll
         for (int i = 0; i < 8; i++) sv[r * 257 + d0 + i] = vv[i];
     }
@@ -198,7 +198,7 @@ __device__ __forceinline__ void prep_fresh(const PrepParams &p, const PrepBlock 
                 if (pos + i >= new_lo) v[i] = sv[(q0 + i) * 257 + d];
             if (has_cache) {
                 if (pos >= new_lo && pos + 8 <= new_hi) {
-                    st_stream(vtc_blk + ci, pack_bf16x8(v));
+                    *reinterpret_cast<uint4 *>(vtc_blk + ci) = pack_bf16x8(v);
                 } else {
                     for (int i = 0; i < 8; i++)
                         if (pos + i >= new_lo && pos + i < new_hi) vtc_blk[ci + i] = f32_to_bf16(v[i]);
@@ -206,7 +206,7 @@ __device__ __forceinline__ void prep_fresh(const PrepParams &p, const PrepBlock 
             }
         }
         note_h_range(p.range_flag, v);
-        st_stream(vtf_blk + ci, pack_h8(v));
+        *reinterpret_cast<uint4 *>(vtf_blk + ci) = pack_h8(v);
     }
 }
 
