@@ -306,7 +306,7 @@ def main():
                          "the HBM byte counters of a profiler run)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path (the attention would shard "
+        print("bench.py measures one GPU only: the library has no multi-GPU path (the attention would shard "
               "by KV head with no exchange inside attention). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
