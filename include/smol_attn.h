@@ -37,7 +37,9 @@
  *
  * Threading: one context per host thread, as the reference's global thread
  * pool is not re-entrant (common/kernels/threading.c:26-47). Calls on one
- * context are ordered on its stream.
+ * context are ordered on its stream. Contexts share no host state (each
+ * builds its own kernel arguments), so threads with one context each may
+ * call concurrently.
  */
 #ifndef SMOL_ATTN_H
 #define SMOL_ATTN_H
@@ -58,6 +60,8 @@ extern "C" {
 #define SMOL_ATTN_ERR_UNSUPPORTED (-4)
 #define SMOL_ATTN_ERR_NO_GPU (-5)
 #define SMOL_ATTN_ERR_RANGE (-6) /* a value left the fp16 staging's range (see Numerics) */
+#define SMOL_ATTN_ERR_TIMEOUT (-7) /* a decode split-K merge gave up waiting for its splits; the
+                                    * rows it merges are NaN (reported by synchronize) */
 
 /* element type of the Q / K / V inputs */
 #define SMOL_ATTN_F32 0
@@ -83,8 +87,10 @@ SMOL_ATTN_API int smol_attn_device_count(void);
  * stream. The context never creates or destroys the stream. */
 SMOL_ATTN_API int smol_attn_ctx_create(int device, void *stream, smol_attn_ctx **out);
 SMOL_ATTN_API int smol_attn_ctx_destroy(smol_attn_ctx *ctx);
-/* waits for the context's stream; returns SMOL_ATTN_ERR_RANGE (and clears
- * the flag) when a call since the last synchronize raised the range flag */
+/* waits for the context's stream; returns SMOL_ATTN_ERR_TIMEOUT when a
+ * decode merge since the last synchronize gave up waiting for its splits,
+ * else SMOL_ATTN_ERR_RANGE when a call raised the range flag (both flags are
+ * cleared) */
 SMOL_ATTN_API int smol_attn_ctx_synchronize(smol_attn_ctx *ctx);
 SMOL_ATTN_API void *smol_attn_ctx_stream(smol_attn_ctx *ctx);
 
@@ -100,7 +106,8 @@ SMOL_ATTN_API int smol_attn_ctx_timing_read(smol_attn_ctx *ctx, double *ms, int 
 /* Options of a context (no counterpart in the reference): switches that pick
  * between equivalent kernels or work splits, for tests and tuning. All are 0
  * by default, which selects by call shape. Results stay within the path's
- * tolerance whatever they are set to. */
+ * tolerance whatever they are set to, except under SMOL_OPT_FAULT_MERGE,
+ * which exists to test the error path. */
 #define SMOL_OPT_PREFILL_KERNEL 0 /* 1: k_attn_fb wherever its keys allow, 2: k_attn_fa */
 #define SMOL_OPT_FB_LISTS 1       /* -1: one k_attn_fb workgroup per tile (no tile lists) */
 #define SMOL_OPT_FB_NT 2          /* 2: two row tiles per k_attn_fb wave */
@@ -116,7 +123,12 @@ SMOL_ATTN_API int smol_attn_ctx_timing_read(smol_attn_ctx *ctx, double *ms, int 
 #define SMOL_OPT_WIN_KSPLIT 8     /* k_attn_win: 1: 128-row tiles over every key; 2: 64-row tiles,
                                    * two key groups (0: 2 when 128-row tiles would leave compute
                                    * units idle) */
-#define SMOL_OPT_COUNT 9
+#define SMOL_OPT_DEC_SPIN 9       /* k_dec: flag polls before a split-K merger gives up (0: 4194304) */
+#define SMOL_OPT_FAULT_MERGE 10   /* fault injection for tests: 1 makes every k_dec merger wait for a
+                                   * flag value no split writes, so it gives up after SMOL_OPT_DEC_SPIN
+                                   * polls, writes NaN rows and synchronize returns
+                                   * SMOL_ATTN_ERR_TIMEOUT; every kernel still ends normally */
+#define SMOL_OPT_COUNT 11
 SMOL_ATTN_API int smol_attn_ctx_set_option(smol_attn_ctx *ctx, int option, int value);
 SMOL_ATTN_API int smol_attn_ctx_get_option(smol_attn_ctx *ctx, int option, int *value);
 

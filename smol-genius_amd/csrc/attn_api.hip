@@ -170,7 +170,15 @@ struct smol_attn_ctx {
     DevBuf qs32; /* fp32 Q scratch of the decode kernel */
     DevBuf out32; /* fp32 result of a call whose output is bf16 */
     DevBuf dec_part; /* k_dec partial slots and flags */
-    int *range_flag = nullptr; /* device int, set by kernels when fp16 staging overflows */
+    /* device flags, 256 bytes: word 0 is set by kernels when fp16 staging
+     * overflows, word 32 (its own 128-byte line) by a k_dec merger that gave
+     * up waiting for its splits; synchronize reads and clears both */
+    int *range_flag = nullptr;
+    /* kernel arguments of k_dec and k_attn_win, built in place per context
+     * (several KB: kept off the stack; one thread per context, so no two
+     * calls build them at once) */
+    DecParams dp;
+    WinParams wp;
     int cu_count = 256;
     int n_xcc = 1;       /* XCDs of the device */
     bool xcd_ok = true;  /* workgroup b runs on XCD b % n_xcc (checked at creation) */
@@ -374,14 +382,18 @@ extern "C" int smol_attn_ctx_synchronize(smol_attn_ctx *ctx) {
     if (!ctx) return fail(SMOL_ATTN_ERR_ARG, "ctx is NULL");
     HIP_TRY(hipSetDevice(ctx->device));
     HIP_TRY(hipStreamSynchronize(ctx->stream));
-    int flag = 0;
-    HIP_TRY(hipMemcpy(&flag, ctx->range_flag, sizeof(int), hipMemcpyDeviceToHost));
-    if (flag) {
-        const int zero = 0;
-        HIP_TRY(hipMemcpy(ctx->range_flag, &zero, sizeof(int), hipMemcpyHostToDevice));
+    int flag[SMOL_FLAG_WORDS] = {};
+    HIP_TRY(hipMemcpy(flag, ctx->range_flag, sizeof(flag), hipMemcpyDeviceToHost));
+    if (flag[0] || flag[SMOL_FLAG_MERGE]) {
+        const int zero[SMOL_FLAG_WORDS] = {};
+        HIP_TRY(hipMemcpy(ctx->range_flag, zero, sizeof(zero), hipMemcpyHostToDevice));
+    }
+    if (flag[SMOL_FLAG_MERGE])
+        return fail(SMOL_ATTN_ERR_TIMEOUT, "a decode split-K merge gave up waiting for its splits (the affected "
+                    "rows are NaN)");
+    if (flag[0])
         return fail(SMOL_ATTN_ERR_RANGE, "a staged Q, K or V value was not finite or reached 65520 in magnitude "
                     "(fp16 staging of the prefill and bidirectional kernels)");
-    }
     return SMOL_ATTN_OK;
 }
 
@@ -916,7 +928,7 @@ static int run_decode(smol_attn_ctx *ctx, const CallShape &cs, const DecCall &dc
                     "in its kernel arguments (%d / %d)", (int)dc.seqs.size(), (int)items.size(), DEC_ARG_SEQS,
                     DEC_ARG_ITEMS);
 
-    static DecParams dp; /* large (kernel arguments of about 3.6 KB): built in place, one thread per context */
+    DecParams &dp = ctx->dp;
     static_assert(sizeof(DecParams) <= 4096, "kernel arguments");
     memset(&dp, 0, sizeof(dp));
     const smol_kv_cache *kv = cs.kv;
@@ -946,6 +958,9 @@ static int run_decode(smol_attn_ctx *ctx, const CallShape &cs, const DecCall &dc
     dp.window = cs.window;
     dp.cap2 = cs.cap > 0.0f ? (float)(cs.cap * LOG2E_D) : 0.0f;
     dp.slot_floats = slot_floats;
+    dp.err_flag = ctx->range_flag + SMOL_FLAG_MERGE;
+    dp.spin_limit = ctx->opt[SMOL_OPT_DEC_SPIN] > 0 ? ctx->opt[SMOL_OPT_DEC_SPIN] : DEC_SPIN_LIMIT;
+    dp.fault_merge = ctx->opt[SMOL_OPT_FAULT_MERGE] ? 1 : 0;
     int rc;
     if (dc.noalloc) {
         /* the per-device scratch: its flags hold earlier calls' epochs (or
@@ -1395,7 +1410,7 @@ extern "C" int smol_attn_bidirectional(smol_attn_ctx *ctx, const void *q, const 
             (long long)n_windows * n_heads * ((max_len + 63) / 64) + 8LL * ((max_len + 63) / 64) <= 0x7FFFFFFF) {
             if ((rc = set_device(ctx))) return rc;
             if (n_tiles == 0) return SMOL_ATTN_OK;
-            static WinParams wp; /* about 1 KB of kernel arguments, built in place (one thread per context) */
+            WinParams &wp = ctx->wp;
             memset(&wp, 0, sizeof(wp));
             wp.q = q; wp.k = k; wp.v = v;
             wp.in_dtype = dtype == SMOL_ATTN_BF16 ? SMOL_IN_BF16 : SMOL_IN_F32;

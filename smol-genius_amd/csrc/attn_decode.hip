@@ -47,7 +47,8 @@
  * was dispatched before it) polls the flags and merges. All splits of a
  * group run on one XCD, so flags and partials meet in that XCD's L2. A
  * merger whose flags do not all arrive within DEC_SPIN_LIMIT polls writes
- * NaN rows instead of waiting for ever.
+ * NaN rows instead of waiting for ever and raises the context's merge flag,
+ * which smol_attn_ctx_synchronize reports as SMOL_ATTN_ERR_TIMEOUT.
  */
 #include "attn_device.h"
 
@@ -870,13 +871,16 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
     if (tid < nsp - 1) {
         const unsigned *flag =
             reinterpret_cast<const unsigned *>(p.part + (slot0 + tid) * p.slot_floats + p.slot_floats - 1);
+        /* fault_merge: a value no split stores, so the wait runs to its bound */
+        const unsigned want = p.fault_merge ? ~p.epoch : p.epoch;
         int spins = 0;
-        while (poll_u32(flag) != p.epoch) {
-            if (++spins >= DEC_SPIN_LIMIT) { ok = 0; break; }
+        while (poll_u32(flag) != want) {
+            if (++spins >= p.spin_limit) { ok = 0; break; }
             __builtin_amdgcn_s_sleep(1);
         }
     }
     ok = __syncthreads_and(ok);
+    if (!ok && tid == 0) *p.err_flag = 1; /* synchronize reports it */
     /* Every load of the merge goes out in one round before anything waits
      * on it: the others' (m, l), then their O partials (which do not depend
      * on the weights). Element e (a row's 4 columns) gets tpe threads,

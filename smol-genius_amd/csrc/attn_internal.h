@@ -190,7 +190,10 @@ typedef struct {
 #define DEC_MAX_SPLIT 32      /* splits per group (the merge's LDS and the partial slots) */
 #define DEC_ARG_SEQS 32       /* sequences passed in the kernel arguments */
 #define DEC_ARG_ITEMS 320     /* workgroup items passed in the kernel arguments */
-#define DEC_SPIN_LIMIT (1 << 22) /* flag polls before a merger gives up (writes NaN) */
+#define DEC_SPIN_LIMIT (1 << 22) /* flag polls before a merger gives up (writes NaN rows and raises
+                                    the context's merge flag) */
+#define SMOL_FLAG_WORDS 64       /* ints of a context's device flag block (256 bytes) */
+#define SMOL_FLAG_MERGE 32       /* word of the merge flag: its own 128-byte line */
 
 /* one workgroup of the grid (index = blockIdx.x); seq < 0: nothing to do.
  * A group's rows are cut into row blocks of at most DEC_RB(hd) rows; each
@@ -232,6 +235,9 @@ typedef struct {
      * O [R][hd], (m, l) [R][2], then the flag (an int) at slot_floats - 1,
      * alone in the slot's last 128 bytes */
     float *part; int slot_floats; unsigned epoch;
+    int *err_flag;             /* set to 1 (plain store) by a merger that gave up waiting */
+    int spin_limit;            /* flag polls before a merger gives up */
+    int fault_merge;           /* 1: mergers wait for a flag value no split writes (tests the give-up path) */
     int n_rb;                  /* row blocks per (sequence, kv head) */
     int n_items;               /* grid size */
     const DecItem *items_dev;  /* the items when n_items > DEC_ARG_ITEMS */

@@ -137,7 +137,13 @@ class SmolAttnRangeError(SmolAttnError):
     overflowed since the last synchronize; those calls' outputs are not valid."""
 
 
+class SmolAttnTimeoutError(SmolAttnError):
+    """SMOL_ATTN_ERR_TIMEOUT: a decode split-K merge gave up waiting for its
+    splits since the last synchronize; the rows it merged are NaN."""
+
+
 ERR_RANGE = -6  # SMOL_ATTN_ERR_RANGE
+ERR_TIMEOUT = -7  # SMOL_ATTN_ERR_TIMEOUT
 
 
 def load(path=LIB_PATH):
@@ -159,7 +165,7 @@ def load(path=LIB_PATH):
 
 def _check(rc, what):
     if rc != 0:
-        cls = SmolAttnRangeError if rc == ERR_RANGE else SmolAttnError
+        cls = {ERR_RANGE: SmolAttnRangeError, ERR_TIMEOUT: SmolAttnTimeoutError}.get(rc, SmolAttnError)
         raise cls("%s failed (%d): %s" % (what, rc, load().smol_attn_last_error().decode()))
 
 
@@ -180,7 +186,7 @@ def _dev(t, what):
 
 # context options (include/smol_attn.h SMOL_OPT_*)
 (OPT_PREFILL_KERNEL, OPT_FB_LISTS, OPT_FB_NT, OPT_DEC_SLABS, OPT_DEC_WAVES, OPT_DEC_SPLIT, OPT_XCD_CHECK,
- OPT_BIDIR_WIN, OPT_WIN_KSPLIT) = range(9)
+ OPT_BIDIR_WIN, OPT_WIN_KSPLIT, OPT_DEC_SPIN, OPT_FAULT_MERGE) = range(11)
 
 
 class Context:
@@ -359,11 +365,13 @@ def prefill_call(ctx, kv, layer, slot, rope, pos0, q, k_new, v_new, n_heads, sca
     out = _out_like(seq_q, n_heads, kv.head_dim, q.device, out)
     args = (ctx.h, kv.h, layer, slot, rope.h if rope else None, pos0, seq_q, _dev(q, "q"), _dev(k_new, "k"),
             _dev(v_new, "v"), _dtype_code(q), n_heads, ctypes.c_float(scale), window, ctypes.c_float(cap))
+    # the call holds only raw device addresses: keep the tensors behind them alive with it
+    keep = (q, k_new, v_new, out, q_norm, k_norm)
     if q_norm is None and k_norm is None:
-        return Prepared(load().smol_attn_prefill, args + (_dev(out, "out"),), "smol_attn_prefill", out)
+        return Prepared(load().smol_attn_prefill, args + (_dev(out, "out"),), "smol_attn_prefill", out, keep)
     return Prepared(load().smol_attn_prefill_qknorm,
                     args + (_norm_w(q_norm, "q_norm"), _norm_w(k_norm, "k_norm"), ctypes.c_float(eps),
-                            _dev(out, "out")), "smol_attn_prefill_qknorm", out)
+                            _dev(out, "out")), "smol_attn_prefill_qknorm", out, keep)
 
 
 def prefill(ctx, kv, layer, slot, rope, pos0, q, k_new, v_new, n_heads, scale, window=0, cap=0.0, out=None,
@@ -384,11 +392,12 @@ def decode_call(ctx, kv, layer, rope, slots, pos, q, k_new, v_new, n_heads, scal
     args = (ctx.h, kv.h, layer, rope.h if rope else None, n, slots.ctypes.data_as(_IP), pos.ctypes.data_as(_IP),
             _dev(q, "q"), _dev(k_new, "k"), _dev(v_new, "v"), _dtype_code(q), n_heads, ctypes.c_float(scale),
             window, ctypes.c_float(cap))
+    keep = (slots, pos, q, k_new, v_new, out, q_norm, k_norm)
     if q_norm is None and k_norm is None:
-        return Prepared(load().smol_attn_decode, args + (_dev(out, "out"),), "smol_attn_decode", out, (slots, pos))
+        return Prepared(load().smol_attn_decode, args + (_dev(out, "out"),), "smol_attn_decode", out, keep)
     return Prepared(load().smol_attn_decode_qknorm,
                     args + (_norm_w(q_norm, "q_norm"), _norm_w(k_norm, "k_norm"), ctypes.c_float(eps),
-                            _dev(out, "out")), "smol_attn_decode_qknorm", out, (slots, pos))
+                            _dev(out, "out")), "smol_attn_decode_qknorm", out, keep)
 
 
 def decode(ctx, kv, layer, rope, slots, pos, q, k_new, v_new, n_heads, scale, window=0, cap=0.0, out=None,
@@ -430,7 +439,7 @@ def bidirectional_call(ctx, q, k, v, seq, n_heads, head_dim, scale, window_start
     out = _out_like(seq, n_heads, head_dim, q.device, out)
     args = (ctx.h, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), _dtype_code(q), seq, n_heads, head_dim,
             ctypes.c_float(scale), ws.ctypes.data_as(_IP), len(ws) - 1, _dev(out, "out"))
-    return Prepared(load().smol_attn_bidirectional, args, "smol_attn_bidirectional", out, (ws,))
+    return Prepared(load().smol_attn_bidirectional, args, "smol_attn_bidirectional", out, (ws, q, k, v, out))
 
 
 def bidirectional(ctx, q, k, v, seq, n_heads, head_dim, scale, window_starts, out=None):

@@ -684,3 +684,90 @@ def test_contexts_on_two_threads(sa, oracle):
     for idx, (_, _, _, want) in enumerate(inputs):
         for got in results[idx]:
             assert_parity(got, want, "thread %d" % idx)
+
+
+def test_contexts_on_two_threads_decode_bidir(sa, oracle, wo):
+    """Two host threads, each with its own context and stream, interleave
+    split-K decode calls (k_dec with several workgroups per sequence merged
+    through the flags) and bidirectional window calls (k_attn_win) at the
+    same time. Each context builds its own kernel arguments, so every result
+    matches the oracle and repeats bit for bit."""
+    import threading
+    from smol_genius_amd import runner
+    from smol_genius_amd.workloads import Bidir, Decode
+    print("two threads decode + bidirectional", flush=True)
+    cases = [
+        (Decode("t0", 16, 8, 128, [1025, 300, 700], 1e6, 0, seed=171), Bidir("b0", 4, 72, [0, 256, 512], seed=172)),
+        (Decode("t1", 8, 1, 256, [2000, 600], 1e4, 1, seed=173),
+         Bidir("b1", 6, 64, [0, 104, 208, 312], seed=174, in_bf16=False)),
+    ]
+    inputs = [(d.inputs(), b.inputs()) for d, b in cases]
+    wants = [(wo.decode(oracle, d, xd), wo.bidir(oracle, b, xb)) for (d, b), (xd, xb) in zip(cases, inputs)]
+    results, errors = {}, []
+    go = threading.Barrier(len(cases))
+
+    def worker(idx):
+        try:
+            (d, b), (xd, xb) = cases[idx], inputs[idx]
+            stream = torch.cuda.Stream()
+            with torch.cuda.stream(stream):
+                c = sa.Context(0, stream=stream.cuda_stream)
+                c.set_option(sa.OPT_DEC_SLABS, 1)  # the most splits per sequence
+                rd = runner.prepare(c, d, xd)
+                rb = runner.prepare(c, b, xb)
+                stream.synchronize()
+                go.wait()
+                outs = []
+                for _ in range(25):
+                    od = rd.step().clone()
+                    ob = rb.step().clone()
+                    outs.append((od, ob))
+                c.synchronize()
+                results[idx] = [(od.cpu().numpy(), ob.cpu().numpy()) for od, ob in outs]
+                c.close()
+        except Exception as e:  # reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(cases))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for idx, (want_d, want_b) in enumerate(wants):
+        first_d, first_b = results[idx][0]
+        assert_parity(first_d, want_d, "thread %d decode" % idx)
+        assert_parity(first_b, want_b, "thread %d bidirectional" % idx)
+        for od, ob in results[idx][1:]:
+            np.testing.assert_array_equal(od, first_d)
+            np.testing.assert_array_equal(ob, first_b)
+
+
+def test_decode_merge_timeout_reported(ctx, sa, oracle, wo, opts):
+    """A k_dec merger whose wait for its splits gives up writes NaN rows and
+    raises the context's merge flag: synchronize then fails with
+    SMOL_ATTN_ERR_TIMEOUT, and the next call is clean again. The give-up is
+    forced from the host (mergers wait for a flag value no split stores,
+    with a bound of 64 polls), so every kernel ends normally."""
+    from smol_genius_amd import runner
+    from smol_genius_amd.workloads import Decode
+    print("decode merge timeout", flush=True)
+    wl = Decode("t", 16, 8, 128, [1025, 300], 1e6, 0, seed=175)
+    x = wl.inputs()
+    if not ctx.get_option(sa.OPT_XCD_CHECK):
+        pytest.skip("workgroups do not follow the XCD round robin here, so k_dec does not split")
+    r = runner.prepare(ctx, wl, x)
+    ctx.synchronize()
+    opts(sa.OPT_DEC_SLABS, 1)
+    opts(sa.OPT_DEC_SPIN, 64)
+    opts(sa.OPT_FAULT_MERGE, 1)
+    r.step()
+    got = r.outputs()
+    print("NaN rows after the forced give-up:", int(np.isnan(got).any(axis=1).sum()), flush=True)
+    assert np.isnan(got).any(), "the merged rows of a timed-out merge are NaN"
+    with pytest.raises(sa.SmolAttnTimeoutError):
+        ctx.synchronize()
+    ctx.set_option(sa.OPT_FAULT_MERGE, 0)
+    r.step()
+    ctx.synchronize()  # the flag was cleared by the failed synchronize
+    assert_parity(r.outputs(), wo.decode(oracle, wl, x), "decode after a timed-out merge")
