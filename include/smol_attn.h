@@ -23,15 +23,19 @@
  * head h uses KV head h / (n_heads / n_kv_heads). Outputs are fp32.
  * Supported head_dim: 64, 72, 80, 96, 128, 256.
  *
- * Numerics: the softmax runs in fp32; the QK^T and PV products run on fp16
- * MFMA operands (bf16 inputs convert exactly). Prefill and bidirectional
- * calls stage Q (times scale * log2 e), K and V as fp16: a staged value that
- * is not finite or whose magnitude reaches 65520 raises the context's range
- * flag, and the next smol_attn_ctx_synchronize returns SMOL_ATTN_ERR_RANGE
- * (the affected outputs are not valid). Single-token decode has no such
- * limit (its cache operands are bf16, Q is split into bf16 hi + lo, and the
- * new key is scored in fp32). The reference-signature drop-ins rescale their
- * inputs by powers of two and repeat the call when the flag is raised.
+ * Numerics: the softmax runs in fp32. Prefill and bidirectional calls form
+ * QK^T from fp16 hi + lo parts of Q (times scale * log2 e) and of K
+ * (Khi.Qhi + Khi.Qlo + Klo.Qhi on the matrix cores, about 21 significant
+ * bits; bf16 cache rows and bf16 inputs without RoPE are exact in fp16 and
+ * have no lo part), and P.V from fp16 probabilities and fp16 V (bf16 inputs
+ * convert exactly). SMOL_OPT_QK_FP16 selects single fp16 Q and K operands
+ * instead. A staged value that is not finite or whose magnitude reaches
+ * 65520 raises the context's range flag, and the next
+ * smol_attn_ctx_synchronize returns SMOL_ATTN_ERR_RANGE (the affected
+ * outputs are not valid). Single-token decode has no such limit (its cache
+ * operands are bf16, Q is split into bf16 hi + lo, and the new key is scored
+ * in fp32). The reference-signature drop-ins rescale their inputs by powers
+ * of two and repeat the call when the flag is raised.
  * The KV cache stores post-RoPE K and V in bf16 (round to nearest even).
  * Keys written by a call are used by that same call at fp16 precision.
  *
@@ -128,7 +132,10 @@ SMOL_ATTN_API int smol_attn_ctx_timing_read(smol_attn_ctx *ctx, double *ms, int 
                                    * flag value no split writes, so it gives up after SMOL_OPT_DEC_SPIN
                                    * polls, writes NaN rows and synchronize returns
                                    * SMOL_ATTN_ERR_TIMEOUT; every kernel still ends normally */
-#define SMOL_OPT_COUNT 11
+#define SMOL_OPT_QK_FP16 11       /* 1: QK^T on single fp16 operands (Q and K each rounded to fp16:
+                                   * faster, within the bar for logits up to about sigma 1.4 on
+                                   * unit-variance rows); 0: fp16 hi + lo operands, see Numerics */
+#define SMOL_OPT_COUNT 12
 SMOL_ATTN_API int smol_attn_ctx_set_option(smol_attn_ctx *ctx, int option, int value);
 SMOL_ATTN_API int smol_attn_ctx_get_option(smol_attn_ctx *ctx, int option, int *value);
 

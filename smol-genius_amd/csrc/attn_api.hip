@@ -43,7 +43,7 @@ extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, h
                               hipEvent_t ev1);
 extern "C" int smol_launch_win(const WinParams *wp, int hd, int n_tiles, int max_len, hipStream_t st, hipEvent_t e0,
                                hipEvent_t e1);
-extern "C" int smol_win_max_keys(int hd);
+extern "C" int smol_win_max_keys(int hd, int in_dtype, int precise);
 extern "C" int smol_launch_to_bf16_trunc(const float *x, uint16_t *y, long long n, hipStream_t st);
 extern "C" int smol_launch_bf16_norm_rope(uint16_t *x, const float *w, float eps, const float *cos_t,
                                           const float *sin_t, int pos0, int seq, int H, int hd, hipStream_t st);
@@ -167,6 +167,7 @@ struct smol_attn_ctx {
     DevBuf desc;   /* device copy of the descriptor tables */
     std::vector<unsigned char> desc_last; /* host bytes of the last upload to `desc` */
     DevBuf qs, kf, vtf, part_o, part_ml, counters;
+    DevBuf kf_lo; /* fp16 lo part of the fresh K (precise QK^T) */
     DevBuf qs32; /* fp32 Q scratch of the decode kernel */
     DevBuf out32; /* fp32 result of a call whose output is bf16 */
     DevBuf dec_part; /* k_dec partial slots and flags */
@@ -358,7 +359,7 @@ extern "C" int smol_attn_ctx_destroy(smol_attn_ctx *ctx) {
     if (!ctx) return SMOL_ATTN_OK;
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
-    DevBuf *bufs[] = {&ctx->desc, &ctx->qs, &ctx->kf, &ctx->vtf, &ctx->part_o, &ctx->part_ml, &ctx->counters,
+    DevBuf *bufs[] = {&ctx->desc, &ctx->qs, &ctx->kf, &ctx->kf_lo, &ctx->vtf, &ctx->part_o, &ctx->part_ml, &ctx->counters,
                       &ctx->qs32, &ctx->out32, &ctx->dec_part};
     for (DevBuf *b : bufs)
         if (b->p) hipFree(b->p);
@@ -785,6 +786,7 @@ struct DecCall {
     std::vector<DecSeq> seqs;
     /* chunk mode: the pre-pass's fresh window and Q scratch */
     int fresh_pos0 = 0, fresh_row0 = 0, fcap = 0;
+    const _Float16 *kf_lo = nullptr; /* the fresh K's lo part (precise QK^T) */
     long long qs_head_stride = 0;
 };
 
@@ -950,6 +952,7 @@ static int run_decode(smol_attn_ctx *ctx, const CallShape &cs, const DecCall &dc
         dp.q_norm = cs.q_norm; dp.k_norm = cs.k_norm; dp.norm_eps = cs.norm_eps;
     } else {
         dp.kf = (const _Float16 *)ctx->kf.p; dp.vtf = (const _Float16 *)ctx->vtf.p; dp.fcap = dc.fcap;
+        dp.kf_lo = dc.kf_lo;
         dp.fresh_pos0 = dc.fresh_pos0; dp.fresh_row0 = dc.fresh_row0;
         dp.qs32 = (const float *)ctx->qs32.p; dp.qs_head_stride = dc.qs_head_stride;
     }
@@ -1014,6 +1017,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
      * split the rows, K/V shared through LDS, split-K across workgroups);
      * SMOL_OPT_PREFILL_KERNEL forces one where the keys allow it */
     const int pk = ctx->opt[SMOL_OPT_PREFILL_KERNEL];
+    const bool precise = ctx->opt[SMOL_OPT_QK_FP16] != 1;
     const bool fa = !cs.dec;
     bool fb = fa && hd <= 128 && pk != 2;
     if (fb) {
@@ -1032,21 +1036,27 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
         w = 2;
         rows_per = 64;
     } else if (fa) {
-        nt = (hd <= 128 && max_rows > 64) ? 2 : 1;
+        /* precise QK^T does not fit two row tiles into two waves per SIMD */
+        nt = (hd <= 128 && max_rows > 64 && !precise) ? 2 : 1;
         w = hd > 128 ? 1 : 2;
         rows_per = 64 * nt;
     }
     if (fa) plan_items(pl, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, true, fb);
 
-    /* workspace */
+    /* workspace; precise QK^T (the default) adds the lo parts of the fp16 Q
+     * scratch and of the fresh K */
     int rc;
     const size_t fcap = (size_t)std::max(pl.fresh_rows, SMOL_SLAB);
+    const size_t qs_elems = (size_t)cs.Hkv * std::max(pl.q_rows, 1) * hdp;
     if (cs.dec) {
-        if ((rc = dev_reserve(ctx->qs32, (size_t)cs.Hkv * std::max(pl.q_rows, 1) * hdp * 4, ctx->stream))) return rc;
+        if ((rc = dev_reserve(ctx->qs32, qs_elems * 4, ctx->stream))) return rc;
     } else {
-        if ((rc = dev_reserve(ctx->qs, (size_t)cs.Hkv * std::max(pl.q_rows, 1) * hdp * 2, ctx->stream))) return rc;
+        if ((rc = dev_reserve(ctx->qs, qs_elems * 2 * (precise ? 2 : 1), ctx->stream))) return rc;
     }
     if ((rc = dev_reserve(ctx->kf, (size_t)cs.Hkv * fcap * hd * 2, ctx->stream))) return rc;
+    if (precise && (rc = dev_reserve(ctx->kf_lo, (size_t)cs.Hkv * fcap * hd * 2, ctx->stream))) return rc;
+    _Float16 *const qs_lo = precise && !cs.dec ? (_Float16 *)ctx->qs.p + qs_elems : nullptr;
+    _Float16 *const kf_lo = precise ? (_Float16 *)ctx->kf_lo.p : nullptr;
     if ((rc = dev_reserve(ctx->vtf, (size_t)cs.Hkv * fcap * hd * 2, ctx->stream))) return rc;
     const size_t n_items = pl.items.size();
     if (fa) {
@@ -1118,6 +1128,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     pp.qs_head_stride = (long long)std::max(pl.q_rows, 1) * hdp;
     pp.kc = kc; pp.vtc = vtc; pp.c_slot_stride = slot_stride; pp.cap = cap;
     pp.kf = (_Float16 *)ctx->kf.p; pp.vtf = (_Float16 *)ctx->vtf.p; pp.fcap = (int)fcap;
+    pp.qs_lo = qs_lo; pp.kf_lo = kf_lo;
     pp.stage = cs.dec ? SMOL_STAGE_QF32 : SMOL_STAGE_F16;
     if (cs.dec) pp.qs32 = (float *)ctx->qs32.p;
     pp.blocks = (const PrepBlockB *)(dd + o_pblk);
@@ -1140,6 +1151,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
         dc.fresh_pos0 = b.fresh_pos0;
         dc.fresh_row0 = b.fresh_row0;
         dc.fcap = (int)fcap;
+        dc.kf_lo = kf_lo;
         dc.qs_head_stride = pp.qs_head_stride;
         return run_decode(ctx, cs, dc);
     }
@@ -1150,6 +1162,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     sp.qs_head_stride = pp.qs_head_stride;
     sp.kc = kc; sp.vtc = vtc; sp.c_slot_stride = slot_stride; sp.cap = cap;
     sp.kf = (const _Float16 *)ctx->kf.p; sp.vtf = (const _Float16 *)ctx->vtf.p; sp.fcap = (int)fcap;
+    sp.qs_lo = qs_lo; sp.kf_lo = kf_lo;
     sp.out = cs.out;
     sp.Hq = cs.Hq; sp.Hkv = cs.Hkv; sp.G = G;
     sp.window = cs.window;
@@ -1404,7 +1417,8 @@ extern "C" int smol_attn_bidirectional(smol_attn_ctx *ctx, const void *q, const 
             max_len = std::max(max_len, ws[w + 1] - ws[w]);
             n_tiles += (ws[w + 1] - ws[w] + 63) / 64;
         }
-        const int wmax = smol_win_max_keys(hd);
+        const bool precise = ctx->opt[SMOL_OPT_QK_FP16] != 1;
+        const int wmax = smol_win_max_keys(hd, dtype == SMOL_ATTN_BF16 ? SMOL_IN_BF16 : SMOL_IN_F32, precise ? 1 : 0);
         const int opt = ctx->opt[SMOL_OPT_BIDIR_WIN];
         if (opt >= 0 && wmax > 0 && max_len <= wmax && n_windows <= WIN_ARG_WINDOWS &&
             (long long)n_windows * n_heads * ((max_len + 63) / 64) + 8LL * ((max_len + 63) / 64) <= 0x7FFFFFFF) {
@@ -1429,6 +1443,7 @@ extern "C" int smol_attn_bidirectional(smol_attn_ctx *ctx, const void *q, const 
             wp.tpu = (max_len + rows - 1) / rows;
             wp.n_xcc = std::max(1, ctx->n_xcc);
             wp.range_flag = ctx->range_flag;
+            wp.precise = precise ? 1 : 0;
             memcpy(wp.ws, ws, (size_t)(n_windows + 1) * sizeof(int));
             const int mk = timing_begin(ctx, 1);
             rc = smol_launch_win(&wp, hd, (int)n_tiles, max_len, ctx->stream, mark_a(ctx, mk), mark_b(ctx, mk));

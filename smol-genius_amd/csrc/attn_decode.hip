@@ -214,6 +214,19 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
                 r.k[t][ks] = HD % 32 == 0 ? bload(rs, kbase, so + (unsigned)((4 * t * HD + 32 * ks) * 2))
                                           : bload(rs, vo_k[t][ks], so);
     };
+    /* chunk mode, a fresh slab: its K's fp16 lo part (zeros without one) */
+    auto issue_klo = [&](int k0, KRaw &r) __attribute__((always_inline)) {
+        const int kr = k0 - fresh_pos0 + p.fresh_row0;
+        const unsigned so = (unsigned)(kr / SMOL_SLAB) * SLAB_BYTES;
+        const bool has = !DIRECT && p.kf_lo != nullptr;
+        const rsrc_t rs = make_rsrc(has ? p.kf_lo + (long long)g * p.fcap * HD : nullptr, has && k0 < ke ? f_bytes : 0);
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++)
+                r.k[t][ks] = HD % 32 == 0 ? bload(rs, kbase, so + (unsigned)((4 * t * HD + 32 * ks) * 2))
+                                          : bload(rs, vo_k[t][ks], so);
+    };
     auto issue_v = [&](int k0, VRaw &r) __attribute__((always_inline)) {
         rsrc_t rs;
         unsigned so;
@@ -554,7 +567,7 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
     hi_min = __builtin_amdgcn_readfirstlane(hi_min);
 
     /* ---- S^T = K.Q^T of one slab: sacc[nr][t] ---- */
-    auto qk = [&](const KRaw &r, f4 (&sacc)[NR][2], auto fresh_tag) __attribute__((always_inline)) {
+    auto qk = [&](const KRaw &r, const KRaw &rl, f4 (&sacc)[NR][2], auto fresh_tag) __attribute__((always_inline)) {
         constexpr bool FRESH = decltype(fresh_tag)::value;
 #pragma unroll
         for (int t = 0; t < 2; t++) {
@@ -563,13 +576,15 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
                 f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int ks = 0; ks < KS; ks++) {
-                    /* the fresh slab's fp16 K as bf16 hi + lo (exact: 11 significant bits) */
+                    /* the fresh slab's K (fp16 hi + fp16 lo, exact in fp32)
+                     * as bf16 hi + lo: 16 significant bits */
                     b8 khs, kls;
                     if constexpr (FRESH) {
                         float kx[8];
                         const h8 k16 = *reinterpret_cast<const h8 *>(&r.k[t][ks]);
+                        const h8 kl16 = *reinterpret_cast<const h8 *>(&rl.k[t][ks]);
 #pragma unroll
-                        for (int i = 0; i < 8; i++) kx[i] = (float)k16[i];
+                        for (int i = 0; i < 8; i++) kx[i] = (float)k16[i] + (float)kl16[i];
                         split8(kx, khs, kls);
                     }
                     if constexpr (PACK) {
@@ -696,8 +711,15 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
     auto slab = [&](KRaw &kx, VRaw &vx) __attribute__((always_inline)) {
         f4 sacc[NR][2];
         const bool fr = !DIRECT && k0 >= fresh_pos0;
-        if (fr) qk(kx, sacc, std::true_type{});
-        else qk(kx, sacc, std::false_type{});
+        if (fr) {
+            /* the one or two fresh slabs of a chunk load their K lo here,
+             * next to use (the cache slabs carry none) */
+            KRaw kl;
+            issue_klo(k0, kl);
+            qk(kx, kl, sacc, std::true_type{});
+        } else {
+            qk(kx, kx, sacc, std::false_type{});
+        }
         issue_k(k0 + DEPTH * step, kx);
         if (fr) smpv(k0, sacc, vx, std::true_type{});
         else smpv(k0, sacc, vx, std::false_type{});

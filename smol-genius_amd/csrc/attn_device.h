@@ -138,6 +138,21 @@ __device__ __forceinline__ uint4 pack_h8(const float *v) {
     return *reinterpret_cast<uint4 *>(&h);
 }
 
+/* 8 values as fp16 hi + lo: hi = fp16(v) (nearest even), lo = fp16(v - hi).
+ * hi + lo carries about 22 significant bits of v (lo's own rounding; v - hi
+ * is exact in fp32), so a product on hi / lo operands reproduces an fp32
+ * product to about 2^-21 relative. */
+__device__ __forceinline__ void pack_h8_hilo(const float *v, uint4 &hi, uint4 &lo) {
+    h8 h, l;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        h[i] = (_Float16)v[i];
+        l[i] = (_Float16)(v[i] - (float)h[i]);
+    }
+    hi = *reinterpret_cast<uint4 *>(&h);
+    lo = *reinterpret_cast<uint4 *>(&l);
+}
+
 __device__ __forceinline__ void unpack_bf16x8(uint4 w, float *v) {
     const uint32_t a[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll

@@ -38,28 +38,36 @@
  * Softmax, lazy rescale and MFMA layouts as in k_attn_dec; each wave holds
  * whole rows, so no cross-wave combine is needed.
  */
-template <int HD>
+/* PREC (precise QK^T): a stage holds the K image twice, fp16 hi then fp16
+ * lo (zero for bf16 cache slabs, which fp16 holds exactly), then V^T. */
+template <int HD, bool PREC>
 struct FaGeom {
     static constexpr int KS = (HD + 31) / 32;
     static constexpr int DT = (HD + 15) / 16;
     static constexpr int HDP = KS * 32;
     static constexpr int KROW = HD <= 128 ? 256 : 512;
     static constexpr int K_BYTES = SMOL_SLAB * KROW;
+    static constexpr int KPARTS = PREC ? 2 : 1;
     static constexpr int V_BYTES = 16 * DT * 64;
-    static constexpr int STAGE = K_BYTES + V_BYTES;
+    static constexpr int STAGE = KPARTS * K_BYTES + V_BYTES;
     static constexpr int CK = SMOL_SLAB * HD / 8; /* 16-byte chunks in a K (or V^T) slab */
     static constexpr int PER = (CK + 255) / 256;  /* K (and V) chunks per thread */
 };
 
-template <int HD, int NT, int W>
+template <int HD, int NT, int W, bool PREC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) void k_attn_fa(SkParams p) {
-    using Gm = FaGeom<HD>;
+    using Gm = FaGeom<HD, PREC>;
     constexpr int KS = Gm::KS, DT = Gm::DT, HDP = Gm::HDP, KROW = Gm::KROW;
     constexpr int STAGE = Gm::STAGE, K_BYTES = Gm::K_BYTES, CK = Gm::CK, PER = Gm::PER;
     constexpr int ROWS = 4 * 16 * NT;
     constexpr unsigned SLAB_BYTES = SMOL_SLAB * HD * 2;
-    constexpr int NSTG = 4;                /* LDS stages: slabs i, i+1 read while i+2 is stored */
-    constexpr int SETS = W == 1 ? 4 : 2;   /* register sets of staged slabs in flight */
+    /* LDS stages: slabs i, i+1 read while i+2 is stored (PREC: three, the
+     * larger stages leave no room for a fourth) */
+    constexpr int NSTG = PREC ? 3 : 4;
+    constexpr int VOFF = Gm::KPARTS * K_BYTES; /* V^T within a stage */
+    /* register sets of staged slabs in flight (two for PREC at head_dim 256,
+     * whose K lo part would not leave registers for four) */
+    constexpr int SETS = W == 1 && !(PREC && HD > 128) ? 4 : 2;
     constexpr int MERGE_BYTES = (2 * SK_MERGE_MAX + 128) * 4;
     constexpr int SMEM = NSTG * STAGE > MERGE_BYTES ? NSTG * STAGE : MERGE_BYTES;
     const int tid = threadIdx.x;
@@ -79,6 +87,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
 
     /* this wave's rows: Q fragments, visible key ranges */
     h8 qf[NT][KS];
+    h8 qfl[PREC ? NT : 1][KS]; /* PREC: Q lo */
     int lo[NT], hi[NT];
     float m[NT], l[NT];
     f4 negm[NT];   /* -m (0 while m = -inf): the accumulator input of S = K.Q^T - m */
@@ -104,10 +113,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
         negm[nt] = f4{0.f, 0.f, 0.f, 0.f};
         thr[nt] = -INFINITY;
         {
-            const _Float16 *qrow =
-                p.qs + (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid ? r : 0)) * HDP;
+            const long long qoff = (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid ? r : 0)) * HDP;
+            const _Float16 *qrow = p.qs + qoff;
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) qf[nt][ks] = valid ? load_h8(qrow + 32 * ks + 8 * j) : zero_h8();
+            if constexpr (PREC) {
+                const _Float16 *qrl = p.qs_lo + qoff;
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) qfl[nt][ks] = valid ? load_h8(qrl + 32 * ks + 8 * j) : zero_h8();
+            }
         }
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) o[nt][dt] = f4{0.f, 0.f, 0.f, 0.f};
@@ -128,6 +142,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
         rv_c = make_rsrc(p.vtc + cb, (long long)p.cap * HD * 2);
     }
     const rsrc_t rk_f = make_rsrc(p.kf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
+    /* the fresh K's lo part; a cache slab's lo part reads zeros (empty range) */
+    const rsrc_t rkl_f = PREC ? make_rsrc(p.kf_lo + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2) : rk_f;
+    const rsrc_t r_none = make_rsrc(nullptr, 0);
     const rsrc_t rv_f = make_rsrc(p.vtf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
 
     /* this thread's staging chunks: global byte offset within the slab and LDS slot */
@@ -141,7 +158,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
         const int f = (kr & 3) | (((kr >> 3) & 3) << 2);
         lk_off[e] = (unsigned)(kr * KROW + 16 * (cb ^ f));
         const int d = q >> 2, jj = q & 3;
-        lv_off[e] = (unsigned)(K_BYTES + d * 64 + 16 * (jj ^ ((d >> 1) & 3)));
+        lv_off[e] = (unsigned)(VOFF + d * 64 + 16 * (jj ^ ((d >> 1) & 3)));
         g_off[e] = c_ok[e] ? (unsigned)(q * 16) : OOB_OFF;
     }
     /* this lane's fragment addresses within a stage */
@@ -149,10 +166,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
     unsigned kfo[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) kfo[ks] = (unsigned)(kt_row * KROW + 16 * ((4 * ks + j) ^ c));
-    const unsigned vfo = (unsigned)(K_BYTES + c * 64 + 16 * (j ^ ((c >> 1) & 3)));
+    const unsigned vfo = (unsigned)(VOFF + c * 64 + 16 * (j ^ ((c >> 1) & 3)));
 
     struct Stg {
         uint4 k[PER], v[PER];
+        uint4 kl[PREC ? PER : 1]; /* PREC: K lo */
         bool bf; /* bf16 cache slab (widen to fp16 when storing) */
     };
     auto issue = [&](int k0, Stg &s) __attribute__((always_inline)) {
@@ -162,6 +180,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
         const rsrc_t rk = fr ? rk_f : rk_c, rv = fr ? rv_f : rv_c;
 #pragma unroll
         for (int e = 0; e < PER; e++) s.k[e] = bload(rk, g_off[e], so);
+        if constexpr (PREC) {
+            const rsrc_t rkl = fr ? rkl_f : r_none;
+#pragma unroll
+            for (int e = 0; e < PER; e++) s.kl[e] = bload(rkl, g_off[e], so);
+        }
 #pragma unroll
         for (int e = 0; e < PER; e++) s.v[e] = bload(rv, g_off[e], so);
         s.bf = !fr;
@@ -181,6 +204,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
                 vw = *reinterpret_cast<const uint4 *>(&vh);
             }
             *reinterpret_cast<uint4 *>(base + lk_off[e]) = kw;
+            if constexpr (PREC) *reinterpret_cast<uint4 *>(base + lk_off[e] + K_BYTES) = s.kl[e];
             *reinterpret_cast<uint4 *>(base + lv_off[e]) = vw;
         }
     };
@@ -188,20 +212,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
         const uint4 w = *reinterpret_cast<const uint4 *>(smem + stage * STAGE + off);
         return *reinterpret_cast<const h8 *>(&w);
     };
-    /* S^T - m = K.Q^T - m of the slab in `stage` (raw S with a softcap) */
+    /* S^T - m = K.Q^T - m of the slab in `stage` (raw S with a softcap);
+     * PREC: Khi.Qhi + Khi.Qlo + Klo.Qhi */
     const bool capped = p.cap2 > 0.0f;
     auto qk = [&](int stage, f4 (&sacc)[NT][2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-            h8 kfr[KS];
+            h8 kfr[KS], kfl[PREC ? KS : 1];
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) kfr[ks] = lds_h8(stage, kfo[ks] + t * 4 * KROW);
+            if constexpr (PREC) {
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) kfl[ks] = lds_h8(stage, kfo[ks] + t * 4 * KROW + K_BYTES);
+            }
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 f4 acc = capped ? f4{0.f, 0.f, 0.f, 0.f} : negm[nt];
 #pragma unroll
-                for (int ks = 0; ks < KS; ks++)
+                for (int ks = 0; ks < KS; ks++) {
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kfr[ks], qf[nt][ks], acc, 0, 0, 0);
+                    if constexpr (PREC) {
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kfr[ks], qfl[nt][ks], acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kfl[ks], qf[nt][ks], acc, 0, 0, 0);
+                    }
+                }
                 sacc[nt][t] = acc;
             }
         }
@@ -251,34 +285,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
             }
         }
     };
-    /* P = exp2(S - m) as fp16, row sums */
-    auto expo = [&](const float (&sv)[NT][8], h8 (&pf)[NT]) __attribute__((always_inline)) {
+    /* P = exp2(S - m) as fp16 (PREC: hi [0] + lo [1]), row sums */
+    constexpr int NP = PREC ? 2 : 1;
+    auto expo = [&](const float (&sv)[NT][8], h8 (&pf)[NP][NT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             float pe[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 pe[e] = __builtin_amdgcn_exp2f(sv[nt][e]);
-                pf[nt][e] = (_Float16)pe[e];
+                const _Float16 ph = (_Float16)pe[e];
+                pf[0][nt][e] = ph;
+                if constexpr (PREC) pf[1][nt][e] = (_Float16)(pe[e] - (float)ph);
             }
             l[nt] += ((pe[0] + pe[1]) + (pe[2] + pe[3])) + ((pe[4] + pe[5]) + (pe[6] + pe[7]));
         }
     };
-    auto pv = [&](int stage, const h8 (&pf)[NT]) __attribute__((always_inline)) {
+    auto pv = [&](int stage, const h8 (&pf)[NP][NT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) {
             const h8 vfr = lds_h8(stage, vfo + dt * 1024);
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++)
-                o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vfr, pf[nt], o[nt][dt], 0, 0, 0);
+            for (int nt = 0; nt < NT; nt++) {
+                o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vfr, pf[0][nt], o[nt][dt], 0, 0, 0);
+                if constexpr (PREC) o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vfr, pf[1][nt], o[nt][dt], 0, 0, 0);
+            }
         }
     };
 
     /* The item's n slabs are walked in a rotated order (slab (i + rot) mod n
      * at step i; the softmax does not depend on the order), so the
      * workgroups of one head, which start together, read different slabs.
-     * Slab i sits in LDS stage i % 4 from the barrier that ends step i-2 to
-     * the one that ends step i. Step i: softmax front of slab i; then its
+     * Slab i sits in LDS stage i % NSTG from the barrier that ends step i-2
+     * to the one that ends step i (with three stages, slab i+2 goes into the
+     * stage of slab i-1, whose last read, step i-1, precedes that barrier). Step i: softmax front of slab i; then its
      * exponentials alongside S of slab i+1 (MFMA and VALU work of the same
      * wave with no dependence between them); then P.V of slab i; then slab
      * i+2 is stored from its register set, which is refilled with slab
@@ -304,17 +344,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
         __syncthreads();
         f4 sa[NT][2], sb[NT][2];
         qk(0, sa);
-        /* u = i % 4, compile-time in each unrolled step */
+        /* u = i % 4, compile-time in each unrolled step (the register sets);
+         * the stage of slab i is i % NSTG */
         auto step = [&](int i, auto u_tag, f4 (&scur)[NT][2], f4 (&snext)[NT][2]) __attribute__((always_inline)) {
             constexpr int u = decltype(u_tag)::value;
+            const int sg = NSTG == 4 ? (i & 3) : i % NSTG;
+            const int sg1 = sg + 1 == NSTG ? 0 : sg + 1, sg2 = sg1 + 1 == NSTG ? 0 : sg1 + 1;
             float sv[NT][8];
-            h8 pf[NT];
+            h8 pf[NP][NT];
             front(slab_k(i), scur, sv);
-            qk((u + 1) & 3, snext);
+            qk(sg1, snext);
             expo(sv, pf);
-            pv(u, pf);
+            pv(sg, pf);
             Stg &s2 = st[(u + 2) % SETS];
-            store(s2, (u + 2) & 3);
+            store(s2, sg2);
             issue(slab_k(i + 2 + SETS), s2);
             __syncthreads();
         };
@@ -396,22 +439,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
 }
 
 /* ev0 / ev1 (may be null): events recorded around the kernel alone */
+/* precise QK^T when the Q scratch has its lo part (not built for two row
+ * tiles at two waves per SIMD, whose registers it would not fit) */
 template <int HD, int NT, int W>
-static void launch_fa_v(const SkParams *sp, dim3 grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
-    hipExtLaunchKernelGGL((k_attn_fa<HD, NT, W>), grid, dim3(256), 0, st, ev0, ev1, 0, *sp);
+static int launch_fa_v(const SkParams *sp, dim3 grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    if (sp->qs_lo) {
+        if constexpr (NT == 2 && W == 2) return -1;
+        else hipExtLaunchKernelGGL((k_attn_fa<HD, NT, W, true>), grid, dim3(256), 0, st, ev0, ev1, 0, *sp);
+    } else {
+        hipExtLaunchKernelGGL((k_attn_fa<HD, NT, W, false>), grid, dim3(256), 0, st, ev0, ev1, 0, *sp);
+    }
+    return 0;
 }
 
 /* w: waves per SIMD the kernel is built for (2 with fewer staged slabs) */
 template <int HD>
 static int launch_fa_hd(const SkParams *sp, int n_items, int nt, int w, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     const dim3 grid(n_items * sp->Hkv);
-    if (nt == 1 && w == 1) launch_fa_v<HD, 1, 1>(sp, grid, st, e0, e1);
+    int rc = -1;
+    if (nt == 1 && w == 1) rc = launch_fa_v<HD, 1, 1>(sp, grid, st, e0, e1);
     else if constexpr (HD <= 128) { /* two tiles or two waves per SIMD fit the registers */
-        if (nt == 1 && w == 2) launch_fa_v<HD, 1, 2>(sp, grid, st, e0, e1);
-        else if (nt == 2 && w == 1) launch_fa_v<HD, 2, 1>(sp, grid, st, e0, e1);
-        else if (nt == 2 && w == 2) launch_fa_v<HD, 2, 2>(sp, grid, st, e0, e1);
-        else return -1;
-    } else return -1;
+        if (nt == 1 && w == 2) rc = launch_fa_v<HD, 1, 2>(sp, grid, st, e0, e1);
+        else if (nt == 2 && w == 1) rc = launch_fa_v<HD, 2, 1>(sp, grid, st, e0, e1);
+        else if (nt == 2 && w == 2) rc = launch_fa_v<HD, 2, 2>(sp, grid, st, e0, e1);
+    }
+    if (rc) return rc;
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 

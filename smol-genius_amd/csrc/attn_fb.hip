@@ -37,18 +37,22 @@
  * are waited for where the schedule needs them and one barrier publishes
  * them.
  */
-/* WPG waves per key group, each holding NT 16-row tiles of the 64-row item */
-template <int HD, int WPG>
+/* WPG waves per key group, each holding NT 16-row tiles of the 64-row item.
+ * PREC (precise QK^T): a stage holds the K image twice, fp16 hi then fp16 lo
+ * (the same layout), then V^T; the larger stage leaves room for three stages
+ * per group instead of five. */
+template <int HD, int WPG, bool PREC>
 struct FbGeom {
     static constexpr int KS = (HD + 31) / 32;
     static constexpr int DT = (HD + 15) / 16;
     static constexpr int HDP = KS * 32;
     static constexpr int KROW = 256;
     static constexpr int K_BYTES = SMOL_SLAB * KROW;
+    static constexpr int KPARTS = PREC ? 2 : 1;
     static constexpr int V_BYTES = 16 * DT * 64;
-    static constexpr int STAGE = (K_BYTES + V_BYTES + 1024 * WPG - 1) / (1024 * WPG) * (1024 * WPG);
+    static constexpr int STAGE = (KPARTS * K_BYTES + V_BYTES + 1024 * WPG - 1) / (1024 * WPG) * (1024 * WPG);
     static constexpr int NDMA = STAGE / (1024 * WPG); /* DMA instructions per wave per slab */
-    static constexpr int NSTG = 2 * 5 * STAGE <= 160 * 1024 ? 5 : 4;
+    static constexpr int NSTG = PREC ? 3 : (2 * 5 * STAGE <= 160 * 1024 ? 5 : 4);
     static constexpr int GROUP_BYTES = NSTG * STAGE;
 };
 
@@ -58,17 +62,18 @@ struct FbGeom {
  * halves the LDS reads per flop. One MFMA pipe per SIMD is kept busy by a
  * single wave (measured: 16x16x32 f16 MFMAs with independent accumulators
  * issue at the same rate from one wave per SIMD as from two). */
-template <int HD, int NT, bool CAP>
+template <int HD, int NT, bool CAP, bool PREC>
 __global__ __launch_bounds__(NT == 1 ? 512 : 256)
 __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_attn_fb(SkParams p) {
     constexpr int WPG = 4 / NT;
-    using Gm = FbGeom<HD, WPG>;
+    using Gm = FbGeom<HD, WPG, PREC>;
     constexpr int KS = Gm::KS, DT = Gm::DT, HDP = Gm::HDP, KROW = Gm::KROW;
     constexpr int K_BYTES = Gm::K_BYTES, STAGE = Gm::STAGE, NDMA = Gm::NDMA, NSTG = Gm::NSTG;
     constexpr unsigned SLAB_BYTES = SMOL_SLAB * HD * 2;
     static_assert(HD <= 128, "k_attn_fb covers head_dim <= 128");
     static_assert(2 * Gm::GROUP_BYTES <= 160 * 1024, "LDS");
     static_assert(NSTG >= 3, "the step pipeline keeps three slabs resident");
+    static_assert(!PREC || K_BYTES % (1024 * WPG) == 0, "each DMA instruction of a wave lands in one part");
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = wave / WPG, wg = wave % WPG;
@@ -105,19 +110,25 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     /* DMA geometry: region q = wg + WPG e of a stage; lane offsets within
      * the slab. The first transfers go out before anything else is set up. */
     const rsrc_t rk = make_rsrc(p.kf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
+    const rsrc_t rkl = PREC ? make_rsrc(p.kf_lo + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2) : rk;
     const rsrc_t rv = make_rsrc(p.vtf + (long long)g * p.fcap * HD, (long long)p.fcap * HD * 2);
+    /* region q of a stage: K (hi), with PREC then K lo, then V^T; the part
+     * of each of this wave's regions is the same in every wave (the K parts
+     * are whole multiples of WPG regions) */
     unsigned d_off[NDMA];
-    bool d_isk[NDMA];
+    int d_part[NDMA]; /* 0: K, 1: K lo, 2: V^T */
 #pragma unroll
     for (int e = 0; e < NDMA; e++) {
         const int q = wg + WPG * e;
-        d_isk[e] = q * 1024 < K_BYTES;
-        if (d_isk[e]) {
-            const int kr = q * 4 + (lane >> 4), slot = lane & 15;
+        const int kparts_bytes = Gm::KPARTS * K_BYTES;
+        d_part[e] = q * 1024 < K_BYTES ? 0 : q * 1024 < kparts_bytes ? 1 : 2;
+        if (d_part[e] < 2) {
+            const int qk = d_part[e] == 0 ? q : q - K_BYTES / 1024;
+            const int kr = qk * 4 + (lane >> 4), slot = lane & 15;
             const int cb = slot ^ ((kr & 3) | (((kr >> 3) & 3) << 2));
             d_off[e] = cb < HD / 8 ? (unsigned)((kr * HD + cb * 8) * 2) : OOB_OFF;
         } else {
-            const int d = (q * 1024 - K_BYTES) / 64 + (lane >> 2), slot = lane & 3;
+            const int d = (q * 1024 - kparts_bytes) / 64 + (lane >> 2), slot = lane & 3;
             const int jj = slot ^ ((d >> 1) & 3);
             d_off[e] = d < HD ? (unsigned)((d * SMOL_SLAB + jj * 8) * 2) : OOB_OFF;
         }
@@ -127,18 +138,21 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
         const unsigned so = (unsigned)(kr / SMOL_SLAB) * SLAB_BYTES;
 #pragma unroll
         for (int e = 0; e < NDMA; e++)
-            dma_1k(d_isk[e] ? rk : rv, d_off[e], so,
+            dma_1k(d_part[e] == 0 ? rk : d_part[e] == 1 ? rkl : rv, d_off[e], so,
                    __builtin_amdgcn_readfirstlane(lds_group + stage * STAGE + (wg + WPG * e) * 1024));
     };
-    /* the prologue stages three slabs; the steps bring the rest in pairs */
+    /* the prologue stages three slabs (PREC: two); the steps bring the rest
+     * in pairs (PREC: one a step) */
+    constexpr int PRO = PREC ? 2 : 3;
 #pragma unroll
-    for (int q = 0; q < 3; q++) dma(slab_k(q), q);
+    for (int q = 0; q < PRO; q++) dma(slab_k(q), q);
 
     /* rows of this wave (the same in both groups): tile nt holds rows
      * 16 (wg NT + nt) + c of the item */
     int lo[NT], hi[NT];
     bool valid[NT];
     h8 qf[NT][KS];
+    h8 qfl[PREC ? NT : 1][KS]; /* PREC: Q lo */
     int lo_max = -(1 << 30), hi_min = 1 << 30;
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
@@ -154,10 +168,15 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
         hi[nt] = valid[nt] ? rh : (1 << 30);
         lo_max = max(lo_max, lo[nt]);
         hi_min = min(hi_min, hi[nt]);
-        const _Float16 *qrow =
-            p.qs + (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid[nt] ? r : 0)) * HDP;
+        const long long qoff = (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid[nt] ? r : 0)) * HDP;
+        const _Float16 *qrow = p.qs + qoff;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) qf[nt][ks] = valid[nt] ? load_h8(qrow + 32 * ks + 8 * j) : zero_h8();
+        if constexpr (PREC) {
+            const _Float16 *qrl = p.qs_lo + qoff;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) qfl[nt][ks] = valid[nt] ? load_h8(qrl + 32 * ks + 8 * j) : zero_h8();
+        }
     }
 #pragma unroll
     for (int sh = 1; sh < 64; sh <<= 1) {
@@ -170,9 +189,11 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     float m[NT], l[NT], thr[NT];
     f4 negm[NT];
     f4 o[NT][DT];
-    /* the row sums on the matrix cores: one more MFMA per step against a
-     * fragment of ones (every element of lsum is the row's sum of its fp16
-     * probabilities, the same weights the P.V product uses) */
+    /* the row sums: without PREC on the matrix cores, one more MFMA per step
+     * against a fragment of ones (every element of lsum is the row's sum of
+     * its fp16 probabilities, the same weights the P.V product uses); with
+     * PREC (P = Phi + Plo, about 22 bits) in fp32 on the vector ALU, each
+     * lane summing its own keys (l), reduced over the row's lanes at the end */
     f4 lsum[NT];
     h8 ones;
 #pragma unroll
@@ -180,6 +201,7 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         m[nt] = -INFINITY;
+        l[nt] = 0.0f;
         lsum[nt] = f4{0.f, 0.f, 0.f, 0.f};
         thr[nt] = -INFINITY;
         negm[nt] = f4{0.f, 0.f, 0.f, 0.f};
@@ -191,11 +213,12 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     unsigned kfo[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) kfo[ks] = (unsigned)(kt_row * KROW + 16 * ((4 * ks + j) ^ c));
-    const unsigned vfo = (unsigned)(K_BYTES + c * 64 + 16 * (j ^ ((c >> 1) & 3)));
+    const unsigned vfo = (unsigned)(Gm::KPARTS * K_BYTES + c * 64 + 16 * (j ^ ((c >> 1) & 3)));
     auto lds_h8 = [&](int stage, unsigned off) __attribute__((always_inline)) -> h8 {
         const uint4 w = *reinterpret_cast<const uint4 *>(gbase + stage * STAGE + off);
         return *reinterpret_cast<const h8 *>(&w);
     };
+    /* K fragments of a slab (hi; PREC reads the lo part inside qk) */
     auto read_k = [&](int stage, h8 (&kf)[2][KS]) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < 2; t++)
@@ -206,27 +229,72 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) vf[dt] = lds_h8(stage, vfo + dt * 1024);
     };
-    /* S^T = K.Q^T, less the running max m (raw S with a softcap) */
-    auto qk = [&](const h8 (&kf)[2][KS], f4 (&sacc)[NT][2]) __attribute__((always_inline)) {
+    /* S^T = K.Q^T, less the running max m (raw S with a softcap); PREC:
+     * Khi.Qhi + Khi.Qlo, then Klo.Qhi (the Klo.Qlo term is below 2^-21 of
+     * S): the K lo fragments are read from `stage` into the registers of
+     * the hi ones once the hi products are issued, which keeps one slab's
+     * fragments live instead of two, and the hi products cover the reads */
+    auto qk = [&](h8 (&kf)[2][KS], int stage, f4 (&sacc)[NT][2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 f4 acc = CAP ? f4{0.f, 0.f, 0.f, 0.f} : negm[nt];
 #pragma unroll
-                for (int ks = 0; ks < KS; ks++)
+                for (int ks = 0; ks < KS; ks++) {
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t][ks], qf[nt][ks], acc, 0, 0, 0);
+                    if constexpr (PREC) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t][ks], qfl[nt][ks], acc, 0, 0, 0);
+                }
                 sacc[nt][t] = acc;
             }
+        if constexpr (PREC) {
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) kf[t][ks] = lds_h8(stage, kfo[ks] + t * 4 * KROW + K_BYTES);
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    f4 acc = sacc[nt][t];
+#pragma unroll
+                    for (int ks = 0; ks < KS; ks++)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t][ks], qf[nt][ks], acc, 0, 0, 0);
+                    sacc[nt][t] = acc;
+                }
+        }
     };
-    auto pv = [&](const h8 (&vf)[DT], const h8 (&pf)[NT]) __attribute__((always_inline)) {
+    /* P fragments: [0] fp16 P (hi), [1] its lo part (PREC) */
+    constexpr int NP = PREC ? 2 : 1;
+    auto pv = [&](const h8 (&vf)[DT], const h8 (&pf)[NP][NT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++)
-                o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pf[nt], o[nt][dt], 0, 0, 0);
+            for (int nt = 0; nt < NT; nt++) {
+                o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pf[0][nt], o[nt][dt], 0, 0, 0);
+                if constexpr (PREC) o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pf[1][nt], o[nt][dt], 0, 0, 0);
+            }
+        if constexpr (!PREC) {
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) lsum[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[nt], lsum[nt], 0, 0, 0);
+            for (int nt = 0; nt < NT; nt++)
+                lsum[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[0][nt], lsum[nt], 0, 0, 0);
+        }
+    };
+    /* P = exp2(S - m) of one row tile as fp16 (PREC: hi + lo, and the fp32
+     * sum of the lane's probabilities in psum) */
+    auto p_frag = [&](const f4 (&s)[2], float sh, h8 (&pf)[NP][NT], int nt, float &psum) __attribute__((always_inline)) {
+        float ps = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float pe = __builtin_amdgcn_exp2f(s[e >> 2][e & 3] - sh);
+            const _Float16 ph = (_Float16)pe;
+            pf[0][nt][e] = ph;
+            if constexpr (PREC) {
+                pf[1][nt][e] = (_Float16)(pe - (float)ph);
+                ps += pe;
+            }
+        }
+        psum = ps;
     };
     /* softcap (raw S -> capped S - m), then the mask of a step that is not
      * wholly inside every row's key range: lane (c, j) holds keys
@@ -255,26 +323,27 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     };
     /* P = exp2(S - m) as fp16, assuming no row's max passes its threshold;
      * returns whether one does (then the rare path below redoes it) */
-    auto expo = [&](const f4 (&s)[NT][2], h8 (&pf)[NT]) __attribute__((always_inline)) -> bool {
+    auto expo = [&](const f4 (&s)[NT][2], h8 (&pf)[NP][NT], float (&psum)[NT]) __attribute__((always_inline)) -> bool {
         bool hit = false;
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++)
+        for (int nt = 0; nt < NT; nt++) {
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                hit |= s[nt][e >> 2][e & 3] > thr[nt];
-                pf[nt][e] = (_Float16)__builtin_amdgcn_exp2f(s[nt][e >> 2][e & 3]);
-            }
+            for (int e = 0; e < 8; e++) hit |= s[nt][e >> 2][e & 3] > thr[nt];
+            p_frag(s[nt], 0.0f, pf, nt, psum[nt]);
+        }
         /* the probabilities are computed here, next to this step's MFMAs,
          * and not sunk into the branch after it (the rare path redoes them) */
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) asm volatile("" : "+v"(pf[nt]));
+        for (int q = 0; q < NP; q++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) asm volatile("" : "+v"(pf[q][nt]));
         return __any(hit);
     };
     /* Rare path (a row's max passed its threshold): move m to the row max,
      * redo P, and rescale what was accumulated against the old m: O and the
      * row sums (after the P.V of the previous slab, issued earlier in the
      * step) and S of the next slab (computed against the old m). */
-    auto rescale = [&](f4 (&s)[NT][2], h8 (&pf)[NT], f4 (&snext)[NT][2]) __attribute__((always_inline)) {
+    auto rescale = [&](f4 (&s)[NT][2], h8 (&pf)[NP][NT], f4 (&snext)[NT][2], float (&psum)[NT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             const float mx = row_max4(fmaxf(fmaxf(fmaxf(s[nt][0][0], s[nt][0][1]), fmaxf(s[nt][0][2], s[nt][0][3])),
@@ -286,12 +355,12 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
 #pragma unroll
             for (int dt = 0; dt < DT; dt++) o[nt][dt] *= alpha;
             lsum[nt] *= alpha;
+            l[nt] *= alpha;
             m[nt] = m_new;
             const float mu = m_new == -INFINITY ? 0.0f : m_new;
             negm[nt] = f4{-mu, -mu, -mu, -mu};
             thr[nt] = m_new == -INFINITY ? -INFINITY : LAZY_T;
-#pragma unroll
-            for (int e = 0; e < 8; e++) pf[nt][e] = (_Float16)__builtin_amdgcn_exp2f(s[nt][e >> 2][e & 3] - sh);
+            p_frag(s[nt], sh, pf, nt, psum[nt]);
             if constexpr (!CAP) {
 #pragma unroll
                 for (int t = 0; t < 2; t++) snext[nt][t] -= sh;
@@ -315,7 +384,11 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
      * to a step. Steps past the group's own slab count (the second group may
      * have one fewer, or none) keep the reads, transfers and barriers and
      * mask every key. */
-    static_assert(NSTG == 5, "the transfer schedule is built for five stages");
+    /* PREC (three stages): step i brings slab i+2 into the stage of slab
+     * i-1, whose last read (its V^T, step i-1) precedes the barrier ending
+     * step i-1, and every step ends in a barrier after vmcnt(0), so the
+     * slab has landed before step i+1 reads its K. */
+    static_assert(PREC ? NSTG == 3 : NSTG == 5, "the transfer schedules are built for five stages (three: PREC)");
     const int steps = n0;
     /* Every transfer of the prologue (and Q) has landed before the first
      * barrier. Counted waits (all but the last slabs' transfers) are not used
@@ -325,13 +398,15 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     f4 sa[NT][2], sb[NT][2];
-    h8 kf[2][KS], vfa[DT], vfb[DT], pfa[NT], pfb[NT];
+    h8 kf[2][KS], vfa[DT], vfb[DT], pfa[NP][NT], pfb[NP][NT];
     read_k(0, kf);
-    qk(kf, sa);
+    qk(kf, 0, sa);
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) vfa[dt] = zero_h8();
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++) pfa[nt] = zero_h8();
+    for (int q = 0; q < NP; q++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) pfa[q][nt] = zero_h8();
     int st_k = 1, st_v = 0; /* stages of slabs i+1 and i */
     auto step = [&](int i, bool odd, f4 (&scur)[NT][2], f4 (&snext)[NT][2], auto &vprev, auto &vnow, auto &pprev,
                     auto &pnow) __attribute__((always_inline)) {
@@ -340,7 +415,10 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
         const bool full = act && k0 >= lo_max && k0 + SMOL_SLAB <= hi_min;
         read_k(st_k, kf);
         read_v(st_v, vnow);
-        if (!odd) { /* slab 'steps' (K read in the last step, its S unused) and later ones are not staged */
+        /* slab 'steps' (K read in the last step, its S unused) and later ones are not staged */
+        if constexpr (PREC) {
+            if (i + 2 < steps) dma(slab_k(i + 2), (i + 2) % NSTG);
+        } else if (!odd) {
             if (i + 3 < steps) dma(slab_k(i + 3), (i + 3) % NSTG);
             if (i + 4 < steps) dma(slab_k(i + 4), (i + 4) % NSTG);
         }
@@ -352,13 +430,19 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
         pv(vprev, pprev);
         __builtin_amdgcn_sched_barrier(0);
         prep_s(k0, act, !full, scur);
-        const bool hit = expo(scur, pnow);
-        qk(kf, snext);
-        if (hit) rescale(scur, pnow, snext);
+        float psum[NT];
+        const bool hit = expo(scur, pnow, psum);
+        qk(kf, st_k, snext);
+        if (hit) rescale(scur, pnow, snext, psum);
+        if constexpr (PREC) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) l[nt] += psum[nt];
+        }
         /* only odd steps end in a barrier: it publishes the pair issued by
          * the step before, and the even step after it refills the stages of
-         * slabs i-1 and i, whose last reads (steps i-1 and i) it orders */
-        if (odd) {
+         * slabs i-1 and i, whose last reads (steps i-1 and i) it orders
+         * (PREC: every step, for its one slab) */
+        if (PREC || odd) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
         }
@@ -377,7 +461,7 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
         pv(vfa, pfa);
     }
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++) l[nt] = lsum[nt][0];
+    for (int nt = 0; nt < NT; nt++) l[nt] = PREC ? row_sum4(l[nt]) : lsum[nt][0];
 
     /* merge: group 1 hands its state to group 0 through LDS (lane-wise: the
      * two waves wg of the groups hold the same rows in the same lanes), one
@@ -420,19 +504,29 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     } /* items */
 }
 
+template <int HD, bool PREC>
+static int launch_fb_v(const SkParams *sp, dim3 grid, int nt, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+    const bool cap = sp->cap2 > 0.0f;
+    if (nt == 1) {
+        if (cap) hipExtLaunchKernelGGL((k_attn_fb<HD, 1, true, PREC>), grid, dim3(512), 0, st, e0, e1, 0, *sp);
+        else hipExtLaunchKernelGGL((k_attn_fb<HD, 1, false, PREC>), grid, dim3(512), 0, st, e0, e1, 0, *sp);
+    } else if (nt == 2) {
+        if (cap) hipExtLaunchKernelGGL((k_attn_fb<HD, 2, true, PREC>), grid, dim3(256), 0, st, e0, e1, 0, *sp);
+        else hipExtLaunchKernelGGL((k_attn_fb<HD, 2, false, PREC>), grid, dim3(256), 0, st, e0, e1, 0, *sp);
+    } else return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+/* precise QK^T (fp16 hi + lo operands) when the Q scratch has its lo part */
 template <int HD>
 static int launch_fb_hd(const SkParams *sp, int n_items, int nt, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     const int n_wg = sp->n_wg > 0 ? sp->n_wg : n_items; /* workgroups per kv head: the heads of the lists */
     const dim3 grid(n_wg * sp->Hkv);
-    const bool cap = sp->cap2 > 0.0f;
-    if (nt == 1) {
-        if (cap) hipExtLaunchKernelGGL((k_attn_fb<HD, 1, true>), grid, dim3(512), 0, st, e0, e1, 0, *sp);
-        else hipExtLaunchKernelGGL((k_attn_fb<HD, 1, false>), grid, dim3(512), 0, st, e0, e1, 0, *sp);
-    } else if (nt == 2) {
-        if (cap) hipExtLaunchKernelGGL((k_attn_fb<HD, 2, true>), grid, dim3(256), 0, st, e0, e1, 0, *sp);
-        else hipExtLaunchKernelGGL((k_attn_fb<HD, 2, false>), grid, dim3(256), 0, st, e0, e1, 0, *sp);
-    } else return -1;
-    return hipGetLastError() == hipSuccess ? 0 : -3;
+    if (sp->qs_lo) {
+        if (!sp->kf_lo) return -1;
+        return launch_fb_v<HD, true>(sp, grid, nt, st, e0, e1);
+    }
+    return launch_fb_v<HD, false>(sp, grid, nt, st, e0, e1);
 }
 
 /* k_attn_fb: one 64-row tile per item, every key in the fresh buffers; nt

@@ -12,9 +12,13 @@
  *              that share their 32-key slab), same two layouts with `fcap`
  *              rows; attention over a call's own keys uses these, so a key
  *              rotated in fp32 is never read back through bf16 rounding.
+ *              With precise QK^T the fresh K also has an fp16 lo part
+ *              (K - fp16(K), same layout), so hi + lo holds the fp32 key to
+ *              about 22 significant bits.
  *   Q scratch  [kv_head][row][hdp], row = q_index * G + head_in_group,
  *              rotated and pre-multiplied by scale * log2(e); hdp = head_dim
- *              rounded up to 32 and zero-filled; fp16 or fp32 (see below).
+ *              rounded up to 32 and zero-filled; fp16 (with its lo part in
+ *              a second array of the same layout for precise QK^T) or fp32.
  */
 #ifndef SMOL_ATTN_INTERNAL_H
 #define SMOL_ATTN_INTERNAL_H
@@ -76,19 +80,21 @@ typedef struct {
 } FbItem;
 
 /* Q-scratch format written by k_prep (fresh K / V^T are fp16 in both):
- *   SMOL_STAGE_F16    fp16 (the fp16-MFMA kernels k_attn_fb and k_attn_fa)
- *   SMOL_STAGE_QF32   fp32 (k_attn_dec splits it into bf16 hi + lo for the
- *                     bf16-MFMA cache slabs and rounds it to fp16 for the fresh slab) */
+ *   SMOL_STAGE_F16    fp16 (the fp16-MFMA kernels k_attn_fb and k_attn_fa),
+ *                     plus the fp16 lo part when PrepParams.qs_lo is set
+ *   SMOL_STAGE_QF32   fp32 (k_dec splits it into bf16 hi + lo) */
 enum { SMOL_STAGE_F16 = 0, SMOL_STAGE_QF32 = 1 };
 
 typedef struct {
     const _Float16 *qs;        /* Q scratch */
+    const _Float16 *qs_lo;     /* its lo part (precise QK^T; null: single-term fp16 QK^T) */
     long long qs_head_stride;  /* rows_total * hdp */
     const uint16_t *kc;        /* cache K at (layer, slot 0), or null */
     const uint16_t *vtc;       /* cache V^T at (layer, slot 0), or null */
     long long c_slot_stride;   /* elements per slot (n_kv * cap * hd) */
     int cap;                   /* cache rows per (slot, kv head) */
     const _Float16 *kf;        /* fresh K [kv][fcap][hd] */
+    const _Float16 *kf_lo;     /* its lo part (precise QK^T) */
     const _Float16 *vtf;       /* fresh V^T [kv][hd][fcap] */
     const float *qs32;         /* fp32 Q scratch (SMOL_STAGE_QF32) */
     int fcap;
@@ -145,8 +151,10 @@ typedef struct {
     float qscale;
     int Hq, Hkv, G, hd, hdp;
     _Float16 *qs; long long qs_head_stride;
+    _Float16 *qs_lo;           /* non-null: Q is also written as its fp16 lo part (Q - fp16(Q)) */
     uint16_t *kc; uint16_t *vtc; long long c_slot_stride; int cap;
     _Float16 *kf; _Float16 *vtf; int fcap;
+    _Float16 *kf_lo;           /* non-null: the fresh K's fp16 lo part */
     int stage;                 /* SMOL_STAGE_F16 or SMOL_STAGE_QF32 */
     float *qs32;
     const PrepBlockB *blocks;
@@ -173,6 +181,7 @@ typedef struct {
                                   4 waves hold 64 rows, each over half the window's slabs, merged in LDS */
     int n_xcc;                 /* XCDs: workgroup b runs on XCD b % n_xcc */
     int *range_flag;           /* set to 1 when a value written as fp16 would overflow */
+    int precise;               /* 1: QK^T on fp16 hi + lo operands (Q always; K for fp32 inputs) */
     int ws[WIN_ARG_WINDOWS + 1];
 } WinParams;
 
@@ -220,6 +229,7 @@ typedef struct {
     /* chunk mode: the call's new keys (and the older rows of their first
      * slab) in the fp16 staging; key k >= fresh_pos0 is fresh row fresh_row0 + k - fresh_pos0 */
     const _Float16 *kf; const _Float16 *vtf; int fcap; int fresh_pos0; int fresh_row0;
+    const _Float16 *kf_lo;     /* the fresh K's fp16 lo part (null: K = fp16 hi alone) */
     /* chunk mode: fp32 Q scratch [kv][rows][hdp], rotated and scaled; row q * G + h */
     const float *qs32; long long qs_head_stride;
     /* decode mode (direct = 1): Q, the new K and V rows of the inputs, rotated here */

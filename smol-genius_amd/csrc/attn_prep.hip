@@ -79,6 +79,12 @@ __device__ __forceinline__ void prep_q(const PrepParams &p, const PrepBlock &blk
                 if (p.stage == SMOL_STAGE_QF32) {
                     *reinterpret_cast<float4 *>(p.qs32 + qi[u]) = make_float4(v[0], v[1], v[2], v[3]);
                     *reinterpret_cast<float4 *>(p.qs32 + qi[u] + 4) = make_float4(v[4], v[5], v[6], v[7]);
+                } else if (p.qs_lo) {
+                    note_h_range(p.range_flag, v);
+                    uint4 hi, lo;
+                    pack_h8_hilo(v, hi, lo);
+                    *reinterpret_cast<uint4 *>(p.qs + qi[u]) = hi;
+                    *reinterpret_cast<uint4 *>(p.qs_lo + qi[u]) = lo;
                 } else {
                     note_h_range(p.range_flag, v);
                     *reinterpret_cast<uint4 *>(p.qs + qi[u]) = pack_h8(v);
@@ -162,7 +168,15 @@ __device__ __forceinline__ void prep_fresh(const PrepParams &p, const PrepBlock 
         }
         if (has_cache && is_new) *reinterpret_cast<uint4 *>(kc + (long long)pos * HD + d0) = pack_bf16x8(kv);
         note_h_range(p.range_flag, kv);
-        *reinterpret_cast<uint4 *>(kf + (long long)(frow_base + r) * HD + d0) = pack_h8(kv);
+        if (p.kf_lo) {
+            uint4 hi, lo;
+            pack_h8_hilo(kv, hi, lo);
+            const long long fo = (long long)g * p.fcap * HD + (long long)(frow_base + r) * HD + d0;
+            *reinterpret_cast<uint4 *>(kf + (long long)(frow_base + r) * HD + d0) = hi;
+            *reinterpret_cast<uint4 *>(p.kf_lo + fo) = lo;
+        } else {
+            *reinterpret_cast<uint4 *>(kf + (long long)(frow_base + r) * HD + d0) = pack_h8(kv);
+        }
 #pragma unroll
         for (int i = 0; i < 8; i++) sv[r * 257 + d0 + i] = vv[i];
     }

@@ -29,15 +29,18 @@
 
 namespace {
 
-template <int HD>
+/* KLO: the slab image holds K twice, fp16 hi then fp16 lo (precise QK^T on
+ * fp32 inputs; bf16 inputs are exact in fp16 and need no lo part) */
+template <int HD, bool KLO>
 struct WinGeom {
     static constexpr int KS = (HD + 31) / 32;  /* 32-wide d chunks of a K fragment */
     static constexpr int DT = (HD + 15) / 16;  /* 16-wide d tiles of the output */
     static constexpr int HDP = KS * 32;
     static constexpr int KROW = 256;
     static constexpr int K_BYTES = SMOL_SLAB * KROW;
+    static constexpr int KPARTS = KLO ? 2 : 1;
     static constexpr int V_BYTES = 16 * DT * 64;
-    static constexpr int SLABB = K_BYTES + V_BYTES;
+    static constexpr int SLABB = KPARTS * K_BYTES + V_BYTES;
     static constexpr int NS_MAX = (160 * 1024) / SLABB; /* slabs the LDS holds */
 };
 
@@ -67,9 +70,12 @@ struct Raw8In {
 
 } // namespace
 
-template <int HD, bool BF, int NS>
+/* PREC: QK^T on fp16 hi + lo operands, Khi.Qhi + Khi.Qlo (+ Klo.Qhi for
+ * fp32 inputs) */
+template <int HD, bool BF, int NS, bool PREC>
 __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
-    using Gm = WinGeom<HD>;
+    constexpr bool KLO = PREC && !BF;
+    using Gm = WinGeom<HD, KLO>;
     constexpr int KS = Gm::KS, DT = Gm::DT, HDP = Gm::HDP, KROW = Gm::KROW;
     constexpr int K_BYTES = Gm::K_BYTES, SLABB = Gm::SLABB;
     static_assert(HD % 8 == 0 && HD <= 128, "head_dim");
@@ -151,7 +157,15 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
                 for (int i = 0; i < 8; i++) v[i] = 0.0f;
             }
             note_h_range(p.range_flag, v);
-            *reinterpret_cast<uint4 *>(smem + (key >> 5) * SLABB + rr * KROW + 16 * slot) = pack_h8(v);
+            unsigned char *kd = smem + (key >> 5) * SLABB + rr * KROW + 16 * slot;
+            if constexpr (KLO) {
+                uint4 hi, lo;
+                pack_h8_hilo(v, hi, lo);
+                *reinterpret_cast<uint4 *>(kd) = hi;
+                *reinterpret_cast<uint4 *>(kd + K_BYTES) = lo;
+            } else {
+                *reinterpret_cast<uint4 *>(kd) = pack_h8(v);
+            }
         }
     };
     /* V^T: block e (keys 8 kb .. 8 kb + 7, dims 8 db .. 8 db + 7; consecutive
@@ -183,7 +197,7 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
             r[i] = pack_h8(v);
         }
         const int sl = kb >> 2, jc = kb & 3;
-        unsigned char *vbase = smem + sl * SLABB + K_BYTES;
+        unsigned char *vbase = smem + sl * SLABB + Gm::KPARTS * K_BYTES;
 #pragma unroll
         for (int dd = 0; dd < 8; dd++) {
             /* column dd: key pairs (2m, 2m + 1) of dim 8 db + dd */
@@ -217,7 +231,7 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
             v_store(u, vin);
         }
     }
-    h8 qf[KS];
+    h8 qf[KS], qfl[PREC ? KS : 1];
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
         float v[8];
@@ -226,8 +240,15 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = ok ? v[i] * p.qscale : 0.0f;
         note_h_range(p.range_flag, v);
-        const uint4 hw = pack_h8(v);
-        qf[ks] = *reinterpret_cast<const h8 *>(&hw);
+        if constexpr (PREC) {
+            uint4 hw, lw;
+            pack_h8_hilo(v, hw, lw);
+            qf[ks] = *reinterpret_cast<const h8 *>(&hw);
+            qfl[ks] = *reinterpret_cast<const h8 *>(&lw);
+        } else {
+            const uint4 hw = pack_h8(v);
+            qf[ks] = *reinterpret_cast<const h8 *>(&hw);
+        }
     }
     __syncthreads();
 
@@ -238,7 +259,7 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
     unsigned kfo[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) kfo[ks] = (unsigned)(kt_row * KROW + 16 * ((4 * ks + j) ^ c));
-    const unsigned vfo = (unsigned)(K_BYTES + c * 64 + 16 * (j ^ ((c >> 1) & 3)));
+    const unsigned vfo = (unsigned)(Gm::KPARTS * K_BYTES + c * 64 + 16 * (j ^ ((c >> 1) & 3)));
     auto lds_h8 = [&](int s, unsigned off) __attribute__((always_inline)) -> h8 {
         const uint4 x = *reinterpret_cast<const uint4 *>(smem + s * SLABB + off);
         return *reinterpret_cast<const h8 *>(&x);
@@ -246,28 +267,37 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
     h8 ones;
 #pragma unroll
     for (int i = 0; i < 8; i++) ones[i] = (_Float16)1.0f;
+    /* row sums: on the matrix cores against a fragment of ones (lsum), or
+     * with PREC (P = Phi + Plo) in fp32 per lane (lp), reduced at the end */
     f4 o[DT], lsum = {0.f, 0.f, 0.f, 0.f};
+    float lp = 0.0f;
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) o[dt] = f4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY;
     /* S of slab s + 1 is formed before the softmax of slab s: the matrix
      * cores work on it while the vector ALU does the softmax */
-    auto read_k = [&](int s, h8 (&kf)[2][KS]) __attribute__((always_inline)) {
+    /* K fragments: [0..1] hi, [2..3] lo (KLO) */
+    constexpr int KF = KLO ? 4 : 2;
+    auto read_k = [&](int s, h8 (&kf)[KF][KS]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int tt = 0; tt < 2; tt++)
+        for (int tt = 0; tt < KF; tt++)
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) kf[tt][ks] = lds_h8(s, kfo[ks] + tt * 4 * KROW);
+            for (int ks = 0; ks < KS; ks++) kf[tt][ks] = lds_h8(s, kfo[ks] + (tt & 1) * 4 * KROW + (tt >> 1) * K_BYTES);
     };
-    auto qk = [&](const h8 (&kf)[2][KS], f4 (&sc)[2]) __attribute__((always_inline)) {
+    auto qk = [&](const h8 (&kf)[KF][KS], f4 (&sc)[2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
             f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[tt][ks], qf[ks], acc, 0, 0, 0);
+            for (int ks = 0; ks < KS; ks++) {
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[tt][ks], qf[ks], acc, 0, 0, 0);
+                if constexpr (PREC) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[tt][ks], qfl[ks], acc, 0, 0, 0);
+                if constexpr (KLO) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[2 + tt][ks], qf[ks], acc, 0, 0, 0);
+            }
             sc[tt] = acc;
         }
     };
-    h8 kf[2][KS];
+    h8 kf[KF][KS];
     f4 scur[2], snext[2];
     if (s_lo < s_hi) {
         read_k(s_lo, kf);
@@ -301,12 +331,25 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
         /* (a group without slabs keeps m = -inf, lsum = 0, o = 0) */
         const float alpha = __builtin_amdgcn_exp2f(m - m_new);
         m = m_new;
-        h8 pf;
+        h8 pf, pfl;
+        float ps = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; e++) pf[e] = (_Float16)__builtin_amdgcn_exp2f(sv[e] - m_new);
+        for (int e = 0; e < 8; e++) {
+            const float pe = __builtin_amdgcn_exp2f(sv[e] - m_new);
+            pf[e] = (_Float16)pe;
+            if constexpr (PREC) {
+                pfl[e] = (_Float16)(pe - (float)pf[e]);
+                ps += pe;
+            }
+        }
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pf, o[dt] * alpha, 0, 0, 0);
-        lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, lsum * alpha, 0, 0, 0);
+        for (int dt = 0; dt < DT; dt++) {
+            f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pf, o[dt] * alpha, 0, 0, 0);
+            if constexpr (PREC) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pfl, acc, 0, 0, 0);
+            o[dt] = acc;
+        }
+        if constexpr (PREC) lp = lp * alpha + ps;
+        else lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, lsum * alpha, 0, 0, 0);
         if (more) {
             scur[0] = snext[0];
             scur[1] = snext[1];
@@ -316,7 +359,7 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
     /* ---- two groups: group 1 hands (O, m, l) to group 0 through LDS, lane
      * by lane (wave wr of either group holds the same rows in the same
      * lanes) ---- */
-    float l = lsum[0];
+    float l = PREC ? row_sum4(lp) : lsum[0];
     if (split) {
         float *xo = reinterpret_cast<float *>(smem) + (wr * 64 + lane) * (4 * DT + 4);
         static_assert(4 * 64 * (4 * DT + 4) * 4 <= NS * SLABB, "merge scratch");
@@ -351,45 +394,59 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
 
 namespace {
 
-template <int HD, bool BF, int NS>
+template <int HD, bool BF, int NS, bool PREC>
 int launch_win_v(const WinParams *wp, int n_tiles, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     (void)n_tiles;
     const long long units = (long long)wp->n_windows * wp->H;
     const dim3 grid((unsigned)((units + wp->n_xcc - 1) / wp->n_xcc * wp->n_xcc * wp->tpu));
     if (e0)
-        hipExtLaunchKernelGGL((k_attn_win<HD, BF, NS>), grid, dim3(WIN_TPB), 0, st, e0, e1, 0, *wp);
+        hipExtLaunchKernelGGL((k_attn_win<HD, BF, NS, PREC>), grid, dim3(WIN_TPB), 0, st, e0, e1, 0, *wp);
     else
-        hipLaunchKernelGGL((k_attn_win<HD, BF, NS>), grid, dim3(WIN_TPB), 0, st, *wp);
+        hipLaunchKernelGGL((k_attn_win<HD, BF, NS, PREC>), grid, dim3(WIN_TPB), 0, st, *wp);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 /* builds by window capacity: 4 or 8 slabs (the short windows of the audio
  * and vision encoders), or as many as the LDS holds */
-template <int HD, bool BF>
+template <int HD, bool BF, bool PREC>
 int launch_win_bf(const WinParams *wp, int n_tiles, int max_len, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+    constexpr int NS_MAX = WinGeom<HD, PREC && !BF>::NS_MAX;
     const int ns = (max_len + SMOL_SLAB - 1) / SMOL_SLAB;
-    if (ns <= 4) return launch_win_v<HD, BF, 4>(wp, n_tiles, st, e0, e1);
-    if (ns <= 8) return launch_win_v<HD, BF, 8>(wp, n_tiles, st, e0, e1);
-    if (ns <= WinGeom<HD>::NS_MAX) return launch_win_v<HD, BF, WinGeom<HD>::NS_MAX>(wp, n_tiles, st, e0, e1);
+    static_assert(NS_MAX >= 4, "the smallest build");
+    if (ns <= 4) return launch_win_v<HD, BF, 4, PREC>(wp, n_tiles, st, e0, e1);
+    if constexpr (NS_MAX > 8) {
+        if (ns <= 8) return launch_win_v<HD, BF, 8, PREC>(wp, n_tiles, st, e0, e1);
+    }
+    if (ns <= NS_MAX) return launch_win_v<HD, BF, NS_MAX, PREC>(wp, n_tiles, st, e0, e1);
     return -1;
 }
 
 template <int HD>
 int launch_win_hd(const WinParams *wp, int n_tiles, int max_len, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
-    return wp->in_dtype == SMOL_IN_BF16 ? launch_win_bf<HD, true>(wp, n_tiles, max_len, st, e0, e1)
-                                        : launch_win_bf<HD, false>(wp, n_tiles, max_len, st, e0, e1);
+    const bool bf = wp->in_dtype == SMOL_IN_BF16;
+    if (wp->precise)
+        return bf ? launch_win_bf<HD, true, true>(wp, n_tiles, max_len, st, e0, e1)
+                  : launch_win_bf<HD, false, true>(wp, n_tiles, max_len, st, e0, e1);
+    return bf ? launch_win_bf<HD, true, false>(wp, n_tiles, max_len, st, e0, e1)
+              : launch_win_bf<HD, false, false>(wp, n_tiles, max_len, st, e0, e1);
+}
+
+template <int HD>
+int win_max_keys(int in_dtype, int precise) {
+    return (precise && in_dtype != SMOL_IN_BF16 ? WinGeom<HD, true>::NS_MAX : WinGeom<HD, false>::NS_MAX) * SMOL_SLAB;
 }
 
 } // namespace
 
-/* The longest window k_attn_win holds at head_dim hd (0: not supported) */
-extern "C" int smol_win_max_keys(int hd) {
+/* The longest window k_attn_win holds at head_dim hd for inputs of type
+ * in_dtype, with precise QK^T or not (0: not supported) */
+extern "C" int smol_win_max_keys(int hd, int in_dtype, int precise) {
     switch (hd) {
-    case 64: return WinGeom<64>::NS_MAX * SMOL_SLAB;
-    case 72: return WinGeom<72>::NS_MAX * SMOL_SLAB;
-    case 80: return WinGeom<80>::NS_MAX * SMOL_SLAB;
-    case 96: return WinGeom<96>::NS_MAX * SMOL_SLAB;
-    case 128: return WinGeom<128>::NS_MAX * SMOL_SLAB;
+    case 64: return win_max_keys<64>(in_dtype, precise);
+    case 72: return win_max_keys<72>(in_dtype, precise);
+    case 80: return win_max_keys<80>(in_dtype, precise);
+    case 96: return win_max_keys<96>(in_dtype, precise);
+    case 128: return win_max_keys<128>(in_dtype, precise);
     default: return 0;
     }
 }
