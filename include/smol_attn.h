@@ -135,7 +135,10 @@ SMOL_ATTN_API int smol_attn_ctx_timing_read(smol_attn_ctx *ctx, double *ms, int 
 #define SMOL_OPT_QK_FP16 11       /* 1: QK^T on single fp16 operands (Q and K each rounded to fp16:
                                    * faster, within the bar for logits up to about sigma 1.4 on
                                    * unit-variance rows); 0: fp16 hi + lo operands, see Numerics */
-#define SMOL_OPT_COUNT 12
+#define SMOL_OPT_FB_GROUPS 12     /* k_attn_fb: 1: one key group of eight waves over 128-row items (long
+                                   * items' keys split over workgroups and merged); 0 or 2: two key
+                                   * groups over 64-row items */
+#define SMOL_OPT_COUNT 13
 SMOL_ATTN_API int smol_attn_ctx_set_option(smol_attn_ctx *ctx, int option, int value);
 SMOL_ATTN_API int smol_attn_ctx_get_option(smol_attn_ctx *ctx, int option, int *value);
 

@@ -724,7 +724,7 @@ static std::vector<PrepBlockB> prep_records(const Plan &pl) {
  * list with the least work so far: an item costs its steps (two slabs each,
  * one per key group) plus about six steps of start-up and epilogue. Item w
  * heads list w; `next` links the rest. */
-static std::vector<FbItem> fb_items(const Plan &pl, int n_wg) {
+static std::vector<FbItem> fb_items(const Plan &pl, int n_wg, bool one_group) {
     const int n = (int)pl.items.size();
     auto record = [&](int i) {
         const SkItem &it = pl.items[i];
@@ -734,6 +734,9 @@ static std::vector<FbItem> fb_items(const Plan &pl, int n_wg) {
         f.key_begin = it.key_begin; f.key_end = it.key_end; f.fresh_off = it.fresh_off; f.row0 = it.row0;
         f.n_rows = b.n_rows; f.q_row0 = b.q_row0; f.out_tok0 = b.out_tok0; f.q_pos0 = b.q_pos0;
         f.key_lo = b.key_lo; f.key_hi = b.key_hi; f.causal = b.causal; f.next = -1;
+        /* merge group and partial slot: a group's items are contiguous in
+         * the plan, so slot i - split is the group's first */
+        f.group = it.group; f.n_split = it.n_split; f.split = it.split; f.part = i;
         return f;
     };
     std::vector<FbItem> out(n);
@@ -746,7 +749,9 @@ static std::vector<FbItem> fb_items(const Plan &pl, int n_wg) {
     auto cost = [&](int i) {
         const SkItem &it = pl.items[i];
         const int slabs = (it.key_end - it.key_begin + SMOL_SLAB - 1) / SMOL_SLAB;
-        return (slabs + 1) / 2 + 6;
+        /* a step per slab (one key group) or per two (two groups), start-up
+         * and epilogue, and a publish and merge for a split item */
+        return one_group ? slabs + 6 + (it.n_split > 1 ? 2 : 0) : (slabs + 1) / 2 + 6;
     };
     std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return cost(a) > cost(b); });
     using Load = std::pair<long long, int>; /* (work, list) */
@@ -1029,7 +1034,17 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
         if (pk != 1 && tiles * cs.Hkv < ctx->cu_count / 4) fb = false;
     }
     int nt = 1, w = 2, rows_per = 64;
-    if (fb) {
+    /* k_attn_fb with two key groups (64-row items, each group half of the
+     * keys; the default) or one key group of eight waves (128-row items whose
+     * key ranges may be split over workgroups and merged: each slab is staged
+     * once for 128 rows and five stages fit with precise QK^T, but at C2's
+     * shape the split items' start-up and merges cost more than that saves) */
+    const bool fb_one = fb && ctx->opt[SMOL_OPT_FB_GROUPS] == 1 && ctx->opt[SMOL_OPT_FB_NT] != 2;
+    if (fb_one) {
+        nt = 0; /* the launcher's code for one key group */
+        w = 2;
+        rows_per = 128;
+    } else if (fb) {
         /* 64-row tiles; SMOL_OPT_FB_NT 2: two row tiles per wave (four waves
          * per workgroup instead of eight) */
         nt = ctx->opt[SMOL_OPT_FB_NT] == 2 ? 2 : 1;
@@ -1041,7 +1056,8 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
         w = hd > 128 ? 1 : 2;
         rows_per = 64 * nt;
     }
-    if (fa) plan_items(pl, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, true, fb);
+    if (fa) plan_items(pl, cs.Hkv, G, cs.window, rows_per, fb_one ? ctx->cu_count : ctx->cu_count * w, true,
+                       fb && !fb_one);
 
     /* workspace; precise QK^T (the default) adds the lo parts of the fp16 Q
      * scratch and of the fresh K */
@@ -1076,7 +1092,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     std::vector<FbItem> fbi;
     int fb_wg = std::max(1, ctx->cu_count / cs.Hkv);
     if (!((int)n_items > fb_wg && ctx->opt[SMOL_OPT_FB_LISTS] != -1)) fb_wg = 0;
-    if (fb) fbi = fb_items(pl, fb_wg);
+    if (fb) fbi = fb_items(pl, fb_wg, fb_one);
 
     /* descriptor tables in one upload: pre-pass blocks and items, each with
      * its batch */

@@ -2,7 +2,7 @@
  * attn_fb.hip - k_attn_fb: prefill and windowed bidirectional attention over
  * keys that all sit in the fresh fp16 staging.
  */
-#include "attn_device.h"
+#include "attn_splitk.h"
 
 /* ---------------------------------------------------------------- k_attn_fb */
 
@@ -37,11 +37,12 @@
  * are waited for where the schedule needs them and one barrier publishes
  * them.
  */
-/* WPG waves per key group, each holding NT 16-row tiles of the 64-row item.
+/* WPG waves per key group, each holding NT 16-row tiles of the item.
  * PREC (precise QK^T): a stage holds the K image twice, fp16 hi then fp16 lo
- * (the same layout), then V^T; the larger stage leaves room for three stages
- * per group instead of five. */
-template <int HD, int WPG, bool PREC>
+ * (the same layout), then V^T; with two key groups the larger stage leaves
+ * room for three stages per group instead of five. ONE: a single key group
+ * of eight waves (128-row items), which keeps five stages either way. */
+template <int HD, int WPG, bool PREC, bool ONE>
 struct FbGeom {
     static constexpr int KS = (HD + 31) / 32;
     static constexpr int DT = (HD + 15) / 16;
@@ -52,7 +53,8 @@ struct FbGeom {
     static constexpr int V_BYTES = 16 * DT * 64;
     static constexpr int STAGE = (KPARTS * K_BYTES + V_BYTES + 1024 * WPG - 1) / (1024 * WPG) * (1024 * WPG);
     static constexpr int NDMA = STAGE / (1024 * WPG); /* DMA instructions per wave per slab */
-    static constexpr int NSTG = PREC ? 3 : (2 * 5 * STAGE <= 160 * 1024 ? 5 : 4);
+    static constexpr int GROUPS = ONE ? 1 : 2;
+    static constexpr int NSTG = PREC && !ONE ? 3 : (GROUPS * 5 * STAGE <= 160 * 1024 ? 5 : 4);
     static constexpr int GROUP_BYTES = NSTG * STAGE;
 };
 
@@ -62,25 +64,56 @@ struct FbGeom {
  * halves the LDS reads per flop. One MFMA pipe per SIMD is kept busy by a
  * single wave (measured: 16x16x32 f16 MFMAs with independent accumulators
  * issue at the same rate from one wave per SIMD as from two). */
-template <int HD, int NT, bool CAP, bool PREC>
+/* The merge of a split item's group by its last workgroup (merge_group of
+ * k_attn_fa on the item's fields), not inlined: its registers then do not add
+ * to those of the slab loop, which runs at two waves per SIMD. */
+template <int HD, int ROWS, int TPB>
+__device__ __attribute__((noinline)) void fb_merge(float *part_o, float *part_ml, int *counters, float *out, int Hkv,
+                                                   int Hq, int G, FbItem it, int g, int tid, float *s_o) {
+    /* the fields merge_group reads (passed by value: the kernel's own
+     * argument block stays private to it, so its fields stay uniform) */
+    SkParams p;
+    memset(&p, 0, sizeof(p));
+    p.part_o = part_o; p.part_ml = part_ml; p.counters = counters; p.out = out;
+    p.Hkv = Hkv; p.Hq = Hq; p.G = G;
+    SkItem si;
+    si.batch = 0; si.row0 = it.row0; si.key_begin = it.key_begin; si.key_end = it.key_end;
+    si.group = it.group; si.n_split = it.n_split; si.split = it.split; si.fresh_off = it.fresh_off;
+    SkBatch sb;
+    sb.n_rows = it.n_rows; sb.q_row0 = it.q_row0; sb.out_tok0 = it.out_tok0; sb.q_pos0 = it.q_pos0;
+    sb.key_lo = it.key_lo; sb.key_hi = it.key_hi; sb.causal = it.causal;
+    sb.fresh_pos0 = 0; sb.fresh_row0 = 0; sb.slot = -1; sb.pad0 = sb.pad1 = 0;
+    merge_group<HD, ROWS, 16, TPB>(p, si, sb, it.part, g, tid, s_o);
+}
+
+/* ONE: the eight waves form a single key group over a 128-row item (each
+ * slab is transferred once for all of them), and an item may cover part of
+ * its tile's keys (see FbItem), merged across workgroups */
+template <int HD, int NT, bool CAP, bool PREC, bool ONE>
 __global__ __launch_bounds__(NT == 1 ? 512 : 256)
 __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_attn_fb(SkParams p) {
-    constexpr int WPG = 4 / NT;
-    using Gm = FbGeom<HD, WPG, PREC>;
+    static_assert(!ONE || NT == 1, "one key group: eight waves of one row tile each");
+    constexpr int WPG = ONE ? 8 : 4 / NT;
+    using Gm = FbGeom<HD, WPG, PREC, ONE>;
     constexpr int KS = Gm::KS, DT = Gm::DT, HDP = Gm::HDP, KROW = Gm::KROW;
     constexpr int K_BYTES = Gm::K_BYTES, STAGE = Gm::STAGE, NDMA = Gm::NDMA, NSTG = Gm::NSTG;
     constexpr unsigned SLAB_BYTES = SMOL_SLAB * HD * 2;
+    /* one barrier a step and one-step transfers (three stages) */
+    constexpr bool B1 = NSTG == 3;
+    constexpr int ROWS = 16 * NT * WPG; /* rows of an item */
     static_assert(HD <= 128, "k_attn_fb covers head_dim <= 128");
-    static_assert(2 * Gm::GROUP_BYTES <= 160 * 1024, "LDS");
+    static_assert(Gm::GROUPS * Gm::GROUP_BYTES <= 160 * 1024, "LDS");
     static_assert(NSTG >= 3, "the step pipeline keeps three slabs resident");
     static_assert(!PREC || K_BYTES % (1024 * WPG) == 0, "each DMA instruction of a wave lands in one part");
+    static_assert(!ONE || (2 * SK_MERGE_MAX + 2 * ROWS) * 4 <= Gm::GROUP_BYTES, "merge scratch");
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int grp = wave / WPG, wg = wave % WPG;
+    const int grp = ONE ? 0 : wave / WPG, wg = wave % WPG;
     const float icap2 = CAP ? 1.0f / p.cap2 : 0.0f;
     const int g = (int)(blockIdx.x % (unsigned)p.Hkv);
     const int w = (int)(blockIdx.x / (unsigned)p.Hkv);
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * Gm::GROUP_BYTES];
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[Gm::GROUPS * Gm::GROUP_BYTES];
+    __shared__ int s_last;
     /* item w, then the rest of this workgroup's list (the host's
      * longest-first assignment when the items outnumber the compute units,
      * where a second wave of workgroups would pay its start-up again) */
@@ -97,9 +130,9 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     unsigned char *gbase = smem + grp * Gm::GROUP_BYTES;
     const unsigned lds_group = (unsigned)(size_t)gbase;
 
-    /* this group's slabs: the first or second half of the item's */
+    /* this group's slabs: the first or second half of the item's (ONE: all) */
     const int n_all = (it.key_end - it.key_begin + SMOL_SLAB - 1) / SMOL_SLAB;
-    const int n0 = (n_all + 1) >> 1;
+    const int n0 = ONE ? n_all : (n_all + 1) >> 1;
     const int s_first = grp == 0 ? 0 : n0;
     const int n_own = grp == 0 ? n0 : n_all - n0;
     auto slab_k = [&](int i) __attribute__((always_inline)) {
@@ -141,9 +174,9 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
             dma_1k(d_part[e] == 0 ? rk : d_part[e] == 1 ? rkl : rv, d_off[e], so,
                    __builtin_amdgcn_readfirstlane(lds_group + stage * STAGE + (wg + WPG * e) * 1024));
     };
-    /* the prologue stages three slabs (PREC: two); the steps bring the rest
-     * in pairs (PREC: one a step) */
-    constexpr int PRO = PREC ? 2 : 3;
+    /* the prologue stages three slabs (three stages: two); the steps bring
+     * the rest in pairs (three stages: one a step) */
+    constexpr int PRO = B1 ? 2 : 3;
 #pragma unroll
     for (int q = 0; q < PRO; q++) dma(slab_k(q), q);
 
@@ -234,34 +267,52 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
      * S): the K lo fragments are read from `stage` into the registers of
      * the hi ones once the hi products are issued, which keeps one slab's
      * fragments live instead of two, and the hi products cover the reads */
-    auto qk = [&](h8 (&kf)[2][KS], int stage, f4 (&sacc)[NT][2]) __attribute__((always_inline)) {
+    auto qk_hi = [&](const h8 (&kt)[KS], int t, f4 (&sacc)[NT][2]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+        for (int nt = 0; nt < NT; nt++) {
+            f4 acc = CAP ? f4{0.f, 0.f, 0.f, 0.f} : negm[nt];
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                f4 acc = CAP ? f4{0.f, 0.f, 0.f, 0.f} : negm[nt];
-#pragma unroll
-                for (int ks = 0; ks < KS; ks++) {
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t][ks], qf[nt][ks], acc, 0, 0, 0);
-                    if constexpr (PREC) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t][ks], qfl[nt][ks], acc, 0, 0, 0);
-                }
-                sacc[nt][t] = acc;
+            for (int ks = 0; ks < KS; ks++) {
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt[ks], qf[nt][ks], acc, 0, 0, 0);
+                if constexpr (PREC) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt[ks], qfl[nt][ks], acc, 0, 0, 0);
             }
+            sacc[nt][t] = acc;
+        }
+    };
+    auto qk_lo = [&](const h8 (&kt)[KS], int t, f4 (&sacc)[NT][2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            f4 acc = sacc[nt][t];
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt[ks], qf[nt][ks], acc, 0, 0, 0);
+            sacc[nt][t] = acc;
+        }
+    };
+    auto read_klo = [&](int stage, int t, h8 (&kt)[KS]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) kt[ks] = lds_h8(stage, kfo[ks] + t * 4 * KROW + K_BYTES);
+    };
+    /* PREC order: the hi products of key rows t = 0; the lo fragments of t = 0
+     * read into their registers while the hi products of t = 1 run; those of
+     * t = 1 while the lo products of t = 0 run; then the lo products of t = 1 */
+    auto qk = [&](h8 (&kf)[2][KS], int stage, f4 (&sacc)[NT][2]) __attribute__((always_inline)) {
         if constexpr (PREC) {
-#pragma unroll
-            for (int t = 0; t < 2; t++)
-#pragma unroll
-                for (int ks = 0; ks < KS; ks++) kf[t][ks] = lds_h8(stage, kfo[ks] + t * 4 * KROW + K_BYTES);
-#pragma unroll
-            for (int t = 0; t < 2; t++)
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++) {
-                    f4 acc = sacc[nt][t];
-#pragma unroll
-                    for (int ks = 0; ks < KS; ks++)
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t][ks], qf[nt][ks], acc, 0, 0, 0);
-                    sacc[nt][t] = acc;
-                }
+            /* the barriers pin the LDS reads and MFMAs in this order; vector
+             * and scalar ALU work (the softmax) may move across them (mask:
+             * VALU | SALU | transcendental) */
+            constexpr int ALU = 0x0002 | 0x0004 | 0x0400;
+            qk_hi(kf[0], 0, sacc);
+            __builtin_amdgcn_sched_barrier(ALU);
+            read_klo(stage, 0, kf[0]);
+            qk_hi(kf[1], 1, sacc);
+            __builtin_amdgcn_sched_barrier(ALU);
+            read_klo(stage, 1, kf[1]);
+            qk_lo(kf[0], 0, sacc);
+            __builtin_amdgcn_sched_barrier(ALU);
+            qk_lo(kf[1], 1, sacc);
+        } else {
+            qk_hi(kf[0], 0, sacc);
+            qk_hi(kf[1], 1, sacc);
         }
     };
     /* P fragments: [0] fp16 P (hi), [1] its lo part (PREC) */
@@ -384,11 +435,11 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
      * to a step. Steps past the group's own slab count (the second group may
      * have one fewer, or none) keep the reads, transfers and barriers and
      * mask every key. */
-    /* PREC (three stages): step i brings slab i+2 into the stage of slab
-     * i-1, whose last read (its V^T, step i-1) precedes the barrier ending
-     * step i-1, and every step ends in a barrier after vmcnt(0), so the
-     * slab has landed before step i+1 reads its K. */
-    static_assert(PREC ? NSTG == 3 : NSTG == 5, "the transfer schedules are built for five stages (three: PREC)");
+    /* Three stages (PREC with two key groups): step i brings slab i+2 into
+     * the stage of slab i-1, whose last read (its V^T, step i-1) precedes the
+     * barrier ending step i-1, and every step ends in a barrier after
+     * vmcnt(0), so the slab has landed before step i+1 reads its K. */
+    static_assert(B1 || NSTG == 5, "the transfer schedules are built for five stages (or three)");
     const int steps = n0;
     /* Every transfer of the prologue (and Q) has landed before the first
      * barrier. Counted waits (all but the last slabs' transfers) are not used
@@ -416,7 +467,7 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
         read_k(st_k, kf);
         read_v(st_v, vnow);
         /* slab 'steps' (K read in the last step, its S unused) and later ones are not staged */
-        if constexpr (PREC) {
+        if constexpr (B1) {
             if (i + 2 < steps) dma(slab_k(i + 2), (i + 2) % NSTG);
         } else if (!odd) {
             if (i + 3 < steps) dma(slab_k(i + 3), (i + 3) % NSTG);
@@ -441,8 +492,8 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
         /* only odd steps end in a barrier: it publishes the pair issued by
          * the step before, and the even step after it refills the stages of
          * slabs i-1 and i, whose last reads (steps i-1 and i) it orders
-         * (PREC: every step, for its one slab) */
-        if (PREC || odd) {
+         * (three stages: every step, for its one slab) */
+        if (B1 || odd) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
         }
@@ -462,6 +513,61 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     }
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) l[nt] = PREC ? row_sum4(l[nt]) : lsum[nt][0];
+
+    if constexpr (ONE) {
+        if (it.n_split == 1) {
+            /* the item holds its tile's every key: the rows are final */
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                if (!valid[nt]) continue;
+                const int r = it.row0 + (wg * NT + nt) * 16 + c;
+                const int qi = r / G, hg = r - qi * G;
+                const float inv = l[nt] > 0.0f ? 1.0f / l[nt] : 0.0f;
+                float *orow = p.out + ((long long)(b.out_tok0 + qi) * p.Hq + (g * G + hg)) * HD;
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) {
+                    const int d = 16 * dt + 4 * j;
+                    if (HD % 16 != 0 && d >= HD) continue;
+                    st_stream(orow + d, o[nt][dt] * inv);
+                }
+            }
+        } else {
+            /* a split item: publish the unnormalised rows and (m, l) into
+             * slot `part` with device-coherent stores, count in once, and the
+             * group's last workgroup merges (as k_attn_fa's split items) */
+            const long long pbase = ((long long)it.part * p.Hkv + g) * ROWS;
+            const rsrc_t ro = make_rsrc(p.part_o + pbase * HD, (long long)ROWS * HD * 4);
+            const rsrc_t rml = make_rsrc(p.part_ml + pbase * 2, (long long)ROWS * 2 * 4);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const int rr = (wg * NT + nt) * 16 + c;
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) {
+                    const int d = 16 * dt + 4 * j;
+                    if (HD % 16 != 0 && d >= HD) continue;
+                    store_f4_sc1(ro, (unsigned)((rr * HD + d) * 4), o[nt][dt]);
+                }
+                if (j == 0) store_f2_sc1(rml, (unsigned)(rr * 8), m[nt], l[nt]);
+            }
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __syncthreads(); /* every wave's stores are acknowledged (and every stage read is done) */
+            if (tid == 0) {
+                const int prev = __hip_atomic_fetch_add(p.counters + ((long long)it.group * p.Hkv + g) * SK_COUNTER_STRIDE,
+                                                        1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                s_last = prev == it.n_split - 1;
+            }
+            __syncthreads();
+            if (s_last)
+                fb_merge<HD, ROWS, 64 * WPG>(p.part_o, p.part_ml, p.counters, p.out, p.Hkv, p.Hq, p.G, it, g, tid,
+                                             reinterpret_cast<float *>(smem));
+        }
+        if (next < 0) break;
+        item = next;
+        __syncthreads(); /* the epilogue is done with LDS */
+        continue;
+    }
 
     /* merge: group 1 hands its state to group 0 through LDS (lane-wise: the
      * two waves wg of the groups hold the same rows in the same lanes), one
@@ -504,15 +610,20 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
     } /* items */
 }
 
+/* nt: 1 or 2 row tiles per wave with two key groups (64-row items), or 0:
+ * one key group of eight waves (128-row items) */
 template <int HD, bool PREC>
 static int launch_fb_v(const SkParams *sp, dim3 grid, int nt, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     const bool cap = sp->cap2 > 0.0f;
-    if (nt == 1) {
-        if (cap) hipExtLaunchKernelGGL((k_attn_fb<HD, 1, true, PREC>), grid, dim3(512), 0, st, e0, e1, 0, *sp);
-        else hipExtLaunchKernelGGL((k_attn_fb<HD, 1, false, PREC>), grid, dim3(512), 0, st, e0, e1, 0, *sp);
+    if (nt == 0) {
+        if (cap) hipExtLaunchKernelGGL((k_attn_fb<HD, 1, true, PREC, true>), grid, dim3(512), 0, st, e0, e1, 0, *sp);
+        else hipExtLaunchKernelGGL((k_attn_fb<HD, 1, false, PREC, true>), grid, dim3(512), 0, st, e0, e1, 0, *sp);
+    } else if (nt == 1) {
+        if (cap) hipExtLaunchKernelGGL((k_attn_fb<HD, 1, true, PREC, false>), grid, dim3(512), 0, st, e0, e1, 0, *sp);
+        else hipExtLaunchKernelGGL((k_attn_fb<HD, 1, false, PREC, false>), grid, dim3(512), 0, st, e0, e1, 0, *sp);
     } else if (nt == 2) {
-        if (cap) hipExtLaunchKernelGGL((k_attn_fb<HD, 2, true, PREC>), grid, dim3(256), 0, st, e0, e1, 0, *sp);
-        else hipExtLaunchKernelGGL((k_attn_fb<HD, 2, false, PREC>), grid, dim3(256), 0, st, e0, e1, 0, *sp);
+        if (cap) hipExtLaunchKernelGGL((k_attn_fb<HD, 2, true, PREC, false>), grid, dim3(256), 0, st, e0, e1, 0, *sp);
+        else hipExtLaunchKernelGGL((k_attn_fb<HD, 2, false, PREC, false>), grid, dim3(256), 0, st, e0, e1, 0, *sp);
     } else return -1;
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
@@ -529,10 +640,12 @@ static int launch_fb_hd(const SkParams *sp, int n_items, int nt, hipStream_t st,
     return launch_fb_v<HD, false>(sp, grid, nt, st, e0, e1);
 }
 
-/* k_attn_fb: one 64-row tile per item, every key in the fresh buffers; nt
- * row tiles per wave (512 threads for nt 1, 256 for nt 2); sp->n_wg
- * workgroups per kv head (0: one per item) each run their list of items;
- * e0 / e1 (may be null): events recorded around the kernel alone */
+/* k_attn_fb: every key in the fresh buffers; nt: 1 or 2 row tiles per wave
+ * over 64-row items (512 threads for nt 1, 256 for nt 2), or 0: 128-row items
+ * of one key group (512 threads; split items merge through part_o / part_ml
+ * and the counters); sp->n_wg workgroups per kv head (0: one per item) each
+ * run their list of items; e0 / e1 (may be null): events recorded around the
+ * kernel alone */
 extern "C" int smol_launch_fb(const SkParams *sp, int hd, int n_items, int nt, hipStream_t st, hipEvent_t e0,
                               hipEvent_t e1) {
     if (n_items <= 0) return 0;

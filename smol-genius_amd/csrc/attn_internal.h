@@ -70,13 +70,16 @@ typedef struct {
 } SkItemB;
 
 /* A work item of k_attn_fb with its batch's fields (one scalar load): a
- * 64-row tile of a batch against the keys [key_begin, key_end), all in the
- * fresh buffers. next: the next item of the same workgroup, or -1. */
+ * 64-row tile (128 rows with one key group) of a batch against the keys
+ * [key_begin, key_end), all in the fresh buffers. next: the next item of the
+ * same workgroup, or -1. With one key group a tile's keys may be split over
+ * several items (a merge group): the item writes its partial into slot
+ * `part` and the last of the group to finish merges them. */
 typedef struct {
     int key_begin, key_end, fresh_off, row0;
     int n_rows, q_row0, out_tok0, q_pos0;
     int key_lo, key_hi, causal, next;
-    int pad[4];
+    int group, n_split, split, part;
 } FbItem;
 
 /* Q-scratch format written by k_prep (fresh K / V^T are fp16 in both):

@@ -463,6 +463,22 @@ def test_decode_direct_cache_rows(ctx, sa, oracle, wo, hq, hkv, hd, rt, bf):
         np.testing.assert_array_equal(v_row, direct_rows[i][1])
 
 
+@pytest.mark.parametrize("case", [
+    (16, 8, 128, 1536, 0, True), (32, 4, 96, 700, 0, False), (16, 4, 64, 1100, 300, False),
+    (16, 16, 64, [0, 100, 700, 750, 1600, 1601, 2000]), (12, 12, 72, [3, 500, 1025, 1090, 1700, 1800]),
+])
+@pytest.mark.parametrize("qk_fp16", [0, 1])
+def test_fb_one_key_group(ctx, sa, oracle, case, qk_fp16, opts):
+    """k_attn_fb with one key group of eight waves (SMOL_OPT_FB_GROUPS 1):
+    128-row items whose long key ranges are split over workgroups and merged
+    by the last of each group. The same cases as the tile lists, with both
+    QK^T modes; with lists and with one workgroup per item the merges add the
+    same partials in the same order, so the two launches agree bit for bit."""
+    opts(sa.OPT_FB_GROUPS, 1)
+    opts(sa.OPT_QK_FP16, qk_fp16)
+    test_fb_tile_lists(ctx, sa, oracle, case, opts)
+
+
 @pytest.mark.parametrize("window,cap", [(16, 0.0), (0, 2.0), (1, 0.0), (40, 1.5), (1, 3.0)])
 def test_decode_window_softcap(ctx, sa, oracle, wo, window, cap):
     """Sliding window and softcap on decode (the new key is scored apart
