@@ -185,3 +185,37 @@ def test_public_headers_compile_alone_as_c(tmp_path, hdr):
     r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Wextra", "-Werror", "-pedantic", "-fsyntax-only",
                         "-I" + INCLUDE, str(src)], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+REF_DECODER = "/root/reference/common/decoder"
+
+
+def _integration_c_blocks():
+    """The ```c code blocks of INTEGRATION.md's decoder-level section, in order."""
+    import re
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    sec = text[text.index("## 2."):text.index("## 3.")]
+    return re.findall(r"```c\n(.*?)```", sec, re.S)
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(REF_DECODER, "qkn_decoder.h")),
+                    reason="the reference tree is not present")
+def test_integration_snippets_compile_against_reference_decoder(tmp_path):
+    """The decoder-level replacement INTEGRATION.md shows for
+    qkn_decoder.c:460-528 / :625-677 (and the device layer loop) compiles as
+    one C11 translation unit against the reference's own qkn_decoder.h and
+    this repository's headers: every qkn_ctx_t / qkn_config_t field and every
+    library signature it uses is checked. A snippet that names a field the
+    reference struct does not have is rejected (the check bites)."""
+    blocks = _integration_c_blocks()
+    assert len(blocks) >= 3, "the section's code blocks"
+    inc = ["-I" + REF_DECODER, "-I" + os.path.join(os.path.dirname(REF_DECODER), "utils"), "-I" + INCLUDE]
+    src = tmp_path / "integration.c"
+    src.write_text("\n".join(blocks))
+    r = subprocess.run(["gcc", "-std=c11", "-Wall", "-Wextra", "-Werror", "-Wno-unused-function", "-fsyntax-only"]
+                       + inc + [str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    bad = tmp_path / "bad.c"
+    bad.write_text("\n".join(blocks).replace("ctx->pref_attn_out", "ctx->pref_attention_out"))
+    r = subprocess.run(["gcc", "-std=c11", "-fsyntax-only"] + inc + [str(bad)], capture_output=True, text=True)
+    assert r.returncode != 0
