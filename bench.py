@@ -50,21 +50,28 @@ DOMINANT = {"qwen06b_prefill": "k_attn_fb", "qwen06b_prefill_qknorm": "k_attn_fb
             "qwen06b_proj_decode": "k_gemv", "qwen06b_proj_prefill": "Cijk_"}
 
 
-def profiled(workload):
-    """(kernel mean ns, HBM bytes per launch) of the workload's dominant kernel as measured by
-    rocprofv3 (kernel trace; FETCH_SIZE / WRITE_SIZE passes) and summarised in
-    profiles/<kernel>_<workload>.md; None for what the summary lacks."""
-    path = os.path.join(ROOT, "profiles", "%s_%s.md" % (DOMINANT.get(workload, "k_attn_fb"), workload))
-    ns = traffic = None
+def profile_fields(workload):
+    """Figures of the workload's dominant kernel as measured by rocprofv3 and summarised in
+    profiles/<kernel>_<workload>.md: kernel_avg_ns (kernel trace), traffic_bytes_per_launch
+    (FETCH_SIZE / WRITE_SIZE passes), mfma_busy_frac and mfma_flops_executed_per_launch (SQ
+    counter passes); absent keys where the summary lacks them."""
+    path = os.path.join(ROOT, "profiles", "%s_%s.md" % (DOMINANT.get(workload, "k_attn_fb").rstrip("_"), workload))
+    out = {}
     try:
         for line in open(path):
-            if line.startswith("traffic_bytes_per_launch:"):
-                traffic = int(line.split(":")[1])
-            elif line.startswith("kernel_avg_ns:"):
-                ns = float(line.split(":")[1])
+            for key, conv in (("traffic_bytes_per_launch", int), ("kernel_avg_ns", float),
+                              ("mfma_busy_frac", float), ("mfma_flops_executed_per_launch", int)):
+                if line.startswith(key + ":"):
+                    out[key] = conv(line.split(":")[1])
     except OSError:
         pass
-    return ns, traffic
+    return out
+
+
+def profiled(workload):
+    """(kernel mean ns, HBM bytes per launch) of the workload's dominant kernel (profile_fields)"""
+    f = profile_fields(workload)
+    return f.get("kernel_avg_ns"), f.get("traffic_bytes_per_launch")
 
 
 def layers_for(bytes_per_layer, lo=2, hi=64):
@@ -350,7 +357,8 @@ def main():
             "metric": "prefill attn TFLOP/s (causal, Qwen3-ASR-0.6B 1536 tokens)",
             "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
             "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-            "dtype": "f16 MFMA operands, f32 softmax/accumulate (bf16 inputs and KV cache)",
+            "dtype": "f16 MFMA operands as hi + lo pairs (Q, K and P: QK^T and P.V to about 21 bits), f32 "
+                     "softmax/accumulate (bf16 inputs and KV cache)",
             "data": "synthetic (seeded N(0,1) bf16 Q/K/V)",
             "config": dict(main_wl.describe(), layers_rotated=n_layers, parallelism="single GPU"),
             "roofline": {"bound": "mfma", "kernel": "k_attn_fb", "achieved": round(achieved, 3),
@@ -366,6 +374,26 @@ def main():
             pa = flops / (prof_ns * 1e-9) / 1e12
             head["roofline"].update(profile_kernel_ms=round(prof_ns * 1e-6, 5), profile_achieved=round(pa, 3),
                                     profile_frac=round(pa / PEAK_MFMA_TFLOPS, 5))
+        pf = profile_fields(main_wl.name)
+        if "mfma_busy_frac" in pf:
+            # matrix-core busy cycles per SIMD over the kernel's cycles (SQ counters), and the MFMA work
+            # executed per launch, hi/lo products included (useful flops are `flops_per_launch`)
+            head["roofline"].update(mfma_busy=pf["mfma_busy_frac"],
+                                    mfma_flops_executed_per_launch=pf.get("mfma_flops_executed_per_launch"),
+                                    mfma_busy_source="profiles/k_attn_fb_qwen06b_prefill.md (SQ_VALU_MFMA_BUSY_CYCLES)")
+        # the same step with SMOL_OPT_QK_FP16 (single fp16 Q and K operands, P in fp16: faster, within
+        # the bar for logits up to about sigma 1.4 only)
+        ctx.set_option(sa.OPT_QK_FP16, 1)
+        x, run, n_layers16, wall16, kt16 = measure(ctx, main_wl, steps, warmup, runner)
+        ctx.set_option(sa.OPT_QK_FP16, 0)
+        del x, run
+        a16 = kt16["attn"][0] / max(1, kt16["attn"][1])
+        detail["qwen06b_prefill_fp16qk"] = {
+            "config": dict(main_wl.describe(), option="SMOL_OPT_QK_FP16=1"),
+            "ms_per_step": round(wall16 / steps * 1e3, 5), "tflops_step": round(flops / (wall16 / steps) / 1e12, 3),
+            "attn_kernel_ms": round(a16, 5), "tflops_kernel": round(flops / (a16 * 1e-3) / 1e12, 3),
+            "mfma_frac_kernel": round(flops / (a16 * 1e-3) / 1e12 / PEAK_MFMA_TFLOPS, 5),
+            "note": "not the default: single fp16 Q/K/P operands meet the bar only for logits up to about sigma 1.4"}
     else:
         head = None
 
@@ -417,10 +445,12 @@ def main():
                      hbm_frac_kernel=round(b / (attn_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 5),
                      GBps_path=round(b / ((attn_ms + prep_ms) * 1e-3) / 1e9, 1),
                      bytes_per_launch=b)
-        pns, ptraffic = profiled(name)
-        if pns:
-            d["profile_kernel_ms"] = round(pns * 1e-6, 5)
-            d["profile_traffic_bytes"] = ptraffic
+        pf = profile_fields(name)
+        if "kernel_avg_ns" in pf:
+            d["profile_kernel_ms"] = round(pf["kernel_avg_ns"] * 1e-6, 5)
+            d["profile_traffic_bytes"] = pf.get("traffic_bytes_per_launch")
+        if "mfma_busy_frac" in pf:
+            d["profile_mfma_busy"] = pf["mfma_busy_frac"]
         if cpu_mod:
             if isinstance(wl, workloads.Decode):
                 d["cpu_baseline"] = cpu_mod.decode_sample(wl, wl.inputs())
