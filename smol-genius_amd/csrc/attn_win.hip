@@ -75,6 +75,11 @@ struct Raw8In {
 template <int HD, bool BF, int NS, bool PREC>
 __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
     constexpr bool KLO = PREC && !BF;
+    /* BFK (bf16 inputs, precise): K stays bf16 and goes straight into LDS
+     * (buffer_load ... lds, no registers), V^T is transposed as bf16, and the
+     * products run on bf16 MFMA with Q and P as bf16 hi + lo (K and V are
+     * exact, Q and P carry 16 bits) */
+    constexpr bool BFK = BF && PREC;
     using Gm = WinGeom<HD, KLO>;
     constexpr int KS = Gm::KS, DT = Gm::DT, HDP = Gm::HDP, KROW = Gm::KROW;
     constexpr int K_BYTES = Gm::K_BYTES, SLABB = Gm::SLABB;
@@ -184,17 +189,22 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
     auto v_store = [&](int u, const Raw8In<BF> (&in)[8]) __attribute__((always_inline)) {
         const int e = tid + WIN_TPB * u, db = e % NDB, kb = e / NDB;
         if (e >= nvb) return;
-        uint4 r[8]; /* fp16 rows: r[i] holds dims 8 db .. 8 db + 7 of key 8 kb + i */
+        uint4 r[8]; /* fp16 (BFK: bf16) rows: r[i] holds dims 8 db .. 8 db + 7 of key 8 kb + i */
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            float v[8];
-            in[i].unpack(v);
-            if (!(8 * kb + i < len && 8 * db < HD)) {
+            const bool ok = 8 * kb + i < len && 8 * db < HD;
+            if constexpr (BFK) {
+                r[i] = ok ? in[i].a : make_uint4(0, 0, 0, 0);
+            } else {
+                float v[8];
+                in[i].unpack(v);
+                if (!ok) {
 #pragma unroll
-                for (int t = 0; t < 8; t++) v[t] = 0.0f;
+                    for (int t = 0; t < 8; t++) v[t] = 0.0f;
+                }
+                note_h_range(p.range_flag, v);
+                r[i] = pack_h8(v);
             }
-            note_h_range(p.range_flag, v);
-            r[i] = pack_h8(v);
         }
         const int sl = kb >> 2, jc = kb & 3;
         unsigned char *vbase = smem + sl * SLABB + Gm::KPARTS * K_BYTES;
@@ -212,7 +222,30 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
             *reinterpret_cast<uint4 *>(vbase + d * 64 + 16 * (jc ^ ((d >> 1) & 3))) = make_uint4(c4[0], c4[1], c4[2], c4[3]);
         }
     };
-    {
+    if constexpr (BFK) {
+        /* K: each wave transfers row quad `wave` (1 KB of the image) of
+         * every slab; lane l lands at slot l % 16 of row 4 wave + l / 16,
+         * reading the key's chunk cb = slot ^ f(row); chunks past head_dim
+         * and keys past the window are out of the buffer's range (zeros).
+         * The range is the window's rows, whose first element is the base. */
+        const rsrc_t rk = make_rsrc(reinterpret_cast<const uint16_t *>(p.k) + (long long)w0 * p.row_stride + hoff,
+                                    ((long long)(len - 1) * p.row_stride + HD) * 2);
+        const int rr = 4 * wave + (lane >> 4), ks16 = lane & 15;
+        const int cbk = ks16 ^ ((rr & 3) | (((rr >> 3) & 3) << 2));
+        const unsigned lds0 = (unsigned)(size_t)smem + (unsigned)(wave * 1024);
+#pragma unroll
+        for (int e = 0; e < NS; e++) {
+            const int key = e * SMOL_SLAB + rr;
+            const unsigned off = key < len && cbk < HD / 8 ? (unsigned)((key * p.row_stride + cbk * 8) * 2) : OOB_OFF;
+            if (e < nslab) dma_1k(rk, off, 0u, __builtin_amdgcn_readfirstlane(lds0 + (unsigned)(e * SLABB)));
+        }
+        Raw8In<BF> vin[8];
+#pragma unroll
+        for (int u = 0; u < NVB; u++) {
+            v_issue(u, vin);
+            v_store(u, vin);
+        }
+    } else {
         /* the first rounds of K and V go out together */
         Raw8In<BF> kin[RK];
         Raw8In<BF> vin[8];
@@ -232,6 +265,7 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
         }
     }
     h8 qf[KS], qfl[PREC ? KS : 1];
+    b8 qbh[BFK ? KS : 1], qbl[BFK ? KS : 1]; /* BFK: Q as bf16 hi + lo */
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
         float v[8];
@@ -239,6 +273,10 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
         const bool ok = q_ok && (HDP == HD || 32 * ks + 8 * j < HD);
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = ok ? v[i] * p.qscale : 0.0f;
+        if constexpr (BFK) {
+            split8(v, qbh[ks], qbl[ks]);
+            continue;
+        }
         note_h_range(p.range_flag, v);
         if constexpr (PREC) {
             uint4 hw, lw;
@@ -250,6 +288,8 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
             qf[ks] = *reinterpret_cast<const h8 *>(&hw);
         }
     }
+    /* the LDS transfers (BFK) have landed before the barrier */
+    if constexpr (BFK) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 
     /* ---- the slabs: S^T = K.Q^T (lane (c, j) holds keys 8 j + 4 t + i of
@@ -290,6 +330,12 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
             f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
+                if constexpr (BFK) {
+                    const b8 kb = *reinterpret_cast<const b8 *>(&kf[tt][ks]); /* the bf16 bits as staged */
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qbh[ks], acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qbl[ks], acc, 0, 0, 0);
+                    continue;
+                }
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[tt][ks], qf[ks], acc, 0, 0, 0);
                 if constexpr (PREC) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[tt][ks], qfl[ks], acc, 0, 0, 0);
                 if constexpr (KLO) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[2 + tt][ks], qf[ks], acc, 0, 0, 0);
@@ -333,20 +379,34 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
         m = m_new;
         h8 pf, pfl;
         float ps = 0.0f;
+        float pe8[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             const float pe = __builtin_amdgcn_exp2f(sv[e] - m_new);
-            pf[e] = (_Float16)pe;
-            if constexpr (PREC) {
-                pfl[e] = (_Float16)(pe - (float)pf[e]);
-                ps += pe;
+            pe8[e] = pe;
+            if constexpr (!BFK) {
+                pf[e] = (_Float16)pe;
+                if constexpr (PREC) pfl[e] = (_Float16)(pe - (float)pf[e]);
             }
+            if constexpr (PREC) ps += pe;
         }
+        if constexpr (BFK) {
+            /* P as bf16 hi + lo against the exact bf16 V^T */
+            b8 pbh, pbl;
+            split8(pe8, pbh, pbl);
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pf, o[dt] * alpha, 0, 0, 0);
-            if constexpr (PREC) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pfl, acc, 0, 0, 0);
-            o[dt] = acc;
+            for (int dt = 0; dt < DT; dt++) {
+                const b8 vb = *reinterpret_cast<const b8 *>(&vf[dt]);
+                f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vb, pbh, o[dt] * alpha, 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vb, pbl, acc, 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pf, o[dt] * alpha, 0, 0, 0);
+                if constexpr (PREC) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pfl, acc, 0, 0, 0);
+                o[dt] = acc;
+            }
         }
         if constexpr (PREC) lp = lp * alpha + ps;
         else lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, lsum * alpha, 0, 0, 0);
