@@ -712,6 +712,89 @@ static void plan_items(Plan &pl, int Hkv, int G, int window, int rows_per, int c
     pl.n_groups = group;
 }
 
+/* k_attn_fb with one key group: 128-row tiles cut into key pieces that fill
+ * each workgroup's list to the same cost. The tiles, largest first, are laid
+ * into lists of capacity C in turn, a tile cut exactly where a list is full
+ * and continued in the next; a piece costs its slabs plus `overhead` steps
+ * (start-up, epilogue, and a publish / merge when the tile is cut), and C is
+ * the total cost over the workgroups a kv head gets (raised until the lists
+ * fit). The pieces of a tile merge (group = tile, partial slots contiguous);
+ * pl.items holds the pieces in slot order and `lists` each list's pieces. */
+static void plan_fb_fill(Plan &pl, int Hkv, int G, int window, int cu_count, std::vector<std::vector<int>> &lists) {
+    const int rows_per = 128, overhead = 3;
+    struct Tile { int batch, row0, lo, hi, n; };
+    std::vector<Tile> tiles;
+    long long total = 0;
+    for (int bi = 0; bi < (int)pl.sb.size(); bi++) {
+        const SkBatch &b = pl.sb[bi];
+        for (int r0 = 0; r0 < b.n_rows; r0 += rows_per) {
+            const int r1 = std::min(r0 + rows_per, b.n_rows) - 1;
+            int lo = b.key_lo, hi = b.key_hi;
+            if (b.causal) {
+                hi = std::min(hi, b.q_pos0 + r1 / G + 1);
+                if (window > 0) lo = std::max(lo, b.q_pos0 + r0 / G - window + 1);
+            }
+            lo = std::max(lo, 0) & ~(SMOL_SLAB - 1);
+            const int n = hi > lo ? (hi - lo + SMOL_SLAB - 1) / SMOL_SLAB : 0;
+            tiles.push_back({bi, r0, lo, std::max(hi, lo), n});
+            total += n + overhead;
+        }
+    }
+    std::stable_sort(tiles.begin(), tiles.end(), [](const Tile &a, const Tile &b) { return a.n > b.n; });
+    const int n_wg = std::max(1, cu_count / std::max(1, Hkv));
+    const int max_split = SK_MERGE_MAX / rows_per;
+    struct Piece { int tile, first, count; };
+    std::vector<std::vector<Piece>> bins;
+    for (double cap = std::max(1.0, (double)total / n_wg);; cap *= 1.02) {
+        bins.assign(1, {});
+        double room = cap;
+        bool ok = true;
+        for (int t = 0; t < (int)tiles.size() && ok; t++) {
+            int first = 0, made = 0;
+            do {
+                if (room < overhead + 1 && !bins.back().empty()) {
+                    bins.push_back({});
+                    room = cap;
+                }
+                const int left = tiles[t].n - first;
+                const int take = std::min(left, std::max(1, (int)(room - overhead)));
+                bins.back().push_back({t, first, take});
+                first += take;
+                room -= take + overhead;
+                if (++made > max_split) ok = false;
+            } while (first < tiles[t].n);
+        }
+        if (ok && (int)bins.size() <= n_wg) break;
+    }
+    /* items in slot order: a tile's pieces contiguous, in key order */
+    std::vector<std::vector<int>> pieces_of(tiles.size());
+    std::vector<std::pair<int, int>> where; /* (bin, index in bin) of each piece, by piece id */
+    std::vector<Piece> all;
+    for (int bi = 0; bi < (int)bins.size(); bi++)
+        for (int k = 0; k < (int)bins[bi].size(); k++) {
+            pieces_of[bins[bi][k].tile].push_back((int)all.size());
+            all.push_back(bins[bi][k]);
+            where.push_back({bi, k});
+        }
+    std::vector<int> slot(all.size());
+    pl.items.clear();
+    for (int t = 0; t < (int)tiles.size(); t++) {
+        const Tile &tl = tiles[t];
+        const SkBatch &sb = pl.sb[tl.batch];
+        const int ns = (int)pieces_of[t].size();
+        for (int sp = 0; sp < ns; sp++) {
+            const Piece &pc = all[pieces_of[t][sp]];
+            slot[pieces_of[t][sp]] = (int)pl.items.size();
+            const int kb = tl.lo + pc.first * SMOL_SLAB;
+            const int ke = sp == ns - 1 ? tl.hi : tl.lo + (pc.first + pc.count) * SMOL_SLAB;
+            pl.items.push_back({tl.batch, tl.row0, kb, std::max(kb, ke), t, ns, sp, sb.fresh_row0 - sb.fresh_pos0});
+        }
+    }
+    pl.n_groups = (int)tiles.size();
+    lists.assign(bins.size(), {});
+    for (int p = 0; p < (int)all.size(); p++) lists[where[p].first].push_back(slot[p]);
+}
+
 /* the pre-pass blocks with their batches */
 static std::vector<PrepBlockB> prep_records(const Plan &pl) {
     std::vector<PrepBlockB> r(pl.pblk.size());
@@ -724,7 +807,8 @@ static std::vector<PrepBlockB> prep_records(const Plan &pl) {
  * list with the least work so far: an item costs its steps (two slabs each,
  * one per key group) plus about six steps of start-up and epilogue. Item w
  * heads list w; `next` links the rest. */
-static std::vector<FbItem> fb_items(const Plan &pl, int n_wg, bool one_group) {
+static std::vector<FbItem> fb_items(const Plan &pl, int n_wg, bool one_group,
+                                    const std::vector<std::vector<int>> *given = nullptr) {
     const int n = (int)pl.items.size();
     auto record = [&](int i) {
         const SkItem &it = pl.items[i];
@@ -744,6 +828,11 @@ static std::vector<FbItem> fb_items(const Plan &pl, int n_wg, bool one_group) {
         for (int i = 0; i < n; i++) out[i] = record(i);
         return out;
     }
+    std::vector<std::vector<int>> lists;
+    if (given) {
+        lists = *given; /* the planner's lists (plan_fb_fill) */
+        n_wg = (int)lists.size();
+    } else {
     std::vector<int> order(n);
     for (int i = 0; i < n; i++) order[i] = i;
     auto cost = [&](int i) {
@@ -757,12 +846,13 @@ static std::vector<FbItem> fb_items(const Plan &pl, int n_wg, bool one_group) {
     using Load = std::pair<long long, int>; /* (work, list) */
     std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
     for (int w = 0; w < n_wg; w++) heap.push({0, w});
-    std::vector<std::vector<int>> lists(n_wg);
+    lists.assign(n_wg, {});
     for (int i : order) {
         Load l = heap.top();
         heap.pop();
         lists[l.second].push_back(i);
         heap.push({l.first + cost(i), l.second});
+    }
     }
     /* new index of every item: the heads first, then the rest list by list */
     std::vector<int> at(n, -1);
@@ -1056,8 +1146,9 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
         w = hd > 128 ? 1 : 2;
         rows_per = 64 * nt;
     }
-    if (fa) plan_items(pl, cs.Hkv, G, cs.window, rows_per, fb_one ? ctx->cu_count : ctx->cu_count * w, true,
-                       fb && !fb_one);
+    std::vector<std::vector<int>> fill_lists;
+    if (fb_one) plan_fb_fill(pl, cs.Hkv, G, cs.window, ctx->cu_count, fill_lists);
+    else if (fa) plan_items(pl, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, true, fb);
 
     /* workspace; precise QK^T (the default) adds the lo parts of the fp16 Q
      * scratch and of the fresh K */
@@ -1092,7 +1183,13 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     std::vector<FbItem> fbi;
     int fb_wg = std::max(1, ctx->cu_count / cs.Hkv);
     if (!((int)n_items > fb_wg && ctx->opt[SMOL_OPT_FB_LISTS] != -1)) fb_wg = 0;
-    if (fb) fbi = fb_items(pl, fb_wg, fb_one);
+    if (fb_one && ctx->opt[SMOL_OPT_FB_LISTS] != -1) {
+        /* one key group: the planner's filled lists, one workgroup each */
+        fb_wg = (int)fill_lists.size();
+        fbi = fb_items(pl, fb_wg, true, &fill_lists);
+    } else if (fb) {
+        fbi = fb_items(pl, fb_wg, fb_one);
+    }
 
     /* descriptor tables in one upload: pre-pass blocks and items, each with
      * its batch */
