@@ -109,6 +109,36 @@ SMOL_ATTN_API int smol_linear_qkv_norm_dev(smol_attn_ctx *ctx, float *q, float *
 SMOL_ATTN_API int smol_rms_norm_dev(smol_attn_ctx *ctx, float *out, const float *x, const float *weight,
                                     const float *residual, int seq, int dim, float eps);
 
+/* ---- the bf16 decoder's row operations ----------------------------------
+ *
+ * On bf16 arrays [seq][dim] (device pointers, enqueued on the context's
+ * stream), every result truncated to bf16 as common/decoder/qkn_bf16_decoder.c
+ * does. With bf() the widening of bf16 bits and tr() the truncation:
+ *   norm(v, w)[i] = tr((bf(v[i]) * r) * w[i]), r = 1 / sqrtf(sum_i bf(v[i])^2 / dim + eps)
+ * The sum of squares runs in a fixed order of its own, so a row can differ
+ * from the reference's in the last bit where a product lies on a bf16
+ * boundary. */
+
+/* out = norm(x, weight): bf16_rms_norm (qkn_bf16_decoder.c:51-71); out may
+ * equal x. */
+SMOL_ATTN_API int smol_bf16_rms_norm_dev(smol_attn_ctx *ctx, uint16_t *out, const uint16_t *x, const float *weight,
+                                         int seq, int dim, float eps);
+
+/* The step between two sublayers, one launch:
+ *   p non-NULL:         x = tr(bf(x) + bf(p_norm ? norm(p, p_norm) : p))
+ *   next_norm non-NULL: xn = norm(x, next_norm), of the updated x
+ * which is bf16_add_inplace (:255-258), optionally behind a post-sublayer
+ * norm and before the next input norm (:551-557, 567-570). p is not
+ * modified. xn may equal x only when p is NULL; no other arrays overlap. */
+SMOL_ATTN_API int smol_bf16_add_norm_dev(smol_attn_ctx *ctx, uint16_t *x, const uint16_t *p, const float *p_norm,
+                                         const float *next_norm, uint16_t *xn, int seq, int dim, float eps);
+
+/* out [seq][inter] = tr(gelu_tanh(bf(g)) * bf(u)) of the interleaved pairs
+ * gate_up [seq][2 * inter] (g = row[2j], u = row[2j + 1]): bf16_geglu
+ * (:235-251). gate_up 4-byte aligned; out does not overlap it. */
+SMOL_ATTN_API int smol_bf16_geglu_dev(smol_attn_ctx *ctx, uint16_t *out, const uint16_t *gate_up, int seq,
+                                      int inter);
+
 #ifdef __cplusplus
 }
 #endif

@@ -154,6 +154,24 @@ SMOL_ATTN_API int smol_qkn_layer_forward(const void *owner, int layer, int pos, 
                                          const smol_qkn_layer_weights *w, int dim, int intermediate, int act);
 SMOL_ATTN_API int smol_qkn_layer_prefill(const void *owner, int layer, int start_pos, int seq_len, float *x,
                                          const smol_qkn_layer_weights *w, int dim, int intermediate, int act);
+
+/* The bf16 decoder's whole layer (a binding with on_device = 1 and bf16 = 1):
+ * qkn_bf16_decoder_forward's layer loop (qkn_bf16_decoder.c:634-697) for one
+ * token at pos, qkn_bf16_decoder_prefill's (:482-571) for seq_len rows from
+ * start_pos. x [rows][dim] bf16, updated in place; every step truncates to
+ * bf16 (smol_linear.h's bf16 row operations, the bf16 projections and the
+ * bf16 attention block above):
+ *   xn = norm(x, input_norm); q, k, v = xn (Wq, Wk, Wv)^T
+ *   attn = the attention block; p = attn Wo^T
+ *   pre_ffn_norm set: x = x + norm(p, post_attn_norm); h = norm(x, pre_ffn_norm)
+ *   otherwise:        x = x + p;                         h = norm(x, post_attn_norm)
+ *   f = geglu(h Wgu^T) Wd^T, normed by post_ffn_norm when set; x = x + f
+ * The FFN is always GeGLU, as in the reference's bf16 decoder. Waiting
+ * behaviour as for the fp32 layer calls. */
+SMOL_ATTN_API int smol_qkn_layer_forward_bf16(const void *owner, int layer, int pos, uint16_t *x,
+                                              const smol_qkn_layer_weights *w, int dim, int intermediate);
+SMOL_ATTN_API int smol_qkn_layer_prefill_bf16(const void *owner, int layer, int start_pos, int seq_len, uint16_t *x,
+                                              const smol_qkn_layer_weights *w, int dim, int intermediate);
 SMOL_ATTN_API int smol_qkn_layer_synchronize(const void *owner);
 /* the binding's stream (a hipStream_t), for ordering the caller's own work */
 SMOL_ATTN_API void *smol_qkn_attn_stream(const void *owner);

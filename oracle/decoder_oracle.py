@@ -144,3 +144,41 @@ class Fp32Layer:
         if w.get("post_ffn_norm") is not None:
             f = o.rms_norm(f, w["post_ffn_norm"], eps)
         return (x + f).astype(np.float32)
+
+
+class Bf16Layer:
+    """A whole bf16 decoder layer around Bf16Block: qkn_bf16_decoder.c:634-697
+    (one token) / :482-571 (prefill). Every array is bf16 bits and every step
+    truncates its result to bf16 (orc_bf16_rms_norm, orc_bf16_linear_nobias,
+    orc_bf16_geglu, orc_bf16_add_inplace):
+
+      xn = norm(x, input_norm); q, k, v = xn Wq^T, xn Wk^T, xn Wv^T
+      a  = block(q, k, v); p = a Wo^T
+      pre_ffn_norm set: p = norm(p, post_attn_norm); x = x + p; h = norm(x, pre_ffn_norm)
+      otherwise:        x = x + p;                    h = norm(x, post_attn_norm)
+      f = geglu(h Wgu^T) Wd^T; f = norm(f, post_ffn_norm) when set; x = x + f
+
+    `weights[layer]` holds numpy arrays under the smol_qkn_layer_weights
+    names (bf16 bits for the projections, fp32 norm weights)."""
+
+    def __init__(self, orc, block, weights):
+        self.orc, self.block, self.w = orc, block, weights
+
+    def step(self, layer, start, x):
+        o, w, eps = self.orc, self.w[layer], self.block.eps
+        x = np.asarray(x, np.uint16)
+        xn = o.bf16_rms_norm(x, w["input_norm"], eps)
+        q, k, v = (o.bf16_linear_nobias(xn, w[n]) for n in ("wq", "wk", "wv"))
+        a = self.block.block(layer, start, q, k, v)
+        p = o.bf16_linear_nobias(a, w["wo"])
+        if w.get("pre_ffn_norm") is not None:
+            p = o.bf16_rms_norm(p, w["post_attn_norm"], eps)
+            x = o.bf16_add(x, p)
+            h = o.bf16_rms_norm(x, w["pre_ffn_norm"], eps)
+        else:
+            x = o.bf16_add(x, p)
+            h = o.bf16_rms_norm(x, w["post_attn_norm"], eps)
+        f = o.bf16_linear_nobias(o.bf16_geglu(o.bf16_linear_nobias(h, w["gate_up"])), w["down"])
+        if w.get("post_ffn_norm") is not None:
+            f = o.bf16_rms_norm(f, w["post_ffn_norm"], eps)
+        return o.bf16_add(x, f)

@@ -180,6 +180,9 @@ class Oracle(_Lib):
         self._swiglu = self._fn("swiglu", [_F, _F, ci, ci])
         self._geglu = self._fn("geglu", [_F, _F, ci, ci])
         self._bf16_linear = self._fn("bf16_linear_nobias", [_U16, _U16, _U16, ci, ci, ci])
+        self._bf16_rms = self._fn("bf16_rms_norm", [_U16, _U16, _F, ci, ci, cf])
+        self._bf16_geglu = self._fn("bf16_geglu", [_U16, _U16, ci, ci])
+        self._bf16_add = self._fn("bf16_add_inplace", [_U16, _U16, ctypes.c_size_t])
 
     def rms_norm(self, x, w, eps):
         """smol_rms_norm (rmsnorm.c:17-75) of rows x [seq, dim]"""
@@ -214,6 +217,29 @@ class Oracle(_Lib):
         u = lambda a: a.ctypes.data_as(_U16)  # noqa: E731
         self._bf16_linear(u(y), u(x), u(w), x.shape[0], x.shape[1], w.shape[0])
         return y
+
+    def bf16_rms_norm(self, x_bits, w, eps):
+        """bf16_rms_norm (qkn_bf16_decoder.c:51-71): bf16 bits rows [seq, dim] -> truncated bf16 bits"""
+        x = np.ascontiguousarray(x_bits, np.uint16)
+        y = np.zeros_like(x)
+        self._bf16_rms(y.ctypes.data_as(_U16), x.ctypes.data_as(_U16), _fp(_f32(w)), x.shape[0], x.shape[1],
+                       ctypes.c_float(eps))
+        return y
+
+    def bf16_geglu(self, gu_bits):
+        """bf16_geglu (qkn_bf16_decoder.c:235-251) of interleaved (gate, up) bf16 bits [seq, 2 * inter]"""
+        gu = np.ascontiguousarray(gu_bits, np.uint16)
+        y = np.zeros((gu.shape[0], gu.shape[1] // 2), np.uint16)
+        self._bf16_geglu(y.ctypes.data_as(_U16), gu.ctypes.data_as(_U16), gu.shape[0], gu.shape[1] // 2)
+        return y
+
+    def bf16_add(self, a_bits, b_bits):
+        """bf16_add_inplace (qkn_bf16_decoder.c:255-258): trunc(a + b) as new bf16 bits"""
+        a = np.array(a_bits, np.uint16, copy=True, order="C")
+        b = np.ascontiguousarray(b_bits, np.uint16)
+        assert a.size == b.size
+        self._bf16_add(a.ctypes.data_as(_U16), b.ctypes.data_as(_U16), a.size)
+        return a
 
     def set_vec_generic(self, on):
         self._generic(1 if on else 0)

@@ -36,6 +36,8 @@
  *       as smol_linear_bf16 / smol_linear_nobias_bf16 / smol_matmul_t_bf16 run
  *       them for seq_len > 1 (matmul.c:336-358, 419-429)
  *   orc_bf16_linear_nobias          common/decoder/qkn_bf16_decoder.c:99-117
+ *   orc_bf16_rms_norm / orc_bf16_geglu / orc_bf16_add_inplace
+ *                                   common/decoder/qkn_bf16_decoder.c:51-71, 235-251, 255-258
  *   orc_rms_norm                    common/kernels/rmsnorm.c:17-75 (the AVX-512 order
  *       of orc_rms_norm_per_head with the whole row as one head)
  *   orc_swiglu / orc_geglu          common/kernels/activation.c:55-88, 104-125
@@ -555,6 +557,35 @@ void orc_bf16_linear_nobias(uint16_t *y, const uint16_t *x, const uint16_t *W, i
             yr[o] = orc_f32_to_bf16_trunc(sum);
         }
     }
+}
+
+/* qkn_bf16_decoder.c:51-71 (bf16_rms_norm) on whole rows: out[s][i] =
+ * trunc((x[s][i] * r) * w[i]), r = 1 / sqrtf(ss / dim + eps), with the
+ * arithmetic of orc_bf16_rms_norm_per_head (the row as one head). out may
+ * equal x. */
+void orc_bf16_rms_norm(uint16_t *out, const uint16_t *x, const float *w, int seq, int dim, float eps) {
+    if (out != x) memcpy(out, x, (size_t)seq * dim * sizeof(uint16_t));
+    orc_bf16_rms_norm_per_head(out, w, seq, 1, dim, eps);
+}
+
+/* qkn_bf16_decoder.c:235-251 (bf16_geglu): g = gu[s][2j], u = gu[s][2j + 1]
+ * widened from bf16, out[s][j] = trunc(gelu_tanh(g) * u) with the GELU of
+ * orc_geglu (0.5 g (1 + tanh(0.7978845608028654 (g + 0.044715 g^3)))). */
+void orc_bf16_geglu(uint16_t *out, const uint16_t *gu, int seq, int inter) {
+    for (int s = 0; s < seq; s++)
+        for (int j = 0; j < inter; j++) {
+            float g = orc_bf16_to_f32(gu[(size_t)s * 2 * inter + 2 * j]);
+            float u = orc_bf16_to_f32(gu[(size_t)s * 2 * inter + 2 * j + 1]);
+            float x3 = g * g * g;
+            float inner = 0.7978845608028654f * (g + 0.044715f * x3);
+            g = 0.5f * g * (1.0f + tanhf(inner));
+            out[(size_t)s * inter + j] = orc_f32_to_bf16_trunc(g * u);
+        }
+}
+
+/* qkn_bf16_decoder.c:255-258 (bf16_add_inplace): a[i] = trunc(a[i] + b[i]) */
+void orc_bf16_add_inplace(uint16_t *a, const uint16_t *b, size_t n) {
+    for (size_t i = 0; i < n; i++) a[i] = orc_f32_to_bf16_trunc(orc_bf16_to_f32(a[i]) + orc_bf16_to_f32(b[i]));
 }
 
 /* rmsnorm.c:17-75: the same arithmetic as rmsnorm.c:78-140 per head, over

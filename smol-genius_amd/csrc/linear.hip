@@ -443,6 +443,87 @@ __global__ __launch_bounds__(256) void k_act_rows(float *y, const float *t, cons
     y[i] = res ? res[i] + v : v;
 }
 
+/* ---- the bf16 decoder's row operations (common/decoder/qkn_bf16_decoder.c)
+ * With bf(b) the bf16 bits b widened and tr(v) the truncation of v to bf16:
+ *   nrm(v, w)[i] = tr((bf(v[i]) * r) * w[i]), r = 1 / sqrtf(sum_i bf(v[i])^2 / dim + eps)
+ *                                                       (bf16_rms_norm, :51-71)
+ *   add(a, b)[i] = tr(bf(a[i]) + bf(b[i]))            (bf16_add_inplace, :255-258)
+ *   geglu(g, u)  = tr(0.5 g (1 + tanhf(0.7978845608028654 (g + 0.044715 g^3))) * u)
+ *                                                       (bf16_geglu, :235-251)
+ * The sums of squares run in a fixed order: per-thread strided fused
+ * multiply-adds, a butterfly over the wave, then the four waves in order. */
+
+__device__ __forceinline__ float bfw(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+__device__ __forceinline__ uint16_t bftr(float v) { return (uint16_t)(__float_as_uint(v) >> 16); }
+
+/* the sum of v over the 256 threads, returned to every thread */
+__device__ __forceinline__ float block_sum256(float v, float *red) {
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+    __syncthreads(); /* red may still be read by an earlier call */
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+/* One workgroup per row s of [seq][dim] bf16 arrays:
+ *   p non-NULL:     q = w_post ? nrm(p, w_post) : p;  x = add(x, q)  (x updated)
+ *   w_next non-NULL: xn = nrm(x, w_next)               (of the updated x)
+ * (the Gemma 3 post-sublayer norm, the residual add and the next sublayer's
+ * input norm, qkn_bf16_decoder.c:551-557 and 567-570, in one pass). xn may
+ * equal x only when p is NULL; each thread reads back only the elements it
+ * wrote itself. */
+__global__ __launch_bounds__(256) void k_bf16_rows(uint16_t *x, const uint16_t *p, const float *w_post,
+                                                   const float *w_next, uint16_t *xn, int dim, float eps) {
+    __shared__ float red[4];
+    const long long base = (long long)blockIdx.x * dim;
+    uint16_t *xr = x + base;
+    float ss = 0.0f;
+    if (p) {
+        const uint16_t *pr = p + base;
+        float rp = 0.0f;
+        if (w_post) {
+            float sp = 0.0f;
+            for (int i = threadIdx.x; i < dim; i += 256) {
+                const float v = bfw(pr[i]);
+                sp = fmaf(v, v, sp);
+            }
+            rp = 1.0f / sqrtf(block_sum256(sp, red) / (float)dim + eps);
+        }
+        for (int i = threadIdx.x; i < dim; i += 256) {
+            float q = bfw(pr[i]);
+            if (w_post) q = bfw(bftr((q * rp) * w_post[i]));
+            const uint16_t xb = bftr(bfw(xr[i]) + q);
+            xr[i] = xb;
+            const float v = bfw(xb);
+            ss = fmaf(v, v, ss);
+        }
+    } else if (w_next) {
+        for (int i = threadIdx.x; i < dim; i += 256) {
+            const float v = bfw(xr[i]);
+            ss = fmaf(v, v, ss);
+        }
+    }
+    if (!w_next) return;
+    const float r = 1.0f / sqrtf(block_sum256(ss, red) / (float)dim + eps);
+    uint16_t *nr = xn + base;
+    for (int i = threadIdx.x; i < dim; i += 256) nr[i] = bftr((bfw(xr[i]) * r) * w_next[i]);
+}
+
+/* out[i] = geglu(bf(gu[2i]), bf(gu[2i + 1])) over n = seq * inter outputs
+ * (row s's pair j sits at flat pair s * inter + j); every step rounded as
+ * written, no fused multiply-add */
+__global__ __launch_bounds__(256) void k_bf16_geglu(uint16_t *out, const uint32_t *gu, long long n) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t pr = gu[i];
+    const float g = __uint_as_float(pr << 16), u = __uint_as_float(pr & 0xffff0000u);
+    const float x3 = __fmul_rn(__fmul_rn(g, g), g);
+    const float inner = __fmul_rn(0.7978845608028654f, __fadd_rn(g, __fmul_rn(0.044715f, x3)));
+    const float gl = __fmul_rn(__fmul_rn(0.5f, g), __fadd_rn(1.0f, tanhf(inner)));
+    out[i] = bftr(__fmul_rn(gl, u));
+}
+
 /* ------------------------------------------------------------------ host */
 
 namespace {
@@ -957,6 +1038,60 @@ extern "C" int smol_rms_norm_dev(smol_attn_ctx *ctx, float *out, const float *x,
     if (e0) LHIP(hipEventRecord(e0, st));
     if (int rc = launch_rmsnorm(out, x, weight, seq, dim, eps, st, residual)) return rc;
     if (e1) LHIP(hipEventRecord(e1, st));
+    return 0;
+}
+
+extern "C" int smol_bf16_add_norm_dev(smol_attn_ctx *ctx, uint16_t *x, const uint16_t *p, const float *p_norm,
+                                      const float *next_norm, uint16_t *xn, int seq, int dim, float eps) {
+    if (!ctx) return lfail(SMOL_ATTN_ERR_ARG, "smol_bf16_add_norm_dev: null context");
+    if (seq < 0 || dim < 0) return lfail(SMOL_ATTN_ERR_ARG, "smol_bf16_add_norm_dev: negative size");
+    if (seq == 0 || dim == 0 || (!p && !next_norm)) return SMOL_ATTN_OK;
+    if (!x || (next_norm && !xn) || (p_norm && !p)) return lfail(SMOL_ATTN_ERR_ARG, "smol_bf16_add_norm_dev: null pointer");
+    const size_t bytes = (size_t)seq * dim * 2;
+    auto overlap = [bytes](const void *a, const void *b) {
+        return a && b && (const char *)a < (const char *)b + bytes && (const char *)b < (const char *)a + bytes;
+    };
+    if (overlap(x, p) || (p && overlap(xn, x)) || overlap(xn, p) || (xn && xn != x && overlap(xn, x)))
+        return lfail(SMOL_ATTN_ERR_ARG, "smol_bf16_add_norm_dev: overlapping arrays (xn may equal x only without p)");
+    LHIP(hipSetDevice(smol_internal_ctx_device(ctx)));
+    hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
+    hipLaunchKernelGGL(k_bf16_rows, dim3((unsigned)seq), dim3(256), 0, st, x, p, p_norm, next_norm, xn, dim, eps);
+    LHIP(hipGetLastError());
+    return 0;
+}
+
+extern "C" int smol_bf16_rms_norm_dev(smol_attn_ctx *ctx, uint16_t *out, const uint16_t *x, const float *weight,
+                                      int seq, int dim, float eps) {
+    if (!ctx) return lfail(SMOL_ATTN_ERR_ARG, "smol_bf16_rms_norm_dev: null context");
+    if (seq < 0 || dim < 0) return lfail(SMOL_ATTN_ERR_ARG, "smol_bf16_rms_norm_dev: negative size");
+    if (seq == 0 || dim == 0) return SMOL_ATTN_OK;
+    if (!out || !x || !weight) return lfail(SMOL_ATTN_ERR_ARG, "smol_bf16_rms_norm_dev: null pointer");
+    const size_t bytes = (size_t)seq * dim * 2;
+    if (out != x && (const char *)out < (const char *)x + bytes && (const char *)x < (const char *)out + bytes)
+        return lfail(SMOL_ATTN_ERR_ARG, "smol_bf16_rms_norm_dev: out partly overlaps x");
+    LHIP(hipSetDevice(smol_internal_ctx_device(ctx)));
+    hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
+    /* the kernel reads x through its residual pointer and writes xn; nothing is added */
+    hipLaunchKernelGGL(k_bf16_rows, dim3((unsigned)seq), dim3(256), 0, st, const_cast<uint16_t *>(x),
+                       (const uint16_t *)nullptr, (const float *)nullptr, weight, out, dim, eps);
+    LHIP(hipGetLastError());
+    return 0;
+}
+
+extern "C" int smol_bf16_geglu_dev(smol_attn_ctx *ctx, uint16_t *out, const uint16_t *gate_up, int seq, int inter) {
+    if (!ctx) return lfail(SMOL_ATTN_ERR_ARG, "smol_bf16_geglu_dev: null context");
+    if (seq < 0 || inter < 0) return lfail(SMOL_ATTN_ERR_ARG, "smol_bf16_geglu_dev: negative size");
+    if (seq == 0 || inter == 0) return SMOL_ATTN_OK;
+    if (!out || !gate_up) return lfail(SMOL_ATTN_ERR_ARG, "smol_bf16_geglu_dev: null pointer");
+    if ((uintptr_t)gate_up & 3) return lfail(SMOL_ATTN_ERR_ARG, "smol_bf16_geglu_dev: gate_up must be 4-byte aligned");
+    const long long n = (long long)seq * inter;
+    if ((const char *)out < (const char *)gate_up + n * 4 && (const char *)gate_up < (const char *)out + n * 2)
+        return lfail(SMOL_ATTN_ERR_ARG, "smol_bf16_geglu_dev: out overlaps gate_up");
+    LHIP(hipSetDevice(smol_internal_ctx_device(ctx)));
+    hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
+    hipLaunchKernelGGL(k_bf16_geglu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, out,
+                       reinterpret_cast<const uint32_t *>(gate_up), n);
+    LHIP(hipGetLastError());
     return 0;
 }
 

@@ -53,6 +53,7 @@ struct Binding {
     std::vector<float *> q_norm, k_norm; /* device [head_dim] or null */
     Buf q, k, v, out32, out16;           /* staging */
     Buf lq, lk, lv, la, lp, lg;          /* a whole layer's activations (smol_qkn_layer_*) */
+    Buf lx, lh;                          /* bf16 layer: normed input, GeGLU output */
 };
 
 std::mutex g_mu;
@@ -89,7 +90,7 @@ void release(Binding *b) {
         if (p) hipFree(p);
     for (float *p : b->k_norm)
         if (p) hipFree(p);
-    for (Buf *x : {&b->q, &b->k, &b->v, &b->out32, &b->out16, &b->lq, &b->lk, &b->lv, &b->la, &b->lp, &b->lg})
+    for (Buf *x : {&b->q, &b->k, &b->v, &b->out32, &b->out16, &b->lq, &b->lk, &b->lv, &b->la, &b->lp, &b->lg, &b->lx, &b->lh})
         if (x->p) hipFree(x->p);
     if (b->kv) smol_kv_cache_destroy(b->kv);
     if (b->rope_global) smol_rope_table_destroy(b->rope_global);
@@ -104,7 +105,7 @@ bool hd_ok(int hd) { return hd == 64 || hd == 72 || hd == 80 || hd == 96 || hd =
 /* The whole block for seq_len rows at start_pos (decode: one launch of the
  * direct decode kernel when seq_len == 1 and `decode` is set). */
 int run_block(Binding *b, int layer, int start_pos, int seq_len, const void *q, const void *k, const void *v,
-              void *attn_out, bool decode, bool sync = true) {
+              void *attn_out, bool decode, bool sync = true, bool own_qk = false) {
     const smol_qkn_attn_config &c = b->cfg;
     if (layer < 0 || layer >= c.n_layers) return qfail(SMOL_ATTN_ERR_ARG, "layer out of range");
     if (start_pos < 0 || seq_len <= 0) return qfail(SMOL_ATTN_ERR_ARG, "bad start_pos / seq_len");
@@ -122,9 +123,10 @@ int run_block(Binding *b, int layer, int start_pos, int seq_len, const void *q, 
 
     /* device inputs: the caller's arrays when they are on the device and are
      * only read; staged copies otherwise (the bf16 contract rounds Q and K in
-     * place, and the caller's inputs stay unmodified) */
+     * place, and the caller's inputs stay unmodified unless they are the
+     * layer step's own scratch, own_qk) */
     const void *dq = q, *dk = k, *dv = v;
-    const bool copy_qk = !c.on_device || c.bf16;
+    const bool copy_qk = !c.on_device || (c.bf16 && !own_qk);
     const hipMemcpyKind kind = c.on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
     if (copy_qk) {
         if ((rc = reserve(b, b->q, q_elems * es)) || (rc = reserve(b, b->k, kv_elems * es))) return rc;
@@ -246,6 +248,54 @@ int run_layer(Binding *b, int layer, int pos, int n, float *x, const smol_qkn_la
     return smol_linear_ops_dev(ctx, x, g, w->down, nullptr, n, inter, dim, &res);
 }
 
+/* One bf16 decoder layer on the device (qkn_bf16_decoder.c:634-697 for one
+ * token, :482-571 for a prefill), x [n][dim] bf16, updated in place; every
+ * step truncates to bf16:
+ *   xn = norm(x, input_norm)                                  k_bf16_rows
+ *   q, k, v = xn (Wq, Wk, Wv)^T                               one launch (n <= 4)
+ *   attention block of the binding (Q, K rounded in place)    run_block
+ *   p = attn Wo^T
+ *   x = x + (pre_ffn_norm ? norm(p, post_attn_norm) : p);
+ *   xn = norm(x, pre_ffn_norm or post_attn_norm)              k_bf16_rows
+ *   g = geglu(xn Wgu^T); f = g Wd^T
+ *   x = x + (post_ffn_norm ? norm(f, post_ffn_norm) : f)      k_bf16_rows */
+int run_layer_bf16(Binding *b, int layer, int pos, int n, uint16_t *x, const smol_qkn_layer_weights *w, int dim,
+                   int inter, bool decode) {
+    const smol_qkn_attn_config &c = b->cfg;
+    if (!c.on_device || !c.bf16)
+        return qfail(SMOL_ATTN_ERR_ARG, "the bf16 device layer step needs a binding with on_device = 1 and bf16 = 1");
+    if (layer < 0 || layer >= c.n_layers) return qfail(SMOL_ATTN_ERR_ARG, "layer out of range");
+    if (!x || !w || dim <= 0 || inter <= 0 || n <= 0 || pos < 0) return qfail(SMOL_ATTN_ERR_ARG, "bad layer arguments");
+    if (!w->input_norm || !w->wq || !w->wk || !w->wv || !w->wo || !w->post_attn_norm || !w->gate_up || !w->down)
+        return qfail(SMOL_ATTN_ERR_ARG, "a required layer weight is NULL");
+    QHIP(hipSetDevice(c.device));
+    const int q_dim = c.n_heads * c.head_dim, kv_dim = c.n_kv_heads * c.head_dim;
+    int rc;
+    if ((rc = reserve(b, b->lq, (size_t)n * q_dim * 2)) || (rc = reserve(b, b->lk, (size_t)n * kv_dim * 2)) ||
+        (rc = reserve(b, b->lv, (size_t)n * kv_dim * 2)) || (rc = reserve(b, b->la, (size_t)n * q_dim * 2)) ||
+        (rc = reserve(b, b->lp, (size_t)n * dim * 2)) || (rc = reserve(b, b->lg, (size_t)n * 2 * inter * 2)) ||
+        (rc = reserve(b, b->lx, (size_t)n * dim * 2)) || (rc = reserve(b, b->lh, (size_t)n * inter * 2)))
+        return rc;
+    uint16_t *q = (uint16_t *)b->lq.p, *k = (uint16_t *)b->lk.p, *v = (uint16_t *)b->lv.p;
+    uint16_t *attn = (uint16_t *)b->la.p, *p = (uint16_t *)b->lp.p, *gu = (uint16_t *)b->lg.p;
+    uint16_t *xn = (uint16_t *)b->lx.p, *g = (uint16_t *)b->lh.p;
+    smol_attn_ctx *ctx = b->ctx;
+    const int BF = SMOL_ATTN_BF16;
+    if ((rc = smol_bf16_rms_norm_dev(ctx, xn, x, w->input_norm, n, dim, c.eps))) return rc;
+    if ((rc = smol_linear_qkv_dev(ctx, q, k, v, BF, xn, BF, w->wq, w->wk, w->wv, n, dim, q_dim, kv_dim))) return rc;
+    if ((rc = run_block(b, layer, pos, n, q, k, v, attn, decode, !decode, true))) return rc;
+    if ((rc = smol_linear_dev(ctx, p, BF, attn, BF, w->wo, nullptr, n, q_dim, dim))) return rc;
+    if (w->pre_ffn_norm)
+        rc = smol_bf16_add_norm_dev(ctx, x, p, w->post_attn_norm, w->pre_ffn_norm, xn, n, dim, c.eps);
+    else
+        rc = smol_bf16_add_norm_dev(ctx, x, p, nullptr, w->post_attn_norm, xn, n, dim, c.eps);
+    if (rc) return rc;
+    if ((rc = smol_linear_dev(ctx, gu, BF, xn, BF, w->gate_up, nullptr, n, dim, 2 * inter))) return rc;
+    if ((rc = smol_bf16_geglu_dev(ctx, g, gu, n, inter))) return rc;
+    if ((rc = smol_linear_dev(ctx, p, BF, g, BF, w->down, nullptr, n, inter, dim))) return rc;
+    return smol_bf16_add_norm_dev(ctx, x, p, w->post_ffn_norm, nullptr, nullptr, n, dim, c.eps);
+}
+
 }  // namespace
 
 extern "C" int smol_qkn_layer_forward(const void *owner, int layer, int pos, float *x,
@@ -260,6 +310,20 @@ extern "C" int smol_qkn_layer_prefill(const void *owner, int layer, int start_po
     Binding *b = find(owner);
     if (!b) return qfail(SMOL_ATTN_ERR_ARG, "owner is not bound");
     return run_layer(b, layer, start_pos, seq_len, x, w, dim, intermediate, act, false);
+}
+
+extern "C" int smol_qkn_layer_forward_bf16(const void *owner, int layer, int pos, uint16_t *x,
+                                           const smol_qkn_layer_weights *w, int dim, int intermediate) {
+    Binding *b = find(owner);
+    if (!b) return qfail(SMOL_ATTN_ERR_ARG, "owner is not bound");
+    return run_layer_bf16(b, layer, pos, 1, x, w, dim, intermediate, true);
+}
+
+extern "C" int smol_qkn_layer_prefill_bf16(const void *owner, int layer, int start_pos, int seq_len, uint16_t *x,
+                                           const smol_qkn_layer_weights *w, int dim, int intermediate) {
+    Binding *b = find(owner);
+    if (!b) return qfail(SMOL_ATTN_ERR_ARG, "owner is not bound");
+    return run_layer_bf16(b, layer, start_pos, seq_len, x, w, dim, intermediate, false);
 }
 
 extern "C" int smol_qkn_layer_synchronize(const void *owner) {

@@ -83,6 +83,8 @@ SIGNATURES = [
     ("smol_qkn_attn_unbind", [_vp], _c_int),
     ("smol_qkn_layer_forward", [_vp, _c_int, _c_int, _vp, _vp, _c_int, _c_int, _c_int], _c_int),
     ("smol_qkn_layer_prefill", [_vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _c_int, _c_int], _c_int),
+    ("smol_qkn_layer_forward_bf16", [_vp, _c_int, _c_int, _vp, _vp, _c_int, _c_int], _c_int),
+    ("smol_qkn_layer_prefill_bf16", [_vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _c_int], _c_int),
     ("smol_qkn_layer_synchronize", [_vp], _c_int),
     ("smol_qkn_attn_stream", [_vp], _vp),
     # bf16-weight projections on device pointers (include/smol_linear.h)
@@ -91,6 +93,9 @@ SIGNATURES = [
                              _c_int], _c_int),
     ("smol_linear_ops_dev", [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp], _c_int),
     ("smol_rms_norm_dev", [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_float], _c_int),
+    ("smol_bf16_rms_norm_dev", [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_float], _c_int),
+    ("smol_bf16_add_norm_dev", [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_float], _c_int),
+    ("smol_bf16_geglu_dev", [_vp, _vp, _vp, _c_int, _c_int], _c_int),
     ("smol_linear_qkv_norm_dev", [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp,
                                   _c_float], _c_int),
     # reference-signature drop-ins (host fp32 arrays)
@@ -560,6 +565,18 @@ class QknAttn:
                                              ctypes.byref(weights.s), dim, inter, act), "smol_qkn_layer_prefill")
         return x
 
+    def layer_forward_bf16(self, layer, pos, x, weights, dim, inter):
+        """smol_qkn_layer_forward_bf16: x [1, dim] device bf16 bits, updated in place"""
+        _check(load().smol_qkn_layer_forward_bf16(self.addr, layer, pos, _dev(x, "x"), ctypes.byref(weights.s),
+                                                  dim, inter), "smol_qkn_layer_forward_bf16")
+        return x
+
+    def layer_prefill_bf16(self, layer, start_pos, x, weights, dim, inter):
+        _check(load().smol_qkn_layer_prefill_bf16(self.addr, layer, start_pos, x.shape[0], _dev(x, "x"),
+                                                  ctypes.byref(weights.s), dim, inter),
+               "smol_qkn_layer_prefill_bf16")
+        return x
+
     def synchronize(self):
         _check(load().smol_qkn_layer_synchronize(self.addr), "smol_qkn_layer_synchronize")
 
@@ -736,6 +753,41 @@ def rms_norm(ctx, x, weight, eps, out=None, residual=None):
     _check(load().smol_rms_norm_dev(ctx.h, _dev(out, "out"), _dev(x, "x"), _dev(weight, "weight"),
                                     _dev(residual, "residual") if residual is not None else None, seq, dim,
                                     ctypes.c_float(eps)), "smol_rms_norm_dev")
+    return out
+
+
+def bf16_rms_norm(ctx, x, weight, eps, out=None):
+    """smol_bf16_rms_norm_dev: bf16-bit rows [seq, dim] (int16 or bfloat16 tensor); out may be x"""
+    import torch
+    seq, dim = x.shape
+    if out is None:
+        out = torch.empty_like(x)
+    _check(load().smol_bf16_rms_norm_dev(ctx.h, _dev(out, "out"), _dev(x, "x"), _dev(weight, "weight"), seq, dim,
+                                         ctypes.c_float(eps)), "smol_bf16_rms_norm_dev")
+    return out
+
+
+def bf16_add_norm(ctx, x, p=None, p_norm=None, next_norm=None, eps=1e-6, xn=None):
+    """smol_bf16_add_norm_dev: x = x + (p_norm ? norm(p) : p) in place, then xn = norm(x, next_norm)"""
+    import torch
+    seq, dim = x.shape
+    if next_norm is not None and xn is None:
+        xn = torch.empty_like(x)
+    opt = lambda t, n: _dev(t, n) if t is not None else None  # noqa: E731
+    _check(load().smol_bf16_add_norm_dev(ctx.h, _dev(x, "x"), opt(p, "p"), opt(p_norm, "p_norm"),
+                                         opt(next_norm, "next_norm"), opt(xn, "xn"), seq, dim, ctypes.c_float(eps)),
+           "smol_bf16_add_norm_dev")
+    return xn
+
+
+def bf16_geglu(ctx, gate_up, out=None):
+    """smol_bf16_geglu_dev: bf16-bit rows [seq, 2 * inter] -> [seq, inter]"""
+    import torch
+    seq, two = gate_up.shape
+    if out is None:
+        out = torch.empty((seq, two // 2), dtype=gate_up.dtype, device=gate_up.device)
+    _check(load().smol_bf16_geglu_dev(ctx.h, _dev(out, "out"), _dev(gate_up, "gate_up"), seq, two // 2),
+           "smol_bf16_geglu_dev")
     return out
 
 

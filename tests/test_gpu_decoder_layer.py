@@ -5,12 +5,15 @@ attention block, SwiGLU / GeGLU, residual adds).
 
 Each case runs every layer over a prefill at position 0, then decode steps,
 then a rewind and a chunk, comparing the residual stream after every layer
-call with the path's bar |gpu - cpu| <= 2e-3 G + 1e-2 |cpu|. G is 1 for
-Qwen3-style layers. A Gemma 3 layer RMS-normalises the attention sublayer's
-output p before adding it, which multiplies the attention kernels' error
-(within their own bar, on fp16 operands) by 1 / rms(p); there G is the sum,
-over the layers run so far in the call, of max(1, 1 / rms(p)) as the oracle
-measures it.
+call with the bar |gpu - cpu| <= 2e-3 n + 1e-2 |cpu|, n the number of layers
+run so far in the call: each layer may add one attention-block error of
+its own (the block's bar is 2e-3 absolute on unit-scale rows) and carries the
+ones before it. The bar does not depend on the data. A Gemma 3 layer
+RMS-normalises the attention sublayer's output p before adding it, which
+scales that sublayer's error by 1 / rms(p); the oracle measures that gain
+(max(1, 1 / rms(p)), up to about 3.4 per layer on these inputs) and the test
+prints it with the ratio, as a record of how far the bar sits from the
+measured error.
 """
 import ctypes
 
@@ -108,9 +111,83 @@ def test_layer_sequence(sa, oracle, dorc, name, cfg, dim, inter, act, gemma, sli
                 G += model.gain
                 got = xd.cpu().numpy()
                 d = np.abs(got.astype(np.float64) - xm)
-                ratio = float((d / (2e-3 * G + 1e-2 * np.abs(xm))).max())
-                print("parity layer %s %s@%d L%d max_abs %.3e G %.2f ratio %.3f" % (
+                ratio = float((d / (2e-3 * (li + 1) + 1e-2 * np.abs(xm))).max())
+                print("parity layer %s %s@%d L%d max_abs %.3e gain_sum %.2f ratio %.3f" % (
                     name, kind, start, li, d.max(), G, ratio), flush=True)
                 assert np.isfinite(got).all() and ratio <= 1.0
+    finally:
+        blk.close()
+
+
+# (name, attention config, dim, intermediate, gemma 3 norms, sliding layers)
+BF16_CONFIGS = [
+    ("gemma3_small_bf16", dict(n_layers=2, n_heads=4, n_kv_heads=2, head_dim=128, eps=1e-6, rope_theta=1e6,
+                               rope_local_theta=1e4, rope_type=1, sliding_window=16, attn_logit_softcap=0.0),
+     320, 640, True, [1, 0]),
+    ("plain_bf16_softcap", dict(n_layers=2, n_heads=8, n_kv_heads=2, head_dim=64, eps=1e-6, rope_theta=1e4,
+                                rope_local_theta=0.0, rope_type=1, sliding_window=0, attn_logit_softcap=30.0),
+     256, 512, False, [0, 0]),
+]
+
+
+def _bits_to_f32(b):
+    return (np.ascontiguousarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+@pytest.mark.parametrize("name,cfg,dim,inter,gemma,sliding", BF16_CONFIGS, ids=[c[0] for c in BF16_CONFIGS])
+def test_bf16_layer_sequence(sa, oracle, dorc, name, cfg, dim, inter, gemma, sliding):
+    """The bf16 decoder's layer (smol_qkn_layer_prefill_bf16 / _forward_bf16)
+    against the oracle's Bf16Layer over the same prefill / decode / rewind
+    sequence. Every step of both truncates to bf16; the device sums the
+    projections and norms in another order, so a value that lies near a bf16
+    boundary can truncate one step apart, and such steps propagate. Bar per
+    element: |gpu - cpu| <= 2^-5 (|cpu| + rms of the cpu row), eight bf16
+    steps of the larger of the element and its row's scale; the share of
+    bit-equal elements is printed."""
+    H, Hkv, hd, L = cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["n_layers"]
+    owner = ctypes.create_string_buffer(256)
+    blk = sa.QknAttn(owner, **cfg, bf16=1, on_device=1, device=0, max_seq=64)
+    model_blk = dorc.Bf16Block(oracle, **cfg)
+    weights, dweights = [], []
+    for li in range(L):
+        s = 300 * (li + 1)
+        w = dict(input_norm=_norm_w(s, dim), wq=_proj(s + 1, H * hd, dim), wk=_proj(s + 2, Hkv * hd, dim),
+                 wv=_proj(s + 3, Hkv * hd, dim), wo=_proj(s + 4, dim, H * hd), post_attn_norm=_norm_w(s + 5, dim),
+                 pre_ffn_norm=_norm_w(s + 6, dim) if gemma else None,
+                 post_ffn_norm=_norm_w(s + 7, dim) if gemma else None,
+                 gate_up=_proj(s + 8, 2 * inter, dim), down=_proj(s + 9, dim, inter))
+        qn, kn = _norm_w(s + 10, hd), _norm_w(s + 11, hd)
+        blk.set_layer(li, sliding[li], qn, kn)
+        model_blk.set_layer(li, sliding[li], qn, kn)
+        weights.append(w)
+
+        def d(a):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a)
+            return torch.from_numpy(a.view(np.int16) if a.dtype == np.uint16 else a).cuda()
+        dweights.append(sa.QknLayerWeights(**{k: d(v) for k, v in w.items()}))
+    model = dorc.Bf16Layer(oracle, model_blk, weights)
+    try:
+        for step, (kind, start, rows) in enumerate(SEQUENCE):
+            x = synth.f32_to_bf16_bits(synth.normal(7100 + step, (rows, dim)))
+            xd = torch.from_numpy(x.view(np.int16)).cuda()
+            xm = x
+            for li in range(L):
+                print("bf16 layer %s %s start %d rows %d layer %d" % (name, kind, start, rows, li), flush=True)
+                if kind == "prefill":
+                    blk.layer_prefill_bf16(li, start, xd, dweights[li], dim, inter)
+                else:
+                    blk.layer_forward_bf16(li, start, xd, dweights[li], dim, inter)
+                blk.synchronize()
+                xm = model.step(li, start, xm)
+                got = xd.cpu().numpy().view(np.uint16)
+                gf, cf = _bits_to_f32(got).astype(np.float64), _bits_to_f32(xm).astype(np.float64)
+                d = np.abs(gf - cf)
+                rms = np.sqrt((cf ** 2).mean(1, keepdims=True))
+                ratio = float((d / (2.0 ** -5 * (np.abs(cf) + rms))).max())
+                print("parity bf16 layer %s %s@%d L%d max_abs %.3e equal %.4f ratio %.3f" % (
+                    name, kind, start, li, d.max(), float((got == xm).mean()), ratio), flush=True)
+                assert np.isfinite(gf).all() and ratio <= 1.0
     finally:
         blk.close()

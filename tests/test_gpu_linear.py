@@ -330,3 +330,59 @@ def test_rms_norm_dev(ctx, sa, oracle):
         sa.rms_norm(ctx, xd, dev(w), 1e-6, out=xd)   # in place
         ctx.synchronize()
         np.testing.assert_allclose(xd.cpu().numpy(), ref, rtol=2e-6, atol=1e-6)
+
+
+def _step_diff(a, b):
+    """|a - b| in bf16 steps of the bits (same-sign values)"""
+    return np.abs(np.asarray(a, np.uint16).astype(np.int32) - np.asarray(b, np.uint16).astype(np.int32))
+
+
+def test_bf16_row_ops(ctx, sa, oracle):
+    """smol_bf16_rms_norm_dev / smol_bf16_add_norm_dev / smol_bf16_geglu_dev
+    against the oracle's bf16_rms_norm, bf16_add and bf16_geglu. The device
+    sums squares in another order and calls the device tanhf, so a result
+    that lies on a truncation boundary may come out one bf16 step away: the
+    bar is at most one step, with at least 99% of the elements bit-equal."""
+    for seq, dim in [(1, 1024), (3, 72), (2, 7), (40, 320), (1536, 1024)]:
+        print("bf16 rows", seq, dim, flush=True)
+        x = synth.f32_to_bf16_bits(synth.normal(90 + dim, (seq, dim), 3.0))
+        p = synth.f32_to_bf16_bits(synth.normal(91 + dim, (seq, dim), 0.5))
+        w1 = (1.0 + 0.1 * synth.normal(92 + dim, (dim,))).astype(np.float32)
+        w2 = (1.0 + 0.1 * synth.normal(93 + dim, (dim,))).astype(np.float32)
+        ref = oracle.bf16_rms_norm(x, w1, 1e-6)
+        xd = dev_bits(x)
+        got = sa.bf16_rms_norm(ctx, xd, dev(w1), 1e-6).cpu().numpy().view(np.uint16)
+        d = _step_diff(got, ref)
+        assert d.max() <= 1 and (d == 0).mean() >= 0.99, (d.max(), (d == 0).mean())
+        sa.bf16_rms_norm(ctx, xd, dev(w1), 1e-6, out=xd)  # in place
+        assert (xd.cpu().numpy().view(np.uint16) == got).all()
+        # x = x + norm(p, w1); xn = norm(x, w2), the bf16 Gemma 3 step
+        xd = dev_bits(x)
+        xn = sa.bf16_add_norm(ctx, xd, dev_bits(p), dev(w1), dev(w2), 1e-6)
+        ctx.synchronize()
+        q_ref = oracle.bf16_rms_norm(p, w1, 1e-6)
+        x_ref = oracle.bf16_add(x, q_ref)
+        x_got = xd.cpu().numpy().view(np.uint16)
+        # a step of the normed p carries into the sum at its own size, which
+        # is more than a step of the sum where x and p cancel
+        err = np.abs(synth.bf16_bits_to_f32(x_got).astype(np.float64) - synth.bf16_bits_to_f32(x_ref))
+        bar = 2.0 ** -7 * (np.abs(synth.bf16_bits_to_f32(x_ref)) + np.abs(synth.bf16_bits_to_f32(q_ref)))
+        assert (err <= bar).all() and (x_got == x_ref).mean() >= 0.99
+        # the second norm, of the x the device computed
+        d = _step_diff(xn.cpu().numpy().view(np.uint16), oracle.bf16_rms_norm(x_got, w2, 1e-6))
+        assert d.max() <= 1 and (d == 0).mean() >= 0.99
+        # plain residual add (no norms): exact
+        xd = dev_bits(x)
+        sa.bf16_add_norm(ctx, xd, dev_bits(p))
+        ctx.synchronize()
+        assert (xd.cpu().numpy().view(np.uint16) == oracle.bf16_add(x, p)).all()
+    for seq, inter in [(1, 3072), (5, 13), (1536, 3072)]:
+        print("bf16 geglu", seq, inter, flush=True)
+        gu = synth.f32_to_bf16_bits(synth.normal(95 + inter, (seq, 2 * inter), 2.0))
+        ref = oracle.bf16_geglu(gu)
+        got = sa.bf16_geglu(ctx, dev_bits(gu)).cpu().numpy().view(np.uint16)
+        gf, rf = synth.bf16_bits_to_f32(got).astype(np.float64), synth.bf16_bits_to_f32(ref).astype(np.float64)
+        g, u = synth.bf16_bits_to_f32(gu[:, 0::2]), synth.bf16_bits_to_f32(gu[:, 1::2])
+        # one bf16 step, plus, where 1 + tanh cancels, an ulp of 1 times 0.5 g u
+        bar = 2.0 ** -7 * np.abs(rf) + 2.0 ** -22 * np.abs(0.5 * g * u)
+        assert (np.abs(gf - rf) <= bar).all() and (got == ref).mean() >= 0.99

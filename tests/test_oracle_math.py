@@ -445,3 +445,60 @@ def test_bf16_norm_rope_planted_mistakes_are_caught(oracle):
     cn, sn = c[pos][:, None, :hd // 2], s[pos][:, None, :hd // 2]
     neox = np.stack([xn[:, :, 0] * cn - xn[:, :, 1] * sn, xn[:, :, 1] * cn + xn[:, :, 0] * sn], 2)
     assert (tr(neox).reshape(seq, H, hd // 2, 2) != rot).any()
+
+
+@pytest.mark.parametrize("dim,eps", [(24, 1e-6), (40, 0.5)])
+def test_bf16_row_norm_brute_force(oracle, dim, eps):
+    """bf16_rms_norm over whole rows is the per-head norm with the row as one
+    head: exact rational arithmetic, each step rounded to float32."""
+    seq = 3
+    x = _bf16_inputs(110 + dim, (seq, dim))
+    w = (1.0 + 0.25 * np.random.default_rng(111).standard_normal(dim)).astype(np.float32)
+    got = oracle.bf16_rms_norm(x, w, eps)
+    np.testing.assert_array_equal(got, _bf16_norm_exact(x, w, seq, 1, dim, eps))
+    # a per-head norm over halves of the row gives different bits
+    assert (oracle.bf16_rms_norm_per_head(x, w[:dim // 2], seq, 2, dim // 2, eps) != got).any()
+
+
+def test_bf16_add_exact(oracle):
+    """trunc(a + b): the float32 sum of two bf16 values is correctly rounded
+    by numpy, so the truncated bits are fixed; rounding to nearest differs."""
+    a = _bf16_inputs(120, (4, 64))
+    b = _bf16_inputs(121, (4, 64))
+    got = oracle.bf16_add(a, b)
+    s = synth.bf16_bits_to_f32(a) + synth.bf16_bits_to_f32(b)
+    np.testing.assert_array_equal(got, (s.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16))
+    assert (synth.f32_to_bf16_bits(s.astype(np.float32)) != got).any()
+
+
+def test_bf16_geglu_against_float64(oracle):
+    """trunc(gelu_tanh(g) * u) within one bf16 step of the same formula
+    evaluated step by step in numpy float32 (its tanh may differ from the C
+    library's by an ulp), equal on most elements; planted mistakes (gate and
+    up swapped, rounding to nearest, the erf GELU) are caught. (float64 is no
+    reference here: for g below about -5, 1 + tanh cancels to 0 in float32.)"""
+    inter = 256
+    gu = _bf16_inputs(130, (3, 2 * inter))
+    got = oracle.bf16_geglu(gu)
+    v = synth.bf16_bits_to_f32(gu)
+    g, u = v[:, 0::2], v[:, 1::2]
+    f = np.float32
+
+    def gelu(a):
+        inner = f(0.7978845608028654) * (a + f(0.044715) * (a * a * a))
+        return f(0.5) * a * (f(1.0) + np.tanh(inner))
+
+    tr = lambda a: (a.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)  # noqa: E731
+    want = tr(gelu(g) * u)
+    d = np.abs(want.astype(np.int32) - got.astype(np.int32))
+    assert (d == 0).mean() > 0.95
+    # one bf16 step, plus, where 1 + tanh cancels, an ulp of 1 times 0.5 g u
+    err = np.abs(synth.bf16_bits_to_f32(got).astype(np.float64) - synth.bf16_bits_to_f32(want))
+    bar = 2.0 ** -7 * np.abs(synth.bf16_bits_to_f32(want)) + 2.0 ** -22 * np.abs(0.5 * g * u)
+    assert (err <= bar).all()
+    assert (np.abs(tr(gelu(u) * g).astype(np.int32) - got.astype(np.int32)) > 1).any()
+    assert (synth.f32_to_bf16_bits((gelu(g) * u).astype(np.float32)) != got).any()
+    from scipy.special import erf
+    g64 = g.astype(np.float64)
+    gelu_erf = 0.5 * g64 * (1.0 + erf(g64 / np.sqrt(2.0)))
+    assert (np.abs(tr(gelu_erf * u).astype(np.int32) - got.astype(np.int32)) > 1).any()
