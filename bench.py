@@ -281,6 +281,23 @@ def measure_decoder(ctx, sa, steps, warmup, prefix=1024, n_layers=28, dim=1024, 
         wall = time.perf_counter() - t0
     finally:
         gc.enable()
+    # the same steps replayed from one HIP graph of the 28-layer step (two launches per token)
+    graph = sa.QknStepGraph(blk, xt, W, dim, inter, 1, pos + warmup + steps + 8)
+    gc.disable()
+    try:
+        for _ in range(warmup):
+            graph.launch(pos)
+            pos += 1
+        blk.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            graph.launch(pos)
+            pos += 1
+        blk.synchronize()
+        wall_graph = time.perf_counter() - t0
+    finally:
+        gc.enable()
+        graph.close()
     wbytes = n_layers * 2 * dim * (H * hd + 2 * Hkv * hd + H * hd + 3 * inter)
     kv_bytes = n_layers * 2 * Hkv * hd * 2 * (prefix + warmup + steps / 2)
     ms_tok = wall / steps * 1e3
@@ -288,13 +305,17 @@ def measure_decoder(ctx, sa, steps, warmup, prefix=1024, n_layers=28, dim=1024, 
                     "intermediate": inter, "cached_tokens": prefix, "weights": "random bf16 on the device"},
          "ms_per_token": round(ms_tok, 4), "tokens_per_s": round(1e3 / ms_tok, 1),
          "launches_per_token": 5 * n_layers,
+         "graph_ms_per_token": round(wall_graph / steps * 1e3, 4),
+         "graph_tokens_per_s": round(steps / wall_graph, 1),
+         "graph_launches_per_token": 2,
          "hbm_GBps_per_token": round((wbytes + kv_bytes) / (wall / steps) / 1e9, 1),
          "bytes_per_token": int(wbytes + kv_bytes),
          "prefill_tokens_per_s": round(prefix / prefill_s, 1),
          "prefill_ms_%d_tokens" % prefix: round(prefill_s * 1e3, 3),
          "prefill_ms_first_call": round(prefill_cold * 1e3, 3),
          "note": "decode: 28 layers per token, norms/activation/residuals fused into the projections, "
-                 "one host wait per timed run; prefill: 28 smol_qkn_layer_prefill calls, each waiting for its "
+                 "one host wait per timed run; graph_*: the same step captured once "
+                 "(smol_qkn_step_graph_create) and replayed per token; prefill: 28 smol_qkn_layer_prefill calls, each waiting for its "
                  "attention block"}
     blk.close()
     del W, x, xt

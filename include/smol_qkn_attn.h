@@ -173,6 +173,38 @@ SMOL_ATTN_API int smol_qkn_layer_forward_bf16(const void *owner, int layer, int 
 SMOL_ATTN_API int smol_qkn_layer_prefill_bf16(const void *owner, int layer, int start_pos, int seq_len, uint16_t *x,
                                               const smol_qkn_layer_weights *w, int dim, int intermediate);
 SMOL_ATTN_API int smol_qkn_layer_synchronize(const void *owner);
+
+/* ---- a whole decode step as one HIP graph -------------------------------
+ *
+ * No counterpart in the reference: qkn_decoder_forward's per-token layer
+ * loop issues five device launches per layer through the calls above; a
+ * step graph captures the loop over every layer once and replays it, so a
+ * token costs two launches (a one-thread kernel that writes the position,
+ * then the graph). For a binding with on_device = 1 and bf16 = 0:
+ *
+ *   create: sizes the cache, the RoPE tables and the layer buffers for
+ *           positions [0, max_pos), then captures smol_qkn_layer_forward of
+ *           layers 0 .. n_layers - 1 on x [1][dim] (device fp32, the residual
+ *           stream) with the weights w[0 .. n_layers - 1]. The decode launches
+ *           are planned for a key length of max_pos (a shorter sequence runs
+ *           the same workgroups, some of them over no keys) and keep their
+ *           split partials and flags in the graph's own device memory.
+ *   launch: one decode step at pos (0 <= pos < max_pos), exactly what the
+ *           layer loop of smol_qkn_layer_forward calls at pos computes. x, the
+ *           weights and the binding's norms must be the captured ones, still
+ *           allocated; the call fails (SMOL_ATTN_ERR_ARG) when a layer buffer,
+ *           the cache or a RoPE table of the binding was reallocated since
+ *           the capture (a longer prefill, for instance): create it again.
+ *   destroy: waits for the binding's stream, then frees the graph.
+ *
+ * Launches are enqueued on the binding's stream and return without waiting;
+ * smol_qkn_layer_synchronize waits and reports a merge time-out. One graph is
+ * replayed by one thread at a time. */
+typedef struct smol_qkn_step_graph smol_qkn_step_graph;
+SMOL_ATTN_API int smol_qkn_step_graph_create(const void *owner, float *x, const smol_qkn_layer_weights *w, int dim,
+                                             int intermediate, int act, int max_pos, smol_qkn_step_graph **out);
+SMOL_ATTN_API int smol_qkn_step_graph_launch(smol_qkn_step_graph *g, int pos);
+SMOL_ATTN_API int smol_qkn_step_graph_destroy(smol_qkn_step_graph *g);
 /* the binding's stream (a hipStream_t), for ordering the caller's own work */
 SMOL_ATTN_API void *smol_qkn_attn_stream(const void *owner);
 

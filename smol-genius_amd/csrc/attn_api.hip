@@ -158,6 +158,22 @@ struct PinnedSlot {
 #define SMOL_RING 16
 #define SMOL_TIMING_KINDS 3 /* 0: pre-pass, 1: attention, 2: other */
 
+/* Decode launches captured into a HIP graph read their sequence record and
+ * their epoch's high bits from this state's device memory, so one graph
+ * replays at any position up to the planning position: before each replay
+ * the host launches k_gdec_step, which writes the position and advances the
+ * step counter. The partial slots are the state's own (never shared with
+ * uncaptured launches, whose epochs come from the host). */
+struct smol_graph_dec {
+    int device = 0;
+    void *mem = nullptr; /* [0, 64): the sequence record; [64, 68): the step counter; slots from 256 */
+    DecSeq *seqs = nullptr;
+    unsigned *step = nullptr;
+    float *part = nullptr;
+    size_t part_bytes = 0;
+    int plan_pos = 0;
+};
+
 struct smol_attn_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -192,6 +208,11 @@ struct smol_attn_ctx {
     std::vector<hipEvent_t> event_pool;
     double t_ms[SMOL_TIMING_KINDS] = {0, 0, 0};
     int t_count[SMOL_TIMING_KINDS] = {0, 0, 0};
+    /* set while a caller captures decode launches into a HIP graph
+     * (smol_internal_gdec_capture): k_dec then reads its positions and epoch
+     * from this state's device memory */
+    smol_graph_dec *gdec = nullptr;
+    bool timing_saved = false; /* timing is off while a capture runs */
     /* state of the projection GEMMs (linear.hip), released with the context */
     void *lin = nullptr;
     void (*lin_free)(void *) = nullptr;
@@ -982,6 +1003,10 @@ static void plan_decode(smol_attn_ctx *ctx, const DecCall &dc, int Hkv, int wind
 }
 
 /* Plans and launches k_dec for the sequences of `dc` */
+/* a partial slot's floats: O [TR][hd], (m, l) [TR][2], then the flag alone
+ * in the slot's last 128-byte line; 256-byte aligned */
+static int dec_slot_floats(int hd, int TR) { return ((((TR * (hd + 2) + 31) & ~31) + 32) + 63) & ~63; }
+
 static int run_decode(smol_attn_ctx *ctx, const CallShape &cs, const DecCall &dc) {
     const int hd = cs.hd, G = cs.Hq / cs.Hkv;
     int max_q = 0;
@@ -997,11 +1022,26 @@ static int run_decode(smol_attn_ctx *ctx, const CallShape &cs, const DecCall &dc
     /* partial slots: O [TR][hd], (m, l) [TR][2], then the flag alone in the
      * slot's last 128-byte line (the merger polls that line device-coherently
      * and reads the others through L2); 256-byte aligned */
-    const int slot_floats = ((((TR * (hd + 2) + 31) & ~31) + 32) + 63) & ~63;
+    const int slot_floats = dec_slot_floats(hd, TR);
     const size_t n_groups = dc.seqs.size() * cs.Hkv * n_rb;
     const size_t part_bytes = n_groups * DEC_MAX_SPLIT * slot_floats * 4;
     DecCall whole_dc;
     const DecCall *pdc = &dc;
+    smol_graph_dec *gd = ctx->gdec;
+    if (gd) {
+        /* captured: one sequence, planned at the state's planning position
+         * (every position up to it runs the same items; splits past a
+         * shorter sequence's keys are empty) */
+        if (!dc.direct || dc.noalloc || dc.seqs.size() != 1)
+            return fail(SMOL_ATTN_ERR_UNSUPPORTED, "a captured decode is one sequence's direct decode step");
+        if (cs.layer + 1 > 255) return fail(SMOL_ATTN_ERR_UNSUPPORTED, "captured decode: layer %d > 254", cs.layer);
+        if (part_bytes > gd->part_bytes)
+            return fail(SMOL_ATTN_ERR_UNSUPPORTED, "captured decode: %zu partial bytes, the state holds %zu",
+                        part_bytes, gd->part_bytes);
+        whole_dc = dc;
+        whole_dc.seqs[0].pos = std::max(dc.seqs[0].pos, gd->plan_pos);
+        pdc = &whole_dc;
+    }
     if (dc.noalloc && part_bytes > SMOL_ATTN_NOALLOC_SCRATCH_BYTES) {
         /* the scratch cannot hold every group's split slots: no splits */
         whole_dc = dc;
@@ -1020,6 +1060,9 @@ static int run_decode(smol_attn_ctx *ctx, const CallShape &cs, const DecCall &dc
         pdc = &whole_dc;
         plan_decode(ctx, *pdc, cs.Hkv, cs.window, n_rb, fit, min_per, items);
     }
+    if (gd && items.size() > DEC_ARG_ITEMS)
+        return fail(SMOL_ATTN_ERR_UNSUPPORTED, "captured decode: %d workgroups exceed the kernel arguments' %d",
+                    (int)items.size(), DEC_ARG_ITEMS);
     if (dc.noalloc && (items.size() > DEC_ARG_ITEMS || dc.seqs.size() > DEC_ARG_SEQS))
         return fail(SMOL_ATTN_ERR_UNSUPPORTED, "%d sequences / %d workgroups exceed what the no-alloc decode passes "
                     "in its kernel arguments (%d / %d)", (int)dc.seqs.size(), (int)items.size(), DEC_ARG_SEQS,
@@ -1060,7 +1103,13 @@ static int run_decode(smol_attn_ctx *ctx, const CallShape &cs, const DecCall &dc
     dp.spin_limit = ctx->opt[SMOL_OPT_DEC_SPIN] > 0 ? ctx->opt[SMOL_OPT_DEC_SPIN] : DEC_SPIN_LIMIT;
     dp.fault_merge = ctx->opt[SMOL_OPT_FAULT_MERGE] ? 1 : 0;
     int rc;
-    if (dc.noalloc) {
+    if (gd) {
+        /* the state's own slots; the epoch's high bits come from its step
+         * counter, the low 8 bits tell this launch from the step's others */
+        dp.part = gd->part;
+        dp.epoch = (unsigned)cs.layer + 1;
+        dp.step_dev = gd->step;
+    } else if (dc.noalloc) {
         /* the per-device scratch: its flags hold earlier calls' epochs (or
          * zero), never this call's, which comes from the device's counter */
         ScratchDev &sd = g_scratch[ctx->device];
@@ -1083,6 +1132,7 @@ static int run_decode(smol_attn_ctx *ctx, const CallShape &cs, const DecCall &dc
     const bool items_arg = items.size() <= DEC_ARG_ITEMS, seqs_arg = dc.seqs.size() <= DEC_ARG_SEQS;
     if (items_arg) memcpy(dp.items, items.data(), items.size() * sizeof(DecItem));
     if (seqs_arg) memcpy(dp.seqs, dc.seqs.data(), dc.seqs.size() * sizeof(DecSeq));
+    if (gd) dp.seqs_dev = gd->seqs;
     if (!items_arg || !seqs_arg) {
         const size_t o_seq = ((items_arg ? 0 : items.size() * sizeof(DecItem)) + 255) & ~(size_t)255;
         std::vector<unsigned char> host(o_seq + (seqs_arg ? 0 : dc.seqs.size() * sizeof(DecSeq)));
@@ -1092,13 +1142,85 @@ static int run_decode(smol_attn_ctx *ctx, const CallShape &cs, const DecCall &dc
         if (!items_arg) dp.items_dev = (const DecItem *)ctx->desc.p;
         if (!seqs_arg) dp.seqs_dev = (const DecSeq *)((unsigned char *)ctx->desc.p + o_seq);
     }
-    const int mk = dc.noalloc ? -1 : timing_begin(ctx, 1);
+    const int mk = dc.noalloc || gd ? -1 : timing_begin(ctx, 1);
     hipEvent_t e0 = mk >= 0 ? ctx->marks[mk].a : nullptr, e1 = mk >= 0 ? ctx->marks[mk].b : nullptr;
     rc = smol_launch_decode(&dp, hd, rows, nw, ctx->stream, e0, e1);
     if (rc)
         return fail(rc == -1 ? SMOL_ATTN_ERR_UNSUPPORTED : SMOL_ATTN_ERR_DEVICE, "k_dec launch (hd %d, %d rows): %s", hd,
                     rows, rc == -1 ? "unsupported configuration" : hipGetErrorString(hipGetLastError()));
     return SMOL_ATTN_OK;
+}
+
+__global__ __launch_bounds__(64) void k_gdec_step(DecSeq *seqs, unsigned *step, int pos, int slot) {
+    if (threadIdx.x == 0) {
+        DecSeq q;
+        q.pos = pos;
+        q.slot = slot;
+        q.tok0 = 0;
+        q.n_q = 1;
+        seqs[0] = q;
+        *step = *step + 1;
+    }
+}
+
+/* for qkn_attn.hip: the state of captured single-sequence decode launches
+ * with n_heads query heads over n_kv_heads cache heads of head_dim hd,
+ * planned at plan_pos (allocated and cleared here, before any capture) */
+extern "C" int smol_internal_gdec_create(smol_attn_ctx *ctx, int n_heads, int n_kv_heads, int hd, int plan_pos,
+                                         smol_graph_dec **out) {
+    if (!ctx || !out || n_kv_heads <= 0 || n_heads % n_kv_heads || plan_pos < 0)
+        return fail(SMOL_ATTN_ERR_ARG, "graph decode state: bad arguments");
+    *out = nullptr;
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    const int rows = n_heads / n_kv_heads, TR = dec_tile_rows(hd, rows), n_rb = (rows + TR - 1) / TR;
+    auto *g = new smol_graph_dec();
+    g->device = ctx->device;
+    g->plan_pos = plan_pos;
+    g->part_bytes = (size_t)n_kv_heads * n_rb * DEC_MAX_SPLIT * dec_slot_floats(hd, TR) * 4;
+    const size_t bytes = 256 + g->part_bytes;
+    hipError_t e = hipMalloc(&g->mem, bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(g->mem, 0, bytes, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        if (g->mem) hipFree(g->mem);
+        delete g;
+        return fail(SMOL_ATTN_ERR_NOMEM, "graph decode state: %s", hipGetErrorString(e));
+    }
+    g->seqs = static_cast<DecSeq *>(g->mem);
+    g->step = reinterpret_cast<unsigned *>(static_cast<char *>(g->mem) + 64);
+    g->part = reinterpret_cast<float *>(static_cast<char *>(g->mem) + 256);
+    *out = g;
+    return SMOL_ATTN_OK;
+}
+
+/* frees the state; the caller has drained every stream that replays it */
+extern "C" void smol_internal_gdec_destroy(smol_graph_dec *g) {
+    if (!g) return;
+    hipSetDevice(g->device);
+    if (g->mem) hipFree(g->mem);
+    delete g;
+}
+
+/* g non-null: decode launches of this context are being captured with g's
+ * state (and per-launch timing is off); null: capture ended */
+extern "C" void smol_internal_gdec_capture(smol_attn_ctx *ctx, smol_graph_dec *g) {
+    if (g && !ctx->gdec) {
+        ctx->timing_saved = ctx->timing;
+        ctx->timing = false;
+    } else if (!g && ctx->gdec) {
+        ctx->timing = ctx->timing_saved;
+    }
+    ctx->gdec = g;
+}
+
+/* before a replay: the captured launches decode position pos of cache slot
+ * `slot` (enqueued on the context's stream) */
+extern "C" int smol_internal_gdec_step(smol_attn_ctx *ctx, smol_graph_dec *g, int pos, int slot) {
+    if (!g || pos < 0 || pos > g->plan_pos) return fail(SMOL_ATTN_ERR_ARG, "graph decode step: pos %d", pos);
+    hipLaunchKernelGGL(k_gdec_step, dim3(1), dim3(64), 0, ctx->stream, g->seqs, g->step, pos, slot);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SMOL_ATTN_OK : fail(SMOL_ATTN_ERR_DEVICE, "k_gdec_step: %s", hipGetErrorString(e));
 }
 
 static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {

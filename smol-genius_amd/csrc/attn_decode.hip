@@ -122,7 +122,7 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
      * lane), so the sequence costs no second memory round trip. A sequence
      * index past 63 is loaded after the item. */
     static_assert(sizeof(DecItem) == 8 && sizeof(DecSeq) == 16, "item / sequence records");
-    const DecSeq *seqs = p.n_seq <= DEC_ARG_SEQS ? p.seqs : p.seqs_dev;
+    const DecSeq *seqs = p.seqs_dev ? p.seqs_dev : p.seqs;
     const uint2 iw = reinterpret_cast<const uint2 *>(p.n_items <= DEC_ARG_ITEMS ? p.items : p.items_dev)[bid];
     const int4 sl = reinterpret_cast<const int4 *>(seqs)[min(lane, max(p.n_seq - 1, 0))];
     /* both loads are in flight before either is used (the compiler would
@@ -149,6 +149,8 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
         sq.tok0 = __builtin_amdgcn_readfirstlane(sq0.tok0);
         sq.n_q = __builtin_amdgcn_readfirstlane(sq0.n_q);
     }
+    /* this launch's flag value (see DecParams::step_dev) */
+    const unsigned epoch = p.step_dev ? (__builtin_amdgcn_readfirstlane(*p.step_dev) << 8) + p.epoch : p.epoch;
     const int G = p.G;
     const int r_base = rb * TR;                   /* first row of this row block */
     const int R = min(TR, sq.n_q * G - r_base);   /* its real rows */
@@ -878,7 +880,7 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __builtin_amdgcn_s_waitcnt(0); /* every store above acknowledged */
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            if (lane == 0) __builtin_amdgcn_raw_buffer_store_b32(p.epoch, rpart, my + FLAG_OFF, 0, CPOL_SC1);
+            if (lane == 0) __builtin_amdgcn_raw_buffer_store_b32(epoch, rpart, my + FLAG_OFF, 0, CPOL_SC1);
         }
         return;
     }
@@ -894,7 +896,7 @@ __global__ __launch_bounds__(64 * NW) void k_dec(const DecParams p) {
         const unsigned *flag =
             reinterpret_cast<const unsigned *>(p.part + (slot0 + tid) * p.slot_floats + p.slot_floats - 1);
         /* fault_merge: a value no split stores, so the wait runs to its bound */
-        const unsigned want = p.fault_merge ? ~p.epoch : p.epoch;
+        const unsigned want = p.fault_merge ? ~epoch : epoch;
         int spins = 0;
         while (poll_u32(flag) != want) {
             if (++spins >= p.spin_limit) { ok = 0; break; }

@@ -248,6 +248,11 @@ typedef struct {
      * O [R][hd], (m, l) [R][2], then the flag (an int) at slot_floats - 1,
      * alone in the slot's last 128 bytes */
     float *part; int slot_floats; unsigned epoch;
+    /* captured launches (a HIP graph replayed at many positions): the call's
+     * epoch is (*step_dev << 8) + epoch, step_dev a counter the host advances
+     * before each replay and epoch the launch's own tag (1..255), and the
+     * sequences come from seqs_dev; null otherwise */
+    const unsigned *step_dev;
     int *err_flag;             /* set to 1 (plain store) by a merger that gave up waiting */
     int spin_limit;            /* flag polls before a merger gives up */
     int fault_merge;           /* 1: mergers wait for a flag value no split writes (tests the give-up path) */
@@ -255,7 +260,7 @@ typedef struct {
     int n_items;               /* grid size */
     const DecItem *items_dev;  /* the items when n_items > DEC_ARG_ITEMS */
     int n_seq;
-    const DecSeq *seqs_dev;    /* the sequences when n_seq > DEC_ARG_SEQS */
+    const DecSeq *seqs_dev;    /* the sequences when n_seq > DEC_ARG_SEQS or step_dev is set */
     DecSeq seqs[DEC_ARG_SEQS];
     DecItem items[DEC_ARG_ITEMS];
 } DecParams;

@@ -27,6 +27,13 @@
 
 extern "C" int smol_internal_fail(int code, const char *msg);
 extern "C" int smol_launch_to_bf16_trunc(const float *x, uint16_t *y, long long n, hipStream_t st);
+/* decode launches under graph capture (attn_api.hip) */
+struct smol_graph_dec;
+extern "C" int smol_internal_gdec_create(smol_attn_ctx *ctx, int n_heads, int n_kv_heads, int hd, int plan_pos,
+                                         smol_graph_dec **out);
+extern "C" void smol_internal_gdec_destroy(smol_graph_dec *g);
+extern "C" void smol_internal_gdec_capture(smol_attn_ctx *ctx, smol_graph_dec *g);
+extern "C" int smol_internal_gdec_step(smol_attn_ctx *ctx, smol_graph_dec *g, int pos, int slot);
 
 namespace {
 
@@ -44,6 +51,7 @@ struct Buf {
 };
 
 struct Binding {
+    unsigned long long serial = 0; /* tells a binding from a later one at the same address */
     smol_qkn_attn_config cfg{};
     hipStream_t stream = nullptr;
     smol_attn_ctx *ctx = nullptr;
@@ -58,6 +66,7 @@ struct Binding {
 
 std::mutex g_mu;
 std::unordered_map<const void *, Binding *> g_bind;
+unsigned long long g_serial = 0;
 
 Binding *find(const void *owner) {
     std::lock_guard<std::mutex> lk(g_mu);
@@ -326,6 +335,118 @@ extern "C" int smol_qkn_layer_prefill_bf16(const void *owner, int layer, int sta
     return run_layer_bf16(b, layer, start_pos, seq_len, x, w, dim, intermediate, false);
 }
 
+/* ---- one decode step of every layer as a HIP graph ---- */
+
+struct smol_qkn_step_graph {
+    const void *owner = nullptr;
+    unsigned long long serial = 0;
+    smol_graph_dec *gd = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int max_pos = 0;
+    std::vector<const void *> fp; /* what the captured launches were built on */
+};
+
+namespace {
+
+/* the binding's buffers and capacities that captured launches point into:
+ * if any of them changes, the graph would read freed memory */
+std::vector<const void *> fingerprint(const Binding *b) {
+    std::vector<const void *> f{b->lq.p, b->lk.p, b->lv.p, b->la.p, b->lp.p, b->lg.p};
+    for (float *p : b->q_norm) f.push_back(p);
+    for (float *p : b->k_norm) f.push_back(p);
+    f.push_back(reinterpret_cast<const void *>((intptr_t)smol_kv_cache_capacity(b->kv)));
+    f.push_back(reinterpret_cast<const void *>((intptr_t)smol_rope_table_capacity(b->rope_global)));
+    f.push_back(reinterpret_cast<const void *>((intptr_t)smol_rope_table_capacity(b->rope_local)));
+    return f;
+}
+
+void destroy_graph(smol_qkn_step_graph *g) {
+    if (g->exec) hipGraphExecDestroy(g->exec);
+    if (g->graph) hipGraphDestroy(g->graph);
+    smol_internal_gdec_destroy(g->gd);
+    delete g;
+}
+
+}  // namespace
+
+extern "C" int smol_qkn_step_graph_create(const void *owner, float *x, const smol_qkn_layer_weights *w, int dim,
+                                          int intermediate, int act, int max_pos, smol_qkn_step_graph **out) {
+    if (!out) return qfail(SMOL_ATTN_ERR_ARG, "NULL out");
+    *out = nullptr;
+    Binding *b = find(owner);
+    if (!b) return qfail(SMOL_ATTN_ERR_ARG, "owner is not bound");
+    const smol_qkn_attn_config &c = b->cfg;
+    if (!c.on_device || c.bf16)
+        return qfail(SMOL_ATTN_ERR_ARG, "a step graph needs a binding with on_device = 1 and bf16 = 0");
+    if (!x || !w || dim <= 0 || intermediate <= 0 || max_pos <= 0) return qfail(SMOL_ATTN_ERR_ARG, "bad step graph arguments");
+    if (c.n_layers > 254) return qfail(SMOL_ATTN_ERR_UNSUPPORTED, "a step graph holds at most 254 layers");
+    QHIP(hipSetDevice(c.device));
+    const int q_dim = c.n_heads * c.head_dim, kv_dim = c.n_kv_heads * c.head_dim;
+    int rc;
+    /* everything the step touches is sized first: nothing may be allocated
+     * while the launches are captured */
+    if ((rc = smol_kv_cache_reserve(b->kv, max_pos))) return rc;
+    if ((rc = smol_rope_table_ensure(b->rope_global, max_pos))) return rc;
+    if (b->rope_local && (rc = smol_rope_table_ensure(b->rope_local, max_pos))) return rc;
+    if ((rc = reserve(b, b->lq, (size_t)q_dim * 4)) || (rc = reserve(b, b->lk, (size_t)kv_dim * 4)) ||
+        (rc = reserve(b, b->lv, (size_t)kv_dim * 4)) || (rc = reserve(b, b->la, (size_t)q_dim * 4)) ||
+        (rc = reserve(b, b->lp, (size_t)dim * 4)) || (rc = reserve(b, b->lg, (size_t)intermediate * 4)))
+        return rc;
+    auto *g = new smol_qkn_step_graph();
+    g->owner = owner;
+    g->serial = b->serial;
+    g->max_pos = max_pos;
+    if ((rc = smol_internal_gdec_create(b->ctx, c.n_heads, c.n_kv_heads, c.head_dim, max_pos - 1, &g->gd))) {
+        destroy_graph(g);
+        return rc;
+    }
+    hipError_t e = hipStreamSynchronize(b->stream);
+    if (e == hipSuccess) e = hipStreamBeginCapture(b->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) {
+        destroy_graph(g);
+        return qfail(SMOL_ATTN_ERR_DEVICE, hipGetErrorString(e));
+    }
+    smol_internal_gdec_capture(b->ctx, g->gd);
+    for (int l = 0; l < c.n_layers && !rc; l++)
+        rc = run_layer(b, l, max_pos - 1, 1, x, &w[l], dim, intermediate, act, true);
+    smol_internal_gdec_capture(b->ctx, nullptr);
+    e = hipStreamEndCapture(b->stream, &g->graph);
+    if (!rc && e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+    if (rc || e != hipSuccess) {
+        destroy_graph(g);
+        return rc ? rc : qfail(SMOL_ATTN_ERR_DEVICE, hipGetErrorString(e));
+    }
+    g->fp = fingerprint(b);
+    *out = g;
+    return SMOL_ATTN_OK;
+}
+
+extern "C" int smol_qkn_step_graph_launch(smol_qkn_step_graph *g, int pos) {
+    if (!g) return qfail(SMOL_ATTN_ERR_ARG, "NULL graph");
+    Binding *b = find(g->owner);
+    if (!b || b->serial != g->serial) return qfail(SMOL_ATTN_ERR_ARG, "the graph's binding is gone");
+    if (pos < 0 || pos >= g->max_pos) return qfail(SMOL_ATTN_ERR_ARG, "pos outside the graph's [0, max_pos)");
+    if (fingerprint(b) != g->fp)
+        return qfail(SMOL_ATTN_ERR_ARG, "a buffer, cache or table of the binding was reallocated since the capture; "
+                                        "create the graph again");
+    QHIP(hipSetDevice(b->cfg.device));
+    if (int rc = smol_internal_gdec_step(b->ctx, g->gd, pos, 0)) return rc;
+    QHIP(hipGraphLaunch(g->exec, b->stream));
+    return SMOL_ATTN_OK;
+}
+
+extern "C" int smol_qkn_step_graph_destroy(smol_qkn_step_graph *g) {
+    if (!g) return SMOL_ATTN_OK;
+    Binding *b = find(g->owner);
+    if (b && b->serial == g->serial) {
+        hipSetDevice(b->cfg.device);
+        hipStreamSynchronize(b->stream);
+    }
+    destroy_graph(g);
+    return SMOL_ATTN_OK;
+}
+
 extern "C" int smol_qkn_layer_synchronize(const void *owner) {
     Binding *b = find(owner);
     if (!b) return qfail(SMOL_ATTN_ERR_ARG, "owner is not bound");
@@ -351,6 +472,10 @@ extern "C" int smol_qkn_attn_bind(const void *owner, const smol_qkn_attn_config 
     smol_qkn_attn_unbind(owner);
     Binding *b = new Binding();
     b->cfg = c;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        b->serial = ++g_serial;
+    }
     b->sliding.assign(c.n_layers, 0);
     b->q_norm.assign(c.n_layers, nullptr);
     b->k_norm.assign(c.n_layers, nullptr);

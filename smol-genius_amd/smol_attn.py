@@ -86,6 +86,9 @@ SIGNATURES = [
     ("smol_qkn_layer_forward_bf16", [_vp, _c_int, _c_int, _vp, _vp, _c_int, _c_int], _c_int),
     ("smol_qkn_layer_prefill_bf16", [_vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _c_int], _c_int),
     ("smol_qkn_layer_synchronize", [_vp], _c_int),
+    ("smol_qkn_step_graph_create", [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_vp)], _c_int),
+    ("smol_qkn_step_graph_launch", [_vp, _c_int], _c_int),
+    ("smol_qkn_step_graph_destroy", [_vp], _c_int),
     ("smol_qkn_attn_stream", [_vp], _vp),
     # bf16-weight projections on device pointers (include/smol_linear.h)
     ("smol_linear_dev", [_vp, _vp, _c_int, _vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int], _c_int),
@@ -502,6 +505,28 @@ class QknLayerWeights:
         self.t = t
         self.s = _LayerWeights(**{k: (ctypes.c_void_p(v.data_ptr()) if v is not None else None)
                                   for k, v in t.items()})
+
+
+class QknStepGraph:
+    """smol_qkn_step_graph_*: one decode step of every layer of a binding,
+    captured on x [1, dim] (device fp32) with weights (one QknLayerWeights per
+    layer); launch(pos) replays it at pos. The tensors are kept alive with it."""
+
+    def __init__(self, blk, x, weights, dim, inter, act, max_pos):
+        self.blk, self.x, self.weights = blk, x, list(weights)
+        arr_t = type(self.weights[0].s) * len(self.weights)
+        self._arr = arr_t(*[w.s for w in self.weights])
+        self.h = _vp()
+        _check(load().smol_qkn_step_graph_create(blk.addr, _dev(x, "x"), self._arr, dim, inter, act, max_pos,
+                                                 ctypes.byref(self.h)), "smol_qkn_step_graph_create")
+
+    def launch(self, pos):
+        _check(load().smol_qkn_step_graph_launch(self.h, pos), "smol_qkn_step_graph_launch")
+
+    def close(self):
+        if self.h:
+            load().smol_qkn_step_graph_destroy(self.h)
+            self.h = _vp()
 
 
 class QknAttn:

@@ -191,3 +191,102 @@ def test_bf16_layer_sequence(sa, oracle, dorc, name, cfg, dim, inter, gemma, sli
                 assert np.isfinite(gf).all() and ratio <= 1.0
     finally:
         blk.close()
+
+
+@pytest.mark.parametrize("name,cfg,dim,inter,act,gemma,sliding", CONFIGS[:2], ids=[c[0] for c in CONFIGS[:2]])
+def test_step_graph(sa, oracle, dorc, name, cfg, dim, inter, act, gemma, sliding):
+    """smol_qkn_step_graph_*: one captured decode step of every layer,
+    replayed at successive positions, after a rewind and after eager work
+    on the same binding, against the same steps run eagerly on a second
+    binding (same kernels, the decode planned for another key length: within
+    1e-5 relative) and against the oracle's layer model (the layer bar).
+    A prefill that grows the binding's buffers makes the next launch fail,
+    and a graph created again works."""
+    H, Hkv, hd, L = cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["n_layers"]
+    owners = [ctypes.create_string_buffer(256) for _ in range(2)]
+    blks = [sa.QknAttn(o, **cfg, bf16=0, on_device=1, device=0, max_seq=64) for o in owners]
+    model_blk = dorc.Fp32Block(oracle, **cfg)
+    weights, dweights = [], []
+    for li in range(L):
+        s = 500 * (li + 1)
+        w = dict(input_norm=_norm_w(s, dim), wq=_proj(s + 1, H * hd, dim), wk=_proj(s + 2, Hkv * hd, dim),
+                 wv=_proj(s + 3, Hkv * hd, dim), wo=_proj(s + 4, dim, H * hd), post_attn_norm=_norm_w(s + 5, dim),
+                 pre_ffn_norm=_norm_w(s + 6, dim) if gemma else None,
+                 post_ffn_norm=_norm_w(s + 7, dim) if gemma else None,
+                 gate_up=_proj(s + 8, 2 * inter, dim), down=_proj(s + 9, dim, inter))
+        qn, kn = _norm_w(s + 10, hd), _norm_w(s + 11, hd)
+        for b in blks:
+            b.set_layer(li, sliding[li], qn, kn)
+        model_blk.set_layer(li, sliding[li], qn, kn)
+        weights.append(w)
+
+        def d(a):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a)
+            return torch.from_numpy(a.view(np.int16) if a.dtype == np.uint16 else a).cuda()
+        dweights.append(sa.QknLayerWeights(**{k: d(v) for k, v in w.items()}))
+    model = dorc.Fp32Layer(oracle, model_blk, weights, act)
+    xg = torch.zeros((1, dim), dtype=torch.float32, device="cuda")
+    graph = None
+    try:
+        # the same 40-row prefill on both bindings and the model
+        x = synth.normal(7200, (40, dim))
+        xm = x
+        for b in blks:
+            xd = torch.from_numpy(x).cuda()
+            for li in range(L):
+                b.layer_prefill(li, 0, xd, dweights[li], dim, inter, act)
+            b.synchronize()
+        for li in range(L):
+            xm = model.step(li, 0, xm)
+        graph = sa.QknStepGraph(blks[0], xg, dweights, dim, inter, act, 64)
+        # decode steps; a rewind to 41; eager work on the graph's binding in between
+        for step, pos in enumerate([40, 41, 42, 43, 41, 42]):
+            x = synth.normal(7300 + step, (1, dim))
+            print("step graph %s replay %d pos %d" % (name, step, pos), flush=True)
+            xg.copy_(torch.from_numpy(x))
+            graph.launch(pos)
+            blks[0].synchronize()
+            got = xg.cpu().numpy()
+            xe = torch.from_numpy(x).cuda()
+            for li in range(L):
+                blks[1].layer_forward(li, pos, xe, dweights[li], dim, inter, act)
+            blks[1].synchronize()
+            eager = xe.cpu().numpy()
+            xm = x
+            for li in range(L):
+                xm = model.step(li, pos, xm)
+            rel = float(np.abs(got - eager).max() / np.abs(eager).max())
+            dm = np.abs(got.astype(np.float64) - xm)
+            ratio = float((dm / (2e-3 * L + 1e-2 * np.abs(xm))).max())
+            print("parity step graph %s pos %d rel_vs_eager %.2e ratio_vs_oracle %.3f" % (name, pos, rel, ratio),
+                  flush=True)
+            assert np.isfinite(got).all() and rel <= 1e-5 and ratio <= 1.0
+            if step == 2:
+                # eager decode on the graph's binding (same position and input as the replay): the
+                # cache rows it writes are the ones the graph wrote
+                xe2 = torch.from_numpy(x).cuda()
+                for li in range(L):
+                    blks[0].layer_forward(li, pos, xe2, dweights[li], dim, inter, act)
+                blks[0].synchronize()
+                assert np.abs(xe2.cpu().numpy() - eager).max() <= 1e-5 * np.abs(eager).max()
+        # a longer prefill reallocates the binding's layer buffers: the graph refuses to run
+        xl = torch.from_numpy(synth.normal(7400, (48, dim))).cuda()
+        for li in range(L):
+            blks[0].layer_prefill(li, 0, xl, dweights[li], dim, inter, act)
+        blks[0].synchronize()
+        with pytest.raises(sa.SmolAttnError):
+            graph.launch(48)
+        graph.close()
+        graph = sa.QknStepGraph(blks[0], xg, dweights, dim, inter, act, 64)
+        x = synth.normal(7500, (1, dim))
+        xg.copy_(torch.from_numpy(x))
+        graph.launch(48)
+        blks[0].synchronize()
+        assert np.isfinite(xg.cpu().numpy()).all()
+    finally:
+        if graph is not None:
+            graph.close()
+        for b in blks:
+            b.close()
