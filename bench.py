@@ -47,7 +47,7 @@ MALL_BYTES = 256 << 20
 DOMINANT = {"qwen06b_prefill": "k_attn_fb", "qwen06b_prefill_qknorm": "k_attn_fb", "siglip_bidir": "k_attn_win",
             "asr_encoder_bidir": "k_attn_win", "qwen06b_decode": "k_dec", "qwen06b_decode_qknorm": "k_dec",
             "gemma_mqa_decode": "k_dec", "qwen06b_decode_x28": "k_dec", "qwen17b_stream": "k_dec",
-            "qwen06b_proj_decode": "k_gemv", "qwen06b_proj_prefill": "Cijk_"}
+            "qwen06b_proj_decode": "k_gemv", "qwen06b_proj_prefill": "k_gemm"}
 
 
 def profile_fields(workload):

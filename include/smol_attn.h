@@ -138,7 +138,9 @@ SMOL_ATTN_API int smol_attn_ctx_timing_read(smol_attn_ctx *ctx, double *ms, int 
 #define SMOL_OPT_FB_GROUPS 12     /* k_attn_fb: 1: one key group of eight waves over 128-row items (long
                                    * items' keys split over workgroups and merged); 0 or 2: two key
                                    * groups over 64-row items */
-#define SMOL_OPT_COUNT 13
+#define SMOL_OPT_GEMM_TILE 13     /* k_gemm (projections of more than 4 rows): 0: tile chosen per shape;
+                                   * 1, 2, 3: 192 x 192, 128 x 128, 64 x 64 (rows x outputs) */
+#define SMOL_OPT_COUNT 14
 SMOL_ATTN_API int smol_attn_ctx_set_option(smol_attn_ctx *ctx, int option, int value);
 SMOL_ATTN_API int smol_attn_ctx_get_option(smol_attn_ctx *ctx, int option, int *value);
 

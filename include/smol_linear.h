@@ -18,10 +18,12 @@
  *
  * Numerics: every product and sum is fp32 arithmetic on the exact bf16
  * weights. For seq <= SMOL_LINEAR_GEMV_MAX_SEQ a GEMV kernel reads fp32 x
- * as it is. Longer inputs run on bf16 MFMA (hipBLASLt): an fp32 x is split
- * into x_hi = bf16(x) and x_lo = bf16(x - x_hi), and y = W x_hi + W x_lo
- * with fp32 accumulation, which carries x to about 2^-17 relative. A bf16 x
- * is used as it is.
+ * as it is. Longer inputs run on the library's bf16 MFMA kernel: an fp32 x
+ * is split as it is staged into x_hi = bf16(x) and x_lo = bf16(x - x_hi),
+ * and y = W x_hi + W x_lo with fp32 accumulation, which carries x to about
+ * 2^-17 relative. A bf16 x is used as it is. The fused operations of
+ * smol_linear_ops_dev (norm, bias, activation, residual) run in the same
+ * launch; y is written once.
  *
  * Errors: SMOL_ATTN_OK or a negative SMOL_ATTN_ERR_* status, with the
  * message in smol_attn_last_error().

@@ -1,4 +1,4 @@
-"""Builds libsmol_attn.so (gfx950) in-tree with hipcc (links hipBLASLt).
+"""Builds libsmol_attn.so (gfx950) in-tree with hipcc.
 
     python smol-genius_amd/build.py
 
@@ -17,7 +17,7 @@ CSRC = os.path.join(HERE, "csrc")
 ROOT = os.path.dirname(HERE)
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libsmol_attn.so")
-SOURCES = ["attn_prep.hip", "attn_decode.hip", "attn_fa.hip", "attn_fb.hip", "attn_win.hip", "attn_api.hip", "qkn_attn.hip", "linear.hip"]
+SOURCES = ["attn_prep.hip", "attn_decode.hip", "attn_fa.hip", "attn_fb.hip", "attn_win.hip", "attn_api.hip", "qkn_attn.hip", "linear.hip", "gemm.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("SMOL_ATTN_ARCH", "gfx950")
 
@@ -29,7 +29,7 @@ FLAGS = [
 
 
 KERNEL_FLAGS = {}
-LIBS = ["-L/opt/rocm/lib", "-lhipblaslt"]
+LIBS = []
 
 
 def _compile(src):

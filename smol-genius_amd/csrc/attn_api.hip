@@ -213,18 +213,12 @@ struct smol_attn_ctx {
      * from this state's device memory */
     smol_graph_dec *gdec = nullptr;
     bool timing_saved = false; /* timing is off while a capture runs */
-    /* state of the projection GEMMs (linear.hip), released with the context */
-    void *lin = nullptr;
-    void (*lin_free)(void *) = nullptr;
 };
 
-/* for linear.hip: the context's device, the slot of its GEMM state and that
- * state's destructor (called by smol_attn_ctx_destroy) */
+/* for linear.hip: the context's device and its compute units */
 extern "C" int smol_internal_ctx_device(smol_attn_ctx *ctx) { return ctx->device; }
-extern "C" void **smol_internal_ctx_lin(smol_attn_ctx *ctx, void (***freer)(void *)) {
-    *freer = &ctx->lin_free;
-    return &ctx->lin;
-}
+extern "C" int smol_internal_ctx_cus(smol_attn_ctx *ctx) { return ctx->cu_count; }
+extern "C" int smol_internal_ctx_option(smol_attn_ctx *ctx, int option) { return ctx->opt[option]; }
 
 static hipEvent_t pool_event(smol_attn_ctx *ctx) {
     if (!ctx->event_pool.empty()) {
@@ -394,7 +388,6 @@ extern "C" int smol_attn_ctx_destroy(smol_attn_ctx *ctx) {
         hipEventDestroy(m.b);
     }
     for (hipEvent_t e : ctx->event_pool) hipEventDestroy(e);
-    if (ctx->lin && ctx->lin_free) ctx->lin_free(ctx->lin);
     if (ctx->own_stream) hipStreamDestroy(ctx->stream);
     delete ctx;
     return SMOL_ATTN_OK;

@@ -265,4 +265,19 @@ typedef struct {
     DecItem items[DEC_ARG_ITEMS];
 } DecParams;
 
+/* ---- k_gemm (gemm.hip): the projections on bf16 MFMA ---- */
+struct GemmParams {
+    const uint16_t *w; /* [N][K] bf16 */
+    const void *x;     /* [M][K] fp32 or bf16 */
+    void *y;           /* [M][N] (act: [M][N / 2]) fp32 or bf16 (truncated) */
+    const float *bias; /* [N] or null */
+    const float *g;    /* [K] norm weight or null (fp32 x) */
+    const float *res;  /* [M][y columns] or null; may equal y */
+    float eps;
+    int M, N, K;
+    int act;           /* SMOL_LINEAR_ACT_* */
+    int tiles_m, tiles;
+    int per_xcd;       /* tiles dealt to each XCD */
+};
+
 #endif

@@ -1,0 +1,429 @@
+/*
+ * gemm.hip - k_gemm: the decoders' bf16-weight projections for more than a
+ * few rows on bf16 MFMA, with the operations around them fused:
+ *
+ *     y[m][n] = res[m][n'] + act( r_m * sum_k (x[m][k] g[k]) W[n][k] + bias[n] )
+ *
+ * (smol_linear_bf16 / smol_linear_nobias_bf16 / smol_matmul_t_bf16,
+ * common/kernels/matmul.c:336-358, 419-429, for seq_len > 1; bf16_linear_nobias,
+ * common/decoder/qkn_bf16_decoder.c:99-117; the input RMSNorm of
+ * common/kernels/rmsnorm.c:17-75 with r_m = 1 / sqrtf(sum_k x[m][k]^2 / K + eps)
+ * and the gated activations of common/kernels/activation.c:55-125 on the
+ * interleaved gate / up rows of the fused weight).
+ *
+ * Operands. W is bf16 [N][K]; x is fp32 or bf16 [M][K]. An fp32 x (times the
+ * norm weight g when there is one) is split as it is staged into x_hi =
+ * bf16(x) and x_lo = bf16(x - x_hi), and every W fragment feeds two MFMAs
+ * (W.x_hi + W.x_lo, fp32 accumulation), which carries x to about 2^-17
+ * relative; a bf16 x is used as it is. The row scale r_m is applied to the
+ * accumulator: sum_k ((x g) r) W and r sum_k (x g) W differ only by fp32
+ * rounding. The sum of squares comes from the same x loads.
+ *
+ * Tiling. A workgroup of four waves computes a BN x BM tile (outputs x rows)
+ * as 2 x 2 wave tiles, with v_mfma_f32_16x16x32_bf16: A = W rows (outputs),
+ * B = x rows, so a lane's four accumulator values are four consecutive
+ * outputs of one row (one 16-byte store, and both members of a gate / up
+ * pair). K advances 64 at a time through two LDS stages: W by direct-to-LDS
+ * transfers, x through registers (split there). LDS rows are 128 bytes with
+ * their 16-byte chunks XOR-swizzled by the row's low 3 bits, so the fragment
+ * reads of eight consecutive lanes hit distinct banks. Tiles are numbered
+ * output-tile-major and dealt to the XCDs in contiguous ranges (workgroup b
+ * runs on XCD b % 8), so each XCD's L2 holds a band of W.
+ */
+#include "attn_device.h"
+#include "smol_linear.h"
+
+#define GEMM_BK 64
+#define GEMM_XCD 8
+
+
+namespace {
+
+/* NSTG LDS stages of BK = 64: W [BN][64] bf16 (128-byte rows), then x
+ * [BM][64] as loaded (bf16: 128-byte rows; fp32: 256-byte rows), then the
+ * norm weight's 64 values */
+template <int BM, int BN, bool XBF, int WN, int WM>
+struct GemmGeom {
+    static constexpr int NW = WN * WM;
+    static constexpr int XROW = XBF ? 128 : 256;
+    static constexpr int W_BYTES = BN * 128;
+    static constexpr int X_BYTES = BM * XROW;
+    static constexpr int G_BYTES = 1024; /* norm weight of the stage's 64 columns (the first 256 bytes) */
+    static constexpr int STAGE = W_BYTES + X_BYTES + G_BYTES;
+    static constexpr int NSTG = 3 * STAGE <= 150 * 1024 ? 3 : 2;
+    static constexpr int TN = BN / WN, TM = BM / WM; /* wave tile */
+    static constexpr int NT = TN / 16, MT = TM / 16;
+    static constexpr int WDMA = W_BYTES / 1024 / NW; /* 1 KB transfers per wave per stage */
+    static constexpr int XDMA = X_BYTES / 1024 / NW;
+};
+
+/* byte offset of 16-byte chunk q of row r in rows of `rb` bytes: the chunk
+ * index XOR the row's low 3 bits, so eight consecutive rows read at one
+ * chunk index hit distinct banks */
+__device__ __forceinline__ unsigned swz(int row, int q, int rb) {
+    return (unsigned)(row * rb + ((q ^ (row & 7)) << 4));
+}
+
+__device__ __forceinline__ float act_fn(float g, int act) {
+    if (act == SMOL_LINEAR_ACT_SWIGLU) return g / (1.0f + expf(-g));
+    const float x3 = g * g * g;
+    const float inner = 0.7978845608028654f * (g + 0.044715f * x3);
+    return 0.5f * g * (1.0f + tanhf(inner));
+}
+
+/* x_hi = bf16_rne(x), x_lo = bf16_rne(x - x_hi) of 8 floats; a non-finite
+ * x goes to hi whole with lo 0, so it reaches y as it would in fp32 (a
+ * finite |x| above bf16's largest finite value, about 3.39e38, rounds to an
+ * infinite x_hi) */
+__device__ __forceinline__ void split_frag(const float *v, b8 &hi, b8 &lo) {
+    /* selects only: a branch here would split the wave per element */
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float x = v[i];
+        const __bf16 h = (__bf16)x;
+        hi[i] = h;
+        lo[i] = (__bf16)(fabsf(x) <= 3.402823466e38f ? x - (float)h : 0.0f);
+    }
+}
+
+} // namespace
+
+template <int BM, int BN, int WN, int WM, bool XBF, bool YBF, bool NORM>
+__global__ __launch_bounds__(64 * WN * WM) __attribute__((amdgpu_waves_per_eu(WN * WM * (BM >= 128 ? 1 : 2) / 4,
+                                                                             WN * WM * (BM >= 128 ? 1 : 2) / 4)))
+void k_gemm(const GemmParams p) {
+    using Gm = GemmGeom<BM, BN, XBF, WN, WM>;
+    constexpr int NW = Gm::NW;
+    constexpr int STAGE = Gm::STAGE, W_BYTES = Gm::W_BYTES, XROW = Gm::XROW, NSTG = Gm::NSTG;
+    constexpr int NT = Gm::NT, MT = Gm::MT, WDMA = Gm::WDMA, XDMA = Gm::XDMA;
+    constexpr int XCH = XROW / 16;                   /* 16-byte chunks of an x row */
+    static_assert(NSTG * STAGE <= 160 * 1024, "LDS");
+    static_assert(WDMA * 1024 * NW == W_BYTES && XDMA * 1024 * NW == Gm::X_BYTES, "staging shape");
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[NSTG * STAGE];
+    __shared__ float s_rinv[NORM ? BM : 1];
+
+    /* the tile: XCD x = b % 8 takes tiles [x per_xcd, (x + 1) per_xcd) */
+    const int b = blockIdx.x;
+    const int tile = (b % GEMM_XCD) * p.per_xcd + b / GEMM_XCD;
+    if (b / GEMM_XCD >= p.per_xcd || tile >= p.tiles) return;
+    const int n0 = (tile / p.tiles_m) * BN, m0 = (tile % p.tiles_m) * BM;
+    const int K = p.K;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave % WN, wm = wave / WN;
+    const int c = lane & 15, j = lane >> 4;
+    const unsigned lds0 = (unsigned)(size_t)smem;
+
+    /* Transfer e of a wave fills 1 KB of the stage: lane L lands at the
+     * stage's 16-byte position 1024 (wave + 4 e) / 16 + L, i.e. at chunk
+     * position (pos % chunks-per-row) of row pos / chunks-per-row, and loads
+     * the global chunk that the swizzle puts there. Rows past the operand
+     * and chunks past K read zero. */
+    const rsrc_t rw = make_rsrc(p.w + (long long)n0 * K, (long long)min(BN, p.N - n0) * K * 2);
+    const long long xes = XBF ? 2 : 4;
+    const rsrc_t rx = make_rsrc(static_cast<const char *>(p.x) + (long long)m0 * K * xes,
+                                (long long)min(BM, p.M - m0) * K * xes);
+    /* the norm weight: staged with each step's transfers (wave 0's one
+     * extra transfer; a vector load of the compiler's would make it wait for
+     * every transfer in flight) */
+    const rsrc_t rg = make_rsrc(NORM ? (const void *)p.g : (const void *)p.w, NORM ? (long long)K * 4 : 0);
+    /* Each tile walks K from its own starting step: rows of W and x lie a
+     * power-of-two stride apart, so one k-slice of every row of a tile maps to
+     * few L2 channels; tiles that start at different slices spread the
+     * device's requests over the channels */
+    const int n_steps = (K + GEMM_BK - 1) / GEMM_BK;
+    const int rot = tile % n_steps;
+    auto kstep = [&](int s) __attribute__((always_inline)) {
+        const int t = s + rot;
+        return t >= n_steps ? t - n_steps : t;
+    };
+    unsigned w_off[WDMA], x_off[XDMA];
+    int w_k[WDMA], x_k[XDMA]; /* first k of the lane's chunk, within the stage */
+#pragma unroll
+    for (int e = 0; e < WDMA; e++) {
+        const int pos = 64 * (wave + NW * e) + lane;
+        const int row = pos / 8, q = (pos % 8) ^ (row & 7);
+        w_k[e] = 8 * q;
+        w_off[e] = (unsigned)((row * K + 8 * q) * 2);
+    }
+#pragma unroll
+    for (int e = 0; e < XDMA; e++) {
+        const int pos = 64 * (wave + NW * e) + lane;
+        const int row = pos / XCH, q = (pos % XCH) ^ (row & 7);
+        x_k[e] = XBF ? 8 * q : 4 * q;
+        x_off[e] = (unsigned)((row * K + x_k[e]) * xes);
+    }
+    auto issue = [&](int s) __attribute__((always_inline)) {
+        const int k0 = kstep(s) * GEMM_BK;
+        const unsigned st = lds0 + (unsigned)((s % NSTG) * STAGE);
+#pragma unroll
+        for (int e = 0; e < WDMA; e++)
+            dma_1k(rw, k0 + w_k[e] < K ? w_off[e] : OOB_OFF, (unsigned)(k0 * 2),
+                   __builtin_amdgcn_readfirstlane(st + (wave + NW * e) * 1024));
+#pragma unroll
+        for (int e = 0; e < XDMA; e++)
+            dma_1k(rx, k0 + x_k[e] < K ? x_off[e] : OOB_OFF, (unsigned)(k0 * xes),
+                   __builtin_amdgcn_readfirstlane(st + W_BYTES + (wave + NW * e) * 1024));
+        if (NORM && wave == 0)
+            dma_1k(rg, lane < 16 && k0 + 4 * lane < K ? (unsigned)(lane * 16) : OOB_OFF, (unsigned)(k0 * 4),
+                   __builtin_amdgcn_readfirstlane(st + W_BYTES + Gm::X_BYTES));
+    };
+
+    float ss[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) ss[mt] = 0.0f;
+
+    f4 acc[NT][MT];
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[t][mt] = f4{0.f, 0.f, 0.f, 0.f};
+
+    /* NSTG - 1 stages in flight ahead of the one being multiplied */
+#pragma unroll
+    for (int s = 0; s < NSTG - 1; s++)
+        if (s < n_steps) issue(s);
+    for (int s = 0; s < n_steps; s++) {
+        /* stage s complete and visible: this thread's transfers drained
+         * (counted waits do not cover their LDS writes), then the barrier,
+         * which also tells every wave that stage s - 1 is no longer read */
+        if (s + NSTG - 1 < n_steps) {
+            /* wait for all but the transfers of the one younger stage in
+             * flight (vmcnt(n): 0x3F70 | n, n < 16) */
+            if constexpr (NSTG == 3) {
+                static_assert(WDMA + XDMA + 1 < 16, "vmcnt field");
+                constexpr int PER = WDMA + XDMA;
+                if (NORM && wave == 0) __builtin_amdgcn_s_waitcnt(0x3F70 | (PER + 1));
+                else __builtin_amdgcn_s_waitcnt(0x3F70 | PER);
+            } else {
+                __builtin_amdgcn_s_waitcnt(0);
+            }
+        } else {
+            __builtin_amdgcn_s_waitcnt(0);
+        }
+        __syncthreads();
+        if (s + NSTG - 1 < n_steps) issue(s + NSTG - 1);
+        const unsigned char *st = smem + (s % NSTG) * STAGE;
+        float gw[2][8];
+        if constexpr (NORM) {
+            const unsigned char *gs = st + W_BYTES + Gm::X_BYTES;
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                const f4 a = *reinterpret_cast<const f4 *>(gs + (32 * ks + 8 * j) * 4);
+                const f4 bb = *reinterpret_cast<const f4 *>(gs + (32 * ks + 8 * j) * 4 + 16);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    gw[ks][i] = a[i];
+                    gw[ks][4 + i] = bb[i];
+                }
+            }
+        }
+        /* the two half-steps (k 0-31, 32-63) as read, prepare, multiply,
+         * with the second half's fragment reads issued before the first
+         * half's products, so the LDS reads and the split (vector ALU) of
+         * one half overlap the matrix work of the other */
+        struct Raw {
+            uint4 a[NT];
+            f4 x[MT][XBF ? 1 : 2];
+        };
+        struct Frag {
+            b8 a[NT], h[MT], l[XBF ? 1 : MT];
+        };
+        auto read = [&](int ks, Raw &r) __attribute__((always_inline)) {
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+                r.a[t] = *reinterpret_cast<const uint4 *>(st + swz(wn * Gm::TN + 16 * t + c, 4 * ks + j, 128));
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const int row = wm * Gm::TM + 16 * mt + c;
+                if constexpr (XBF) {
+                    r.x[mt][0] = *reinterpret_cast<const f4 *>(st + W_BYTES + swz(row, 4 * ks + j, 128));
+                } else {
+                    r.x[mt][0] = *reinterpret_cast<const f4 *>(st + W_BYTES + swz(row, 8 * ks + 2 * j, 256));
+                    r.x[mt][1] = *reinterpret_cast<const f4 *>(st + W_BYTES + swz(row, 8 * ks + 2 * j + 1, 256));
+                }
+            }
+        };
+        auto prepare = [&](int ks, const Raw &r, Frag &f) __attribute__((always_inline)) {
+#pragma unroll
+            for (int t = 0; t < NT; t++) f.a[t] = as_b8(r.a[t]);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                if constexpr (XBF) {
+                    const f4 v = r.x[mt][0];
+                    f.h[mt] = as_b8(make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                               __float_as_uint(v[3])));
+                } else {
+                    const f4 v0 = r.x[mt][0], v1 = r.x[mt][1];
+                    float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                    if constexpr (NORM) {
+                        if (wn == 0) {
+#pragma unroll
+                            for (int i = 0; i < 8; i++) ss[mt] = fmaf(v[i], v[i], ss[mt]);
+                        }
+#pragma unroll
+                        for (int i = 0; i < 8; i++) v[i] *= gw[ks][i];
+                    }
+                    split_frag(v, f.h[mt], f.l[mt]);
+                }
+            }
+        };
+        /* the hi products, then the lo ones: no MFMA waits for the one just
+         * issued */
+        auto multiply = [&](const Frag &f) __attribute__((always_inline)) {
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+                    acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.a[t], f.h[mt], acc[t][mt], 0, 0, 0);
+            if constexpr (!XBF) {
+#pragma unroll
+                for (int t = 0; t < NT; t++)
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++)
+                        acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.a[t], f.l[mt], acc[t][mt], 0, 0, 0);
+            }
+        };
+        {
+            Raw r0, r1;
+            Frag f0, f1;
+            read(0, r0);
+            prepare(0, r0, f0);
+            read(1, r1);
+            __builtin_amdgcn_sched_barrier(0);
+            multiply(f0);
+            prepare(1, r1, f1);
+            multiply(f1);
+        }
+    }
+
+    /* the rows' scale: in the waves with wn = 0, lanes c, c + 16, c + 32,
+     * c + 48 hold row c's partial sums of squares */
+    if constexpr (NORM) {
+        if (wn == 0) {
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const float t = row_sum4(ss[mt]);
+                if (j == 0) s_rinv[wm * Gm::TM + 16 * mt + c] = 1.0f / sqrtf(t / (float)K + p.eps);
+            }
+        }
+        __syncthreads();
+    }
+
+    /* epilogue: lane (c, j) holds outputs n = 4 j + e of row m = c of each
+     * 16 x 16 product tile */
+    const bool has_act = p.act != SMOL_LINEAR_ACT_NONE;
+    const int ycols = has_act ? p.N / 2 : p.N;
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        const int ml = wm * Gm::TM + 16 * mt + c;
+        const int m = m0 + ml;
+        if (m >= p.M) continue;
+        const float r = NORM ? s_rinv[ml] : 1.0f;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const int n = n0 + wn * Gm::TN + 16 * t + 4 * j;
+            if (n >= p.N) continue;
+            float v[4] = {acc[t][mt][0], acc[t][mt][1], acc[t][mt][2], acc[t][mt][3]};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if (NORM) v[e] *= r;
+                if (p.bias) v[e] += n + e < p.N ? p.bias[n + e] : 0.0f;
+            }
+            if (has_act) {
+                const int col = n / 2;
+                float o[2] = {act_fn(v[0], p.act) * v[1], act_fn(v[2], p.act) * v[3]};
+                const long long yi = (long long)m * ycols + col;
+                const int nv = min(2, ycols - col);
+                if (p.res) {
+#pragma unroll
+                    for (int e = 0; e < 2; e++)
+                        if (e < nv) o[e] += p.res[yi + e];
+                }
+                if constexpr (YBF) {
+                    uint16_t *y = static_cast<uint16_t *>(p.y) + yi;
+#pragma unroll
+                    for (int e = 0; e < 2; e++)
+                        if (e < nv) y[e] = (uint16_t)(__float_as_uint(o[e]) >> 16);
+                } else {
+                    float *y = static_cast<float *>(p.y) + yi;
+                    if (nv == 2 && ((yi & 1) == 0)) *reinterpret_cast<float2 *>(y) = make_float2(o[0], o[1]);
+                    else
+                        for (int e = 0; e < nv; e++) y[e] = o[e];
+                }
+            } else {
+                const long long yi = (long long)m * ycols + n;
+                const int nv = min(4, p.N - n);
+                if (p.res) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (e < nv) v[e] += p.res[yi + e];
+                }
+                if constexpr (YBF) {
+                    uint16_t *y = static_cast<uint16_t *>(p.y) + yi;
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (e < nv) y[e] = (uint16_t)(__float_as_uint(v[e]) >> 16);
+                } else {
+                    float *y = static_cast<float *>(p.y) + yi;
+                    if (nv == 4 && ((yi & 3) == 0)) *reinterpret_cast<float4 *>(y) = make_float4(v[0], v[1], v[2], v[3]);
+                    else
+                        for (int e = 0; e < nv; e++) y[e] = v[e];
+                }
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ launch */
+
+template <int BM, int BN, int WN, int WM, bool XBF, bool YBF>
+static int launch_gemm_t(const GemmParams &p, bool norm, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+    const dim3 grid((unsigned)(GEMM_XCD * p.per_xcd)), block(64 * WN * WM);
+    if constexpr (!XBF) {
+        if (norm) {
+            hipExtLaunchKernelGGL((k_gemm<BM, BN, WN, WM, false, YBF, true>), grid, block, 0, st, e0, e1, 0, p);
+            return hipGetLastError() == hipSuccess ? 0 : -3;
+        }
+    }
+    hipExtLaunchKernelGGL((k_gemm<BM, BN, WN, WM, XBF, YBF, false>), grid, block, 0, st, e0, e1, 0, p);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+template <int BM, int BN, int WN, int WM>
+static int launch_gemm_b(const GemmParams &p, bool xbf, bool ybf, bool norm, hipStream_t st, hipEvent_t e0,
+                         hipEvent_t e1) {
+    if (xbf) return ybf ? launch_gemm_t<BM, BN, WN, WM, true, true>(p, false, st, e0, e1)
+                        : launch_gemm_t<BM, BN, WN, WM, true, false>(p, false, st, e0, e1);
+    return ybf ? launch_gemm_t<BM, BN, WN, WM, false, true>(p, norm, st, e0, e1)
+               : launch_gemm_t<BM, BN, WN, WM, false, false>(p, norm, st, e0, e1);
+}
+
+/* tile sizes the host may choose (rows of x = BM, outputs = BN) */
+extern "C" int smol_gemm_tile(int cfg, int *bm, int *bn) {
+    static const int t[3][2] = {{192, 192}, {128, 128}, {64, 64}};
+    if (cfg < 0 || cfg > 2) return -1;
+    *bm = t[cfg][0];
+    *bn = t[cfg][1];
+    return 0;
+}
+
+/* p's tile fields are filled here from the configuration; K % 8 == 0 and a
+ * 16-byte aligned W and x are the caller's to check */
+extern "C" int smol_launch_gemm(GemmParams *p, int cfg, bool xbf, bool ybf, hipStream_t st, hipEvent_t e0,
+                                hipEvent_t e1) {
+    int bm, bn;
+    if (smol_gemm_tile(cfg, &bm, &bn)) return -1;
+    if (xbf && p->g) return -1;
+    p->tiles_m = (p->M + bm - 1) / bm;
+    p->tiles = p->tiles_m * ((p->N + bn - 1) / bn);
+    p->per_xcd = (p->tiles + GEMM_XCD - 1) / GEMM_XCD;
+    if (p->tiles <= 0) return 0;
+    const bool norm = p->g != nullptr;
+    switch (cfg) {
+    case 0: return launch_gemm_b<192, 192, 2, 2>(*p, xbf, ybf, norm, st, e0, e1);
+    case 1: return launch_gemm_b<128, 128, 2, 4>(*p, xbf, ybf, norm, st, e0, e1);
+    default: return launch_gemm_b<64, 64, 2, 2>(*p, xbf, ybf, norm, st, e0, e1);
+    }
+}

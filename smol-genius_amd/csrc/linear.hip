@@ -20,18 +20,13 @@
  *            step is issued before the first FMA. Sums: per-lane fp32, then
  *            a wave all-reduce (cross-row swaps + DPP row rotations), then
  *            the kp waves' totals in a fixed order through LDS.
- *   GEMM     longer inputs: hipBLASLt bf16 x bf16 -> fp32 on MFMA. An fp32
- *            x is first split by k_split_hilo into x_hi = bf16_rne(x) and
- *            x_lo = bf16_rne(x - x_hi), and y = W x_hi + W x_lo (second
- *            product accumulates with beta = 1): x is carried to ~2^-17
- *            relative, the weights are exact. A bias is written into y
- *            first (k_bias_rows) and the first product adds to it.
- *            hipBLASLt is column-major: y^T (out x seq, ld out) =
- *            op(A) B with A = W as an (in x out, ld in) matrix and op = T,
- *            B = x as (in x seq, ld in).
+ *   k_gemm   longer inputs (gemm.hip): bf16 MFMA tiles with the input
+ *            RMSNorm, the bias, the gated activation and the residual add
+ *            fused; an fp32 x is split into bf16 hi + lo as it is staged
+ *            (y = W x_hi + W x_lo, x carried to ~2^-17 relative, the
+ *            weights exact).
  */
 #include <hip/hip_runtime.h>
-#include <hipblaslt/hipblaslt.h>
 
 #include <limits.h>
 #include <math.h>
@@ -51,10 +46,14 @@
 
 extern "C" int smol_internal_fail(int code, const char *msg);
 extern "C" int smol_internal_ctx_device(smol_attn_ctx *ctx);
-extern "C" void **smol_internal_ctx_lin(smol_attn_ctx *ctx, void (***freer)(void *));
 extern "C" void smol_internal_timing_events(smol_attn_ctx *ctx, int kind, hipEvent_t *a, hipEvent_t *b);
 extern "C" smol_attn_ctx *smol_internal_legacy_ctx(const char *fn);
 extern "C" int smol_launch_to_bf16_trunc(const float *x, uint16_t *y, long long n, hipStream_t st);
+extern "C" int smol_internal_ctx_cus(smol_attn_ctx *ctx);
+extern "C" int smol_internal_ctx_option(smol_attn_ctx *ctx, int option);
+extern "C" int smol_gemm_tile(int cfg, int *bm, int *bn);
+extern "C" int smol_launch_gemm(GemmParams *p, int cfg, bool xbf, bool ybf, hipStream_t st, hipEvent_t e0,
+                                hipEvent_t e1);
 
 #define GEMV_R 4      /* output rows per row group (one wave, or kp waves) */
 #define GEMV_U 2      /* chunks of 8 elements per lane per step */
@@ -355,50 +354,6 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
     }
 }
 
-/* x fp32 -> x_hi = bf16_rne(x), x_lo = bf16_rne(x - x_hi); 8 elements per
- * thread. A finite x whose rounding overflows keeps the truncated hi; a
- * non-finite x goes to hi with lo = 0, so it reaches y as it would in fp32. */
-__device__ __forceinline__ void split1(float x, uint16_t &h, uint16_t &l) {
-    const bool fin = fabsf(x) <= 3.402823466e38f;
-    uint16_t hb = f32_to_bf16(x);
-    if (fin && !(fabsf(__uint_as_float((uint32_t)hb << 16)) <= 3.402823466e38f))
-        hb = (uint16_t)(__float_as_uint(x) >> 16);
-    h = hb;
-    l = fin ? f32_to_bf16(x - __uint_as_float((uint32_t)hb << 16)) : (uint16_t)0;
-}
-
-__global__ __launch_bounds__(256) void k_split_hilo(const float *x, uint16_t *hi, uint16_t *lo, long long n,
-                                                    bool vec) {
-    const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
-    const long long i0 = t * 8;
-    if (i0 >= n) return;
-    if (vec && i0 + 8 <= n) {
-        const float4 a = *reinterpret_cast<const float4 *>(x + i0);
-        const float4 b = *reinterpret_cast<const float4 *>(x + i0 + 4);
-        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        uint16_t h[8], l[8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) split1(v[e], h[e], l[e]);
-        uint4 H, L;
-        H.x = h[0] | ((uint32_t)h[1] << 16); H.y = h[2] | ((uint32_t)h[3] << 16);
-        H.z = h[4] | ((uint32_t)h[5] << 16); H.w = h[6] | ((uint32_t)h[7] << 16);
-        L.x = l[0] | ((uint32_t)l[1] << 16); L.y = l[2] | ((uint32_t)l[3] << 16);
-        L.z = l[4] | ((uint32_t)l[5] << 16); L.w = l[6] | ((uint32_t)l[7] << 16);
-        *reinterpret_cast<uint4 *>(hi + i0) = H;
-        *reinterpret_cast<uint4 *>(lo + i0) = L;
-    } else {
-        for (long long i = i0; i < n; i++) split1(x[i], hi[i], lo[i]);
-    }
-}
-
-/* y[s][o] = b[o] (or 0); add: y[s][o] += b[o] */
-__global__ __launch_bounds__(256) void k_bias_rows(float *y, const float *b, int seq, int out, bool add) {
-    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (long long)seq * out) return;
-    const float v = b ? b[i % out] : 0.0f;
-    y[i] = add ? y[i] + v : v;
-}
-
 /* out[s][i] = (x[s][i] * w[i]) * r_s, r_s = 1 / sqrtf(sum_i x[s][i]^2 / dim + eps)
  * (rmsnorm.c:17-75); one workgroup per row, the sum in a fixed order
  * (per-thread strided partials, then a tree in LDS) */
@@ -421,26 +376,6 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(float *out, const float *x
         const float v = (xr[i] * w[i]) * rinv;
         orow[i] = rr ? rr[i] + v : v;
     }
-}
-
-/* y[s][j] = act(t[s][2j]) * t[s][2j + 1] (+ res[s][j]); activation.c:55-88
- * (SiLU) and :104-125 (GELU, tanh form) */
-__global__ __launch_bounds__(256) void k_act_rows(float *y, const float *t, const float *res, int seq, int half,
-                                                  int act) {
-    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (long long)seq * half) return;
-    const long long s = i / half, j = i % half;
-    float g = t[s * 2 * half + 2 * j];
-    const float u = t[s * 2 * half + 2 * j + 1];
-    if (act == SMOL_LINEAR_ACT_SWIGLU) {
-        g = g / (1.0f + expf(-g));
-    } else {
-        const float x3 = g * g * g;
-        const float inner = 0.7978845608028654f * (g + 0.044715f * x3);
-        g = 0.5f * g * (1.0f + tanhf(inner));
-    }
-    const float v = g * u;
-    y[i] = res ? res[i] + v : v;
 }
 
 /* ---- the bf16 decoder's row operations (common/decoder/qkn_bf16_decoder.c)
@@ -536,16 +471,6 @@ int lfail(int code, const char *msg) { return smol_internal_fail(code, msg); }
         if (e_ != hipSuccess) return lfail(SMOL_ATTN_ERR_DEVICE, hipGetErrorString(e_));    \
     } while (0)
 
-#define LBLAS(expr)                                                                         \
-    do {                                                                                    \
-        hipblasStatus_t s_ = (expr);                                                        \
-        if (s_ != HIPBLAS_STATUS_SUCCESS) {                                                 \
-            char m_[160];                                                                   \
-            snprintf(m_, sizeof m_, "hipBLASLt: %s failed (status %d)", #expr, (int)s_);    \
-            return lfail(SMOL_ATTN_ERR_DEVICE, m_);                                         \
-        }                                                                                   \
-    } while (0)
-
 struct Buf {
     void *p = nullptr;
     size_t cap = 0;
@@ -564,138 +489,6 @@ int reserve(Buf &b, size_t bytes, hipStream_t st) {
     }
     LHIP(hipMalloc(&b.p, want));
     b.cap = want;
-    return 0;
-}
-
-/* one GEMM shape: y^T (out x seq) = W (in x out)^T x (in x seq) */
-struct Plan {
-    hipblasLtMatmulDesc_t desc = nullptr;
-    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
-    hipblasLtMatmulAlgo_t algo{};
-    size_t ws = 0;
-};
-
-#define LIN_WS_BYTES ((size_t)64 << 20)
-
-struct LinState {
-    int device = 0;
-    hipblasLtHandle_t h = nullptr;
-    void *ws = nullptr;
-    Buf xs;  /* x_hi then x_lo, bf16 */
-    Buf y32; /* fp32 result of a bf16-output GEMM */
-    Buf xn;  /* normalised input of a fused-norm GEMM */
-    Buf t;   /* pre-activation product of a fused-activation GEMM */
-    std::map<std::tuple<int, int, int>, Plan> plans;
-};
-
-void lin_free(void *p) {
-    LinState *L = static_cast<LinState *>(p);
-    hipSetDevice(L->device);
-    for (auto &kv : L->plans) {
-        Plan &pl = kv.second;
-        if (pl.a) hipblasLtMatrixLayoutDestroy(pl.a);
-        if (pl.b) hipblasLtMatrixLayoutDestroy(pl.b);
-        if (pl.c) hipblasLtMatrixLayoutDestroy(pl.c);
-        if (pl.desc) hipblasLtMatmulDescDestroy(pl.desc);
-    }
-    if (L->h) hipblasLtDestroy(L->h);
-    if (L->ws) hipFree(L->ws);
-    if (L->xs.p) hipFree(L->xs.p);
-    if (L->y32.p) hipFree(L->y32.p);
-    if (L->xn.p) hipFree(L->xn.p);
-    if (L->t.p) hipFree(L->t.p);
-    delete L;
-}
-
-/* the context's GEMM state, created on first use */
-int lin_state(smol_attn_ctx *ctx, LinState **out) {
-    void (**freer)(void *) = nullptr;
-    void **slot = smol_internal_ctx_lin(ctx, &freer);
-    if (!*slot) {
-        LinState *L = new LinState();
-        L->device = smol_internal_ctx_device(ctx);
-        if (hipblasLtCreate(&L->h) != HIPBLAS_STATUS_SUCCESS) {
-            delete L;
-            return lfail(SMOL_ATTN_ERR_DEVICE, "hipBLASLt: hipblasLtCreate failed");
-        }
-        if (hipMalloc(&L->ws, LIN_WS_BYTES) != hipSuccess) {
-            hipblasLtDestroy(L->h);
-            delete L;
-            return lfail(SMOL_ATTN_ERR_NOMEM, "linear: workspace allocation failed");
-        }
-        *slot = L;
-        *freer = lin_free;
-    }
-    *out = static_cast<LinState *>(*slot);
-    return 0;
-}
-
-int get_plan(LinState *L, int seq, int in, int out, Plan **res) {
-    const auto key = std::make_tuple(seq, in, out);
-    auto it = L->plans.find(key);
-    if (it != L->plans.end()) {
-        *res = &it->second;
-        return 0;
-    }
-    Plan pl;
-    auto drop = [&]() {
-        if (pl.a) hipblasLtMatrixLayoutDestroy(pl.a);
-        if (pl.b) hipblasLtMatrixLayoutDestroy(pl.b);
-        if (pl.c) hipblasLtMatrixLayoutDestroy(pl.c);
-        if (pl.desc) hipblasLtMatmulDescDestroy(pl.desc);
-    };
-    hipblasLtMatmulPreference_t pref = nullptr;
-    hipblasLtMatmulHeuristicResult_t heur[1];
-    int n_found = 0;
-    const hipblasOperation_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N;
-    const uint64_t ws = LIN_WS_BYTES;
-    hipblasStatus_t st = hipblasLtMatmulDescCreate(&pl.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
-    if (st == HIPBLAS_STATUS_SUCCESS)
-        st = hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof opT);
-    if (st == HIPBLAS_STATUS_SUCCESS)
-        st = hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof opN);
-    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&pl.a, HIP_R_16BF, in, out, in);
-    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&pl.b, HIP_R_16BF, in, seq, in);
-    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&pl.c, HIP_R_32F, out, seq, out);
-    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatmulPreferenceCreate(&pref);
-    if (st == HIPBLAS_STATUS_SUCCESS)
-        st = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof ws);
-    if (st == HIPBLAS_STATUS_SUCCESS)
-        st = hipblasLtMatmulAlgoGetHeuristic(L->h, pl.desc, pl.a, pl.b, pl.c, pl.c, pref, 1, heur, &n_found);
-    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
-    if (st == HIPBLAS_STATUS_NOT_SUPPORTED || (st == HIPBLAS_STATUS_SUCCESS && n_found < 1)) {
-        drop();
-        return 1; /* no algorithm for this shape */
-    }
-    if (st != HIPBLAS_STATUS_SUCCESS) {
-        drop();
-        char m[160];
-        snprintf(m, sizeof m, "hipBLASLt: GEMM set-up failed for seq %d, in %d, out %d (status %d)", seq, in, out,
-                 (int)st);
-        return lfail(SMOL_ATTN_ERR_DEVICE, m);
-    }
-    pl.algo = heur[0].algo;
-    pl.ws = heur[0].workspaceSize;
-    auto ins = L->plans.emplace(key, pl);
-    *res = &ins.first->second;
-    return 0;
-}
-
-int gemm(LinState *L, hipStream_t st, float *y, const uint16_t *w, const uint16_t *xb, int seq, int in, int out,
-         float beta) {
-    Plan *pl = nullptr;
-    if (int rc = get_plan(L, seq, in, out, &pl)) return rc < 0 ? rc : lfail(SMOL_ATTN_ERR_UNSUPPORTED, "no GEMM");
-    const float alpha = 1.0f;
-    LBLAS(hipblasLtMatmul(L->h, pl->desc, &alpha, w, pl->a, xb, pl->b, &beta, y, pl->c, y, pl->c, &pl->algo, L->ws,
-                          pl->ws, st));
-    return 0;
-}
-
-int launch_bias(float *y, const float *b, int seq, int out, hipStream_t st, bool add = false) {
-    const long long n = (long long)seq * out;
-    if (n <= 0) return 0;
-    hipLaunchKernelGGL(k_bias_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y, b, seq, out, add);
-    LHIP(hipGetLastError());
     return 0;
 }
 
@@ -813,92 +606,61 @@ int run_gemv_rows(smol_attn_ctx *ctx, hipStream_t st, void *y, bool ybf, const v
     return 0;
 }
 
-/* 1: hipBLASLt has a kernel for the shape, 0: it has none, < 0: error */
-int gemm_available(LinState *L, int seq, int in, int out) {
-    Plan *pl = nullptr;
-    const int rc = get_plan(L, seq, in, out, &pl);
-    return rc < 0 ? rc : rc == 0;
-}
-
-/* y32 (+)= x W^T on MFMA (acc: y32 already holds the start value) */
-int gemm_core(LinState *L, hipStream_t st, float *y32, const void *x, bool xbf, const uint16_t *w, int seq,
-              int in, int out, bool acc) {
-    const uint16_t *xh = static_cast<const uint16_t *>(x), *xl = nullptr;
-    if (!xbf) {
-        const long long n = (long long)seq * in;
-        const long long lo_off = (n + 127) & ~127LL; /* x_lo starts 256-byte aligned */
-        if (int rc = reserve(L->xs, (size_t)(lo_off + n) * 2, st)) return rc;
-        uint16_t *h = static_cast<uint16_t *>(L->xs.p);
-        uint16_t *l = h + lo_off;
-        const long long threads = (n + 7) / 8;
-        hipLaunchKernelGGL(k_split_hilo, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
-                           static_cast<const float *>(x), h, l, n, aligned16(x));
-        LHIP(hipGetLastError());
-        xh = h;
-        xl = l;
+/* k_gemm's tile configurations (gemm.hip): 192 x 192, 128 x 128 and 64 x 64
+ * (rows x outputs); one workgroup per compute unit for the first two, two
+ * for the last. The time of a launch is about its rounds of workgroups over
+ * the device times a round's time, and a round is bound by how fast each
+ * compute unit is fed its tiles' bytes; the weights below are the measured
+ * time of one round per unit of tile area relative to 192 x 192
+ * (M = 1536, K = 1024: 72.5, 26.4 and 23.3 us a round). */
+int gemm_cfg(smol_attn_ctx *ctx, int M, int N) {
+    static const int per_cu[3] = {1, 1, 2};
+    static const float cost[3] = {1.0f, 0.82f, 2.89f};
+    const int forced = smol_internal_ctx_option(ctx, SMOL_OPT_GEMM_TILE);
+    if (forced >= 1 && forced <= 3) return forced - 1;
+    const int cus = smol_internal_ctx_cus(ctx);
+    int best = 0;
+    double best_t = 1e300;
+    for (int cfg = 0; cfg < 3; cfg++) {
+        int bm, bn;
+        smol_gemm_tile(cfg, &bm, &bn);
+        const long long tiles = (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+        const long long slots = (long long)cus * per_cu[cfg];
+        const double t = (double)((tiles + slots - 1) / slots) * bm * bn * cost[cfg];
+        if (t < best_t) {
+            best_t = t;
+            best = cfg;
+        }
     }
-    if (int rc = gemm(L, st, y32, w, xh, seq, in, out, acc ? 1.0f : 0.0f)) return rc;
-    if (xl)
-        if (int rc = gemm(L, st, y32, w, xl, seq, in, out, 1.0f)) return rc;
-    return 0;
+    return best;
 }
 
-/* the GEMM path with the fused operations run as their own kernels:
- * norm -> L->xn, product (+ bias) -> y or L->t, activation (+ residual) -> y */
-int run_gemm_ops(smol_attn_ctx *ctx, LinState *L, hipStream_t st, float *y, const float *x, const uint16_t *w,
-                 const float *bias, int seq, int in, int out, const GemvFuse &f) {
-    if (int ok = gemm_available(L, seq, in, out); ok <= 0)
-        return ok < 0 ? ok : run_gemv_rows(ctx, st, y, false, x, false, w, bias, seq, in, out, &f);
+/* y = res + act(norm(x) W^T + bias) for seq rows on k_gemm; falls back to
+ * GEMV launches over blocks of rows where the operands do not suit the
+ * tiles' 16-byte staging (in_dim % 8 != 0, unaligned x or W) */
+int run_gemm(smol_attn_ctx *ctx, hipStream_t st, void *y, bool ybf, const void *x, bool xbf, const uint16_t *w,
+             const float *bias, int seq, int in, int out, const GemvFuse *f = nullptr) {
+    if (in % 8 != 0 || !aligned16(x) || !aligned16(w) || (f && f->norm_w && !aligned16(f->norm_w)) ||
+        (long long)out * in * 2 > 0x7FFF0000LL || (long long)seq * in * 4 > 0x7FFF0000LL)
+        return run_gemv_rows(ctx, st, y, ybf, x, xbf, w, bias, seq, in, out, f);
+    GemmParams p{};
+    p.w = w;
+    p.x = x;
+    p.y = y;
+    p.bias = bias;
+    if (f) {
+        p.g = f->norm_w;
+        p.eps = f->eps;
+        p.act = f->act;
+        p.res = f->res;
+    }
+    p.M = seq;
+    p.N = out;
+    p.K = in;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     smol_internal_timing_events(ctx, LIN_TIMING_KIND, &e0, &e1);
-    if (e0) LHIP(hipEventRecord(e0, st));
-    const float *xin = x;
-    if (f.norm_w) {
-        if (int rc = reserve(L->xn, (size_t)seq * in * 4, st)) return rc;
-        if (int rc = launch_rmsnorm(static_cast<float *>(L->xn.p), x, f.norm_w, seq, in, f.eps, st)) return rc;
-        xin = static_cast<const float *>(L->xn.p);
-    }
-    if (f.act) {
-        if (int rc = reserve(L->t, (size_t)seq * out * 4, st)) return rc;
-        float *t = static_cast<float *>(L->t.p);
-        if (bias)
-            if (int rc = launch_bias(t, bias, seq, out, st)) return rc;
-        if (int rc = gemm_core(L, st, t, xin, false, w, seq, in, out, bias != nullptr)) return rc;
-        const long long n = (long long)seq * (out / 2);
-        hipLaunchKernelGGL(k_act_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y, t, f.res, seq,
-                           out / 2, f.act);
-        LHIP(hipGetLastError());
-    } else {
-        if (f.res && f.res != y)
-            LHIP(hipMemcpyAsync(y, f.res, (size_t)seq * out * 4, hipMemcpyDeviceToDevice, st));
-        if (bias)
-            if (int rc = launch_bias(y, bias, seq, out, st, f.res != nullptr)) return rc;
-        if (int rc = gemm_core(L, st, y, xin, false, w, seq, in, out, f.res || bias)) return rc;
-    }
-    if (e1) LHIP(hipEventRecord(e1, st));
-    return 0;
-}
-
-/* the GEMM path for one weight: y (fp32 or bf16) = x W^T (+ bias) */
-int run_gemm(smol_attn_ctx *ctx, LinState *L, hipStream_t st, void *y, bool ybf, const void *x, bool xbf,
-             const uint16_t *w, const float *bias, int seq, int in, int out) {
-    if (int ok = gemm_available(L, seq, in, out); ok <= 0)
-        return ok < 0 ? ok : run_gemv_rows(ctx, st, y, ybf, x, xbf, w, bias, seq, in, out);
-    const size_t ny = (size_t)seq * out;
-    float *y32 = static_cast<float *>(y);
-    if (ybf) {
-        if (int rc = reserve(L->y32, ny * 4, st)) return rc;
-        y32 = static_cast<float *>(L->y32.p);
-    }
-    hipEvent_t e0 = nullptr, e1 = nullptr;
-    smol_internal_timing_events(ctx, LIN_TIMING_KIND, &e0, &e1);
-    if (e0) LHIP(hipEventRecord(e0, st));
-    if (bias)
-        if (int rc = launch_bias(y32, bias, seq, out, st)) return rc;
-    if (int rc = gemm_core(L, st, y32, x, xbf, w, seq, in, out, bias != nullptr)) return rc;
-    if (e1) LHIP(hipEventRecord(e1, st));
-    if (ybf && smol_launch_to_bf16_trunc(y32, static_cast<uint16_t *>(y), (long long)ny, st))
-        return lfail(SMOL_ATTN_ERR_DEVICE, "linear: truncation launch failed");
+    const int rc = smol_launch_gemm(&p, gemm_cfg(ctx, seq, out), xbf, ybf, st, e0, e1);
+    if (rc) return lfail(SMOL_ATTN_ERR_DEVICE, rc == -1 ? "k_gemm: unsupported operands" : "k_gemm launch failed");
     return 0;
 }
 
@@ -921,9 +683,7 @@ extern "C" int smol_linear_dev(smol_attn_ctx *ctx, void *y, int y_dtype, const v
     const bool xbf = x_dtype == SMOL_ATTN_BF16, ybf = y_dtype == SMOL_ATTN_BF16;
     if (seq <= SMOL_LINEAR_GEMV_MAX_SEQ || in_dim == 0)
         return run_gemv_rows(ctx, st, y, ybf, x, xbf, w, bias, seq, in_dim, out_dim);
-    LinState *L = nullptr;
-    if (int rc = lin_state(ctx, &L)) return rc;
-    return run_gemm(ctx, L, st, y, ybf, x, xbf, w, bias, seq, in_dim, out_dim);
+    return run_gemm(ctx, st, y, ybf, x, xbf, w, bias, seq, in_dim, out_dim);
 }
 
 extern "C" int smol_linear_qkv_dev(smol_attn_ctx *ctx, void *q, void *k, void *v, int y_dtype, const void *x,
@@ -979,9 +739,7 @@ extern "C" int smol_linear_ops_dev(smol_attn_ctx *ctx, float *y, const float *x,
     hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
     const GemvFuse f{ops->norm_weight, ops->norm_eps, ops->act, ops->residual};
     if (seq <= SMOL_LINEAR_GEMV_MAX_SEQ) return run_gemv_rows(ctx, st, y, false, x, false, w, bias, seq, in_dim, out_dim, &f);
-    LinState *L = nullptr;
-    if (int rc = lin_state(ctx, &L)) return rc;
-    return run_gemm_ops(ctx, L, st, y, x, w, bias, seq, in_dim, out_dim, f);
+    return run_gemm(ctx, st, y, false, x, false, w, bias, seq, in_dim, out_dim, &f);
 }
 
 extern "C" int smol_linear_qkv_norm_dev(smol_attn_ctx *ctx, float *q, float *k, float *v, const float *x,
@@ -1002,17 +760,12 @@ extern "C" int smol_linear_qkv_norm_dev(smol_attn_ctx *ctx, float *q, float *k, 
     LHIP(hipSetDevice(smol_internal_ctx_device(ctx)));
     hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
     if (seq > SMOL_LINEAR_GEMV_MAX_SEQ) {
-        /* the GEMM path: normalise once, then the three products */
-        LinState *L = nullptr;
-        if (int rc = lin_state(ctx, &L)) return rc;
-        if (int rc = reserve(L->xn, (size_t)seq * in_dim * 4, st)) return rc;
-        float *xn = static_cast<float *>(L->xn.p);
-        if (int rc = launch_rmsnorm(xn, x, norm_weight, seq, in_dim, norm_eps, st)) return rc;
-        /* xn is the state's own buffer: the products below must not reuse it */
-        const float *w_in = xn;
-        if (int rc = run_gemm(ctx, L, st, q, false, w_in, false, wq, nullptr, seq, in_dim, q_dim)) return rc;
-        if (int rc = run_gemm(ctx, L, st, k, false, w_in, false, wk, nullptr, seq, in_dim, kv_dim)) return rc;
-        return run_gemm(ctx, L, st, v, false, w_in, false, wv, nullptr, seq, in_dim, kv_dim);
+        /* the GEMM path: each of the three products normalises its rows
+         * from the x it stages */
+        const GemvFuse f{norm_weight, norm_eps, SMOL_LINEAR_ACT_NONE, nullptr};
+        if (int rc = run_gemm(ctx, st, q, false, x, false, wq, nullptr, seq, in_dim, q_dim, &f)) return rc;
+        if (int rc = run_gemm(ctx, st, k, false, x, false, wk, nullptr, seq, in_dim, kv_dim, &f)) return rc;
+        return run_gemm(ctx, st, v, false, x, false, wv, nullptr, seq, in_dim, kv_dim, &f);
     }
     GemvSeg segs[GEMV_SEGS];
     int n = 0;
