@@ -146,6 +146,9 @@ GEMM_CASES = [
     (64, 3072, 1024, False, False, False),
     (40, 512, 96, False, True, True),
     (33, 256, 80, True, False, True),
+    (200, 1000, 390, True, False, False),   # K a multiple of 8 but not of the 64-wide K step; ragged tiles
+    (193, 520, 200, False, True, False),    # bf16 x, tiles past M and N
+    (1536, 1024, 2048, False, False, True), # the 128 x 128 tiles
 ]
 
 
@@ -285,6 +288,8 @@ OPS_CASES = [
     (64, 512, 96, True, 2, "sep", True),
     (40, 1003, 40, True, 1, "y", True),
     (300, 3072, 1024, False, 0, "sep", True),
+    (130, 1000, 390, True, 1, "sep", True),   # norm weight past a partial last K step
+    (1536, 1024, 6144, True, 1, None, False), # the full prefill gate_up (192 x 192 tiles)
 ]
 
 
