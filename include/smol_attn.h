@@ -140,7 +140,10 @@ SMOL_ATTN_API int smol_attn_ctx_timing_read(smol_attn_ctx *ctx, double *ms, int 
                                    * groups over 64-row items */
 #define SMOL_OPT_GEMM_TILE 13     /* k_gemm (projections of more than 4 rows): 0: tile chosen per shape;
                                    * 1, 2, 3: 192 x 192, 128 x 128, 64 x 64 (rows x outputs) */
-#define SMOL_OPT_COUNT 14
+#define SMOL_OPT_FB_QPREP 14      /* k_attn_fb at head_dim 64 / 128 with precise QK^T and no per-head
+                                   * Q norm: 0: each item rotates and scales its own Q rows from the
+                                   * inputs; 1: the pre-pass stages them (as for k_attn_fa) */
+#define SMOL_OPT_COUNT 15
 SMOL_ATTN_API int smol_attn_ctx_set_option(smol_attn_ctx *ctx, int option, int value);
 SMOL_ATTN_API int smol_attn_ctx_get_option(smol_attn_ctx *ctx, int option, int *value);
 

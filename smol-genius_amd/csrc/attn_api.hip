@@ -810,9 +810,13 @@ static void plan_fb_fill(Plan &pl, int Hkv, int G, int window, int cu_count, std
 }
 
 /* the pre-pass blocks with their batches */
-static std::vector<PrepBlockB> prep_records(const Plan &pl) {
-    std::vector<PrepBlockB> r(pl.pblk.size());
-    for (size_t i = 0; i < pl.pblk.size(); i++) r[i] = {pl.pblk[i], pl.pb[pl.pblk[i].batch]};
+/* the pre-pass blocks with their batches; without_q: the Q blocks are left
+ * out (k_attn_fb prepares its Q rows itself) */
+static std::vector<PrepBlockB> prep_records(const Plan &pl, bool without_q) {
+    std::vector<PrepBlockB> r;
+    r.reserve(pl.pblk.size());
+    for (const PrepBlock &b : pl.pblk)
+        if (!(without_q && b.kind == 1)) r.push_back({b, pl.pb[b.batch]});
     return r;
 }
 
@@ -1261,6 +1265,20 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
         w = hd > 128 ? 1 : 2;
         rows_per = 64 * nt;
     }
+    /* k_attn_fb prepares its own Q rows from the inputs (head_dim 64 and
+     * 128, precise QK^T, one row tile per wave, no per-head Q norm): k_prep
+     * then writes no Q scratch, 4 bytes an element written and read back
+     * less. (With the norm, the weights' loads and the row sums at each
+     * item's start cost the attention kernel about what k_prep saves.)
+     * SMOL_OPT_FB_QPREP 1: k_prep stages Q as for k_attn_fa. The item's
+     * Q-scratch row q_row0 + r then names input token (q_row0 + r) / G and
+     * head g * G + (q_row0 + r) % G, and its RoPE row is q_pos0 + r / G:
+     * true of every plan with one pre-pass batch whose Q starts at input
+     * token 0, with one attention batch when Q is rotated. */
+    const bool q_in = fb && precise && (hd == 64 || hd == 128) && nt != 2 && !cs.q_norm &&
+                      ctx->opt[SMOL_OPT_FB_QPREP] != 1 &&
+                      pl.pb.size() == 1 && pl.pb[0].q_tok0 == 0 && pl.pb[0].q_row0 == 0 &&
+                      (!(cs.rope && cs.rope_q) || (pl.sb.size() == 1 && pl.sb[0].q_pos0 == pl.pb[0].q_pos0));
     std::vector<std::vector<int>> fill_lists;
     if (fb_one) plan_fb_fill(pl, cs.Hkv, G, cs.window, ctx->cu_count, fill_lists);
     else if (fa) plan_items(pl, cs.Hkv, G, cs.window, rows_per, ctx->cu_count * w, true, fb);
@@ -1308,7 +1326,7 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
 
     /* descriptor tables in one upload: pre-pass blocks and items, each with
      * its batch */
-    const std::vector<PrepBlockB> pbr = prep_records(pl);
+    const std::vector<PrepBlockB> pbr = prep_records(pl, q_in);
     std::vector<SkItemB> itr;
     if (fa && !fb) {
         itr.resize(pl.items.size());
@@ -1364,8 +1382,8 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     pp.range_flag = ctx->range_flag;
     /* a call with no pre-pass blocks launches nothing here and records no
      * timing mark */
-    int mk = pl.pblk.empty() ? -1 : timing_begin(ctx, 0);
-    rc = smol_launch_prep(&pp, (int)pl.pblk.size(), ctx->stream, mark_a(ctx, mk), mark_b(ctx, mk));
+    int mk = pbr.empty() ? -1 : timing_begin(ctx, 0);
+    rc = smol_launch_prep(&pp, (int)pbr.size(), ctx->stream, mark_a(ctx, mk), mark_b(ctx, mk));
     if (rc)
         return fail(rc == -1 ? SMOL_ATTN_ERR_UNSUPPORTED : SMOL_ATTN_ERR_DEVICE, "k_prep launch (hd %d): %s", hd,
                     rc == -1 ? "unsupported configuration" : hipGetErrorString(hipGetLastError()));
@@ -1403,6 +1421,12 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
     if (fb) {
         sp.fb_items = (const FbItem *)(dd + o_sc);
         sp.n_wg = fb_wg;
+    }
+    if (q_in) {
+        sp.q_in = cs.q; sp.q_dtype = cs.dtype; sp.q_stride = cs.q_stride;
+        sp.rope_cos = pp.rope_cos; sp.rope_sin = pp.rope_sin;
+        sp.q_rope_kind = pp.rope_q ? pp.rope_kind : SMOL_ROPE_OFF;
+        sp.qscale = pp.qscale;
     }
     mk = timing_begin(ctx, 1);
     rc = fb ? smol_launch_fb(&sp, hd, (int)n_items, nt, ctx->stream, mark_a(ctx, mk), mark_b(ctx, mk))
@@ -1724,7 +1748,7 @@ extern "C" int smol_kv_cache_write(smol_kv_cache *kv, int layer, int slot, int p
     const size_t fcap = (size_t)nf;
     if ((rc = dev_reserve(ctx->kf, (size_t)kv->n_kv * fcap * hd * 2, ctx->stream))) return rc;
     if ((rc = dev_reserve(ctx->vtf, (size_t)kv->n_kv * fcap * hd * 2, ctx->stream))) return rc;
-    const std::vector<PrepBlockB> pbr = prep_records(pl);
+    const std::vector<PrepBlockB> pbr = prep_records(pl, false);
     if ((rc = upload_desc(ctx, pbr.data(), pbr.size() * sizeof(PrepBlockB)))) return rc;
     PrepParams pp;
     memset(&pp, 0, sizeof(pp));

@@ -86,10 +86,98 @@ __device__ __attribute__((noinline)) void fb_merge(float *part_o, float *part_ml
     merge_group<HD, ROWS, 16, TPB>(p, si, sb, it.part, g, tid, s_o);
 }
 
+/* The Q fragments of one 16-row tile straight from the inputs (SkParams.q_in):
+ * lane (c, j) holds elements d = 32 ks + 8 j + i of its row (Q scratch row
+ * `row` = token * G + head in group, at RoPE position `pos`), so the NeoX
+ * partner of a first-half element (d + HD / 2) is in the same lane for head_dim
+ * 64 and 128. The arithmetic is that of k_prep's Q blocks without a norm:
+ * the rotation of rope.c:68-164, the scale, then the split into fp16 hi + lo
+ * (calls with a per-head Q norm stage Q in k_prep). */
+template <int HD>
+__device__ __forceinline__ void q_from_input(const SkParams &p, int row, int pos, int g, int G, int j, bool valid,
+                                             h8 (&qf)[(HD + 31) / 32], h8 (&ql)[(HD + 31) / 32]) {
+    static_assert(HD == 64 || HD == 128, "partners in the lane");
+    constexpr int KS = HD / 32, HALF = HD / 2;
+    const int tok = row / G, hg = row - tok * G;
+    const long long base = (long long)tok * p.q_stride + (long long)(g * G + hg) * HD;
+    const bool bf = p.q_dtype == SMOL_IN_BF16;
+    float v[KS][8];
+    /* every load of the tile goes out before any is used; the branches
+     * (uniform over the launch) leave out the loads a call does not need:
+     * the second 16 bytes of a bf16 row part, the tables of the second half
+     * under NeoX (they repeat the first) */
+    uint4 ra[KS], rb[KS];
+    float4 c0[KS], c1[KS], s0[KS], s1[KS];
+    const bool rope = p.q_rope_kind != SMOL_ROPE_OFF;
+    const bool neox = p.q_rope_kind == SMOL_ROPE_NEOX_K;
+    const char *dummy = static_cast<const char *>(p.q_in);
+    const float *fdummy = reinterpret_cast<const float *>(dummy);
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+        const int d0 = 32 * ks + 8 * j;
+        const char *a = valid ? static_cast<const char *>(p.q_in) + (base + d0) * (bf ? 2 : 4) : dummy;
+        ra[ks] = *reinterpret_cast<const uint4 *>(a);
+        rb[ks] = uint4{0u, 0u, 0u, 0u};
+        if (!bf) rb[ks] = *reinterpret_cast<const uint4 *>(valid ? a + 16 : dummy);
+        c0[ks] = c1[ks] = s0[ks] = s1[ks] = float4{0.f, 0.f, 0.f, 0.f};
+        if (rope && !(neox && d0 >= HALF)) {
+            const float *cs = valid ? p.rope_cos + (long long)pos * HD + d0 : fdummy;
+            const float *sn = valid ? p.rope_sin + (long long)pos * HD + d0 : fdummy;
+            c0[ks] = *reinterpret_cast<const float4 *>(cs); c1[ks] = *reinterpret_cast<const float4 *>(cs + 4);
+            s0[ks] = *reinterpret_cast<const float4 *>(sn); s1[ks] = *reinterpret_cast<const float4 *>(sn + 4);
+        }
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+        if (bf) {
+            unpack_bf16x8(ra[ks], v[ks]);
+        } else {
+            const uint32_t t[8] = {ra[ks].x, ra[ks].y, ra[ks].z, ra[ks].w, rb[ks].x, rb[ks].y, rb[ks].z, rb[ks].w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[ks][i] = __uint_as_float(t[i]);
+        }
+    }
+    if (p.q_rope_kind == SMOL_ROPE_NEOX_K) {
+#pragma unroll
+        for (int ks = 0; ks < KS / 2; ks++) {
+            const float cv[8] = {c0[ks].x, c0[ks].y, c0[ks].z, c0[ks].w, c1[ks].x, c1[ks].y, c1[ks].z, c1[ks].w};
+            const float sv[8] = {s0[ks].x, s0[ks].y, s0[ks].z, s0[ks].w, s1[ks].x, s1[ks].y, s1[ks].z, s1[ks].w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float x1 = v[ks][i], x2 = v[ks + KS / 2][i];
+                v[ks][i] = fmaf(x1, cv[i], -(x2 * sv[i]));
+                v[ks + KS / 2][i] = fmaf(x2, cv[i], x1 * sv[i]);
+            }
+        }
+    } else if (p.q_rope_kind == SMOL_ROPE_INTERLEAVED_K) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            const float cv[8] = {c0[ks].x, c0[ks].y, c0[ks].z, c0[ks].w, c1[ks].x, c1[ks].y, c1[ks].z, c1[ks].w};
+            const float sv[8] = {s0[ks].x, s0[ks].y, s0[ks].z, s0[ks].w, s1[ks].x, s1[ks].y, s1[ks].z, s1[ks].w};
+#pragma unroll
+            for (int i = 0; i < 8; i += 2) {
+                const float x0 = v[ks][i], x1 = v[ks][i + 1];
+                v[ks][i] = x0 * cv[i] - x1 * sv[i];
+                v[ks][i + 1] = x1 * cv[i + 1] + x0 * sv[i + 1];
+            }
+        }
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[ks][i] = valid ? v[ks][i] * p.qscale : 0.0f;
+        note_h_range(p.range_flag, v[ks]);
+        uint4 hi, lo;
+        pack_h8_hilo(v[ks], hi, lo);
+        qf[ks] = *reinterpret_cast<const h8 *>(&hi);
+        ql[ks] = *reinterpret_cast<const h8 *>(&lo);
+    }
+}
+
 /* ONE: the eight waves form a single key group over a 128-row item (each
  * slab is transferred once for all of them), and an item may cover part of
  * its tile's keys (see FbItem), merged across workgroups */
-template <int HD, int NT, bool CAP, bool PREC, bool ONE>
+template <int HD, int NT, bool CAP, bool PREC, bool ONE, bool QIN = false>
 __global__ __launch_bounds__(NT == 1 ? 512 : 256)
 __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_attn_fb(SkParams p) {
     static_assert(!ONE || NT == 1, "one key group: eight waves of one row tile each");
@@ -201,6 +289,11 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
         hi[nt] = valid[nt] ? rh : (1 << 30);
         lo_max = max(lo_max, lo[nt]);
         hi_min = min(hi_min, hi[nt]);
+        if constexpr (QIN) {
+            q_from_input<HD>(p, b.q_row0 + (valid[nt] ? r : 0), b.q_pos0 + (valid[nt] ? r : 0) / G, g, G, j,
+                         valid[nt], qf[nt], qfl[PREC ? nt : 0]);
+            continue;
+        }
         const long long qoff = (long long)g * p.qs_head_stride + (long long)(b.q_row0 + (valid[nt] ? r : 0)) * HDP;
         const _Float16 *qrow = p.qs + qoff;
 #pragma unroll
@@ -628,11 +721,35 @@ static int launch_fb_v(const SkParams *sp, dim3 grid, int nt, hipStream_t st, hi
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-/* precise QK^T (fp16 hi + lo operands) when the Q scratch has its lo part */
+/* Q from the inputs (precise QK^T, head_dim 64 or 128, nt 0 or 1) */
+template <int HD>
+static int launch_fb_qin(const SkParams *sp, dim3 grid, int nt, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+    if constexpr (HD == 64 || HD == 128) {
+        const bool cap = sp->cap2 > 0.0f;
+        if (nt == 0) {
+            if (cap) hipExtLaunchKernelGGL((k_attn_fb<HD, 1, true, true, true, true>), grid, dim3(512), 0, st, e0, e1, 0, *sp);
+            else hipExtLaunchKernelGGL((k_attn_fb<HD, 1, false, true, true, true>), grid, dim3(512), 0, st, e0, e1, 0, *sp);
+        } else if (nt == 1) {
+            if (cap) hipExtLaunchKernelGGL((k_attn_fb<HD, 1, true, true, false, true>), grid, dim3(512), 0, st, e0, e1, 0, *sp);
+            else hipExtLaunchKernelGGL((k_attn_fb<HD, 1, false, true, false, true>), grid, dim3(512), 0, st, e0, e1, 0, *sp);
+        } else {
+            return -1;
+        }
+        return hipGetLastError() == hipSuccess ? 0 : -3;
+    }
+    return -1;
+}
+
+/* precise QK^T (fp16 hi + lo operands) when the Q scratch has its lo part
+ * (or Q comes from the inputs) */
 template <int HD>
 static int launch_fb_hd(const SkParams *sp, int n_items, int nt, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     const int n_wg = sp->n_wg > 0 ? sp->n_wg : n_items; /* workgroups per kv head: the heads of the lists */
     const dim3 grid(n_wg * sp->Hkv);
+    if (sp->q_in) {
+        if (!sp->kf_lo) return -1;
+        return launch_fb_qin<HD>(sp, grid, nt, st, e0, e1);
+    }
     if (sp->qs_lo) {
         if (!sp->kf_lo) return -1;
         return launch_fb_v<HD, true>(sp, grid, nt, st, e0, e1);

@@ -114,6 +114,13 @@ typedef struct {
     const FbItem *fb_items;
     int n_wg;
     int *range_flag;           /* k_attn_fa: set to 1 when a cache value widened to fp16 overflows */
+    /* k_attn_fb with Q from the inputs (q_in non-null; no Q scratch): each
+     * item rotates and scales its Q rows itself, the arithmetic of k_prep's
+     * Q blocks; Q-scratch row r of an item then names input token r / G,
+     * head g * G + r % G */
+    const void *q_in; int q_dtype; long long q_stride;
+    const float *rope_cos; const float *rope_sin; int q_rope_kind;
+    float qscale;
 } SkParams;
 
 /* Pre-pass: normalises (optional per-head RMSNorm), rotates and scales Q into

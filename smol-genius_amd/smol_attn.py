@@ -194,7 +194,8 @@ def _dev(t, what):
 
 # context options (include/smol_attn.h SMOL_OPT_*)
 (OPT_PREFILL_KERNEL, OPT_FB_LISTS, OPT_FB_NT, OPT_DEC_SLABS, OPT_DEC_WAVES, OPT_DEC_SPLIT, OPT_XCD_CHECK,
- OPT_BIDIR_WIN, OPT_WIN_KSPLIT, OPT_DEC_SPIN, OPT_FAULT_MERGE, OPT_QK_FP16, OPT_FB_GROUPS, OPT_GEMM_TILE) = range(14)
+ OPT_BIDIR_WIN, OPT_WIN_KSPLIT, OPT_DEC_SPIN, OPT_FAULT_MERGE, OPT_QK_FP16, OPT_FB_GROUPS, OPT_GEMM_TILE,
+ OPT_FB_QPREP) = range(15)
 
 
 class Context:

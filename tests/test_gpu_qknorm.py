@@ -139,6 +139,50 @@ def test_prefill_qknorm(ctx, sa, oracle, wo, case):
     assert exact > 0.999, exact
 
 
+FB_Q_CASES = [  # P, S, hd, Hq, Hkv, rope_type, bf16 inputs, q norm (which keeps Q in the pre-pass)
+    (5, 150, 128, 16, 8, 0, True, False),     # RoPE rows from position 5
+    (0, 200, 64, 8, 2, 1, False, False),
+    (0, 130, 128, 6, 3, 1, False, False),
+    (17, 90, 64, 4, 4, 0, True, False),
+    (0, 100, 128, 8, 2, 0, True, True),
+]
+
+
+@pytest.mark.parametrize("case", FB_Q_CASES)
+def test_prefill_fb_q_from_inputs(ctx, sa, oracle, wo, case):
+    """k_attn_fb at head_dim 64 / 128 rotates and scales its own Q rows from
+    the inputs (SMOL_OPT_FB_QPREP 0), or reads them from the pre-pass's Q
+    scratch (1): both meet the oracle, and they differ only by the rounding
+    of the rotation (fused multiply-adds in k_attn_fb)."""
+    from smol_genius_amd.workloads import Prefill
+    P, S, hd, Hq, Hkv, rt, bf, qn = case
+    print("prefill fb q", case, flush=True)
+    wl = Prefill("t", Hq, Hkv, hd, P, S, 1e4, seed=110 + P + S + hd, in_bf16=bf)
+    wl.rope_type = rt
+    x = wl.inputs()
+    if qn:
+        x["q"] = spread_rows(x["q"], bf)
+    qw = weight(111 + hd, hd) if qn else None
+    want = wo.prefill(oracle, wl, x, q_norm=qw, eps=EPS)
+    outs = []
+    ctx.set_option(sa.OPT_PREFILL_KERNEL, 1)
+    try:
+        for mode in (0, 1):
+            ctx.set_option(sa.OPT_FB_QPREP, mode)
+            kv = sa.KVCache(ctx, 1, 1, Hkv, hd, P + S)
+            if P:
+                kv.write(0, 0, 0, x["cache_k"], x["cache_v"])
+            rope = sa.RopeTable(ctx, hd, wl.theta, rt)
+            got = sa.prefill(ctx, kv, 0, 0, rope, P, dev(x["q"], bf), dev(x["k"], bf), dev(x["v"], bf), Hq,
+                             wl.scale, q_norm=None if qw is None else dev(qw), eps=EPS).cpu().numpy()
+            assert_parity(got, want, "prefill fb q %s mode %d" % (case, mode))
+            outs.append(got)
+    finally:
+        ctx.set_option(sa.OPT_FB_QPREP, 0)
+        ctx.set_option(sa.OPT_PREFILL_KERNEL, 0)
+    assert np.abs(outs[0] - outs[1]).max() <= 1e-4 * max(1.0, np.abs(want).max())
+
+
 @pytest.mark.parametrize("hq,hkv,hd,rt,qn,kn", [(16, 8, 128, 0, True, True), (8, 1, 256, 1, True, True),
                                                 (4, 4, 64, 0, True, False), (6, 2, 72, 0, False, True)])
 def test_decode_qknorm(ctx, sa, oracle, wo, hq, hkv, hd, rt, qn, kn):
