@@ -171,7 +171,7 @@ def measure_projections(ctx, sa, wl, steps, warmup):
             layer(i % wl.layers)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        per = {}
+        per, launches = {}, {}
         ctx.timing_read()
         for k in wl.kinds:
             ctx.set_timing(True)
@@ -181,14 +181,16 @@ def measure_projections(ctx, sa, wl, steps, warmup):
             torch.cuda.synchronize()
             ctx.set_timing(False)
             ms, cnt = ctx.timing_read()["other"]
-            per[k] = ms / max(1, cnt)
+            # per call: the GEMM path runs Q, K and V as three launches
+            per[k] = ms / steps
+            launches[k] = cnt / steps
     finally:
         gc.enable()
     d = {"config": wl.describe(), "ms_per_step": round(wall / steps * 1e3, 5),
          "step": "one layer: 4 projection calls"}
     tot_ms = sum(per.values())
     for k, ms in per.items():
-        e = {"kernel_ms": round(ms, 5), "bytes_per_launch": wl.algorithmic_bytes(k)}
+        e = {"kernel_ms": round(ms, 5), "launches": launches[k], "bytes_per_call": wl.algorithmic_bytes(k)}
         if wl.seq <= 4:
             gbs = wl.algorithmic_bytes(k) / (ms * 1e-3) / 1e9
             e.update(GBps_kernel=round(gbs, 1), hbm_frac=round(gbs / PEAK_HBM_GBS, 4))

@@ -285,6 +285,10 @@ struct GemmParams {
     int act;           /* SMOL_LINEAR_ACT_* */
     int tiles_m, tiles;
     int per_xcd;       /* tiles dealt to each XCD */
+    /* rm > 0: XCD x takes the tiles of region (x / rn, x % rn) of an rm x rn
+     * split of the tile grid; 0: tiles [x per_xcd, (x + 1) per_xcd) in
+     * row-block-fastest order */
+    int rm, rn;
 };
 
 #endif

@@ -19,16 +19,23 @@
  * accumulator: sum_k ((x g) r) W and r sum_k (x g) W differ only by fp32
  * rounding. The sum of squares comes from the same x loads.
  *
- * Tiling. A workgroup of four waves computes a BN x BM tile (outputs x rows)
- * as 2 x 2 wave tiles, with v_mfma_f32_16x16x32_bf16: A = W rows (outputs),
- * B = x rows, so a lane's four accumulator values are four consecutive
- * outputs of one row (one 16-byte store, and both members of a gate / up
- * pair). K advances 64 at a time through two LDS stages: W by direct-to-LDS
- * transfers, x through registers (split there). LDS rows are 128 bytes with
- * their 16-byte chunks XOR-swizzled by the row's low 3 bits, so the fragment
- * reads of eight consecutive lanes hit distinct banks. Tiles are numbered
- * output-tile-major and dealt to the XCDs in contiguous ranges (workgroup b
- * runs on XCD b % 8), so each XCD's L2 holds a band of W.
+ * Tiling. One workgroup computes a BN x BM tile (outputs x rows) with
+ * v_mfma_f32_16x16x32_bf16: A = W rows (outputs), B = x rows, so a lane's
+ * four accumulator values are four consecutive outputs of one row (one
+ * 16-byte store, and both members of a gate / up pair). Three tile sizes
+ * (192 x 192 with four waves, 128 x 128 with eight, 64 x 64 with four, two
+ * workgroups per compute unit); the host picks one from the launch's
+ * rounds over the device. With a bf16 x the waves form a 2 x (NW / 2) grid;
+ * with an fp32 x every wave owns rows of its own (1 x NW) and so splits
+ * each element once per workgroup: the split's vector work, not the matrix
+ * cores, bounds the fp32 steps. K advances 64 at a time through NSTG LDS
+ * stages (three where they fit in 150 KB, else two): W, x and the norm
+ * weight all by direct-to-LDS transfers (buffer_load ... lds), the next
+ * stages in flight while one is multiplied. LDS rows are 128 or 256 bytes
+ * with their 16-byte chunks XOR-swizzled by the row's low 3 bits, so the
+ * fragment reads of eight consecutive lanes hit distinct banks. The tile
+ * grid is cut into eight regions, one per XCD (workgroup b runs on XCD
+ * b % 8), shaped to keep the fewest x and W bytes per XCD L2.
  */
 #include "attn_device.h"
 #include "smol_linear.h"
@@ -74,16 +81,28 @@ __device__ __forceinline__ float act_fn(float g, int act) {
 /* x_hi = bf16_rne(x), x_lo = bf16_rne(x - x_hi) of 8 floats; a non-finite
  * x goes to hi whole with lo 0, so it reaches y as it would in fp32 (a
  * finite |x| above bf16's largest finite value, about 3.39e38, rounds to an
- * infinite x_hi) */
+ * infinite x_hi). Per pair: bf16(x) converted over a zero low half is x_hi
+ * as a float (one packed conversion each), the two differences, the
+ * finiteness selects, one byte permute for the hi pair and one packed
+ * conversion for the lo pair. */
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+typedef float fl2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void split_frag(const float *v, b8 &hi, b8 &lo) {
+    uint32_t hw[4], lw[4];
     /* selects only: a branch here would split the wave per element */
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float x = v[i];
-        const __bf16 h = (__bf16)x;
-        hi[i] = h;
-        lo[i] = (__bf16)(fabsf(x) <= 3.402823466e38f ? x - (float)h : 0.0f);
+    for (int i = 0; i < 4; i++) {
+        const float x0 = v[2 * i], x1 = v[2 * i + 1];
+        const bf2 t0 = __builtin_convertvector((fl2){0.0f, x0}, bf2);
+        const bf2 t1 = __builtin_convertvector((fl2){0.0f, x1}, bf2);
+        const uint32_t u0 = __builtin_bit_cast(uint32_t, t0), u1 = __builtin_bit_cast(uint32_t, t1);
+        const float l0 = fabsf(x0) <= 3.402823466e38f ? x0 - __uint_as_float(u0) : 0.0f;
+        const float l1 = fabsf(x1) <= 3.402823466e38f ? x1 - __uint_as_float(u1) : 0.0f;
+        hw[i] = __builtin_amdgcn_perm(u1, u0, 0x07060302u);
+        lw[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector((fl2){l0, l1}, bf2));
     }
+    hi = as_b8(make_uint4(hw[0], hw[1], hw[2], hw[3]));
+    lo = as_b8(make_uint4(lw[0], lw[1], lw[2], lw[3]));
 }
 
 } // namespace
@@ -102,11 +121,26 @@ void k_gemm(const GemmParams p) {
     __shared__ __attribute__((aligned(1024))) unsigned char smem[NSTG * STAGE];
     __shared__ float s_rinv[NORM ? BM : 1];
 
-    /* the tile: XCD x = b % 8 takes tiles [x per_xcd, (x + 1) per_xcd) */
-    const int b = blockIdx.x;
-    const int tile = (b % GEMM_XCD) * p.per_xcd + b / GEMM_XCD;
-    if (b / GEMM_XCD >= p.per_xcd || tile >= p.tiles) return;
-    const int n0 = (tile / p.tiles_m) * BN, m0 = (tile % p.tiles_m) * BM;
+    /* the tile: workgroup b runs on XCD b % 8 */
+    const int b = blockIdx.x, xcd = b % GEMM_XCD, idx = b / GEMM_XCD;
+    int tm, tn;
+    if (p.rm > 0) {
+        /* XCD x: region (x / rn, x % rn) of the tile grid, so the rows of x
+         * and of W that its tiles share stay in its own L2 */
+        const int tiles_n = p.tiles / p.tiles_m;
+        const int ri = xcd / p.rn, rj = xcd % p.rn;
+        const int m_lo = ri * p.tiles_m / p.rm, m_hi = (ri + 1) * p.tiles_m / p.rm;
+        const int n_lo = rj * tiles_n / p.rn, n_hi = (rj + 1) * tiles_n / p.rn;
+        if (idx >= (m_hi - m_lo) * (n_hi - n_lo)) return;
+        tm = m_lo + idx % (m_hi - m_lo);
+        tn = n_lo + idx / (m_hi - m_lo);
+    } else {
+        const int t = xcd * p.per_xcd + idx;
+        if (idx >= p.per_xcd || t >= p.tiles) return;
+        tm = t % p.tiles_m;
+        tn = t / p.tiles_m;
+    }
+    const int n0 = tn * BN, m0 = tm * BM;
     const int K = p.K;
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -128,16 +162,7 @@ void k_gemm(const GemmParams p) {
      * extra transfer; a vector load of the compiler's would make it wait for
      * every transfer in flight) */
     const rsrc_t rg = make_rsrc(NORM ? (const void *)p.g : (const void *)p.w, NORM ? (long long)K * 4 : 0);
-    /* Each tile walks K from its own starting step: rows of W and x lie a
-     * power-of-two stride apart, so one k-slice of every row of a tile maps to
-     * few L2 channels; tiles that start at different slices spread the
-     * device's requests over the channels */
     const int n_steps = (K + GEMM_BK - 1) / GEMM_BK;
-    const int rot = tile % n_steps;
-    auto kstep = [&](int s) __attribute__((always_inline)) {
-        const int t = s + rot;
-        return t >= n_steps ? t - n_steps : t;
-    };
     unsigned w_off[WDMA], x_off[XDMA];
     int w_k[WDMA], x_k[XDMA]; /* first k of the lane's chunk, within the stage */
 #pragma unroll
@@ -155,7 +180,7 @@ void k_gemm(const GemmParams p) {
         x_off[e] = (unsigned)((row * K + x_k[e]) * xes);
     }
     auto issue = [&](int s) __attribute__((always_inline)) {
-        const int k0 = kstep(s) * GEMM_BK;
+        const int k0 = s * GEMM_BK;
         const unsigned st = lds0 + (unsigned)((s % NSTG) * STAGE);
 #pragma unroll
         for (int e = 0; e < WDMA; e++)
@@ -391,13 +416,17 @@ static int launch_gemm_t(const GemmParams &p, bool norm, hipStream_t st, hipEven
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-template <int BM, int BN, int WN, int WM>
+/* wave layouts: a bf16 x as WN x WM = 2 x (NW / 2) wave tiles; an fp32 x
+ * with every wave on rows of its own (1 x NW), so each element is split once
+ * per workgroup (with two waves across the outputs, both would split the
+ * same fragment: the split, not the matrix cores, bounds the fp32 steps) */
+template <int BM, int BN, int NW>
 static int launch_gemm_b(const GemmParams &p, bool xbf, bool ybf, bool norm, hipStream_t st, hipEvent_t e0,
                          hipEvent_t e1) {
-    if (xbf) return ybf ? launch_gemm_t<BM, BN, WN, WM, true, true>(p, false, st, e0, e1)
-                        : launch_gemm_t<BM, BN, WN, WM, true, false>(p, false, st, e0, e1);
-    return ybf ? launch_gemm_t<BM, BN, WN, WM, false, true>(p, norm, st, e0, e1)
-               : launch_gemm_t<BM, BN, WN, WM, false, false>(p, norm, st, e0, e1);
+    if (xbf) return ybf ? launch_gemm_t<BM, BN, 2, NW / 2, true, true>(p, false, st, e0, e1)
+                        : launch_gemm_t<BM, BN, 2, NW / 2, true, false>(p, false, st, e0, e1);
+    return ybf ? launch_gemm_t<BM, BN, 1, NW, false, true>(p, norm, st, e0, e1)
+               : launch_gemm_t<BM, BN, 1, NW, false, false>(p, norm, st, e0, e1);
 }
 
 /* tile sizes the host may choose (rows of x = BM, outputs = BN) */
@@ -417,13 +446,38 @@ extern "C" int smol_launch_gemm(GemmParams *p, int cfg, bool xbf, bool ybf, hipS
     if (smol_gemm_tile(cfg, &bm, &bn)) return -1;
     if (xbf && p->g) return -1;
     p->tiles_m = (p->M + bm - 1) / bm;
-    p->tiles = p->tiles_m * ((p->N + bn - 1) / bn);
-    p->per_xcd = (p->tiles + GEMM_XCD - 1) / GEMM_XCD;
+    const int tiles_n = (p->N + bn - 1) / bn;
+    p->tiles = p->tiles_m * tiles_n;
     if (p->tiles <= 0) return 0;
+    if (p->rm > 0) {
+        /* the region split with the fewest operand bytes per XCD (x rows
+         * of its row blocks + W rows of its column blocks); a grid smaller
+         * than the split in either direction keeps the contiguous deal */
+        static const int splits[4][2] = {{1, 8}, {2, 4}, {4, 2}, {8, 1}};
+        const double xrow = (double)p->K * (xbf ? 2 : 4), wrow = (double)p->K * 2;
+        double best = 1e300;
+        p->rm = 0;
+        for (const auto &sp : splits) {
+            if (sp[0] > p->tiles_m || sp[1] > tiles_n) continue;
+            const double bytes = (double)((p->tiles_m + sp[0] - 1) / sp[0]) * bm * xrow +
+                                 (double)((tiles_n + sp[1] - 1) / sp[1]) * bn * wrow;
+            if (bytes < best) {
+                best = bytes;
+                p->rm = sp[0];
+                p->rn = sp[1];
+            }
+        }
+    }
+    if (p->rm > 0) {
+        const int hm = (p->tiles_m + p->rm - 1) / p->rm, hn = (tiles_n + p->rn - 1) / p->rn;
+        p->per_xcd = hm * hn;
+    } else {
+        p->per_xcd = (p->tiles + GEMM_XCD - 1) / GEMM_XCD;
+    }
     const bool norm = p->g != nullptr;
     switch (cfg) {
-    case 0: return launch_gemm_b<192, 192, 2, 2>(*p, xbf, ybf, norm, st, e0, e1);
-    case 1: return launch_gemm_b<128, 128, 2, 4>(*p, xbf, ybf, norm, st, e0, e1);
-    default: return launch_gemm_b<64, 64, 2, 2>(*p, xbf, ybf, norm, st, e0, e1);
+    case 0: return launch_gemm_b<192, 192, 4>(*p, xbf, ybf, norm, st, e0, e1);
+    case 1: return launch_gemm_b<128, 128, 8>(*p, xbf, ybf, norm, st, e0, e1);
+    default: return launch_gemm_b<64, 64, 4>(*p, xbf, ybf, norm, st, e0, e1);
     }
 }

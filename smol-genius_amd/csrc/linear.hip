@@ -609,13 +609,13 @@ int run_gemv_rows(smol_attn_ctx *ctx, hipStream_t st, void *y, bool ybf, const v
 /* k_gemm's tile configurations (gemm.hip): 192 x 192, 128 x 128 and 64 x 64
  * (rows x outputs); one workgroup per compute unit for the first two, two
  * for the last. The time of a launch is about its rounds of workgroups over
- * the device times a round's time, and a round is bound by how fast each
- * compute unit is fed its tiles' bytes; the weights below are the measured
- * time of one round per unit of tile area relative to 192 x 192
- * (M = 1536, K = 1024: 72.5, 26.4 and 23.3 us a round). */
+ * the device times a round's time; the weights below are the measured time
+ * of one round per unit of tile area relative to 192 x 192 (M = 1536,
+ * K = 1024, fp32 x: about 50, 22 and 16 us a round; the bf16 x ratios are
+ * alike). */
 int gemm_cfg(smol_attn_ctx *ctx, int M, int N) {
     static const int per_cu[3] = {1, 1, 2};
-    static const float cost[3] = {1.0f, 0.82f, 2.89f};
+    static const float cost[3] = {1.0f, 0.99f, 2.9f};
     const int forced = smol_internal_ctx_option(ctx, SMOL_OPT_GEMM_TILE);
     if (forced >= 1 && forced <= 3) return forced - 1;
     const int cus = smol_internal_ctx_cus(ctx);
@@ -657,6 +657,7 @@ int run_gemm(smol_attn_ctx *ctx, hipStream_t st, void *y, bool ybf, const void *
     p.M = seq;
     p.N = out;
     p.K = in;
+    p.rm = 1; /* the launcher chooses the region split */
     hipEvent_t e0 = nullptr, e1 = nullptr;
     smol_internal_timing_events(ctx, LIN_TIMING_KIND, &e0, &e1);
     const int rc = smol_launch_gemm(&p, gemm_cfg(ctx, seq, out), xbf, ybf, st, e0, e1);

@@ -174,6 +174,40 @@ def test_gemm(ctx, sa, oracle, case):
         check(y.cpu().numpy(), ref, x, w, b, "gemm %s" % (case,))
 
 
+@pytest.mark.parametrize("tile", [1, 2, 3], ids=["192", "128", "64"])
+def test_gemm_every_tile(ctx, sa, oracle, tile):
+    """Each tile configuration forced (both wave layouts: fp32 and bf16 x), on
+    ragged grids and on grids cut into per-XCD regions, plain and with the
+    fused norm / activation / residual."""
+    ctx.set_option(sa.OPT_GEMM_TILE, tile)
+    try:
+        for seq, n_in, n_out, has_b, xbf in [(200, 1000, 390, True, False), (193, 520, 200, False, True),
+                                             (1536, 1024, 1024, False, False), (777, 1024, 2000, True, True)]:
+            print("gemm tile", tile, seq, n_in, n_out, xbf, flush=True)
+            x, w, b = linear_inputs(8500 + n_in + n_out + tile, seq, n_in, n_out, has_b)
+            if xbf:
+                xbits = synth.f32_to_bf16_bits(x)
+                x = synth.bf16_bits_to_f32(xbits)
+                xd = dev_bits(xbits).view(torch.bfloat16)
+            else:
+                xd = dev(x)
+            y = sa.linear(ctx, xd, dev_bits(w), dev(b) if has_b else None)
+            ctx.synchronize()
+            check(y.cpu().numpy(), oracle.linear_bf16(x, w, b), x, w, b, "gemm tile %d %s" % (tile, (seq, n_in, n_out)))
+        seq, n_in, n_out = 300, 1000, 392
+        x, w, b = linear_inputs(8600 + tile, seq, n_in, n_out, True)
+        g = (1.0 + 0.1 * synth.normal(8601, (n_in,))).astype(np.float32)
+        r = synth.normal(8602, (seq, n_out // 2))
+        ref = (r.astype(np.float64) + oracle.glu(oracle.linear_bf16(oracle.rms_norm(x, g, 1e-6), w, b), 1)).astype(
+            np.float32)
+        rd = dev(r)
+        y = sa.linear_ops(ctx, dev(x), dev_bits(w), dev(b), norm_weight=dev(g), eps=1e-6, act=1, residual=rd, out=rd)
+        ctx.synchronize()
+        assert_parity(y.cpu().numpy(), ref, "gemm tile %d ops" % tile)
+    finally:
+        ctx.set_option(sa.OPT_GEMM_TILE, 0)
+
+
 def test_gemm_full_prefill_shapes(ctx, sa, oracle):
     """Qwen3-0.6B projections of a 1536-token prefill: sampled rows against the
     oracle, every row against a float64 product on the device."""
