@@ -586,8 +586,8 @@ int run_gemv(smol_attn_ctx *ctx, hipStream_t st, const void *x, bool xbf, bool y
 }
 
 /* y = x W^T (+ bias) as GEMV launches over blocks of up to
- * SMOL_LINEAR_GEMV_MAX_SEQ rows (in_dim 0, and shapes hipBLASLt has no
- * kernel for) */
+ * SMOL_LINEAR_GEMV_MAX_SEQ rows (in_dim 0, and operands k_gemm's 16-byte
+ * staging cannot take) */
 int run_gemv_rows(smol_attn_ctx *ctx, hipStream_t st, void *y, bool ybf, const void *x, bool xbf,
                   const uint16_t *w, const float *bias, int seq, int in, int out, const GemvFuse *f = nullptr) {
     const size_t xe = xbf ? 2 : 4, ye = ybf ? 2 : 4;
