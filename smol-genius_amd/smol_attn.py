@@ -162,6 +162,14 @@ def load(path=LIB_PATH):
     if not os.path.exists(path):
         raise SmolAttnError("%s is missing: run `python smol-genius_amd/build.py` "
                             "(the attention path has no CPU fallback)" % path)
+    # torch carries its own HIP runtime under the soname the library links
+    # against: with torch imported first the library binds to that one copy;
+    # loaded the other way round, torch's runtime and the library's each
+    # initialise separately and the library's finds no device
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(path)
     for name, argtypes, restype in SIGNATURES:
         f = getattr(lib, name)
