@@ -23,12 +23,13 @@
  * v_mfma_f32_16x16x32_bf16: A = W rows (outputs), B = x rows, so a lane's
  * four accumulator values are four consecutive outputs of one row (one
  * 16-byte store, and both members of a gate / up pair). Three tile sizes
- * (192 x 192 with four waves, 128 x 128 with eight, 64 x 64 with four, two
- * workgroups per compute unit); the host picks one from the launch's
- * rounds over the device. With a bf16 x the waves form a 2 x (NW / 2) grid;
- * with an fp32 x every wave owns rows of its own (1 x NW) and so splits
- * each element once per workgroup: the split's vector work, not the matrix
- * cores, bounds the fp32 steps. K advances 64 at a time through NSTG LDS
+ * (192 x 192 and 128 x 128 with eight waves, 64 x 64 with four and two
+ * workgroups per compute unit: two waves per SIMD in each); the host picks
+ * one from the launch's rounds over the device. With a bf16 x the waves
+ * form a 2 x (NW / 2) grid; with an fp32 x each wave of the two smaller
+ * tiles owns rows of its own (1 x NW) and so splits each element once per
+ * workgroup: the split's vector work, not the matrix cores, bounds the fp32
+ * steps. K advances 64 at a time through NSTG LDS
  * stages (three where they fit in 150 KB, else two): W, x and the norm
  * weight all by direct-to-LDS transfers (buffer_load ... lds), the next
  * stages in flight while one is multiplied. LDS rows are 128 or 256 bytes
@@ -416,17 +417,21 @@ static int launch_gemm_t(const GemmParams &p, bool norm, hipStream_t st, hipEven
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-/* wave layouts: a bf16 x as WN x WM = 2 x (NW / 2) wave tiles; an fp32 x
- * with every wave on rows of its own (1 x NW), so each element is split once
- * per workgroup (with two waves across the outputs, both would split the
- * same fragment: the split, not the matrix cores, bounds the fp32 steps) */
-template <int BM, int BN, int NW>
+/* wave layouts, (WNF x WMF) for an fp32 x and (WNB x WMB) for a bf16 x:
+ * with an fp32 x each wave should own rows of its own (WN = 1), so each
+ * element is split once per workgroup (two waves across the outputs both
+ * split the same fragment: the split, not the matrix cores, bounds the fp32
+ * steps); the 192-row tile keeps two waves across the outputs, since its
+ * eight waves' rows would not be whole 16-row tiles otherwise, and eight
+ * waves (two per SIMD, one hiding the other's LDS and split latency) beat
+ * four with rows of their own */
+template <int BM, int BN, int WNF, int WMF, int WNB, int WMB>
 static int launch_gemm_b(const GemmParams &p, bool xbf, bool ybf, bool norm, hipStream_t st, hipEvent_t e0,
                          hipEvent_t e1) {
-    if (xbf) return ybf ? launch_gemm_t<BM, BN, 2, NW / 2, true, true>(p, false, st, e0, e1)
-                        : launch_gemm_t<BM, BN, 2, NW / 2, true, false>(p, false, st, e0, e1);
-    return ybf ? launch_gemm_t<BM, BN, 1, NW, false, true>(p, norm, st, e0, e1)
-               : launch_gemm_t<BM, BN, 1, NW, false, false>(p, norm, st, e0, e1);
+    if (xbf) return ybf ? launch_gemm_t<BM, BN, WNB, WMB, true, true>(p, false, st, e0, e1)
+                        : launch_gemm_t<BM, BN, WNB, WMB, true, false>(p, false, st, e0, e1);
+    return ybf ? launch_gemm_t<BM, BN, WNF, WMF, false, true>(p, norm, st, e0, e1)
+               : launch_gemm_t<BM, BN, WNF, WMF, false, false>(p, norm, st, e0, e1);
 }
 
 /* tile sizes the host may choose (rows of x = BM, outputs = BN) */
@@ -476,8 +481,8 @@ extern "C" int smol_launch_gemm(GemmParams *p, int cfg, bool xbf, bool ybf, hipS
     }
     const bool norm = p->g != nullptr;
     switch (cfg) {
-    case 0: return launch_gemm_b<192, 192, 4>(*p, xbf, ybf, norm, st, e0, e1);
-    case 1: return launch_gemm_b<128, 128, 8>(*p, xbf, ybf, norm, st, e0, e1);
-    default: return launch_gemm_b<64, 64, 4>(*p, xbf, ybf, norm, st, e0, e1);
+    case 0: return launch_gemm_b<192, 192, 2, 4, 2, 4>(*p, xbf, ybf, norm, st, e0, e1);
+    case 1: return launch_gemm_b<128, 128, 1, 8, 2, 4>(*p, xbf, ybf, norm, st, e0, e1);
+    default: return launch_gemm_b<64, 64, 1, 4, 2, 2>(*p, xbf, ybf, norm, st, e0, e1);
     }
 }

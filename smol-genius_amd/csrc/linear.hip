@@ -611,11 +611,11 @@ int run_gemv_rows(smol_attn_ctx *ctx, hipStream_t st, void *y, bool ybf, const v
  * for the last. The time of a launch is about its rounds of workgroups over
  * the device times a round's time; the weights below are the measured time
  * of one round per unit of tile area relative to 192 x 192 (M = 1536,
- * K = 1024, fp32 x: about 50, 22 and 16 us a round; the bf16 x ratios are
- * alike). */
+ * K = 1024, fp32 x: about 41-51, 22-24 and 16-18 us a round; the bf16 x
+ * ratios are alike). */
 int gemm_cfg(smol_attn_ctx *ctx, int M, int N) {
     static const int per_cu[3] = {1, 1, 2};
-    static const float cost[3] = {1.0f, 0.99f, 2.9f};
+    static const float cost[3] = {1.0f, 1.15f, 3.4f};
     const int forced = smol_internal_ctx_option(ctx, SMOL_OPT_GEMM_TILE);
     if (forced >= 1 && forced <= 3) return forced - 1;
     const int cus = smol_internal_ctx_cus(ctx);
