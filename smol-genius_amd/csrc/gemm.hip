@@ -79,28 +79,28 @@ __device__ __forceinline__ float act_fn(float g, int act) {
     return 0.5f * g * (1.0f + tanhf(inner));
 }
 
-/* x_hi = bf16_rne(x), x_lo = bf16_rne(x - x_hi) of 8 floats; a non-finite
- * x goes to hi whole with lo 0, so it reaches y as it would in fp32 (a
- * finite |x| above bf16's largest finite value, about 3.39e38, rounds to an
- * infinite x_hi). Per pair: bf16(x) converted over a zero low half is x_hi
- * as a float (one packed conversion each), the two differences, the
- * finiteness selects, one byte permute for the hi pair and one packed
- * conversion for the lo pair. */
+/* x_hi = bf16_rne(x), x_lo = bf16_rne(xc - bf16_rne(xc)) of 8 floats, xc =
+ * x clamped to bf16's largest finite magnitude (about 3.39e38): the same
+ * x_lo for every |x| up to that bound, 0 for an infinite x (which goes to
+ * x_hi whole and so reaches y as it would in fp32), never an infinite or
+ * NaN lo part beside a finite one. Per pair: one packed conversion for the
+ * hi pair, two clamps, two conversions over a zero low half (which are
+ * bf16(xc) as floats), two differences, one packed conversion for the lo
+ * pair. */
 typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 typedef float fl2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void split_frag(const float *v, b8 &hi, b8 &lo) {
+    constexpr float BF16_MAX = 3.3895313892515355e38f;
     uint32_t hw[4], lw[4];
-    /* selects only: a branch here would split the wave per element */
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const float x0 = v[2 * i], x1 = v[2 * i + 1];
-        const bf2 t0 = __builtin_convertvector((fl2){0.0f, x0}, bf2);
-        const bf2 t1 = __builtin_convertvector((fl2){0.0f, x1}, bf2);
-        const uint32_t u0 = __builtin_bit_cast(uint32_t, t0), u1 = __builtin_bit_cast(uint32_t, t1);
-        const float l0 = fabsf(x0) <= 3.402823466e38f ? x0 - __uint_as_float(u0) : 0.0f;
-        const float l1 = fabsf(x1) <= 3.402823466e38f ? x1 - __uint_as_float(u1) : 0.0f;
-        hw[i] = __builtin_amdgcn_perm(u1, u0, 0x07060302u);
-        lw[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector((fl2){l0, l1}, bf2));
+        hw[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector((fl2){x0, x1}, bf2));
+        const float c0 = __builtin_amdgcn_fmed3f(x0, -BF16_MAX, BF16_MAX);
+        const float c1 = __builtin_amdgcn_fmed3f(x1, -BF16_MAX, BF16_MAX);
+        const float h0 = __builtin_bit_cast(float, __builtin_convertvector((fl2){0.0f, c0}, bf2));
+        const float h1 = __builtin_bit_cast(float, __builtin_convertvector((fl2){0.0f, c1}, bf2));
+        lw[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector((fl2){c0 - h0, c1 - h1}, bf2));
     }
     hi = as_b8(make_uint4(hw[0], hw[1], hw[2], hw[3]));
     lo = as_b8(make_uint4(lw[0], lw[1], lw[2], lw[3]));
@@ -180,9 +180,9 @@ void k_gemm(const GemmParams p) {
         x_k[e] = XBF ? 8 * q : 4 * q;
         x_off[e] = (unsigned)((row * K + x_k[e]) * xes);
     }
-    auto issue = [&](int s) __attribute__((always_inline)) {
+    auto issue = [&](int s, int stage) __attribute__((always_inline)) {
         const int k0 = s * GEMM_BK;
-        const unsigned st = lds0 + (unsigned)((s % NSTG) * STAGE);
+        const unsigned st = lds0 + (unsigned)(stage * STAGE);
 #pragma unroll
         for (int e = 0; e < WDMA; e++)
             dma_1k(rw, k0 + w_k[e] < K ? w_off[e] : OOB_OFF, (unsigned)(k0 * 2),
@@ -209,8 +209,13 @@ void k_gemm(const GemmParams p) {
     /* NSTG - 1 stages in flight ahead of the one being multiplied */
 #pragma unroll
     for (int s = 0; s < NSTG - 1; s++)
-        if (s < n_steps) issue(s);
-    for (int s = 0; s < n_steps; s++) {
+        if (s < n_steps) issue(s, s);
+    /* unrolled by the ring's length, so every stage offset is a constant */
+    for (int s0 = 0; s0 < n_steps; s0 += NSTG)
+#pragma unroll
+    for (int u = 0; u < NSTG; u++) {
+        const int s = s0 + u;
+        if (s >= n_steps) break;
         /* stage s complete and visible: this thread's transfers drained
          * (counted waits do not cover their LDS writes), then the barrier,
          * which also tells every wave that stage s - 1 is no longer read */
@@ -229,8 +234,8 @@ void k_gemm(const GemmParams p) {
             __builtin_amdgcn_s_waitcnt(0);
         }
         __syncthreads();
-        if (s + NSTG - 1 < n_steps) issue(s + NSTG - 1);
-        const unsigned char *st = smem + (s % NSTG) * STAGE;
+        if (s + NSTG - 1 < n_steps) issue(s + NSTG - 1, (u + NSTG - 1) % NSTG);
+        const unsigned char *st = smem + u * STAGE;
         float gw[2][8];
         if constexpr (NORM) {
             const unsigned char *gs = st + W_BYTES + Gm::X_BYTES;
