@@ -246,8 +246,24 @@ def test_bf16_two_pass_attention(oracle):
         want = brute_causal(synth.bf16_bits_to_f32(q), synth.bf16_bits_to_f32(k),
                             synth.bf16_bits_to_f32(v), sq, sk, Hq, Hkv, hd, sc, qo,
                             window=win, cap=cap)
-        # truncation toward zero: |out| <= |want| + tiny and within one bf16 ulp (2^-7 rel)
+        # the fp32 sums stray from float64 by at most `margin` (1e-5 relative plus 1e-6 for rows
+        # that cancel: V is unit scale and the weights sum to 1)
+        w32 = want.astype(np.float32)
+        margin = 1e-5 * np.abs(w32) + 1e-6
+        # truncation toward zero: |out| <= |want| and within one bf16 ulp (2^-7 relative) of it
         np.testing.assert_allclose(out, want, rtol=2 ** -7, atol=1e-6)
+        assert (np.abs(out) <= np.abs(want) + margin).all()
+        # the bits are the truncation of the float32 result wherever that result is farther
+        # from a bf16 boundary than the margin
+        t = synth.bf16_bits_to_f32((w32.view(np.uint32) >> 16).astype(np.uint16))
+        step = np.abs(synth.bf16_bits_to_f32(((t.view(np.uint32) >> 16) + 1).astype(np.uint16)) - t)
+        clear = (np.abs(w32 - t) > margin) & (np.abs(w32 - t) < step - margin)
+        assert clear.mean() > 0.9
+        np.testing.assert_array_equal(out[clear], t[clear])
+        # planted: rounding to nearest instead of truncation breaks both checks
+        rne = synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(w32))
+        assert (np.abs(rne) > np.abs(want) + margin).any()
+        assert (rne[clear] != t[clear]).any()
 
 
 # ------------------------------------------------------- per-head RMSNorm
