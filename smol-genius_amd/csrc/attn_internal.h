@@ -289,6 +289,15 @@ struct GemmParams {
      * split of the tile grid; 0: tiles [x per_xcd, (x + 1) per_xcd) in
      * row-block-fastest order */
     int rm, rn;
+    /* nseg > 0: up to three outputs side by side (the Q, K and V of one x):
+     * segment s covers the concatenated columns [seg_c[s], seg_c[s + 1]) of
+     * the N, reads seg_w[s] and writes seg_y[s] with seg_c[s + 1] - seg_c[s]
+     * columns; every boundary a multiple of the tile width; no bias or
+     * activation. nseg 0: the one output w, y of N columns */
+    int nseg;
+    int seg_c[4];
+    const uint16_t *seg_w[3];
+    void *seg_y[3];
 };
 
 #endif

@@ -141,8 +141,21 @@ void k_gemm(const GemmParams p) {
         tm = t % p.tiles_m;
         tn = t / p.tiles_m;
     }
-    const int n0 = tn * BN, m0 = tm * BM;
+    const int m0 = tm * BM;
     const int K = p.K;
+    /* the tile's output: its segment's weight rows, y and width (a tile
+     * never straddles two segments) */
+    int n0 = tn * BN, NN = p.N;
+    const uint16_t *Wt = p.w;
+    void *Yt = p.y;
+    if (p.nseg > 0) {
+        const int sg = (n0 >= p.seg_c[1] ? 1 : 0) + (p.nseg > 2 && n0 >= p.seg_c[2] ? 1 : 0);
+        const int c0 = sg == 0 ? 0 : sg == 1 ? p.seg_c[1] : p.seg_c[2];
+        NN = (sg == 0 ? p.seg_c[1] : sg == 1 ? p.seg_c[2] : p.seg_c[3]) - c0;
+        Wt = sg == 0 ? p.seg_w[0] : sg == 1 ? p.seg_w[1] : p.seg_w[2];
+        Yt = sg == 0 ? p.seg_y[0] : sg == 1 ? p.seg_y[1] : p.seg_y[2];
+        n0 -= c0;
+    }
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -155,14 +168,14 @@ void k_gemm(const GemmParams p) {
      * position (pos % chunks-per-row) of row pos / chunks-per-row, and loads
      * the global chunk that the swizzle puts there. Rows past the operand
      * and chunks past K read zero. */
-    const rsrc_t rw = make_rsrc(p.w + (long long)n0 * K, (long long)min(BN, p.N - n0) * K * 2);
+    const rsrc_t rw = make_rsrc(Wt + (long long)n0 * K, (long long)min(BN, NN - n0) * K * 2);
     const long long xes = XBF ? 2 : 4;
     const rsrc_t rx = make_rsrc(static_cast<const char *>(p.x) + (long long)m0 * K * xes,
                                 (long long)min(BM, p.M - m0) * K * xes);
     /* the norm weight: staged with each step's transfers (wave 0's one
      * extra transfer; a vector load of the compiler's would make it wait for
      * every transfer in flight) */
-    const rsrc_t rg = make_rsrc(NORM ? (const void *)p.g : (const void *)p.w, NORM ? (long long)K * 4 : 0);
+    const rsrc_t rg = make_rsrc(NORM ? (const void *)p.g : (const void *)Wt, NORM ? (long long)K * 4 : 0);
     const int n_steps = (K + GEMM_BK - 1) / GEMM_BK;
     unsigned w_off[WDMA], x_off[XDMA];
     int w_k[WDMA], x_k[XDMA]; /* first k of the lane's chunk, within the stage */
@@ -345,7 +358,7 @@ void k_gemm(const GemmParams p) {
     /* epilogue: lane (c, j) holds outputs n = 4 j + e of row m = c of each
      * 16 x 16 product tile */
     const bool has_act = p.act != SMOL_LINEAR_ACT_NONE;
-    const int ycols = has_act ? p.N / 2 : p.N;
+    const int ycols = has_act ? NN / 2 : NN;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
         const int ml = wm * Gm::TM + 16 * mt + c;
@@ -355,12 +368,12 @@ void k_gemm(const GemmParams p) {
 #pragma unroll
         for (int t = 0; t < NT; t++) {
             const int n = n0 + wn * Gm::TN + 16 * t + 4 * j;
-            if (n >= p.N) continue;
+            if (n >= NN) continue;
             float v[4] = {acc[t][mt][0], acc[t][mt][1], acc[t][mt][2], acc[t][mt][3]};
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 if (NORM) v[e] *= r;
-                if (p.bias) v[e] += n + e < p.N ? p.bias[n + e] : 0.0f;
+                if (p.bias) v[e] += n + e < NN ? p.bias[n + e] : 0.0f;
             }
             if (has_act) {
                 const int col = n / 2;
@@ -373,31 +386,31 @@ void k_gemm(const GemmParams p) {
                         if (e < nv) o[e] += p.res[yi + e];
                 }
                 if constexpr (YBF) {
-                    uint16_t *y = static_cast<uint16_t *>(p.y) + yi;
+                    uint16_t *y = static_cast<uint16_t *>(Yt) + yi;
 #pragma unroll
                     for (int e = 0; e < 2; e++)
                         if (e < nv) y[e] = (uint16_t)(__float_as_uint(o[e]) >> 16);
                 } else {
-                    float *y = static_cast<float *>(p.y) + yi;
+                    float *y = static_cast<float *>(Yt) + yi;
                     if (nv == 2 && ((yi & 1) == 0)) *reinterpret_cast<float2 *>(y) = make_float2(o[0], o[1]);
                     else
                         for (int e = 0; e < nv; e++) y[e] = o[e];
                 }
             } else {
                 const long long yi = (long long)m * ycols + n;
-                const int nv = min(4, p.N - n);
+                const int nv = min(4, NN - n);
                 if (p.res) {
 #pragma unroll
                     for (int e = 0; e < 4; e++)
                         if (e < nv) v[e] += p.res[yi + e];
                 }
                 if constexpr (YBF) {
-                    uint16_t *y = static_cast<uint16_t *>(p.y) + yi;
+                    uint16_t *y = static_cast<uint16_t *>(Yt) + yi;
 #pragma unroll
                     for (int e = 0; e < 4; e++)
                         if (e < nv) y[e] = (uint16_t)(__float_as_uint(v[e]) >> 16);
                 } else {
-                    float *y = static_cast<float *>(p.y) + yi;
+                    float *y = static_cast<float *>(Yt) + yi;
                     if (nv == 4 && ((yi & 3) == 0)) *reinterpret_cast<float4 *>(y) = make_float4(v[0], v[1], v[2], v[3]);
                     else
                         for (int e = 0; e < nv; e++) y[e] = v[e];

@@ -36,6 +36,7 @@
 
 #include <map>
 #include <mutex>
+#include <numeric>
 #include <tuple>
 #include <unordered_map>
 #include <vector>
@@ -613,17 +614,22 @@ int run_gemv_rows(smol_attn_ctx *ctx, hipStream_t st, void *y, bool ybf, const v
  * of one round per unit of tile area relative to 192 x 192 (M = 1536,
  * K = 1024, fp32 x: about 41-51, 22-24 and 16-18 us a round; the bf16 x
  * ratios are alike). */
-int gemm_cfg(smol_attn_ctx *ctx, int M, int N) {
+int gemm_cfg(smol_attn_ctx *ctx, int M, int N, int seg_align = 0) {
     static const int per_cu[3] = {1, 1, 2};
     static const float cost[3] = {1.0f, 1.15f, 3.4f};
     const int forced = smol_internal_ctx_option(ctx, SMOL_OPT_GEMM_TILE);
-    if (forced >= 1 && forced <= 3) return forced - 1;
+    if (forced >= 1 && forced <= 3) {
+        int bm, bn;
+        smol_gemm_tile(forced - 1, &bm, &bn);
+        return seg_align % bn == 0 ? forced - 1 : -1;
+    }
     const int cus = smol_internal_ctx_cus(ctx);
-    int best = 0;
+    int best = -1;
     double best_t = 1e300;
     for (int cfg = 0; cfg < 3; cfg++) {
         int bm, bn;
         smol_gemm_tile(cfg, &bm, &bn);
+        if (seg_align % bn != 0) continue; /* segment boundaries on tile edges */
         const long long tiles = (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
         const long long slots = (long long)cus * per_cu[cfg];
         const double t = (double)((tiles + slots - 1) / slots) * bm * bn * cost[cfg];
@@ -665,6 +671,46 @@ int run_gemm(smol_attn_ctx *ctx, hipStream_t st, void *y, bool ybf, const void *
     return 0;
 }
 
+/* Q, K and V of one x on k_gemm as one launch: the three outputs side by
+ * side as column segments of one product (x is staged and split once per
+ * row tile instead of three times); 1 when the shapes do not allow it
+ * (segment widths not multiples of a tile width, operands the staging
+ * cannot take), and the caller runs three products */
+int run_gemm_qkv(smol_attn_ctx *ctx, hipStream_t st, void *q, void *k, void *v, bool ybf, const void *x, bool xbf,
+                 const uint16_t *wq, const uint16_t *wk, const uint16_t *wv, int seq, int in, int q_dim, int kv_dim,
+                 const GemvFuse *f) {
+    if (!q_dim || !kv_dim || in % 8 != 0 || !aligned16(x) || !aligned16(wq) || !aligned16(wk) || !aligned16(wv) ||
+        (f && f->norm_w && !aligned16(f->norm_w)) || (long long)q_dim * in * 2 > 0x7FFF0000LL ||
+        (long long)kv_dim * in * 2 > 0x7FFF0000LL || (long long)seq * in * 4 > 0x7FFF0000LL)
+        return 1;
+    const int cfg = gemm_cfg(ctx, seq, q_dim + 2 * kv_dim, std::gcd(q_dim, kv_dim));
+    if (cfg < 0) return 1;
+    GemmParams p{};
+    p.w = wq;
+    p.x = x;
+    p.y = q;
+    if (f) {
+        p.g = f->norm_w;
+        p.eps = f->eps;
+    }
+    p.M = seq;
+    p.N = q_dim + 2 * kv_dim;
+    p.K = in;
+    p.rm = 1;
+    p.nseg = 3;
+    p.seg_c[0] = 0;
+    p.seg_c[1] = q_dim;
+    p.seg_c[2] = q_dim + kv_dim;
+    p.seg_c[3] = q_dim + 2 * kv_dim;
+    p.seg_w[0] = wq; p.seg_w[1] = wk; p.seg_w[2] = wv;
+    p.seg_y[0] = q; p.seg_y[1] = k; p.seg_y[2] = v;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    smol_internal_timing_events(ctx, LIN_TIMING_KIND, &e0, &e1);
+    const int rc = smol_launch_gemm(&p, cfg, xbf, ybf, st, e0, e1);
+    if (rc) return lfail(SMOL_ATTN_ERR_DEVICE, rc == -1 ? "k_gemm: unsupported operands" : "k_gemm launch failed");
+    return 0;
+}
+
 int check_dtype(int t) { return t == SMOL_ATTN_F32 || t == SMOL_ATTN_BF16; }
 
 }  // namespace
@@ -694,6 +740,14 @@ extern "C" int smol_linear_qkv_dev(smol_attn_ctx *ctx, void *q, void *k, void *v
     if (!check_dtype(x_dtype) || !check_dtype(y_dtype)) return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_qkv_dev: dtype");
     if (seq < 0 || in_dim < 0 || q_dim < 0 || kv_dim < 0)
         return lfail(SMOL_ATTN_ERR_ARG, "smol_linear_qkv_dev: negative size");
+    if (seq > SMOL_LINEAR_GEMV_MAX_SEQ && in_dim > 0 && q_dim > 0 && kv_dim > 0 && q && k && v && x && wq && wk &&
+        wv && (long long)seq * in_dim <= INT_MAX / 4 && (long long)seq * (q_dim + 2LL * kv_dim) <= INT_MAX / 4) {
+        LHIP(hipSetDevice(smol_internal_ctx_device(ctx)));
+        hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
+        const int rc = run_gemm_qkv(ctx, st, q, k, v, y_dtype == SMOL_ATTN_BF16, x, x_dtype == SMOL_ATTN_BF16, wq, wk,
+                                    wv, seq, in_dim, q_dim, kv_dim, nullptr);
+        if (rc <= 0) return rc;
+    }
     if (seq > SMOL_LINEAR_GEMV_MAX_SEQ || in_dim == 0) {
         if (int rc = smol_linear_dev(ctx, q, y_dtype, x, x_dtype, wq, nullptr, seq, in_dim, q_dim)) return rc;
         if (int rc = smol_linear_dev(ctx, k, y_dtype, x, x_dtype, wk, nullptr, seq, in_dim, kv_dim)) return rc;
@@ -761,9 +815,11 @@ extern "C" int smol_linear_qkv_norm_dev(smol_attn_ctx *ctx, float *q, float *k, 
     LHIP(hipSetDevice(smol_internal_ctx_device(ctx)));
     hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
     if (seq > SMOL_LINEAR_GEMV_MAX_SEQ) {
-        /* the GEMM path: each of the three products normalises its rows
-         * from the x it stages */
+        /* the GEMM path: the products normalise their rows from the x they
+         * stage (one launch for the three where the shapes allow) */
         const GemvFuse f{norm_weight, norm_eps, SMOL_LINEAR_ACT_NONE, nullptr};
+        const int rq = run_gemm_qkv(ctx, st, q, k, v, false, x, false, wq, wk, wv, seq, in_dim, q_dim, kv_dim, &f);
+        if (rq <= 0) return rq;
         if (int rc = run_gemm(ctx, st, q, false, x, false, wq, nullptr, seq, in_dim, q_dim, &f)) return rc;
         if (int rc = run_gemm(ctx, st, k, false, x, false, wk, nullptr, seq, in_dim, kv_dim, &f)) return rc;
         return run_gemm(ctx, st, v, false, x, false, wv, nullptr, seq, in_dim, kv_dim, &f);

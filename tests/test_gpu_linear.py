@@ -137,6 +137,48 @@ def test_qkv(ctx, sa, oracle, shape):
             check(got.cpu().numpy(), oracle.linear_bf16(x, w), x, w, None, "qkv %s %s" % (shape, nm))
 
 
+@pytest.mark.parametrize("case", [  # seq, in, q_dim, kv_dim, forced tile (0: by shape), norm, x bf16
+    (1536, 1024, 2048, 1024, 0, False, False),   # Q on 128-wide tiles, K and V after it, one launch
+    (1536, 1024, 2048, 1024, 3, True, False),    # 64-wide tiles, with the input norm
+    (300, 512, 320, 64, 0, True, False),         # K and V one 64-wide tile column each, ragged rows
+    (200, 256, 200, 40, 0, False, False),        # widths no tile divides: three launches
+    (130, 1024, 256, 128, 2, False, True),       # bf16 x
+    (130, 1024, 384, 192, 1, False, False),      # 192-wide tiles forced
+])
+def test_qkv_one_launch(ctx, sa, oracle, case):
+    """Q, K and V of one x as column segments of one k_gemm launch where
+    every segment boundary falls on a tile edge (else three launches); each
+    output against the oracle, rows past the call untouched."""
+    seq, n_in, q_dim, kv_dim, tile, norm, xbf = case
+    print("qkv one launch", case, flush=True)
+    x, wq, _ = linear_inputs(7300 + n_in + q_dim, seq, n_in, q_dim, False)
+    _, wk, _ = linear_inputs(7400 + n_in + kv_dim, seq, n_in, kv_dim, False)
+    _, wv, _ = linear_inputs(7500 + n_in + kv_dim, seq, n_in, kv_dim, False)
+    g = (1.0 + 0.1 * synth.normal(7600 + n_in, (n_in,))).astype(np.float32) if norm else None
+    if xbf:
+        xbits = synth.f32_to_bf16_bits(x)
+        x = synth.bf16_bits_to_f32(xbits)
+        xd = dev_bits(xbits).view(torch.bfloat16)
+    else:
+        xd = dev(x)
+    ctx.set_option(sa.OPT_GEMM_TILE, tile)
+    try:
+        if norm:
+            q, k, v = sa.linear_qkv_norm(ctx, xd, dev_bits(wq), dev_bits(wk), dev_bits(wv), dev(g), 1e-6)
+        else:
+            q, k, v = sa.linear_qkv(ctx, xd, dev_bits(wq), dev_bits(wk), dev_bits(wv))
+        ctx.synchronize()
+    finally:
+        ctx.set_option(sa.OPT_GEMM_TILE, 0)
+    xn = oracle.rms_norm(x, g, 1e-6) if norm else x
+    for got, w, nm in ((q, wq, "q"), (k, wk, "k"), (v, wv, "v")):
+        ref = oracle.linear_bf16(xn, w)
+        if norm:
+            assert_parity(got.cpu().numpy(), ref, "qkv one launch %s %s" % (case, nm))
+        else:
+            check(got.cpu().numpy(), ref, x, w, None, "qkv one launch %s %s" % (case, nm))
+
+
 GEMM_CASES = [
     # seq, in, out, bias, x bf16, y bf16
     (5, 1024, 4096, False, False, False),
