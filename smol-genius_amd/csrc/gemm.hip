@@ -229,23 +229,13 @@ void k_gemm(const GemmParams p) {
     for (int u = 0; u < NSTG; u++) {
         const int s = s0 + u;
         if (s >= n_steps) break;
-        /* stage s complete and visible: this thread's transfers drained
-         * (counted waits do not cover their LDS writes), then the barrier,
-         * which also tells every wave that stage s - 1 is no longer read */
-        if (s + NSTG - 1 < n_steps) {
-            /* wait for all but the transfers of the one younger stage in
-             * flight (vmcnt(n): 0x3F70 | n, n < 16) */
-            if constexpr (NSTG == 3) {
-                static_assert(WDMA + XDMA + 1 < 16, "vmcnt field");
-                constexpr int PER = WDMA + XDMA;
-                if (NORM && wave == 0) __builtin_amdgcn_s_waitcnt(0x3F70 | (PER + 1));
-                else __builtin_amdgcn_s_waitcnt(0x3F70 | PER);
-            } else {
-                __builtin_amdgcn_s_waitcnt(0);
-            }
-        } else {
-            __builtin_amdgcn_s_waitcnt(0);
-        }
+        /* stage s complete and visible: all of this thread's transfers
+         * drained (vmcnt(0), explicit: the compiler's own waits do not count
+         * the inline-asm transfers; a count that leaves the younger stage in
+         * flight measured no faster, and on pages touched for the first time
+         * transfers need not land in issue order), then the barrier, which
+         * also tells every wave that stage s - 1 is no longer read */
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (s + NSTG - 1 < n_steps) issue(s + NSTG - 1, (u + NSTG - 1) % NSTG);
         const unsigned char *st = smem + u * STAGE;
