@@ -191,7 +191,8 @@ REF_DECODER = "/root/reference/common/decoder"
 
 
 def _integration_c_blocks():
-    """The ```c code blocks of INTEGRATION.md's decoder-level section, in order."""
+    """The ```c code blocks of the integration guide's decoder-level section
+    (its second section), in order."""
     import re
     text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     sec = text[text.index("## 2."):text.index("## 3.")]
@@ -201,7 +202,7 @@ def _integration_c_blocks():
 @pytest.mark.skipif(not os.path.exists(os.path.join(REF_DECODER, "qkn_decoder.h")),
                     reason="the reference tree is not present")
 def test_integration_snippets_compile_against_reference_decoder(tmp_path):
-    """The decoder-level replacement INTEGRATION.md shows for
+    """The decoder-level replacement the integration guide shows for
     qkn_decoder.c:460-528 / :625-677 (and the device layer loop) compiles as
     one C11 translation unit against the reference's own qkn_decoder.h and
     this repository's headers: every qkn_ctx_t / qkn_config_t field and every
