@@ -324,6 +324,91 @@ def measure_decoder(ctx, sa, steps, warmup, prefix=1024, n_layers=28, dim=1024, 
     return d
 
 
+def measure_decoder_bf16(ctx, sa, steps, warmup, prefix=1024, n_layers=28, dim=1024, inter=3072):
+    """The bf16 decoder's layers (smol_qkn_layer_*_bf16: bf16 residual stream,
+    truncating projections and row operations, GeGLU) at the Qwen3-0.6B sizes
+    of measure_decoder: a `prefix`-token prefill of the 28 layers, then
+    single-token steps. Random bf16 weights generated on the device."""
+    import ctypes
+    import gc
+    import torch
+    gc.collect()
+    torch.cuda.synchronize()
+    H, Hkv, hd = 16, 8, 128
+    owner = ctypes.create_string_buffer(256)
+    blk = sa.QknAttn(owner, n_layers=n_layers, n_heads=H, n_kv_heads=Hkv, head_dim=hd, eps=1e-6, rope_theta=1e6,
+                     rope_local_theta=0.0, rope_type=0, sliding_window=0, attn_logit_softcap=0.0, bf16=1,
+                     on_device=1, device=0, max_seq=prefix + steps + warmup + 8)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(12)
+
+    def proj(o, i):
+        return (torch.randn((o, i), generator=g, device="cuda") * i ** -0.5).to(torch.bfloat16)
+
+    def nw(n):
+        return 1.0 + 0.1 * torch.randn((n,), generator=g, device="cuda")
+
+    W = []
+    for li in range(n_layers):
+        blk.set_layer(li, 0, (1.0 + 0.1 * np.random.default_rng(li).standard_normal(hd)).astype(np.float32),
+                      (1.0 + 0.1 * np.random.default_rng(100 + li).standard_normal(hd)).astype(np.float32))
+        W.append(sa.QknLayerWeights(input_norm=nw(dim), wq=proj(H * hd, dim), wk=proj(Hkv * hd, dim),
+                                    wv=proj(Hkv * hd, dim), wo=proj(dim, H * hd), post_attn_norm=nw(dim),
+                                    pre_ffn_norm=None, post_ffn_norm=None, gate_up=proj(2 * inter, dim),
+                                    down=proj(dim, inter)))
+    lib = sa.load()
+    addr = blk.addr
+    x0 = torch.randn((prefix, dim), generator=g, device="cuda").to(torch.bfloat16).view(torch.int16)
+    x = x0.clone()
+    prefill_s = []
+    for rep in range(3):
+        x.copy_(x0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for li in range(n_layers):
+            if lib.smol_qkn_layer_prefill_bf16(addr, li, 0, prefix, ctypes.c_void_p(x.data_ptr()),
+                                               ctypes.byref(W[li].s), dim, inter):
+                raise RuntimeError(lib.smol_attn_last_error().decode())
+        blk.synchronize()
+        prefill_s.append(time.perf_counter() - t0)
+    prefill_s = min(prefill_s[1:])
+    xt = torch.randn((1, dim), generator=g, device="cuda").to(torch.bfloat16).view(torch.int16)
+    xp = ctypes.c_void_p(xt.data_ptr())
+
+    def token(pos):
+        for li in range(n_layers):
+            if lib.smol_qkn_layer_forward_bf16(addr, li, pos, xp, ctypes.byref(W[li].s), dim, inter):
+                raise RuntimeError(lib.smol_attn_last_error().decode())
+
+    pos = prefix
+    gc.disable()
+    try:
+        for _ in range(warmup):
+            token(pos)
+            pos += 1
+        blk.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            token(pos)
+            pos += 1
+        blk.synchronize()
+        wall = time.perf_counter() - t0
+    finally:
+        gc.enable()
+    ms_tok = wall / steps * 1e3
+    d = {"config": {"workload": "qwen06b_bf16_decoder_step", "layers": n_layers, "hidden": dim,
+                    "heads": [H, Hkv, hd], "intermediate": inter, "cached_tokens": prefix,
+                    "activations": "bf16 (truncating, GeGLU)", "weights": "random bf16 on the device"},
+         "ms_per_token": round(ms_tok, 4), "tokens_per_s": round(1e3 / ms_tok, 1),
+         "prefill_tokens_per_s": round(prefix / prefill_s, 1),
+         "prefill_ms_%d_tokens" % prefix: round(prefill_s * 1e3, 3),
+         "note": "the bf16 decoder's layer order (qkn_bf16_decoder.c:482-571, 634-697) at the fp32 step's "
+                 "sizes; no CPU baseline of its own"}
+    blk.close()
+    del W, x, xt
+    return d
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -500,6 +585,8 @@ def main():
         if cpu_mod:
             d["cpu_baseline"] = cpu_mod.decoder_step_sample()
         detail["qwen06b_decoder_step"] = d
+    if args.only in (None, "qwen06b_bf16_decoder_step"):
+        detail["qwen06b_bf16_decoder_step"] = measure_decoder_bf16(ctx, sa, max(10, steps // 5), max(2, warmup // 2))
 
     # ---------------- CPU baseline of the headline (reference CPU attention on this host)
     if cpu_mod and head is not None:

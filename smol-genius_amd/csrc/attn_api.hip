@@ -45,8 +45,9 @@ extern "C" int smol_launch_win(const WinParams *wp, int hd, int n_tiles, int max
                                hipEvent_t e1);
 extern "C" int smol_win_max_keys(int hd, int in_dtype, int precise);
 extern "C" int smol_launch_to_bf16_trunc(const float *x, uint16_t *y, long long n, hipStream_t st);
-extern "C" int smol_launch_bf16_norm_rope(uint16_t *x, const float *w, float eps, const float *cos_t,
-                                          const float *sin_t, int pos0, int seq, int H, int hd, hipStream_t st);
+extern "C" int smol_launch_bf16_norm_rope(uint16_t *x, const float *w, uint16_t *x2, const float *w2, int H2,
+                                          float eps, const float *cos_t, const float *sin_t, int pos0, int seq, int H,
+                                          int hd, hipStream_t st);
 extern "C" int smol_launch_norm_rope(float *x, const float *w, float eps, const float *cos_t, const float *sin_t,
                                      const int *pos, int seq, int n_heads, int hd, int kind, hipStream_t st);
 
@@ -1837,25 +1838,43 @@ extern "C" int smol_attn_norm_rope(smol_attn_ctx *ctx, const smol_rope_table *ro
     return SMOL_ATTN_OK;
 }
 
-extern "C" int smol_attn_norm_rope_bf16(smol_attn_ctx *ctx, const smol_rope_table *rope, uint16_t *x,
-                                        const float *weight, float eps, int pos0, int seq, int n_heads,
-                                        int head_dim) {
-    if (!ctx || !x || seq <= 0 || n_heads <= 0 || head_dim <= 0 || (head_dim & 7) || pos0 < 0)
+/* the Q rows (q, q_weight, n_heads) and, when k is not NULL, the K rows (k,
+ * k_weight, n_kv_heads) of one call in one launch */
+static int norm_rope_bf16(smol_attn_ctx *ctx, const smol_rope_table *rope, uint16_t *x, const float *weight,
+                          uint16_t *k, const float *k_weight, int n_kv_heads, float eps, int pos0, int seq,
+                          int n_heads, int head_dim) {
+    if (!ctx || !x || seq <= 0 || n_heads <= 0 || head_dim <= 0 || (head_dim & 7) || pos0 < 0 ||
+        (k && n_kv_heads <= 0))
         return fail(SMOL_ATTN_ERR_ARG, "bad arguments (head_dim must be a multiple of 8)");
     if (rope && (rope->hd != head_dim || rope->type != SMOL_ROPE_INTERLEAVED))
         return fail(SMOL_ATTN_ERR_ARG, "the bf16 rotation needs an interleaved table of head_dim %d", head_dim);
     if (rope && rope->ctx != ctx) return fail(SMOL_ATTN_ERR_ARG, "rope table belongs to another context");
-    if (weight && !(eps >= 0.0f)) return fail(SMOL_ATTN_ERR_ARG, "norm eps %g", (double)eps);
-    if (((uintptr_t)x & 15) || ((uintptr_t)weight & 3))
+    if ((weight || k_weight) && !(eps >= 0.0f)) return fail(SMOL_ATTN_ERR_ARG, "norm eps %g", (double)eps);
+    if (((uintptr_t)x & 15) || ((uintptr_t)weight & 3) || ((uintptr_t)k & 15) || ((uintptr_t)k_weight & 3))
         return fail(SMOL_ATTN_ERR_ARG, "x must be 16-byte and weight 4-byte aligned");
     int rc = set_device(ctx);
     if (rc) return rc;
-    if (!rope && !weight) return SMOL_ATTN_OK;
+    if (!rope && !weight && !k_weight) return SMOL_ATTN_OK;
     if (rope && (rc = smol_rope_table_ensure(const_cast<smol_rope_table *>(rope), pos0 + seq))) return rc;
-    if (smol_launch_bf16_norm_rope(x, weight, eps, rope ? rope->cos_d : nullptr, rope ? rope->sin_d : nullptr, pos0,
-                                   seq, n_heads, head_dim, ctx->stream))
+    if (smol_launch_bf16_norm_rope(x, weight, k, k_weight, n_kv_heads, eps, rope ? rope->cos_d : nullptr,
+                                   rope ? rope->sin_d : nullptr, pos0, seq, n_heads, head_dim, ctx->stream))
         return fail(SMOL_ATTN_ERR_DEVICE, "bf16 norm/rope launch: %s", hipGetErrorString(hipGetLastError()));
     return SMOL_ATTN_OK;
+}
+
+extern "C" int smol_attn_norm_rope_bf16(smol_attn_ctx *ctx, const smol_rope_table *rope, uint16_t *x,
+                                        const float *weight, float eps, int pos0, int seq, int n_heads,
+                                        int head_dim) {
+    return norm_rope_bf16(ctx, rope, x, weight, nullptr, nullptr, 0, eps, pos0, seq, n_heads, head_dim);
+}
+
+/* for qkn_attn.hip: smol_attn_norm_rope_bf16 of a call's Q and K rows (each
+ * with its own norm weight) as one launch */
+extern "C" int smol_internal_norm_rope_bf16_qk(smol_attn_ctx *ctx, const smol_rope_table *rope, uint16_t *q,
+                                               const float *q_weight, uint16_t *k, const float *k_weight, float eps,
+                                               int pos0, int seq, int n_heads, int n_kv_heads, int head_dim) {
+    if (!k) return fail(SMOL_ATTN_ERR_ARG, "k is NULL");
+    return norm_rope_bf16(ctx, rope, q, q_weight, k, k_weight, n_kv_heads, eps, pos0, seq, n_heads, head_dim);
 }
 
 /* ============================================ reference-signature drop-ins */

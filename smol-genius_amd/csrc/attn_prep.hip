@@ -332,15 +332,22 @@ __device__ __forceinline__ float sqrt_rn(float x) {
  *   v' = trunc((v * r) * w[d])
  *   x0' = trunc(fma(x0, c, -(x1 * s))), x1' = trunc(fma(x1, c, x0 * s))
  * with c, s the table entries of column 2i. hd is a multiple of 8. */
-__global__ __launch_bounds__(256) void k_bf16_norm_rope(uint16_t *x, const float *w, float eps, const float *cos_t,
-                                                        const float *sin_t, int pos0, int seq, int H, int hd) {
-    const long long rows = (long long)seq * H;
+/* rows [0, seq H) of x (weight w) and then rows [0, seq H2) of x2 (weight
+ * w2; x2 NULL: none), one thread per head row */
+__global__ __launch_bounds__(256) void k_bf16_norm_rope(uint16_t *x, const float *w, uint16_t *x2, const float *w2,
+                                                        float eps, const float *cos_t, const float *sin_t, int pos0,
+                                                        int seq, int H, int H2, int hd) {
+    const long long rows1 = (long long)seq * H, rows = rows1 + (x2 ? (long long)seq * H2 : 0);
     const long long step = (long long)gridDim.x * blockDim.x;
-    for (long long r = (long long)blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += step) {
-        uint4 *row = reinterpret_cast<uint4 *>(x + r * hd);
+    for (long long rr = (long long)blockIdx.x * blockDim.x + threadIdx.x; rr < rows; rr += step) {
+        const bool second = rr >= rows1;
+        const long long r = second ? rr - rows1 : rr;
+        const int Hr = second ? H2 : H;
+        const float *w_r = second ? w2 : w;
+        uint4 *row = reinterpret_cast<uint4 *>((second ? x2 : x) + r * hd);
         const int n8 = hd >> 3;
         float ri = 1.0f;
-        if (w) {
+        if (w_r) {
             float ss = 0.0f;
             for (int c8 = 0; c8 < n8; c8++) {
                 float v[8];
@@ -350,14 +357,14 @@ __global__ __launch_bounds__(256) void k_bf16_norm_rope(uint16_t *x, const float
             }
             ri = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)hd), eps)));
         }
-        const float *ct = cos_t ? cos_t + (long long)(pos0 + r / H) * hd : nullptr;
-        const float *st = cos_t ? sin_t + (long long)(pos0 + r / H) * hd : nullptr;
+        const float *ct = cos_t ? cos_t + (long long)(pos0 + r / Hr) * hd : nullptr;
+        const float *st = cos_t ? sin_t + (long long)(pos0 + r / Hr) * hd : nullptr;
         for (int c8 = 0; c8 < n8; c8++) {
             float v[8];
             unpack_bf16x8(row[c8], v);
-            if (w) {
+            if (w_r) {
 #pragma unroll
-                for (int i = 0; i < 8; i++) v[i] = __uint_as_float(__float_as_uint(__fmul_rn(__fmul_rn(v[i], ri), w[c8 * 8 + i])) & 0xFFFF0000u);
+                for (int i = 0; i < 8; i++) v[i] = __uint_as_float(__float_as_uint(__fmul_rn(__fmul_rn(v[i], ri), w_r[c8 * 8 + i])) & 0xFFFF0000u);
             }
             if (ct) {
 #pragma unroll
@@ -377,12 +384,16 @@ __global__ __launch_bounds__(256) void k_bf16_norm_rope(uint16_t *x, const float
     }
 }
 
-extern "C" int smol_launch_bf16_norm_rope(uint16_t *x, const float *w, float eps, const float *cos_t,
-                                          const float *sin_t, int pos0, int seq, int H, int hd, hipStream_t st) {
-    const long long rows = (long long)seq * H;
+/* x2 / w2 / H2: a second tensor at the same positions (NULL: none), the K
+ * rows of the call that normalises and rotates its Q rows in x */
+extern "C" int smol_launch_bf16_norm_rope(uint16_t *x, const float *w, uint16_t *x2, const float *w2, int H2,
+                                          float eps, const float *cos_t, const float *sin_t, int pos0, int seq, int H,
+                                          int hd, hipStream_t st) {
+    const long long rows = (long long)seq * H + (x2 ? (long long)seq * H2 : 0);
     if (rows <= 0) return 0;
     const int blocks = (int)std::min<long long>((rows + 255) / 256, 4096);
-    hipLaunchKernelGGL(k_bf16_norm_rope, dim3(blocks), dim3(256), 0, st, x, w, eps, cos_t, sin_t, pos0, seq, H, hd);
+    hipLaunchKernelGGL(k_bf16_norm_rope, dim3(blocks), dim3(256), 0, st, x, w, x2, w2, eps, cos_t, sin_t, pos0, seq,
+                       H, H2, hd);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 

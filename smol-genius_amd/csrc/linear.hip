@@ -90,9 +90,20 @@ struct GemvParams {
     float eps;
     int act;             /* SMOL_LINEAR_ACT_*: rows (2j, 2j + 1) are (gate, up), y[s][j] = act(gate) up */
     const float *res;    /* [seq][y columns] or null: added to the result (may equal y) */
+    /* the bf16 decoder's operations (bf16 y, one segment, not FUSE; every
+     * step truncated as qkn_bf16_decoder.c does): act GEGLU: y[s][j] =
+     * geglu(tr(gate), tr(up)) as k_bf16_geglu; res16: y = tr(bf(res16) +
+     * bf(tr(sum))) as k_bf16_rows' add (may equal y); x_trunc: an fp32 x is
+     * truncated to bf16 as it is loaded */
+    const uint16_t *res16;
+    int x_trunc;
 };
 
 /* ---------------------------------------------------------------- kernels */
+
+/* bf16 bits widened to fp32, and fp32 truncated to bf16 bits */
+__device__ __forceinline__ float bfw(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+__device__ __forceinline__ uint16_t bftr(float v) { return (uint16_t)(__float_as_uint(v) >> 16); }
 
 /* sum over the 64 lanes, the total in every lane */
 __device__ __forceinline__ float wave_sum(float v) {
@@ -153,6 +164,7 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
         for (int s = 0; s < SEQ; s++) acc[r][s] = 0.0f;
 
     const int C = (in + 7) >> 3; /* chunks per row */
+    const uint32_t xmask = !FUSE && p.x_trunc ? 0xffff0000u : 0xffffffffu;
     const int stride = 64 * kp;
     for (int c0 = wave * 64; c0 < C; c0 += stride * GEMV_U) {
         float wf[GEMV_U][GEMV_R][8];
@@ -205,7 +217,7 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
                         const uint4 a = xv[u][s][0], b = xv[u][s][1];
                         const uint32_t t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-                        for (int e = 0; e < 8; e++) xf[u][s][e] = __uint_as_float(t[e]);
+                        for (int e = 0; e < 8; e++) xf[u][s][e] = __uint_as_float(t[e] & xmask);
                     }
                 }
             }
@@ -234,7 +246,7 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
                             xf[u][s][e] = __uint_as_float((uint32_t)h << 16);
                         } else {
                             xf[u][s][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                                xr, ok ? (unsigned)(s * in + i) * 4u : OOB_OFF, 0, 0));
+                                xr, ok ? (unsigned)(s * in + i) * 4u : OOB_OFF, 0, 0) & xmask);
                         }
                     }
                 }
@@ -334,6 +346,25 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
         }
         return;
     }
+    if constexpr (YBF) {
+        if (p.act) {
+            /* bf16 GeGLU (one segment): lane i holds row r, the up row of
+             * gate row r (even) is in lane i + 1; both truncated first, then
+             * the arithmetic of k_bf16_geglu */
+            const int r = lane % GEMV_R, s = lane / GEMV_R;
+            const int row = row_base + r;
+            const float vt = bfw(bftr(mine + (p.bias[0] && row < p.rows ? p.bias[0][row] : 0.0f)));
+            const float u = __shfl_down(vt, 1);
+            if (lane < GEMV_R * SEQ && row < p.rows && (r & 1) == 0) {
+                const float g = vt;
+                const float x3 = __fmul_rn(__fmul_rn(g, g), g);
+                const float inner = __fmul_rn(0.7978845608028654f, __fadd_rn(g, __fmul_rn(0.044715f, x3)));
+                const float gl = __fmul_rn(__fmul_rn(0.5f, g), __fadd_rn(1.0f, tanhf(inner)));
+                static_cast<uint16_t *>(p.y[0])[(long long)s * (p.out[0] >> 1) + (row >> 1)] = bftr(__fmul_rn(gl, u));
+            }
+            return;
+        }
+    }
     if (lane < GEMV_R * SEQ) {
         const int r = lane % GEMV_R, s = lane / GEMV_R;
         const int row = row_base + r;
@@ -347,9 +378,12 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
             void *y = sg == 0 ? p.y[0] : sg == 1 ? p.y[1] : p.y[2];
             const int o = row - r0;
             const float v = mine + (bias ? bias[o] : 0.0f);
-            if constexpr (YBF)
-                static_cast<uint16_t *>(y)[(long long)s * out + o] = (uint16_t)(__float_as_uint(v) >> 16);
-            else
+            if constexpr (YBF) {
+                const long long j = (long long)s * out + o;
+                uint16_t t = (uint16_t)(__float_as_uint(v) >> 16);
+                if (p.res16) t = bftr(bfw(p.res16[j]) + bfw(t)); /* the residual is segment 0's */
+                static_cast<uint16_t *>(y)[j] = t;
+            } else
                 static_cast<float *>(y)[(long long)s * out + o] = v;
         }
     }
@@ -387,10 +421,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(float *out, const float *x
  *   geglu(g, u)  = tr(0.5 g (1 + tanhf(0.7978845608028654 (g + 0.044715 g^3))) * u)
  *                                                       (bf16_geglu, :235-251)
  * The sums of squares run in a fixed order: per-thread strided fused
- * multiply-adds, a butterfly over the wave, then the four waves in order. */
-
-__device__ __forceinline__ float bfw(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
-__device__ __forceinline__ uint16_t bftr(float v) { return (uint16_t)(__float_as_uint(v) >> 16); }
+ * multiply-adds, a butterfly over the wave, then the four waves in order
+ * (bfw / bftr: the widening and the truncation, defined with the GEMV). */
 
 /* the sum of v over the 256 threads, returned to every thread */
 __device__ __forceinline__ float block_sum256(float v, float *red) {
@@ -535,8 +567,15 @@ bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 /* one GEMV launch over n_seg weight segments (f: fused operations, one
  * segment, fp32 x and y) */
+/* the bf16 decoder's operations of a GEMV with a bf16 y (GemvParams) */
+struct GemvBf16Ops {
+    int act;               /* SMOL_LINEAR_ACT_NONE or _GEGLU */
+    const uint16_t *res16; /* or null */
+    bool x_trunc;
+};
+
 int run_gemv(smol_attn_ctx *ctx, hipStream_t st, const void *x, bool xbf, bool ybf, int seq, int in, int n_seg,
-             const GemvSeg *segs, const GemvFuse *f = nullptr) {
+             const GemvSeg *segs, const GemvFuse *f = nullptr, const GemvBf16Ops *bo = nullptr) {
     GemvParams p{};
     p.x = x;
     p.in = in;
@@ -545,6 +584,10 @@ int run_gemv(smol_attn_ctx *ctx, hipStream_t st, const void *x, bool xbf, bool y
         p.eps = f->eps;
         p.act = f->act;
         p.res = f->res;
+    } else if (bo) {
+        p.act = bo->act;
+        p.res16 = bo->res16;
+        p.x_trunc = bo->x_trunc ? 1 : 0;
     }
     int rows = 0;
     bool vec = (in % 8) == 0 && aligned16(x) && aligned16(p.norm_w);
@@ -731,6 +774,24 @@ extern "C" int smol_linear_dev(smol_attn_ctx *ctx, void *y, int y_dtype, const v
     if (seq <= SMOL_LINEAR_GEMV_MAX_SEQ || in_dim == 0)
         return run_gemv_rows(ctx, st, y, ybf, x, xbf, w, bias, seq, in_dim, out_dim);
     return run_gemm(ctx, st, y, ybf, x, xbf, w, bias, seq, in_dim, out_dim);
+}
+
+/* For the bf16 decoder's layer (qkn_attn.hip), seq <= SMOL_LINEAR_GEMV_MAX_SEQ
+ * only: y [seq][out or out / 2] bf16 = the truncating projection of x (bf16,
+ * or fp32 truncated to bf16 as it is loaded: x_f32_trunc), then act GEGLU of
+ * the (gate, up) pairs (bf16_geglu) or the residual add y = tr(bf(res16) +
+ * bf(y)) (bf16_add_inplace; res16 may equal y), in the one GEMV launch. */
+extern "C" int smol_internal_linear_bf16_ops(smol_attn_ctx *ctx, uint16_t *y, const void *x, int x_f32_trunc,
+                                             const uint16_t *w, int seq, int in_dim, int out_dim, int act,
+                                             const uint16_t *res16) {
+    if (!ctx || !y || !x || !w || seq <= 0 || seq > SMOL_LINEAR_GEMV_MAX_SEQ || in_dim <= 0 || out_dim <= 0 ||
+        (act != SMOL_LINEAR_ACT_NONE && act != SMOL_LINEAR_ACT_GEGLU) || (act && ((out_dim & 1) || res16)))
+        return lfail(SMOL_ATTN_ERR_ARG, "smol_internal_linear_bf16_ops: arguments");
+    LHIP(hipSetDevice(smol_internal_ctx_device(ctx)));
+    hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
+    const GemvSeg sg{w, nullptr, y, out_dim};
+    const GemvBf16Ops bo{act, res16, x_f32_trunc != 0};
+    return run_gemv(ctx, st, x, x_f32_trunc == 0, true, seq, in_dim, 1, &sg, nullptr, &bo);
 }
 
 extern "C" int smol_linear_qkv_dev(smol_attn_ctx *ctx, void *q, void *k, void *v, int y_dtype, const void *x,

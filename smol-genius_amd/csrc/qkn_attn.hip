@@ -35,6 +35,13 @@ extern "C" void smol_internal_gdec_destroy(smol_graph_dec *g);
 extern "C" void smol_internal_gdec_capture(smol_attn_ctx *ctx, smol_graph_dec *g);
 extern "C" int smol_internal_gdec_step(smol_attn_ctx *ctx, smol_graph_dec *g, int pos, int slot);
 
+extern "C" int smol_internal_norm_rope_bf16_qk(smol_attn_ctx *ctx, const smol_rope_table *rope, uint16_t *q,
+                                               const float *q_weight, uint16_t *k, const float *k_weight, float eps,
+                                               int pos0, int seq, int n_heads, int n_kv_heads, int head_dim);
+extern "C" int smol_internal_linear_bf16_ops(smol_attn_ctx *ctx, uint16_t *y, const void *x, int x_f32_trunc,
+                                             const uint16_t *w, int seq, int in_dim, int out_dim, int act,
+                                             const uint16_t *res16);
+
 namespace {
 
 int qfail(int code, const char *msg) { return smol_internal_fail(code, msg); }
@@ -113,8 +120,11 @@ bool hd_ok(int hd) { return hd == 64 || hd == 72 || hd == 80 || hd == 96 || hd =
 
 /* The whole block for seq_len rows at start_pos (decode: one launch of the
  * direct decode kernel when seq_len == 1 and `decode` is set). */
+/* out32 (bf16 bindings on the device): non-NULL receives the fp32 result
+ * and the bf16 conversion into attn_out is left to the caller (the layer's
+ * o_proj truncates it as it loads it) */
 int run_block(Binding *b, int layer, int start_pos, int seq_len, const void *q, const void *k, const void *v,
-              void *attn_out, bool decode, bool sync = true, bool own_qk = false) {
+              void *attn_out, bool decode, bool sync = true, bool own_qk = false, float **out32 = nullptr) {
     const smol_qkn_attn_config &c = b->cfg;
     if (layer < 0 || layer >= c.n_layers) return qfail(SMOL_ATTN_ERR_ARG, "layer out of range");
     if (start_pos < 0 || seq_len <= 0) return qfail(SMOL_ATTN_ERR_ARG, "bad start_pos / seq_len");
@@ -161,10 +171,8 @@ int run_block(Binding *b, int layer, int start_pos, int seq_len, const void *q, 
     if (c.bf16) {
         /* per-head norm + rotation rounded by truncation, then the rows go
          * into the cache as their bits (no further rounding: bf16 in) */
-        if ((rc = smol_attn_norm_rope_bf16(b->ctx, rope, (uint16_t *)dq, qn, c.eps, start_pos, seq_len, c.n_heads, hd)))
-            return rc;
-        if ((rc = smol_attn_norm_rope_bf16(b->ctx, rope, (uint16_t *)dk, kn, c.eps, start_pos, seq_len, c.n_kv_heads,
-                                           hd)))
+        if ((rc = smol_internal_norm_rope_bf16_qk(b->ctx, rope, (uint16_t *)dq, qn, (uint16_t *)dk, kn, c.eps,
+                                                  start_pos, seq_len, c.n_heads, c.n_kv_heads, hd)))
             return rc;
         if (decode) {
             const int slot = 0;
@@ -175,6 +183,10 @@ int run_block(Binding *b, int layer, int start_pos, int seq_len, const void *q, 
                                    c.n_heads, scale, window, cap, out);
         }
         if (rc) return rc;
+        if (out32 && c.on_device) {
+            *out32 = out;
+            return sync ? smol_attn_ctx_synchronize(b->ctx) : SMOL_ATTN_OK;
+        }
         uint16_t *o16 = (uint16_t *)attn_out;
         if (!c.on_device) {
             if ((rc = reserve(b, b->out16, q_elems * 2))) return rc;
@@ -292,15 +304,35 @@ int run_layer_bf16(Binding *b, int layer, int pos, int n, uint16_t *x, const smo
     const int BF = SMOL_ATTN_BF16;
     if ((rc = smol_bf16_rms_norm_dev(ctx, xn, x, w->input_norm, n, dim, c.eps))) return rc;
     if ((rc = smol_linear_qkv_dev(ctx, q, k, v, BF, xn, BF, w->wq, w->wk, w->wv, n, dim, q_dim, kv_dim))) return rc;
-    if ((rc = run_block(b, layer, pos, n, q, k, v, attn, decode, !decode, true))) return rc;
-    if ((rc = smol_linear_dev(ctx, p, BF, attn, BF, w->wo, nullptr, n, q_dim, dim))) return rc;
+    /* a few rows (decode): the GEMV launches take the attention output as
+     * fp32 and truncate it as they load it, and fold GeGLU into gate_up and
+     * the last residual add into down (the same truncations, three launches
+     * fewer) */
+    const bool few = n <= SMOL_LINEAR_GEMV_MAX_SEQ;
+    float *attn32 = nullptr;
+    if ((rc = run_block(b, layer, pos, n, q, k, v, attn, decode, !decode, true, few ? &attn32 : nullptr))) return rc;
+    if (few && attn32) {
+        if ((rc = smol_internal_linear_bf16_ops(ctx, p, attn32, 1, w->wo, n, q_dim, dim, SMOL_LINEAR_ACT_NONE,
+                                                nullptr)))
+            return rc;
+    } else if ((rc = smol_linear_dev(ctx, p, BF, attn, BF, w->wo, nullptr, n, q_dim, dim))) {
+        return rc;
+    }
     if (w->pre_ffn_norm)
         rc = smol_bf16_add_norm_dev(ctx, x, p, w->post_attn_norm, w->pre_ffn_norm, xn, n, dim, c.eps);
     else
         rc = smol_bf16_add_norm_dev(ctx, x, p, nullptr, w->post_attn_norm, xn, n, dim, c.eps);
     if (rc) return rc;
-    if ((rc = smol_linear_dev(ctx, gu, BF, xn, BF, w->gate_up, nullptr, n, dim, 2 * inter))) return rc;
-    if ((rc = smol_bf16_geglu_dev(ctx, g, gu, n, inter))) return rc;
+    if (few) {
+        if ((rc = smol_internal_linear_bf16_ops(ctx, g, xn, 0, w->gate_up, n, dim, 2 * inter, SMOL_LINEAR_ACT_GEGLU,
+                                                nullptr)))
+            return rc;
+        if (!w->post_ffn_norm)
+            return smol_internal_linear_bf16_ops(ctx, x, g, 0, w->down, n, inter, dim, SMOL_LINEAR_ACT_NONE, x);
+    } else {
+        if ((rc = smol_linear_dev(ctx, gu, BF, xn, BF, w->gate_up, nullptr, n, dim, 2 * inter))) return rc;
+        if ((rc = smol_bf16_geglu_dev(ctx, g, gu, n, inter))) return rc;
+    }
     if ((rc = smol_linear_dev(ctx, p, BF, g, BF, w->down, nullptr, n, inter, dim))) return rc;
     return smol_bf16_add_norm_dev(ctx, x, p, w->post_ffn_norm, nullptr, nullptr, n, dim, c.eps);
 }
