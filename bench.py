@@ -403,7 +403,7 @@ def measure_decoder_bf16(ctx, sa, steps, warmup, prefix=1024, n_layers=28, dim=1
          "prefill_tokens_per_s": round(prefix / prefill_s, 1),
          "prefill_ms_%d_tokens" % prefix: round(prefill_s * 1e3, 3),
          "note": "the bf16 decoder's layer order (qkn_bf16_decoder.c:482-571, 634-697) at the fp32 step's "
-                 "sizes; no CPU baseline of its own"}
+                 "sizes"}
     blk.close()
     del W, x, xt
     return d
@@ -586,7 +586,10 @@ def main():
             d["cpu_baseline"] = cpu_mod.decoder_step_sample()
         detail["qwen06b_decoder_step"] = d
     if args.only in (None, "qwen06b_bf16_decoder_step"):
-        detail["qwen06b_bf16_decoder_step"] = measure_decoder_bf16(ctx, sa, max(10, steps // 5), max(2, warmup // 2))
+        d = measure_decoder_bf16(ctx, sa, max(10, steps // 5), max(2, warmup // 2))
+        if cpu_mod:
+            d["cpu_baseline"] = cpu_mod.bf16_decoder_step_sample()
+        detail["qwen06b_bf16_decoder_step"] = d
 
     # ---------------- CPU baseline of the headline (reference CPU attention on this host)
     if cpu_mod and head is not None:

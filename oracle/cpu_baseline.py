@@ -247,3 +247,50 @@ def decoder_step_sample(n_layers=28, dim=1024, inter=3072, H=16, Hkv=8, hd=128, 
             "ms_per_token": round(sec * 1e3, 3), **host_facts(),
             "sample": "%d repetitions of one token through %d layers (%d cached tokens), scaled to %d layers" % (
                 reps, sample_layers, prefix, n_layers)}
+
+
+def bf16_decoder_step_sample(n_layers=28, dim=1024, inter=3072, H=16, Hkv=8, hd=128, prefix=1024, sample_layers=2,
+                             min_seconds=3.0, max_reps=20):
+    """One token through the bf16 decoder's layers (qkn_bf16_decoder.c:634-697) at
+    the Qwen3-0.6B sizes, on the oracle's single-threaded restatement of them
+    (decoder_oracle.Bf16Layer: truncating norms, projections, per-head norm,
+    interleaved rotation, two-pass attention over a `prefix`-row cache of random
+    bf16 rows, GeGLU, residual adds). The reference's own bf16 routines are
+    static inside its decoder and are not built here, so this is a port baseline.
+    Timed on `sample_layers` layers and scaled to n_layers."""
+    from decoder_oracle import Bf16Block, Bf16Layer
+    orc = Oracle()
+    rng = np.random.default_rng(6)
+
+    def bits(o, i):
+        w = (rng.standard_normal((o, i)) / np.sqrt(i)).astype(np.float32)
+        return (w.view(np.uint32) >> 16).astype(np.uint16)
+
+    blk = Bf16Block(orc, n_layers=sample_layers, n_heads=H, n_kv_heads=Hkv, head_dim=hd, eps=1e-6,
+                    rope_theta=1e6, rope_local_theta=0.0, rope_type=1, sliding_window=0, attn_logit_softcap=0.0,
+                    capacity=prefix + max_reps + 4)
+    weights = []
+    for li in range(sample_layers):
+        blk.set_layer(li, 0, (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32),
+                      (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32))
+        blk.ck[li, :prefix] = bits(prefix, Hkv * hd)
+        blk.cv[li, :prefix] = bits(prefix, Hkv * hd)
+        weights.append(dict(input_norm=(1 + 0.1 * rng.standard_normal(dim)).astype(np.float32),
+                            wq=bits(H * hd, dim), wk=bits(Hkv * hd, dim), wv=bits(Hkv * hd, dim),
+                            wo=bits(dim, H * hd), post_attn_norm=(1 + 0.1 * rng.standard_normal(dim)).astype(np.float32),
+                            gate_up=bits(2 * inter, dim), down=bits(dim, inter)))
+    layer = Bf16Layer(orc, blk, weights)
+    x0 = bits(1, dim)
+    reps, t = 0, 0.0
+    while reps < 2 or (t < min_seconds and reps < max_reps):
+        x = x0.copy()
+        t0 = time.perf_counter()
+        for li in range(sample_layers):
+            x = layer.step(li, prefix, x)
+        t += time.perf_counter() - t0
+        reps += 1
+    sec = t / reps * n_layers / sample_layers
+    return {"value": round(1.0 / sec, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "ms_per_token": round(sec * 1e3, 3), **host_facts(),
+            "sample": "%d repetitions of one token through %d layers (%d cached tokens) on the oracle's "
+                      "single-threaded bf16 layer, scaled to %d layers" % (reps, sample_layers, prefix, n_layers)}
