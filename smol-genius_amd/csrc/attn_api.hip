@@ -812,12 +812,29 @@ static void plan_fb_fill(Plan &pl, int Hkv, int G, int window, int cu_count, std
 
 /* the pre-pass blocks with their batches */
 /* the pre-pass blocks with their batches; without_q: the Q blocks are left
- * out (k_attn_fb prepares its Q rows itself) */
-static std::vector<PrepBlockB> prep_records(const Plan &pl, bool without_q) {
+ * out (k_attn_fb prepares its Q rows itself). A fresh slab becomes two
+ * blocks, its K and its V (count 1 and 2), when the launch then still fits
+ * the device in one round (`slots` workgroups at once): separate blocks keep
+ * twice as many loads in flight, a second round costs more than that */
+static std::vector<PrepBlockB> prep_records(const Plan &pl, bool without_q, int Hkv, int slots) {
+    long long n = 0, nf = 0;
+    for (const PrepBlock &b : pl.pblk) {
+        if (without_q && b.kind == 1) continue;
+        n++;
+        nf += b.kind == 0;
+    }
+    const bool split = (n + nf) * Hkv <= slots;
     std::vector<PrepBlockB> r;
-    r.reserve(pl.pblk.size());
-    for (const PrepBlock &b : pl.pblk)
-        if (!(without_q && b.kind == 1)) r.push_back({b, pl.pb[b.batch]});
+    r.reserve(pl.pblk.size() * 2);
+    for (const PrepBlock &b : pl.pblk) {
+        if (without_q && b.kind == 1) continue;
+        if (split && b.kind == 0 && b.count == 0) {
+            r.push_back({{b.batch, 0, b.first, 1}, pl.pb[b.batch]});
+            r.push_back({{b.batch, 0, b.first, 2}, pl.pb[b.batch]});
+        } else {
+            r.push_back({b, pl.pb[b.batch]});
+        }
+    }
     return r;
 }
 
@@ -1327,7 +1344,9 @@ static int run_plan(smol_attn_ctx *ctx, Plan &pl, const CallShape &cs) {
 
     /* descriptor tables in one upload: pre-pass blocks and items, each with
      * its batch */
-    const std::vector<PrepBlockB> pbr = prep_records(pl, q_in);
+    /* k_prep holds three workgroups a compute unit (registers of the normed
+     * build, 33 KB of LDS each) */
+    const std::vector<PrepBlockB> pbr = prep_records(pl, q_in, cs.Hkv, 3 * ctx->cu_count);
     std::vector<SkItemB> itr;
     if (fa && !fb) {
         itr.resize(pl.items.size());
@@ -1511,8 +1530,8 @@ extern "C" int smol_attn_prefill_qknorm(smol_attn_ctx *ctx, smol_kv_cache *kv, i
     const int f0 = pos0 & ~(SMOL_SLAB - 1);
     const int nf = ((pos0 + seq_q + SMOL_SLAB - 1) & ~(SMOL_SLAB - 1)) - f0;
     pl.pb.push_back({0, seq_q, 0, pos0, 0, seq_q, pos0, f0, nf, 0, slot, 0});
+    add_q_blocks(pl, 0, seq_q); /* the Q blocks (the longer ones) dispatched first */
     add_fresh_blocks(pl, 0, nf);
-    add_q_blocks(pl, 0, seq_q);
     pl.sb.push_back({seq_q * G, 0, 0, pos0, 0, pos0 + seq_q, 1, f0, 0, slot, 0, 0});
     pl.q_rows = seq_q * G;
     pl.fresh_rows = nf;
@@ -1620,8 +1639,8 @@ extern "C" int smol_attn_causal(smol_attn_ctx *ctx, const void *q, const void *k
     Plan pl;
     const int nf = (seq_k + SMOL_SLAB - 1) & ~(SMOL_SLAB - 1);
     pl.pb.push_back({0, seq_q, 0, 0, 0, seq_k, 0, 0, nf, 0, -1, 0});
+    add_q_blocks(pl, 0, seq_q); /* the Q blocks (the longer ones) dispatched first */
     add_fresh_blocks(pl, 0, nf);
-    add_q_blocks(pl, 0, seq_q);
     pl.sb.push_back({seq_q * G, 0, 0, q_offset, 0, seq_k, 1, 0, 0, -1, 0, 0});
     pl.q_rows = seq_q * G;
     pl.fresh_rows = nf;
@@ -1707,8 +1726,8 @@ extern "C" int smol_attn_bidirectional(smol_attn_ctx *ctx, const void *q, const 
     Plan pl;
     const int nf = (seq + SMOL_SLAB - 1) & ~(SMOL_SLAB - 1);
     pl.pb.push_back({0, seq, 0, 0, 0, seq, 0, 0, nf, 0, -1, 0});
+    add_q_blocks(pl, 0, seq); /* the Q blocks (the longer ones) dispatched first */
     add_fresh_blocks(pl, 0, nf);
-    add_q_blocks(pl, 0, seq);
     for (int w = 0; w < n_windows; w++) {
         const int a = ws[w], b = ws[w + 1];
         if (b <= a) continue;
@@ -1749,7 +1768,7 @@ extern "C" int smol_kv_cache_write(smol_kv_cache *kv, int layer, int slot, int p
     const size_t fcap = (size_t)nf;
     if ((rc = dev_reserve(ctx->kf, (size_t)kv->n_kv * fcap * hd * 2, ctx->stream))) return rc;
     if ((rc = dev_reserve(ctx->vtf, (size_t)kv->n_kv * fcap * hd * 2, ctx->stream))) return rc;
-    const std::vector<PrepBlockB> pbr = prep_records(pl, false);
+    const std::vector<PrepBlockB> pbr = prep_records(pl, false, kv->n_kv, 3 * ctx->cu_count);
     if ((rc = upload_desc(ctx, pbr.data(), pbr.size() * sizeof(PrepBlockB)))) return rc;
     PrepParams pp;
     memset(&pp, 0, sizeof(pp));
@@ -1763,7 +1782,7 @@ extern "C" int smol_kv_cache_write(smol_kv_cache *kv, int layer, int slot, int p
     pp.cap = kv->cap;
     pp.kf = (_Float16 *)ctx->kf.p; pp.vtf = (_Float16 *)ctx->vtf.p; pp.fcap = (int)fcap;
     pp.blocks = (const PrepBlockB *)ctx->desc.p;
-    rc = smol_launch_prep(&pp, (int)pl.pblk.size(), ctx->stream, nullptr, nullptr);
+    rc = smol_launch_prep(&pp, (int)pbr.size(), ctx->stream, nullptr, nullptr);
     if (!on_device) {
         hipStreamSynchronize(ctx->stream);
         hipFree(kd);

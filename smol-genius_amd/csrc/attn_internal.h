@@ -145,7 +145,7 @@ typedef struct {
     int batch;
     int kind;            /* 0: fresh slab, 1: Q tokens */
     int first;           /* slab index within the fresh window / first Q token */
-    int count;           /* Q tokens in this block */
+    int count;           /* Q tokens in this block; fresh slab: 0 its K and V, 1 its K, 2 its V */
 } PrepBlock;
 
 /* A pre-pass block with its batch (one round of scalar loads) */

@@ -110,9 +110,12 @@ __device__ __forceinline__ void prep_fresh(const PrepParams &p, const PrepBlock 
     _Float16 *kf = p.kf + (long long)g * p.fcap * HD;
     _Float16 *vtf = p.vtf + (long long)g * p.fcap * HD;
     const int new_lo = b.kv_pos0, new_hi = b.kv_pos0 + b.n_kv;
+    /* blk.count: 0 the slab's K and V, 1 its K only, 2 its V only (two
+     * blocks per slab double the workgroups that keep loads in flight) */
+    const bool doK = blk.count != 2, doV = blk.count != 1;
 
     /* per-head RMSNorm of the new K rows: row r by lanes 8r .. 8r+7 */
-    if constexpr (NORM) {
+    if (NORM && doK) {
         const int r = tid >> 3, pos = pos_base + r;
         if (pos >= new_lo && pos < new_hi) {
             const long long row = (long long)(b.kv_in0 + pos - new_lo) * p.kv_stride + (long long)g * HD;
@@ -137,11 +140,11 @@ __device__ __forceinline__ void prep_fresh(const PrepParams &p, const PrepBlock 
         const int pos = pos_base + r;
         if (NKC % 256 != 0 && e >= NKC) continue;
         if (pos < new_lo) {
-            if (has_cache) kold[u] = *reinterpret_cast<const uint4 *>(kc + (long long)pos * HD + d0);
+            if (has_cache && doK) kold[u] = *reinterpret_cast<const uint4 *>(kc + (long long)pos * HD + d0);
         } else if (pos < new_hi) {
             const long long row = (long long)(b.kv_in0 + pos - new_lo) * p.kv_stride + (long long)g * HD;
-            kin[u].load(p.k, row, d0, p.rope_cos, p.rope_sin, pos, p.k_norm);
-            raw_load<BF>(vin[u], p.v, row + d0);
+            if (doK) kin[u].load(p.k, row, d0, p.rope_cos, p.rope_sin, pos, p.k_norm);
+            if (doV) raw_load<BF>(vin[u], p.v, row + d0);
         }
     }
 #pragma unroll
@@ -151,35 +154,46 @@ __device__ __forceinline__ void prep_fresh(const PrepParams &p, const PrepBlock 
         const int pos = pos_base + r;
         const bool valid = NKC % 256 == 0 || e < NKC;
         const bool is_new = valid && pos >= new_lo && pos < new_hi;
-        float kv[8], vv[8];
-        /* every lane computes the new-row values (the NeoX partner shuffle
-         * needs all lanes); rows that are not new discard them */
-        kin[u].finish(kv, d0, NORM && is_new ? s_kr[r] : 1.0f);
-        raw_unpack<BF>(vin[u], vv);
-        if (!valid) continue;
-        if (!is_new) {
+        if (doK) {
+            float kv[8];
+            /* every lane computes the new-row values (the NeoX partner
+             * shuffle needs all lanes); rows that are not new discard them */
+            kin[u].finish(kv, d0, NORM && is_new ? s_kr[r] : 1.0f);
+            if (valid) {
+                if (!is_new) {
+                    if (pos < new_lo && has_cache) unpack_bf16x8(kold[u], kv);
+                    else {
 #pragma unroll
-            for (int i = 0; i < 8; i++) vv[i] = 0.0f;
-            if (pos < new_lo && has_cache) unpack_bf16x8(kold[u], kv);
-            else {
-#pragma unroll
-                for (int i = 0; i < 8; i++) kv[i] = 0.0f;
+                        for (int i = 0; i < 8; i++) kv[i] = 0.0f;
+                    }
+                }
+                if (has_cache && is_new) *reinterpret_cast<uint4 *>(kc + (long long)pos * HD + d0) = pack_bf16x8(kv);
+                note_h_range(p.range_flag, kv);
+                if (p.kf_lo) {
+                    uint4 hi, lo;
+                    pack_h8_hilo(kv, hi, lo);
+                    const long long fo = (long long)g * p.fcap * HD + (long long)(frow_base + r) * HD + d0;
+                    *reinterpret_cast<uint4 *>(kf + (long long)(frow_base + r) * HD + d0) = hi;
+                    *reinterpret_cast<uint4 *>(p.kf_lo + fo) = lo;
+                } else {
+                    *reinterpret_cast<uint4 *>(kf + (long long)(frow_base + r) * HD + d0) = pack_h8(kv);
+                }
             }
         }
-        if (has_cache && is_new) *reinterpret_cast<uint4 *>(kc + (long long)pos * HD + d0) = pack_bf16x8(kv);
-        note_h_range(p.range_flag, kv);
-        if (p.kf_lo) {
-            uint4 hi, lo;
-            pack_h8_hilo(kv, hi, lo);
-            const long long fo = (long long)g * p.fcap * HD + (long long)(frow_base + r) * HD + d0;
-            *reinterpret_cast<uint4 *>(kf + (long long)(frow_base + r) * HD + d0) = hi;
-            *reinterpret_cast<uint4 *>(p.kf_lo + fo) = lo;
-        } else {
-            *reinterpret_cast<uint4 *>(kf + (long long)(frow_base + r) * HD + d0) = pack_h8(kv);
-        }
+        if (doV) {
+            float vv[8];
+            raw_unpack<BF>(vin[u], vv);
+            if (valid) {
+                if (!is_new) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) sv[r * 257 + d0 + i] = vv[i];
+                    for (int i = 0; i < 8; i++) vv[i] = 0.0f;
+                }
+#pragma unroll
+                for (int i = 0; i < 8; i++) sv[r * 257 + d0 + i] = vv[i];
+            }
+        }
     }
+    if (!doV) return;
     __syncthreads();
     /* V^T (slab-blocked, the slab's 32 positions of column d are contiguous):
      * chunk (d, 8 consecutive positions q0..q0+7) */
