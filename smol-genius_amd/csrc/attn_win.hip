@@ -23,6 +23,10 @@
  *         slot cb ^ f(r), f(r) = (r & 3) | ((r >> 3) & 3) << 2.
  *   V^T : 16*DT rows of 64 bytes (32 keys); chunk jc (keys 8jc..8jc+7) of
  *         row d sits in slot jc ^ ((d >> 1) & 3).
+ *   V   : (bf16 inputs with the precise products, in place of V^T) 32 key
+ *         rows of 256 bytes as in the inputs; chunk q of key row r sits in
+ *         slot q ^ 2 fv(r), fv(r) = (r & 3) | ((r >> 3) & 1) << 2, and the
+ *         V^T fragments are read from it with the LDS transpose read.
  * Columns past head_dim and keys past the window are zeros.
  */
 #include "attn_device.h"
@@ -30,8 +34,9 @@
 namespace {
 
 /* KLO: the slab image holds K twice, fp16 hi then fp16 lo (precise QK^T on
- * fp32 inputs; bf16 inputs are exact in fp16 and need no lo part) */
-template <int HD, bool KLO>
+ * fp32 inputs; bf16 inputs are exact in fp16 and need no lo part). VROW: V
+ * as rows of the inputs (256-byte rows) instead of the V^T image. */
+template <int HD, bool KLO, bool VROW>
 struct WinGeom {
     static constexpr int KS = (HD + 31) / 32;  /* 32-wide d chunks of a K fragment */
     static constexpr int DT = (HD + 15) / 16;  /* 16-wide d tiles of the output */
@@ -39,7 +44,7 @@ struct WinGeom {
     static constexpr int KROW = 256;
     static constexpr int K_BYTES = SMOL_SLAB * KROW;
     static constexpr int KPARTS = KLO ? 2 : 1;
-    static constexpr int V_BYTES = 16 * DT * 64;
+    static constexpr int V_BYTES = VROW ? SMOL_SLAB * KROW : 16 * DT * 64;
     static constexpr int SLABB = KPARTS * K_BYTES + V_BYTES;
     static constexpr int NS_MAX = (160 * 1024) / SLABB; /* slabs the LDS holds */
 };
@@ -75,12 +80,13 @@ struct Raw8In {
 template <int HD, bool BF, int NS, bool PREC>
 __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
     constexpr bool KLO = PREC && !BF;
-    /* BFK (bf16 inputs, precise): K stays bf16 and goes straight into LDS
-     * (buffer_load ... lds, no registers), V^T is transposed as bf16, and the
-     * products run on bf16 MFMA with Q and P as bf16 hi + lo (K and V are
-     * exact, Q and P carry 16 bits) */
+    /* BFK (bf16 inputs, precise): K and V stay bf16 and go straight into
+     * LDS (buffer_load ... lds, no registers), the V^T fragments come from
+     * the V rows by the LDS transpose read, and the products run on bf16
+     * MFMA with Q and P as bf16 hi + lo (K and V are exact, Q and P carry 16
+     * bits) */
     constexpr bool BFK = BF && PREC;
-    using Gm = WinGeom<HD, KLO>;
+    using Gm = WinGeom<HD, KLO, BFK>;
     constexpr int KS = Gm::KS, DT = Gm::DT, HDP = Gm::HDP, KROW = Gm::KROW;
     constexpr int K_BYTES = Gm::K_BYTES, SLABB = Gm::SLABB;
     static_assert(HD % 8 == 0 && HD <= 128, "head_dim");
@@ -189,22 +195,18 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
     auto v_store = [&](int u, const Raw8In<BF> (&in)[8]) __attribute__((always_inline)) {
         const int e = tid + WIN_TPB * u, db = e % NDB, kb = e / NDB;
         if (e >= nvb) return;
-        uint4 r[8]; /* fp16 (BFK: bf16) rows: r[i] holds dims 8 db .. 8 db + 7 of key 8 kb + i */
+        uint4 r[8]; /* fp16 rows: r[i] holds dims 8 db .. 8 db + 7 of key 8 kb + i */
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const bool ok = 8 * kb + i < len && 8 * db < HD;
-            if constexpr (BFK) {
-                r[i] = ok ? in[i].a : make_uint4(0, 0, 0, 0);
-            } else {
-                float v[8];
-                in[i].unpack(v);
-                if (!ok) {
+            float v[8];
+            in[i].unpack(v);
+            if (!ok) {
 #pragma unroll
-                    for (int t = 0; t < 8; t++) v[t] = 0.0f;
-                }
-                note_h_range(p.range_flag, v);
-                r[i] = pack_h8(v);
+                for (int t = 0; t < 8; t++) v[t] = 0.0f;
             }
+            note_h_range(p.range_flag, v);
+            r[i] = pack_h8(v);
         }
         const int sl = kb >> 2, jc = kb & 3;
         unsigned char *vbase = smem + sl * SLABB + Gm::KPARTS * K_BYTES;
@@ -223,27 +225,28 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
         }
     };
     if constexpr (BFK) {
-        /* K: each wave transfers row quad `wave` (1 KB of the image) of
-         * every slab; lane l lands at slot l % 16 of row 4 wave + l / 16,
-         * reading the key's chunk cb = slot ^ f(row); chunks past head_dim
-         * and keys past the window are out of the buffer's range (zeros).
-         * The range is the window's rows, whose first element is the base. */
-        const rsrc_t rk = make_rsrc(reinterpret_cast<const uint16_t *>(p.k) + (long long)w0 * p.row_stride + hoff,
-                                    ((long long)(len - 1) * p.row_stride + HD) * 2);
+        /* K and V: each wave transfers row quad `wave` (1 KB of each image)
+         * of every slab; lane l lands at slot l % 16 of row 4 wave + l / 16,
+         * reading the key's chunk slot ^ f(row) (K) or slot ^ 2 fv(row) (V);
+         * chunks past head_dim and keys past the window are out of the
+         * buffer's range (zeros). The range is the window's rows, whose first
+         * element is the base. */
+        const long long wbase = (long long)w0 * p.row_stride + hoff, wbytes = ((long long)(len - 1) * p.row_stride + HD) * 2;
+        const rsrc_t rk = make_rsrc(reinterpret_cast<const uint16_t *>(p.k) + wbase, wbytes);
+        const rsrc_t rv = make_rsrc(reinterpret_cast<const uint16_t *>(p.v) + wbase, wbytes);
         const int rr = 4 * wave + (lane >> 4), ks16 = lane & 15;
         const int cbk = ks16 ^ ((rr & 3) | (((rr >> 3) & 3) << 2));
+        const int cbv = ks16 ^ (2 * ((rr & 3) | (((rr >> 3) & 1) << 2)));
         const unsigned lds0 = (unsigned)(size_t)smem + (unsigned)(wave * 1024);
 #pragma unroll
         for (int e = 0; e < NS; e++) {
             const int key = e * SMOL_SLAB + rr;
-            const unsigned off = key < len && cbk < HD / 8 ? (unsigned)((key * p.row_stride + cbk * 8) * 2) : OOB_OFF;
-            if (e < nslab) dma_1k(rk, off, 0u, __builtin_amdgcn_readfirstlane(lds0 + (unsigned)(e * SLABB)));
-        }
-        Raw8In<BF> vin[8];
-#pragma unroll
-        for (int u = 0; u < NVB; u++) {
-            v_issue(u, vin);
-            v_store(u, vin);
+            const unsigned offk = key < len && cbk < HD / 8 ? (unsigned)((key * p.row_stride + cbk * 8) * 2) : OOB_OFF;
+            const unsigned offv = key < len && cbv < HD / 8 ? (unsigned)((key * p.row_stride + cbv * 8) * 2) : OOB_OFF;
+            if (e < nslab) {
+                dma_1k(rk, offk, 0u, __builtin_amdgcn_readfirstlane(lds0 + (unsigned)(e * SLABB)));
+                dma_1k(rv, offv, 0u, __builtin_amdgcn_readfirstlane(lds0 + (unsigned)(e * SLABB + K_BYTES)));
+            }
         }
     } else {
         /* the first rounds of K and V go out together */
@@ -304,6 +307,31 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
         const uint4 x = *reinterpret_cast<const uint4 *>(smem + s * SLABB + off);
         return *reinterpret_cast<const h8 *>(&x);
     };
+    /* BFK: the V^T fragment of dim tile dt (lane (c, j): dim 16 dt + c, keys
+     * 8 j .. 8 j + 7) as two transpose reads of the V rows. Each reads four
+     * keys: within a group of 16 lanes, lane q points at 4 dims of one key
+     * row (key 8 j + 4 h + q / 4, dims 16 dt + 4 (q % 4) ..) and lane c
+     * receives dim 16 dt + c of the four keys its group's lanes 4 k + c / 4
+     * point at. The rows of one read (keys 8 j + 4 h + 0..3, over j) take
+     * distinct chunk pairs per pair of groups through fv. */
+    unsigned vto[BFK ? DT : 1];
+    if constexpr (BFK) {
+        const int fv = (c >> 2) | ((j & 1) << 2);
+        const int kr = 8 * j + (c >> 2);
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+            vto[dt] = (unsigned)(K_BYTES + kr * KROW + ((((2 * dt) ^ (2 * fv)) | ((c >> 1) & 1)) << 4) + 8 * (c & 1));
+    }
+    auto lds_vt = [&](int s, int dt) __attribute__((always_inline)) -> h8 {
+        typedef short v4s __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) v4s lds_v4s;
+        const unsigned char *a = smem + s * SLABB + vto[dt];
+        const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s *)(a));
+        const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s *)(a + 4 * KROW));
+        const uint2 x = __builtin_bit_cast(uint2, lo4), y = __builtin_bit_cast(uint2, hi4);
+        const uint4 w = make_uint4(x.x, x.y, y.x, y.y);
+        return *reinterpret_cast<const h8 *>(&w);
+    };
     h8 ones;
 #pragma unroll
     for (int i = 0; i < 8; i++) ones[i] = (_Float16)1.0f;
@@ -352,7 +380,7 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
     for (int s = s_lo; s < s_hi; s++) {
         h8 vf[DT];
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) vf[dt] = lds_h8(s, vfo + dt * 1024);
+        for (int dt = 0; dt < DT; dt++) vf[dt] = BFK ? lds_vt(s, dt) : lds_h8(s, vfo + dt * 1024);
         const bool more = s + 1 < s_hi;
         if (more) {
             read_k(s + 1, kf);
@@ -470,7 +498,7 @@ int launch_win_v(const WinParams *wp, int n_tiles, hipStream_t st, hipEvent_t e0
  * and vision encoders), or as many as the LDS holds */
 template <int HD, bool BF, bool PREC>
 int launch_win_bf(const WinParams *wp, int n_tiles, int max_len, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
-    constexpr int NS_MAX = WinGeom<HD, PREC && !BF>::NS_MAX;
+    constexpr int NS_MAX = WinGeom<HD, PREC && !BF, PREC && BF>::NS_MAX;
     const int ns = (max_len + SMOL_SLAB - 1) / SMOL_SLAB;
     static_assert(NS_MAX >= 4, "the smallest build");
     if (ns <= 4) return launch_win_v<HD, BF, 4, PREC>(wp, n_tiles, st, e0, e1);
@@ -493,7 +521,9 @@ int launch_win_hd(const WinParams *wp, int n_tiles, int max_len, hipStream_t st,
 
 template <int HD>
 int win_max_keys(int in_dtype, int precise) {
-    return (precise && in_dtype != SMOL_IN_BF16 ? WinGeom<HD, true>::NS_MAX : WinGeom<HD, false>::NS_MAX) * SMOL_SLAB;
+    const bool bf = in_dtype == SMOL_IN_BF16;
+    return (precise ? (bf ? WinGeom<HD, false, true>::NS_MAX : WinGeom<HD, true, false>::NS_MAX)
+                    : WinGeom<HD, false, false>::NS_MAX) * SMOL_SLAB;
 }
 
 } // namespace

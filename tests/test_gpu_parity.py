@@ -223,9 +223,12 @@ def test_window_kernel(ctx, sa, oracle, opts, hd, bf):
     two key groups (a 1-key window leaves the second group without slabs),
     and the same call through the staged path for comparison. A window past
     the limit takes the staged path by itself."""
-    # the LDS holds 160 KB of 32-key slabs: K 32 x 256 B, V^T 16 ceil(hd / 16) x 64 B
-    lim = (160 * 1024 // (8192 + 16 * ((hd + 15) // 16) * 64)) * 32
-    assert lim >= 256
+    # the LDS holds 160 KB of 32-key slabs; with the precise products (the
+    # default) a bf16 slab is K and V as rows of 32 x 256 B, an fp32 one K hi
+    # and K lo (2 x 32 x 256 B) and V^T (16 ceil(hd / 16) rows of 64 B)
+    slab = 2 * 8192 if bf else 2 * 8192 + 16 * ((hd + 15) // 16) * 64
+    lim = (160 * 1024 // slab) * 32
+    assert lim >= 192
     H = 3
     for ws in ([0, 1, 32, 65, 130, 200], [7, 7 + lim], [0, lim + 1, lim + 40]):
         print("window kernel", hd, bf, ws, flush=True)
