@@ -378,6 +378,27 @@ __device__ __forceinline__ void dma_1k(rsrc_t r, unsigned voff, unsigned soff, u
 
 #define SK_WAVES 4
 
+/* fp16 hi + lo of two floats (the probabilities of the precise P.V):
+ * hi = fp16_rne(p), lo = fp16_rne(p - hi). p - hi is exact in fp32 (hi is p
+ * rounded to 11 bits), and v_fma_mix_f32 forms it straight from the packed
+ * fp16 hi (-1 * hi + p, one rounding of an exact value), which saves the
+ * unpacking of hi: per pair two packed conversions and two mixes. Both halves
+ * come back packed as the MFMA operand holds them (element e in the low half
+ * of dword e / 2). The kernels run with fp16 and fp32 denormals preserved, so
+ * a denormal hi is read exactly. */
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void split_h2(float p0, float p1, uint32_t &hi, uint32_t &lo) {
+    typedef _Float16 hv2 __attribute__((ext_vector_type(2)));
+    typedef float fv2 __attribute__((ext_vector_type(2)));
+    hi = __builtin_bit_cast(uint32_t, __builtin_convertvector((fv2){p0, p1}, hv2));
+    float l0, l1;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(l0) : "v"(hi), "v"(p0));
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(l1) : "v"(hi), "v"(p1));
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((fv2){l0, l1}, hv2));
+}
+#pragma clang diagnostic pop
+
 /* Reductions over the four lanes c, c+16, c+32, c+48 that hold one softmax
  * row, with the gfx950 cross-row swaps (VALU, no LDS round trip). Each swap
  * hands every lane the pair {x[l], x[l ^ 32]} (resp. l ^ 16), so all four

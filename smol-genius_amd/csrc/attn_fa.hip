@@ -292,11 +292,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, W))) voi
         for (int nt = 0; nt < NT; nt++) {
             float pe[8];
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                pe[e] = __builtin_amdgcn_exp2f(sv[nt][e]);
-                const _Float16 ph = (_Float16)pe[e];
-                pf[0][nt][e] = ph;
-                if constexpr (PREC) pf[1][nt][e] = (_Float16)(pe[e] - (float)ph);
+            for (int e = 0; e < 8; e++) pe[e] = __builtin_amdgcn_exp2f(sv[nt][e]);
+            if constexpr (PREC) {
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    uint32_t hi, lo;
+                    split_h2(pe[e], pe[e + 1], hi, lo);
+                    reinterpret_cast<uint32_t *>(&pf[0][nt])[e >> 1] = hi;
+                    reinterpret_cast<uint32_t *>(&pf[1][nt])[e >> 1] = lo;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) pf[0][nt][e] = (_Float16)pe[e];
             }
             l[nt] += ((pe[0] + pe[1]) + (pe[2] + pe[3])) + ((pe[4] + pe[5]) + (pe[6] + pe[7]));
         }

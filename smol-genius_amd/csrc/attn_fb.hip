@@ -428,15 +428,21 @@ __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, NT == 1 ? 2 : 1))) void k_at
      * sum of the lane's probabilities in psum) */
     auto p_frag = [&](const f4 (&s)[2], float sh, h8 (&pf)[NP][NT], int nt, float &psum) __attribute__((always_inline)) {
         float ps = 0.0f;
+        if constexpr (PREC) {
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const float pe = __builtin_amdgcn_exp2f(s[e >> 2][e & 3] - sh);
-            const _Float16 ph = (_Float16)pe;
-            pf[0][nt][e] = ph;
-            if constexpr (PREC) {
-                pf[1][nt][e] = (_Float16)(pe - (float)ph);
-                ps += pe;
+            for (int e = 0; e < 8; e += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(s[e >> 2][e & 3] - sh);
+                const float p1 = __builtin_amdgcn_exp2f(s[(e + 1) >> 2][(e + 1) & 3] - sh);
+                uint32_t hi, lo;
+                split_h2(p0, p1, hi, lo);
+                reinterpret_cast<uint32_t *>(&pf[0][nt])[e >> 1] = hi;
+                reinterpret_cast<uint32_t *>(&pf[1][nt])[e >> 1] = lo;
+                ps += p0;
+                ps += p1;
             }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) pf[0][nt][e] = (_Float16)__builtin_amdgcn_exp2f(s[e >> 2][e & 3] - sh);
         }
         psum = ps;
     };

@@ -412,11 +412,17 @@ __global__ __launch_bounds__(WIN_TPB) void k_attn_win(const WinParams p) {
         for (int e = 0; e < 8; e++) {
             const float pe = __builtin_amdgcn_exp2f(sv[e] - m_new);
             pe8[e] = pe;
-            if constexpr (!BFK) {
-                pf[e] = (_Float16)pe;
-                if constexpr (PREC) pfl[e] = (_Float16)(pe - (float)pf[e]);
-            }
+            if constexpr (!BFK && !PREC) pf[e] = (_Float16)pe;
             if constexpr (PREC) ps += pe;
+        }
+        if constexpr (!BFK && PREC) {
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                uint32_t hi, lo;
+                split_h2(pe8[e], pe8[e + 1], hi, lo);
+                reinterpret_cast<uint32_t *>(&pf)[e >> 1] = hi;
+                reinterpret_cast<uint32_t *>(&pfl)[e >> 1] = lo;
+            }
         }
         if constexpr (BFK) {
             /* P as bf16 hi + lo against the exact bf16 V^T */
