@@ -28,8 +28,7 @@
  * one from the launch's rounds over the device. With a bf16 x the waves
  * form a 2 x (NW / 2) grid; with an fp32 x each wave of the two smaller
  * tiles owns rows of its own (1 x NW) and so splits each element once per
- * workgroup: the split's vector work, not the matrix cores, bounds the fp32
- * steps. K advances 64 at a time through NSTG LDS
+ * workgroup. K advances 64 at a time through NSTG LDS
  * stages (three where they fit in 150 KB, else two): W, x and the norm
  * weight all by direct-to-LDS transfers (buffer_load ... lds), the next
  * stages in flight while one is multiplied. LDS rows are 128 or 256 bytes
