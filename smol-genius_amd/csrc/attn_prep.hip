@@ -398,6 +398,75 @@ __global__ __launch_bounds__(256) void k_bf16_norm_rope(uint16_t *x, const float
     }
 }
 
+/* The same operations for one position (a decode step: at most 256 head
+ * rows): one workgroup first stages the rows (16-byte loads), both weight
+ * vectors and the table row in LDS with coalesced loads (one round of loads
+ * instead of a chain of dependent ones per thread), then one thread per row runs
+ * k_bf16_norm_rope's operation order on the staged values, so the bits are
+ * the same. LDS: the rows (bf16), then w, w2, cos and sin (hd floats each). */
+__global__ __launch_bounds__(256) void k_bf16_norm_rope1(uint16_t *x, const float *w, uint16_t *x2, const float *w2,
+                                                         float eps, const float *cos_t, const float *sin_t, int pos,
+                                                         int H, int H2, int hd) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds_nr[];
+    const int tid = threadIdx.x;
+    const int rows1 = H, rows = H + (x2 ? H2 : 0);
+    const int c1 = rows1 * hd / 8, ch = rows * hd / 8; /* 16-byte chunks of the rows */
+    uint4 *s_rows = reinterpret_cast<uint4 *>(lds_nr);
+    float *s_w = reinterpret_cast<float *>(lds_nr + (size_t)rows * hd * 2);
+    float *s_w2 = s_w + hd, *s_c = s_w2 + hd, *s_s = s_c + hd;
+    for (int e = tid; e < ch; e += blockDim.x)
+        s_rows[e] = e < c1 ? reinterpret_cast<const uint4 *>(x)[e] : reinterpret_cast<const uint4 *>(x2)[e - c1];
+    for (int e = tid; e < hd; e += blockDim.x) {
+        s_w[e] = w ? w[e] : 1.0f;
+        s_w2[e] = w2 ? w2[e] : 1.0f;
+        if (cos_t) {
+            s_c[e] = cos_t[(long long)pos * hd + e];
+            s_s[e] = sin_t[(long long)pos * hd + e];
+        }
+    }
+    __syncthreads();
+    if (tid >= rows) return;
+    const bool second = tid >= rows1;
+    const bool norm = second ? w2 != nullptr : w != nullptr;
+    const float *w_r = second ? s_w2 : s_w;
+    const int n8 = hd >> 3;
+    const uint4 *src = s_rows + (size_t)tid * n8;
+    uint4 *row = reinterpret_cast<uint4 *>(second ? x2 + (size_t)(tid - rows1) * hd : x + (size_t)tid * hd);
+    float ri = 1.0f;
+    if (norm) {
+        float ss = 0.0f;
+        for (int c8 = 0; c8 < n8; c8++) {
+            float v[8];
+            unpack_bf16x8(src[c8], v);
+#pragma unroll
+            for (int i = 0; i < 8; i++) ss = __fmaf_rn(v[i], v[i], ss);
+        }
+        ri = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)hd), eps)));
+    }
+    for (int c8 = 0; c8 < n8; c8++) {
+        float v[8];
+        unpack_bf16x8(src[c8], v);
+        if (norm) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = __uint_as_float(__float_as_uint(__fmul_rn(__fmul_rn(v[i], ri), w_r[c8 * 8 + i])) & 0xFFFF0000u);
+        }
+        if (cos_t) {
+#pragma unroll
+            for (int i = 0; i < 8; i += 2) {
+                const float c = s_c[c8 * 8 + i], sn = s_s[c8 * 8 + i];
+                const float x0 = v[i], x1 = v[i + 1];
+                v[i] = __fmaf_rn(x0, c, -__fmul_rn(x1, sn));
+                v[i + 1] = __fmaf_rn(x1, c, __fmul_rn(x0, sn));
+            }
+        }
+        uint32_t o[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            o[k] = (__float_as_uint(v[2 * k]) >> 16) | (__float_as_uint(v[2 * k + 1]) & 0xFFFF0000u);
+        row[c8] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
 /* x2 / w2 / H2: a second tensor at the same positions (NULL: none), the K
  * rows of the call that normalises and rotates its Q rows in x */
 extern "C" int smol_launch_bf16_norm_rope(uint16_t *x, const float *w, uint16_t *x2, const float *w2, int H2,
@@ -405,6 +474,12 @@ extern "C" int smol_launch_bf16_norm_rope(uint16_t *x, const float *w, uint16_t 
                                           int hd, hipStream_t st) {
     const long long rows = (long long)seq * H + (x2 ? (long long)seq * H2 : 0);
     if (rows <= 0) return 0;
+    const size_t lds1 = (size_t)rows * hd * 2 + 4 * (size_t)hd * 4;
+    if (seq == 1 && rows <= 256 && lds1 <= 64 * 1024) {
+        hipLaunchKernelGGL(k_bf16_norm_rope1, dim3(1), dim3(256), lds1, st, x, w, x2, w2, eps, cos_t, sin_t, pos0, H,
+                           x2 ? H2 : 0, hd);
+        return hipGetLastError() == hipSuccess ? 0 : -3;
+    }
     const int blocks = (int)std::min<long long>((rows + 255) / 256, 4096);
     hipLaunchKernelGGL(k_bf16_norm_rope, dim3(blocks), dim3(256), 0, st, x, w, x2, w2, eps, cos_t, sin_t, pos0, seq,
                        H, H2, hd);

@@ -144,13 +144,15 @@ def test_qkn_block_device_io_matches_host_io(sa, oracle, dorc, bf16):
 
 @pytest.mark.parametrize("hd", [64, 72, 80, 96, 128, 256])
 @pytest.mark.parametrize("mode", ["norm", "rope", "norm+rope"])
-def test_norm_rope_bf16_bits(sa, oracle, hd, mode):
+@pytest.mark.parametrize("seq", [37, 1])
+def test_norm_rope_bf16_bits(sa, oracle, hd, mode, seq):
     """smol_attn_norm_rope_bf16 reproduces the oracle's truncating norm and
-    rotation bit for bit, over several binades and far positions."""
-    print("norm_rope_bf16", hd, mode, flush=True)
+    rotation bit for bit, over several binades and far positions; one
+    position (a decode step) takes the LDS-staged kernel."""
+    print("norm_rope_bf16", hd, mode, seq, flush=True)
     ctx = sa.Context(0)
     try:
-        seq, H, pos0 = 37, 3, 4000
+        H, pos0 = 3, 4000
         r = np.random.default_rng(hd)
         x = synth.f32_to_bf16_bits((r.standard_normal((seq, H * hd)) *
                                     np.exp2(r.integers(-8, 8, (seq, H * hd)))).astype(np.float32))
