@@ -153,9 +153,37 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
     /* the norm weight (reads zero when there is none, then unused) */
     const bool norm = FUSE && p.norm_w;
     const rsrc_t gr = make_rsrc(norm ? (const void *)p.norm_w : (const void *)h.w[0], norm ? (long long)in * 4 : 0);
+    /* FUSE with an fp32 x: the fp32 RMSNorm (scale applied to the sums);
+     * with a bf16 x (N16): the bf16 decoder's input norm, x replaced by
+     * tr((bf(x) * r) * w) as it is loaded (k_bf16_rows' values) */
+    constexpr bool N16 = FUSE && XBF, F32N = FUSE && !XBF;
     float ssq[SEQ];
 #pragma unroll
     for (int s = 0; s < SEQ; s++) ssq[s] = 0.0f;
+    /* N16: r of each input row before the products, in k_bf16_rows' order
+     * (the host launches 256 threads: per-thread strided fused
+     * multiply-adds, a butterfly over each wave, the four waves in order),
+     * so the normalised x has that kernel's bits */
+    float r16[SEQ];
+    if constexpr (N16) {
+        __shared__ float red16[4][SEQ];
+        const uint16_t *xb = static_cast<const uint16_t *>(h.x);
+#pragma unroll
+        for (int s = 0; s < SEQ; s++) {
+            float ss = 0.0f;
+            for (int i = threadIdx.x; i < in; i += 256) {
+                const float v = bfw(xb[(long long)s * in + i]);
+                ss = fmaf(v, v, ss);
+            }
+#pragma unroll
+            for (int m = 32; m > 0; m >>= 1) ss += __shfl_xor(ss, m, 64);
+            if (lane == 0) red16[wid][s] = ss;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < SEQ; s++)
+            r16[s] = 1.0f / sqrtf((((red16[0][s] + red16[1][s]) + red16[2][s]) + red16[3][s]) / (float)in + p.eps);
+    }
 
     float acc[GEMV_R][SEQ];
 #pragma unroll
@@ -252,7 +280,15 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
                 }
             }
         }
-        if constexpr (FUSE) {
+        if constexpr (N16) {
+#pragma unroll
+            for (int u = 0; u < GEMV_U; u++)
+#pragma unroll
+                for (int s = 0; s < SEQ; s++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) xf[u][s][e] = bfw(bftr((xf[u][s][e] * r16[s]) * gf[u][e]));
+        }
+        if constexpr (F32N) {
             /* sum of squares of the raw x, then x * g (rmsnorm.c:17-75 scales after the product) */
 #pragma unroll
             for (int u = 0; u < GEMV_U; u++)
@@ -283,7 +319,7 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
             const float t = wave_sum(acc[r][s]);
             if (lane == s * GEMV_R + r) mine = t;
         }
-    if constexpr (FUSE) {
+    if constexpr (F32N) {
         if (norm) {
 #pragma unroll
             for (int s = 0; s < SEQ; s++) {
@@ -295,7 +331,7 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
     if (kp > 1) {
         if (lane < GEMV_R * SEQ) {
             red[wid][lane] = mine;
-            if constexpr (FUSE) red_ss[wid][lane] = myss;
+            if constexpr (F32N) red_ss[wid][lane] = myss;
         }
         __syncthreads();
         if (wave != 0) return;
@@ -304,11 +340,11 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
             myss = 0.0f;
             for (int w = 0; w < kp; w++) {
                 mine += red[wid + w][lane];
-                if constexpr (FUSE) myss += red_ss[wid + w][lane];
+                if constexpr (F32N) myss += red_ss[wid + w][lane];
             }
         }
     }
-    if constexpr (FUSE) {
+    if constexpr (F32N) {
         const int r = lane % GEMV_R, s = lane / GEMV_R;
         const int o = row_base + r;
         const bool live = lane < GEMV_R * SEQ && o < p.rows;
@@ -555,7 +591,8 @@ int launch_gemv_v(const GemvParams &p, bool vec, hipStream_t st) {
 
 template <int SEQ>
 int launch_gemv_s(const GemvParams &p, bool xbf, bool ybf, bool vec, bool fuse, hipStream_t st) {
-    if (fuse) return launch_gemv_v<SEQ, false, false, true>(p, vec, st);
+    if (fuse)
+        return xbf ? launch_gemv_v<SEQ, true, true, true>(p, vec, st) : launch_gemv_v<SEQ, false, false, true>(p, vec, st);
     if (xbf)
         return ybf ? launch_gemv_v<SEQ, true, true, false>(p, vec, st)
                    : launch_gemv_v<SEQ, true, false, false>(p, vec, st);
@@ -572,6 +609,8 @@ struct GemvBf16Ops {
     int act;               /* SMOL_LINEAR_ACT_NONE or _GEGLU */
     const uint16_t *res16; /* or null */
     bool x_trunc;
+    const float *norm16 = nullptr; /* bf16 x: the input RMSNorm's weight (k_bf16_rows' values), or null */
+    float eps = 0.0f;
 };
 
 int run_gemv(smol_attn_ctx *ctx, hipStream_t st, const void *x, bool xbf, bool ybf, int seq, int in, int n_seg,
@@ -588,7 +627,11 @@ int run_gemv(smol_attn_ctx *ctx, hipStream_t st, const void *x, bool xbf, bool y
         p.act = bo->act;
         p.res16 = bo->res16;
         p.x_trunc = bo->x_trunc ? 1 : 0;
+        p.norm_w = bo->norm16;
+        p.eps = bo->eps;
     }
+    const bool n16 = bo && bo->norm16;
+    if (n16 && (!xbf || !ybf)) return 1;
     int rows = 0;
     bool vec = (in % 8) == 0 && aligned16(x) && aligned16(p.norm_w);
     for (int i = 0; i < GEMV_SEGS; i++) {
@@ -613,11 +656,16 @@ int run_gemv(smol_attn_ctx *ctx, hipStream_t st, const void *x, bool xbf, bool y
     p.kp = std::max(1, std::min(GEMV_MAX_KP, (chunks + 64 * GEMV_U - 1) / (64 * GEMV_U)));
     p.groups = std::max(1, std::min(GEMV_WG_WAVES / p.kp, (rows + GEMV_R - 1) / GEMV_R));
     if (rows <= 0) return 0;
+    if (n16) {
+        /* the norm's order needs 256 threads a workgroup */
+        if (4 % p.kp != 0) return 1;
+        p.groups = 4 / p.kp;
+    }
     hipEvent_t e0 = nullptr, e1 = nullptr;
     smol_internal_timing_events(ctx, LIN_TIMING_KIND, &e0, &e1);
     if (e0) LHIP(hipEventRecord(e0, st));
     int rc;
-    const bool fuse = f != nullptr;
+    const bool fuse = f != nullptr || n16;
     switch (seq) {
     case 1: rc = launch_gemv_s<1>(p, xbf, ybf, vec, fuse, st); break;
     case 2: rc = launch_gemv_s<2>(p, xbf, ybf, vec, fuse, st); break;
@@ -829,6 +877,31 @@ extern "C" int smol_linear_qkv_dev(smol_attn_ctx *ctx, void *q, void *k, void *v
         segs[n++] = GemvSeg{wv, nullptr, v, kv_dim};
     }
     return run_gemv(ctx, st, x, x_dtype == SMOL_ATTN_BF16, y_dtype == SMOL_ATTN_BF16, seq, in_dim, n, segs);
+}
+
+/* The bf16 decoder's input RMSNorm (qkn_bf16_decoder.c:51-71) and its Q/K/V
+ * projections for at most SMOL_LINEAR_GEMV_MAX_SEQ rows in one GEMV launch:
+ * the normalised row is formed as x is loaded, with the bits k_bf16_rows
+ * (smol_bf16_rms_norm_dev) would write, so the outputs equal the two launches'
+ * bit for bit. Returns 1, launching nothing, where the shape does not allow
+ * it (more rows, an in_dim needing eight waves a row, misaligned operands are
+ * still handled; the caller then runs the norm and the projections apart). */
+extern "C" int smol_internal_linear_qkv_bf16_norm(smol_attn_ctx *ctx, uint16_t *q, uint16_t *k, uint16_t *v,
+                                                  const uint16_t *x, const float *norm_w, float eps,
+                                                  const uint16_t *wq, const uint16_t *wk, const uint16_t *wv, int seq,
+                                                  int in_dim, int q_dim, int kv_dim) {
+    if (!ctx || !q || !k || !v || !x || !norm_w || !wq || !wk || !wv || seq <= 0 ||
+        seq > SMOL_LINEAR_GEMV_MAX_SEQ || in_dim <= 0 || q_dim <= 0 || kv_dim <= 0 ||
+        (long long)seq * in_dim > INT_MAX / 4 || (long long)q_dim + 2LL * kv_dim > INT_MAX / 4)
+        return 1;
+    LHIP(hipSetDevice(smol_internal_ctx_device(ctx)));
+    hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
+    const GemvSeg segs[3] = {GemvSeg{wq, nullptr, q, q_dim}, GemvSeg{wk, nullptr, k, kv_dim},
+                             GemvSeg{wv, nullptr, v, kv_dim}};
+    GemvBf16Ops bo{SMOL_LINEAR_ACT_NONE, nullptr, false};
+    bo.norm16 = norm_w;
+    bo.eps = eps;
+    return run_gemv(ctx, st, x, true, true, seq, in_dim, 3, segs, nullptr, &bo);
 }
 
 extern "C" int smol_linear_ops_dev(smol_attn_ctx *ctx, float *y, const float *x, const uint16_t *w,

@@ -41,6 +41,10 @@ extern "C" int smol_internal_norm_rope_bf16_qk(smol_attn_ctx *ctx, const smol_ro
 extern "C" int smol_internal_linear_bf16_ops(smol_attn_ctx *ctx, uint16_t *y, const void *x, int x_f32_trunc,
                                              const uint16_t *w, int seq, int in_dim, int out_dim, int act,
                                              const uint16_t *res16);
+extern "C" int smol_internal_linear_qkv_bf16_norm(smol_attn_ctx *ctx, uint16_t *q, uint16_t *k, uint16_t *v,
+                                                  const uint16_t *x, const float *norm_w, float eps,
+                                                  const uint16_t *wq, const uint16_t *wk, const uint16_t *wv, int seq,
+                                                  int in_dim, int q_dim, int kv_dim);
 
 namespace {
 
@@ -302,8 +306,15 @@ int run_layer_bf16(Binding *b, int layer, int pos, int n, uint16_t *x, const smo
     uint16_t *xn = (uint16_t *)b->lx.p, *g = (uint16_t *)b->lh.p;
     smol_attn_ctx *ctx = b->ctx;
     const int BF = SMOL_ATTN_BF16;
-    if ((rc = smol_bf16_rms_norm_dev(ctx, xn, x, w->input_norm, n, dim, c.eps))) return rc;
-    if ((rc = smol_linear_qkv_dev(ctx, q, k, v, BF, xn, BF, w->wq, w->wk, w->wv, n, dim, q_dim, kv_dim))) return rc;
+    /* a few rows: the input norm inside the Q/K/V GEMV (the same bits, one launch fewer) */
+    rc = n <= SMOL_LINEAR_GEMV_MAX_SEQ ? smol_internal_linear_qkv_bf16_norm(ctx, q, k, v, x, w->input_norm, c.eps, w->wq,
+                                                                           w->wk, w->wv, n, dim, q_dim, kv_dim)
+                                      : 1;
+    if (rc < 0) return rc;
+    if (rc == 1) {
+        if ((rc = smol_bf16_rms_norm_dev(ctx, xn, x, w->input_norm, n, dim, c.eps))) return rc;
+        if ((rc = smol_linear_qkv_dev(ctx, q, k, v, BF, xn, BF, w->wq, w->wk, w->wv, n, dim, q_dim, kv_dim))) return rc;
+    }
     /* a few rows (decode): the GEMV launches take the attention output as
      * fp32 and truncate it as they load it, and fold GeGLU into gate_up and
      * the last residual add into down (the same truncations, three launches
