@@ -97,6 +97,11 @@ struct GemvParams {
      * truncated to bf16 as it is loaded */
     const uint16_t *res16;
     int x_trunc;
+    /* N16 only: add16 [seq][in] bf16 or null: x is first replaced by
+     * tr(bf(x) + bf(add16)) (k_bf16_rows' residual add), and workgroup 0
+     * writes that sum to xout16 (or not, when null) */
+    const uint16_t *add16;
+    uint16_t *xout16;
 };
 
 /* ---------------------------------------------------------------- kernels */
@@ -131,6 +136,10 @@ template <int SEQ, bool XBF, bool YBF, bool VEC, bool FUSE>
 __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
     __shared__ float red[GEMV_MAX_KP][GEMV_R * SEQ];
     __shared__ float red_ss[GEMV_MAX_KP][GEMV_R * SEQ];
+    /* FUSE with an fp32 x: the fp32 RMSNorm (scale applied to the sums);
+     * with a bf16 x (N16): the bf16 decoder's input norm, x replaced by
+     * tr((bf(x) * r) * w) as it is loaded (k_bf16_rows' values) */
+    constexpr bool N16 = FUSE && XBF, F32N = FUSE && !XBF;
     const GemvParams &h = p;
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -150,13 +159,10 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
         wr[r] = make_rsrc(live ? w + (long long)(row - r0) * in : h.w[0], live ? (long long)in * 2 : 0);
     }
     const rsrc_t xr = make_rsrc(h.x, (long long)SEQ * in * (XBF ? 2 : 4));
+    const rsrc_t ar = make_rsrc(N16 && p.add16 ? (const void *)p.add16 : h.x, N16 && p.add16 ? (long long)SEQ * in * 2 : 0);
     /* the norm weight (reads zero when there is none, then unused) */
     const bool norm = FUSE && p.norm_w;
     const rsrc_t gr = make_rsrc(norm ? (const void *)p.norm_w : (const void *)h.w[0], norm ? (long long)in * 4 : 0);
-    /* FUSE with an fp32 x: the fp32 RMSNorm (scale applied to the sums);
-     * with a bf16 x (N16): the bf16 decoder's input norm, x replaced by
-     * tr((bf(x) * r) * w) as it is loaded (k_bf16_rows' values) */
-    constexpr bool N16 = FUSE && XBF, F32N = FUSE && !XBF;
     float ssq[SEQ];
 #pragma unroll
     for (int s = 0; s < SEQ; s++) ssq[s] = 0.0f;
@@ -168,11 +174,18 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
     if constexpr (N16) {
         __shared__ float red16[4][SEQ];
         const uint16_t *xb = static_cast<const uint16_t *>(h.x);
+        const bool wr_x = p.xout16 && blockIdx.x == 0;
 #pragma unroll
         for (int s = 0; s < SEQ; s++) {
             float ss = 0.0f;
             for (int i = threadIdx.x; i < in; i += 256) {
-                const float v = bfw(xb[(long long)s * in + i]);
+                const long long j = (long long)s * in + i;
+                float v = bfw(xb[j]);
+                if (p.add16) {
+                    const uint16_t t = bftr(v + bfw(p.add16[j]));
+                    if (wr_x) p.xout16[j] = t;
+                    v = bfw(t);
+                }
                 ss = fmaf(v, v, ss);
             }
 #pragma unroll
@@ -201,6 +214,7 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
         if constexpr (VEC) {
             uint4 wv[GEMV_U][GEMV_R];
             uint4 xv[GEMV_U][SEQ][XBF ? 1 : 2];
+            uint4 av[GEMV_U][SEQ];
             uint4 gv[GEMV_U][2];
 #pragma unroll
             for (int u = 0; u < GEMV_U; u++) {
@@ -216,6 +230,7 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
                 for (int s = 0; s < SEQ; s++) {
                     if constexpr (XBF) {
                         xv[u][s][0] = bload(xr, ok ? (unsigned)(s * in + c * 8) * 2u : OOB_OFF, 0);
+                        if constexpr (N16) av[u][s] = bload(ar, ok ? (unsigned)(s * in + c * 8) * 2u : OOB_OFF, 0);
                     } else {
                         const unsigned o = (unsigned)(s * in + c * 8) * 4u;
                         xv[u][s][0] = bload(xr, ok ? o : OOB_OFF, 0);
@@ -241,6 +256,12 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
                 for (int s = 0; s < SEQ; s++) {
                     if constexpr (XBF) {
                         unpack_bf16x8(xv[u][s][0], xf[u][s]);
+                        if constexpr (N16) {
+                            float af[8];
+                            unpack_bf16x8(av[u][s], af);
+#pragma unroll
+                            for (int e = 0; e < 8; e++) xf[u][s][e] = bfw(bftr(xf[u][s][e] + af[e]));
+                        }
                     } else {
                         const uint4 a = xv[u][s][0], b = xv[u][s][1];
                         const uint32_t t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
@@ -272,6 +293,11 @@ __global__ __launch_bounds__(64 * GEMV_MAX_KP) void k_gemv(const GemvParams p) {
                             const unsigned short h = __builtin_amdgcn_raw_buffer_load_b16(
                                 xr, ok ? (unsigned)(s * in + i) * 2u : OOB_OFF, 0, 0);
                             xf[u][s][e] = __uint_as_float((uint32_t)h << 16);
+                            if constexpr (N16) {
+                                const unsigned short ha = __builtin_amdgcn_raw_buffer_load_b16(
+                                    ar, ok ? (unsigned)(s * in + i) * 2u : OOB_OFF, 0, 0);
+                                xf[u][s][e] = bfw(bftr(xf[u][s][e] + __uint_as_float((uint32_t)ha << 16)));
+                            }
                         } else {
                             xf[u][s][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
                                 xr, ok ? (unsigned)(s * in + i) * 4u : OOB_OFF, 0, 0) & xmask);
@@ -611,6 +637,8 @@ struct GemvBf16Ops {
     bool x_trunc;
     const float *norm16 = nullptr; /* bf16 x: the input RMSNorm's weight (k_bf16_rows' values), or null */
     float eps = 0.0f;
+    const uint16_t *add16 = nullptr; /* with norm16: x + add16 (truncated) is normalised */
+    uint16_t *xout16 = nullptr;      /* with add16: that sum is written here */
 };
 
 int run_gemv(smol_attn_ctx *ctx, hipStream_t st, const void *x, bool xbf, bool ybf, int seq, int in, int n_seg,
@@ -629,6 +657,8 @@ int run_gemv(smol_attn_ctx *ctx, hipStream_t st, const void *x, bool xbf, bool y
         p.x_trunc = bo->x_trunc ? 1 : 0;
         p.norm_w = bo->norm16;
         p.eps = bo->eps;
+        p.add16 = bo->norm16 ? bo->add16 : nullptr;
+        p.xout16 = bo->norm16 ? bo->xout16 : nullptr;
     }
     const bool n16 = bo && bo->norm16;
     if (n16 && (!xbf || !ybf)) return 1;
@@ -902,6 +932,32 @@ extern "C" int smol_internal_linear_qkv_bf16_norm(smol_attn_ctx *ctx, uint16_t *
     bo.norm16 = norm_w;
     bo.eps = eps;
     return run_gemv(ctx, st, x, true, true, seq, in_dim, 3, segs, nullptr, &bo);
+}
+
+/* The bf16 decoder's residual add, post-attention RMSNorm and GeGLU gate_up
+ * projection (qkn_bf16_decoder.c:551-557 without the Gemma 3 post-sublayer
+ * norm, then :560-563) for at most SMOL_LINEAR_GEMV_MAX_SEQ rows in one GEMV
+ * launch: x_new = tr(bf(x) + bf(p)) is written to x_new (x is left as it is:
+ * every workgroup reads it), normalised as k_bf16_rows does and multiplied,
+ * and g = geglu of the truncated (gate, up) pairs. Returns 1, launching
+ * nothing, where the shape does not allow it. */
+extern "C" int smol_internal_linear_bf16_addnorm_geglu(smol_attn_ctx *ctx, uint16_t *g, const uint16_t *x,
+                                                       const uint16_t *p, uint16_t *x_new, const float *norm_w,
+                                                       float eps, const uint16_t *w_gate_up, int seq, int in_dim,
+                                                       int out_dim) {
+    if (!ctx || !g || !x || !p || !x_new || !norm_w || !w_gate_up || seq <= 0 || seq > SMOL_LINEAR_GEMV_MAX_SEQ ||
+        in_dim <= 0 || out_dim <= 0 || (out_dim & 1) || (long long)seq * in_dim > INT_MAX / 4 ||
+        (long long)seq * out_dim > INT_MAX / 4)
+        return 1;
+    LHIP(hipSetDevice(smol_internal_ctx_device(ctx)));
+    hipStream_t st = static_cast<hipStream_t>(smol_attn_ctx_stream(ctx));
+    const GemvSeg sg{w_gate_up, nullptr, g, out_dim};
+    GemvBf16Ops bo{SMOL_LINEAR_ACT_GEGLU, nullptr, false};
+    bo.norm16 = norm_w;
+    bo.eps = eps;
+    bo.add16 = p;
+    bo.xout16 = x_new;
+    return run_gemv(ctx, st, x, true, true, seq, in_dim, 1, &sg, nullptr, &bo);
 }
 
 extern "C" int smol_linear_ops_dev(smol_attn_ctx *ctx, float *y, const float *x, const uint16_t *w,

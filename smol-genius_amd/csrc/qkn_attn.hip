@@ -45,6 +45,10 @@ extern "C" int smol_internal_linear_qkv_bf16_norm(smol_attn_ctx *ctx, uint16_t *
                                                   const uint16_t *x, const float *norm_w, float eps,
                                                   const uint16_t *wq, const uint16_t *wk, const uint16_t *wv, int seq,
                                                   int in_dim, int q_dim, int kv_dim);
+extern "C" int smol_internal_linear_bf16_addnorm_geglu(smol_attn_ctx *ctx, uint16_t *g, const uint16_t *x,
+                                                       const uint16_t *p, uint16_t *x_new, const float *norm_w,
+                                                       float eps, const uint16_t *w_gate_up, int seq, int in_dim,
+                                                       int out_dim);
 
 namespace {
 
@@ -328,6 +332,16 @@ int run_layer_bf16(Binding *b, int layer, int pos, int n, uint16_t *x, const smo
             return rc;
     } else if ((rc = smol_linear_dev(ctx, p, BF, attn, BF, w->wo, nullptr, n, q_dim, dim))) {
         return rc;
+    }
+    if (few && !w->pre_ffn_norm && !w->post_ffn_norm) {
+        /* the residual add and the post-attention norm inside the gate_up
+         * GEMV (the same bits; x + p goes to xn, which the down GEMV adds
+         * its result to, writing x) */
+        rc = smol_internal_linear_bf16_addnorm_geglu(ctx, g, x, p, xn, w->post_attn_norm, c.eps, w->gate_up, n, dim,
+                                                     2 * inter);
+        if (rc < 0) return rc;
+        if (rc == 0)
+            return smol_internal_linear_bf16_ops(ctx, x, g, 0, w->down, n, inter, dim, SMOL_LINEAR_ACT_NONE, xn);
     }
     if (w->pre_ffn_norm)
         rc = smol_bf16_add_norm_dev(ctx, x, p, w->post_attn_norm, w->pre_ffn_norm, xn, n, dim, c.eps);
